@@ -1,0 +1,116 @@
+"""Pins for the CPU attention oracle (oracle/sparse_attention.py)."""
+import math
+
+import pytest
+import torch
+
+from oracle import sparse_attention as sa
+
+
+def _rand(S, H, hn, seed, dtype=torch.float64, mult=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randn(S, H, hn, generator=g, dtype=dtype) * mult for _ in range(3)]
+
+
+def test_dense_special_case_matches_dense_softmax():
+    S, H, hn = 7, 3, 4
+    q, k, v = _rand(S, H, hn, 0, mult=0.5)
+    src, dst = torch.meshgrid(torch.arange(S), torch.arange(S), indexing="ij")
+    ei = torch.stack([src.reshape(-1), dst.reshape(-1)])
+    out = sa.graphormer_sparse_attention(k, q, v, ei)
+    # dense: scores[h, t, s] = q_t . k_s / sqrt(hn); no clamp is hit at this scale
+    scores = torch.einsum("thd,shd->hts", q, k) / math.sqrt(hn)
+    assert scores.abs().max() < 5
+    p = torch.exp(scores)
+    dense = torch.einsum("hts,shd->thd", p, v) / (p.sum(-1).transpose(0, 1).unsqueeze(-1) + 1e-6)
+    torch.testing.assert_close(out, dense, rtol=1e-12, atol=1e-12)
+
+
+def test_single_edge_closed_form():
+    q, k, v = _rand(3, 2, 4, 1)
+    ei = torch.tensor([[2], [0]])
+    out = sa.graphormer_sparse_attention(k, q, v, ei)
+    s = ((k[2] * q[0]).sum(-1) / 2.0).clamp(-5, 5)
+    expect = v[2] * (torch.exp(s) / (torch.exp(s) + 1e-6)).unsqueeze(-1)
+    torch.testing.assert_close(out[0], expect)
+    assert out[1].abs().max() == 0 and out[2].abs().max() == 0   # queries without edges
+
+
+def test_equal_scores_give_mean_of_v():
+    q, k, v = _rand(6, 2, 4, 2)
+    q.zero_()
+    ei = torch.tensor([[1, 2, 3, 5], [0, 0, 0, 0]])
+    out = sa.graphormer_sparse_attention(k, q, v, ei)
+    torch.testing.assert_close(out[0], v[[1, 2, 3, 5]].sum(0) / (4 + 1e-6))
+
+
+def test_clamp_bounds_scores():
+    q, k, v = _rand(4, 1, 4, 3)
+    q[0] = 1.0
+    k[1] = 4.0       # a = 16*4/2 = +32 -> clamps to +5
+    k[2] = -3.0      # a = -6 -> clamps to -5
+    ei = torch.tensor([[1, 2], [0, 0]])
+    out = sa.graphormer_sparse_attention(k, q, v, ei)
+    p1, p2 = math.exp(5.0), math.exp(-5.0)
+    expect = (p1 * v[1] + p2 * v[2]) / (p1 + p2 + 1e-6)
+    torch.testing.assert_close(out[0], expect)
+
+
+def test_permutation_invariance():
+    q, k, v = _rand(20, 4, 8, 4)
+    g = torch.Generator().manual_seed(5)
+    ei = torch.randint(0, 20, (2, 90), generator=g)
+    perm = torch.randperm(90, generator=g)
+    a = sa.graphormer_sparse_attention(k, q, v, ei)
+    b = sa.graphormer_sparse_attention(k, q, v, ei[:, perm])
+    torch.testing.assert_close(a, b)
+
+
+def test_gradcheck_float64():
+    q, k, v = _rand(6, 2, 4, 6)
+    ei = torch.tensor([[0, 1, 2, 3, 4, 5, 1, 2], [1, 1, 1, 2, 2, 3, 5, 5]])
+    bias = torch.randn(6, 6, 2, dtype=torch.float64)
+    for t in (q, k, v, bias):
+        t.requires_grad_(True)
+    assert torch.autograd.gradcheck(lambda k_, q_, v_, b_: sa.graphormer_sparse_attention(k_, q_, v_, ei, b_),
+                                    (k, q, v, bias))
+
+
+@pytest.mark.parametrize("with_bias,with_mask", [(False, False), (True, False), (False, True)])
+def test_closed_form_backward_matches_autograd(with_bias, with_mask):
+    S, H, hn, E = 30, 4, 8, 200
+    q, k, v = _rand(S, H, hn, 7, mult=1.5)        # some scores hit the clamp
+    g = torch.Generator().manual_seed(8)
+    ei = torch.randint(0, S, (2, E), generator=g)
+    bias = torch.randn(E, H, generator=g, dtype=torch.float64) if with_bias else None
+    factor = ((torch.rand(E, H, generator=g) > 0.5).double() * 2.0) if with_mask else None
+    dout = torch.randn(S, H, hn, generator=g, dtype=torch.float64)
+    qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+    bb = bias.clone().requires_grad_(True) if bias is not None else None
+    out, Z = sa.attention_forward_stats(kk, qq, vv, ei, bb, factor)
+    out.backward(dout)
+    dq, dk, dv, dbias = sa.attention_backward_closed_form(k, q, v, ei, out.detach(), Z.detach(), dout, bias, factor)
+    torch.testing.assert_close(dq, qq.grad)
+    torch.testing.assert_close(dk, kk.grad)
+    torch.testing.assert_close(dv, vv.grad)
+    if with_bias:
+        torch.testing.assert_close(dbias, bb.grad)
+
+
+def test_stats_forward_equals_reference_forward():
+    q, k, v = _rand(25, 4, 8, 9)
+    g = torch.Generator().manual_seed(10)
+    ei = torch.randint(0, 25, (2, 120), generator=g)
+    out, _ = sa.attention_forward_stats(k, q, v, ei)
+    torch.testing.assert_close(out, sa.graphormer_sparse_attention(k, q, v, ei))
+
+
+def test_gps_mask_equals_factor_form():
+    q, k, v = _rand(25, 4, 8, 11)
+    g = torch.Generator().manual_seed(12)
+    ei = torch.randint(0, 25, (2, 120), generator=g)
+    keep = torch.rand(120, 4, generator=g) > 0.5
+    a = sa.gps_sparse_attention(q, k, v, ei, keep, 2.0)
+    b, _ = sa.attention_forward_stats(k, q, v, ei, None, keep.double() * 2.0)
+    torch.testing.assert_close(a, b)
+    torch.testing.assert_close(sa.gps_sparse_attention(q, k, v, ei), sa.graphormer_sparse_attention(k, q, v, ei))
