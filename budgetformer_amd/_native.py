@@ -1,0 +1,147 @@
+"""ctypes binding of the HIP library's C ABI (include/budgetformer_hip.h).
+
+This module is the only place that touches the shared library. Loading fails
+loudly when the library has not been built: there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+from . import build as _build
+
+_HEADER = os.path.join(_build.ROOT, "include", "budgetformer_hip.h")
+
+BF_OK, BF_ERR_INVALID, BF_ERR_UNSUPPORTED, BF_ERR_HIP = 0, 1, 2, 3
+BF_DTYPE_F32, BF_DTYPE_BF16 = 0, 1
+
+i32, i64, u64, sz = C.c_int32, C.c_int64, C.c_uint64, C.c_size_t
+vp = C.c_void_p
+P_i32 = vp  # device pointers are passed as plain addresses
+P_i64 = vp
+P_f32 = vp
+
+
+class AttnIndex(C.Structure):
+    """Mirror of ``struct bf_attn_index``."""
+    _fields_ = [
+        ("n_q", i64), ("n_kv", i64), ("nnz", i64),
+        ("qptr", vp), ("kv", vp), ("kptr", vp), ("kq", vp), ("ke", vp),
+        ("chunk", i32), ("q_cap", i32),
+        ("q_nitems", vp), ("q_item_off", vp), ("q_item_row", vp), ("q_total", vp),
+        ("k_cap", i32),
+        ("k_nitems", vp), ("k_item_off", vp), ("k_item_row", vp), ("k_total", vp),
+    ]
+
+
+# name -> (restype, argtypes)
+_SIGS = {
+    "bf_version": (C.c_int, []),
+    "bf_last_error": (C.c_char_p, []),
+    "bf_prof_enable": (C.c_int, [i32]),
+    "bf_prof_reset": (C.c_int, []),
+    "bf_prof_collect": (C.c_int, []),
+    "bf_prof_count": (i32, []),
+    "bf_prof_get": (C.c_int, [i32, C.POINTER(C.c_char_p), C.POINTER(C.c_double), C.POINTER(i64)]),
+    "bf_random_walk": (C.c_int, [P_i64, P_i32, i64, i64, i64, i32, i32, P_f32, u64, u64, P_i64, vp]),
+    "bf_walk_uniforms": (C.c_int, [i64, i64, i32, i32, u64, u64, P_f32, vp]),
+    "bf_rw_select": (C.c_int, [P_i64, P_i32, i64, i64, i64, i32, i32, i32, i64, P_f32, u64, u64, P_i32, P_i32, vp]),
+    "bf_real_select_merge": (C.c_int, [P_i64, P_i32, i64, i64, i64, i32, i64, P_i32, P_i32, i32, i32, P_i32, i32,
+                                       P_i32, vp]),
+    "bf_build_edge_table_workspace_size": (C.c_int, [i64, i32, C.POINTER(sz)]),
+    "bf_build_edge_table": (C.c_int, [P_i64, P_i32, P_i64, P_i32, i64, i64, i64, i64, i32, i32, i32, i32, i64,
+                                      P_f32, u64, u64, P_i32, P_i32, vp, sz, vp]),
+    "bf_table_csr_nnz": (C.c_int, [P_i32, i64, i32, C.POINTER(i64), vp, sz, vp]),
+    "bf_table_to_csr": (C.c_int, [P_i32, P_i32, i64, i32, i32, P_i64, P_i32, vp, sz, vp]),
+    "bf_scan_workspace_size": (C.c_int, [i64, C.POINTER(sz)]),
+    "bf_coo_to_csr_workspace_size": (C.c_int, [i64, i64, C.POINTER(sz)]),
+    "bf_coo_to_csr": (C.c_int, [P_i64, P_i64, i64, i64, i64, P_i64, P_i32, vp, sz, vp]),
+    "bf_reverse_index_workspace_size": (C.c_int, [i64, i64, C.POINTER(sz)]),
+    "bf_reverse_index": (C.c_int, [P_i64, P_i32, i64, i64, i64, P_i64, P_i32, P_i32, vp, sz, vp]),
+    "bf_expand_rows": (C.c_int, [P_i64, i64, i64, P_i64, vp]),
+    "bf_split_capacity": (i64, [i64, i32]),
+    "bf_split_plan_workspace_size": (C.c_int, [i64, C.POINTER(sz)]),
+    "bf_split_plan": (C.c_int, [P_i64, i64, i32, P_i32, P_i32, P_i32, i64, P_i32, vp, sz, vp]),
+    "bf_attn_partials_floats": (i64, [C.POINTER(AttnIndex), i32, i32]),
+    "bf_attn_fwd": (C.c_int, [C.POINTER(AttnIndex), i32, i32, i32, vp, vp, vp, P_f32, P_f32, vp, P_f32, P_f32, vp]),
+    "bf_attn_bwd": (C.c_int, [C.POINTER(AttnIndex), i32, i32, i32, vp, vp, vp, P_f32, P_f32, vp, P_f32, vp,
+                              vp, vp, vp, P_f32, P_f32, P_f32, vp]),
+}
+
+_lib = None
+
+
+def header_functions() -> list:
+    """Names of every function the C header declares."""
+    text = open(_HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(bf_\w+)\s*\(", text)))
+
+
+def lib_path() -> str:
+    return _build.lib_path()
+
+
+def load():
+    """Load the HIP library (once). Raises if it was not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = lib_path()
+    if not os.path.exists(path):
+        raise RuntimeError(
+            f"budgetformer_amd: HIP library not found at {path}; build it with "
+            f"`python -m budgetformer_amd.build` (no CPU fallback exists)")
+    lib = C.CDLL(path)
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+class HipError(RuntimeError):
+    """A HIP runtime call or kernel launch inside the library failed."""
+
+
+def check(rc: int, what: str) -> None:
+    if rc == BF_OK:
+        return
+    msg = (load().bf_last_error() or b"").decode(errors="replace")
+    text = f"{what}: {msg}"
+    if rc == BF_ERR_INVALID:
+        raise ValueError(text)
+    if rc == BF_ERR_UNSUPPORTED:
+        raise NotImplementedError(text)
+    raise HipError(text)
+
+
+def call(name: str, *args) -> None:
+    check(getattr(load(), name)(*args), name)
+
+
+class KernelTimer:
+    """Per-kernel HIP-event timing inside the library (bf_prof_*)."""
+
+    def __enter__(self):
+        call("bf_prof_reset")
+        call("bf_prof_enable", 1)
+        return self
+
+    def __exit__(self, *exc):
+        call("bf_prof_enable", 0)
+        return False
+
+    @staticmethod
+    def stats() -> dict:
+        """{kernel name: (total_ms, launches)} of everything collected so far."""
+        lib = load()
+        call("bf_prof_collect")
+        out = {}
+        for i in range(lib.bf_prof_count()):
+            name, ms, n = C.c_char_p(), C.c_double(), i64()
+            call("bf_prof_get", i, C.byref(name), C.byref(ms), C.byref(n))
+            out[name.value.decode()] = (ms.value, n.value)
+        return out

@@ -1,0 +1,740 @@
+// Sparse edge attention, forward and backward, for gfx950.
+//
+// Semantics: models/graphormer_dist_node_level.py:215-263 (GT :215-262, GraphGPS
+// models/graphgps_dist_node_level.py:151-177 through the per-edge factor):
+//   a = clamp(sum_j k[s,h,j] * q[t,h,j] / sqrt(hn), -5, 5) [+ bias[e,h]]
+//   p = exp(a)   (no max subtraction; the clamp bounds it when bias is absent)
+//   Z[t,h] = sum_e p,  out[t,h,:] = sum_e p * f[e,h] * v[s,h,:] / (Z[t,h] + 1e-6)
+//
+// Work mapping. A row of D = H*hn activations is split across a group of
+// LPR = D/EPL lanes (EPL = elements per 16-byte load: 4 fp32 or 8 bf16), so a
+// 64-lane wavefront serves 64/LPR rows at once and every gather of a K/V/Q/dO
+// row is one fully coalesced dwordx4 per lane. Per-head dot products reduce
+// over LPH = hn/EPL lanes with xor shuffles. Rows (queries in the forward and
+// the dq pass, key/value nodes in the dk/dv pass) are walked sequentially by
+// their group, several edges per iteration so that their gathers overlap.
+// Rows longer than `chunk` (the Graphormer global token row, hub key/value
+// nodes) are cut into items by a split plan; items write float partials that
+// a reduce kernel sums in item order. Nothing uses atomics: results are
+// deterministic run to run.
+//
+// MFMA is not used: each score is an hn-long dot product of two gathered rows,
+// not a dense contraction, and the kernels are bound by gather bandwidth.
+#include "bf_common.h"
+
+namespace bf {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kUnroll = 4;
+constexpr float kEps = 1e-6f;
+constexpr float kClamp = 5.0f;
+
+struct Shape {
+  int D;          // H * hn
+  int H;
+  int lpr_log2;   // lanes per row (power of two)
+  int lph_log2;   // lanes per head (power of two)
+  int act_lanes;  // D / EPL lanes carry data; the rest of the group idles
+  float inv_scale;
+};
+
+struct GroupPos {
+  int g_lane;
+  int head;
+  int col0;
+  bool act;
+  bool lead;      // first lane of its head
+};
+
+template <typename T>
+__device__ __forceinline__ GroupPos group_pos(const Shape& sh) {
+  constexpr int V = Elem<T>::kPerVec;
+  GroupPos g;
+  g.g_lane = threadIdx.x & ((1 << sh.lpr_log2) - 1);
+  g.act = g.g_lane < sh.act_lanes;
+  g.head = g.act ? (g.g_lane >> sh.lph_log2) : 0;  // idle lanes never index past H
+  g.col0 = g.g_lane * V;
+  g.lead = g.act && ((g.g_lane & ((1 << sh.lph_log2) - 1)) == 0);
+  return g;
+}
+
+__device__ __forceinline__ int64_t group_index(const Shape& sh) {
+  return int64_t(blockIdx.x) * (kBlock >> sh.lpr_log2) + (threadIdx.x >> sh.lpr_log2);
+}
+
+template <typename T, int V>
+__device__ __forceinline__ void load_row(const T* base, int64_t row, int D, const GroupPos& g, float (&o)[V]) {
+  if (g.act) {
+    Elem<T>::load(base + row * D + g.col0, o);
+  } else {
+#pragma unroll
+    for (int i = 0; i < V; ++i) o[i] = 0.f;
+  }
+}
+
+// ------------------------------------------------------------------ forward
+// Accumulates sum_e p*f*v (acc) and sum_e p (z) over entries [beg, end) of one row.
+template <typename T>
+__device__ __forceinline__ void fwd_segment(const T* __restrict__ k, const T* __restrict__ v,
+                                            const int32_t* __restrict__ kv,
+                                            const float* __restrict__ bias,
+                                            const float* __restrict__ factor,
+                                            int64_t beg, int64_t end, const Shape& sh,
+                                            const GroupPos& g,
+                                            const float (&qv)[Elem<T>::kPerVec],
+                                            float (&acc)[Elem<T>::kPerVec], float& z) {
+  constexpr int V = Elem<T>::kPerVec;
+  const int lph = 1 << sh.lph_log2;
+  for (int64_t e0 = beg; e0 < end; e0 += kUnroll) {
+    int s[kUnroll];
+    bool ok[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      ok[u] = e0 + u < end;
+      s[u] = ok[u] ? kv[e0 + u] : 0;
+    }
+    float kk[kUnroll][V], vv[kUnroll][V];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      if (ok[u] && g.act) {
+        Elem<T>::load(k + int64_t(s[u]) * sh.D + g.col0, kk[u]);
+        Elem<T>::load(v + int64_t(s[u]) * sh.D + g.col0, vv[u]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < V; ++i) kk[u][i] = vv[u][i] = 0.f;
+      }
+    }
+    float d[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      float t = 0.f;
+#pragma unroll
+      for (int i = 0; i < V; ++i) t += (kk[u][i] * qv[i]) * sh.inv_scale;
+      d[u] = t;
+    }
+    for (int o = 1; o < lph; o <<= 1) {
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) d[u] += __shfl_xor(d[u], o, 64);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      if (!ok[u]) continue;
+      const int64_t e = e0 + u;
+      float a = fminf(fmaxf(d[u], -kClamp), kClamp);
+      if (bias) a += bias[e * sh.H + g.head];
+      const float p = expf(a);
+      const float w = factor ? p * factor[e * sh.H + g.head] : p;
+#pragma unroll
+      for (int i = 0; i < V; ++i) acc[i] += w * vv[u][i];
+      z += p;
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void attn_fwd_rows_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    const int64_t* __restrict__ qptr, const int32_t* __restrict__ kv,
+    const float* __restrict__ bias, const float* __restrict__ factor,
+    T* __restrict__ out, float* __restrict__ Z, int64_t n_q, Shape sh, int chunk) {
+  constexpr int V = Elem<T>::kPerVec;
+  const int64_t row = group_index(sh);
+  if (row >= n_q) return;
+  const int64_t beg = qptr[row], end = qptr[row + 1];
+  if (end - beg > chunk) return;  // split row: items + reduce write it
+  const GroupPos g = group_pos<T>(sh);
+  float qv[V], acc[V];
+  load_row<T, V>(q, row, sh.D, g, qv);
+#pragma unroll
+  for (int i = 0; i < V; ++i) acc[i] = 0.f;
+  float z = 0.f;
+  fwd_segment<T>(k, v, kv, bias, factor, beg, end, sh, g, qv, acc, z);
+  if (g.act) {
+    const float den = z + kEps;
+    float o[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) o[i] = acc[i] / den;
+    Elem<T>::store(out + row * sh.D + g.col0, o);
+    if (g.lead) Z[row * sh.H + g.head] = z;
+  }
+}
+
+struct Items {
+  const int64_t* ptr;
+  const int32_t* item_off;
+  const int32_t* item_row;
+  const int32_t* nitems;
+  const int32_t* total;
+  int chunk;
+  int stride;     // floats per partial record
+};
+
+// Resolves a split item to (row, beg, end); false if past the plan's end.
+__device__ __forceinline__ bool item_range(const Items& it, int64_t item, int& row, int& j,
+                                           int64_t& beg, int64_t& end) {
+  if (item >= *it.total) return false;
+  row = it.item_row[item];
+  j = int(item - it.item_off[row]);
+  const int64_t rb = it.ptr[row], re = it.ptr[row + 1];
+  beg = rb + int64_t(j) * it.chunk;
+  end = min(beg + it.chunk, re);
+  return true;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void attn_fwd_items_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    const int32_t* __restrict__ kv, const float* __restrict__ bias,
+    const float* __restrict__ factor, float* __restrict__ partials, Items it, Shape sh) {
+  constexpr int V = Elem<T>::kPerVec;
+  const int64_t item = group_index(sh);
+  int row, j;
+  int64_t beg, end;
+  if (!item_range(it, item, row, j, beg, end)) return;
+  const GroupPos g = group_pos<T>(sh);
+  float qv[V], acc[V];
+  load_row<T, V>(q, row, sh.D, g, qv);
+#pragma unroll
+  for (int i = 0; i < V; ++i) acc[i] = 0.f;
+  float z = 0.f;
+  fwd_segment<T>(k, v, kv, bias, factor, beg, end, sh, g, qv, acc, z);
+  float* rec = partials + item * it.stride;
+  if (g.act) {
+#pragma unroll
+    for (int i = 0; i < V; ++i) rec[g.col0 + i] = acc[i];
+    if (g.lead) rec[sh.D + g.head] = z;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void attn_fwd_reduce_kernel(
+    const float* __restrict__ partials, T* __restrict__ out, float* __restrict__ Z, Items it, Shape sh) {
+  constexpr int V = Elem<T>::kPerVec;
+  const int64_t item = group_index(sh);
+  int row, j;
+  int64_t beg, end;
+  if (!item_range(it, item, row, j, beg, end) || j != 0) return;
+  const GroupPos g = group_pos<T>(sh);
+  if (!g.act) return;
+  const int n = it.nitems[row];
+  float acc[V];
+  float z = 0.f;
+#pragma unroll
+  for (int i = 0; i < V; ++i) acc[i] = 0.f;
+  for (int m = 0; m < n; ++m) {
+    const float* rec = partials + (item + m) * it.stride;
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] += rec[g.col0 + i];
+    z += rec[sh.D + g.head];
+  }
+  const float den = z + kEps;
+  float o[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) o[i] = acc[i] / den;
+  Elem<T>::store(out + int64_t(row) * sh.D + g.col0, o);
+  if (g.lead) Z[int64_t(row) * sh.H + g.head] = z;
+}
+
+// ------------------------------------------------------------------ backward, query-major (dq)
+// Per-row constants of the backward: D' = Z + eps and Delta = sum_j dO*out per head.
+struct RowGrad {
+  float dprime;
+  float delta;
+};
+
+template <typename T>
+__device__ __forceinline__ RowGrad row_grad(const T* __restrict__ out, const T* __restrict__ dout,
+                                            const float* __restrict__ Z, int64_t row, const Shape& sh,
+                                            const GroupPos& g, float (&gv)[Elem<T>::kPerVec]) {
+  constexpr int V = Elem<T>::kPerVec;
+  float ov[V];
+  load_row<T, V>(dout, row, sh.D, g, gv);
+  load_row<T, V>(out, row, sh.D, g, ov);
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < V; ++i) t += gv[i] * ov[i];
+  RowGrad r;
+  r.delta = group_sum(t, 1 << sh.lph_log2);
+  r.dprime = (g.act ? Z[row * sh.H + g.head] : 0.f) + kEps;
+  return r;
+}
+
+// dq contributions of entries [beg, end) of one query row; writes dbias per entry.
+template <typename T>
+__device__ __forceinline__ void dq_segment(const T* __restrict__ k, const T* __restrict__ v,
+                                           const int32_t* __restrict__ kv,
+                                           const float* __restrict__ bias,
+                                           const float* __restrict__ factor,
+                                           float* __restrict__ dbias, int64_t beg, int64_t end,
+                                           const Shape& sh, const GroupPos& g, const RowGrad& rg,
+                                           const float (&qv)[Elem<T>::kPerVec],
+                                           const float (&gv)[Elem<T>::kPerVec],
+                                           float (&dq)[Elem<T>::kPerVec]) {
+  constexpr int V = Elem<T>::kPerVec;
+  const int lph = 1 << sh.lph_log2;
+  const float gz = -rg.delta / rg.dprime;
+  for (int64_t e0 = beg; e0 < end; e0 += kUnroll) {
+    int s[kUnroll];
+    bool ok[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      ok[u] = e0 + u < end;
+      s[u] = ok[u] ? kv[e0 + u] : 0;
+    }
+    float kk[kUnroll][V], vv[kUnroll][V];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      if (ok[u] && g.act) {
+        Elem<T>::load(k + int64_t(s[u]) * sh.D + g.col0, kk[u]);
+        Elem<T>::load(v + int64_t(s[u]) * sh.D + g.col0, vv[u]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < V; ++i) kk[u][i] = vv[u][i] = 0.f;
+      }
+    }
+    float d[kUnroll], w[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      float t = 0.f, r = 0.f;
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        t += (kk[u][i] * qv[i]) * sh.inv_scale;
+        r += gv[i] * vv[u][i];
+      }
+      d[u] = t;
+      w[u] = r;
+    }
+    for (int o = 1; o < lph; o <<= 1) {
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        d[u] += __shfl_xor(d[u], o, 64);
+        w[u] += __shfl_xor(w[u], o, 64);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      if (!ok[u]) continue;
+      const int64_t e = e0 + u;
+      const float apre = d[u];
+      float a = fminf(fmaxf(apre, -kClamp), kClamp);
+      if (bias) a += bias[e * sh.H + g.head];
+      const float p = expf(a);
+      const float f = factor ? factor[e * sh.H + g.head] : 1.f;
+      const float gb = (f * (w[u] / rg.dprime) + gz) * p;
+      if (dbias && g.lead) dbias[e * sh.H + g.head] = gb;
+      const float ga = (apre >= -kClamp && apre <= kClamp) ? gb : 0.f;
+#pragma unroll
+      for (int i = 0; i < V; ++i) dq[i] += (ga * kk[u][i]) * sh.inv_scale;
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void attn_bwd_q_rows_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    const int64_t* __restrict__ qptr, const int32_t* __restrict__ kv,
+    const float* __restrict__ bias, const float* __restrict__ factor,
+    const T* __restrict__ out, const float* __restrict__ Z, const T* __restrict__ dout,
+    T* __restrict__ dq, float* __restrict__ dbias, float* __restrict__ delta, int64_t n_q,
+    Shape sh, int chunk) {
+  constexpr int V = Elem<T>::kPerVec;
+  const int64_t row = group_index(sh);
+  if (row >= n_q) return;
+  const int64_t beg = qptr[row], end = qptr[row + 1];
+  if (end - beg > chunk) return;
+  const GroupPos g = group_pos<T>(sh);
+  float qv[V], gv[V], acc[V];
+  load_row<T, V>(q, row, sh.D, g, qv);
+  const RowGrad rg = row_grad<T>(out, dout, Z, row, sh, g, gv);
+#pragma unroll
+  for (int i = 0; i < V; ++i) acc[i] = 0.f;
+  dq_segment<T>(k, v, kv, bias, factor, dbias, beg, end, sh, g, rg, qv, gv, acc);
+  if (g.act) {
+    Elem<T>::store(dq + row * sh.D + g.col0, acc);
+    if (g.lead) delta[row * sh.H + g.head] = rg.delta;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void attn_bwd_q_items_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    const int32_t* __restrict__ kv, const float* __restrict__ bias,
+    const float* __restrict__ factor, const T* __restrict__ out, const float* __restrict__ Z,
+    const T* __restrict__ dout, float* __restrict__ dbias, float* __restrict__ delta,
+    float* __restrict__ partials, Items it, Shape sh) {
+  constexpr int V = Elem<T>::kPerVec;
+  const int64_t item = group_index(sh);
+  int row, j;
+  int64_t beg, end;
+  if (!item_range(it, item, row, j, beg, end)) return;
+  const GroupPos g = group_pos<T>(sh);
+  float qv[V], gv[V], acc[V];
+  load_row<T, V>(q, row, sh.D, g, qv);
+  const RowGrad rg = row_grad<T>(out, dout, Z, row, sh, g, gv);
+#pragma unroll
+  for (int i = 0; i < V; ++i) acc[i] = 0.f;
+  dq_segment<T>(k, v, kv, bias, factor, dbias, beg, end, sh, g, rg, qv, gv, acc);
+  if (g.act) {
+    float* rec = partials + item * it.stride;
+#pragma unroll
+    for (int i = 0; i < V; ++i) rec[g.col0 + i] = acc[i];
+    if (j == 0 && g.lead) delta[int64_t(row) * sh.H + g.head] = rg.delta;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void attn_bwd_q_reduce_kernel(
+    const float* __restrict__ partials, T* __restrict__ dq, Items it, Shape sh) {
+  constexpr int V = Elem<T>::kPerVec;
+  const int64_t item = group_index(sh);
+  int row, j;
+  int64_t beg, end;
+  if (!item_range(it, item, row, j, beg, end) || j != 0) return;
+  const GroupPos g = group_pos<T>(sh);
+  if (!g.act) return;
+  const int n = it.nitems[row];
+  float acc[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) acc[i] = 0.f;
+  for (int m = 0; m < n; ++m) {
+    const float* rec = partials + (item + m) * it.stride;
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] += rec[g.col0 + i];
+  }
+  Elem<T>::store(dq + int64_t(row) * sh.D + g.col0, acc);
+}
+
+// ------------------------------------------------------------------ backward, key-major (dk, dv)
+template <typename T>
+__device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __restrict__ dout,
+                                            const int32_t* __restrict__ kq,
+                                            const int32_t* __restrict__ ke,
+                                            const float* __restrict__ bias,
+                                            const float* __restrict__ factor,
+                                            const float* __restrict__ Z,
+                                            const float* __restrict__ delta, int64_t beg,
+                                            int64_t end, const Shape& sh, const GroupPos& g,
+                                            const float (&kk)[Elem<T>::kPerVec],
+                                            const float (&vv)[Elem<T>::kPerVec],
+                                            float (&dk)[Elem<T>::kPerVec],
+                                            float (&dv)[Elem<T>::kPerVec]) {
+  constexpr int V = Elem<T>::kPerVec;
+  const int lph = 1 << sh.lph_log2;
+  const bool need_e = bias != nullptr || factor != nullptr;
+  for (int64_t i0 = beg; i0 < end; i0 += kUnroll) {
+    int t[kUnroll];
+    bool ok[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      ok[u] = i0 + u < end;
+      t[u] = ok[u] ? kq[i0 + u] : 0;
+    }
+    float qq[kUnroll][V], gg[kUnroll][V], zz[kUnroll], dl[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      if (ok[u] && g.act) {
+        Elem<T>::load(q + int64_t(t[u]) * sh.D + g.col0, qq[u]);
+        Elem<T>::load(dout + int64_t(t[u]) * sh.D + g.col0, gg[u]);
+        zz[u] = Z[int64_t(t[u]) * sh.H + g.head];
+        dl[u] = delta[int64_t(t[u]) * sh.H + g.head];
+      } else {
+#pragma unroll
+        for (int i = 0; i < V; ++i) qq[u][i] = gg[u][i] = 0.f;
+        zz[u] = 0.f;
+        dl[u] = 0.f;
+      }
+    }
+    float d[kUnroll], w[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      float a = 0.f, r = 0.f;
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        a += (kk[i] * qq[u][i]) * sh.inv_scale;
+        r += gg[u][i] * vv[i];
+      }
+      d[u] = a;
+      w[u] = r;
+    }
+    for (int o = 1; o < lph; o <<= 1) {
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        d[u] += __shfl_xor(d[u], o, 64);
+        w[u] += __shfl_xor(w[u], o, 64);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      if (!ok[u]) continue;
+      const int64_t e = need_e ? int64_t(ke[i0 + u]) : 0;
+      const float apre = d[u];
+      float a = fminf(fmaxf(apre, -kClamp), kClamp);
+      if (bias) a += bias[e * sh.H + g.head];
+      const float p = expf(a);
+      const float f = factor ? factor[e * sh.H + g.head] : 1.f;
+      const float dprime = zz[u] + kEps;
+      const float gb = (f * (w[u] / dprime) - dl[u] / dprime) * p;
+      const float ga = (apre >= -kClamp && apre <= kClamp) ? gb : 0.f;
+      const float pf = (p * f) / dprime;
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        dv[i] += pf * gg[u][i];
+        dk[i] += (ga * qq[u][i]) * sh.inv_scale;
+      }
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void attn_bwd_kv_rows_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    const int64_t* __restrict__ kptr, const int32_t* __restrict__ kq,
+    const int32_t* __restrict__ ke, const float* __restrict__ bias,
+    const float* __restrict__ factor, const float* __restrict__ Z,
+    const T* __restrict__ dout, const float* __restrict__ delta, T* __restrict__ dk,
+    T* __restrict__ dv, int64_t n_kv, Shape sh, int chunk) {
+  constexpr int V = Elem<T>::kPerVec;
+  const int64_t row = group_index(sh);
+  if (row >= n_kv) return;
+  const int64_t beg = kptr[row], end = kptr[row + 1];
+  if (end - beg > chunk) return;
+  const GroupPos g = group_pos<T>(sh);
+  float kk[V], vv[V], ak[V], av[V];
+  load_row<T, V>(k, row, sh.D, g, kk);
+  load_row<T, V>(v, row, sh.D, g, vv);
+#pragma unroll
+  for (int i = 0; i < V; ++i) ak[i] = av[i] = 0.f;
+  dkv_segment<T>(q, dout, kq, ke, bias, factor, Z, delta, beg, end, sh, g, kk, vv, ak, av);
+  if (g.act) {
+    Elem<T>::store(dk + row * sh.D + g.col0, ak);
+    Elem<T>::store(dv + row * sh.D + g.col0, av);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void attn_bwd_kv_items_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    const int32_t* __restrict__ kq, const int32_t* __restrict__ ke,
+    const float* __restrict__ bias, const float* __restrict__ factor,
+    const float* __restrict__ Z, const T* __restrict__ dout, const float* __restrict__ delta,
+    float* __restrict__ partials, Items it, Shape sh) {
+  constexpr int V = Elem<T>::kPerVec;
+  const int64_t item = group_index(sh);
+  int row, j;
+  int64_t beg, end;
+  if (!item_range(it, item, row, j, beg, end)) return;
+  const GroupPos g = group_pos<T>(sh);
+  float kk[V], vv[V], ak[V], av[V];
+  load_row<T, V>(k, row, sh.D, g, kk);
+  load_row<T, V>(v, row, sh.D, g, vv);
+#pragma unroll
+  for (int i = 0; i < V; ++i) ak[i] = av[i] = 0.f;
+  dkv_segment<T>(q, dout, kq, ke, bias, factor, Z, delta, beg, end, sh, g, kk, vv, ak, av);
+  if (g.act) {
+    float* rec = partials + item * it.stride;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      rec[g.col0 + i] = ak[i];
+      rec[sh.D + g.col0 + i] = av[i];
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void attn_bwd_kv_reduce_kernel(
+    const float* __restrict__ partials, T* __restrict__ dk, T* __restrict__ dv, Items it, Shape sh) {
+  constexpr int V = Elem<T>::kPerVec;
+  const int64_t item = group_index(sh);
+  int row, j;
+  int64_t beg, end;
+  if (!item_range(it, item, row, j, beg, end) || j != 0) return;
+  const GroupPos g = group_pos<T>(sh);
+  if (!g.act) return;
+  const int n = it.nitems[row];
+  float ak[V], av[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) ak[i] = av[i] = 0.f;
+  for (int m = 0; m < n; ++m) {
+    const float* rec = partials + (item + m) * it.stride;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      ak[i] += rec[g.col0 + i];
+      av[i] += rec[sh.D + g.col0 + i];
+    }
+  }
+  Elem<T>::store(dk + int64_t(row) * sh.D + g.col0, ak);
+  Elem<T>::store(dv + int64_t(row) * sh.D + g.col0, av);
+}
+
+// ------------------------------------------------------------------ host side
+int make_shape(int32_t dtype, int32_t H, int32_t hn, Shape& sh) {
+  BF_CHECK_ARG(dtype == BF_DTYPE_F32 || dtype == BF_DTYPE_BF16, "attention: unknown dtype %d", dtype);
+  BF_CHECK_ARG(H > 0 && hn > 0, "attention: num_heads=%d head_dim=%d must be positive", H, hn);
+  const int V = dtype == BF_DTYPE_F32 ? Elem<float>::kPerVec : Elem<uint16_t>::kPerVec;
+  if (hn % V != 0 || !is_pow2(hn / V)) {
+    set_error("attention: head_dim %d unsupported for %s (needs head_dim/%d a power of two)", hn,
+              dtype == BF_DTYPE_F32 ? "float32" : "bfloat16", V);
+    return BF_ERR_UNSUPPORTED;
+  }
+  const int D = H * hn;
+  const int lanes = D / V;
+  if (lanes > 64) {
+    set_error("attention: row width %d elements exceeds one wavefront (%d lanes x %d)", D, 64, V);
+    return BF_ERR_UNSUPPORTED;
+  }
+  int lpr = 1;
+  while (lpr < lanes) lpr <<= 1;
+  sh.D = D;
+  sh.H = H;
+  sh.lpr_log2 = ilog2(lpr);
+  sh.lph_log2 = ilog2(hn / V);
+  sh.act_lanes = lanes;
+  sh.inv_scale = 1.0f / sqrtf(float(hn));
+  return BF_OK;
+}
+
+int check_index(const bf_attn_index* idx, bool backward) {
+  BF_CHECK_ARG(idx != nullptr, "attention: index is NULL");
+  BF_CHECK_ARG(idx->n_q >= 0 && idx->n_kv >= 0 && idx->nnz >= 0, "attention: negative sizes");
+  BF_CHECK_ARG(idx->n_q < (int64_t(1) << 31) && idx->n_kv < (int64_t(1) << 31) &&
+                   idx->nnz < (int64_t(1) << 31),
+               "attention: sizes must fit int32 ids");
+  BF_CHECK_ARG(idx->chunk >= 1, "attention: chunk must be >= 1");
+  BF_CHECK_ARG(idx->qptr && (idx->kv || idx->nnz == 0), "attention: qptr/kv missing");
+  BF_CHECK_ARG(idx->q_nitems && idx->q_item_off && idx->q_item_row && idx->q_total,
+               "attention: query-side split plan missing");
+  if (backward) {
+    BF_CHECK_ARG(idx->kptr && ((idx->kq && idx->ke) || idx->nnz == 0), "attention: reverse index missing");
+    BF_CHECK_ARG(idx->k_nitems && idx->k_item_off && idx->k_item_row && idx->k_total,
+                 "attention: key-side split plan missing");
+  }
+  return BF_OK;
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline unsigned grid_for(int64_t rows, const Shape& sh) {
+  const int64_t per_block = kBlock >> sh.lpr_log2;
+  return unsigned(ceil_div(rows, per_block));
+}
+
+template <typename T>
+int fwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const void* k, const void* v,
+             const float* bias, const float* factor, void* out, float* Z, float* partials,
+             hipStream_t st) {
+  const T* Q = static_cast<const T*>(q);
+  const T* K = static_cast<const T*>(k);
+  const T* Vv = static_cast<const T*>(v);
+  T* O = static_cast<T*>(out);
+  if (idx->n_q > 0) {
+    BF_LAUNCH("attn_fwd_rows_kernel", attn_fwd_rows_kernel<T>, dim3(grid_for(idx->n_q, sh)), dim3(kBlock), 0, st,
+                       Q, K, Vv, idx->qptr, idx->kv, bias, factor, O, Z, idx->n_q, sh, idx->chunk);
+    BF_CHECK_LAUNCH();
+  }
+  if (idx->q_cap > 0) {
+    Items it{idx->qptr, idx->q_item_off, idx->q_item_row, idx->q_nitems, idx->q_total, idx->chunk,
+             2 * sh.D + sh.H};
+    BF_LAUNCH("attn_fwd_items_kernel", attn_fwd_items_kernel<T>, dim3(grid_for(idx->q_cap, sh)), dim3(kBlock), 0, st,
+                       Q, K, Vv, idx->kv, bias, factor, partials, it, sh);
+    BF_CHECK_LAUNCH();
+    BF_LAUNCH("attn_fwd_reduce_kernel", attn_fwd_reduce_kernel<T>, dim3(grid_for(idx->q_cap, sh)), dim3(kBlock), 0, st,
+                       partials, O, Z, it, sh);
+    BF_CHECK_LAUNCH();
+  }
+  return BF_OK;
+}
+
+template <typename T>
+int bwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const void* k, const void* v,
+             const float* bias, const float* factor, const void* out, const float* Z,
+             const void* dout, void* dq, void* dk, void* dv, float* dbias, float* delta,
+             float* partials, hipStream_t st) {
+  const T* Q = static_cast<const T*>(q);
+  const T* K = static_cast<const T*>(k);
+  const T* Vv = static_cast<const T*>(v);
+  const T* O = static_cast<const T*>(out);
+  const T* dO = static_cast<const T*>(dout);
+  const int stride = 2 * sh.D + sh.H;
+  if (idx->n_q > 0) {
+    BF_LAUNCH("attn_bwd_q_rows_kernel", attn_bwd_q_rows_kernel<T>, dim3(grid_for(idx->n_q, sh)), dim3(kBlock), 0, st,
+                       Q, K, Vv, idx->qptr, idx->kv, bias, factor, O, Z, dO, static_cast<T*>(dq),
+                       dbias, delta, idx->n_q, sh, idx->chunk);
+    BF_CHECK_LAUNCH();
+  }
+  if (idx->q_cap > 0) {
+    Items it{idx->qptr, idx->q_item_off, idx->q_item_row, idx->q_nitems, idx->q_total, idx->chunk, stride};
+    BF_LAUNCH("attn_bwd_q_items_kernel", attn_bwd_q_items_kernel<T>, dim3(grid_for(idx->q_cap, sh)), dim3(kBlock), 0, st,
+                       Q, K, Vv, idx->kv, bias, factor, O, Z, dO, dbias, delta, partials, it, sh);
+    BF_CHECK_LAUNCH();
+    BF_LAUNCH("attn_bwd_q_reduce_kernel", attn_bwd_q_reduce_kernel<T>, dim3(grid_for(idx->q_cap, sh)), dim3(kBlock), 0, st,
+                       partials, static_cast<T*>(dq), it, sh);
+    BF_CHECK_LAUNCH();
+  }
+  if (idx->n_kv > 0) {
+    BF_LAUNCH("attn_bwd_kv_rows_kernel", attn_bwd_kv_rows_kernel<T>, dim3(grid_for(idx->n_kv, sh)), dim3(kBlock), 0, st,
+                       Q, K, Vv, idx->kptr, idx->kq, idx->ke, bias, factor, Z, dO, delta,
+                       static_cast<T*>(dk), static_cast<T*>(dv), idx->n_kv, sh, idx->chunk);
+    BF_CHECK_LAUNCH();
+  }
+  if (idx->k_cap > 0) {
+    Items it{idx->kptr, idx->k_item_off, idx->k_item_row, idx->k_nitems, idx->k_total, idx->chunk, stride};
+    BF_LAUNCH("attn_bwd_kv_items_kernel", attn_bwd_kv_items_kernel<T>, dim3(grid_for(idx->k_cap, sh)), dim3(kBlock), 0, st,
+                       Q, K, Vv, idx->kq, idx->ke, bias, factor, Z, dO, delta, partials, it, sh);
+    BF_CHECK_LAUNCH();
+    BF_LAUNCH("attn_bwd_kv_reduce_kernel", attn_bwd_kv_reduce_kernel<T>, dim3(grid_for(idx->k_cap, sh)), dim3(kBlock), 0, st,
+                       partials, static_cast<T*>(dk), static_cast<T*>(dv), it, sh);
+    BF_CHECK_LAUNCH();
+  }
+  return BF_OK;
+}
+
+}  // namespace
+}  // namespace bf
+
+using namespace bf;
+
+extern "C" int64_t bf_attn_partials_floats(const bf_attn_index* idx, int32_t num_heads, int32_t head_dim) {
+  if (!idx) return 0;
+  const int64_t cap = idx->q_cap > idx->k_cap ? idx->q_cap : idx->k_cap;
+  const int64_t D = int64_t(num_heads) * head_dim;
+  return cap * (2 * D + num_heads);
+}
+
+extern "C" int bf_attn_fwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
+                           const void* q, const void* k, const void* v, const float* bias,
+                           const float* factor, void* out, float* Z, float* partials, void* stream) {
+  Shape sh;
+  int rc = make_shape(dtype, num_heads, head_dim, sh);
+  if (rc) return rc;
+  if ((rc = check_index(idx, false))) return rc;
+  BF_CHECK_ARG(q && k && v && out && Z, "attn_fwd: null tensor");
+  BF_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out),
+               "attn_fwd: q/k/v/out must be 16-byte aligned");
+  BF_CHECK_ARG(idx->q_cap == 0 || partials, "attn_fwd: partials buffer required for split rows");
+  if (dtype == BF_DTYPE_F32)
+    return fwd_impl<float>(idx, sh, q, k, v, bias, factor, out, Z, partials, as_stream(stream));
+  return fwd_impl<uint16_t>(idx, sh, q, k, v, bias, factor, out, Z, partials, as_stream(stream));
+}
+
+extern "C" int bf_attn_bwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
+                           const void* q, const void* k, const void* v, const float* bias,
+                           const float* factor, const void* out, const float* Z, const void* dout,
+                           void* dq, void* dk, void* dv, float* dbias, float* delta, float* partials,
+                           void* stream) {
+  Shape sh;
+  int rc = make_shape(dtype, num_heads, head_dim, sh);
+  if (rc) return rc;
+  if ((rc = check_index(idx, true))) return rc;
+  BF_CHECK_ARG(q && k && v && out && Z && dout && dq && dk && dv && delta, "attn_bwd: null tensor");
+  BF_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out) && aligned16(dout) &&
+                   aligned16(dq) && aligned16(dk) && aligned16(dv),
+               "attn_bwd: tensors must be 16-byte aligned");
+  BF_CHECK_ARG((idx->q_cap == 0 && idx->k_cap == 0) || partials,
+               "attn_bwd: partials buffer required for split rows");
+  if (dtype == BF_DTYPE_F32)
+    return bwd_impl<float>(idx, sh, q, k, v, bias, factor, out, Z, dout, dq, dk, dv, dbias, delta,
+                           partials, as_stream(stream));
+  return bwd_impl<uint16_t>(idx, sh, q, k, v, bias, factor, out, Z, dout, dq, dk, dv, dbias, delta,
+                            partials, as_stream(stream));
+}

@@ -1,0 +1,168 @@
+// Shared device/host helpers for the BudgetFormer MI355X (gfx950) kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdarg.h>
+
+#include "../../include/budgetformer_hip.h"
+
+namespace bf {
+
+// ---------------------------------------------------------------- errors
+void set_error(const char* fmt, ...);
+
+#define BF_CHECK_ARG(cond, ...)                         \
+  do {                                                  \
+    if (!(cond)) {                                      \
+      ::bf::set_error(__VA_ARGS__);                     \
+      return BF_ERR_INVALID;                            \
+    }                                                   \
+  } while (0)
+
+#define BF_CHECK_HIP(expr)                                                          \
+  do {                                                                              \
+    hipError_t _e = (expr);                                                         \
+    if (_e != hipSuccess) {                                                         \
+      ::bf::set_error("%s failed: %s (%s:%d)", #expr, hipGetErrorString(_e),        \
+                      __FILE__, __LINE__);                                          \
+      return BF_ERR_HIP;                                                            \
+    }                                                                               \
+  } while (0)
+
+#define BF_CHECK_LAUNCH() BF_CHECK_HIP(hipGetLastError())
+
+// Optional per-kernel timing (bf_prof_enable): an event pair around each launch.
+bool prof_enabled();
+void prof_begin(const char* name, hipStream_t st, int* token);
+void prof_end(int token, hipStream_t st);
+
+#define BF_LAUNCH(name, kern, grid, block, lds, st, ...)                 \
+  do {                                                                  \
+    int _bf_tok = -1;                                                   \
+    if (::bf::prof_enabled()) ::bf::prof_begin(name, st, &_bf_tok);     \
+    hipLaunchKernelGGL(kern, grid, block, lds, st, __VA_ARGS__);        \
+    if (_bf_tok >= 0) ::bf::prof_end(_bf_tok, st);                      \
+  } while (0)
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+__host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+inline bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
+
+inline int ilog2(int64_t x) {
+  int r = 0;
+  while ((int64_t(1) << (r + 1)) <= x) ++r;
+  return r;
+}
+
+// ---------------------------------------------------------------- bf16
+// bf16 stored as raw uint16 (upper half of an IEEE float).
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(uint32_t(h) << 16);
+}
+
+// Round-to-nearest-even float -> bf16 (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t x = __float_as_uint(f);
+  if ((x & 0x7fffffffu) > 0x7f800000u) return uint16_t((x >> 16) | 0x40u);
+  uint32_t lsb = (x >> 16) & 1u;
+  x += 0x7fffu + lsb;
+  return uint16_t(x >> 16);
+}
+
+// Element traits: each lane moves 16 bytes (one dwordx4) of a row.
+template <typename T> struct Elem;
+
+template <> struct Elem<float> {
+  static constexpr int kPerVec = 4;
+  __device__ __forceinline__ static void load(const float* p, float (&o)[4]) {
+    const float4 v = *reinterpret_cast<const float4*>(p);
+    o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+  }
+  __device__ __forceinline__ static void store(float* p, const float (&o)[4]) {
+    *reinterpret_cast<float4*>(p) = make_float4(o[0], o[1], o[2], o[3]);
+  }
+};
+
+template <> struct Elem<uint16_t> {
+  static constexpr int kPerVec = 8;
+  __device__ __forceinline__ static void load(const uint16_t* p, float (&o)[8]) {
+    const uint4 v = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o[2 * i] = __uint_as_float(w[i] << 16);
+      o[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+  __device__ __forceinline__ static void store(uint16_t* p, const float (&o)[8]) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = uint32_t(f32_to_bf16(o[2 * i])) | (uint32_t(f32_to_bf16(o[2 * i + 1])) << 16);
+    *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+};
+
+// Butterfly sum over aligned groups of `width` lanes (width a power of two <= 64).
+__device__ __forceinline__ float group_sum(float x, int width) {
+  for (int o = 1; o < width; o <<= 1) x += __shfl_xor(x, o, 64);
+  return x;
+}
+
+// ---------------------------------------------------------------- keys
+// (src*1103515245 + dst*214013 + c) mod 2^31 with c = seed*2654435761 + 12345,
+// computed as the low 31 bits of the uint32-wrapped sum (utils/fullgraph_sp_support.py:984-989).
+__host__ __device__ __forceinline__ uint32_t edge_key(uint32_t src, uint32_t dst, uint32_t c) {
+  return (src * 1103515245u + dst * 214013u + c) & 0x7fffffffu;
+}
+
+inline uint32_t key_const(int64_t seed) {
+  return uint32_t(uint64_t(seed) * 2654435761ull + 12345ull);
+}
+
+// ---------------------------------------------------------------- Philox4x32-10
+// Counter-based RNG of Salmon, Moraes, Dror, Shaw, "Parallel random numbers:
+// as easy as 1, 2, 3" (SC'11): 10 rounds of a 4x32 multiply-xor bijection with
+// a Weyl-sequence key schedule.
+struct U32x4 { uint32_t x, y, z, w; };
+
+__host__ __device__ __forceinline__ void mulhilo32(uint32_t a, uint32_t b, uint32_t& hi, uint32_t& lo) {
+  const uint64_t p = uint64_t(a) * uint64_t(b);
+  hi = uint32_t(p >> 32);
+  lo = uint32_t(p);
+}
+
+__host__ __device__ __forceinline__ U32x4 philox4x32_10(U32x4 c, uint32_t k0, uint32_t k1) {
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    uint32_t hi0, lo0, hi1, lo1;
+    mulhilo32(0xD2511F53u, c.x, hi0, lo0);
+    mulhilo32(0xCD9E8D57u, c.z, hi1, lo1);
+    c = U32x4{hi1 ^ c.y ^ k0, lo1, hi0 ^ c.w ^ k1, lo0};
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  return c;
+}
+
+// Uniform in [0, 1 - 2^-24]: top 24 bits times 2^-24 (exact in fp32).
+__host__ __device__ __forceinline__ float u24(uint32_t x) {
+  return float(x >> 8) * (1.0f / 16777216.0f);
+}
+
+// Uniform for walk `w`, step `l`: one Philox call serves 4 consecutive steps.
+// counter = (w_lo, w_hi, offset_lo + l/4, offset_hi), key = (seed_lo, seed_hi).
+__host__ __device__ __forceinline__ float walk_uniform(uint64_t seed, uint64_t offset, uint64_t w, int l) {
+  const uint64_t blk = offset + uint64_t(l >> 2);
+  U32x4 c{uint32_t(w), uint32_t(w >> 32), uint32_t(blk), uint32_t(blk >> 32)};
+  const U32x4 r = philox4x32_10(c, uint32_t(seed), uint32_t(seed >> 32));
+  const int j = l & 3;
+  const uint32_t x = j == 0 ? r.x : j == 1 ? r.y : j == 2 ? r.z : r.w;
+  return u24(x);
+}
+
+}  // namespace bf

@@ -1,0 +1,360 @@
+// Budgeted query-centric edge construction for gfx950.
+//
+// Reference chain (utils/fullgraph_sp_support.py:2943-3026 _build_merged_edges):
+//   real part: per dst, the k_real smallest key(src, dst, seed+17) among the
+//              graph edges into dst                          (:1312-1491, :1195-1228)
+//   RW part:   uniform walks from every node (torch_cluster / DGL, gt_sp/utils.py:
+//              1387-1473), hop pool (kv = walks[w,d], q = walks[w,0]) kept iff
+//              d == 1 or the walk moved (gt_sp/utils.py:1232-1248), then per q the
+//              k_rw smallest key(kv, q, seed+37)             (:1494-1517)
+//   merge:     coalesce (set union, src-major) when both parts are non-empty,
+//              pass-through otherwise                          (gt_sp/utils.py:877-887)
+//
+// MI355X design. Every RW pool entry of query q comes from q's own P walks, so
+// the pool is never materialised: one lane runs one walk (coalesced rowptr/col
+// gathers, Philox counter RNG or injected uniforms), the P lanes of a query
+// stage their P*L candidates in LDS and rank them there. The real-edge top-k
+// scans q's in-neighbour list with a 16-lane group (per-lane sorted register
+// lists, then k rounds of a group min), and the same group merges both parts
+// through LDS with a rank sort (dedup = first occurrence wins) into a
+// fixed-stride int32 table row. Keys are 31-bit, so (key << 32 | id) orders by
+// key and equal keys are the same pair: selection with multiplicity needs no
+// position tie-break.
+#include "bf_common.h"
+
+namespace bf {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr uint64_t kNone = ~uint64_t(0);
+
+__device__ __forceinline__ int64_t walk_step(const int64_t* __restrict__ rowptr,
+                                             const int32_t* __restrict__ col, int64_t cur, float u) {
+  const int64_t beg = rowptr[cur];
+  const int64_t deg = rowptr[cur + 1] - beg;
+  if (deg <= 0) return cur;                       // dead end: stay
+  int64_t idx = int64_t(u * float(deg));          // fp32 multiply (RNE), truncate
+  if (idx > deg - 1) idx = deg - 1;
+  return col[beg + idx];
+}
+
+__global__ __launch_bounds__(kThreads) void random_walk_kernel(
+    const int64_t* __restrict__ rowptr, const int32_t* __restrict__ col, int64_t q_lo, int64_t n_walks,
+    int P, int L, const float* __restrict__ u, uint64_t seed, uint64_t offset, int64_t* __restrict__ walks) {
+  const int64_t wl = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (wl >= n_walks) return;
+  const int64_t q = q_lo + wl / P;
+  const int64_t w = q * P + (wl % P);
+  int64_t cur = q;
+  int64_t* row = walks + wl * (L + 1);
+  row[0] = cur;
+  for (int l = 0; l < L; ++l) {
+    const float uu = u ? u[wl * L + l] : walk_uniform(seed, offset, uint64_t(w), l);
+    cur = walk_step(rowptr, col, cur, uu);
+    row[l + 1] = cur;
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void walk_uniforms_kernel(int64_t q_lo, int64_t n_walks, int P, int L,
+                                                                 uint64_t seed, uint64_t offset,
+                                                                 float* __restrict__ u) {
+  const int64_t wl = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (wl >= n_walks) return;
+  const int64_t w = (q_lo + wl / P) * P + (wl % P);
+  for (int l = 0; l < L; ++l) u[wl * L + l] = walk_uniform(seed, offset, uint64_t(w), l);
+}
+
+// One lane per walk; the P lanes of a query are adjacent. Candidates are staged
+// in LDS as (key << 32 | kv) (kNone = filtered step) and ranked by the P lanes.
+__global__ __launch_bounds__(kThreads) void rw_select_kernel(
+    const int64_t* __restrict__ rowptr, const int32_t* __restrict__ col, int64_t q_lo, int64_t n_q,
+    int P, int L, int K, uint32_t kc, const float* __restrict__ u, uint64_t seed, uint64_t offset,
+    int32_t* __restrict__ sel_kv, int32_t* __restrict__ sel_cnt) {
+  extern __shared__ uint64_t cand[];  // [kThreads * L]
+  const int qpb = kThreads / P;
+  const int tid = threadIdx.x;
+  const int ql = tid / P;
+  const int p = tid - ql * P;
+  const int64_t qi = int64_t(blockIdx.x) * qpb + ql;
+  const bool active = ql < qpb && qi < n_q;
+  if (active) {
+    const int64_t q = q_lo + qi;
+    const int64_t w = q * P + p;
+    const int64_t wl = qi * P + p;
+    int64_t cur = q;
+    for (int l = 0; l < L; ++l) {
+      const float uu = u ? u[wl * L + l] : walk_uniform(seed, offset, uint64_t(w), l);
+      const int64_t nxt = walk_step(rowptr, col, cur, uu);
+      const bool keep = (l == 0) || (nxt != cur);
+      cand[tid * L + l] = keep ? (uint64_t(edge_key(uint32_t(nxt), uint32_t(q), kc)) << 32) | uint32_t(nxt) : kNone;
+      cur = nxt;
+    }
+  }
+  __syncthreads();
+  if (!active) return;
+  const int M = P * L;
+  const uint64_t* c = cand + ql * M;
+  for (int i = p; i < M; i += P) {
+    const uint64_t ci = c[i];
+    if (ci == kNone) continue;
+    int rank = 0;
+    for (int j = 0; j < M; ++j) {
+      const uint64_t cj = c[j];
+      rank += (cj < ci) || (cj == ci && j < i);
+    }
+    if (rank < K) sel_kv[qi * K + rank] = int32_t(uint32_t(ci));
+  }
+  if (p == 0) {
+    int nv = 0;
+    for (int j = 0; j < M; ++j) nv += c[j] != kNone;
+    const int cnt = nv < K ? nv : K;
+    sel_cnt[qi] = cnt;
+    for (int r = cnt; r < K; ++r) sel_kv[qi * K + r] = -1;
+  }
+}
+
+constexpr int kGroup = 16;                  // lanes per query in the real-edge pass
+constexpr int kQPB = kThreads / kGroup;     // queries per block
+constexpr int kMaxRow = 64;                 // k_real + k_rw
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t x, int o) {
+  const uint32_t lo = __shfl_xor(uint32_t(x), o, 64);
+  const uint32_t hi = __shfl_xor(uint32_t(x >> 32), o, 64);
+  return (uint64_t(hi) << 32) | lo;
+}
+
+template <int KMAX>
+__global__ __launch_bounds__(kThreads) void real_select_merge_kernel(
+    const int64_t* __restrict__ in_ptr, const int32_t* __restrict__ in_src, int64_t q_lo, int64_t n_q,
+    int k_real, uint32_t kc, const int32_t* __restrict__ rw_kv, const int32_t* __restrict__ rw_cnt, int k_rw,
+    int dedup, int32_t* __restrict__ table, int width, int32_t* __restrict__ row_len) {
+  __shared__ int32_t lst[kQPB][kMaxRow];
+  __shared__ int32_t dupf[kQPB][kMaxRow];
+  const int gq = threadIdx.x / kGroup;
+  const int gl = threadIdx.x % kGroup;
+  const int64_t qi = int64_t(blockIdx.x) * kQPB + gq;
+  const bool active = qi < n_q;
+  int n_r = 0, n_w = 0;
+  if (active && k_real > 0) {
+    const int64_t q = q_lo + qi;
+    uint64_t lk[KMAX];
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) lk[j] = kNone;
+    const int64_t beg = in_ptr[q], end = in_ptr[q + 1];
+    for (int64_t i = beg + gl; i < end; i += kGroup) {
+      const uint32_t s = uint32_t(in_src[i]);
+      const uint64_t c = (uint64_t(edge_key(s, uint32_t(q), kc)) << 32) | s;
+      if (c < lk[KMAX - 1]) {
+#pragma unroll
+        for (int j = KMAX - 1; j > 0; --j) lk[j] = c < lk[j - 1] ? lk[j - 1] : (c < lk[j] ? c : lk[j]);
+        lk[0] = c < lk[0] ? c : lk[0];
+      }
+    }
+    const int lane = threadIdx.x & 63;
+    const int gbase = lane & ~(kGroup - 1);
+    for (int r = 0; r < k_real; ++r) {
+      const uint64_t h = lk[0];
+      uint64_t m = h;
+      for (int o = 1; o < kGroup; o <<= 1) {
+        const uint64_t y = shfl_xor_u64(m, o);
+        m = y < m ? y : m;
+      }
+      if (m == kNone) break;
+      const uint64_t bal = __ballot(h == m);
+      const uint64_t mine = (bal >> gbase) & ((uint64_t(1) << kGroup) - 1);
+      const int winner = __ffsll((unsigned long long)mine) - 1;
+      if (gl == winner) {
+#pragma unroll
+        for (int j = 0; j < KMAX - 1; ++j) lk[j] = lk[j + 1];
+        lk[KMAX - 1] = kNone;
+      }
+      if (gl == 0) lst[gq][r] = int32_t(uint32_t(m));
+      n_r = r + 1;
+    }
+  }
+  if (active && rw_kv != nullptr && k_rw > 0) {
+    n_w = rw_cnt[qi];
+    for (int i = gl; i < n_w; i += kGroup) lst[gq][n_r + i] = rw_kv[qi * k_rw + i];
+  }
+  __syncthreads();
+  const int n_tot = n_r + n_w;
+  if (active && dedup) {
+    for (int i = gl; i < n_tot; i += kGroup) {
+      const int32_t v = lst[gq][i];
+      int dup = 0;
+      for (int j = 0; j < i; ++j) dup |= lst[gq][j] == v;
+      dupf[gq][i] = dup;
+    }
+  }
+  __syncthreads();
+  if (!active) return;
+  int len = 0;
+  int32_t* out = table + qi * width;
+  for (int i = 0; i < n_tot; ++i) len += dedup ? !dupf[gq][i] : 1;
+  for (int i = gl; i < n_tot; i += kGroup) {
+    const int32_t v = lst[gq][i];
+    int rank = 0;
+    if (dedup) {
+      if (dupf[gq][i]) continue;
+      for (int j = 0; j < n_tot; ++j) rank += !dupf[gq][j] && lst[gq][j] < v;
+    } else {
+      for (int j = 0; j < n_tot; ++j) {
+        const int32_t w = lst[gq][j];
+        rank += (w < v) || (w == v && j < i);
+      }
+    }
+    out[rank] = v;
+  }
+  for (int c = len + gl; c < width; c += kGroup) out[c] = -1;
+  if (gl == 0) row_len[qi] = len;
+}
+
+int check_graph(const int64_t* ptr, const int32_t* idx, int64_t num_nodes, int64_t q_lo, int64_t n_q) {
+  BF_CHECK_ARG(ptr != nullptr, "edge build: row pointer is NULL");
+  BF_CHECK_ARG(num_nodes >= 0 && num_nodes < (int64_t(1) << 31), "edge build: num_nodes %lld outside int32 ids",
+               (long long)num_nodes);
+  BF_CHECK_ARG(q_lo >= 0 && n_q >= 0 && q_lo + n_q <= num_nodes, "edge build: query range [%lld,%lld) outside [0,%lld)",
+               (long long)q_lo, (long long)(q_lo + n_q), (long long)num_nodes);
+  (void)idx;
+  return BF_OK;
+}
+
+int launch_rw_select(const int64_t* rowptr, const int32_t* col, int64_t q_lo, int64_t n_q, int P, int L, int K,
+                     uint32_t kc, const float* u, uint64_t seed, uint64_t offset, int32_t* sel_kv,
+                     int32_t* sel_cnt, hipStream_t st) {
+  if (n_q == 0) return BF_OK;
+  const int qpb = kThreads / P;
+  const size_t lds = size_t(kThreads) * L * sizeof(uint64_t);
+  BF_LAUNCH("rw_select_kernel", rw_select_kernel, dim3(unsigned(ceil_div(n_q, qpb))), dim3(kThreads), lds, st, rowptr, col,
+                     q_lo, n_q, P, L, K, kc, u, seed, offset, sel_kv, sel_cnt);
+  BF_CHECK_LAUNCH();
+  return BF_OK;
+}
+
+int launch_real_merge(const int64_t* in_ptr, const int32_t* in_src, int64_t q_lo, int64_t n_q, int k_real,
+                      uint32_t kc, const int32_t* rw_kv, const int32_t* rw_cnt, int k_rw, int dedup,
+                      int32_t* table, int width, int32_t* row_len, hipStream_t st) {
+  if (n_q == 0) return BF_OK;
+  const dim3 grid(unsigned(ceil_div(n_q, kQPB)));
+#define BF_LAUNCH_MERGE(KM)                                                                              \
+  BF_LAUNCH("real_select_merge_kernel", real_select_merge_kernel<KM>, grid, dim3(kThreads), 0, st, in_ptr, in_src, q_lo, n_q, \
+                     k_real, kc, rw_kv, rw_cnt, k_rw, dedup, table, width, row_len)
+  if (k_real <= 4)
+    BF_LAUNCH_MERGE(4);
+  else if (k_real <= 8)
+    BF_LAUNCH_MERGE(8);
+  else if (k_real <= 16)
+    BF_LAUNCH_MERGE(16);
+  else
+    BF_LAUNCH_MERGE(32);
+#undef BF_LAUNCH_MERGE
+  BF_CHECK_LAUNCH();
+  return BF_OK;
+}
+
+inline size_t align_up(size_t x) { return (x + 255) & ~size_t(255); }
+
+}  // namespace
+}  // namespace bf
+
+using namespace bf;
+
+extern "C" int bf_random_walk(const int64_t* rowptr, const int32_t* col, int64_t num_nodes, int64_t q_lo,
+                              int64_t n_q, int32_t walks_per_node, int32_t walk_length, const float* u,
+                              uint64_t philox_seed, uint64_t philox_offset, int64_t* walks, void* stream) {
+  int rc = check_graph(rowptr, col, num_nodes, q_lo, n_q);
+  if (rc) return rc;
+  BF_CHECK_ARG(walks_per_node >= 1 && walk_length >= 1, "random_walk: P=%d L=%d must be >= 1", walks_per_node,
+               walk_length);
+  BF_CHECK_ARG(walks != nullptr || n_q == 0, "random_walk: walks is NULL");
+  const int64_t n_walks = n_q * walks_per_node;
+  if (n_walks == 0) return BF_OK;
+  BF_LAUNCH("random_walk_kernel", random_walk_kernel, dim3(unsigned(ceil_div(n_walks, kThreads))), dim3(kThreads), 0,
+                     as_stream(stream), rowptr, col, q_lo, n_walks, walks_per_node, walk_length, u, philox_seed,
+                     philox_offset, walks);
+  BF_CHECK_LAUNCH();
+  return BF_OK;
+}
+
+extern "C" int bf_walk_uniforms(int64_t q_lo, int64_t n_q, int32_t walks_per_node, int32_t walk_length,
+                                uint64_t philox_seed, uint64_t philox_offset, float* u, void* stream) {
+  BF_CHECK_ARG(q_lo >= 0 && n_q >= 0 && walks_per_node >= 1 && walk_length >= 1, "walk_uniforms: bad arguments");
+  const int64_t n_walks = n_q * walks_per_node;
+  if (n_walks == 0) return BF_OK;
+  BF_CHECK_ARG(u != nullptr, "walk_uniforms: u is NULL");
+  BF_LAUNCH("walk_uniforms_kernel", walk_uniforms_kernel, dim3(unsigned(ceil_div(n_walks, kThreads))), dim3(kThreads), 0,
+                     as_stream(stream), q_lo, n_walks, walks_per_node, walk_length, philox_seed, philox_offset, u);
+  BF_CHECK_LAUNCH();
+  return BF_OK;
+}
+
+extern "C" int bf_rw_select(const int64_t* rowptr, const int32_t* col, int64_t num_nodes, int64_t q_lo,
+                            int64_t n_q, int32_t walks_per_node, int32_t walk_length, int32_t k_rw,
+                            int64_t key_seed, const float* u, uint64_t philox_seed, uint64_t philox_offset,
+                            int32_t* sel_kv, int32_t* sel_cnt, void* stream) {
+  int rc = check_graph(rowptr, col, num_nodes, q_lo, n_q);
+  if (rc) return rc;
+  BF_CHECK_ARG(walks_per_node >= 1 && walks_per_node <= kThreads, "rw_select: walks_per_node %d outside [1,%d]",
+               walks_per_node, kThreads);
+  BF_CHECK_ARG(walk_length >= 1 && walk_length <= 32, "rw_select: walk_length %d outside [1,32]", walk_length);
+  BF_CHECK_ARG(walks_per_node * walk_length <= 64, "rw_select: P*L=%d exceeds 64", walks_per_node * walk_length);
+  BF_CHECK_ARG(k_rw >= 1 && k_rw <= 32, "rw_select: k_rw %d outside [1,32]", k_rw);
+  BF_CHECK_ARG((sel_kv && sel_cnt) || n_q == 0, "rw_select: null output");
+  return launch_rw_select(rowptr, col, q_lo, n_q, walks_per_node, walk_length, k_rw, key_const(key_seed), u,
+                          philox_seed, philox_offset, sel_kv, sel_cnt, as_stream(stream));
+}
+
+extern "C" int bf_real_select_merge(const int64_t* in_ptr, const int32_t* in_src, int64_t num_nodes, int64_t q_lo,
+                                    int64_t n_q, int32_t k_real, int64_t key_seed, const int32_t* rw_kv,
+                                    const int32_t* rw_cnt, int32_t k_rw, int32_t dedup, int32_t* table,
+                                    int32_t width, int32_t* row_len, void* stream) {
+  int rc = check_graph(in_ptr, in_src, num_nodes, q_lo, n_q);
+  if (rc) return rc;
+  if (k_real < 0) k_real = 0;
+  if (rw_kv == nullptr) k_rw = 0;
+  BF_CHECK_ARG(k_real <= 32 && k_rw >= 0 && k_rw <= 32, "real_select_merge: k_real=%d k_rw=%d must be <= 32",
+               k_real, k_rw);
+  BF_CHECK_ARG(k_rw == 0 || rw_cnt != nullptr, "real_select_merge: rw_cnt is NULL");
+  BF_CHECK_ARG(width >= k_real + k_rw && width >= 1, "real_select_merge: width %d < k_real + k_rw = %d", width,
+               k_real + k_rw);
+  BF_CHECK_ARG((table && row_len) || n_q == 0, "real_select_merge: null output");
+  return launch_real_merge(in_ptr, in_src, q_lo, n_q, k_real, key_const(key_seed), k_rw ? rw_kv : nullptr, rw_cnt,
+                           k_rw, dedup ? 1 : 0, table, width, row_len, as_stream(stream));
+}
+
+extern "C" int bf_build_edge_table_workspace_size(int64_t n_q, int32_t k_rw, size_t* bytes) {
+  BF_CHECK_ARG(bytes && n_q >= 0 && k_rw >= 0, "build_edge_table_workspace_size: bad arguments");
+  *bytes = align_up(size_t(n_q) * size_t(k_rw > 0 ? k_rw : 0) * 4) + align_up(size_t(n_q) * 4) + 256;
+  return BF_OK;
+}
+
+extern "C" int bf_build_edge_table(const int64_t* rowptr, const int32_t* col, const int64_t* in_ptr,
+                                   const int32_t* in_src, int64_t num_nodes, int64_t num_edges, int64_t q_lo,
+                                   int64_t n_q, int32_t walks_per_node, int32_t walk_length, int32_t k_real,
+                                   int32_t k_rw, int64_t edge_seed, const float* u, uint64_t philox_seed,
+                                   uint64_t philox_offset, int32_t* table, int32_t* row_len, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  BF_CHECK_ARG(num_edges >= 0, "build_edge_table: num_edges < 0");
+  const bool use_rw = k_rw > 0 && walks_per_node > 0 && walk_length > 0 && num_nodes > 0;
+  const bool use_real = k_real > 0 && num_edges > 0;
+  const int32_t width = (k_real > 0 ? k_real : 0) + (k_rw > 0 ? k_rw : 0);
+  BF_CHECK_ARG(width >= 1, "build_edge_table: empty budget (k_real=%d, k_rw=%d)", k_real, k_rw);
+  size_t need = 0;
+  bf_build_edge_table_workspace_size(n_q, use_rw ? k_rw : 0, &need);
+  BF_CHECK_ARG(workspace && workspace_bytes >= need, "build_edge_table: workspace %zu < %zu bytes",
+               workspace_bytes, need);
+  hipStream_t st = as_stream(stream);
+  int32_t* sel_kv = nullptr;
+  int32_t* sel_cnt = nullptr;
+  if (use_rw) {
+    sel_kv = static_cast<int32_t*>(workspace);
+    sel_cnt = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + align_up(size_t(n_q) * k_rw * 4));
+    int rc = bf_rw_select(rowptr, col, num_nodes, q_lo, n_q, walks_per_node, walk_length, k_rw,
+                          edge_seed + 37, u, philox_seed, philox_offset, sel_kv, sel_cnt, st);
+    if (rc) return rc;
+  }
+  // the reference coalesces only when both parts are globally non-empty
+  return bf_real_select_merge(in_ptr, in_src, num_nodes, q_lo, n_q, use_real ? k_real : 0, edge_seed + 17,
+                              use_rw ? sel_kv : nullptr, sel_cnt, use_rw ? k_rw : 0,
+                              (use_real && use_rw) ? 1 : 0, table, width, row_len, st);
+}

@@ -1,0 +1,362 @@
+// Edge-index format kernels: query-major table -> attention CSR (with the
+// Graphormer global token), reference COO -> CSR, the key-major reverse index
+// used by the deterministic dK/dV pass and by the COO adaptor, and split plans
+// for rows longer than the attention chunk.
+//
+// Sorting and prefix sums use rocPRIM through hipCUB (LSD radix sort is stable,
+// which makes the reverse index ordered by (kv, CSR position) = (src, dst)).
+#include <hipcub/hipcub.hpp>
+
+#include "bf_common.h"
+
+namespace bf {
+namespace {
+
+constexpr int kThreads = 256;
+
+inline unsigned blocks_for(int64_t n) { return unsigned(ceil_div(n, kThreads)); }
+
+inline size_t align_up(size_t x) { return (x + 255) & ~size_t(255); }
+
+int bits_for(uint64_t maxval) {
+  int b = 1;
+  while (b < 64 && (uint64_t(1) << b) <= maxval) ++b;
+  return b;
+}
+
+size_t scan_temp_bytes_i64(int64_t n) {
+  size_t bytes = 0;
+  (void)hipcub::DeviceScan::InclusiveSum(nullptr, bytes, static_cast<const int64_t*>(nullptr),
+                                   static_cast<int64_t*>(nullptr), int(n > 0 ? n : 1));
+  return bytes;
+}
+
+// ---------------------------------------------------------------- table -> CSR
+__global__ void row_lengths_kernel(const int32_t* __restrict__ row_len, int64_t n_rows, int token,
+                                   int64_t* __restrict__ lens) {
+  const int64_t n_q = n_rows + (token ? 1 : 0);
+  const int64_t t = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (t >= n_q) return;
+  int64_t len;
+  if (token)
+    len = t == 0 ? n_rows : int64_t(row_len[t - 1]) + 1;
+  else
+    len = row_len[t];
+  lens[t] = len;
+}
+
+__global__ void table_fill_kernel(const int32_t* __restrict__ table, const int32_t* __restrict__ row_len,
+                                  int64_t n_rows, int width, int token, const int64_t* __restrict__ qptr,
+                                  int32_t* __restrict__ kv) {
+  // one thread per table slot; token row 0 is filled by token_row_kernel
+  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= n_rows * width) return;
+  const int64_t r = i / width;
+  const int c = int(i - r * width);
+  const int len = row_len[r];
+  if (c >= len) return;
+  if (token) {
+    const int64_t base = qptr[r + 1];  // query r+1
+    if (c == 0) kv[base] = 0;
+    kv[base + 1 + c] = table[i] + 1;
+  } else {
+    kv[qptr[r] + c] = table[i];
+  }
+}
+
+__global__ void token_fill_kernel(const int32_t* __restrict__ row_len, int64_t n_rows,
+                                  const int64_t* __restrict__ qptr, int32_t* __restrict__ kv) {
+  // query 0 lists kv 1..n_rows; rows with len 0 still get their kv-0 entry
+  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= n_rows) return;
+  kv[i] = int32_t(i + 1);
+  if (row_len[i] == 0) kv[qptr[i + 1]] = 0;
+}
+
+__global__ void sum_lengths_kernel(const int32_t* __restrict__ row_len, int64_t n_rows,
+                                   unsigned long long* __restrict__ total) {
+  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  unsigned long long v = i < n_rows ? (unsigned long long)row_len[i] : 0ull;
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  if ((threadIdx.x & 63) == 0 && v) atomicAdd(total, v);
+}
+
+// ---------------------------------------------------------------- sorted keys -> row pointers
+// ptr[r] = first position i with row(i) >= r, from row ids sorted ascending.
+template <typename K>
+__global__ void boundaries_kernel(const K* __restrict__ keys, int64_t n, uint64_t divisor, int64_t n_rows,
+                                  int64_t* __restrict__ ptr) {
+  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (i > n) return;
+  int64_t r_here = i < n ? int64_t(uint64_t(keys[i]) / divisor) : n_rows;
+  int64_t r_prev = i > 0 ? int64_t(uint64_t(keys[i - 1]) / divisor) : -1;
+  if (r_here > n_rows) r_here = n_rows;
+  if (r_prev > n_rows) r_prev = n_rows;
+  for (int64_t r = r_prev + 1; r <= r_here; ++r) ptr[r] = i;
+}
+
+__global__ void coo_keys_kernel(const int64_t* __restrict__ src, const int64_t* __restrict__ dst, int64_t nnz,
+                                uint64_t n_kv, uint64_t* __restrict__ keys) {
+  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= nnz) return;
+  keys[i] = uint64_t(dst[i]) * n_kv + uint64_t(src[i]);
+}
+
+__global__ void coo_kv_kernel(const uint64_t* __restrict__ keys, int64_t nnz, uint64_t n_kv,
+                              int32_t* __restrict__ kv) {
+  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= nnz) return;
+  kv[i] = int32_t(keys[i] % n_kv);
+}
+
+// ---------------------------------------------------------------- reverse index
+__global__ void iota_kernel(int32_t* __restrict__ x, int64_t n) {
+  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (i < n) x[i] = int32_t(i);
+}
+
+// rows[i] = r with ptr[r] <= i < ptr[r+1] (binary search; balanced for any row length).
+template <typename R>
+__global__ void expand_rows_kernel(const int64_t* __restrict__ ptr, int64_t n_rows, int64_t nnz,
+                                   R* __restrict__ rows) {
+  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= nnz) return;
+  int64_t lo = 0, hi = n_rows;  // invariant: ptr[lo] <= i < ptr[hi]
+  while (hi - lo > 1) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (ptr[mid] <= i) lo = mid; else hi = mid;
+  }
+  rows[i] = R(lo);
+}
+
+__global__ void gather_rows_kernel(const int32_t* __restrict__ rows_of_entry, const int32_t* __restrict__ ke,
+                                   int64_t nnz, int32_t* __restrict__ kq) {
+  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (i < nnz) kq[i] = rows_of_entry[ke[i]];
+}
+
+// ---------------------------------------------------------------- split plans
+__global__ void split_count_kernel(const int64_t* __restrict__ ptr, int64_t n_rows, int chunk,
+                                   int32_t* __restrict__ nitems) {
+  const int64_t r = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (r >= n_rows) return;
+  const int64_t len = ptr[r + 1] - ptr[r];
+  nitems[r] = len > chunk ? int32_t(ceil_div(len, chunk)) : 0;
+}
+
+__global__ void split_fill_kernel(const int32_t* __restrict__ nitems, const int32_t* __restrict__ item_off,
+                                  int64_t n_rows, int64_t cap, int32_t* __restrict__ item_row,
+                                  int32_t* __restrict__ total) {
+  const int64_t r = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (r >= n_rows) return;
+  const int n = nitems[r];
+  const int64_t off = item_off[r];
+  for (int j = 0; j < n; ++j)
+    if (off + j < cap) item_row[off + j] = int32_t(r);
+  if (r == n_rows - 1) {
+    const int64_t t = off + n;
+    *total = int32_t(t < cap ? t : cap);
+  }
+}
+
+__global__ void set_int_kernel(int32_t* p, int32_t v) { *p = v; }
+
+}  // namespace
+}  // namespace bf
+
+using namespace bf;
+
+extern "C" int bf_scan_workspace_size(int64_t n, size_t* bytes) {
+  BF_CHECK_ARG(bytes && n >= 0, "scan_workspace_size: bad arguments");
+  *bytes = align_up(size_t(n > 0 ? n : 1) * sizeof(int64_t)) + align_up(scan_temp_bytes_i64(n)) + 256;
+  return BF_OK;
+}
+
+extern "C" int bf_table_csr_nnz(const int32_t* row_len, int64_t n_rows, int32_t global_token,
+                                int64_t* nnz_host, void* workspace, size_t workspace_bytes, void* stream) {
+  BF_CHECK_ARG(nnz_host && n_rows >= 0, "table_csr_nnz: bad arguments");
+  BF_CHECK_ARG(workspace && workspace_bytes >= sizeof(unsigned long long), "table_csr_nnz: workspace too small");
+  hipStream_t st = as_stream(stream);
+  auto* total = static_cast<unsigned long long*>(workspace);
+  BF_CHECK_HIP(hipMemsetAsync(total, 0, sizeof(*total), st));
+  if (n_rows > 0) {
+    BF_LAUNCH("sum_lengths_kernel", sum_lengths_kernel, dim3(blocks_for(n_rows)), dim3(kThreads), 0, st, row_len, n_rows, total);
+    BF_CHECK_LAUNCH();
+  }
+  unsigned long long h = 0;
+  BF_CHECK_HIP(hipMemcpyAsync(&h, total, sizeof(h), hipMemcpyDeviceToHost, st));
+  BF_CHECK_HIP(hipStreamSynchronize(st));
+  *nnz_host = int64_t(h) + (global_token ? 2 * n_rows : 0);
+  return BF_OK;
+}
+
+extern "C" int bf_table_to_csr(const int32_t* table, const int32_t* row_len, int64_t n_rows, int32_t width,
+                               int32_t global_token, int64_t* qptr, int32_t* kv, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  BF_CHECK_ARG(n_rows >= 0 && width >= 0 && qptr, "table_to_csr: bad arguments");
+  BF_CHECK_ARG(n_rows == 0 || (table && row_len && kv) || (width == 0 && row_len), "table_to_csr: null tensor");
+  const int64_t n_q = n_rows + (global_token ? 1 : 0);
+  size_t need = 0;
+  bf_scan_workspace_size(n_q, &need);
+  BF_CHECK_ARG(workspace && workspace_bytes >= need, "table_to_csr: workspace %zu < %zu bytes", workspace_bytes, need);
+  hipStream_t st = as_stream(stream);
+  BF_CHECK_HIP(hipMemsetAsync(qptr, 0, sizeof(int64_t), st));
+  if (n_q == 0) return BF_OK;
+  auto* lens = static_cast<int64_t*>(workspace);
+  void* temp = static_cast<char*>(workspace) + align_up(size_t(n_q) * sizeof(int64_t));
+  size_t temp_bytes = scan_temp_bytes_i64(n_q);
+  BF_LAUNCH("row_lengths_kernel", row_lengths_kernel, dim3(blocks_for(n_q)), dim3(kThreads), 0, st, row_len, n_rows,
+                     int(global_token != 0), lens);
+  BF_CHECK_LAUNCH();
+  BF_CHECK_HIP(hipcub::DeviceScan::InclusiveSum(temp, temp_bytes, lens, qptr + 1, int(n_q), st));
+  if (n_rows * width > 0) {
+    BF_LAUNCH("table_fill_kernel", table_fill_kernel, dim3(blocks_for(n_rows * width)), dim3(kThreads), 0, st, table,
+                       row_len, n_rows, width, int(global_token != 0), qptr, kv);
+    BF_CHECK_LAUNCH();
+  }
+  if (global_token && n_rows > 0) {
+    BF_LAUNCH("token_fill_kernel", token_fill_kernel, dim3(blocks_for(n_rows)), dim3(kThreads), 0, st, row_len, n_rows, qptr, kv);
+    BF_CHECK_LAUNCH();
+  }
+  return BF_OK;
+}
+
+extern "C" int bf_coo_to_csr_workspace_size(int64_t nnz, int64_t n_q, size_t* bytes) {
+  BF_CHECK_ARG(bytes && nnz >= 0 && n_q >= 0, "coo_to_csr_workspace_size: bad arguments");
+  size_t sort_bytes = 0;
+  (void)hipcub::DeviceRadixSort::SortKeys(nullptr, sort_bytes, static_cast<const uint64_t*>(nullptr),
+                                    static_cast<uint64_t*>(nullptr), int(nnz > 0 ? nnz : 1));
+  *bytes = 2 * align_up(size_t(nnz > 0 ? nnz : 1) * sizeof(uint64_t)) + align_up(sort_bytes) + 256;
+  (void)n_q;
+  return BF_OK;
+}
+
+extern "C" int bf_coo_to_csr(const int64_t* src, const int64_t* dst, int64_t nnz, int64_t n_q, int64_t n_kv,
+                             int64_t* qptr, int32_t* kv, void* workspace, size_t workspace_bytes, void* stream) {
+  BF_CHECK_ARG(nnz >= 0 && n_q >= 0 && n_kv > 0 && qptr, "coo_to_csr: bad arguments");
+  BF_CHECK_ARG(n_kv < (int64_t(1) << 31) && nnz < (int64_t(1) << 31), "coo_to_csr: sizes must fit int32");
+  size_t need = 0;
+  bf_coo_to_csr_workspace_size(nnz, n_q, &need);
+  BF_CHECK_ARG(workspace && workspace_bytes >= need, "coo_to_csr: workspace %zu < %zu bytes", workspace_bytes, need);
+  hipStream_t st = as_stream(stream);
+  if (nnz == 0) {
+    BF_CHECK_HIP(hipMemsetAsync(qptr, 0, size_t(n_q + 1) * sizeof(int64_t), st));
+    return BF_OK;
+  }
+  auto* keys_in = static_cast<uint64_t*>(workspace);
+  auto* keys_out = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + align_up(size_t(nnz) * 8));
+  void* temp = static_cast<char*>(workspace) + 2 * align_up(size_t(nnz) * 8);
+  size_t temp_bytes = 0;
+  (void)hipcub::DeviceRadixSort::SortKeys(nullptr, temp_bytes, keys_in, keys_out, int(nnz));
+  BF_LAUNCH("coo_keys_kernel", coo_keys_kernel, dim3(blocks_for(nnz)), dim3(kThreads), 0, st, src, dst, nnz,
+                     uint64_t(n_kv), keys_in);
+  BF_CHECK_LAUNCH();
+  const int end_bit = bits_for(uint64_t(n_q) * uint64_t(n_kv));
+  BF_CHECK_HIP(hipcub::DeviceRadixSort::SortKeys(temp, temp_bytes, keys_in, keys_out, int(nnz), 0, end_bit, st));
+  BF_LAUNCH("coo_kv_kernel", coo_kv_kernel, dim3(blocks_for(nnz)), dim3(kThreads), 0, st, keys_out, nnz,
+                     uint64_t(n_kv), kv);
+  BF_CHECK_LAUNCH();
+  BF_LAUNCH("boundaries_kernel", boundaries_kernel<uint64_t>, dim3(blocks_for(nnz + 1)), dim3(kThreads), 0, st, keys_out,
+                     nnz, uint64_t(n_kv), n_q, qptr);
+  BF_CHECK_LAUNCH();
+  return BF_OK;
+}
+
+extern "C" int bf_reverse_index_workspace_size(int64_t nnz, int64_t n_kv, size_t* bytes) {
+  BF_CHECK_ARG(bytes && nnz >= 0 && n_kv >= 0, "reverse_index_workspace_size: bad arguments");
+  size_t sort_bytes = 0;
+  const int n = int(nnz > 0 ? nnz : 1);
+  (void)hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, static_cast<const uint32_t*>(nullptr),
+                                     static_cast<uint32_t*>(nullptr), static_cast<const int32_t*>(nullptr),
+                                     static_cast<int32_t*>(nullptr), n);
+  *bytes = 3 * align_up(size_t(n) * 4) + align_up(sort_bytes) + 256;
+  return BF_OK;
+}
+
+extern "C" int bf_reverse_index(const int64_t* qptr, const int32_t* kv, int64_t n_q, int64_t n_kv, int64_t nnz,
+                                int64_t* kptr, int32_t* kq, int32_t* ke, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  BF_CHECK_ARG(qptr && kptr && n_q >= 0 && n_kv >= 0 && nnz >= 0, "reverse_index: bad arguments");
+  BF_CHECK_ARG(nnz < (int64_t(1) << 31) && n_q < (int64_t(1) << 31), "reverse_index: sizes must fit int32");
+  size_t need = 0;
+  bf_reverse_index_workspace_size(nnz, n_kv, &need);
+  BF_CHECK_ARG(workspace && workspace_bytes >= need, "reverse_index: workspace %zu < %zu bytes", workspace_bytes, need);
+  hipStream_t st = as_stream(stream);
+  if (nnz == 0) {
+    BF_CHECK_HIP(hipMemsetAsync(kptr, 0, size_t(n_kv + 1) * sizeof(int64_t), st));
+    return BF_OK;
+  }
+  BF_CHECK_ARG(kv && kq && ke, "reverse_index: null tensor");
+  const size_t slab = align_up(size_t(nnz) * 4);
+  auto* keys_out = static_cast<uint32_t*>(workspace);
+  auto* vals_in = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + slab);
+  auto* rows_of_entry = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + 2 * slab);
+  void* temp = static_cast<char*>(workspace) + 3 * slab;
+  size_t temp_bytes = 0;
+  (void)hipcub::DeviceRadixSort::SortPairs(nullptr, temp_bytes, reinterpret_cast<const uint32_t*>(kv), keys_out,
+                                     vals_in, ke, int(nnz));
+  BF_LAUNCH("iota_kernel", iota_kernel, dim3(blocks_for(nnz)), dim3(kThreads), 0, st, vals_in, nnz);
+  BF_CHECK_LAUNCH();
+  const int end_bit = bits_for(uint64_t(n_kv > 0 ? n_kv : 1));
+  BF_CHECK_HIP(hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, reinterpret_cast<const uint32_t*>(kv),
+                                                  keys_out, vals_in, ke, int(nnz), 0, end_bit, st));
+  BF_LAUNCH("boundaries_kernel", boundaries_kernel<uint32_t>, dim3(blocks_for(nnz + 1)), dim3(kThreads), 0, st, keys_out,
+                     nnz, uint64_t(1), n_kv, kptr);
+  BF_CHECK_LAUNCH();
+  BF_LAUNCH("expand_rows_kernel", expand_rows_kernel<int32_t>, dim3(blocks_for(nnz)), dim3(kThreads), 0, st, qptr, n_q, nnz,
+                     rows_of_entry);
+  BF_CHECK_LAUNCH();
+  BF_LAUNCH("gather_rows_kernel", gather_rows_kernel, dim3(blocks_for(nnz)), dim3(kThreads), 0, st, rows_of_entry, ke, nnz, kq);
+  BF_CHECK_LAUNCH();
+  return BF_OK;
+}
+
+extern "C" int bf_expand_rows(const int64_t* ptr, int64_t n_rows, int64_t nnz, int64_t* rows, void* stream) {
+  BF_CHECK_ARG(ptr && n_rows >= 0 && nnz >= 0 && (rows || nnz == 0), "expand_rows: bad arguments");
+  BF_CHECK_ARG(nnz == 0 || n_rows > 0, "expand_rows: entries without rows");
+  if (nnz == 0) return BF_OK;
+  BF_LAUNCH("expand_rows_kernel", expand_rows_kernel<int64_t>, dim3(blocks_for(nnz)), dim3(kThreads), 0, as_stream(stream),
+                     ptr, n_rows, nnz, rows);
+  BF_CHECK_LAUNCH();
+  return BF_OK;
+}
+
+extern "C" int64_t bf_split_capacity(int64_t nnz, int32_t chunk) {
+  if (chunk < 1 || nnz < 0) return 0;
+  // rows split only when len > chunk: items <= sum(len/chunk + 1) <= 2*nnz/chunk
+  return 2 * (nnz / chunk) + 1;
+}
+
+extern "C" int bf_split_plan(const int64_t* ptr, int64_t n_rows, int32_t chunk, int32_t* nitems, int32_t* item_off,
+                             int32_t* item_row, int64_t cap, int32_t* total, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  BF_CHECK_ARG(ptr && n_rows >= 0 && chunk >= 1 && total, "split_plan: bad arguments");
+  BF_CHECK_ARG(cap >= 0 && cap < (int64_t(1) << 31), "split_plan: bad capacity");
+  hipStream_t st = as_stream(stream);
+  if (n_rows == 0) {
+    BF_LAUNCH("set_int_kernel", set_int_kernel, dim3(1), dim3(1), 0, st, total, 0);
+    BF_CHECK_LAUNCH();
+    return BF_OK;
+  }
+  BF_CHECK_ARG(nitems && item_off && (item_row || cap == 0), "split_plan: null tensor");
+  size_t temp_bytes = 0;
+  (void)hipcub::DeviceScan::ExclusiveSum(nullptr, temp_bytes, nitems, item_off, int(n_rows));
+  BF_CHECK_ARG(workspace && workspace_bytes >= temp_bytes, "split_plan: workspace %zu < %zu bytes",
+               workspace_bytes, temp_bytes);
+  BF_LAUNCH("split_count_kernel", split_count_kernel, dim3(blocks_for(n_rows)), dim3(kThreads), 0, st, ptr, n_rows, chunk, nitems);
+  BF_CHECK_LAUNCH();
+  BF_CHECK_HIP(hipcub::DeviceScan::ExclusiveSum(workspace, temp_bytes, nitems, item_off, int(n_rows), st));
+  BF_LAUNCH("split_fill_kernel", split_fill_kernel, dim3(blocks_for(n_rows)), dim3(kThreads), 0, st, nitems, item_off, n_rows,
+                     cap, item_row, total);
+  BF_CHECK_LAUNCH();
+  return BF_OK;
+}
+
+extern "C" int bf_split_plan_workspace_size(int64_t n_rows, size_t* bytes) {
+  BF_CHECK_ARG(bytes && n_rows >= 0, "split_plan_workspace_size: bad arguments");
+  size_t temp_bytes = 0;
+  (void)hipcub::DeviceScan::ExclusiveSum(nullptr, temp_bytes, static_cast<const int32_t*>(nullptr),
+                                   static_cast<int32_t*>(nullptr), int(n_rows > 0 ? n_rows : 1));
+  *bytes = align_up(temp_bytes) + 256;
+  return BF_OK;
+}

@@ -1,0 +1,101 @@
+"""Budgeted query-centric edge construction on the HIP kernels.
+
+``build_attention_edges`` is the device-side equivalent of the reference's
+per-epoch build (``_build_merged_edges``, utils/fullgraph_sp_support.py:
+2943-3026, driven by ``_build_attention_edges`` :3341-3362) for a fixed budget
+state (b_real, b_rw): it returns an ``EdgeTable`` — the query-major
+``[n_q, b_real+b_rw]`` int32 table plus row lengths — which the attention
+modules consume directly, or which ``EdgeTable.to_edge_index()`` turns into the
+reference's COO ``[2, E']`` (coalesced src-major order, then the Graphormer
+virtual edges in fix_edge_index order, gt_sp/utils.py:113-130).
+
+RNG: with ``u`` (float32 [n_q*P, L]) the walk consumes injected uniforms (the
+parity contract); without it the walk draws Philox4x32-10 uniforms keyed by
+``philox_seed`` (default: the edge seed) and the global walk id, so any query
+shard draws exactly what a full build would.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Optional
+
+import torch
+
+from . import hip_ops
+from .graph import CSRGraph
+from .hip_ops import AttentionIndex
+
+REAL_SEED_OFFSET = 17   # utils/fullgraph_sp_support.py:1413
+RW_SEED_OFFSET = 37     # utils/fullgraph_sp_support.py:1514
+
+
+@dataclass
+class EdgeTable:
+    table: torch.Tensor            # int32 [n_q, width], rows ascending kv, -1 padded
+    row_len: torch.Tensor          # int32 [n_q]
+    num_nodes: int
+    q_lo: int = 0
+    global_token: bool = False     # Graphormer virtual node applied when indexing
+    _index: dict = field(default_factory=dict, repr=False)
+
+    @property
+    def n_rows(self) -> int:
+        return int(self.table.shape[0])
+
+    @property
+    def width(self) -> int:
+        return int(self.table.shape[1])
+
+    def attention_index(self, chunk: int = hip_ops.DEFAULT_CHUNK) -> AttentionIndex:
+        """CSR view for the attention kernels (cached per chunk)."""
+        idx = self._index.get(chunk)
+        if idx is None:
+            if self.q_lo != 0 or self.n_rows != self.num_nodes:
+                if self.global_token:
+                    raise NotImplementedError("the Graphormer global token needs the full query set")
+            n_kv = self.num_nodes + (1 if self.global_token else 0)
+            idx = AttentionIndex.from_table(self.table, self.row_len, self.global_token, n_kv=n_kv, chunk=chunk)
+            self._index[chunk] = idx
+        return idx
+
+    def to_edge_index(self) -> torch.Tensor:
+        """Reference-format COO [2, E'] int64 (row 0 kv/src, row 1 query/dst).
+
+        Merged part in coalesce order (sorted by (src, dst)); with the global
+        token, ids shifted by one and the 2N virtual edges appended as
+        fix_edge_index does.
+        """
+        base = AttentionIndex.from_table(self.table, self.row_len, False, n_kv=self.num_nodes)
+        coo = base.to_coo()
+        if self.q_lo:
+            coo = torch.stack([coo[0], coo[1] + self.q_lo])
+        if not self.global_token:
+            return coo
+        n = self.num_nodes
+        ar = torch.arange(1, n + 1, dtype=torch.int64, device=coo.device)
+        zeros = torch.zeros(n, dtype=torch.int64, device=coo.device)
+        return torch.cat([coo + 1, torch.stack([ar, zeros]), torch.stack([zeros, ar])], dim=1)
+
+
+def build_attention_edges(graph: CSRGraph, *, real_edges_per_query: int, rw_edges_per_query: int,
+                          walk_length: int = 4, walks_per_node: int = 2, edge_seed: int = 42,
+                          q_lo: int = 0, n_q: Optional[int] = None, u: Optional[torch.Tensor] = None,
+                          philox_seed: Optional[int] = None, philox_offset: int = 0,
+                          global_token: bool = False) -> EdgeTable:
+    """Budgeted edge table for queries [q_lo, q_lo+n_q) of ``graph``.
+
+    b_real <= 0 drops the real part, b_rw <= 0 (or walks_per_node <= 0) drops
+    the RW part (utils/fullgraph_sp_support.py:1395-1400, 1506-1508); both parts
+    present -> set union per query, one part -> its multiset.
+    """
+    n_q = graph.num_nodes - q_lo if n_q is None else n_q
+    b_r = max(int(real_edges_per_query), 0)
+    b_w = max(int(rw_edges_per_query), 0) if walks_per_node > 0 else 0
+    if b_r + b_w <= 0:
+        raise ValueError("empty edge budget: real_edges_per_query + rw_edges_per_query must be > 0")
+    walk_length = max(1, int(walk_length))
+    table, row_len = hip_ops.build_edge_table(
+        graph.rowptr, graph.col, graph.in_ptr, graph.in_src, graph.num_edges, q_lo, n_q,
+        max(int(walks_per_node), 1), walk_length, b_r, b_w, int(edge_seed), u=u,
+        philox_seed=int(edge_seed if philox_seed is None else philox_seed), philox_offset=philox_offset)
+    return EdgeTable(table, row_len, graph.num_nodes, q_lo=q_lo, global_token=global_token)

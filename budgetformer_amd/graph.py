@@ -1,0 +1,127 @@
+"""Graph topology in HBM and synthetic graphs of the benchmark shapes.
+
+``CSRGraph`` holds the coalesced CSR the walk reads (source rows, ascending
+neighbours; ``_get_random_walk_graph``, gt_sp/utils.py:890-936) and the
+in-neighbour CSR the real-edge top-k reads (for a symmetric graph the same
+arrays). Ids are int32, offsets int64, so a 1.6B-edge graph's col is 6.4 GB.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional
+
+import numpy as np
+import torch
+
+from . import hip_ops
+
+
+@dataclass
+class CSRGraph:
+    rowptr: torch.Tensor          # int64 [N+1], rows = sources
+    col: torch.Tensor             # int32 [E], ascending within a row
+    in_ptr: torch.Tensor          # int64 [N+1], rows = destinations
+    in_src: torch.Tensor          # int32 [E]
+    num_nodes: int
+
+    @property
+    def num_edges(self) -> int:
+        return int(self.col.numel())
+
+    @property
+    def device(self):
+        return self.rowptr.device
+
+    @property
+    def symmetric(self) -> bool:
+        return self.in_ptr is self.rowptr and self.in_src is self.col
+
+    @classmethod
+    def from_csr(cls, rowptr, col, num_nodes: int, in_ptr=None, in_src=None, device="cuda"):
+        rowptr = torch.as_tensor(rowptr, dtype=torch.int64).to(device).contiguous()
+        col = torch.as_tensor(col).to(torch.int32).to(device).contiguous()
+        if in_ptr is None:
+            in_ptr, in_src = rowptr, col
+        else:
+            in_ptr = torch.as_tensor(in_ptr, dtype=torch.int64).to(device).contiguous()
+            in_src = torch.as_tensor(in_src).to(torch.int32).to(device).contiguous()
+        return cls(rowptr, col, in_ptr, in_src, int(num_nodes))
+
+    @classmethod
+    def from_edge_index(cls, edge_index: torch.Tensor, num_nodes: int, symmetric: bool = False, device="cuda"):
+        """From the reference's coalesced ``edge_index_global`` [2, E] (row 0 source, row 1 target).
+
+        Both CSRs are built on the device (radix sort); duplicates are kept, so
+        pass a coalesced edge list as the reference does.
+        """
+        ei = edge_index.to(device)
+        rowptr, col = hip_ops.coo_to_csr(torch.stack([ei[1], ei[0]]), num_nodes, num_nodes)
+        if symmetric:
+            return cls(rowptr, col, rowptr, col, int(num_nodes))
+        in_ptr, in_src = hip_ops.coo_to_csr(ei, num_nodes, num_nodes)
+        return cls(rowptr, col, in_ptr, in_src, int(num_nodes))
+
+
+def chung_lu_csr(num_nodes: int, num_edges: int, exponent: float = 2.1, seed: int = 42,
+                 max_degree: Optional[int] = None):
+    """Symmetric power-law (Chung-Lu) graph as coalesced CSR numpy arrays.
+
+    Expected degree of node i is proportional to (i + i0)^(-1/(exponent-1)),
+    optionally capped at ``max_degree``; endpoints are drawn proportionally to
+    it, self loops dropped, pairs symmetrised and deduplicated, and the
+    directed edge count topped up / trimmed to ``num_edges`` (even).
+    Returns (rowptr int64 [N+1], col int32 [E]).
+    """
+    rng = np.random.default_rng(seed)
+    i0 = 10.0
+    w = (np.arange(num_nodes, dtype=np.float64) + i0) ** (-1.0 / (exponent - 1.0))
+    w *= num_edges / w.sum()
+    if max_degree is not None:
+        w = np.minimum(w, float(max_degree))
+    p = w / w.sum()
+    target_pairs = num_edges // 2
+    keys = np.zeros(0, dtype=np.int64)
+    draw = int(target_pairs * 1.15) + 16
+    for _ in range(20):
+        a = rng.choice(num_nodes, size=draw, p=p)
+        b = rng.choice(num_nodes, size=draw, p=p)
+        keep = a != b
+        lo = np.minimum(a[keep], b[keep]).astype(np.int64)
+        hi = np.maximum(a[keep], b[keep]).astype(np.int64)
+        keys = np.unique(np.concatenate([keys, lo * num_nodes + hi]))
+        if keys.size >= target_pairs:
+            break
+        draw = int((target_pairs - keys.size) * 1.5) + 16
+    if keys.size > target_pairs:
+        keys = rng.choice(keys, size=target_pairs, replace=False)
+    lo, hi = keys // num_nodes, keys % num_nodes
+    src = np.concatenate([lo, hi])
+    dst = np.concatenate([hi, lo])
+    lin = np.unique(src * num_nodes + dst)
+    src, dst = lin // num_nodes, lin % num_nodes
+    rowptr = np.zeros(num_nodes + 1, dtype=np.int64)
+    np.add.at(rowptr, src + 1, 1)
+    return np.cumsum(rowptr), dst.astype(np.int32)
+
+
+def uniform_random_csr(num_nodes: int, num_edges: int, seed: int = 42):
+    """Symmetric G(n, m) graph (config c1's plumbing graph) as coalesced CSR."""
+    rng = np.random.default_rng(seed)
+    pairs = set()
+    target = num_edges // 2
+    while len(pairs) < target:
+        a = rng.integers(0, num_nodes, size=2 * (target - len(pairs)) + 8)
+        b = rng.integers(0, num_nodes, size=a.size)
+        for x, y in zip(a.tolist(), b.tolist()):
+            if x != y:
+                pairs.add((min(x, y), max(x, y)))
+                if len(pairs) >= target:
+                    break
+    arr = np.array(sorted(pairs), dtype=np.int64)
+    src = np.concatenate([arr[:, 0], arr[:, 1]])
+    dst = np.concatenate([arr[:, 1], arr[:, 0]])
+    lin = np.unique(src * num_nodes + dst)
+    src, dst = lin // num_nodes, lin % num_nodes
+    rowptr = np.zeros(num_nodes + 1, dtype=np.int64)
+    np.add.at(rowptr, src + 1, 1)
+    return np.cumsum(rowptr), dst.astype(np.int32)

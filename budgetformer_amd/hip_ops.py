@@ -1,0 +1,365 @@
+"""Tensor-level wrappers around the C ABI.
+
+Each function takes device tensors, checks shapes/dtypes on the host, draws
+scratch memory from PyTorch's caching allocator (so a failed allocation is a
+``torch.cuda.OutOfMemoryError``) and enqueues the HIP kernels on the current
+stream. PyTorch is used only for device memory and streams.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, field
+from typing import Optional
+
+import torch
+
+from . import _native as N
+
+DEFAULT_CHUNK = 64
+
+
+def _p(t: Optional[torch.Tensor]):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _stream(device: torch.device):
+    return C.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _require(t: torch.Tensor, name: str, dtype: torch.dtype, device: torch.device = None):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be a HIP device tensor (got {t.device}); the HIP path has no CPU fallback")
+    if device is not None and t.device != device:
+        raise ValueError(f"{name} is on {t.device}, expected {device}")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype} (got {t.dtype})")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def _size_query(fn_name: str, *args) -> int:
+    out = C.c_size_t(0)
+    N.call(fn_name, *args, C.byref(out))
+    return int(out.value)
+
+
+# ------------------------------------------------------------------ edge construction
+def random_walk(rowptr, col, q_lo: int, n_q: int, walks_per_node: int, walk_length: int,
+                u: Optional[torch.Tensor] = None, philox_seed: int = 0, philox_offset: int = 0) -> torch.Tensor:
+    """Walks [n_q*P, L+1] int64 from queries [q_lo, q_lo+n_q) (bf_random_walk)."""
+    dev = rowptr.device
+    _require(rowptr, "rowptr", torch.int64)
+    _require(col, "col", torch.int32, dev)
+    if u is not None:
+        _require(u, "u", torch.float32, dev)
+        if tuple(u.shape) != (n_q * walks_per_node, walk_length):
+            raise ValueError(f"u must be [{n_q * walks_per_node}, {walk_length}], got {tuple(u.shape)}")
+    walks = torch.empty(n_q * walks_per_node, walk_length + 1, dtype=torch.int64, device=dev)
+    N.call("bf_random_walk", _p(rowptr), _p(col), rowptr.numel() - 1, q_lo, n_q, walks_per_node, walk_length,
+           _p(u), philox_seed & (2 ** 64 - 1), philox_offset & (2 ** 64 - 1), _p(walks), _stream(dev))
+    return walks
+
+
+def walk_uniforms(q_lo: int, n_q: int, walks_per_node: int, walk_length: int, philox_seed: int,
+                  philox_offset: int = 0, device="cuda") -> torch.Tensor:
+    """The Philox uniforms of the production walk as a [n_q*P, L] float32 tensor."""
+    u = torch.empty(n_q * walks_per_node, walk_length, dtype=torch.float32, device=device)
+    N.call("bf_walk_uniforms", q_lo, n_q, walks_per_node, walk_length, philox_seed & (2 ** 64 - 1),
+           philox_offset & (2 ** 64 - 1), _p(u), _stream(u.device))
+    return u
+
+
+def rw_select(rowptr, col, q_lo: int, n_q: int, walks_per_node: int, walk_length: int, k_rw: int,
+              key_seed: int, u=None, philox_seed: int = 0, philox_offset: int = 0):
+    """Per-query top-k_rw of the query's own walk pool: (sel_kv [n_q,k_rw], sel_cnt [n_q])."""
+    dev = rowptr.device
+    _require(rowptr, "rowptr", torch.int64)
+    _require(col, "col", torch.int32, dev)
+    if u is not None:
+        _require(u, "u", torch.float32, dev)
+    sel = torch.empty(n_q, k_rw, dtype=torch.int32, device=dev)
+    cnt = torch.empty(n_q, dtype=torch.int32, device=dev)
+    N.call("bf_rw_select", _p(rowptr), _p(col), rowptr.numel() - 1, q_lo, n_q, walks_per_node, walk_length, k_rw,
+           key_seed, _p(u), philox_seed & (2 ** 64 - 1), philox_offset & (2 ** 64 - 1), _p(sel), _p(cnt),
+           _stream(dev))
+    return sel, cnt
+
+
+def real_select_merge(in_ptr, in_src, q_lo: int, n_q: int, k_real: int, key_seed: int,
+                      rw_kv=None, rw_cnt=None, k_rw: int = 0, dedup: bool = True, width: Optional[int] = None):
+    """Real-edge top-k_real merged with an RW selection: (table [n_q,width], row_len [n_q])."""
+    dev = in_ptr.device
+    _require(in_ptr, "in_ptr", torch.int64)
+    _require(in_src, "in_src", torch.int32, dev)
+    width = width if width is not None else max(1, max(k_real, 0) + (k_rw if rw_kv is not None else 0))
+    table = torch.empty(n_q, width, dtype=torch.int32, device=dev)
+    row_len = torch.empty(n_q, dtype=torch.int32, device=dev)
+    N.call("bf_real_select_merge", _p(in_ptr), _p(in_src), in_ptr.numel() - 1, q_lo, n_q, k_real, key_seed,
+           _p(rw_kv), _p(rw_cnt), k_rw, int(bool(dedup)), _p(table), width, _p(row_len), _stream(dev))
+    return table, row_len
+
+
+def build_edge_table(rowptr, col, in_ptr, in_src, num_edges: int, q_lo: int, n_q: int, walks_per_node: int,
+                     walk_length: int, k_real: int, k_rw: int, edge_seed: int, u=None, philox_seed: int = 0,
+                     philox_offset: int = 0):
+    """Fused budgeted build (bf_build_edge_table): (table [n_q, k_real+k_rw], row_len [n_q])."""
+    dev = rowptr.device
+    _require(rowptr, "rowptr", torch.int64)
+    _require(col, "col", torch.int32, dev)
+    _require(in_ptr, "in_ptr", torch.int64, dev)
+    _require(in_src, "in_src", torch.int32, dev)
+    if u is not None:
+        _require(u, "u", torch.float32, dev)
+        if tuple(u.shape) != (n_q * walks_per_node, walk_length):
+            raise ValueError(f"u must be [{n_q * walks_per_node}, {walk_length}], got {tuple(u.shape)}")
+    width = max(k_real, 0) + max(k_rw, 0)
+    table = torch.empty(n_q, width, dtype=torch.int32, device=dev)
+    row_len = torch.empty(n_q, dtype=torch.int32, device=dev)
+    ws_bytes = _size_query("bf_build_edge_table_workspace_size", n_q, max(k_rw, 0))
+    ws = _workspace(ws_bytes, dev)
+    N.call("bf_build_edge_table", _p(rowptr), _p(col), _p(in_ptr), _p(in_src), rowptr.numel() - 1, num_edges,
+           q_lo, n_q, walks_per_node, walk_length, k_real, k_rw, edge_seed, _p(u), philox_seed & (2 ** 64 - 1),
+           philox_offset & (2 ** 64 - 1), _p(table), _p(row_len), _p(ws), ws.numel(), _stream(dev))
+    return table, row_len
+
+
+# ------------------------------------------------------------------ index formats
+def table_to_csr(table: torch.Tensor, row_len: torch.Tensor, global_token: bool = False):
+    """Query-major table -> (qptr [n_q+1] int64, kv [nnz] int32)."""
+    dev = table.device
+    _require(table, "table", torch.int32)
+    _require(row_len, "row_len", torch.int32, dev)
+    n_rows, width = table.shape
+    n_q = n_rows + (1 if global_token else 0)
+    ws = _workspace(_size_query("bf_scan_workspace_size", n_q), dev)
+    nnz = C.c_int64(0)
+    N.call("bf_table_csr_nnz", _p(row_len), n_rows, int(global_token), C.byref(nnz), _p(ws), ws.numel(),
+           _stream(dev))
+    qptr = torch.empty(n_q + 1, dtype=torch.int64, device=dev)
+    kv = torch.empty(max(nnz.value, 1), dtype=torch.int32, device=dev)[: nnz.value]
+    N.call("bf_table_to_csr", _p(table), _p(row_len), n_rows, width, int(global_token), _p(qptr), _p(kv),
+           _p(ws), ws.numel(), _stream(dev))
+    return qptr, kv
+
+
+def coo_to_csr(edge_index: torch.Tensor, n_q: int, n_kv: int):
+    """Reference COO [2, nnz] (row 0 = kv, row 1 = query) -> (qptr, kv), rows ascending in kv."""
+    dev = edge_index.device
+    if edge_index.dim() != 2 or edge_index.size(0) < 2:
+        raise ValueError(f"edge_index must be [2, E] (got {tuple(edge_index.shape)})")
+    src = edge_index[0].to(torch.int64).contiguous()
+    dst = edge_index[1].to(torch.int64).contiguous()
+    nnz = src.numel()
+    if nnz:
+        lo = torch.stack([src.min(), dst.min()]).min().item()
+        if lo < 0 or src.max().item() >= n_kv or dst.max().item() >= n_q:
+            raise ValueError(f"edge_index ids outside [0,{n_kv}) x [0,{n_q})")
+    ws = _workspace(_size_query("bf_coo_to_csr_workspace_size", nnz, n_q), dev)
+    qptr = torch.empty(n_q + 1, dtype=torch.int64, device=dev)
+    kv = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)[:nnz]
+    N.call("bf_coo_to_csr", _p(src), _p(dst), nnz, n_q, n_kv, _p(qptr), _p(kv), _p(ws), ws.numel(), _stream(dev))
+    return qptr, kv
+
+
+def reverse_index(qptr: torch.Tensor, kv: torch.Tensor, n_kv: int):
+    """Key-major view: (kptr [n_kv+1], kq [nnz], ke [nnz]) sorted by (kv, CSR position)."""
+    dev = qptr.device
+    _require(qptr, "qptr", torch.int64)
+    _require(kv, "kv", torch.int32, dev)
+    nnz = kv.numel()
+    ws = _workspace(_size_query("bf_reverse_index_workspace_size", nnz, n_kv), dev)
+    kptr = torch.empty(n_kv + 1, dtype=torch.int64, device=dev)
+    kq = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)[:nnz]
+    ke = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)[:nnz]
+    N.call("bf_reverse_index", _p(qptr), _p(kv), qptr.numel() - 1, n_kv, nnz, _p(kptr), _p(kq), _p(ke), _p(ws),
+           ws.numel(), _stream(dev))
+    return kptr, kq, ke
+
+
+def expand_rows(ptr: torch.Tensor, nnz: int) -> torch.Tensor:
+    """Row id (int64) of every CSR entry."""
+    _require(ptr, "ptr", torch.int64)
+    rows = torch.empty(max(nnz, 1), dtype=torch.int64, device=ptr.device)[:nnz]
+    N.call("bf_expand_rows", _p(ptr), ptr.numel() - 1, nnz, _p(rows), _stream(ptr.device))
+    return rows
+
+
+@dataclass
+class SplitPlan:
+    cap: int
+    nitems: torch.Tensor
+    item_off: torch.Tensor
+    item_row: torch.Tensor
+    total: torch.Tensor
+
+
+def split_plan(ptr: torch.Tensor, chunk: int) -> SplitPlan:
+    dev = ptr.device
+    n_rows = ptr.numel() - 1
+    nnz_bound = int(ptr[-1].item()) if n_rows > 0 else 0
+    cap = int(N.load().bf_split_capacity(nnz_bound, chunk))
+    nitems = torch.empty(max(n_rows, 1), dtype=torch.int32, device=dev)
+    item_off = torch.empty(max(n_rows, 1), dtype=torch.int32, device=dev)
+    item_row = torch.empty(max(cap, 1), dtype=torch.int32, device=dev)
+    total = torch.zeros(1, dtype=torch.int32, device=dev)
+    ws = _workspace(_size_query("bf_split_plan_workspace_size", n_rows), dev)
+    N.call("bf_split_plan", _p(ptr), n_rows, chunk, _p(nitems), _p(item_off), _p(item_row), cap, _p(total),
+           _p(ws), ws.numel(), _stream(dev))
+    return SplitPlan(cap, nitems, item_off, item_row, total)
+
+
+# ------------------------------------------------------------------ attention index
+@dataclass
+class AttentionIndex:
+    """One edge set in the layout the attention kernels walk.
+
+    Query-major CSR (qptr, kv) for the forward and the dq pass; the key-major
+    reverse index (kptr, kq, ke) for the dk/dv pass is built on first use and
+    then reused by every layer and step that shares the edge set.
+    """
+    n_q: int
+    n_kv: int
+    qptr: torch.Tensor
+    kv: torch.Tensor
+    chunk: int = DEFAULT_CHUNK
+    qplan: Optional[SplitPlan] = None
+    kptr: Optional[torch.Tensor] = None
+    kq: Optional[torch.Tensor] = None
+    ke: Optional[torch.Tensor] = None
+    kplan: Optional[SplitPlan] = None
+    _rows: Optional[torch.Tensor] = field(default=None, repr=False)
+
+    @property
+    def nnz(self) -> int:
+        return self.kv.numel()
+
+    @property
+    def device(self):
+        return self.qptr.device
+
+    def ensure_forward(self):
+        if self.qplan is None:
+            self.qplan = split_plan(self.qptr, self.chunk)
+        return self
+
+    def ensure_backward(self):
+        self.ensure_forward()
+        if self.kptr is None:
+            self.kptr, self.kq, self.ke = reverse_index(self.qptr, self.kv, self.n_kv)
+        if self.kplan is None:
+            self.kplan = split_plan(self.kptr, self.chunk)
+        return self
+
+    def entry_rows(self) -> torch.Tensor:
+        """Query id of every CSR entry (int64), for per-edge bias gathers."""
+        if self._rows is None:
+            self._rows = expand_rows(self.qptr, self.nnz)
+        return self._rows
+
+    def to_coo(self) -> torch.Tensor:
+        """[2, nnz] int64 in (src, dst) order — the order PyG coalesce produces."""
+        self.ensure_backward()
+        src = expand_rows(self.kptr, self.nnz)
+        return torch.stack([src, self.kq.to(torch.int64)])
+
+    def struct(self, backward: bool) -> N.AttnIndex:
+        self.ensure_backward() if backward else self.ensure_forward()
+        s = N.AttnIndex()
+        s.n_q, s.n_kv, s.nnz = self.n_q, self.n_kv, self.nnz
+        s.qptr, s.kv = self.qptr.data_ptr(), self.kv.data_ptr() if self.nnz else None
+        s.chunk = self.chunk
+        qp = self.qplan
+        s.q_cap, s.q_nitems, s.q_item_off, s.q_item_row, s.q_total = (
+            qp.cap, qp.nitems.data_ptr(), qp.item_off.data_ptr(), qp.item_row.data_ptr(), qp.total.data_ptr())
+        if backward:
+            kp = self.kplan
+            s.kptr = self.kptr.data_ptr()
+            s.kq = self.kq.data_ptr() if self.nnz else None
+            s.ke = self.ke.data_ptr() if self.nnz else None
+            s.k_cap, s.k_nitems, s.k_item_off, s.k_item_row, s.k_total = (
+                kp.cap, kp.nitems.data_ptr(), kp.item_off.data_ptr(), kp.item_row.data_ptr(), kp.total.data_ptr())
+        return s
+
+    @classmethod
+    def from_table(cls, table, row_len, global_token: bool = False, n_kv: Optional[int] = None,
+                   chunk: int = DEFAULT_CHUNK):
+        qptr, kv = table_to_csr(table, row_len, global_token)
+        n_q = qptr.numel() - 1
+        return cls(n_q=n_q, n_kv=n_kv if n_kv is not None else n_q, qptr=qptr, kv=kv, chunk=chunk)
+
+    @classmethod
+    def from_coo(cls, edge_index, n_q: int, n_kv: Optional[int] = None, chunk: int = DEFAULT_CHUNK):
+        n_kv = n_q if n_kv is None else n_kv
+        qptr, kv = coo_to_csr(edge_index, n_q, n_kv)
+        return cls(n_q=n_q, n_kv=n_kv, qptr=qptr, kv=kv, chunk=chunk)
+
+
+# ------------------------------------------------------------------ attention
+_DT = {torch.float32: N.BF_DTYPE_F32, torch.bfloat16: N.BF_DTYPE_BF16}
+
+
+def _check_qkv(q, k, v):
+    if q.dtype not in _DT:
+        raise TypeError(f"attention supports float32 and bfloat16 activations (got {q.dtype})")
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _require(t, n, q.dtype, q.device)
+        if t.dim() != 3:
+            raise ValueError(f"{n} must be [rows, heads, head_dim] (got {tuple(t.shape)})")
+    if k.shape != v.shape or q.shape[1:] != k.shape[1:]:
+        raise ValueError(f"q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)} disagree")
+
+
+def _check_edge_tensor(t, name, idx: AttentionIndex, heads: int, device):
+    if t is None:
+        return
+    _require(t, name, torch.float32, device)
+    if tuple(t.shape) != (idx.nnz, heads):
+        raise ValueError(f"{name} must be [{idx.nnz}, {heads}] (got {tuple(t.shape)})")
+
+
+def attn_forward(idx: AttentionIndex, q, k, v, bias=None, factor=None):
+    """out [n_q,H,hn] (activation dtype), Z [n_q,H] float32."""
+    _check_qkv(q, k, v)
+    H, hn = q.shape[1], q.shape[2]
+    if q.shape[0] != idx.n_q or k.shape[0] != idx.n_kv:
+        raise ValueError(f"q rows {q.shape[0]} / kv rows {k.shape[0]} do not match index ({idx.n_q}, {idx.n_kv})")
+    if idx.device != q.device:
+        raise ValueError("index and activations are on different devices")
+    _check_edge_tensor(bias, "bias", idx, H, q.device)
+    _check_edge_tensor(factor, "factor", idx, H, q.device)
+    st = idx.struct(backward=False)
+    out = torch.empty_like(q)
+    Z = torch.empty(idx.n_q, H, dtype=torch.float32, device=q.device)
+    parts = torch.empty(max(int(N.load().bf_attn_partials_floats(C.byref(st), H, hn)), 1), dtype=torch.float32,
+                        device=q.device)
+    N.call("bf_attn_fwd", C.byref(st), _DT[q.dtype], H, hn, _p(q), _p(k), _p(v), _p(bias), _p(factor), _p(out),
+           _p(Z), _p(parts), _stream(q.device))
+    return out, Z
+
+
+def attn_backward(idx: AttentionIndex, q, k, v, out, Z, dout, bias=None, factor=None, need_dbias: bool = False):
+    """(dq, dk, dv, dbias-or-None) for attn_forward's outputs."""
+    _check_qkv(q, k, v)
+    H, hn = q.shape[1], q.shape[2]
+    _require(out, "out", q.dtype, q.device)
+    _require(dout, "dout", q.dtype, q.device)
+    _require(Z, "Z", torch.float32, q.device)
+    _check_edge_tensor(bias, "bias", idx, H, q.device)
+    _check_edge_tensor(factor, "factor", idx, H, q.device)
+    st = idx.struct(backward=True)
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    dbias = torch.empty(idx.nnz, H, dtype=torch.float32, device=q.device) if need_dbias else None
+    delta = torch.empty(idx.n_q, H, dtype=torch.float32, device=q.device)
+    parts = torch.empty(max(int(N.load().bf_attn_partials_floats(C.byref(st), H, hn)), 1), dtype=torch.float32,
+                        device=q.device)
+    N.call("bf_attn_bwd", C.byref(st), _DT[q.dtype], H, hn, _p(q), _p(k), _p(v), _p(bias), _p(factor), _p(out),
+           _p(Z), _p(dout), _p(dq), _p(dk), _p(dv), _p(dbias), _p(delta), _p(parts), _stream(q.device))
+    return dq, dk, dv, dbias

@@ -1,0 +1,232 @@
+/*
+ * budgetformer_hip.h — C ABI of the MI355X (gfx950) BudgetFormer hot path.
+ *
+ * Plain pointers and sizes only. Every pointer argument named like a tensor is
+ * device memory (HBM) unless stated otherwise; `stream` is a hipStream_t (NULL
+ * = the legacy default stream). All work is enqueued asynchronously on that
+ * stream. Every entry point returns BF_OK (0) or an error code; bf_last_error()
+ * returns the message of the last failure on the calling thread.
+ *
+ * Scratch memory is never allocated inside the library: entry points that need
+ * it take a workspace pointer and have a *_workspace_size query, so callers
+ * can draw it from their own allocator (e.g. PyTorch's caching allocator, which
+ * turns a failed allocation into torch.cuda.OutOfMemoryError as the reference's
+ * fallback handlers expect, gt_sp/utils.py:1200-1230).
+ *
+ * Reference interfaces each entry point replaces are cited as file:line
+ * relative to the cz-up/BudgetFormer source tree.
+ */
+#ifndef BUDGETFORMER_HIP_H
+#define BUDGETFORMER_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  BF_OK = 0,
+  BF_ERR_INVALID = 1,      /* bad argument (shape, range, alignment)      */
+  BF_ERR_UNSUPPORTED = 2,  /* valid but not implemented (e.g. head dim)    */
+  BF_ERR_HIP = 3           /* a HIP runtime call or kernel launch failed   */
+};
+
+enum { BF_DTYPE_F32 = 0, BF_DTYPE_BF16 = 1 };
+
+/* Library version (major*10000 + minor*100 + patch). */
+int bf_version(void);
+/* Message of the last failed call on this thread ("" if none). */
+const char* bf_last_error(void);
+
+/* Optional per-kernel timing (no reference counterpart; replaces the CUDA-event
+ * stage timers of gt_sp/comm_profiler.py:29-53 at kernel granularity). While
+ * enabled, every kernel the library launches is bracketed by a HIP event pair
+ * on its stream; bf_prof_collect waits for them and accumulates elapsed ms per
+ * kernel name, read back with bf_prof_count / bf_prof_get.                  */
+int bf_prof_enable(int32_t on);
+int bf_prof_reset(void);
+int bf_prof_collect(void);
+int32_t bf_prof_count(void);
+int bf_prof_get(int32_t i, const char** name, double* total_ms, int64_t* launches);
+
+/* ======================================================================
+ * Edge construction
+ * ====================================================================== */
+
+/* Uniform first-order random walks, one lane per walk.
+ * Replaces _run_random_walk (gt_sp/utils.py:1387-1473), i.e. the
+ * torch_cluster.random_walk / dgl.sampling.random_walk call, for the starts
+ * arange(N).repeat_interleave(P) of gt_sp/utils.py:1198-1199 restricted to the
+ * query range [q_lo, q_lo+n_q).
+ *   rowptr [num_nodes+1] int64, col [E] int32: coalesced CSR (source rows).
+ *   u: NULL, or float32 [n_q*P, L] injected uniforms (row (q-q_lo)*P+p);
+ *      when NULL, u comes from Philox4x32-10 keyed by philox_seed with
+ *      counter (global walk id q*P+p, philox_offset + l/4).
+ *   walks: int64 [n_q*P, L+1]; walks[:,0] = start; a dead end stays.
+ * Step rule: idx = (int64)(u * (float)deg) in fp32, clamped to deg-1.      */
+int bf_random_walk(const int64_t* rowptr, const int32_t* col, int64_t num_nodes,
+                   int64_t q_lo, int64_t n_q, int32_t walks_per_node, int32_t walk_length,
+                   const float* u, uint64_t philox_seed, uint64_t philox_offset,
+                   int64_t* walks, void* stream);
+
+/* The Philox uniforms bf_random_walk draws when u == NULL, written as the
+ * float32 [n_q*P, L] tensor that reproduces them through the u argument. */
+int bf_walk_uniforms(int64_t q_lo, int64_t n_q, int32_t walks_per_node, int32_t walk_length,
+                     uint64_t philox_seed, uint64_t philox_offset, float* u, void* stream);
+
+/* Per-query top-k of the random-walk pool, fused with the walk.
+ * Replaces build_head_hop_edges (gt_sp/utils.py:1251-1278) +
+ * compute_hop_buckets_random_walk's hop loop (gt_sp/utils.py:1232-1248) +
+ * _sample_edges_per_query_random(pool, k_rw, edge_seed+37)
+ * (utils/fullgraph_sp_support.py:1494-1517, 1195-1228): for query q the pool
+ * holds (walks[w,d], q) for its own walks w, d=1..L, kept iff d==1 or the walk
+ * moved at step d; the k_rw smallest keys key(kv, q, seed) are kept counting
+ * multiplicity. Output sel_kv int32 [n_q, k_rw] (key order, -1 padded),
+ * sel_cnt int32 [n_q]. Requires P*L <= 64.                                   */
+int bf_rw_select(const int64_t* rowptr, const int32_t* col, int64_t num_nodes,
+                 int64_t q_lo, int64_t n_q, int32_t walks_per_node, int32_t walk_length,
+                 int32_t k_rw, int64_t key_seed, const float* u, uint64_t philox_seed,
+                 uint64_t philox_offset, int32_t* sel_kv, int32_t* sel_cnt, void* stream);
+
+/* Per-query top-k of the real (graph) edges merged with an RW selection into
+ * the query-major table. Replaces _sample_edges_per_query_random(edge_index,
+ * k_real, edge_seed+17) (utils/fullgraph_sp_support.py:1312-1491, 1195-1228)
+ * followed by _merge_edge_index_list (gt_sp/utils.py:877-887) as used by
+ * _build_merged_edges (utils/fullgraph_sp_support.py:2943-3026).
+ *   in_ptr [num_nodes+1] int64, in_src int32: in-neighbour CSR (row q lists the
+ *     sources of edges into q; equals the CSR for a symmetric graph).
+ *   k_real <= 0 drops the real part; rw_kv/rw_cnt NULL (or k_rw 0) drops the
+ *   RW part. dedup != 0 merges as a set (the reference coalesces when both
+ *   parts are globally non-empty); dedup == 0 keeps duplicates.
+ *   table int32 [n_q, width] rows ascending, -1 padded; row_len int32 [n_q].
+ *   Requires k_real <= 32, k_rw <= 32, width >= k_real + k_rw.               */
+int bf_real_select_merge(const int64_t* in_ptr, const int32_t* in_src, int64_t num_nodes,
+                         int64_t q_lo, int64_t n_q, int32_t k_real, int64_t key_seed,
+                         const int32_t* rw_kv, const int32_t* rw_cnt, int32_t k_rw,
+                         int32_t dedup, int32_t* table, int32_t width, int32_t* row_len,
+                         void* stream);
+
+/* Whole budgeted build: bf_rw_select then bf_real_select_merge with
+ * key seeds edge_seed+37 / edge_seed+17 (utils/fullgraph_sp_support.py:970-972,
+ * 1413, 1514) and the reference's global merge rule (dedup iff both parts are
+ * non-empty). Replaces _build_merged_edges (utils/fullgraph_sp_support.py:
+ * 2943-3026) without the Graphormer token. width = k_real + k_rw.
+ * Workspace: bf_build_edge_table_workspace_size.                            */
+int bf_build_edge_table_workspace_size(int64_t n_q, int32_t k_rw, size_t* bytes);
+int bf_build_edge_table(const int64_t* rowptr, const int32_t* col,
+                        const int64_t* in_ptr, const int32_t* in_src, int64_t num_nodes,
+                        int64_t num_edges, int64_t q_lo, int64_t n_q,
+                        int32_t walks_per_node, int32_t walk_length,
+                        int32_t k_real, int32_t k_rw, int64_t edge_seed,
+                        const float* u, uint64_t philox_seed, uint64_t philox_offset,
+                        int32_t* table, int32_t* row_len,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* ======================================================================
+ * Edge index formats
+ * ====================================================================== */
+
+/* Query-major table -> attention CSR (qptr int64 [n_q+1], kv int32 [nnz]).
+ * global_token != 0 applies the Graphormer virtual node (fix_edge_index,
+ * gt_sp/utils.py:113-130): ids shift by one, query 0 attends to kv 1..n_rows,
+ * every query t >= 1 also attends to kv 0; then n_q = n_rows + 1.
+ * nnz = sum(row_len) (+ 2*n_rows with the token); bf_table_csr_nnz gives it on
+ * the host (it synchronises the stream). Workspace: bf_scan_workspace_size(n_q+1). */
+int bf_table_csr_nnz(const int32_t* row_len, int64_t n_rows, int32_t global_token,
+                     int64_t* nnz_host, void* workspace, size_t workspace_bytes, void* stream);
+int bf_table_to_csr(const int32_t* table, const int32_t* row_len, int64_t n_rows, int32_t width,
+                    int32_t global_token, int64_t* qptr, int32_t* kv,
+                    void* workspace, size_t workspace_bytes, void* stream);
+int bf_scan_workspace_size(int64_t n, size_t* bytes);
+
+/* Reference COO edge_index [2, nnz] (row 0 = key/value node, row 1 = query
+ * node; models/graphormer_dist_node_level.py:231-232) -> attention CSR with
+ * rows ascending in kv. Workspace: bf_coo_to_csr_workspace_size.            */
+int bf_coo_to_csr_workspace_size(int64_t nnz, int64_t n_q, size_t* bytes);
+int bf_coo_to_csr(const int64_t* src, const int64_t* dst, int64_t nnz, int64_t n_q, int64_t n_kv,
+                  int64_t* qptr, int32_t* kv, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Reverse (key-major) index of an attention CSR: kptr int64 [n_kv+1], and for
+ * each reverse entry its query kq int32 [nnz] and its CSR position ke int32
+ * [nnz], sorted by (kv, position) — i.e. by (src, dst), the order PyG's
+ * coalesce gives (gt_sp/utils.py:887). Drives the deterministic dK/dV pass and
+ * the COO adaptor. Workspace: bf_reverse_index_workspace_size.              */
+int bf_reverse_index_workspace_size(int64_t nnz, int64_t n_kv, size_t* bytes);
+int bf_reverse_index(const int64_t* qptr, const int32_t* kv, int64_t n_q, int64_t n_kv, int64_t nnz,
+                     int64_t* kptr, int32_t* kq, int32_t* ke,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* Row id of every entry of a CSR (rows[i] = r for ptr[r] <= i < ptr[r+1]). */
+int bf_expand_rows(const int64_t* ptr, int64_t n_rows, int64_t nnz, int64_t* rows, void* stream);
+
+/* Split plan for rows longer than `chunk`: such a row is processed as
+ * ceil(len/chunk) items whose partial sums are reduced in a fixed order.
+ *   nitems int32 [n_rows] (0 for short rows), item_off int32 [n_rows],
+ *   item_row int32 [cap], total int32 [1] (device), cap = bf_split_capacity. */
+int64_t bf_split_capacity(int64_t nnz, int32_t chunk);
+int bf_split_plan_workspace_size(int64_t n_rows, size_t* bytes);
+int bf_split_plan(const int64_t* ptr, int64_t n_rows, int32_t chunk, int32_t* nitems,
+                  int32_t* item_off, int32_t* item_row, int64_t cap, int32_t* total,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* ======================================================================
+ * Sparse edge attention
+ * ====================================================================== */
+
+/* Everything the attention kernels need to walk one edge set. */
+typedef struct bf_attn_index {
+  int64_t n_q;              /* queries (rows of qptr)                         */
+  int64_t n_kv;             /* key/value rows                                  */
+  int64_t nnz;              /* edges                                           */
+  const int64_t* qptr;      /* [n_q+1]                                         */
+  const int32_t* kv;        /* [nnz]   kv id per edge, query-major             */
+  const int64_t* kptr;      /* [n_kv+1] reverse offsets (backward only)        */
+  const int32_t* kq;        /* [nnz]   query per reverse entry (backward only) */
+  const int32_t* ke;        /* [nnz]   CSR position per reverse entry          */
+  int32_t chunk;            /* split threshold used by both plans              */
+  int32_t q_cap;            /* capacity of the query-side plan                 */
+  const int32_t* q_nitems;  /* query-side split plan (bf_split_plan on qptr)   */
+  const int32_t* q_item_off;
+  const int32_t* q_item_row;
+  const int32_t* q_total;
+  int32_t k_cap;            /* capacity of the kv-side plan                    */
+  const int32_t* k_nitems;  /* kv-side split plan (bf_split_plan on kptr)      */
+  const int32_t* k_item_off;
+  const int32_t* k_item_row;
+  const int32_t* k_total;
+} bf_attn_index;
+
+/* float32 scratch the attention calls need for split rows. */
+int64_t bf_attn_partials_floats(const bf_attn_index* idx, int32_t num_heads, int32_t head_dim);
+
+/* Forward. Replaces CoreAttention.sparse_attention_bias
+ * (models/graphormer_dist_node_level.py:155-265; GT models/gt_dist_node_level.py:
+ * 179-262; GraphGPS models/graphgps_dist_node_level.py:151-177) on one edge set:
+ *   a = clamp(sum_j k[s,h,j]*q[t,h,j]/sqrt(hn), -5, 5) [+ bias[e,h]],
+ *   p = exp(a), Z[t,h] = sum_e p, out[t,h,:] = sum_e p*f[e,h]*v[s,h,:] / (Z+1e-6)
+ * with f = factor (GPS dropout keep*scale) or 1.
+ *   q [n_q, H*hn], k, v [n_kv, H*hn] in `dtype`, rows 16-byte aligned;
+ *   bias, factor: NULL or float32 [nnz, H] (per CSR position);
+ *   out [n_q, H*hn] in `dtype`; Z float32 [n_q, H];
+ *   partials: float32 [bf_attn_partials_floats].                           */
+int bf_attn_fwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
+                const void* q, const void* k, const void* v, const float* bias, const float* factor,
+                void* out, float* Z, float* partials, void* stream);
+
+/* Backward of bf_attn_fwd (the autograd of the reference graph of ops,
+ * models/graphormer_dist_node_level.py:231-263). Deterministic: dq by a
+ * query-major pass, dk/dv by a key-major pass over the reverse index; no atomics.
+ *   dbias: NULL or float32 [nnz, H]; delta: float32 [n_q, H] scratch.        */
+int bf_attn_bwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
+                const void* q, const void* k, const void* v, const float* bias, const float* factor,
+                const void* out, const float* Z, const void* dout,
+                void* dq, void* dk, void* dv, float* dbias, float* delta, float* partials,
+                void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BUDGETFORMER_HIP_H */

@@ -1,0 +1,56 @@
+"""CPU checks of the C ABI: the library loads, exports every declared symbol,
+and its host-side argument checks reject bad calls without touching a GPU."""
+import ctypes as C
+import re
+
+import pytest
+
+from budgetformer_amd import _native as N
+
+
+def test_library_loads_and_exports_every_header_symbol():
+    lib = N.load()
+    names = N.header_functions()
+    assert len(names) >= 20
+    for name in names:
+        assert hasattr(lib, name), name
+        assert name in N._SIGS, f"{name} has no ctypes signature"
+    assert lib.bf_version() >= 100
+
+
+def test_every_entry_point_cites_the_reference():
+    text = open(N._HEADER).read()
+    for fn in ("bf_random_walk", "bf_rw_select", "bf_real_select_merge", "bf_build_edge_table",
+               "bf_table_to_csr", "bf_coo_to_csr", "bf_reverse_index", "bf_attn_fwd", "bf_attn_bwd"):
+        pos = text.index(fn + "(")
+        block = text[max(0, text.rfind("/*", 0, pos)):pos]
+        assert re.search(r"\w+\.py:\d+", block), fn
+
+
+def test_argument_errors_surface_as_exceptions():
+    lib = N.load()
+    rc = lib.bf_random_walk(None, None, 10, 0, 5, 2, 4, None, 0, 0, None, None)
+    assert rc == N.BF_ERR_INVALID
+    assert b"row pointer" in lib.bf_last_error()
+    with pytest.raises(ValueError):
+        N.call("bf_rw_select", None, None, 10, 0, 5, 2, 4, 4, 0, None, 0, 0, None, None, None)
+    idx = N.AttnIndex()
+    with pytest.raises(NotImplementedError):     # head_dim 6 does not split into 16-byte lanes
+        N.call("bf_attn_fwd", C.byref(idx), N.BF_DTYPE_F32, 2, 6, None, None, None, None, None, None, None, None,
+               None)
+
+
+def test_split_capacity_bound():
+    lib = N.load()
+    for nnz, chunk in ((0, 64), (63, 64), (1000, 7), (10 ** 9, 256)):
+        cap = lib.bf_split_capacity(nnz, chunk)
+        # rows are split only when longer than chunk: sum(ceil(len/chunk)) <= 2*nnz/chunk
+        assert cap >= 2 * (nnz // chunk)
+
+
+def test_workspace_queries_run_on_cpu():
+    out = C.c_size_t(0)
+    N.call("bf_reverse_index_workspace_size", 1000, 100, C.byref(out))
+    assert out.value >= 3 * 1000 * 4
+    N.call("bf_build_edge_table_workspace_size", 1000, 4, C.byref(out))
+    assert out.value >= 1000 * 4 * 4
