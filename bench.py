@@ -65,6 +65,27 @@ def kernel_bytes(s, D, H, lens_q, lens_k, chunk):
     }
 
 
+def rocprof_summary(stats_csv: str, top: int = 25) -> str:
+    """Markdown table of a rocprofv3 ``*_kernel_stats.csv`` (kernel, calls, avg/min/max us, share)."""
+    import csv
+    import re
+    rows = list(csv.DictReader(open(stats_csv)))
+    out = ["| kernel | calls | avg us | min us | max us | % of GPU time |", "|---|---:|---:|---:|---:|---:|"]
+    for r in rows[:top]:
+        name = r["Name"]
+        m = re.search(r"(\w+_kernel)\b", name)
+        if "rocprim" in name:
+            kind = re.search(r"detail::(radix_sort_onesweep_\w+?|scan_impl|init_lookback\w*?)[<(]", name)
+            short = "rocprim::" + (kind.group(1) if kind else "kernel")
+        elif m:
+            short = m.group(1) + ("<bf16>" if "<unsigned short>" in name else "<float>" if "<float>" in name else "")
+        else:
+            short = name.split("(")[0][:60]
+        out.append(f"| {short} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | {float(r['MinNs']) / 1e3:.2f} | "
+                   f"{float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.2f} |")
+    return "\n".join(out)
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -83,7 +104,14 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
+    ap.add_argument("--chunk", type=int, default=None, help="split threshold (rows longer than this are split)")
+    ap.add_argument("--item", type=int, default=None, help="entries per split item")
+    ap.add_argument("--rocprof-summary", metavar="KERNEL_STATS_CSV",
+                    help="print a markdown summary of a rocprofv3 kernel_stats.csv and exit")
     args = ap.parse_args(argv)
+    if args.rocprof_summary:
+        print(rocprof_summary(args.rocprof_summary))
+        return 0
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the path would shard "
               f"by query range (see the sharding design), but no multi-GPU figure is produced here.",
@@ -119,11 +147,14 @@ def main(argv=None):
     torch.cuda.synchronize()
     print(f"[bench] {cfg['name']}: realized E={g.num_edges:,}; setup {time.time() - t_setup:.1f}s", flush=True)
 
+    chunk = args.chunk or hip_ops.DEFAULT_CHUNK
+    item = args.item or hip_ops.DEFAULT_ITEM
+
     def build():
         tab = build_attention_edges(g, real_edges_per_query=cfg["b_r"], rw_edges_per_query=cfg["b_w"],
                                     walk_length=cfg["L"], walks_per_node=cfg["P"], edge_seed=42,
                                     global_token=cfg["token"])
-        idx = tab.attention_index()
+        idx = tab.attention_index(chunk=chunk, item=item)
         idx.ensure_backward()
         return tab, idx
 
@@ -200,7 +231,7 @@ def main(argv=None):
         "config": {"workload": cfg["name"], "num_nodes": n, "num_edges": g.num_edges, "queries": S,
                    "table_entries": table_entries, "attention_edges": nnz, "heads": H, "head_dim": hn,
                    "walk_length": cfg["L"], "walks_per_node": cfg["P"], "budget": [cfg["b_r"], cfg["b_w"]],
-                   "global_token": cfg["token"]},
+                   "global_token": cfg["token"], "split_chunk": chunk, "split_item": item},
         "attn_fwd_bwd_ms": round(attn_ms, 4),
         "attn_algorithmic_bytes": a_fwd + a_bwd,
         "attn_frac_of_hbm_peak": round(attn_gbs / HBM_PEAK_GBS, 4),

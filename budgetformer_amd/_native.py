@@ -9,9 +9,10 @@ import ctypes as C
 import os
 import re
 
-from . import build as _build
-
-_HEADER = os.path.join(_build.ROOT, "include", "budgetformer_hip.h")
+_PKG = os.path.dirname(os.path.abspath(__file__))
+_ROOT = os.path.dirname(_PKG)
+_HEADER = os.path.join(_ROOT, "include", "budgetformer_hip.h")
+_LIB = os.path.join(_PKG, "_lib", "libbudgetformer_hip.so")
 
 BF_OK, BF_ERR_INVALID, BF_ERR_UNSUPPORTED, BF_ERR_HIP = 0, 1, 2, 3
 BF_DTYPE_F32, BF_DTYPE_BF16 = 0, 1
@@ -28,10 +29,11 @@ class AttnIndex(C.Structure):
     _fields_ = [
         ("n_q", i64), ("n_kv", i64), ("nnz", i64),
         ("qptr", vp), ("kv", vp), ("kptr", vp), ("kq", vp), ("ke", vp),
-        ("chunk", i32), ("q_cap", i32),
-        ("q_nitems", vp), ("q_item_off", vp), ("q_item_row", vp), ("q_total", vp),
-        ("k_cap", i32),
-        ("k_nitems", vp), ("k_item_off", vp), ("k_item_row", vp), ("k_total", vp),
+        ("chunk", i32), ("item", i32),
+        ("q_items", i32), ("q_heavy", i32),
+        ("q_nitems", vp), ("q_item_off", vp), ("q_item_row", vp), ("q_heavy_rows", vp),
+        ("k_items", i32), ("k_heavy", i32),
+        ("k_nitems", vp), ("k_item_off", vp), ("k_item_row", vp), ("k_heavy_rows", vp),
     ]
 
 
@@ -52,17 +54,18 @@ _SIGS = {
     "bf_build_edge_table_workspace_size": (C.c_int, [i64, i32, C.POINTER(sz)]),
     "bf_build_edge_table": (C.c_int, [P_i64, P_i32, P_i64, P_i32, i64, i64, i64, i64, i32, i32, i32, i32, i64,
                                       P_f32, u64, u64, P_i32, P_i32, vp, sz, vp]),
-    "bf_table_csr_nnz": (C.c_int, [P_i32, i64, i32, C.POINTER(i64), vp, sz, vp]),
-    "bf_table_to_csr": (C.c_int, [P_i32, P_i32, i64, i32, i32, P_i64, P_i32, vp, sz, vp]),
+    "bf_table_csr_ptr": (C.c_int, [P_i32, i64, i32, P_i64, C.POINTER(i64), vp, sz, vp]),
+    "bf_table_to_csr": (C.c_int, [P_i32, P_i32, i64, i32, i32, P_i64, P_i32, vp]),
     "bf_scan_workspace_size": (C.c_int, [i64, C.POINTER(sz)]),
     "bf_coo_to_csr_workspace_size": (C.c_int, [i64, i64, C.POINTER(sz)]),
     "bf_coo_to_csr": (C.c_int, [P_i64, P_i64, i64, i64, i64, P_i64, P_i32, vp, sz, vp]),
     "bf_reverse_index_workspace_size": (C.c_int, [i64, i64, C.POINTER(sz)]),
     "bf_reverse_index": (C.c_int, [P_i64, P_i32, i64, i64, i64, P_i64, P_i32, P_i32, vp, sz, vp]),
     "bf_expand_rows": (C.c_int, [P_i64, i64, i64, P_i64, vp]),
-    "bf_split_capacity": (i64, [i64, i32]),
+    "bf_split_item_capacity": (i64, [i64, i32, i32]),
+    "bf_split_row_capacity": (i64, [i64, i32]),
     "bf_split_plan_workspace_size": (C.c_int, [i64, C.POINTER(sz)]),
-    "bf_split_plan": (C.c_int, [P_i64, i64, i32, P_i32, P_i32, P_i32, i64, P_i32, vp, sz, vp]),
+    "bf_split_plan": (C.c_int, [P_i64, i64, i32, i32, P_i32, P_i32, P_i32, i64, P_i32, i64, P_i32, vp, sz, vp]),
     "bf_attn_partials_floats": (i64, [C.POINTER(AttnIndex), i32, i32]),
     "bf_attn_fwd": (C.c_int, [C.POINTER(AttnIndex), i32, i32, i32, vp, vp, vp, P_f32, P_f32, vp, P_f32, P_f32, vp]),
     "bf_attn_bwd": (C.c_int, [C.POINTER(AttnIndex), i32, i32, i32, vp, vp, vp, P_f32, P_f32, vp, P_f32, vp,
@@ -80,7 +83,7 @@ def header_functions() -> list:
 
 
 def lib_path() -> str:
-    return _build.lib_path()
+    return _LIB
 
 
 def load():

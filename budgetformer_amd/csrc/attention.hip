@@ -160,26 +160,127 @@ __global__ __launch_bounds__(kBlock) void attn_fwd_rows_kernel(
   }
 }
 
+// A split item: entries [beg, end) of one long row, processed by a whole
+// workgroup; each LPR-lane group takes a contiguous sub-range and the groups'
+// sums are combined through LDS in group order.
 struct Items {
   const int64_t* ptr;
   const int32_t* item_off;
   const int32_t* item_row;
   const int32_t* nitems;
-  const int32_t* total;
-  int chunk;
-  int stride;     // floats per partial record
+  const int32_t* heavy_rows;
+  int item_size;
+  int stride;     // floats per partial record: 2*D + H
 };
 
-// Resolves a split item to (row, beg, end); false if past the plan's end.
-__device__ __forceinline__ bool item_range(const Items& it, int64_t item, int& row, int& j,
-                                           int64_t& beg, int64_t& end) {
-  if (item >= *it.total) return false;
-  row = it.item_row[item];
-  j = int(item - it.item_off[row]);
-  const int64_t rb = it.ptr[row], re = it.ptr[row + 1];
-  beg = rb + int64_t(j) * it.chunk;
-  end = min(beg + it.chunk, re);
-  return true;
+struct ItemRange {
+  int row;
+  int j;          // item index within its row
+  int64_t beg;    // this group's sub-range
+  int64_t end;
+};
+
+__device__ __forceinline__ ItemRange item_group_range(const Items& it, const Shape& sh) {
+  const int64_t item = blockIdx.x;
+  ItemRange r;
+  r.row = it.item_row[item];
+  r.j = int(item - it.item_off[r.row]);
+  const int64_t rb = it.ptr[r.row], re = it.ptr[r.row + 1];
+  const int64_t ib = rb + int64_t(r.j) * it.item_size;
+  const int64_t ie = min(ib + int64_t(it.item_size), re);
+  const int gpb = kBlock >> sh.lpr_log2;
+  const int grp = threadIdx.x >> sh.lpr_log2;
+  const int64_t sub = (int64_t(it.item_size) + gpb - 1) / gpb;
+  r.beg = min(ib + grp * sub, ie);
+  r.end = min(r.beg + sub, ie);
+  return r;
+}
+
+// Sums `nv` lane vectors of V floats (and, if with_z, one float per head) over
+// the groups of the workgroup, in group order. Every thread must call it; the
+// result is valid in group 0.
+template <int V>
+__device__ __forceinline__ void block_combine(float* lds, int stride, const Shape& sh, const GroupPos& g,
+                                              float (&a)[V], float (&b)[V], bool with_b, float& z, bool with_z) {
+  const int gpb = kBlock >> sh.lpr_log2;
+  const int grp = threadIdx.x >> sh.lpr_log2;
+  float* rec = lds + grp * stride;
+  if (g.act) {
+#pragma unroll
+    for (int i = 0; i < V; ++i) rec[g.col0 + i] = a[i];
+    if (with_b) {
+#pragma unroll
+      for (int i = 0; i < V; ++i) rec[sh.D + g.col0 + i] = b[i];
+    }
+    if (with_z && g.lead) rec[2 * sh.D + g.head] = z;
+  }
+  __syncthreads();
+  if (grp == 0 && g.act) {
+#pragma unroll
+    for (int i = 0; i < V; ++i) a[i] = 0.f;
+    if (with_b) {
+#pragma unroll
+      for (int i = 0; i < V; ++i) b[i] = 0.f;
+    }
+    z = 0.f;
+    for (int gg = 0; gg < gpb; ++gg) {
+      const float* r = lds + gg * stride;
+#pragma unroll
+      for (int i = 0; i < V; ++i) a[i] += r[g.col0 + i];
+      if (with_b) {
+#pragma unroll
+        for (int i = 0; i < V; ++i) b[i] += r[sh.D + g.col0 + i];
+      }
+      if (with_z) z += r[2 * sh.D + g.head];
+    }
+  }
+}
+
+// Writes group 0's combined record for the current item.
+template <int V>
+__device__ __forceinline__ void store_record(float* partials, int stride, const Shape& sh, const GroupPos& g,
+                                             const float (&a)[V], const float (&b)[V], bool with_b, float z,
+                                             bool with_z) {
+  const int grp = threadIdx.x >> sh.lpr_log2;
+  if (grp != 0 || !g.act) return;
+  float* rec = partials + int64_t(blockIdx.x) * stride;
+#pragma unroll
+  for (int i = 0; i < V; ++i) rec[g.col0 + i] = a[i];
+  if (with_b) {
+#pragma unroll
+    for (int i = 0; i < V; ++i) rec[sh.D + g.col0 + i] = b[i];
+  }
+  if (with_z && g.lead) rec[2 * sh.D + g.head] = z;
+}
+
+// Sums the records of one split row (workgroup per row, groups strided over
+// items, then combined in group order). Result valid in group 0.
+template <int V>
+__device__ __forceinline__ int reduce_row_records(const float* __restrict__ partials, float* lds, const Items& it,
+                                                  const Shape& sh, const GroupPos& g, float (&a)[V], float (&b)[V],
+                                                  bool with_b, float& z, bool with_z) {
+  const int row = it.heavy_rows[blockIdx.x];
+  const int64_t first = it.item_off[row];
+  const int n = it.nitems[row];
+  const int gpb = kBlock >> sh.lpr_log2;
+  const int grp = threadIdx.x >> sh.lpr_log2;
+#pragma unroll
+  for (int i = 0; i < V; ++i) a[i] = b[i] = 0.f;
+  z = 0.f;
+  if (g.act) {
+    for (int m = grp; m < n; m += gpb) {
+      const float* rec = partials + (first + m) * it.stride;
+#pragma unroll
+      for (int i = 0; i < V; ++i) a[i] += rec[g.col0 + i];
+      if (with_b) {
+#pragma unroll
+        for (int i = 0; i < V; ++i) b[i] += rec[sh.D + g.col0 + i];
+      }
+      if (with_z) z += rec[2 * sh.D + g.head];
+    }
+  }
+  block_combine<V>(lds, it.stride, sh, g, a, b, with_b, z, with_z);
+  return row;
 }
 
 template <typename T>
@@ -188,46 +289,28 @@ __global__ __launch_bounds__(kBlock) void attn_fwd_items_kernel(
     const int32_t* __restrict__ kv, const float* __restrict__ bias,
     const float* __restrict__ factor, float* __restrict__ partials, Items it, Shape sh) {
   constexpr int V = Elem<T>::kPerVec;
-  const int64_t item = group_index(sh);
-  int row, j;
-  int64_t beg, end;
-  if (!item_range(it, item, row, j, beg, end)) return;
+  extern __shared__ float lds[];
+  const ItemRange r = item_group_range(it, sh);
   const GroupPos g = group_pos<T>(sh);
-  float qv[V], acc[V];
-  load_row<T, V>(q, row, sh.D, g, qv);
+  float qv[V], acc[V], unused[V];
+  load_row<T, V>(q, r.row, sh.D, g, qv);
 #pragma unroll
-  for (int i = 0; i < V; ++i) acc[i] = 0.f;
+  for (int i = 0; i < V; ++i) acc[i] = unused[i] = 0.f;
   float z = 0.f;
-  fwd_segment<T>(k, v, kv, bias, factor, beg, end, sh, g, qv, acc, z);
-  float* rec = partials + item * it.stride;
-  if (g.act) {
-#pragma unroll
-    for (int i = 0; i < V; ++i) rec[g.col0 + i] = acc[i];
-    if (g.lead) rec[sh.D + g.head] = z;
-  }
+  fwd_segment<T>(k, v, kv, bias, factor, r.beg, r.end, sh, g, qv, acc, z);
+  block_combine<V>(lds, it.stride, sh, g, acc, unused, false, z, true);
+  store_record<V>(partials, it.stride, sh, g, acc, unused, false, z, true);
 }
 
 template <typename T>
 __global__ __launch_bounds__(kBlock) void attn_fwd_reduce_kernel(
     const float* __restrict__ partials, T* __restrict__ out, float* __restrict__ Z, Items it, Shape sh) {
   constexpr int V = Elem<T>::kPerVec;
-  const int64_t item = group_index(sh);
-  int row, j;
-  int64_t beg, end;
-  if (!item_range(it, item, row, j, beg, end) || j != 0) return;
+  extern __shared__ float lds[];
   const GroupPos g = group_pos<T>(sh);
-  if (!g.act) return;
-  const int n = it.nitems[row];
-  float acc[V];
-  float z = 0.f;
-#pragma unroll
-  for (int i = 0; i < V; ++i) acc[i] = 0.f;
-  for (int m = 0; m < n; ++m) {
-    const float* rec = partials + (item + m) * it.stride;
-#pragma unroll
-    for (int i = 0; i < V; ++i) acc[i] += rec[g.col0 + i];
-    z += rec[sh.D + g.head];
-  }
+  float acc[V], unused[V], z;
+  const int row = reduce_row_records<V>(partials, lds, it, sh, g, acc, unused, false, z, true);
+  if ((threadIdx.x >> sh.lpr_log2) != 0 || !g.act) return;
   const float den = z + kEps;
   float o[V];
 #pragma unroll
@@ -364,44 +447,30 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_q_items_kernel(
     const T* __restrict__ dout, float* __restrict__ dbias, float* __restrict__ delta,
     float* __restrict__ partials, Items it, Shape sh) {
   constexpr int V = Elem<T>::kPerVec;
-  const int64_t item = group_index(sh);
-  int row, j;
-  int64_t beg, end;
-  if (!item_range(it, item, row, j, beg, end)) return;
+  extern __shared__ float lds[];
+  const ItemRange r = item_group_range(it, sh);
   const GroupPos g = group_pos<T>(sh);
-  float qv[V], gv[V], acc[V];
-  load_row<T, V>(q, row, sh.D, g, qv);
-  const RowGrad rg = row_grad<T>(out, dout, Z, row, sh, g, gv);
+  float qv[V], gv[V], acc[V], unused[V];
+  load_row<T, V>(q, r.row, sh.D, g, qv);
+  const RowGrad rg = row_grad<T>(out, dout, Z, r.row, sh, g, gv);
 #pragma unroll
-  for (int i = 0; i < V; ++i) acc[i] = 0.f;
-  dq_segment<T>(k, v, kv, bias, factor, dbias, beg, end, sh, g, rg, qv, gv, acc);
-  if (g.act) {
-    float* rec = partials + item * it.stride;
-#pragma unroll
-    for (int i = 0; i < V; ++i) rec[g.col0 + i] = acc[i];
-    if (j == 0 && g.lead) delta[int64_t(row) * sh.H + g.head] = rg.delta;
-  }
+  for (int i = 0; i < V; ++i) acc[i] = unused[i] = 0.f;
+  dq_segment<T>(k, v, kv, bias, factor, dbias, r.beg, r.end, sh, g, rg, qv, gv, acc);
+  float z = 0.f;
+  block_combine<V>(lds, it.stride, sh, g, acc, unused, false, z, false);
+  store_record<V>(partials, it.stride, sh, g, acc, unused, false, z, false);
+  if (r.j == 0 && (threadIdx.x >> sh.lpr_log2) == 0 && g.lead) delta[int64_t(r.row) * sh.H + g.head] = rg.delta;
 }
 
 template <typename T>
 __global__ __launch_bounds__(kBlock) void attn_bwd_q_reduce_kernel(
     const float* __restrict__ partials, T* __restrict__ dq, Items it, Shape sh) {
   constexpr int V = Elem<T>::kPerVec;
-  const int64_t item = group_index(sh);
-  int row, j;
-  int64_t beg, end;
-  if (!item_range(it, item, row, j, beg, end) || j != 0) return;
+  extern __shared__ float lds[];
   const GroupPos g = group_pos<T>(sh);
-  if (!g.act) return;
-  const int n = it.nitems[row];
-  float acc[V];
-#pragma unroll
-  for (int i = 0; i < V; ++i) acc[i] = 0.f;
-  for (int m = 0; m < n; ++m) {
-    const float* rec = partials + (item + m) * it.stride;
-#pragma unroll
-    for (int i = 0; i < V; ++i) acc[i] += rec[g.col0 + i];
-  }
+  float acc[V], unused[V], z;
+  const int row = reduce_row_records<V>(partials, lds, it, sh, g, acc, unused, false, z, false);
+  if ((threadIdx.x >> sh.lpr_log2) != 0 || !g.act) return;
   Elem<T>::store(dq + int64_t(row) * sh.D + g.col0, acc);
 }
 
@@ -520,49 +589,29 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_items_kernel(
     const float* __restrict__ Z, const T* __restrict__ dout, const float* __restrict__ delta,
     float* __restrict__ partials, Items it, Shape sh) {
   constexpr int V = Elem<T>::kPerVec;
-  const int64_t item = group_index(sh);
-  int row, j;
-  int64_t beg, end;
-  if (!item_range(it, item, row, j, beg, end)) return;
+  extern __shared__ float lds[];
+  const ItemRange r = item_group_range(it, sh);
   const GroupPos g = group_pos<T>(sh);
   float kk[V], vv[V], ak[V], av[V];
-  load_row<T, V>(k, row, sh.D, g, kk);
-  load_row<T, V>(v, row, sh.D, g, vv);
+  load_row<T, V>(k, r.row, sh.D, g, kk);
+  load_row<T, V>(v, r.row, sh.D, g, vv);
 #pragma unroll
   for (int i = 0; i < V; ++i) ak[i] = av[i] = 0.f;
-  dkv_segment<T>(q, dout, kq, ke, bias, factor, Z, delta, beg, end, sh, g, kk, vv, ak, av);
-  if (g.act) {
-    float* rec = partials + item * it.stride;
-#pragma unroll
-    for (int i = 0; i < V; ++i) {
-      rec[g.col0 + i] = ak[i];
-      rec[sh.D + g.col0 + i] = av[i];
-    }
-  }
+  dkv_segment<T>(q, dout, kq, ke, bias, factor, Z, delta, r.beg, r.end, sh, g, kk, vv, ak, av);
+  float z = 0.f;
+  block_combine<V>(lds, it.stride, sh, g, ak, av, true, z, false);
+  store_record<V>(partials, it.stride, sh, g, ak, av, true, z, false);
 }
 
 template <typename T>
 __global__ __launch_bounds__(kBlock) void attn_bwd_kv_reduce_kernel(
     const float* __restrict__ partials, T* __restrict__ dk, T* __restrict__ dv, Items it, Shape sh) {
   constexpr int V = Elem<T>::kPerVec;
-  const int64_t item = group_index(sh);
-  int row, j;
-  int64_t beg, end;
-  if (!item_range(it, item, row, j, beg, end) || j != 0) return;
+  extern __shared__ float lds[];
   const GroupPos g = group_pos<T>(sh);
-  if (!g.act) return;
-  const int n = it.nitems[row];
-  float ak[V], av[V];
-#pragma unroll
-  for (int i = 0; i < V; ++i) ak[i] = av[i] = 0.f;
-  for (int m = 0; m < n; ++m) {
-    const float* rec = partials + (item + m) * it.stride;
-#pragma unroll
-    for (int i = 0; i < V; ++i) {
-      ak[i] += rec[g.col0 + i];
-      av[i] += rec[sh.D + g.col0 + i];
-    }
-  }
+  float ak[V], av[V], z;
+  const int row = reduce_row_records<V>(partials, lds, it, sh, g, ak, av, true, z, false);
+  if ((threadIdx.x >> sh.lpr_log2) != 0 || !g.act) return;
   Elem<T>::store(dk + int64_t(row) * sh.D + g.col0, ak);
   Elem<T>::store(dv + int64_t(row) * sh.D + g.col0, av);
 }
@@ -600,13 +649,15 @@ int check_index(const bf_attn_index* idx, bool backward) {
   BF_CHECK_ARG(idx->n_q < (int64_t(1) << 31) && idx->n_kv < (int64_t(1) << 31) &&
                    idx->nnz < (int64_t(1) << 31),
                "attention: sizes must fit int32 ids");
-  BF_CHECK_ARG(idx->chunk >= 1, "attention: chunk must be >= 1");
+  BF_CHECK_ARG(idx->chunk >= 1 && idx->item >= 1, "attention: chunk and item must be >= 1");
   BF_CHECK_ARG(idx->qptr && (idx->kv || idx->nnz == 0), "attention: qptr/kv missing");
-  BF_CHECK_ARG(idx->q_nitems && idx->q_item_off && idx->q_item_row && idx->q_total,
+  BF_CHECK_ARG(idx->q_items >= 0 && idx->q_heavy >= 0, "attention: bad query-side plan counts");
+  BF_CHECK_ARG(idx->q_items == 0 || (idx->q_nitems && idx->q_item_off && idx->q_item_row && idx->q_heavy_rows),
                "attention: query-side split plan missing");
   if (backward) {
     BF_CHECK_ARG(idx->kptr && ((idx->kq && idx->ke) || idx->nnz == 0), "attention: reverse index missing");
-    BF_CHECK_ARG(idx->k_nitems && idx->k_item_off && idx->k_item_row && idx->k_total,
+    BF_CHECK_ARG(idx->k_items >= 0 && idx->k_heavy >= 0, "attention: bad key-side plan counts");
+    BF_CHECK_ARG(idx->k_items == 0 || (idx->k_nitems && idx->k_item_off && idx->k_item_row && idx->k_heavy_rows),
                  "attention: key-side split plan missing");
   }
   return BF_OK;
@@ -619,27 +670,40 @@ inline unsigned grid_for(int64_t rows, const Shape& sh) {
   return unsigned(ceil_div(rows, per_block));
 }
 
+inline size_t combine_lds_bytes(const Shape& sh) {
+  return size_t(kBlock >> sh.lpr_log2) * size_t(2 * sh.D + sh.H) * sizeof(float);
+}
+
+inline Items query_items(const bf_attn_index* idx, const Shape& sh) {
+  return Items{idx->qptr, idx->q_item_off, idx->q_item_row, idx->q_nitems, idx->q_heavy_rows, idx->item,
+               2 * sh.D + sh.H};
+}
+
+inline Items key_items(const bf_attn_index* idx, const Shape& sh) {
+  return Items{idx->kptr, idx->k_item_off, idx->k_item_row, idx->k_nitems, idx->k_heavy_rows, idx->item,
+               2 * sh.D + sh.H};
+}
+
 template <typename T>
 int fwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const void* k, const void* v,
-             const float* bias, const float* factor, void* out, float* Z, float* partials,
-             hipStream_t st) {
+             const float* bias, const float* factor, void* out, float* Z, float* partials, hipStream_t st) {
   const T* Q = static_cast<const T*>(q);
   const T* K = static_cast<const T*>(k);
   const T* Vv = static_cast<const T*>(v);
   T* O = static_cast<T*>(out);
   if (idx->n_q > 0) {
     BF_LAUNCH("attn_fwd_rows_kernel", attn_fwd_rows_kernel<T>, dim3(grid_for(idx->n_q, sh)), dim3(kBlock), 0, st,
-                       Q, K, Vv, idx->qptr, idx->kv, bias, factor, O, Z, idx->n_q, sh, idx->chunk);
+              Q, K, Vv, idx->qptr, idx->kv, bias, factor, O, Z, idx->n_q, sh, idx->chunk);
     BF_CHECK_LAUNCH();
   }
-  if (idx->q_cap > 0) {
-    Items it{idx->qptr, idx->q_item_off, idx->q_item_row, idx->q_nitems, idx->q_total, idx->chunk,
-             2 * sh.D + sh.H};
-    BF_LAUNCH("attn_fwd_items_kernel", attn_fwd_items_kernel<T>, dim3(grid_for(idx->q_cap, sh)), dim3(kBlock), 0, st,
-                       Q, K, Vv, idx->kv, bias, factor, partials, it, sh);
+  if (idx->q_items > 0) {
+    const Items it = query_items(idx, sh);
+    const size_t lds = combine_lds_bytes(sh);
+    BF_LAUNCH("attn_fwd_items_kernel", attn_fwd_items_kernel<T>, dim3(unsigned(idx->q_items)), dim3(kBlock), lds, st,
+              Q, K, Vv, idx->kv, bias, factor, partials, it, sh);
     BF_CHECK_LAUNCH();
-    BF_LAUNCH("attn_fwd_reduce_kernel", attn_fwd_reduce_kernel<T>, dim3(grid_for(idx->q_cap, sh)), dim3(kBlock), 0, st,
-                       partials, O, Z, it, sh);
+    BF_LAUNCH("attn_fwd_reduce_kernel", attn_fwd_reduce_kernel<T>, dim3(unsigned(idx->q_heavy)), dim3(kBlock), lds,
+              st, partials, O, Z, it, sh);
     BF_CHECK_LAUNCH();
   }
   return BF_OK;
@@ -655,35 +719,35 @@ int bwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
   const T* Vv = static_cast<const T*>(v);
   const T* O = static_cast<const T*>(out);
   const T* dO = static_cast<const T*>(dout);
-  const int stride = 2 * sh.D + sh.H;
+  const size_t lds = combine_lds_bytes(sh);
   if (idx->n_q > 0) {
     BF_LAUNCH("attn_bwd_q_rows_kernel", attn_bwd_q_rows_kernel<T>, dim3(grid_for(idx->n_q, sh)), dim3(kBlock), 0, st,
-                       Q, K, Vv, idx->qptr, idx->kv, bias, factor, O, Z, dO, static_cast<T*>(dq),
-                       dbias, delta, idx->n_q, sh, idx->chunk);
+              Q, K, Vv, idx->qptr, idx->kv, bias, factor, O, Z, dO, static_cast<T*>(dq), dbias, delta, idx->n_q, sh,
+              idx->chunk);
     BF_CHECK_LAUNCH();
   }
-  if (idx->q_cap > 0) {
-    Items it{idx->qptr, idx->q_item_off, idx->q_item_row, idx->q_nitems, idx->q_total, idx->chunk, stride};
-    BF_LAUNCH("attn_bwd_q_items_kernel", attn_bwd_q_items_kernel<T>, dim3(grid_for(idx->q_cap, sh)), dim3(kBlock), 0, st,
-                       Q, K, Vv, idx->kv, bias, factor, O, Z, dO, dbias, delta, partials, it, sh);
+  if (idx->q_items > 0) {
+    const Items it = query_items(idx, sh);
+    BF_LAUNCH("attn_bwd_q_items_kernel", attn_bwd_q_items_kernel<T>, dim3(unsigned(idx->q_items)), dim3(kBlock), lds,
+              st, Q, K, Vv, idx->kv, bias, factor, O, Z, dO, dbias, delta, partials, it, sh);
     BF_CHECK_LAUNCH();
-    BF_LAUNCH("attn_bwd_q_reduce_kernel", attn_bwd_q_reduce_kernel<T>, dim3(grid_for(idx->q_cap, sh)), dim3(kBlock), 0, st,
-                       partials, static_cast<T*>(dq), it, sh);
+    BF_LAUNCH("attn_bwd_q_reduce_kernel", attn_bwd_q_reduce_kernel<T>, dim3(unsigned(idx->q_heavy)), dim3(kBlock),
+              lds, st, partials, static_cast<T*>(dq), it, sh);
     BF_CHECK_LAUNCH();
   }
   if (idx->n_kv > 0) {
-    BF_LAUNCH("attn_bwd_kv_rows_kernel", attn_bwd_kv_rows_kernel<T>, dim3(grid_for(idx->n_kv, sh)), dim3(kBlock), 0, st,
-                       Q, K, Vv, idx->kptr, idx->kq, idx->ke, bias, factor, Z, dO, delta,
-                       static_cast<T*>(dk), static_cast<T*>(dv), idx->n_kv, sh, idx->chunk);
+    BF_LAUNCH("attn_bwd_kv_rows_kernel", attn_bwd_kv_rows_kernel<T>, dim3(grid_for(idx->n_kv, sh)), dim3(kBlock), 0,
+              st, Q, K, Vv, idx->kptr, idx->kq, idx->ke, bias, factor, Z, dO, delta, static_cast<T*>(dk),
+              static_cast<T*>(dv), idx->n_kv, sh, idx->chunk);
     BF_CHECK_LAUNCH();
   }
-  if (idx->k_cap > 0) {
-    Items it{idx->kptr, idx->k_item_off, idx->k_item_row, idx->k_nitems, idx->k_total, idx->chunk, stride};
-    BF_LAUNCH("attn_bwd_kv_items_kernel", attn_bwd_kv_items_kernel<T>, dim3(grid_for(idx->k_cap, sh)), dim3(kBlock), 0, st,
-                       Q, K, Vv, idx->kq, idx->ke, bias, factor, Z, dO, delta, partials, it, sh);
+  if (idx->k_items > 0) {
+    const Items it = key_items(idx, sh);
+    BF_LAUNCH("attn_bwd_kv_items_kernel", attn_bwd_kv_items_kernel<T>, dim3(unsigned(idx->k_items)), dim3(kBlock),
+              lds, st, Q, K, Vv, idx->kq, idx->ke, bias, factor, Z, dO, delta, partials, it, sh);
     BF_CHECK_LAUNCH();
-    BF_LAUNCH("attn_bwd_kv_reduce_kernel", attn_bwd_kv_reduce_kernel<T>, dim3(grid_for(idx->k_cap, sh)), dim3(kBlock), 0, st,
-                       partials, static_cast<T*>(dk), static_cast<T*>(dv), it, sh);
+    BF_LAUNCH("attn_bwd_kv_reduce_kernel", attn_bwd_kv_reduce_kernel<T>, dim3(unsigned(idx->k_heavy)), dim3(kBlock),
+              lds, st, partials, static_cast<T*>(dk), static_cast<T*>(dv), it, sh);
     BF_CHECK_LAUNCH();
   }
   return BF_OK;
@@ -696,9 +760,9 @@ using namespace bf;
 
 extern "C" int64_t bf_attn_partials_floats(const bf_attn_index* idx, int32_t num_heads, int32_t head_dim) {
   if (!idx) return 0;
-  const int64_t cap = idx->q_cap > idx->k_cap ? idx->q_cap : idx->k_cap;
+  const int64_t items = idx->q_items > idx->k_items ? idx->q_items : idx->k_items;
   const int64_t D = int64_t(num_heads) * head_dim;
-  return cap * (2 * D + num_heads);
+  return items * (2 * D + num_heads);
 }
 
 extern "C" int bf_attn_fwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
@@ -711,7 +775,7 @@ extern "C" int bf_attn_fwd(const bf_attn_index* idx, int32_t dtype, int32_t num_
   BF_CHECK_ARG(q && k && v && out && Z, "attn_fwd: null tensor");
   BF_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out),
                "attn_fwd: q/k/v/out must be 16-byte aligned");
-  BF_CHECK_ARG(idx->q_cap == 0 || partials, "attn_fwd: partials buffer required for split rows");
+  BF_CHECK_ARG(idx->q_items == 0 || partials, "attn_fwd: partials buffer required for split rows");
   if (dtype == BF_DTYPE_F32)
     return fwd_impl<float>(idx, sh, q, k, v, bias, factor, out, Z, partials, as_stream(stream));
   return fwd_impl<uint16_t>(idx, sh, q, k, v, bias, factor, out, Z, partials, as_stream(stream));
@@ -730,7 +794,7 @@ extern "C" int bf_attn_bwd(const bf_attn_index* idx, int32_t dtype, int32_t num_
   BF_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out) && aligned16(dout) &&
                    aligned16(dq) && aligned16(dk) && aligned16(dv),
                "attn_bwd: tensors must be 16-byte aligned");
-  BF_CHECK_ARG((idx->q_cap == 0 && idx->k_cap == 0) || partials,
+  BF_CHECK_ARG((idx->q_items == 0 && idx->k_items == 0) || partials,
                "attn_bwd: partials buffer required for split rows");
   if (dtype == BF_DTYPE_F32)
     return bwd_impl<float>(idx, sh, q, k, v, bias, factor, out, Z, dout, dq, dk, dv, dbias, delta,

@@ -73,14 +73,6 @@ __global__ void token_fill_kernel(const int32_t* __restrict__ row_len, int64_t n
   if (row_len[i] == 0) kv[qptr[i + 1]] = 0;
 }
 
-__global__ void sum_lengths_kernel(const int32_t* __restrict__ row_len, int64_t n_rows,
-                                   unsigned long long* __restrict__ total) {
-  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
-  unsigned long long v = i < n_rows ? (unsigned long long)row_len[i] : 0ull;
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  if ((threadIdx.x & 63) == 0 && v) atomicAdd(total, v);
-}
-
 // ---------------------------------------------------------------- sorted keys -> row pointers
 // ptr[r] = first position i with row(i) >= r, from row ids sorted ascending.
 template <typename K>
@@ -136,30 +128,44 @@ __global__ void gather_rows_kernel(const int32_t* __restrict__ rows_of_entry, co
 }
 
 // ---------------------------------------------------------------- split plans
-__global__ void split_count_kernel(const int64_t* __restrict__ ptr, int64_t n_rows, int chunk,
-                                   int32_t* __restrict__ nitems) {
+__global__ void split_count_kernel(const int64_t* __restrict__ ptr, int64_t n_rows, int threshold, int item_size,
+                                   int32_t* __restrict__ nitems, int32_t* __restrict__ heavy_flag) {
   const int64_t r = int64_t(blockIdx.x) * kThreads + threadIdx.x;
   if (r >= n_rows) return;
   const int64_t len = ptr[r + 1] - ptr[r];
-  nitems[r] = len > chunk ? int32_t(ceil_div(len, chunk)) : 0;
+  const bool heavy = len > threshold;
+  nitems[r] = heavy ? int32_t(ceil_div(len, item_size)) : 0;
+  heavy_flag[r] = heavy ? 1 : 0;
 }
 
-__global__ void split_fill_kernel(const int32_t* __restrict__ nitems, const int32_t* __restrict__ item_off,
-                                  int64_t n_rows, int64_t cap, int32_t* __restrict__ item_row,
-                                  int32_t* __restrict__ total) {
+// Heavy-row list (compacted by the scan of the flags) and the two plan counts.
+__global__ void split_rows_kernel(const int32_t* __restrict__ nitems, const int32_t* __restrict__ item_off,
+                                  const int32_t* __restrict__ heavy_off, int64_t n_rows, int64_t item_cap,
+                                  int32_t* __restrict__ heavy_rows, int64_t heavy_cap, int32_t* __restrict__ counts) {
   const int64_t r = int64_t(blockIdx.x) * kThreads + threadIdx.x;
   if (r >= n_rows) return;
   const int n = nitems[r];
-  const int64_t off = item_off[r];
-  for (int j = 0; j < n; ++j)
-    if (off + j < cap) item_row[off + j] = int32_t(r);
+  if (n > 0 && heavy_off[r] < heavy_cap) heavy_rows[heavy_off[r]] = int32_t(r);
   if (r == n_rows - 1) {
-    const int64_t t = off + n;
-    *total = int32_t(t < cap ? t : cap);
+    const int64_t items = int64_t(item_off[r]) + n;
+    const int64_t heavy = int64_t(heavy_off[r]) + (n > 0 ? 1 : 0);
+    counts[0] = int32_t(items < item_cap ? items : item_cap);
+    counts[1] = int32_t(heavy < heavy_cap ? heavy : heavy_cap);
   }
 }
 
-__global__ void set_int_kernel(int32_t* p, int32_t v) { *p = v; }
+// item_row[i] = the heavy row owning item i: the last row whose first item is <= i.
+__global__ void split_items_kernel(const int32_t* __restrict__ item_off, int64_t n_rows,
+                                   const int32_t* __restrict__ counts, int32_t* __restrict__ item_row) {
+  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= counts[0]) return;
+  int64_t lo = 0, hi = n_rows;  // item_off[lo] <= i < item_off[hi] (item_off[n_rows] taken as +inf)
+  while (hi - lo > 1) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (item_off[mid] <= i) lo = mid; else hi = mid;
+  }
+  item_row[i] = int32_t(lo);
+}
 
 }  // namespace
 }  // namespace bf
@@ -172,50 +178,44 @@ extern "C" int bf_scan_workspace_size(int64_t n, size_t* bytes) {
   return BF_OK;
 }
 
-extern "C" int bf_table_csr_nnz(const int32_t* row_len, int64_t n_rows, int32_t global_token,
+extern "C" int bf_table_csr_ptr(const int32_t* row_len, int64_t n_rows, int32_t global_token, int64_t* qptr,
                                 int64_t* nnz_host, void* workspace, size_t workspace_bytes, void* stream) {
-  BF_CHECK_ARG(nnz_host && n_rows >= 0, "table_csr_nnz: bad arguments");
-  BF_CHECK_ARG(workspace && workspace_bytes >= sizeof(unsigned long long), "table_csr_nnz: workspace too small");
+  BF_CHECK_ARG(qptr && nnz_host && n_rows >= 0 && (row_len || n_rows == 0), "table_csr_ptr: bad arguments");
+  const int64_t n_q = n_rows + (global_token ? 1 : 0);
+  size_t need = 0;
+  bf_scan_workspace_size(n_q, &need);
+  BF_CHECK_ARG(workspace && workspace_bytes >= need, "table_csr_ptr: workspace %zu < %zu bytes", workspace_bytes, need);
   hipStream_t st = as_stream(stream);
-  auto* total = static_cast<unsigned long long*>(workspace);
-  BF_CHECK_HIP(hipMemsetAsync(total, 0, sizeof(*total), st));
-  if (n_rows > 0) {
-    BF_LAUNCH("sum_lengths_kernel", sum_lengths_kernel, dim3(blocks_for(n_rows)), dim3(kThreads), 0, st, row_len, n_rows, total);
+  BF_CHECK_HIP(hipMemsetAsync(qptr, 0, sizeof(int64_t), st));
+  if (n_q > 0) {
+    auto* lens = static_cast<int64_t*>(workspace);
+    void* temp = static_cast<char*>(workspace) + align_up(size_t(n_q) * sizeof(int64_t));
+    size_t temp_bytes = scan_temp_bytes_i64(n_q);
+    BF_LAUNCH("row_lengths_kernel", row_lengths_kernel, dim3(blocks_for(n_q)), dim3(kThreads), 0, st, row_len, n_rows,
+              int(global_token != 0), lens);
     BF_CHECK_LAUNCH();
+    BF_CHECK_HIP(hipcub::DeviceScan::InclusiveSum(temp, temp_bytes, lens, qptr + 1, int(n_q), st));
   }
-  unsigned long long h = 0;
-  BF_CHECK_HIP(hipMemcpyAsync(&h, total, sizeof(h), hipMemcpyDeviceToHost, st));
+  int64_t h = 0;
+  BF_CHECK_HIP(hipMemcpyAsync(&h, qptr + n_q, sizeof(h), hipMemcpyDeviceToHost, st));
   BF_CHECK_HIP(hipStreamSynchronize(st));
-  *nnz_host = int64_t(h) + (global_token ? 2 * n_rows : 0);
+  *nnz_host = h;
   return BF_OK;
 }
 
 extern "C" int bf_table_to_csr(const int32_t* table, const int32_t* row_len, int64_t n_rows, int32_t width,
-                               int32_t global_token, int64_t* qptr, int32_t* kv, void* workspace,
-                               size_t workspace_bytes, void* stream) {
+                               int32_t global_token, const int64_t* qptr, int32_t* kv, void* stream) {
   BF_CHECK_ARG(n_rows >= 0 && width >= 0 && qptr, "table_to_csr: bad arguments");
-  BF_CHECK_ARG(n_rows == 0 || (table && row_len && kv) || (width == 0 && row_len), "table_to_csr: null tensor");
-  const int64_t n_q = n_rows + (global_token ? 1 : 0);
-  size_t need = 0;
-  bf_scan_workspace_size(n_q, &need);
-  BF_CHECK_ARG(workspace && workspace_bytes >= need, "table_to_csr: workspace %zu < %zu bytes", workspace_bytes, need);
+  BF_CHECK_ARG(n_rows == 0 || (table && row_len && kv), "table_to_csr: null tensor");
   hipStream_t st = as_stream(stream);
-  BF_CHECK_HIP(hipMemsetAsync(qptr, 0, sizeof(int64_t), st));
-  if (n_q == 0) return BF_OK;
-  auto* lens = static_cast<int64_t*>(workspace);
-  void* temp = static_cast<char*>(workspace) + align_up(size_t(n_q) * sizeof(int64_t));
-  size_t temp_bytes = scan_temp_bytes_i64(n_q);
-  BF_LAUNCH("row_lengths_kernel", row_lengths_kernel, dim3(blocks_for(n_q)), dim3(kThreads), 0, st, row_len, n_rows,
-                     int(global_token != 0), lens);
-  BF_CHECK_LAUNCH();
-  BF_CHECK_HIP(hipcub::DeviceScan::InclusiveSum(temp, temp_bytes, lens, qptr + 1, int(n_q), st));
   if (n_rows * width > 0) {
     BF_LAUNCH("table_fill_kernel", table_fill_kernel, dim3(blocks_for(n_rows * width)), dim3(kThreads), 0, st, table,
-                       row_len, n_rows, width, int(global_token != 0), qptr, kv);
+              row_len, n_rows, width, int(global_token != 0), qptr, kv);
     BF_CHECK_LAUNCH();
   }
   if (global_token && n_rows > 0) {
-    BF_LAUNCH("token_fill_kernel", token_fill_kernel, dim3(blocks_for(n_rows)), dim3(kThreads), 0, st, row_len, n_rows, qptr, kv);
+    BF_LAUNCH("token_fill_kernel", token_fill_kernel, dim3(blocks_for(n_rows)), dim3(kThreads), 0, st, row_len,
+              n_rows, qptr, kv);
     BF_CHECK_LAUNCH();
   }
   return BF_OK;
@@ -321,42 +321,60 @@ extern "C" int bf_expand_rows(const int64_t* ptr, int64_t n_rows, int64_t nnz, i
   return BF_OK;
 }
 
-extern "C" int64_t bf_split_capacity(int64_t nnz, int32_t chunk) {
-  if (chunk < 1 || nnz < 0) return 0;
-  // rows split only when len > chunk: items <= sum(len/chunk + 1) <= 2*nnz/chunk
-  return 2 * (nnz / chunk) + 1;
+extern "C" int64_t bf_split_item_capacity(int64_t nnz, int32_t threshold, int32_t item_size) {
+  if (threshold < 1 || item_size < 1 || nnz < 0) return 0;
+  // only rows longer than threshold split: sum ceil(len/item) <= nnz/item + #heavy rows
+  return nnz / item_size + nnz / threshold + 1;
 }
 
-extern "C" int bf_split_plan(const int64_t* ptr, int64_t n_rows, int32_t chunk, int32_t* nitems, int32_t* item_off,
-                             int32_t* item_row, int64_t cap, int32_t* total, void* workspace,
-                             size_t workspace_bytes, void* stream) {
-  BF_CHECK_ARG(ptr && n_rows >= 0 && chunk >= 1 && total, "split_plan: bad arguments");
-  BF_CHECK_ARG(cap >= 0 && cap < (int64_t(1) << 31), "split_plan: bad capacity");
-  hipStream_t st = as_stream(stream);
-  if (n_rows == 0) {
-    BF_LAUNCH("set_int_kernel", set_int_kernel, dim3(1), dim3(1), 0, st, total, 0);
-    BF_CHECK_LAUNCH();
-    return BF_OK;
-  }
-  BF_CHECK_ARG(nitems && item_off && (item_row || cap == 0), "split_plan: null tensor");
-  size_t temp_bytes = 0;
-  (void)hipcub::DeviceScan::ExclusiveSum(nullptr, temp_bytes, nitems, item_off, int(n_rows));
-  BF_CHECK_ARG(workspace && workspace_bytes >= temp_bytes, "split_plan: workspace %zu < %zu bytes",
-               workspace_bytes, temp_bytes);
-  BF_LAUNCH("split_count_kernel", split_count_kernel, dim3(blocks_for(n_rows)), dim3(kThreads), 0, st, ptr, n_rows, chunk, nitems);
-  BF_CHECK_LAUNCH();
-  BF_CHECK_HIP(hipcub::DeviceScan::ExclusiveSum(workspace, temp_bytes, nitems, item_off, int(n_rows), st));
-  BF_LAUNCH("split_fill_kernel", split_fill_kernel, dim3(blocks_for(n_rows)), dim3(kThreads), 0, st, nitems, item_off, n_rows,
-                     cap, item_row, total);
-  BF_CHECK_LAUNCH();
-  return BF_OK;
+extern "C" int64_t bf_split_row_capacity(int64_t nnz, int32_t threshold) {
+  if (threshold < 1 || nnz < 0) return 0;
+  return nnz / threshold + 1;
 }
 
 extern "C" int bf_split_plan_workspace_size(int64_t n_rows, size_t* bytes) {
   BF_CHECK_ARG(bytes && n_rows >= 0, "split_plan_workspace_size: bad arguments");
   size_t temp_bytes = 0;
   (void)hipcub::DeviceScan::ExclusiveSum(nullptr, temp_bytes, static_cast<const int32_t*>(nullptr),
-                                   static_cast<int32_t*>(nullptr), int(n_rows > 0 ? n_rows : 1));
-  *bytes = align_up(temp_bytes) + 256;
+                                         static_cast<int32_t*>(nullptr), int(n_rows > 0 ? n_rows : 1));
+  *bytes = 2 * align_up(size_t(n_rows > 0 ? n_rows : 1) * 4) + align_up(temp_bytes) + 256;
+  return BF_OK;
+}
+
+extern "C" int bf_split_plan(const int64_t* ptr, int64_t n_rows, int32_t threshold, int32_t item_size,
+                             int32_t* nitems, int32_t* item_off, int32_t* item_row, int64_t item_cap,
+                             int32_t* heavy_rows, int64_t heavy_cap, int32_t* counts, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  BF_CHECK_ARG(ptr && n_rows >= 0 && threshold >= 1 && item_size >= 1 && counts, "split_plan: bad arguments");
+  BF_CHECK_ARG(item_cap >= 0 && item_cap < (int64_t(1) << 31) && heavy_cap >= 0 && heavy_cap < (int64_t(1) << 31),
+               "split_plan: bad capacity");
+  BF_CHECK_ARG(n_rows < (int64_t(1) << 31), "split_plan: too many rows");
+  hipStream_t st = as_stream(stream);
+  BF_CHECK_HIP(hipMemsetAsync(counts, 0, 2 * sizeof(int32_t), st));
+  if (n_rows == 0) return BF_OK;
+  BF_CHECK_ARG(nitems && item_off && (item_row || item_cap == 0) && (heavy_rows || heavy_cap == 0),
+               "split_plan: null tensor");
+  size_t need = 0;
+  bf_split_plan_workspace_size(n_rows, &need);
+  BF_CHECK_ARG(workspace && workspace_bytes >= need, "split_plan: workspace %zu < %zu bytes", workspace_bytes, need);
+  const size_t slab = align_up(size_t(n_rows) * 4);
+  auto* heavy_flag = static_cast<int32_t*>(workspace);
+  auto* heavy_off = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + slab);
+  void* temp = static_cast<char*>(workspace) + 2 * slab;
+  size_t temp_bytes = 0;
+  (void)hipcub::DeviceScan::ExclusiveSum(nullptr, temp_bytes, nitems, item_off, int(n_rows));
+  BF_LAUNCH("split_count_kernel", split_count_kernel, dim3(blocks_for(n_rows)), dim3(kThreads), 0, st, ptr, n_rows,
+            threshold, item_size, nitems, heavy_flag);
+  BF_CHECK_LAUNCH();
+  BF_CHECK_HIP(hipcub::DeviceScan::ExclusiveSum(temp, temp_bytes, nitems, item_off, int(n_rows), st));
+  BF_CHECK_HIP(hipcub::DeviceScan::ExclusiveSum(temp, temp_bytes, heavy_flag, heavy_off, int(n_rows), st));
+  BF_LAUNCH("split_rows_kernel", split_rows_kernel, dim3(blocks_for(n_rows)), dim3(kThreads), 0, st, nitems, item_off,
+            heavy_off, n_rows, item_cap, heavy_rows, heavy_cap, counts);
+  BF_CHECK_LAUNCH();
+  if (item_cap > 0) {
+    BF_LAUNCH("split_items_kernel", split_items_kernel, dim3(blocks_for(item_cap)), dim3(kThreads), 0, st, item_off,
+              n_rows, counts, item_row);
+    BF_CHECK_LAUNCH();
+  }
   return BF_OK;
 }

@@ -46,16 +46,17 @@ class EdgeTable:
     def width(self) -> int:
         return int(self.table.shape[1])
 
-    def attention_index(self, chunk: int = hip_ops.DEFAULT_CHUNK) -> AttentionIndex:
-        """CSR view for the attention kernels (cached per chunk)."""
-        idx = self._index.get(chunk)
+    def attention_index(self, chunk: int = hip_ops.DEFAULT_CHUNK, item: int = hip_ops.DEFAULT_ITEM) -> AttentionIndex:
+        """CSR view for the attention kernels (cached per split setting)."""
+        idx = self._index.get((chunk, item))
         if idx is None:
             if self.q_lo != 0 or self.n_rows != self.num_nodes:
                 if self.global_token:
                     raise NotImplementedError("the Graphormer global token needs the full query set")
             n_kv = self.num_nodes + (1 if self.global_token else 0)
-            idx = AttentionIndex.from_table(self.table, self.row_len, self.global_token, n_kv=n_kv, chunk=chunk)
-            self._index[chunk] = idx
+            idx = AttentionIndex.from_table(self.table, self.row_len, self.global_token, n_kv=n_kv, chunk=chunk,
+                                            item=item)
+            self._index[(chunk, item)] = idx
         return idx
 
     def to_edge_index(self) -> torch.Tensor:

@@ -15,7 +15,8 @@ import torch
 
 from . import _native as N
 
-DEFAULT_CHUNK = 64
+DEFAULT_CHUNK = 64      # rows longer than this go through the split plan
+DEFAULT_ITEM = 512      # entries per split item (one workgroup)
 
 
 def _p(t: Optional[torch.Tensor]):
@@ -138,13 +139,13 @@ def table_to_csr(table: torch.Tensor, row_len: torch.Tensor, global_token: bool 
     n_rows, width = table.shape
     n_q = n_rows + (1 if global_token else 0)
     ws = _workspace(_size_query("bf_scan_workspace_size", n_q), dev)
-    nnz = C.c_int64(0)
-    N.call("bf_table_csr_nnz", _p(row_len), n_rows, int(global_token), C.byref(nnz), _p(ws), ws.numel(),
-           _stream(dev))
     qptr = torch.empty(n_q + 1, dtype=torch.int64, device=dev)
+    nnz = C.c_int64(0)
+    N.call("bf_table_csr_ptr", _p(row_len), n_rows, int(global_token), _p(qptr), C.byref(nnz), _p(ws), ws.numel(),
+           _stream(dev))
     kv = torch.empty(max(nnz.value, 1), dtype=torch.int32, device=dev)[: nnz.value]
     N.call("bf_table_to_csr", _p(table), _p(row_len), n_rows, width, int(global_token), _p(qptr), _p(kv),
-           _p(ws), ws.numel(), _stream(dev))
+           _stream(dev))
     return qptr, kv
 
 
@@ -192,26 +193,31 @@ def expand_rows(ptr: torch.Tensor, nnz: int) -> torch.Tensor:
 
 @dataclass
 class SplitPlan:
-    cap: int
+    """Rows longer than `threshold` cut into `item_size`-entry items (host-known counts)."""
+    items: int
+    heavy: int
     nitems: torch.Tensor
     item_off: torch.Tensor
     item_row: torch.Tensor
-    total: torch.Tensor
+    heavy_rows: torch.Tensor
 
 
-def split_plan(ptr: torch.Tensor, chunk: int) -> SplitPlan:
+def split_plan(ptr: torch.Tensor, nnz: int, threshold: int = DEFAULT_CHUNK, item_size: int = DEFAULT_ITEM) -> SplitPlan:
     dev = ptr.device
+    lib = N.load()
     n_rows = ptr.numel() - 1
-    nnz_bound = int(ptr[-1].item()) if n_rows > 0 else 0
-    cap = int(N.load().bf_split_capacity(nnz_bound, chunk))
+    item_cap = int(lib.bf_split_item_capacity(nnz, threshold, item_size))
+    heavy_cap = int(lib.bf_split_row_capacity(nnz, threshold))
     nitems = torch.empty(max(n_rows, 1), dtype=torch.int32, device=dev)
     item_off = torch.empty(max(n_rows, 1), dtype=torch.int32, device=dev)
-    item_row = torch.empty(max(cap, 1), dtype=torch.int32, device=dev)
-    total = torch.zeros(1, dtype=torch.int32, device=dev)
+    item_row = torch.empty(max(item_cap, 1), dtype=torch.int32, device=dev)
+    heavy_rows = torch.empty(max(heavy_cap, 1), dtype=torch.int32, device=dev)
+    counts = torch.zeros(2, dtype=torch.int32, device=dev)
     ws = _workspace(_size_query("bf_split_plan_workspace_size", n_rows), dev)
-    N.call("bf_split_plan", _p(ptr), n_rows, chunk, _p(nitems), _p(item_off), _p(item_row), cap, _p(total),
-           _p(ws), ws.numel(), _stream(dev))
-    return SplitPlan(cap, nitems, item_off, item_row, total)
+    N.call("bf_split_plan", _p(ptr), n_rows, threshold, item_size, _p(nitems), _p(item_off), _p(item_row), item_cap,
+           _p(heavy_rows), heavy_cap, _p(counts), _p(ws), ws.numel(), _stream(dev))
+    items, heavy = (int(x) for x in counts.cpu().tolist())
+    return SplitPlan(items, heavy, nitems, item_off, item_row, heavy_rows)
 
 
 # ------------------------------------------------------------------ attention index
@@ -228,6 +234,7 @@ class AttentionIndex:
     qptr: torch.Tensor
     kv: torch.Tensor
     chunk: int = DEFAULT_CHUNK
+    item: int = DEFAULT_ITEM
     qplan: Optional[SplitPlan] = None
     kptr: Optional[torch.Tensor] = None
     kq: Optional[torch.Tensor] = None
@@ -245,7 +252,7 @@ class AttentionIndex:
 
     def ensure_forward(self):
         if self.qplan is None:
-            self.qplan = split_plan(self.qptr, self.chunk)
+            self.qplan = split_plan(self.qptr, self.nnz, self.chunk, self.item)
         return self
 
     def ensure_backward(self):
@@ -253,7 +260,7 @@ class AttentionIndex:
         if self.kptr is None:
             self.kptr, self.kq, self.ke = reverse_index(self.qptr, self.kv, self.n_kv)
         if self.kplan is None:
-            self.kplan = split_plan(self.kptr, self.chunk)
+            self.kplan = split_plan(self.kptr, self.nnz, self.chunk, self.item)
         return self
 
     def entry_rows(self) -> torch.Tensor:
@@ -273,31 +280,34 @@ class AttentionIndex:
         s = N.AttnIndex()
         s.n_q, s.n_kv, s.nnz = self.n_q, self.n_kv, self.nnz
         s.qptr, s.kv = self.qptr.data_ptr(), self.kv.data_ptr() if self.nnz else None
-        s.chunk = self.chunk
+        s.chunk, s.item = self.chunk, self.item
         qp = self.qplan
-        s.q_cap, s.q_nitems, s.q_item_off, s.q_item_row, s.q_total = (
-            qp.cap, qp.nitems.data_ptr(), qp.item_off.data_ptr(), qp.item_row.data_ptr(), qp.total.data_ptr())
+        s.q_items, s.q_heavy = qp.items, qp.heavy
+        s.q_nitems, s.q_item_off, s.q_item_row, s.q_heavy_rows = (
+            qp.nitems.data_ptr(), qp.item_off.data_ptr(), qp.item_row.data_ptr(), qp.heavy_rows.data_ptr())
         if backward:
             kp = self.kplan
             s.kptr = self.kptr.data_ptr()
             s.kq = self.kq.data_ptr() if self.nnz else None
             s.ke = self.ke.data_ptr() if self.nnz else None
-            s.k_cap, s.k_nitems, s.k_item_off, s.k_item_row, s.k_total = (
-                kp.cap, kp.nitems.data_ptr(), kp.item_off.data_ptr(), kp.item_row.data_ptr(), kp.total.data_ptr())
+            s.k_items, s.k_heavy = kp.items, kp.heavy
+            s.k_nitems, s.k_item_off, s.k_item_row, s.k_heavy_rows = (
+                kp.nitems.data_ptr(), kp.item_off.data_ptr(), kp.item_row.data_ptr(), kp.heavy_rows.data_ptr())
         return s
 
     @classmethod
     def from_table(cls, table, row_len, global_token: bool = False, n_kv: Optional[int] = None,
-                   chunk: int = DEFAULT_CHUNK):
+                   chunk: int = DEFAULT_CHUNK, item: int = DEFAULT_ITEM):
         qptr, kv = table_to_csr(table, row_len, global_token)
         n_q = qptr.numel() - 1
-        return cls(n_q=n_q, n_kv=n_kv if n_kv is not None else n_q, qptr=qptr, kv=kv, chunk=chunk)
+        return cls(n_q=n_q, n_kv=n_kv if n_kv is not None else n_q, qptr=qptr, kv=kv, chunk=chunk, item=item)
 
     @classmethod
-    def from_coo(cls, edge_index, n_q: int, n_kv: Optional[int] = None, chunk: int = DEFAULT_CHUNK):
+    def from_coo(cls, edge_index, n_q: int, n_kv: Optional[int] = None, chunk: int = DEFAULT_CHUNK,
+                 item: int = DEFAULT_ITEM):
         n_kv = n_q if n_kv is None else n_kv
         qptr, kv = coo_to_csr(edge_index, n_q, n_kv)
-        return cls(n_q=n_q, n_kv=n_kv, qptr=qptr, kv=kv, chunk=chunk)
+        return cls(n_q=n_q, n_kv=n_kv, qptr=qptr, kv=kv, chunk=chunk, item=item)
 
 
 # ------------------------------------------------------------------ attention

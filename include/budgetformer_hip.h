@@ -132,14 +132,14 @@ int bf_build_edge_table(const int64_t* rowptr, const int32_t* col,
  * global_token != 0 applies the Graphormer virtual node (fix_edge_index,
  * gt_sp/utils.py:113-130): ids shift by one, query 0 attends to kv 1..n_rows,
  * every query t >= 1 also attends to kv 0; then n_q = n_rows + 1.
- * nnz = sum(row_len) (+ 2*n_rows with the token); bf_table_csr_nnz gives it on
- * the host (it synchronises the stream). Workspace: bf_scan_workspace_size(n_q+1). */
-int bf_table_csr_nnz(const int32_t* row_len, int64_t n_rows, int32_t global_token,
+ * bf_table_csr_ptr writes qptr (a prefix sum of the row lengths) and returns
+ * nnz = qptr[n_q] on the host (it synchronises the stream, so the caller can
+ * size kv); bf_table_to_csr then fills kv. Workspace: bf_scan_workspace_size(n_q). */
+int bf_scan_workspace_size(int64_t n, size_t* bytes);
+int bf_table_csr_ptr(const int32_t* row_len, int64_t n_rows, int32_t global_token, int64_t* qptr,
                      int64_t* nnz_host, void* workspace, size_t workspace_bytes, void* stream);
 int bf_table_to_csr(const int32_t* table, const int32_t* row_len, int64_t n_rows, int32_t width,
-                    int32_t global_token, int64_t* qptr, int32_t* kv,
-                    void* workspace, size_t workspace_bytes, void* stream);
-int bf_scan_workspace_size(int64_t n, size_t* bytes);
+                    int32_t global_token, const int64_t* qptr, int32_t* kv, void* stream);
 
 /* Reference COO edge_index [2, nnz] (row 0 = key/value node, row 1 = query
  * node; models/graphormer_dist_node_level.py:231-232) -> attention CSR with
@@ -161,14 +161,19 @@ int bf_reverse_index(const int64_t* qptr, const int32_t* kv, int64_t n_q, int64_
 /* Row id of every entry of a CSR (rows[i] = r for ptr[r] <= i < ptr[r+1]). */
 int bf_expand_rows(const int64_t* ptr, int64_t n_rows, int64_t nnz, int64_t* rows, void* stream);
 
-/* Split plan for rows longer than `chunk`: such a row is processed as
- * ceil(len/chunk) items whose partial sums are reduced in a fixed order.
+/* Split plan for rows longer than `threshold`: such a row is processed as
+ * ceil(len/item_size) items (one workgroup each) whose partial sums are reduced
+ * in item order by one workgroup per split row, so results are deterministic.
  *   nitems int32 [n_rows] (0 for short rows), item_off int32 [n_rows],
- *   item_row int32 [cap], total int32 [1] (device), cap = bf_split_capacity. */
-int64_t bf_split_capacity(int64_t nnz, int32_t chunk);
+ *   item_row int32 [item_cap], heavy_rows int32 [heavy_cap] (the split rows,
+ *   ascending), counts int32 [2] on the device = (#items, #split rows).
+ *   Capacities: bf_split_item_capacity / bf_split_row_capacity.              */
+int64_t bf_split_item_capacity(int64_t nnz, int32_t threshold, int32_t item_size);
+int64_t bf_split_row_capacity(int64_t nnz, int32_t threshold);
 int bf_split_plan_workspace_size(int64_t n_rows, size_t* bytes);
-int bf_split_plan(const int64_t* ptr, int64_t n_rows, int32_t chunk, int32_t* nitems,
-                  int32_t* item_off, int32_t* item_row, int64_t cap, int32_t* total,
+int bf_split_plan(const int64_t* ptr, int64_t n_rows, int32_t threshold, int32_t item_size,
+                  int32_t* nitems, int32_t* item_off, int32_t* item_row, int64_t item_cap,
+                  int32_t* heavy_rows, int64_t heavy_cap, int32_t* counts,
                   void* workspace, size_t workspace_bytes, void* stream);
 
 /* ======================================================================
@@ -177,25 +182,26 @@ int bf_split_plan(const int64_t* ptr, int64_t n_rows, int32_t chunk, int32_t* ni
 
 /* Everything the attention kernels need to walk one edge set. */
 typedef struct bf_attn_index {
-  int64_t n_q;              /* queries (rows of qptr)                         */
-  int64_t n_kv;             /* key/value rows                                  */
-  int64_t nnz;              /* edges                                           */
-  const int64_t* qptr;      /* [n_q+1]                                         */
-  const int32_t* kv;        /* [nnz]   kv id per edge, query-major             */
-  const int64_t* kptr;      /* [n_kv+1] reverse offsets (backward only)        */
-  const int32_t* kq;        /* [nnz]   query per reverse entry (backward only) */
-  const int32_t* ke;        /* [nnz]   CSR position per reverse entry          */
-  int32_t chunk;            /* split threshold used by both plans              */
-  int32_t q_cap;            /* capacity of the query-side plan                 */
-  const int32_t* q_nitems;  /* query-side split plan (bf_split_plan on qptr)   */
+  int64_t n_q;                  /* queries (rows of qptr)                          */
+  int64_t n_kv;                 /* key/value rows                                   */
+  int64_t nnz;                  /* edges                                            */
+  const int64_t* qptr;          /* [n_q+1]                                          */
+  const int32_t* kv;            /* [nnz]   kv id per edge, query-major              */
+  const int64_t* kptr;          /* [n_kv+1] reverse offsets (backward only)         */
+  const int32_t* kq;            /* [nnz]   query per reverse entry (backward only)  */
+  const int32_t* ke;            /* [nnz]   CSR position per reverse entry           */
+  int32_t chunk;                /* rows longer than this use the split plan         */
+  int32_t item;                 /* entries per split item                           */
+  int32_t q_items, q_heavy;     /* query-side plan (bf_split_plan on qptr): counts  */
+  const int32_t* q_nitems;
   const int32_t* q_item_off;
   const int32_t* q_item_row;
-  const int32_t* q_total;
-  int32_t k_cap;            /* capacity of the kv-side plan                    */
-  const int32_t* k_nitems;  /* kv-side split plan (bf_split_plan on kptr)      */
+  const int32_t* q_heavy_rows;
+  int32_t k_items, k_heavy;     /* key-side plan (bf_split_plan on kptr)            */
+  const int32_t* k_nitems;
   const int32_t* k_item_off;
   const int32_t* k_item_row;
-  const int32_t* k_total;
+  const int32_t* k_heavy_rows;
 } bf_attn_index;
 
 /* float32 scratch the attention calls need for split rows. */

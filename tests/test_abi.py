@@ -41,11 +41,16 @@ def test_argument_errors_surface_as_exceptions():
 
 
 def test_split_capacity_bound():
+    """Capacities bound every row-length distribution (brute force over small cases)."""
+    import itertools
     lib = N.load()
-    for nnz, chunk in ((0, 64), (63, 64), (1000, 7), (10 ** 9, 256)):
-        cap = lib.bf_split_capacity(nnz, chunk)
-        # rows are split only when longer than chunk: sum(ceil(len/chunk)) <= 2*nnz/chunk
-        assert cap >= 2 * (nnz // chunk)
+    for lens in itertools.product([0, 1, 3, 4, 5, 9, 17], repeat=3):
+        nnz = sum(lens)
+        for thr, item in ((1, 1), (3, 4), (4, 2), (2, 8)):
+            items = sum(-(-l // item) for l in lens if l > thr)
+            rows = sum(1 for l in lens if l > thr)
+            assert lib.bf_split_item_capacity(nnz, thr, item) >= items
+            assert lib.bf_split_row_capacity(nnz, thr) >= rows
 
 
 def test_workspace_queries_run_on_cpu():

@@ -69,8 +69,8 @@ def test_fp32_random_coo(hip_device, S, H, hn, E):
         assert _rel_err(got, ref) < 1e-5
 
 
-@pytest.mark.parametrize("chunk", [4, 64])
-def test_fp32_global_token_split_rows(hip_device, chunk):
+@pytest.mark.parametrize("chunk,item", [(4, 4), (4, 37), (64, 512)])
+def test_fp32_global_token_split_rows(hip_device, chunk, item):
     """Graphormer token: query 0 is dense over all kv and kv 0 feeds every query."""
     from budgetformer_amd.hip_ops import AttentionIndex
     S, H, hn = 500, 8, 16
@@ -78,10 +78,10 @@ def test_fp32_global_token_split_rows(hip_device, chunk):
     ei = ei[:, (ei[0] > 0) & (ei[1] > 0)]
     ar = torch.arange(1, S)
     ei = torch.cat([ei, torch.stack([ar, torch.zeros_like(ar)]), torch.stack([torch.zeros_like(ar), ar])], 1)
-    idx = AttentionIndex.from_coo(ei.to(hip_device), S, chunk=chunk)
+    idx = AttentionIndex.from_coo(ei.to(hip_device), S, chunk=chunk, item=item)
     out, dq, dk, dv, _ = _run(hip_device, q, k, v, idx, dout)
     ro, rZ, rdq, rdk, rdv, _ = _oracle(q, k, v, ei, dout)
-    assert idx.qplan.total.item() > 0 and idx.kplan.total.item() > 0   # split paths exercised
+    assert idx.qplan.items > 0 and idx.kplan.items > 0 and idx.qplan.heavy > 0   # split paths exercised
     for got, ref in ((out, ro), (dq, rdq), (dk, rdk), (dv, rdv)):
         assert _rel_err(got, ref) < 1e-5
 
@@ -90,7 +90,7 @@ def test_fp32_bias_and_dbias(hip_device):
     from budgetformer_amd.hip_ops import AttentionIndex
     S, H, hn = 200, 8, 16
     q, k, v, ei, dout = _inputs(S, H, hn, 1500, seed=11, mult=1.5)
-    idx = AttentionIndex.from_coo(ei.to(hip_device), S, chunk=16)
+    idx = AttentionIndex.from_coo(ei.to(hip_device), S, chunk=6, item=10)
     ei_o = _coo_order(idx)
     bias_e = torch.randn(idx.nnz, H, generator=torch.Generator().manual_seed(3))
     out, dq, dk, dv, db = _run(hip_device, q, k, v, idx, dout, bias_e=bias_e)
@@ -148,7 +148,7 @@ def test_deterministic(hip_device):
     from budgetformer_amd.hip_ops import AttentionIndex
     S, H, hn = 300, 8, 16
     q, k, v, ei, dout = _inputs(S, H, hn, 6000, seed=15)
-    idx = AttentionIndex.from_coo(ei.to(hip_device), S, chunk=8)
+    idx = AttentionIndex.from_coo(ei.to(hip_device), S, chunk=8, item=24)
     a = _run(hip_device, q, k, v, idx, dout)
     b = _run(hip_device, q, k, v, idx, dout)
     for x, y in zip(a[:4], b[:4]):
