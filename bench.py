@@ -86,6 +86,47 @@ def rocprof_summary(stats_csv: str, top: int = 25) -> str:
     return "\n".join(out)
 
 
+def _short_kernel(name: str) -> str:
+    import re
+    m = re.search(r"(\w+_kernel)\b", name)
+    if "rocprim" in name:
+        return "rocprim"
+    return m.group(1) if m else name.split("(")[0][:60]
+
+
+def _counter_means(path: str) -> dict:
+    """{kernel: mean Counter_Value per dispatch} from a rocprofv3 counter_collection.csv."""
+    import collections
+    import csv
+    acc = collections.defaultdict(list)
+    for r in csv.DictReader(open(path)):
+        acc[_short_kernel(r["Kernel_Name"])].append(float(r["Counter_Value"]))
+    return {k: sum(v) / len(v) for k, v in acc.items()}
+
+
+def pmc_summary(fetch_csv, write_csv, copy_fetch_csv, copy_write_csv, copy_bytes, kernels_of_interest):
+    """HBM-side bytes per dispatch from FETCH_SIZE / WRITE_SIZE runs, each scaled by what the
+    same counter reads for a plain copy of ``copy_bytes`` bytes. Returns (markdown, dict)."""
+    f, w = _counter_means(fetch_csv), _counter_means(write_csv)
+    cf, cw = _counter_means(copy_fetch_csv), _counter_means(copy_write_csv)
+    copy_name = max(cf, key=cf.get)
+    f_scale = copy_bytes / (cf[copy_name] * 1024.0)
+    w_scale = copy_bytes / (cw[copy_name] * 1024.0)
+    lines = [f"Calibration ({copy_name}, {copy_bytes / 2**30:.2f} GiB read + written): FETCH_SIZE reads "
+             f"{cf[copy_name]:.0f} KiB -> scale {f_scale:.3f}; WRITE_SIZE reads {cw[copy_name]:.0f} KiB -> scale "
+             f"{w_scale:.3f}.", "",
+             "| kernel | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM-side bytes per dispatch (scaled) |",
+             "|---|---:|---:|---:|"]
+    out = {"fetch_scale": f_scale, "write_scale": w_scale, "kernels": {}}
+    for k in kernels_of_interest:
+        if k not in f or k not in w:
+            continue
+        traffic = f[k] * 1024.0 * f_scale + w[k] * 1024.0 * w_scale
+        out["kernels"][k] = {"fetch_kib": round(f[k], 1), "write_kib": round(w[k], 1), "traffic_bytes": int(traffic)}
+        lines.append(f"| {k} | {f[k]:.0f} | {w[k]:.0f} | {traffic:,.0f} |")
+    return "\n".join(lines), out
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -108,9 +149,24 @@ def main(argv=None):
     ap.add_argument("--item", type=int, default=None, help="entries per split item")
     ap.add_argument("--rocprof-summary", metavar="KERNEL_STATS_CSV",
                     help="print a markdown summary of a rocprofv3 kernel_stats.csv and exit")
+    ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "COPY_FETCH_CSV", "COPY_WRITE_CSV"),
+                    help="summarise FETCH_SIZE/WRITE_SIZE counter runs (calibrated by a copy kernel) and exit")
+    ap.add_argument("--copy-bytes", type=int, default=2 ** 30, help="bytes the calibration copy reads and writes")
+    ap.add_argument("--pmc-json", help="with --pmc-summary: also write the per-kernel traffic as JSON here")
     args = ap.parse_args(argv)
     if args.rocprof_summary:
         print(rocprof_summary(args.rocprof_summary))
+        return 0
+    if args.pmc_summary:
+        names = ["attn_fwd_rows_kernel", "attn_bwd_q_rows_kernel", "attn_bwd_kv_rows_kernel", "attn_fwd_items_kernel",
+                 "attn_bwd_q_items_kernel", "attn_bwd_kv_items_kernel", "attn_fwd_reduce_kernel",
+                 "attn_bwd_q_reduce_kernel", "attn_bwd_kv_reduce_kernel", "rw_select_kernel",
+                 "real_select_merge_kernel"]
+        md, data = pmc_summary(*args.pmc_summary, args.copy_bytes, names)
+        print(md)
+        if args.pmc_json:
+            with open(args.pmc_json, "w") as fh:
+                json.dump(data, fh, indent=1)
         return 0
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the path would shard "
@@ -206,8 +262,15 @@ def main(argv=None):
         kernels[name] = rec
     dominant = max((n_ for n_ in kernels if n_ in kb), key=lambda n_: kernels[n_]["avg_ms"])
     dom = kernels[dominant]
+    traffic = None
+    pmc_path = os.path.join(ROOT, "profiles", f"attention_{args.config}_{cfg['dtype']}_pmc.json")
+    if os.path.exists(pmc_path) and chunk == hip_ops.DEFAULT_CHUNK and item == hip_ops.DEFAULT_ITEM:
+        with open(pmc_path) as fh:
+            rec = json.load(fh).get("kernels", {}).get(dominant)
+        traffic = rec["traffic_bytes"] if rec else None
     roofline = {"kernel": dominant, "bound": "hbm", "achieved": dom["achieved_gbs"], "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(dom["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": None}
+                "unit": "GB/s", "frac": round(dom["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "algorithmic_bytes": dom["algorithmic_bytes"]}
 
     # edge-builder figures: valid RW pool steps = walks moved or first step
     n_walks = n * cfg["P"]
