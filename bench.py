@@ -272,8 +272,12 @@ def main(argv=None):
                 "unit": "GB/s", "frac": round(dom["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
                 "algorithmic_bytes": dom["algorithmic_bytes"]}
 
-    # edge-builder figures: valid RW pool steps = walks moved or first step
+    # edge-builder figures: RW pool edges = valid hop entries (d == 1, or the walk moved at step d)
     n_walks = n * cfg["P"]
+    walks = hip_ops.random_walk(g.rowptr, g.col, 0, n, cfg["P"], cfg["L"], philox_seed=42)
+    moved = walks[:, 2:] != walks[:, 1:-1]
+    pool_edges = int(n_walks + moved.sum().item())
+    del walks, moved
     rw_ms = kernels.get("rw_select_kernel", {}).get("avg_ms")
     merge_ms = kernels.get("real_select_merge_kernel", {}).get("avg_ms")
     table_entries = int(tab.row_len.sum().item())
@@ -299,6 +303,8 @@ def main(argv=None):
         "attn_algorithmic_bytes": a_fwd + a_bwd,
         "attn_frac_of_hbm_peak": round(attn_gbs / HBM_PEAK_GBS, 4),
         "edge_build_ms": round(build_ms, 4),
+        "rw_pool_edges": pool_edges,
+        "rw_edges_per_s": round(pool_edges / (rw_ms * 1e-3), 1) if rw_ms else None,
         "rw_walk_steps_per_s": round(n_walks * cfg["L"] / (rw_ms * 1e-3), 1) if rw_ms else None,
         "rw_select_ms": rw_ms,
         "real_select_merge_ms": merge_ms,
