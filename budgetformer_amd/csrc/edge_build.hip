@@ -64,6 +64,23 @@ __global__ __launch_bounds__(kThreads) void walk_uniforms_kernel(int64_t q_lo, i
   for (int l = 0; l < L; ++l) u[wl * L + l] = walk_uniform(seed, offset, uint64_t(w), l);
 }
 
+// Walks from arbitrary start nodes; walk i draws its Philox stream as walk id (id_base + i).
+__global__ __launch_bounds__(kThreads) void random_walk_starts_kernel(
+    const int64_t* __restrict__ rowptr, const int32_t* __restrict__ col, const int64_t* __restrict__ starts,
+    int64_t n_walks, int L, const float* __restrict__ u, uint64_t seed, uint64_t offset, uint64_t id_base,
+    int64_t* __restrict__ walks) {
+  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= n_walks) return;
+  int64_t cur = starts[i];
+  int64_t* row = walks + i * (L + 1);
+  row[0] = cur;
+  for (int l = 0; l < L; ++l) {
+    const float uu = u ? u[i * L + l] : walk_uniform(seed, offset, id_base + uint64_t(i), l);
+    cur = walk_step(rowptr, col, cur, uu);
+    row[l + 1] = cur;
+  }
+}
+
 // One lane per walk; the P lanes of a query are adjacent. Candidates are staged
 // in LDS as (key << 32 | kv) (kNone = filtered step) and ranked by the P lanes.
 __global__ __launch_bounds__(kThreads) void rw_select_kernel(
@@ -272,6 +289,23 @@ extern "C" int bf_random_walk(const int64_t* rowptr, const int32_t* col, int64_t
   BF_LAUNCH("random_walk_kernel", random_walk_kernel, dim3(unsigned(ceil_div(n_walks, kThreads))), dim3(kThreads), 0,
                      as_stream(stream), rowptr, col, q_lo, n_walks, walks_per_node, walk_length, u, philox_seed,
                      philox_offset, walks);
+  BF_CHECK_LAUNCH();
+  return BF_OK;
+}
+
+extern "C" int bf_random_walk_starts(const int64_t* rowptr, const int32_t* col, int64_t num_nodes,
+                                    const int64_t* starts, int64_t n_walks, int32_t walk_length, const float* u,
+                                    uint64_t philox_seed, uint64_t philox_offset, uint64_t walk_id_base,
+                                    int64_t* walks, void* stream) {
+  int rc = check_graph(rowptr, col, num_nodes, 0, 0);
+  if (rc) return rc;
+  BF_CHECK_ARG(n_walks >= 0 && walk_length >= 1, "random_walk_starts: n_walks=%lld L=%d", (long long)n_walks,
+               walk_length);
+  if (n_walks == 0) return BF_OK;
+  BF_CHECK_ARG(starts && walks, "random_walk_starts: null tensor");
+  BF_LAUNCH("random_walk_starts_kernel", random_walk_starts_kernel, dim3(unsigned(ceil_div(n_walks, kThreads))),
+            dim3(kThreads), 0, as_stream(stream), rowptr, col, starts, n_walks, walk_length, u, philox_seed,
+            philox_offset, walk_id_base, walks);
   BF_CHECK_LAUNCH();
   return BF_OK;
 }

@@ -378,3 +378,160 @@ extern "C" int bf_split_plan(const int64_t* ptr, int64_t n_rows, int32_t thresho
   }
   return BF_OK;
 }
+
+// ---------------------------------------------------------------- hop pool and coalesce
+namespace bf {
+namespace {
+
+// Hop pool flags in pool order (d-major, then walk): entry (d, w) is kept iff
+// walks[w, d] >= 0 and (d == 1 or walks[w, d] != walks[w, d-1]).
+__global__ void hop_flags_kernel(const int64_t* __restrict__ walks, int64_t n_walks,
+                                                             int L, int min_hop, int32_t* __restrict__ flags) {
+  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  const int D = L - min_hop + 1;
+  if (i >= n_walks * D) return;
+  const int d = min_hop + int(i / n_walks);
+  const int64_t w = i % n_walks;
+  const int64_t kv = walks[w * (L + 1) + d];
+  flags[i] = (kv >= 0 && (d == 1 || kv != walks[w * (L + 1) + d - 1])) ? 1 : 0;
+}
+
+__global__ void hop_fill_kernel(const int64_t* __restrict__ walks, int64_t n_walks,
+                                                            int L, int min_hop, const int32_t* __restrict__ flags,
+                                                            const int64_t* __restrict__ pos,
+                                                            int64_t* __restrict__ pool_kv,
+                                                            int64_t* __restrict__ pool_q) {
+  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  const int D = L - min_hop + 1;
+  if (i >= n_walks * D || !flags[i]) return;
+  const int d = min_hop + int(i / n_walks);
+  const int64_t w = i % n_walks;
+  pool_kv[pos[i]] = walks[w * (L + 1) + d];
+  pool_q[pos[i]] = walks[w * (L + 1)];
+}
+
+__global__ void i32_to_i64_kernel(const int32_t* __restrict__ a, int64_t n, int64_t* __restrict__ b) {
+  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (i < n) b[i] = a[i];
+}
+
+__global__ void coalesce_keys_kernel(const int64_t* __restrict__ src, const int64_t* __restrict__ dst, int64_t nnz,
+                                     uint64_t n, uint64_t* __restrict__ keys) {
+  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (i < nnz) keys[i] = uint64_t(src[i]) * n + uint64_t(dst[i]);
+}
+
+__global__ void unique_flags_kernel(const uint64_t* __restrict__ keys, int64_t nnz, int64_t* __restrict__ flags) {
+  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (i < nnz) flags[i] = (i == 0 || keys[i] != keys[i - 1]) ? 1 : 0;
+}
+
+__global__ void unique_fill_kernel(const uint64_t* __restrict__ keys, const int64_t* __restrict__ incl, int64_t nnz,
+                                   uint64_t n, int64_t* __restrict__ out_src, int64_t* __restrict__ out_dst) {
+  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= nnz) return;
+  if (i == 0 || keys[i] != keys[i - 1]) {
+    const int64_t p = incl[i] - 1;
+    out_src[p] = int64_t(keys[i] / n);
+    out_dst[p] = int64_t(keys[i] % n);
+  }
+}
+
+}  // namespace
+}  // namespace bf
+
+extern "C" int bf_hop_pool_workspace_size(int64_t n_walks, int32_t walk_length, int32_t min_hop, size_t* bytes) {
+  BF_CHECK_ARG(bytes && n_walks >= 0 && walk_length >= 1 && min_hop >= 1, "hop_pool_workspace_size: bad arguments");
+  const int64_t m = n_walks * (min_hop <= walk_length ? walk_length - min_hop + 1 : 0);
+  size_t scan_bytes = 0;
+  (void)hipcub::DeviceScan::ExclusiveSum(nullptr, scan_bytes, static_cast<const int64_t*>(nullptr),
+                                         static_cast<int64_t*>(nullptr), int(m > 0 ? m : 1));
+  *bytes = align_up(size_t(m > 0 ? m : 1) * 4) + 2 * align_up(size_t(m > 0 ? m : 1) * 8) + align_up(scan_bytes) + 256;
+  return BF_OK;
+}
+
+extern "C" int bf_hop_pool(const int64_t* walks, int64_t n_walks, int32_t walk_length, int32_t min_hop,
+                           int64_t* pool_kv, int64_t* pool_q, int64_t* count_host, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  BF_CHECK_ARG(count_host && n_walks >= 0 && walk_length >= 1 && min_hop >= 1, "hop_pool: bad arguments");
+  *count_host = 0;
+  if (min_hop > walk_length || n_walks == 0) return BF_OK;
+  const int64_t m = n_walks * (walk_length - min_hop + 1);
+  BF_CHECK_ARG(m < (int64_t(1) << 31), "hop_pool: %lld candidates exceed int32 scan range", (long long)m);
+  BF_CHECK_ARG(walks && pool_kv && pool_q, "hop_pool: null tensor");
+  size_t need = 0;
+  bf_hop_pool_workspace_size(n_walks, walk_length, min_hop, &need);
+  BF_CHECK_ARG(workspace && workspace_bytes >= need, "hop_pool: workspace %zu < %zu bytes", workspace_bytes, need);
+  hipStream_t st = as_stream(stream);
+  auto* flags = static_cast<int32_t*>(workspace);
+  auto* flags64 = reinterpret_cast<int64_t*>(static_cast<char*>(workspace) + align_up(size_t(m) * 4));
+  auto* pos = reinterpret_cast<int64_t*>(reinterpret_cast<char*>(flags64) + align_up(size_t(m) * 8));
+  void* temp = reinterpret_cast<char*>(pos) + align_up(size_t(m) * 8);
+  size_t temp_bytes = 0;
+  (void)hipcub::DeviceScan::ExclusiveSum(nullptr, temp_bytes, flags64, pos, int(m));
+  BF_LAUNCH("hop_flags_kernel", hop_flags_kernel, dim3(blocks_for(m)), dim3(kThreads), 0, st, walks, n_walks,
+            walk_length, min_hop, flags);
+  BF_CHECK_LAUNCH();
+  BF_LAUNCH("i32_to_i64_kernel", i32_to_i64_kernel, dim3(blocks_for(m)), dim3(kThreads), 0, st, flags, m, flags64);
+  BF_CHECK_LAUNCH();
+  BF_CHECK_HIP(hipcub::DeviceScan::ExclusiveSum(temp, temp_bytes, flags64, pos, int(m), st));
+  BF_LAUNCH("hop_fill_kernel", hop_fill_kernel, dim3(blocks_for(m)), dim3(kThreads), 0, st, walks, n_walks,
+            walk_length, min_hop, flags, pos, pool_kv, pool_q);
+  BF_CHECK_LAUNCH();
+  int64_t last_pos = 0;
+  int32_t last_flag = 0;
+  BF_CHECK_HIP(hipMemcpyAsync(&last_pos, pos + m - 1, sizeof(last_pos), hipMemcpyDeviceToHost, st));
+  BF_CHECK_HIP(hipMemcpyAsync(&last_flag, flags + m - 1, sizeof(last_flag), hipMemcpyDeviceToHost, st));
+  BF_CHECK_HIP(hipStreamSynchronize(st));
+  *count_host = last_pos + last_flag;
+  return BF_OK;
+}
+
+extern "C" int bf_coalesce_workspace_size(int64_t nnz, size_t* bytes) {
+  BF_CHECK_ARG(bytes && nnz >= 0, "coalesce_workspace_size: bad arguments");
+  const int n = int(nnz > 0 ? nnz : 1);
+  size_t sort_bytes = 0, scan_bytes = 0;
+  (void)hipcub::DeviceRadixSort::SortKeys(nullptr, sort_bytes, static_cast<const uint64_t*>(nullptr),
+                                          static_cast<uint64_t*>(nullptr), n);
+  (void)hipcub::DeviceScan::InclusiveSum(nullptr, scan_bytes, static_cast<const int64_t*>(nullptr),
+                                         static_cast<int64_t*>(nullptr), n);
+  *bytes = 4 * align_up(size_t(n) * 8) + align_up(sort_bytes > scan_bytes ? sort_bytes : scan_bytes) + 256;
+  return BF_OK;
+}
+
+extern "C" int bf_coalesce(const int64_t* src, const int64_t* dst, int64_t nnz, int64_t num_nodes, int64_t* out_src,
+                           int64_t* out_dst, int64_t* count_host, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+  BF_CHECK_ARG(count_host && nnz >= 0 && num_nodes > 0, "coalesce: bad arguments");
+  BF_CHECK_ARG(nnz < (int64_t(1) << 31) && num_nodes < (int64_t(1) << 32), "coalesce: sizes out of range");
+  *count_host = 0;
+  if (nnz == 0) return BF_OK;
+  BF_CHECK_ARG(src && dst && out_src && out_dst, "coalesce: null tensor");
+  size_t need = 0;
+  bf_coalesce_workspace_size(nnz, &need);
+  BF_CHECK_ARG(workspace && workspace_bytes >= need, "coalesce: workspace %zu < %zu bytes", workspace_bytes, need);
+  hipStream_t st = as_stream(stream);
+  const size_t slab = align_up(size_t(nnz) * 8);
+  auto* keys_in = static_cast<uint64_t*>(workspace);
+  auto* keys = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + slab);
+  auto* flags = reinterpret_cast<int64_t*>(static_cast<char*>(workspace) + 2 * slab);
+  auto* incl = reinterpret_cast<int64_t*>(static_cast<char*>(workspace) + 3 * slab);
+  void* temp = static_cast<char*>(workspace) + 4 * slab;
+  size_t sort_bytes = 0, scan_bytes = 0;
+  (void)hipcub::DeviceRadixSort::SortKeys(nullptr, sort_bytes, keys_in, keys, int(nnz));
+  (void)hipcub::DeviceScan::InclusiveSum(nullptr, scan_bytes, flags, incl, int(nnz));
+  BF_LAUNCH("coalesce_keys_kernel", coalesce_keys_kernel, dim3(blocks_for(nnz)), dim3(kThreads), 0, st, src, dst, nnz,
+            uint64_t(num_nodes), keys_in);
+  BF_CHECK_LAUNCH();
+  const int end_bit = bits_for(uint64_t(num_nodes) * uint64_t(num_nodes));
+  BF_CHECK_HIP(hipcub::DeviceRadixSort::SortKeys(temp, sort_bytes, keys_in, keys, int(nnz), 0, end_bit, st));
+  BF_LAUNCH("unique_flags_kernel", unique_flags_kernel, dim3(blocks_for(nnz)), dim3(kThreads), 0, st, keys, nnz, flags);
+  BF_CHECK_LAUNCH();
+  BF_CHECK_HIP(hipcub::DeviceScan::InclusiveSum(temp, scan_bytes, flags, incl, int(nnz), st));
+  BF_LAUNCH("unique_fill_kernel", unique_fill_kernel, dim3(blocks_for(nnz)), dim3(kThreads), 0, st, keys, incl, nnz,
+            uint64_t(num_nodes), out_src, out_dst);
+  BF_CHECK_LAUNCH();
+  BF_CHECK_HIP(hipMemcpyAsync(count_host, incl + nnz - 1, sizeof(int64_t), hipMemcpyDeviceToHost, st));
+  BF_CHECK_HIP(hipStreamSynchronize(st));
+  return BF_OK;
+}

@@ -23,6 +23,7 @@ import torch
 
 from . import hip_ops
 from .graph import CSRGraph
+from .gt_sp.utils import plan_edge_build
 from .hip_ops import AttentionIndex
 
 REAL_SEED_OFFSET = 17   # utils/fullgraph_sp_support.py:1413
@@ -82,12 +83,17 @@ def build_attention_edges(graph: CSRGraph, *, real_edges_per_query: int, rw_edge
                           walk_length: int = 4, walks_per_node: int = 2, edge_seed: int = 42,
                           q_lo: int = 0, n_q: Optional[int] = None, u: Optional[torch.Tensor] = None,
                           philox_seed: Optional[int] = None, philox_offset: int = 0,
-                          global_token: bool = False) -> EdgeTable:
+                          global_token: bool = False, usable_bytes: Optional[int] = None) -> EdgeTable:
     """Budgeted edge table for queries [q_lo, q_lo+n_q) of ``graph``.
 
     b_real <= 0 drops the real part, b_rw <= 0 (or walks_per_node <= 0) drops
     the RW part (utils/fullgraph_sp_support.py:1395-1400, 1506-1508); both parts
     present -> set union per query, one part -> its multiset.
+
+    The build is planned by ``gt_sp.utils.plan_edge_build``: when its transient
+    does not fit next to the table (``usable_bytes``, default: the device's free
+    HBM), the query range is built in shards on the device — bit-identical,
+    since every walk's RNG counter is its global walk id.
     """
     n_q = graph.num_nodes - q_lo if n_q is None else n_q
     b_r = max(int(real_edges_per_query), 0)
@@ -95,8 +101,20 @@ def build_attention_edges(graph: CSRGraph, *, real_edges_per_query: int, rw_edge
     if b_r + b_w <= 0:
         raise ValueError("empty edge budget: real_edges_per_query + rw_edges_per_query must be > 0")
     walk_length = max(1, int(walk_length))
-    table, row_len = hip_ops.build_edge_table(
-        graph.rowptr, graph.col, graph.in_ptr, graph.in_src, graph.num_edges, q_lo, n_q,
-        max(int(walks_per_node), 1), walk_length, b_r, b_w, int(edge_seed), u=u,
-        philox_seed=int(edge_seed if philox_seed is None else philox_seed), philox_offset=philox_offset)
+    P = max(int(walks_per_node), 1)
+    seed = int(edge_seed if philox_seed is None else philox_seed)
+    plan = plan_edge_build(graph.device, n_q, b_r, b_w, q_lo=q_lo, usable_bytes=usable_bytes)
+    if len(plan.shards) == 1:
+        table, row_len = hip_ops.build_edge_table(
+            graph.rowptr, graph.col, graph.in_ptr, graph.in_src, graph.num_edges, q_lo, n_q, P, walk_length,
+            b_r, b_w, int(edge_seed), u=u, philox_seed=seed, philox_offset=philox_offset)
+    else:
+        table = torch.empty(n_q, b_r + b_w, dtype=torch.int32, device=graph.device)
+        row_len = torch.empty(n_q, dtype=torch.int32, device=graph.device)
+        for lo, cnt in plan.shards:
+            a = lo - q_lo
+            u_s = None if u is None else u[a * P:(a + cnt) * P]
+            hip_ops.build_edge_table(graph.rowptr, graph.col, graph.in_ptr, graph.in_src, graph.num_edges, lo, cnt,
+                                     P, walk_length, b_r, b_w, int(edge_seed), u=u_s, philox_seed=seed,
+                                     philox_offset=philox_offset, out=(table[a:a + cnt], row_len[a:a + cnt]))
     return EdgeTable(table, row_len, graph.num_nodes, q_lo=q_lo, global_token=global_token)

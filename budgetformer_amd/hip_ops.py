@@ -67,6 +67,57 @@ def random_walk(rowptr, col, q_lo: int, n_q: int, walks_per_node: int, walk_leng
     return walks
 
 
+def random_walk_starts(rowptr, col, starts: torch.Tensor, walk_length: int, u: Optional[torch.Tensor] = None,
+                       philox_seed: int = 0, philox_offset: int = 0, walk_id_base: int = 0) -> torch.Tensor:
+    """Walks [len(starts), L+1] int64 from arbitrary start nodes (bf_random_walk_starts)."""
+    dev = rowptr.device
+    _require(rowptr, "rowptr", torch.int64)
+    _require(col, "col", torch.int32, dev)
+    _require(starts, "starts", torch.int64, dev)
+    n = starts.numel()
+    if n:
+        lo, hi = int(starts.min().item()), int(starts.max().item())
+        if lo < 0 or hi >= rowptr.numel() - 1:
+            raise ValueError(f"starts outside [0, {rowptr.numel() - 1})")
+    if u is not None:
+        _require(u, "u", torch.float32, dev)
+        if tuple(u.shape) != (n, walk_length):
+            raise ValueError(f"u must be [{n}, {walk_length}], got {tuple(u.shape)}")
+    walks = torch.empty(n, walk_length + 1, dtype=torch.int64, device=dev)
+    N.call("bf_random_walk_starts", _p(rowptr), _p(col), rowptr.numel() - 1, _p(starts), n, walk_length, _p(u),
+           philox_seed & (2 ** 64 - 1), philox_offset & (2 ** 64 - 1), walk_id_base & (2 ** 64 - 1), _p(walks),
+           _stream(dev))
+    return walks
+
+
+def hop_pool(walks: torch.Tensor, min_hop: int = 1) -> torch.Tensor:
+    """RW pool [2, M] int64 (kv, query) of a walk tensor, in the reference's d-major order."""
+    dev = walks.device
+    _require(walks, "walks", torch.int64)
+    n, L = walks.shape[0], walks.shape[1] - 1
+    cap = n * max(L - min_hop + 1, 0)
+    out = torch.empty(2, max(cap, 1), dtype=torch.int64, device=dev)
+    ws = _workspace(_size_query("bf_hop_pool_workspace_size", n, L, min_hop), dev)
+    cnt = C.c_int64(0)
+    N.call("bf_hop_pool", _p(walks), n, L, min_hop, C.c_void_p(out[0].data_ptr()), C.c_void_p(out[1].data_ptr()),
+           C.byref(cnt), _p(ws), ws.numel(), _stream(dev))
+    return out[:, : cnt.value]
+
+
+def coalesce(edge_index: torch.Tensor, num_nodes: int) -> torch.Tensor:
+    """Sort by (src, dst) and drop duplicates (torch_geometric.utils.coalesce), on the device."""
+    dev = edge_index.device
+    src = edge_index[0].to(torch.int64).contiguous()
+    dst = edge_index[1].to(torch.int64).contiguous()
+    nnz = src.numel()
+    out = torch.empty(2, max(nnz, 1), dtype=torch.int64, device=dev)
+    ws = _workspace(_size_query("bf_coalesce_workspace_size", nnz), dev)
+    cnt = C.c_int64(0)
+    N.call("bf_coalesce", _p(src), _p(dst), nnz, num_nodes, C.c_void_p(out[0].data_ptr()),
+           C.c_void_p(out[1].data_ptr()), C.byref(cnt), _p(ws), ws.numel(), _stream(dev))
+    return out[:, : cnt.value]
+
+
 def walk_uniforms(q_lo: int, n_q: int, walks_per_node: int, walk_length: int, philox_seed: int,
                   philox_offset: int = 0, device="cuda") -> torch.Tensor:
     """The Philox uniforms of the production walk as a [n_q*P, L] float32 tensor."""
@@ -108,8 +159,11 @@ def real_select_merge(in_ptr, in_src, q_lo: int, n_q: int, k_real: int, key_seed
 
 def build_edge_table(rowptr, col, in_ptr, in_src, num_edges: int, q_lo: int, n_q: int, walks_per_node: int,
                      walk_length: int, k_real: int, k_rw: int, edge_seed: int, u=None, philox_seed: int = 0,
-                     philox_offset: int = 0):
-    """Fused budgeted build (bf_build_edge_table): (table [n_q, k_real+k_rw], row_len [n_q])."""
+                     philox_offset: int = 0, out=None):
+    """Fused budgeted build (bf_build_edge_table): (table [n_q, k_real+k_rw], row_len [n_q]).
+
+    ``out=(table, row_len)`` writes into caller-provided (contiguous) tensors.
+    """
     dev = rowptr.device
     _require(rowptr, "rowptr", torch.int64)
     _require(col, "col", torch.int32, dev)
@@ -120,8 +174,15 @@ def build_edge_table(rowptr, col, in_ptr, in_src, num_edges: int, q_lo: int, n_q
         if tuple(u.shape) != (n_q * walks_per_node, walk_length):
             raise ValueError(f"u must be [{n_q * walks_per_node}, {walk_length}], got {tuple(u.shape)}")
     width = max(k_real, 0) + max(k_rw, 0)
-    table = torch.empty(n_q, width, dtype=torch.int32, device=dev)
-    row_len = torch.empty(n_q, dtype=torch.int32, device=dev)
+    if out is None:
+        table = torch.empty(n_q, width, dtype=torch.int32, device=dev)
+        row_len = torch.empty(n_q, dtype=torch.int32, device=dev)
+    else:
+        table, row_len = out
+        _require(table, "table", torch.int32, dev)
+        _require(row_len, "row_len", torch.int32, dev)
+        if tuple(table.shape) != (n_q, width) or tuple(row_len.shape) != (n_q,):
+            raise ValueError(f"out tensors must be [{n_q}, {width}] and [{n_q}]")
     ws_bytes = _size_query("bf_build_edge_table_workspace_size", n_q, max(k_rw, 0))
     ws = _workspace(ws_bytes, dev)
     N.call("bf_build_edge_table", _p(rowptr), _p(col), _p(in_ptr), _p(in_src), rowptr.numel() - 1, num_edges,

@@ -71,6 +71,27 @@ int bf_random_walk(const int64_t* rowptr, const int32_t* col, int64_t num_nodes,
                    const float* u, uint64_t philox_seed, uint64_t philox_offset,
                    int64_t* walks, void* stream);
 
+/* Walks from arbitrary start nodes: the general form of the _run_random_walk
+ * seam (gt_sp/utils.py:1387, argument `starts`). Walk i starts at starts[i]
+ * (int64 [n_walks]) and, without u, draws Philox walk id walk_id_base + i, so
+ * starts = arange(N).repeat_interleave(P) with base 0 reproduces bf_random_walk. */
+int bf_random_walk_starts(const int64_t* rowptr, const int32_t* col, int64_t num_nodes,
+                          const int64_t* starts, int64_t n_walks, int32_t walk_length,
+                          const float* u, uint64_t philox_seed, uint64_t philox_offset,
+                          uint64_t walk_id_base, int64_t* walks, void* stream);
+
+/* The RW hop pool of a walk tensor, in the reference's order.
+ * Replaces the hop loop of compute_hop_buckets_random_walk (gt_sp/utils.py:
+ * 1232-1248) for one bucket: for d = min_hop..L (d-major), then walk order,
+ * emit (kv = walks[w,d], q = walks[w,0]) iff kv >= 0 and (d == 1 or
+ * kv != walks[w,d-1]). pool_kv / pool_q int64 need capacity n_walks*(L-min_hop+1);
+ * the pool size is returned in *count_host (the call synchronises the stream).
+ * Workspace: bf_hop_pool_workspace_size.                                       */
+int bf_hop_pool_workspace_size(int64_t n_walks, int32_t walk_length, int32_t min_hop, size_t* bytes);
+int bf_hop_pool(const int64_t* walks, int64_t n_walks, int32_t walk_length, int32_t min_hop,
+                int64_t* pool_kv, int64_t* pool_q, int64_t* count_host,
+                void* workspace, size_t workspace_bytes, void* stream);
+
 /* The Philox uniforms bf_random_walk draws when u == NULL, written as the
  * float32 [n_q*P, L] tensor that reproduces them through the u argument. */
 int bf_walk_uniforms(int64_t q_lo, int64_t n_q, int32_t walks_per_node, int32_t walk_length,
@@ -147,6 +168,16 @@ int bf_table_to_csr(const int32_t* table, const int32_t* row_len, int64_t n_rows
 int bf_coo_to_csr_workspace_size(int64_t nnz, int64_t n_q, size_t* bytes);
 int bf_coo_to_csr(const int64_t* src, const int64_t* dst, int64_t nnz, int64_t n_q, int64_t n_kv,
                   int64_t* qptr, int32_t* kv, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Coalesce of a COO edge list: torch_geometric.utils.coalesce as used by
+ * _merge_edge_index_list (gt_sp/utils.py:877-887): sorted by (src, dst) with
+ * duplicates removed. out_src / out_dst int64 need capacity nnz; the number of
+ * unique edges is returned in *count_host (the call synchronises the stream).
+ * Workspace: bf_coalesce_workspace_size.                                       */
+int bf_coalesce_workspace_size(int64_t nnz, size_t* bytes);
+int bf_coalesce(const int64_t* src, const int64_t* dst, int64_t nnz, int64_t num_nodes,
+                int64_t* out_src, int64_t* out_dst, int64_t* count_host,
+                void* workspace, size_t workspace_bytes, void* stream);
 
 /* Reverse (key-major) index of an attention CSR: kptr int64 [n_kv+1], and for
  * each reverse entry its query kq int32 [nnz] and its CSR position ke int32
