@@ -37,6 +37,18 @@ CONFIGS = {
                     "B=8 (4,4), fp32",
                n=169_343, e=1_166_243, kind="chung_lu", H=8, hn=16, L=4, P=2, b_r=4, b_w=4, dtype="float32",
                token=True),
+    "c3": dict(name="c3: Chung-Lu power-law N=2,449,029 E=61,859,140 (max deg 17K), GT hidden 128, 8 heads, L=4 P=4 "
+                    "B=16 (8,8), bf16",
+               n=2_449_029, e=61_859_140, kind="device", max_degree=17_000, H=8, hn=16, L=4, P=4, b_r=8, b_w=8,
+               dtype="bfloat16", token=False, cpu_sample=200_000),
+    "c4": dict(name="c4: power-law N=2,923,922 E=13,975,788, GraphGPS hidden 128, 8 heads, L=8 P=4 B=32 (16,16), "
+                    "bf16 (attention dropout off)",
+               n=2_923_922, e=13_975_788, kind="device", H=8, hn=16, L=8, P=4, b_r=16, b_w=16, dtype="bfloat16",
+               token=False, cpu_sample=200_000),
+    "c5": dict(name="c5: one GPU's 27.8M-query shard of a power-law graph N=111,059,956 E=1.6B (max deg 100K), "
+                    "Graphormer hidden 128, 8 heads, L=4 P=2 B=8 (4,4), bf16",
+               n=111_059_956, e=1_600_000_000, kind="device", max_degree=100_000, H=8, hn=16, L=4, P=2, b_r=4,
+               b_w=4, dtype="bfloat16", token=False, n_q=27_800_000, cpu_sample=None),
 }
 
 
@@ -179,25 +191,32 @@ def main(argv=None):
 
     from budgetformer_amd import _native, hip_ops
     from budgetformer_amd.edges import build_attention_edges
-    from budgetformer_amd.graph import CSRGraph, chung_lu_csr, uniform_random_csr
+    from budgetformer_amd.graph import CSRGraph, chung_lu_csr, chung_lu_device, uniform_random_csr
 
     cfg = CONFIGS[args.config]
     dev = torch.device("cuda:0")
     _native.load()
     t_setup = time.time()
-    if cfg["kind"] == "chung_lu":
-        rowptr, col = chung_lu_csr(cfg["n"], cfg["e"], exponent=2.1, seed=42)
-    else:
-        rowptr, col = uniform_random_csr(cfg["n"], cfg["e"], seed=42)
     n = cfg["n"]
-    g = CSRGraph.from_csr(rowptr, col, n, device=dev)
+    rowptr = col = None
+    if cfg["kind"] == "device":
+        g = chung_lu_device(n, cfg["e"], exponent=2.1, seed=42, max_degree=cfg.get("max_degree"), device=dev)
+    else:
+        if cfg["kind"] == "chung_lu":
+            rowptr, col = chung_lu_csr(n, cfg["e"], exponent=2.1, seed=42)
+        else:
+            rowptr, col = uniform_random_csr(n, cfg["e"], seed=42)
+        g = CSRGraph.from_csr(rowptr, col, n, device=dev)
     H, hn = cfg["H"], cfg["hn"]
     D = H * hn
     dt = getattr(torch, cfg["dtype"])
     s_bytes = torch.finfo(dt).bits // 8
-    S = n + (1 if cfg["token"] else 0)
+    n_rows = cfg.get("n_q") or n                       # queries this GPU builds
+    S = n_rows + (1 if cfg["token"] else 0)            # attention query rows
+    S_kv = n + (1 if cfg["token"] else 0)              # key/value rows
     gq = torch.Generator(device=dev).manual_seed(43)
-    q, k, v = (torch.randn(S, H, hn, generator=gq, device=dev, dtype=torch.float32).to(dt) for _ in range(3))
+    q = torch.randn(S, H, hn, generator=gq, device=dev, dtype=torch.float32).to(dt)
+    k, v = (torch.randn(S_kv, H, hn, generator=gq, device=dev, dtype=torch.float32).to(dt) for _ in range(2))
     dout = torch.randn(S, H, hn, generator=torch.Generator(device=dev).manual_seed(47), device=dev,
                        dtype=torch.float32).to(dt)
     torch.cuda.synchronize()
@@ -208,7 +227,7 @@ def main(argv=None):
 
     def build():
         tab = build_attention_edges(g, real_edges_per_query=cfg["b_r"], rw_edges_per_query=cfg["b_w"],
-                                    walk_length=cfg["L"], walks_per_node=cfg["P"], edge_seed=42,
+                                    walk_length=cfg["L"], walks_per_node=cfg["P"], edge_seed=42, n_q=n_rows,
                                     global_token=cfg["token"])
         idx = tab.attention_index(chunk=chunk, item=item)
         idx.ensure_backward()
@@ -245,7 +264,7 @@ def main(argv=None):
           f"{attn_ms:.3f})", flush=True)
 
     nnz = idx.nnz
-    a_fwd, a_bwd = attention_bytes(s_bytes, D, H, S, S, nnz)
+    a_fwd, a_bwd = attention_bytes(s_bytes, D, H, S, S_kv, nnz)
     attn_gbs = (a_fwd + a_bwd) / (attn_ms * 1e-3) / 1e9
 
     # per-kernel roofline of the three row kernels
@@ -273,11 +292,13 @@ def main(argv=None):
                 "algorithmic_bytes": dom["algorithmic_bytes"]}
 
     # edge-builder figures: RW pool edges = valid hop entries (d == 1, or the walk moved at step d)
-    n_walks = n * cfg["P"]
-    walks = hip_ops.random_walk(g.rowptr, g.col, 0, n, cfg["P"], cfg["L"], philox_seed=42)
-    moved = walks[:, 2:] != walks[:, 1:-1]
-    pool_edges = int(n_walks + moved.sum().item())
-    del walks, moved
+    n_walks = n_rows * cfg["P"]
+    pool_edges = 0
+    for lo in range(0, n_rows, 4_000_000):             # count in slices to bound the walk tensor
+        cnt = min(4_000_000, n_rows - lo)
+        walks = hip_ops.random_walk(g.rowptr, g.col, lo, cnt, cfg["P"], cfg["L"], philox_seed=42)
+        pool_edges += cnt * cfg["P"] + int((walks[:, 2:] != walks[:, 1:-1]).sum().item())
+        del walks
     rw_ms = kernels.get("rw_select_kernel", {}).get("avg_ms")
     merge_ms = kernels.get("real_select_merge_kernel", {}).get("avg_ms")
     table_entries = int(tab.row_len.sum().item())
@@ -296,6 +317,7 @@ def main(argv=None):
         "dtype": "f32" if dt == torch.float32 else "bf16",
         "data": "synthetic (seeded Chung-Lu graph and N(0,1) activations; no dataset)",
         "config": {"workload": cfg["name"], "num_nodes": n, "num_edges": g.num_edges, "queries": S,
+                   "kv_rows": S_kv,
                    "table_entries": table_entries, "attention_edges": nnz, "heads": H, "head_dim": hn,
                    "walk_length": cfg["L"], "walks_per_node": cfg["P"], "budget": [cfg["b_r"], cfg["b_w"]],
                    "global_token": cfg["token"], "split_chunk": chunk, "split_item": item},
@@ -314,13 +336,25 @@ def main(argv=None):
     }
 
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(cfg, rowptr, col, idx, q, k, v, dout, s_bytes, D, H, S, nnz)
+        if cfg.get("cpu_sample", 0) is None:
+            result["cpu_baseline"] = {"value": None, "unit": "GB/s", "cores": os.cpu_count(), "kind": "port",
+                                      "sample": "skipped: the CPU oracle would need the 111M-row K/V and 1.6B-edge "
+                                                "topology in host memory; see c3/c4 for sampled CPU timings"}
+        else:
+            result["cpu_baseline"] = cpu_baseline(cfg, g, tab, idx, q, k, v, dout, s_bytes, D, H)
     print(json.dumps(result), flush=True)
     return 0
 
 
-def cpu_baseline(cfg, rowptr, col, idx, q, k, v, dout, s_bytes, D, H, S, nnz):
-    """The CPU oracle (the reference algorithm restated in torch/numpy) on this host's cores."""
+def cpu_baseline(cfg, g, tab, idx, q, k, v, dout, s_bytes, D, H):
+    """The CPU oracle (the reference algorithm restated in torch/numpy) on this host's cores.
+
+    Small configs run the whole workload; large ones (``cpu_sample`` set) run
+    the first ``cpu_sample`` queries (their attention edges with the touched
+    K/V rows relabelled, and their edge-table rows) and scale the time linearly
+    to the full query count.
+    """
+    import numpy as np
     import torch
 
     from oracle import edge_table as et
@@ -329,33 +363,56 @@ def cpu_baseline(cfg, rowptr, col, idx, q, k, v, dout, s_bytes, D, H, S, nnz):
 
     threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
-    ei = torch.stack([idx.kv.cpu().long(), idx.entry_rows().cpu()])
-    qc, kc, vc, dc = (t.float().cpu() for t in (q, k, v, dout))
+    n = cfg["n"]
+    n_rows = cfg.get("n_q") or n
+    sample = cfg.get("cpu_sample") or n_rows
+    sample = min(sample, n_rows)
+    scale = n_rows / sample
+    # attention edges of the first `sample` query rows (+ the token row when present)
+    q_hi = sample + (1 if cfg["token"] else 0)
+    e_hi = int(idx.qptr[q_hi].item())
+    rows = idx.entry_rows()[:e_hi].cpu()
+    kv = idx.kv[:e_hi].cpu().long()
+    uniq, inv = torch.unique(kv, return_inverse=True)
+    ei = torch.stack([inv, rows])
+    # the oracle (like the reference) indexes queries and kv rows in one node space: pad both to M rows
+    M = max(q_hi, uniq.numel())
+
+    def padded(t):
+        out = torch.zeros(M, *t.shape[1:], dtype=torch.float32)
+        out[: t.shape[0]] = t.float().cpu()
+        return out
+
+    qc, dc = padded(q[:q_hi]), padded(dout[:q_hi])
+    kc, vc = padded(k[uniq.to(k.device)]), padded(v[uniq.to(v.device)])
     times = []
-    budget_s = 25.0
     t_all = time.perf_counter()
     while True:
         t0 = time.perf_counter()
         sa.attention_fwd_bwd_autograd(kc, qc, vc, ei, dc)
         times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_all > budget_s / 2 or len(times) >= 3:
+        if time.perf_counter() - t_all > 12.0 or len(times) >= 3:
             break
-    attn_s = min(times)
-    a_fwd, a_bwd = attention_bytes(s_bytes, D, H, S, S, nnz)
-    n = cfg["n"]
-    u = philox.walk_uniforms(0, n, cfg["P"], cfg["L"], 42)
+    attn_s = min(times) * scale
+    nnz = idx.nnz
+    a_fwd, a_bwd = attention_bytes(s_bytes, D, H, idx.n_q, idx.n_kv, nnz)
+    # edge build of the same queries
+    rowptr = g.rowptr.cpu().numpy()
+    col = g.col.cpu().numpy()
+    u = philox.walk_uniforms(0, sample, cfg["P"], cfg["L"], 42)
     t0 = time.perf_counter()
-    et.build_edge_table(rowptr, col, n, cfg["b_r"], cfg["b_w"], cfg["L"], cfg["P"], 42, u)
-    build_s = time.perf_counter() - t0
+    et.build_edge_table(rowptr, col, n, cfg["b_r"], cfg["b_w"], cfg["L"], cfg["P"], 42, u, q_lo=0, n_q=sample)
+    build_s = (time.perf_counter() - t0) * scale
+    what = "full" if sample == n_rows else f"first {sample:,} of {n_rows:,} queries, time scaled x{scale:.2f} to"
     print(f"[bench] cpu baseline: attn fwd+bwd {attn_s * 1e3:.1f} ms, edge build {build_s * 1e3:.1f} ms "
-          f"({threads} threads)", flush=True)
+          f"({threads} threads; {what} the workload)", flush=True)
     return {
         "value": round((a_fwd + a_bwd) / attn_s / 1e9, 2),
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"full {cfg['name'].split(':')[0]} workload: attention fwd+bwd over all {nnz:,} edges "
-                  f"(torch CPU autograd, best of {len(times)}), edge build over all {n:,} queries (numpy)",
+        "sample": f"{what} {cfg['name'].split(':')[0]} workload: attention fwd+bwd (torch CPU autograd, fp32, best "
+                  f"of {len(times)}) and the numpy edge build of those queries",
         "attn_fwd_bwd_ms": round(attn_s * 1e3, 2),
         "edge_build_ms": round(build_s * 1e3, 2),
         "cpu_model": cpu_model(),

@@ -343,6 +343,14 @@ __device__ __forceinline__ RowGrad row_grad(const T* __restrict__ out, const T* 
   return r;
 }
 
+// Per (query, head) record the key-major pass gathers: {1/D', Delta/D'} in one
+// float2, so each reverse entry touches one 64-byte stats line instead of two.
+__device__ __forceinline__ void store_row_stat(float2* __restrict__ rstat, int64_t row, const Shape& sh,
+                                               const GroupPos& g, const RowGrad& rg) {
+  const float inv = 1.0f / rg.dprime;
+  rstat[row * sh.H + g.head] = make_float2(inv, rg.delta * inv);
+}
+
 // dq contributions of entries [beg, end) of one query row; writes dbias per entry.
 template <typename T>
 __device__ __forceinline__ void dq_segment(const T* __restrict__ k, const T* __restrict__ v,
@@ -419,7 +427,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_q_rows_kernel(
     const int64_t* __restrict__ qptr, const int32_t* __restrict__ kv,
     const float* __restrict__ bias, const float* __restrict__ factor,
     const T* __restrict__ out, const float* __restrict__ Z, const T* __restrict__ dout,
-    T* __restrict__ dq, float* __restrict__ dbias, float* __restrict__ delta, int64_t n_q,
+    T* __restrict__ dq, float* __restrict__ dbias, float2* __restrict__ rstat, int64_t n_q,
     Shape sh, int chunk) {
   constexpr int V = Elem<T>::kPerVec;
   const int64_t row = group_index(sh);
@@ -435,7 +443,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_q_rows_kernel(
   dq_segment<T>(k, v, kv, bias, factor, dbias, beg, end, sh, g, rg, qv, gv, acc);
   if (g.act) {
     Elem<T>::store(dq + row * sh.D + g.col0, acc);
-    if (g.lead) delta[row * sh.H + g.head] = rg.delta;
+    if (g.lead) store_row_stat(rstat, row, sh, g, rg);
   }
 }
 
@@ -444,7 +452,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_q_items_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const int32_t* __restrict__ kv, const float* __restrict__ bias,
     const float* __restrict__ factor, const T* __restrict__ out, const float* __restrict__ Z,
-    const T* __restrict__ dout, float* __restrict__ dbias, float* __restrict__ delta,
+    const T* __restrict__ dout, float* __restrict__ dbias, float2* __restrict__ rstat,
     float* __restrict__ partials, Items it, Shape sh) {
   constexpr int V = Elem<T>::kPerVec;
   extern __shared__ float lds[];
@@ -459,7 +467,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_q_items_kernel(
   float z = 0.f;
   block_combine<V>(lds, it.stride, sh, g, acc, unused, false, z, false);
   store_record<V>(partials, it.stride, sh, g, acc, unused, false, z, false);
-  if (r.j == 0 && (threadIdx.x >> sh.lpr_log2) == 0 && g.lead) delta[int64_t(r.row) * sh.H + g.head] = rg.delta;
+  if (r.j == 0 && (threadIdx.x >> sh.lpr_log2) == 0 && g.lead) store_row_stat(rstat, r.row, sh, g, rg);
 }
 
 template <typename T>
@@ -481,8 +489,7 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
                                             const int32_t* __restrict__ ke,
                                             const float* __restrict__ bias,
                                             const float* __restrict__ factor,
-                                            const float* __restrict__ Z,
-                                            const float* __restrict__ delta, int64_t beg,
+                                            const float2* __restrict__ rstat, int64_t beg,
                                             int64_t end, const Shape& sh, const GroupPos& g,
                                             const float (&kk)[Elem<T>::kPerVec],
                                             const float (&vv)[Elem<T>::kPerVec],
@@ -499,19 +506,18 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
       ok[u] = i0 + u < end;
       t[u] = ok[u] ? kq[i0 + u] : 0;
     }
-    float qq[kUnroll][V], gg[kUnroll][V], zz[kUnroll], dl[kUnroll];
+    float qq[kUnroll][V], gg[kUnroll][V];
+    float2 rs[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       if (ok[u] && g.act) {
         Elem<T>::load(q + int64_t(t[u]) * sh.D + g.col0, qq[u]);
         Elem<T>::load(dout + int64_t(t[u]) * sh.D + g.col0, gg[u]);
-        zz[u] = Z[int64_t(t[u]) * sh.H + g.head];
-        dl[u] = delta[int64_t(t[u]) * sh.H + g.head];
+        rs[u] = rstat[int64_t(t[u]) * sh.H + g.head];
       } else {
 #pragma unroll
         for (int i = 0; i < V; ++i) qq[u][i] = gg[u][i] = 0.f;
-        zz[u] = 0.f;
-        dl[u] = 0.f;
+        rs[u] = make_float2(0.f, 0.f);
       }
     }
     float d[kUnroll], w[kUnroll];
@@ -542,10 +548,9 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
       if (bias) a += bias[e * sh.H + g.head];
       const float p = expf(a);
       const float f = factor ? factor[e * sh.H + g.head] : 1.f;
-      const float dprime = zz[u] + kEps;
-      const float gb = (f * (w[u] / dprime) - dl[u] / dprime) * p;
+      const float gb = (f * w[u] * rs[u].x - rs[u].y) * p;     // rs = {1/D', Delta/D'}
       const float ga = (apre >= -kClamp && apre <= kClamp) ? gb : 0.f;
-      const float pf = (p * f) / dprime;
+      const float pf = p * f * rs[u].x;
 #pragma unroll
       for (int i = 0; i < V; ++i) {
         dv[i] += pf * gg[u][i];
@@ -560,9 +565,8 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_rows_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const int64_t* __restrict__ kptr, const int32_t* __restrict__ kq,
     const int32_t* __restrict__ ke, const float* __restrict__ bias,
-    const float* __restrict__ factor, const float* __restrict__ Z,
-    const T* __restrict__ dout, const float* __restrict__ delta, T* __restrict__ dk,
-    T* __restrict__ dv, int64_t n_kv, Shape sh, int chunk) {
+    const float* __restrict__ factor, const T* __restrict__ dout, const float2* __restrict__ rstat,
+    T* __restrict__ dk, T* __restrict__ dv, int64_t n_kv, Shape sh, int chunk) {
   constexpr int V = Elem<T>::kPerVec;
   const int64_t row = group_index(sh);
   if (row >= n_kv) return;
@@ -574,7 +578,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_rows_kernel(
   load_row<T, V>(v, row, sh.D, g, vv);
 #pragma unroll
   for (int i = 0; i < V; ++i) ak[i] = av[i] = 0.f;
-  dkv_segment<T>(q, dout, kq, ke, bias, factor, Z, delta, beg, end, sh, g, kk, vv, ak, av);
+  dkv_segment<T>(q, dout, kq, ke, bias, factor, rstat, beg, end, sh, g, kk, vv, ak, av);
   if (g.act) {
     Elem<T>::store(dk + row * sh.D + g.col0, ak);
     Elem<T>::store(dv + row * sh.D + g.col0, av);
@@ -586,7 +590,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_items_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const int32_t* __restrict__ kq, const int32_t* __restrict__ ke,
     const float* __restrict__ bias, const float* __restrict__ factor,
-    const float* __restrict__ Z, const T* __restrict__ dout, const float* __restrict__ delta,
+    const T* __restrict__ dout, const float2* __restrict__ rstat,
     float* __restrict__ partials, Items it, Shape sh) {
   constexpr int V = Elem<T>::kPerVec;
   extern __shared__ float lds[];
@@ -597,7 +601,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_items_kernel(
   load_row<T, V>(v, r.row, sh.D, g, vv);
 #pragma unroll
   for (int i = 0; i < V; ++i) ak[i] = av[i] = 0.f;
-  dkv_segment<T>(q, dout, kq, ke, bias, factor, Z, delta, r.beg, r.end, sh, g, kk, vv, ak, av);
+  dkv_segment<T>(q, dout, kq, ke, bias, factor, rstat, r.beg, r.end, sh, g, kk, vv, ak, av);
   float z = 0.f;
   block_combine<V>(lds, it.stride, sh, g, ak, av, true, z, false);
   store_record<V>(partials, it.stride, sh, g, ak, av, true, z, false);
@@ -712,8 +716,9 @@ int fwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
 template <typename T>
 int bwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const void* k, const void* v,
              const float* bias, const float* factor, const void* out, const float* Z,
-             const void* dout, void* dq, void* dk, void* dv, float* dbias, float* delta,
+             const void* dout, void* dq, void* dk, void* dv, float* dbias, float* rstat_f,
              float* partials, hipStream_t st) {
+  float2* rstat = reinterpret_cast<float2*>(rstat_f);
   const T* Q = static_cast<const T*>(q);
   const T* K = static_cast<const T*>(k);
   const T* Vv = static_cast<const T*>(v);
@@ -722,14 +727,14 @@ int bwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
   const size_t lds = combine_lds_bytes(sh);
   if (idx->n_q > 0) {
     BF_LAUNCH("attn_bwd_q_rows_kernel", attn_bwd_q_rows_kernel<T>, dim3(grid_for(idx->n_q, sh)), dim3(kBlock), 0, st,
-              Q, K, Vv, idx->qptr, idx->kv, bias, factor, O, Z, dO, static_cast<T*>(dq), dbias, delta, idx->n_q, sh,
+              Q, K, Vv, idx->qptr, idx->kv, bias, factor, O, Z, dO, static_cast<T*>(dq), dbias, rstat, idx->n_q, sh,
               idx->chunk);
     BF_CHECK_LAUNCH();
   }
   if (idx->q_items > 0) {
     const Items it = query_items(idx, sh);
     BF_LAUNCH("attn_bwd_q_items_kernel", attn_bwd_q_items_kernel<T>, dim3(unsigned(idx->q_items)), dim3(kBlock), lds,
-              st, Q, K, Vv, idx->kv, bias, factor, O, Z, dO, dbias, delta, partials, it, sh);
+              st, Q, K, Vv, idx->kv, bias, factor, O, Z, dO, dbias, rstat, partials, it, sh);
     BF_CHECK_LAUNCH();
     BF_LAUNCH("attn_bwd_q_reduce_kernel", attn_bwd_q_reduce_kernel<T>, dim3(unsigned(idx->q_heavy)), dim3(kBlock),
               lds, st, partials, static_cast<T*>(dq), it, sh);
@@ -737,14 +742,14 @@ int bwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
   }
   if (idx->n_kv > 0) {
     BF_LAUNCH("attn_bwd_kv_rows_kernel", attn_bwd_kv_rows_kernel<T>, dim3(grid_for(idx->n_kv, sh)), dim3(kBlock), 0,
-              st, Q, K, Vv, idx->kptr, idx->kq, idx->ke, bias, factor, Z, dO, delta, static_cast<T*>(dk),
+              st, Q, K, Vv, idx->kptr, idx->kq, idx->ke, bias, factor, dO, rstat, static_cast<T*>(dk),
               static_cast<T*>(dv), idx->n_kv, sh, idx->chunk);
     BF_CHECK_LAUNCH();
   }
   if (idx->k_items > 0) {
     const Items it = key_items(idx, sh);
     BF_LAUNCH("attn_bwd_kv_items_kernel", attn_bwd_kv_items_kernel<T>, dim3(unsigned(idx->k_items)), dim3(kBlock),
-              lds, st, Q, K, Vv, idx->kq, idx->ke, bias, factor, Z, dO, delta, partials, it, sh);
+              lds, st, Q, K, Vv, idx->kq, idx->ke, bias, factor, dO, rstat, partials, it, sh);
     BF_CHECK_LAUNCH();
     BF_LAUNCH("attn_bwd_kv_reduce_kernel", attn_bwd_kv_reduce_kernel<T>, dim3(unsigned(idx->k_heavy)), dim3(kBlock),
               lds, st, partials, static_cast<T*>(dk), static_cast<T*>(dv), it, sh);
@@ -784,21 +789,22 @@ extern "C" int bf_attn_fwd(const bf_attn_index* idx, int32_t dtype, int32_t num_
 extern "C" int bf_attn_bwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
                            const void* q, const void* k, const void* v, const float* bias,
                            const float* factor, const void* out, const float* Z, const void* dout,
-                           void* dq, void* dk, void* dv, float* dbias, float* delta, float* partials,
+                           void* dq, void* dk, void* dv, float* dbias, float* rowstat, float* partials,
                            void* stream) {
   Shape sh;
   int rc = make_shape(dtype, num_heads, head_dim, sh);
   if (rc) return rc;
   if ((rc = check_index(idx, true))) return rc;
-  BF_CHECK_ARG(q && k && v && out && Z && dout && dq && dk && dv && delta, "attn_bwd: null tensor");
+  BF_CHECK_ARG(q && k && v && out && Z && dout && dq && dk && dv && rowstat, "attn_bwd: null tensor");
+  BF_CHECK_ARG((reinterpret_cast<uintptr_t>(rowstat) & 7u) == 0, "attn_bwd: rowstat must be 8-byte aligned");
   BF_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out) && aligned16(dout) &&
                    aligned16(dq) && aligned16(dk) && aligned16(dv),
                "attn_bwd: tensors must be 16-byte aligned");
   BF_CHECK_ARG((idx->q_items == 0 && idx->k_items == 0) || partials,
                "attn_bwd: partials buffer required for split rows");
   if (dtype == BF_DTYPE_F32)
-    return bwd_impl<float>(idx, sh, q, k, v, bias, factor, out, Z, dout, dq, dk, dv, dbias, delta,
+    return bwd_impl<float>(idx, sh, q, k, v, bias, factor, out, Z, dout, dq, dk, dv, dbias, rowstat,
                            partials, as_stream(stream));
-  return bwd_impl<uint16_t>(idx, sh, q, k, v, bias, factor, out, Z, dout, dq, dk, dv, dbias, delta,
+  return bwd_impl<uint16_t>(idx, sh, q, k, v, bias, factor, out, Z, dout, dq, dk, dv, dbias, rowstat,
                             partials, as_stream(stream));
 }

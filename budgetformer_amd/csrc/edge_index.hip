@@ -102,11 +102,6 @@ __global__ void coo_kv_kernel(const uint64_t* __restrict__ keys, int64_t nnz, ui
 }
 
 // ---------------------------------------------------------------- reverse index
-__global__ void iota_kernel(int32_t* __restrict__ x, int64_t n) {
-  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
-  if (i < n) x[i] = int32_t(i);
-}
-
 // rows[i] = r with ptr[r] <= i < ptr[r+1] (binary search; balanced for any row length).
 template <typename R>
 __global__ void expand_rows_kernel(const int64_t* __restrict__ ptr, int64_t n_rows, int64_t nnz,
@@ -121,10 +116,48 @@ __global__ void expand_rows_kernel(const int64_t* __restrict__ ptr, int64_t n_ro
   rows[i] = R(lo);
 }
 
-__global__ void gather_rows_kernel(const int32_t* __restrict__ rows_of_entry, const int32_t* __restrict__ ke,
-                                   int64_t nnz, int32_t* __restrict__ kq) {
+// Row ids of a CSR's entries in two streaming passes: each non-empty row marks
+// its first entry with its id, then an inclusive max-scan fills the rest.
+__global__ void row_marks_kernel(const int64_t* __restrict__ ptr, int64_t n_rows, int32_t* __restrict__ marks) {
+  const int64_t r = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (r >= n_rows) return;
+  const int64_t b = ptr[r];
+  if (ptr[r + 1] > b) marks[b] = int32_t(r);
+}
+
+__global__ void pack_row_entry_kernel(const int32_t* __restrict__ rows, int64_t nnz, uint64_t* __restrict__ vals) {
   const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
-  if (i < nnz) kq[i] = rows_of_entry[ke[i]];
+  if (i < nnz) vals[i] = (uint64_t(uint32_t(rows[i])) << 32) | uint32_t(i);
+}
+
+__global__ void unpack_row_entry_kernel(const uint64_t* __restrict__ vals, int64_t nnz, int32_t* __restrict__ kq,
+                                        int32_t* __restrict__ ke) {
+  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= nnz) return;
+  const uint64_t x = vals[i];
+  kq[i] = int32_t(x >> 32);
+  ke[i] = int32_t(uint32_t(x));
+}
+
+struct MaxOp {
+  __device__ __forceinline__ int32_t operator()(int32_t a, int32_t b) const { return a > b ? a : b; }
+};
+
+size_t row_ids_temp_bytes(int64_t nnz) {
+  size_t bytes = 0;
+  (void)hipcub::DeviceScan::InclusiveScan(nullptr, bytes, static_cast<const int32_t*>(nullptr),
+                                          static_cast<int32_t*>(nullptr), MaxOp(), int(nnz > 0 ? nnz : 1));
+  return bytes;
+}
+
+// rows[i] for every entry of a CSR (int32); marks and rows may not alias.
+int row_ids(const int64_t* ptr, int64_t n_rows, int64_t nnz, int32_t* marks, int32_t* rows, void* temp,
+            size_t temp_bytes, hipStream_t st) {
+  BF_CHECK_HIP(hipMemsetAsync(marks, 0, size_t(nnz) * sizeof(int32_t), st));
+  BF_LAUNCH("row_marks_kernel", row_marks_kernel, dim3(blocks_for(n_rows)), dim3(kThreads), 0, st, ptr, n_rows, marks);
+  BF_CHECK_LAUNCH();
+  BF_CHECK_HIP(hipcub::DeviceScan::InclusiveScan(temp, temp_bytes, marks, rows, MaxOp(), int(nnz), st));
+  return BF_OK;
 }
 
 // ---------------------------------------------------------------- split plans
@@ -267,9 +300,12 @@ extern "C" int bf_reverse_index_workspace_size(int64_t nnz, int64_t n_kv, size_t
   size_t sort_bytes = 0;
   const int n = int(nnz > 0 ? nnz : 1);
   (void)hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, static_cast<const uint32_t*>(nullptr),
-                                     static_cast<uint32_t*>(nullptr), static_cast<const int32_t*>(nullptr),
-                                     static_cast<int32_t*>(nullptr), n);
-  *bytes = 3 * align_up(size_t(n) * 4) + align_up(sort_bytes) + 256;
+                                           static_cast<uint32_t*>(nullptr), static_cast<const uint64_t*>(nullptr),
+                                           static_cast<uint64_t*>(nullptr), n);
+  const size_t scan_bytes = row_ids_temp_bytes(nnz);
+  // keys_out (4) + marks (4) + rows (4) + packed values in/out (8 + 8) bytes per entry, then temp
+  *bytes = 3 * align_up(size_t(n) * 4) + 2 * align_up(size_t(n) * 8) +
+           align_up(sort_bytes > scan_bytes ? sort_bytes : scan_bytes) + 256;
   return BF_OK;
 }
 
@@ -287,26 +323,29 @@ extern "C" int bf_reverse_index(const int64_t* qptr, const int32_t* kv, int64_t 
     return BF_OK;
   }
   BF_CHECK_ARG(kv && kq && ke, "reverse_index: null tensor");
-  const size_t slab = align_up(size_t(nnz) * 4);
-  auto* keys_out = static_cast<uint32_t*>(workspace);
-  auto* vals_in = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + slab);
-  auto* rows_of_entry = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + 2 * slab);
-  void* temp = static_cast<char*>(workspace) + 3 * slab;
-  size_t temp_bytes = 0;
-  (void)hipcub::DeviceRadixSort::SortPairs(nullptr, temp_bytes, reinterpret_cast<const uint32_t*>(kv), keys_out,
-                                     vals_in, ke, int(nnz));
-  BF_LAUNCH("iota_kernel", iota_kernel, dim3(blocks_for(nnz)), dim3(kThreads), 0, st, vals_in, nnz);
+  char* p = static_cast<char*>(workspace);
+  auto take = [&](size_t b) { char* q = p; p += align_up(b); return q; };
+  auto* keys_out = reinterpret_cast<uint32_t*>(take(size_t(nnz) * 4));
+  auto* marks = reinterpret_cast<int32_t*>(take(size_t(nnz) * 4));
+  auto* rows = reinterpret_cast<int32_t*>(take(size_t(nnz) * 4));
+  auto* vals_in = reinterpret_cast<uint64_t*>(take(size_t(nnz) * 8));
+  auto* vals_out = reinterpret_cast<uint64_t*>(take(size_t(nnz) * 8));
+  void* temp = p;
+  const size_t temp_bytes = workspace_bytes - size_t(p - static_cast<char*>(workspace));
+  int rc = row_ids(qptr, n_q, nnz, marks, rows, temp, temp_bytes, st);
+  if (rc) return rc;
+  BF_LAUNCH("pack_row_entry_kernel", pack_row_entry_kernel, dim3(blocks_for(nnz)), dim3(kThreads), 0, st, rows, nnz,
+            vals_in);
   BF_CHECK_LAUNCH();
   const int end_bit = bits_for(uint64_t(n_kv > 0 ? n_kv : 1));
-  BF_CHECK_HIP(hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, reinterpret_cast<const uint32_t*>(kv),
-                                                  keys_out, vals_in, ke, int(nnz), 0, end_bit, st));
+  size_t tb = temp_bytes;
+  BF_CHECK_HIP(hipcub::DeviceRadixSort::SortPairs(temp, tb, reinterpret_cast<const uint32_t*>(kv), keys_out, vals_in,
+                                                  vals_out, int(nnz), 0, end_bit, st));
   BF_LAUNCH("boundaries_kernel", boundaries_kernel<uint32_t>, dim3(blocks_for(nnz + 1)), dim3(kThreads), 0, st, keys_out,
-                     nnz, uint64_t(1), n_kv, kptr);
+            nnz, uint64_t(1), n_kv, kptr);
   BF_CHECK_LAUNCH();
-  BF_LAUNCH("expand_rows_kernel", expand_rows_kernel<int32_t>, dim3(blocks_for(nnz)), dim3(kThreads), 0, st, qptr, n_q, nnz,
-                     rows_of_entry);
-  BF_CHECK_LAUNCH();
-  BF_LAUNCH("gather_rows_kernel", gather_rows_kernel, dim3(blocks_for(nnz)), dim3(kThreads), 0, st, rows_of_entry, ke, nnz, kq);
+  BF_LAUNCH("unpack_row_entry_kernel", unpack_row_entry_kernel, dim3(blocks_for(nnz)), dim3(kThreads), 0, st, vals_out,
+            nnz, kq, ke);
   BF_CHECK_LAUNCH();
   return BF_OK;
 }

@@ -62,6 +62,30 @@ class CSRGraph:
         return cls(rowptr, col, in_ptr, in_src, int(num_nodes))
 
 
+def chung_lu_device(num_nodes: int, num_edges: int, exponent: float = 2.1, seed: int = 42,
+                    max_degree: Optional[float] = None, i0: float = 10.0, device="cuda") -> CSRGraph:
+    """Symmetric Chung-Lu graph with ``num_edges // 2`` distinct pairs, generated in HBM (bf_chung_lu).
+
+    Same degree law as ``chung_lu_csr`` but a different random stream; used for
+    the large benchmark shapes (tens of millions to 1.6B edges).
+    """
+    import ctypes as C
+    from . import _native as N
+    dev = torch.device(device)
+    pairs = int(num_edges) // 2
+    ws_bytes = C.c_size_t(0)
+    N.call("bf_chung_lu_workspace_size", num_nodes, pairs, C.byref(ws_bytes))
+    ws = torch.empty(ws_bytes.value, dtype=torch.uint8, device=dev)
+    rowptr = torch.empty(num_nodes + 1, dtype=torch.int64, device=dev)
+    col = torch.empty(2 * pairs, dtype=torch.int32, device=dev)
+    m = C.c_int64(0)
+    N.call("bf_chung_lu", num_nodes, pairs, float(exponent), float(i0), float(max_degree or 0.0), seed & (2 ** 64 - 1),
+           C.c_void_p(rowptr.data_ptr()), C.c_void_p(col.data_ptr()), C.byref(m), C.c_void_p(ws.data_ptr()),
+           ws.numel(), C.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
+    del ws
+    return CSRGraph(rowptr, col, rowptr, col, int(num_nodes))
+
+
 def chung_lu_csr(num_nodes: int, num_edges: int, exponent: float = 2.1, seed: int = 42,
                  max_degree: Optional[int] = None):
     """Symmetric power-law (Chung-Lu) graph as coalesced CSR numpy arrays.

@@ -428,9 +428,9 @@ def attn_backward(idx: AttentionIndex, q, k, v, out, Z, dout, bias=None, factor=
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
     dbias = torch.empty(idx.nnz, H, dtype=torch.float32, device=q.device) if need_dbias else None
-    delta = torch.empty(idx.n_q, H, dtype=torch.float32, device=q.device)
+    rowstat = torch.empty(idx.n_q, H, 2, dtype=torch.float32, device=q.device)
     parts = torch.empty(max(int(N.load().bf_attn_partials_floats(C.byref(st), H, hn)), 1), dtype=torch.float32,
                         device=q.device)
     N.call("bf_attn_bwd", C.byref(st), _DT[q.dtype], H, hn, _p(q), _p(k), _p(v), _p(bias), _p(factor), _p(out),
-           _p(Z), _p(dout), _p(dq), _p(dk), _p(dv), _p(dbias), _p(delta), _p(parts), _stream(q.device))
+           _p(Z), _p(dout), _p(dq), _p(dk), _p(dv), _p(dbias), _p(rowstat), _p(parts), _stream(q.device))
     return dq, dk, dv, dbias

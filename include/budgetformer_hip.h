@@ -145,6 +145,19 @@ int bf_build_edge_table(const int64_t* rowptr, const int32_t* col,
                         int32_t* table, int32_t* row_len,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* Synthetic symmetric power-law (Chung-Lu) graph generated on the device (no
+ * reference counterpart: the reference loads datasets from disk; the benchmark
+ * shapes here are synthetic). Expected degree of node i is proportional to
+ * (i + i0)^(-1/(exponent-1)), scaled to sum 2*pairs and capped at max_degree
+ * (<= 0: no cap); `pairs` distinct unordered pairs are drawn (Philox keyed by
+ * seed), then symmetrised. rowptr int64 [num_nodes+1], col int32 [2*pairs];
+ * *num_edges_host = 2*pairs. Synchronises the stream. Workspace:
+ * bf_chung_lu_workspace_size.                                                */
+int bf_chung_lu_workspace_size(int64_t num_nodes, int64_t pairs, size_t* bytes);
+int bf_chung_lu(int64_t num_nodes, int64_t pairs, double exponent, double i0, double max_degree,
+                uint64_t seed, int64_t* rowptr, int32_t* col, int64_t* num_edges_host,
+                void* workspace, size_t workspace_bytes, void* stream);
+
 /* ======================================================================
  * Edge index formats
  * ====================================================================== */
@@ -255,11 +268,13 @@ int bf_attn_fwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int3
 /* Backward of bf_attn_fwd (the autograd of the reference graph of ops,
  * models/graphormer_dist_node_level.py:231-263). Deterministic: dq by a
  * query-major pass, dk/dv by a key-major pass over the reverse index; no atomics.
- *   dbias: NULL or float32 [nnz, H]; delta: float32 [n_q, H] scratch.        */
+ *   dbias: NULL or float32 [nnz, H]; rowstat: float32 [n_q, H, 2] scratch
+ *   (per query and head {1/(Z+1e-6), Delta/(Z+1e-6)}, Delta = sum_j dO*out,
+ *   written by the query-major pass and read by the key-major pass).        */
 int bf_attn_bwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
                 const void* q, const void* k, const void* v, const float* bias, const float* factor,
                 const void* out, const float* Z, const void* dout,
-                void* dq, void* dk, void* dv, float* dbias, float* delta, float* partials,
+                void* dq, void* dk, void* dv, float* dbias, float* rowstat, float* partials,
                 void* stream);
 
 #ifdef __cplusplus

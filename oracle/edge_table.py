@@ -300,16 +300,39 @@ def coo_to_table(edge_index: np.ndarray, num_queries: int, width: int):
 
 
 def build_edge_table(rowptr, col, num_nodes: int, b_real: int, b_rw: int, walk_length: int,
-                     walks_per_node: int, edge_seed: int, u: np.ndarray):
-    """The [N, b_real+b_rw] table the GPU builder must reproduce bit-exactly.
+                     walks_per_node: int, edge_seed: int, u: np.ndarray, q_lo: int = 0, n_q: int = None):
+    """The [n_q, b_real+b_rw] table the GPU builder must reproduce bit-exactly.
 
     Same semantics as build_merged_edges without the global token, on a graph
     given as coalesced CSR (source rows); real candidates of query q are the
-    sources of edges into q.
+    sources of edges into q. With a query range [q_lo, q_lo+n_q) only those
+    queries are built (every selection is per query, so rows equal the full
+    build's); ``u`` then holds the range's walks, [n_q*P, L]. Both parts are
+    judged non-empty globally, as the reference's merge does.
     """
     rowptr = np.asarray(rowptr, dtype=np.int64)
     col = np.asarray(col, dtype=np.int64)
-    src = np.repeat(np.arange(num_nodes, dtype=np.int64), np.diff(rowptr))
-    ei = np.stack([src, col])
-    merged = build_merged_edges(ei, num_nodes, b_real, b_rw, walk_length, walks_per_node, edge_seed, u)
-    return coo_to_table(merged, num_nodes, max(1, b_real + b_rw))
+    n_q = num_nodes - q_lo if n_q is None else n_q
+    if q_lo == 0 and n_q == num_nodes:
+        src = np.repeat(np.arange(num_nodes, dtype=np.int64), np.diff(rowptr))
+        merged = build_merged_edges(np.stack([src, col]), num_nodes, b_real, b_rw, walk_length, walks_per_node,
+                                    edge_seed, u)
+        return coo_to_table(merged, num_nodes, max(1, b_real + b_rw))
+    parts = []
+    if b_real > 0 and col.size > 0:
+        src = np.repeat(np.arange(num_nodes, dtype=np.int64), np.diff(rowptr))
+        keep = (col >= q_lo) & (col < q_lo + n_q)
+        ei = np.stack([src[keep], col[keep]])
+        if ei.shape[1]:
+            parts.append(sample_edges_per_query_random(ei, b_real, edge_block_seed(edge_seed, REAL_SEED_OFFSET)))
+    both = b_real > 0 and col.size > 0 and b_rw > 0 and walks_per_node > 0
+    if b_rw > 0 and walks_per_node > 0:
+        walks = random_walk(rowptr, col, walk_starts(num_nodes, walks_per_node, q_lo, q_lo + n_q), walk_length, u)
+        pool = hop_edges_from_walks(walks, 1)
+        parts.append(sample_edges_per_query_random(pool, b_rw, edge_block_seed(edge_seed, RW_SEED_OFFSET)))
+    if both:
+        merged = coalesce(np.concatenate(parts, axis=1), num_nodes)
+    else:
+        merged = parts[0] if parts else np.zeros((2, 0), dtype=np.int64)
+    merged = np.stack([merged[0], merged[1] - q_lo])
+    return coo_to_table(merged, n_q, max(1, b_real + b_rw))

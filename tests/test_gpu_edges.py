@@ -24,7 +24,6 @@ def test_random_walk_injected_u_bit_exact(hip_device, P, L):
     from budgetformer_amd import hip_ops
     n = 3000
     rowptr, col = _graph(n, 20000, seed=P * 10 + L)
-    rowptr[-1:]  # dead ends exist: nodes with zero degree after trimming
     g = _dev_graph(rowptr, col, n, hip_device)
     u = np.random.default_rng(L).random((n * P, L), dtype=np.float32)
     u[0] = np.float32(1) - np.float32(2 ** -24)      # last-neighbour edge case
@@ -140,7 +139,30 @@ def test_c2_scale_properties(hip_device):
     assert ((t >= 0) == valid).all()
     rows_sorted = np.where(valid[:, 1:], np.diff(t, axis=1) > 0, True).all()
     assert rows_sorted                                   # two parts: strictly ascending (set)
-    # spot-check 2000 rows bit-exactly against the oracle on a shard
+    # and the full table is bit-exact against the oracle with the same Philox uniforms
     u = philox.walk_uniforms(0, n, 2, 4, 42)
     ref_t, ref_len = et.build_edge_table(rowptr, col, n, 4, 4, 4, 2, 42, u)
     assert np.array_equal(t, ref_t) and np.array_equal(rl, ref_len)
+
+
+def test_device_chung_lu_graph_properties(hip_device):
+    """The on-device generator yields a coalesced symmetric simple graph with a power-law degree profile."""
+    from budgetformer_amd import hip_ops
+    from budgetformer_amd.graph import chung_lu_device
+    n, e = 200_000, 2_000_000
+    g = chung_lu_device(n, e, exponent=2.1, seed=7, max_degree=3000, device=hip_device)
+    rowptr = g.rowptr.cpu().numpy()
+    col = g.col.cpu().numpy().astype(np.int64)
+    assert rowptr[0] == 0 and rowptr[-1] == e and col.size == e
+    deg = np.diff(rowptr)
+    src = np.repeat(np.arange(n), deg)
+    assert (src != col).all()                                        # no self loops
+    lin = src * n + col
+    assert (np.diff(lin) > 0).all()                                  # sorted, unique
+    assert np.array_equal(np.sort(col * n + src), lin)               # symmetric
+    assert deg.max() <= 3000 * 1.5 and deg[:100].mean() > 20 * np.median(deg[deg > 0])
+    # the device transpose (in-neighbour CSR) of a symmetric graph is the graph itself
+    in_ptr, in_src = hip_ops.coo_to_csr(torch.stack([torch.from_numpy(src), torch.from_numpy(col)]).to(hip_device), n, n)
+    assert torch.equal(in_ptr, g.rowptr) and torch.equal(in_src, g.col)
+    g2 = chung_lu_device(n, e, exponent=2.1, seed=7, max_degree=3000, device=hip_device)
+    assert torch.equal(g2.col, g.col)                                # deterministic

@@ -229,3 +229,18 @@ def test_build_edge_table_rows_sorted_and_bounded():
         row = table[q, :row_len[q]]
         assert (np.diff(row) > 0).all()          # two parts -> deduplicated, ascending
         assert (table[q, row_len[q]:] == -1).all()
+
+
+def test_query_range_build_equals_rows_of_full_build():
+    from oracle import philox
+    rng = np.random.default_rng(11)
+    n = 400
+    raw = rng.integers(0, n, (1500, 2))
+    edges = sorted({(int(a), int(b)) for a, b in raw if a != b} | {(int(b), int(a)) for a, b in raw if a != b})
+    rowptr, col = et.csr_from_coo(np.array(edges).T, n)
+    u = philox.walk_uniforms(0, n, 2, 4, 9)
+    for b_r, b_w in ((4, 4), (3, 0), (0, 3)):
+        full_t, full_l = et.build_edge_table(rowptr, col, n, b_r, b_w, 4, 2, 9, u)
+        for lo, cnt in ((0, n), (100, 70), (350, 50)):
+            t, l = et.build_edge_table(rowptr, col, n, b_r, b_w, 4, 2, 9, u[lo * 2:(lo + cnt) * 2], q_lo=lo, n_q=cnt)
+            assert np.array_equal(t, full_t[lo:lo + cnt]) and np.array_equal(l, full_l[lo:lo + cnt])
