@@ -66,14 +66,16 @@ def kernel_bytes(s, D, H, lens_q, lens_k, chunk):
     lk = lens_k[lens_k <= chunk]
     nq, eq = lq.size, int(lq.sum())
     nk, ek = lk.size, int(lk.sum())
+    nk_touched = int((lk > 0).sum())
     row = s * D
     return {
         # Q read, O write, K and V gathered per edge, kv ids, Z write, qptr
         "attn_fwd_rows_kernel": row * (2 * nq + 2 * eq) + 4 * eq + 4 * H * nq + 16 * nq,
-        # Q, dO, O read, dQ write, K and V per edge, kv ids, Z read + Delta write, qptr
-        "attn_bwd_q_rows_kernel": row * (4 * nq + 2 * eq) + 4 * eq + 8 * H * nq + 16 * nq,
-        # K, V read, dK, dV write, Q and dO per edge, Z and Delta per edge, kq ids, kptr
-        "attn_bwd_kv_rows_kernel": row * (4 * nk + 2 * ek) + 8 * H * ek + 4 * ek + 16 * nk,
+        # Q, dO, O read, dQ write, K and V per edge, kv ids, Z read + row stats write, qptr
+        "attn_bwd_q_rows_kernel": row * (4 * nq + 2 * eq) + 4 * eq + 12 * H * nq + 16 * nq,
+        # dK, dV written for every row; K, V read for rows with entries; Q and dO per edge,
+        # the {1/D', Delta/D'} row stats per edge, kq ids, kptr
+        "attn_bwd_kv_rows_kernel": row * (2 * nk + 2 * nk_touched + 2 * ek) + 8 * H * ek + 4 * ek + 16 * nk,
     }
 
 

@@ -31,6 +31,8 @@ HIPCC_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{os.path.join(ROOT, 'include')}",
 ]
+# Extra compile definitions for tuning sweeps (e.g. "-DBF_ATTN_UNROLL=4"); empty by default.
+HIPCC_FLAGS += os.environ.get("BF_HIPCC_EXTRA", "").split()
 
 
 def lib_path() -> str:

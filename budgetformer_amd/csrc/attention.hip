@@ -26,7 +26,10 @@ namespace bf {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kUnroll = 4;
+#ifndef BF_ATTN_UNROLL
+#define BF_ATTN_UNROLL 4
+#endif
+constexpr int kUnroll = BF_ATTN_UNROLL;   // edges whose gathers are in flight together per group
 constexpr float kEps = 1e-6f;
 constexpr float kClamp = 5.0f;
 
@@ -94,23 +97,24 @@ __device__ __forceinline__ void fwd_segment(const T* __restrict__ k, const T* __
       ok[u] = e0 + u < end;
       s[u] = ok[u] ? kv[e0 + u] : 0;
     }
-    float kk[kUnroll][V], vv[kUnroll][V];
+    typename Elem<T>::Raw kr[kUnroll], vr[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       if (ok[u] && g.act) {
-        Elem<T>::load(k + int64_t(s[u]) * sh.D + g.col0, kk[u]);
-        Elem<T>::load(v + int64_t(s[u]) * sh.D + g.col0, vv[u]);
+        kr[u] = Elem<T>::load_raw(k + int64_t(s[u]) * sh.D + g.col0);
+        vr[u] = Elem<T>::load_raw(v + int64_t(s[u]) * sh.D + g.col0);
       } else {
-#pragma unroll
-        for (int i = 0; i < V; ++i) kk[u][i] = vv[u][i] = 0.f;
+        kr[u] = vr[u] = Elem<T>::zero_raw();
       }
     }
     float d[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
+      float kk[V];
+      Elem<T>::unpack(kr[u], kk);
       float t = 0.f;
 #pragma unroll
-      for (int i = 0; i < V; ++i) t += (kk[u][i] * qv[i]) * sh.inv_scale;
+      for (int i = 0; i < V; ++i) t += (kk[i] * qv[i]) * sh.inv_scale;
       d[u] = t;
     }
     for (int o = 1; o < lph; o <<= 1) {
@@ -125,8 +129,10 @@ __device__ __forceinline__ void fwd_segment(const T* __restrict__ k, const T* __
       if (bias) a += bias[e * sh.H + g.head];
       const float p = expf(a);
       const float w = factor ? p * factor[e * sh.H + g.head] : p;
+      float vv[V];
+      Elem<T>::unpack(vr[u], vv);
 #pragma unroll
-      for (int i = 0; i < V; ++i) acc[i] += w * vv[u][i];
+      for (int i = 0; i < V; ++i) acc[i] += w * vv[i];
       z += p;
     }
   }
@@ -373,25 +379,27 @@ __device__ __forceinline__ void dq_segment(const T* __restrict__ k, const T* __r
       ok[u] = e0 + u < end;
       s[u] = ok[u] ? kv[e0 + u] : 0;
     }
-    float kk[kUnroll][V], vv[kUnroll][V];
+    typename Elem<T>::Raw kr[kUnroll], vr[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       if (ok[u] && g.act) {
-        Elem<T>::load(k + int64_t(s[u]) * sh.D + g.col0, kk[u]);
-        Elem<T>::load(v + int64_t(s[u]) * sh.D + g.col0, vv[u]);
+        kr[u] = Elem<T>::load_raw(k + int64_t(s[u]) * sh.D + g.col0);
+        vr[u] = Elem<T>::load_raw(v + int64_t(s[u]) * sh.D + g.col0);
       } else {
-#pragma unroll
-        for (int i = 0; i < V; ++i) kk[u][i] = vv[u][i] = 0.f;
+        kr[u] = vr[u] = Elem<T>::zero_raw();
       }
     }
     float d[kUnroll], w[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
+      float kk[V], vv[V];
+      Elem<T>::unpack(kr[u], kk);
+      Elem<T>::unpack(vr[u], vv);
       float t = 0.f, r = 0.f;
 #pragma unroll
       for (int i = 0; i < V; ++i) {
-        t += (kk[u][i] * qv[i]) * sh.inv_scale;
-        r += gv[i] * vv[u][i];
+        t += (kk[i] * qv[i]) * sh.inv_scale;
+        r += gv[i] * vv[i];
       }
       d[u] = t;
       w[u] = r;
@@ -415,8 +423,10 @@ __device__ __forceinline__ void dq_segment(const T* __restrict__ k, const T* __r
       const float gb = (f * (w[u] / rg.dprime) + gz) * p;
       if (dbias && g.lead) dbias[e * sh.H + g.head] = gb;
       const float ga = (apre >= -kClamp && apre <= kClamp) ? gb : 0.f;
+      float kk[V];
+      Elem<T>::unpack(kr[u], kk);
 #pragma unroll
-      for (int i = 0; i < V; ++i) dq[i] += (ga * kk[u][i]) * sh.inv_scale;
+      for (int i = 0; i < V; ++i) dq[i] += (ga * kk[i]) * sh.inv_scale;
     }
   }
 }
@@ -506,28 +516,30 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
       ok[u] = i0 + u < end;
       t[u] = ok[u] ? kq[i0 + u] : 0;
     }
-    float qq[kUnroll][V], gg[kUnroll][V];
+    typename Elem<T>::Raw qr[kUnroll], gr[kUnroll];
     float2 rs[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       if (ok[u] && g.act) {
-        Elem<T>::load(q + int64_t(t[u]) * sh.D + g.col0, qq[u]);
-        Elem<T>::load(dout + int64_t(t[u]) * sh.D + g.col0, gg[u]);
+        qr[u] = Elem<T>::load_raw(q + int64_t(t[u]) * sh.D + g.col0);
+        gr[u] = Elem<T>::load_raw(dout + int64_t(t[u]) * sh.D + g.col0);
         rs[u] = rstat[int64_t(t[u]) * sh.H + g.head];
       } else {
-#pragma unroll
-        for (int i = 0; i < V; ++i) qq[u][i] = gg[u][i] = 0.f;
+        qr[u] = gr[u] = Elem<T>::zero_raw();
         rs[u] = make_float2(0.f, 0.f);
       }
     }
     float d[kUnroll], w[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
+      float qq[V], gg[V];
+      Elem<T>::unpack(qr[u], qq);
+      Elem<T>::unpack(gr[u], gg);
       float a = 0.f, r = 0.f;
 #pragma unroll
       for (int i = 0; i < V; ++i) {
-        a += (kk[i] * qq[u][i]) * sh.inv_scale;
-        r += gg[u][i] * vv[i];
+        a += (kk[i] * qq[i]) * sh.inv_scale;
+        r += gg[i] * vv[i];
       }
       d[u] = a;
       w[u] = r;
@@ -551,10 +563,13 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
       const float gb = (f * w[u] * rs[u].x - rs[u].y) * p;     // rs = {1/D', Delta/D'}
       const float ga = (apre >= -kClamp && apre <= kClamp) ? gb : 0.f;
       const float pf = p * f * rs[u].x;
+      float qq[V], gg[V];
+      Elem<T>::unpack(qr[u], qq);
+      Elem<T>::unpack(gr[u], gg);
 #pragma unroll
       for (int i = 0; i < V; ++i) {
-        dv[i] += pf * gg[u][i];
-        dk[i] += (ga * qq[u][i]) * sh.inv_scale;
+        dv[i] += pf * gg[i];
+        dk[i] += (ga * qq[i]) * sh.inv_scale;
       }
     }
   }
@@ -566,18 +581,27 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_rows_kernel(
     const int64_t* __restrict__ kptr, const int32_t* __restrict__ kq,
     const int32_t* __restrict__ ke, const float* __restrict__ bias,
     const float* __restrict__ factor, const T* __restrict__ dout, const float2* __restrict__ rstat,
-    T* __restrict__ dk, T* __restrict__ dv, int64_t n_kv, Shape sh, int chunk) {
+    T* __restrict__ dk, T* __restrict__ dv, const int32_t* __restrict__ order, int64_t n_kv, Shape sh, int chunk) {
   constexpr int V = Elem<T>::kPerVec;
-  const int64_t row = group_index(sh);
-  if (row >= n_kv) return;
+  const int64_t slot = group_index(sh);
+  if (slot >= n_kv) return;
+  // rows visited longest-first so the groups sharing a wavefront carry similar work
+  const int64_t row = order ? int64_t(order[slot]) : slot;
   const int64_t beg = kptr[row], end = kptr[row + 1];
   if (end - beg > chunk) return;
   const GroupPos g = group_pos<T>(sh);
   float kk[V], vv[V], ak[V], av[V];
-  load_row<T, V>(k, row, sh.D, g, kk);
-  load_row<T, V>(v, row, sh.D, g, vv);
 #pragma unroll
   for (int i = 0; i < V; ++i) ak[i] = av[i] = 0.f;
+  if (beg == end) {               // key/value row no query attends to: zero gradient, no reads
+    if (g.act) {
+      Elem<T>::store(dk + row * sh.D + g.col0, ak);
+      Elem<T>::store(dv + row * sh.D + g.col0, av);
+    }
+    return;
+  }
+  load_row<T, V>(k, row, sh.D, g, kk);
+  load_row<T, V>(v, row, sh.D, g, vv);
   dkv_segment<T>(q, dout, kq, ke, bias, factor, rstat, beg, end, sh, g, kk, vv, ak, av);
   if (g.act) {
     Elem<T>::store(dk + row * sh.D + g.col0, ak);
@@ -743,7 +767,7 @@ int bwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
   if (idx->n_kv > 0) {
     BF_LAUNCH("attn_bwd_kv_rows_kernel", attn_bwd_kv_rows_kernel<T>, dim3(grid_for(idx->n_kv, sh)), dim3(kBlock), 0,
               st, Q, K, Vv, idx->kptr, idx->kq, idx->ke, bias, factor, dO, rstat, static_cast<T*>(dk),
-              static_cast<T*>(dv), idx->n_kv, sh, idx->chunk);
+              static_cast<T*>(dv), idx->k_order, idx->n_kv, sh, idx->chunk);
     BF_CHECK_LAUNCH();
   }
   if (idx->k_items > 0) {

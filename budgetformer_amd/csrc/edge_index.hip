@@ -139,6 +139,16 @@ __global__ void unpack_row_entry_kernel(const uint64_t* __restrict__ vals, int64
   ke[i] = int32_t(uint32_t(x));
 }
 
+// Sort key placing long rows first: 255 - min(len, 255).
+__global__ void length_keys_kernel(const int64_t* __restrict__ ptr, int64_t n_rows, uint8_t* __restrict__ keys,
+                                   int32_t* __restrict__ ids) {
+  const int64_t r = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (r >= n_rows) return;
+  const int64_t len = ptr[r + 1] - ptr[r];
+  keys[r] = uint8_t(255 - (len < 255 ? len : 255));
+  ids[r] = int32_t(r);
+}
+
 struct MaxOp {
   __device__ __forceinline__ int32_t operator()(int32_t a, int32_t b) const { return a > b ? a : b; }
 };
@@ -572,5 +582,39 @@ extern "C" int bf_coalesce(const int64_t* src, const int64_t* dst, int64_t nnz, 
   BF_CHECK_LAUNCH();
   BF_CHECK_HIP(hipMemcpyAsync(count_host, incl + nnz - 1, sizeof(int64_t), hipMemcpyDeviceToHost, st));
   BF_CHECK_HIP(hipStreamSynchronize(st));
+  return BF_OK;
+}
+
+extern "C" int bf_row_order_workspace_size(int64_t n_rows, size_t* bytes) {
+  BF_CHECK_ARG(bytes && n_rows >= 0, "row_order_workspace_size: bad arguments");
+  size_t sort_bytes = 0;
+  const int n = int(n_rows > 0 ? n_rows : 1);
+  (void)hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, static_cast<const uint8_t*>(nullptr),
+                                           static_cast<uint8_t*>(nullptr), static_cast<const int32_t*>(nullptr),
+                                           static_cast<int32_t*>(nullptr), n);
+  *bytes = 2 * align_up(size_t(n)) + align_up(size_t(n) * 4) + align_up(sort_bytes) + 256;
+  return BF_OK;
+}
+
+extern "C" int bf_row_order(const int64_t* ptr, int64_t n_rows, int32_t* order, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  BF_CHECK_ARG(ptr && n_rows >= 0 && n_rows < (int64_t(1) << 31), "row_order: bad arguments");
+  if (n_rows == 0) return BF_OK;
+  BF_CHECK_ARG(order != nullptr, "row_order: null output");
+  size_t need = 0;
+  bf_row_order_workspace_size(n_rows, &need);
+  BF_CHECK_ARG(workspace && workspace_bytes >= need, "row_order: workspace %zu < %zu bytes", workspace_bytes, need);
+  hipStream_t st = as_stream(stream);
+  char* p = static_cast<char*>(workspace);
+  auto take = [&](size_t b) { char* q = p; p += align_up(b); return q; };
+  auto* keys_in = reinterpret_cast<uint8_t*>(take(size_t(n_rows)));
+  auto* keys_out = reinterpret_cast<uint8_t*>(take(size_t(n_rows)));
+  auto* ids = reinterpret_cast<int32_t*>(take(size_t(n_rows) * 4));
+  void* temp = p;
+  size_t tb = workspace_bytes - size_t(p - static_cast<char*>(workspace));
+  BF_LAUNCH("length_keys_kernel", length_keys_kernel, dim3(blocks_for(n_rows)), dim3(kThreads), 0, st, ptr, n_rows,
+            keys_in, ids);
+  BF_CHECK_LAUNCH();
+  BF_CHECK_HIP(hipcub::DeviceRadixSort::SortPairs(temp, tb, keys_in, keys_out, ids, order, int(n_rows), 0, 8, st));
   return BF_OK;
 }

@@ -252,6 +252,15 @@ def expand_rows(ptr: torch.Tensor, nnz: int) -> torch.Tensor:
     return rows
 
 
+def row_order(ptr: torch.Tensor) -> torch.Tensor:
+    """Rows of a CSR longest-first (bf_row_order), int32 [n_rows]."""
+    n_rows = ptr.numel() - 1
+    order = torch.empty(max(n_rows, 1), dtype=torch.int32, device=ptr.device)
+    ws = _workspace(_size_query("bf_row_order_workspace_size", n_rows), ptr.device)
+    N.call("bf_row_order", _p(ptr), n_rows, _p(order), _p(ws), ws.numel(), _stream(ptr.device))
+    return order
+
+
 @dataclass
 class SplitPlan:
     """Rows longer than `threshold` cut into `item_size`-entry items (host-known counts)."""
@@ -301,6 +310,7 @@ class AttentionIndex:
     kq: Optional[torch.Tensor] = None
     ke: Optional[torch.Tensor] = None
     kplan: Optional[SplitPlan] = None
+    korder: Optional[torch.Tensor] = None
     _rows: Optional[torch.Tensor] = field(default=None, repr=False)
 
     @property
@@ -322,6 +332,8 @@ class AttentionIndex:
             self.kptr, self.kq, self.ke = reverse_index(self.qptr, self.kv, self.n_kv)
         if self.kplan is None:
             self.kplan = split_plan(self.kptr, self.nnz, self.chunk, self.item)
+        if self.korder is None:
+            self.korder = row_order(self.kptr)
         return self
 
     def entry_rows(self) -> torch.Tensor:
@@ -354,6 +366,7 @@ class AttentionIndex:
             s.k_items, s.k_heavy = kp.items, kp.heavy
             s.k_nitems, s.k_item_off, s.k_item_row, s.k_heavy_rows = (
                 kp.nitems.data_ptr(), kp.item_off.data_ptr(), kp.item_row.data_ptr(), kp.heavy_rows.data_ptr())
+            s.k_order = self.korder.data_ptr() if self.n_kv > 0 else None
         return s
 
     @classmethod

@@ -220,6 +220,14 @@ int bf_split_plan(const int64_t* ptr, int64_t n_rows, int32_t threshold, int32_t
                   int32_t* heavy_rows, int64_t heavy_cap, int32_t* counts,
                   void* workspace, size_t workspace_bytes, void* stream);
 
+/* Rows of a CSR ordered longest-first (lengths capped at 255; ties in row
+ * order). The key-major attention pass walks its rows in this order so the
+ * groups sharing a wavefront carry similar work. Workspace:
+ * bf_row_order_workspace_size.                                              */
+int bf_row_order_workspace_size(int64_t n_rows, size_t* bytes);
+int bf_row_order(const int64_t* ptr, int64_t n_rows, int32_t* order, void* workspace,
+                 size_t workspace_bytes, void* stream);
+
 /* ======================================================================
  * Sparse edge attention
  * ====================================================================== */
@@ -246,6 +254,7 @@ typedef struct bf_attn_index {
   const int32_t* k_item_off;
   const int32_t* k_item_row;
   const int32_t* k_heavy_rows;
+  const int32_t* k_order;       /* [n_kv] key rows longest-first (bf_row_order), or NULL */
 } bf_attn_index;
 
 /* float32 scratch the attention calls need for split rows. */
