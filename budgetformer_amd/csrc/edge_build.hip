@@ -140,11 +140,77 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t x, int o) {
   return (uint64_t(hi) << 32) | lo;
 }
 
+// Top-k_real of one hub's in-neighbour list with a whole workgroup: every
+// thread keeps a sorted register list of its strided share, then k rounds of a
+// block-wide minimum (wave shuffles, then LDS across the 4 waves) pop the
+// winners in key order. Output: hub_sel [n_hubs, k_real] kv ids, hub_cnt.
+template <int KMAX>
+__global__ __launch_bounds__(kThreads) void real_select_hub_kernel(
+    const int64_t* __restrict__ in_ptr, const int32_t* __restrict__ in_src, const int32_t* __restrict__ hubs,
+    int k_real, uint32_t kc, int32_t* __restrict__ hub_sel, int32_t* __restrict__ hub_cnt) {
+  __shared__ uint64_t wave_min[kThreads / 64];
+  __shared__ int wave_win[kThreads / 64];
+  const int h = blockIdx.x;
+  const int64_t q = hubs[h];
+  uint64_t lk[KMAX];
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) lk[j] = kNone;
+  const int64_t beg = in_ptr[q], end = in_ptr[q + 1];
+  for (int64_t i = beg + threadIdx.x; i < end; i += kThreads) {
+    const uint32_t s = uint32_t(in_src[i]);
+    const uint64_t c = (uint64_t(edge_key(s, uint32_t(q), kc)) << 32) | s;
+    if (c < lk[KMAX - 1]) {
+#pragma unroll
+      for (int j = KMAX - 1; j > 0; --j) lk[j] = c < lk[j - 1] ? lk[j - 1] : (c < lk[j] ? c : lk[j]);
+      lk[0] = c < lk[0] ? c : lk[0];
+    }
+  }
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  int cnt = 0;
+  for (int r = 0; r < k_real; ++r) {
+    const uint64_t head = lk[0];
+    uint64_t m = head;
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint64_t y = shfl_xor_u64(m, o);
+      m = y < m ? y : m;
+    }
+    const uint64_t bal = __ballot(head == m);
+    if (lane == 0) {
+      wave_min[wave] = m;
+      wave_win[wave] = __ffsll((unsigned long long)bal) - 1;
+    }
+    __syncthreads();
+    uint64_t best = wave_min[0];
+    int best_wave = 0;
+#pragma unroll
+    for (int w = 1; w < kThreads / 64; ++w) {
+      if (wave_min[w] < best) {
+        best = wave_min[w];
+        best_wave = w;
+      }
+    }
+    const int winner = best_wave * 64 + wave_win[best_wave];
+    __syncthreads();
+    if (best == kNone) break;   // the same value in every thread: uniform exit
+    if (int(threadIdx.x) == winner) {
+#pragma unroll
+      for (int j = 0; j < KMAX - 1; ++j) lk[j] = lk[j + 1];
+      lk[KMAX - 1] = kNone;
+    }
+    if (threadIdx.x == 0) hub_sel[int64_t(h) * k_real + r] = int32_t(uint32_t(best));
+    cnt = r + 1;
+  }
+  if (threadIdx.x == 0) hub_cnt[h] = cnt;
+}
+
 template <int KMAX>
 __global__ __launch_bounds__(kThreads) void real_select_merge_kernel(
     const int64_t* __restrict__ in_ptr, const int32_t* __restrict__ in_src, int64_t q_lo, int64_t n_q,
     int k_real, uint32_t kc, const int32_t* __restrict__ rw_kv, const int32_t* __restrict__ rw_cnt, int k_rw,
-    int dedup, int32_t* __restrict__ table, int width, int32_t* __restrict__ row_len) {
+    int dedup, int32_t* __restrict__ table, int width, int32_t* __restrict__ row_len,
+    const int32_t* __restrict__ hubs, const int32_t* __restrict__ hub_sel, const int32_t* __restrict__ hub_cnt,
+    int64_t n_hubs, int64_t hub_threshold) {
   __shared__ int32_t lst[kQPB][kMaxRow];
   __shared__ int32_t dupf[kQPB][kMaxRow];
   const int gq = threadIdx.x / kGroup;
@@ -152,7 +218,22 @@ __global__ __launch_bounds__(kThreads) void real_select_merge_kernel(
   const int64_t qi = int64_t(blockIdx.x) * kQPB + gq;
   const bool active = qi < n_q;
   int n_r = 0, n_w = 0;
-  if (active && k_real > 0) {
+  int64_t hub = -1;
+  if (active && k_real > 0 && n_hubs > 0) {
+    const int64_t q = q_lo + qi;
+    if (in_ptr[q + 1] - in_ptr[q] > hub_threshold) {   // selection precomputed by real_select_hub_kernel
+      int64_t lo = 0, hi = n_hubs;
+      while (lo < hi) {
+        const int64_t mid = (lo + hi) >> 1;
+        if (hubs[mid] < q) lo = mid + 1; else hi = mid;
+      }
+      if (lo < n_hubs && hubs[lo] == q) hub = lo;
+    }
+  }
+  if (hub >= 0) {
+    n_r = hub_cnt[hub];
+    for (int i = gl; i < n_r; i += kGroup) lst[gq][i] = hub_sel[hub * k_real + i];
+  } else if (active && k_real > 0) {
     const int64_t q = q_lo + qi;
     uint64_t lk[KMAX];
 #pragma unroll
@@ -250,12 +331,30 @@ int launch_rw_select(const int64_t* rowptr, const int32_t* col, int64_t q_lo, in
 
 int launch_real_merge(const int64_t* in_ptr, const int32_t* in_src, int64_t q_lo, int64_t n_q, int k_real,
                       uint32_t kc, const int32_t* rw_kv, const int32_t* rw_cnt, int k_rw, int dedup,
-                      int32_t* table, int width, int32_t* row_len, hipStream_t st) {
+                      int32_t* table, int width, int32_t* row_len, const int32_t* hubs, int64_t n_hubs,
+                      int64_t hub_threshold, int32_t* hub_sel, int32_t* hub_cnt, hipStream_t st) {
   if (n_q == 0) return BF_OK;
+  if (k_real <= 0) n_hubs = 0;
+  if (n_hubs > 0) {
+#define BF_LAUNCH_HUB(KM)                                                                                       \
+  BF_LAUNCH("real_select_hub_kernel", real_select_hub_kernel<KM>, dim3(unsigned(n_hubs)), dim3(kThreads), 0, st, \
+            in_ptr, in_src, hubs, k_real, kc, hub_sel, hub_cnt)
+    if (k_real <= 4)
+      BF_LAUNCH_HUB(4);
+    else if (k_real <= 8)
+      BF_LAUNCH_HUB(8);
+    else if (k_real <= 16)
+      BF_LAUNCH_HUB(16);
+    else
+      BF_LAUNCH_HUB(32);
+#undef BF_LAUNCH_HUB
+    BF_CHECK_LAUNCH();
+  }
   const dim3 grid(unsigned(ceil_div(n_q, kQPB)));
-#define BF_LAUNCH_MERGE(KM)                                                                              \
-  BF_LAUNCH("real_select_merge_kernel", real_select_merge_kernel<KM>, grid, dim3(kThreads), 0, st, in_ptr, in_src, q_lo, n_q, \
-                     k_real, kc, rw_kv, rw_cnt, k_rw, dedup, table, width, row_len)
+#define BF_LAUNCH_MERGE(KM)                                                                                      \
+  BF_LAUNCH("real_select_merge_kernel", real_select_merge_kernel<KM>, grid, dim3(kThreads), 0, st, in_ptr, in_src, \
+            q_lo, n_q, k_real, kc, rw_kv, rw_cnt, k_rw, dedup, table, width, row_len, hubs, hub_sel, hub_cnt,    \
+            n_hubs, hub_threshold)
   if (k_real <= 4)
     BF_LAUNCH_MERGE(4);
   else if (k_real <= 8)
@@ -341,7 +440,8 @@ extern "C" int bf_rw_select(const int64_t* rowptr, const int32_t* col, int64_t n
 extern "C" int bf_real_select_merge(const int64_t* in_ptr, const int32_t* in_src, int64_t num_nodes, int64_t q_lo,
                                     int64_t n_q, int32_t k_real, int64_t key_seed, const int32_t* rw_kv,
                                     const int32_t* rw_cnt, int32_t k_rw, int32_t dedup, int32_t* table,
-                                    int32_t width, int32_t* row_len, void* stream) {
+                                    int32_t width, int32_t* row_len, const int32_t* hubs, int64_t n_hubs,
+                                    int64_t hub_threshold, int32_t* hub_sel, int32_t* hub_cnt, void* stream) {
   int rc = check_graph(in_ptr, in_src, num_nodes, q_lo, n_q);
   if (rc) return rc;
   if (k_real < 0) k_real = 0;
@@ -352,13 +452,20 @@ extern "C" int bf_real_select_merge(const int64_t* in_ptr, const int32_t* in_src
   BF_CHECK_ARG(width >= k_real + k_rw && width >= 1, "real_select_merge: width %d < k_real + k_rw = %d", width,
                k_real + k_rw);
   BF_CHECK_ARG((table && row_len) || n_q == 0, "real_select_merge: null output");
+  BF_CHECK_ARG(n_hubs >= 0 && n_hubs < (int64_t(1) << 31), "real_select_merge: bad hub count");
+  BF_CHECK_ARG(n_hubs == 0 || (hubs && hub_sel && hub_cnt && hub_threshold >= 0),
+               "real_select_merge: hub arrays missing");
   return launch_real_merge(in_ptr, in_src, q_lo, n_q, k_real, key_const(key_seed), k_rw ? rw_kv : nullptr, rw_cnt,
-                           k_rw, dedup ? 1 : 0, table, width, row_len, as_stream(stream));
+                           k_rw, dedup ? 1 : 0, table, width, row_len, hubs, n_hubs, hub_threshold, hub_sel,
+                           hub_cnt, as_stream(stream));
 }
 
-extern "C" int bf_build_edge_table_workspace_size(int64_t n_q, int32_t k_rw, size_t* bytes) {
-  BF_CHECK_ARG(bytes && n_q >= 0 && k_rw >= 0, "build_edge_table_workspace_size: bad arguments");
-  *bytes = align_up(size_t(n_q) * size_t(k_rw > 0 ? k_rw : 0) * 4) + align_up(size_t(n_q) * 4) + 256;
+extern "C" int bf_build_edge_table_workspace_size(int64_t n_q, int32_t k_rw, int64_t n_hubs, int32_t k_real,
+                                                  size_t* bytes) {
+  BF_CHECK_ARG(bytes && n_q >= 0 && k_rw >= 0 && n_hubs >= 0, "build_edge_table_workspace_size: bad arguments");
+  const size_t kr = size_t(k_real > 0 ? k_real : 0);
+  *bytes = align_up(size_t(n_q) * size_t(k_rw > 0 ? k_rw : 0) * 4) + align_up(size_t(n_q) * 4) +
+           align_up(size_t(n_hubs) * kr * 4) + align_up(size_t(n_hubs) * 4) + 256;
   return BF_OK;
 }
 
@@ -366,29 +473,36 @@ extern "C" int bf_build_edge_table(const int64_t* rowptr, const int32_t* col, co
                                    const int32_t* in_src, int64_t num_nodes, int64_t num_edges, int64_t q_lo,
                                    int64_t n_q, int32_t walks_per_node, int32_t walk_length, int32_t k_real,
                                    int32_t k_rw, int64_t edge_seed, const float* u, uint64_t philox_seed,
-                                   uint64_t philox_offset, int32_t* table, int32_t* row_len, void* workspace,
+                                   uint64_t philox_offset, const int32_t* hubs, int64_t n_hubs,
+                                   int64_t hub_threshold, int32_t* table, int32_t* row_len, void* workspace,
                                    size_t workspace_bytes, void* stream) {
   BF_CHECK_ARG(num_edges >= 0, "build_edge_table: num_edges < 0");
   const bool use_rw = k_rw > 0 && walks_per_node > 0 && walk_length > 0 && num_nodes > 0;
   const bool use_real = k_real > 0 && num_edges > 0;
   const int32_t width = (k_real > 0 ? k_real : 0) + (k_rw > 0 ? k_rw : 0);
   BF_CHECK_ARG(width >= 1, "build_edge_table: empty budget (k_real=%d, k_rw=%d)", k_real, k_rw);
+  if (!use_real) n_hubs = 0;
   size_t need = 0;
-  bf_build_edge_table_workspace_size(n_q, use_rw ? k_rw : 0, &need);
+  bf_build_edge_table_workspace_size(n_q, use_rw ? k_rw : 0, n_hubs, k_real, &need);
   BF_CHECK_ARG(workspace && workspace_bytes >= need, "build_edge_table: workspace %zu < %zu bytes",
                workspace_bytes, need);
   hipStream_t st = as_stream(stream);
-  int32_t* sel_kv = nullptr;
-  int32_t* sel_cnt = nullptr;
+  char* wp = static_cast<char*>(workspace);
+  int32_t* sel_kv = reinterpret_cast<int32_t*>(wp);
+  wp += align_up(size_t(n_q) * size_t(use_rw ? k_rw : 0) * 4);
+  int32_t* sel_cnt = reinterpret_cast<int32_t*>(wp);
+  wp += align_up(size_t(n_q) * 4);
+  int32_t* hub_sel = reinterpret_cast<int32_t*>(wp);
+  wp += align_up(size_t(n_hubs) * size_t(k_real > 0 ? k_real : 0) * 4);
+  int32_t* hub_cnt = reinterpret_cast<int32_t*>(wp);
   if (use_rw) {
-    sel_kv = static_cast<int32_t*>(workspace);
-    sel_cnt = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + align_up(size_t(n_q) * k_rw * 4));
     int rc = bf_rw_select(rowptr, col, num_nodes, q_lo, n_q, walks_per_node, walk_length, k_rw,
                           edge_seed + 37, u, philox_seed, philox_offset, sel_kv, sel_cnt, st);
     if (rc) return rc;
   }
   // the reference coalesces only when both parts are globally non-empty
   return bf_real_select_merge(in_ptr, in_src, num_nodes, q_lo, n_q, use_real ? k_real : 0, edge_seed + 17,
-                              use_rw ? sel_kv : nullptr, sel_cnt, use_rw ? k_rw : 0,
-                              (use_real && use_rw) ? 1 : 0, table, width, row_len, st);
+                              use_rw ? sel_kv : nullptr, use_rw ? sel_cnt : nullptr, use_rw ? k_rw : 0,
+                              (use_real && use_rw) ? 1 : 0, table, width, row_len, hubs, n_hubs, hub_threshold,
+                              hub_sel, hub_cnt, st);
 }

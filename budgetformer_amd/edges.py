@@ -104,10 +104,19 @@ def build_attention_edges(graph: CSRGraph, *, real_edges_per_query: int, rw_edge
     P = max(int(walks_per_node), 1)
     seed = int(edge_seed if philox_seed is None else philox_seed)
     plan = plan_edge_build(graph.device, n_q, b_r, b_w, q_lo=q_lo, usable_bytes=usable_bytes)
+    all_hubs = graph.hubs() if b_r > 0 else None
+
+    def hubs_in(lo, cnt):
+        if all_hubs is None or all_hubs.numel() == 0:
+            return None
+        bounds = torch.tensor([lo, lo + cnt], dtype=torch.int32, device=all_hubs.device)
+        a, b = torch.searchsorted(all_hubs, bounds).tolist()
+        return all_hubs[a:b] if b > a else None
+
     if len(plan.shards) == 1:
         table, row_len = hip_ops.build_edge_table(
             graph.rowptr, graph.col, graph.in_ptr, graph.in_src, graph.num_edges, q_lo, n_q, P, walk_length,
-            b_r, b_w, int(edge_seed), u=u, philox_seed=seed, philox_offset=philox_offset)
+            b_r, b_w, int(edge_seed), u=u, philox_seed=seed, philox_offset=philox_offset, hubs=hubs_in(q_lo, n_q))
     else:
         table = torch.empty(n_q, b_r + b_w, dtype=torch.int32, device=graph.device)
         row_len = torch.empty(n_q, dtype=torch.int32, device=graph.device)
@@ -116,5 +125,6 @@ def build_attention_edges(graph: CSRGraph, *, real_edges_per_query: int, rw_edge
             u_s = None if u is None else u[a * P:(a + cnt) * P]
             hip_ops.build_edge_table(graph.rowptr, graph.col, graph.in_ptr, graph.in_src, graph.num_edges, lo, cnt,
                                      P, walk_length, b_r, b_w, int(edge_seed), u=u_s, philox_seed=seed,
-                                     philox_offset=philox_offset, out=(table[a:a + cnt], row_len[a:a + cnt]))
+                                     philox_offset=philox_offset, out=(table[a:a + cnt], row_len[a:a + cnt]),
+                                     hubs=hubs_in(lo, cnt))
     return EdgeTable(table, row_len, graph.num_nodes, q_lo=q_lo, global_token=global_token)

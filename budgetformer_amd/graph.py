@@ -36,6 +36,17 @@ class CSRGraph:
     def symmetric(self) -> bool:
         return self.in_ptr is self.rowptr and self.in_src is self.col
 
+    def hubs(self, threshold: int = hip_ops.HUB_THRESHOLD) -> torch.Tensor:
+        """Ascending ids of queries whose in-degree exceeds ``threshold`` (int32), cached per threshold.
+
+        The real-edge top-k of these rows runs one workgroup per row.
+        """
+        cache = self.__dict__.setdefault("_hubs", {})
+        if threshold not in cache:
+            plan = hip_ops.split_plan(self.in_ptr, self.num_edges, threshold, max(threshold, 1))
+            cache[threshold] = plan.heavy_rows[: plan.heavy].clone()
+        return cache[threshold]
+
     @classmethod
     def from_csr(cls, rowptr, col, num_nodes: int, in_ptr=None, in_src=None, device="cuda"):
         rowptr = torch.as_tensor(rowptr, dtype=torch.int64).to(device).contiguous()

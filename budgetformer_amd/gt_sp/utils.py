@@ -61,7 +61,7 @@ def estimate_edge_build_bytes(n_queries: int, real_edges_per_query: int, rw_edge
     """
     n = max(0, int(n_queries))
     b_r, b_w = max(0, int(real_edges_per_query)), max(0, int(rw_edges_per_query))
-    transient = _align(n * b_w * 4) + _align(n * 4) + _WS_ALIGN if b_w > 0 else 2 * _WS_ALIGN
+    transient = _align(n * b_w * 4) + _align(n * 4) + _WS_ALIGN
     output = n * (b_r + b_w) * 4 + n * 4
     return {"transient": int(transient), "output": int(output), "per_query_transient": 4 * (b_w + 1)}
 

@@ -17,6 +17,7 @@ from . import _native as N
 
 DEFAULT_CHUNK = 64      # rows longer than this go through the split plan
 DEFAULT_ITEM = 512      # entries per split item (one workgroup)
+HUB_THRESHOLD = 1024    # in-degree above which a query's real-edge top-k uses a whole workgroup
 
 
 def _p(t: Optional[torch.Tensor]):
@@ -144,7 +145,8 @@ def rw_select(rowptr, col, q_lo: int, n_q: int, walks_per_node: int, walk_length
 
 
 def real_select_merge(in_ptr, in_src, q_lo: int, n_q: int, k_real: int, key_seed: int,
-                      rw_kv=None, rw_cnt=None, k_rw: int = 0, dedup: bool = True, width: Optional[int] = None):
+                      rw_kv=None, rw_cnt=None, k_rw: int = 0, dedup: bool = True, width: Optional[int] = None,
+                      hubs: Optional[torch.Tensor] = None, hub_threshold: int = HUB_THRESHOLD):
     """Real-edge top-k_real merged with an RW selection: (table [n_q,width], row_len [n_q])."""
     dev = in_ptr.device
     _require(in_ptr, "in_ptr", torch.int64)
@@ -152,14 +154,19 @@ def real_select_merge(in_ptr, in_src, q_lo: int, n_q: int, k_real: int, key_seed
     width = width if width is not None else max(1, max(k_real, 0) + (k_rw if rw_kv is not None else 0))
     table = torch.empty(n_q, width, dtype=torch.int32, device=dev)
     row_len = torch.empty(n_q, dtype=torch.int32, device=dev)
+    n_hubs = 0 if hubs is None or k_real <= 0 else hubs.numel()
+    hub_sel = torch.empty(max(n_hubs * max(k_real, 0), 1), dtype=torch.int32, device=dev)
+    hub_cnt = torch.empty(max(n_hubs, 1), dtype=torch.int32, device=dev)
     N.call("bf_real_select_merge", _p(in_ptr), _p(in_src), in_ptr.numel() - 1, q_lo, n_q, k_real, key_seed,
-           _p(rw_kv), _p(rw_cnt), k_rw, int(bool(dedup)), _p(table), width, _p(row_len), _stream(dev))
+           _p(rw_kv), _p(rw_cnt), k_rw, int(bool(dedup)), _p(table), width, _p(row_len),
+           _p(hubs) if n_hubs else None, n_hubs, hub_threshold, _p(hub_sel), _p(hub_cnt), _stream(dev))
     return table, row_len
 
 
 def build_edge_table(rowptr, col, in_ptr, in_src, num_edges: int, q_lo: int, n_q: int, walks_per_node: int,
                      walk_length: int, k_real: int, k_rw: int, edge_seed: int, u=None, philox_seed: int = 0,
-                     philox_offset: int = 0, out=None):
+                     philox_offset: int = 0, out=None, hubs: Optional[torch.Tensor] = None,
+                     hub_threshold: int = HUB_THRESHOLD):
     """Fused budgeted build (bf_build_edge_table): (table [n_q, k_real+k_rw], row_len [n_q]).
 
     ``out=(table, row_len)`` writes into caller-provided (contiguous) tensors.
@@ -183,11 +190,15 @@ def build_edge_table(rowptr, col, in_ptr, in_src, num_edges: int, q_lo: int, n_q
         _require(row_len, "row_len", torch.int32, dev)
         if tuple(table.shape) != (n_q, width) or tuple(row_len.shape) != (n_q,):
             raise ValueError(f"out tensors must be [{n_q}, {width}] and [{n_q}]")
-    ws_bytes = _size_query("bf_build_edge_table_workspace_size", n_q, max(k_rw, 0))
+    n_hubs = 0 if hubs is None else hubs.numel()
+    if n_hubs:
+        _require(hubs, "hubs", torch.int32, dev)
+    ws_bytes = _size_query("bf_build_edge_table_workspace_size", n_q, max(k_rw, 0), n_hubs, max(k_real, 0))
     ws = _workspace(ws_bytes, dev)
     N.call("bf_build_edge_table", _p(rowptr), _p(col), _p(in_ptr), _p(in_src), rowptr.numel() - 1, num_edges,
            q_lo, n_q, walks_per_node, walk_length, k_real, k_rw, edge_seed, _p(u), philox_seed & (2 ** 64 - 1),
-           philox_offset & (2 ** 64 - 1), _p(table), _p(row_len), _p(ws), ws.numel(), _stream(dev))
+           philox_offset & (2 ** 64 - 1), _p(hubs) if n_hubs else None, n_hubs, hub_threshold, _p(table),
+           _p(row_len), _p(ws), ws.numel(), _stream(dev))
     return table, row_len
 
 

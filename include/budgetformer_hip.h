@@ -121,27 +121,35 @@ int bf_rw_select(const int64_t* rowptr, const int32_t* col, int64_t num_nodes,
  *   k_real <= 0 drops the real part; rw_kv/rw_cnt NULL (or k_rw 0) drops the
  *   RW part. dedup != 0 merges as a set (the reference coalesces when both
  *   parts are globally non-empty); dedup == 0 keeps duplicates.
+ *   hubs int32 [n_hubs] (ascending query ids whose in-degree exceeds
+ *     hub_threshold, or n_hubs = 0): their top-k is computed by one workgroup
+ *     each into hub_sel int32 [n_hubs, k_real] / hub_cnt int32 [n_hubs]
+ *     (caller-provided scratch) instead of by a 16-lane group.
  *   table int32 [n_q, width] rows ascending, -1 padded; row_len int32 [n_q].
  *   Requires k_real <= 32, k_rw <= 32, width >= k_real + k_rw.               */
 int bf_real_select_merge(const int64_t* in_ptr, const int32_t* in_src, int64_t num_nodes,
                          int64_t q_lo, int64_t n_q, int32_t k_real, int64_t key_seed,
                          const int32_t* rw_kv, const int32_t* rw_cnt, int32_t k_rw,
                          int32_t dedup, int32_t* table, int32_t width, int32_t* row_len,
-                         void* stream);
+                         const int32_t* hubs, int64_t n_hubs, int64_t hub_threshold,
+                         int32_t* hub_sel, int32_t* hub_cnt, void* stream);
 
 /* Whole budgeted build: bf_rw_select then bf_real_select_merge with
  * key seeds edge_seed+37 / edge_seed+17 (utils/fullgraph_sp_support.py:970-972,
  * 1413, 1514) and the reference's global merge rule (dedup iff both parts are
  * non-empty). Replaces _build_merged_edges (utils/fullgraph_sp_support.py:
- * 2943-3026) without the Graphormer token. width = k_real + k_rw.
+ * 2943-3026) without the Graphormer token. width = k_real + k_rw. hubs /
+ * n_hubs / hub_threshold as in bf_real_select_merge (n_hubs may be 0).
  * Workspace: bf_build_edge_table_workspace_size.                            */
-int bf_build_edge_table_workspace_size(int64_t n_q, int32_t k_rw, size_t* bytes);
+int bf_build_edge_table_workspace_size(int64_t n_q, int32_t k_rw, int64_t n_hubs, int32_t k_real,
+                                       size_t* bytes);
 int bf_build_edge_table(const int64_t* rowptr, const int32_t* col,
                         const int64_t* in_ptr, const int32_t* in_src, int64_t num_nodes,
                         int64_t num_edges, int64_t q_lo, int64_t n_q,
                         int32_t walks_per_node, int32_t walk_length,
                         int32_t k_real, int32_t k_rw, int64_t edge_seed,
                         const float* u, uint64_t philox_seed, uint64_t philox_offset,
+                        const int32_t* hubs, int64_t n_hubs, int64_t hub_threshold,
                         int32_t* table, int32_t* row_len,
                         void* workspace, size_t workspace_bytes, void* stream);
 

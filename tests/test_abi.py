@@ -57,5 +57,5 @@ def test_workspace_queries_run_on_cpu():
     out = C.c_size_t(0)
     N.call("bf_reverse_index_workspace_size", 1000, 100, C.byref(out))
     assert out.value >= 3 * 1000 * 4
-    N.call("bf_build_edge_table_workspace_size", 1000, 4, C.byref(out))
+    N.call("bf_build_edge_table_workspace_size", 1000, 4, 0, 4, C.byref(out))
     assert out.value >= 1000 * 4 * 4

@@ -166,3 +166,26 @@ def test_device_chung_lu_graph_properties(hip_device):
     assert torch.equal(in_ptr, g.rowptr) and torch.equal(in_src, g.col)
     g2 = chung_lu_device(n, e, exponent=2.1, seed=7, max_degree=3000, device=hip_device)
     assert torch.equal(g2.col, g.col)                                # deterministic
+
+
+@pytest.mark.parametrize("b_r,b_w,thr", [(4, 4, 16), (8, 8, 64), (3, 0, 8), (16, 16, 32)])
+def test_hub_path_bit_exact(hip_device, b_r, b_w, thr):
+    """Rows above the hub threshold take the workgroup top-k; the table must not change."""
+    from budgetformer_amd import hip_ops
+    from budgetformer_amd.edges import build_attention_edges
+    n, P, L = 3000, 4, 4
+    rowptr, col = _graph(n, 40000, seed=thr)
+    g = _dev_graph(rowptr, col, n, hip_device)
+    u = np.random.default_rng(thr).random((n * P, L), dtype=np.float32)
+    ut = torch.from_numpy(u).to(hip_device)
+    hubs = g.hubs(thr)
+    assert hubs.numel() > 10 and (np.diff(rowptr)[hubs.cpu().numpy()] > thr).all()
+    a = hip_ops.build_edge_table(g.rowptr, g.col, g.in_ptr, g.in_src, g.num_edges, 0, n, P, L, b_r, b_w, 42, u=ut,
+                                 hubs=hubs, hub_threshold=thr)
+    b = hip_ops.build_edge_table(g.rowptr, g.col, g.in_ptr, g.in_src, g.num_edges, 0, n, P, L, b_r, b_w, 42, u=ut)
+    ref_t, ref_len = et.build_edge_table(rowptr, col, n, b_r, b_w, L, P, 42, u)
+    assert np.array_equal(a[0].cpu().numpy(), ref_t) and np.array_equal(b[0].cpu().numpy(), ref_t)
+    # a shard whose hub list is restricted to the shard
+    tab = build_attention_edges(g, real_edges_per_query=b_r, rw_edges_per_query=b_w, walk_length=L,
+                                walks_per_node=P, edge_seed=42, u=ut[200 * P:1700 * P], q_lo=200, n_q=1500)
+    assert np.array_equal(tab.table.cpu().numpy(), ref_t[200:1700])

@@ -11,7 +11,7 @@ def test_estimate_matches_library_workspace_query():
     from budgetformer_amd import _native as N
     for n_q, b_w in ((1, 1), (1000, 4), (169_343, 4), (27_800_000, 4), (5, 16)):
         out = C.c_size_t(0)
-        N.call("bf_build_edge_table_workspace_size", n_q, b_w, C.byref(out))
+        N.call("bf_build_edge_table_workspace_size", n_q, b_w, 0, 4, C.byref(out))
         assert gu.estimate_edge_build_bytes(n_q, 4, b_w)["transient"] == out.value
 
 
