@@ -9,13 +9,15 @@ by ``python -m budgetformer_amd.build``). There is no CPU fallback: every entry
 point raises if the library is missing or a tensor is not on a HIP device.
 """
 from . import _native
-from .attention import CoreAttention, GPSCoreAttention, GTCoreAttention, sparse_edge_attention
+from .attention import (CoreAttention, ExphormerCoreAttention, GPSCoreAttention, GTCoreAttention,
+                        sparse_edge_attention)
 from .edges import EdgeTable, build_attention_edges
 from .graph import CSRGraph
 from .hip_ops import AttentionIndex
 
 __all__ = [
-    "AttentionIndex", "CSRGraph", "CoreAttention", "EdgeTable", "GPSCoreAttention", "GTCoreAttention",
+    "AttentionIndex", "CSRGraph", "CoreAttention", "EdgeTable", "ExphormerCoreAttention", "GPSCoreAttention",
+    "GTCoreAttention",
     "build_attention_edges", "sparse_edge_attention",
 ]
 

@@ -6,6 +6,7 @@ attn_type=None)`` signatures of
   models/graphormer_dist_node_level.py:61-613   (sparse path :155-265, dispatch :591-613)
   models/gt_dist_node_level.py:51-522           (sparse path :179-262, dispatch :505-522)
   models/graphgps_dist_node_level.py:135-209    (sparse path :151-177)
+  models/exphormer_dist_node_level.py:45-121    (typed-edge modulation)
 and compute the sparse path with the HIP forward/backward kernels. Only
 ``attn_type="sparse"`` is on this path; the dense "full"/"flash"/"performer"
 variants are not part of it and raise.
@@ -229,3 +230,60 @@ class GPSCoreAttention(nn.Module):
         if attn_type != "sparse":
             raise NotImplementedError(f"attn_type={attn_type!r} is not on the sparse edge-attention path")
         return self._sparse(q, k, v, edge_index, q.size(2), self.hidden_size_per_attention_head)
+
+
+class ExphormerCoreAttention(nn.Module):
+    """Exphormer core attention (models/exphormer_dist_node_level.py:45-121) on the HIP kernels.
+
+    score = sum_j (k_j * q_j / sqrt(d)) * E[type]_j with E = edge_proj(edge_type_emb(type)).
+    Since E depends only on the edge type (2 types), edge e of type t is routed
+    to key/value row ``src + t * N_kv`` of the stacked keys ``cat(k*E_0, k*E_1)``
+    and values ``cat(v, v)``: the HIP kernels compute exactly the reference
+    score, and autograd of the two elementwise products returns dk, dv and the
+    gradients of the edge encoder.
+    """
+
+    N_EDGE_TYPES = 2
+
+    def __init__(self, hidden_size, attention_dropout_rate, num_heads):
+        super().__init__()
+        self.hidden_size_per_attention_head = hidden_size // num_heads
+        self.num_attention_heads_per_partition = num_heads
+        self.num_heads = num_heads
+        self.scale = math.sqrt(self.hidden_size_per_attention_head)
+        self.att_dropout = nn.Dropout(attention_dropout_rate)
+        hidden_size = num_heads * self.hidden_size_per_attention_head
+        self.edge_type_emb = nn.Embedding(self.N_EDGE_TYPES, hidden_size)
+        self.edge_proj = nn.Linear(hidden_size, hidden_size, bias=False)
+        self._typed_key = None
+        self._typed_idx = None
+
+    def edge_modulation(self, device):
+        types = torch.arange(self.N_EDGE_TYPES, device=device)
+        return self.edge_proj(self.edge_type_emb(types)).view(self.N_EDGE_TYPES, self.num_heads,
+                                                              self.hidden_size_per_attention_head)
+
+    def forward(self, q, k, v, attn_bias=None, edge_index=None, attn_type=None):
+        batch_size, s_len = q.size(0), q.size(1)
+        num_heads, hn = q.size(2), self.hidden_size_per_attention_head
+        qf = q.reshape(-1, num_heads, hn)
+        kf = k.reshape(-1, num_heads, hn)
+        vf = v.reshape(-1, num_heads, hn)
+        n_kv = kf.size(0)
+        if isinstance(edge_index, torch.Tensor) and edge_index.dim() == 2 and edge_index.size(0) == 3:
+            key = (edge_index.data_ptr(), tuple(edge_index.shape), edge_index._version, str(q.device),
+                   qf.size(0), n_kv)
+            if self._typed_key != key:      # one conversion per edge set, shared by every layer call
+                ei = edge_index.to(q.device)
+                shifted = torch.stack([ei[0].long() + ei[2].long() * n_kv, ei[1].long()])
+                self._typed_idx = AttentionIndex.from_coo(shifted, qf.size(0), self.N_EDGE_TYPES * n_kv)
+                self._typed_key = key
+            idx = self._typed_idx
+            E = self.edge_modulation(q.device).to(kf.dtype)
+            k_typed = torch.cat([kf * E[t] for t in range(self.N_EDGE_TYPES)], dim=0)
+            v_typed = torch.cat([vf] * self.N_EDGE_TYPES, dim=0)
+            out = sparse_edge_attention(qf, k_typed, v_typed, idx)
+        else:
+            idx = resolve_index(edge_index, qf.size(0), n_kv, q.device)
+            out = sparse_edge_attention(qf, kf, vf, idx)
+        return out.view(batch_size, s_len, -1)

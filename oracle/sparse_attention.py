@@ -11,6 +11,8 @@ Restated reference code (paths relative to the reference root):
       (argument order (q, k, v, ...); bias [b, np, s, s] permuted to [s, s, np])
   GraphGPS GPSCoreAttention._sparse               models/graphgps_dist_node_level.py:151-177
       (normalise per edge, then dropout, then aggregate)
+  Exphormer ExphormerCoreAttention.forward        models/exphormer_dist_node_level.py:77-121
+      (score = sum(k*q/sqrt(d) * E[type]); E = Linear(Embedding(type)))
 ``torch_scatter.scatter(..., reduce='add')`` into a zero tensor is restated as
 ``index_add_`` (same sum, deterministic order on the CPU). Backward is torch
 autograd of the same graph of ops, which is what the reference trains with.
@@ -91,6 +93,28 @@ def gps_sparse_attention(q, k, v, edge_index, drop_mask=None, drop_scale=1.0):
         norm = norm * drop_mask.to(norm.dtype).unsqueeze(-1) * drop_scale
     msg = v[edge_index[0].to(torch.long)] * norm
     return torch.zeros_like(v).index_add(0, dst, msg)
+
+
+def exphormer_sparse_attention(q, k, v, edge_index, edge_mod=None):
+    """models/exphormer_dist_node_level.py:92-119.
+
+    edge_index: [2, E] or [3, E] (row 2 = integer edge type); edge_mod: [n_types, H, hn]
+    modulation E (the module computes it as edge_proj(edge_type_emb(type))).
+    """
+    num_heads, hn = q.size(1), q.size(2)
+    scale = math.sqrt(hn)
+    edge_type = edge_index[2].long() if edge_index.size(0) == 3 else None
+    ei = edge_index[:2]
+    src = k[ei[0].long()]
+    dest = q[ei[1].long()]
+    score = torch.mul(src, dest) / scale
+    if edge_type is not None:
+        score = torch.mul(score, edge_mod[edge_type])
+    score = torch.exp(score.sum(-1, keepdim=True).clamp(-CLAMP, CLAMP))
+    msg = v[ei[0].long()] * score
+    wV = torch.zeros_like(v).index_add(0, ei[1].long(), msg)
+    Z = score.new_zeros(v.size(0), num_heads, 1).index_add(0, ei[1].long(), score)
+    return wV / (Z + EPS)
 
 
 def attention_forward_stats(k, q, v, edge_index, bias_e=None, factor_e=None):

@@ -180,3 +180,24 @@ def test_unsupported_head_dim_raises(hip_device):
     idx = AttentionIndex.from_coo(ei.to(hip_device), 10)
     with pytest.raises(NotImplementedError):
         _run(hip_device, q, k, v, idx, dout)
+
+
+def test_exphormer_typed_edges_match_oracle(hip_device):
+    from budgetformer_amd.attention import ExphormerCoreAttention
+    S, H, hn = 150, 8, 16
+    q, k, v, ei, dout = _inputs(S, H, hn, 1200, seed=31)
+    types = torch.randint(0, 2, (ei.size(1),), generator=torch.Generator().manual_seed(3))
+    ei3 = torch.cat([ei, types[None]])
+    mod = ExphormerCoreAttention(H * hn, 0.0, H).to(hip_device)
+    qd, kd, vd = (t[None].to(hip_device).requires_grad_(True) for t in (q, k, v))
+    out = mod(qd, kd, vd, None, ei3.to(hip_device))
+    out.backward(dout[None].to(hip_device).reshape(1, S, H * hn))
+    # oracle in float64 with the module's own edge encoder
+    E = mod.edge_modulation(hip_device).detach().double().cpu()
+    q64, k64, v64 = (t.double().requires_grad_(True) for t in (q, k, v))
+    ref = sa.exphormer_sparse_attention(q64, k64, v64, ei3, E)
+    ref.backward(dout.double())
+    assert _rel_err(out.view(S, H, hn), ref) < 1e-5
+    for got, r in ((qd.grad[0], q64.grad), (kd.grad[0], k64.grad), (vd.grad[0], v64.grad)):
+        assert _rel_err(got, r) < 1e-5
+    assert mod.edge_proj.weight.grad is not None and mod.edge_type_emb.weight.grad is not None

@@ -114,3 +114,23 @@ def test_gps_mask_equals_factor_form():
     b, _ = sa.attention_forward_stats(k, q, v, ei, None, keep.double() * 2.0)
     torch.testing.assert_close(a, b)
     torch.testing.assert_close(sa.gps_sparse_attention(q, k, v, ei), sa.graphormer_sparse_attention(k, q, v, ei))
+
+
+def test_exphormer_oracle_reduces_to_plain_and_to_typed_keys():
+    q, k, v = _rand(30, 4, 8, 21)
+    g = torch.Generator().manual_seed(22)
+    ei = torch.randint(0, 30, (2, 200), generator=g)
+    types = torch.randint(0, 2, (200,), generator=g)
+    ones = torch.ones(2, 4, 8, dtype=torch.float64)
+    # E = 1 for both types: plain sparse attention
+    torch.testing.assert_close(sa.exphormer_sparse_attention(q, k, v, torch.cat([ei, types[None]]), ones),
+                               sa.graphormer_sparse_attention(k, q, v, ei))
+    # typed keys: route type t to row src + t*N of cat(k*E0, k*E1), values cat(v, v)
+    E = torch.randn(2, 4, 8, generator=g, dtype=torch.float64)
+    ref = sa.exphormer_sparse_attention(q, k, v, torch.cat([ei, types[None]]), E)
+    k2 = torch.cat([k * E[0], k * E[1]])
+    v2 = torch.cat([v, v])
+    q2 = torch.cat([q, torch.zeros_like(q)])
+    shifted = torch.stack([ei[0] + types * 30, ei[1]])
+    got = sa.graphormer_sparse_attention(k2, q2, v2, shifted)[:30]
+    torch.testing.assert_close(got, ref)
