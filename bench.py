@@ -59,23 +59,20 @@ def attention_bytes(s, D, H, n_q, n_kv, nnz):
     return a_fwd, a_bwd
 
 
-def kernel_bytes(s, D, H, lens_q, lens_k, chunk):
-    """Algorithmic bytes of the three row kernels (rows <= chunk; longer rows go to the split kernels)."""
-    import numpy as np
-    lq = lens_q[lens_q <= chunk]
-    lk = lens_k[lens_k <= chunk]
-    nq, eq = lq.size, int(lq.sum())
-    nk, ek = lk.size, int(lk.sum())
-    nk_touched = int((lk > 0).sum())
+def kernel_bytes(s, D, H, lens_q, lens_k):
+    """Algorithmic bytes of the three pass kernels (each covers every entry: short rows and split items)."""
+    n_q, nnz = lens_q.size, int(lens_q.sum())
+    n_kv = lens_k.size
+    nk_touched = int((lens_k > 0).sum())
     row = s * D
     return {
         # Q read, O write, K and V gathered per edge, kv ids, Z write, qptr
-        "attn_fwd_rows_kernel": row * (2 * nq + 2 * eq) + 4 * eq + 4 * H * nq + 16 * nq,
+        "attn_fwd_kernel": row * (2 * n_q + 2 * nnz) + 4 * nnz + 4 * H * n_q + 8 * n_q,
         # Q, dO, O read, dQ write, K and V per edge, kv ids, Z read + row stats write, qptr
-        "attn_bwd_q_rows_kernel": row * (4 * nq + 2 * eq) + 4 * eq + 12 * H * nq + 16 * nq,
-        # dK, dV written for every row; K, V read for rows with entries; Q and dO per edge,
-        # the {1/D', Delta/D'} row stats per edge, kq ids, kptr
-        "attn_bwd_kv_rows_kernel": row * (2 * nk + 2 * nk_touched + 2 * ek) + 8 * H * ek + 4 * ek + 16 * nk,
+        "attn_bwd_q_kernel": row * (4 * n_q + 2 * nnz) + 4 * nnz + 12 * H * n_q + 8 * n_q,
+        # dK, dV written for every row; K, V read for rows with entries; Q and dO per entry,
+        # the {1/D', Delta/D'} row stats per entry, kq ids, kptr, row order
+        "attn_bwd_kv_kernel": row * (2 * n_kv + 2 * nk_touched + 2 * nnz) + 8 * H * nnz + 4 * nnz + 12 * n_kv,
     }
 
 
@@ -172,10 +169,8 @@ def main(argv=None):
         print(rocprof_summary(args.rocprof_summary))
         return 0
     if args.pmc_summary:
-        names = ["attn_fwd_rows_kernel", "attn_bwd_q_rows_kernel", "attn_bwd_kv_rows_kernel", "attn_fwd_items_kernel",
-                 "attn_bwd_q_items_kernel", "attn_bwd_kv_items_kernel", "attn_fwd_reduce_kernel",
-                 "attn_bwd_q_reduce_kernel", "attn_bwd_kv_reduce_kernel", "rw_select_kernel",
-                 "real_select_merge_kernel"]
+        names = ["attn_fwd_kernel", "attn_bwd_q_kernel", "attn_bwd_kv_kernel", "attn_fwd_reduce_kernel",
+                 "attn_bwd_kv_reduce_kernel", "rw_select_kernel", "real_select_merge_kernel"]
         md, data = pmc_summary(*args.pmc_summary, args.copy_bytes, names)
         print(md)
         if args.pmc_json:
@@ -269,10 +264,10 @@ def main(argv=None):
     a_fwd, a_bwd = attention_bytes(s_bytes, D, H, S, S_kv, nnz)
     attn_gbs = (a_fwd + a_bwd) / (attn_ms * 1e-3) / 1e9
 
-    # per-kernel roofline of the three row kernels
+    # per-kernel roofline of the three pass kernels
     lens_q = np.diff(idx.qptr.cpu().numpy())
     lens_k = np.diff(idx.kptr.cpu().numpy())
-    kb = kernel_bytes(s_bytes, D, H, lens_q, lens_k, idx.chunk)
+    kb = kernel_bytes(s_bytes, D, H, lens_q, lens_k)
     kernels = {}
     for name, (ms, launches) in sorted(kstats.items(), key=lambda x: -x[1][0]):
         avg = ms / max(launches, 1)
@@ -322,7 +317,9 @@ def main(argv=None):
                    "kv_rows": S_kv,
                    "table_entries": table_entries, "attention_edges": nnz, "heads": H, "head_dim": hn,
                    "walk_length": cfg["L"], "walks_per_node": cfg["P"], "budget": [cfg["b_r"], cfg["b_w"]],
-                   "global_token": cfg["token"], "split_chunk": chunk, "split_item": item},
+                   "global_token": cfg["token"], "split_chunk": chunk, "split_item": item,
+                   "split_plan": {"q_items": idx.qplan.items, "q_heavy": idx.qplan.heavy,
+                                  "k_items": idx.kplan.items, "k_heavy": idx.kplan.heavy}},
         "attn_fwd_bwd_ms": round(attn_ms, 4),
         "attn_algorithmic_bytes": a_fwd + a_bwd,
         "attn_frac_of_hbm_peak": round(attn_gbs / HBM_PEAK_GBS, 4),

@@ -15,8 +15,9 @@
 // their group, several edges per iteration so that their gathers overlap.
 // Rows longer than `chunk` (the Graphormer global token row, hub key/value
 // nodes) are cut into items by a split plan; items write float partials that
-// a reduce kernel sums in item order. Nothing uses atomics: results are
-// deterministic run to run.
+// a reduce sums in item order. Nothing uses atomics: results are deterministic
+// run to run. Launches per layer: forward (items + rows), forward reduce,
+// dq pass (items + rows), dk/dv pass (dq reduce + items + rows), dk/dv reduce.
 //
 // MFMA is not used: each score is an hn-long dot product of two gathered rows,
 // not a dense contraction, and the kernels are bound by gather bandwidth.
@@ -26,10 +27,27 @@ namespace bf {
 namespace {
 
 constexpr int kBlock = 256;
-#ifndef BF_ATTN_UNROLL
-#define BF_ATTN_UNROLL 4
+// Edges whose gathers are in flight together per group, per pass and element
+// type (measured on MI355X: more edges per group cost registers, hence waves).
+#ifndef BF_UNROLL_FWD
+#define BF_UNROLL_FWD 3
 #endif
-constexpr int kUnroll = BF_ATTN_UNROLL;   // edges whose gathers are in flight together per group
+#ifndef BF_UNROLL_Q
+#define BF_UNROLL_Q 3
+#endif
+#ifndef BF_UNROLL_KV_F32
+#define BF_UNROLL_KV_F32 3
+#endif
+#ifndef BF_UNROLL_KV_BF16
+#define BF_UNROLL_KV_BF16 4
+#endif
+template <typename T> struct Unroll;
+template <> struct Unroll<float> {
+  static constexpr int fwd = BF_UNROLL_FWD, q = BF_UNROLL_Q, kv = BF_UNROLL_KV_F32;
+};
+template <> struct Unroll<uint16_t> {
+  static constexpr int fwd = BF_UNROLL_FWD, q = BF_UNROLL_Q, kv = BF_UNROLL_KV_BF16;
+};
 constexpr float kEps = 1e-6f;
 constexpr float kClamp = 5.0f;
 
@@ -62,10 +80,6 @@ __device__ __forceinline__ GroupPos group_pos(const Shape& sh) {
   return g;
 }
 
-__device__ __forceinline__ int64_t group_index(const Shape& sh) {
-  return int64_t(blockIdx.x) * (kBlock >> sh.lpr_log2) + (threadIdx.x >> sh.lpr_log2);
-}
-
 template <typename T, int V>
 __device__ __forceinline__ void load_row(const T* base, int64_t row, int D, const GroupPos& g, float (&o)[V]) {
   if (g.act) {
@@ -88,6 +102,7 @@ __device__ __forceinline__ void fwd_segment(const T* __restrict__ k, const T* __
                                             const float (&qv)[Elem<T>::kPerVec],
                                             float (&acc)[Elem<T>::kPerVec], float& z) {
   constexpr int V = Elem<T>::kPerVec;
+  constexpr int kUnroll = Unroll<T>::fwd;
   const int lph = 1 << sh.lph_log2;
   for (int64_t e0 = beg; e0 < end; e0 += kUnroll) {
     int s[kUnroll];
@@ -138,59 +153,37 @@ __device__ __forceinline__ void fwd_segment(const T* __restrict__ k, const T* __
   }
 }
 
-template <typename T>
-__global__ __launch_bounds__(kBlock) void attn_fwd_rows_kernel(
-    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
-    const int64_t* __restrict__ qptr, const int32_t* __restrict__ kv,
-    const float* __restrict__ bias, const float* __restrict__ factor,
-    T* __restrict__ out, float* __restrict__ Z, int64_t n_q, Shape sh, int chunk) {
-  constexpr int V = Elem<T>::kPerVec;
-  const int64_t row = group_index(sh);
-  if (row >= n_q) return;
-  const int64_t beg = qptr[row], end = qptr[row + 1];
-  if (end - beg > chunk) return;  // split row: items + reduce write it
-  const GroupPos g = group_pos<T>(sh);
-  float qv[V], acc[V];
-  load_row<T, V>(q, row, sh.D, g, qv);
-#pragma unroll
-  for (int i = 0; i < V; ++i) acc[i] = 0.f;
-  float z = 0.f;
-  fwd_segment<T>(k, v, kv, bias, factor, beg, end, sh, g, qv, acc, z);
-  if (g.act) {
-    const float den = z + kEps;
-    float o[V];
-#pragma unroll
-    for (int i = 0; i < V; ++i) o[i] = acc[i] / den;
-    Elem<T>::store(out + row * sh.D + g.col0, o);
-    if (g.lead) Z[row * sh.H + g.head] = z;
-  }
-}
-
+// ------------------------------------------------------------------ split rows
 // A split item: entries [beg, end) of one long row, processed by a whole
 // workgroup; each LPR-lane group takes a contiguous sub-range and the groups'
-// sums are combined through LDS in group order.
+// sums are combined through LDS in group order. Every pass runs as ONE launch
+// whose first workgroups take the items (the longest work, dispatched first)
+// and whose remaining workgroups take the short rows, so the items overlap the
+// row work instead of running as a tail of their own.
 struct Items {
   const int64_t* ptr;
   const int32_t* item_off;
   const int32_t* item_row;
   const int32_t* nitems;
   const int32_t* heavy_rows;
+  float* partials;  // this plan's records, one per item
   int item_size;
-  int stride;     // floats per partial record: 2*D + H
+  int stride;       // floats per partial record: 2*D + H
 };
 
 struct ItemRange {
   int row;
   int j;          // item index within its row
+  bool single;    // the row has one item: the item writes the final result, no record
   int64_t beg;    // this group's sub-range
   int64_t end;
 };
 
-__device__ __forceinline__ ItemRange item_group_range(const Items& it, const Shape& sh) {
-  const int64_t item = blockIdx.x;
+__device__ __forceinline__ ItemRange item_group_range(const Items& it, const Shape& sh, int64_t item) {
   ItemRange r;
   r.row = it.item_row[item];
   r.j = int(item - it.item_off[r.row]);
+  r.single = it.nitems[r.row] == 1;
   const int64_t rb = it.ptr[r.row], re = it.ptr[r.row + 1];
   const int64_t ib = rb + int64_t(r.j) * it.item_size;
   const int64_t ie = min(ib + int64_t(it.item_size), re);
@@ -200,6 +193,11 @@ __device__ __forceinline__ ItemRange item_group_range(const Items& it, const Sha
   r.beg = min(ib + grp * sub, ie);
   r.end = min(r.beg + sub, ie);
   return r;
+}
+
+// Row handled by this lane's group when the row workgroups start at `first_block`.
+__device__ __forceinline__ int64_t row_slot(const Shape& sh, unsigned first_block) {
+  return int64_t(blockIdx.x - first_block) * (kBlock >> sh.lpr_log2) + (threadIdx.x >> sh.lpr_log2);
 }
 
 // Sums `nv` lane vectors of V floats (and, if with_z, one float per head) over
@@ -242,14 +240,14 @@ __device__ __forceinline__ void block_combine(float* lds, int stride, const Shap
   }
 }
 
-// Writes group 0's combined record for the current item.
+// Writes group 0's combined record for item `item`.
 template <int V>
-__device__ __forceinline__ void store_record(float* partials, int stride, const Shape& sh, const GroupPos& g,
+__device__ __forceinline__ void store_record(const Items& it, int64_t item, const Shape& sh, const GroupPos& g,
                                              const float (&a)[V], const float (&b)[V], bool with_b, float z,
                                              bool with_z) {
   const int grp = threadIdx.x >> sh.lpr_log2;
   if (grp != 0 || !g.act) return;
-  float* rec = partials + int64_t(blockIdx.x) * stride;
+  float* rec = it.partials + item * it.stride;
 #pragma unroll
   for (int i = 0; i < V; ++i) rec[g.col0 + i] = a[i];
   if (with_b) {
@@ -259,70 +257,118 @@ __device__ __forceinline__ void store_record(float* partials, int stride, const 
   if (with_z && g.lead) rec[2 * sh.D + g.head] = z;
 }
 
-// Sums the records of one split row (workgroup per row, groups strided over
-// items, then combined in group order). Result valid in group 0.
+// Sums the records of split row number `heavy` (one workgroup; groups strided
+// over the items with several records in flight each, then combined in group
+// order). Returns the row id, or -1 for a row with a single item (finished by
+// that item); the sums are valid in group 0.
 template <int V>
-__device__ __forceinline__ int reduce_row_records(const float* __restrict__ partials, float* lds, const Items& it,
-                                                  const Shape& sh, const GroupPos& g, float (&a)[V], float (&b)[V],
-                                                  bool with_b, float& z, bool with_z) {
-  const int row = it.heavy_rows[blockIdx.x];
+__device__ __forceinline__ int reduce_row_records(const Items& it, int64_t heavy, float* lds, const Shape& sh,
+                                                  const GroupPos& g, float (&a)[V], float (&b)[V], bool with_b,
+                                                  float& z, bool with_z) {
+  const int row = it.heavy_rows[heavy];
   const int64_t first = it.item_off[row];
   const int n = it.nitems[row];
+  if (n == 1) return -1;   // written by its only item (uniform over the workgroup: no barrier skipped unevenly)
   const int gpb = kBlock >> sh.lpr_log2;
   const int grp = threadIdx.x >> sh.lpr_log2;
 #pragma unroll
   for (int i = 0; i < V; ++i) a[i] = b[i] = 0.f;
   z = 0.f;
   if (g.act) {
-    for (int m = grp; m < n; m += gpb) {
-      const float* rec = partials + (first + m) * it.stride;
+    constexpr int R = 8;
+    for (int m0 = grp; m0 < n; m0 += R * gpb) {
+      float ra[R][V], rb[R][V], rz[R];
 #pragma unroll
-      for (int i = 0; i < V; ++i) a[i] += rec[g.col0 + i];
-      if (with_b) {
+      for (int u = 0; u < R; ++u) {
+        const int m = m0 + u * gpb;
+        const bool ok = m < n;
+        const float* rec = it.partials + (first + (ok ? m : 0)) * it.stride;
 #pragma unroll
-        for (int i = 0; i < V; ++i) b[i] += rec[sh.D + g.col0 + i];
+        for (int i = 0; i < V; ++i) ra[u][i] = ok ? rec[g.col0 + i] : 0.f;
+        if (with_b) {
+#pragma unroll
+          for (int i = 0; i < V; ++i) rb[u][i] = ok ? rec[sh.D + g.col0 + i] : 0.f;
+        }
+        rz[u] = (with_z && ok) ? rec[2 * sh.D + g.head] : 0.f;
       }
-      if (with_z) z += rec[2 * sh.D + g.head];
+#pragma unroll
+      for (int u = 0; u < R; ++u) {
+#pragma unroll
+        for (int i = 0; i < V; ++i) a[i] += ra[u][i];
+        if (with_b) {
+#pragma unroll
+          for (int i = 0; i < V; ++i) b[i] += rb[u][i];
+        }
+        z += rz[u];
+      }
     }
   }
   block_combine<V>(lds, it.stride, sh, g, a, b, with_b, z, with_z);
   return row;
 }
 
-template <typename T>
-__global__ __launch_bounds__(kBlock) void attn_fwd_items_kernel(
-    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
-    const int32_t* __restrict__ kv, const float* __restrict__ bias,
-    const float* __restrict__ factor, float* __restrict__ partials, Items it, Shape sh) {
-  constexpr int V = Elem<T>::kPerVec;
-  extern __shared__ float lds[];
-  const ItemRange r = item_group_range(it, sh);
-  const GroupPos g = group_pos<T>(sh);
-  float qv[V], acc[V], unused[V];
-  load_row<T, V>(q, r.row, sh.D, g, qv);
-#pragma unroll
-  for (int i = 0; i < V; ++i) acc[i] = unused[i] = 0.f;
-  float z = 0.f;
-  fwd_segment<T>(k, v, kv, bias, factor, r.beg, r.end, sh, g, qv, acc, z);
-  block_combine<V>(lds, it.stride, sh, g, acc, unused, false, z, true);
-  store_record<V>(partials, it.stride, sh, g, acc, unused, false, z, true);
-}
-
-template <typename T>
-__global__ __launch_bounds__(kBlock) void attn_fwd_reduce_kernel(
-    const float* __restrict__ partials, T* __restrict__ out, float* __restrict__ Z, Items it, Shape sh) {
-  constexpr int V = Elem<T>::kPerVec;
-  extern __shared__ float lds[];
-  const GroupPos g = group_pos<T>(sh);
-  float acc[V], unused[V], z;
-  const int row = reduce_row_records<V>(partials, lds, it, sh, g, acc, unused, false, z, true);
-  if ((threadIdx.x >> sh.lpr_log2) != 0 || !g.act) return;
+// ------------------------------------------------------------------ forward kernels
+// out = acc / (Z + eps) and Z of one finished query row.
+template <typename T, int V>
+__device__ __forceinline__ void store_out(T* __restrict__ out, float* __restrict__ Z, int64_t row, const Shape& sh,
+                                          const GroupPos& g, const float (&acc)[V], float z) {
+  if (!g.act) return;
   const float den = z + kEps;
   float o[V];
 #pragma unroll
   for (int i = 0; i < V; ++i) o[i] = acc[i] / den;
-  Elem<T>::store(out + int64_t(row) * sh.D + g.col0, o);
-  if (g.lead) Z[int64_t(row) * sh.H + g.head] = z;
+  Elem<T>::store(out + row * sh.D + g.col0, o);
+  if (g.lead) Z[row * sh.H + g.head] = z;
+}
+
+// Blocks [0, n_items) take the query-side items, the rest one short query row per group.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void attn_fwd_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    const int64_t* __restrict__ qptr, const int32_t* __restrict__ kv,
+    const float* __restrict__ bias, const float* __restrict__ factor,
+    T* __restrict__ out, float* __restrict__ Z, Items it, int n_items, int64_t n_q, Shape sh, int chunk) {
+  constexpr int V = Elem<T>::kPerVec;
+  const GroupPos g = group_pos<T>(sh);
+  float qv[V], acc[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) acc[i] = 0.f;
+  float z = 0.f;
+  if (int(blockIdx.x) < n_items) {
+    extern __shared__ float lds[];
+    const ItemRange r = item_group_range(it, sh, blockIdx.x);
+    float unused[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) unused[i] = 0.f;
+    load_row<T, V>(q, r.row, sh.D, g, qv);
+    fwd_segment<T>(k, v, kv, bias, factor, r.beg, r.end, sh, g, qv, acc, z);
+    block_combine<V>(lds, it.stride, sh, g, acc, unused, false, z, true);
+    if (r.single) {
+      if ((threadIdx.x >> sh.lpr_log2) == 0) store_out(out, Z, r.row, sh, g, acc, z);
+    } else {
+      store_record<V>(it, blockIdx.x, sh, g, acc, unused, false, z, true);
+    }
+    return;
+  }
+  const int64_t row = row_slot(sh, unsigned(n_items));
+  if (row >= n_q) return;
+  const int64_t beg = qptr[row], end = qptr[row + 1];
+  if (end - beg > chunk) return;  // split row: its items and the reduce write it
+  load_row<T, V>(q, row, sh.D, g, qv);
+  fwd_segment<T>(k, v, kv, bias, factor, beg, end, sh, g, qv, acc, z);
+  store_out(out, Z, row, sh, g, acc, z);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void attn_fwd_reduce_kernel(T* __restrict__ out, float* __restrict__ Z,
+                                                                 Items it, Shape sh) {
+  constexpr int V = Elem<T>::kPerVec;
+  extern __shared__ float lds[];
+  const GroupPos g = group_pos<T>(sh);
+  float acc[V], unused[V], z;
+  const int row = reduce_row_records<V>(it, blockIdx.x, lds, sh, g, acc, unused, false, z, true);
+  if (row < 0 || (threadIdx.x >> sh.lpr_log2) != 0) return;
+  store_out(out, Z, row, sh, g, acc, z);
 }
 
 // ------------------------------------------------------------------ backward, query-major (dq)
@@ -369,6 +415,7 @@ __device__ __forceinline__ void dq_segment(const T* __restrict__ k, const T* __r
                                            const float (&gv)[Elem<T>::kPerVec],
                                            float (&dq)[Elem<T>::kPerVec]) {
   constexpr int V = Elem<T>::kPerVec;
+  constexpr int kUnroll = Unroll<T>::q;
   const int lph = 1 << sh.lph_log2;
   const float gz = -rg.delta / rg.dprime;
   for (int64_t e0 = beg; e0 < end; e0 += kUnroll) {
@@ -412,6 +459,8 @@ __device__ __forceinline__ void dq_segment(const T* __restrict__ k, const T* __r
       }
     }
 #pragma unroll
+    for (int u = 0; u < kUnroll; ++u) Elem<T>::pin(kr[u]);
+#pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       if (!ok[u]) continue;
       const int64_t e = e0 + u;
@@ -431,65 +480,50 @@ __device__ __forceinline__ void dq_segment(const T* __restrict__ k, const T* __r
   }
 }
 
+// Blocks [0, n_items) take the query-side items, the rest one short query row per group.
 template <typename T>
-__global__ __launch_bounds__(kBlock) void attn_bwd_q_rows_kernel(
+__global__ __launch_bounds__(kBlock) void attn_bwd_q_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const int64_t* __restrict__ qptr, const int32_t* __restrict__ kv,
     const float* __restrict__ bias, const float* __restrict__ factor,
     const T* __restrict__ out, const float* __restrict__ Z, const T* __restrict__ dout,
-    T* __restrict__ dq, float* __restrict__ dbias, float2* __restrict__ rstat, int64_t n_q,
-    Shape sh, int chunk) {
+    T* __restrict__ dq, float* __restrict__ dbias, float2* __restrict__ rstat, Items it, int n_items,
+    int64_t n_q, Shape sh, int chunk) {
   constexpr int V = Elem<T>::kPerVec;
-  const int64_t row = group_index(sh);
+  const GroupPos g = group_pos<T>(sh);
+  float qv[V], gv[V], acc[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) acc[i] = 0.f;
+  if (int(blockIdx.x) < n_items) {
+    extern __shared__ float lds[];
+    const ItemRange r = item_group_range(it, sh, blockIdx.x);
+    float unused[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) unused[i] = 0.f;
+    load_row<T, V>(q, r.row, sh.D, g, qv);
+    const RowGrad rg = row_grad<T>(out, dout, Z, r.row, sh, g, gv);
+    dq_segment<T>(k, v, kv, bias, factor, dbias, r.beg, r.end, sh, g, rg, qv, gv, acc);
+    float z = 0.f;
+    block_combine<V>(lds, it.stride, sh, g, acc, unused, false, z, false);
+    if (r.single) {
+      if ((threadIdx.x >> sh.lpr_log2) == 0 && g.act) Elem<T>::store(dq + int64_t(r.row) * sh.D + g.col0, acc);
+    } else {
+      store_record<V>(it, blockIdx.x, sh, g, acc, unused, false, z, false);
+    }
+    if (r.j == 0 && (threadIdx.x >> sh.lpr_log2) == 0 && g.lead) store_row_stat(rstat, r.row, sh, g, rg);
+    return;
+  }
+  const int64_t row = row_slot(sh, unsigned(n_items));
   if (row >= n_q) return;
   const int64_t beg = qptr[row], end = qptr[row + 1];
   if (end - beg > chunk) return;
-  const GroupPos g = group_pos<T>(sh);
-  float qv[V], gv[V], acc[V];
   load_row<T, V>(q, row, sh.D, g, qv);
   const RowGrad rg = row_grad<T>(out, dout, Z, row, sh, g, gv);
-#pragma unroll
-  for (int i = 0; i < V; ++i) acc[i] = 0.f;
   dq_segment<T>(k, v, kv, bias, factor, dbias, beg, end, sh, g, rg, qv, gv, acc);
   if (g.act) {
     Elem<T>::store(dq + row * sh.D + g.col0, acc);
     if (g.lead) store_row_stat(rstat, row, sh, g, rg);
   }
-}
-
-template <typename T>
-__global__ __launch_bounds__(kBlock) void attn_bwd_q_items_kernel(
-    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
-    const int32_t* __restrict__ kv, const float* __restrict__ bias,
-    const float* __restrict__ factor, const T* __restrict__ out, const float* __restrict__ Z,
-    const T* __restrict__ dout, float* __restrict__ dbias, float2* __restrict__ rstat,
-    float* __restrict__ partials, Items it, Shape sh) {
-  constexpr int V = Elem<T>::kPerVec;
-  extern __shared__ float lds[];
-  const ItemRange r = item_group_range(it, sh);
-  const GroupPos g = group_pos<T>(sh);
-  float qv[V], gv[V], acc[V], unused[V];
-  load_row<T, V>(q, r.row, sh.D, g, qv);
-  const RowGrad rg = row_grad<T>(out, dout, Z, r.row, sh, g, gv);
-#pragma unroll
-  for (int i = 0; i < V; ++i) acc[i] = unused[i] = 0.f;
-  dq_segment<T>(k, v, kv, bias, factor, dbias, r.beg, r.end, sh, g, rg, qv, gv, acc);
-  float z = 0.f;
-  block_combine<V>(lds, it.stride, sh, g, acc, unused, false, z, false);
-  store_record<V>(partials, it.stride, sh, g, acc, unused, false, z, false);
-  if (r.j == 0 && (threadIdx.x >> sh.lpr_log2) == 0 && g.lead) store_row_stat(rstat, r.row, sh, g, rg);
-}
-
-template <typename T>
-__global__ __launch_bounds__(kBlock) void attn_bwd_q_reduce_kernel(
-    const float* __restrict__ partials, T* __restrict__ dq, Items it, Shape sh) {
-  constexpr int V = Elem<T>::kPerVec;
-  extern __shared__ float lds[];
-  const GroupPos g = group_pos<T>(sh);
-  float acc[V], unused[V], z;
-  const int row = reduce_row_records<V>(partials, lds, it, sh, g, acc, unused, false, z, false);
-  if ((threadIdx.x >> sh.lpr_log2) != 0 || !g.act) return;
-  Elem<T>::store(dq + int64_t(row) * sh.D + g.col0, acc);
 }
 
 // ------------------------------------------------------------------ backward, key-major (dk, dv)
@@ -506,6 +540,7 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
                                             float (&dk)[Elem<T>::kPerVec],
                                             float (&dv)[Elem<T>::kPerVec]) {
   constexpr int V = Elem<T>::kPerVec;
+  constexpr int kUnroll = Unroll<T>::kv;
   const int lph = 1 << sh.lph_log2;
   const bool need_e = bias != nullptr || factor != nullptr;
   for (int64_t i0 = beg; i0 < end; i0 += kUnroll) {
@@ -553,6 +588,11 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
+      Elem<T>::pin(qr[u]);
+      Elem<T>::pin(gr[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
       if (!ok[u]) continue;
       const int64_t e = need_e ? int64_t(ke[i0 + u]) : 0;
       const float apre = d[u];
@@ -575,24 +615,54 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
   }
 }
 
+// Blocks [0, q_heavy) reduce the query-side split rows into dq (their items ran
+// in the dq pass), blocks [q_heavy, q_heavy + k_items) take the key-side items,
+// the rest one short key row per group, longest rows first.
 template <typename T>
-__global__ __launch_bounds__(kBlock) void attn_bwd_kv_rows_kernel(
+__global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const int64_t* __restrict__ kptr, const int32_t* __restrict__ kq,
     const int32_t* __restrict__ ke, const float* __restrict__ bias,
     const float* __restrict__ factor, const T* __restrict__ dout, const float2* __restrict__ rstat,
-    T* __restrict__ dk, T* __restrict__ dv, const int32_t* __restrict__ order, int64_t n_kv, Shape sh, int chunk) {
+    T* __restrict__ dq, T* __restrict__ dk, T* __restrict__ dv, const int32_t* __restrict__ order,
+    Items qit, int q_heavy, Items kit, int k_items, int64_t n_kv, Shape sh, int chunk) {
   constexpr int V = Elem<T>::kPerVec;
-  const int64_t slot = group_index(sh);
+  extern __shared__ float lds[];
+  const GroupPos g = group_pos<T>(sh);
+  float ak[V], av[V];
+  const int b = int(blockIdx.x);
+  if (b < q_heavy) {
+    float z;
+    const int row = reduce_row_records<V>(qit, b, lds, sh, g, ak, av, false, z, false);
+    if (row >= 0 && (threadIdx.x >> sh.lpr_log2) == 0 && g.act) Elem<T>::store(dq + int64_t(row) * sh.D + g.col0, ak);
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < V; ++i) ak[i] = av[i] = 0.f;
+  if (b < q_heavy + k_items) {
+    const int64_t item = b - q_heavy;
+    const ItemRange r = item_group_range(kit, sh, item);
+    float kk[V], vv[V];
+    load_row<T, V>(k, r.row, sh.D, g, kk);
+    load_row<T, V>(v, r.row, sh.D, g, vv);
+    dkv_segment<T>(q, dout, kq, ke, bias, factor, rstat, r.beg, r.end, sh, g, kk, vv, ak, av);
+    float z = 0.f;
+    block_combine<V>(lds, kit.stride, sh, g, ak, av, true, z, false);
+    if (r.single) {
+      if ((threadIdx.x >> sh.lpr_log2) == 0 && g.act) {
+        Elem<T>::store(dk + int64_t(r.row) * sh.D + g.col0, ak);
+        Elem<T>::store(dv + int64_t(r.row) * sh.D + g.col0, av);
+      }
+    } else {
+      store_record<V>(kit, item, sh, g, ak, av, true, z, false);
+    }
+    return;
+  }
+  const int64_t slot = row_slot(sh, unsigned(q_heavy + k_items));
   if (slot >= n_kv) return;
-  // rows visited longest-first so the groups sharing a wavefront carry similar work
   const int64_t row = order ? int64_t(order[slot]) : slot;
   const int64_t beg = kptr[row], end = kptr[row + 1];
   if (end - beg > chunk) return;
-  const GroupPos g = group_pos<T>(sh);
-  float kk[V], vv[V], ak[V], av[V];
-#pragma unroll
-  for (int i = 0; i < V; ++i) ak[i] = av[i] = 0.f;
   if (beg == end) {               // key/value row no query attends to: zero gradient, no reads
     if (g.act) {
       Elem<T>::store(dk + row * sh.D + g.col0, ak);
@@ -600,6 +670,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_rows_kernel(
     }
     return;
   }
+  float kk[V], vv[V];
   load_row<T, V>(k, row, sh.D, g, kk);
   load_row<T, V>(v, row, sh.D, g, vv);
   dkv_segment<T>(q, dout, kq, ke, bias, factor, rstat, beg, end, sh, g, kk, vv, ak, av);
@@ -610,36 +681,14 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_rows_kernel(
 }
 
 template <typename T>
-__global__ __launch_bounds__(kBlock) void attn_bwd_kv_items_kernel(
-    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
-    const int32_t* __restrict__ kq, const int32_t* __restrict__ ke,
-    const float* __restrict__ bias, const float* __restrict__ factor,
-    const T* __restrict__ dout, const float2* __restrict__ rstat,
-    float* __restrict__ partials, Items it, Shape sh) {
-  constexpr int V = Elem<T>::kPerVec;
-  extern __shared__ float lds[];
-  const ItemRange r = item_group_range(it, sh);
-  const GroupPos g = group_pos<T>(sh);
-  float kk[V], vv[V], ak[V], av[V];
-  load_row<T, V>(k, r.row, sh.D, g, kk);
-  load_row<T, V>(v, r.row, sh.D, g, vv);
-#pragma unroll
-  for (int i = 0; i < V; ++i) ak[i] = av[i] = 0.f;
-  dkv_segment<T>(q, dout, kq, ke, bias, factor, rstat, r.beg, r.end, sh, g, kk, vv, ak, av);
-  float z = 0.f;
-  block_combine<V>(lds, it.stride, sh, g, ak, av, true, z, false);
-  store_record<V>(partials, it.stride, sh, g, ak, av, true, z, false);
-}
-
-template <typename T>
-__global__ __launch_bounds__(kBlock) void attn_bwd_kv_reduce_kernel(
-    const float* __restrict__ partials, T* __restrict__ dk, T* __restrict__ dv, Items it, Shape sh) {
+__global__ __launch_bounds__(kBlock) void attn_bwd_kv_reduce_kernel(T* __restrict__ dk, T* __restrict__ dv,
+                                                                    Items it, Shape sh) {
   constexpr int V = Elem<T>::kPerVec;
   extern __shared__ float lds[];
   const GroupPos g = group_pos<T>(sh);
   float ak[V], av[V], z;
-  const int row = reduce_row_records<V>(partials, lds, it, sh, g, ak, av, true, z, false);
-  if ((threadIdx.x >> sh.lpr_log2) != 0 || !g.act) return;
+  const int row = reduce_row_records<V>(it, blockIdx.x, lds, sh, g, ak, av, true, z, false);
+  if (row < 0 || (threadIdx.x >> sh.lpr_log2) != 0 || !g.act) return;
   Elem<T>::store(dk + int64_t(row) * sh.D + g.col0, ak);
   Elem<T>::store(dv + int64_t(row) * sh.D + g.col0, av);
 }
@@ -702,14 +751,16 @@ inline size_t combine_lds_bytes(const Shape& sh) {
   return size_t(kBlock >> sh.lpr_log2) * size_t(2 * sh.D + sh.H) * sizeof(float);
 }
 
-inline Items query_items(const bf_attn_index* idx, const Shape& sh) {
-  return Items{idx->qptr, idx->q_item_off, idx->q_item_row, idx->q_nitems, idx->q_heavy_rows, idx->item,
-               2 * sh.D + sh.H};
+inline Items query_items(const bf_attn_index* idx, const Shape& sh, float* partials) {
+  return Items{idx->qptr, idx->q_item_off, idx->q_item_row, idx->q_nitems, idx->q_heavy_rows, partials,
+               idx->item, 2 * sh.D + sh.H};
 }
 
-inline Items key_items(const bf_attn_index* idx, const Shape& sh) {
-  return Items{idx->kptr, idx->k_item_off, idx->k_item_row, idx->k_nitems, idx->k_heavy_rows, idx->item,
-               2 * sh.D + sh.H};
+// Key-side records follow the query-side ones, so the dk/dv launch can reduce
+// the dq split rows while its items write their own records.
+inline Items key_items(const bf_attn_index* idx, const Shape& sh, float* partials) {
+  return Items{idx->kptr, idx->k_item_off, idx->k_item_row, idx->k_nitems, idx->k_heavy_rows,
+               partials + int64_t(idx->q_items) * (2 * sh.D + sh.H), idx->item, 2 * sh.D + sh.H};
 }
 
 template <typename T>
@@ -719,19 +770,18 @@ int fwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
   const T* K = static_cast<const T*>(k);
   const T* Vv = static_cast<const T*>(v);
   T* O = static_cast<T*>(out);
-  if (idx->n_q > 0) {
-    BF_LAUNCH("attn_fwd_rows_kernel", attn_fwd_rows_kernel<T>, dim3(grid_for(idx->n_q, sh)), dim3(kBlock), 0, st,
-              Q, K, Vv, idx->qptr, idx->kv, bias, factor, O, Z, idx->n_q, sh, idx->chunk);
+  const Items it = query_items(idx, sh, partials);
+  const int n_items = idx->q_items;
+  const int64_t blocks = int64_t(n_items) + grid_for(idx->n_q, sh);
+  if (blocks > 0) {
+    const size_t lds = n_items > 0 ? combine_lds_bytes(sh) : 0;
+    BF_LAUNCH("attn_fwd_kernel", attn_fwd_kernel<T>, dim3(unsigned(blocks)), dim3(kBlock), lds, st, Q, K, Vv,
+              idx->qptr, idx->kv, bias, factor, O, Z, it, n_items, idx->n_q, sh, idx->chunk);
     BF_CHECK_LAUNCH();
   }
-  if (idx->q_items > 0) {
-    const Items it = query_items(idx, sh);
-    const size_t lds = combine_lds_bytes(sh);
-    BF_LAUNCH("attn_fwd_items_kernel", attn_fwd_items_kernel<T>, dim3(unsigned(idx->q_items)), dim3(kBlock), lds, st,
-              Q, K, Vv, idx->kv, bias, factor, partials, it, sh);
-    BF_CHECK_LAUNCH();
-    BF_LAUNCH("attn_fwd_reduce_kernel", attn_fwd_reduce_kernel<T>, dim3(unsigned(idx->q_heavy)), dim3(kBlock), lds,
-              st, partials, O, Z, it, sh);
+  if (idx->q_heavy > 0) {
+    BF_LAUNCH("attn_fwd_reduce_kernel", attn_fwd_reduce_kernel<T>, dim3(unsigned(idx->q_heavy)), dim3(kBlock),
+              combine_lds_bytes(sh), st, O, Z, it, sh);
     BF_CHECK_LAUNCH();
   }
   return BF_OK;
@@ -748,35 +798,27 @@ int bwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
   const T* Vv = static_cast<const T*>(v);
   const T* O = static_cast<const T*>(out);
   const T* dO = static_cast<const T*>(dout);
-  const size_t lds = combine_lds_bytes(sh);
-  if (idx->n_q > 0) {
-    BF_LAUNCH("attn_bwd_q_rows_kernel", attn_bwd_q_rows_kernel<T>, dim3(grid_for(idx->n_q, sh)), dim3(kBlock), 0, st,
-              Q, K, Vv, idx->qptr, idx->kv, bias, factor, O, Z, dO, static_cast<T*>(dq), dbias, rstat, idx->n_q, sh,
-              idx->chunk);
+  const Items qit = query_items(idx, sh, partials);
+  const Items kit = key_items(idx, sh, partials);
+  const int64_t q_blocks = int64_t(idx->q_items) + grid_for(idx->n_q, sh);
+  if (q_blocks > 0) {
+    const size_t lds = idx->q_items > 0 ? combine_lds_bytes(sh) : 0;
+    BF_LAUNCH("attn_bwd_q_kernel", attn_bwd_q_kernel<T>, dim3(unsigned(q_blocks)), dim3(kBlock), lds, st, Q, K, Vv,
+              idx->qptr, idx->kv, bias, factor, O, Z, dO, static_cast<T*>(dq), dbias, rstat, qit, idx->q_items,
+              idx->n_q, sh, idx->chunk);
     BF_CHECK_LAUNCH();
   }
-  if (idx->q_items > 0) {
-    const Items it = query_items(idx, sh);
-    BF_LAUNCH("attn_bwd_q_items_kernel", attn_bwd_q_items_kernel<T>, dim3(unsigned(idx->q_items)), dim3(kBlock), lds,
-              st, Q, K, Vv, idx->kv, bias, factor, O, Z, dO, dbias, rstat, partials, it, sh);
-    BF_CHECK_LAUNCH();
-    BF_LAUNCH("attn_bwd_q_reduce_kernel", attn_bwd_q_reduce_kernel<T>, dim3(unsigned(idx->q_heavy)), dim3(kBlock),
-              lds, st, partials, static_cast<T*>(dq), it, sh);
-    BF_CHECK_LAUNCH();
-  }
-  if (idx->n_kv > 0) {
-    BF_LAUNCH("attn_bwd_kv_rows_kernel", attn_bwd_kv_rows_kernel<T>, dim3(grid_for(idx->n_kv, sh)), dim3(kBlock), 0,
-              st, Q, K, Vv, idx->kptr, idx->kq, idx->ke, bias, factor, dO, rstat, static_cast<T*>(dk),
-              static_cast<T*>(dv), idx->k_order, idx->n_kv, sh, idx->chunk);
+  const int64_t kv_blocks = int64_t(idx->q_heavy) + idx->k_items + grid_for(idx->n_kv, sh);
+  if (kv_blocks > 0) {
+    const size_t lds = (idx->q_heavy > 0 || idx->k_items > 0) ? combine_lds_bytes(sh) : 0;
+    BF_LAUNCH("attn_bwd_kv_kernel", attn_bwd_kv_kernel<T>, dim3(unsigned(kv_blocks)), dim3(kBlock), lds, st, Q, K,
+              Vv, idx->kptr, idx->kq, idx->ke, bias, factor, dO, rstat, static_cast<T*>(dq), static_cast<T*>(dk),
+              static_cast<T*>(dv), idx->k_order, qit, idx->q_heavy, kit, idx->k_items, idx->n_kv, sh, idx->chunk);
     BF_CHECK_LAUNCH();
   }
-  if (idx->k_items > 0) {
-    const Items it = key_items(idx, sh);
-    BF_LAUNCH("attn_bwd_kv_items_kernel", attn_bwd_kv_items_kernel<T>, dim3(unsigned(idx->k_items)), dim3(kBlock),
-              lds, st, Q, K, Vv, idx->kq, idx->ke, bias, factor, dO, rstat, partials, it, sh);
-    BF_CHECK_LAUNCH();
+  if (idx->k_heavy > 0) {
     BF_LAUNCH("attn_bwd_kv_reduce_kernel", attn_bwd_kv_reduce_kernel<T>, dim3(unsigned(idx->k_heavy)), dim3(kBlock),
-              lds, st, partials, static_cast<T*>(dk), static_cast<T*>(dv), it, sh);
+              combine_lds_bytes(sh), st, static_cast<T*>(dk), static_cast<T*>(dv), kit, sh);
     BF_CHECK_LAUNCH();
   }
   return BF_OK;
@@ -789,7 +831,7 @@ using namespace bf;
 
 extern "C" int64_t bf_attn_partials_floats(const bf_attn_index* idx, int32_t num_heads, int32_t head_dim) {
   if (!idx) return 0;
-  const int64_t items = idx->q_items > idx->k_items ? idx->q_items : idx->k_items;
+  const int64_t items = int64_t(idx->q_items) + idx->k_items;   // query-side records, then key-side
   const int64_t D = int64_t(num_heads) * head_dim;
   return items * (2 * D + num_heads);
 }

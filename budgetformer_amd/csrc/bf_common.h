@@ -84,6 +84,7 @@ template <> struct Elem<float> {
   __device__ __forceinline__ static void unpack(const Raw& v, float (&o)[4]) {
     o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
   }
+  __device__ __forceinline__ static void pin(Raw&) {}   // fp32: unpacking is free, nothing to re-derive
   __device__ __forceinline__ static void load(const float* p, float (&o)[4]) {
     const float4 v = *reinterpret_cast<const float4*>(p);
     o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
@@ -98,6 +99,10 @@ template <> struct Elem<uint16_t> {
   using Raw = uint4;
   __device__ __forceinline__ static Raw load_raw(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
   __device__ __forceinline__ static Raw zero_raw() { return make_uint4(0u, 0u, 0u, 0u); }
+  // Optimisation barrier: values unpacked from `v` before this point are not
+  // reused after it, so a second use re-unpacks (two ALU ops per pair) instead
+  // of holding eight floats live per gathered row.
+  __device__ __forceinline__ static void pin(Raw& v) { asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w)); }
   __device__ __forceinline__ static void unpack(const Raw& v, float (&o)[8]) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll

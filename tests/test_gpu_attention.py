@@ -86,6 +86,27 @@ def test_fp32_global_token_split_rows(hip_device, chunk, item):
         assert _rel_err(got, ref) < 1e-5
 
 
+@pytest.mark.parametrize("chunk,item", [(4, 37), (8, 16)])
+def test_bf16_split_rows_single_and_multi_item(hip_device, chunk, item):
+    """Split rows with one item (finished by that item) and with several (summed by the reduce), bf16."""
+    from budgetformer_amd.hip_ops import AttentionIndex
+    S, H, hn = 600, 8, 16
+    q, k, v, ei, dout = _inputs(S, H, hn, 6000, seed=17, dtype=torch.bfloat16)
+    ei = ei[:, (ei[0] > 0) & (ei[1] > 0)]
+    ar = torch.arange(1, S)
+    ei = torch.cat([ei, torch.stack([ar, torch.zeros_like(ar)]), torch.stack([torch.zeros_like(ar), ar])], 1)
+    idx = AttentionIndex.from_coo(ei.to(hip_device), S, chunk=chunk, item=item)
+    idx.ensure_backward()
+    for plan in (idx.qplan, idx.kplan):
+        n = plan.nitems.cpu()
+        heavy = plan.heavy_rows[: plan.heavy].cpu().long()
+        assert (n[heavy] == 1).any() and (n[heavy] > 1).any()
+    out, dq, dk, dv, _ = _run(hip_device, q, k, v, idx, dout)
+    ro, rZ, rdq, rdk, rdv, _ = _oracle(q, k, v, ei, dout)
+    for got, ref in ((out, ro), (dq, rdq), (dk, rdk), (dv, rdv)):
+        assert _rel_err(got, ref) < 2e-2
+
+
 def test_fp32_bias_and_dbias(hip_device):
     from budgetformer_amd.hip_ops import AttentionIndex
     S, H, hn = 200, 8, 16
