@@ -39,7 +39,7 @@ constexpr int kBlock = 256;
 #define BF_UNROLL_KV_F32 3
 #endif
 #ifndef BF_UNROLL_KV_BF16
-#define BF_UNROLL_KV_BF16 4
+#define BF_UNROLL_KV_BF16 3
 #endif
 template <typename T> struct Unroll;
 template <> struct Unroll<float> {
@@ -80,14 +80,9 @@ __device__ __forceinline__ GroupPos group_pos(const Shape& sh) {
   return g;
 }
 
-template <typename T, int V>
-__device__ __forceinline__ void load_row(const T* base, int64_t row, int D, const GroupPos& g, float (&o)[V]) {
-  if (g.act) {
-    Elem<T>::load(base + row * D + g.col0, o);
-  } else {
-#pragma unroll
-    for (int i = 0; i < V; ++i) o[i] = 0.f;
-  }
+template <typename T>
+__device__ __forceinline__ typename Elem<T>::Raw load_row_raw(const T* base, int64_t row, int D, const GroupPos& g) {
+  return g.act ? Elem<T>::load_raw(base + row * D + g.col0) : Elem<T>::zero_raw();
 }
 
 // ------------------------------------------------------------------ forward
@@ -98,8 +93,7 @@ __device__ __forceinline__ void fwd_segment(const T* __restrict__ k, const T* __
                                             const float* __restrict__ bias,
                                             const float* __restrict__ factor,
                                             int64_t beg, int64_t end, const Shape& sh,
-                                            const GroupPos& g,
-                                            const float (&qv)[Elem<T>::kPerVec],
+                                            const GroupPos& g, const typename Elem<T>::Raw& qr,
                                             float (&acc)[Elem<T>::kPerVec], float& z) {
   constexpr int V = Elem<T>::kPerVec;
   constexpr int kUnroll = Unroll<T>::fwd;
@@ -124,14 +118,7 @@ __device__ __forceinline__ void fwd_segment(const T* __restrict__ k, const T* __
     }
     float d[kUnroll];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      float kk[V];
-      Elem<T>::unpack(kr[u], kk);
-      float t = 0.f;
-#pragma unroll
-      for (int i = 0; i < V; ++i) t += (kk[i] * qv[i]) * sh.inv_scale;
-      d[u] = t;
-    }
+    for (int u = 0; u < kUnroll; ++u) d[u] = Elem<T>::dot(kr[u], qr, 0.f);
     for (int o = 1; o < lph; o <<= 1) {
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) d[u] += __shfl_xor(d[u], o, 64);
@@ -140,14 +127,14 @@ __device__ __forceinline__ void fwd_segment(const T* __restrict__ k, const T* __
     for (int u = 0; u < kUnroll; ++u) {
       if (!ok[u]) continue;
       const int64_t e = e0 + u;
-      float a = fminf(fmaxf(d[u], -kClamp), kClamp);
+      float a = fminf(fmaxf(d[u] * sh.inv_scale, -kClamp), kClamp);
       if (bias) a += bias[e * sh.H + g.head];
-      const float p = expf(a);
+      const float p = __expf(a);   // a is clamped to [-5, 5] (+ bias): exp2-based form is within 2 ulp
       const float w = factor ? p * factor[e * sh.H + g.head] : p;
       float vv[V];
       Elem<T>::unpack(vr[u], vv);
 #pragma unroll
-      for (int i = 0; i < V; ++i) acc[i] += w * vv[i];
+      for (int i = 0; i < V; ++i) acc[i] = fmaf(w, vv[i], acc[i]);
       z += p;
     }
   }
@@ -330,7 +317,7 @@ __global__ __launch_bounds__(kBlock) void attn_fwd_kernel(
     T* __restrict__ out, float* __restrict__ Z, Items it, int n_items, int64_t n_q, Shape sh, int chunk) {
   constexpr int V = Elem<T>::kPerVec;
   const GroupPos g = group_pos<T>(sh);
-  float qv[V], acc[V];
+  float acc[V];
 #pragma unroll
   for (int i = 0; i < V; ++i) acc[i] = 0.f;
   float z = 0.f;
@@ -340,8 +327,8 @@ __global__ __launch_bounds__(kBlock) void attn_fwd_kernel(
     float unused[V];
 #pragma unroll
     for (int i = 0; i < V; ++i) unused[i] = 0.f;
-    load_row<T, V>(q, r.row, sh.D, g, qv);
-    fwd_segment<T>(k, v, kv, bias, factor, r.beg, r.end, sh, g, qv, acc, z);
+    const typename Elem<T>::Raw qr = load_row_raw(q, r.row, sh.D, g);
+    fwd_segment<T>(k, v, kv, bias, factor, r.beg, r.end, sh, g, qr, acc, z);
     block_combine<V>(lds, it.stride, sh, g, acc, unused, false, z, true);
     if (r.single) {
       if ((threadIdx.x >> sh.lpr_log2) == 0) store_out(out, Z, r.row, sh, g, acc, z);
@@ -354,8 +341,8 @@ __global__ __launch_bounds__(kBlock) void attn_fwd_kernel(
   if (row >= n_q) return;
   const int64_t beg = qptr[row], end = qptr[row + 1];
   if (end - beg > chunk) return;  // split row: its items and the reduce write it
-  load_row<T, V>(q, row, sh.D, g, qv);
-  fwd_segment<T>(k, v, kv, bias, factor, beg, end, sh, g, qv, acc, z);
+  const typename Elem<T>::Raw qr = load_row_raw(q, row, sh.D, g);
+  fwd_segment<T>(k, v, kv, bias, factor, beg, end, sh, g, qr, acc, z);
   store_out(out, Z, row, sh, g, acc, z);
 }
 
@@ -381,16 +368,11 @@ struct RowGrad {
 template <typename T>
 __device__ __forceinline__ RowGrad row_grad(const T* __restrict__ out, const T* __restrict__ dout,
                                             const float* __restrict__ Z, int64_t row, const Shape& sh,
-                                            const GroupPos& g, float (&gv)[Elem<T>::kPerVec]) {
-  constexpr int V = Elem<T>::kPerVec;
-  float ov[V];
-  load_row<T, V>(dout, row, sh.D, g, gv);
-  load_row<T, V>(out, row, sh.D, g, ov);
-  float t = 0.f;
-#pragma unroll
-  for (int i = 0; i < V; ++i) t += gv[i] * ov[i];
+                                            const GroupPos& g, typename Elem<T>::Raw& gr) {
+  gr = load_row_raw(dout, row, sh.D, g);
+  const typename Elem<T>::Raw orow = load_row_raw(out, row, sh.D, g);
   RowGrad r;
-  r.delta = group_sum(t, 1 << sh.lph_log2);
+  r.delta = group_sum(Elem<T>::dot(gr, orow, 0.f), 1 << sh.lph_log2);
   r.dprime = (g.act ? Z[row * sh.H + g.head] : 0.f) + kEps;
   return r;
 }
@@ -411,13 +393,14 @@ __device__ __forceinline__ void dq_segment(const T* __restrict__ k, const T* __r
                                            const float* __restrict__ factor,
                                            float* __restrict__ dbias, int64_t beg, int64_t end,
                                            const Shape& sh, const GroupPos& g, const RowGrad& rg,
-                                           const float (&qv)[Elem<T>::kPerVec],
-                                           const float (&gv)[Elem<T>::kPerVec],
+                                           const typename Elem<T>::Raw& qr,
+                                           const typename Elem<T>::Raw& gr,
                                            float (&dq)[Elem<T>::kPerVec]) {
   constexpr int V = Elem<T>::kPerVec;
   constexpr int kUnroll = Unroll<T>::q;
   const int lph = 1 << sh.lph_log2;
-  const float gz = -rg.delta / rg.dprime;
+  const float inv_dprime = 1.0f / rg.dprime;
+  const float gz = -rg.delta * inv_dprime;
   for (int64_t e0 = beg; e0 < end; e0 += kUnroll) {
     int s[kUnroll];
     bool ok[kUnroll];
@@ -439,17 +422,8 @@ __device__ __forceinline__ void dq_segment(const T* __restrict__ k, const T* __r
     float d[kUnroll], w[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      float kk[V], vv[V];
-      Elem<T>::unpack(kr[u], kk);
-      Elem<T>::unpack(vr[u], vv);
-      float t = 0.f, r = 0.f;
-#pragma unroll
-      for (int i = 0; i < V; ++i) {
-        t += (kk[i] * qv[i]) * sh.inv_scale;
-        r += gv[i] * vv[i];
-      }
-      d[u] = t;
-      w[u] = r;
+      d[u] = Elem<T>::dot(kr[u], qr, 0.f);
+      w[u] = Elem<T>::dot(vr[u], gr, 0.f);
     }
     for (int o = 1; o < lph; o <<= 1) {
 #pragma unroll
@@ -459,23 +433,21 @@ __device__ __forceinline__ void dq_segment(const T* __restrict__ k, const T* __r
       }
     }
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) Elem<T>::pin(kr[u]);
-#pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       if (!ok[u]) continue;
       const int64_t e = e0 + u;
-      const float apre = d[u];
+      const float apre = d[u] * sh.inv_scale;
       float a = fminf(fmaxf(apre, -kClamp), kClamp);
       if (bias) a += bias[e * sh.H + g.head];
-      const float p = expf(a);
+      const float p = __expf(a);   // a is clamped to [-5, 5] (+ bias): exp2-based form is within 2 ulp
       const float f = factor ? factor[e * sh.H + g.head] : 1.f;
-      const float gb = (f * (w[u] / rg.dprime) + gz) * p;
+      const float gb = fmaf(f * w[u], inv_dprime, gz) * p;
       if (dbias && g.lead) dbias[e * sh.H + g.head] = gb;
-      const float ga = (apre >= -kClamp && apre <= kClamp) ? gb : 0.f;
+      const float gs = (apre >= -kClamp && apre <= kClamp) ? gb * sh.inv_scale : 0.f;
       float kk[V];
       Elem<T>::unpack(kr[u], kk);
 #pragma unroll
-      for (int i = 0; i < V; ++i) dq[i] += (ga * kk[i]) * sh.inv_scale;
+      for (int i = 0; i < V; ++i) dq[i] = fmaf(gs, kk[i], dq[i]);
     }
   }
 }
@@ -491,18 +463,19 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_q_kernel(
     int64_t n_q, Shape sh, int chunk) {
   constexpr int V = Elem<T>::kPerVec;
   const GroupPos g = group_pos<T>(sh);
-  float qv[V], gv[V], acc[V];
+  float acc[V];
 #pragma unroll
   for (int i = 0; i < V; ++i) acc[i] = 0.f;
+  typename Elem<T>::Raw gr;
   if (int(blockIdx.x) < n_items) {
     extern __shared__ float lds[];
     const ItemRange r = item_group_range(it, sh, blockIdx.x);
     float unused[V];
 #pragma unroll
     for (int i = 0; i < V; ++i) unused[i] = 0.f;
-    load_row<T, V>(q, r.row, sh.D, g, qv);
-    const RowGrad rg = row_grad<T>(out, dout, Z, r.row, sh, g, gv);
-    dq_segment<T>(k, v, kv, bias, factor, dbias, r.beg, r.end, sh, g, rg, qv, gv, acc);
+    const typename Elem<T>::Raw qr = load_row_raw(q, r.row, sh.D, g);
+    const RowGrad rg = row_grad<T>(out, dout, Z, r.row, sh, g, gr);
+    dq_segment<T>(k, v, kv, bias, factor, dbias, r.beg, r.end, sh, g, rg, qr, gr, acc);
     float z = 0.f;
     block_combine<V>(lds, it.stride, sh, g, acc, unused, false, z, false);
     if (r.single) {
@@ -517,9 +490,9 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_q_kernel(
   if (row >= n_q) return;
   const int64_t beg = qptr[row], end = qptr[row + 1];
   if (end - beg > chunk) return;
-  load_row<T, V>(q, row, sh.D, g, qv);
-  const RowGrad rg = row_grad<T>(out, dout, Z, row, sh, g, gv);
-  dq_segment<T>(k, v, kv, bias, factor, dbias, beg, end, sh, g, rg, qv, gv, acc);
+  const typename Elem<T>::Raw qr = load_row_raw(q, row, sh.D, g);
+  const RowGrad rg = row_grad<T>(out, dout, Z, row, sh, g, gr);
+  dq_segment<T>(k, v, kv, bias, factor, dbias, beg, end, sh, g, rg, qr, gr, acc);
   if (g.act) {
     Elem<T>::store(dq + row * sh.D + g.col0, acc);
     if (g.lead) store_row_stat(rstat, row, sh, g, rg);
@@ -535,8 +508,8 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
                                             const float* __restrict__ factor,
                                             const float2* __restrict__ rstat, int64_t beg,
                                             int64_t end, const Shape& sh, const GroupPos& g,
-                                            const float (&kk)[Elem<T>::kPerVec],
-                                            const float (&vv)[Elem<T>::kPerVec],
+                                            const typename Elem<T>::Raw& krow,
+                                            const typename Elem<T>::Raw& vrow,
                                             float (&dk)[Elem<T>::kPerVec],
                                             float (&dv)[Elem<T>::kPerVec]) {
   constexpr int V = Elem<T>::kPerVec;
@@ -567,17 +540,8 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
     float d[kUnroll], w[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      float qq[V], gg[V];
-      Elem<T>::unpack(qr[u], qq);
-      Elem<T>::unpack(gr[u], gg);
-      float a = 0.f, r = 0.f;
-#pragma unroll
-      for (int i = 0; i < V; ++i) {
-        a += (kk[i] * qq[i]) * sh.inv_scale;
-        r += gg[i] * vv[i];
-      }
-      d[u] = a;
-      w[u] = r;
+      d[u] = Elem<T>::dot(qr[u], krow, 0.f);
+      w[u] = Elem<T>::dot(gr[u], vrow, 0.f);
     }
     for (int o = 1; o < lph; o <<= 1) {
 #pragma unroll
@@ -588,28 +552,23 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      Elem<T>::pin(qr[u]);
-      Elem<T>::pin(gr[u]);
-    }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
       if (!ok[u]) continue;
       const int64_t e = need_e ? int64_t(ke[i0 + u]) : 0;
-      const float apre = d[u];
+      const float apre = d[u] * sh.inv_scale;
       float a = fminf(fmaxf(apre, -kClamp), kClamp);
       if (bias) a += bias[e * sh.H + g.head];
-      const float p = expf(a);
+      const float p = __expf(a);   // a is clamped to [-5, 5] (+ bias): exp2-based form is within 2 ulp
       const float f = factor ? factor[e * sh.H + g.head] : 1.f;
-      const float gb = (f * w[u] * rs[u].x - rs[u].y) * p;     // rs = {1/D', Delta/D'}
-      const float ga = (apre >= -kClamp && apre <= kClamp) ? gb : 0.f;
+      const float gb = fmaf(f * w[u], rs[u].x, -rs[u].y) * p;   // rs = {1/D', Delta/D'}
+      const float gs = (apre >= -kClamp && apre <= kClamp) ? gb * sh.inv_scale : 0.f;
       const float pf = p * f * rs[u].x;
       float qq[V], gg[V];
       Elem<T>::unpack(qr[u], qq);
       Elem<T>::unpack(gr[u], gg);
 #pragma unroll
       for (int i = 0; i < V; ++i) {
-        dv[i] += pf * gg[i];
-        dk[i] += (ga * qq[i]) * sh.inv_scale;
+        dv[i] = fmaf(pf, gg[i], dv[i]);
+        dk[i] = fmaf(gs, qq[i], dk[i]);
       }
     }
   }
@@ -642,10 +601,8 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
   if (b < q_heavy + k_items) {
     const int64_t item = b - q_heavy;
     const ItemRange r = item_group_range(kit, sh, item);
-    float kk[V], vv[V];
-    load_row<T, V>(k, r.row, sh.D, g, kk);
-    load_row<T, V>(v, r.row, sh.D, g, vv);
-    dkv_segment<T>(q, dout, kq, ke, bias, factor, rstat, r.beg, r.end, sh, g, kk, vv, ak, av);
+    const typename Elem<T>::Raw kr = load_row_raw(k, r.row, sh.D, g), vr = load_row_raw(v, r.row, sh.D, g);
+    dkv_segment<T>(q, dout, kq, ke, bias, factor, rstat, r.beg, r.end, sh, g, kr, vr, ak, av);
     float z = 0.f;
     block_combine<V>(lds, kit.stride, sh, g, ak, av, true, z, false);
     if (r.single) {
@@ -670,10 +627,8 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
     }
     return;
   }
-  float kk[V], vv[V];
-  load_row<T, V>(k, row, sh.D, g, kk);
-  load_row<T, V>(v, row, sh.D, g, vv);
-  dkv_segment<T>(q, dout, kq, ke, bias, factor, rstat, beg, end, sh, g, kk, vv, ak, av);
+  const typename Elem<T>::Raw kr = load_row_raw(k, row, sh.D, g), vr = load_row_raw(v, row, sh.D, g);
+  dkv_segment<T>(q, dout, kq, ke, bias, factor, rstat, beg, end, sh, g, kr, vr, ak, av);
   if (g.act) {
     Elem<T>::store(dk + row * sh.D + g.col0, ak);
     Elem<T>::store(dv + row * sh.D + g.col0, av);

@@ -84,7 +84,13 @@ template <> struct Elem<float> {
   __device__ __forceinline__ static void unpack(const Raw& v, float (&o)[4]) {
     o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
   }
-  __device__ __forceinline__ static void pin(Raw&) {}   // fp32: unpacking is free, nothing to re-derive
+  // acc + sum of the four products of a and b, in element order
+  __device__ __forceinline__ static float dot(const Raw& a, const Raw& b, float acc) {
+    acc = fmaf(a.x, b.x, acc);
+    acc = fmaf(a.y, b.y, acc);
+    acc = fmaf(a.z, b.z, acc);
+    return fmaf(a.w, b.w, acc);
+  }
   __device__ __forceinline__ static void load(const float* p, float (&o)[4]) {
     const float4 v = *reinterpret_cast<const float4*>(p);
     o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
@@ -97,12 +103,18 @@ template <> struct Elem<float> {
 template <> struct Elem<uint16_t> {
   static constexpr int kPerVec = 8;
   using Raw = uint4;
+  typedef __bf16 Pair __attribute__((ext_vector_type(2)));
+  __device__ __forceinline__ static Pair as_pair(uint32_t w) { return __builtin_bit_cast(Pair, w); }
   __device__ __forceinline__ static Raw load_raw(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
   __device__ __forceinline__ static Raw zero_raw() { return make_uint4(0u, 0u, 0u, 0u); }
-  // Optimisation barrier: values unpacked from `v` before this point are not
-  // reused after it, so a second use re-unpacks (two ALU ops per pair) instead
-  // of holding eight floats live per gathered row.
-  __device__ __forceinline__ static void pin(Raw& v) { asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w)); }
+  // acc + sum of the eight products of a and b, straight from the packed pairs
+  // (v_dot2 with an fp32 accumulator; bf16 products are exact in fp32)
+  __device__ __forceinline__ static float dot(const Raw& a, const Raw& b, float acc) {
+    acc = __builtin_amdgcn_fdot2_f32_bf16(as_pair(a.x), as_pair(b.x), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(as_pair(a.y), as_pair(b.y), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(as_pair(a.z), as_pair(b.z), acc, false);
+    return __builtin_amdgcn_fdot2_f32_bf16(as_pair(a.w), as_pair(b.w), acc, false);
+  }
   __device__ __forceinline__ static void unpack(const Raw& v, float (&o)[8]) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
