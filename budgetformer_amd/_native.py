@@ -60,6 +60,12 @@ _SIGS = {
     "bf_rw_select": (C.c_int, [P_i64, P_i32, i64, i64, i64, i32, i32, i32, i64, P_f32, u64, u64, P_i32, P_i32, vp]),
     "bf_real_select_merge": (C.c_int, [P_i64, P_i32, i64, i64, i64, i32, i64, P_i32, P_i32, i32, i32, P_i32, i32,
                                        P_i32, P_i32, i64, i64, P_i32, P_i32, vp]),
+    "bf_rw_select_rows": (C.c_int, [P_i64, P_i32, i64, P_i32, i64, i32, i32, i32, i64, P_f32, u64, u64, P_i64, P_i32,
+                                    P_i32, P_i32, vp]),
+    "bf_real_select_rows": (C.c_int, [P_i64, P_i32, i64, P_i32, i64, i32, i64, P_i32, i64, i64, P_i32, P_i32, P_i32,
+                                      P_i32, vp]),
+    "bf_assemble_rows": (C.c_int, [P_i32, P_i32, i32, i32, P_i32, P_i32, i32, i32, i32, i64, P_i32, i32, P_i32, vp]),
+    "bf_mark_in_neighbors": (C.c_int, [P_i64, P_i32, i64, vp, vp, vp]),
     "bf_build_edge_table_workspace_size": (C.c_int, [i64, i32, i64, i32, C.POINTER(sz)]),
     "bf_build_edge_table": (C.c_int, [P_i64, P_i32, P_i64, P_i32, i64, i64, i64, i64, i32, i32, i32, i32, i64,
                                       P_f32, u64, u64, P_i32, i64, i64, P_i32, P_i32, vp, sz, vp]),

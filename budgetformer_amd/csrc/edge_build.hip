@@ -81,11 +81,34 @@ __global__ __launch_bounds__(kThreads) void random_walk_starts_kernel(
   }
 }
 
+// Query of table row qi: the explicit id list when given (dst-filtered builds),
+// else the contiguous range starting at q_lo. -1 marks an id outside the graph.
+__device__ __forceinline__ int64_t row_query(const int32_t* __restrict__ qids, int64_t q_lo, int64_t qi,
+                                             int64_t num_nodes) {
+  if (!qids) return q_lo + qi;
+  const int64_t q = qids[qi];
+  return (q >= 0 && q < num_nodes) ? q : -1;
+}
+
+// Whether x occurs in the ascending list a[lo, hi).
+__device__ __forceinline__ bool sorted_contains(const int32_t* __restrict__ a, int64_t lo, int64_t hi, int32_t x) {
+  const int64_t end = hi;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (a[mid] < x) lo = mid + 1; else hi = mid;
+  }
+  return lo < end && a[lo] == x;
+}
+
 // One lane per walk; the P lanes of a query are adjacent. Candidates are staged
 // in LDS as (key << 32 | kv) (kNone = filtered step) and ranked by the P lanes.
+// With sub_ptr/sub_src (an in-neighbour CSR with ascending rows) a candidate kv
+// that is already a graph edge kv -> q is dropped: the probe pools' RW-minus-real
+// subtraction (utils/fullgraph_sp_support.py:1797-1812, 1536-1551).
 __global__ __launch_bounds__(kThreads) void rw_select_kernel(
-    const int64_t* __restrict__ rowptr, const int32_t* __restrict__ col, int64_t q_lo, int64_t n_q,
-    int P, int L, int K, uint32_t kc, const float* __restrict__ u, uint64_t seed, uint64_t offset,
+    const int64_t* __restrict__ rowptr, const int32_t* __restrict__ col, int64_t num_nodes, int64_t q_lo,
+    const int32_t* __restrict__ qids, int64_t n_q, int P, int L, int K, uint32_t kc, const float* __restrict__ u,
+    uint64_t seed, uint64_t offset, const int64_t* __restrict__ sub_ptr, const int32_t* __restrict__ sub_src,
     int32_t* __restrict__ sel_kv, int32_t* __restrict__ sel_cnt) {
   extern __shared__ uint64_t cand[];  // [kThreads * L]
   const int qpb = kThreads / P;
@@ -95,14 +118,19 @@ __global__ __launch_bounds__(kThreads) void rw_select_kernel(
   const int64_t qi = int64_t(blockIdx.x) * qpb + ql;
   const bool active = ql < qpb && qi < n_q;
   if (active) {
-    const int64_t q = q_lo + qi;
+    const int64_t q = row_query(qids, q_lo, qi, num_nodes);
     const int64_t w = q * P + p;
     const int64_t wl = qi * P + p;
     int64_t cur = q;
     for (int l = 0; l < L; ++l) {
+      if (q < 0) {
+        cand[tid * L + l] = kNone;
+        continue;
+      }
       const float uu = u ? u[wl * L + l] : walk_uniform(seed, offset, uint64_t(w), l);
       const int64_t nxt = walk_step(rowptr, col, cur, uu);
-      const bool keep = (l == 0) || (nxt != cur);
+      bool keep = (l == 0) || (nxt != cur);
+      if (keep && sub_ptr) keep = !sorted_contains(sub_src, sub_ptr[q], sub_ptr[q + 1], int32_t(nxt));
       cand[tid * L + l] = keep ? (uint64_t(edge_key(uint32_t(nxt), uint32_t(q), kc)) << 32) | uint32_t(nxt) : kNone;
       cur = nxt;
     }
@@ -204,23 +232,62 @@ __global__ __launch_bounds__(kThreads) void real_select_hub_kernel(
   if (threadIdx.x == 0) hub_cnt[h] = cnt;
 }
 
+// Writes one table row from the LDS list lst[0, n_tot): with dedup the set of
+// values ascending (first occurrence wins), without it the multiset ascending
+// (stable), or with key_order the list as it stands (the selection order, i.e.
+// ascending key). Every thread of the block calls it (it holds a barrier).
+__device__ __forceinline__ void write_row(int32_t (*lst)[kMaxRow], int32_t (*dupf)[kMaxRow], int gq, int gl,
+                                          bool active, int n_tot, int dedup, int key_order, int32_t* __restrict__ out,
+                                          int width, int32_t* __restrict__ len_out) {
+  if (active && dedup) {
+    for (int i = gl; i < n_tot; i += kGroup) {
+      const int32_t v = lst[gq][i];
+      int dup = 0;
+      for (int j = 0; j < i; ++j) dup |= lst[gq][j] == v;
+      dupf[gq][i] = dup;
+    }
+  }
+  __syncthreads();
+  if (!active) return;
+  int len = 0;
+  for (int i = 0; i < n_tot; ++i) len += dedup ? !dupf[gq][i] : 1;
+  for (int i = gl; i < n_tot; i += kGroup) {
+    const int32_t v = lst[gq][i];
+    int rank = 0;
+    if (dedup) {
+      if (dupf[gq][i]) continue;
+      for (int j = 0; j < n_tot; ++j) rank += !dupf[gq][j] && lst[gq][j] < v;
+    } else if (key_order) {
+      rank = i;
+    } else {
+      for (int j = 0; j < n_tot; ++j) {
+        const int32_t w = lst[gq][j];
+        rank += (w < v) || (w == v && j < i);
+      }
+    }
+    out[rank] = v;
+  }
+  for (int c = len + gl; c < width; c += kGroup) out[c] = -1;
+  if (gl == 0) *len_out = len;
+}
+
 template <int KMAX>
 __global__ __launch_bounds__(kThreads) void real_select_merge_kernel(
-    const int64_t* __restrict__ in_ptr, const int32_t* __restrict__ in_src, int64_t q_lo, int64_t n_q,
-    int k_real, uint32_t kc, const int32_t* __restrict__ rw_kv, const int32_t* __restrict__ rw_cnt, int k_rw,
-    int dedup, int32_t* __restrict__ table, int width, int32_t* __restrict__ row_len,
-    const int32_t* __restrict__ hubs, const int32_t* __restrict__ hub_sel, const int32_t* __restrict__ hub_cnt,
-    int64_t n_hubs, int64_t hub_threshold) {
+    const int64_t* __restrict__ in_ptr, const int32_t* __restrict__ in_src, int64_t num_nodes, int64_t q_lo,
+    const int32_t* __restrict__ qids, int64_t n_q, int k_real, uint32_t kc, const int32_t* __restrict__ rw_kv,
+    const int32_t* __restrict__ rw_cnt, int k_rw, int dedup, int key_order, int32_t* __restrict__ table, int width,
+    int32_t* __restrict__ row_len, const int32_t* __restrict__ hubs, const int32_t* __restrict__ hub_sel,
+    const int32_t* __restrict__ hub_cnt, int64_t n_hubs, int64_t hub_threshold) {
   __shared__ int32_t lst[kQPB][kMaxRow];
   __shared__ int32_t dupf[kQPB][kMaxRow];
   const int gq = threadIdx.x / kGroup;
   const int gl = threadIdx.x % kGroup;
   const int64_t qi = int64_t(blockIdx.x) * kQPB + gq;
   const bool active = qi < n_q;
+  const int64_t q = active ? row_query(qids, q_lo, qi, num_nodes) : -1;
   int n_r = 0, n_w = 0;
   int64_t hub = -1;
-  if (active && k_real > 0 && n_hubs > 0) {
-    const int64_t q = q_lo + qi;
+  if (q >= 0 && k_real > 0 && n_hubs > 0) {
     if (in_ptr[q + 1] - in_ptr[q] > hub_threshold) {   // selection precomputed by real_select_hub_kernel
       int64_t lo = 0, hi = n_hubs;
       while (lo < hi) {
@@ -233,8 +300,7 @@ __global__ __launch_bounds__(kThreads) void real_select_merge_kernel(
   if (hub >= 0) {
     n_r = hub_cnt[hub];
     for (int i = gl; i < n_r; i += kGroup) lst[gq][i] = hub_sel[hub * k_real + i];
-  } else if (active && k_real > 0) {
-    const int64_t q = q_lo + qi;
+  } else if (q >= 0 && k_real > 0) {
     uint64_t lk[KMAX];
 #pragma unroll
     for (int j = 0; j < KMAX; ++j) lk[j] = kNone;
@@ -275,36 +341,50 @@ __global__ __launch_bounds__(kThreads) void real_select_merge_kernel(
     for (int i = gl; i < n_w; i += kGroup) lst[gq][n_r + i] = rw_kv[qi * k_rw + i];
   }
   __syncthreads();
-  const int n_tot = n_r + n_w;
-  if (active && dedup) {
-    for (int i = gl; i < n_tot; i += kGroup) {
-      const int32_t v = lst[gq][i];
-      int dup = 0;
-      for (int j = 0; j < i; ++j) dup |= lst[gq][j] == v;
-      dupf[gq][i] = dup;
-    }
+  write_row(lst, dupf, gq, gl, active, n_r + n_w, dedup, key_order, table + (active ? qi : 0) * width, width,
+            row_len + (active ? qi : 0));
+}
+
+// One candidate of a nested budget probe: per row the first b_r entries of a
+// key-ordered real selection and the first b_w of a key-ordered RW selection
+// (both from one ranking, so every candidate budget is a prefix), merged as the
+// full build merges them (utils/fullgraph_sp_support.py:1824-1879).
+__global__ __launch_bounds__(kThreads) void assemble_rows_kernel(
+    const int32_t* __restrict__ real_kv, const int32_t* __restrict__ real_cnt, int real_stride, int b_r,
+    const int32_t* __restrict__ rw_kv, const int32_t* __restrict__ rw_cnt, int rw_stride, int b_w, int dedup,
+    int64_t n, int32_t* __restrict__ table, int width, int32_t* __restrict__ row_len) {
+  __shared__ int32_t lst[kQPB][kMaxRow];
+  __shared__ int32_t dupf[kQPB][kMaxRow];
+  const int gq = threadIdx.x / kGroup;
+  const int gl = threadIdx.x % kGroup;
+  const int64_t qi = int64_t(blockIdx.x) * kQPB + gq;
+  const bool active = qi < n;
+  int n_r = 0, n_w = 0;
+  if (active) {
+    if (real_kv && b_r > 0) n_r = min(real_cnt[qi], b_r);
+    if (rw_kv && b_w > 0) n_w = min(rw_cnt[qi], b_w);
+    for (int i = gl; i < n_r; i += kGroup) lst[gq][i] = real_kv[qi * real_stride + i];
+    for (int i = gl; i < n_w; i += kGroup) lst[gq][n_r + i] = rw_kv[qi * rw_stride + i];
   }
   __syncthreads();
-  if (!active) return;
-  int len = 0;
-  int32_t* out = table + qi * width;
-  for (int i = 0; i < n_tot; ++i) len += dedup ? !dupf[gq][i] : 1;
-  for (int i = gl; i < n_tot; i += kGroup) {
-    const int32_t v = lst[gq][i];
-    int rank = 0;
-    if (dedup) {
-      if (dupf[gq][i]) continue;
-      for (int j = 0; j < n_tot; ++j) rank += !dupf[gq][j] && lst[gq][j] < v;
-    } else {
-      for (int j = 0; j < n_tot; ++j) {
-        const int32_t w = lst[gq][j];
-        rank += (w < v) || (w == v && j < i);
-      }
-    }
-    out[rank] = v;
+  write_row(lst, dupf, gq, gl, active, n_r + n_w, dedup, 0, table + (active ? qi : 0) * width, width,
+            row_len + (active ? qi : 0));
+}
+
+// One BFS layer of the probe's reception cone (utils/fullgraph_sp_support.py:
+// 2261-2309): reached[s] = 1 for every edge s -> v with frontier[v] set. A
+// 16-lane group walks v's in-neighbour row; concurrent stores all write 1.
+__global__ __launch_bounds__(kThreads) void mark_in_neighbors_kernel(
+    const int64_t* __restrict__ in_ptr, const int32_t* __restrict__ in_src, int64_t num_nodes,
+    const uint8_t* __restrict__ frontier, uint8_t* __restrict__ reached) {
+  const int64_t v = int64_t(blockIdx.x) * kQPB + threadIdx.x / kGroup;
+  const int gl = threadIdx.x % kGroup;
+  if (v >= num_nodes || !frontier[v]) return;
+  const int64_t beg = in_ptr[v], end = in_ptr[v + 1];
+  for (int64_t i = beg + gl; i < end; i += kGroup) {
+    const int32_t src = in_src[i];
+    if (src >= 0 && src < num_nodes) reached[src] = 1;
   }
-  for (int c = len + gl; c < width; c += kGroup) out[c] = -1;
-  if (gl == 0) row_len[qi] = len;
 }
 
 int check_graph(const int64_t* ptr, const int32_t* idx, int64_t num_nodes, int64_t q_lo, int64_t n_q) {
@@ -317,22 +397,24 @@ int check_graph(const int64_t* ptr, const int32_t* idx, int64_t num_nodes, int64
   return BF_OK;
 }
 
-int launch_rw_select(const int64_t* rowptr, const int32_t* col, int64_t q_lo, int64_t n_q, int P, int L, int K,
-                     uint32_t kc, const float* u, uint64_t seed, uint64_t offset, int32_t* sel_kv,
-                     int32_t* sel_cnt, hipStream_t st) {
+int launch_rw_select(const int64_t* rowptr, const int32_t* col, int64_t num_nodes, int64_t q_lo,
+                     const int32_t* qids, int64_t n_q, int P, int L, int K, uint32_t kc, const float* u,
+                     uint64_t seed, uint64_t offset, const int64_t* sub_ptr, const int32_t* sub_src,
+                     int32_t* sel_kv, int32_t* sel_cnt, hipStream_t st) {
   if (n_q == 0) return BF_OK;
   const int qpb = kThreads / P;
   const size_t lds = size_t(kThreads) * L * sizeof(uint64_t);
   BF_LAUNCH("rw_select_kernel", rw_select_kernel, dim3(unsigned(ceil_div(n_q, qpb))), dim3(kThreads), lds, st, rowptr, col,
-                     q_lo, n_q, P, L, K, kc, u, seed, offset, sel_kv, sel_cnt);
+            num_nodes, q_lo, qids, n_q, P, L, K, kc, u, seed, offset, sub_ptr, sub_src, sel_kv, sel_cnt);
   BF_CHECK_LAUNCH();
   return BF_OK;
 }
 
-int launch_real_merge(const int64_t* in_ptr, const int32_t* in_src, int64_t q_lo, int64_t n_q, int k_real,
-                      uint32_t kc, const int32_t* rw_kv, const int32_t* rw_cnt, int k_rw, int dedup,
-                      int32_t* table, int width, int32_t* row_len, const int32_t* hubs, int64_t n_hubs,
-                      int64_t hub_threshold, int32_t* hub_sel, int32_t* hub_cnt, hipStream_t st) {
+int launch_real_merge(const int64_t* in_ptr, const int32_t* in_src, int64_t num_nodes, int64_t q_lo,
+                      const int32_t* qids, int64_t n_q, int k_real, uint32_t kc, const int32_t* rw_kv,
+                      const int32_t* rw_cnt, int k_rw, int dedup, int key_order, int32_t* table, int width,
+                      int32_t* row_len, const int32_t* hubs, int64_t n_hubs, int64_t hub_threshold,
+                      int32_t* hub_sel, int32_t* hub_cnt, hipStream_t st) {
   if (n_q == 0) return BF_OK;
   if (k_real <= 0) n_hubs = 0;
   if (n_hubs > 0) {
@@ -353,8 +435,8 @@ int launch_real_merge(const int64_t* in_ptr, const int32_t* in_src, int64_t q_lo
   const dim3 grid(unsigned(ceil_div(n_q, kQPB)));
 #define BF_LAUNCH_MERGE(KM)                                                                                      \
   BF_LAUNCH("real_select_merge_kernel", real_select_merge_kernel<KM>, grid, dim3(kThreads), 0, st, in_ptr, in_src, \
-            q_lo, n_q, k_real, kc, rw_kv, rw_cnt, k_rw, dedup, table, width, row_len, hubs, hub_sel, hub_cnt,    \
-            n_hubs, hub_threshold)
+            num_nodes, q_lo, qids, n_q, k_real, kc, rw_kv, rw_cnt, k_rw, dedup, key_order, table, width, row_len,   \
+            hubs, hub_sel, hub_cnt, n_hubs, hub_threshold)
   if (k_real <= 4)
     BF_LAUNCH_MERGE(4);
   else if (k_real <= 8)
@@ -433,8 +515,29 @@ extern "C" int bf_rw_select(const int64_t* rowptr, const int32_t* col, int64_t n
   BF_CHECK_ARG(walks_per_node * walk_length <= 64, "rw_select: P*L=%d exceeds 64", walks_per_node * walk_length);
   BF_CHECK_ARG(k_rw >= 1 && k_rw <= 32, "rw_select: k_rw %d outside [1,32]", k_rw);
   BF_CHECK_ARG((sel_kv && sel_cnt) || n_q == 0, "rw_select: null output");
-  return launch_rw_select(rowptr, col, q_lo, n_q, walks_per_node, walk_length, k_rw, key_const(key_seed), u,
-                          philox_seed, philox_offset, sel_kv, sel_cnt, as_stream(stream));
+  return launch_rw_select(rowptr, col, num_nodes, q_lo, nullptr, n_q, walks_per_node, walk_length, k_rw,
+                          key_const(key_seed), u, philox_seed, philox_offset, nullptr, nullptr, sel_kv, sel_cnt,
+                          as_stream(stream));
+}
+
+extern "C" int bf_rw_select_rows(const int64_t* rowptr, const int32_t* col, int64_t num_nodes, const int32_t* qids,
+                                 int64_t n_q, int32_t walks_per_node, int32_t walk_length, int32_t k_rw,
+                                 int64_t key_seed, const float* u, uint64_t philox_seed, uint64_t philox_offset,
+                                 const int64_t* sub_ptr, const int32_t* sub_src, int32_t* sel_kv, int32_t* sel_cnt,
+                                 void* stream) {
+  int rc = check_graph(rowptr, col, num_nodes, 0, 0);
+  if (rc) return rc;
+  BF_CHECK_ARG(n_q >= 0 && (qids || n_q == 0), "rw_select_rows: query id list is NULL");
+  BF_CHECK_ARG(walks_per_node >= 1 && walks_per_node <= kThreads, "rw_select_rows: walks_per_node %d outside [1,%d]",
+               walks_per_node, kThreads);
+  BF_CHECK_ARG(walk_length >= 1 && walk_length <= 32, "rw_select_rows: walk_length %d outside [1,32]", walk_length);
+  BF_CHECK_ARG(walks_per_node * walk_length <= 64, "rw_select_rows: P*L=%d exceeds 64", walks_per_node * walk_length);
+  BF_CHECK_ARG(k_rw >= 1 && k_rw <= 32, "rw_select_rows: k_rw %d outside [1,32]", k_rw);
+  BF_CHECK_ARG((sub_ptr == nullptr) == (sub_src == nullptr), "rw_select_rows: sub_ptr and sub_src go together");
+  BF_CHECK_ARG((sel_kv && sel_cnt) || n_q == 0, "rw_select_rows: null output");
+  return launch_rw_select(rowptr, col, num_nodes, 0, qids, n_q, walks_per_node, walk_length, k_rw,
+                          key_const(key_seed), u, philox_seed, philox_offset, sub_ptr, sub_src, sel_kv, sel_cnt,
+                          as_stream(stream));
 }
 
 extern "C" int bf_real_select_merge(const int64_t* in_ptr, const int32_t* in_src, int64_t num_nodes, int64_t q_lo,
@@ -455,9 +558,50 @@ extern "C" int bf_real_select_merge(const int64_t* in_ptr, const int32_t* in_src
   BF_CHECK_ARG(n_hubs >= 0 && n_hubs < (int64_t(1) << 31), "real_select_merge: bad hub count");
   BF_CHECK_ARG(n_hubs == 0 || (hubs && hub_sel && hub_cnt && hub_threshold >= 0),
                "real_select_merge: hub arrays missing");
-  return launch_real_merge(in_ptr, in_src, q_lo, n_q, k_real, key_const(key_seed), k_rw ? rw_kv : nullptr, rw_cnt,
-                           k_rw, dedup ? 1 : 0, table, width, row_len, hubs, n_hubs, hub_threshold, hub_sel,
-                           hub_cnt, as_stream(stream));
+  return launch_real_merge(in_ptr, in_src, num_nodes, q_lo, nullptr, n_q, k_real, key_const(key_seed),
+                           k_rw ? rw_kv : nullptr, rw_cnt, k_rw, dedup ? 1 : 0, 0, table, width, row_len, hubs, n_hubs,
+                           hub_threshold, hub_sel, hub_cnt, as_stream(stream));
+}
+
+extern "C" int bf_real_select_rows(const int64_t* in_ptr, const int32_t* in_src, int64_t num_nodes,
+                                   const int32_t* qids, int64_t n_q, int32_t k_real, int64_t key_seed,
+                                   const int32_t* hubs, int64_t n_hubs, int64_t hub_threshold, int32_t* hub_sel,
+                                   int32_t* hub_cnt, int32_t* sel_kv, int32_t* sel_cnt, void* stream) {
+  int rc = check_graph(in_ptr, in_src, num_nodes, 0, 0);
+  if (rc) return rc;
+  BF_CHECK_ARG(n_q >= 0 && (qids || n_q == 0), "real_select_rows: query id list is NULL");
+  BF_CHECK_ARG(k_real >= 1 && k_real <= 32, "real_select_rows: k_real %d outside [1,32]", k_real);
+  BF_CHECK_ARG((sel_kv && sel_cnt) || n_q == 0, "real_select_rows: null output");
+  BF_CHECK_ARG(n_hubs >= 0 && n_hubs < (int64_t(1) << 31), "real_select_rows: bad hub count");
+  BF_CHECK_ARG(n_hubs == 0 || (hubs && hub_sel && hub_cnt && hub_threshold >= 0),
+               "real_select_rows: hub arrays missing");
+  return launch_real_merge(in_ptr, in_src, num_nodes, 0, qids, n_q, k_real, key_const(key_seed), nullptr, nullptr, 0,
+                           0, 1, sel_kv, k_real, sel_cnt, hubs, n_hubs, hub_threshold, hub_sel, hub_cnt,
+                           as_stream(stream));
+}
+
+extern "C" int bf_assemble_rows(const int32_t* real_kv, const int32_t* real_cnt, int32_t real_stride, int32_t b_real,
+                                const int32_t* rw_kv, const int32_t* rw_cnt, int32_t rw_stride, int32_t b_rw,
+                                int32_t dedup, int64_t n_rows, int32_t* table, int32_t width, int32_t* row_len,
+                                void* stream) {
+  BF_CHECK_ARG(n_rows >= 0, "assemble_rows: n_rows < 0");
+  if (real_kv == nullptr) b_real = 0;
+  if (rw_kv == nullptr) b_rw = 0;
+  BF_CHECK_ARG(b_real >= 0 && b_rw >= 0, "assemble_rows: negative budget");
+  BF_CHECK_ARG(b_real <= real_stride || real_kv == nullptr, "assemble_rows: b_real %d exceeds the real stride %d",
+               b_real, real_stride);
+  BF_CHECK_ARG(b_rw <= rw_stride || rw_kv == nullptr, "assemble_rows: b_rw %d exceeds the RW stride %d", b_rw,
+               rw_stride);
+  BF_CHECK_ARG(b_real + b_rw <= kMaxRow, "assemble_rows: b_real + b_rw = %d exceeds %d", b_real + b_rw, kMaxRow);
+  BF_CHECK_ARG(width >= b_real + b_rw && width >= 1, "assemble_rows: width %d < %d", width, b_real + b_rw);
+  BF_CHECK_ARG((b_real == 0 || real_cnt) && (b_rw == 0 || rw_cnt), "assemble_rows: counts missing");
+  BF_CHECK_ARG((table && row_len) || n_rows == 0, "assemble_rows: null output");
+  if (n_rows == 0) return BF_OK;
+  BF_LAUNCH("assemble_rows_kernel", assemble_rows_kernel, dim3(unsigned(ceil_div(n_rows, kQPB))), dim3(kThreads), 0,
+            as_stream(stream), b_real ? real_kv : nullptr, real_cnt, real_stride, b_real, b_rw ? rw_kv : nullptr,
+            rw_cnt, rw_stride, b_rw, dedup ? 1 : 0, n_rows, table, width, row_len);
+  BF_CHECK_LAUNCH();
+  return BF_OK;
 }
 
 extern "C" int bf_build_edge_table_workspace_size(int64_t n_q, int32_t k_rw, int64_t n_hubs, int32_t k_real,
@@ -505,4 +649,16 @@ extern "C" int bf_build_edge_table(const int64_t* rowptr, const int32_t* col, co
                               use_rw ? sel_kv : nullptr, use_rw ? sel_cnt : nullptr, use_rw ? k_rw : 0,
                               (use_real && use_rw) ? 1 : 0, table, width, row_len, hubs, n_hubs, hub_threshold,
                               hub_sel, hub_cnt, st);
+}
+
+extern "C" int bf_mark_in_neighbors(const int64_t* in_ptr, const int32_t* in_src, int64_t num_nodes,
+                                    const uint8_t* frontier, uint8_t* reached, void* stream) {
+  int rc = check_graph(in_ptr, in_src, num_nodes, 0, 0);
+  if (rc) return rc;
+  if (num_nodes == 0) return BF_OK;
+  BF_CHECK_ARG(in_src && frontier && reached, "mark_in_neighbors: null tensor");
+  BF_LAUNCH("mark_in_neighbors_kernel", mark_in_neighbors_kernel, dim3(unsigned(ceil_div(num_nodes, kQPB))),
+            dim3(kThreads), 0, as_stream(stream), in_ptr, in_src, num_nodes, frontier, reached);
+  BF_CHECK_LAUNCH();
+  return BF_OK;
 }

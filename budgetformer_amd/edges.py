@@ -37,6 +37,7 @@ class EdgeTable:
     num_nodes: int
     q_lo: int = 0
     global_token: bool = False     # Graphormer virtual node applied when indexing
+    query_ids: Optional[torch.Tensor] = None   # int32 [n_q] ascending: row i serves query_ids[i] (filtered builds)
     _index: dict = field(default_factory=dict, repr=False)
 
     @property
@@ -50,6 +51,10 @@ class EdgeTable:
     def attention_index(self, chunk: int = hip_ops.DEFAULT_CHUNK, item: int = hip_ops.DEFAULT_ITEM) -> AttentionIndex:
         """CSR view for the attention kernels (cached per split setting)."""
         idx = self._index.get((chunk, item))
+        if idx is None and self.query_ids is not None:
+            n_kv = self.num_nodes + (1 if self.global_token else 0)
+            idx = AttentionIndex.from_coo(self.to_edge_index(), n_kv, n_kv, chunk=chunk, item=item)
+            self._index[(chunk, item)] = idx
         if idx is None:
             if self.q_lo != 0 or self.n_rows != self.num_nodes:
                 if self.global_token:
@@ -69,7 +74,9 @@ class EdgeTable:
         """
         base = AttentionIndex.from_table(self.table, self.row_len, False, n_kv=self.num_nodes)
         coo = base.to_coo()
-        if self.q_lo:
+        if self.query_ids is not None:
+            coo = torch.stack([coo[0], self.query_ids.to(torch.int64)[coo[1]]])
+        elif self.q_lo:
             coo = torch.stack([coo[0], coo[1] + self.q_lo])
         if not self.global_token:
             return coo

@@ -163,6 +163,104 @@ def real_select_merge(in_ptr, in_src, q_lo: int, n_q: int, k_real: int, key_seed
     return table, row_len
 
 
+def _check_qids(qids: torch.Tensor, num_nodes: int, dev) -> None:
+    _require(qids, "query_ids", torch.int32, dev)
+    if qids.dim() != 1:
+        raise ValueError("query_ids must be 1-D")
+    if qids.numel():
+        lo, hi = torch.aminmax(qids)
+        if int(lo) < 0 or int(hi) >= num_nodes:
+            raise ValueError(f"query_ids must lie in [0, {num_nodes}) (got [{int(lo)}, {int(hi)}])")
+
+
+def rw_select_rows(rowptr, col, qids: torch.Tensor, walks_per_node: int, walk_length: int, k_rw: int,
+                   key_seed: int, u=None, philox_seed: int = 0, philox_offset: int = 0, subtract=None):
+    """bf_rw_select for an explicit query list; ``subtract=(in_ptr, in_src)`` drops candidates that are
+    already graph edges into the query. Returns (sel_kv [n,k_rw] key order, sel_cnt [n])."""
+    dev = rowptr.device
+    _require(rowptr, "rowptr", torch.int64)
+    _require(col, "col", torch.int32, dev)
+    n_nodes = rowptr.numel() - 1
+    _check_qids(qids, n_nodes, dev)
+    n = qids.numel()
+    if u is not None:
+        _require(u, "u", torch.float32, dev)
+        if tuple(u.shape) != (n * walks_per_node, walk_length):
+            raise ValueError(f"u must be [{n * walks_per_node}, {walk_length}], got {tuple(u.shape)}")
+    sub_ptr = sub_src = None
+    if subtract is not None:
+        sub_ptr, sub_src = subtract
+        _require(sub_ptr, "subtract in_ptr", torch.int64, dev)
+        _require(sub_src, "subtract in_src", torch.int32, dev)
+        if sub_ptr.numel() != n_nodes + 1:
+            raise ValueError("subtract in_ptr must have num_nodes + 1 entries")
+    sel = torch.empty(n, k_rw, dtype=torch.int32, device=dev)
+    cnt = torch.empty(n, dtype=torch.int32, device=dev)
+    N.call("bf_rw_select_rows", _p(rowptr), _p(col), n_nodes, _p(qids), n, walks_per_node, walk_length, k_rw,
+           key_seed, _p(u), philox_seed & (2 ** 64 - 1), philox_offset & (2 ** 64 - 1), _p(sub_ptr), _p(sub_src),
+           _p(sel), _p(cnt), _stream(dev))
+    return sel, cnt
+
+
+def real_select_rows(in_ptr, in_src, qids: torch.Tensor, k_real: int, key_seed: int,
+                     hubs: Optional[torch.Tensor] = None, hub_threshold: int = HUB_THRESHOLD):
+    """Real-edge top-k_real in key order for an explicit query list: (sel_kv [n,k_real], sel_cnt [n])."""
+    dev = in_ptr.device
+    _require(in_ptr, "in_ptr", torch.int64)
+    _require(in_src, "in_src", torch.int32, dev)
+    _check_qids(qids, in_ptr.numel() - 1, dev)
+    n = qids.numel()
+    sel = torch.empty(n, k_real, dtype=torch.int32, device=dev)
+    cnt = torch.empty(n, dtype=torch.int32, device=dev)
+    n_hubs = 0 if hubs is None else hubs.numel()
+    if n_hubs:
+        _require(hubs, "hubs", torch.int32, dev)
+    hub_sel = torch.empty(max(n_hubs * k_real, 1), dtype=torch.int32, device=dev)
+    hub_cnt = torch.empty(max(n_hubs, 1), dtype=torch.int32, device=dev)
+    N.call("bf_real_select_rows", _p(in_ptr), _p(in_src), in_ptr.numel() - 1, _p(qids), n, k_real, key_seed,
+           _p(hubs) if n_hubs else None, n_hubs, hub_threshold, _p(hub_sel), _p(hub_cnt), _p(sel), _p(cnt),
+           _stream(dev))
+    return sel, cnt
+
+
+def assemble_rows(real=None, rw=None, b_real: int = 0, b_rw: int = 0, dedup: bool = True):
+    """One budget candidate from key-ordered selections ``real=(sel, cnt)`` / ``rw=(sel, cnt)``:
+    (table [n, b_real+b_rw], row_len [n])."""
+    parts = [x for x in (real, rw) if x is not None]
+    if not parts:
+        raise ValueError("assemble_rows needs at least one selection")
+    dev = parts[0][0].device
+    n = parts[0][0].shape[0]
+    for sel, cnt in parts:
+        _require(sel, "selection", torch.int32, dev)
+        _require(cnt, "selection counts", torch.int32, dev)
+        if sel.shape[0] != n or cnt.shape != (n,):
+            raise ValueError("selections must have the same row count")
+    b_real = b_real if real is not None else 0
+    b_rw = b_rw if rw is not None else 0
+    width = max(1, b_real + b_rw)
+    table = torch.empty(n, width, dtype=torch.int32, device=dev)
+    row_len = torch.empty(n, dtype=torch.int32, device=dev)
+    N.call("bf_assemble_rows", _p(real[0]) if real is not None else None, _p(real[1]) if real is not None else None,
+           real[0].shape[1] if real is not None else 0, b_real, _p(rw[0]) if rw is not None else None,
+           _p(rw[1]) if rw is not None else None, rw[0].shape[1] if rw is not None else 0, b_rw, int(bool(dedup)), n,
+           _p(table), width, _p(row_len), _stream(dev))
+    return table, row_len
+
+
+def mark_in_neighbors(in_ptr, in_src, frontier: torch.Tensor, reached: torch.Tensor) -> None:
+    """reached[s] = 1 for every edge s -> v with frontier[v] (uint8 masks over the nodes)."""
+    dev = in_ptr.device
+    _require(in_ptr, "in_ptr", torch.int64)
+    _require(in_src, "in_src", torch.int32, dev)
+    n = in_ptr.numel() - 1
+    for t, name in ((frontier, "frontier"), (reached, "reached")):
+        _require(t, name, torch.uint8, dev)
+        if t.numel() != n:
+            raise ValueError(f"{name} must have num_nodes = {n} entries")
+    N.call("bf_mark_in_neighbors", _p(in_ptr), _p(in_src), n, _p(frontier), _p(reached), _stream(dev))
+
+
 def build_edge_table(rowptr, col, in_ptr, in_src, num_edges: int, q_lo: int, n_q: int, walks_per_node: int,
                      walk_length: int, k_real: int, k_rw: int, edge_seed: int, u=None, philox_seed: int = 0,
                      philox_offset: int = 0, out=None, hubs: Optional[torch.Tensor] = None,

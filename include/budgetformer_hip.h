@@ -111,6 +111,23 @@ int bf_rw_select(const int64_t* rowptr, const int32_t* col, int64_t num_nodes,
                  int32_t k_rw, int64_t key_seed, const float* u, uint64_t philox_seed,
                  uint64_t philox_offset, int32_t* sel_kv, int32_t* sel_cnt, void* stream);
 
+/* bf_rw_select for an explicit query list (the Adaptive-Budget probe's
+ * dst-filtered build): row i serves query qids[i] (int32 [n_q], ids outside
+ * [0, num_nodes) give empty rows), its walks keep their global ids q*P+p, so
+ * each row equals the full build's row for that query. With sub_ptr/sub_src
+ * (an in-neighbour CSR, rows ascending) a candidate kv that is a graph edge
+ * kv -> q is removed before ranking: the probe pools' RW-minus-real
+ * subtraction. Replaces _build_probe_edge_pools' RW half
+ * (utils/fullgraph_sp_support.py:1743-1821: filter by dst :1520-1533,
+ * _subtract_edge_index :1536-1551) followed by the RW sampling of
+ * _assemble_edges_from_pools (:1824-1879, via :1262-1309). u, when given, is
+ * float32 [n_q*P, L] in row order.                                          */
+int bf_rw_select_rows(const int64_t* rowptr, const int32_t* col, int64_t num_nodes,
+                      const int32_t* qids, int64_t n_q, int32_t walks_per_node,
+                      int32_t walk_length, int32_t k_rw, int64_t key_seed, const float* u,
+                      uint64_t philox_seed, uint64_t philox_offset, const int64_t* sub_ptr,
+                      const int32_t* sub_src, int32_t* sel_kv, int32_t* sel_cnt, void* stream);
+
 /* Per-query top-k of the real (graph) edges merged with an RW selection into
  * the query-major table. Replaces _sample_edges_per_query_random(edge_index,
  * k_real, edge_seed+17) (utils/fullgraph_sp_support.py:1312-1491, 1195-1228)
@@ -133,6 +150,41 @@ int bf_real_select_merge(const int64_t* in_ptr, const int32_t* in_src, int64_t n
                          int32_t dedup, int32_t* table, int32_t width, int32_t* row_len,
                          const int32_t* hubs, int64_t n_hubs, int64_t hub_threshold,
                          int32_t* hub_sel, int32_t* hub_cnt, void* stream);
+
+/* Real-edge top-k_real for an explicit query list, in key order (so every
+ * smaller budget is a prefix: the probe's nested candidates). Replaces the
+ * probe's real pool (_filter_edge_index_by_dst / _filter_by_dst_csr,
+ * utils/fullgraph_sp_support.py:1520-1533, 1766-1777) sampled by
+ * _sample_edges_per_query_random(real_pool, k_real, edge_seed+17) in
+ * _assemble_edges_from_pools (:1824-1879, via :1262-1309).
+ *   qids int32 [n_q]; sel_kv int32 [n_q, k_real] (-1 padded), sel_cnt [n_q].
+ *   hubs: ascending query ids (a subset of qids) whose in-degree exceeds
+ *   hub_threshold, with hub_sel [n_hubs, k_real] / hub_cnt [n_hubs] scratch. */
+int bf_real_select_rows(const int64_t* in_ptr, const int32_t* in_src, int64_t num_nodes,
+                        const int32_t* qids, int64_t n_q, int32_t k_real, int64_t key_seed,
+                        const int32_t* hubs, int64_t n_hubs, int64_t hub_threshold,
+                        int32_t* hub_sel, int32_t* hub_cnt, int32_t* sel_kv, int32_t* sel_cnt,
+                        void* stream);
+
+/* One budget candidate from key-ordered selections: per row the first b_real
+ * entries of real_kv and the first b_rw of rw_kv, merged as
+ * _assemble_edges_from_pools merges them (utils/fullgraph_sp_support.py:
+ * 1824-1879 -> gt_sp/utils.py:877-887): dedup != 0 gives the set union
+ * ascending (both parts globally non-empty), else the multiset ascending.
+ * NULL real_kv / rw_kv (or a zero budget) drops that part. b_real + b_rw <= 64.
+ *   table int32 [n_rows, width] (-1 padded), row_len int32 [n_rows].        */
+int bf_assemble_rows(const int32_t* real_kv, const int32_t* real_cnt, int32_t real_stride,
+                     int32_t b_real, const int32_t* rw_kv, const int32_t* rw_cnt,
+                     int32_t rw_stride, int32_t b_rw, int32_t dedup, int64_t n_rows,
+                     int32_t* table, int32_t width, int32_t* row_len, void* stream);
+
+/* One layer of the probe's reception-cone expansion
+ * (_expand_probe_idx_for_reception, utils/fullgraph_sp_support.py:2261-2309):
+ * reached[s] = 1 for every edge s -> v of the in-neighbour CSR with
+ * frontier[v] != 0. frontier, reached: uint8 [num_nodes]; reached is not
+ * cleared first.                                                           */
+int bf_mark_in_neighbors(const int64_t* in_ptr, const int32_t* in_src, int64_t num_nodes,
+                         const uint8_t* frontier, uint8_t* reached, void* stream);
 
 /* Whole budgeted build: bf_rw_select then bf_real_select_merge with
  * key seeds edge_seed+37 / edge_seed+17 (utils/fullgraph_sp_support.py:970-972,

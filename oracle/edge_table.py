@@ -336,3 +336,106 @@ def build_edge_table(rowptr, col, num_nodes: int, b_real: int, b_rw: int, walk_l
         merged = parts[0] if parts else np.zeros((2, 0), dtype=np.int64)
     merged = np.stack([merged[0], merged[1] - q_lo])
     return coo_to_table(merged, n_q, max(1, b_real + b_rw))
+
+
+# ---------------------------------------------------------------- adaptive-budget probe
+# The budget controller's gain probe (utils/fullgraph_sp_support.py): the dst
+# filter (:2261-2309), the filtered pools (:1743-1821) and the per-candidate
+# assembly (:1824-1879, sampling by :1262-1309).
+def reception_cone(edge_index: np.ndarray, probe_ids, n_layers: int):
+    """_expand_probe_idx_for_reception (utils/fullgraph_sp_support.py:2261-2309).
+
+    probe ids plus every node reaching them within n_layers-1 hops along the
+    edges (src -> dst); the mask is sized by edge_index.max()+1, so probe ids
+    at or beyond it are dropped. Returns probe_ids unchanged for n_layers <= 1,
+    an empty probe set or an edgeless graph.
+    """
+    probe = np.asarray(probe_ids, dtype=np.int64).reshape(-1)
+    ei = np.asarray(edge_index, dtype=np.int64)
+    if n_layers <= 1 or probe.size == 0 or ei.size == 0:
+        return probe_ids
+    n = int(ei.max()) + 1
+    probe = probe[(probe >= 0) & (probe < n)]
+    reached = np.zeros(n, dtype=bool)
+    reached[probe] = True
+    frontier = probe
+    for _ in range(n_layers - 1):
+        if frontier.size == 0:
+            break
+        edges = ei[:, np.isin(ei[1], frontier)]
+        if edges.size == 0:
+            break
+        srcs = np.unique(edges[0])
+        srcs = srcs[(srcs >= 0) & (srcs < n)]
+        new = srcs[~reached[srcs]]
+        if new.size == 0:
+            break
+        reached[new] = True
+        frontier = new
+    return np.nonzero(reached)[0].astype(np.int64)
+
+
+def filter_edge_index_by_dst(edge_index: np.ndarray, dst_nodes) -> np.ndarray:
+    """_filter_edge_index_by_dst (utils/fullgraph_sp_support.py:1520-1533): entries whose dst is listed."""
+    ei = np.asarray(edge_index, dtype=np.int64)
+    if ei.size == 0:
+        return ei
+    dst_nodes = np.asarray(dst_nodes, dtype=np.int64).reshape(-1)
+    return ei[:, np.isin(ei[1], dst_nodes)]
+
+
+def subtract_edge_index(a: np.ndarray, b: np.ndarray, num_nodes: int) -> np.ndarray:
+    """_subtract_edge_index (utils/fullgraph_sp_support.py:1536-1551): drop entries of a whose pair is in b."""
+    if a is None or a.size == 0 or b is None or b.size == 0:
+        return a
+    n = max(1, int(num_nodes))
+    keep = ~np.isin(a[0] * n + a[1], b[0] * n + b[1])
+    return a[:, keep]
+
+
+def probe_edge_pools(edge_index_global: np.ndarray, num_nodes: int, dst_filter, walk_length: int,
+                     walks_per_node: int, u: np.ndarray, use_real: bool = True, use_rw: bool = True) -> dict:
+    """_build_probe_edge_pools (utils/fullgraph_sp_support.py:1743-1821).
+
+    real = graph edges into the filter; rw = the full RW pool (walks from every
+    node, ``u`` [N*P, L]) restricted to the filter, minus every pair of the real
+    pool when both pools are non-empty.
+    """
+    ei = np.asarray(edge_index_global, dtype=np.int64)
+    real = filter_edge_index_by_dst(ei, dst_filter) if use_real else None
+    rw = None
+    if use_rw and walks_per_node > 0:
+        rowptr, col = csr_from_coo(ei, num_nodes)
+        pool = build_head_hop_edges(rowptr, col, num_nodes, walk_length, walks_per_node, u)
+        rw = filter_edge_index_by_dst(pool, dst_filter)
+        if rw.size and real is not None and real.size:
+            rw = subtract_edge_index(rw, real, num_nodes)
+    return {"real": real, "rw": rw}
+
+
+def assemble_edges_from_pools(pools: dict, num_nodes: int, b_real: int, b_rw: int, edge_seed: int,
+                              graphormer_global_token: bool = False, exphormer: bool = False) -> np.ndarray:
+    """_assemble_edges_from_pools (utils/fullgraph_sp_support.py:1824-1879).
+
+    Per pool: the top-b per dst under seed+17 (real) / seed+37 (rw), a zero
+    budget dropping the pool (:1262-1309); then the typed [3, E] concatenation
+    for Exphormer, else _merge_edge_index_list and, for Graphormer,
+    fix_edge_index.
+    """
+    real, rw = pools.get("real"), pools.get("rw")
+    if real is not None:
+        real = sample_edges_per_query_random(real, b_real, edge_block_seed(edge_seed, REAL_SEED_OFFSET)) \
+            if b_real > 0 else None
+    if rw is not None:
+        rw = sample_edges_per_query_random(rw, b_rw, edge_block_seed(edge_seed, RW_SEED_OFFSET)) if b_rw > 0 else None
+    if exphormer:
+        typed = [np.concatenate([x, np.full((1, x.shape[1]), t, dtype=np.int64)])
+                 for t, x in ((0, real), (1, rw)) if x is not None and x.size > 0]
+        return np.concatenate(typed, axis=1) if typed else np.zeros((3, 0), dtype=np.int64)
+    parts = [x for x in (real, rw) if x is not None and x.size > 0]
+    merged = merge_edge_index_list(parts) if parts else None
+    if merged is None:
+        merged = np.zeros((2, 0), dtype=np.int64)
+    if graphormer_global_token:
+        merged = fix_edge_index(merged, num_nodes)
+    return merged
