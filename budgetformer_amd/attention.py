@@ -271,9 +271,9 @@ class ExphormerCoreAttention(nn.Module):
         vf = v.reshape(-1, num_heads, hn)
         n_kv = kf.size(0)
         if isinstance(edge_index, torch.Tensor) and edge_index.dim() == 2 and edge_index.size(0) == 3:
-            key = (edge_index.data_ptr(), tuple(edge_index.shape), edge_index._version, str(q.device),
-                   qf.size(0), n_kv)
-            if self._typed_key != key:      # one conversion per edge set, shared by every layer call
+            # the key holds the edge tensor itself, so a match is that tensor, not a reused address
+            key = (edge_index, edge_index._version, str(q.device), qf.size(0), n_kv)
+            if self._typed_key is None or self._typed_key[0] is not edge_index or self._typed_key[1:] != key[1:]:
                 ei = edge_index.to(q.device)
                 shifted = torch.stack([ei[0].long() + ei[2].long() * n_kv, ei[1].long()])
                 self._typed_idx = AttentionIndex.from_coo(shifted, qf.size(0), self.N_EDGE_TYPES * n_kv)

@@ -224,13 +224,15 @@ def _get_random_walk_graph(edge_index: torch.Tensor, num_nodes: int, device):
     dev = torch.device(device)
     key = (int(edge_index.data_ptr()), int(edge_index.size(1)), int(num_nodes), dev.type, dev.index)
     hit = _RANDOM_WALK_GRAPH_CACHE.get(key)
-    if hit is not None:
-        return hit
+    # the entry pins its source tensor, so a hit is the same tensor (same version), not a reused address
+    if hit is not None and hit[0] is edge_index and hit[1] == edge_index._version:
+        return hit[2]
     ei = hip_ops.coalesce(edge_index.to(dev), num_nodes)
     rowptr, col = hip_ops.coo_to_csr(torch.stack([ei[1], ei[0]]), num_nodes, num_nodes)
     placeholder = torch.empty((2, 0), dtype=edge_index.dtype, device=dev)
-    _RANDOM_WALK_GRAPH_CACHE[key] = (placeholder, rowptr, col)
-    return _RANDOM_WALK_GRAPH_CACHE[key]
+    _RANDOM_WALK_GRAPH_CACHE.clear()
+    _RANDOM_WALK_GRAPH_CACHE[key] = (edge_index, edge_index._version, (placeholder, rowptr, col))
+    return _RANDOM_WALK_GRAPH_CACHE[key][2]
 
 
 def _run_random_walk(edge_index, rowptr: torch.Tensor, col: torch.Tensor, starts: torch.Tensor, walk_length: int,

@@ -71,9 +71,97 @@ def test_build_merged_edges_reference_surface(hip_device, model, b):
     n, P, L = 1500, 2, 4
     rowptr, col, ei = _graph(n, 12000, seed=5)
     args = types.SimpleNamespace(model=model, num_global_node=1, seed=42, walks_per_node=P, walk_length=L,
-                                 max_total_edges_per_query=b, num_heads=8)
+                                 max_total_edges_per_query=b, num_heads=8, random_edge_blocks=True)
     got = _build_merged_edges(args, torch.from_numpy(ei).to(hip_device), n, hip_device, hip_device, n, edge_seed=44)
     u = philox.walk_uniforms(0, n, P, L, 44)
     ref = et.build_merged_edges(ei, n, (b + 1) // 2, b // 2, L, P, 44, u,
                                 graphormer_global_token=(model == "graphormer"))
     assert np.array_equal(got.cpu().numpy(), ref)
+
+
+def _pairs(ei):
+    return sorted(zip(ei[0].tolist(), ei[1].tolist()))
+
+
+def test_build_merged_edges_exphormer_typed_and_unbudgeted(hip_device):
+    from budgetformer_amd.utils import fullgraph_sp_support as fs
+    n, P, L, seed = 1200, 2, 4, 31
+    rowptr, col, ei = _graph(n, 9000, seed=6)
+    ei_t = torch.from_numpy(ei).to(hip_device)
+    u = philox.walk_uniforms(0, n, P, L, seed)
+    # Exphormer RW mode, fixed budgets (3, 5): real part type 0, RW part type 1, not merged
+    args = types.SimpleNamespace(model="exphormer", expander_degree=0, seed=1, walks_per_node=P, walk_length=L,
+                                 fixed_real_edges_per_query=3, fixed_rw_edges_per_query=5, num_heads=8)
+    typed = fs._build_merged_edges(args, ei_t, n, hip_device, hip_device, n, edge_seed=seed).cpu().numpy()
+    assert typed.shape[0] == 3
+    real = et.build_merged_edges(ei, n, 3, 0, L, P, seed, u)
+    rw = et.build_merged_edges(ei, n, 0, 5, L, P, seed, u)
+    assert _pairs(typed[:2, typed[2] == 0]) == _pairs(real) and _pairs(typed[:2, typed[2] == 1]) == _pairs(rw)
+    # unbudgeted (no fixed / adaptive / random-block budgets): whole graph merged with the whole pool
+    args = types.SimpleNamespace(model="graphormer", num_global_node=1, seed=1, walks_per_node=P, walk_length=L,
+                                 include_real_edges=1, num_heads=8)
+    got = fs._build_merged_edges(args, ei_t, n, hip_device, hip_device, n, edge_seed=seed).cpu().numpy()
+    pool = et.build_head_hop_edges(rowptr, col, n, L, P, u)
+    assert np.array_equal(got, et.fix_edge_index(et.merge_edge_index_list([ei, pool]), n))
+
+
+def test_full_rw_pool_cache_and_attention_edges_cache(hip_device):
+    from budgetformer_amd.utils import fullgraph_sp_support as fs
+    n, P, L, seed = 1000, 2, 4, 12
+    rowptr, col, ei = _graph(n, 7000, seed=8)
+    ei_t = torch.from_numpy(ei).to(hip_device)
+    args = types.SimpleNamespace(model="gt", seed=3, walks_per_node=P, walk_length=L, max_total_edges_per_query=8,
+                                 num_heads=8, random_edge_blocks=True)
+    pool = fs._build_or_retrieve_full_rw_pool(args, ei_t, n, hip_device, L, P, 8, seed)
+    assert np.array_equal(pool.cpu().numpy(),
+                          et.build_head_hop_edges(rowptr, col, n, L, P, philox.walk_uniforms(0, n, P, L, seed)))
+    assert fs._build_or_retrieve_full_rw_pool(args, ei_t, n, hip_device, L, P, 8, seed) is pool   # single-slot hit
+    fs.clear_merged_edge_cache()
+    a = fs._build_attention_edges(args, ei_t, n, hip_device, hip_device, None, 0, 0, n, edge_seed=seed)
+    b = fs._build_attention_edges(args, ei_t, n, hip_device, hip_device, None, 0, 0, n, edge_seed=seed)
+    assert b is a and len(fs._MERGED_EDGE_CACHE) == 1                                   # cached under the key
+    ref = et.build_merged_edges(ei, n, 4, 4, L, P, seed, philox.walk_uniforms(0, n, P, L, seed))
+    assert np.array_equal(a.cpu().numpy(), ref)
+    c = fs._build_attention_edges(args, ei_t, n, hip_device, hip_device, None, 0, 0, n, edge_seed=seed + 1)
+    assert len(fs._MERGED_EDGE_CACHE) == 2 and not torch.equal(c, a)
+
+
+def test_probe_seams_match_oracle(hip_device):
+    from budgetformer_amd.utils import fullgraph_sp_support as fs
+    n, P, L, seed = 1500, 2, 4, 5
+    rowptr, col, ei = _graph(n, 10000, seed=9)
+    ei_t = torch.from_numpy(ei).to(hip_device)
+    probe = torch.tensor([3, 90, 700, 1499])
+    F = fs._expand_probe_idx_for_reception(probe, ei_t, 2)
+    assert np.array_equal(F.numpy(), et.reception_cone(ei, probe.numpy(), 2))
+    u = philox.walk_uniforms(0, n, P, L, seed)
+    ref_pools = et.probe_edge_pools(ei, n, F.numpy(), L, P, u)
+    for model, state in (("graphormer", {"real_edges_per_query": 4, "rw_edges_per_query": 4}),
+                         ("gt", {"real_edges_per_query": 6, "rw_edges_per_query": 2}),
+                         ("gt", {"real_edges_per_query": 0, "rw_edges_per_query": 3})):
+        args = types.SimpleNamespace(model=model, num_global_node=1, seed=1, walks_per_node=P, walk_length=L,
+                                     max_total_edges_per_query=8, num_heads=8, random_edge_blocks=True)
+        got = fs._build_probe_attention_edges(args, ei_t, n, hip_device, hip_device, None, 0, 0, n, probe,
+                                              edge_seed=seed, edge_budget_state=state, edge_dst_filter=F)
+        ref = et.assemble_edges_from_pools(ref_pools, n, state["real_edges_per_query"], state["rw_edges_per_query"],
+                                           seed, graphormer_global_token=(model == "graphormer"))
+        if state["real_edges_per_query"] and state["rw_edges_per_query"]:
+            assert np.array_equal(got.cpu().numpy(), ref)
+        else:
+            assert _pairs(got.cpu().numpy()) == _pairs(ref)
+
+
+def test_graph_caches_do_not_confuse_tensors_at_a_reused_address(hip_device):
+    """Two edge lists of the same shape, the first freed before the second is made: the cached CSR
+    must follow the tensor, not its (reusable) device address."""
+    from budgetformer_amd.utils import fullgraph_sp_support as fs
+    n, P, L, seed = 900, 2, 4, 3
+    args = types.SimpleNamespace(model="gt", seed=1, walks_per_node=P, walk_length=L, max_total_edges_per_query=6,
+                                 num_heads=8, random_edge_blocks=True)
+    for graph_seed in (21, 22):
+        rowptr, col, ei = _graph(n, 6000, seed=graph_seed)
+        ei_t = torch.from_numpy(ei).to(hip_device)
+        got = fs._build_merged_edges(args, ei_t, n, hip_device, hip_device, n, edge_seed=seed)
+        ref = et.build_merged_edges(ei, n, 3, 3, L, P, seed, philox.walk_uniforms(0, n, P, L, seed))
+        assert np.array_equal(got.cpu().numpy(), ref)
+        del ei_t, got
