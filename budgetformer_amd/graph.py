@@ -73,6 +73,87 @@ class CSRGraph:
         return cls(rowptr, col, in_ptr, in_src, int(num_nodes))
 
 
+# ------------------------------------------------------------------ topology ingest
+_SORT_LIMIT = (1 << 31) - 1      # entries one device radix sort takes (int32 counts)
+
+
+def load_edge_index(path: str) -> torch.Tensor:
+    """``edge_index.pt`` as utils/preprocess_data.py:425-427 writes it (``torch.save`` of a [2, E]
+    integer tensor), loaded on the host as utils/fullgraph_sp_support.py:690-715 first tries:
+    ``weights_only=True`` with ``mmap=True`` (without mmap for files that do not support it).
+    The reference's ``weights_only=False`` fallbacks are not taken: they would unpickle
+    arbitrary objects from the file."""
+    try:
+        t = torch.load(path, map_location="cpu", weights_only=True, mmap=True)
+    except RuntimeError:
+        t = torch.load(path, map_location="cpu", weights_only=True)
+    if not isinstance(t, torch.Tensor) or t.dim() != 2 or t.size(0) != 2 or t.dtype.is_floating_point:
+        raise ValueError(f"{path}: expected a [2, E] integer tensor, got {type(t).__name__}"
+                         f"{tuple(t.shape) if isinstance(t, torch.Tensor) else ''}")
+    return t
+
+
+def coalesce_edges(edge_index: torch.Tensor, num_nodes: int, max_chunk: int = _SORT_LIMIT) -> torch.Tensor:
+    """torch_geometric ``coalesce`` (sort by (src, dst), drop duplicates) on the device, for any E.
+
+    Up to ``max_chunk`` entries it is one ``bf_coalesce``; beyond that the
+    entries are cut into ascending source ranges of at most ``max_chunk``
+    entries each (a histogram of the sources picks the cuts), each range is
+    coalesced alone and the results are concatenated, which is the same order.
+    """
+    n = int(num_nodes)
+    E = int(edge_index.size(1))
+    if E <= max_chunk:
+        return hip_ops.coalesce(edge_index, n)
+    src = edge_index[0]
+    counts = torch.bincount(src.to(torch.int64), minlength=n)
+    if int(counts.max()) > max_chunk:
+        raise ValueError(f"one source holds more than {max_chunk} entries; cannot cut it into sort ranges")
+    cum = torch.cumsum(counts, 0).cpu()
+    parts, lo, taken = [], 0, 0
+    while lo < n:
+        # largest hi with cum[hi-1] - taken <= max_chunk
+        hi = int(torch.searchsorted(cum, torch.tensor([taken + max_chunk]), right=True)[0])
+        hi = max(hi, lo + 1)
+        sel = edge_index[:, (src >= lo) & (src < hi)]
+        if sel.numel():
+            parts.append(hip_ops.coalesce(sel, n))
+        taken = int(cum[hi - 1])
+        lo = hi
+    return torch.cat(parts, dim=1) if parts else edge_index.new_zeros((2, 0), dtype=torch.int64)
+
+
+def to_bidirected(edge_index: torch.Tensor, num_nodes: int, max_chunk: int = _SORT_LIMIT) -> torch.Tensor:
+    """``_to_bidirected_edge_index`` (utils/fullgraph_sp_support.py:570-572): coalesce(E ∪ flip(E))."""
+    return coalesce_edges(torch.cat([edge_index, edge_index.flip(0)], dim=1), num_nodes, max_chunk)
+
+
+def load_graph(dataset_path: str, device="cuda", to_bidirected_edges: bool = False,
+               num_nodes: Optional[int] = None):
+    """Topology ingest of ``_load_data`` (utils/fullgraph_sp_support.py:637-687): ``edge_index.pt``
+    from ``dataset_path`` moved to the device, optionally made bidirected, and the walk CSR built there.
+
+    ``num_nodes`` defaults to the row count of ``x.pt`` (read through mmap, as
+    the reference sizes the graph by the features), else max id + 1. Returns
+    (CSRGraph, edge_index_global on the device).
+    """
+    import os
+    ei = load_edge_index(os.path.join(dataset_path, "edge_index.pt"))
+    if num_nodes is None:
+        x_path = os.path.join(dataset_path, "x.pt")
+        if os.path.exists(x_path):
+            num_nodes = int(torch.load(x_path, map_location="cpu", weights_only=True, mmap=True).shape[0])
+        else:
+            num_nodes = int(ei.max()) + 1 if ei.numel() else 0
+    ei = ei.to(device=device, dtype=torch.int64, non_blocking=False)
+    if to_bidirected_edges:
+        ei = to_bidirected(ei, num_nodes)
+        graph = CSRGraph.from_edge_index(ei, num_nodes, symmetric=True, device=device)
+    else:
+        graph = CSRGraph.from_edge_index(coalesce_edges(ei, num_nodes), num_nodes, device=device)
+    return graph, ei
+
+
 def chung_lu_device(num_nodes: int, num_edges: int, exponent: float = 2.1, seed: int = 42,
                     max_degree: Optional[float] = None, i0: float = 10.0, device="cuda") -> CSRGraph:
     """Symmetric Chung-Lu graph with ``num_edges // 2`` distinct pairs, generated in HBM (bf_chung_lu).

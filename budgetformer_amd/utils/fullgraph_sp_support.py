@@ -307,6 +307,23 @@ def _build_merged_edges(args, edge_index_global, num_nodes, final_device, rw_dev
     return table.to_edge_index().to(out_dev)
 
 
+# ------------------------------------------------------------------ topology ingest
+def _to_bidirected_edge_index(edge_index: torch.Tensor, num_nodes: int) -> torch.Tensor:
+    """utils/fullgraph_sp_support.py:570-572 on the device (``budgetformer_amd.graph.to_bidirected``)."""
+    from ..graph import to_bidirected
+    out_dev = edge_index.device
+    return to_bidirected(edge_index.to(_hip_device(out_dev)), int(num_nodes)).to(out_dev)
+
+
+def _torch_load_cpu(path: str):
+    """utils/fullgraph_sp_support.py:690-715, restricted to the loads that execute nothing from the
+    file (``weights_only=True``, with and without mmap)."""
+    try:
+        return torch.load(path, map_location="cpu", weights_only=True, mmap=True)
+    except RuntimeError:
+        return torch.load(path, map_location="cpu", weights_only=True)
+
+
 # ------------------------------------------------------------------ per-epoch entry, merged-edge cache
 def _resolve_edge_policy(args, edge_index_global=None, edge_policy=None) -> str:
     """utils/fullgraph_sp_support.py:379-391."""
