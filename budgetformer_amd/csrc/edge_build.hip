@@ -271,20 +271,26 @@ __device__ __forceinline__ void write_row(int32_t (*lst)[kMaxRow], int32_t (*dup
   if (gl == 0) *len_out = len;
 }
 
+// Group-per-query top-k and merge. Row li of the launch serves query
+// qids[li] (or q_lo + li); it writes table row li, or with by_query the row
+// q - q_lo of an n_rows-row table (the heavy-query list of a light/heavy
+// split build; list entries outside the table are skipped).
 template <int KMAX>
 __global__ __launch_bounds__(kThreads) void real_select_merge_kernel(
     const int64_t* __restrict__ in_ptr, const int32_t* __restrict__ in_src, int64_t num_nodes, int64_t q_lo,
-    const int32_t* __restrict__ qids, int64_t n_q, int k_real, uint32_t kc, const int32_t* __restrict__ rw_kv,
-    const int32_t* __restrict__ rw_cnt, int k_rw, int dedup, int key_order, int32_t* __restrict__ table, int width,
-    int32_t* __restrict__ row_len, const int32_t* __restrict__ hubs, const int32_t* __restrict__ hub_sel,
-    const int32_t* __restrict__ hub_cnt, int64_t n_hubs, int64_t hub_threshold) {
+    const int32_t* __restrict__ qids, int64_t n_q, int by_query, int64_t n_rows, int k_real, uint32_t kc,
+    const int32_t* __restrict__ rw_kv, const int32_t* __restrict__ rw_cnt, int k_rw, int dedup, int key_order,
+    int32_t* __restrict__ table, int width, int32_t* __restrict__ row_len, const int32_t* __restrict__ hubs,
+    const int32_t* __restrict__ hub_sel, const int32_t* __restrict__ hub_cnt, int64_t n_hubs,
+    int64_t hub_threshold) {
   __shared__ int32_t lst[kQPB][kMaxRow];
   __shared__ int32_t dupf[kQPB][kMaxRow];
   const int gq = threadIdx.x / kGroup;
   const int gl = threadIdx.x % kGroup;
-  const int64_t qi = int64_t(blockIdx.x) * kQPB + gq;
-  const bool active = qi < n_q;
-  const int64_t q = active ? row_query(qids, q_lo, qi, num_nodes) : -1;
+  const int64_t li = int64_t(blockIdx.x) * kQPB + gq;
+  const int64_t q = li < n_q ? row_query(qids, q_lo, li, num_nodes) : -1;
+  const bool active = li < n_q && (!by_query || (q >= q_lo && q < q_lo + n_rows));
+  const int64_t qi = by_query ? q - q_lo : li;     // table / RW-selection row
   int n_r = 0, n_w = 0;
   int64_t hub = -1;
   if (q >= 0 && k_real > 0 && n_hubs > 0) {
@@ -371,6 +377,69 @@ __global__ __launch_bounds__(kThreads) void assemble_rows_kernel(
             row_len + (active ? qi : 0));
 }
 
+// Thread-per-query top-k and merge for the light queries (in-degree <=
+// light_max): the thread scans its in-neighbour row into a sorted register
+// list of KR (key << 32 | src), gathers the RW selection, sorts the KR + KW
+// values with an odd-even transposition network and writes the row ascending
+// (unique values when dedup). The same rows as real_select_merge_kernel, at a
+// fraction of the instructions: the power-law bulk of queries has a few
+// in-neighbours. Heavier queries are left to the group kernel.
+template <int KR, int KW>
+__global__ __launch_bounds__(kThreads) void real_select_light_kernel(
+    const int64_t* __restrict__ in_ptr, const int32_t* __restrict__ in_src, int64_t q_lo, int64_t n_q,
+    int k_real, uint32_t kc, const int32_t* __restrict__ rw_kv, const int32_t* __restrict__ rw_cnt, int k_rw,
+    int dedup, int32_t* __restrict__ table, int width, int32_t* __restrict__ row_len, int64_t light_max) {
+  constexpr int NV = KR + KW;
+  constexpr int32_t kPad = 0x7fffffff;          // sorts after every node id (ids < 2^31 - 1)
+  const int64_t qi = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (qi >= n_q) return;
+  const int64_t q = q_lo + qi;
+  int32_t v[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) v[j] = kPad;
+  if (k_real > 0) {
+    const int64_t beg = in_ptr[q], end = in_ptr[q + 1];
+    if (end - beg > light_max) return;          // a heavy query: the group kernel writes its row
+    uint64_t lk[KR];
+#pragma unroll
+    for (int j = 0; j < KR; ++j) lk[j] = kNone;
+    for (int64_t i = beg; i < end; ++i) {
+      const uint32_t s = uint32_t(in_src[i]);
+      const uint64_t c = (uint64_t(edge_key(s, uint32_t(q), kc)) << 32) | s;
+      if (c < lk[KR - 1]) {
+#pragma unroll
+        for (int j = KR - 1; j > 0; --j) lk[j] = c < lk[j - 1] ? lk[j - 1] : (c < lk[j] ? c : lk[j]);
+        lk[0] = c < lk[0] ? c : lk[0];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < KR; ++j) v[j] = (j < k_real && lk[j] != kNone) ? int32_t(uint32_t(lk[j])) : kPad;
+  }
+  if (rw_kv != nullptr && KW > 0) {
+    const int n_w = rw_cnt[qi];
+#pragma unroll
+    for (int j = 0; j < KW; ++j) v[KR + j] = (j < n_w && j < k_rw) ? rw_kv[qi * k_rw + j] : kPad;
+  }
+#pragma unroll
+  for (int r = 0; r < NV; ++r) {
+#pragma unroll
+    for (int j = r & 1; j + 1 < NV; j += 2) {
+      const int32_t a = v[j], b = v[j + 1];
+      v[j] = a < b ? a : b;
+      v[j + 1] = a < b ? b : a;
+    }
+  }
+  int32_t* out = table + qi * width;
+  int len = 0;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const bool keep = v[j] != kPad && !(dedup && j > 0 && v[j] == v[j - 1]);
+    if (keep) out[len++] = v[j];
+  }
+  for (int c = len; c < width; ++c) out[c] = -1;
+  row_len[qi] = len;
+}
+
 // One BFS layer of the probe's reception cone (utils/fullgraph_sp_support.py:
 // 2261-2309): reached[s] = 1 for every edge s -> v with frontier[v] set. A
 // 16-lane group walks v's in-neighbour row; concurrent stores all write 1.
@@ -410,12 +479,44 @@ int launch_rw_select(const int64_t* rowptr, const int32_t* col, int64_t num_node
   return BF_OK;
 }
 
+// Light/heavy split of a range build: every query of the range goes to the
+// thread-per-query kernel, which leaves rows with in-degree > light_max to the
+// group kernel over `heavy` (those queries of the range, ascending).
+struct LightSplit {
+  const int32_t* heavy = nullptr;
+  int64_t n_heavy = 0;
+  int64_t light_max = -1;     // < 0: no split, the group kernel takes every row
+};
+
+int launch_light(const int64_t* in_ptr, const int32_t* in_src, int64_t q_lo, int64_t n_q, int k_real, uint32_t kc,
+                 const int32_t* rw_kv, const int32_t* rw_cnt, int k_rw, int dedup, int32_t* table, int width,
+                 int32_t* row_len, int64_t light_max, hipStream_t st) {
+  const dim3 grid(unsigned(ceil_div(n_q, kThreads)));
+#define BF_LAUNCH_LIGHT(KR, KW)                                                                                     \
+  BF_LAUNCH("real_select_light_kernel", (real_select_light_kernel<KR, KW>), grid, dim3(kThreads), 0, st, in_ptr,  \
+            in_src, q_lo, n_q, k_real, kc, rw_kv, rw_cnt, k_rw, dedup, table, width, row_len, light_max)
+  const int kw = rw_kv ? k_rw : 0;
+  if (k_real <= 4 && kw <= 4)
+    BF_LAUNCH_LIGHT(4, 4);
+  else if (k_real <= 4)
+    BF_LAUNCH_LIGHT(4, 8);
+  else if (kw <= 4)
+    BF_LAUNCH_LIGHT(8, 4);
+  else
+    BF_LAUNCH_LIGHT(8, 8);
+#undef BF_LAUNCH_LIGHT
+  BF_CHECK_LAUNCH();
+  return BF_OK;
+}
+
 int launch_real_merge(const int64_t* in_ptr, const int32_t* in_src, int64_t num_nodes, int64_t q_lo,
                       const int32_t* qids, int64_t n_q, int k_real, uint32_t kc, const int32_t* rw_kv,
                       const int32_t* rw_cnt, int k_rw, int dedup, int key_order, int32_t* table, int width,
                       int32_t* row_len, const int32_t* hubs, int64_t n_hubs, int64_t hub_threshold,
-                      int32_t* hub_sel, int32_t* hub_cnt, hipStream_t st) {
+                      int32_t* hub_sel, int32_t* hub_cnt, hipStream_t st, LightSplit split = LightSplit()) {
   if (n_q == 0) return BF_OK;
+  const bool light = split.light_max >= 0 && qids == nullptr && !key_order && k_real <= 8 &&
+                     (rw_kv == nullptr || k_rw <= 8);
   if (k_real <= 0) n_hubs = 0;
   if (n_hubs > 0) {
 #define BF_LAUNCH_HUB(KM)                                                                                       \
@@ -432,11 +533,18 @@ int launch_real_merge(const int64_t* in_ptr, const int32_t* in_src, int64_t num_
 #undef BF_LAUNCH_HUB
     BF_CHECK_LAUNCH();
   }
-  const dim3 grid(unsigned(ceil_div(n_q, kQPB)));
+  if (light) {
+    int rc = launch_light(in_ptr, in_src, q_lo, n_q, k_real, kc, rw_kv, rw_cnt, k_rw, dedup, table, width, row_len,
+                          k_real > 0 ? split.light_max : (int64_t(1) << 62), st);
+    if (rc || split.n_heavy == 0 || k_real == 0) return rc;
+  }
+  const int32_t* list = light ? split.heavy : qids;
+  const int64_t n_list = light ? split.n_heavy : n_q;
+  const dim3 grid(unsigned(ceil_div(n_list, kQPB)));
 #define BF_LAUNCH_MERGE(KM)                                                                                      \
   BF_LAUNCH("real_select_merge_kernel", real_select_merge_kernel<KM>, grid, dim3(kThreads), 0, st, in_ptr, in_src, \
-            num_nodes, q_lo, qids, n_q, k_real, kc, rw_kv, rw_cnt, k_rw, dedup, key_order, table, width, row_len,   \
-            hubs, hub_sel, hub_cnt, n_hubs, hub_threshold)
+            num_nodes, q_lo, list, n_list, light ? 1 : 0, n_q, k_real, kc, rw_kv, rw_cnt, k_rw, dedup, key_order,  \
+            table, width, row_len, hubs, hub_sel, hub_cnt, n_hubs, hub_threshold)
   if (k_real <= 4)
     BF_LAUNCH_MERGE(4);
   else if (k_real <= 8)
@@ -544,7 +652,8 @@ extern "C" int bf_real_select_merge(const int64_t* in_ptr, const int32_t* in_src
                                     int64_t n_q, int32_t k_real, int64_t key_seed, const int32_t* rw_kv,
                                     const int32_t* rw_cnt, int32_t k_rw, int32_t dedup, int32_t* table,
                                     int32_t width, int32_t* row_len, const int32_t* hubs, int64_t n_hubs,
-                                    int64_t hub_threshold, int32_t* hub_sel, int32_t* hub_cnt, void* stream) {
+                                    int64_t hub_threshold, int32_t* hub_sel, int32_t* hub_cnt, const int32_t* heavy,
+                                    int64_t n_heavy, int64_t light_max, void* stream) {
   int rc = check_graph(in_ptr, in_src, num_nodes, q_lo, n_q);
   if (rc) return rc;
   if (k_real < 0) k_real = 0;
@@ -558,9 +667,14 @@ extern "C" int bf_real_select_merge(const int64_t* in_ptr, const int32_t* in_src
   BF_CHECK_ARG(n_hubs >= 0 && n_hubs < (int64_t(1) << 31), "real_select_merge: bad hub count");
   BF_CHECK_ARG(n_hubs == 0 || (hubs && hub_sel && hub_cnt && hub_threshold >= 0),
                "real_select_merge: hub arrays missing");
+  BF_CHECK_ARG(n_heavy >= 0 && (n_heavy == 0 || heavy), "real_select_merge: heavy list missing");
+  LightSplit split;
+  split.heavy = heavy;
+  split.n_heavy = n_heavy;
+  split.light_max = light_max;
   return launch_real_merge(in_ptr, in_src, num_nodes, q_lo, nullptr, n_q, k_real, key_const(key_seed),
                            k_rw ? rw_kv : nullptr, rw_cnt, k_rw, dedup ? 1 : 0, 0, table, width, row_len, hubs, n_hubs,
-                           hub_threshold, hub_sel, hub_cnt, as_stream(stream));
+                           hub_threshold, hub_sel, hub_cnt, as_stream(stream), split);
 }
 
 extern "C" int bf_real_select_rows(const int64_t* in_ptr, const int32_t* in_src, int64_t num_nodes,
@@ -618,7 +732,8 @@ extern "C" int bf_build_edge_table(const int64_t* rowptr, const int32_t* col, co
                                    int64_t n_q, int32_t walks_per_node, int32_t walk_length, int32_t k_real,
                                    int32_t k_rw, int64_t edge_seed, const float* u, uint64_t philox_seed,
                                    uint64_t philox_offset, const int32_t* hubs, int64_t n_hubs,
-                                   int64_t hub_threshold, int32_t* table, int32_t* row_len, void* workspace,
+                                   int64_t hub_threshold, const int32_t* heavy, int64_t n_heavy,
+                                   int64_t light_max, int32_t* table, int32_t* row_len, void* workspace,
                                    size_t workspace_bytes, void* stream) {
   BF_CHECK_ARG(num_edges >= 0, "build_edge_table: num_edges < 0");
   const bool use_rw = k_rw > 0 && walks_per_node > 0 && walk_length > 0 && num_nodes > 0;
@@ -648,7 +763,7 @@ extern "C" int bf_build_edge_table(const int64_t* rowptr, const int32_t* col, co
   return bf_real_select_merge(in_ptr, in_src, num_nodes, q_lo, n_q, use_real ? k_real : 0, edge_seed + 17,
                               use_rw ? sel_kv : nullptr, use_rw ? sel_cnt : nullptr, use_rw ? k_rw : 0,
                               (use_real && use_rw) ? 1 : 0, table, width, row_len, hubs, n_hubs, hub_threshold,
-                              hub_sel, hub_cnt, st);
+                              hub_sel, hub_cnt, heavy, n_heavy, light_max, st);
 }
 
 extern "C" int bf_mark_in_neighbors(const int64_t* in_ptr, const int32_t* in_src, int64_t num_nodes,

@@ -112,18 +112,30 @@ def build_attention_edges(graph: CSRGraph, *, real_edges_per_query: int, rw_edge
     seed = int(edge_seed if philox_seed is None else philox_seed)
     plan = plan_edge_build(graph.device, n_q, b_r, b_w, q_lo=q_lo, usable_bytes=usable_bytes)
     all_hubs = graph.hubs() if b_r > 0 else None
+    # queries above LIGHT_MAX in-neighbours take the group path; the rest one thread each (k <= 8)
+    light = b_r > 0 and b_r <= 8 and b_w <= 8
+    all_heavy = graph.heavy() if light else None
 
-    def hubs_in(lo, cnt):
-        if all_hubs is None or all_hubs.numel() == 0:
+    def in_range(lst, lo, cnt):
+        if lst is None or lst.numel() == 0:
             return None
-        bounds = torch.tensor([lo, lo + cnt], dtype=torch.int32, device=all_hubs.device)
-        a, b = torch.searchsorted(all_hubs, bounds).tolist()
-        return all_hubs[a:b] if b > a else None
+        if lo == 0 and cnt == graph.num_nodes:
+            return lst
+        bounds = torch.tensor([lo, lo + cnt], dtype=torch.int32, device=lst.device)
+        a, b = torch.searchsorted(lst, bounds).tolist()
+        return lst[a:b] if b > a else None
+
+    def split_args(lo, cnt):
+        if not light:
+            return {"hubs": in_range(all_hubs, lo, cnt)}
+        heavy = in_range(all_heavy, lo, cnt)
+        return {"hubs": in_range(all_hubs, lo, cnt), "light_max": hip_ops.LIGHT_MAX,
+                "heavy": heavy if heavy is not None else torch.empty(0, dtype=torch.int32, device=graph.device)}
 
     if len(plan.shards) == 1:
         table, row_len = hip_ops.build_edge_table(
             graph.rowptr, graph.col, graph.in_ptr, graph.in_src, graph.num_edges, q_lo, n_q, P, walk_length,
-            b_r, b_w, int(edge_seed), u=u, philox_seed=seed, philox_offset=philox_offset, hubs=hubs_in(q_lo, n_q))
+            b_r, b_w, int(edge_seed), u=u, philox_seed=seed, philox_offset=philox_offset, **split_args(q_lo, n_q))
     else:
         table = torch.empty(n_q, b_r + b_w, dtype=torch.int32, device=graph.device)
         row_len = torch.empty(n_q, dtype=torch.int32, device=graph.device)
@@ -133,5 +145,5 @@ def build_attention_edges(graph: CSRGraph, *, real_edges_per_query: int, rw_edge
             hip_ops.build_edge_table(graph.rowptr, graph.col, graph.in_ptr, graph.in_src, graph.num_edges, lo, cnt,
                                      P, walk_length, b_r, b_w, int(edge_seed), u=u_s, philox_seed=seed,
                                      philox_offset=philox_offset, out=(table[a:a + cnt], row_len[a:a + cnt]),
-                                     hubs=hubs_in(lo, cnt))
+                                     **split_args(lo, cnt))
     return EdgeTable(table, row_len, graph.num_nodes, q_lo=q_lo, global_token=global_token)

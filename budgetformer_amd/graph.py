@@ -36,6 +36,11 @@ class CSRGraph:
     def symmetric(self) -> bool:
         return self.in_ptr is self.rowptr and self.in_src is self.col
 
+    def heavy(self, light_max: int = hip_ops.LIGHT_MAX) -> torch.Tensor:
+        """Ascending ids of queries whose in-degree exceeds ``light_max`` (int32), cached: the
+        real-edge top-k of the others runs one query per thread."""
+        return self.hubs(light_max)
+
     def hubs(self, threshold: int = hip_ops.HUB_THRESHOLD) -> torch.Tensor:
         """Ascending ids of queries whose in-degree exceeds ``threshold`` (int32), cached per threshold.
 

@@ -18,6 +18,7 @@ from . import _native as N
 DEFAULT_CHUNK = 64      # rows longer than this go through the split plan
 DEFAULT_ITEM = 512      # entries per split item (one workgroup)
 HUB_THRESHOLD = 1024    # in-degree above which a query's real-edge top-k uses a whole workgroup
+LIGHT_MAX = 32          # in-degree up to which a query's real-edge top-k runs in one thread (k <= 8)
 
 
 def _p(t: Optional[torch.Tensor]):
@@ -146,8 +147,12 @@ def rw_select(rowptr, col, q_lo: int, n_q: int, walks_per_node: int, walk_length
 
 def real_select_merge(in_ptr, in_src, q_lo: int, n_q: int, k_real: int, key_seed: int,
                       rw_kv=None, rw_cnt=None, k_rw: int = 0, dedup: bool = True, width: Optional[int] = None,
-                      hubs: Optional[torch.Tensor] = None, hub_threshold: int = HUB_THRESHOLD):
-    """Real-edge top-k_real merged with an RW selection: (table [n_q,width], row_len [n_q])."""
+                      hubs: Optional[torch.Tensor] = None, hub_threshold: int = HUB_THRESHOLD,
+                      heavy: Optional[torch.Tensor] = None, light_max: int = -1):
+    """Real-edge top-k_real merged with an RW selection: (table [n_q,width], row_len [n_q]).
+
+    ``light_max >= 0`` with ``heavy`` (every query of the range whose in-degree
+    exceeds it, ascending) serves the light queries one per thread."""
     dev = in_ptr.device
     _require(in_ptr, "in_ptr", torch.int64)
     _require(in_src, "in_src", torch.int32, dev)
@@ -157,9 +162,15 @@ def real_select_merge(in_ptr, in_src, q_lo: int, n_q: int, k_real: int, key_seed
     n_hubs = 0 if hubs is None or k_real <= 0 else hubs.numel()
     hub_sel = torch.empty(max(n_hubs * max(k_real, 0), 1), dtype=torch.int32, device=dev)
     hub_cnt = torch.empty(max(n_hubs, 1), dtype=torch.int32, device=dev)
+    n_heavy = 0 if heavy is None else heavy.numel()
+    if n_heavy:
+        _require(heavy, "heavy", torch.int32, dev)
+    if light_max >= 0 and heavy is None:
+        raise ValueError("light_max >= 0 needs the heavy-query list")
     N.call("bf_real_select_merge", _p(in_ptr), _p(in_src), in_ptr.numel() - 1, q_lo, n_q, k_real, key_seed,
            _p(rw_kv), _p(rw_cnt), k_rw, int(bool(dedup)), _p(table), width, _p(row_len),
-           _p(hubs) if n_hubs else None, n_hubs, hub_threshold, _p(hub_sel), _p(hub_cnt), _stream(dev))
+           _p(hubs) if n_hubs else None, n_hubs, hub_threshold, _p(hub_sel), _p(hub_cnt),
+           _p(heavy) if n_heavy else None, n_heavy, int(light_max), _stream(dev))
     return table, row_len
 
 
@@ -264,10 +275,12 @@ def mark_in_neighbors(in_ptr, in_src, frontier: torch.Tensor, reached: torch.Ten
 def build_edge_table(rowptr, col, in_ptr, in_src, num_edges: int, q_lo: int, n_q: int, walks_per_node: int,
                      walk_length: int, k_real: int, k_rw: int, edge_seed: int, u=None, philox_seed: int = 0,
                      philox_offset: int = 0, out=None, hubs: Optional[torch.Tensor] = None,
-                     hub_threshold: int = HUB_THRESHOLD):
+                     hub_threshold: int = HUB_THRESHOLD, heavy: Optional[torch.Tensor] = None,
+                     light_max: int = -1):
     """Fused budgeted build (bf_build_edge_table): (table [n_q, k_real+k_rw], row_len [n_q]).
 
     ``out=(table, row_len)`` writes into caller-provided (contiguous) tensors.
+    ``heavy`` / ``light_max`` as in ``real_select_merge``.
     """
     dev = rowptr.device
     _require(rowptr, "rowptr", torch.int64)
@@ -291,12 +304,18 @@ def build_edge_table(rowptr, col, in_ptr, in_src, num_edges: int, q_lo: int, n_q
     n_hubs = 0 if hubs is None else hubs.numel()
     if n_hubs:
         _require(hubs, "hubs", torch.int32, dev)
+    n_heavy = 0 if heavy is None else heavy.numel()
+    if n_heavy:
+        _require(heavy, "heavy", torch.int32, dev)
+    if light_max >= 0 and heavy is None:
+        raise ValueError("light_max >= 0 needs the heavy-query list")
     ws_bytes = _size_query("bf_build_edge_table_workspace_size", n_q, max(k_rw, 0), n_hubs, max(k_real, 0))
     ws = _workspace(ws_bytes, dev)
     N.call("bf_build_edge_table", _p(rowptr), _p(col), _p(in_ptr), _p(in_src), rowptr.numel() - 1, num_edges,
            q_lo, n_q, walks_per_node, walk_length, k_real, k_rw, edge_seed, _p(u), philox_seed & (2 ** 64 - 1),
-           philox_offset & (2 ** 64 - 1), _p(hubs) if n_hubs else None, n_hubs, hub_threshold, _p(table),
-           _p(row_len), _p(ws), ws.numel(), _stream(dev))
+           philox_offset & (2 ** 64 - 1), _p(hubs) if n_hubs else None, n_hubs, hub_threshold,
+           _p(heavy) if n_heavy else None, n_heavy, int(light_max), _p(table), _p(row_len), _p(ws), ws.numel(),
+           _stream(dev))
     return table, row_len
 
 

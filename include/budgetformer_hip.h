@@ -142,6 +142,11 @@ int bf_rw_select_rows(const int64_t* rowptr, const int32_t* col, int64_t num_nod
  *     hub_threshold, or n_hubs = 0): their top-k is computed by one workgroup
  *     each into hub_sel int32 [n_hubs, k_real] / hub_cnt int32 [n_hubs]
  *     (caller-provided scratch) instead of by a 16-lane group.
+ *   light_max >= 0 (with k_real <= 8, k_rw <= 8) splits the work: queries of
+ *     in-degree <= light_max are served one per thread; heavy int32 [n_heavy]
+ *     must list every query of [q_lo, q_lo+n_q) with in-degree > light_max,
+ *     ascending (hubs included), and those take the 16-lane group path.
+ *     light_max < 0: no split (heavy ignored). The table is the same either way.
  *   table int32 [n_q, width] rows ascending, -1 padded; row_len int32 [n_q].
  *   Requires k_real <= 32, k_rw <= 32, width >= k_real + k_rw.               */
 int bf_real_select_merge(const int64_t* in_ptr, const int32_t* in_src, int64_t num_nodes,
@@ -149,7 +154,8 @@ int bf_real_select_merge(const int64_t* in_ptr, const int32_t* in_src, int64_t n
                          const int32_t* rw_kv, const int32_t* rw_cnt, int32_t k_rw,
                          int32_t dedup, int32_t* table, int32_t width, int32_t* row_len,
                          const int32_t* hubs, int64_t n_hubs, int64_t hub_threshold,
-                         int32_t* hub_sel, int32_t* hub_cnt, void* stream);
+                         int32_t* hub_sel, int32_t* hub_cnt, const int32_t* heavy,
+                         int64_t n_heavy, int64_t light_max, void* stream);
 
 /* Real-edge top-k_real for an explicit query list, in key order (so every
  * smaller budget is a prefix: the probe's nested candidates). Replaces the
@@ -191,7 +197,8 @@ int bf_mark_in_neighbors(const int64_t* in_ptr, const int32_t* in_src, int64_t n
  * 1413, 1514) and the reference's global merge rule (dedup iff both parts are
  * non-empty). Replaces _build_merged_edges (utils/fullgraph_sp_support.py:
  * 2943-3026) without the Graphormer token. width = k_real + k_rw. hubs /
- * n_hubs / hub_threshold as in bf_real_select_merge (n_hubs may be 0).
+ * n_hubs / hub_threshold and heavy / n_heavy / light_max as in
+ * bf_real_select_merge (n_hubs may be 0; light_max < 0 disables the split).
  * Workspace: bf_build_edge_table_workspace_size.                            */
 int bf_build_edge_table_workspace_size(int64_t n_q, int32_t k_rw, int64_t n_hubs, int32_t k_real,
                                        size_t* bytes);
@@ -202,6 +209,7 @@ int bf_build_edge_table(const int64_t* rowptr, const int32_t* col,
                         int32_t k_real, int32_t k_rw, int64_t edge_seed,
                         const float* u, uint64_t philox_seed, uint64_t philox_offset,
                         const int32_t* hubs, int64_t n_hubs, int64_t hub_threshold,
+                        const int32_t* heavy, int64_t n_heavy, int64_t light_max,
                         int32_t* table, int32_t* row_len,
                         void* workspace, size_t workspace_bytes, void* stream);
 

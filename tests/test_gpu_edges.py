@@ -189,3 +189,25 @@ def test_hub_path_bit_exact(hip_device, b_r, b_w, thr):
     tab = build_attention_edges(g, real_edges_per_query=b_r, rw_edges_per_query=b_w, walk_length=L,
                                 walks_per_node=P, edge_seed=42, u=ut[200 * P:1700 * P], q_lo=200, n_q=1500)
     assert np.array_equal(tab.table.cpu().numpy(), ref_t[200:1700])
+
+
+@pytest.mark.parametrize("b_r,b_w", [(4, 4), (8, 8), (3, 0), (8, 2)])
+def test_light_heavy_split_bit_exact(hip_device, b_r, b_w):
+    """Thread-per-query rows (in-degree <= light_max) and group rows give the same table at any cut."""
+    from budgetformer_amd import hip_ops
+    n, P, L = 3000, 2, 4
+    rowptr, col = _graph(n, 40000, seed=b_r * 3 + b_w)
+    g = _dev_graph(rowptr, col, n, hip_device)
+    u = np.random.default_rng(b_r).random((n * P, L), dtype=np.float32)
+    ut = torch.from_numpy(u).to(hip_device)
+    ref_t, ref_len = et.build_edge_table(rowptr, col, n, b_r, b_w, L, P, 42, u)
+    for light_max in (1, 5, 32, 10 ** 9):
+        heavy = g.heavy(light_max)
+        t, rl = hip_ops.build_edge_table(g.rowptr, g.col, g.in_ptr, g.in_src, g.num_edges, 0, n, P, L, b_r, b_w, 42,
+                                         u=ut, hubs=g.hubs(16), hub_threshold=16, heavy=heavy, light_max=light_max)
+        assert np.array_equal(t.cpu().numpy(), ref_t) and np.array_equal(rl.cpu().numpy(), ref_len), light_max
+    # a shard with its heavy list cut to the range
+    from budgetformer_amd.edges import build_attention_edges
+    tab = build_attention_edges(g, real_edges_per_query=b_r, rw_edges_per_query=b_w, walk_length=L,
+                                walks_per_node=P, edge_seed=42, u=ut[300 * P:2300 * P], q_lo=300, n_q=2000)
+    assert np.array_equal(tab.table.cpu().numpy(), ref_t[300:2300])
