@@ -500,7 +500,17 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_q_kernel(
 }
 
 // ------------------------------------------------------------------ backward, key-major (dk, dv)
-template <typename T>
+// q and dO rows are gathered B times per pass at random points; when the two
+// tables exceed the 256 MB Infinity Cache they are read non-temporally, which
+// keeps the row stats and the hub K/V rows cached instead (kStreamBytes).
+constexpr size_t kStreamBytes = size_t(256) << 20;
+
+template <typename T, bool NT>
+__device__ __forceinline__ typename Elem<T>::Raw gather_row(const T* base, int64_t row, int D, int col0) {
+  return NT ? Elem<T>::load_raw_nt(base + row * D + col0) : Elem<T>::load_raw(base + row * D + col0);
+}
+
+template <typename T, bool NT>
 __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __restrict__ dout,
                                             const int32_t* __restrict__ kq,
                                             const int32_t* __restrict__ ke,
@@ -529,8 +539,8 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       if (ok[u] && g.act) {
-        qr[u] = Elem<T>::load_raw(q + int64_t(t[u]) * sh.D + g.col0);
-        gr[u] = Elem<T>::load_raw(dout + int64_t(t[u]) * sh.D + g.col0);
+        qr[u] = gather_row<T, NT>(q, t[u], sh.D, g.col0);
+        gr[u] = gather_row<T, NT>(dout, t[u], sh.D, g.col0);
         rs[u] = rstat[int64_t(t[u]) * sh.H + g.head];
       } else {
         qr[u] = gr[u] = Elem<T>::zero_raw();
@@ -577,7 +587,7 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
 // Blocks [0, q_heavy) reduce the query-side split rows into dq (their items ran
 // in the dq pass), blocks [q_heavy, q_heavy + k_items) take the key-side items,
 // the rest one short key row per group, longest rows first.
-template <typename T>
+template <typename T, bool NT>
 __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const int64_t* __restrict__ kptr, const int32_t* __restrict__ kq,
@@ -602,7 +612,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
     const int64_t item = b - q_heavy;
     const ItemRange r = item_group_range(kit, sh, item);
     const typename Elem<T>::Raw kr = load_row_raw(k, r.row, sh.D, g), vr = load_row_raw(v, r.row, sh.D, g);
-    dkv_segment<T>(q, dout, kq, ke, bias, factor, rstat, r.beg, r.end, sh, g, kr, vr, ak, av);
+    dkv_segment<T, NT>(q, dout, kq, ke, bias, factor, rstat, r.beg, r.end, sh, g, kr, vr, ak, av);
     float z = 0.f;
     block_combine<V>(lds, kit.stride, sh, g, ak, av, true, z, false);
     if (r.single) {
@@ -628,7 +638,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
     return;
   }
   const typename Elem<T>::Raw kr = load_row_raw(k, row, sh.D, g), vr = load_row_raw(v, row, sh.D, g);
-  dkv_segment<T>(q, dout, kq, ke, bias, factor, rstat, beg, end, sh, g, kr, vr, ak, av);
+  dkv_segment<T, NT>(q, dout, kq, ke, bias, factor, rstat, beg, end, sh, g, kr, vr, ak, av);
   if (g.act) {
     Elem<T>::store(dk + row * sh.D + g.col0, ak);
     Elem<T>::store(dv + row * sh.D + g.col0, av);
@@ -766,9 +776,16 @@ int bwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
   const int64_t kv_blocks = int64_t(idx->q_heavy) + idx->k_items + grid_for(idx->n_kv, sh);
   if (kv_blocks > 0) {
     const size_t lds = (idx->q_heavy > 0 || idx->k_items > 0) ? combine_lds_bytes(sh) : 0;
-    BF_LAUNCH("attn_bwd_kv_kernel", attn_bwd_kv_kernel<T>, dim3(unsigned(kv_blocks)), dim3(kBlock), lds, st, Q, K,
-              Vv, idx->kptr, idx->kq, idx->ke, bias, factor, dO, rstat, static_cast<T*>(dq), static_cast<T*>(dk),
-              static_cast<T*>(dv), idx->k_order, qit, idx->q_heavy, kit, idx->k_items, idx->n_kv, sh, idx->chunk);
+    const bool stream_rows = size_t(idx->n_q) * size_t(sh.D) * sizeof(T) * 2 > kStreamBytes;
+#define BF_LAUNCH_KV(NT)                                                                                           \
+  BF_LAUNCH("attn_bwd_kv_kernel", (attn_bwd_kv_kernel<T, NT>), dim3(unsigned(kv_blocks)), dim3(kBlock), lds, st, Q, K, \
+            Vv, idx->kptr, idx->kq, idx->ke, bias, factor, dO, rstat, static_cast<T*>(dq), static_cast<T*>(dk),       \
+            static_cast<T*>(dv), idx->k_order, qit, idx->q_heavy, kit, idx->k_items, idx->n_kv, sh, idx->chunk)
+    if (stream_rows)
+      BF_LAUNCH_KV(true);
+    else
+      BF_LAUNCH_KV(false);
+#undef BF_LAUNCH_KV
     BF_CHECK_LAUNCH();
   }
   if (idx->k_heavy > 0) {

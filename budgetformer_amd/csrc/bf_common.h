@@ -80,6 +80,11 @@ template <> struct Elem<float> {
   static constexpr int kPerVec = 4;
   using Raw = float4;
   __device__ __forceinline__ static Raw load_raw(const float* p) { return *reinterpret_cast<const float4*>(p); }
+  __device__ __forceinline__ static Raw load_raw_nt(const float* p) {
+    typedef float V4 __attribute__((ext_vector_type(4)));
+    const V4 v = __builtin_nontemporal_load(reinterpret_cast<const V4*>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+  }
   __device__ __forceinline__ static Raw zero_raw() { return make_float4(0.f, 0.f, 0.f, 0.f); }
   __device__ __forceinline__ static void unpack(const Raw& v, float (&o)[4]) {
     o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
@@ -106,6 +111,12 @@ template <> struct Elem<uint16_t> {
   typedef __bf16 Pair __attribute__((ext_vector_type(2)));
   __device__ __forceinline__ static Pair as_pair(uint32_t w) { return __builtin_bit_cast(Pair, w); }
   __device__ __forceinline__ static Raw load_raw(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+  // non-temporal: the line is not kept in the caches (rows gathered once per pass from a table larger than them)
+  __device__ __forceinline__ static Raw load_raw_nt(const uint16_t* p) {
+    typedef unsigned V4 __attribute__((ext_vector_type(4)));
+    const V4 v = __builtin_nontemporal_load(reinterpret_cast<const V4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+  }
   __device__ __forceinline__ static Raw zero_raw() { return make_uint4(0u, 0u, 0u, 0u); }
   // acc + sum of the eight products of a and b, straight from the packed pairs
   // (v_dot2 with an fp32 accumulator; bf16 products are exact in fp32)

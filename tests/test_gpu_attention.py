@@ -222,3 +222,16 @@ def test_exphormer_typed_edges_match_oracle(hip_device):
     for got, r in ((qd.grad[0], q64.grad), (kd.grad[0], k64.grad), (vd.grad[0], v64.grad)):
         assert _rel_err(got, r) < 1e-5
     assert mod.edge_proj.weight.grad is not None and mod.edge_type_emb.weight.grad is not None
+
+
+@pytest.mark.parametrize("dtype,H,tol", [(torch.float32, 8, 1e-5), (torch.bfloat16, 16, 2e-2)])
+def test_streaming_kv_pass_on_a_table_larger_than_the_cache(hip_device, dtype, H, tol):
+    """q and dO tables above 256 MB take the non-temporal gathers of the dk/dv pass; same results."""
+    from budgetformer_amd.hip_ops import AttentionIndex
+    hn, S = 16, 300_000                                           # 2 * S * H*hn * s = 307 MB > 256 MB
+    q, k, v, ei, dout = _inputs(S, H, hn, S, seed=23, dtype=dtype)
+    idx = AttentionIndex.from_coo(ei.to(hip_device), S)
+    out, dq, dk, dv, _ = _run(hip_device, q, k, v, idx, dout)
+    ro, rZ, rdq, rdk, rdv, _ = _oracle(q, k, v, ei, dout)
+    for got, ref in ((out, ro), (dq, rdq), (dk, rdk), (dv, rdv)):
+        assert _rel_err(got, ref) < tol
