@@ -45,32 +45,40 @@ __global__ void row_lengths_kernel(const int32_t* __restrict__ row_len, int64_t 
   lens[t] = len;
 }
 
+// Writes entry pos of query row `row`: kv, and (row << 32 | pos) when the
+// caller wants the reverse index's sort values produced here.
+__device__ __forceinline__ void put_entry(int32_t* __restrict__ kv, uint64_t* __restrict__ rowpos, int64_t pos,
+                                          int64_t row, int32_t id) {
+  kv[pos] = id;
+  if (rowpos) rowpos[pos] = (uint64_t(uint32_t(row)) << 32) | uint32_t(pos);
+}
+
+// One thread per table slot, then (with the Graphormer token) one thread per
+// query for the token row: query 0 lists kv 1..n_rows, and query r+1 starts
+// with kv 0 followed by its table row shifted by one.
 __global__ void table_fill_kernel(const int32_t* __restrict__ table, const int32_t* __restrict__ row_len,
                                   int64_t n_rows, int width, int token, const int64_t* __restrict__ qptr,
-                                  int32_t* __restrict__ kv) {
-  // one thread per table slot; token row 0 is filled by token_row_kernel
+                                  int32_t* __restrict__ kv, uint64_t* __restrict__ rowpos) {
   const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
-  if (i >= n_rows * width) return;
+  const int64_t slots = n_rows * width;
+  if (i >= slots) {
+    const int64_t t = i - slots;
+    if (!token || t >= n_rows) return;
+    put_entry(kv, rowpos, t, 0, int32_t(t + 1));
+    if (row_len[t] == 0) put_entry(kv, rowpos, qptr[t + 1], t + 1, 0);
+    return;
+  }
   const int64_t r = i / width;
   const int c = int(i - r * width);
   const int len = row_len[r];
   if (c >= len) return;
   if (token) {
     const int64_t base = qptr[r + 1];  // query r+1
-    if (c == 0) kv[base] = 0;
-    kv[base + 1 + c] = table[i] + 1;
+    if (c == 0) put_entry(kv, rowpos, base, r + 1, 0);
+    put_entry(kv, rowpos, base + 1 + c, r + 1, table[i] + 1);
   } else {
-    kv[qptr[r] + c] = table[i];
+    put_entry(kv, rowpos, qptr[r] + c, r, table[i]);
   }
-}
-
-__global__ void token_fill_kernel(const int32_t* __restrict__ row_len, int64_t n_rows,
-                                  const int64_t* __restrict__ qptr, int32_t* __restrict__ kv) {
-  // query 0 lists kv 1..n_rows; rows with len 0 still get their kv-0 entry
-  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
-  if (i >= n_rows) return;
-  kv[i] = int32_t(i + 1);
-  if (row_len[i] == 0) kv[qptr[i + 1]] = 0;
 }
 
 // ---------------------------------------------------------------- sorted keys -> row pointers
@@ -139,14 +147,55 @@ __global__ void unpack_row_entry_kernel(const uint64_t* __restrict__ vals, int64
   ke[i] = int32_t(uint32_t(x));
 }
 
-// Sort key placing long rows first: 255 - min(len, 255).
-__global__ void length_keys_kernel(const int64_t* __restrict__ ptr, int64_t n_rows, uint8_t* __restrict__ keys,
-                                   int32_t* __restrict__ ids) {
-  const int64_t r = int64_t(blockIdx.x) * kThreads + threadIdx.x;
-  if (r >= n_rows) return;
+// Row order, longest first: bucket 255 - min(len, 255), counted per block in
+// LDS and reserved per block with one global atomic per bucket. Rows of one
+// bucket come out in an arbitrary order: the order only decides which group
+// serves which row, never a row's arithmetic.
+constexpr int kBuckets = 256;
+static_assert(kBuckets == kThreads, "the order kernels keep one bucket per thread");
+
+__device__ __forceinline__ int length_bucket(const int64_t* __restrict__ ptr, int64_t r) {
   const int64_t len = ptr[r + 1] - ptr[r];
-  keys[r] = uint8_t(255 - (len < 255 ? len : 255));
-  ids[r] = int32_t(r);
+  return 255 - int(len < 255 ? len : 255);
+}
+
+__global__ __launch_bounds__(kThreads) void order_hist_kernel(const int64_t* __restrict__ ptr, int64_t n_rows,
+                                                              uint32_t* __restrict__ hist) {
+  __shared__ uint32_t h[kBuckets];
+  h[threadIdx.x] = 0;
+  __syncthreads();
+  for (int64_t r = int64_t(blockIdx.x) * kThreads + threadIdx.x; r < n_rows; r += int64_t(gridDim.x) * kThreads)
+    atomicAdd(&h[length_bucket(ptr, r)], 1u);
+  __syncthreads();
+  if (h[threadIdx.x]) atomicAdd(&hist[threadIdx.x], h[threadIdx.x]);
+}
+
+__global__ __launch_bounds__(kThreads) void order_scatter_kernel(const int64_t* __restrict__ ptr, int64_t n_rows,
+                                                                 const uint32_t* __restrict__ hist,
+                                                                 uint32_t* __restrict__ cursor,
+                                                                 int32_t* __restrict__ order) {
+  __shared__ uint32_t base[kBuckets];
+  __shared__ uint32_t cnt[kBuckets];
+  const int tid = threadIdx.x;
+  base[tid] = hist[tid];
+  cnt[tid] = 0;
+  __syncthreads();
+  for (int o = 1; o < kBuckets; o <<= 1) {      // inclusive scan of the bucket sizes
+    const uint32_t x = tid >= o ? base[tid - o] : 0u;
+    __syncthreads();
+    base[tid] += x;
+    __syncthreads();
+  }
+  const uint32_t start = tid ? base[tid - 1] : 0u;
+  __syncthreads();
+  base[tid] = start;
+  const int64_t r = int64_t(blockIdx.x) * kThreads + tid;
+  const int b = r < n_rows ? length_bucket(ptr, r) : 0;
+  const uint32_t rank = r < n_rows ? atomicAdd(&cnt[b], 1u) : 0u;
+  __syncthreads();
+  if (cnt[tid]) base[tid] += atomicAdd(&cursor[tid], cnt[tid]);
+  __syncthreads();
+  if (r < n_rows) order[base[b] + rank] = int32_t(r);
 }
 
 struct MaxOp {
@@ -171,27 +220,34 @@ int row_ids(const int64_t* ptr, int64_t n_rows, int64_t nnz, int32_t* marks, int
 }
 
 // ---------------------------------------------------------------- split plans
+// Per row: its item count, and (items << 32 | is_heavy) so that ONE exclusive
+// scan yields both the first item and the heavy-list slot of every row.
 __global__ void split_count_kernel(const int64_t* __restrict__ ptr, int64_t n_rows, int threshold, int item_size,
-                                   int32_t* __restrict__ nitems, int32_t* __restrict__ heavy_flag) {
+                                   int32_t* __restrict__ nitems, uint64_t* __restrict__ packed) {
   const int64_t r = int64_t(blockIdx.x) * kThreads + threadIdx.x;
   if (r >= n_rows) return;
   const int64_t len = ptr[r + 1] - ptr[r];
   const bool heavy = len > threshold;
-  nitems[r] = heavy ? int32_t(ceil_div(len, item_size)) : 0;
-  heavy_flag[r] = heavy ? 1 : 0;
+  const uint32_t n = heavy ? uint32_t(ceil_div(len, item_size)) : 0u;
+  nitems[r] = int32_t(n);
+  packed[r] = (uint64_t(n) << 32) | (heavy ? 1u : 0u);
 }
 
-// Heavy-row list (compacted by the scan of the flags) and the two plan counts.
-__global__ void split_rows_kernel(const int32_t* __restrict__ nitems, const int32_t* __restrict__ item_off,
-                                  const int32_t* __restrict__ heavy_off, int64_t n_rows, int64_t item_cap,
+// item_off, the heavy-row list (compacted by the scanned flags) and the two plan counts.
+__global__ void split_rows_kernel(const int32_t* __restrict__ nitems, const uint64_t* __restrict__ packed_off,
+                                  int64_t n_rows, int64_t item_cap, int32_t* __restrict__ item_off,
                                   int32_t* __restrict__ heavy_rows, int64_t heavy_cap, int32_t* __restrict__ counts) {
   const int64_t r = int64_t(blockIdx.x) * kThreads + threadIdx.x;
   if (r >= n_rows) return;
   const int n = nitems[r];
-  if (n > 0 && heavy_off[r] < heavy_cap) heavy_rows[heavy_off[r]] = int32_t(r);
+  const uint64_t off = packed_off[r];
+  const int64_t first_item = int64_t(off >> 32);
+  const int64_t slot = int64_t(uint32_t(off));
+  item_off[r] = int32_t(first_item);
+  if (n > 0 && slot < heavy_cap) heavy_rows[slot] = int32_t(r);
   if (r == n_rows - 1) {
-    const int64_t items = int64_t(item_off[r]) + n;
-    const int64_t heavy = int64_t(heavy_off[r]) + (n > 0 ? 1 : 0);
+    const int64_t items = first_item + n;
+    const int64_t heavy = slot + (n > 0 ? 1 : 0);
     counts[0] = int32_t(items < item_cap ? items : item_cap);
     counts[1] = int32_t(heavy < heavy_cap ? heavy : heavy_cap);
   }
@@ -247,18 +303,14 @@ extern "C" int bf_table_csr_ptr(const int32_t* row_len, int64_t n_rows, int32_t 
 }
 
 extern "C" int bf_table_to_csr(const int32_t* table, const int32_t* row_len, int64_t n_rows, int32_t width,
-                               int32_t global_token, const int64_t* qptr, int32_t* kv, void* stream) {
+                               int32_t global_token, const int64_t* qptr, int32_t* kv, uint64_t* rowpos,
+                               void* stream) {
   BF_CHECK_ARG(n_rows >= 0 && width >= 0 && qptr, "table_to_csr: bad arguments");
   BF_CHECK_ARG(n_rows == 0 || (table && row_len && kv), "table_to_csr: null tensor");
-  hipStream_t st = as_stream(stream);
-  if (n_rows * width > 0) {
-    BF_LAUNCH("table_fill_kernel", table_fill_kernel, dim3(blocks_for(n_rows * width)), dim3(kThreads), 0, st, table,
-              row_len, n_rows, width, int(global_token != 0), qptr, kv);
-    BF_CHECK_LAUNCH();
-  }
-  if (global_token && n_rows > 0) {
-    BF_LAUNCH("token_fill_kernel", token_fill_kernel, dim3(blocks_for(n_rows)), dim3(kThreads), 0, st, row_len,
-              n_rows, qptr, kv);
+  const int64_t threads = n_rows * width + (global_token ? n_rows : 0);
+  if (threads > 0) {
+    BF_LAUNCH("table_fill_kernel", table_fill_kernel, dim3(blocks_for(threads)), dim3(kThreads), 0, as_stream(stream),
+              table, row_len, n_rows, width, int(global_token != 0), qptr, kv, rowpos);
     BF_CHECK_LAUNCH();
   }
   return BF_OK;
@@ -360,6 +412,50 @@ extern "C" int bf_reverse_index(const int64_t* qptr, const int32_t* kv, int64_t 
   return BF_OK;
 }
 
+extern "C" int bf_reverse_index_packed_workspace_size(int64_t nnz, int64_t n_kv, size_t* bytes) {
+  BF_CHECK_ARG(bytes && nnz >= 0 && n_kv >= 0, "reverse_index_packed_workspace_size: bad arguments");
+  size_t sort_bytes = 0;
+  const int n = int(nnz > 0 ? nnz : 1);
+  (void)hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, static_cast<const uint32_t*>(nullptr),
+                                           static_cast<uint32_t*>(nullptr), static_cast<const uint64_t*>(nullptr),
+                                           static_cast<uint64_t*>(nullptr), n);
+  *bytes = align_up(size_t(n) * 4) + align_up(size_t(n) * 8) + align_up(sort_bytes) + 256;
+  return BF_OK;
+}
+
+extern "C" int bf_reverse_index_packed(const int32_t* kv, const uint64_t* rowpos, int64_t nnz, int64_t n_kv,
+                                       int64_t* kptr, int32_t* kq, int32_t* ke, void* workspace,
+                                       size_t workspace_bytes, void* stream) {
+  BF_CHECK_ARG(kptr && n_kv >= 0 && nnz >= 0, "reverse_index_packed: bad arguments");
+  BF_CHECK_ARG(nnz < (int64_t(1) << 31), "reverse_index_packed: sizes must fit int32");
+  size_t need = 0;
+  bf_reverse_index_packed_workspace_size(nnz, n_kv, &need);
+  BF_CHECK_ARG(workspace && workspace_bytes >= need, "reverse_index_packed: workspace %zu < %zu bytes",
+               workspace_bytes, need);
+  hipStream_t st = as_stream(stream);
+  if (nnz == 0) {
+    BF_CHECK_HIP(hipMemsetAsync(kptr, 0, size_t(n_kv + 1) * sizeof(int64_t), st));
+    return BF_OK;
+  }
+  BF_CHECK_ARG(kv && rowpos && kq && ke, "reverse_index_packed: null tensor");
+  char* p = static_cast<char*>(workspace);
+  auto take = [&](size_t b) { char* q = p; p += align_up(b); return q; };
+  auto* keys_out = reinterpret_cast<uint32_t*>(take(size_t(nnz) * 4));
+  auto* vals_out = reinterpret_cast<uint64_t*>(take(size_t(nnz) * 8));
+  void* temp = p;
+  size_t tb = workspace_bytes - size_t(p - static_cast<char*>(workspace));
+  const int end_bit = bits_for(uint64_t(n_kv > 0 ? n_kv : 1));
+  BF_CHECK_HIP(hipcub::DeviceRadixSort::SortPairs(temp, tb, reinterpret_cast<const uint32_t*>(kv), keys_out, rowpos,
+                                                  vals_out, int(nnz), 0, end_bit, st));
+  BF_LAUNCH("boundaries_kernel", boundaries_kernel<uint32_t>, dim3(blocks_for(nnz + 1)), dim3(kThreads), 0, st, keys_out,
+            nnz, uint64_t(1), n_kv, kptr);
+  BF_CHECK_LAUNCH();
+  BF_LAUNCH("unpack_row_entry_kernel", unpack_row_entry_kernel, dim3(blocks_for(nnz)), dim3(kThreads), 0, st, vals_out,
+            nnz, kq, ke);
+  BF_CHECK_LAUNCH();
+  return BF_OK;
+}
+
 extern "C" int bf_expand_rows(const int64_t* ptr, int64_t n_rows, int64_t nnz, int64_t* rows, void* stream) {
   BF_CHECK_ARG(ptr && n_rows >= 0 && nnz >= 0 && (rows || nnz == 0), "expand_rows: bad arguments");
   BF_CHECK_ARG(nnz == 0 || n_rows > 0, "expand_rows: entries without rows");
@@ -384,9 +480,9 @@ extern "C" int64_t bf_split_row_capacity(int64_t nnz, int32_t threshold) {
 extern "C" int bf_split_plan_workspace_size(int64_t n_rows, size_t* bytes) {
   BF_CHECK_ARG(bytes && n_rows >= 0, "split_plan_workspace_size: bad arguments");
   size_t temp_bytes = 0;
-  (void)hipcub::DeviceScan::ExclusiveSum(nullptr, temp_bytes, static_cast<const int32_t*>(nullptr),
-                                         static_cast<int32_t*>(nullptr), int(n_rows > 0 ? n_rows : 1));
-  *bytes = 2 * align_up(size_t(n_rows > 0 ? n_rows : 1) * 4) + align_up(temp_bytes) + 256;
+  (void)hipcub::DeviceScan::ExclusiveSum(nullptr, temp_bytes, static_cast<const uint64_t*>(nullptr),
+                                         static_cast<uint64_t*>(nullptr), int(n_rows > 0 ? n_rows : 1));
+  *bytes = 2 * align_up(size_t(n_rows > 0 ? n_rows : 1) * 8) + align_up(temp_bytes) + 256;
   return BF_OK;
 }
 
@@ -399,26 +495,27 @@ extern "C" int bf_split_plan(const int64_t* ptr, int64_t n_rows, int32_t thresho
                "split_plan: bad capacity");
   BF_CHECK_ARG(n_rows < (int64_t(1) << 31), "split_plan: too many rows");
   hipStream_t st = as_stream(stream);
-  BF_CHECK_HIP(hipMemsetAsync(counts, 0, 2 * sizeof(int32_t), st));
-  if (n_rows == 0) return BF_OK;
+  if (n_rows == 0) {
+    BF_CHECK_HIP(hipMemsetAsync(counts, 0, 2 * sizeof(int32_t), st));
+    return BF_OK;
+  }
   BF_CHECK_ARG(nitems && item_off && (item_row || item_cap == 0) && (heavy_rows || heavy_cap == 0),
                "split_plan: null tensor");
   size_t need = 0;
   bf_split_plan_workspace_size(n_rows, &need);
   BF_CHECK_ARG(workspace && workspace_bytes >= need, "split_plan: workspace %zu < %zu bytes", workspace_bytes, need);
-  const size_t slab = align_up(size_t(n_rows) * 4);
-  auto* heavy_flag = static_cast<int32_t*>(workspace);
-  auto* heavy_off = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + slab);
+  const size_t slab = align_up(size_t(n_rows) * 8);
+  auto* packed = static_cast<uint64_t*>(workspace);
+  auto* packed_off = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + slab);
   void* temp = static_cast<char*>(workspace) + 2 * slab;
   size_t temp_bytes = 0;
-  (void)hipcub::DeviceScan::ExclusiveSum(nullptr, temp_bytes, nitems, item_off, int(n_rows));
+  (void)hipcub::DeviceScan::ExclusiveSum(nullptr, temp_bytes, packed, packed_off, int(n_rows));
   BF_LAUNCH("split_count_kernel", split_count_kernel, dim3(blocks_for(n_rows)), dim3(kThreads), 0, st, ptr, n_rows,
-            threshold, item_size, nitems, heavy_flag);
+            threshold, item_size, nitems, packed);
   BF_CHECK_LAUNCH();
-  BF_CHECK_HIP(hipcub::DeviceScan::ExclusiveSum(temp, temp_bytes, nitems, item_off, int(n_rows), st));
-  BF_CHECK_HIP(hipcub::DeviceScan::ExclusiveSum(temp, temp_bytes, heavy_flag, heavy_off, int(n_rows), st));
-  BF_LAUNCH("split_rows_kernel", split_rows_kernel, dim3(blocks_for(n_rows)), dim3(kThreads), 0, st, nitems, item_off,
-            heavy_off, n_rows, item_cap, heavy_rows, heavy_cap, counts);
+  BF_CHECK_HIP(hipcub::DeviceScan::ExclusiveSum(temp, temp_bytes, packed, packed_off, int(n_rows), st));
+  BF_LAUNCH("split_rows_kernel", split_rows_kernel, dim3(blocks_for(n_rows)), dim3(kThreads), 0, st, nitems,
+            packed_off, n_rows, item_cap, item_off, heavy_rows, heavy_cap, counts);
   BF_CHECK_LAUNCH();
   if (item_cap > 0) {
     BF_LAUNCH("split_items_kernel", split_items_kernel, dim3(blocks_for(item_cap)), dim3(kThreads), 0, st, item_off,
@@ -587,12 +684,7 @@ extern "C" int bf_coalesce(const int64_t* src, const int64_t* dst, int64_t nnz, 
 
 extern "C" int bf_row_order_workspace_size(int64_t n_rows, size_t* bytes) {
   BF_CHECK_ARG(bytes && n_rows >= 0, "row_order_workspace_size: bad arguments");
-  size_t sort_bytes = 0;
-  const int n = int(n_rows > 0 ? n_rows : 1);
-  (void)hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, static_cast<const uint8_t*>(nullptr),
-                                           static_cast<uint8_t*>(nullptr), static_cast<const int32_t*>(nullptr),
-                                           static_cast<int32_t*>(nullptr), n);
-  *bytes = 2 * align_up(size_t(n)) + align_up(size_t(n) * 4) + align_up(sort_bytes) + 256;
+  *bytes = 2 * kBuckets * sizeof(uint32_t) + 256;
   return BF_OK;
 }
 
@@ -605,16 +697,15 @@ extern "C" int bf_row_order(const int64_t* ptr, int64_t n_rows, int32_t* order, 
   bf_row_order_workspace_size(n_rows, &need);
   BF_CHECK_ARG(workspace && workspace_bytes >= need, "row_order: workspace %zu < %zu bytes", workspace_bytes, need);
   hipStream_t st = as_stream(stream);
-  char* p = static_cast<char*>(workspace);
-  auto take = [&](size_t b) { char* q = p; p += align_up(b); return q; };
-  auto* keys_in = reinterpret_cast<uint8_t*>(take(size_t(n_rows)));
-  auto* keys_out = reinterpret_cast<uint8_t*>(take(size_t(n_rows)));
-  auto* ids = reinterpret_cast<int32_t*>(take(size_t(n_rows) * 4));
-  void* temp = p;
-  size_t tb = workspace_bytes - size_t(p - static_cast<char*>(workspace));
-  BF_LAUNCH("length_keys_kernel", length_keys_kernel, dim3(blocks_for(n_rows)), dim3(kThreads), 0, st, ptr, n_rows,
-            keys_in, ids);
+  auto* hist = static_cast<uint32_t*>(workspace);
+  uint32_t* cursor = hist + kBuckets;
+  BF_CHECK_HIP(hipMemsetAsync(hist, 0, 2 * kBuckets * sizeof(uint32_t), st));
+  const int64_t blocks = blocks_for(n_rows);
+  BF_LAUNCH("order_hist_kernel", order_hist_kernel, dim3(unsigned(blocks < 2048 ? blocks : 2048)), dim3(kThreads), 0,
+            st, ptr, n_rows, hist);
   BF_CHECK_LAUNCH();
-  BF_CHECK_HIP(hipcub::DeviceRadixSort::SortPairs(temp, tb, keys_in, keys_out, ids, order, int(n_rows), 0, 8, st));
+  BF_LAUNCH("order_scatter_kernel", order_scatter_kernel, dim3(unsigned(blocks)), dim3(kThreads), 0, st, ptr, n_rows,
+            hist, cursor, order);
+  BF_CHECK_LAUNCH();
   return BF_OK;
 }

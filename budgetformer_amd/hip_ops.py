@@ -320,8 +320,9 @@ def build_edge_table(rowptr, col, in_ptr, in_src, num_edges: int, q_lo: int, n_q
 
 
 # ------------------------------------------------------------------ index formats
-def table_to_csr(table: torch.Tensor, row_len: torch.Tensor, global_token: bool = False):
-    """Query-major table -> (qptr [n_q+1] int64, kv [nnz] int32)."""
+def table_to_csr(table: torch.Tensor, row_len: torch.Tensor, global_token: bool = False, with_rowpos: bool = False):
+    """Query-major table -> (qptr [n_q+1] int64, kv [nnz] int32), plus rowpos (uint64 as int64 [nnz],
+    (query << 32 | position)) with ``with_rowpos``: the reverse index's sort values."""
     dev = table.device
     _require(table, "table", torch.int32)
     _require(row_len, "row_len", torch.int32, dev)
@@ -333,9 +334,10 @@ def table_to_csr(table: torch.Tensor, row_len: torch.Tensor, global_token: bool 
     N.call("bf_table_csr_ptr", _p(row_len), n_rows, int(global_token), _p(qptr), C.byref(nnz), _p(ws), ws.numel(),
            _stream(dev))
     kv = torch.empty(max(nnz.value, 1), dtype=torch.int32, device=dev)[: nnz.value]
+    rowpos = torch.empty(max(nnz.value, 1), dtype=torch.int64, device=dev)[: nnz.value] if with_rowpos else None
     N.call("bf_table_to_csr", _p(table), _p(row_len), n_rows, width, int(global_token), _p(qptr), _p(kv),
-           _stream(dev))
-    return qptr, kv
+           _p(rowpos), _stream(dev))
+    return (qptr, kv, rowpos) if with_rowpos else (qptr, kv)
 
 
 def coo_to_csr(edge_index: torch.Tensor, n_q: int, n_kv: int):
@@ -372,6 +374,23 @@ def reverse_index(qptr: torch.Tensor, kv: torch.Tensor, n_kv: int):
     return kptr, kq, ke
 
 
+def reverse_index_packed(kv: torch.Tensor, rowpos: torch.Tensor, n_kv: int):
+    """reverse_index from table_to_csr's rowpos (one sort, no row recovery)."""
+    dev = kv.device
+    _require(kv, "kv", torch.int32)
+    _require(rowpos, "rowpos", torch.int64, dev)
+    nnz = kv.numel()
+    if rowpos.numel() != nnz:
+        raise ValueError("rowpos must have one value per entry")
+    ws = _workspace(_size_query("bf_reverse_index_packed_workspace_size", nnz, n_kv), dev)
+    kptr = torch.empty(n_kv + 1, dtype=torch.int64, device=dev)
+    kq = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)[:nnz]
+    ke = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)[:nnz]
+    N.call("bf_reverse_index_packed", _p(kv), _p(rowpos), nnz, n_kv, _p(kptr), _p(kq), _p(ke), _p(ws), ws.numel(),
+           _stream(dev))
+    return kptr, kq, ke
+
+
 def expand_rows(ptr: torch.Tensor, nnz: int) -> torch.Tensor:
     """Row id (int64) of every CSR entry."""
     _require(ptr, "ptr", torch.int64)
@@ -391,16 +410,31 @@ def row_order(ptr: torch.Tensor) -> torch.Tensor:
 
 @dataclass
 class SplitPlan:
-    """Rows longer than `threshold` cut into `item_size`-entry items (host-known counts)."""
+    """Rows longer than `threshold` cut into `item_size`-entry items.
+
+    ``items`` / ``heavy`` are host ints once resolved (-1 while ``counts``, the
+    device copy, is still pending: several plans resolve with one read)."""
     items: int
     heavy: int
     nitems: torch.Tensor
     item_off: torch.Tensor
     item_row: torch.Tensor
     heavy_rows: torch.Tensor
+    counts: Optional[torch.Tensor] = None
 
 
-def split_plan(ptr: torch.Tensor, nnz: int, threshold: int = DEFAULT_CHUNK, item_size: int = DEFAULT_ITEM) -> SplitPlan:
+def resolve_plans(*plans) -> None:
+    """Read the counts of every pending plan with a single device-to-host copy."""
+    pending = [p for p in plans if p is not None and p.items < 0]
+    if not pending:
+        return
+    vals = (pending[0].counts if len(pending) == 1 else torch.cat([p.counts for p in pending])).cpu().tolist()
+    for i, p in enumerate(pending):
+        p.items, p.heavy, p.counts = int(vals[2 * i]), int(vals[2 * i + 1]), None
+
+
+def split_plan(ptr: torch.Tensor, nnz: int, threshold: int = DEFAULT_CHUNK, item_size: int = DEFAULT_ITEM,
+               resolve: bool = True) -> SplitPlan:
     dev = ptr.device
     lib = N.load()
     n_rows = ptr.numel() - 1
@@ -410,12 +444,14 @@ def split_plan(ptr: torch.Tensor, nnz: int, threshold: int = DEFAULT_CHUNK, item
     item_off = torch.empty(max(n_rows, 1), dtype=torch.int32, device=dev)
     item_row = torch.empty(max(item_cap, 1), dtype=torch.int32, device=dev)
     heavy_rows = torch.empty(max(heavy_cap, 1), dtype=torch.int32, device=dev)
-    counts = torch.zeros(2, dtype=torch.int32, device=dev)
+    counts = torch.empty(2, dtype=torch.int32, device=dev)
     ws = _workspace(_size_query("bf_split_plan_workspace_size", n_rows), dev)
     N.call("bf_split_plan", _p(ptr), n_rows, threshold, item_size, _p(nitems), _p(item_off), _p(item_row), item_cap,
            _p(heavy_rows), heavy_cap, _p(counts), _p(ws), ws.numel(), _stream(dev))
-    items, heavy = (int(x) for x in counts.cpu().tolist())
-    return SplitPlan(items, heavy, nitems, item_off, item_row, heavy_rows)
+    plan = SplitPlan(-1, -1, nitems, item_off, item_row, heavy_rows, counts)
+    if resolve:
+        resolve_plans(plan)
+    return plan
 
 
 # ------------------------------------------------------------------ attention index
@@ -440,6 +476,7 @@ class AttentionIndex:
     kplan: Optional[SplitPlan] = None
     korder: Optional[torch.Tensor] = None
     _rows: Optional[torch.Tensor] = field(default=None, repr=False)
+    _rowpos: Optional[torch.Tensor] = field(default=None, repr=False)   # from_table: sort values, until used
 
     @property
     def nnz(self) -> int:
@@ -452,16 +489,23 @@ class AttentionIndex:
     def ensure_forward(self):
         if self.qplan is None:
             self.qplan = split_plan(self.qptr, self.nnz, self.chunk, self.item)
+        resolve_plans(self.qplan)
         return self
 
     def ensure_backward(self):
-        self.ensure_forward()
+        if self.qplan is None:
+            self.qplan = split_plan(self.qptr, self.nnz, self.chunk, self.item, resolve=False)
         if self.kptr is None:
-            self.kptr, self.kq, self.ke = reverse_index(self.qptr, self.kv, self.n_kv)
+            if self._rowpos is not None:
+                self.kptr, self.kq, self.ke = reverse_index_packed(self.kv, self._rowpos, self.n_kv)
+                self._rowpos = None
+            else:
+                self.kptr, self.kq, self.ke = reverse_index(self.qptr, self.kv, self.n_kv)
         if self.kplan is None:
-            self.kplan = split_plan(self.kptr, self.nnz, self.chunk, self.item)
+            self.kplan = split_plan(self.kptr, self.nnz, self.chunk, self.item, resolve=False)
         if self.korder is None:
             self.korder = row_order(self.kptr)
+        resolve_plans(self.qplan, self.kplan)      # both plans' counts in one read
         return self
 
     def entry_rows(self) -> torch.Tensor:
@@ -500,9 +544,10 @@ class AttentionIndex:
     @classmethod
     def from_table(cls, table, row_len, global_token: bool = False, n_kv: Optional[int] = None,
                    chunk: int = DEFAULT_CHUNK, item: int = DEFAULT_ITEM):
-        qptr, kv = table_to_csr(table, row_len, global_token)
+        qptr, kv, rowpos = table_to_csr(table, row_len, global_token, with_rowpos=True)
         n_q = qptr.numel() - 1
-        return cls(n_q=n_q, n_kv=n_kv if n_kv is not None else n_q, qptr=qptr, kv=kv, chunk=chunk, item=item)
+        return cls(n_q=n_q, n_kv=n_kv if n_kv is not None else n_q, qptr=qptr, kv=kv, chunk=chunk, item=item,
+                   _rowpos=rowpos)
 
     @classmethod
     def from_coo(cls, edge_index, n_q: int, n_kv: Optional[int] = None, chunk: int = DEFAULT_CHUNK,

@@ -236,12 +236,15 @@ int bf_chung_lu(int64_t num_nodes, int64_t pairs, double exponent, double i0, do
  * every query t >= 1 also attends to kv 0; then n_q = n_rows + 1.
  * bf_table_csr_ptr writes qptr (a prefix sum of the row lengths) and returns
  * nnz = qptr[n_q] on the host (it synchronises the stream, so the caller can
- * size kv); bf_table_to_csr then fills kv. Workspace: bf_scan_workspace_size(n_q). */
+ * size kv); bf_table_to_csr then fills kv, and, when rowpos is not NULL,
+ * rowpos uint64 [nnz] = (query << 32 | position) per entry: the sort values
+ * bf_reverse_index_packed takes. Workspace: bf_scan_workspace_size(n_q).    */
 int bf_scan_workspace_size(int64_t n, size_t* bytes);
 int bf_table_csr_ptr(const int32_t* row_len, int64_t n_rows, int32_t global_token, int64_t* qptr,
                      int64_t* nnz_host, void* workspace, size_t workspace_bytes, void* stream);
 int bf_table_to_csr(const int32_t* table, const int32_t* row_len, int64_t n_rows, int32_t width,
-                    int32_t global_token, const int64_t* qptr, int32_t* kv, void* stream);
+                    int32_t global_token, const int64_t* qptr, int32_t* kv, uint64_t* rowpos,
+                    void* stream);
 
 /* Reference COO edge_index [2, nnz] (row 0 = key/value node, row 1 = query
  * node; models/graphormer_dist_node_level.py:231-232) -> attention CSR with
@@ -270,6 +273,15 @@ int bf_reverse_index(const int64_t* qptr, const int32_t* kv, int64_t n_q, int64_
                      int64_t* kptr, int32_t* kq, int32_t* ke,
                      void* workspace, size_t workspace_bytes, void* stream);
 
+/* bf_reverse_index when the (query << 32 | position) value of every entry is
+ * already at hand (bf_table_to_csr's rowpos): the same kptr / kq / ke from
+ * one sort, without recovering the rows. Workspace:
+ * bf_reverse_index_packed_workspace_size.                                   */
+int bf_reverse_index_packed_workspace_size(int64_t nnz, int64_t n_kv, size_t* bytes);
+int bf_reverse_index_packed(const int32_t* kv, const uint64_t* rowpos, int64_t nnz, int64_t n_kv,
+                            int64_t* kptr, int32_t* kq, int32_t* ke, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
 /* Row id of every entry of a CSR (rows[i] = r for ptr[r] <= i < ptr[r+1]). */
 int bf_expand_rows(const int64_t* ptr, int64_t n_rows, int64_t nnz, int64_t* rows, void* stream);
 
@@ -288,10 +300,11 @@ int bf_split_plan(const int64_t* ptr, int64_t n_rows, int32_t threshold, int32_t
                   int32_t* heavy_rows, int64_t heavy_cap, int32_t* counts,
                   void* workspace, size_t workspace_bytes, void* stream);
 
-/* Rows of a CSR ordered longest-first (lengths capped at 255; ties in row
- * order). The key-major attention pass walks its rows in this order so the
- * groups sharing a wavefront carry similar work. Workspace:
- * bf_row_order_workspace_size.                                              */
+/* Rows of a CSR ordered longest-first (lengths capped at 255; rows of equal
+ * capped length in an unspecified order that may change from call to call).
+ * The key-major attention pass walks its rows in this order so the groups
+ * sharing a wavefront carry similar work; a row's arithmetic does not depend
+ * on its place. Workspace: bf_row_order_workspace_size.                     */
 int bf_row_order_workspace_size(int64_t n_rows, size_t* bytes);
 int bf_row_order(const int64_t* ptr, int64_t n_rows, int32_t* order, void* workspace,
                  size_t workspace_bytes, void* stream);

@@ -211,3 +211,51 @@ def test_light_heavy_split_bit_exact(hip_device, b_r, b_w):
     tab = build_attention_edges(g, real_edges_per_query=b_r, rw_edges_per_query=b_w, walk_length=L,
                                 walks_per_node=P, edge_seed=42, u=ut[300 * P:2300 * P], q_lo=300, n_q=2000)
     assert np.array_equal(tab.table.cpu().numpy(), ref_t[300:2300])
+
+
+@pytest.mark.parametrize("token", [False, True])
+def test_index_formats_against_numpy(hip_device, token):
+    """table -> CSR (with the fused token fill), both reverse-index routes, the split plan and the row order."""
+    from budgetformer_amd import hip_ops
+    rng = np.random.default_rng(11 + token)
+    n, width = 5000, 6
+    row_len = rng.integers(0, width + 1, n).astype(np.int32)
+    table = np.full((n, width), -1, dtype=np.int32)
+    for r in range(n):
+        table[r, :row_len[r]] = np.sort(rng.choice(n // 3 if r % 7 else 40, row_len[r], replace=False))
+    t, rl = torch.from_numpy(table).to(hip_device), torch.from_numpy(row_len).to(hip_device)
+    qptr, kv, rowpos = hip_ops.table_to_csr(t, rl, token, with_rowpos=True)
+    # numpy CSR of the same table
+    rows, vals = [], []
+    if token:
+        rows += [0] * n
+        vals += list(range(1, n + 1))
+    for r in range(n):
+        q = r + 1 if token else r
+        ids = ([0] if token else []) + [int(x) + (1 if token else 0) for x in table[r, :row_len[r]]]
+        rows += [q] * len(ids)
+        vals += ids
+    n_q = n + (1 if token else 0)
+    assert np.array_equal(kv.cpu().numpy(), np.array(vals, dtype=np.int32))
+    assert np.array_equal(np.diff(qptr.cpu().numpy()), np.bincount(np.array(rows), minlength=n_q))
+    pos = np.arange(len(vals))
+    assert np.array_equal(rowpos.cpu().numpy(), (np.array(rows, dtype=np.int64) << 32) | pos)
+    a = hip_ops.reverse_index(qptr, kv, n_q)
+    b = hip_ops.reverse_index_packed(kv, rowpos, n_q)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+    order = np.lexsort((pos, np.array(vals)))                    # (kv, position) order
+    assert np.array_equal(b[1].cpu().numpy(), np.array(rows)[order]) and np.array_equal(b[2].cpu().numpy(), order)
+    # row order: a permutation, capped lengths non-increasing
+    ro = hip_ops.row_order(b[0]).cpu().numpy()
+    lens = np.minimum(np.diff(b[0].cpu().numpy()), 255)
+    assert np.array_equal(np.sort(ro), np.arange(n_q)) and (np.diff(lens[ro]) <= 0).all()
+    # split plan (threshold 4, items of 5) against a direct count
+    plan = hip_ops.split_plan(b[0], kv.numel(), 4, 5)
+    L = np.diff(b[0].cpu().numpy())
+    heavy = np.nonzero(L > 4)[0]
+    assert plan.heavy == heavy.size and np.array_equal(plan.heavy_rows[:plan.heavy].cpu().numpy(), heavy)
+    nit = np.where(L > 4, -(-L // 5), 0)
+    assert plan.items == nit.sum() and np.array_equal(plan.nitems[:n_q].cpu().numpy(), nit)
+    assert np.array_equal(plan.item_off[:n_q].cpu().numpy(), np.concatenate([[0], np.cumsum(nit)[:-1]]))
+    assert np.array_equal(plan.item_row[:plan.items].cpu().numpy(), np.repeat(np.arange(n_q), nit))
