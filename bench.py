@@ -297,7 +297,8 @@ def main(argv=None):
         pool_edges += cnt * cfg["P"] + int((walks[:, 2:] != walks[:, 1:-1]).sum().item())
         del walks
     rw_ms = kernels.get("rw_select_kernel", {}).get("avg_ms")
-    merge_ms = kernels.get("real_select_merge_kernel", {}).get("avg_ms")
+    # real-edge top-k + merge: the fused light/heavy kernel, or the hub + group kernels
+    merge_ms = sum(r["avg_ms"] for n_, r in kernels.items() if n_.startswith("real_select")) or None
     table_entries = int(tab.row_len.sum().item())
 
     result = {

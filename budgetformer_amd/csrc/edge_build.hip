@@ -161,6 +161,10 @@ __global__ __launch_bounds__(kThreads) void rw_select_kernel(
 constexpr int kGroup = 16;                  // lanes per query in the real-edge pass
 constexpr int kQPB = kThreads / kGroup;     // queries per block
 constexpr int kMaxRow = 64;                 // k_real + k_rw
+#ifndef BF_SCAN_UNROLL
+#define BF_SCAN_UNROLL 8
+#endif
+constexpr int kScanUnroll = BF_SCAN_UNROLL;  // in-neighbour loads in flight per lane
 
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t x, int o) {
   const uint32_t lo = __shfl_xor(uint32_t(x), o, 64);
@@ -168,31 +172,46 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t x, int o) {
   return (uint64_t(hi) << 32) | lo;
 }
 
+// Folds candidates src[i], src[i+stride], ... (< end) of query q into the
+// sorted register list lk (the KMAX smallest (key << 32 | src) seen). U loads
+// are issued before any is used, so a lane keeps U gathers in flight instead
+// of one; the slots past end re-read src[end-1] (in bounds) and are skipped.
+// The list is the same whatever order the candidates arrive in.
+template <int U, int KMAX>
+__device__ __forceinline__ void scan_topk(const int32_t* __restrict__ src, int64_t i, int64_t end, int stride,
+                                          uint32_t q, uint32_t kc, uint64_t (&lk)[KMAX]) {
+  for (; i < end; i += int64_t(stride) * U) {
+    uint32_t s[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t j = i + int64_t(u) * stride;
+      s[u] = uint32_t(src[j < end ? j : end - 1]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint64_t c = (uint64_t(edge_key(s[u], q, kc)) << 32) | s[u];
+      if (i + int64_t(u) * stride < end && c < lk[KMAX - 1]) {
+#pragma unroll
+        for (int j = KMAX - 1; j > 0; --j) lk[j] = c < lk[j - 1] ? lk[j - 1] : (c < lk[j] ? c : lk[j]);
+        lk[0] = c < lk[0] ? c : lk[0];
+      }
+    }
+  }
+}
+
 // Top-k_real of one hub's in-neighbour list with a whole workgroup: every
 // thread keeps a sorted register list of its strided share, then k rounds of a
 // block-wide minimum (wave shuffles, then LDS across the 4 waves) pop the
-// winners in key order. Output: hub_sel [n_hubs, k_real] kv ids, hub_cnt.
+// winners in key order into out[0, cnt) (written by thread 0). Returns cnt,
+// the same in every thread. Every thread of the block must call it.
 template <int KMAX>
-__global__ __launch_bounds__(kThreads) void real_select_hub_kernel(
-    const int64_t* __restrict__ in_ptr, const int32_t* __restrict__ in_src, const int32_t* __restrict__ hubs,
-    int k_real, uint32_t kc, int32_t* __restrict__ hub_sel, int32_t* __restrict__ hub_cnt) {
-  __shared__ uint64_t wave_min[kThreads / 64];
-  __shared__ int wave_win[kThreads / 64];
-  const int h = blockIdx.x;
-  const int64_t q = hubs[h];
+__device__ __forceinline__ int hub_topk(const int64_t* __restrict__ in_ptr, const int32_t* __restrict__ in_src,
+                                        int64_t q, int k_real, uint32_t kc, uint64_t* wave_min, int* wave_win,
+                                        int32_t* out) {
   uint64_t lk[KMAX];
 #pragma unroll
   for (int j = 0; j < KMAX; ++j) lk[j] = kNone;
-  const int64_t beg = in_ptr[q], end = in_ptr[q + 1];
-  for (int64_t i = beg + threadIdx.x; i < end; i += kThreads) {
-    const uint32_t s = uint32_t(in_src[i]);
-    const uint64_t c = (uint64_t(edge_key(s, uint32_t(q), kc)) << 32) | s;
-    if (c < lk[KMAX - 1]) {
-#pragma unroll
-      for (int j = KMAX - 1; j > 0; --j) lk[j] = c < lk[j - 1] ? lk[j - 1] : (c < lk[j] ? c : lk[j]);
-      lk[0] = c < lk[0] ? c : lk[0];
-    }
-  }
+  scan_topk<kScanUnroll>(in_src, in_ptr[q] + threadIdx.x, in_ptr[q + 1], kThreads, uint32_t(q), kc, lk);
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   int cnt = 0;
@@ -226,10 +245,59 @@ __global__ __launch_bounds__(kThreads) void real_select_hub_kernel(
       for (int j = 0; j < KMAX - 1; ++j) lk[j] = lk[j + 1];
       lk[KMAX - 1] = kNone;
     }
-    if (threadIdx.x == 0) hub_sel[int64_t(h) * k_real + r] = int32_t(uint32_t(best));
+    if (threadIdx.x == 0) out[r] = int32_t(uint32_t(best));
     cnt = r + 1;
   }
+  return cnt;
+}
+
+// Output: hub_sel [n_hubs, k_real] kv ids in key order, hub_cnt.
+template <int KMAX>
+__global__ __launch_bounds__(kThreads) void real_select_hub_kernel(
+    const int64_t* __restrict__ in_ptr, const int32_t* __restrict__ in_src, const int32_t* __restrict__ hubs,
+    int k_real, uint32_t kc, int32_t* __restrict__ hub_sel, int32_t* __restrict__ hub_cnt) {
+  __shared__ uint64_t wave_min[kThreads / 64];
+  __shared__ int wave_win[kThreads / 64];
+  const int h = blockIdx.x;
+  const int cnt = hub_topk<KMAX>(in_ptr, in_src, hubs[h], k_real, kc, wave_min, wave_win,
+                                 hub_sel + int64_t(h) * k_real);
   if (threadIdx.x == 0) hub_cnt[h] = cnt;
+}
+
+// Top-k_real of query q's in-neighbour list by one 16-lane group: per-lane
+// sorted register lists of its strided share, then k rounds of a group
+// minimum; the winners land in row[0, n) in key order (lane 0 writes).
+// Returns n, the same in the group's lanes.
+template <int KMAX>
+__device__ __forceinline__ int group_topk(const int64_t* __restrict__ in_ptr, const int32_t* __restrict__ in_src,
+                                          int64_t q, int k_real, uint32_t kc, int gl, int32_t* row) {
+  uint64_t lk[KMAX];
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) lk[j] = kNone;
+  scan_topk<kScanUnroll>(in_src, in_ptr[q] + gl, in_ptr[q + 1], kGroup, uint32_t(q), kc, lk);
+  const int lane = threadIdx.x & 63;
+  const int gbase = lane & ~(kGroup - 1);
+  int n = 0;
+  for (int r = 0; r < k_real; ++r) {
+    const uint64_t h = lk[0];
+    uint64_t m = h;
+    for (int o = 1; o < kGroup; o <<= 1) {
+      const uint64_t y = shfl_xor_u64(m, o);
+      m = y < m ? y : m;
+    }
+    if (m == kNone) break;      // uniform over the group
+    const uint64_t bal = __ballot(h == m);
+    const uint64_t mine = (bal >> gbase) & ((uint64_t(1) << kGroup) - 1);
+    const int winner = __ffsll((unsigned long long)mine) - 1;
+    if (gl == winner) {
+#pragma unroll
+      for (int j = 0; j < KMAX - 1; ++j) lk[j] = lk[j + 1];
+      lk[KMAX - 1] = kNone;
+    }
+    if (gl == 0) row[r] = int32_t(uint32_t(m));
+    n = r + 1;
+  }
+  return n;
 }
 
 // Writes one table row from the LDS list lst[0, n_tot): with dedup the set of
@@ -271,14 +339,12 @@ __device__ __forceinline__ void write_row(int32_t (*lst)[kMaxRow], int32_t (*dup
   if (gl == 0) *len_out = len;
 }
 
-// Group-per-query top-k and merge. Row li of the launch serves query
-// qids[li] (or q_lo + li); it writes table row li, or with by_query the row
-// q - q_lo of an n_rows-row table (the heavy-query list of a light/heavy
-// split build; list entries outside the table are skipped).
+// Group-per-query top-k and merge: row li of the launch serves query
+// qids[li] (or q_lo + li) and writes table row li.
 template <int KMAX>
 __global__ __launch_bounds__(kThreads) void real_select_merge_kernel(
     const int64_t* __restrict__ in_ptr, const int32_t* __restrict__ in_src, int64_t num_nodes, int64_t q_lo,
-    const int32_t* __restrict__ qids, int64_t n_q, int by_query, int64_t n_rows, int k_real, uint32_t kc,
+    const int32_t* __restrict__ qids, int64_t n_q, int k_real, uint32_t kc,
     const int32_t* __restrict__ rw_kv, const int32_t* __restrict__ rw_cnt, int k_rw, int dedup, int key_order,
     int32_t* __restrict__ table, int width, int32_t* __restrict__ row_len, const int32_t* __restrict__ hubs,
     const int32_t* __restrict__ hub_sel, const int32_t* __restrict__ hub_cnt, int64_t n_hubs,
@@ -289,8 +355,8 @@ __global__ __launch_bounds__(kThreads) void real_select_merge_kernel(
   const int gl = threadIdx.x % kGroup;
   const int64_t li = int64_t(blockIdx.x) * kQPB + gq;
   const int64_t q = li < n_q ? row_query(qids, q_lo, li, num_nodes) : -1;
-  const bool active = li < n_q && (!by_query || (q >= q_lo && q < q_lo + n_rows));
-  const int64_t qi = by_query ? q - q_lo : li;     // table / RW-selection row
+  const bool active = li < n_q;
+  const int64_t qi = li;
   int n_r = 0, n_w = 0;
   int64_t hub = -1;
   if (q >= 0 && k_real > 0 && n_hubs > 0) {
@@ -307,40 +373,7 @@ __global__ __launch_bounds__(kThreads) void real_select_merge_kernel(
     n_r = hub_cnt[hub];
     for (int i = gl; i < n_r; i += kGroup) lst[gq][i] = hub_sel[hub * k_real + i];
   } else if (q >= 0 && k_real > 0) {
-    uint64_t lk[KMAX];
-#pragma unroll
-    for (int j = 0; j < KMAX; ++j) lk[j] = kNone;
-    const int64_t beg = in_ptr[q], end = in_ptr[q + 1];
-    for (int64_t i = beg + gl; i < end; i += kGroup) {
-      const uint32_t s = uint32_t(in_src[i]);
-      const uint64_t c = (uint64_t(edge_key(s, uint32_t(q), kc)) << 32) | s;
-      if (c < lk[KMAX - 1]) {
-#pragma unroll
-        for (int j = KMAX - 1; j > 0; --j) lk[j] = c < lk[j - 1] ? lk[j - 1] : (c < lk[j] ? c : lk[j]);
-        lk[0] = c < lk[0] ? c : lk[0];
-      }
-    }
-    const int lane = threadIdx.x & 63;
-    const int gbase = lane & ~(kGroup - 1);
-    for (int r = 0; r < k_real; ++r) {
-      const uint64_t h = lk[0];
-      uint64_t m = h;
-      for (int o = 1; o < kGroup; o <<= 1) {
-        const uint64_t y = shfl_xor_u64(m, o);
-        m = y < m ? y : m;
-      }
-      if (m == kNone) break;
-      const uint64_t bal = __ballot(h == m);
-      const uint64_t mine = (bal >> gbase) & ((uint64_t(1) << kGroup) - 1);
-      const int winner = __ffsll((unsigned long long)mine) - 1;
-      if (gl == winner) {
-#pragma unroll
-        for (int j = 0; j < KMAX - 1; ++j) lk[j] = lk[j + 1];
-        lk[KMAX - 1] = kNone;
-      }
-      if (gl == 0) lst[gq][r] = int32_t(uint32_t(m));
-      n_r = r + 1;
-    }
+    n_r = group_topk<KMAX>(in_ptr, in_src, q, k_real, kc, gl, lst[gq]);
   }
   if (active && rw_kv != nullptr && k_rw > 0) {
     n_w = rw_cnt[qi];
@@ -385,14 +418,13 @@ __global__ __launch_bounds__(kThreads) void assemble_rows_kernel(
 // fraction of the instructions: the power-law bulk of queries has a few
 // in-neighbours. Heavier queries are left to the group kernel.
 template <int KR, int KW>
-__global__ __launch_bounds__(kThreads) void real_select_light_kernel(
-    const int64_t* __restrict__ in_ptr, const int32_t* __restrict__ in_src, int64_t q_lo, int64_t n_q,
-    int k_real, uint32_t kc, const int32_t* __restrict__ rw_kv, const int32_t* __restrict__ rw_cnt, int k_rw,
-    int dedup, int32_t* __restrict__ table, int width, int32_t* __restrict__ row_len, int64_t light_max) {
+__device__ __forceinline__ void light_row(const int64_t* __restrict__ in_ptr, const int32_t* __restrict__ in_src,
+                                          int64_t q_lo, int64_t qi, int k_real, uint32_t kc,
+                                          const int32_t* __restrict__ rw_kv, const int32_t* __restrict__ rw_cnt,
+                                          int k_rw, int dedup, int32_t* __restrict__ table, int width,
+                                          int32_t* __restrict__ row_len, int64_t light_max) {
   constexpr int NV = KR + KW;
   constexpr int32_t kPad = 0x7fffffff;          // sorts after every node id (ids < 2^31 - 1)
-  const int64_t qi = int64_t(blockIdx.x) * kThreads + threadIdx.x;
-  if (qi >= n_q) return;
   const int64_t q = q_lo + qi;
   int32_t v[NV];
 #pragma unroll
@@ -403,15 +435,7 @@ __global__ __launch_bounds__(kThreads) void real_select_light_kernel(
     uint64_t lk[KR];
 #pragma unroll
     for (int j = 0; j < KR; ++j) lk[j] = kNone;
-    for (int64_t i = beg; i < end; ++i) {
-      const uint32_t s = uint32_t(in_src[i]);
-      const uint64_t c = (uint64_t(edge_key(s, uint32_t(q), kc)) << 32) | s;
-      if (c < lk[KR - 1]) {
-#pragma unroll
-        for (int j = KR - 1; j > 0; --j) lk[j] = c < lk[j - 1] ? lk[j - 1] : (c < lk[j] ? c : lk[j]);
-        lk[0] = c < lk[0] ? c : lk[0];
-      }
-    }
+    scan_topk<kScanUnroll>(in_src, beg, end, 1, uint32_t(q), kc, lk);
 #pragma unroll
     for (int j = 0; j < KR; ++j) v[j] = (j < k_real && lk[j] != kNone) ? int32_t(uint32_t(lk[j])) : kPad;
   }
@@ -438,6 +462,63 @@ __global__ __launch_bounds__(kThreads) void real_select_light_kernel(
   }
   for (int c = len; c < width; ++c) out[c] = -1;
   row_len[qi] = len;
+}
+
+// The light/heavy split build in ONE launch: blocks [0, n_hubs) take a hub
+// row each (workgroup top-k, then the merge), the next blocks 16 heavy rows
+// each (group top-k; hub rows skipped), the rest 256 light rows each (one
+// per thread). The long hub and heavy work is dispatched first and overlaps
+// the light bulk. hubs / heavy: ascending queries of [q_lo, q_lo+n_q) with
+// in-degree above hub_threshold / light_max.
+template <int KR, int KW>
+__global__ __launch_bounds__(kThreads) void real_select_fused_kernel(
+    const int64_t* __restrict__ in_ptr, const int32_t* __restrict__ in_src, int64_t q_lo, int64_t n_q,
+    int k_real, uint32_t kc, const int32_t* __restrict__ rw_kv, const int32_t* __restrict__ rw_cnt, int k_rw,
+    int dedup, int32_t* __restrict__ table, int width, int32_t* __restrict__ row_len,
+    const int32_t* __restrict__ hubs, int64_t n_hubs, int64_t hub_threshold, const int32_t* __restrict__ heavy,
+    int64_t n_heavy, int64_t light_max) {
+  __shared__ int32_t lst[kQPB][kMaxRow];
+  __shared__ int32_t dupf[kQPB][kMaxRow];
+  __shared__ uint64_t wave_min[kThreads / 64];
+  __shared__ int wave_win[kThreads / 64];
+  const int64_t b = blockIdx.x;
+  const int64_t heavy_blocks = ceil_div(n_heavy, int64_t(kQPB));
+  const int gq = threadIdx.x / kGroup;
+  const int gl = threadIdx.x % kGroup;
+  if (b < n_hubs) {
+    const int64_t q = hubs[b];
+    if (q < q_lo || q >= q_lo + n_q) return;           // uniform over the block
+    const int64_t qi = q - q_lo;
+    const int n_r = hub_topk<KR>(in_ptr, in_src, q, k_real, kc, wave_min, wave_win, lst[0]);
+    int n_w = 0;
+    if (rw_kv != nullptr && k_rw > 0) {
+      n_w = rw_cnt[qi];
+      for (int i = threadIdx.x; i < n_w; i += kThreads) lst[0][n_r + i] = rw_kv[qi * k_rw + i];
+    }
+    __syncthreads();
+    write_row(lst, dupf, gq, gl, gq == 0, n_r + n_w, dedup, 0, table + qi * width, width, row_len + qi);
+    return;
+  }
+  if (b < n_hubs + heavy_blocks) {
+    const int64_t li = (b - n_hubs) * kQPB + gq;
+    int64_t q = li < n_heavy ? int64_t(heavy[li]) : -1;
+    if (q < q_lo || q >= q_lo + n_q || in_ptr[q + 1] - in_ptr[q] > hub_threshold) q = -1;   // hubs: done above
+    const bool active = q >= 0;
+    const int64_t qi = active ? q - q_lo : 0;
+    int n_r = 0, n_w = 0;
+    if (active && k_real > 0) n_r = group_topk<KR>(in_ptr, in_src, q, k_real, kc, gl, lst[gq]);
+    if (active && rw_kv != nullptr && k_rw > 0) {
+      n_w = rw_cnt[qi];
+      for (int i = gl; i < n_w; i += kGroup) lst[gq][n_r + i] = rw_kv[qi * k_rw + i];
+    }
+    __syncthreads();
+    write_row(lst, dupf, gq, gl, active, n_r + n_w, dedup, 0, table + qi * width, width, row_len + qi);
+    return;
+  }
+  const int64_t qi = (b - n_hubs - heavy_blocks) * kThreads + threadIdx.x;
+  if (qi < n_q)
+    light_row<KR, KW>(in_ptr, in_src, q_lo, qi, k_real, kc, rw_kv, rw_cnt, k_rw, dedup, table, width, row_len,
+                      light_max);
 }
 
 // One BFS layer of the probe's reception cone (utils/fullgraph_sp_support.py:
@@ -488,27 +569,6 @@ struct LightSplit {
   int64_t light_max = -1;     // < 0: no split, the group kernel takes every row
 };
 
-int launch_light(const int64_t* in_ptr, const int32_t* in_src, int64_t q_lo, int64_t n_q, int k_real, uint32_t kc,
-                 const int32_t* rw_kv, const int32_t* rw_cnt, int k_rw, int dedup, int32_t* table, int width,
-                 int32_t* row_len, int64_t light_max, hipStream_t st) {
-  const dim3 grid(unsigned(ceil_div(n_q, kThreads)));
-#define BF_LAUNCH_LIGHT(KR, KW)                                                                                     \
-  BF_LAUNCH("real_select_light_kernel", (real_select_light_kernel<KR, KW>), grid, dim3(kThreads), 0, st, in_ptr,  \
-            in_src, q_lo, n_q, k_real, kc, rw_kv, rw_cnt, k_rw, dedup, table, width, row_len, light_max)
-  const int kw = rw_kv ? k_rw : 0;
-  if (k_real <= 4 && kw <= 4)
-    BF_LAUNCH_LIGHT(4, 4);
-  else if (k_real <= 4)
-    BF_LAUNCH_LIGHT(4, 8);
-  else if (kw <= 4)
-    BF_LAUNCH_LIGHT(8, 4);
-  else
-    BF_LAUNCH_LIGHT(8, 8);
-#undef BF_LAUNCH_LIGHT
-  BF_CHECK_LAUNCH();
-  return BF_OK;
-}
-
 int launch_real_merge(const int64_t* in_ptr, const int32_t* in_src, int64_t num_nodes, int64_t q_lo,
                       const int32_t* qids, int64_t n_q, int k_real, uint32_t kc, const int32_t* rw_kv,
                       const int32_t* rw_cnt, int k_rw, int dedup, int key_order, int32_t* table, int width,
@@ -518,6 +578,28 @@ int launch_real_merge(const int64_t* in_ptr, const int32_t* in_src, int64_t num_
   const bool light = split.light_max >= 0 && qids == nullptr && !key_order && k_real <= 8 &&
                      (rw_kv == nullptr || k_rw <= 8);
   if (k_real <= 0) n_hubs = 0;
+  if (light) {
+    const int64_t heavy = k_real > 0 ? split.n_heavy : 0;
+    const int64_t blocks = n_hubs + ceil_div(heavy, int64_t(kQPB)) + ceil_div(n_q, int64_t(kThreads));
+    const int64_t hub_thr = n_hubs > 0 ? hub_threshold : (int64_t(1) << 62);
+    const int64_t light_max = k_real > 0 ? split.light_max : (int64_t(1) << 62);
+#define BF_LAUNCH_FUSED(KR, KW)                                                                                     \
+  BF_LAUNCH("real_select_fused_kernel", (real_select_fused_kernel<KR, KW>), dim3(unsigned(blocks)), dim3(kThreads), \
+            0, st, in_ptr, in_src, q_lo, n_q, k_real, kc, rw_kv, rw_cnt, k_rw, dedup, table, width, row_len, hubs,    \
+            n_hubs, hub_thr, split.heavy, heavy, light_max)
+    const int kw = rw_kv ? k_rw : 0;
+    if (k_real <= 4 && kw <= 4)
+      BF_LAUNCH_FUSED(4, 4);
+    else if (k_real <= 4)
+      BF_LAUNCH_FUSED(4, 8);
+    else if (kw <= 4)
+      BF_LAUNCH_FUSED(8, 4);
+    else
+      BF_LAUNCH_FUSED(8, 8);
+#undef BF_LAUNCH_FUSED
+    BF_CHECK_LAUNCH();
+    return BF_OK;
+  }
   if (n_hubs > 0) {
 #define BF_LAUNCH_HUB(KM)                                                                                       \
   BF_LAUNCH("real_select_hub_kernel", real_select_hub_kernel<KM>, dim3(unsigned(n_hubs)), dim3(kThreads), 0, st, \
@@ -533,18 +615,11 @@ int launch_real_merge(const int64_t* in_ptr, const int32_t* in_src, int64_t num_
 #undef BF_LAUNCH_HUB
     BF_CHECK_LAUNCH();
   }
-  if (light) {
-    int rc = launch_light(in_ptr, in_src, q_lo, n_q, k_real, kc, rw_kv, rw_cnt, k_rw, dedup, table, width, row_len,
-                          k_real > 0 ? split.light_max : (int64_t(1) << 62), st);
-    if (rc || split.n_heavy == 0 || k_real == 0) return rc;
-  }
-  const int32_t* list = light ? split.heavy : qids;
-  const int64_t n_list = light ? split.n_heavy : n_q;
-  const dim3 grid(unsigned(ceil_div(n_list, kQPB)));
+  const dim3 grid(unsigned(ceil_div(n_q, kQPB)));
 #define BF_LAUNCH_MERGE(KM)                                                                                      \
   BF_LAUNCH("real_select_merge_kernel", real_select_merge_kernel<KM>, grid, dim3(kThreads), 0, st, in_ptr, in_src, \
-            num_nodes, q_lo, list, n_list, light ? 1 : 0, n_q, k_real, kc, rw_kv, rw_cnt, k_rw, dedup, key_order,  \
-            table, width, row_len, hubs, hub_sel, hub_cnt, n_hubs, hub_threshold)
+            num_nodes, q_lo, qids, n_q, k_real, kc, rw_kv, rw_cnt, k_rw, dedup, key_order, table, width,          \
+            row_len, hubs, hub_sel, hub_cnt, n_hubs, hub_threshold)
   if (k_real <= 4)
     BF_LAUNCH_MERGE(4);
   else if (k_real <= 8)

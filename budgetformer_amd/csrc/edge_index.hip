@@ -170,6 +170,11 @@ __global__ __launch_bounds__(kThreads) void order_hist_kernel(const int64_t* __r
   if (h[threadIdx.x]) atomicAdd(&hist[threadIdx.x], h[threadIdx.x]);
 }
 
+// Each block orders kOrderChunk consecutive rows: it counts them per bucket in
+// LDS, reserves one range per bucket with a single global atomic (few blocks,
+// so the popular short-row buckets see little contention), then places them.
+constexpr int kOrderChunk = 16 * kThreads;
+
 __global__ __launch_bounds__(kThreads) void order_scatter_kernel(const int64_t* __restrict__ ptr, int64_t n_rows,
                                                                  const uint32_t* __restrict__ hist,
                                                                  uint32_t* __restrict__ cursor,
@@ -189,13 +194,17 @@ __global__ __launch_bounds__(kThreads) void order_scatter_kernel(const int64_t* 
   const uint32_t start = tid ? base[tid - 1] : 0u;
   __syncthreads();
   base[tid] = start;
-  const int64_t r = int64_t(blockIdx.x) * kThreads + tid;
-  const int b = r < n_rows ? length_bucket(ptr, r) : 0;
-  const uint32_t rank = r < n_rows ? atomicAdd(&cnt[b], 1u) : 0u;
+  const int64_t r0 = int64_t(blockIdx.x) * kOrderChunk;
+  const int64_t r1 = r0 + kOrderChunk < n_rows ? r0 + kOrderChunk : n_rows;
+  for (int64_t r = r0 + tid; r < r1; r += kThreads) atomicAdd(&cnt[length_bucket(ptr, r)], 1u);
   __syncthreads();
   if (cnt[tid]) base[tid] += atomicAdd(&cursor[tid], cnt[tid]);
+  cnt[tid] = 0;
   __syncthreads();
-  if (r < n_rows) order[base[b] + rank] = int32_t(r);
+  for (int64_t r = r0 + tid; r < r1; r += kThreads) {
+    const int b = length_bucket(ptr, r);
+    order[base[b] + atomicAdd(&cnt[b], 1u)] = int32_t(r);
+  }
 }
 
 struct MaxOp {
@@ -233,10 +242,13 @@ __global__ void split_count_kernel(const int64_t* __restrict__ ptr, int64_t n_ro
   packed[r] = (uint64_t(n) << 32) | (heavy ? 1u : 0u);
 }
 
-// item_off, the heavy-row list (compacted by the scanned flags) and the two plan counts.
+// item_off, the heavy-row list (compacted by the scanned flags), item_row of
+// each item (written by its row's thread: a split row has few items) and the
+// two plan counts.
 __global__ void split_rows_kernel(const int32_t* __restrict__ nitems, const uint64_t* __restrict__ packed_off,
                                   int64_t n_rows, int64_t item_cap, int32_t* __restrict__ item_off,
-                                  int32_t* __restrict__ heavy_rows, int64_t heavy_cap, int32_t* __restrict__ counts) {
+                                  int32_t* __restrict__ item_row, int32_t* __restrict__ heavy_rows,
+                                  int64_t heavy_cap, int32_t* __restrict__ counts) {
   const int64_t r = int64_t(blockIdx.x) * kThreads + threadIdx.x;
   if (r >= n_rows) return;
   const int n = nitems[r];
@@ -245,6 +257,7 @@ __global__ void split_rows_kernel(const int32_t* __restrict__ nitems, const uint
   const int64_t slot = int64_t(uint32_t(off));
   item_off[r] = int32_t(first_item);
   if (n > 0 && slot < heavy_cap) heavy_rows[slot] = int32_t(r);
+  for (int64_t j = 0; j < n && first_item + j < item_cap; ++j) item_row[first_item + j] = int32_t(r);
   if (r == n_rows - 1) {
     const int64_t items = first_item + n;
     const int64_t heavy = slot + (n > 0 ? 1 : 0);
@@ -253,18 +266,6 @@ __global__ void split_rows_kernel(const int32_t* __restrict__ nitems, const uint
   }
 }
 
-// item_row[i] = the heavy row owning item i: the last row whose first item is <= i.
-__global__ void split_items_kernel(const int32_t* __restrict__ item_off, int64_t n_rows,
-                                   const int32_t* __restrict__ counts, int32_t* __restrict__ item_row) {
-  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
-  if (i >= counts[0]) return;
-  int64_t lo = 0, hi = n_rows;  // item_off[lo] <= i < item_off[hi] (item_off[n_rows] taken as +inf)
-  while (hi - lo > 1) {
-    const int64_t mid = (lo + hi) >> 1;
-    if (item_off[mid] <= i) lo = mid; else hi = mid;
-  }
-  item_row[i] = int32_t(lo);
-}
 
 }  // namespace
 }  // namespace bf
@@ -515,13 +516,8 @@ extern "C" int bf_split_plan(const int64_t* ptr, int64_t n_rows, int32_t thresho
   BF_CHECK_LAUNCH();
   BF_CHECK_HIP(hipcub::DeviceScan::ExclusiveSum(temp, temp_bytes, packed, packed_off, int(n_rows), st));
   BF_LAUNCH("split_rows_kernel", split_rows_kernel, dim3(blocks_for(n_rows)), dim3(kThreads), 0, st, nitems,
-            packed_off, n_rows, item_cap, item_off, heavy_rows, heavy_cap, counts);
+            packed_off, n_rows, item_cap, item_off, item_row, heavy_rows, heavy_cap, counts);
   BF_CHECK_LAUNCH();
-  if (item_cap > 0) {
-    BF_LAUNCH("split_items_kernel", split_items_kernel, dim3(blocks_for(item_cap)), dim3(kThreads), 0, st, item_off,
-              n_rows, counts, item_row);
-    BF_CHECK_LAUNCH();
-  }
   return BF_OK;
 }
 
@@ -704,8 +700,8 @@ extern "C" int bf_row_order(const int64_t* ptr, int64_t n_rows, int32_t* order, 
   BF_LAUNCH("order_hist_kernel", order_hist_kernel, dim3(unsigned(blocks < 2048 ? blocks : 2048)), dim3(kThreads), 0,
             st, ptr, n_rows, hist);
   BF_CHECK_LAUNCH();
-  BF_LAUNCH("order_scatter_kernel", order_scatter_kernel, dim3(unsigned(blocks)), dim3(kThreads), 0, st, ptr, n_rows,
-            hist, cursor, order);
+  BF_LAUNCH("order_scatter_kernel", order_scatter_kernel, dim3(unsigned(ceil_div(n_rows, int64_t(kOrderChunk)))),
+            dim3(kThreads), 0, st, ptr, n_rows, hist, cursor, order);
   BF_CHECK_LAUNCH();
   return BF_OK;
 }
