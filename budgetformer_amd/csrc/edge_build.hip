@@ -165,6 +165,10 @@ constexpr int kMaxRow = 64;                 // k_real + k_rw
 #define BF_SCAN_UNROLL 8
 #endif
 constexpr int kScanUnroll = BF_SCAN_UNROLL;  // in-neighbour loads in flight per lane
+#ifndef BF_SCAN_X4_UNROLL
+#define BF_SCAN_X4_UNROLL 4
+#endif
+constexpr int kScanX4Unroll = BF_SCAN_X4_UNROLL;  // 16-byte chunks in flight per thread (light rows)
 
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t x, int o) {
   const uint32_t lo = __shfl_xor(uint32_t(x), o, 64);
@@ -410,35 +414,127 @@ __global__ __launch_bounds__(kThreads) void assemble_rows_kernel(
             row_len + (active ? qi : 0));
 }
 
-// Thread-per-query top-k and merge for the light queries (in-degree <=
-// light_max): the thread scans its in-neighbour row into a sorted register
-// list of KR (key << 32 | src), gathers the RW selection, sorts the KR + KW
-// values with an odd-even transposition network and writes the row ascending
-// (unique values when dedup). The same rows as real_select_merge_kernel, at a
-// fraction of the instructions: the power-law bulk of queries has a few
-// in-neighbours. Heavier queries are left to the group kernel.
+// ---- 32-bit key lists of the fused light/heavy kernel.
+// For a fixed query q, key(src) = (src*A + base_q) mod 2^31 with A odd is a
+// bijection of src < 2^31, so a row's candidates never tie and the KR smallest
+// keys alone name the winners: src = ((key - base_q) * A^-1) mod 2^31. A list
+// entry is then one 32-bit value, inserted without a branch.
+constexpr uint32_t kKeyMul = 1103515245u;
+constexpr uint32_t kKeyMulInv = 0xeeb9eb65u;   // kKeyMul * kKeyMulInv == 1 (mod 2^32)
+constexpr uint32_t kNoKey = 0xffffffffu;       // above every 31-bit key
+
+__device__ __forceinline__ uint32_t key_base(uint32_t q, uint32_t kc) { return q * 214013u + kc; }
+__device__ __forceinline__ uint32_t key_of(uint32_t src, uint32_t base) { return (src * kKeyMul + base) & 0x7fffffffu; }
+__device__ __forceinline__ int32_t src_of(uint32_t key, uint32_t base) {
+  return int32_t(((key - base) * kKeyMulInv) & 0x7fffffffu);
+}
+
+// Inserts c into the ascending list lk (the largest value drops out): a
+// min/max carry chain, no branch. c == kNoKey leaves lk unchanged.
+template <int K>
+__device__ __forceinline__ void insert_key(uint32_t (&lk)[K], uint32_t c) {
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    const uint32_t lo = lk[j] < c ? lk[j] : c;
+    c = lk[j] < c ? c : lk[j];
+    lk[j] = lo;
+  }
+}
+
+// Lane gl of a G-lane group folds row[gl], row[gl+G], ... (< deg) into lk;
+// U loads in flight per lane, slots past deg re-read row[deg-1] and are dropped.
+template <int U, int K>
+__device__ __forceinline__ void scan_keys(const int32_t* __restrict__ row, int32_t deg, int gl, int G, uint32_t base,
+                                          uint32_t (&lk)[K]) {
+  for (int32_t i = gl; i < deg; i += G * U) {
+    uint32_t sv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int32_t j = i + u * G;
+      sv[u] = uint32_t(row[j < deg ? j : deg - 1]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) insert_key(lk, i + u * G < deg ? key_of(sv[u], base) : kNoKey);
+  }
+}
+
+// One thread's scan of src[beg, end) through the aligned 4-entry chunks that
+// cover it, with 16-byte loads (src 16-byte aligned), U chunks in flight:
+// each load instruction moves 4 entries per lane instead of 1.
+template <int U, int K>
+__device__ __forceinline__ void scan_keys_x4(const int32_t* __restrict__ src, int64_t beg, int64_t end,
+                                             uint32_t base, uint32_t (&lk)[K]) {
+  if (end <= beg) return;
+  const int4* __restrict__ v4 = reinterpret_cast<const int4*>(src);
+  const int64_t c0 = beg >> 2, c_last = (end - 1) >> 2;
+  const uint32_t deg = uint32_t(end - beg);
+  const int32_t lead = int32_t(beg - c0 * 4);        // entries of chunk c0 before beg
+  for (int64_t c = c0; c <= c_last; c += U) {
+    int4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = v4[c + u <= c_last ? c + u : c_last];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int32_t e[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+      const int32_t rel0 = int32_t(c + u - c0) * 4 - lead;     // row offset of e[0]
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        insert_key(lk, uint32_t(rel0 + t) < deg ? key_of(uint32_t(e[t]), base) : kNoKey);
+    }
+  }
+}
+
+// a <- the K smallest of a and b (both ascending), ascending: the
+// half-cleaner min(a[j], b[K-1-j]) leaves them as a bitonic sequence, which a
+// bitonic merge network sorts. Equal values are both kept.
+template <int K>
+__device__ __forceinline__ void merge_keys(uint32_t (&a)[K], const uint32_t (&b)[K]) {
+  static_assert((K & (K - 1)) == 0, "K must be a power of two");
+#pragma unroll
+  for (int j = 0; j < K; ++j) a[j] = b[K - 1 - j] < a[j] ? b[K - 1 - j] : a[j];
+#pragma unroll
+  for (int s = K / 2; s > 0; s >>= 1) {
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      if ((i & s) == 0) {
+        const uint32_t x = a[i], y = a[i + s];
+        a[i] = x < y ? x : y;
+        a[i + s] = x < y ? y : x;
+      }
+    }
+  }
+}
+
+// Butterfly over the G lanes of an aligned lane group: afterwards every lane
+// holds the group's K smallest keys, ascending. Each round pairs lanes whose
+// coverage is disjoint, so the multiset is exact.
+template <int G, int K>
+__device__ __forceinline__ void group_merge_keys(uint32_t (&lk)[K]) {
+#pragma unroll
+  for (int o = 1; o < G; o <<= 1) {
+    uint32_t other[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) other[j] = __shfl_xor(lk[j], o, 64);
+    merge_keys<K>(lk, other);
+  }
+}
+
+// Writes table row qi from the real winners lk[0, k_real) (kNoKey = none) and
+// the RW selection rw_kv[qi, 0 .. rw_cnt[qi]): the KR + KW ids are sorted by
+// an odd-even transposition network in registers and stored ascending
+// (unique values when dedup), padded with -1 to width.
 template <int KR, int KW>
-__device__ __forceinline__ void light_row(const int64_t* __restrict__ in_ptr, const int32_t* __restrict__ in_src,
-                                          int64_t q_lo, int64_t qi, int k_real, uint32_t kc,
-                                          const int32_t* __restrict__ rw_kv, const int32_t* __restrict__ rw_cnt,
-                                          int k_rw, int dedup, int32_t* __restrict__ table, int width,
-                                          int32_t* __restrict__ row_len, int64_t light_max) {
+__device__ __forceinline__ void emit_row(const uint32_t (&lk)[KR], uint32_t base, int k_real,
+                                         const int32_t* __restrict__ rw_kv, const int32_t* __restrict__ rw_cnt,
+                                         int k_rw, int64_t qi, int dedup, int32_t* __restrict__ table, int width,
+                                         int32_t* __restrict__ row_len) {
   constexpr int NV = KR + KW;
   constexpr int32_t kPad = 0x7fffffff;          // sorts after every node id (ids < 2^31 - 1)
-  const int64_t q = q_lo + qi;
   int32_t v[NV];
 #pragma unroll
-  for (int j = 0; j < NV; ++j) v[j] = kPad;
-  if (k_real > 0) {
-    const int64_t beg = in_ptr[q], end = in_ptr[q + 1];
-    if (end - beg > light_max) return;          // a heavy query: the group kernel writes its row
-    uint64_t lk[KR];
+  for (int j = 0; j < KR; ++j) v[j] = (j < k_real && lk[j] != kNoKey) ? src_of(lk[j], base) : kPad;
 #pragma unroll
-    for (int j = 0; j < KR; ++j) lk[j] = kNone;
-    scan_topk<kScanUnroll>(in_src, beg, end, 1, uint32_t(q), kc, lk);
-#pragma unroll
-    for (int j = 0; j < KR; ++j) v[j] = (j < k_real && lk[j] != kNone) ? int32_t(uint32_t(lk[j])) : kPad;
-  }
+  for (int j = 0; j < KW; ++j) v[KR + j] = kPad;
   if (rw_kv != nullptr && KW > 0) {
     const int n_w = rw_cnt[qi];
 #pragma unroll
@@ -448,9 +544,9 @@ __device__ __forceinline__ void light_row(const int64_t* __restrict__ in_ptr, co
   for (int r = 0; r < NV; ++r) {
 #pragma unroll
     for (int j = r & 1; j + 1 < NV; j += 2) {
-      const int32_t a = v[j], b = v[j + 1];
-      v[j] = a < b ? a : b;
-      v[j + 1] = a < b ? b : a;
+      const int32_t x = v[j], y = v[j + 1];
+      v[j] = x < y ? x : y;
+      v[j + 1] = x < y ? y : x;
     }
   }
   int32_t* out = table + qi * width;
@@ -464,61 +560,72 @@ __device__ __forceinline__ void light_row(const int64_t* __restrict__ in_ptr, co
   row_len[qi] = len;
 }
 
-// The light/heavy split build in ONE launch: blocks [0, n_hubs) take a hub
-// row each (workgroup top-k, then the merge), the next blocks 16 heavy rows
-// each (group top-k; hub rows skipped), the rest 256 light rows each (one
-// per thread). The long hub and heavy work is dispatched first and overlaps
-// the light bulk. hubs / heavy: ascending queries of [q_lo, q_lo+n_q) with
-// in-degree above hub_threshold / light_max.
+// The light/heavy split build in ONE launch, without LDS: blocks
+// [0, hub_blocks) take 4 hub rows each (one wave per row), the next blocks 16
+// heavy rows each (a 16-lane group per row; hub rows skipped), the rest 256
+// light rows each (one per thread, 16-byte loads when in_src is 16-byte
+// aligned). A group scans its row into per-lane sorted lists of KR
+// (key << 32 | src), merges them by a butterfly, and its first lane writes the
+// row. The long hub and heavy work is dispatched first and overlaps the light
+// bulk. hubs / heavy: ascending queries of [q_lo, q_lo+n_q) with in-degree
+// above hub_threshold / light_max.
+constexpr int kHubsPerBlock = kThreads / 64;
+
 template <int KR, int KW>
 __global__ __launch_bounds__(kThreads) void real_select_fused_kernel(
     const int64_t* __restrict__ in_ptr, const int32_t* __restrict__ in_src, int64_t q_lo, int64_t n_q,
     int k_real, uint32_t kc, const int32_t* __restrict__ rw_kv, const int32_t* __restrict__ rw_cnt, int k_rw,
     int dedup, int32_t* __restrict__ table, int width, int32_t* __restrict__ row_len,
     const int32_t* __restrict__ hubs, int64_t n_hubs, int64_t hub_threshold, const int32_t* __restrict__ heavy,
-    int64_t n_heavy, int64_t light_max) {
-  __shared__ int32_t lst[kQPB][kMaxRow];
-  __shared__ int32_t dupf[kQPB][kMaxRow];
-  __shared__ uint64_t wave_min[kThreads / 64];
-  __shared__ int wave_win[kThreads / 64];
+    int64_t n_heavy, int64_t light_max, int vec4) {
   const int64_t b = blockIdx.x;
+  const int64_t hub_blocks = ceil_div(n_hubs, int64_t(kHubsPerBlock));
   const int64_t heavy_blocks = ceil_div(n_heavy, int64_t(kQPB));
-  const int gq = threadIdx.x / kGroup;
-  const int gl = threadIdx.x % kGroup;
-  if (b < n_hubs) {
-    const int64_t q = hubs[b];
-    if (q < q_lo || q >= q_lo + n_q) return;           // uniform over the block
-    const int64_t qi = q - q_lo;
-    const int n_r = hub_topk<KR>(in_ptr, in_src, q, k_real, kc, wave_min, wave_win, lst[0]);
-    int n_w = 0;
-    if (rw_kv != nullptr && k_rw > 0) {
-      n_w = rw_cnt[qi];
-      for (int i = threadIdx.x; i < n_w; i += kThreads) lst[0][n_r + i] = rw_kv[qi * k_rw + i];
+  uint32_t lk[KR];
+#pragma unroll
+  for (int j = 0; j < KR; ++j) lk[j] = kNoKey;
+  if (b < hub_blocks) {
+    const int64_t li = b * kHubsPerBlock + (threadIdx.x >> 6);
+    const int64_t q = li < n_hubs ? int64_t(hubs[li]) : -1;
+    if (q < q_lo || q >= q_lo + n_q) return;           // uniform over the wave
+    const int lane = threadIdx.x & 63;
+    const uint32_t base = key_base(uint32_t(q), kc);
+    if (k_real > 0) {
+      const int64_t beg = in_ptr[q];
+      scan_keys<kScanUnroll>(in_src + beg, int32_t(in_ptr[q + 1] - beg), lane, 64, base, lk);
+      group_merge_keys<64, KR>(lk);
     }
-    __syncthreads();
-    write_row(lst, dupf, gq, gl, gq == 0, n_r + n_w, dedup, 0, table + qi * width, width, row_len + qi);
+    if (lane == 0) emit_row<KR, KW>(lk, base, k_real, rw_kv, rw_cnt, k_rw, q - q_lo, dedup, table, width, row_len);
     return;
   }
-  if (b < n_hubs + heavy_blocks) {
-    const int64_t li = (b - n_hubs) * kQPB + gq;
-    int64_t q = li < n_heavy ? int64_t(heavy[li]) : -1;
-    if (q < q_lo || q >= q_lo + n_q || in_ptr[q + 1] - in_ptr[q] > hub_threshold) q = -1;   // hubs: done above
-    const bool active = q >= 0;
-    const int64_t qi = active ? q - q_lo : 0;
-    int n_r = 0, n_w = 0;
-    if (active && k_real > 0) n_r = group_topk<KR>(in_ptr, in_src, q, k_real, kc, gl, lst[gq]);
-    if (active && rw_kv != nullptr && k_rw > 0) {
-      n_w = rw_cnt[qi];
-      for (int i = gl; i < n_w; i += kGroup) lst[gq][n_r + i] = rw_kv[qi * k_rw + i];
+  if (b < hub_blocks + heavy_blocks) {
+    const int64_t li = (b - hub_blocks) * kQPB + threadIdx.x / kGroup;
+    const int gl = threadIdx.x % kGroup;
+    const int64_t q = li < n_heavy ? int64_t(heavy[li]) : -1;
+    if (q < q_lo || q >= q_lo + n_q) return;           // uniform over the group
+    const int64_t beg = in_ptr[q], deg = in_ptr[q + 1] - beg;
+    if (deg > hub_threshold) return;                    // a hub: a wave writes its row
+    const uint32_t base = key_base(uint32_t(q), kc);
+    if (k_real > 0) {
+      scan_keys<kScanUnroll>(in_src + beg, int32_t(deg), gl, kGroup, base, lk);
+      group_merge_keys<kGroup, KR>(lk);
     }
-    __syncthreads();
-    write_row(lst, dupf, gq, gl, active, n_r + n_w, dedup, 0, table + qi * width, width, row_len + qi);
+    if (gl == 0) emit_row<KR, KW>(lk, base, k_real, rw_kv, rw_cnt, k_rw, q - q_lo, dedup, table, width, row_len);
     return;
   }
-  const int64_t qi = (b - n_hubs - heavy_blocks) * kThreads + threadIdx.x;
-  if (qi < n_q)
-    light_row<KR, KW>(in_ptr, in_src, q_lo, qi, k_real, kc, rw_kv, rw_cnt, k_rw, dedup, table, width, row_len,
-                      light_max);
+  const int64_t qi = (b - hub_blocks - heavy_blocks) * kThreads + threadIdx.x;
+  if (qi >= n_q) return;
+  const int64_t q = q_lo + qi;
+  const uint32_t base = key_base(uint32_t(q), kc);
+  if (k_real > 0) {
+    const int64_t beg = in_ptr[q], end = in_ptr[q + 1];
+    if (end - beg > light_max) return;          // a heavy query: a group writes its row
+    if (vec4)
+      scan_keys_x4<kScanX4Unroll>(in_src, beg, end, base, lk);
+    else
+      scan_keys<kScanUnroll>(in_src + beg, int32_t(end - beg), 0, 1, base, lk);
+  }
+  emit_row<KR, KW>(lk, base, k_real, rw_kv, rw_cnt, k_rw, qi, dedup, table, width, row_len);
 }
 
 // One BFS layer of the probe's reception cone (utils/fullgraph_sp_support.py:
@@ -580,13 +687,15 @@ int launch_real_merge(const int64_t* in_ptr, const int32_t* in_src, int64_t num_
   if (k_real <= 0) n_hubs = 0;
   if (light) {
     const int64_t heavy = k_real > 0 ? split.n_heavy : 0;
-    const int64_t blocks = n_hubs + ceil_div(heavy, int64_t(kQPB)) + ceil_div(n_q, int64_t(kThreads));
+    const int64_t blocks = ceil_div(n_hubs, int64_t(kHubsPerBlock)) + ceil_div(heavy, int64_t(kQPB)) +
+                           ceil_div(n_q, int64_t(kThreads));
+    const int vec4 = (reinterpret_cast<uintptr_t>(in_src) & 15) == 0;
     const int64_t hub_thr = n_hubs > 0 ? hub_threshold : (int64_t(1) << 62);
     const int64_t light_max = k_real > 0 ? split.light_max : (int64_t(1) << 62);
 #define BF_LAUNCH_FUSED(KR, KW)                                                                                     \
   BF_LAUNCH("real_select_fused_kernel", (real_select_fused_kernel<KR, KW>), dim3(unsigned(blocks)), dim3(kThreads), \
             0, st, in_ptr, in_src, q_lo, n_q, k_real, kc, rw_kv, rw_cnt, k_rw, dedup, table, width, row_len, hubs,    \
-            n_hubs, hub_thr, split.heavy, heavy, light_max)
+            n_hubs, hub_thr, split.heavy, heavy, light_max, vec4)
     const int kw = rw_kv ? k_rw : 0;
     if (k_real <= 4 && kw <= 4)
       BF_LAUNCH_FUSED(4, 4);
