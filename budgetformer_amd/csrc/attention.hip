@@ -697,7 +697,7 @@ int check_index(const bf_attn_index* idx, bool backward) {
   BF_CHECK_ARG(idx->q_items == 0 || (idx->q_nitems && idx->q_item_off && idx->q_item_row && idx->q_heavy_rows),
                "attention: query-side split plan missing");
   if (backward) {
-    BF_CHECK_ARG(idx->kptr && ((idx->kq && idx->ke) || idx->nnz == 0), "attention: reverse index missing");
+    BF_CHECK_ARG(idx->kptr && (idx->kq || idx->nnz == 0), "attention: reverse index missing");
     BF_CHECK_ARG(idx->k_items >= 0 && idx->k_heavy >= 0, "attention: bad key-side plan counts");
     BF_CHECK_ARG(idx->k_items == 0 || (idx->k_nitems && idx->k_item_off && idx->k_item_row && idx->k_heavy_rows),
                  "attention: key-side split plan missing");
@@ -833,6 +833,8 @@ extern "C" int bf_attn_bwd(const bf_attn_index* idx, int32_t dtype, int32_t num_
   int rc = make_shape(dtype, num_heads, head_dim, sh);
   if (rc) return rc;
   if ((rc = check_index(idx, true))) return rc;
+  BF_CHECK_ARG(idx->ke || idx->nnz == 0 || (!bias && !factor),
+               "attn_bwd: a bias or factor needs the reverse entries' CSR positions (ke)");
   BF_CHECK_ARG(q && k && v && out && Z && dout && dq && dk && dv && rowstat, "attn_bwd: null tensor");
   BF_CHECK_ARG((reinterpret_cast<uintptr_t>(rowstat) & 7u) == 0, "attn_bwd: rowstat must be 8-byte aligned");
   BF_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out) && aligned16(dout) &&

@@ -45,12 +45,14 @@ __global__ void row_lengths_kernel(const int32_t* __restrict__ row_len, int64_t 
   lens[t] = len;
 }
 
-// Writes entry pos of query row `row`: kv, and (row << 32 | pos) when the
-// caller wants the reverse index's sort values produced here.
-__device__ __forceinline__ void put_entry(int32_t* __restrict__ kv, uint64_t* __restrict__ rowpos, int64_t pos,
-                                          int64_t row, int32_t id) {
+// Writes entry pos (slot `slot` of query row `row`): kv, and when rkey is
+// given the entry's reverse-index sort key (id << kshift | row << sbits | slot):
+// a stable radix sort over the id bits alone then leaves each kv's entries in
+// (row, slot) order, which is CSR order.
+__device__ __forceinline__ void put_entry(int32_t* __restrict__ kv, uint64_t* __restrict__ rkey, int64_t pos,
+                                          int64_t row, int slot, int32_t id, int kshift, int sbits) {
   kv[pos] = id;
-  if (rowpos) rowpos[pos] = (uint64_t(uint32_t(row)) << 32) | uint32_t(pos);
+  if (rkey) rkey[pos] = (uint64_t(uint32_t(id)) << kshift) | (uint64_t(row) << sbits) | uint64_t(slot);
 }
 
 // One thread per table slot, then (with the Graphormer token) one thread per
@@ -58,14 +60,15 @@ __device__ __forceinline__ void put_entry(int32_t* __restrict__ kv, uint64_t* __
 // with kv 0 followed by its table row shifted by one.
 __global__ void table_fill_kernel(const int32_t* __restrict__ table, const int32_t* __restrict__ row_len,
                                   int64_t n_rows, int width, int token, const int64_t* __restrict__ qptr,
-                                  int32_t* __restrict__ kv, uint64_t* __restrict__ rowpos) {
+                                  int32_t* __restrict__ kv, uint64_t* __restrict__ rkey, int kshift, int sbits) {
   const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
   const int64_t slots = n_rows * width;
   if (i >= slots) {
     const int64_t t = i - slots;
     if (!token || t >= n_rows) return;
-    put_entry(kv, rowpos, t, 0, int32_t(t + 1));
-    if (row_len[t] == 0) put_entry(kv, rowpos, qptr[t + 1], t + 1, 0);
+    // the token row's entry for kv t+1 sits at position t: its key carries slot 0
+    put_entry(kv, rkey, t, 0, 0, int32_t(t + 1), kshift, sbits);
+    if (row_len[t] == 0) put_entry(kv, rkey, qptr[t + 1], t + 1, 0, 0, kshift, sbits);
     return;
   }
   const int64_t r = i / width;
@@ -74,10 +77,10 @@ __global__ void table_fill_kernel(const int32_t* __restrict__ table, const int32
   if (c >= len) return;
   if (token) {
     const int64_t base = qptr[r + 1];  // query r+1
-    if (c == 0) put_entry(kv, rowpos, base, r + 1, 0);
-    put_entry(kv, rowpos, base + 1 + c, r + 1, table[i] + 1);
+    if (c == 0) put_entry(kv, rkey, base, r + 1, 0, 0, kshift, sbits);
+    put_entry(kv, rkey, base + 1 + c, r + 1, c + 1, table[i] + 1, kshift, sbits);
   } else {
-    put_entry(kv, rowpos, qptr[r] + c, r, table[i]);
+    put_entry(kv, rkey, qptr[r] + c, r, c, table[i], kshift, sbits);
   }
 }
 
@@ -145,6 +148,39 @@ __global__ void unpack_row_entry_kernel(const uint64_t* __restrict__ vals, int64
   const uint64_t x = vals[i];
   kq[i] = int32_t(x >> 32);
   ke[i] = int32_t(uint32_t(x));
+}
+
+// Sorted reverse-index keys -> kptr (boundaries of the id field), kq, and ke
+// when asked for. ke of a token-row entry (query 0 with the Graphormer token)
+// is id - 1, the position table_fill gave it; every other entry sits at
+// qptr[query] + slot.
+__device__ __forceinline__ int32_t entry_of(uint64_t x, int kshift, int sbits, int token,
+                                            const int64_t* __restrict__ qptr) {
+  const int64_t q = int64_t((x >> sbits) & ((uint64_t(1) << (kshift - sbits)) - 1));
+  const int64_t slot = int64_t(x & ((uint64_t(1) << sbits) - 1));
+  return int32_t(token && q == 0 ? int64_t(x >> kshift) - 1 : qptr[q] + slot);
+}
+
+__global__ void unpack_rkey_kernel(const uint64_t* __restrict__ keys, int64_t nnz, int kshift, int sbits, int token,
+                                   const int64_t* __restrict__ qptr, int64_t n_kv, int64_t* __restrict__ kptr,
+                                   int32_t* __restrict__ kq, int32_t* __restrict__ ke) {
+  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (i > nnz) return;
+  const uint64_t x = i < nnz ? keys[i] : 0;
+  int64_t r_here = i < nnz ? int64_t(x >> kshift) : n_kv;
+  int64_t r_prev = i > 0 ? int64_t(keys[i - 1] >> kshift) : -1;
+  if (r_here > n_kv) r_here = n_kv;
+  if (r_prev > n_kv) r_prev = n_kv;
+  for (int64_t r = r_prev + 1; r <= r_here; ++r) kptr[r] = i;
+  if (i == nnz) return;
+  kq[i] = int32_t((x >> sbits) & ((uint64_t(1) << (kshift - sbits)) - 1));
+  if (ke) ke[i] = entry_of(x, kshift, sbits, token, qptr);
+}
+
+__global__ void reverse_entries_kernel(const uint64_t* __restrict__ keys, int64_t nnz, int kshift, int sbits,
+                                       int token, const int64_t* __restrict__ qptr, int32_t* __restrict__ ke) {
+  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (i < nnz) ke[i] = entry_of(keys[i], kshift, sbits, token, qptr);
 }
 
 // Row order, longest first: bucket 255 - min(len, 255), counted per block in
@@ -304,14 +340,21 @@ extern "C" int bf_table_csr_ptr(const int32_t* row_len, int64_t n_rows, int32_t 
 }
 
 extern "C" int bf_table_to_csr(const int32_t* table, const int32_t* row_len, int64_t n_rows, int32_t width,
-                               int32_t global_token, const int64_t* qptr, int32_t* kv, uint64_t* rowpos,
-                               void* stream) {
+                               int32_t global_token, const int64_t* qptr, int32_t* kv, uint64_t* rkey,
+                               int32_t q_bits, int32_t slot_bits, void* stream) {
   BF_CHECK_ARG(n_rows >= 0 && width >= 0 && qptr, "table_to_csr: bad arguments");
   BF_CHECK_ARG(n_rows == 0 || (table && row_len && kv), "table_to_csr: null tensor");
+  if (rkey) {
+    const int64_t n_q = n_rows + (global_token ? 1 : 0);
+    BF_CHECK_ARG(q_bits >= bits_for(uint64_t(n_q)) && slot_bits >= bits_for(uint64_t(width)) &&
+                     q_bits + slot_bits <= 33,
+                 "table_to_csr: key fields (%d query bits, %d slot bits) do not hold %lld queries of width %d "
+                 "beside a 31-bit id", q_bits, slot_bits, (long long)n_q, width);
+  }
   const int64_t threads = n_rows * width + (global_token ? n_rows : 0);
   if (threads > 0) {
     BF_LAUNCH("table_fill_kernel", table_fill_kernel, dim3(blocks_for(threads)), dim3(kThreads), 0, as_stream(stream),
-              table, row_len, n_rows, width, int(global_token != 0), qptr, kv, rowpos);
+              table, row_len, n_rows, width, int(global_token != 0), qptr, kv, rkey, q_bits + slot_bits, slot_bits);
     BF_CHECK_LAUNCH();
   }
   return BF_OK;
@@ -413,24 +456,27 @@ extern "C" int bf_reverse_index(const int64_t* qptr, const int32_t* kv, int64_t 
   return BF_OK;
 }
 
-extern "C" int bf_reverse_index_packed_workspace_size(int64_t nnz, int64_t n_kv, size_t* bytes) {
-  BF_CHECK_ARG(bytes && nnz >= 0 && n_kv >= 0, "reverse_index_packed_workspace_size: bad arguments");
+extern "C" int bf_reverse_index_packed_workspace_size(int64_t nnz, size_t* bytes) {
+  BF_CHECK_ARG(bytes && nnz >= 0, "reverse_index_packed_workspace_size: bad arguments");
   size_t sort_bytes = 0;
-  const int n = int(nnz > 0 ? nnz : 1);
-  (void)hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, static_cast<const uint32_t*>(nullptr),
-                                           static_cast<uint32_t*>(nullptr), static_cast<const uint64_t*>(nullptr),
-                                           static_cast<uint64_t*>(nullptr), n);
-  *bytes = align_up(size_t(n) * 4) + align_up(size_t(n) * 8) + align_up(sort_bytes) + 256;
+  (void)hipcub::DeviceRadixSort::SortKeys(nullptr, sort_bytes, static_cast<const uint64_t*>(nullptr),
+                                          static_cast<uint64_t*>(nullptr), int(nnz > 0 ? nnz : 1));
+  *bytes = align_up(sort_bytes) + 256;
   return BF_OK;
 }
 
-extern "C" int bf_reverse_index_packed(const int32_t* kv, const uint64_t* rowpos, int64_t nnz, int64_t n_kv,
-                                       int64_t* kptr, int32_t* kq, int32_t* ke, void* workspace,
+extern "C" int bf_reverse_index_packed(const uint64_t* rkey, const int64_t* qptr, int64_t nnz, int64_t n_q,
+                                       int64_t n_kv, int32_t q_bits, int32_t slot_bits, int32_t global_token,
+                                       uint64_t* sorted, int64_t* kptr, int32_t* kq, int32_t* ke, void* workspace,
                                        size_t workspace_bytes, void* stream) {
-  BF_CHECK_ARG(kptr && n_kv >= 0 && nnz >= 0, "reverse_index_packed: bad arguments");
+  BF_CHECK_ARG(kptr && qptr && n_q >= 0 && n_kv >= 0 && nnz >= 0, "reverse_index_packed: bad arguments");
   BF_CHECK_ARG(nnz < (int64_t(1) << 31), "reverse_index_packed: sizes must fit int32");
+  const int kshift = q_bits + slot_bits;
+  const int id_bits = bits_for(uint64_t(n_kv > 0 ? n_kv : 1));
+  BF_CHECK_ARG(q_bits >= bits_for(uint64_t(n_q)) && slot_bits >= 1 && kshift + id_bits <= 64,
+               "reverse_index_packed: key fields (%d + %d + %d bits) do not fit", q_bits, slot_bits, id_bits);
   size_t need = 0;
-  bf_reverse_index_packed_workspace_size(nnz, n_kv, &need);
+  bf_reverse_index_packed_workspace_size(nnz, &need);
   BF_CHECK_ARG(workspace && workspace_bytes >= need, "reverse_index_packed: workspace %zu < %zu bytes",
                workspace_bytes, need);
   hipStream_t st = as_stream(stream);
@@ -438,21 +484,26 @@ extern "C" int bf_reverse_index_packed(const int32_t* kv, const uint64_t* rowpos
     BF_CHECK_HIP(hipMemsetAsync(kptr, 0, size_t(n_kv + 1) * sizeof(int64_t), st));
     return BF_OK;
   }
-  BF_CHECK_ARG(kv && rowpos && kq && ke, "reverse_index_packed: null tensor");
-  char* p = static_cast<char*>(workspace);
-  auto take = [&](size_t b) { char* q = p; p += align_up(b); return q; };
-  auto* keys_out = reinterpret_cast<uint32_t*>(take(size_t(nnz) * 4));
-  auto* vals_out = reinterpret_cast<uint64_t*>(take(size_t(nnz) * 8));
-  void* temp = p;
-  size_t tb = workspace_bytes - size_t(p - static_cast<char*>(workspace));
-  const int end_bit = bits_for(uint64_t(n_kv > 0 ? n_kv : 1));
-  BF_CHECK_HIP(hipcub::DeviceRadixSort::SortPairs(temp, tb, reinterpret_cast<const uint32_t*>(kv), keys_out, rowpos,
-                                                  vals_out, int(nnz), 0, end_bit, st));
-  BF_LAUNCH("boundaries_kernel", boundaries_kernel<uint32_t>, dim3(blocks_for(nnz + 1)), dim3(kThreads), 0, st, keys_out,
-            nnz, uint64_t(1), n_kv, kptr);
+  BF_CHECK_ARG(rkey && sorted && kq, "reverse_index_packed: null tensor");
+  size_t tb = workspace_bytes;
+  // only the id bits are sorted; the stable passes keep each id's entries in CSR order
+  BF_CHECK_HIP(hipcub::DeviceRadixSort::SortKeys(workspace, tb, rkey, sorted, int(nnz), kshift, kshift + id_bits, st));
+  BF_LAUNCH("unpack_rkey_kernel", unpack_rkey_kernel, dim3(blocks_for(nnz + 1)), dim3(kThreads), 0, st, sorted, nnz,
+            kshift, slot_bits, int(global_token != 0), qptr, n_kv, kptr, kq, ke);
   BF_CHECK_LAUNCH();
-  BF_LAUNCH("unpack_row_entry_kernel", unpack_row_entry_kernel, dim3(blocks_for(nnz)), dim3(kThreads), 0, st, vals_out,
-            nnz, kq, ke);
+  return BF_OK;
+}
+
+extern "C" int bf_reverse_entries(const uint64_t* sorted, const int64_t* qptr, int64_t nnz, int64_t n_q,
+                                  int32_t q_bits, int32_t slot_bits, int32_t global_token, int32_t* ke,
+                                  void* stream) {
+  BF_CHECK_ARG(qptr && nnz >= 0 && nnz < (int64_t(1) << 31) && n_q >= 0, "reverse_entries: bad arguments");
+  BF_CHECK_ARG(q_bits >= bits_for(uint64_t(n_q)) && slot_bits >= 1 && q_bits + slot_bits <= 33,
+               "reverse_entries: bad key fields (%d + %d bits)", q_bits, slot_bits);
+  if (nnz == 0) return BF_OK;
+  BF_CHECK_ARG(sorted && ke, "reverse_entries: null tensor");
+  BF_LAUNCH("reverse_entries_kernel", reverse_entries_kernel, dim3(blocks_for(nnz)), dim3(kThreads), 0,
+            as_stream(stream), sorted, nnz, q_bits + slot_bits, slot_bits, int(global_token != 0), qptr, ke);
   BF_CHECK_LAUNCH();
   return BF_OK;
 }

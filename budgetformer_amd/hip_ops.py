@@ -320,9 +320,23 @@ def build_edge_table(rowptr, col, in_ptr, in_src, num_edges: int, q_lo: int, n_q
 
 
 # ------------------------------------------------------------------ index formats
-def table_to_csr(table: torch.Tensor, row_len: torch.Tensor, global_token: bool = False, with_rowpos: bool = False):
-    """Query-major table -> (qptr [n_q+1] int64, kv [nnz] int32), plus rowpos (uint64 as int64 [nnz],
-    (query << 32 | position)) with ``with_rowpos``: the reverse index's sort values."""
+def _bits_for(maxval: int) -> int:
+    """Bits that hold every value in [0, maxval] (at least 1)."""
+    return max(1, int(maxval).bit_length())
+
+
+@dataclass
+class ReverseKeys:
+    """table_to_csr's per-entry reverse-index sort keys: id << (q_bits + slot_bits) | query << slot_bits | slot."""
+    keys: torch.Tensor          # uint64 as int64 [nnz]
+    q_bits: int
+    slot_bits: int
+    global_token: bool
+
+
+def table_to_csr(table: torch.Tensor, row_len: torch.Tensor, global_token: bool = False, with_keys: bool = False):
+    """Query-major table -> (qptr [n_q+1] int64, kv [nnz] int32), plus the reverse-index sort keys
+    (``ReverseKeys``, or None when the query and slot fields need more than 33 bits) with ``with_keys``."""
     dev = table.device
     _require(table, "table", torch.int32)
     _require(row_len, "row_len", torch.int32, dev)
@@ -334,10 +348,14 @@ def table_to_csr(table: torch.Tensor, row_len: torch.Tensor, global_token: bool 
     N.call("bf_table_csr_ptr", _p(row_len), n_rows, int(global_token), _p(qptr), C.byref(nnz), _p(ws), ws.numel(),
            _stream(dev))
     kv = torch.empty(max(nnz.value, 1), dtype=torch.int32, device=dev)[: nnz.value]
-    rowpos = torch.empty(max(nnz.value, 1), dtype=torch.int64, device=dev)[: nnz.value] if with_rowpos else None
+    rk = None
+    q_bits, slot_bits = _bits_for(n_q), _bits_for(width)
+    if with_keys and q_bits + slot_bits <= 33:
+        rk = ReverseKeys(torch.empty(max(nnz.value, 1), dtype=torch.int64, device=dev)[: nnz.value], q_bits,
+                         slot_bits, bool(global_token))
     N.call("bf_table_to_csr", _p(table), _p(row_len), n_rows, width, int(global_token), _p(qptr), _p(kv),
-           _p(rowpos), _stream(dev))
-    return (qptr, kv, rowpos) if with_rowpos else (qptr, kv)
+           _p(rk.keys) if rk is not None else None, q_bits, slot_bits, _stream(dev))
+    return (qptr, kv, rk) if with_keys else (qptr, kv)
 
 
 def coo_to_csr(edge_index: torch.Tensor, n_q: int, n_kv: int):
@@ -374,21 +392,36 @@ def reverse_index(qptr: torch.Tensor, kv: torch.Tensor, n_kv: int):
     return kptr, kq, ke
 
 
-def reverse_index_packed(kv: torch.Tensor, rowpos: torch.Tensor, n_kv: int):
-    """reverse_index from table_to_csr's rowpos (one sort, no row recovery)."""
-    dev = kv.device
-    _require(kv, "kv", torch.int32)
-    _require(rowpos, "rowpos", torch.int64, dev)
-    nnz = kv.numel()
-    if rowpos.numel() != nnz:
-        raise ValueError("rowpos must have one value per entry")
-    ws = _workspace(_size_query("bf_reverse_index_packed_workspace_size", nnz, n_kv), dev)
+def reverse_index_packed(rk: ReverseKeys, qptr: torch.Tensor, n_kv: int, entries: bool = True):
+    """reverse_index from table_to_csr's sort keys (one sort of the id bits, no row recovery):
+    (kptr, kq, ke, sorted). ``entries=False`` skips ke (a gather of qptr that only a bias or factor
+    needs; ``reverse_entries(sorted, qptr)`` gives it later) and returns ke = None."""
+    dev = qptr.device
+    _require(qptr, "qptr", torch.int64)
+    _require(rk.keys, "keys", torch.int64, dev)
+    nnz = rk.keys.numel()
+    ws = _workspace(_size_query("bf_reverse_index_packed_workspace_size", nnz), dev)
+    srt = ReverseKeys(torch.empty(max(nnz, 1), dtype=torch.int64, device=dev)[:nnz], rk.q_bits, rk.slot_bits,
+                      rk.global_token)
     kptr = torch.empty(n_kv + 1, dtype=torch.int64, device=dev)
     kq = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)[:nnz]
-    ke = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)[:nnz]
-    N.call("bf_reverse_index_packed", _p(kv), _p(rowpos), nnz, n_kv, _p(kptr), _p(kq), _p(ke), _p(ws), ws.numel(),
+    ke = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)[:nnz] if entries else None
+    N.call("bf_reverse_index_packed", _p(rk.keys), _p(qptr), nnz, qptr.numel() - 1, n_kv, rk.q_bits, rk.slot_bits,
+           int(rk.global_token), _p(srt.keys), _p(kptr), _p(kq), _p(ke) if entries else None, _p(ws), ws.numel(),
            _stream(dev))
-    return kptr, kq, ke
+    return kptr, kq, ke, srt
+
+
+def reverse_entries(srt: ReverseKeys, qptr: torch.Tensor) -> torch.Tensor:
+    """ke (CSR position per reverse entry, int32) from reverse_index_packed's sorted keys."""
+    dev = qptr.device
+    _require(qptr, "qptr", torch.int64)
+    _require(srt.keys, "keys", torch.int64, dev)
+    nnz = srt.keys.numel()
+    ke = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)[:nnz]
+    N.call("bf_reverse_entries", _p(srt.keys), _p(qptr), nnz, qptr.numel() - 1, srt.q_bits, srt.slot_bits,
+           int(srt.global_token), _p(ke), _stream(dev))
+    return ke
 
 
 def expand_rows(ptr: torch.Tensor, nnz: int) -> torch.Tensor:
@@ -476,7 +509,8 @@ class AttentionIndex:
     kplan: Optional[SplitPlan] = None
     korder: Optional[torch.Tensor] = None
     _rows: Optional[torch.Tensor] = field(default=None, repr=False)
-    _rowpos: Optional[torch.Tensor] = field(default=None, repr=False)   # from_table: sort values, until used
+    _rkeys: Optional[ReverseKeys] = field(default=None, repr=False)   # from_table: sort keys, until used
+    _sorted: Optional[ReverseKeys] = field(default=None, repr=False)  # sorted keys, until ke is needed
 
     @property
     def nnz(self) -> int:
@@ -496,9 +530,10 @@ class AttentionIndex:
         if self.qplan is None:
             self.qplan = split_plan(self.qptr, self.nnz, self.chunk, self.item, resolve=False)
         if self.kptr is None:
-            if self._rowpos is not None:
-                self.kptr, self.kq, self.ke = reverse_index_packed(self.kv, self._rowpos, self.n_kv)
-                self._rowpos = None
+            if self._rkeys is not None and self._rkeys.q_bits + self._rkeys.slot_bits + _bits_for(self.n_kv) <= 64:
+                self.kptr, self.kq, _, self._sorted = reverse_index_packed(self._rkeys, self.qptr, self.n_kv,
+                                                                           entries=False)
+                self._rkeys = None
             else:
                 self.kptr, self.kq, self.ke = reverse_index(self.qptr, self.kv, self.n_kv)
         if self.kplan is None:
@@ -506,6 +541,14 @@ class AttentionIndex:
         if self.korder is None:
             self.korder = row_order(self.kptr)
         resolve_plans(self.qplan, self.kplan)      # both plans' counts in one read
+        return self
+
+    def ensure_entries(self):
+        """The CSR position of every reverse entry (ke), which the dk/dv pass reads only with a bias or factor."""
+        self.ensure_backward()
+        if self.ke is None and self.nnz:
+            self.ke = reverse_entries(self._sorted, self.qptr)
+            self._sorted = None
         return self
 
     def entry_rows(self) -> torch.Tensor:
@@ -520,8 +563,10 @@ class AttentionIndex:
         src = expand_rows(self.kptr, self.nnz)
         return torch.stack([src, self.kq.to(torch.int64)])
 
-    def struct(self, backward: bool) -> N.AttnIndex:
+    def struct(self, backward: bool, entries: bool = False) -> N.AttnIndex:
         self.ensure_backward() if backward else self.ensure_forward()
+        if backward and entries:
+            self.ensure_entries()
         s = N.AttnIndex()
         s.n_q, s.n_kv, s.nnz = self.n_q, self.n_kv, self.nnz
         s.qptr, s.kv = self.qptr.data_ptr(), self.kv.data_ptr() if self.nnz else None
@@ -534,7 +579,7 @@ class AttentionIndex:
             kp = self.kplan
             s.kptr = self.kptr.data_ptr()
             s.kq = self.kq.data_ptr() if self.nnz else None
-            s.ke = self.ke.data_ptr() if self.nnz else None
+            s.ke = self.ke.data_ptr() if (self.nnz and self.ke is not None) else None
             s.k_items, s.k_heavy = kp.items, kp.heavy
             s.k_nitems, s.k_item_off, s.k_item_row, s.k_heavy_rows = (
                 kp.nitems.data_ptr(), kp.item_off.data_ptr(), kp.item_row.data_ptr(), kp.heavy_rows.data_ptr())
@@ -544,10 +589,10 @@ class AttentionIndex:
     @classmethod
     def from_table(cls, table, row_len, global_token: bool = False, n_kv: Optional[int] = None,
                    chunk: int = DEFAULT_CHUNK, item: int = DEFAULT_ITEM):
-        qptr, kv, rowpos = table_to_csr(table, row_len, global_token, with_rowpos=True)
+        qptr, kv, rk = table_to_csr(table, row_len, global_token, with_keys=True)
         n_q = qptr.numel() - 1
         return cls(n_q=n_q, n_kv=n_kv if n_kv is not None else n_q, qptr=qptr, kv=kv, chunk=chunk, item=item,
-                   _rowpos=rowpos)
+                   _rkeys=rk)
 
     @classmethod
     def from_coo(cls, edge_index, n_q: int, n_kv: Optional[int] = None, chunk: int = DEFAULT_CHUNK,
@@ -609,7 +654,7 @@ def attn_backward(idx: AttentionIndex, q, k, v, out, Z, dout, bias=None, factor=
     _require(Z, "Z", torch.float32, q.device)
     _check_edge_tensor(bias, "bias", idx, H, q.device)
     _check_edge_tensor(factor, "factor", idx, H, q.device)
-    st = idx.struct(backward=True)
+    st = idx.struct(backward=True, entries=bias is not None or factor is not None)
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)

@@ -236,15 +236,18 @@ int bf_chung_lu(int64_t num_nodes, int64_t pairs, double exponent, double i0, do
  * every query t >= 1 also attends to kv 0; then n_q = n_rows + 1.
  * bf_table_csr_ptr writes qptr (a prefix sum of the row lengths) and returns
  * nnz = qptr[n_q] on the host (it synchronises the stream, so the caller can
- * size kv); bf_table_to_csr then fills kv, and, when rowpos is not NULL,
- * rowpos uint64 [nnz] = (query << 32 | position) per entry: the sort values
- * bf_reverse_index_packed takes. Workspace: bf_scan_workspace_size(n_q).    */
+ * size kv); bf_table_to_csr then fills kv, and, when rkey is not NULL,
+ * rkey uint64 [nnz] = (id << (q_bits + slot_bits) | query << slot_bits | slot)
+ * per entry, the sort keys bf_reverse_index_packed takes (slot = position in
+ * the query's row; the token row's entries carry slot 0). Needs
+ * q_bits >= bits of n_q, slot_bits >= bits of width and q_bits + slot_bits
+ * <= 33 (BF_ERR_INVALID otherwise). Workspace: bf_scan_workspace_size(n_q). */
 int bf_scan_workspace_size(int64_t n, size_t* bytes);
 int bf_table_csr_ptr(const int32_t* row_len, int64_t n_rows, int32_t global_token, int64_t* qptr,
                      int64_t* nnz_host, void* workspace, size_t workspace_bytes, void* stream);
 int bf_table_to_csr(const int32_t* table, const int32_t* row_len, int64_t n_rows, int32_t width,
-                    int32_t global_token, const int64_t* qptr, int32_t* kv, uint64_t* rowpos,
-                    void* stream);
+                    int32_t global_token, const int64_t* qptr, int32_t* kv, uint64_t* rkey,
+                    int32_t q_bits, int32_t slot_bits, void* stream);
 
 /* Reference COO edge_index [2, nnz] (row 0 = key/value node, row 1 = query
  * node; models/graphormer_dist_node_level.py:231-232) -> attention CSR with
@@ -273,14 +276,22 @@ int bf_reverse_index(const int64_t* qptr, const int32_t* kv, int64_t n_q, int64_
                      int64_t* kptr, int32_t* kq, int32_t* ke,
                      void* workspace, size_t workspace_bytes, void* stream);
 
-/* bf_reverse_index when the (query << 32 | position) value of every entry is
- * already at hand (bf_table_to_csr's rowpos): the same kptr / kq / ke from
- * one sort, without recovering the rows. Workspace:
- * bf_reverse_index_packed_workspace_size.                                   */
-int bf_reverse_index_packed_workspace_size(int64_t nnz, int64_t n_kv, size_t* bytes);
-int bf_reverse_index_packed(const int32_t* kv, const uint64_t* rowpos, int64_t nnz, int64_t n_kv,
-                            int64_t* kptr, int32_t* kq, int32_t* ke, void* workspace,
-                            size_t workspace_bytes, void* stream);
+/* bf_reverse_index from bf_table_to_csr's sort keys: one radix sort of the
+ * 8-byte keys over their id bits only (stable, so each id's entries stay in
+ * CSR order) into sorted uint64 [nnz], then one pass that writes kptr and
+ * decodes kq. ke (may be NULL) is decoded in the same pass: qptr[query] +
+ * slot, id - 1 for the token row when global_token; it is a random gather of
+ * qptr, which the dk/dv pass needs only with a bias or factor, so a caller may
+ * keep `sorted` and call bf_reverse_entries later instead. Same kptr / kq /
+ * ke as bf_reverse_index. Workspace: bf_reverse_index_packed_workspace_size. */
+int bf_reverse_index_packed_workspace_size(int64_t nnz, size_t* bytes);
+int bf_reverse_index_packed(const uint64_t* rkey, const int64_t* qptr, int64_t nnz, int64_t n_q, int64_t n_kv,
+                            int32_t q_bits, int32_t slot_bits, int32_t global_token, uint64_t* sorted,
+                            int64_t* kptr, int32_t* kq, int32_t* ke, void* workspace, size_t workspace_bytes,
+                            void* stream);
+/* ke [nnz] from bf_reverse_index_packed's sorted keys.                       */
+int bf_reverse_entries(const uint64_t* sorted, const int64_t* qptr, int64_t nnz, int64_t n_q, int32_t q_bits,
+                       int32_t slot_bits, int32_t global_token, int32_t* ke, void* stream);
 
 /* Row id of every entry of a CSR (rows[i] = r for ptr[r] <= i < ptr[r+1]). */
 int bf_expand_rows(const int64_t* ptr, int64_t n_rows, int64_t nnz, int64_t* rows, void* stream);
@@ -322,7 +333,8 @@ typedef struct bf_attn_index {
   const int32_t* kv;            /* [nnz]   kv id per edge, query-major              */
   const int64_t* kptr;          /* [n_kv+1] reverse offsets (backward only)         */
   const int32_t* kq;            /* [nnz]   query per reverse entry (backward only)  */
-  const int32_t* ke;            /* [nnz]   CSR position per reverse entry           */
+  const int32_t* ke;            /* [nnz]   CSR position per reverse entry (backward
+                                   with a bias or factor only; else may be NULL)   */
   int32_t chunk;                /* rows longer than this use the split plan         */
   int32_t item;                 /* entries per split item                           */
   int32_t q_items, q_heavy;     /* query-side plan (bf_split_plan on qptr): counts  */

@@ -120,6 +120,38 @@ def test_fp32_bias_and_dbias(hip_device):
         assert _rel_err(got, ref) < 1e-5
 
 
+@pytest.mark.parametrize("token", [False, True])
+def test_table_index_plain_then_bias_backward(hip_device, token):
+    """An index built from a table keeps its reverse entries' CSR positions lazy: a plain backward
+    runs without them, a later backward with a bias and a factor derives them from the sorted keys."""
+    import numpy as np
+    from budgetformer_amd.hip_ops import AttentionIndex
+    rng = np.random.default_rng(21 + token)
+    n, width, H, hn = 400, 6, 8, 16
+    row_len = rng.integers(0, width + 1, n).astype(np.int32)
+    table = np.full((n, width), -1, dtype=np.int32)
+    for r in range(n):
+        table[r, :row_len[r]] = np.sort(rng.choice(n, row_len[r], replace=False))
+    idx = AttentionIndex.from_table(torch.from_numpy(table).to(hip_device), torch.from_numpy(row_len).to(hip_device),
+                                    global_token=token, chunk=5, item=7)
+    S = idx.n_q
+    q, k, v, _, dout = _inputs(S, H, hn, 1, seed=31, mult=1.4)
+    ei_o = _coo_order(idx)
+    out, dq, dk, dv, _ = _run(hip_device, q, k, v, idx, dout)
+    assert idx.ke is None                       # not derived for a plain backward
+    ro, rZ, rdq, rdk, rdv, _ = _oracle(q, k, v, ei_o, dout)
+    for got, ref in ((out, ro), (dq, rdq), (dk, rdk), (dv, rdv)):
+        assert _rel_err(got, ref) < 1e-5
+    g = torch.Generator().manual_seed(5)
+    bias_e = torch.randn(idx.nnz, H, generator=g)
+    factor = (torch.rand(idx.nnz, H, generator=g) >= 0.3).float() / 0.7
+    out, dq, dk, dv, db = _run(hip_device, q, k, v, idx, dout, bias_e=bias_e, factor_e=factor)
+    assert idx.ke is not None
+    ro, rZ, rdq, rdk, rdv, rdb = _oracle(q, k, v, ei_o, dout, bias_e=bias_e, factor_e=factor)
+    for got, ref in ((out, ro), (dq, rdq), (dk, rdk), (dv, rdv), (db, rdb)):
+        assert _rel_err(got, ref) < 1e-5
+
+
 def test_fp32_gps_dropout_factor(hip_device):
     from budgetformer_amd.hip_ops import AttentionIndex
     S, H, hn = 200, 8, 16

@@ -224,7 +224,7 @@ def test_index_formats_against_numpy(hip_device, token):
     for r in range(n):
         table[r, :row_len[r]] = np.sort(rng.choice(n // 3 if r % 7 else 40, row_len[r], replace=False))
     t, rl = torch.from_numpy(table).to(hip_device), torch.from_numpy(row_len).to(hip_device)
-    qptr, kv, rowpos = hip_ops.table_to_csr(t, rl, token, with_rowpos=True)
+    qptr, kv, rk = hip_ops.table_to_csr(t, rl, token, with_keys=True)
     # numpy CSR of the same table
     rows, vals = [], []
     if token:
@@ -239,11 +239,21 @@ def test_index_formats_against_numpy(hip_device, token):
     assert np.array_equal(kv.cpu().numpy(), np.array(vals, dtype=np.int32))
     assert np.array_equal(np.diff(qptr.cpu().numpy()), np.bincount(np.array(rows), minlength=n_q))
     pos = np.arange(len(vals))
-    assert np.array_equal(rowpos.cpu().numpy(), (np.array(rows, dtype=np.int64) << 32) | pos)
+    # sort keys: id << (q_bits + slot_bits) | query << slot_bits | slot (token-row entries: slot 0)
+    rows_a = np.array(rows, dtype=np.int64)
+    slot = pos - qptr.cpu().numpy()[rows_a]
+    if token:
+        slot[rows_a == 0] = 0
+    expect = (np.array(vals, dtype=np.int64) << (rk.q_bits + rk.slot_bits)) | (rows_a << rk.slot_bits) | slot
+    assert (rk.q_bits, rk.slot_bits) == (int(n_q).bit_length(), int(width).bit_length())
+    assert np.array_equal(rk.keys.cpu().numpy(), expect)
     a = hip_ops.reverse_index(qptr, kv, n_q)
-    b = hip_ops.reverse_index_packed(kv, rowpos, n_q)
-    for x, y in zip(a, b):
+    b = hip_ops.reverse_index_packed(rk, qptr, n_q)
+    for x, y in zip(a, b[:3]):
         assert torch.equal(x, y)
+    lazy = hip_ops.reverse_index_packed(rk, qptr, n_q, entries=False)
+    assert lazy[2] is None and torch.equal(lazy[0], a[0]) and torch.equal(lazy[1], a[1])
+    assert torch.equal(hip_ops.reverse_entries(lazy[3], qptr), a[2])
     order = np.lexsort((pos, np.array(vals)))                    # (kv, position) order
     assert np.array_equal(b[1].cpu().numpy(), np.array(rows)[order]) and np.array_equal(b[2].cpu().numpy(), order)
     # row order: a permutation, capped lengths non-increasing
