@@ -89,7 +89,8 @@ def rocprof_summary(stats_csv: str, top: int = 25) -> str:
             kind = re.search(r"detail::(radix_sort_onesweep_\w+?|scan_impl|init_lookback\w*?)[<(]", name)
             short = "rocprim::" + (kind.group(1) if kind else "kernel")
         elif m:
-            short = m.group(1) + ("<bf16>" if "<unsigned short>" in name else "<float>" if "<float>" in name else "")
+            targs = re.match(r"\s*<([^<>()]*)>", name[m.end():])
+            short = m.group(1) + (f"<{targs.group(1).replace('unsigned short', 'bf16')}>" if targs else "")
         else:
             short = name.split("(")[0][:60]
         out.append(f"| {short} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | {float(r['MinNs']) / 1e3:.2f} | "
@@ -170,7 +171,8 @@ def main(argv=None):
         return 0
     if args.pmc_summary:
         names = ["attn_fwd_kernel", "attn_bwd_q_kernel", "attn_bwd_kv_kernel", "attn_fwd_reduce_kernel",
-                 "attn_bwd_kv_reduce_kernel", "rw_select_kernel", "real_select_merge_kernel"]
+                 "attn_bwd_kv_reduce_kernel", "rw_select_kernel", "real_select_fused_kernel",
+                 "table_fill_kernel", "unpack_rkey_kernel"]
         md, data = pmc_summary(*args.pmc_summary, args.copy_bytes, names)
         print(md)
         if args.pmc_json:
@@ -243,16 +245,22 @@ def main(argv=None):
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
            torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        ev[i][0].record()
+        tab, idx = build()
+        ev[i][1].record()
+        layer(idx)
+        ev[i][2].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    # per-kernel durations from a separate pass of the same steps: the library's per-launch event
+    # pairs cost host time, so they stay out of the timed loop above
     with _native.KernelTimer() as timer:
-        t0 = time.perf_counter()
         for i in range(args.steps):
-            ev[i][0].record()
             tab, idx = build()
-            ev[i][1].record()
             layer(idx)
-            ev[i][2].record()
         torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
         kstats = timer.stats()
     build_ms = sum(a.elapsed_time(b) for a, b, _ in ev) / args.steps
     attn_ms = sum(b.elapsed_time(c) for _, b, c in ev) / args.steps
