@@ -519,34 +519,43 @@ __device__ __forceinline__ void group_merge_keys(uint32_t (&lk)[K]) {
   }
 }
 
+constexpr int pow2_at_least(int x) { return x <= 1 ? 1 : 2 * pow2_at_least((x + 1) / 2); }
+
 // Writes table row qi from the real winners lk[0, k_real) (kNoKey = none) and
-// the RW selection rw_kv[qi, 0 .. rw_cnt[qi]): the KR + KW ids are sorted by
-// an odd-even transposition network in registers and stored ascending
-// (unique values when dedup), padded with -1 to width.
+// the RW selection rw_kv[qi, 0 .. rw_cnt[qi]): the KR + KW ids, padded to a
+// power of two, are sorted by a bitonic network in registers and stored
+// ascending (unique values when dedup), padded with -1 to width.
 template <int KR, int KW>
 __device__ __forceinline__ void emit_row(const uint32_t (&lk)[KR], uint32_t base, int k_real,
                                          const int32_t* __restrict__ rw_kv, const int32_t* __restrict__ rw_cnt,
                                          int k_rw, int64_t qi, int dedup, int32_t* __restrict__ table, int width,
                                          int32_t* __restrict__ row_len) {
-  constexpr int NV = KR + KW;
+  constexpr int NV = pow2_at_least(KR + KW);
   constexpr int32_t kPad = 0x7fffffff;          // sorts after every node id (ids < 2^31 - 1)
   int32_t v[NV];
 #pragma unroll
   for (int j = 0; j < KR; ++j) v[j] = (j < k_real && lk[j] != kNoKey) ? src_of(lk[j], base) : kPad;
 #pragma unroll
-  for (int j = 0; j < KW; ++j) v[KR + j] = kPad;
+  for (int j = KR; j < NV; ++j) v[j] = kPad;
   if (rw_kv != nullptr && KW > 0) {
     const int n_w = rw_cnt[qi];
 #pragma unroll
     for (int j = 0; j < KW; ++j) v[KR + j] = (j < n_w && j < k_rw) ? rw_kv[qi * k_rw + j] : kPad;
   }
 #pragma unroll
-  for (int r = 0; r < NV; ++r) {
+  for (int k = 2; k <= NV; k <<= 1) {
 #pragma unroll
-    for (int j = r & 1; j + 1 < NV; j += 2) {
-      const int32_t x = v[j], y = v[j + 1];
-      v[j] = x < y ? x : y;
-      v[j + 1] = x < y ? y : x;
+    for (int j = k >> 1; j > 0; j >>= 1) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int l = i ^ j;
+        if (l > i) {
+          const int32_t x = v[i], y = v[l];
+          const bool up = (i & k) == 0;
+          v[i] = (x < y) == up ? x : y;
+          v[l] = (x < y) == up ? y : x;
+        }
+      }
     }
   }
   int32_t* out = table + qi * width;
@@ -682,8 +691,8 @@ int launch_real_merge(const int64_t* in_ptr, const int32_t* in_src, int64_t num_
                       int32_t* row_len, const int32_t* hubs, int64_t n_hubs, int64_t hub_threshold,
                       int32_t* hub_sel, int32_t* hub_cnt, hipStream_t st, LightSplit split = LightSplit()) {
   if (n_q == 0) return BF_OK;
-  const bool light = split.light_max >= 0 && qids == nullptr && !key_order && k_real <= 8 &&
-                     (rw_kv == nullptr || k_rw <= 8);
+  const bool light = split.light_max >= 0 && qids == nullptr && !key_order && k_real <= 16 &&
+                     (rw_kv == nullptr || k_rw <= 16);
   if (k_real <= 0) n_hubs = 0;
   if (light) {
     const int64_t heavy = k_real > 0 ? split.n_heavy : 0;
@@ -697,14 +706,22 @@ int launch_real_merge(const int64_t* in_ptr, const int32_t* in_src, int64_t num_
             0, st, in_ptr, in_src, q_lo, n_q, k_real, kc, rw_kv, rw_cnt, k_rw, dedup, table, width, row_len, hubs,    \
             n_hubs, hub_thr, split.heavy, heavy, light_max, vec4)
     const int kw = rw_kv ? k_rw : 0;
-    if (k_real <= 4 && kw <= 4)
+    const int kr = k_real <= 4 ? 4 : k_real <= 8 ? 8 : 16;
+    const int kwp = kw <= 4 ? 4 : kw <= 8 ? 8 : 16;
+    if (kr == 4 && kwp == 4)
       BF_LAUNCH_FUSED(4, 4);
-    else if (k_real <= 4)
+    else if (kr == 4 && kwp == 8)
       BF_LAUNCH_FUSED(4, 8);
-    else if (kw <= 4)
+    else if (kr == 8 && kwp == 4)
       BF_LAUNCH_FUSED(8, 4);
-    else
+    else if (kr == 8 && kwp == 8)
       BF_LAUNCH_FUSED(8, 8);
+    else if (kr == 16 && kwp == 16)
+      BF_LAUNCH_FUSED(16, 16);
+    else if (kr == 16)
+      BF_LAUNCH_FUSED(16, 8);
+    else
+      BF_LAUNCH_FUSED(8, 16);
 #undef BF_LAUNCH_FUSED
     BF_CHECK_LAUNCH();
     return BF_OK;

@@ -112,8 +112,8 @@ def build_attention_edges(graph: CSRGraph, *, real_edges_per_query: int, rw_edge
     seed = int(edge_seed if philox_seed is None else philox_seed)
     plan = plan_edge_build(graph.device, n_q, b_r, b_w, q_lo=q_lo, usable_bytes=usable_bytes)
     all_hubs = graph.hubs() if b_r > 0 else None
-    # queries above LIGHT_MAX in-neighbours take the group path; the rest one thread each (k <= 8)
-    light = b_r > 0 and b_r <= 8 and b_w <= 8
+    # queries above LIGHT_MAX in-neighbours take the group path; the rest one thread each (k <= 16)
+    light = b_r > 0 and b_r <= 16 and b_w <= 16
     all_heavy = graph.heavy() if light else None
 
     def in_range(lst, lo, cnt):

@@ -191,11 +191,13 @@ def test_hub_path_bit_exact(hip_device, b_r, b_w, thr):
     assert np.array_equal(tab.table.cpu().numpy(), ref_t[200:1700])
 
 
-@pytest.mark.parametrize("b_r,b_w", [(4, 4), (8, 8), (3, 0), (8, 2)])
+@pytest.mark.parametrize("b_r,b_w", [(4, 4), (8, 8), (3, 0), (8, 2), (16, 16), (12, 5), (5, 13), (16, 0)])
 def test_light_heavy_split_bit_exact(hip_device, b_r, b_w):
-    """Thread-per-query rows (in-degree <= light_max) and group rows give the same table at any cut."""
+    """Thread-per-query rows (in-degree <= light_max) and group rows give the same table at any cut,
+    for every register-list size of the fused kernel (4, 8, 16 real x 4, 8, 16 RW)."""
     from budgetformer_amd import hip_ops
-    n, P, L = 3000, 2, 4
+    n, L = 3000, 4
+    P = 4 if b_w > 8 else 2
     rowptr, col = _graph(n, 40000, seed=b_r * 3 + b_w)
     g = _dev_graph(rowptr, col, n, hip_device)
     u = np.random.default_rng(b_r).random((n * P, L), dtype=np.float32)
