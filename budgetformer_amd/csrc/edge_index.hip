@@ -206,13 +206,14 @@ __global__ __launch_bounds__(kThreads) void order_hist_kernel(const int64_t* __r
   if (h[threadIdx.x]) atomicAdd(&hist[threadIdx.x], h[threadIdx.x]);
 }
 
-// Each block orders kOrderChunk consecutive rows: it counts them per bucket in
+// Each block orders `chunk` consecutive rows: it counts them per bucket in
 // LDS, reserves one range per bucket with a single global atomic (few blocks,
 // so the popular short-row buckets see little contention), then places them.
-constexpr int kOrderChunk = 16 * kThreads;
+// Smaller chunks were measured no faster on 169K rows and slower on 2.4M.
+constexpr int64_t kOrderChunk = 16 * kThreads;
 
 __global__ __launch_bounds__(kThreads) void order_scatter_kernel(const int64_t* __restrict__ ptr, int64_t n_rows,
-                                                                 const uint32_t* __restrict__ hist,
+                                                                 int64_t chunk, const uint32_t* __restrict__ hist,
                                                                  uint32_t* __restrict__ cursor,
                                                                  int32_t* __restrict__ order) {
   __shared__ uint32_t base[kBuckets];
@@ -230,8 +231,8 @@ __global__ __launch_bounds__(kThreads) void order_scatter_kernel(const int64_t* 
   const uint32_t start = tid ? base[tid - 1] : 0u;
   __syncthreads();
   base[tid] = start;
-  const int64_t r0 = int64_t(blockIdx.x) * kOrderChunk;
-  const int64_t r1 = r0 + kOrderChunk < n_rows ? r0 + kOrderChunk : n_rows;
+  const int64_t r0 = int64_t(blockIdx.x) * chunk;
+  const int64_t r1 = r0 + chunk < n_rows ? r0 + chunk : n_rows;
   for (int64_t r = r0 + tid; r < r1; r += kThreads) atomicAdd(&cnt[length_bucket(ptr, r)], 1u);
   __syncthreads();
   if (cnt[tid]) base[tid] += atomicAdd(&cursor[tid], cnt[tid]);
@@ -279,29 +280,49 @@ __global__ void split_count_kernel(const int64_t* __restrict__ ptr, int64_t n_ro
 }
 
 // item_off, the heavy-row list (compacted by the scanned flags), item_row of
-// each item (written by its row's thread: a split row has few items) and the
-// two plan counts.
-__global__ void split_rows_kernel(const int32_t* __restrict__ nitems, const uint64_t* __restrict__ packed_off,
-                                  int64_t n_rows, int64_t item_cap, int32_t* __restrict__ item_off,
-                                  int32_t* __restrict__ item_row, int32_t* __restrict__ heavy_rows,
-                                  int64_t heavy_cap, int32_t* __restrict__ counts) {
+// each item and the two plan counts. A row's thread writes the item_row of its
+// first kOwnItems items; rows with more (the Graphormer token row and column,
+// hubs) are queued in LDS and their remaining items written by the whole block.
+constexpr int kOwnItems = 8;
+
+__global__ __launch_bounds__(kThreads) void split_rows_kernel(
+    const int32_t* __restrict__ nitems, const uint64_t* __restrict__ packed_off, int64_t n_rows, int64_t item_cap,
+    int32_t* __restrict__ item_off, int32_t* __restrict__ item_row, int32_t* __restrict__ heavy_rows,
+    int64_t heavy_cap, int32_t* __restrict__ counts) {
+  __shared__ int64_t long_first[kThreads];
+  __shared__ int32_t long_n[kThreads], long_row[kThreads];
+  __shared__ int n_long;
+  if (threadIdx.x == 0) n_long = 0;
+  __syncthreads();
   const int64_t r = int64_t(blockIdx.x) * kThreads + threadIdx.x;
-  if (r >= n_rows) return;
-  const int n = nitems[r];
-  const uint64_t off = packed_off[r];
-  const int64_t first_item = int64_t(off >> 32);
-  const int64_t slot = int64_t(uint32_t(off));
-  item_off[r] = int32_t(first_item);
-  if (n > 0 && slot < heavy_cap) heavy_rows[slot] = int32_t(r);
-  for (int64_t j = 0; j < n && first_item + j < item_cap; ++j) item_row[first_item + j] = int32_t(r);
-  if (r == n_rows - 1) {
-    const int64_t items = first_item + n;
-    const int64_t heavy = slot + (n > 0 ? 1 : 0);
-    counts[0] = int32_t(items < item_cap ? items : item_cap);
-    counts[1] = int32_t(heavy < heavy_cap ? heavy : heavy_cap);
+  if (r < n_rows) {
+    const int n = nitems[r];
+    const uint64_t off = packed_off[r];
+    const int64_t first_item = int64_t(off >> 32);
+    const int64_t slot = int64_t(uint32_t(off));
+    item_off[r] = int32_t(first_item);
+    if (n > 0 && slot < heavy_cap) heavy_rows[slot] = int32_t(r);
+    for (int64_t j = 0; j < n && j < kOwnItems && first_item + j < item_cap; ++j) item_row[first_item + j] = int32_t(r);
+    if (n > kOwnItems) {
+      const int k = atomicAdd(&n_long, 1);
+      long_first[k] = first_item;
+      long_n[k] = n;
+      long_row[k] = int32_t(r);
+    }
+    if (r == n_rows - 1) {
+      const int64_t items = first_item + n;
+      const int64_t heavy = slot + (n > 0 ? 1 : 0);
+      counts[0] = int32_t(items < item_cap ? items : item_cap);
+      counts[1] = int32_t(heavy < heavy_cap ? heavy : heavy_cap);
+    }
+  }
+  __syncthreads();
+  for (int k = 0; k < n_long; ++k) {
+    const int64_t first_item = long_first[k];
+    for (int64_t j = kOwnItems + threadIdx.x; j < long_n[k] && first_item + j < item_cap; j += kThreads)
+      item_row[first_item + j] = long_row[k];
   }
 }
-
 
 }  // namespace
 }  // namespace bf
@@ -751,8 +772,9 @@ extern "C" int bf_row_order(const int64_t* ptr, int64_t n_rows, int32_t* order, 
   BF_LAUNCH("order_hist_kernel", order_hist_kernel, dim3(unsigned(blocks < 2048 ? blocks : 2048)), dim3(kThreads), 0,
             st, ptr, n_rows, hist);
   BF_CHECK_LAUNCH();
-  BF_LAUNCH("order_scatter_kernel", order_scatter_kernel, dim3(unsigned(ceil_div(n_rows, int64_t(kOrderChunk)))),
-            dim3(kThreads), 0, st, ptr, n_rows, hist, cursor, order);
+  const int64_t chunk = kOrderChunk;
+  BF_LAUNCH("order_scatter_kernel", order_scatter_kernel, dim3(unsigned(ceil_div(n_rows, chunk))), dim3(kThreads), 0,
+            st, ptr, n_rows, chunk, hist, cursor, order);
   BF_CHECK_LAUNCH();
   return BF_OK;
 }
