@@ -153,6 +153,9 @@ class EdgeBuildPlan:
     usable_bytes: int                      # budget the plan was made against (-1: unknown)
 
 
+_SMALL_BUILD_BYTES = 64 * 1024 * 1024
+
+
 def plan_edge_build(device, n_queries: int, real_edges_per_query: int, rw_edges_per_query: int, q_lo: int = 0,
                     usable_bytes: int = None) -> EdgeBuildPlan:
     """Shard the query range so each shard's transient fits next to the output table.
@@ -162,6 +165,11 @@ def plan_edge_build(device, n_queries: int, real_edges_per_query: int, rw_edges_
     """
     dev = torch.device(device)
     full = estimate_edge_build_bytes(n_queries, real_edges_per_query, rw_edges_per_query)
+    if usable_bytes is None and _GPU_PROCESS_MEMORY_CAP_BYTES <= 0 and \
+            full["transient"] + full["output"] <= _SMALL_BUILD_BYTES:
+        # too small to be worth sharding: one build, without querying the driver's free memory
+        # (a shortfall this small surfaces as the allocator's own OutOfMemoryError)
+        return EdgeBuildPlan(dev, [(q_lo, n_queries)], full["transient"], full["output"], -1)
     usable = _rw_gpu_usable_bytes(dev) if usable_bytes is None else int(usable_bytes)
     if usable < 0 or _FORCE_RW_ON_GPU or full["transient"] + full["output"] <= usable:
         return EdgeBuildPlan(dev, [(q_lo, n_queries)], full["transient"], full["output"], usable)

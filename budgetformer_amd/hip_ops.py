@@ -26,7 +26,10 @@ def _p(t: Optional[torch.Tensor]):
 
 
 def _stream(device: torch.device):
-    return C.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+    """The current HIP stream of ``device`` as a raw handle (what torch.cuda.current_stream(device).cuda_stream
+    gives, without building a Stream object on every call)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    return C.c_void_p(torch._C._cuda_getCurrentRawStream(idx))
 
 
 def _require(t: torch.Tensor, name: str, dtype: torch.dtype, device: torch.device = None):
@@ -461,23 +464,35 @@ def resolve_plans(*plans) -> None:
     pending = [p for p in plans if p is not None and p.items < 0]
     if not pending:
         return
-    vals = (pending[0].counts if len(pending) == 1 else torch.cat([p.counts for p in pending])).cpu().tolist()
+    # plans made with one shared counts buffer (split_plan(..., counts=...)) come back in one copy
+    base = pending[0].counts
+    shared = all(p.counts.untyped_storage().data_ptr() == base.untyped_storage().data_ptr() for p in pending)
+    if len(pending) == 1:
+        vals = base.cpu().tolist()
+    elif shared:
+        whole = torch.empty(0, dtype=torch.int32, device=base.device).set_(base.untyped_storage())
+        allv = whole.cpu().tolist()
+        vals = sum((allv[p.counts.storage_offset():p.counts.storage_offset() + 2] for p in pending), [])
+    else:
+        vals = torch.cat([p.counts for p in pending]).cpu().tolist()
     for i, p in enumerate(pending):
         p.items, p.heavy, p.counts = int(vals[2 * i]), int(vals[2 * i + 1]), None
 
 
 def split_plan(ptr: torch.Tensor, nnz: int, threshold: int = DEFAULT_CHUNK, item_size: int = DEFAULT_ITEM,
-               resolve: bool = True) -> SplitPlan:
+               resolve: bool = True, counts: Optional[torch.Tensor] = None) -> SplitPlan:
+    """Split plan of a CSR. ``counts`` (int32 [2], optional) receives the two plan counts on the device;
+    plans that share one buffer resolve with a single copy."""
     dev = ptr.device
     lib = N.load()
     n_rows = ptr.numel() - 1
     item_cap = int(lib.bf_split_item_capacity(nnz, threshold, item_size))
     heavy_cap = int(lib.bf_split_row_capacity(nnz, threshold))
-    nitems = torch.empty(max(n_rows, 1), dtype=torch.int32, device=dev)
-    item_off = torch.empty(max(n_rows, 1), dtype=torch.int32, device=dev)
-    item_row = torch.empty(max(item_cap, 1), dtype=torch.int32, device=dev)
-    heavy_rows = torch.empty(max(heavy_cap, 1), dtype=torch.int32, device=dev)
-    counts = torch.empty(2, dtype=torch.int32, device=dev)
+    r = max(n_rows, 1)
+    buf = torch.empty(2 * r + max(item_cap, 1) + max(heavy_cap, 1), dtype=torch.int32, device=dev)
+    nitems, item_off, item_row, heavy_rows = torch.split(buf, [r, r, max(item_cap, 1), max(heavy_cap, 1)])
+    if counts is None:
+        counts = torch.empty(2, dtype=torch.int32, device=dev)
     ws = _workspace(_size_query("bf_split_plan_workspace_size", n_rows), dev)
     N.call("bf_split_plan", _p(ptr), n_rows, threshold, item_size, _p(nitems), _p(item_off), _p(item_row), item_cap,
            _p(heavy_rows), heavy_cap, _p(counts), _p(ws), ws.numel(), _stream(dev))
@@ -511,6 +526,7 @@ class AttentionIndex:
     _rows: Optional[torch.Tensor] = field(default=None, repr=False)
     _rkeys: Optional[ReverseKeys] = field(default=None, repr=False)   # from_table: sort keys, until used
     _sorted: Optional[ReverseKeys] = field(default=None, repr=False)  # sorted keys, until ke is needed
+    _counts: Optional[torch.Tensor] = field(default=None, repr=False)  # both plans' device counts
 
     @property
     def nnz(self) -> int:
@@ -526,9 +542,16 @@ class AttentionIndex:
         resolve_plans(self.qplan)
         return self
 
+    def _plan_counts(self, side: int) -> torch.Tensor:
+        """Device slot for one side's plan counts; both sides share one buffer, read back together."""
+        if self._counts is None:
+            self._counts = torch.empty(4, dtype=torch.int32, device=self.device)
+        return self._counts[2 * side:2 * side + 2]
+
     def ensure_backward(self):
         if self.qplan is None:
-            self.qplan = split_plan(self.qptr, self.nnz, self.chunk, self.item, resolve=False)
+            self.qplan = split_plan(self.qptr, self.nnz, self.chunk, self.item, resolve=False,
+                                    counts=self._plan_counts(0))
         if self.kptr is None:
             if self._rkeys is not None and self._rkeys.q_bits + self._rkeys.slot_bits + _bits_for(self.n_kv) <= 64:
                 self.kptr, self.kq, _, self._sorted = reverse_index_packed(self._rkeys, self.qptr, self.n_kv,
@@ -537,7 +560,8 @@ class AttentionIndex:
             else:
                 self.kptr, self.kq, self.ke = reverse_index(self.qptr, self.kv, self.n_kv)
         if self.kplan is None:
-            self.kplan = split_plan(self.kptr, self.nnz, self.chunk, self.item, resolve=False)
+            self.kplan = split_plan(self.kptr, self.nnz, self.chunk, self.item, resolve=False,
+                                    counts=self._plan_counts(1))
         if self.korder is None:
             self.korder = row_order(self.kptr)
         resolve_plans(self.qplan, self.kplan)      # both plans' counts in one read
