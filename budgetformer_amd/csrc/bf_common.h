@@ -210,4 +210,20 @@ __host__ __device__ __forceinline__ float walk_uniform(uint64_t seed, uint64_t o
   return u24(x);
 }
 
+// walk_uniform for the steps l = 0, 1, 2, ... of one walk in order: one Philox
+// call per 4 steps instead of one per step (the same values).
+struct WalkStream {
+  uint64_t seed, offset, w;
+  U32x4 r;
+  __device__ __forceinline__ float at(int l) {
+    const int j = l & 3;
+    if (j == 0) {
+      const uint64_t blk = offset + uint64_t(l >> 2);
+      r = philox4x32_10(U32x4{uint32_t(w), uint32_t(w >> 32), uint32_t(blk), uint32_t(blk >> 32)}, uint32_t(seed),
+                        uint32_t(seed >> 32));
+    }
+    return u24(j == 0 ? r.x : j == 1 ? r.y : j == 2 ? r.z : r.w);
+  }
+};
+
 }  // namespace bf

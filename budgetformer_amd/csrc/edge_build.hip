@@ -48,8 +48,9 @@ __global__ __launch_bounds__(kThreads) void random_walk_kernel(
   int64_t cur = q;
   int64_t* row = walks + wl * (L + 1);
   row[0] = cur;
+  WalkStream rng{seed, offset, uint64_t(w), {}};
   for (int l = 0; l < L; ++l) {
-    const float uu = u ? u[wl * L + l] : walk_uniform(seed, offset, uint64_t(w), l);
+    const float uu = u ? u[wl * L + l] : rng.at(l);
     cur = walk_step(rowptr, col, cur, uu);
     row[l + 1] = cur;
   }
@@ -61,7 +62,8 @@ __global__ __launch_bounds__(kThreads) void walk_uniforms_kernel(int64_t q_lo, i
   const int64_t wl = int64_t(blockIdx.x) * kThreads + threadIdx.x;
   if (wl >= n_walks) return;
   const int64_t w = (q_lo + wl / P) * P + (wl % P);
-  for (int l = 0; l < L; ++l) u[wl * L + l] = walk_uniform(seed, offset, uint64_t(w), l);
+  WalkStream rng{seed, offset, uint64_t(w), {}};
+  for (int l = 0; l < L; ++l) u[wl * L + l] = rng.at(l);
 }
 
 // Walks from arbitrary start nodes; walk i draws its Philox stream as walk id (id_base + i).
@@ -74,8 +76,9 @@ __global__ __launch_bounds__(kThreads) void random_walk_starts_kernel(
   int64_t cur = starts[i];
   int64_t* row = walks + i * (L + 1);
   row[0] = cur;
+  WalkStream rng{seed, offset, id_base + uint64_t(i), {}};
   for (int l = 0; l < L; ++l) {
-    const float uu = u ? u[i * L + l] : walk_uniform(seed, offset, id_base + uint64_t(i), l);
+    const float uu = u ? u[i * L + l] : rng.at(l);
     cur = walk_step(rowptr, col, cur, uu);
     row[l + 1] = cur;
   }
@@ -122,12 +125,13 @@ __global__ __launch_bounds__(kThreads) void rw_select_kernel(
     const int64_t w = q * P + p;
     const int64_t wl = qi * P + p;
     int64_t cur = q;
+    WalkStream rng{seed, offset, uint64_t(w), {}};
     for (int l = 0; l < L; ++l) {
       if (q < 0) {
         cand[tid * L + l] = kNone;
         continue;
       }
-      const float uu = u ? u[wl * L + l] : walk_uniform(seed, offset, uint64_t(w), l);
+      const float uu = u ? u[wl * L + l] : rng.at(l);
       const int64_t nxt = walk_step(rowptr, col, cur, uu);
       bool keep = (l == 0) || (nxt != cur);
       if (keep && sub_ptr) keep = !sorted_contains(sub_src, sub_ptr[q], sub_ptr[q + 1], int32_t(nxt));

@@ -64,7 +64,7 @@ def _rows(table, row_len):
 
 
 @pytest.mark.parametrize("b_r,b_w,P,L", [(4, 4, 2, 4), (3, 0, 2, 4), (0, 3, 2, 4), (8, 8, 4, 4), (16, 16, 4, 8),
-                                         (2, 5, 1, 3), (1, 1, 2, 4)])
+                                         (2, 5, 1, 3), (1, 1, 2, 4), (20, 12, 4, 8)])
 def test_edge_table_bit_exact(hip_device, b_r, b_w, P, L):
     from budgetformer_amd.edges import build_attention_edges
     n = 2500
@@ -213,6 +213,24 @@ def test_light_heavy_split_bit_exact(hip_device, b_r, b_w):
     tab = build_attention_edges(g, real_edges_per_query=b_r, rw_edges_per_query=b_w, walk_length=L,
                                 walks_per_node=P, edge_seed=42, u=ut[300 * P:2300 * P], q_lo=300, n_q=2000)
     assert np.array_equal(tab.table.cpu().numpy(), ref_t[300:2300])
+
+
+def test_light_rows_with_unaligned_in_neighbour_array(hip_device):
+    """in_src not 16-byte aligned: the light rows fall back from 16-byte chunk loads to 4-byte loads."""
+    from budgetformer_amd import hip_ops
+    n, P, L, b_r, b_w = 2500, 2, 4, 4, 4
+    rowptr, col = _graph(n, 30000, seed=5)
+    g = _dev_graph(rowptr, col, n, hip_device)
+    u = torch.from_numpy(np.random.default_rng(5).random((n * P, L), dtype=np.float32)).to(hip_device)
+    buf = torch.empty(g.in_src.numel() + 1, dtype=torch.int32, device=hip_device)
+    buf[1:] = g.in_src
+    shifted = buf[1:]
+    assert shifted.data_ptr() % 16 != 0
+    ref_t, ref_len = et.build_edge_table(rowptr, col, n, b_r, b_w, L, P, 42, u.cpu().numpy())
+    for src in (g.in_src, shifted):
+        t, rl = hip_ops.build_edge_table(g.rowptr, g.col, g.in_ptr, src, g.num_edges, 0, n, P, L, b_r, b_w, 42, u=u,
+                                         hubs=g.hubs(64), hub_threshold=64, heavy=g.heavy(8), light_max=8)
+        assert np.array_equal(t.cpu().numpy(), ref_t) and np.array_equal(rl.cpu().numpy(), ref_len)
 
 
 @pytest.mark.parametrize("token", [False, True])
