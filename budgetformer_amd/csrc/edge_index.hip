@@ -283,7 +283,7 @@ __global__ void split_count_kernel(const int64_t* __restrict__ ptr, int64_t n_ro
 // each item and the two plan counts. A row's thread writes the item_row of its
 // first kOwnItems items; rows with more (the Graphormer token row and column,
 // hubs) are queued in LDS and their remaining items written by the whole block.
-constexpr int kOwnItems = 8;
+constexpr int kOwnItems = 32;
 
 __global__ __launch_bounds__(kThreads) void split_rows_kernel(
     const int32_t* __restrict__ nitems, const uint64_t* __restrict__ packed_off, int64_t n_rows, int64_t item_cap,
