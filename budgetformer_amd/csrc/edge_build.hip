@@ -113,11 +113,16 @@ __global__ __launch_bounds__(kThreads) void rw_select_kernel(
     const int32_t* __restrict__ qids, int64_t n_q, int P, int L, int K, uint32_t kc, const float* __restrict__ u,
     uint64_t seed, uint64_t offset, const int64_t* __restrict__ sub_ptr, const int32_t* __restrict__ sub_src,
     int32_t* __restrict__ sel_kv, int32_t* __restrict__ sel_cnt) {
-  extern __shared__ uint64_t cand[];  // [kThreads * L]
+  // [qpb][P*L + 1]: the odd row stride puts the rows the queries of a wave read
+  // at one time in different LDS banks (an unpadded stride of P*L*8 bytes maps
+  // them all to the same bank)
+  extern __shared__ uint64_t cand[];
   const int qpb = kThreads / P;
   const int tid = threadIdx.x;
   const int ql = tid / P;
   const int p = tid - ql * P;
+  const int M = P * L;
+  uint64_t* const mine = cand + ql * (M + 1) + p * L;      // this walk's L candidates
   const int64_t qi = int64_t(blockIdx.x) * qpb + ql;
   const bool active = ql < qpb && qi < n_q;
   if (active) {
@@ -128,21 +133,20 @@ __global__ __launch_bounds__(kThreads) void rw_select_kernel(
     WalkStream rng{seed, offset, uint64_t(w), {}};
     for (int l = 0; l < L; ++l) {
       if (q < 0) {
-        cand[tid * L + l] = kNone;
+        mine[l] = kNone;
         continue;
       }
       const float uu = u ? u[wl * L + l] : rng.at(l);
       const int64_t nxt = walk_step(rowptr, col, cur, uu);
       bool keep = (l == 0) || (nxt != cur);
       if (keep && sub_ptr) keep = !sorted_contains(sub_src, sub_ptr[q], sub_ptr[q + 1], int32_t(nxt));
-      cand[tid * L + l] = keep ? (uint64_t(edge_key(uint32_t(nxt), uint32_t(q), kc)) << 32) | uint32_t(nxt) : kNone;
+      mine[l] = keep ? (uint64_t(edge_key(uint32_t(nxt), uint32_t(q), kc)) << 32) | uint32_t(nxt) : kNone;
       cur = nxt;
     }
   }
   __syncthreads();
   if (!active) return;
-  const int M = P * L;
-  const uint64_t* c = cand + ql * M;
+  const uint64_t* c = cand + ql * (M + 1);
   for (int i = p; i < M; i += P) {
     const uint64_t ci = c[i];
     if (ci == kNone) continue;
@@ -673,7 +677,7 @@ int launch_rw_select(const int64_t* rowptr, const int32_t* col, int64_t num_node
                      int32_t* sel_kv, int32_t* sel_cnt, hipStream_t st) {
   if (n_q == 0) return BF_OK;
   const int qpb = kThreads / P;
-  const size_t lds = size_t(kThreads) * L * sizeof(uint64_t);
+  const size_t lds = size_t(qpb) * (size_t(P) * L + 1) * sizeof(uint64_t);
   BF_LAUNCH("rw_select_kernel", rw_select_kernel, dim3(unsigned(ceil_div(n_q, qpb))), dim3(kThreads), lds, st, rowptr, col,
             num_nodes, q_lo, qids, n_q, P, L, K, kc, u, seed, offset, sub_ptr, sub_src, sel_kv, sel_cnt);
   BF_CHECK_LAUNCH();
