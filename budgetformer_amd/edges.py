@@ -61,7 +61,7 @@ class EdgeTable:
                     raise NotImplementedError("the Graphormer global token needs the full query set")
             n_kv = self.num_nodes + (1 if self.global_token else 0)
             idx = AttentionIndex.from_table(self.table, self.row_len, self.global_token, n_kv=n_kv, chunk=chunk,
-                                            item=item)
+                                            item=item, check=False)
             self._index[(chunk, item)] = idx
         return idx
 

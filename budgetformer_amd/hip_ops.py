@@ -612,11 +612,29 @@ class AttentionIndex:
 
     @classmethod
     def from_table(cls, table, row_len, global_token: bool = False, n_kv: Optional[int] = None,
-                   chunk: int = DEFAULT_CHUNK, item: int = DEFAULT_ITEM):
+                   chunk: int = DEFAULT_CHUNK, item: int = DEFAULT_ITEM, check: bool = True):
+        """Index of a query-major table. ``check`` validates the table on the device first (row lengths
+        within the width, the ids of every row's first row_len slots within [0, n_kv)) with one host
+        read; the edge builder's own tables skip it (valid by construction)."""
+        n_q_tab = table.shape[0] + (1 if global_token else 0)
+        n_kv = n_kv if n_kv is not None else n_q_tab
+        if check and table.numel():
+            _require(table, "table", torch.int32)
+            _require(row_len, "row_len", torch.int32, table.device)
+            width = table.shape[1]
+            lens = row_len.to(torch.int64)
+            used = torch.arange(width, device=table.device)[None, :] < lens[:, None]
+            ids = torch.where(used, table, torch.zeros((), dtype=table.dtype, device=table.device))
+            lo = torch.where(used, table, torch.full((), 2**31 - 1, dtype=table.dtype, device=table.device))
+            stats = torch.stack([lens.min(), lens.max(), lo.min().to(torch.int64), ids.max().to(torch.int64)]).tolist()
+            shift = 1 if global_token else 0
+            if stats[0] < 0 or stats[1] > width:
+                raise ValueError(f"row_len must lie in [0, {width}] (got [{stats[0]}, {stats[1]}])")
+            if stats[1] > 0 and (stats[2] < 0 or stats[3] + shift >= n_kv):
+                raise ValueError(f"table ids must lie in [0, {n_kv - shift}) (got [{stats[2]}, {stats[3]}])")
         qptr, kv, rk = table_to_csr(table, row_len, global_token, with_keys=True)
         n_q = qptr.numel() - 1
-        return cls(n_q=n_q, n_kv=n_kv if n_kv is not None else n_q, qptr=qptr, kv=kv, chunk=chunk, item=item,
-                   _rkeys=rk)
+        return cls(n_q=n_q, n_kv=n_kv, qptr=qptr, kv=kv, chunk=chunk, item=item, _rkeys=rk)
 
     @classmethod
     def from_coo(cls, edge_index, n_q: int, n_kv: Optional[int] = None, chunk: int = DEFAULT_CHUNK,

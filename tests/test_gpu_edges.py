@@ -234,6 +234,30 @@ def test_light_rows_with_unaligned_in_neighbour_array(hip_device):
 
 
 @pytest.mark.parametrize("token", [False, True])
+def test_from_table_rejects_invalid_tables(hip_device, token):
+    """An external table is validated on the host side before any index kernel reads it."""
+    from budgetformer_amd.hip_ops import AttentionIndex
+    n, width = 50, 4
+    table = torch.full((n, width), -1, dtype=torch.int32, device=hip_device)
+    row_len = torch.zeros(n, dtype=torch.int32, device=hip_device)
+    table[:, 0] = torch.arange(n, dtype=torch.int32, device=hip_device)
+    row_len[:] = 1
+    AttentionIndex.from_table(table, row_len, token)                       # valid
+    bad = table.clone()
+    bad[7, 0] = n + 3                                                       # id beyond the kv rows
+    with pytest.raises(ValueError):
+        AttentionIndex.from_table(bad, row_len, token)
+    bad = table.clone()
+    bad[9, 0] = -1                                                          # padding inside row_len
+    with pytest.raises(ValueError):
+        AttentionIndex.from_table(bad, row_len, token)
+    long = row_len.clone()
+    long[3] = width + 1
+    with pytest.raises(ValueError):
+        AttentionIndex.from_table(table, long, token)
+
+
+@pytest.mark.parametrize("token", [False, True])
 def test_index_formats_against_numpy(hip_device, token):
     """table -> CSR (with the fused token fill), both reverse-index routes, the split plan and the row order."""
     from budgetformer_amd import hip_ops
