@@ -172,11 +172,13 @@ __device__ __forceinline__ ItemRange item_group_range(const Items& it, const Sha
   r.j = int(item - it.item_off[r.row]);
   r.single = it.nitems[r.row] == 1;
   const int64_t rb = it.ptr[r.row], re = it.ptr[r.row + 1];
-  const int64_t ib = rb + int64_t(r.j) * it.item_size;
-  const int64_t ie = min(ib + int64_t(it.item_size), re);
+  // the row's n items are balanced: ceil(len / n) entries each, the last one shorter
+  const int64_t size = (re - rb + it.nitems[r.row] - 1) / it.nitems[r.row];
+  const int64_t ib = rb + int64_t(r.j) * size;
+  const int64_t ie = min(ib + size, re);
   const int gpb = kBlock >> sh.lpr_log2;
   const int grp = threadIdx.x >> sh.lpr_log2;
-  const int64_t sub = (int64_t(it.item_size) + gpb - 1) / gpb;
+  const int64_t sub = (size + gpb - 1) / gpb;
   r.beg = min(ib + grp * sub, ie);
   r.end = min(r.beg + sub, ie);
   return r;

@@ -274,7 +274,8 @@ __global__ void split_count_kernel(const int64_t* __restrict__ ptr, int64_t n_ro
   if (r >= n_rows) return;
   const int64_t len = ptr[r + 1] - ptr[r];
   const bool heavy = len > threshold;
-  const uint32_t n = heavy ? uint32_t(ceil_div(len, item_size)) : 0u;
+  int64_t n = heavy ? ceil_div(len, int64_t(item_size)) : 0;
+  if (n > BF_MAX_ITEMS_PER_ROW) n = BF_MAX_ITEMS_PER_ROW;
   nitems[r] = int32_t(n);
   packed[r] = (uint64_t(n) << 32) | (heavy ? 1u : 0u);
 }

@@ -297,12 +297,16 @@ int bf_reverse_entries(const uint64_t* sorted, const int64_t* qptr, int64_t nnz,
 int bf_expand_rows(const int64_t* ptr, int64_t n_rows, int64_t nnz, int64_t* rows, void* stream);
 
 /* Split plan for rows longer than `threshold`: such a row is processed as
- * ceil(len/item_size) items (one workgroup each) whose partial sums are reduced
- * in item order by one workgroup per split row, so results are deterministic.
+ * n = min(ceil(len/item_size), BF_MAX_ITEMS_PER_ROW) items of ceil(len/n)
+ * entries (the last one shorter), one workgroup each, whose partial sums are
+ * reduced in item order by one workgroup per split row, so results are
+ * deterministic. The cap keeps the reduce of a very long row (the Graphormer
+ * token row and column) short.
  *   nitems int32 [n_rows] (0 for short rows), item_off int32 [n_rows],
  *   item_row int32 [item_cap], heavy_rows int32 [heavy_cap] (the split rows,
  *   ascending), counts int32 [2] on the device = (#items, #split rows).
  *   Capacities: bf_split_item_capacity / bf_split_row_capacity.              */
+#define BF_MAX_ITEMS_PER_ROW 160
 int64_t bf_split_item_capacity(int64_t nnz, int32_t threshold, int32_t item_size);
 int64_t bf_split_row_capacity(int64_t nnz, int32_t threshold);
 int bf_split_plan_workspace_size(int64_t n_rows, size_t* bytes);

@@ -69,9 +69,10 @@ def test_fp32_random_coo(hip_device, S, H, hn, E):
         assert _rel_err(got, ref) < 1e-5
 
 
-@pytest.mark.parametrize("chunk,item", [(4, 4), (4, 37), (64, 512)])
+@pytest.mark.parametrize("chunk,item", [(4, 4), (4, 37), (64, 512), (4, 2)])
 def test_fp32_global_token_split_rows(hip_device, chunk, item):
-    """Graphormer token: query 0 is dense over all kv and kv 0 feeds every query."""
+    """Graphormer token: query 0 is dense over all kv and kv 0 feeds every query. With items of 2
+    the token row and column exceed the per-row item cap and run as 160 balanced items."""
     from budgetformer_amd.hip_ops import AttentionIndex
     S, H, hn = 500, 8, 16
     q, k, v, ei, dout = _inputs(S, H, hn, 2500, seed=7, mult=1.3)

@@ -309,7 +309,7 @@ def test_index_formats_against_numpy(hip_device, token):
     L = np.diff(b[0].cpu().numpy())
     heavy = np.nonzero(L > 4)[0]
     assert plan.heavy == heavy.size and np.array_equal(plan.heavy_rows[:plan.heavy].cpu().numpy(), heavy)
-    nit = np.where(L > 4, -(-L // 5), 0)
+    nit = np.where(L > 4, np.minimum(-(-L // 5), 160), 0)              # BF_MAX_ITEMS_PER_ROW = 160
     assert plan.items == nit.sum() and np.array_equal(plan.nitems[:n_q].cpu().numpy(), nit)
     assert np.array_equal(plan.item_off[:n_q].cpu().numpy(), np.concatenate([[0], np.cumsum(nit)[:-1]]))
     assert np.array_equal(plan.item_row[:plan.items].cpu().numpy(), np.repeat(np.arange(n_q), nit))
