@@ -15,8 +15,8 @@ import torch
 
 from . import _native as N
 
-DEFAULT_CHUNK = 64      # rows longer than this go through the split plan
-DEFAULT_ITEM = 512      # entries per split item (one workgroup)
+DEFAULT_CHUNK = 128     # rows longer than this go through the split plan
+DEFAULT_ITEM = 768      # entries per split item (one workgroup), before balancing
 HUB_THRESHOLD = 1024    # in-degree above which a query's real-edge top-k uses a whole workgroup
 LIGHT_MAX = 32          # in-degree up to which a query's real-edge top-k runs in one thread (k <= 16)
 
