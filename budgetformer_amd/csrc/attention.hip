@@ -507,6 +507,12 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_q_kernel(
 // keeps the row stats and the hub K/V rows cached instead (kStreamBytes).
 constexpr size_t kStreamBytes = size_t(256) << 20;
 
+// Short kv rows per lane group: 1, or 4 past 16M kv rows, where fewer and
+// longer-lived workgroups were measured 7% faster (c5, 111M rows) while on
+// small tables the extra rows per group cost parallelism (c2: 2x slower).
+constexpr int64_t kManyKvRows = int64_t(1) << 24;
+inline int kv_rows_per_group(int64_t n_kv) { return n_kv > kManyKvRows ? 4 : 1; }
+
 template <typename T, bool NT>
 __device__ __forceinline__ typename Elem<T>::Raw gather_row(const T* base, int64_t row, int D, int col0) {
   return NT ? Elem<T>::load_raw_nt(base + row * D + col0) : Elem<T>::load_raw(base + row * D + col0);
@@ -596,7 +602,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
     const int32_t* __restrict__ ke, const float* __restrict__ bias,
     const float* __restrict__ factor, const T* __restrict__ dout, const float2* __restrict__ rstat,
     T* __restrict__ dq, T* __restrict__ dk, T* __restrict__ dv, const int32_t* __restrict__ order,
-    Items qit, int q_heavy, Items kit, int k_items, int64_t n_kv, Shape sh, int chunk) {
+    Items qit, int q_heavy, Items kit, int k_items, int64_t n_kv, Shape sh, int chunk, int rows_per_group) {
   constexpr int V = Elem<T>::kPerVec;
   extern __shared__ float lds[];
   const GroupPos g = group_pos<T>(sh);
@@ -627,23 +633,23 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
     }
     return;
   }
-  const int64_t slot = row_slot(sh, unsigned(q_heavy + k_items));
-  if (slot >= n_kv) return;
-  const int64_t row = order ? int64_t(order[slot]) : slot;
-  const int64_t beg = kptr[row], end = kptr[row + 1];
-  if (end - beg > chunk) return;
-  if (beg == end) {               // key/value row no query attends to: zero gradient, no reads
+  // each group takes rows_per_group consecutive rows of the order (similar lengths)
+  const int64_t first = row_slot(sh, unsigned(q_heavy + k_items)) * rows_per_group;
+  const int64_t last = first + rows_per_group < n_kv ? first + rows_per_group : n_kv;
+  for (int64_t slot = first; slot < last; ++slot) {
+    const int64_t row = order ? int64_t(order[slot]) : slot;
+    const int64_t beg = kptr[row], end = kptr[row + 1];
+    if (end - beg > chunk) continue;
+#pragma unroll
+    for (int i = 0; i < V; ++i) ak[i] = av[i] = 0.f;
+    if (beg < end) {              // a row no query attends to gets zero gradients without reads
+      const typename Elem<T>::Raw kr = load_row_raw(k, row, sh.D, g), vr = load_row_raw(v, row, sh.D, g);
+      dkv_segment<T, NT>(q, dout, kq, ke, bias, factor, rstat, beg, end, sh, g, kr, vr, ak, av);
+    }
     if (g.act) {
       Elem<T>::store(dk + row * sh.D + g.col0, ak);
       Elem<T>::store(dv + row * sh.D + g.col0, av);
     }
-    return;
-  }
-  const typename Elem<T>::Raw kr = load_row_raw(k, row, sh.D, g), vr = load_row_raw(v, row, sh.D, g);
-  dkv_segment<T, NT>(q, dout, kq, ke, bias, factor, rstat, beg, end, sh, g, kr, vr, ak, av);
-  if (g.act) {
-    Elem<T>::store(dk + row * sh.D + g.col0, ak);
-    Elem<T>::store(dv + row * sh.D + g.col0, av);
   }
 }
 
@@ -775,14 +781,16 @@ int bwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
               idx->n_q, sh, idx->chunk);
     BF_CHECK_LAUNCH();
   }
-  const int64_t kv_blocks = int64_t(idx->q_heavy) + idx->k_items + grid_for(idx->n_kv, sh);
+  const int rows_per_group = kv_rows_per_group(idx->n_kv);
+  const int64_t kv_blocks = int64_t(idx->q_heavy) + idx->k_items + grid_for(ceil_div(idx->n_kv, rows_per_group), sh);
   if (kv_blocks > 0) {
     const size_t lds = (idx->q_heavy > 0 || idx->k_items > 0) ? combine_lds_bytes(sh) : 0;
     const bool stream_rows = size_t(idx->n_q) * size_t(sh.D) * sizeof(T) * 2 > kStreamBytes;
 #define BF_LAUNCH_KV(NT)                                                                                           \
   BF_LAUNCH("attn_bwd_kv_kernel", (attn_bwd_kv_kernel<T, NT>), dim3(unsigned(kv_blocks)), dim3(kBlock), lds, st, Q, K, \
             Vv, idx->kptr, idx->kq, idx->ke, bias, factor, dO, rstat, static_cast<T*>(dq), static_cast<T*>(dk),       \
-            static_cast<T*>(dv), idx->k_order, qit, idx->q_heavy, kit, idx->k_items, idx->n_kv, sh, idx->chunk)
+            static_cast<T*>(dv), idx->k_order, qit, idx->q_heavy, kit, idx->k_items, idx->n_kv, sh, idx->chunk,     \
+            rows_per_group)
     if (stream_rows)
       BF_LAUNCH_KV(true);
     else

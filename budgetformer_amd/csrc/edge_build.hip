@@ -594,7 +594,7 @@ __global__ __launch_bounds__(kThreads) void real_select_fused_kernel(
     int k_real, uint32_t kc, const int32_t* __restrict__ rw_kv, const int32_t* __restrict__ rw_cnt, int k_rw,
     int dedup, int32_t* __restrict__ table, int width, int32_t* __restrict__ row_len,
     const int32_t* __restrict__ hubs, int64_t n_hubs, int64_t hub_threshold, const int32_t* __restrict__ heavy,
-    int64_t n_heavy, int64_t light_max, int vec4) {
+    int64_t n_heavy, int64_t light_max, int vec4, int64_t num_nodes) {
   const int64_t b = blockIdx.x;
   const int64_t hub_blocks = ceil_div(n_hubs, int64_t(kHubsPerBlock));
   const int64_t heavy_blocks = ceil_div(n_heavy, int64_t(kQPB));
@@ -637,7 +637,8 @@ __global__ __launch_bounds__(kThreads) void real_select_fused_kernel(
   if (k_real > 0) {
     const int64_t beg = in_ptr[q], end = in_ptr[q + 1];
     if (end - beg > light_max) return;          // a heavy query: a group writes its row
-    if (vec4)
+    // 16-byte chunks read up to 3 entries past `end`: only where they stay inside the array
+    if (vec4 && ((end - 1) | 3) < in_ptr[num_nodes])
       scan_keys_x4<kScanX4Unroll>(in_src, beg, end, base, lk);
     else
       scan_keys<kScanUnroll>(in_src + beg, int32_t(end - beg), 0, 1, base, lk);
@@ -712,7 +713,7 @@ int launch_real_merge(const int64_t* in_ptr, const int32_t* in_src, int64_t num_
 #define BF_LAUNCH_FUSED(KR, KW)                                                                                     \
   BF_LAUNCH("real_select_fused_kernel", (real_select_fused_kernel<KR, KW>), dim3(unsigned(blocks)), dim3(kThreads), \
             0, st, in_ptr, in_src, q_lo, n_q, k_real, kc, rw_kv, rw_cnt, k_rw, dedup, table, width, row_len, hubs,    \
-            n_hubs, hub_thr, split.heavy, heavy, light_max, vec4)
+            n_hubs, hub_thr, split.heavy, heavy, light_max, vec4, num_nodes)
     const int kw = rw_kv ? k_rw : 0;
     const int kr = k_real <= 4 ? 4 : k_real <= 8 ? 8 : 16;
     const int kwp = kw <= 4 ? 4 : kw <= 8 ? 8 : 16;

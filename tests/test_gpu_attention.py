@@ -268,3 +268,33 @@ def test_streaming_kv_pass_on_a_table_larger_than_the_cache(hip_device, dtype, H
     ro, rZ, rdq, rdk, rdv, _ = _oracle(q, k, v, ei, dout)
     for got, ref in ((out, ro), (dq, rdq), (dk, rdk), (dv, rdv)):
         assert _rel_err(got, ref) < tol
+
+
+def test_kv_pass_past_16m_rows_equals_the_compact_problem(hip_device):
+    """Past 16M kv rows the dk/dv pass gives each lane group several short rows. Every row is still
+    computed alone, so the gradients of a 17M-row problem with 30K attended rows must equal, bit for
+    bit, those of the same edges over the 30K rows alone, and every other row must be zero."""
+    from budgetformer_amd import hip_ops
+    from budgetformer_amd.hip_ops import AttentionIndex
+    g = torch.Generator(device=hip_device).manual_seed(3)
+    n_q, n_big, n_touch, E, H, hn = 20000, 17_000_000, 30000, 200000, 8, 16
+    touched = torch.randperm(n_big, generator=g, device=hip_device)[:n_touch].sort().values
+    src_c = torch.randint(0, n_touch, (E,), generator=g, device=hip_device)
+    dst = torch.randint(0, n_q, (E,), generator=g, device=hip_device)
+    big = AttentionIndex.from_coo(torch.stack([touched[src_c], dst]), n_q, n_big)
+    small = AttentionIndex.from_coo(torch.stack([src_c, dst]), n_q, n_touch)
+    q = torch.randn(n_q, H, hn, generator=g, device=hip_device).to(torch.bfloat16)
+    dout = torch.randn(n_q, H, hn, generator=g, device=hip_device).to(torch.bfloat16)
+    k = torch.empty(n_big, H, hn, device=hip_device, dtype=torch.bfloat16).normal_(generator=g)
+    v = torch.empty(n_big, H, hn, device=hip_device, dtype=torch.bfloat16).normal_(generator=g)
+    kc, vc = k[touched].contiguous(), v[touched].contiguous()
+    out_b, z_b = hip_ops.attn_forward(big, q, k, v)
+    out_s, z_s = hip_ops.attn_forward(small, q, kc, vc)
+    assert torch.equal(out_b, out_s) and torch.equal(z_b, z_s)
+    dq_b, dk_b, dv_b, _ = hip_ops.attn_backward(big, q, k, v, out_b, z_b, dout)
+    dq_s, dk_s, dv_s, _ = hip_ops.attn_backward(small, q, kc, vc, out_s, z_s, dout)
+    assert torch.equal(dq_b, dq_s)
+    assert torch.equal(dk_b[touched], dk_s) and torch.equal(dv_b[touched], dv_s)
+    dk_b[touched] = 0
+    dv_b[touched] = 0
+    assert not dk_b.any() and not dv_b.any()
