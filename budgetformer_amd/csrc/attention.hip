@@ -507,11 +507,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_q_kernel(
 // keeps the row stats and the hub K/V rows cached instead (kStreamBytes).
 constexpr size_t kStreamBytes = size_t(256) << 20;
 
-// Short kv rows per lane group: 1, or 4 past 16M kv rows, where fewer and
-// longer-lived workgroups were measured 7% faster (c5, 111M rows) while on
-// small tables the extra rows per group cost parallelism (c2: 2x slower).
-constexpr int64_t kManyKvRows = int64_t(1) << 24;
-inline int kv_rows_per_group(int64_t n_kv) { return n_kv > kManyKvRows ? 4 : 1; }
+
 
 template <typename T, bool NT>
 __device__ __forceinline__ typename Elem<T>::Raw gather_row(const T* base, int64_t row, int D, int col0) {
@@ -714,6 +710,15 @@ int check_index(const bf_attn_index* idx, bool backward) {
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Short kv rows per lane group in the dk/dv pass: 1, or 4 past 16M kv rows,
+// where fewer and longer-lived workgroups were measured faster (c5's 111M kv
+// rows: 44.9 -> 40.4 ms) while on small tables the extra rows per group cost
+// parallelism (c2: 2x slower). The query-side passes keep one row per group:
+// four were measured no faster for the dq pass and 4% slower for the forward
+// at c5's 27.8M queries.
+constexpr int64_t kManyRows = int64_t(1) << 24;
+inline int kv_rows_per_group(int64_t n_kv) { return n_kv > kManyRows ? 4 : 1; }
 
 inline unsigned grid_for(int64_t rows, const Shape& sh) {
   const int64_t per_block = kBlock >> sh.lpr_log2;

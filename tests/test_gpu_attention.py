@@ -298,3 +298,31 @@ def test_kv_pass_past_16m_rows_equals_the_compact_problem(hip_device):
     dk_b[touched] = 0
     dv_b[touched] = 0
     assert not dk_b.any() and not dv_b.any()
+
+
+def test_query_passes_past_16m_rows_equal_the_compact_problem(hip_device):
+    """A 17M-query problem with 30K attending queries equals its compaction bit for bit (forward and
+    both backward passes), and the other queries get zero outputs and gradients."""
+    from budgetformer_amd import hip_ops
+    from budgetformer_amd.hip_ops import AttentionIndex
+    g = torch.Generator(device=hip_device).manual_seed(4)
+    n_big, n_touch, n_kv, E, H, hn = 17_000_000, 30000, 20000, 200000, 8, 16
+    touched = torch.randperm(n_big, generator=g, device=hip_device)[:n_touch].sort().values
+    dst_c = torch.randint(0, n_touch, (E,), generator=g, device=hip_device)
+    src = torch.randint(0, n_kv, (E,), generator=g, device=hip_device)
+    big = AttentionIndex.from_coo(torch.stack([src, touched[dst_c]]), n_big, n_kv)
+    small = AttentionIndex.from_coo(torch.stack([src, dst_c]), n_touch, n_kv)
+    q = torch.empty(n_big, H, hn, device=hip_device, dtype=torch.bfloat16).normal_(generator=g)
+    dout = torch.empty(n_big, H, hn, device=hip_device, dtype=torch.bfloat16).normal_(generator=g)
+    k = torch.randn(n_kv, H, hn, generator=g, device=hip_device).to(torch.bfloat16)
+    v = torch.randn(n_kv, H, hn, generator=g, device=hip_device).to(torch.bfloat16)
+    qc, doc = q[touched].contiguous(), dout[touched].contiguous()
+    out_b, z_b = hip_ops.attn_forward(big, q, k, v)
+    out_s, z_s = hip_ops.attn_forward(small, qc, k, v)
+    assert torch.equal(out_b[touched], out_s) and torch.equal(z_b[touched], z_s)
+    dq_b, dk_b, dv_b, _ = hip_ops.attn_backward(big, q, k, v, out_b, z_b, dout)
+    dq_s, dk_s, dv_s, _ = hip_ops.attn_backward(small, qc, k, v, out_s, z_s, doc)
+    assert torch.equal(dq_b[touched], dq_s) and torch.equal(dk_b, dk_s) and torch.equal(dv_b, dv_s)
+    for t in (out_b, z_b, dq_b):
+        t[touched] = 0
+        assert not t.any()
