@@ -60,7 +60,8 @@ __device__ __forceinline__ void put_entry(int32_t* __restrict__ kv, uint64_t* __
 // with kv 0 followed by its table row shifted by one.
 __global__ void table_fill_kernel(const int32_t* __restrict__ table, const int32_t* __restrict__ row_len,
                                   int64_t n_rows, int width, int token, const int64_t* __restrict__ qptr,
-                                  int32_t* __restrict__ kv, uint64_t* __restrict__ rkey, int kshift, int sbits) {
+                                  int32_t* __restrict__ kv, uint64_t* __restrict__ rkey, int kshift, int sbits,
+                                  int slots32) {
   const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
   const int64_t slots = n_rows * width;
   if (i >= slots) {
@@ -71,7 +72,9 @@ __global__ void table_fill_kernel(const int32_t* __restrict__ table, const int32
     if (row_len[t] == 0) put_entry(kv, rkey, qptr[t + 1], t + 1, 0, 0, kshift, sbits);
     return;
   }
-  const int64_t r = i / width;
+  // 32-bit division when the slot count allows (the host checks it): a 64-bit
+  // divide by a runtime width costs several times more instructions
+  const int64_t r = slots32 ? int64_t(uint32_t(i) / uint32_t(width)) : i / width;
   const int c = int(i - r * width);
   const int len = row_len[r];
   if (c >= len) return;
@@ -376,7 +379,8 @@ extern "C" int bf_table_to_csr(const int32_t* table, const int32_t* row_len, int
   const int64_t threads = n_rows * width + (global_token ? n_rows : 0);
   if (threads > 0) {
     BF_LAUNCH("table_fill_kernel", table_fill_kernel, dim3(blocks_for(threads)), dim3(kThreads), 0, as_stream(stream),
-              table, row_len, n_rows, width, int(global_token != 0), qptr, kv, rkey, q_bits + slot_bits, slot_bits);
+              table, row_len, n_rows, width, int(global_token != 0), qptr, kv, rkey, q_bits + slot_bits, slot_bits,
+              int(n_rows * width < (int64_t(1) << 32)));
     BF_CHECK_LAUNCH();
   }
   return BF_OK;
