@@ -636,15 +636,20 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
     const int64_t row = order ? int64_t(order[slot]) : slot;
     const int64_t beg = kptr[row], end = kptr[row + 1];
     if (end - beg > chunk) continue;
+    if (beg == end) {             // a row no query attends to: zero gradients, no reads, written past the caches
+      if (g.act) {
+        store_zero16_nt(dk + row * sh.D + g.col0);
+        store_zero16_nt(dv + row * sh.D + g.col0);
+      }
+      continue;
+    }
 #pragma unroll
     for (int i = 0; i < V; ++i) ak[i] = av[i] = 0.f;
-    if (beg < end) {              // a row no query attends to gets zero gradients without reads
-      const typename Elem<T>::Raw kr = load_row_raw(k, row, sh.D, g), vr = load_row_raw(v, row, sh.D, g);
-      dkv_segment<T, NT>(q, dout, kq, ke, bias, factor, rstat, beg, end, sh, g, kr, vr, ak, av);
-    }
-    if (g.act) {
-      Elem<T>::store(dk + row * sh.D + g.col0, ak);
-      Elem<T>::store(dv + row * sh.D + g.col0, av);
+    const typename Elem<T>::Raw kr = load_row_raw(k, row, sh.D, g), vr = load_row_raw(v, row, sh.D, g);
+    dkv_segment<T, NT>(q, dout, kq, ke, bias, factor, rstat, beg, end, sh, g, kr, vr, ak, av);
+    if (g.act) {                  // written once, not read again in the pass: past the caches
+      Elem<T>::store_nt(dk + row * sh.D + g.col0, ak);
+      Elem<T>::store_nt(dv + row * sh.D + g.col0, av);
     }
   }
 }

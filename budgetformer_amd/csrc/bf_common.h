@@ -103,6 +103,12 @@ template <> struct Elem<float> {
   __device__ __forceinline__ static void store(float* p, const float (&o)[4]) {
     *reinterpret_cast<float4*>(p) = make_float4(o[0], o[1], o[2], o[3]);
   }
+  // non-temporal: for rows written once and not read again in the same pass
+  __device__ __forceinline__ static void store_nt(float* p, const float (&o)[4]) {
+    typedef float V4 __attribute__((ext_vector_type(4)));
+    const V4 v = {o[0], o[1], o[2], o[3]};
+    __builtin_nontemporal_store(v, reinterpret_cast<V4*>(p));
+  }
 };
 
 template <> struct Elem<uint16_t> {
@@ -150,7 +156,24 @@ template <> struct Elem<uint16_t> {
       w[i] = uint32_t(f32_to_bf16(o[2 * i])) | (uint32_t(f32_to_bf16(o[2 * i + 1])) << 16);
     *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
   }
+  __device__ __forceinline__ static void store_nt(uint16_t* p, const float (&o)[8]) {
+    typedef unsigned V4 __attribute__((ext_vector_type(4)));
+    V4 w;
+    w.x = uint32_t(f32_to_bf16(o[0])) | (uint32_t(f32_to_bf16(o[1])) << 16);
+    w.y = uint32_t(f32_to_bf16(o[2])) | (uint32_t(f32_to_bf16(o[3])) << 16);
+    w.z = uint32_t(f32_to_bf16(o[4])) | (uint32_t(f32_to_bf16(o[5])) << 16);
+    w.w = uint32_t(f32_to_bf16(o[6])) | (uint32_t(f32_to_bf16(o[7])) << 16);
+    __builtin_nontemporal_store(w, reinterpret_cast<V4*>(p));
+  }
 };
+
+// 16 zero bytes at p (16-byte aligned) by a non-temporal vector store: rows
+// written once and not read again in the pass do not displace cached data.
+__device__ __forceinline__ void store_zero16_nt(void* p) {
+  typedef unsigned V4 __attribute__((ext_vector_type(4)));
+  const V4 z = {0u, 0u, 0u, 0u};
+  __builtin_nontemporal_store(z, reinterpret_cast<V4*>(p));
+}
 
 // Butterfly sum over aligned groups of `width` lanes (width a power of two <= 64).
 __device__ __forceinline__ float group_sum(float x, int width) {
