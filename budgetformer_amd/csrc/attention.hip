@@ -85,6 +85,14 @@ __device__ __forceinline__ typename Elem<T>::Raw load_row_raw(const T* base, int
   return g.act ? Elem<T>::load_raw(base + row * D + g.col0) : Elem<T>::zero_raw();
 }
 
+// A pass's own rows (read or written once, in row order) go past the caches:
+// the caches then keep the rows the pass gathers at random (c2 query-side
+// passes: 5% faster; c5: 4-5%).
+template <typename T>
+__device__ __forceinline__ typename Elem<T>::Raw load_row_raw_nt(const T* base, int64_t row, int D, const GroupPos& g) {
+  return g.act ? Elem<T>::load_raw_nt(base + row * D + g.col0) : Elem<T>::zero_raw();
+}
+
 // ------------------------------------------------------------------ forward
 // Accumulates sum_e p*f*v (acc) and sum_e p (z) over entries [beg, end) of one row.
 template <typename T>
@@ -306,7 +314,7 @@ __device__ __forceinline__ void store_out(T* __restrict__ out, float* __restrict
   float o[V];
 #pragma unroll
   for (int i = 0; i < V; ++i) o[i] = acc[i] / den;
-  Elem<T>::store(out + row * sh.D + g.col0, o);
+  Elem<T>::store_nt(out + row * sh.D + g.col0, o);
   if (g.lead) Z[row * sh.H + g.head] = z;
 }
 
@@ -343,7 +351,7 @@ __global__ __launch_bounds__(kBlock) void attn_fwd_kernel(
   if (row >= n_q) return;
   const int64_t beg = qptr[row], end = qptr[row + 1];
   if (end - beg > chunk) return;  // split row: its items and the reduce write it
-  const typename Elem<T>::Raw qr = load_row_raw(q, row, sh.D, g);
+  const typename Elem<T>::Raw qr = load_row_raw_nt(q, row, sh.D, g);
   fwd_segment<T>(k, v, kv, bias, factor, beg, end, sh, g, qr, acc, z);
   store_out(out, Z, row, sh, g, acc, z);
 }
@@ -371,8 +379,8 @@ template <typename T>
 __device__ __forceinline__ RowGrad row_grad(const T* __restrict__ out, const T* __restrict__ dout,
                                             const float* __restrict__ Z, int64_t row, const Shape& sh,
                                             const GroupPos& g, typename Elem<T>::Raw& gr) {
-  gr = load_row_raw(dout, row, sh.D, g);
-  const typename Elem<T>::Raw orow = load_row_raw(out, row, sh.D, g);
+  gr = load_row_raw_nt(dout, row, sh.D, g);
+  const typename Elem<T>::Raw orow = load_row_raw_nt(out, row, sh.D, g);
   RowGrad r;
   r.delta = group_sum(Elem<T>::dot(gr, orow, 0.f), 1 << sh.lph_log2);
   r.dprime = (g.act ? Z[row * sh.H + g.head] : 0.f) + kEps;
@@ -492,11 +500,11 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_q_kernel(
   if (row >= n_q) return;
   const int64_t beg = qptr[row], end = qptr[row + 1];
   if (end - beg > chunk) return;
-  const typename Elem<T>::Raw qr = load_row_raw(q, row, sh.D, g);
+  const typename Elem<T>::Raw qr = load_row_raw_nt(q, row, sh.D, g);
   const RowGrad rg = row_grad<T>(out, dout, Z, row, sh, g, gr);
   dq_segment<T>(k, v, kv, bias, factor, dbias, beg, end, sh, g, rg, qr, gr, acc);
   if (g.act) {
-    Elem<T>::store(dq + row * sh.D + g.col0, acc);
+    Elem<T>::store_nt(dq + row * sh.D + g.col0, acc);
     if (g.lead) store_row_stat(rstat, row, sh, g, rg);
   }
 }
