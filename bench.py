@@ -1,7 +1,7 @@
 #!/usr/bin/env python
 """Benchmark of BudgetFormer's per-layer hot path on one MI355X.
 
-A step is one pass of the hot path over config c2:
+A step is one pass of the hot path over config c2 (the headline configuration):
   1. budgeted edge construction (Philox walks, real/RW top-k, merge) into the
      [N, 8] table, the Graphormer global-token CSR, the reverse index and the
      split plans;

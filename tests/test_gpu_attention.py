@@ -1,6 +1,6 @@
 """GPU parity of the HIP sparse attention (forward and backward) against the CPU oracle.
 
-Tolerances: fp32 within 1e-5 relative, bf16 within 2e-2
+Tolerances (the parity bar of this path): fp32 within 1e-5 relative, bf16 within 2e-2
 relative, measured as max|got - ref| / max|ref| per tensor against a float64
 evaluation of the oracle on the same (rounded) inputs.
 """
