@@ -59,3 +59,29 @@ def test_workspace_queries_run_on_cpu():
     assert out.value >= 3 * 1000 * 4
     N.call("bf_build_edge_table_workspace_size", 1000, 4, 0, 4, C.byref(out))
     assert out.value >= 1000 * 4 * 4
+
+
+def test_key_inverse_constant_recovers_sources():
+    """The fused real-edge select keeps 31-bit keys only and recovers each winner's source as
+    ((key - base_q) * kKeyMulInv) mod 2^31. Pin the constant in the kernel source against the oracle's
+    key: it must be the inverse of the source multiplier and return every source exactly."""
+    import pathlib
+    import re
+
+    import numpy as np
+
+    from oracle import edge_table as et
+
+    src_text = (pathlib.Path(__file__).resolve().parents[1] / "budgetformer_amd" / "csrc" / "edge_build.hip").read_text()
+    mul = int(re.search(r"kKeyMul = (0x[0-9a-fA-F]+|\d+)u;", src_text).group(1), 0)
+    inv = int(re.search(r"kKeyMulInv = (0x[0-9a-fA-F]+|\d+)u;", src_text).group(1), 0)
+    assert (mul * inv) % 2**32 == 1
+    rng = np.random.default_rng(0)
+    s = rng.integers(0, 2**31 - 1, 20000, dtype=np.int64)
+    q = rng.integers(0, 2**31 - 1, 20000, dtype=np.int64)
+    for seed in (0, 17, 42 + 17, 987654 + 37):
+        key = et.edge_key(s, q, seed).astype(np.int64)
+        # base_q = q*214013 + seed*2654435761 + 12345 (mod 2^32): the key with src = 0
+        base = et.edge_key(np.zeros_like(q), q, seed).astype(np.int64)
+        back = (((key - base) % 2**32) * inv) % 2**32 & 0x7FFFFFFF
+        assert np.array_equal(back, s)
