@@ -527,6 +527,7 @@ class AttentionIndex:
     _rkeys: Optional[ReverseKeys] = field(default=None, repr=False)   # from_table: sort keys, until used
     _sorted: Optional[ReverseKeys] = field(default=None, repr=False)  # sorted keys, until ke is needed
     _counts: Optional[torch.Tensor] = field(default=None, repr=False)  # both plans' device counts
+    _structs: dict = field(default_factory=dict, repr=False)          # C view per (backward, with ke)
 
     @property
     def nnz(self) -> int:
@@ -591,6 +592,16 @@ class AttentionIndex:
         self.ensure_backward() if backward else self.ensure_forward()
         if backward and entries:
             self.ensure_entries()
+        # the index does not change once built: every layer and step reuses the same struct
+        key = (backward, backward and self.ke is not None)
+        cached = self._structs.get(key)
+        if cached is not None:
+            return cached
+        s = self._make_struct(backward)
+        self._structs[key] = s
+        return s
+
+    def _make_struct(self, backward: bool) -> N.AttnIndex:
         s = N.AttnIndex()
         s.n_q, s.n_kv, s.nnz = self.n_q, self.n_kv, self.nnz
         s.qptr, s.kv = self.qptr.data_ptr(), self.kv.data_ptr() if self.nnz else None
