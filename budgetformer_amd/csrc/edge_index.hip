@@ -58,32 +58,54 @@ __device__ __forceinline__ void put_entry(int32_t* __restrict__ kv, uint64_t* __
 // One thread per table slot, then (with the Graphormer token) one thread per
 // query for the token row: query 0 lists kv 1..n_rows, and query r+1 starts
 // with kv 0 followed by its table row shifted by one.
-__global__ void table_fill_kernel(const int32_t* __restrict__ table, const int32_t* __restrict__ row_len,
-                                  int64_t n_rows, int width, int token, const int64_t* __restrict__ qptr,
-                                  int32_t* __restrict__ kv, uint64_t* __restrict__ rkey, int kshift, int sbits,
-                                  int slots32) {
-  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+constexpr int kFillPerThread = 4;   // table slots per thread: their loads are issued before any store
+
+__global__ __launch_bounds__(kThreads) void table_fill_kernel(
+    const int32_t* __restrict__ table, const int32_t* __restrict__ row_len, int64_t n_rows, int width, int token,
+    const int64_t* __restrict__ qptr, int32_t* __restrict__ kv, uint64_t* __restrict__ rkey, int kshift, int sbits,
+    int slots32) {
   const int64_t slots = n_rows * width;
-  if (i >= slots) {
-    const int64_t t = i - slots;
-    if (!token || t >= n_rows) return;
-    // the token row's entry for kv t+1 sits at position t: its key carries slot 0
-    put_entry(kv, rkey, t, 0, 0, int32_t(t + 1), kshift, sbits);
-    if (row_len[t] == 0) put_entry(kv, rkey, qptr[t + 1], t + 1, 0, 0, kshift, sbits);
-    return;
+  const int64_t total = slots + (token ? n_rows : 0);
+  const int64_t base = int64_t(blockIdx.x) * (kThreads * kFillPerThread) + threadIdx.x;
+  int32_t val[kFillPerThread], len[kFillPerThread], col[kFillPerThread];
+  int64_t row[kFillPerThread], start[kFillPerThread];
+#pragma unroll
+  for (int u = 0; u < kFillPerThread; ++u) {
+    const int64_t i = base + int64_t(u) * kThreads;
+    len[u] = -1;                                  // no table slot: nothing to write
+    row[u] = start[u] = 0;
+    col[u] = val[u] = 0;
+    if (i < slots) {
+      // 32-bit division when the slot count allows (the host checks it): a
+      // 64-bit divide by a runtime width costs several times more instructions
+      const int64_t r = slots32 ? int64_t(uint32_t(i) / uint32_t(width)) : i / width;
+      row[u] = r;
+      col[u] = int32_t(i - r * width);
+      len[u] = row_len[r];
+      start[u] = qptr[r + token];                 // with the token, table row r is query r+1
+      val[u] = table[i];
+    }
   }
-  // 32-bit division when the slot count allows (the host checks it): a 64-bit
-  // divide by a runtime width costs several times more instructions
-  const int64_t r = slots32 ? int64_t(uint32_t(i) / uint32_t(width)) : i / width;
-  const int c = int(i - r * width);
-  const int len = row_len[r];
-  if (c >= len) return;
-  if (token) {
-    const int64_t base = qptr[r + 1];  // query r+1
-    if (c == 0) put_entry(kv, rkey, base, r + 1, 0, 0, kshift, sbits);
-    put_entry(kv, rkey, base + 1 + c, r + 1, c + 1, table[i] + 1, kshift, sbits);
-  } else {
-    put_entry(kv, rkey, qptr[r] + c, r, c, table[i], kshift, sbits);
+#pragma unroll
+  for (int u = 0; u < kFillPerThread; ++u) {
+    const int64_t i = base + int64_t(u) * kThreads;
+    if (i >= slots) {
+      if (i >= total) continue;
+      // the token row's entry for kv t+1 sits at position t: its key carries slot 0
+      const int64_t t = i - slots;
+      put_entry(kv, rkey, t, 0, 0, int32_t(t + 1), kshift, sbits);
+      if (row_len[t] == 0) put_entry(kv, rkey, qptr[t + 1], t + 1, 0, 0, kshift, sbits);
+      continue;
+    }
+    const int c = col[u];
+    if (c >= len[u]) continue;
+    const int64_t r = row[u];
+    if (token) {
+      if (c == 0) put_entry(kv, rkey, start[u], r + 1, 0, 0, kshift, sbits);
+      put_entry(kv, rkey, start[u] + 1 + c, r + 1, c + 1, val[u] + 1, kshift, sbits);
+    } else {
+      put_entry(kv, rkey, start[u] + c, r, c, val[u], kshift, sbits);
+    }
   }
 }
 
@@ -164,20 +186,33 @@ __device__ __forceinline__ int32_t entry_of(uint64_t x, int kshift, int sbits, i
   return int32_t(token && q == 0 ? int64_t(x >> kshift) - 1 : qptr[q] + slot);
 }
 
-__global__ void unpack_rkey_kernel(const uint64_t* __restrict__ keys, int64_t nnz, int kshift, int sbits, int token,
-                                   const int64_t* __restrict__ qptr, int64_t n_kv, int64_t* __restrict__ kptr,
-                                   int32_t* __restrict__ kq, int32_t* __restrict__ ke) {
-  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
-  if (i > nnz) return;
-  const uint64_t x = i < nnz ? keys[i] : 0;
-  int64_t r_here = i < nnz ? int64_t(x >> kshift) : n_kv;
-  int64_t r_prev = i > 0 ? int64_t(keys[i - 1] >> kshift) : -1;
-  if (r_here > n_kv) r_here = n_kv;
-  if (r_prev > n_kv) r_prev = n_kv;
-  for (int64_t r = r_prev + 1; r <= r_here; ++r) kptr[r] = i;
-  if (i == nnz) return;
-  kq[i] = int32_t((x >> sbits) & ((uint64_t(1) << (kshift - sbits)) - 1));
-  if (ke) ke[i] = entry_of(x, kshift, sbits, token, qptr);
+constexpr int kUnpackPerThread = 4;  // sorted keys per thread (kThreads apart), loaded before any store
+
+__global__ __launch_bounds__(kThreads) void unpack_rkey_kernel(
+    const uint64_t* __restrict__ keys, int64_t nnz, int kshift, int sbits, int token,
+    const int64_t* __restrict__ qptr, int64_t n_kv, int64_t* __restrict__ kptr, int32_t* __restrict__ kq,
+    int32_t* __restrict__ ke) {
+  const int64_t base = int64_t(blockIdx.x) * (kThreads * kUnpackPerThread) + threadIdx.x;
+  uint64_t cur[kUnpackPerThread], prev[kUnpackPerThread];
+#pragma unroll
+  for (int u = 0; u < kUnpackPerThread; ++u) {
+    const int64_t i = base + int64_t(u) * kThreads;
+    cur[u] = i < nnz ? keys[i] : 0;
+    prev[u] = (i > 0 && i <= nnz) ? keys[i - 1] : 0;
+  }
+#pragma unroll
+  for (int u = 0; u < kUnpackPerThread; ++u) {
+    const int64_t i = base + int64_t(u) * kThreads;
+    if (i > nnz) break;
+    int64_t r_here = i < nnz ? int64_t(cur[u] >> kshift) : n_kv;
+    int64_t r_prev = i > 0 ? int64_t(prev[u] >> kshift) : -1;
+    if (r_here > n_kv) r_here = n_kv;
+    if (r_prev > n_kv) r_prev = n_kv;
+    for (int64_t r = r_prev + 1; r <= r_here; ++r) kptr[r] = i;
+    if (i == nnz) break;
+    kq[i] = int32_t((cur[u] >> sbits) & ((uint64_t(1) << (kshift - sbits)) - 1));
+    if (ke) ke[i] = entry_of(cur[u], kshift, sbits, token, qptr);
+  }
 }
 
 __global__ void reverse_entries_kernel(const uint64_t* __restrict__ keys, int64_t nnz, int kshift, int sbits,
@@ -378,7 +413,8 @@ extern "C" int bf_table_to_csr(const int32_t* table, const int32_t* row_len, int
   }
   const int64_t threads = n_rows * width + (global_token ? n_rows : 0);
   if (threads > 0) {
-    BF_LAUNCH("table_fill_kernel", table_fill_kernel, dim3(blocks_for(threads)), dim3(kThreads), 0, as_stream(stream),
+    BF_LAUNCH("table_fill_kernel", table_fill_kernel, dim3(unsigned(ceil_div(threads, int64_t(kThreads) * kFillPerThread))),
+              dim3(kThreads), 0, as_stream(stream),
               table, row_len, n_rows, width, int(global_token != 0), qptr, kv, rkey, q_bits + slot_bits, slot_bits,
               int(n_rows * width < (int64_t(1) << 32)));
     BF_CHECK_LAUNCH();
@@ -514,7 +550,8 @@ extern "C" int bf_reverse_index_packed(const uint64_t* rkey, const int64_t* qptr
   size_t tb = workspace_bytes;
   // only the id bits are sorted; the stable passes keep each id's entries in CSR order
   BF_CHECK_HIP(hipcub::DeviceRadixSort::SortKeys(workspace, tb, rkey, sorted, int(nnz), kshift, kshift + id_bits, st));
-  BF_LAUNCH("unpack_rkey_kernel", unpack_rkey_kernel, dim3(blocks_for(nnz + 1)), dim3(kThreads), 0, st, sorted, nnz,
+  BF_LAUNCH("unpack_rkey_kernel", unpack_rkey_kernel,
+            dim3(unsigned(ceil_div(nnz + 1, int64_t(kThreads) * kUnpackPerThread))), dim3(kThreads), 0, st, sorted, nnz,
             kshift, slot_bits, int(global_token != 0), qptr, n_kv, kptr, kq, ke);
   BF_CHECK_LAUNCH();
   return BF_OK;
