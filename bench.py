@@ -411,9 +411,10 @@ def cpu_baseline(cfg, g, tab, idx, q, k, v, dout, s_bytes, D, H):
     t0 = time.perf_counter()
     et.build_edge_table(rowptr, col, n, cfg["b_r"], cfg["b_w"], cfg["L"], cfg["P"], 42, u, q_lo=0, n_q=sample)
     build_s = (time.perf_counter() - t0) * scale
-    what = "full" if sample == n_rows else f"first {sample:,} of {n_rows:,} queries, time scaled x{scale:.2f} to"
+    what = "the full workload" if sample == n_rows else \
+        f"first {sample:,} of {n_rows:,} queries, time scaled x{scale:.2f} to the workload"
     print(f"[bench] cpu baseline: attn fwd+bwd {attn_s * 1e3:.1f} ms, edge build {build_s * 1e3:.1f} ms "
-          f"({threads} threads; {what} the workload)", flush=True)
+          f"({threads} threads; {what})", flush=True)
     return {
         "value": round((a_fwd + a_bwd) / attn_s / 1e9, 2),
         "unit": "GB/s",
