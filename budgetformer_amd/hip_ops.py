@@ -470,9 +470,12 @@ def resolve_plans(*plans) -> None:
     if len(pending) == 1:
         vals = base.cpu().tolist()
     elif shared:
-        whole = torch.empty(0, dtype=torch.int32, device=base.device).set_(base.untyped_storage())
-        allv = whole.cpu().tolist()
-        vals = sum((allv[p.counts.storage_offset():p.counts.storage_offset() + 2] for p in pending), [])
+        # copy only the span of the storage that holds the pending counts
+        offs = [p.counts.storage_offset() for p in pending]
+        lo, hi = min(offs), max(offs) + 2
+        span = torch.empty(0, dtype=torch.int32, device=base.device).set_(base.untyped_storage(), lo, (hi - lo,))
+        allv = span.cpu().tolist()
+        vals = sum((allv[o - lo:o - lo + 2] for o in offs), [])
     else:
         vals = torch.cat([p.counts for p in pending]).cpu().tolist()
     for i, p in enumerate(pending):
