@@ -59,20 +59,38 @@ def attention_bytes(s, D, H, n_q, n_kv, nnz):
     return a_fwd, a_bwd
 
 
-def kernel_bytes(s, D, H, lens_q, lens_k):
-    """Algorithmic bytes of the three pass kernels (each covers every entry: short rows and split items)."""
+def token_records(s, D, n_q, q_items):
+    """Records of key 0's dK/dV terms the dq pass writes with a token column: one per workgroup of 256
+    lanes, a row taking the next power of two >= D*s/16 lanes."""
+    lpr = 1
+    while lpr < D * s // 16:
+        lpr *= 2
+    return q_items + -(-n_q // (256 // lpr))
+
+
+def kernel_bytes(s, D, H, lens_q, lens_k, n_token_rec=0):
+    """Algorithmic bytes of the three pass kernels (each covers every entry: short rows and split items).
+
+    With a token column (n_token_rec records) the dq pass also writes key 0's dK/dV terms, 2*D floats per
+    record, and the dk/dv pass reads those records instead of gathering key 0's entries and its K, V rows."""
     n_q, nnz = lens_q.size, int(lens_q.sum())
     n_kv = lens_k.size
     nk_touched = int((lens_k > 0).sum())
+    gathered = nnz
+    rec_bytes = n_token_rec * 2 * D * 4
+    if n_token_rec:
+        gathered -= int(lens_k[0])
+        nk_touched -= int(lens_k[0] > 0)
     row = s * D
     return {
         # Q read, O write, K and V gathered per edge, kv ids, Z write, qptr
         "attn_fwd_kernel": row * (2 * n_q + 2 * nnz) + 4 * nnz + 4 * H * n_q + 8 * n_q,
-        # Q, dO, O read, dQ write, K and V per edge, kv ids, Z read + row stats write, qptr
-        "attn_bwd_q_kernel": row * (4 * n_q + 2 * nnz) + 4 * nnz + 12 * H * n_q + 8 * n_q,
-        # dK, dV written for every row; K, V read for rows with entries; Q and dO per entry,
-        # the {1/D', Delta/D'} row stats per entry, kq ids, kptr, row order
-        "attn_bwd_kv_kernel": row * (2 * n_kv + 2 * nk_touched + 2 * nnz) + 8 * H * nnz + 4 * nnz + 12 * n_kv,
+        # Q, dO, O read, dQ write, K and V per edge, kv ids, Z read + row stats write, qptr (+ token records)
+        "attn_bwd_q_kernel": row * (4 * n_q + 2 * nnz) + 4 * nnz + 12 * H * n_q + 8 * n_q + rec_bytes,
+        # dK, dV written for every row; K, V read for rows with entries; Q and dO per gathered entry,
+        # the {1/D', Delta/D'} row stats per gathered entry, kq ids, kptr, row order (+ token records)
+        "attn_bwd_kv_kernel": row * (2 * n_kv + 2 * nk_touched + 2 * gathered) + 8 * H * gathered
+        + 4 * gathered + 12 * n_kv + rec_bytes,
     }
 
 
@@ -275,7 +293,8 @@ def main(argv=None):
     # per-kernel roofline of the three pass kernels
     lens_q = np.diff(idx.qptr.cpu().numpy())
     lens_k = np.diff(idx.kptr.cpu().numpy())
-    kb = kernel_bytes(s_bytes, D, H, lens_q, lens_k)
+    n_rec = token_records(s_bytes, D, idx.n_q, idx.qplan.items) if idx.token_column else 0
+    kb = kernel_bytes(s_bytes, D, H, lens_q, lens_k, n_rec)
     kernels = {}
     for name, (ms, launches) in sorted(kstats.items(), key=lambda x: -x[1][0]):
         avg = ms / max(launches, 1)

@@ -34,7 +34,7 @@ class AttnIndex(C.Structure):
         ("q_nitems", vp), ("q_item_off", vp), ("q_item_row", vp), ("q_heavy_rows", vp),
         ("k_items", i32), ("k_heavy", i32),
         ("k_nitems", vp), ("k_item_off", vp), ("k_item_row", vp), ("k_heavy_rows", vp),
-        ("k_order", vp),
+        ("k_order", vp), ("token_column", i32),
     ]
 
 

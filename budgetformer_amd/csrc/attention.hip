@@ -462,6 +462,64 @@ __device__ __forceinline__ void dq_segment(const T* __restrict__ k, const T* __r
   }
 }
 
+// The token-column entry (this row, key 0) at CSR position e, handled on its
+// own when the index has a token column: its dq term and dbias as dq_segment
+// computes them, plus the row's terms of key 0's gradients, fk = g_a*q/sqrt(hn)
+// and fv = p*f*dO/D' — the same products the dk/dv pass would form after
+// gathering this row's q, dO and row stats again.
+template <typename T>
+__device__ __forceinline__ void token_entry(const T* __restrict__ k, const T* __restrict__ v,
+                                            const float* __restrict__ bias, const float* __restrict__ factor,
+                                            float* __restrict__ dbias, int64_t e, const Shape& sh, const GroupPos& g,
+                                            const RowGrad& rg, const typename Elem<T>::Raw& qr,
+                                            const typename Elem<T>::Raw& gr, float (&dq)[Elem<T>::kPerVec],
+                                            float (&fk)[Elem<T>::kPerVec], float (&fv)[Elem<T>::kPerVec]) {
+  constexpr int V = Elem<T>::kPerVec;
+  const typename Elem<T>::Raw kr = load_row_raw(k, 0, sh.D, g), vr = load_row_raw(v, 0, sh.D, g);
+  float d = Elem<T>::dot(kr, qr, 0.f), w = Elem<T>::dot(vr, gr, 0.f);
+  for (int o = 1; o < (1 << sh.lph_log2); o <<= 1) {
+    d += __shfl_xor(d, o, 64);
+    w += __shfl_xor(w, o, 64);
+  }
+  const float inv_dprime = 1.0f / rg.dprime;
+  const float apre = d * sh.inv_scale;
+  float a = fminf(fmaxf(apre, -kClamp), kClamp);
+  if (bias) a += bias[e * sh.H + g.head];
+  const float p = __expf(a);
+  const float f = factor ? factor[e * sh.H + g.head] : 1.f;
+  const float gb = fmaf(f * w, inv_dprime, -rg.delta * inv_dprime) * p;
+  if (dbias && g.lead) dbias[e * sh.H + g.head] = gb;
+  const float gs = (apre >= -kClamp && apre <= kClamp) ? gb * sh.inv_scale : 0.f;
+  const float pf = p * f * inv_dprime;
+  float kk[V], qq[V], gg[V];
+  Elem<T>::unpack(kr, kk);
+  Elem<T>::unpack(qr, qq);
+  Elem<T>::unpack(gr, gg);
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    dq[i] = fmaf(gs, kk[i], dq[i]);
+    fk[i] = gs * qq[i];
+    fv[i] = pf * gg[i];
+  }
+}
+
+// Sums the token-column records [a0, a1) (2*D floats each: key 0's dK terms,
+// then its dV terms) into dk, dv.
+template <int V>
+__device__ __forceinline__ void sum_token_records(const float* __restrict__ rec0, int64_t a0, int64_t a1,
+                                                  const Shape& sh, const GroupPos& g, float (&dk)[V],
+                                                  float (&dv)[V]) {
+  if (!g.act) return;
+  for (int64_t m = a0; m < a1; ++m) {
+    const float* rec = rec0 + m * (2 * sh.D);
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      dk[i] += rec[g.col0 + i];
+      dv[i] += rec[sh.D + g.col0 + i];
+    }
+  }
+}
+
 // Blocks [0, n_items) take the query-side items, the rest one short query row per group.
 template <typename T>
 __global__ __launch_bounds__(kBlock) void attn_bwd_q_kernel(
@@ -470,42 +528,121 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_q_kernel(
     const float* __restrict__ bias, const float* __restrict__ factor,
     const T* __restrict__ out, const float* __restrict__ Z, const T* __restrict__ dout,
     T* __restrict__ dq, float* __restrict__ dbias, float2* __restrict__ rstat, Items it, int n_items,
-    int64_t n_q, Shape sh, int chunk) {
+    int64_t n_q, Shape sh, int chunk, float* __restrict__ token_rec) {
   constexpr int V = Elem<T>::kPerVec;
+  extern __shared__ float lds[];
   const GroupPos g = group_pos<T>(sh);
+  const int grp = threadIdx.x >> sh.lpr_log2;
   float acc[V];
 #pragma unroll
   for (int i = 0; i < V; ++i) acc[i] = 0.f;
   typename Elem<T>::Raw gr;
+  // With a token column every workgroup writes one record of its rows' key-0 terms (fk, fv: the
+  // row's g_a*q/sqrt(hn) and p*f*dO/D'), kept out of the registers of the main loop.
   if (int(blockIdx.x) < n_items) {
-    extern __shared__ float lds[];
     const ItemRange r = item_group_range(it, sh, blockIdx.x);
     float unused[V];
 #pragma unroll
     for (int i = 0; i < V; ++i) unused[i] = 0.f;
     const typename Elem<T>::Raw qr = load_row_raw(q, r.row, sh.D, g);
     const RowGrad rg = row_grad<T>(out, dout, Z, r.row, sh, g, gr);
-    dq_segment<T>(k, v, kv, bias, factor, dbias, r.beg, r.end, sh, g, rg, qr, gr, acc);
+    int64_t beg = r.beg;
+    if (token_rec && grp == 0) {
+      // a token-column row opens with key 0, in group 0's range of the row's first item
+      float fk[V], fv[V];
+#pragma unroll
+      for (int i = 0; i < V; ++i) fk[i] = fv[i] = 0.f;
+      if (r.row > 0 && beg < r.end && beg == it.ptr[r.row]) {
+        token_entry<T>(k, v, bias, factor, dbias, beg, sh, g, rg, qr, gr, acc, fk, fv);
+        ++beg;
+      }
+      if (g.act) {
+        float* rec = token_rec + int64_t(blockIdx.x) * (2 * sh.D);
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+          rec[g.col0 + i] = fk[i];
+          rec[sh.D + g.col0 + i] = fv[i];
+        }
+      }
+    }
+    dq_segment<T>(k, v, kv, bias, factor, dbias, beg, r.end, sh, g, rg, qr, gr, acc);
     float z = 0.f;
     block_combine<V>(lds, it.stride, sh, g, acc, unused, false, z, false);
     if (r.single) {
-      if ((threadIdx.x >> sh.lpr_log2) == 0 && g.act) Elem<T>::store(dq + int64_t(r.row) * sh.D + g.col0, acc);
+      if (grp == 0 && g.act) Elem<T>::store(dq + int64_t(r.row) * sh.D + g.col0, acc);
     } else {
       store_record<V>(it, blockIdx.x, sh, g, acc, unused, false, z, false);
     }
-    if (r.j == 0 && (threadIdx.x >> sh.lpr_log2) == 0 && g.lead) store_row_stat(rstat, r.row, sh, g, rg);
+    if (r.j == 0 && grp == 0 && g.lead) store_row_stat(rstat, r.row, sh, g, rg);
     return;
   }
   const int64_t row = row_slot(sh, unsigned(n_items));
-  if (row >= n_q) return;
-  const int64_t beg = qptr[row], end = qptr[row + 1];
-  if (end - beg > chunk) return;
-  const typename Elem<T>::Raw qr = load_row_raw_nt(q, row, sh.D, g);
-  const RowGrad rg = row_grad<T>(out, dout, Z, row, sh, g, gr);
-  dq_segment<T>(k, v, kv, bias, factor, dbias, beg, end, sh, g, rg, qr, gr, acc);
-  if (g.act) {
-    Elem<T>::store_nt(dq + row * sh.D + g.col0, acc);
-    if (g.lead) store_row_stat(rstat, row, sh, g, rg);
+  int64_t beg = 0, end = 0;
+  bool live = row < n_q;
+  if (live) {
+    beg = qptr[row];
+    end = qptr[row + 1];
+    live = end - beg <= chunk;    // a split row: its items and the reduce write it
+  }
+  if (!token_rec && !live) return;
+  typename Elem<T>::Raw qr = Elem<T>::zero_raw();
+  RowGrad rg{1.f, 0.f};
+  if (live) {
+    qr = load_row_raw_nt(q, row, sh.D, g);
+    rg = row_grad<T>(out, dout, Z, row, sh, g, gr);
+  }
+  if (token_rec) {
+    float fk[V], fv[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) fk[i] = fv[i] = 0.f;
+    if (live && row > 0 && beg < end) {
+      token_entry<T>(k, v, bias, factor, dbias, beg, sh, g, rg, qr, gr, acc, fk, fv);
+      ++beg;
+    }
+    // sum the wave's groups (a fixed butterfly), then park the wave's sum in LDS
+    for (int o = 1 << sh.lpr_log2; o < 64; o <<= 1) {
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        fk[i] += __shfl_xor(fk[i], o, 64);
+        fv[i] += __shfl_xor(fv[i], o, 64);
+      }
+    }
+    if ((threadIdx.x & 63) < (1 << sh.lpr_log2) && g.act) {
+      float* slot = lds + (threadIdx.x >> 6) * (2 * sh.D);
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        slot[g.col0 + i] = fk[i];
+        slot[sh.D + g.col0 + i] = fv[i];
+      }
+    }
+  }
+  if (live) {
+    dq_segment<T>(k, v, kv, bias, factor, dbias, beg, end, sh, g, rg, qr, gr, acc);
+    if (g.act) {
+      Elem<T>::store_nt(dq + row * sh.D + g.col0, acc);
+      if (g.lead) store_row_stat(rstat, row, sh, g, rg);
+    }
+  }
+  if (!token_rec) return;
+  __syncthreads();
+  if (threadIdx.x < (1u << sh.lpr_log2) && g.act) {   // the workgroup's record: its waves in order
+    float sk[V], sv[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) sk[i] = sv[i] = 0.f;
+    for (int w = 0; w < kBlock / 64; ++w) {
+      const float* slot = lds + w * (2 * sh.D);
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        sk[i] += slot[g.col0 + i];
+        sv[i] += slot[sh.D + g.col0 + i];
+      }
+    }
+    float* rec = token_rec + int64_t(blockIdx.x) * (2 * sh.D);
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      rec[g.col0 + i] = sk[i];
+      rec[sh.D + g.col0 + i] = sv[i];
+    }
   }
 }
 
@@ -606,7 +743,8 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
     const int32_t* __restrict__ ke, const float* __restrict__ bias,
     const float* __restrict__ factor, const T* __restrict__ dout, const float2* __restrict__ rstat,
     T* __restrict__ dq, T* __restrict__ dk, T* __restrict__ dv, const int32_t* __restrict__ order,
-    Items qit, int q_heavy, Items kit, int k_items, int64_t n_kv, Shape sh, int chunk, int rows_per_group) {
+    Items qit, int q_heavy, Items kit, int k_items, int64_t n_kv, Shape sh, int chunk, int rows_per_group,
+    const float* __restrict__ token_rec, int64_t n_token_rec) {
   constexpr int V = Elem<T>::kPerVec;
   extern __shared__ float lds[];
   const GroupPos g = group_pos<T>(sh);
@@ -623,8 +761,19 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
   if (b < q_heavy + k_items) {
     const int64_t item = b - q_heavy;
     const ItemRange r = item_group_range(kit, sh, item);
-    const typename Elem<T>::Raw kr = load_row_raw(k, r.row, sh.D, g), vr = load_row_raw(v, r.row, sh.D, g);
-    dkv_segment<T, NT>(q, dout, kq, ke, bias, factor, rstat, r.beg, r.end, sh, g, kr, vr, ak, av);
+    if (token_rec && r.row == 0) {
+      // key 0's terms were summed per dq-pass workgroup: item j of n takes records [R*j/n, R*(j+1)/n),
+      // its groups contiguous shares of them
+      const int n0 = kit.nitems[0];
+      const int64_t lo = n_token_rec * r.j / n0, hi = n_token_rec * (r.j + 1) / n0;
+      const int gpb = kBlock >> sh.lpr_log2;
+      const int64_t sub = (hi - lo + gpb - 1) / gpb;
+      const int64_t a0 = min(lo + (threadIdx.x >> sh.lpr_log2) * sub, hi), a1 = min(a0 + sub, hi);
+      sum_token_records<V>(token_rec, a0, a1, sh, g, ak, av);
+    } else {
+      const typename Elem<T>::Raw kr = load_row_raw(k, r.row, sh.D, g), vr = load_row_raw(v, r.row, sh.D, g);
+      dkv_segment<T, NT>(q, dout, kq, ke, bias, factor, rstat, r.beg, r.end, sh, g, kr, vr, ak, av);
+    }
     float z = 0.f;
     block_combine<V>(lds, kit.stride, sh, g, ak, av, true, z, false);
     if (r.single) {
@@ -644,6 +793,16 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
     const int64_t row = order ? int64_t(order[slot]) : slot;
     const int64_t beg = kptr[row], end = kptr[row + 1];
     if (end - beg > chunk) continue;
+    if (token_rec && row == 0) {  // a short token column: this group sums every record
+#pragma unroll
+      for (int i = 0; i < V; ++i) ak[i] = av[i] = 0.f;
+      sum_token_records<V>(token_rec, 0, n_token_rec, sh, g, ak, av);
+      if (g.act) {
+        Elem<T>::store_nt(dk + g.col0, ak);
+        Elem<T>::store_nt(dv + g.col0, av);
+      }
+      continue;
+    }
     if (beg == end) {             // a row no query attends to: zero gradients, no reads, written past the caches
       if (g.act) {
         store_zero16_nt(dk + row * sh.D + g.col0);
@@ -792,11 +951,15 @@ int bwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
   const Items qit = query_items(idx, sh, partials);
   const Items kit = key_items(idx, sh, partials);
   const int64_t q_blocks = int64_t(idx->q_items) + grid_for(idx->n_q, sh);
+  // token column: one record of key 0's terms per dq-pass workgroup, after the item records
+  float* token_rec = idx->token_column && idx->n_kv > 0 && q_blocks > 0
+                         ? partials + (int64_t(idx->q_items) + idx->k_items) * (2 * sh.D + sh.H)
+                         : nullptr;
   if (q_blocks > 0) {
-    const size_t lds = idx->q_items > 0 ? combine_lds_bytes(sh) : 0;
+    const size_t lds = (idx->q_items > 0 || token_rec) ? combine_lds_bytes(sh) : 0;
     BF_LAUNCH("attn_bwd_q_kernel", attn_bwd_q_kernel<T>, dim3(unsigned(q_blocks)), dim3(kBlock), lds, st, Q, K, Vv,
               idx->qptr, idx->kv, bias, factor, O, Z, dO, static_cast<T*>(dq), dbias, rstat, qit, idx->q_items,
-              idx->n_q, sh, idx->chunk);
+              idx->n_q, sh, idx->chunk, token_rec);
     BF_CHECK_LAUNCH();
   }
   const int rows_per_group = kv_rows_per_group(idx->n_kv);
@@ -808,7 +971,7 @@ int bwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
   BF_LAUNCH("attn_bwd_kv_kernel", (attn_bwd_kv_kernel<T, NT>), dim3(unsigned(kv_blocks)), dim3(kBlock), lds, st, Q, K, \
             Vv, idx->kptr, idx->kq, idx->ke, bias, factor, dO, rstat, static_cast<T*>(dq), static_cast<T*>(dk),       \
             static_cast<T*>(dv), idx->k_order, qit, idx->q_heavy, kit, idx->k_items, idx->n_kv, sh, idx->chunk,     \
-            rows_per_group)
+            rows_per_group, token_rec, q_blocks)
     if (stream_rows)
       BF_LAUNCH_KV(true);
     else
@@ -830,10 +993,19 @@ int bwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
 using namespace bf;
 
 extern "C" int64_t bf_attn_partials_floats(const bf_attn_index* idx, int32_t num_heads, int32_t head_dim) {
-  if (!idx) return 0;
+  if (!idx || num_heads <= 0 || head_dim <= 0) return 0;
   const int64_t items = int64_t(idx->q_items) + idx->k_items;   // query-side records, then key-side
   const int64_t D = int64_t(num_heads) * head_dim;
-  return items * (2 * D + num_heads);
+  int64_t floats = items * (2 * D + num_heads);
+  if (idx->token_column) {
+    // one 2*D record per dq-pass workgroup; float32 rows take the most lanes per row, hence the most
+    // workgroups (bfloat16 rows half as many lanes)
+    int64_t lpr = 1;
+    while (lpr < (D + 3) / 4 && lpr < 64) lpr <<= 1;
+    const int64_t rows_per_block = kBlock / lpr;
+    floats += (int64_t(idx->q_items) + ceil_div(idx->n_q, rows_per_block)) * 2 * D;
+  }
+  return floats;
 }
 
 extern "C" int bf_attn_fwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
@@ -868,8 +1040,8 @@ extern "C" int bf_attn_bwd(const bf_attn_index* idx, int32_t dtype, int32_t num_
   BF_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out) && aligned16(dout) &&
                    aligned16(dq) && aligned16(dk) && aligned16(dv),
                "attn_bwd: tensors must be 16-byte aligned");
-  BF_CHECK_ARG((idx->q_items == 0 && idx->k_items == 0) || partials,
-               "attn_bwd: partials buffer required for split rows");
+  BF_CHECK_ARG((idx->q_items == 0 && idx->k_items == 0 && !idx->token_column) || partials,
+               "attn_bwd: partials buffer required for split rows and the token column");
   if (dtype == BF_DTYPE_F32)
     return bwd_impl<float>(idx, sh, q, k, v, bias, factor, out, Z, dout, dq, dk, dv, dbias, rowstat,
                            partials, as_stream(stream));

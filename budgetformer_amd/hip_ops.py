@@ -526,6 +526,9 @@ class AttentionIndex:
     ke: Optional[torch.Tensor] = None
     kplan: Optional[SplitPlan] = None
     korder: Optional[torch.Tensor] = None
+    # key 0 is the Graphormer token column (attended by queries 1..n_q-1 once each, first in their rows, and
+    # by nothing else): the dq pass then sums its dK/dV terms instead of the dk/dv pass re-gathering them
+    token_column: bool = False
     _rows: Optional[torch.Tensor] = field(default=None, repr=False)
     _rkeys: Optional[ReverseKeys] = field(default=None, repr=False)   # from_table: sort keys, until used
     _sorted: Optional[ReverseKeys] = field(default=None, repr=False)  # sorted keys, until ke is needed
@@ -622,6 +625,7 @@ class AttentionIndex:
             s.k_nitems, s.k_item_off, s.k_item_row, s.k_heavy_rows = (
                 kp.nitems.data_ptr(), kp.item_off.data_ptr(), kp.item_row.data_ptr(), kp.heavy_rows.data_ptr())
             s.k_order = self.korder.data_ptr() if self.n_kv > 0 else None
+        s.token_column = int(self.token_column)
         return s
 
     @classmethod
@@ -648,7 +652,9 @@ class AttentionIndex:
                 raise ValueError(f"table ids must lie in [0, {n_kv - shift}) (got [{stats[2]}, {stats[3]}])")
         qptr, kv, rk = table_to_csr(table, row_len, global_token, with_keys=True)
         n_q = qptr.numel() - 1
-        return cls(n_q=n_q, n_kv=n_kv, qptr=qptr, kv=kv, chunk=chunk, item=item, _rkeys=rk)
+        # the token fill puts key 0 first in every row t >= 1 and shifts the table's own ids past it
+        return cls(n_q=n_q, n_kv=n_kv, qptr=qptr, kv=kv, chunk=chunk, item=item, _rkeys=rk,
+                   token_column=bool(global_token))
 
     @classmethod
     def from_coo(cls, edge_index, n_q: int, n_kv: Optional[int] = None, chunk: int = DEFAULT_CHUNK,

@@ -352,9 +352,17 @@ typedef struct bf_attn_index {
   const int32_t* k_item_row;
   const int32_t* k_heavy_rows;
   const int32_t* k_order;       /* [n_kv] key rows longest-first (bf_row_order), or NULL */
+  int32_t token_column;         /* 1: key 0 is the Graphormer token column — attended by
+                                   queries 1..n_q-1 exactly once each, at the first
+                                   position of their rows, and by no other entry
+                                   (bf_table_to_csr with global_token gives this);
+                                   the dq pass then also sums key 0's dK/dV terms,
+                                   which the dk/dv pass would otherwise re-gather.
+                                   0: no such promise. */
 } bf_attn_index;
 
-/* float32 scratch the attention calls need for split rows. */
+/* float32 scratch the attention calls need for split rows (and, with
+ * token_column, one record of 2*D floats per dq-pass workgroup). */
 int64_t bf_attn_partials_floats(const bf_attn_index* idx, int32_t num_heads, int32_t head_dim);
 
 /* Forward. Replaces CoreAttention.sparse_attention_bias

@@ -69,10 +69,12 @@ def test_fp32_random_coo(hip_device, S, H, hn, E):
         assert _rel_err(got, ref) < 1e-5
 
 
+@pytest.mark.parametrize("token_column", [False, True])
 @pytest.mark.parametrize("chunk,item", [(4, 4), (4, 37), (64, 512), (4, 2)])
-def test_fp32_global_token_split_rows(hip_device, chunk, item):
+def test_fp32_global_token_split_rows(hip_device, chunk, item, token_column):
     """Graphormer token: query 0 is dense over all kv and kv 0 feeds every query. With items of 2
-    the token row and column exceed the per-row item cap and run as 160 balanced items."""
+    the token row and column exceed the per-row item cap and run as 160 balanced items. The COO
+    has the token-column layout, so key 0's terms can also come from the dq pass (token_column)."""
     from budgetformer_amd.hip_ops import AttentionIndex
     S, H, hn = 500, 8, 16
     q, k, v, ei, dout = _inputs(S, H, hn, 2500, seed=7, mult=1.3)
@@ -80,6 +82,7 @@ def test_fp32_global_token_split_rows(hip_device, chunk, item):
     ar = torch.arange(1, S)
     ei = torch.cat([ei, torch.stack([ar, torch.zeros_like(ar)]), torch.stack([torch.zeros_like(ar), ar])], 1)
     idx = AttentionIndex.from_coo(ei.to(hip_device), S, chunk=chunk, item=item)
+    idx.token_column = token_column
     out, dq, dk, dv, _ = _run(hip_device, q, k, v, idx, dout)
     ro, rZ, rdq, rdk, rdv, _ = _oracle(q, k, v, ei, dout)
     assert idx.qplan.items > 0 and idx.kplan.items > 0 and idx.qplan.heavy > 0   # split paths exercised
@@ -87,8 +90,9 @@ def test_fp32_global_token_split_rows(hip_device, chunk, item):
         assert _rel_err(got, ref) < 1e-5
 
 
+@pytest.mark.parametrize("token_column", [False, True])
 @pytest.mark.parametrize("chunk,item", [(4, 37), (8, 16)])
-def test_bf16_split_rows_single_and_multi_item(hip_device, chunk, item):
+def test_bf16_split_rows_single_and_multi_item(hip_device, chunk, item, token_column):
     """Split rows with one item (finished by that item) and with several (summed by the reduce), bf16."""
     from budgetformer_amd.hip_ops import AttentionIndex
     S, H, hn = 600, 8, 16
@@ -97,6 +101,7 @@ def test_bf16_split_rows_single_and_multi_item(hip_device, chunk, item):
     ar = torch.arange(1, S)
     ei = torch.cat([ei, torch.stack([ar, torch.zeros_like(ar)]), torch.stack([torch.zeros_like(ar), ar])], 1)
     idx = AttentionIndex.from_coo(ei.to(hip_device), S, chunk=chunk, item=item)
+    idx.token_column = token_column
     idx.ensure_backward()
     for plan in (idx.qplan, idx.kplan):
         n = plan.nitems.cpu()
@@ -151,6 +156,50 @@ def test_table_index_plain_then_bias_backward(hip_device, token):
     ro, rZ, rdq, rdk, rdv, rdb = _oracle(q, k, v, ei_o, dout, bias_e=bias_e, factor_e=factor)
     for got, ref in ((out, ro), (dq, rdq), (dk, rdk), (dv, rdv), (db, rdb)):
         assert _rel_err(got, ref) < 1e-5
+
+
+@pytest.mark.parametrize("dtype,chunk,item,n", [(torch.float32, 128, 768, 3000), (torch.float32, 5, 7, 400),
+                                                 (torch.bfloat16, 16, 24, 1500), (torch.float32, 128, 768, 60)])
+def test_token_column_terms_summed_by_the_dq_pass(hip_device, dtype, chunk, item, n):
+    """With a token column (key 0 first in every row t >= 1, as the table fill lays it out) the dq pass
+    sums key 0's dK/dV terms per workgroup and the dk/dv pass reduces those records instead of gathering
+    each query's q, dO and row stats again. Against the gathering pass on the same index: out, dq, dbias
+    and every other key row equal bit for bit (the same arithmetic), key 0 within the parity bar
+    (another summation order); both against the oracle. (chunk, item) = (5, 7) also splits the query
+    rows, so key 0 opens item 0 of a split row; n = 60 leaves the token column shorter than `chunk`,
+    one group then sums every record."""
+    import numpy as np
+    from budgetformer_amd.hip_ops import AttentionIndex
+    rng = np.random.default_rng(n + chunk)
+    width, H, hn = 6, 8, 16
+    row_len = rng.integers(0, width + 1, n).astype(np.int32)
+    table = np.full((n, width), -1, dtype=np.int32)
+    for r in range(n):
+        table[r, :row_len[r]] = np.sort(rng.choice(n, row_len[r], replace=False))
+    tab_d, len_d = torch.from_numpy(table).to(hip_device), torch.from_numpy(row_len).to(hip_device)
+    runs = []
+    for token_column in (True, False):
+        idx = AttentionIndex.from_table(tab_d, len_d, global_token=True, chunk=chunk, item=item)
+        assert idx.token_column
+        idx.token_column = token_column
+        S = idx.n_q
+        q, k, v, _, dout = _inputs(S, H, hn, 1, seed=n, dtype=dtype, mult=1.3)
+        g = torch.Generator().manual_seed(9)
+        bias_e = torch.randn(idx.nnz, H, generator=g) if dtype == torch.float32 else None
+        factor = ((torch.rand(idx.nnz, H, generator=g) >= 0.25).float() / 0.75) if dtype == torch.float32 else None
+        runs.append(_run(hip_device, q, k, v, idx, dout, bias_e=bias_e, factor_e=factor))
+    (out_f, dq_f, dk_f, dv_f, db_f), (out_g, dq_g, dk_g, dv_g, db_g) = runs
+    assert torch.equal(out_f, out_g) and torch.equal(dq_f, dq_g)
+    assert (db_f is None and db_g is None) or torch.equal(db_f, db_g)
+    assert torch.equal(dk_f[1:], dk_g[1:]) and torch.equal(dv_f[1:], dv_g[1:])
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    assert _rel_err(dk_f[0], dk_g[0]) < tol and _rel_err(dv_f[0], dv_g[0]) < tol
+    ei_o = _coo_order(idx)
+    ro, rZ, rdq, rdk, rdv, rdb = _oracle(q, k, v, ei_o, dout, bias_e=bias_e, factor_e=factor)
+    for got, ref in ((out_f, ro), (dq_f, rdq), (dk_f, rdk), (dv_f, rdv)):
+        assert _rel_err(got, ref) < tol
+    if db_f is not None:
+        assert _rel_err(db_f, rdb) < tol
 
 
 def test_fp32_gps_dropout_factor(hip_device):
