@@ -743,6 +743,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
     const int32_t* __restrict__ ke, const float* __restrict__ bias,
     const float* __restrict__ factor, const T* __restrict__ dout, const float2* __restrict__ rstat,
     T* __restrict__ dq, T* __restrict__ dk, T* __restrict__ dv, const int32_t* __restrict__ order,
+    const uint64_t* __restrict__ spans,
     Items qit, int q_heavy, Items kit, int k_items, int64_t n_kv, Shape sh, int chunk, int rows_per_group,
     const float* __restrict__ token_rec, int64_t n_token_rec) {
   constexpr int V = Elem<T>::kPerVec;
@@ -791,7 +792,15 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
   const int64_t last = first + rows_per_group < n_kv ? first + rows_per_group : n_kv;
   for (int64_t slot = first; slot < last; ++slot) {
     const int64_t row = order ? int64_t(order[slot]) : slot;
-    const int64_t beg = kptr[row], end = kptr[row + 1];
+    int64_t beg, end;
+    if (spans) {                  // the slot's (begin << 32 | length): read in slot order, not at random
+      const uint64_t sp = spans[slot];
+      beg = int64_t(sp >> 32);
+      end = beg + int64_t(sp & 0xffffffffu);
+    } else {
+      beg = kptr[row];
+      end = kptr[row + 1];
+    }
     if (end - beg > chunk) continue;
     if (token_rec && row == 0) {  // a short token column: this group sums every record
 #pragma unroll
@@ -877,6 +886,7 @@ int check_index(const bf_attn_index* idx, bool backward) {
     BF_CHECK_ARG(idx->k_items >= 0 && idx->k_heavy >= 0, "attention: bad key-side plan counts");
     BF_CHECK_ARG(idx->k_items == 0 || (idx->k_nitems && idx->k_item_off && idx->k_item_row && idx->k_heavy_rows),
                  "attention: key-side split plan missing");
+    BF_CHECK_ARG(!idx->k_spans || idx->k_order, "attention: k_spans describe the slots of k_order, which is NULL");
   }
   return BF_OK;
 }
@@ -970,7 +980,8 @@ int bwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
 #define BF_LAUNCH_KV(NT)                                                                                           \
   BF_LAUNCH("attn_bwd_kv_kernel", (attn_bwd_kv_kernel<T, NT>), dim3(unsigned(kv_blocks)), dim3(kBlock), lds, st, Q, K, \
             Vv, idx->kptr, idx->kq, idx->ke, bias, factor, dO, rstat, static_cast<T*>(dq), static_cast<T*>(dk),       \
-            static_cast<T*>(dv), idx->k_order, qit, idx->q_heavy, kit, idx->k_items, idx->n_kv, sh, idx->chunk,     \
+            static_cast<T*>(dv), idx->k_order, idx->k_spans, qit, idx->q_heavy, kit, idx->k_items, idx->n_kv, sh,     \
+            idx->chunk,                                                                                              \
             rows_per_group, token_rec, q_blocks)
     if (stream_rows)
       BF_LAUNCH_KV(true);

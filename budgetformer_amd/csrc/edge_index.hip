@@ -246,14 +246,17 @@ __global__ __launch_bounds__(kThreads) void order_hist_kernel(const int64_t* __r
 
 // Each block orders `chunk` consecutive rows: it counts them per bucket in
 // LDS, reserves one range per bucket with a single global atomic (few blocks,
-// so the popular short-row buckets see little contention), then places them.
+// so the popular short-row buckets see little contention), then places them,
+// and with `spans` each slot's row as (begin << 32 | length), which the reader
+// then takes from the slot instead of a random read of the row pointers.
 // Smaller chunks were measured no faster on 169K rows and slower on 2.4M.
 constexpr int64_t kOrderChunk = 16 * kThreads;
 
 __global__ __launch_bounds__(kThreads) void order_scatter_kernel(const int64_t* __restrict__ ptr, int64_t n_rows,
                                                                  int64_t chunk, const uint32_t* __restrict__ hist,
                                                                  uint32_t* __restrict__ cursor,
-                                                                 int32_t* __restrict__ order) {
+                                                                 int32_t* __restrict__ order,
+                                                                 uint64_t* __restrict__ spans) {
   __shared__ uint32_t base[kBuckets];
   __shared__ uint32_t cnt[kBuckets];
   const int tid = threadIdx.x;
@@ -277,8 +280,11 @@ __global__ __launch_bounds__(kThreads) void order_scatter_kernel(const int64_t* 
   cnt[tid] = 0;
   __syncthreads();
   for (int64_t r = r0 + tid; r < r1; r += kThreads) {
-    const int b = length_bucket(ptr, r);
-    order[base[b] + atomicAdd(&cnt[b], 1u)] = int32_t(r);
+    const int64_t beg = ptr[r], len = ptr[r + 1] - beg;
+    const int b = 255 - int(len < 255 ? len : 255);
+    const uint32_t slot = base[b] + atomicAdd(&cnt[b], 1u);
+    order[slot] = int32_t(r);
+    if (spans) spans[slot] = (uint64_t(beg) << 32) | uint64_t(len);
   }
 }
 
@@ -798,7 +804,7 @@ extern "C" int bf_row_order_workspace_size(int64_t n_rows, size_t* bytes) {
   return BF_OK;
 }
 
-extern "C" int bf_row_order(const int64_t* ptr, int64_t n_rows, int32_t* order, void* workspace,
+extern "C" int bf_row_order(const int64_t* ptr, int64_t n_rows, int32_t* order, uint64_t* spans, void* workspace,
                             size_t workspace_bytes, void* stream) {
   BF_CHECK_ARG(ptr && n_rows >= 0 && n_rows < (int64_t(1) << 31), "row_order: bad arguments");
   if (n_rows == 0) return BF_OK;
@@ -816,7 +822,7 @@ extern "C" int bf_row_order(const int64_t* ptr, int64_t n_rows, int32_t* order, 
   BF_CHECK_LAUNCH();
   const int64_t chunk = kOrderChunk;
   BF_LAUNCH("order_scatter_kernel", order_scatter_kernel, dim3(unsigned(ceil_div(n_rows, chunk))), dim3(kThreads), 0,
-            st, ptr, n_rows, chunk, hist, cursor, order);
+            st, ptr, n_rows, chunk, hist, cursor, order, spans);
   BF_CHECK_LAUNCH();
   return BF_OK;
 }

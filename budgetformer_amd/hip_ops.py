@@ -435,13 +435,15 @@ def expand_rows(ptr: torch.Tensor, nnz: int) -> torch.Tensor:
     return rows
 
 
-def row_order(ptr: torch.Tensor) -> torch.Tensor:
-    """Rows of a CSR longest-first (bf_row_order), int32 [n_rows]."""
+def row_order(ptr: torch.Tensor, spans: bool = False):
+    """Rows of a CSR longest-first (bf_row_order), int32 [n_rows]; with ``spans`` also each slot's row as
+    (begin << 32 | length), int64 [n_rows] (needs ptr[-1] < 2**32)."""
     n_rows = ptr.numel() - 1
     order = torch.empty(max(n_rows, 1), dtype=torch.int32, device=ptr.device)
+    sp = torch.empty(max(n_rows, 1), dtype=torch.int64, device=ptr.device) if spans else None
     ws = _workspace(_size_query("bf_row_order_workspace_size", n_rows), ptr.device)
-    N.call("bf_row_order", _p(ptr), n_rows, _p(order), _p(ws), ws.numel(), _stream(ptr.device))
-    return order
+    N.call("bf_row_order", _p(ptr), n_rows, _p(order), _p(sp), _p(ws), ws.numel(), _stream(ptr.device))
+    return (order, sp) if spans else order
 
 
 @dataclass
@@ -526,6 +528,7 @@ class AttentionIndex:
     ke: Optional[torch.Tensor] = None
     kplan: Optional[SplitPlan] = None
     korder: Optional[torch.Tensor] = None
+    kspans: Optional[torch.Tensor] = None      # per korder slot: (kptr[row] << 32 | row length)
     # key 0 is the Graphormer token column (attended by queries 1..n_q-1 once each, first in their rows, and
     # by nothing else): the dq pass then sums its dK/dV terms instead of the dk/dv pass re-gathering them
     token_column: bool = False
@@ -570,7 +573,7 @@ class AttentionIndex:
             self.kplan = split_plan(self.kptr, self.nnz, self.chunk, self.item, resolve=False,
                                     counts=self._plan_counts(1))
         if self.korder is None:
-            self.korder = row_order(self.kptr)
+            self.korder, self.kspans = row_order(self.kptr, spans=True)
         resolve_plans(self.qplan, self.kplan)      # both plans' counts in one read
         return self
 
@@ -625,6 +628,7 @@ class AttentionIndex:
             s.k_nitems, s.k_item_off, s.k_item_row, s.k_heavy_rows = (
                 kp.nitems.data_ptr(), kp.item_off.data_ptr(), kp.item_row.data_ptr(), kp.heavy_rows.data_ptr())
             s.k_order = self.korder.data_ptr() if self.n_kv > 0 else None
+            s.k_spans = self.kspans.data_ptr() if (self.n_kv > 0 and self.kspans is not None) else None
         s.token_column = int(self.token_column)
         return s
 

@@ -319,9 +319,12 @@ int bf_split_plan(const int64_t* ptr, int64_t n_rows, int32_t threshold, int32_t
  * capped length in an unspecified order that may change from call to call).
  * The key-major attention pass walks its rows in this order so the groups
  * sharing a wavefront carry similar work; a row's arithmetic does not depend
- * on its place. Workspace: bf_row_order_workspace_size.                     */
+ * on its place. spans (may be NULL; needs ptr[n_rows] < 2^32) receives, per
+ * slot, the slot's row as (ptr[row] << 32 | row length), so a reader walking
+ * the order finds each row's entries without a random read of ptr.
+ * Workspace: bf_row_order_workspace_size.                                    */
 int bf_row_order_workspace_size(int64_t n_rows, size_t* bytes);
-int bf_row_order(const int64_t* ptr, int64_t n_rows, int32_t* order, void* workspace,
+int bf_row_order(const int64_t* ptr, int64_t n_rows, int32_t* order, uint64_t* spans, void* workspace,
                  size_t workspace_bytes, void* stream);
 
 /* ======================================================================
@@ -359,6 +362,9 @@ typedef struct bf_attn_index {
                                    the dq pass then also sums key 0's dK/dV terms,
                                    which the dk/dv pass would otherwise re-gather.
                                    0: no such promise. */
+  const uint64_t* k_spans;      /* [n_kv] or NULL: bf_row_order's spans of k_order (needs
+                                   k_order); the dk/dv pass then reads each row's entry
+                                   range from its slot instead of from kptr            */
 } bf_attn_index;
 
 /* float32 scratch the attention calls need for split rows (and, with

@@ -301,9 +301,14 @@ def test_index_formats_against_numpy(hip_device, token):
     order = np.lexsort((pos, np.array(vals)))                    # (kv, position) order
     assert np.array_equal(b[1].cpu().numpy(), np.array(rows)[order]) and np.array_equal(b[2].cpu().numpy(), order)
     # row order: a permutation, capped lengths non-increasing
-    ro = hip_ops.row_order(b[0]).cpu().numpy()
-    lens = np.minimum(np.diff(b[0].cpu().numpy()), 255)
+    ro, sp = hip_ops.row_order(b[0], spans=True)
+    ro, sp = ro.cpu().numpy(), sp.cpu().numpy().astype(np.uint64)
+    kp = b[0].cpu().numpy()
+    lens = np.minimum(np.diff(kp), 255)
     assert np.array_equal(np.sort(ro), np.arange(n_q)) and (np.diff(lens[ro]) <= 0).all()
+    # spans: each slot's row as (begin << 32 | length)
+    assert np.array_equal(sp >> np.uint64(32), kp[ro].astype(np.uint64))
+    assert np.array_equal(sp & np.uint64(0xFFFFFFFF), (kp[ro + 1] - kp[ro]).astype(np.uint64))
     # split plan (threshold 4, items of 5) against a direct count
     plan = hip_ops.split_plan(b[0], kv.numel(), 4, 5)
     L = np.diff(b[0].cpu().numpy())
