@@ -287,6 +287,7 @@ def main(argv=None):
           f"{attn_ms:.3f})", flush=True)
 
     nnz = idx.nnz
+    idx.resolve()                                      # plan counts for the report (after the timed loops)
     a_fwd, a_bwd = attention_bytes(s_bytes, D, H, S, S_kv, nnz)
     attn_gbs = (a_fwd + a_bwd) / (attn_ms * 1e-3) / 1e9
 

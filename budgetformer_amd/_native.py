@@ -16,6 +16,7 @@ _LIB = os.path.join(_PKG, "_lib", "libbudgetformer_hip.so")
 
 BF_OK, BF_ERR_INVALID, BF_ERR_UNSUPPORTED, BF_ERR_HIP = 0, 1, 2, 3
 BF_DTYPE_F32, BF_DTYPE_BF16 = 0, 1
+BF_MAX_ITEMS_PER_ROW = 160          # items a split row is cut into at most (the header's #define)
 
 i32, i64, u64, sz = C.c_int32, C.c_int64, C.c_uint64, C.c_size_t
 vp = C.c_void_p
@@ -34,7 +35,7 @@ class AttnIndex(C.Structure):
         ("q_nitems", vp), ("q_item_off", vp), ("q_item_row", vp), ("q_heavy_rows", vp),
         ("k_items", i32), ("k_heavy", i32),
         ("k_nitems", vp), ("k_item_off", vp), ("k_item_row", vp), ("k_heavy_rows", vp),
-        ("k_order", vp), ("token_column", i32), ("k_spans", vp),
+        ("k_order", vp), ("token_column", i32), ("k_spans", vp), ("plan_counts", vp),
     ]
 
 

@@ -324,14 +324,18 @@ __global__ __launch_bounds__(kBlock) void attn_fwd_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const int64_t* __restrict__ qptr, const int32_t* __restrict__ kv,
     const float* __restrict__ bias, const float* __restrict__ factor,
-    T* __restrict__ out, float* __restrict__ Z, Items it, int n_items, int64_t n_q, Shape sh, int chunk) {
+    T* __restrict__ out, float* __restrict__ Z, Items it, int n_items_arg, int64_t n_q, Shape sh, int chunk,
+    const int32_t* __restrict__ plan_counts) {
   constexpr int V = Elem<T>::kPerVec;
   const GroupPos g = group_pos<T>(sh);
+  // blocks [0, n_items_arg) are item slots (the capacity when the counts are on the device; the
+  // unused ones exit early, while the items run), the rest one short row per group
   float acc[V];
 #pragma unroll
   for (int i = 0; i < V; ++i) acc[i] = 0.f;
   float z = 0.f;
-  if (int(blockIdx.x) < n_items) {
+  if (int(blockIdx.x) < n_items_arg) {
+    if (plan_counts && int(blockIdx.x) >= plan_counts[0]) return;
     extern __shared__ float lds[];
     const ItemRange r = item_group_range(it, sh, blockIdx.x);
     float unused[V];
@@ -347,7 +351,7 @@ __global__ __launch_bounds__(kBlock) void attn_fwd_kernel(
     }
     return;
   }
-  const int64_t row = row_slot(sh, unsigned(n_items));
+  const int64_t row = row_slot(sh, unsigned(n_items_arg));
   if (row >= n_q) return;
   const int64_t beg = qptr[row], end = qptr[row + 1];
   if (end - beg > chunk) return;  // split row: its items and the reduce write it
@@ -358,8 +362,10 @@ __global__ __launch_bounds__(kBlock) void attn_fwd_kernel(
 
 template <typename T>
 __global__ __launch_bounds__(kBlock) void attn_fwd_reduce_kernel(T* __restrict__ out, float* __restrict__ Z,
-                                                                 Items it, Shape sh) {
+                                                                 Items it, Shape sh,
+                                                                 const int32_t* __restrict__ plan_counts) {
   constexpr int V = Elem<T>::kPerVec;
+  if (plan_counts && int(blockIdx.x) >= plan_counts[1]) return;
   extern __shared__ float lds[];
   const GroupPos g = group_pos<T>(sh);
   float acc[V], unused[V], z;
@@ -504,14 +510,16 @@ __device__ __forceinline__ void token_entry(const T* __restrict__ k, const T* __
 }
 
 // Sums the token-column records [a0, a1) (2*D floats each: key 0's dK terms,
-// then its dV terms) into dk, dv.
+// then its dV terms) into dk, dv. Record m is the dq pass's workgroup m for
+// its n_items item workgroups and workgroup m - n_items + item_slots after
+// them (the row workgroups follow all item slots).
 template <int V>
 __device__ __forceinline__ void sum_token_records(const float* __restrict__ rec0, int64_t a0, int64_t a1,
-                                                  const Shape& sh, const GroupPos& g, float (&dk)[V],
-                                                  float (&dv)[V]) {
+                                                  int64_t n_items, int64_t item_slots, const Shape& sh,
+                                                  const GroupPos& g, float (&dk)[V], float (&dv)[V]) {
   if (!g.act) return;
   for (int64_t m = a0; m < a1; ++m) {
-    const float* rec = rec0 + m * (2 * sh.D);
+    const float* rec = rec0 + (m < n_items ? m : m - n_items + item_slots) * (2 * sh.D);
 #pragma unroll
     for (int i = 0; i < V; ++i) {
       dk[i] += rec[g.col0 + i];
@@ -527,19 +535,22 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_q_kernel(
     const int64_t* __restrict__ qptr, const int32_t* __restrict__ kv,
     const float* __restrict__ bias, const float* __restrict__ factor,
     const T* __restrict__ out, const float* __restrict__ Z, const T* __restrict__ dout,
-    T* __restrict__ dq, float* __restrict__ dbias, float2* __restrict__ rstat, Items it, int n_items,
-    int64_t n_q, Shape sh, int chunk, float* __restrict__ token_rec) {
+    T* __restrict__ dq, float* __restrict__ dbias, float2* __restrict__ rstat, Items it, int n_items_arg,
+    int64_t n_q, Shape sh, int chunk, float* __restrict__ token_rec, const int32_t* __restrict__ plan_counts) {
   constexpr int V = Elem<T>::kPerVec;
   extern __shared__ float lds[];
   const GroupPos g = group_pos<T>(sh);
   const int grp = threadIdx.x >> sh.lpr_log2;
+  // blocks [0, n_items_arg) are item slots (the capacity when the counts are on the device: an unused
+  // slot exits at once and writes no token record), the rest one short row per group
   float acc[V];
 #pragma unroll
   for (int i = 0; i < V; ++i) acc[i] = 0.f;
   typename Elem<T>::Raw gr;
   // With a token column every workgroup writes one record of its rows' key-0 terms (fk, fv: the
   // row's g_a*q/sqrt(hn) and p*f*dO/D'), kept out of the registers of the main loop.
-  if (int(blockIdx.x) < n_items) {
+  if (int(blockIdx.x) < n_items_arg) {
+    if (plan_counts && int(blockIdx.x) >= plan_counts[0]) return;
     const ItemRange r = item_group_range(it, sh, blockIdx.x);
     float unused[V];
 #pragma unroll
@@ -576,7 +587,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_q_kernel(
     if (r.j == 0 && grp == 0 && g.lead) store_row_stat(rstat, r.row, sh, g, rg);
     return;
   }
-  const int64_t row = row_slot(sh, unsigned(n_items));
+  const int64_t row = row_slot(sh, unsigned(n_items_arg));
   int64_t beg = 0, end = 0;
   bool live = row < n_q;
   if (live) {
@@ -744,14 +755,22 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
     const float* __restrict__ factor, const T* __restrict__ dout, const float2* __restrict__ rstat,
     T* __restrict__ dq, T* __restrict__ dk, T* __restrict__ dv, const int32_t* __restrict__ order,
     const uint64_t* __restrict__ spans,
-    Items qit, int q_heavy, Items kit, int k_items, int64_t n_kv, Shape sh, int chunk, int rows_per_group,
-    const float* __restrict__ token_rec, int64_t n_token_rec) {
+    Items qit, int q_heavy_arg, Items kit, int k_items_arg, int64_t n_kv, Shape sh, int chunk, int rows_per_group,
+    const float* __restrict__ token_rec, int q_items_arg, int64_t q_row_blocks, const int32_t* __restrict__ plan_counts) {
   constexpr int V = Elem<T>::kPerVec;
   extern __shared__ float lds[];
   const GroupPos g = group_pos<T>(sh);
+  // Block regions: [0, q_heavy_arg) dq split-row reduces, then k_items_arg key-side item slots, then
+  // the short key rows. With the counts on the device the *_arg values are capacities and a slot past
+  // the true count exits at once (early in the dispatch, beside the running items).
+  const int q_items = plan_counts ? plan_counts[0] : q_items_arg;
+  // token-column records: the dq pass's q_items item workgroups, then its q_row_blocks row workgroups
+  // (whose records start at slot q_items_arg); record m of the n_token_rec is at token_slot(m)
+  const int64_t n_token_rec = q_items + q_row_blocks;
   float ak[V], av[V];
   const int b = int(blockIdx.x);
-  if (b < q_heavy) {
+  if (b < q_heavy_arg) {
+    if (plan_counts && b >= plan_counts[1]) return;
     float z;
     const int row = reduce_row_records<V>(qit, b, lds, sh, g, ak, av, false, z, false);
     if (row >= 0 && (threadIdx.x >> sh.lpr_log2) == 0 && g.act) Elem<T>::store(dq + int64_t(row) * sh.D + g.col0, ak);
@@ -759,8 +778,9 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
   }
 #pragma unroll
   for (int i = 0; i < V; ++i) ak[i] = av[i] = 0.f;
-  if (b < q_heavy + k_items) {
-    const int64_t item = b - q_heavy;
+  if (b < q_heavy_arg + k_items_arg) {
+    const int64_t item = b - q_heavy_arg;
+    if (plan_counts && item >= plan_counts[2]) return;
     const ItemRange r = item_group_range(kit, sh, item);
     if (token_rec && r.row == 0) {
       // key 0's terms were summed per dq-pass workgroup: item j of n takes records [R*j/n, R*(j+1)/n),
@@ -770,7 +790,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
       const int gpb = kBlock >> sh.lpr_log2;
       const int64_t sub = (hi - lo + gpb - 1) / gpb;
       const int64_t a0 = min(lo + (threadIdx.x >> sh.lpr_log2) * sub, hi), a1 = min(a0 + sub, hi);
-      sum_token_records<V>(token_rec, a0, a1, sh, g, ak, av);
+      sum_token_records<V>(token_rec, a0, a1, q_items, q_items_arg, sh, g, ak, av);
     } else {
       const typename Elem<T>::Raw kr = load_row_raw(k, r.row, sh.D, g), vr = load_row_raw(v, r.row, sh.D, g);
       dkv_segment<T, NT>(q, dout, kq, ke, bias, factor, rstat, r.beg, r.end, sh, g, kr, vr, ak, av);
@@ -788,7 +808,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
     return;
   }
   // each group takes rows_per_group consecutive rows of the order (similar lengths)
-  const int64_t first = row_slot(sh, unsigned(q_heavy + k_items)) * rows_per_group;
+  const int64_t first = row_slot(sh, unsigned(q_heavy_arg + k_items_arg)) * rows_per_group;
   const int64_t last = first + rows_per_group < n_kv ? first + rows_per_group : n_kv;
   for (int64_t slot = first; slot < last; ++slot) {
     const int64_t row = order ? int64_t(order[slot]) : slot;
@@ -805,7 +825,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
     if (token_rec && row == 0) {  // a short token column: this group sums every record
 #pragma unroll
       for (int i = 0; i < V; ++i) ak[i] = av[i] = 0.f;
-      sum_token_records<V>(token_rec, 0, n_token_rec, sh, g, ak, av);
+      sum_token_records<V>(token_rec, 0, n_token_rec, q_items, q_items_arg, sh, g, ak, av);
       if (g.act) {
         Elem<T>::store_nt(dk + g.col0, ak);
         Elem<T>::store_nt(dv + g.col0, av);
@@ -832,8 +852,10 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
 
 template <typename T>
 __global__ __launch_bounds__(kBlock) void attn_bwd_kv_reduce_kernel(T* __restrict__ dk, T* __restrict__ dv,
-                                                                    Items it, Shape sh) {
+                                                                    Items it, Shape sh,
+                                                                    const int32_t* __restrict__ plan_counts) {
   constexpr int V = Elem<T>::kPerVec;
+  if (plan_counts && int(blockIdx.x) >= plan_counts[3]) return;
   extern __shared__ float lds[];
   const GroupPos g = group_pos<T>(sh);
   float ak[V], av[V], z;
@@ -936,12 +958,12 @@ int fwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
   if (blocks > 0) {
     const size_t lds = n_items > 0 ? combine_lds_bytes(sh) : 0;
     BF_LAUNCH("attn_fwd_kernel", attn_fwd_kernel<T>, dim3(unsigned(blocks)), dim3(kBlock), lds, st, Q, K, Vv,
-              idx->qptr, idx->kv, bias, factor, O, Z, it, n_items, idx->n_q, sh, idx->chunk);
+              idx->qptr, idx->kv, bias, factor, O, Z, it, n_items, idx->n_q, sh, idx->chunk, idx->plan_counts);
     BF_CHECK_LAUNCH();
   }
   if (idx->q_heavy > 0) {
     BF_LAUNCH("attn_fwd_reduce_kernel", attn_fwd_reduce_kernel<T>, dim3(unsigned(idx->q_heavy)), dim3(kBlock),
-              combine_lds_bytes(sh), st, O, Z, it, sh);
+              combine_lds_bytes(sh), st, O, Z, it, sh, idx->plan_counts);
     BF_CHECK_LAUNCH();
   }
   return BF_OK;
@@ -969,7 +991,7 @@ int bwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
     const size_t lds = (idx->q_items > 0 || token_rec) ? combine_lds_bytes(sh) : 0;
     BF_LAUNCH("attn_bwd_q_kernel", attn_bwd_q_kernel<T>, dim3(unsigned(q_blocks)), dim3(kBlock), lds, st, Q, K, Vv,
               idx->qptr, idx->kv, bias, factor, O, Z, dO, static_cast<T*>(dq), dbias, rstat, qit, idx->q_items,
-              idx->n_q, sh, idx->chunk, token_rec);
+              idx->n_q, sh, idx->chunk, token_rec, idx->plan_counts);
     BF_CHECK_LAUNCH();
   }
   const int rows_per_group = kv_rows_per_group(idx->n_kv);
@@ -982,7 +1004,7 @@ int bwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
             Vv, idx->kptr, idx->kq, idx->ke, bias, factor, dO, rstat, static_cast<T*>(dq), static_cast<T*>(dk),       \
             static_cast<T*>(dv), idx->k_order, idx->k_spans, qit, idx->q_heavy, kit, idx->k_items, idx->n_kv, sh,     \
             idx->chunk,                                                                                              \
-            rows_per_group, token_rec, q_blocks)
+            rows_per_group, token_rec, idx->q_items, int64_t(grid_for(idx->n_q, sh)), idx->plan_counts)
     if (stream_rows)
       BF_LAUNCH_KV(true);
     else
@@ -992,7 +1014,7 @@ int bwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
   }
   if (idx->k_heavy > 0) {
     BF_LAUNCH("attn_bwd_kv_reduce_kernel", attn_bwd_kv_reduce_kernel<T>, dim3(unsigned(idx->k_heavy)), dim3(kBlock),
-              combine_lds_bytes(sh), st, static_cast<T*>(dk), static_cast<T*>(dv), kit, sh);
+              combine_lds_bytes(sh), st, static_cast<T*>(dk), static_cast<T*>(dv), kit, sh, idx->plan_counts);
     BF_CHECK_LAUNCH();
   }
   return BF_OK;

@@ -16,6 +16,10 @@ import torch
 from . import _native as N
 
 DEFAULT_CHUNK = 128     # rows longer than this go through the split plan
+# A plan whose capacities (items + split rows) stay within this leaves its counts on the device: the
+# attention grids are then sized for the capacities and their extra workgroups exit at once, which
+# costs less than reading the counts back. Larger plans send their counts to pinned host memory.
+DEVICE_COUNTS_MAX_SLOTS = 1 << 15
 DEFAULT_ITEM = 768      # entries per split item (one workgroup), before balancing
 HUB_THRESHOLD = 1024    # in-degree above which a query's real-edge top-k uses a whole workgroup
 LIGHT_MAX = 32          # in-degree up to which a query's real-edge top-k runs in one thread (k <= 16)
@@ -459,11 +463,25 @@ class SplitPlan:
     item_row: torch.Tensor
     heavy_rows: torch.Tensor
     counts: Optional[torch.Tensor] = None
+    item_cap: int = 0           # capacities the arrays were sized for (upper bounds of the counts)
+    heavy_cap: int = 0
+    host_counts: Optional[torch.Tensor] = None   # pinned copy of `counts`, complete once `ready` is
+    ready: Optional[object] = None               # (a torch.cuda.Event recorded after the copy)
+
+    @property
+    def pending(self) -> bool:
+        return self.items < 0
 
 
 def resolve_plans(*plans) -> None:
-    """Read the counts of every pending plan with a single device-to-host copy."""
+    """Read the counts of every pending plan: from its pinned copy once that has landed, else with a
+    single device-to-host copy for all of them."""
     pending = [p for p in plans if p is not None and p.items < 0]
+    for p in [p for p in pending if p.ready is not None]:
+        p.ready.synchronize()
+        p.items, p.heavy = (int(x) for x in p.host_counts.tolist())
+        p.counts = p.host_counts = p.ready = None
+    pending = [p for p in pending if p.items < 0]
     if not pending:
         return
     # plans made with one shared counts buffer (split_plan(..., counts=...)) come back in one copy
@@ -485,9 +503,13 @@ def resolve_plans(*plans) -> None:
 
 
 def split_plan(ptr: torch.Tensor, nnz: int, threshold: int = DEFAULT_CHUNK, item_size: int = DEFAULT_ITEM,
-               resolve: bool = True, counts: Optional[torch.Tensor] = None) -> SplitPlan:
+               resolve: bool = True, counts: Optional[torch.Tensor] = None,
+               known: Optional[tuple] = None, host_copy: bool = True) -> SplitPlan:
     """Split plan of a CSR. ``counts`` (int32 [2], optional) receives the two plan counts on the device;
-    plans that share one buffer resolve with a single copy."""
+    plans that share one buffer resolve with a single copy. ``known`` = (items, split rows) when the
+    caller knows them from the row lengths' bounds: the plan then needs no read of the counts. Without
+    ``resolve`` the counts are copied to pinned host memory behind the plan's kernels (``host_copy``)
+    or left on the device only."""
     dev = ptr.device
     lib = N.load()
     n_rows = ptr.numel() - 1
@@ -501,9 +523,18 @@ def split_plan(ptr: torch.Tensor, nnz: int, threshold: int = DEFAULT_CHUNK, item
     ws = _workspace(_size_query("bf_split_plan_workspace_size", n_rows), dev)
     N.call("bf_split_plan", _p(ptr), n_rows, threshold, item_size, _p(nitems), _p(item_off), _p(item_row), item_cap,
            _p(heavy_rows), heavy_cap, _p(counts), _p(ws), ws.numel(), _stream(dev))
-    plan = SplitPlan(-1, -1, nitems, item_off, item_row, heavy_rows, counts)
-    if resolve:
+    plan = SplitPlan(-1, -1, nitems, item_off, item_row, heavy_rows, counts, item_cap, heavy_cap)
+    if known is not None:
+        plan.items, plan.heavy = int(known[0]), int(known[1])
+    elif resolve:
         resolve_plans(plan)
+    elif host_copy:
+        # the counts travel to pinned host memory behind the plan's kernels; reading them later waits
+        # only for this copy, typically long done while the stream runs on
+        plan.host_counts = torch.empty(2, dtype=torch.int32, pin_memory=True)
+        plan.host_counts.copy_(counts, non_blocking=True)
+        plan.ready = torch.cuda.Event()
+        plan.ready.record(torch.cuda.current_stream(dev))
     return plan
 
 
@@ -536,6 +567,13 @@ class AttentionIndex:
     _rkeys: Optional[ReverseKeys] = field(default=None, repr=False)   # from_table: sort keys, until used
     _sorted: Optional[ReverseKeys] = field(default=None, repr=False)  # sorted keys, until ke is needed
     _counts: Optional[torch.Tensor] = field(default=None, repr=False)  # both plans' device counts
+    # True: every plan leaves its counts on the device and the attention calls size their grids for the
+    # capacities (no host read at all between building the index and using it, e.g. for a caller that
+    # cannot synchronise). False: only plans with small capacities do (DEVICE_COUNTS_MAX_SLOTS); the
+    # others are read from their pinned copies when a call needs them
+    device_counts: bool = False
+    # (items, split rows) of the query-side plan when the row lengths fix them (from_table)
+    _q_known: Optional[tuple] = field(default=None, repr=False)
     _structs: dict = field(default_factory=dict, repr=False)          # C view per (backward, with ke)
 
     @property
@@ -546,10 +584,25 @@ class AttentionIndex:
     def device(self):
         return self.qptr.device
 
+    def resolve(self):
+        """Read the plans' counts into host ints (one device-to-host copy)."""
+        resolve_plans(self.qplan, self.kplan)
+        return self
+
+    def _host_copy(self) -> bool:
+        """Whether a new plan sends its counts to the host (else they stay on the device)."""
+        if self.device_counts:
+            return False
+        lib = N.load()
+        slots = int(lib.bf_split_item_capacity(self.nnz, self.chunk, self.item)) + \
+            int(lib.bf_split_row_capacity(self.nnz, self.chunk))
+        return slots > DEVICE_COUNTS_MAX_SLOTS
+
     def ensure_forward(self):
         if self.qplan is None:
-            self.qplan = split_plan(self.qptr, self.nnz, self.chunk, self.item)
-        resolve_plans(self.qplan)
+            self.qplan = split_plan(self.qptr, self.nnz, self.chunk, self.item, resolve=False,
+                                    counts=self._plan_counts(0), known=self._q_known,
+                                    host_copy=self._host_copy())
         return self
 
     def _plan_counts(self, side: int) -> torch.Tensor:
@@ -561,7 +614,8 @@ class AttentionIndex:
     def ensure_backward(self):
         if self.qplan is None:
             self.qplan = split_plan(self.qptr, self.nnz, self.chunk, self.item, resolve=False,
-                                    counts=self._plan_counts(0))
+                                    counts=self._plan_counts(0), known=self._q_known,
+                                    host_copy=self._host_copy())
         if self.kptr is None:
             if self._rkeys is not None and self._rkeys.q_bits + self._rkeys.slot_bits + _bits_for(self.n_kv) <= 64:
                 self.kptr, self.kq, _, self._sorted = reverse_index_packed(self._rkeys, self.qptr, self.n_kv,
@@ -571,10 +625,9 @@ class AttentionIndex:
                 self.kptr, self.kq, self.ke = reverse_index(self.qptr, self.kv, self.n_kv)
         if self.kplan is None:
             self.kplan = split_plan(self.kptr, self.nnz, self.chunk, self.item, resolve=False,
-                                    counts=self._plan_counts(1))
+                                    counts=self._plan_counts(1), host_copy=self._host_copy())
         if self.korder is None:
             self.korder, self.kspans = row_order(self.kptr, spans=True)
-        resolve_plans(self.qplan, self.kplan)      # both plans' counts in one read
         return self
 
     def ensure_entries(self):
@@ -616,7 +669,12 @@ class AttentionIndex:
         s.qptr, s.kv = self.qptr.data_ptr(), self.kv.data_ptr() if self.nnz else None
         s.chunk, s.item = self.chunk, self.item
         qp = self.qplan
-        s.q_items, s.q_heavy = qp.items, qp.heavy
+        # plans with a pinned copy of their counts take them from it; the others stay pending, their
+        # capacities size the grids and the kernels read the counts from the device
+        resolve_plans(*[p for p in (qp, self.kplan if backward else None) if p is not None and p.ready is not None])
+        on_device = qp.pending or (backward and self.kplan.pending)
+        s.q_items, s.q_heavy = (qp.item_cap, qp.heavy_cap) if on_device else (qp.items, qp.heavy)
+        s.plan_counts = self._counts.data_ptr() if on_device else None
         s.q_nitems, s.q_item_off, s.q_item_row, s.q_heavy_rows = (
             qp.nitems.data_ptr(), qp.item_off.data_ptr(), qp.item_row.data_ptr(), qp.heavy_rows.data_ptr())
         if backward:
@@ -624,7 +682,7 @@ class AttentionIndex:
             s.kptr = self.kptr.data_ptr()
             s.kq = self.kq.data_ptr() if self.nnz else None
             s.ke = self.ke.data_ptr() if (self.nnz and self.ke is not None) else None
-            s.k_items, s.k_heavy = kp.items, kp.heavy
+            s.k_items, s.k_heavy = (kp.item_cap, kp.heavy_cap) if on_device else (kp.items, kp.heavy)
             s.k_nitems, s.k_item_off, s.k_item_row, s.k_heavy_rows = (
                 kp.nitems.data_ptr(), kp.item_off.data_ptr(), kp.item_row.data_ptr(), kp.heavy_rows.data_ptr())
             s.k_order = self.korder.data_ptr() if self.n_kv > 0 else None
@@ -656,9 +714,17 @@ class AttentionIndex:
                 raise ValueError(f"table ids must lie in [0, {n_kv - shift}) (got [{stats[2]}, {stats[3]}])")
         qptr, kv, rk = table_to_csr(table, row_len, global_token, with_keys=True)
         n_q = qptr.numel() - 1
+        # A table row holds at most `width` entries (+ key 0 with the token), so when that is within
+        # `chunk` only the token row (every key, n_rows entries) can be split: the query plan's counts
+        # follow from the sizes, with no read of the device.
+        known = None
+        if table.shape[1] + (1 if global_token else 0) <= chunk:
+            n_rows = table.shape[0]
+            split = bool(global_token) and n_rows > chunk
+            known = (min(-(-n_rows // item), N.BF_MAX_ITEMS_PER_ROW) if split else 0, 1 if split else 0)
         # the token fill puts key 0 first in every row t >= 1 and shifts the table's own ids past it
         return cls(n_q=n_q, n_kv=n_kv, qptr=qptr, kv=kv, chunk=chunk, item=item, _rkeys=rk,
-                   token_column=bool(global_token))
+                   token_column=bool(global_token), _q_known=known)
 
     @classmethod
     def from_coo(cls, edge_index, n_q: int, n_kv: Optional[int] = None, chunk: int = DEFAULT_CHUNK,

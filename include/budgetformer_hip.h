@@ -365,6 +365,14 @@ typedef struct bf_attn_index {
   const uint64_t* k_spans;      /* [n_kv] or NULL: bf_row_order's spans of k_order (needs
                                    k_order); the dk/dv pass then reads each row's entry
                                    range from its slot instead of from kptr            */
+  const int32_t* plan_counts;   /* NULL: q_items, q_heavy, k_items, k_heavy above are the
+                                   plans' counts. Else a device int32 [4] holding them
+                                   (bf_split_plan's counts, query side then key side),
+                                   and the four fields above are upper bounds — the
+                                   capacities the plans were built with — which size the
+                                   grids and the scratch; workgroups past the true counts
+                                   exit. No host read is then needed between building
+                                   an index and running attention on it.            */
 } bf_attn_index;
 
 /* float32 scratch the attention calls need for split rows (and, with

@@ -40,6 +40,11 @@ def test_argument_errors_surface_as_exceptions():
                None)
 
 
+def test_python_constants_match_the_header():
+    text = open(N._HEADER).read()
+    assert int(re.search(r"#define BF_MAX_ITEMS_PER_ROW (\d+)", text).group(1)) == N.BF_MAX_ITEMS_PER_ROW
+
+
 def test_split_capacity_bound():
     """Capacities bound every row-length distribution (brute force over small cases)."""
     import itertools

@@ -85,6 +85,7 @@ def test_fp32_global_token_split_rows(hip_device, chunk, item, token_column):
     idx.token_column = token_column
     out, dq, dk, dv, _ = _run(hip_device, q, k, v, idx, dout)
     ro, rZ, rdq, rdk, rdv, _ = _oracle(q, k, v, ei, dout)
+    idx.resolve()
     assert idx.qplan.items > 0 and idx.kplan.items > 0 and idx.qplan.heavy > 0   # split paths exercised
     for got, ref in ((out, ro), (dq, rdq), (dk, rdk), (dv, rdv)):
         assert _rel_err(got, ref) < 1e-5
@@ -102,7 +103,7 @@ def test_bf16_split_rows_single_and_multi_item(hip_device, chunk, item, token_co
     ei = torch.cat([ei, torch.stack([ar, torch.zeros_like(ar)]), torch.stack([torch.zeros_like(ar), ar])], 1)
     idx = AttentionIndex.from_coo(ei.to(hip_device), S, chunk=chunk, item=item)
     idx.token_column = token_column
-    idx.ensure_backward()
+    idx.ensure_backward().resolve()
     for plan in (idx.qplan, idx.kplan):
         n = plan.nitems.cpu()
         heavy = plan.heavy_rows[: plan.heavy].cpu().long()
@@ -189,6 +190,9 @@ def test_token_column_terms_summed_by_the_dq_pass(hip_device, dtype, chunk, item
         factor = ((torch.rand(idx.nnz, H, generator=g) >= 0.25).float() / 0.75) if dtype == torch.float32 else None
         runs.append(_run(hip_device, q, k, v, idx, dout, bias_e=bias_e, factor_e=factor))
     (out_f, dq_f, dk_f, dv_f, db_f), (out_g, dq_g, dk_g, dv_g, db_g) = runs
+    if width + 1 <= chunk:        # the query plan's counts came from the sizes: they equal the device's
+        assert idx._q_known is not None
+        assert (idx.qplan.items, idx.qplan.heavy) == tuple(idx._counts[:2].tolist())
     assert torch.equal(out_f, out_g) and torch.equal(dq_f, dq_g)
     assert (db_f is None and db_g is None) or torch.equal(db_f, db_g)
     assert torch.equal(dk_f[1:], dk_g[1:]) and torch.equal(dv_f[1:], dv_g[1:])
@@ -200,6 +204,35 @@ def test_token_column_terms_summed_by_the_dq_pass(hip_device, dtype, chunk, item
         assert _rel_err(got, ref) < tol
     if db_f is not None:
         assert _rel_err(db_f, rdb) < tol
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_device_plan_counts_equal_host_plan_counts(hip_device, dtype, monkeypatch):
+    """With the plans' counts left on the device the grids are sized for the capacities and the kernels
+    read the counts themselves; the result is the same bit for bit as with host counts (split rows on
+    both sides, the token column, a bias and a factor)."""
+    from budgetformer_amd import hip_ops
+    from budgetformer_amd.hip_ops import AttentionIndex
+    S, H, hn = 700, 8, 16
+    q, k, v, ei, dout = _inputs(S, H, hn, 5000, seed=23, dtype=dtype, mult=1.2)
+    ei = ei[:, (ei[0] > 0) & (ei[1] > 0)]
+    ar = torch.arange(1, S)
+    ei = torch.cat([ei, torch.stack([ar, torch.zeros_like(ar)]), torch.stack([torch.zeros_like(ar), ar])], 1)
+    runs = []
+    for on_device in (True, False):
+        # host counts: every plan sends its counts to pinned host memory, however small
+        monkeypatch.setattr(hip_ops, "DEVICE_COUNTS_MAX_SLOTS", 1 << 15 if on_device else -1)
+        idx = AttentionIndex.from_coo(ei.to(hip_device), S, chunk=6, item=9)
+        idx.token_column, idx.device_counts = True, on_device
+        g = torch.Generator().manual_seed(2)
+        bias_e = torch.randn(idx.nnz, H, generator=g) if dtype == torch.float32 else None
+        factor = (torch.rand(idx.nnz, H, generator=g) >= 0.3).float() / 0.7 if dtype == torch.float32 else None
+        runs.append(_run(hip_device, q, k, v, idx, dout, bias_e=bias_e, factor_e=factor))
+        assert idx.qplan.pending == on_device and idx.kplan.pending == on_device
+        idx.resolve()
+        assert idx.qplan.items > 0 and idx.kplan.items > 0 and idx.qplan.heavy > 0 and idx.kplan.heavy > 0
+    for a, b in zip(*runs):
+        assert (a is None and b is None) or torch.equal(a, b)
 
 
 def test_fp32_gps_dropout_factor(hip_device):
