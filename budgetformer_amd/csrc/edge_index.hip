@@ -382,7 +382,7 @@ extern "C" int bf_scan_workspace_size(int64_t n, size_t* bytes) {
 
 extern "C" int bf_table_csr_ptr(const int32_t* row_len, int64_t n_rows, int32_t global_token, int64_t* qptr,
                                 int64_t* nnz_host, void* workspace, size_t workspace_bytes, void* stream) {
-  BF_CHECK_ARG(qptr && nnz_host && n_rows >= 0 && (row_len || n_rows == 0), "table_csr_ptr: bad arguments");
+  BF_CHECK_ARG(qptr && n_rows >= 0 && (row_len || n_rows == 0), "table_csr_ptr: bad arguments");
   const int64_t n_q = n_rows + (global_token ? 1 : 0);
   size_t need = 0;
   bf_scan_workspace_size(n_q, &need);
@@ -398,6 +398,7 @@ extern "C" int bf_table_csr_ptr(const int32_t* row_len, int64_t n_rows, int32_t 
     BF_CHECK_LAUNCH();
     BF_CHECK_HIP(hipcub::DeviceScan::InclusiveSum(temp, temp_bytes, lens, qptr + 1, int(n_q), st));
   }
+  if (!nnz_host) return BF_OK;   // the caller reads qptr[n_q] itself, when it needs it
   int64_t h = 0;
   BF_CHECK_HIP(hipMemcpyAsync(&h, qptr + n_q, sizeof(h), hipMemcpyDeviceToHost, st));
   BF_CHECK_HIP(hipStreamSynchronize(st));

@@ -341,24 +341,36 @@ class ReverseKeys:
     global_token: bool
 
 
-def table_to_csr(table: torch.Tensor, row_len: torch.Tensor, global_token: bool = False, with_keys: bool = False):
-    """Query-major table -> (qptr [n_q+1] int64, kv [nnz] int32), plus the reverse-index sort keys
-    (``ReverseKeys``, or None when the query and slot fields need more than 33 bits) with ``with_keys``."""
+def table_qptr(table: torch.Tensor, row_len: torch.Tensor, global_token: bool = False) -> torch.Tensor:
+    """qptr [n_q+1] int64 of a query-major table (bf_table_csr_ptr without the host read of nnz)."""
     dev = table.device
     _require(table, "table", torch.int32)
     _require(row_len, "row_len", torch.int32, dev)
-    n_rows, width = table.shape
+    n_rows = table.shape[0]
     n_q = n_rows + (1 if global_token else 0)
     ws = _workspace(_size_query("bf_scan_workspace_size", n_q), dev)
     qptr = torch.empty(n_q + 1, dtype=torch.int64, device=dev)
-    nnz = C.c_int64(0)
-    N.call("bf_table_csr_ptr", _p(row_len), n_rows, int(global_token), _p(qptr), C.byref(nnz), _p(ws), ws.numel(),
+    N.call("bf_table_csr_ptr", _p(row_len), n_rows, int(global_token), _p(qptr), None, _p(ws), ws.numel(),
            _stream(dev))
-    kv = torch.empty(max(nnz.value, 1), dtype=torch.int32, device=dev)[: nnz.value]
+    return qptr
+
+
+def table_to_csr(table: torch.Tensor, row_len: torch.Tensor, global_token: bool = False, with_keys: bool = False,
+                 qptr: Optional[torch.Tensor] = None):
+    """Query-major table -> (qptr [n_q+1] int64, kv [nnz] int32), plus the reverse-index sort keys
+    (``ReverseKeys``, or None when the query and slot fields need more than 33 bits) with ``with_keys``.
+    ``qptr`` from ``table_qptr`` saves the scan; nnz is read from it (one host read)."""
+    dev = table.device
+    if qptr is None:
+        qptr = table_qptr(table, row_len, global_token)
+    n_rows, width = table.shape
+    n_q = n_rows + (1 if global_token else 0)
+    nnz = int(qptr[n_q].item())
+    kv = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)[:nnz]
     rk = None
     q_bits, slot_bits = _bits_for(n_q), _bits_for(width)
     if with_keys and q_bits + slot_bits <= 33:
-        rk = ReverseKeys(torch.empty(max(nnz.value, 1), dtype=torch.int64, device=dev)[: nnz.value], q_bits,
+        rk = ReverseKeys(torch.empty(max(nnz, 1), dtype=torch.int64, device=dev)[:nnz], q_bits,
                          slot_bits, bool(global_token))
     N.call("bf_table_to_csr", _p(table), _p(row_len), n_rows, width, int(global_token), _p(qptr), _p(kv),
            _p(rk.keys) if rk is not None else None, q_bits, slot_bits, _stream(dev))
@@ -712,19 +724,25 @@ class AttentionIndex:
                 raise ValueError(f"row_len must lie in [0, {width}] (got [{stats[0]}, {stats[1]}])")
             if stats[1] > 0 and (stats[2] < 0 or stats[3] + shift >= n_kv):
                 raise ValueError(f"table ids must lie in [0, {n_kv - shift}) (got [{stats[2]}, {stats[3]}])")
-        qptr, kv, rk = table_to_csr(table, row_len, global_token, with_keys=True)
-        n_q = qptr.numel() - 1
         # A table row holds at most `width` entries (+ key 0 with the token), so when that is within
         # `chunk` only the token row (every key, n_rows entries) can be split: the query plan's counts
         # follow from the sizes, with no read of the device.
+        n_rows, width = table.shape
         known = None
-        if table.shape[1] + (1 if global_token else 0) <= chunk:
-            n_rows = table.shape[0]
+        if width + (1 if global_token else 0) <= chunk:
             split = bool(global_token) and n_rows > chunk
             known = (min(-(-n_rows // item), N.BF_MAX_ITEMS_PER_ROW) if split else 0, 1 if split else 0)
+        qptr = table_qptr(table, row_len, global_token)
         # the token fill puts key 0 first in every row t >= 1 and shifts the table's own ids past it
-        return cls(n_q=n_q, n_kv=n_kv, qptr=qptr, kv=kv, chunk=chunk, item=item, _rkeys=rk,
-                   token_column=bool(global_token), _q_known=known)
+        idx = cls(n_q=n_q_tab, n_kv=n_kv, qptr=qptr, kv=None, chunk=chunk, item=item,
+                  token_column=bool(global_token), _q_known=known)
+        if known is not None:
+            # the query plan needs only qptr: its launches go out before the host waits for nnz
+            bound = n_rows * width + (2 * n_rows if global_token else 0)
+            idx.qplan = split_plan(qptr, bound, chunk, item, resolve=False, counts=idx._plan_counts(0),
+                                   known=known)
+        qptr, idx.kv, idx._rkeys = table_to_csr(table, row_len, global_token, with_keys=True, qptr=qptr)
+        return idx
 
     @classmethod
     def from_coo(cls, edge_index, n_q: int, n_kv: Optional[int] = None, chunk: int = DEFAULT_CHUNK,

@@ -236,7 +236,8 @@ int bf_chung_lu(int64_t num_nodes, int64_t pairs, double exponent, double i0, do
  * every query t >= 1 also attends to kv 0; then n_q = n_rows + 1.
  * bf_table_csr_ptr writes qptr (a prefix sum of the row lengths) and returns
  * nnz = qptr[n_q] on the host (it synchronises the stream, so the caller can
- * size kv); bf_table_to_csr then fills kv, and, when rkey is not NULL,
+ * size kv; with nnz_host NULL it only enqueues the scan and the caller reads
+ * qptr[n_q] when it needs it); bf_table_to_csr then fills kv, and, when rkey is not NULL,
  * rkey uint64 [nnz] = (id << (q_bits + slot_bits) | query << slot_bits | slot)
  * per entry, the sort keys bf_reverse_index_packed takes (slot = position in
  * the query's row; the token row's entries carry slot 0). Needs
