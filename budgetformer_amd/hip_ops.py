@@ -16,10 +16,6 @@ import torch
 from . import _native as N
 
 DEFAULT_CHUNK = 128     # rows longer than this go through the split plan
-# A plan whose capacities (items + split rows) stay within this leaves its counts on the device: the
-# attention grids are then sized for the capacities and their extra workgroups exit at once, which
-# costs less than reading the counts back. Larger plans send their counts to pinned host memory.
-DEVICE_COUNTS_MAX_SLOTS = 1 << 15
 DEFAULT_ITEM = 768      # entries per split item (one workgroup), before balancing
 HUB_THRESHOLD = 1024    # in-degree above which a query's real-edge top-k uses a whole workgroup
 LIGHT_MAX = 32          # in-degree up to which a query's real-edge top-k runs in one thread (k <= 16)
@@ -579,10 +575,10 @@ class AttentionIndex:
     _rkeys: Optional[ReverseKeys] = field(default=None, repr=False)   # from_table: sort keys, until used
     _sorted: Optional[ReverseKeys] = field(default=None, repr=False)  # sorted keys, until ke is needed
     _counts: Optional[torch.Tensor] = field(default=None, repr=False)  # both plans' device counts
-    # True: every plan leaves its counts on the device and the attention calls size their grids for the
+    # True: the plans leave their counts on the device and the attention calls size their grids for the
     # capacities (no host read at all between building the index and using it, e.g. for a caller that
-    # cannot synchronise). False: only plans with small capacities do (DEVICE_COUNTS_MAX_SLOTS); the
-    # others are read from their pinned copies when a call needs them
+    # cannot synchronise). False: a plan copies its counts to pinned host memory behind its kernels and
+    # a call reads them when it is launched, by which time the copy has landed
     device_counts: bool = False
     # (items, split rows) of the query-side plan when the row lengths fix them (from_table)
     _q_known: Optional[tuple] = field(default=None, repr=False)
@@ -602,13 +598,8 @@ class AttentionIndex:
         return self
 
     def _host_copy(self) -> bool:
-        """Whether a new plan sends its counts to the host (else they stay on the device)."""
-        if self.device_counts:
-            return False
-        lib = N.load()
-        slots = int(lib.bf_split_item_capacity(self.nnz, self.chunk, self.item)) + \
-            int(lib.bf_split_row_capacity(self.nnz, self.chunk))
-        return slots > DEVICE_COUNTS_MAX_SLOTS
+        """Whether a new plan sends its counts to pinned host memory (else they stay on the device)."""
+        return not self.device_counts
 
     def ensure_forward(self):
         if self.qplan is None:

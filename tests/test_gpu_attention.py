@@ -207,11 +207,10 @@ def test_token_column_terms_summed_by_the_dq_pass(hip_device, dtype, chunk, item
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_device_plan_counts_equal_host_plan_counts(hip_device, dtype, monkeypatch):
+def test_device_plan_counts_equal_host_plan_counts(hip_device, dtype):
     """With the plans' counts left on the device the grids are sized for the capacities and the kernels
     read the counts themselves; the result is the same bit for bit as with host counts (split rows on
     both sides, the token column, a bias and a factor)."""
-    from budgetformer_amd import hip_ops
     from budgetformer_amd.hip_ops import AttentionIndex
     S, H, hn = 700, 8, 16
     q, k, v, ei, dout = _inputs(S, H, hn, 5000, seed=23, dtype=dtype, mult=1.2)
@@ -220,8 +219,6 @@ def test_device_plan_counts_equal_host_plan_counts(hip_device, dtype, monkeypatc
     ei = torch.cat([ei, torch.stack([ar, torch.zeros_like(ar)]), torch.stack([torch.zeros_like(ar), ar])], 1)
     runs = []
     for on_device in (True, False):
-        # host counts: every plan sends its counts to pinned host memory, however small
-        monkeypatch.setattr(hip_ops, "DEVICE_COUNTS_MAX_SLOTS", 1 << 15 if on_device else -1)
         idx = AttentionIndex.from_coo(ei.to(hip_device), S, chunk=6, item=9)
         idx.token_column, idx.device_counts = True, on_device
         g = torch.Generator().manual_seed(2)
