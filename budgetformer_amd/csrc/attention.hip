@@ -686,59 +686,76 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
   constexpr int kUnroll = Unroll<T>::kv;
   const int lph = 1 << sh.lph_log2;
   const bool need_e = bias != nullptr || factor != nullptr;
-  for (int64_t i0 = beg; i0 < end; i0 += kUnroll) {
-    int t[kUnroll];
-    bool ok[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      ok[u] = i0 + u < end;
-      t[u] = ok[u] ? kq[i0 + u] : 0;
-    }
-    typename Elem<T>::Raw qr[kUnroll], gr[kUnroll];
-    float2 rs[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      if (ok[u] && g.act) {
-        qr[u] = gather_row<T, NT>(q, t[u], sh.D, g.col0);
-        gr[u] = gather_row<T, NT>(dout, t[u], sh.D, g.col0);
-        rs[u] = rstat[int64_t(t[u]) * sh.H + g.head];
-      } else {
-        qr[u] = gr[u] = Elem<T>::zero_raw();
-        rs[u] = make_float2(0.f, 0.f);
-      }
-    }
-    float d[kUnroll], w[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      d[u] = Elem<T>::dot(qr[u], krow, 0.f);
-      w[u] = Elem<T>::dot(gr[u], vrow, 0.f);
-    }
-    for (int o = 1; o < lph; o <<= 1) {
+  // bf16: the query ids of a chunk of entries come in one coalesced load, one id per lane of the
+  // group, and each iteration takes its ids by lane shuffle, so the gathers wait for one id load per
+  // chunk instead of one per iteration (chunks are a whole number of iterations). float32 loads them
+  // per iteration: the id register would cost it a wave per SIMD.
+  constexpr bool kChunkIds = sizeof(T) == 2;
+  const int lpr = 1 << sh.lpr_log2;
+  const int64_t chunk_len = kChunkIds ? (lpr / kUnroll) * kUnroll : end - beg;
+  for (int64_t c0 = beg; c0 < end; c0 += chunk_len) {
+    const int64_t c1 = c0 + chunk_len < end ? c0 + chunk_len : end;
+    int ids = 0;
+    if constexpr (kChunkIds) ids = (g.g_lane < chunk_len && c0 + g.g_lane < c1) ? kq[c0 + g.g_lane] : 0;
+    for (int64_t i0 = c0; i0 < c1; i0 += kUnroll) {
+      int t[kUnroll];
+      bool ok[kUnroll];
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
-        d[u] += __shfl_xor(d[u], o, 64);
-        w[u] += __shfl_xor(w[u], o, 64);
+        ok[u] = i0 + u < c1;
+        if constexpr (kChunkIds) {
+          const int src = __shfl(ids, int(i0 - c0) + u, lpr);   // every lane of the group takes part
+          t[u] = ok[u] ? src : 0;
+        } else {
+          t[u] = ok[u] ? kq[i0 + u] : 0;
+        }
       }
-    }
+      typename Elem<T>::Raw qr[kUnroll], gr[kUnroll];
+      float2 rs[kUnroll];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      if (!ok[u]) continue;
-      const int64_t e = need_e ? int64_t(ke[i0 + u]) : 0;
-      const float apre = d[u] * sh.inv_scale;
-      float a = fminf(fmaxf(apre, -kClamp), kClamp);
-      if (bias) a += bias[e * sh.H + g.head];
-      const float p = __expf(a);   // a is clamped to [-5, 5] (+ bias): exp2-based form is within 2 ulp
-      const float f = factor ? factor[e * sh.H + g.head] : 1.f;
-      const float gb = fmaf(f * w[u], rs[u].x, -rs[u].y) * p;   // rs = {1/D', Delta/D'}
-      const float gs = (apre >= -kClamp && apre <= kClamp) ? gb * sh.inv_scale : 0.f;
-      const float pf = p * f * rs[u].x;
-      float qq[V], gg[V];
-      Elem<T>::unpack(qr[u], qq);
-      Elem<T>::unpack(gr[u], gg);
+      for (int u = 0; u < kUnroll; ++u) {
+        if (ok[u] && g.act) {
+          qr[u] = gather_row<T, NT>(q, t[u], sh.D, g.col0);
+          gr[u] = gather_row<T, NT>(dout, t[u], sh.D, g.col0);
+          rs[u] = rstat[int64_t(t[u]) * sh.H + g.head];
+        } else {
+          qr[u] = gr[u] = Elem<T>::zero_raw();
+          rs[u] = make_float2(0.f, 0.f);
+        }
+      }
+      float d[kUnroll], w[kUnroll];
 #pragma unroll
-      for (int i = 0; i < V; ++i) {
-        dv[i] = fmaf(pf, gg[i], dv[i]);
-        dk[i] = fmaf(gs, qq[i], dk[i]);
+      for (int u = 0; u < kUnroll; ++u) {
+        d[u] = Elem<T>::dot(qr[u], krow, 0.f);
+        w[u] = Elem<T>::dot(gr[u], vrow, 0.f);
+      }
+      for (int o = 1; o < lph; o <<= 1) {
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+          d[u] += __shfl_xor(d[u], o, 64);
+          w[u] += __shfl_xor(w[u], o, 64);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        if (!ok[u]) continue;
+        const int64_t e = need_e ? int64_t(ke[i0 + u]) : 0;
+        const float apre = d[u] * sh.inv_scale;
+        float a = fminf(fmaxf(apre, -kClamp), kClamp);
+        if (bias) a += bias[e * sh.H + g.head];
+        const float p = __expf(a);   // a is clamped to [-5, 5] (+ bias): exp2-based form is within 2 ulp
+        const float f = factor ? factor[e * sh.H + g.head] : 1.f;
+        const float gb = fmaf(f * w[u], rs[u].x, -rs[u].y) * p;   // rs = {1/D', Delta/D'}
+        const float gs = (apre >= -kClamp && apre <= kClamp) ? gb * sh.inv_scale : 0.f;
+        const float pf = p * f * rs[u].x;
+        float qq[V], gg[V];
+        Elem<T>::unpack(qr[u], qq);
+        Elem<T>::unpack(gr[u], gg);
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+          dv[i] = fmaf(pf, gg[i], dv[i]);
+          dk[i] = fmaf(gs, qq[i], dk[i]);
+        }
       }
     }
   }
