@@ -94,6 +94,37 @@ __device__ __forceinline__ typename Elem<T>::Raw load_row_raw_nt(const T* base, 
 }
 
 // ------------------------------------------------------------------ forward
+// Entry ids of a row walked kUnroll at a time. bf16: a chunk of them comes in
+// one coalesced load, one id per lane of the group, and each iteration takes
+// its ids by lane shuffle, so the gathers wait for one id load per chunk
+// instead of one per iteration (chunks are a whole number of iterations).
+// float32: loaded per iteration (the id register would cost a wave per SIMD).
+template <typename T, int kUnroll>
+struct ChunkIds {
+  static constexpr bool kChunk = sizeof(T) == 2;
+  int lpr, len;
+  int64_t c0;
+  int ids = 0;
+  __device__ __forceinline__ ChunkIds(const Shape& sh, int64_t beg)
+      : lpr(1 << sh.lpr_log2), len(((1 << sh.lpr_log2) / kUnroll) * kUnroll), c0(beg - len) {}
+  // at the start of each chunk (uniform over the group): load its ids
+  __device__ __forceinline__ void next(const int32_t* __restrict__ idx, int64_t e0, int64_t end, const GroupPos& g) {
+    if constexpr (kChunk) {
+      if (e0 - c0 == len) {
+        c0 = e0;
+        ids = (g.g_lane < len && c0 + g.g_lane < end) ? idx[c0 + g.g_lane] : 0;
+      }
+    }
+  }
+  // id of entry e0 + u (every lane of the group calls it)
+  __device__ __forceinline__ int get(const int32_t* __restrict__ idx, int64_t e0, int u, bool ok) const {
+    if constexpr (kChunk) {
+      return __shfl(ids, int(e0 - c0) + u, lpr);
+    } else {
+      return ok ? idx[e0 + u] : 0;
+    }
+  }
+};
 // Accumulates sum_e p*f*v (acc) and sum_e p (z) over entries [beg, end) of one row.
 template <typename T>
 __device__ __forceinline__ void fwd_segment(const T* __restrict__ k, const T* __restrict__ v,
@@ -106,13 +137,16 @@ __device__ __forceinline__ void fwd_segment(const T* __restrict__ k, const T* __
   constexpr int V = Elem<T>::kPerVec;
   constexpr int kUnroll = Unroll<T>::fwd;
   const int lph = 1 << sh.lph_log2;
+  ChunkIds<T, kUnroll> ids(sh, beg);
   for (int64_t e0 = beg; e0 < end; e0 += kUnroll) {
     int s[kUnroll];
     bool ok[kUnroll];
+    ids.next(kv, e0, end, g);
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       ok[u] = e0 + u < end;
-      s[u] = ok[u] ? kv[e0 + u] : 0;
+      const int id = ids.get(kv, e0, u, ok[u]);
+      s[u] = ok[u] ? id : 0;
     }
     typename Elem<T>::Raw kr[kUnroll], vr[kUnroll];
 #pragma unroll
@@ -417,13 +451,16 @@ __device__ __forceinline__ void dq_segment(const T* __restrict__ k, const T* __r
   const int lph = 1 << sh.lph_log2;
   const float inv_dprime = 1.0f / rg.dprime;
   const float gz = -rg.delta * inv_dprime;
+  ChunkIds<T, kUnroll> ids(sh, beg);
   for (int64_t e0 = beg; e0 < end; e0 += kUnroll) {
     int s[kUnroll];
     bool ok[kUnroll];
+    ids.next(kv, e0, end, g);
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       ok[u] = e0 + u < end;
-      s[u] = ok[u] ? kv[e0 + u] : 0;
+      const int id = ids.get(kv, e0, u, ok[u]);
+      s[u] = ok[u] ? id : 0;
     }
     typename Elem<T>::Raw kr[kUnroll], vr[kUnroll];
 #pragma unroll
@@ -686,76 +723,62 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
   constexpr int kUnroll = Unroll<T>::kv;
   const int lph = 1 << sh.lph_log2;
   const bool need_e = bias != nullptr || factor != nullptr;
-  // bf16: the query ids of a chunk of entries come in one coalesced load, one id per lane of the
-  // group, and each iteration takes its ids by lane shuffle, so the gathers wait for one id load per
-  // chunk instead of one per iteration (chunks are a whole number of iterations). float32 loads them
-  // per iteration: the id register would cost it a wave per SIMD.
-  constexpr bool kChunkIds = sizeof(T) == 2;
-  const int lpr = 1 << sh.lpr_log2;
-  const int64_t chunk_len = kChunkIds ? (lpr / kUnroll) * kUnroll : end - beg;
-  for (int64_t c0 = beg; c0 < end; c0 += chunk_len) {
-    const int64_t c1 = c0 + chunk_len < end ? c0 + chunk_len : end;
-    int ids = 0;
-    if constexpr (kChunkIds) ids = (g.g_lane < chunk_len && c0 + g.g_lane < c1) ? kq[c0 + g.g_lane] : 0;
-    for (int64_t i0 = c0; i0 < c1; i0 += kUnroll) {
-      int t[kUnroll];
-      bool ok[kUnroll];
+  ChunkIds<T, kUnroll> ids(sh, beg);
+  for (int64_t i0 = beg; i0 < end; i0 += kUnroll) {
+    int t[kUnroll];
+    bool ok[kUnroll];
+    ids.next(kq, i0, end, g);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      ok[u] = i0 + u < end;
+      const int id = ids.get(kq, i0, u, ok[u]);
+      t[u] = ok[u] ? id : 0;
+    }
+    typename Elem<T>::Raw qr[kUnroll], gr[kUnroll];
+    float2 rs[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      if (ok[u] && g.act) {
+        qr[u] = gather_row<T, NT>(q, t[u], sh.D, g.col0);
+        gr[u] = gather_row<T, NT>(dout, t[u], sh.D, g.col0);
+        rs[u] = rstat[int64_t(t[u]) * sh.H + g.head];
+      } else {
+        qr[u] = gr[u] = Elem<T>::zero_raw();
+        rs[u] = make_float2(0.f, 0.f);
+      }
+    }
+    float d[kUnroll], w[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      d[u] = Elem<T>::dot(qr[u], krow, 0.f);
+      w[u] = Elem<T>::dot(gr[u], vrow, 0.f);
+    }
+    for (int o = 1; o < lph; o <<= 1) {
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
-        ok[u] = i0 + u < c1;
-        if constexpr (kChunkIds) {
-          const int src = __shfl(ids, int(i0 - c0) + u, lpr);   // every lane of the group takes part
-          t[u] = ok[u] ? src : 0;
-        } else {
-          t[u] = ok[u] ? kq[i0 + u] : 0;
-        }
+        d[u] += __shfl_xor(d[u], o, 64);
+        w[u] += __shfl_xor(w[u], o, 64);
       }
-      typename Elem<T>::Raw qr[kUnroll], gr[kUnroll];
-      float2 rs[kUnroll];
+    }
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        if (ok[u] && g.act) {
-          qr[u] = gather_row<T, NT>(q, t[u], sh.D, g.col0);
-          gr[u] = gather_row<T, NT>(dout, t[u], sh.D, g.col0);
-          rs[u] = rstat[int64_t(t[u]) * sh.H + g.head];
-        } else {
-          qr[u] = gr[u] = Elem<T>::zero_raw();
-          rs[u] = make_float2(0.f, 0.f);
-        }
-      }
-      float d[kUnroll], w[kUnroll];
+    for (int u = 0; u < kUnroll; ++u) {
+      if (!ok[u]) continue;
+      const int64_t e = need_e ? int64_t(ke[i0 + u]) : 0;
+      const float apre = d[u] * sh.inv_scale;
+      float a = fminf(fmaxf(apre, -kClamp), kClamp);
+      if (bias) a += bias[e * sh.H + g.head];
+      const float p = __expf(a);   // a is clamped to [-5, 5] (+ bias): exp2-based form is within 2 ulp
+      const float f = factor ? factor[e * sh.H + g.head] : 1.f;
+      const float gb = fmaf(f * w[u], rs[u].x, -rs[u].y) * p;   // rs = {1/D', Delta/D'}
+      const float gs = (apre >= -kClamp && apre <= kClamp) ? gb * sh.inv_scale : 0.f;
+      const float pf = p * f * rs[u].x;
+      float qq[V], gg[V];
+      Elem<T>::unpack(qr[u], qq);
+      Elem<T>::unpack(gr[u], gg);
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        d[u] = Elem<T>::dot(qr[u], krow, 0.f);
-        w[u] = Elem<T>::dot(gr[u], vrow, 0.f);
-      }
-      for (int o = 1; o < lph; o <<= 1) {
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-          d[u] += __shfl_xor(d[u], o, 64);
-          w[u] += __shfl_xor(w[u], o, 64);
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        if (!ok[u]) continue;
-        const int64_t e = need_e ? int64_t(ke[i0 + u]) : 0;
-        const float apre = d[u] * sh.inv_scale;
-        float a = fminf(fmaxf(apre, -kClamp), kClamp);
-        if (bias) a += bias[e * sh.H + g.head];
-        const float p = __expf(a);   // a is clamped to [-5, 5] (+ bias): exp2-based form is within 2 ulp
-        const float f = factor ? factor[e * sh.H + g.head] : 1.f;
-        const float gb = fmaf(f * w[u], rs[u].x, -rs[u].y) * p;   // rs = {1/D', Delta/D'}
-        const float gs = (apre >= -kClamp && apre <= kClamp) ? gb * sh.inv_scale : 0.f;
-        const float pf = p * f * rs[u].x;
-        float qq[V], gg[V];
-        Elem<T>::unpack(qr[u], qq);
-        Elem<T>::unpack(gr[u], gg);
-#pragma unroll
-        for (int i = 0; i < V; ++i) {
-          dv[i] = fmaf(pf, gg[i], dv[i]);
-          dk[i] = fmaf(gs, qq[i], dk[i]);
-        }
+      for (int i = 0; i < V; ++i) {
+        dv[i] = fmaf(pf, gg[i], dv[i]);
+        dk[i] = fmaf(gs, qq[i], dk[i]);
       }
     }
   }
