@@ -805,7 +805,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
   // the true count exits at once (early in the dispatch, beside the running items).
   const int q_items = plan_counts ? plan_counts[0] : q_items_arg;
   // token-column records: the dq pass's q_items item workgroups, then its q_row_blocks row workgroups
-  // (whose records start at slot q_items_arg); record m of the n_token_rec is at token_slot(m)
+  // (whose records start at slot q_items_arg; sum_token_records maps record m to its slot)
   const int64_t n_token_rec = q_items + q_row_blocks;
   float ak[V], av[V];
   const int b = int(blockIdx.x);

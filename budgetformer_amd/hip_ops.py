@@ -675,8 +675,9 @@ class AttentionIndex:
         # plans with a pinned copy of their counts take them from it; the others stay pending, their
         # capacities size the grids and the kernels read the counts from the device
         resolve_plans(*[p for p in (qp, self.kplan if backward else None) if p is not None and p.ready is not None])
+        # (a plan whose counts are known passes them: the device copy then holds the same values)
         on_device = qp.pending or (backward and self.kplan.pending)
-        s.q_items, s.q_heavy = (qp.item_cap, qp.heavy_cap) if on_device else (qp.items, qp.heavy)
+        s.q_items, s.q_heavy = (qp.item_cap, qp.heavy_cap) if qp.pending else (qp.items, qp.heavy)
         s.plan_counts = self._counts.data_ptr() if on_device else None
         s.q_nitems, s.q_item_off, s.q_item_row, s.q_heavy_rows = (
             qp.nitems.data_ptr(), qp.item_off.data_ptr(), qp.item_row.data_ptr(), qp.heavy_rows.data_ptr())
@@ -685,7 +686,7 @@ class AttentionIndex:
             s.kptr = self.kptr.data_ptr()
             s.kq = self.kq.data_ptr() if self.nnz else None
             s.ke = self.ke.data_ptr() if (self.nnz and self.ke is not None) else None
-            s.k_items, s.k_heavy = (kp.item_cap, kp.heavy_cap) if on_device else (kp.items, kp.heavy)
+            s.k_items, s.k_heavy = (kp.item_cap, kp.heavy_cap) if kp.pending else (kp.items, kp.heavy)
             s.k_nitems, s.k_item_off, s.k_item_row, s.k_heavy_rows = (
                 kp.nitems.data_ptr(), kp.item_off.data_ptr(), kp.item_row.data_ptr(), kp.heavy_rows.data_ptr())
             s.k_order = self.korder.data_ptr() if self.n_kv > 0 else None

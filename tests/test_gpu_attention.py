@@ -168,7 +168,7 @@ def test_token_column_terms_summed_by_the_dq_pass(hip_device, dtype, chunk, item
     and every other key row equal bit for bit (the same arithmetic), key 0 within the parity bar
     (another summation order); both against the oracle. (chunk, item) = (5, 7) also splits the query
     rows, so key 0 opens item 0 of a split row; n = 60 leaves the token column shorter than `chunk`,
-    one group then sums every record."""
+    one group then sums every record. A third run leaves the split plans' counts on the device."""
     import numpy as np
     from budgetformer_amd.hip_ops import AttentionIndex
     rng = np.random.default_rng(n + chunk)
@@ -179,17 +179,20 @@ def test_token_column_terms_summed_by_the_dq_pass(hip_device, dtype, chunk, item
         table[r, :row_len[r]] = np.sort(rng.choice(n, row_len[r], replace=False))
     tab_d, len_d = torch.from_numpy(table).to(hip_device), torch.from_numpy(row_len).to(hip_device)
     runs = []
-    for token_column in (True, False):
+    for token_column, on_device in ((True, False), (False, False), (True, True)):
         idx = AttentionIndex.from_table(tab_d, len_d, global_token=True, chunk=chunk, item=item)
         assert idx.token_column
-        idx.token_column = token_column
+        idx.token_column, idx.device_counts = token_column, on_device
         S = idx.n_q
         q, k, v, _, dout = _inputs(S, H, hn, 1, seed=n, dtype=dtype, mult=1.3)
         g = torch.Generator().manual_seed(9)
         bias_e = torch.randn(idx.nnz, H, generator=g) if dtype == torch.float32 else None
         factor = ((torch.rand(idx.nnz, H, generator=g) >= 0.25).float() / 0.75) if dtype == torch.float32 else None
         runs.append(_run(hip_device, q, k, v, idx, dout, bias_e=bias_e, factor_e=factor))
-    (out_f, dq_f, dk_f, dv_f, db_f), (out_g, dq_g, dk_g, dv_g, db_g) = runs
+    (out_f, dq_f, dk_f, dv_f, db_f), (out_g, dq_g, dk_g, dv_g, db_g), on_dev = runs
+    # the key plan's counts left on the device (the query plan's known from the sizes): the same result
+    for a, b in zip(runs[0], on_dev):
+        assert (a is None and b is None) or torch.equal(a, b)
     if width + 1 <= chunk:        # the query plan's counts came from the sizes: they equal the device's
         assert idx._q_known is not None
         assert (idx.qplan.items, idx.qplan.heavy) == tuple(idx._counts[:2].tolist())
