@@ -33,9 +33,10 @@ size_t scan_temp_bytes_i64(int64_t n) {
 
 // ---------------------------------------------------------------- table -> CSR
 __global__ void row_lengths_kernel(const int32_t* __restrict__ row_len, int64_t n_rows, int token,
-                                   int64_t* __restrict__ lens) {
+                                   int64_t* __restrict__ lens, int64_t* __restrict__ qptr) {
   const int64_t n_q = n_rows + (token ? 1 : 0);
   const int64_t t = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (t == 0) qptr[0] = 0;     // the scan writes qptr[1..n_q]
   if (t >= n_q) return;
   int64_t len;
   if (token)
@@ -288,6 +289,25 @@ __global__ __launch_bounds__(kThreads) void order_scatter_kernel(const int64_t* 
   }
 }
 
+// The split plan of a CSR whose only row longer than the threshold is row 0,
+// cut into n_items items (0: no split row): what split_count / scan /
+// split_rows would write, in one pass and with no scan.
+__global__ void split_first_row_kernel(int64_t n_rows, int n_items, int32_t* __restrict__ nitems,
+                                       int32_t* __restrict__ item_off, int32_t* __restrict__ item_row,
+                                       int32_t* __restrict__ heavy_rows, int32_t* __restrict__ counts) {
+  const int64_t r = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (r < n_rows) {
+    nitems[r] = r == 0 ? n_items : 0;
+    item_off[r] = r == 0 ? 0 : n_items;
+  }
+  if (r < n_items) item_row[r] = 0;
+  if (r == 0) {
+    if (n_items) heavy_rows[0] = 0;
+    counts[0] = n_items;
+    counts[1] = n_items ? 1 : 0;
+  }
+}
+
 struct MaxOp {
   __device__ __forceinline__ int32_t operator()(int32_t a, int32_t b) const { return a > b ? a : b; }
 };
@@ -388,13 +408,13 @@ extern "C" int bf_table_csr_ptr(const int32_t* row_len, int64_t n_rows, int32_t 
   bf_scan_workspace_size(n_q, &need);
   BF_CHECK_ARG(workspace && workspace_bytes >= need, "table_csr_ptr: workspace %zu < %zu bytes", workspace_bytes, need);
   hipStream_t st = as_stream(stream);
-  BF_CHECK_HIP(hipMemsetAsync(qptr, 0, sizeof(int64_t), st));
+  if (n_q == 0) BF_CHECK_HIP(hipMemsetAsync(qptr, 0, sizeof(int64_t), st));
   if (n_q > 0) {
     auto* lens = static_cast<int64_t*>(workspace);
     void* temp = static_cast<char*>(workspace) + align_up(size_t(n_q) * sizeof(int64_t));
     size_t temp_bytes = scan_temp_bytes_i64(n_q);
     BF_LAUNCH("row_lengths_kernel", row_lengths_kernel, dim3(blocks_for(n_q)), dim3(kThreads), 0, st, row_len, n_rows,
-              int(global_token != 0), lens);
+              int(global_token != 0), lens, qptr);
     BF_CHECK_LAUNCH();
     BF_CHECK_HIP(hipcub::DeviceScan::InclusiveSum(temp, temp_bytes, lens, qptr + 1, int(n_q), st));
   }
@@ -638,6 +658,22 @@ extern "C" int bf_split_plan(const int64_t* ptr, int64_t n_rows, int32_t thresho
   BF_CHECK_HIP(hipcub::DeviceScan::ExclusiveSum(temp, temp_bytes, packed, packed_off, int(n_rows), st));
   BF_LAUNCH("split_rows_kernel", split_rows_kernel, dim3(blocks_for(n_rows)), dim3(kThreads), 0, st, nitems,
             packed_off, n_rows, item_cap, item_off, item_row, heavy_rows, heavy_cap, counts);
+  BF_CHECK_LAUNCH();
+  return BF_OK;
+}
+
+extern "C" int bf_split_plan_first_row(int64_t n_rows, int32_t n_items, int32_t* nitems, int32_t* item_off,
+                                       int32_t* item_row, int64_t item_cap, int32_t* heavy_rows, int64_t heavy_cap,
+                                       int32_t* counts, void* stream) {
+  BF_CHECK_ARG(n_rows >= 0 && n_rows < (int64_t(1) << 31) && n_items >= 0 && n_items <= BF_MAX_ITEMS_PER_ROW &&
+                   counts && (n_items == 0 || n_rows > 0),
+               "split_plan_first_row: bad arguments");
+  BF_CHECK_ARG(item_cap >= n_items && heavy_cap >= (n_items ? 1 : 0), "split_plan_first_row: capacity too small");
+  BF_CHECK_ARG(n_rows == 0 || (nitems && item_off), "split_plan_first_row: null tensor");
+  BF_CHECK_ARG(n_items == 0 || (item_row && heavy_rows), "split_plan_first_row: null tensor");
+  const int64_t threads = n_rows > 1 ? n_rows : 1;
+  BF_LAUNCH("split_first_row_kernel", split_first_row_kernel, dim3(blocks_for(threads)), dim3(kThreads), 0,
+            as_stream(stream), n_rows, n_items, nitems, item_off, item_row, heavy_rows, counts);
   BF_CHECK_LAUNCH();
   return BF_OK;
 }

@@ -510,6 +510,23 @@ def resolve_plans(*plans) -> None:
         p.items, p.heavy, p.counts = int(vals[2 * i]), int(vals[2 * i + 1]), None
 
 
+def split_plan_first_row(n_rows: int, n_items: int, nnz: int, threshold: int, item_size: int,
+                         counts: torch.Tensor) -> SplitPlan:
+    """Split plan of a CSR whose only row longer than ``threshold`` is row 0, cut into ``n_items`` items
+    (bf_split_plan_first_row): the arrays and counts ``split_plan`` would give, in one pass."""
+    dev = counts.device
+    lib = N.load()
+    item_cap = int(lib.bf_split_item_capacity(nnz, threshold, item_size))
+    heavy_cap = int(lib.bf_split_row_capacity(nnz, threshold))
+    r = max(n_rows, 1)
+    buf = torch.empty(2 * r + max(item_cap, 1) + max(heavy_cap, 1), dtype=torch.int32, device=dev)
+    nitems, item_off, item_row, heavy_rows = torch.split(buf, [r, r, max(item_cap, 1), max(heavy_cap, 1)])
+    N.call("bf_split_plan_first_row", n_rows, n_items, _p(nitems), _p(item_off), _p(item_row), item_cap,
+           _p(heavy_rows), heavy_cap, _p(counts), _stream(dev))
+    return SplitPlan(n_items, 1 if n_items else 0, nitems, item_off, item_row, heavy_rows, counts, item_cap,
+                     heavy_cap)
+
+
 def split_plan(ptr: torch.Tensor, nnz: int, threshold: int = DEFAULT_CHUNK, item_size: int = DEFAULT_ITEM,
                resolve: bool = True, counts: Optional[torch.Tensor] = None,
                known: Optional[tuple] = None, host_copy: bool = True) -> SplitPlan:
@@ -729,10 +746,10 @@ class AttentionIndex:
         idx = cls(n_q=n_q_tab, n_kv=n_kv, qptr=qptr, kv=None, chunk=chunk, item=item,
                   token_column=bool(global_token), _q_known=known)
         if known is not None:
-            # the query plan needs only qptr: its launches go out before the host waits for nnz
+            # only the token row can be split: its plan is written in one pass, before the host waits
+            # for nnz
             bound = n_rows * width + (2 * n_rows if global_token else 0)
-            idx.qplan = split_plan(qptr, bound, chunk, item, resolve=False, counts=idx._plan_counts(0),
-                                   known=known)
+            idx.qplan = split_plan_first_row(n_q_tab, known[0], bound, chunk, item, idx._plan_counts(0))
         qptr, idx.kv, idx._rkeys = table_to_csr(table, row_len, global_token, with_keys=True, qptr=qptr)
         return idx
 

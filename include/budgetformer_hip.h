@@ -316,6 +316,15 @@ int bf_split_plan(const int64_t* ptr, int64_t n_rows, int32_t threshold, int32_t
                   int32_t* heavy_rows, int64_t heavy_cap, int32_t* counts,
                   void* workspace, size_t workspace_bytes, void* stream);
 
+/* The split plan of a CSR whose only row longer than the threshold is row 0
+ * (the Graphormer token row of a table's CSR, every other row holding at most
+ * the table width + 1 entries), cut into n_items items (0: no split row):
+ * the same arrays and counts bf_split_plan writes, in one pass and without a
+ * scan. The caller vouches for the premise; n_items <= BF_MAX_ITEMS_PER_ROW. */
+int bf_split_plan_first_row(int64_t n_rows, int32_t n_items, int32_t* nitems, int32_t* item_off,
+                            int32_t* item_row, int64_t item_cap, int32_t* heavy_rows, int64_t heavy_cap,
+                            int32_t* counts, void* stream);
+
 /* Rows of a CSR ordered longest-first (lengths capped at 255; rows of equal
  * capped length in an unspecified order that may change from call to call).
  * The key-major attention pass walks its rows in this order so the groups

@@ -318,3 +318,29 @@ def test_index_formats_against_numpy(hip_device, token):
     assert plan.items == nit.sum() and np.array_equal(plan.nitems[:n_q].cpu().numpy(), nit)
     assert np.array_equal(plan.item_off[:n_q].cpu().numpy(), np.concatenate([[0], np.cumsum(nit)[:-1]]))
     assert np.array_equal(plan.item_row[:plan.items].cpu().numpy(), np.repeat(np.arange(n_q), nit))
+
+
+@pytest.mark.parametrize("n_rows,chunk,item", [(3000, 128, 768), (1000, 16, 7), (50, 128, 768)])
+def test_first_row_plan_equals_the_generic_plan(hip_device, n_rows, chunk, item):
+    """A table's CSR with the token: only row 0 (the token row) can be longer than `chunk`, and the
+    one-pass plan of that row equals the generic count/scan/rows plan array for array."""
+    from budgetformer_amd import hip_ops
+    rng = np.random.default_rng(n_rows)
+    width = 6
+    row_len = rng.integers(0, width + 1, n_rows).astype(np.int32)
+    table = np.full((n_rows, width), -1, dtype=np.int32)
+    for r in range(n_rows):
+        table[r, :row_len[r]] = np.sort(rng.choice(n_rows, row_len[r], replace=False))
+    t = torch.from_numpy(table).to(hip_device)
+    qptr = hip_ops.table_qptr(t, torch.from_numpy(row_len).to(hip_device), global_token=True)
+    nnz = int(qptr[-1].item())
+    gen = hip_ops.split_plan(qptr, nnz, chunk, item)
+    n_items = min(-(-n_rows // item), 160) if n_rows > chunk else 0
+    one = hip_ops.split_plan_first_row(n_rows + 1, n_items, nnz, chunk, item,
+                                       torch.empty(2, dtype=torch.int32, device=hip_device))
+    assert (one.items, one.heavy) == (gen.items, gen.heavy) == (n_items, 1 if n_items else 0)
+    assert one.counts.tolist() == [gen.items, gen.heavy]
+    n_q = n_rows + 1
+    assert torch.equal(one.nitems[:n_q], gen.nitems[:n_q]) and torch.equal(one.item_off[:n_q], gen.item_off[:n_q])
+    assert torch.equal(one.item_row[:gen.items], gen.item_row[:gen.items])
+    assert torch.equal(one.heavy_rows[:gen.heavy], gen.heavy_rows[:gen.heavy])
