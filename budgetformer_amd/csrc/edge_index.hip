@@ -229,6 +229,16 @@ __global__ void reverse_entries_kernel(const uint64_t* __restrict__ keys, int64_
 constexpr int kBuckets = 256;
 static_assert(kBuckets == kThreads, "the order kernels keep one bucket per thread");
 
+// A row's split-plan entry: (items << 32) | (1 if it splits), items =
+// ceil(len / item_size) capped at BF_MAX_ITEMS_PER_ROW for rows longer than
+// the threshold, else 0. The plan is the exclusive sum of these over the rows.
+__device__ __forceinline__ uint64_t split_count(int64_t len, int threshold, int item_size) {
+  if (len <= threshold) return 0;
+  int64_t n = ceil_div(len, int64_t(item_size));
+  if (n > BF_MAX_ITEMS_PER_ROW) n = BF_MAX_ITEMS_PER_ROW;
+  return (uint64_t(n) << 32) | 1u;
+}
+
 __device__ __forceinline__ int length_bucket(const int64_t* __restrict__ ptr, int64_t r) {
   const int64_t len = ptr[r + 1] - ptr[r];
   return 255 - int(len < 255 ? len : 255);
@@ -257,7 +267,9 @@ __global__ __launch_bounds__(kThreads) void order_scatter_kernel(const int64_t* 
                                                                  int64_t chunk, const uint32_t* __restrict__ hist,
                                                                  uint32_t* __restrict__ cursor,
                                                                  int32_t* __restrict__ order,
-                                                                 uint64_t* __restrict__ spans) {
+                                                                 uint64_t* __restrict__ spans, int threshold,
+                                                                 int item_size, int64_t n_slots,
+                                                                 uint64_t* __restrict__ packed) {
   __shared__ uint32_t base[kBuckets];
   __shared__ uint32_t cnt[kBuckets];
   const int tid = threadIdx.x;
@@ -286,6 +298,7 @@ __global__ __launch_bounds__(kThreads) void order_scatter_kernel(const int64_t* 
     const uint32_t slot = base[b] + atomicAdd(&cnt[b], 1u);
     order[slot] = int32_t(r);
     if (spans) spans[slot] = (uint64_t(beg) << 32) | uint64_t(len);
+    if (packed && slot < n_slots) packed[slot] = split_count(len, threshold, item_size);
   }
 }
 
@@ -330,51 +343,51 @@ int row_ids(const int64_t* ptr, int64_t n_rows, int64_t nnz, int32_t* marks, int
 }
 
 // ---------------------------------------------------------------- split plans
-// Per row: its item count, and (items << 32 | is_heavy) so that ONE exclusive
-// scan yields both the first item and the heavy-list slot of every row.
+// Per row (items << 32 | is_heavy), so that ONE exclusive scan yields both the
+// first item and the heavy-list slot of every row.
 __global__ void split_count_kernel(const int64_t* __restrict__ ptr, int64_t n_rows, int threshold, int item_size,
-                                   int32_t* __restrict__ nitems, uint64_t* __restrict__ packed) {
+                                   uint64_t* __restrict__ packed) {
   const int64_t r = int64_t(blockIdx.x) * kThreads + threadIdx.x;
-  if (r >= n_rows) return;
-  const int64_t len = ptr[r + 1] - ptr[r];
-  const bool heavy = len > threshold;
-  int64_t n = heavy ? ceil_div(len, int64_t(item_size)) : 0;
-  if (n > BF_MAX_ITEMS_PER_ROW) n = BF_MAX_ITEMS_PER_ROW;
-  nitems[r] = int32_t(n);
-  packed[r] = (uint64_t(n) << 32) | (heavy ? 1u : 0u);
+  if (r < n_rows) packed[r] = split_count(ptr[r + 1] - ptr[r], threshold, item_size);
 }
 
-// item_off, the heavy-row list (compacted by the scanned flags), item_row of
-// each item and the two plan counts. A row's thread writes the item_row of its
-// first kOwnItems items; rows with more (the Graphormer token row and column,
-// hubs) are queued in LDS and their remaining items written by the whole block.
+// nitems, item_off, the heavy-row list (compacted by the scanned flags),
+// item_row of each item and the two plan counts, one thread per slot: slot j
+// is row j, or with an order row order[j], and then only the split rows'
+// entries are written. A row's thread writes the item_row of its first
+// kOwnItems items; rows with more (the Graphormer token row and column, hubs)
+// are queued in LDS and their remaining items written by the whole block.
 constexpr int kOwnItems = 32;
-
 __global__ __launch_bounds__(kThreads) void split_rows_kernel(
-    const int32_t* __restrict__ nitems, const uint64_t* __restrict__ packed_off, int64_t n_rows, int64_t item_cap,
-    int32_t* __restrict__ item_off, int32_t* __restrict__ item_row, int32_t* __restrict__ heavy_rows,
-    int64_t heavy_cap, int32_t* __restrict__ counts) {
+    const uint64_t* __restrict__ packed, const uint64_t* __restrict__ packed_off, const int32_t* __restrict__ order,
+    int64_t n_slots, int64_t item_cap, int32_t* __restrict__ nitems, int32_t* __restrict__ item_off,
+    int32_t* __restrict__ item_row, int32_t* __restrict__ heavy_rows, int64_t heavy_cap,
+    int32_t* __restrict__ counts) {
   __shared__ int64_t long_first[kThreads];
   __shared__ int32_t long_n[kThreads], long_row[kThreads];
   __shared__ int n_long;
   if (threadIdx.x == 0) n_long = 0;
   __syncthreads();
-  const int64_t r = int64_t(blockIdx.x) * kThreads + threadIdx.x;
-  if (r < n_rows) {
-    const int n = nitems[r];
-    const uint64_t off = packed_off[r];
+  const int64_t j = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (j < n_slots) {
+    const int n = int(packed[j] >> 32);
+    const uint64_t off = packed_off[j];
     const int64_t first_item = int64_t(off >> 32);
     const int64_t slot = int64_t(uint32_t(off));
-    item_off[r] = int32_t(first_item);
-    if (n > 0 && slot < heavy_cap) heavy_rows[slot] = int32_t(r);
-    for (int64_t j = 0; j < n && j < kOwnItems && first_item + j < item_cap; ++j) item_row[first_item + j] = int32_t(r);
-    if (n > kOwnItems) {
-      const int k = atomicAdd(&n_long, 1);
-      long_first[k] = first_item;
-      long_n[k] = n;
-      long_row[k] = int32_t(r);
+    if (!order || n > 0) {
+      const int32_t r = order ? order[j] : int32_t(j);
+      nitems[r] = n;
+      item_off[r] = int32_t(first_item);
+      if (n > 0 && slot < heavy_cap) heavy_rows[slot] = r;
+      for (int64_t i = 0; i < n && i < kOwnItems && first_item + i < item_cap; ++i) item_row[first_item + i] = r;
+      if (n > kOwnItems) {
+        const int k = atomicAdd(&n_long, 1);
+        long_first[k] = first_item;
+        long_n[k] = n;
+        long_row[k] = r;
+      }
     }
-    if (r == n_rows - 1) {
+    if (j == n_slots - 1) {
       const int64_t items = first_item + n;
       const int64_t heavy = slot + (n > 0 ? 1 : 0);
       counts[0] = int32_t(items < item_cap ? items : item_cap);
@@ -653,11 +666,12 @@ extern "C" int bf_split_plan(const int64_t* ptr, int64_t n_rows, int32_t thresho
   size_t temp_bytes = 0;
   (void)hipcub::DeviceScan::ExclusiveSum(nullptr, temp_bytes, packed, packed_off, int(n_rows));
   BF_LAUNCH("split_count_kernel", split_count_kernel, dim3(blocks_for(n_rows)), dim3(kThreads), 0, st, ptr, n_rows,
-            threshold, item_size, nitems, packed);
+            threshold, item_size, packed);
   BF_CHECK_LAUNCH();
   BF_CHECK_HIP(hipcub::DeviceScan::ExclusiveSum(temp, temp_bytes, packed, packed_off, int(n_rows), st));
-  BF_LAUNCH("split_rows_kernel", split_rows_kernel, dim3(blocks_for(n_rows)), dim3(kThreads), 0, st, nitems,
-            packed_off, n_rows, item_cap, item_off, item_row, heavy_rows, heavy_cap, counts);
+  BF_LAUNCH("split_rows_kernel", split_rows_kernel, dim3(blocks_for(n_rows)), dim3(kThreads), 0, st, packed,
+            packed_off, static_cast<const int32_t*>(nullptr), n_rows, item_cap, nitems, item_off, item_row,
+            heavy_rows, heavy_cap, counts);
   BF_CHECK_LAUNCH();
   return BF_OK;
 }
@@ -835,9 +849,37 @@ extern "C" int bf_coalesce(const int64_t* src, const int64_t* dst, int64_t nnz, 
   return BF_OK;
 }
 
+namespace {
+// hist / cursor of the order kernels, then (plans only) the slots' packed
+// counts, their exclusive sums and the scan's temporary storage.
+constexpr size_t kOrderHistBytes = 2 * kBuckets * sizeof(uint32_t);
+
+size_t plan_slots_scan_bytes(int64_t n_slots) {
+  size_t temp_bytes = 0;
+  (void)hipcub::DeviceScan::ExclusiveSum(nullptr, temp_bytes, static_cast<const uint64_t*>(nullptr),
+                                         static_cast<uint64_t*>(nullptr), int(n_slots > 0 ? n_slots : 1));
+  return temp_bytes;
+}
+
+int launch_row_order(const int64_t* ptr, int64_t n_rows, int32_t* order, uint64_t* spans, uint32_t* hist,
+                     int threshold, int item_size, int64_t n_slots, uint64_t* packed, hipStream_t st) {
+  uint32_t* cursor = hist + kBuckets;
+  BF_CHECK_HIP(hipMemsetAsync(hist, 0, kOrderHistBytes, st));
+  const int64_t blocks = blocks_for(n_rows);
+  BF_LAUNCH("order_hist_kernel", order_hist_kernel, dim3(unsigned(blocks < 2048 ? blocks : 2048)), dim3(kThreads), 0,
+            st, ptr, n_rows, hist);
+  BF_CHECK_LAUNCH();
+  const int64_t chunk = kOrderChunk;
+  BF_LAUNCH("order_scatter_kernel", order_scatter_kernel, dim3(unsigned(ceil_div(n_rows, chunk))), dim3(kThreads), 0,
+            st, ptr, n_rows, chunk, hist, cursor, order, spans, threshold, item_size, n_slots, packed);
+  BF_CHECK_LAUNCH();
+  return BF_OK;
+}
+}  // namespace
+
 extern "C" int bf_row_order_workspace_size(int64_t n_rows, size_t* bytes) {
   BF_CHECK_ARG(bytes && n_rows >= 0, "row_order_workspace_size: bad arguments");
-  *bytes = 2 * kBuckets * sizeof(uint32_t) + 256;
+  *bytes = kOrderHistBytes + 256;
   return BF_OK;
 }
 
@@ -849,17 +891,54 @@ extern "C" int bf_row_order(const int64_t* ptr, int64_t n_rows, int32_t* order, 
   size_t need = 0;
   bf_row_order_workspace_size(n_rows, &need);
   BF_CHECK_ARG(workspace && workspace_bytes >= need, "row_order: workspace %zu < %zu bytes", workspace_bytes, need);
+  return launch_row_order(ptr, n_rows, order, spans, static_cast<uint32_t*>(workspace), 0, 1, 0, nullptr,
+                          as_stream(stream));
+}
+
+extern "C" int bf_row_order_and_plan_workspace_size(int64_t n_rows, int64_t heavy_cap, size_t* bytes) {
+  BF_CHECK_ARG(bytes && n_rows >= 0 && heavy_cap >= 0, "row_order_and_plan_workspace_size: bad arguments");
+  const int64_t n_slots = heavy_cap < n_rows ? heavy_cap : n_rows;
+  const size_t slab = align_up(size_t(n_slots > 0 ? n_slots : 1) * 8);
+  *bytes = align_up(kOrderHistBytes) + 2 * slab + align_up(plan_slots_scan_bytes(n_slots)) + 256;
+  return BF_OK;
+}
+
+extern "C" int bf_row_order_and_plan(const int64_t* ptr, int64_t n_rows, int32_t threshold, int32_t item_size,
+                                     int32_t* order, uint64_t* spans, int32_t* nitems, int32_t* item_off,
+                                     int32_t* item_row, int64_t item_cap, int32_t* heavy_rows, int64_t heavy_cap,
+                                     int32_t* counts, void* workspace, size_t workspace_bytes, void* stream) {
+  BF_CHECK_ARG(ptr && n_rows >= 0 && n_rows < (int64_t(1) << 31) && counts, "row_order_and_plan: bad arguments");
+  BF_CHECK_ARG(threshold >= 1 && threshold < 255 && item_size >= 1,
+               "row_order_and_plan: threshold must lie in [1, 254] and item_size be >= 1");
+  BF_CHECK_ARG(item_cap >= 0 && item_cap < (int64_t(1) << 31) && heavy_cap >= 1 && heavy_cap < (int64_t(1) << 31),
+               "row_order_and_plan: bad capacity");
   hipStream_t st = as_stream(stream);
-  auto* hist = static_cast<uint32_t*>(workspace);
-  uint32_t* cursor = hist + kBuckets;
-  BF_CHECK_HIP(hipMemsetAsync(hist, 0, 2 * kBuckets * sizeof(uint32_t), st));
-  const int64_t blocks = blocks_for(n_rows);
-  BF_LAUNCH("order_hist_kernel", order_hist_kernel, dim3(unsigned(blocks < 2048 ? blocks : 2048)), dim3(kThreads), 0,
-            st, ptr, n_rows, hist);
-  BF_CHECK_LAUNCH();
-  const int64_t chunk = kOrderChunk;
-  BF_LAUNCH("order_scatter_kernel", order_scatter_kernel, dim3(unsigned(ceil_div(n_rows, chunk))), dim3(kThreads), 0,
-            st, ptr, n_rows, chunk, hist, cursor, order, spans);
+  if (n_rows == 0) {
+    BF_CHECK_HIP(hipMemsetAsync(counts, 0, 2 * sizeof(int32_t), st));
+    return BF_OK;
+  }
+  BF_CHECK_ARG(order && nitems && item_off && (item_row || item_cap == 0) && heavy_rows,
+               "row_order_and_plan: null tensor");
+  size_t need = 0;
+  bf_row_order_and_plan_workspace_size(n_rows, heavy_cap, &need);
+  BF_CHECK_ARG(workspace && workspace_bytes >= need, "row_order_and_plan: workspace %zu < %zu bytes",
+               workspace_bytes, need);
+  // Rows longer than the threshold (< 255) have the highest capped lengths, so
+  // the order puts them in its first slots, and there are at most heavy_cap of
+  // them: the plan needs only the first n_slots slots.
+  const int64_t n_slots = heavy_cap < n_rows ? heavy_cap : n_rows;
+  const size_t slab = align_up(size_t(n_slots) * 8);
+  char* ws = static_cast<char*>(workspace);
+  auto* hist = reinterpret_cast<uint32_t*>(ws);
+  auto* packed = reinterpret_cast<uint64_t*>(ws + align_up(kOrderHistBytes));
+  auto* packed_off = reinterpret_cast<uint64_t*>(ws + align_up(kOrderHistBytes) + slab);
+  void* temp = ws + align_up(kOrderHistBytes) + 2 * slab;
+  size_t temp_bytes = plan_slots_scan_bytes(n_slots);
+  const int rc = launch_row_order(ptr, n_rows, order, spans, hist, threshold, item_size, n_slots, packed, st);
+  if (rc) return rc;
+  BF_CHECK_HIP(hipcub::DeviceScan::ExclusiveSum(temp, temp_bytes, packed, packed_off, int(n_slots), st));
+  BF_LAUNCH("split_rows_kernel", split_rows_kernel, dim3(blocks_for(n_slots)), dim3(kThreads), 0, st, packed,
+            packed_off, order, n_slots, item_cap, nitems, item_off, item_row, heavy_rows, heavy_cap, counts);
   BF_CHECK_LAUNCH();
   return BF_OK;
 }

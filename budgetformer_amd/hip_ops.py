@@ -458,6 +458,36 @@ def row_order(ptr: torch.Tensor, spans: bool = False):
     return (order, sp) if spans else order
 
 
+def row_order_and_plan(ptr: torch.Tensor, nnz: int, threshold: int, item_size: int,
+                       counts: Optional[torch.Tensor] = None, host_copy: bool = True):
+    """(order, spans, plan): ``row_order(ptr, spans=True)`` and the split plan of the rows it puts first
+    (bf_row_order_and_plan; threshold in [1, 254]), split rows and their items numbered longest first.
+    The plan's counts are handled as in ``split_plan(..., resolve=False)``."""
+    dev = ptr.device
+    lib = N.load()
+    n_rows = ptr.numel() - 1
+    r = max(n_rows, 1)
+    item_cap = int(lib.bf_split_item_capacity(nnz, threshold, item_size))
+    heavy_cap = int(lib.bf_split_row_capacity(nnz, threshold))
+    order = torch.empty(r, dtype=torch.int32, device=dev)
+    spans = torch.empty(r, dtype=torch.int64, device=dev)
+    buf = torch.empty(2 * r + max(item_cap, 1) + max(heavy_cap, 1), dtype=torch.int32, device=dev)
+    nitems, item_off, item_row, heavy_rows = torch.split(buf, [r, r, max(item_cap, 1), max(heavy_cap, 1)])
+    if counts is None:
+        counts = torch.empty(2, dtype=torch.int32, device=dev)
+    ws = _workspace(_size_query("bf_row_order_and_plan_workspace_size", n_rows, heavy_cap), dev)
+    N.call("bf_row_order_and_plan", _p(ptr), n_rows, threshold, item_size, _p(order), _p(spans), _p(nitems),
+           _p(item_off), _p(item_row), item_cap, _p(heavy_rows), heavy_cap, _p(counts), _p(ws), ws.numel(),
+           _stream(dev))
+    plan = SplitPlan(-1, -1, nitems, item_off, item_row, heavy_rows, counts, item_cap, heavy_cap)
+    if host_copy:
+        plan.host_counts = torch.empty(2, dtype=torch.int32, pin_memory=True)
+        plan.host_counts.copy_(counts, non_blocking=True)
+        plan.ready = torch.cuda.Event()
+        plan.ready.record(torch.cuda.current_stream(dev))
+    return order, spans, plan
+
+
 @dataclass
 class SplitPlan:
     """Rows longer than `threshold` cut into `item_size`-entry items.
@@ -643,6 +673,11 @@ class AttentionIndex:
                 self._rkeys = None
             else:
                 self.kptr, self.kq, self.ke = reverse_index(self.qptr, self.kv, self.n_kv)
+        if self.kplan is None and self.korder is None and 1 <= self.chunk <= 254:
+            # the rows to split are the longest-first order's first slots: one pass writes both
+            self.korder, self.kspans, self.kplan = row_order_and_plan(
+                self.kptr, self.nnz, self.chunk, self.item, counts=self._plan_counts(1),
+                host_copy=self._host_copy())
         if self.kplan is None:
             self.kplan = split_plan(self.kptr, self.nnz, self.chunk, self.item, resolve=False,
                                     counts=self._plan_counts(1), host_copy=self._host_copy())

@@ -337,6 +337,22 @@ int bf_row_order_workspace_size(int64_t n_rows, size_t* bytes);
 int bf_row_order(const int64_t* ptr, int64_t n_rows, int32_t* order, uint64_t* spans, void* workspace,
                  size_t workspace_bytes, void* stream);
 
+/* bf_row_order, then the split plan of the rows it puts first (what
+ * bf_split_plan writes for the rows that split). With 1 <= threshold <= 254
+ * the rows longer than the threshold have the highest capped lengths, so they
+ * are the order's first slots, and there are at most heavy_cap of them
+ * (bf_split_row_capacity): the plan is scanned over min(heavy_cap, n_rows)
+ * slots instead of all rows, from item counts the order pass writes as it
+ * places each row. The split rows (heavy_rows) and their items are numbered in
+ * slot order, longest first, instead of ascending row id, and only the split
+ * rows' nitems / item_off entries are written. No counterpart in the
+ * reference: it replaces bf_row_order + bf_split_plan over the reverse index. */
+int bf_row_order_and_plan_workspace_size(int64_t n_rows, int64_t heavy_cap, size_t* bytes);
+int bf_row_order_and_plan(const int64_t* ptr, int64_t n_rows, int32_t threshold, int32_t item_size,
+                          int32_t* order, uint64_t* spans, int32_t* nitems, int32_t* item_off,
+                          int32_t* item_row, int64_t item_cap, int32_t* heavy_rows, int64_t heavy_cap,
+                          int32_t* counts, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ======================================================================
  * Sparse edge attention
  * ====================================================================== */

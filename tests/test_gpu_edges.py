@@ -344,3 +344,26 @@ def test_first_row_plan_equals_the_generic_plan(hip_device, n_rows, chunk, item)
     assert torch.equal(one.nitems[:n_q], gen.nitems[:n_q]) and torch.equal(one.item_off[:n_q], gen.item_off[:n_q])
     assert torch.equal(one.item_row[:gen.items], gen.item_row[:gen.items])
     assert torch.equal(one.heavy_rows[:gen.heavy], gen.heavy_rows[:gen.heavy])
+
+
+@pytest.mark.parametrize("chunk,item", [(128, 768), (4, 5), (16, 3)])
+def test_plan_from_the_row_order_equals_the_generic_plan(hip_device, chunk, item):
+    """The split rows are the longest-first order's first slots: the plan written from them holds the
+    same split rows, item counts and counts as the generic plan, only numbered in slot order."""
+    from budgetformer_amd import hip_ops
+    n, e = 3000, 30000
+    rowptr, col = _graph(n, e, seed=chunk * 10 + item)
+    ptr = torch.from_numpy(rowptr).to(hip_device)
+    nnz = int(rowptr[-1])
+    gen = hip_ops.split_plan(ptr, nnz, chunk, item)
+    order, spans, plan = hip_ops.row_order_and_plan(ptr, nnz, chunk, item)
+    hip_ops.resolve_plans(plan)
+    assert (plan.items, plan.heavy) == (gen.items, gen.heavy) and gen.heavy > 0
+    heavy = plan.heavy_rows[:plan.heavy].cpu().numpy()
+    assert np.array_equal(np.sort(heavy), gen.heavy_rows[:gen.heavy].cpu().numpy())
+    assert np.array_equal(heavy, order[:plan.heavy].cpu().numpy())           # slot order
+    nit, off = plan.nitems.cpu().numpy(), plan.item_off.cpu().numpy()
+    assert np.array_equal(nit[heavy], gen.nitems.cpu().numpy()[heavy])
+    # items numbered in slot order, each row's items contiguous
+    assert np.array_equal(off[heavy], np.concatenate([[0], np.cumsum(nit[heavy])[:-1]]))
+    assert np.array_equal(plan.item_row[:plan.items].cpu().numpy(), np.repeat(heavy, nit[heavy]))
