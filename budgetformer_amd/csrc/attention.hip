@@ -787,7 +787,7 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
 // Blocks [0, q_heavy) reduce the query-side split rows into dq (their items ran
 // in the dq pass), blocks [q_heavy, q_heavy + k_items) take the key-side items,
 // the rest one short key row per group, longest rows first.
-template <typename T, bool NT>
+template <typename T, bool NT, bool PRE>
 __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const int64_t* __restrict__ kptr, const int32_t* __restrict__ kq,
@@ -850,11 +850,33 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
   // each group takes rows_per_group consecutive rows of the order (similar lengths)
   const int64_t first = row_slot(sh, unsigned(q_heavy_arg + k_items_arg)) * rows_per_group;
   const int64_t last = first + rows_per_group < n_kv ? first + rows_per_group : n_kv;
+  // With several rows per group their slots come in one round of loads: lane i of the group reads
+  // slot first + i and each iteration takes its row and span from that lane, so a row's wait for its
+  // slot does not follow the previous row's work (the group's lanes loop together, so the source
+  // lane is active whenever its readers are). A separate instance (PRE), launched for bf16 only: the
+  // registers held across the loop would cost the fp32 kernel a wave (95 -> 100 VGPRs), and the one-row
+  // bf16 kernel 6 VGPRs for nothing.
+  constexpr bool pre = PRE;
+  int32_t pre_row = 0;
+  uint64_t pre_span = 0;
+  if (pre && g.g_lane < rows_per_group && first + g.g_lane < last) {
+    pre_row = order ? order[first + g.g_lane] : int32_t(first + g.g_lane);
+    if (spans) pre_span = spans[first + g.g_lane];
+  }
+  const int lane0 = int(threadIdx.x & 63) - g.g_lane;
   for (int64_t slot = first; slot < last; ++slot) {
-    const int64_t row = order ? int64_t(order[slot]) : slot;
+    const int src = lane0 + int(slot - first);
+    const int64_t row = pre ? int64_t(__shfl(pre_row, src, 64)) : (order ? int64_t(order[slot]) : slot);
     int64_t beg, end;
     if (spans) {                  // the slot's (begin << 32 | length): read in slot order, not at random
-      const uint64_t sp = spans[slot];
+      uint64_t sp;
+      if (pre) {
+        const uint32_t lo = uint32_t(__shfl(int(uint32_t(pre_span)), src, 64));
+        const uint32_t hi = uint32_t(__shfl(int(uint32_t(pre_span >> 32)), src, 64));
+        sp = (uint64_t(hi) << 32) | lo;
+      } else {
+        sp = spans[slot];
+      }
       beg = int64_t(sp >> 32);
       end = beg + int64_t(sp & 0xffffffffu);
     } else {
@@ -1039,16 +1061,29 @@ int bwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
   if (kv_blocks > 0) {
     const size_t lds = (idx->q_heavy > 0 || idx->k_items > 0) ? combine_lds_bytes(sh) : 0;
     const bool stream_rows = size_t(idx->n_q) * size_t(sh.D) * sizeof(T) * 2 > kStreamBytes;
-#define BF_LAUNCH_KV(NT)                                                                                           \
-  BF_LAUNCH("attn_bwd_kv_kernel", (attn_bwd_kv_kernel<T, NT>), dim3(unsigned(kv_blocks)), dim3(kBlock), lds, st, Q, K, \
-            Vv, idx->kptr, idx->kq, idx->ke, bias, factor, dO, rstat, static_cast<T*>(dq), static_cast<T*>(dk),       \
+#define BF_LAUNCH_KV(NT, PRE)                                                                                      \
+  BF_LAUNCH("attn_bwd_kv_kernel", (attn_bwd_kv_kernel<T, NT, PRE>), dim3(unsigned(kv_blocks)), dim3(kBlock), lds, st, \
+            Q, K, Vv, idx->kptr, idx->kq, idx->ke, bias, factor, dO, rstat, static_cast<T*>(dq), static_cast<T*>(dk),       \
             static_cast<T*>(dv), idx->k_order, idx->k_spans, qit, idx->q_heavy, kit, idx->k_items, idx->n_kv, sh,     \
             idx->chunk,                                                                                              \
             rows_per_group, token_rec, idx->q_items, int64_t(grid_for(idx->n_q, sh)), idx->plan_counts)
-    if (stream_rows)
-      BF_LAUNCH_KV(true);
-    else
-      BF_LAUNCH_KV(false);
+    if constexpr (sizeof(T) == 2) {
+      // the group's slots prefetched (several rows per group)
+      const bool pre = rows_per_group > 1 && rows_per_group <= (1 << sh.lpr_log2);
+      if (pre && stream_rows)
+        BF_LAUNCH_KV(true, true);
+      else if (pre)
+        BF_LAUNCH_KV(false, true);
+      else if (stream_rows)
+        BF_LAUNCH_KV(true, false);
+      else
+        BF_LAUNCH_KV(false, false);
+    } else {
+      if (stream_rows)
+        BF_LAUNCH_KV(true, false);
+      else
+        BF_LAUNCH_KV(false, false);
+    }
 #undef BF_LAUNCH_KV
     BF_CHECK_LAUNCH();
   }

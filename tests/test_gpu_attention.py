@@ -70,11 +70,13 @@ def test_fp32_random_coo(hip_device, S, H, hn, E):
 
 
 @pytest.mark.parametrize("token_column", [False, True])
-@pytest.mark.parametrize("chunk,item", [(4, 4), (4, 37), (64, 512), (4, 2)])
+@pytest.mark.parametrize("chunk,item", [(4, 4), (4, 37), (64, 512), (4, 2), (300, 64)])
 def test_fp32_global_token_split_rows(hip_device, chunk, item, token_column):
     """Graphormer token: query 0 is dense over all kv and kv 0 feeds every query. With items of 2
     the token row and column exceed the per-row item cap and run as 160 balanced items. The COO
-    has the token-column layout, so key 0's terms can also come from the dq pass (token_column)."""
+    has the token-column layout, so key 0's terms can also come from the dq pass (token_column).
+    A chunk above 254 takes the key plan from the generic count/scan/rows pass instead of the
+    row order's first slots."""
     from budgetformer_amd.hip_ops import AttentionIndex
     S, H, hn = 500, 8, 16
     q, k, v, ei, dout = _inputs(S, H, hn, 2500, seed=7, mult=1.3)
