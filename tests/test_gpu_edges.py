@@ -367,3 +367,27 @@ def test_plan_from_the_row_order_equals_the_generic_plan(hip_device, chunk, item
     # items numbered in slot order, each row's items contiguous
     assert np.array_equal(off[heavy], np.concatenate([[0], np.cumsum(nit[heavy])[:-1]]))
     assert np.array_equal(plan.item_row[:plan.items].cpu().numpy(), np.repeat(heavy, nit[heavy]))
+
+
+@pytest.mark.parametrize("n,width,lo", [(120_000, 12, 8), (600_000, 4, 2)])
+def test_packed_reverse_index_past_1m_entries(hip_device, n, width, lo):
+    """Past 1M entries the sorts run as onesweep radix passes instead of a merge sort, the packed reverse
+    index over only its 17 or 20 kv-id bits. The result must equal the pair-sort route and numpy's stable
+    order."""
+    from budgetformer_amd import hip_ops
+    rng = np.random.default_rng(n)
+    row_len = rng.integers(lo, width + 1, n).astype(np.int32)
+    base = rng.integers(0, n, n)
+    table = ((base[:, None] + np.arange(width)[None, :] * 104729) % n).astype(np.int32)   # distinct per row
+    table[np.arange(width)[None, :] >= row_len[:, None]] = -1
+    assert row_len.sum() > 1_000_000
+    t, rl = torch.from_numpy(table).to(hip_device), torch.from_numpy(row_len).to(hip_device)
+    qptr, kv, rk = hip_ops.table_to_csr(t, rl, False, with_keys=True)
+    a = hip_ops.reverse_index(qptr, kv, n)
+    b = hip_ops.reverse_index_packed(rk, qptr, n)
+    for x, y in zip(a, b[:3]):
+        assert torch.equal(x, y)
+    vals = kv.cpu().numpy()
+    order = np.argsort(vals, kind="stable")
+    assert np.array_equal(b[2].cpu().numpy(), order)
+    assert np.array_equal(np.diff(b[0].cpu().numpy()), np.bincount(vals, minlength=n))
