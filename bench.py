@@ -440,7 +440,7 @@ def cpu_baseline(cfg, g, tab, idx, q, k, v, dout, s_bytes, D, H):
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"{what} {cfg['name'].split(':')[0]} workload: attention fwd+bwd (torch CPU autograd, fp32, best "
+        "sample": f"{cfg['name'].split(':')[0]}, {what}: attention fwd+bwd (torch CPU autograd, fp32, best "
                   f"of {len(times)}) and the numpy edge build of those queries",
         "attn_fwd_bwd_ms": round(attn_s * 1e3, 2),
         "edge_build_ms": round(build_s * 1e3, 2),
