@@ -982,9 +982,14 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // rows: 44.9 -> 40.4 ms) while on small tables the extra rows per group cost
 // parallelism (c2: 2x slower). The query-side passes keep one row per group:
 // four were measured no faster for the dq pass and 4% slower for the forward
-// at c5's 27.8M queries.
+// at c5's 27.8M queries. In bf16, where a group's slots are loaded in one
+// round, four rows per group also pay from 1M kv rows on (c3's 2.45M: dk/dv
+// pass 3.30 -> 3.26 ms; c4's 2.92M: 3.63 -> 3.61 ms; two rows gave the same).
 constexpr int64_t kManyRows = int64_t(1) << 24;
-inline int kv_rows_per_group(int64_t n_kv) { return n_kv > kManyRows ? 4 : 1; }
+constexpr int64_t kManyRowsBf16 = int64_t(1) << 20;
+inline int kv_rows_per_group(int64_t n_kv, size_t elem_bytes) {
+  return n_kv > (elem_bytes == 2 ? kManyRowsBf16 : kManyRows) ? 4 : 1;
+}
 
 inline unsigned grid_for(int64_t rows, const Shape& sh) {
   const int64_t per_block = kBlock >> sh.lpr_log2;
@@ -1056,7 +1061,7 @@ int bwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
               idx->n_q, sh, idx->chunk, token_rec, idx->plan_counts);
     BF_CHECK_LAUNCH();
   }
-  const int rows_per_group = kv_rows_per_group(idx->n_kv);
+  const int rows_per_group = kv_rows_per_group(idx->n_kv, sizeof(T));
   const int64_t kv_blocks = int64_t(idx->q_heavy) + idx->k_items + grid_for(ceil_div(idx->n_kv, rows_per_group), sh);
   if (kv_blocks > 0) {
     const size_t lds = (idx->q_heavy > 0 || idx->k_items > 0) ? combine_lds_bytes(sh) : 0;

@@ -354,14 +354,16 @@ def test_streaming_kv_pass_on_a_table_larger_than_the_cache(hip_device, dtype, H
         assert _rel_err(got, ref) < tol
 
 
-def test_kv_pass_past_16m_rows_equals_the_compact_problem(hip_device):
-    """Past 16M kv rows the dk/dv pass gives each lane group several short rows. Every row is still
-    computed alone, so the gradients of a 17M-row problem with 30K attended rows must equal, bit for
-    bit, those of the same edges over the 30K rows alone, and every other row must be zero."""
+@pytest.mark.parametrize("n_big", [2_000_000, 17_000_000])
+def test_kv_pass_with_four_rows_per_group_equals_the_compact_problem(hip_device, n_big):
+    """Past 1M kv rows in bf16 (16M in fp32) the dk/dv pass gives each lane group four short rows. Every
+    row is still computed alone, so the gradients of a 2M- or 17M-row problem with 30K attended rows
+    must equal, bit for bit, those of the same edges over the 30K rows alone (one row per group), and
+    every other row must be zero."""
     from budgetformer_amd import hip_ops
     from budgetformer_amd.hip_ops import AttentionIndex
     g = torch.Generator(device=hip_device).manual_seed(3)
-    n_q, n_big, n_touch, E, H, hn = 20000, 17_000_000, 30000, 200000, 8, 16
+    n_q, n_touch, E, H, hn = 20000, 30000, 200000, 8, 16
     touched = torch.randperm(n_big, generator=g, device=hip_device)[:n_touch].sort().values
     src_c = torch.randint(0, n_touch, (E,), generator=g, device=hip_device)
     dst = torch.randint(0, n_q, (E,), generator=g, device=hip_device)
