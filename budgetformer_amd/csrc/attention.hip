@@ -291,8 +291,11 @@ __device__ __forceinline__ void store_record(const Items& it, int64_t item, cons
 // Sums the records of split row number `heavy` (one workgroup; groups strided
 // over the items with several records in flight each, then combined in group
 // order). Returns the row id, or -1 for a row with a single item (finished by
-// that item); the sums are valid in group 0.
-template <int V>
+// that item); the sums are valid in group 0. R records in flight per group:
+// the stand-alone reduce kernels take as many as their registers allow (the
+// 160 items of the token row in one round at D = 128), the dk/dv kernel's dq
+// reduces 8, which keep that kernel's register count.
+template <int V, int R = 8>
 __device__ __forceinline__ int reduce_row_records(const Items& it, int64_t heavy, float* lds, const Shape& sh,
                                                   const GroupPos& g, float (&a)[V], float (&b)[V], bool with_b,
                                                   float& z, bool with_z) {
@@ -306,7 +309,6 @@ __device__ __forceinline__ int reduce_row_records(const Items& it, int64_t heavy
   for (int i = 0; i < V; ++i) a[i] = b[i] = 0.f;
   z = 0.f;
   if (g.act) {
-    constexpr int R = 8;
     for (int m0 = grp; m0 < n; m0 += R * gpb) {
       float ra[R][V], rb[R][V], rz[R];
 #pragma unroll
@@ -403,7 +405,7 @@ __global__ __launch_bounds__(kBlock) void attn_fwd_reduce_kernel(T* __restrict__
   extern __shared__ float lds[];
   const GroupPos g = group_pos<T>(sh);
   float acc[V], unused[V], z;
-  const int row = reduce_row_records<V>(it, blockIdx.x, lds, sh, g, acc, unused, false, z, true);
+  const int row = reduce_row_records<V, 80 / V>(it, blockIdx.x, lds, sh, g, acc, unused, false, z, true);
   if (row < 0 || (threadIdx.x >> sh.lpr_log2) != 0) return;
   store_out(out, Z, row, sh, g, acc, z);
 }
@@ -921,7 +923,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_reduce_kernel(T* __restric
   extern __shared__ float lds[];
   const GroupPos g = group_pos<T>(sh);
   float ak[V], av[V], z;
-  const int row = reduce_row_records<V>(it, blockIdx.x, lds, sh, g, ak, av, true, z, false);
+  const int row = reduce_row_records<V, 40 / V>(it, blockIdx.x, lds, sh, g, ak, av, true, z, false);
   if (row < 0 || (threadIdx.x >> sh.lpr_log2) != 0 || !g.act) return;
   Elem<T>::store(dk + int64_t(row) * sh.D + g.col0, ak);
   Elem<T>::store(dv + int64_t(row) * sh.D + g.col0, av);
