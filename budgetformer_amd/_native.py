@@ -16,7 +16,8 @@ _LIB = os.path.join(_PKG, "_lib", "libbudgetformer_hip.so")
 
 BF_OK, BF_ERR_INVALID, BF_ERR_UNSUPPORTED, BF_ERR_HIP = 0, 1, 2, 3
 BF_DTYPE_F32, BF_DTYPE_BF16 = 0, 1
-BF_MAX_ITEMS_PER_ROW = 160          # items a split row is cut into at most (the header's #define)
+BF_MAX_ITEMS_PER_ROW = 160          # items a split row is cut into at most (the header's #define) ...
+BF_LONG_ROW_FACTOR = 64             # ... unless it is longer than 160 * 64 items' worth (the header's #define)
 
 i32, i64, u64, sz = C.c_int32, C.c_int64, C.c_uint64, C.c_size_t
 vp = C.c_void_p
@@ -70,8 +71,8 @@ _SIGS = {
     "bf_build_edge_table_workspace_size": (C.c_int, [i64, i32, i64, i32, C.POINTER(sz)]),
     "bf_build_edge_table": (C.c_int, [P_i64, P_i32, P_i64, P_i32, i64, i64, i64, i64, i32, i32, i32, i32, i64,
                                       P_f32, u64, u64, P_i32, i64, i64, P_i32, i64, i64, P_i32, P_i32, vp, sz, vp]),
-    "bf_table_csr_ptr": (C.c_int, [P_i32, i64, i32, P_i64, C.POINTER(i64), vp, sz, vp]),
-    "bf_table_to_csr": (C.c_int, [P_i32, P_i32, i64, i32, i32, P_i64, P_i32, vp, i32, i32, vp]),
+    "bf_table_csr_ptr": (C.c_int, [P_i32, i64, i32, i64, P_i64, C.POINTER(i64), vp, sz, vp]),
+    "bf_table_to_csr": (C.c_int, [P_i32, P_i32, i64, i32, i32, i64, P_i64, P_i32, vp, i32, i32, vp]),
     "bf_scan_workspace_size": (C.c_int, [i64, C.POINTER(sz)]),
     "bf_coo_to_csr_workspace_size": (C.c_int, [i64, i64, C.POINTER(sz)]),
     "bf_coo_to_csr": (C.c_int, [P_i64, P_i64, i64, i64, i64, P_i64, P_i32, vp, sz, vp]),
@@ -84,6 +85,7 @@ _SIGS = {
     "bf_expand_rows": (C.c_int, [P_i64, i64, i64, P_i64, vp]),
     "bf_split_item_capacity": (i64, [i64, i32, i32]),
     "bf_split_row_capacity": (i64, [i64, i32]),
+    "bf_split_row_items": (i64, [i64, i32]),
     "bf_split_plan_workspace_size": (C.c_int, [i64, C.POINTER(sz)]),
     "bf_split_plan": (C.c_int, [P_i64, i64, i32, i32, P_i32, P_i32, P_i32, i64, P_i32, i64, P_i32, vp, sz, vp]),
     "bf_split_plan_first_row": (C.c_int, [i64, i32, P_i32, P_i32, P_i32, i64, P_i32, i64, P_i32, vp]),
@@ -93,8 +95,10 @@ _SIGS = {
     "bf_row_order_and_plan": (C.c_int, [P_i64, i64, i32, i32, P_i32, vp, P_i32, P_i32, P_i32, i64, P_i32, i64,
                                         P_i32, vp, sz, vp]),
     "bf_attn_partials_floats": (i64, [C.POINTER(AttnIndex), i32, i32]),
+    "bf_attn_bwd_kv_variant": (C.c_int, [C.POINTER(AttnIndex), i32, i32, i32, C.POINTER(i32), C.POINTER(i32),
+                                         C.POINTER(i32)]),
     "bf_attn_fwd": (C.c_int, [C.POINTER(AttnIndex), i32, i32, i32, vp, vp, vp, P_f32, P_f32, vp, P_f32, P_f32, vp]),
-    "bf_attn_bwd": (C.c_int, [C.POINTER(AttnIndex), i32, i32, i32, vp, vp, vp, P_f32, P_f32, vp, P_f32, vp,
+    "bf_attn_bwd": (C.c_int, [C.POINTER(AttnIndex), i32, i32, i32, vp, vp, vp, P_f32, P_f32, P_f32, vp,
                               vp, vp, vp, P_f32, P_f32, P_f32, vp]),
 }
 

@@ -36,15 +36,16 @@ class _SparseEdgeAttention(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, bias_e, factor_e, index):
         out, Z = hip_ops.attn_forward(index, q, k, v, bias_e, factor_e)
-        ctx.save_for_backward(q, k, v, out, Z, bias_e, factor_e)
+        # the backward needs Z, not out (it sums Delta = dO . out from the entries in float32)
+        ctx.save_for_backward(q, k, v, Z, bias_e, factor_e)
         ctx.index = index
         ctx.need_dbias = bias_e is not None and ctx.needs_input_grad[3]
         return out
 
     @staticmethod
     def backward(ctx, dout):
-        q, k, v, out, Z, bias_e, factor_e = ctx.saved_tensors
-        dq, dk, dv, dbias = hip_ops.attn_backward(ctx.index, q, k, v, out, Z, dout.contiguous(), bias_e, factor_e,
+        q, k, v, Z, bias_e, factor_e = ctx.saved_tensors
+        dq, dk, dv, dbias = hip_ops.attn_backward(ctx.index, q, k, v, None, Z, dout.contiguous(), bias_e, factor_e,
                                                   need_dbias=ctx.need_dbias)
         return dq, dk, dv, dbias, None, None
 

@@ -17,7 +17,8 @@
 // nodes) are cut into items by a split plan; items write float partials that
 // a reduce sums in item order. Nothing uses atomics: results are deterministic
 // run to run. Launches per layer: forward (items + rows), forward reduce,
-// dq pass (items + rows), dk/dv pass (dq reduce + items + rows), dk/dv reduce.
+// dq pass (items + rows), dq reduce, dk/dv pass (items + rows), dk/dv reduce
+// (each reduce only when some split row has more than one item).
 //
 // MFMA is not used: each score is an hn-long dot product of two gathered rows,
 // not a dense contraction, and the kernels are bound by gather bandwidth.
@@ -99,6 +100,8 @@ __device__ __forceinline__ typename Elem<T>::Raw load_row_raw_nt(const T* base, 
 // its ids by lane shuffle, so the gathers wait for one id load per chunk
 // instead of one per iteration (chunks are a whole number of iterations).
 // float32: loaded per iteration (the id register would cost a wave per SIMD).
+// A group narrower than kUnroll lanes (bf16 rows of 8 or 16 elements) cannot
+// hold one iteration's ids and loads them per iteration as well (len = 0).
 template <typename T, int kUnroll>
 struct ChunkIds {
   static constexpr bool kChunk = sizeof(T) == 2;
@@ -106,11 +109,13 @@ struct ChunkIds {
   int64_t c0;
   int ids = 0;
   __device__ __forceinline__ ChunkIds(const Shape& sh, int64_t beg)
-      : lpr(1 << sh.lpr_log2), len(((1 << sh.lpr_log2) / kUnroll) * kUnroll), c0(beg - len) {}
+      : lpr(1 << sh.lpr_log2),
+        len((1 << sh.lpr_log2) >= kUnroll ? ((1 << sh.lpr_log2) / kUnroll) * kUnroll : 0),
+        c0(beg - len) {}
   // at the start of each chunk (uniform over the group): load its ids
   __device__ __forceinline__ void next(const int32_t* __restrict__ idx, int64_t e0, int64_t end, const GroupPos& g) {
     if constexpr (kChunk) {
-      if (e0 - c0 == len) {
+      if (len > 0 && e0 - c0 == len) {
         c0 = e0;
         ids = (g.g_lane < len && c0 + g.g_lane < end) ? idx[c0 + g.g_lane] : 0;
       }
@@ -119,10 +124,9 @@ struct ChunkIds {
   // id of entry e0 + u (every lane of the group calls it)
   __device__ __forceinline__ int get(const int32_t* __restrict__ idx, int64_t e0, int u, bool ok) const {
     if constexpr (kChunk) {
-      return __shfl(ids, int(e0 - c0) + u, lpr);
-    } else {
-      return ok ? idx[e0 + u] : 0;
+      if (len > 0) return __shfl(ids, int(e0 - c0) + u, lpr);
     }
+    return ok ? idx[e0 + u] : 0;
   }
 };
 // Accumulates sum_e p*f*v (acc) and sum_e p (z) over entries [beg, end) of one row.
@@ -292,9 +296,8 @@ __device__ __forceinline__ void store_record(const Items& it, int64_t item, cons
 // over the items with several records in flight each, then combined in group
 // order). Returns the row id, or -1 for a row with a single item (finished by
 // that item); the sums are valid in group 0. R records in flight per group:
-// the stand-alone reduce kernels take as many as their registers allow (the
-// 160 items of the token row in one round at D = 128), the dk/dv kernel's dq
-// reduces 8, which keep that kernel's register count.
+// as many as the reduce kernel's registers allow (the 160 items of the token
+// row in one round at D = 128 in the forward).
 template <int V, int R = 8>
 __device__ __forceinline__ int reduce_row_records(const Items& it, int64_t heavy, float* lds, const Shape& sh,
                                                   const GroupPos& g, float (&a)[V], float (&b)[V], bool with_b,
@@ -411,48 +414,69 @@ __global__ __launch_bounds__(kBlock) void attn_fwd_reduce_kernel(T* __restrict__
 }
 
 // ------------------------------------------------------------------ backward, query-major (dq)
-// Per-row constants of the backward: D' = Z + eps and Delta = sum_j dO*out per head.
-struct RowGrad {
-  float dprime;
-  float delta;
+// Per query row t and head, with D' = Z + eps, w_e = (dO_t . v_s) / D' and
+// m_e = [-5 <= a_pre <= 5] / sqrt(hn) per entry e = (s -> t):
+//   Delta  = sum_j dO_j out_j = sum_e p_e f_e w_e       (c below)
+//   g_b,e  = (f_e w_e - Delta / D') p_e                  (dbias: the bias is added after the clamp)
+//   dq_t   = sum_e g_b,e m_e k_s = A - (Delta / D') B,
+//            A = sum_e f_e w_e p_e m_e k_s,  B = sum_e p_e m_e k_s.
+// Delta is summed from the entries in the same loop as A and B, in float32,
+// instead of being read back from the output tensor: a bfloat16 `out` carries
+// its 2^-9 rounding into every g_b, which dominates the rows whose gradient
+// nearly cancels (the reference under autocast keeps `out` in float32), and the
+// pass no longer reads `out` at all.
+
+// One entry's per-head scalars (every lane of the head holds them).
+struct EntryTerms {
+  float p;   // exp(clamp(a) [+ bias])
+  float f;   // factor or 1
+  float w;   // (dO . v) / D'
+  float m;   // [inside the clamp] / sqrt(hn)
 };
 
-template <typename T>
-__device__ __forceinline__ RowGrad row_grad(const T* __restrict__ out, const T* __restrict__ dout,
-                                            const float* __restrict__ Z, int64_t row, const Shape& sh,
-                                            const GroupPos& g, typename Elem<T>::Raw& gr) {
-  gr = load_row_raw_nt(dout, row, sh.D, g);
-  const typename Elem<T>::Raw orow = load_row_raw_nt(out, row, sh.D, g);
-  RowGrad r;
-  r.delta = group_sum(Elem<T>::dot(gr, orow, 0.f), 1 << sh.lph_log2);
-  r.dprime = (g.act ? Z[row * sh.H + g.head] : 0.f) + kEps;
-  return r;
+template <bool EXTRA>
+__device__ __forceinline__ EntryTerms entry_terms(float d, float wraw, float inv_dprime,
+                                                  const float* __restrict__ bias,
+                                                  const float* __restrict__ factor, int64_t e, const Shape& sh,
+                                                  const GroupPos& g) {
+  EntryTerms t;
+  const float apre = d * sh.inv_scale;
+  float a = fminf(fmaxf(apre, -kClamp), kClamp);
+  if (EXTRA && bias) a += bias[e * sh.H + g.head];
+  t.p = __expf(a);   // a is clamped to [-5, 5] (+ bias): exp2-based form is within 2 ulp
+  t.f = (EXTRA && factor) ? factor[e * sh.H + g.head] : 1.f;
+  t.w = wraw * inv_dprime;
+  t.m = (apre >= -kClamp && apre <= kClamp) ? sh.inv_scale : 0.f;
+  return t;
 }
 
-// Per (query, head) record the key-major pass gathers: {1/D', Delta/D'} in one
-// float2, so each reverse entry touches one 64-byte stats line instead of two.
-__device__ __forceinline__ void store_row_stat(float2* __restrict__ rstat, int64_t row, const Shape& sh,
-                                               const GroupPos& g, const RowGrad& rg) {
-  const float inv = 1.0f / rg.dprime;
-  rstat[row * sh.H + g.head] = make_float2(inv, rg.delta * inv);
+template <int V>
+__device__ __forceinline__ void add_entry(const EntryTerms& t, const float (&kk)[V], float (&A)[V], float (&B)[V],
+                                          float& c) {
+  const float fwp = t.f * t.w * t.p;
+  const float ca = fwp * t.m, cb = t.p * t.m;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    A[i] = fmaf(ca, kk[i], A[i]);
+    B[i] = fmaf(cb, kk[i], B[i]);
+  }
+  c += fwp;
 }
 
-// dq contributions of entries [beg, end) of one query row; writes dbias per entry.
-template <typename T>
+// A, B and c over entries [beg, end) of one query row. EXTRA: with a bias or
+// factor (compiled in only for the instance that uses them).
+template <typename T, bool EXTRA>
 __device__ __forceinline__ void dq_segment(const T* __restrict__ k, const T* __restrict__ v,
                                            const int32_t* __restrict__ kv,
                                            const float* __restrict__ bias,
                                            const float* __restrict__ factor,
-                                           float* __restrict__ dbias, int64_t beg, int64_t end,
-                                           const Shape& sh, const GroupPos& g, const RowGrad& rg,
-                                           const typename Elem<T>::Raw& qr,
+                                           int64_t beg, int64_t end, const Shape& sh, const GroupPos& g,
+                                           float inv_dprime, const typename Elem<T>::Raw& qr,
                                            const typename Elem<T>::Raw& gr,
-                                           float (&dq)[Elem<T>::kPerVec]) {
+                                           float (&A)[Elem<T>::kPerVec], float (&B)[Elem<T>::kPerVec], float& c) {
   constexpr int V = Elem<T>::kPerVec;
   constexpr int kUnroll = Unroll<T>::q;
   const int lph = 1 << sh.lph_log2;
-  const float inv_dprime = 1.0f / rg.dprime;
-  const float gz = -rg.delta * inv_dprime;
   ChunkIds<T, kUnroll> ids(sh, beg);
   for (int64_t e0 = beg; e0 < end; e0 += kUnroll) {
     int s[kUnroll];
@@ -490,35 +514,34 @@ __device__ __forceinline__ void dq_segment(const T* __restrict__ k, const T* __r
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       if (!ok[u]) continue;
-      const int64_t e = e0 + u;
-      const float apre = d[u] * sh.inv_scale;
-      float a = fminf(fmaxf(apre, -kClamp), kClamp);
-      if (bias) a += bias[e * sh.H + g.head];
-      const float p = __expf(a);   // a is clamped to [-5, 5] (+ bias): exp2-based form is within 2 ulp
-      const float f = factor ? factor[e * sh.H + g.head] : 1.f;
-      const float gb = fmaf(f * w[u], inv_dprime, gz) * p;
-      if (dbias && g.lead) dbias[e * sh.H + g.head] = gb;
-      const float gs = (apre >= -kClamp && apre <= kClamp) ? gb * sh.inv_scale : 0.f;
+      const EntryTerms t = entry_terms<EXTRA>(d[u], w[u], inv_dprime, bias, factor, e0 + u, sh, g);
       float kk[V];
       Elem<T>::unpack(kr[u], kk);
-#pragma unroll
-      for (int i = 0; i < V; ++i) dq[i] = fmaf(gs, kk[i], dq[i]);
+      add_entry<V>(t, kk, A, B, c);
     }
   }
 }
 
-// The token-column entry (this row, key 0) at CSR position e, handled on its
-// own when the index has a token column: its dq term and dbias as dq_segment
-// computes them, plus the row's terms of key 0's gradients, fk = g_a*q/sqrt(hn)
-// and fv = p*f*dO/D' — the same products the dk/dv pass would form after
-// gathering this row's q, dO and row stats again.
-template <typename T>
-__device__ __forceinline__ void token_entry(const T* __restrict__ k, const T* __restrict__ v,
-                                            const float* __restrict__ bias, const float* __restrict__ factor,
-                                            float* __restrict__ dbias, int64_t e, const Shape& sh, const GroupPos& g,
-                                            const RowGrad& rg, const typename Elem<T>::Raw& qr,
-                                            const typename Elem<T>::Raw& gr, float (&dq)[Elem<T>::kPerVec],
-                                            float (&fk)[Elem<T>::kPerVec], float (&fv)[Elem<T>::kPerVec]) {
+// The key-0 entry (CSR position e) of a token-column row. ADD: also added to
+// A, B and c like any entry (a short row takes it first, so the sums keep the
+// order of the entries); its scalars finish key 0's gradient terms once the
+// row's Delta / D' is known (finish_token). A split row's items sum it in
+// order with the rest, and the step that finishes the row recomputes these
+// scalars without adding them again.
+struct TokenEntry {
+  float fw;    // f (dO . v_0), before the 1/D'
+  float p;
+  float f;
+  float m;     // [inside the clamp] / sqrt(hn)
+};
+
+template <typename T, bool EXTRA, bool ADD>
+__device__ __forceinline__ TokenEntry token_entry(const T* __restrict__ k, const T* __restrict__ v,
+                                                  const float* __restrict__ bias, const float* __restrict__ factor,
+                                                  int64_t e, const Shape& sh, const GroupPos& g, float inv_dprime,
+                                                  const typename Elem<T>::Raw& qr, const typename Elem<T>::Raw& gr,
+                                                  float (&A)[Elem<T>::kPerVec], float (&B)[Elem<T>::kPerVec],
+                                                  float& c) {
   constexpr int V = Elem<T>::kPerVec;
   const typename Elem<T>::Raw kr = load_row_raw(k, 0, sh.D, g), vr = load_row_raw(v, 0, sh.D, g);
   float d = Elem<T>::dot(kr, qr, 0.f), w = Elem<T>::dot(vr, gr, 0.f);
@@ -526,25 +549,70 @@ __device__ __forceinline__ void token_entry(const T* __restrict__ k, const T* __
     d += __shfl_xor(d, o, 64);
     w += __shfl_xor(w, o, 64);
   }
-  const float inv_dprime = 1.0f / rg.dprime;
-  const float apre = d * sh.inv_scale;
-  float a = fminf(fmaxf(apre, -kClamp), kClamp);
-  if (bias) a += bias[e * sh.H + g.head];
-  const float p = __expf(a);
-  const float f = factor ? factor[e * sh.H + g.head] : 1.f;
-  const float gb = fmaf(f * w, inv_dprime, -rg.delta * inv_dprime) * p;
-  if (dbias && g.lead) dbias[e * sh.H + g.head] = gb;
-  const float gs = (apre >= -kClamp && apre <= kClamp) ? gb * sh.inv_scale : 0.f;
-  const float pf = p * f * inv_dprime;
-  float kk[V], qq[V], gg[V];
-  Elem<T>::unpack(kr, kk);
+  const EntryTerms t = entry_terms<EXTRA>(d, w, inv_dprime, bias, factor, e, sh, g);
+  if (ADD) {
+    float kk[V];
+    Elem<T>::unpack(kr, kk);
+    add_entry<V>(t, kk, A, B, c);
+  }
+  return TokenEntry{t.f * w, t.p, t.f, t.m};
+}
+
+// Key 0's terms from this row, dd = Delta / D': fk = g_b m q (its dK term),
+// fv = p f dO / D' (its dV term); and its dbias g_b at CSR position e. The
+// same expressions the key-major pass evaluates for an entry it gathers.
+template <typename T, bool EXTRA>
+__device__ __forceinline__ void finish_token(const TokenEntry& te, float inv_dprime, float dd,
+                                             const typename Elem<T>::Raw& qr, const typename Elem<T>::Raw& gr,
+                                             float* __restrict__ dbias, int64_t e, const Shape& sh, const GroupPos& g,
+                                             float (&fk)[Elem<T>::kPerVec], float (&fv)[Elem<T>::kPerVec]) {
+  constexpr int V = Elem<T>::kPerVec;
+  const float gb = fmaf(te.fw, inv_dprime, -dd) * te.p;
+  if (EXTRA && dbias && g.lead) dbias[e * sh.H + g.head] = gb;
+  const float gs = gb * te.m;
+  const float pf = te.p * te.f * inv_dprime;
+  float qq[V], gg[V];
   Elem<T>::unpack(qr, qq);
   Elem<T>::unpack(gr, gg);
 #pragma unroll
   for (int i = 0; i < V; ++i) {
-    dq[i] = fmaf(gs, kk[i], dq[i]);
     fk[i] = gs * qq[i];
     fv[i] = pf * gg[i];
+  }
+}
+
+// dq = A - dd B of a finished row and its row stats {1/D', Delta/D'}, which the key-major pass gathers
+// (one 8-byte record per query and head, so each reverse entry touches one stats line).
+template <typename T, int V>
+__device__ __forceinline__ void store_dq(T* __restrict__ dq, float2* __restrict__ rstat, int64_t row, const Shape& sh,
+                                         const GroupPos& g, const float (&A)[V], const float (&B)[V], float inv_dprime,
+                                         float dd, bool nt) {
+  if (!g.act) return;
+  float o[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) o[i] = fmaf(-dd, B[i], A[i]);
+  if (nt)
+    Elem<T>::store_nt(dq + row * sh.D + g.col0, o);
+  else
+    Elem<T>::store(dq + row * sh.D + g.col0, o);
+  if (g.lead) rstat[row * sh.H + g.head] = make_float2(inv_dprime, dd);
+}
+
+template <typename T>
+__device__ __forceinline__ float row_inv_dprime(const float* __restrict__ Z, int64_t row, const Shape& sh,
+                                                const GroupPos& g) {
+  return 1.0f / ((g.act ? Z[row * sh.H + g.head] : 0.f) + kEps);
+}
+
+// Writes one token-column record (2*D floats: key 0's dK terms, then its dV terms).
+template <int V>
+__device__ __forceinline__ void store_token_record(float* __restrict__ rec, const Shape& sh, const GroupPos& g,
+                                                   const float (&fk)[V], const float (&fv)[V]) {
+  if (!g.act) return;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    rec[g.col0 + i] = fk[i];
+    rec[sh.D + g.col0 + i] = fv[i];
   }
 }
 
@@ -568,62 +636,54 @@ __device__ __forceinline__ void sum_token_records(const float* __restrict__ rec0
 }
 
 // Blocks [0, n_items) take the query-side items, the rest one short query row per group.
-template <typename T>
+// With a token column (rows from tok_first on open with key 0) every workgroup also writes one
+// record of its rows' key-0 terms; a split row's key-0 terms are finished with the row: by its item
+// when the row has one, else by the dq reduce, which writes them into the row's first item's record.
+template <typename T, bool EXTRA>
 __global__ __launch_bounds__(kBlock) void attn_bwd_q_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const int64_t* __restrict__ qptr, const int32_t* __restrict__ kv,
     const float* __restrict__ bias, const float* __restrict__ factor,
-    const T* __restrict__ out, const float* __restrict__ Z, const T* __restrict__ dout,
+    const float* __restrict__ Z, const T* __restrict__ dout,
     T* __restrict__ dq, float* __restrict__ dbias, float2* __restrict__ rstat, Items it, int n_items_arg,
-    int64_t n_q, Shape sh, int chunk, float* __restrict__ token_rec, const int32_t* __restrict__ plan_counts) {
+    int64_t n_q, Shape sh, int chunk, float* __restrict__ token_rec, int tok_first,
+    const int32_t* __restrict__ plan_counts) {
   constexpr int V = Elem<T>::kPerVec;
   extern __shared__ float lds[];
   const GroupPos g = group_pos<T>(sh);
   const int grp = threadIdx.x >> sh.lpr_log2;
-  // blocks [0, n_items_arg) are item slots (the capacity when the counts are on the device: an unused
-  // slot exits at once and writes no token record), the rest one short row per group
-  float acc[V];
+  float A[V], B[V], c = 0.f;
 #pragma unroll
-  for (int i = 0; i < V; ++i) acc[i] = 0.f;
-  typename Elem<T>::Raw gr;
-  // With a token column every workgroup writes one record of its rows' key-0 terms (fk, fv: the
-  // row's g_a*q/sqrt(hn) and p*f*dO/D'), kept out of the registers of the main loop.
+  for (int i = 0; i < V; ++i) A[i] = B[i] = 0.f;
   if (int(blockIdx.x) < n_items_arg) {
+    // blocks [0, n_items_arg) are item slots (the capacity when the counts are on the device: an unused
+    // slot exits at once and writes no token record)
     if (plan_counts && int(blockIdx.x) >= plan_counts[0]) return;
     const ItemRange r = item_group_range(it, sh, blockIdx.x);
-    float unused[V];
-#pragma unroll
-    for (int i = 0; i < V; ++i) unused[i] = 0.f;
     const typename Elem<T>::Raw qr = load_row_raw(q, r.row, sh.D, g);
-    const RowGrad rg = row_grad<T>(out, dout, Z, r.row, sh, g, gr);
-    int64_t beg = r.beg;
-    if (token_rec && grp == 0) {
-      // a token-column row opens with key 0, in group 0's range of the row's first item
-      float fk[V], fv[V];
+    const typename Elem<T>::Raw gr = load_row_raw(dout, r.row, sh.D, g);
+    const float inv_dprime = row_inv_dprime<T>(Z, r.row, sh, g);
+    const int64_t e_tok = it.ptr[r.row];
+    const bool tok_row = token_rec != nullptr && r.row >= tok_first && e_tok < it.ptr[r.row + 1];
+    dq_segment<T, EXTRA>(k, v, kv, bias, factor, r.beg, r.end, sh, g, inv_dprime, qr, gr, A, B, c);
+    block_combine<V>(lds, it.stride, sh, g, A, B, true, c, true);
+    float fk[V], fv[V];
 #pragma unroll
-      for (int i = 0; i < V; ++i) fk[i] = fv[i] = 0.f;
-      if (r.row > 0 && beg < r.end && beg == it.ptr[r.row]) {
-        token_entry<T>(k, v, bias, factor, dbias, beg, sh, g, rg, qr, gr, acc, fk, fv);
-        ++beg;
-      }
-      if (g.act) {
-        float* rec = token_rec + int64_t(blockIdx.x) * (2 * sh.D);
-#pragma unroll
-        for (int i = 0; i < V; ++i) {
-          rec[g.col0 + i] = fk[i];
-          rec[sh.D + g.col0 + i] = fv[i];
-        }
-      }
-    }
-    dq_segment<T>(k, v, kv, bias, factor, dbias, beg, r.end, sh, g, rg, qr, gr, acc);
-    float z = 0.f;
-    block_combine<V>(lds, it.stride, sh, g, acc, unused, false, z, false);
+    for (int i = 0; i < V; ++i) fk[i] = fv[i] = 0.f;
     if (r.single) {
-      if (grp == 0 && g.act) Elem<T>::store(dq + int64_t(r.row) * sh.D + g.col0, acc);
+      if (grp == 0) {
+        const float dd = c * inv_dprime;
+        if (tok_row) {
+          const TokenEntry te = token_entry<T, EXTRA, false>(k, v, bias, factor, e_tok, sh, g, inv_dprime, qr, gr,
+                                                             A, B, c);
+          finish_token<T, EXTRA>(te, inv_dprime, dd, qr, gr, dbias, e_tok, sh, g, fk, fv);
+        }
+        store_dq<T, V>(dq, rstat, r.row, sh, g, A, B, inv_dprime, dd, false);
+      }
     } else {
-      store_record<V>(it, blockIdx.x, sh, g, acc, unused, false, z, false);
+      store_record<V>(it, blockIdx.x, sh, g, A, B, true, c, true);
     }
-    if (r.j == 0 && grp == 0 && g.lead) store_row_stat(rstat, r.row, sh, g, rg);
+    if (token_rec && grp == 0) store_token_record<V>(token_rec + int64_t(blockIdx.x) * (2 * sh.D), sh, g, fk, fv);
     return;
   }
   const int64_t row = row_slot(sh, unsigned(n_items_arg));
@@ -635,45 +695,40 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_q_kernel(
     live = end - beg <= chunk;    // a split row: its items and the reduce write it
   }
   if (!token_rec && !live) return;
-  typename Elem<T>::Raw qr = Elem<T>::zero_raw();
-  RowGrad rg{1.f, 0.f};
+  typename Elem<T>::Raw qr = Elem<T>::zero_raw(), gr = Elem<T>::zero_raw();
+  float inv_dprime = 1.f;
   if (live) {
     qr = load_row_raw_nt(q, row, sh.D, g);
-    rg = row_grad<T>(out, dout, Z, row, sh, g, gr);
+    gr = load_row_raw_nt(dout, row, sh.D, g);
+    inv_dprime = row_inv_dprime<T>(Z, row, sh, g);
   }
-  if (token_rec) {
-    float fk[V], fv[V];
-#pragma unroll
-    for (int i = 0; i < V; ++i) fk[i] = fv[i] = 0.f;
-    if (live && row > 0 && beg < end) {
-      token_entry<T>(k, v, bias, factor, dbias, beg, sh, g, rg, qr, gr, acc, fk, fv);
-      ++beg;
-    }
-    // sum the wave's groups (a fixed butterfly), then park the wave's sum in LDS
-    for (int o = 1 << sh.lpr_log2; o < 64; o <<= 1) {
-#pragma unroll
-      for (int i = 0; i < V; ++i) {
-        fk[i] += __shfl_xor(fk[i], o, 64);
-        fv[i] += __shfl_xor(fv[i], o, 64);
-      }
-    }
-    if ((threadIdx.x & 63) < (1 << sh.lpr_log2) && g.act) {
-      float* slot = lds + (threadIdx.x >> 6) * (2 * sh.D);
-#pragma unroll
-      for (int i = 0; i < V; ++i) {
-        slot[g.col0 + i] = fk[i];
-        slot[sh.D + g.col0 + i] = fv[i];
-      }
-    }
+  const bool tok = token_rec != nullptr && live && row >= tok_first && beg < end;
+  const int64_t e_tok = beg;
+  TokenEntry te{};
+  if (tok) {
+    te = token_entry<T, EXTRA, true>(k, v, bias, factor, e_tok, sh, g, inv_dprime, qr, gr, A, B, c);
+    ++beg;
   }
+  float dd = 0.f;
   if (live) {
-    dq_segment<T>(k, v, kv, bias, factor, dbias, beg, end, sh, g, rg, qr, gr, acc);
-    if (g.act) {
-      Elem<T>::store_nt(dq + row * sh.D + g.col0, acc);
-      if (g.lead) store_row_stat(rstat, row, sh, g, rg);
-    }
+    dq_segment<T, EXTRA>(k, v, kv, bias, factor, beg, end, sh, g, inv_dprime, qr, gr, A, B, c);
+    dd = c * inv_dprime;
+    store_dq<T, V>(dq, rstat, row, sh, g, A, B, inv_dprime, dd, true);
   }
   if (!token_rec) return;
+  float fk[V], fv[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) fk[i] = fv[i] = 0.f;
+  if (tok) finish_token<T, EXTRA>(te, inv_dprime, dd, qr, gr, dbias, e_tok, sh, g, fk, fv);
+  // sum the wave's groups (a fixed butterfly), park the wave's sum in LDS, then the waves in order
+  for (int o = 1 << sh.lpr_log2; o < 64; o <<= 1) {
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      fk[i] += __shfl_xor(fk[i], o, 64);
+      fv[i] += __shfl_xor(fv[i], o, 64);
+    }
+  }
+  if ((threadIdx.x & 63) < (1u << sh.lpr_log2)) store_token_record<V>(lds + (threadIdx.x >> 6) * (2 * sh.D), sh, g, fk, fv);
   __syncthreads();
   if (threadIdx.x < (1u << sh.lpr_log2) && g.act) {   // the workgroup's record: its waves in order
     float sk[V], sv[V];
@@ -687,12 +742,42 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_q_kernel(
         sv[i] += slot[sh.D + g.col0 + i];
       }
     }
-    float* rec = token_rec + int64_t(blockIdx.x) * (2 * sh.D);
+    store_token_record<V>(token_rec + int64_t(blockIdx.x) * (2 * sh.D), sh, g, sk, sv);
+  }
+}
+
+// One workgroup per query-side split row with more than one item: sums the
+// items' records {A, B, c} in item order and finishes the row, writing dq, the
+// row stats and, for a token-column row, key 0's terms (and dbias) into the
+// record of the row's first item. Runs between the dq pass and the key-major
+// pass, which gathers the row stats.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void attn_bwd_q_reduce_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, const float* __restrict__ bias,
+    const float* __restrict__ factor, const float* __restrict__ Z, const T* __restrict__ dout, T* __restrict__ dq,
+    float* __restrict__ dbias, float2* __restrict__ rstat, Items it, Shape sh, float* __restrict__ token_rec,
+    int tok_first, const int32_t* __restrict__ plan_counts) {
+  constexpr int V = Elem<T>::kPerVec;
+  if (plan_counts && int(blockIdx.x) >= plan_counts[1]) return;
+  extern __shared__ float lds[];
+  const GroupPos g = group_pos<T>(sh);
+  float A[V], B[V], c;
+  const int row = reduce_row_records<V, 40 / V>(it, blockIdx.x, lds, sh, g, A, B, true, c, true);
+  if (row < 0 || (threadIdx.x >> sh.lpr_log2) != 0) return;
+  const float inv_dprime = row_inv_dprime<T>(Z, row, sh, g);
+  const int64_t e_tok = it.ptr[row];
+  const bool tok = token_rec != nullptr && row >= tok_first && e_tok < it.ptr[row + 1];
+  float fk[V], fv[V];
 #pragma unroll
-    for (int i = 0; i < V; ++i) {
-      rec[g.col0 + i] = sk[i];
-      rec[sh.D + g.col0 + i] = sv[i];
-    }
+  for (int i = 0; i < V; ++i) fk[i] = fv[i] = 0.f;
+  const float dd = c * inv_dprime;
+  store_dq<T, V>(dq, rstat, row, sh, g, A, B, inv_dprime, dd, false);
+  if (tok) {   // key 0 was summed by item 0; its scalars are recomputed here to finish its terms
+    const typename Elem<T>::Raw qr = load_row_raw(q, row, sh.D, g);
+    const typename Elem<T>::Raw gr = load_row_raw(dout, row, sh.D, g);
+    const TokenEntry te = token_entry<T, true, false>(k, v, bias, factor, e_tok, sh, g, inv_dprime, qr, gr, A, B, c);
+    finish_token<T, true>(te, inv_dprime, dd, qr, gr, dbias, e_tok, sh, g, fk, fv);
+    store_token_record<V>(token_rec + int64_t(it.item_off[row]) * (2 * sh.D), sh, g, fk, fv);
   }
 }
 
@@ -709,12 +794,18 @@ __device__ __forceinline__ typename Elem<T>::Raw gather_row(const T* base, int64
   return NT ? Elem<T>::load_raw_nt(base + row * D + col0) : Elem<T>::load_raw(base + row * D + col0);
 }
 
-template <typename T, bool NT>
+// dK and dV of one kv row over its reverse entries [beg, end); with dbias, each
+// entry's g_b = (f w - Delta/D') p at its CSR position (the row stats carry the
+// exact Delta/D' the dq pass summed). EXTRA: the per-entry bias, factor and
+// dbias are compiled in only for the instance that uses them, so the plain
+// pass keeps its register count (fp32: 95 VGPRs, five waves per SIMD).
+template <typename T, bool NT, bool EXTRA>
 __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __restrict__ dout,
                                             const int32_t* __restrict__ kq,
                                             const int32_t* __restrict__ ke,
                                             const float* __restrict__ bias,
                                             const float* __restrict__ factor,
+                                            float* __restrict__ dbias,
                                             const float2* __restrict__ rstat, int64_t beg,
                                             int64_t end, const Shape& sh, const GroupPos& g,
                                             const typename Elem<T>::Raw& krow,
@@ -724,7 +815,6 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
   constexpr int V = Elem<T>::kPerVec;
   constexpr int kUnroll = Unroll<T>::kv;
   const int lph = 1 << sh.lph_log2;
-  const bool need_e = bias != nullptr || factor != nullptr;
   ChunkIds<T, kUnroll> ids(sh, beg);
   for (int64_t i0 = beg; i0 < end; i0 += kUnroll) {
     int t[kUnroll];
@@ -765,13 +855,14 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       if (!ok[u]) continue;
-      const int64_t e = need_e ? int64_t(ke[i0 + u]) : 0;
+      const int64_t e = EXTRA ? int64_t(ke[i0 + u]) : 0;
       const float apre = d[u] * sh.inv_scale;
       float a = fminf(fmaxf(apre, -kClamp), kClamp);
-      if (bias) a += bias[e * sh.H + g.head];
+      if (EXTRA && bias) a += bias[e * sh.H + g.head];
       const float p = __expf(a);   // a is clamped to [-5, 5] (+ bias): exp2-based form is within 2 ulp
-      const float f = factor ? factor[e * sh.H + g.head] : 1.f;
+      const float f = (EXTRA && factor) ? factor[e * sh.H + g.head] : 1.f;
       const float gb = fmaf(f * w[u], rs[u].x, -rs[u].y) * p;   // rs = {1/D', Delta/D'}
+      if (EXTRA && dbias && g.lead) dbias[e * sh.H + g.head] = gb;
       const float gs = (apre >= -kClamp && apre <= kClamp) ? gb * sh.inv_scale : 0.f;
       const float pf = p * f * rs[u].x;
       float qq[V], gg[V];
@@ -786,42 +877,34 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
   }
 }
 
-// Blocks [0, q_heavy) reduce the query-side split rows into dq (their items ran
-// in the dq pass), blocks [q_heavy, q_heavy + k_items) take the key-side items,
-// the rest one short key row per group, longest rows first.
-template <typename T, bool NT, bool PRE>
+// Blocks [0, k_items) take the key-side items, the rest one short key row per
+// group, longest rows first. EXTRA: with a bias, factor or dbias (needs ke).
+template <typename T, bool NT, bool PRE, bool EXTRA>
 __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const int64_t* __restrict__ kptr, const int32_t* __restrict__ kq,
     const int32_t* __restrict__ ke, const float* __restrict__ bias,
-    const float* __restrict__ factor, const T* __restrict__ dout, const float2* __restrict__ rstat,
-    T* __restrict__ dq, T* __restrict__ dk, T* __restrict__ dv, const int32_t* __restrict__ order,
-    const uint64_t* __restrict__ spans,
-    Items qit, int q_heavy_arg, Items kit, int k_items_arg, int64_t n_kv, Shape sh, int chunk, int rows_per_group,
-    const float* __restrict__ token_rec, int q_items_arg, int64_t q_row_blocks, const int32_t* __restrict__ plan_counts) {
+    const float* __restrict__ factor, float* __restrict__ dbias, const T* __restrict__ dout,
+    const float2* __restrict__ rstat, T* __restrict__ dk, T* __restrict__ dv, const int32_t* __restrict__ order,
+    const uint64_t* __restrict__ spans, Items kit, int k_items_arg, int64_t n_kv, Shape sh, int chunk,
+    int rows_per_group, const float* __restrict__ token_rec, int q_items_arg, int64_t q_row_blocks,
+    const int32_t* __restrict__ plan_counts) {
   constexpr int V = Elem<T>::kPerVec;
   extern __shared__ float lds[];
   const GroupPos g = group_pos<T>(sh);
-  // Block regions: [0, q_heavy_arg) dq split-row reduces, then k_items_arg key-side item slots, then
-  // the short key rows. With the counts on the device the *_arg values are capacities and a slot past
-  // the true count exits at once (early in the dispatch, beside the running items).
+  // Block regions: k_items_arg key-side item slots, then the short key rows. With the counts on the
+  // device k_items_arg is a capacity and a slot past the true count exits at once (early in the
+  // dispatch, beside the running items).
   const int q_items = plan_counts ? plan_counts[0] : q_items_arg;
   // token-column records: the dq pass's q_items item workgroups, then its q_row_blocks row workgroups
   // (whose records start at slot q_items_arg; sum_token_records maps record m to its slot)
   const int64_t n_token_rec = q_items + q_row_blocks;
   float ak[V], av[V];
   const int b = int(blockIdx.x);
-  if (b < q_heavy_arg) {
-    if (plan_counts && b >= plan_counts[1]) return;
-    float z;
-    const int row = reduce_row_records<V>(qit, b, lds, sh, g, ak, av, false, z, false);
-    if (row >= 0 && (threadIdx.x >> sh.lpr_log2) == 0 && g.act) Elem<T>::store(dq + int64_t(row) * sh.D + g.col0, ak);
-    return;
-  }
 #pragma unroll
   for (int i = 0; i < V; ++i) ak[i] = av[i] = 0.f;
-  if (b < q_heavy_arg + k_items_arg) {
-    const int64_t item = b - q_heavy_arg;
+  if (b < k_items_arg) {
+    const int64_t item = b;
     if (plan_counts && item >= plan_counts[2]) return;
     const ItemRange r = item_group_range(kit, sh, item);
     if (token_rec && r.row == 0) {
@@ -835,7 +918,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
       sum_token_records<V>(token_rec, a0, a1, q_items, q_items_arg, sh, g, ak, av);
     } else {
       const typename Elem<T>::Raw kr = load_row_raw(k, r.row, sh.D, g), vr = load_row_raw(v, r.row, sh.D, g);
-      dkv_segment<T, NT>(q, dout, kq, ke, bias, factor, rstat, r.beg, r.end, sh, g, kr, vr, ak, av);
+      dkv_segment<T, NT, EXTRA>(q, dout, kq, ke, bias, factor, dbias, rstat, r.beg, r.end, sh, g, kr, vr, ak, av);
     }
     float z = 0.f;
     block_combine<V>(lds, kit.stride, sh, g, ak, av, true, z, false);
@@ -850,7 +933,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
     return;
   }
   // each group takes rows_per_group consecutive rows of the order (similar lengths)
-  const int64_t first = row_slot(sh, unsigned(q_heavy_arg + k_items_arg)) * rows_per_group;
+  const int64_t first = row_slot(sh, unsigned(k_items_arg)) * rows_per_group;
   const int64_t last = first + rows_per_group < n_kv ? first + rows_per_group : n_kv;
   // With several rows per group their slots come in one round of loads: lane i of the group reads
   // slot first + i and each iteration takes its row and span from that lane, so a row's wait for its
@@ -906,7 +989,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
 #pragma unroll
     for (int i = 0; i < V; ++i) ak[i] = av[i] = 0.f;
     const typename Elem<T>::Raw kr = load_row_raw(k, row, sh.D, g), vr = load_row_raw(v, row, sh.D, g);
-    dkv_segment<T, NT>(q, dout, kq, ke, bias, factor, rstat, beg, end, sh, g, kr, vr, ak, av);
+    dkv_segment<T, NT, EXTRA>(q, dout, kq, ke, bias, factor, dbias, rstat, beg, end, sh, g, kr, vr, ak, av);
     if (g.act) {                  // written once, not read again in the pass: past the caches
       Elem<T>::store_nt(dk + row * sh.D + g.col0, ak);
       Elem<T>::store_nt(dv + row * sh.D + g.col0, av);
@@ -965,6 +1048,7 @@ int check_index(const bf_attn_index* idx, bool backward) {
   BF_CHECK_ARG(idx->chunk >= 1 && idx->item >= 1, "attention: chunk and item must be >= 1");
   BF_CHECK_ARG(idx->qptr && (idx->kv || idx->nnz == 0), "attention: qptr/kv missing");
   BF_CHECK_ARG(idx->q_items >= 0 && idx->q_heavy >= 0, "attention: bad query-side plan counts");
+  BF_CHECK_ARG(idx->token_column >= 0 && idx->token_column <= 2, "attention: token_column must be 0, 1 or 2");
   BF_CHECK_ARG(idx->q_items == 0 || (idx->q_nitems && idx->q_item_off && idx->q_item_row && idx->q_heavy_rows),
                "attention: query-side split plan missing");
   if (backward) {
@@ -1040,40 +1124,59 @@ int fwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
 
 template <typename T>
 int bwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const void* k, const void* v,
-             const float* bias, const float* factor, const void* out, const float* Z,
-             const void* dout, void* dq, void* dk, void* dv, float* dbias, float* rstat_f,
-             float* partials, hipStream_t st) {
+             const float* bias, const float* factor, const float* Z, const void* dout, void* dq, void* dk, void* dv,
+             float* dbias, float* rstat_f, float* partials, hipStream_t st) {
   float2* rstat = reinterpret_cast<float2*>(rstat_f);
   const T* Q = static_cast<const T*>(q);
   const T* K = static_cast<const T*>(k);
   const T* Vv = static_cast<const T*>(v);
-  const T* O = static_cast<const T*>(out);
   const T* dO = static_cast<const T*>(dout);
   const Items qit = query_items(idx, sh, partials);
   const Items kit = key_items(idx, sh, partials);
   const int64_t q_blocks = int64_t(idx->q_items) + grid_for(idx->n_q, sh);
+  const int tok_first = idx->token_column == 2 ? 0 : 1;
   // token column: one record of key 0's terms per dq-pass workgroup, after the item records
   float* token_rec = idx->token_column && idx->n_kv > 0 && q_blocks > 0
                          ? partials + (int64_t(idx->q_items) + idx->k_items) * (2 * sh.D + sh.H)
                          : nullptr;
   if (q_blocks > 0) {
     const size_t lds = (idx->q_items > 0 || token_rec) ? combine_lds_bytes(sh) : 0;
-    BF_LAUNCH("attn_bwd_q_kernel", attn_bwd_q_kernel<T>, dim3(unsigned(q_blocks)), dim3(kBlock), lds, st, Q, K, Vv,
-              idx->qptr, idx->kv, bias, factor, O, Z, dO, static_cast<T*>(dq), dbias, rstat, qit, idx->q_items,
-              idx->n_q, sh, idx->chunk, token_rec, idx->plan_counts);
+#define BF_LAUNCH_Q(EX)                                                                                          \
+  BF_LAUNCH("attn_bwd_q_kernel", (attn_bwd_q_kernel<T, EX>), dim3(unsigned(q_blocks)), dim3(kBlock), lds, st, Q, K, \
+            Vv, idx->qptr, idx->kv, bias, factor, Z, dO, static_cast<T*>(dq), dbias, rstat, qit, idx->q_items,      \
+            idx->n_q, sh, idx->chunk, token_rec, tok_first, idx->plan_counts)
+    if (bias || factor || dbias)
+      BF_LAUNCH_Q(true);
+    else
+      BF_LAUNCH_Q(false);
+#undef BF_LAUNCH_Q
+    BF_CHECK_LAUNCH();
+  }
+  // the query-side split rows finish (dq, row stats) before the key-major pass gathers their stats
+  if (idx->q_heavy > 0) {
+    BF_LAUNCH("attn_bwd_q_reduce_kernel", attn_bwd_q_reduce_kernel<T>, dim3(unsigned(idx->q_heavy)), dim3(kBlock),
+              combine_lds_bytes(sh), st, Q, K, Vv, bias, factor, Z, dO, static_cast<T*>(dq), dbias, rstat, qit, sh,
+              token_rec, tok_first, idx->plan_counts);
     BF_CHECK_LAUNCH();
   }
   const int rows_per_group = kv_rows_per_group(idx->n_kv, sizeof(T));
-  const int64_t kv_blocks = int64_t(idx->q_heavy) + idx->k_items + grid_for(ceil_div(idx->n_kv, rows_per_group), sh);
+  const int64_t kv_blocks = int64_t(idx->k_items) + grid_for(ceil_div(idx->n_kv, rows_per_group), sh);
   if (kv_blocks > 0) {
-    const size_t lds = (idx->q_heavy > 0 || idx->k_items > 0) ? combine_lds_bytes(sh) : 0;
+    const size_t lds = idx->k_items > 0 ? combine_lds_bytes(sh) : 0;
     const bool stream_rows = size_t(idx->n_q) * size_t(sh.D) * sizeof(T) * 2 > kStreamBytes;
-#define BF_LAUNCH_KV(NT, PRE)                                                                                      \
-  BF_LAUNCH("attn_bwd_kv_kernel", (attn_bwd_kv_kernel<T, NT, PRE>), dim3(unsigned(kv_blocks)), dim3(kBlock), lds, st, \
-            Q, K, Vv, idx->kptr, idx->kq, idx->ke, bias, factor, dO, rstat, static_cast<T*>(dq), static_cast<T*>(dk),       \
-            static_cast<T*>(dv), idx->k_order, idx->k_spans, qit, idx->q_heavy, kit, idx->k_items, idx->n_kv, sh,     \
-            idx->chunk,                                                                                              \
+    const bool extra = bias != nullptr || factor != nullptr || dbias != nullptr;
+#define BF_LAUNCH_KV1(NT, PRE, EX)                                                                                 \
+  BF_LAUNCH("attn_bwd_kv_kernel", (attn_bwd_kv_kernel<T, NT, PRE, EX>), dim3(unsigned(kv_blocks)), dim3(kBlock), lds, st, \
+            Q, K, Vv, idx->kptr, idx->kq, idx->ke, bias, factor, dbias, dO, rstat, static_cast<T*>(dk),              \
+            static_cast<T*>(dv), idx->k_order, idx->k_spans, kit, idx->k_items, idx->n_kv, sh, idx->chunk,           \
             rows_per_group, token_rec, idx->q_items, int64_t(grid_for(idx->n_q, sh)), idx->plan_counts)
+#define BF_LAUNCH_KV(NT, PRE)           \
+  do {                                  \
+    if (extra)                          \
+      BF_LAUNCH_KV1(NT, PRE, true);     \
+    else                                \
+      BF_LAUNCH_KV1(NT, PRE, false);    \
+  } while (0)
     if constexpr (sizeof(T) == 2) {
       // the group's slots prefetched (several rows per group)
       const bool pre = rows_per_group > 1 && rows_per_group <= (1 << sh.lpr_log2);
@@ -1092,6 +1195,7 @@ int bwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
         BF_LAUNCH_KV(false, false);
     }
 #undef BF_LAUNCH_KV
+#undef BF_LAUNCH_KV1
     BF_CHECK_LAUNCH();
   }
   if (idx->k_heavy > 0) {
@@ -1123,6 +1227,21 @@ extern "C" int64_t bf_attn_partials_floats(const bf_attn_index* idx, int32_t num
   return floats;
 }
 
+extern "C" int bf_attn_bwd_kv_variant(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
+                                      int32_t* rows_per_group, int32_t* stream_rows, int32_t* prefetch_slots) {
+  Shape sh;
+  int rc = make_shape(dtype, num_heads, head_dim, sh);
+  if (rc) return rc;
+  BF_CHECK_ARG(idx && idx->n_q >= 0 && idx->n_kv >= 0, "attn_bwd_kv_variant: bad index");
+  BF_CHECK_ARG(rows_per_group && stream_rows && prefetch_slots, "attn_bwd_kv_variant: null output");
+  const size_t s = dtype == BF_DTYPE_F32 ? sizeof(float) : sizeof(uint16_t);
+  const int rpg = kv_rows_per_group(idx->n_kv, s);
+  *rows_per_group = rpg;
+  *stream_rows = size_t(idx->n_q) * size_t(sh.D) * s * 2 > kStreamBytes ? 1 : 0;
+  *prefetch_slots = (s == 2 && rpg > 1 && rpg <= (1 << sh.lpr_log2)) ? 1 : 0;
+  return BF_OK;
+}
+
 extern "C" int bf_attn_fwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
                            const void* q, const void* k, const void* v, const float* bias,
                            const float* factor, void* out, float* Z, float* partials, void* stream) {
@@ -1141,25 +1260,25 @@ extern "C" int bf_attn_fwd(const bf_attn_index* idx, int32_t dtype, int32_t num_
 
 extern "C" int bf_attn_bwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
                            const void* q, const void* k, const void* v, const float* bias,
-                           const float* factor, const void* out, const float* Z, const void* dout,
+                           const float* factor, const float* Z, const void* dout,
                            void* dq, void* dk, void* dv, float* dbias, float* rowstat, float* partials,
                            void* stream) {
   Shape sh;
   int rc = make_shape(dtype, num_heads, head_dim, sh);
   if (rc) return rc;
   if ((rc = check_index(idx, true))) return rc;
-  BF_CHECK_ARG(idx->ke || idx->nnz == 0 || (!bias && !factor),
-               "attn_bwd: a bias or factor needs the reverse entries' CSR positions (ke)");
-  BF_CHECK_ARG(q && k && v && out && Z && dout && dq && dk && dv && rowstat, "attn_bwd: null tensor");
+  BF_CHECK_ARG(idx->ke || idx->nnz == 0 || (!bias && !factor && !dbias),
+               "attn_bwd: a bias, factor or dbias needs the reverse entries' CSR positions (ke)");
+  BF_CHECK_ARG(q && k && v && Z && dout && dq && dk && dv && rowstat, "attn_bwd: null tensor");
   BF_CHECK_ARG((reinterpret_cast<uintptr_t>(rowstat) & 7u) == 0, "attn_bwd: rowstat must be 8-byte aligned");
-  BF_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out) && aligned16(dout) &&
-                   aligned16(dq) && aligned16(dk) && aligned16(dv),
+  BF_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(dout) && aligned16(dq) && aligned16(dk) &&
+                   aligned16(dv),
                "attn_bwd: tensors must be 16-byte aligned");
   BF_CHECK_ARG((idx->q_items == 0 && idx->k_items == 0 && !idx->token_column) || partials,
                "attn_bwd: partials buffer required for split rows and the token column");
   if (dtype == BF_DTYPE_F32)
-    return bwd_impl<float>(idx, sh, q, k, v, bias, factor, out, Z, dout, dq, dk, dv, dbias, rowstat,
-                           partials, as_stream(stream));
-  return bwd_impl<uint16_t>(idx, sh, q, k, v, bias, factor, out, Z, dout, dq, dk, dv, dbias, rowstat,
-                            partials, as_stream(stream));
+    return bwd_impl<float>(idx, sh, q, k, v, bias, factor, Z, dout, dq, dk, dv, dbias, rowstat, partials,
+                           as_stream(stream));
+  return bwd_impl<uint16_t>(idx, sh, q, k, v, bias, factor, Z, dout, dq, dk, dv, dbias, rowstat, partials,
+                            as_stream(stream));
 }

@@ -52,6 +52,20 @@ __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + 
 
 inline bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
 
+// Items a split row of `len` entries is cut into: ceil(len / item_size), at
+// most BF_MAX_ITEMS_PER_ROW, except that a row of more than
+// BF_MAX_ITEMS_PER_ROW * BF_LONG_ROW_FACTOR items' worth of entries (the
+// Graphormer token row of a 100M-node graph) takes ceil(len / (item_size *
+// BF_LONG_ROW_FACTOR)) items, so its items still spread over the whole chip.
+__host__ __device__ inline int64_t split_row_items(int64_t len, int item_size) {
+  int64_t n = ceil_div(len, int64_t(item_size));
+  if (n > BF_MAX_ITEMS_PER_ROW) {
+    const int64_t big = ceil_div(len, int64_t(item_size) * BF_LONG_ROW_FACTOR);
+    n = big > BF_MAX_ITEMS_PER_ROW ? big : BF_MAX_ITEMS_PER_ROW;
+  }
+  return n;
+}
+
 inline int ilog2(int64_t x) {
   int r = 0;
   while ((int64_t(1) << (r + 1)) <= x) ++r;

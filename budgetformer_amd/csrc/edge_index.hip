@@ -32,18 +32,16 @@ size_t scan_temp_bytes_i64(int64_t n) {
 }
 
 // ---------------------------------------------------------------- table -> CSR
-__global__ void row_lengths_kernel(const int32_t* __restrict__ row_len, int64_t n_rows, int token,
-                                   int64_t* __restrict__ lens, int64_t* __restrict__ qptr) {
-  const int64_t n_q = n_rows + (token ? 1 : 0);
+// Row lengths of a table's attention CSR. With the Graphormer token (token):
+// every table row gains kv 0; with a token row (lead = 1) attention row 0 is
+// the token row of token_len entries and table row r is attention row r + 1.
+__global__ void row_lengths_kernel(const int32_t* __restrict__ row_len, int64_t n_rows, int token, int lead,
+                                   int64_t token_len, int64_t* __restrict__ lens, int64_t* __restrict__ qptr) {
+  const int64_t n_q = n_rows + lead;
   const int64_t t = int64_t(blockIdx.x) * kThreads + threadIdx.x;
   if (t == 0) qptr[0] = 0;     // the scan writes qptr[1..n_q]
   if (t >= n_q) return;
-  int64_t len;
-  if (token)
-    len = t == 0 ? n_rows : int64_t(row_len[t - 1]) + 1;
-  else
-    len = row_len[t];
-  lens[t] = len;
+  lens[t] = (lead && t == 0) ? token_len : int64_t(row_len[t - lead]) + token;
 }
 
 // Writes entry pos (slot `slot` of query row `row`): kv, and when rkey is
@@ -57,16 +55,21 @@ __device__ __forceinline__ void put_entry(int32_t* __restrict__ kv, uint64_t* __
 }
 
 // One thread per table slot, then (with the Graphormer token) one thread per
-// query for the token row: query 0 lists kv 1..n_rows, and query r+1 starts
-// with kv 0 followed by its table row shifted by one.
+// index t < max(n_rows, token_len): with a token row (lead = 1) thread t
+// writes the token row's entry for kv t+1 at position t, and every thread
+// t < n_rows whose table row is empty writes that row's kv 0 entry (a
+// non-empty row's slot-0 thread writes it). Table row r is attention row
+// r + lead and, with the token, starts with kv 0 followed by its table row
+// shifted by one.
 constexpr int kFillPerThread = 4;   // table slots per thread: their loads are issued before any store
 
 __global__ __launch_bounds__(kThreads) void table_fill_kernel(
     const int32_t* __restrict__ table, const int32_t* __restrict__ row_len, int64_t n_rows, int width, int token,
-    const int64_t* __restrict__ qptr, int32_t* __restrict__ kv, uint64_t* __restrict__ rkey, int kshift, int sbits,
-    int slots32) {
+    int lead, int64_t token_len, const int64_t* __restrict__ qptr, int32_t* __restrict__ kv,
+    uint64_t* __restrict__ rkey, int kshift, int sbits, int slots32) {
   const int64_t slots = n_rows * width;
-  const int64_t total = slots + (token ? n_rows : 0);
+  const int64_t extra = token ? (lead && token_len > n_rows ? token_len : n_rows) : 0;
+  const int64_t total = slots + extra;
   const int64_t base = int64_t(blockIdx.x) * (kThreads * kFillPerThread) + threadIdx.x;
   int32_t val[kFillPerThread], len[kFillPerThread], col[kFillPerThread];
   int64_t row[kFillPerThread], start[kFillPerThread];
@@ -83,7 +86,7 @@ __global__ __launch_bounds__(kThreads) void table_fill_kernel(
       row[u] = r;
       col[u] = int32_t(i - r * width);
       len[u] = row_len[r];
-      start[u] = qptr[r + token];                 // with the token, table row r is query r+1
+      start[u] = qptr[r + lead];                  // table row r is attention row r + lead
       val[u] = table[i];
     }
   }
@@ -92,18 +95,18 @@ __global__ __launch_bounds__(kThreads) void table_fill_kernel(
     const int64_t i = base + int64_t(u) * kThreads;
     if (i >= slots) {
       if (i >= total) continue;
-      // the token row's entry for kv t+1 sits at position t: its key carries slot 0
       const int64_t t = i - slots;
-      put_entry(kv, rkey, t, 0, 0, int32_t(t + 1), kshift, sbits);
-      if (row_len[t] == 0) put_entry(kv, rkey, qptr[t + 1], t + 1, 0, 0, kshift, sbits);
+      // the token row's entry for kv t+1 sits at position t: its key carries slot 0
+      if (lead && t < token_len) put_entry(kv, rkey, t, 0, 0, int32_t(t + 1), kshift, sbits);
+      if (t < n_rows && row_len[t] == 0) put_entry(kv, rkey, qptr[t + lead], t + lead, 0, 0, kshift, sbits);
       continue;
     }
     const int c = col[u];
     if (c >= len[u]) continue;
-    const int64_t r = row[u];
+    const int64_t r = row[u] + lead;
     if (token) {
-      if (c == 0) put_entry(kv, rkey, start[u], r + 1, 0, 0, kshift, sbits);
-      put_entry(kv, rkey, start[u] + 1 + c, r + 1, c + 1, val[u] + 1, kshift, sbits);
+      if (c == 0) put_entry(kv, rkey, start[u], r, 0, 0, kshift, sbits);
+      put_entry(kv, rkey, start[u] + 1 + c, r, c + 1, val[u] + 1, kshift, sbits);
     } else {
       put_entry(kv, rkey, start[u] + c, r, c, val[u], kshift, sbits);
     }
@@ -230,13 +233,11 @@ constexpr int kBuckets = 256;
 static_assert(kBuckets == kThreads, "the order kernels keep one bucket per thread");
 
 // A row's split-plan entry: (items << 32) | (1 if it splits), items =
-// ceil(len / item_size) capped at BF_MAX_ITEMS_PER_ROW for rows longer than
-// the threshold, else 0. The plan is the exclusive sum of these over the rows.
+// split_row_items(len) for rows longer than the threshold, else 0. The plan is
+// the exclusive sum of these over the rows.
 __device__ __forceinline__ uint64_t split_count(int64_t len, int threshold, int item_size) {
   if (len <= threshold) return 0;
-  int64_t n = ceil_div(len, int64_t(item_size));
-  if (n > BF_MAX_ITEMS_PER_ROW) n = BF_MAX_ITEMS_PER_ROW;
-  return (uint64_t(n) << 32) | 1u;
+  return (uint64_t(split_row_items(len, item_size)) << 32) | 1u;
 }
 
 __device__ __forceinline__ int length_bucket(const int64_t* __restrict__ ptr, int64_t r) {
@@ -413,10 +414,14 @@ extern "C" int bf_scan_workspace_size(int64_t n, size_t* bytes) {
   return BF_OK;
 }
 
-extern "C" int bf_table_csr_ptr(const int32_t* row_len, int64_t n_rows, int32_t global_token, int64_t* qptr,
-                                int64_t* nnz_host, void* workspace, size_t workspace_bytes, void* stream) {
+extern "C" int bf_table_csr_ptr(const int32_t* row_len, int64_t n_rows, int32_t global_token, int64_t token_row,
+                                int64_t* qptr, int64_t* nnz_host, void* workspace, size_t workspace_bytes,
+                                void* stream) {
   BF_CHECK_ARG(qptr && n_rows >= 0 && (row_len || n_rows == 0), "table_csr_ptr: bad arguments");
-  const int64_t n_q = n_rows + (global_token ? 1 : 0);
+  BF_CHECK_ARG(!global_token || token_row < (int64_t(1) << 31) - 1, "table_csr_ptr: token row of %lld entries",
+               (long long)token_row);
+  const int lead = (global_token && token_row >= 0) ? 1 : 0;
+  const int64_t n_q = n_rows + lead;
   size_t need = 0;
   bf_scan_workspace_size(n_q, &need);
   BF_CHECK_ARG(workspace && workspace_bytes >= need, "table_csr_ptr: workspace %zu < %zu bytes", workspace_bytes, need);
@@ -427,7 +432,7 @@ extern "C" int bf_table_csr_ptr(const int32_t* row_len, int64_t n_rows, int32_t 
     void* temp = static_cast<char*>(workspace) + align_up(size_t(n_q) * sizeof(int64_t));
     size_t temp_bytes = scan_temp_bytes_i64(n_q);
     BF_LAUNCH("row_lengths_kernel", row_lengths_kernel, dim3(blocks_for(n_q)), dim3(kThreads), 0, st, row_len, n_rows,
-              int(global_token != 0), lens, qptr);
+              int(global_token != 0), lead, lead ? token_row : int64_t(0), lens, qptr);
     BF_CHECK_LAUNCH();
     BF_CHECK_HIP(hipcub::DeviceScan::InclusiveSum(temp, temp_bytes, lens, qptr + 1, int(n_q), st));
   }
@@ -440,23 +445,29 @@ extern "C" int bf_table_csr_ptr(const int32_t* row_len, int64_t n_rows, int32_t 
 }
 
 extern "C" int bf_table_to_csr(const int32_t* table, const int32_t* row_len, int64_t n_rows, int32_t width,
-                               int32_t global_token, const int64_t* qptr, int32_t* kv, uint64_t* rkey,
-                               int32_t q_bits, int32_t slot_bits, void* stream) {
+                               int32_t global_token, int64_t token_row, const int64_t* qptr, int32_t* kv,
+                               uint64_t* rkey, int32_t q_bits, int32_t slot_bits, void* stream) {
   BF_CHECK_ARG(n_rows >= 0 && width >= 0 && qptr, "table_to_csr: bad arguments");
-  BF_CHECK_ARG(n_rows == 0 || (table && row_len && kv), "table_to_csr: null tensor");
+  BF_CHECK_ARG(!global_token || token_row < (int64_t(1) << 31) - 1, "table_to_csr: token row of %lld entries",
+               (long long)token_row);
+  const int lead = (global_token && token_row >= 0) ? 1 : 0;
+  const int64_t token_len = lead ? token_row : 0;
+  BF_CHECK_ARG((n_rows == 0 || (table && row_len)) && (kv || (n_rows == 0 && token_len == 0)),
+               "table_to_csr: null tensor");
   if (rkey) {
-    const int64_t n_q = n_rows + (global_token ? 1 : 0);
+    const int64_t n_q = n_rows + lead;
     BF_CHECK_ARG(q_bits >= bits_for(uint64_t(n_q)) && slot_bits >= bits_for(uint64_t(width)) &&
                      q_bits + slot_bits <= 33,
                  "table_to_csr: key fields (%d query bits, %d slot bits) do not hold %lld queries of width %d "
                  "beside a 31-bit id", q_bits, slot_bits, (long long)n_q, width);
   }
-  const int64_t threads = n_rows * width + (global_token ? n_rows : 0);
+  const int64_t extra = global_token ? (token_len > n_rows ? token_len : n_rows) : 0;
+  const int64_t threads = n_rows * width + extra;
   if (threads > 0) {
     BF_LAUNCH("table_fill_kernel", table_fill_kernel, dim3(unsigned(ceil_div(threads, int64_t(kThreads) * kFillPerThread))),
               dim3(kThreads), 0, as_stream(stream),
-              table, row_len, n_rows, width, int(global_token != 0), qptr, kv, rkey, q_bits + slot_bits, slot_bits,
-              int(n_rows * width < (int64_t(1) << 32)));
+              table, row_len, n_rows, width, int(global_token != 0), lead, token_len, qptr, kv, rkey,
+              q_bits + slot_bits, slot_bits, int(n_rows * width < (int64_t(1) << 32)));
     BF_CHECK_LAUNCH();
   }
   return BF_OK;
@@ -568,7 +579,7 @@ extern "C" int bf_reverse_index_packed_workspace_size(int64_t nnz, size_t* bytes
 }
 
 extern "C" int bf_reverse_index_packed(const uint64_t* rkey, const int64_t* qptr, int64_t nnz, int64_t n_q,
-                                       int64_t n_kv, int32_t q_bits, int32_t slot_bits, int32_t global_token,
+                                       int64_t n_kv, int32_t q_bits, int32_t slot_bits, int32_t token_row,
                                        uint64_t* sorted, int64_t* kptr, int32_t* kq, int32_t* ke, void* workspace,
                                        size_t workspace_bytes, void* stream) {
   BF_CHECK_ARG(kptr && qptr && n_q >= 0 && n_kv >= 0 && nnz >= 0, "reverse_index_packed: bad arguments");
@@ -592,13 +603,13 @@ extern "C" int bf_reverse_index_packed(const uint64_t* rkey, const int64_t* qptr
   BF_CHECK_HIP(hipcub::DeviceRadixSort::SortKeys(workspace, tb, rkey, sorted, int(nnz), kshift, kshift + id_bits, st));
   BF_LAUNCH("unpack_rkey_kernel", unpack_rkey_kernel,
             dim3(unsigned(ceil_div(nnz + 1, int64_t(kThreads) * kUnpackPerThread))), dim3(kThreads), 0, st, sorted, nnz,
-            kshift, slot_bits, int(global_token != 0), qptr, n_kv, kptr, kq, ke);
+            kshift, slot_bits, int(token_row != 0), qptr, n_kv, kptr, kq, ke);
   BF_CHECK_LAUNCH();
   return BF_OK;
 }
 
 extern "C" int bf_reverse_entries(const uint64_t* sorted, const int64_t* qptr, int64_t nnz, int64_t n_q,
-                                  int32_t q_bits, int32_t slot_bits, int32_t global_token, int32_t* ke,
+                                  int32_t q_bits, int32_t slot_bits, int32_t token_row, int32_t* ke,
                                   void* stream) {
   BF_CHECK_ARG(qptr && nnz >= 0 && nnz < (int64_t(1) << 31) && n_q >= 0, "reverse_entries: bad arguments");
   BF_CHECK_ARG(q_bits >= bits_for(uint64_t(n_q)) && slot_bits >= 1 && q_bits + slot_bits <= 33,
@@ -606,7 +617,7 @@ extern "C" int bf_reverse_entries(const uint64_t* sorted, const int64_t* qptr, i
   if (nnz == 0) return BF_OK;
   BF_CHECK_ARG(sorted && ke, "reverse_entries: null tensor");
   BF_LAUNCH("reverse_entries_kernel", reverse_entries_kernel, dim3(blocks_for(nnz)), dim3(kThreads), 0,
-            as_stream(stream), sorted, nnz, q_bits + slot_bits, slot_bits, int(global_token != 0), qptr, ke);
+            as_stream(stream), sorted, nnz, q_bits + slot_bits, slot_bits, int(token_row != 0), qptr, ke);
   BF_CHECK_LAUNCH();
   return BF_OK;
 }
@@ -625,6 +636,11 @@ extern "C" int64_t bf_split_item_capacity(int64_t nnz, int32_t threshold, int32_
   if (threshold < 1 || item_size < 1 || nnz < 0) return 0;
   // only rows longer than threshold split: sum ceil(len/item) <= nnz/item + #heavy rows
   return nnz / item_size + nnz / threshold + 1;
+}
+
+extern "C" int64_t bf_split_row_items(int64_t len, int32_t item_size) {
+  if (len <= 0 || item_size < 1) return 0;
+  return split_row_items(len, item_size);
 }
 
 extern "C" int64_t bf_split_row_capacity(int64_t nnz, int32_t threshold) {
@@ -679,8 +695,7 @@ extern "C" int bf_split_plan(const int64_t* ptr, int64_t n_rows, int32_t thresho
 extern "C" int bf_split_plan_first_row(int64_t n_rows, int32_t n_items, int32_t* nitems, int32_t* item_off,
                                        int32_t* item_row, int64_t item_cap, int32_t* heavy_rows, int64_t heavy_cap,
                                        int32_t* counts, void* stream) {
-  BF_CHECK_ARG(n_rows >= 0 && n_rows < (int64_t(1) << 31) && n_items >= 0 && n_items <= BF_MAX_ITEMS_PER_ROW &&
-                   counts && (n_items == 0 || n_rows > 0),
+  BF_CHECK_ARG(n_rows >= 0 && n_rows < (int64_t(1) << 31) && n_items >= 0 && counts && (n_items == 0 || n_rows > 0),
                "split_plan_first_row: bad arguments");
   BF_CHECK_ARG(item_cap >= n_items && heavy_cap >= (n_items ? 1 : 0), "split_plan_first_row: capacity too small");
   BF_CHECK_ARG(n_rows == 0 || (nitems && item_off), "split_plan_first_row: null tensor");

@@ -48,29 +48,40 @@ class EdgeTable:
     def width(self) -> int:
         return int(self.table.shape[1])
 
+    @property
+    def holds_token_row(self) -> bool:
+        """With the global token: whether this table's queries include node 0's shard, which then also
+        carries the token's own row (query 0, attending every node)."""
+        return self.global_token and self.query_ids is None and self.q_lo == 0
+
     def attention_index(self, chunk: int = hip_ops.DEFAULT_CHUNK, item: int = hip_ops.DEFAULT_ITEM) -> AttentionIndex:
-        """CSR view for the attention kernels (cached per split setting)."""
+        """CSR view for the attention kernels (cached per split setting).
+
+        Query rows: the table's rows, preceded by the token row when ``holds_token_row`` (so a full
+        build has N + 1 rows, ids shifted by one). A query shard [q_lo, q_lo + n) with q_lo > 0 has n
+        rows, row r serving node q_lo + r (attention id q_lo + r + 1), each opening with kv 0; kv rows
+        are always all N (+ 1) nodes."""
         idx = self._index.get((chunk, item))
         if idx is None and self.query_ids is not None:
             n_kv = self.num_nodes + (1 if self.global_token else 0)
             idx = AttentionIndex.from_coo(self.to_edge_index(), n_kv, n_kv, chunk=chunk, item=item)
             self._index[(chunk, item)] = idx
         if idx is None:
-            if self.q_lo != 0 or self.n_rows != self.num_nodes:
-                if self.global_token:
-                    raise NotImplementedError("the Graphormer global token needs the full query set")
             n_kv = self.num_nodes + (1 if self.global_token else 0)
+            token_row = (self.num_nodes if self.holds_token_row else -1) if self.global_token else None
             idx = AttentionIndex.from_table(self.table, self.row_len, self.global_token, n_kv=n_kv, chunk=chunk,
-                                            item=item, check=False)
+                                            item=item, check=False, token_row=token_row)
             self._index[(chunk, item)] = idx
         return idx
 
     def to_edge_index(self) -> torch.Tensor:
-        """Reference-format COO [2, E'] int64 (row 0 kv/src, row 1 query/dst).
+        """Reference-format COO [2, E'] int64 (row 0 kv/src, row 1 query/dst, global ids).
 
         Merged part in coalesce order (sorted by (src, dst)); with the global
-        token, ids shifted by one and the 2N virtual edges appended as
-        fix_edge_index does.
+        token, ids shifted by one and the virtual edges appended as
+        fix_edge_index does (gt_sp/utils.py:113-130): [(v+1) -> 0 for every node
+        v] when this table holds the token row, then [0 -> (q+1)] for each of
+        its queries q (all N for a full build).
         """
         base = AttentionIndex.from_table(self.table, self.row_len, False, n_kv=self.num_nodes)
         coo = base.to_coo()
@@ -82,8 +93,17 @@ class EdgeTable:
             return coo
         n = self.num_nodes
         ar = torch.arange(1, n + 1, dtype=torch.int64, device=coo.device)
-        zeros = torch.zeros(n, dtype=torch.int64, device=coo.device)
-        return torch.cat([coo + 1, torch.stack([ar, zeros]), torch.stack([zeros, ar])], dim=1)
+        if self.query_ids is not None:
+            # a filtered (probe) build keeps every virtual edge, as the reference applies fix_edge_index
+            # to the whole probe edge set
+            return torch.cat([coo + 1, torch.stack([ar, torch.zeros_like(ar)]),
+                              torch.stack([torch.zeros_like(ar), ar])], dim=1)
+        qs = torch.arange(self.q_lo + 1, self.q_lo + self.n_rows + 1, dtype=torch.int64, device=coo.device)
+        parts = [coo + 1]
+        if self.holds_token_row:
+            parts.append(torch.stack([ar, torch.zeros_like(ar)]))
+        parts.append(torch.stack([torch.zeros_like(qs), qs]))
+        return torch.cat(parts, dim=1)
 
 
 def build_attention_edges(graph: CSRGraph, *, real_edges_per_query: int, rw_edges_per_query: int,

@@ -334,43 +334,64 @@ class ReverseKeys:
     keys: torch.Tensor          # uint64 as int64 [nnz]
     q_bits: int
     slot_bits: int
-    global_token: bool
+    token_row: bool             # attention row 0 is the Graphormer token row
 
 
-def table_qptr(table: torch.Tensor, row_len: torch.Tensor, global_token: bool = False) -> torch.Tensor:
-    """qptr [n_q+1] int64 of a query-major table (bf_table_csr_ptr without the host read of nnz)."""
+def _token_row(n_rows: int, global_token: bool, token_row: Optional[int]) -> int:
+    """The token row's length (>= 0) or -1 for none: by default a table with the token covers the full
+    query set, so its token row lists all n_rows nodes."""
+    if not global_token:
+        return -1
+    return n_rows if token_row is None else int(token_row)
+
+
+def table_qptr(table: torch.Tensor, row_len: torch.Tensor, global_token: bool = False,
+               token_row: Optional[int] = None) -> torch.Tensor:
+    """qptr [n_q+1] int64 of a query-major table (bf_table_csr_ptr without the host read of nnz).
+    ``token_row``: see ``table_to_csr``."""
     dev = table.device
     _require(table, "table", torch.int32)
     _require(row_len, "row_len", torch.int32, dev)
     n_rows = table.shape[0]
-    n_q = n_rows + (1 if global_token else 0)
+    tr = _token_row(n_rows, global_token, token_row)
+    n_q = n_rows + (1 if tr >= 0 else 0)
     ws = _workspace(_size_query("bf_scan_workspace_size", n_q), dev)
     qptr = torch.empty(n_q + 1, dtype=torch.int64, device=dev)
-    N.call("bf_table_csr_ptr", _p(row_len), n_rows, int(global_token), _p(qptr), None, _p(ws), ws.numel(),
+    N.call("bf_table_csr_ptr", _p(row_len), n_rows, int(global_token), tr, _p(qptr), None, _p(ws), ws.numel(),
            _stream(dev))
     return qptr
 
 
 def table_to_csr(table: torch.Tensor, row_len: torch.Tensor, global_token: bool = False, with_keys: bool = False,
-                 qptr: Optional[torch.Tensor] = None):
+                 qptr: Optional[torch.Tensor] = None, token_row: Optional[int] = None):
     """Query-major table -> (qptr [n_q+1] int64, kv [nnz] int32), plus the reverse-index sort keys
     (``ReverseKeys``, or None when the query and slot fields need more than 33 bits) with ``with_keys``.
-    ``qptr`` from ``table_qptr`` saves the scan; nnz is read from it (one host read)."""
+    ``qptr`` from ``table_qptr`` saves the scan; nnz is read from it (one host read).
+
+    With ``global_token`` every table row also attends to kv 0 and ids shift by one; ``token_row`` is the
+    length of the token's own row, placed as attention row 0 (default n_rows: the full query set; N for
+    a query shard that starts at node 0), or -1 for a shard without it (every row then starts with kv 0)."""
     dev = table.device
-    if qptr is None:
-        qptr = table_qptr(table, row_len, global_token)
     n_rows, width = table.shape
-    n_q = n_rows + (1 if global_token else 0)
+    tr = _token_row(n_rows, global_token, token_row)
+    if qptr is None:
+        qptr = table_qptr(table, row_len, global_token, tr)
+    n_q = n_rows + (1 if tr >= 0 else 0)
     nnz = int(qptr[n_q].item())
     kv = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)[:nnz]
     rk = None
     q_bits, slot_bits = _bits_for(n_q), _bits_for(width)
     if with_keys and q_bits + slot_bits <= 33:
         rk = ReverseKeys(torch.empty(max(nnz, 1), dtype=torch.int64, device=dev)[:nnz], q_bits,
-                         slot_bits, bool(global_token))
-    N.call("bf_table_to_csr", _p(table), _p(row_len), n_rows, width, int(global_token), _p(qptr), _p(kv),
+                         slot_bits, tr >= 0)
+    N.call("bf_table_to_csr", _p(table), _p(row_len), n_rows, width, int(global_token), tr, _p(qptr), _p(kv),
            _p(rk.keys) if rk is not None else None, q_bits, slot_bits, _stream(dev))
     return (qptr, kv, rk) if with_keys else (qptr, kv)
+
+
+def split_row_items(length: int, item_size: int = DEFAULT_ITEM) -> int:
+    """Items a split row of ``length`` entries is cut into (bf_split_row_items)."""
+    return int(N.load().bf_split_row_items(int(length), int(item_size)))
 
 
 def coo_to_csr(edge_index: torch.Tensor, n_q: int, n_kv: int):
@@ -417,12 +438,12 @@ def reverse_index_packed(rk: ReverseKeys, qptr: torch.Tensor, n_kv: int, entries
     nnz = rk.keys.numel()
     ws = _workspace(_size_query("bf_reverse_index_packed_workspace_size", nnz), dev)
     srt = ReverseKeys(torch.empty(max(nnz, 1), dtype=torch.int64, device=dev)[:nnz], rk.q_bits, rk.slot_bits,
-                      rk.global_token)
+                      rk.token_row)
     kptr = torch.empty(n_kv + 1, dtype=torch.int64, device=dev)
     kq = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)[:nnz]
     ke = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)[:nnz] if entries else None
     N.call("bf_reverse_index_packed", _p(rk.keys), _p(qptr), nnz, qptr.numel() - 1, n_kv, rk.q_bits, rk.slot_bits,
-           int(rk.global_token), _p(srt.keys), _p(kptr), _p(kq), _p(ke) if entries else None, _p(ws), ws.numel(),
+           int(rk.token_row), _p(srt.keys), _p(kptr), _p(kq), _p(ke) if entries else None, _p(ws), ws.numel(),
            _stream(dev))
     return kptr, kq, ke, srt
 
@@ -435,7 +456,7 @@ def reverse_entries(srt: ReverseKeys, qptr: torch.Tensor) -> torch.Tensor:
     nnz = srt.keys.numel()
     ke = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)[:nnz]
     N.call("bf_reverse_entries", _p(srt.keys), _p(qptr), nnz, qptr.numel() - 1, srt.q_bits, srt.slot_bits,
-           int(srt.global_token), _p(ke), _stream(dev))
+           int(srt.token_row), _p(ke), _stream(dev))
     return ke
 
 
@@ -615,9 +636,10 @@ class AttentionIndex:
     kplan: Optional[SplitPlan] = None
     korder: Optional[torch.Tensor] = None
     kspans: Optional[torch.Tensor] = None      # per korder slot: (kptr[row] << 32 | row length)
-    # key 0 is the Graphormer token column (attended by queries 1..n_q-1 once each, first in their rows, and
-    # by nothing else): the dq pass then sums its dK/dV terms instead of the dk/dv pass re-gathering them
-    token_column: bool = False
+    # key 0 is the Graphormer token column, attended once by each query row from 1 on (1) or from 0 on (2: a
+    # query shard without the token row), first in the row, and by nothing else (0: no such promise): the
+    # dq pass then sums its dK/dV terms instead of the dk/dv pass re-gathering them
+    token_column: int = 0
     _rows: Optional[torch.Tensor] = field(default=None, repr=False)
     _rkeys: Optional[ReverseKeys] = field(default=None, repr=False)   # from_table: sort keys, until used
     _sorted: Optional[ReverseKeys] = field(default=None, repr=False)  # sorted keys, until ke is needed
@@ -748,16 +770,24 @@ class AttentionIndex:
 
     @classmethod
     def from_table(cls, table, row_len, global_token: bool = False, n_kv: Optional[int] = None,
-                   chunk: int = DEFAULT_CHUNK, item: int = DEFAULT_ITEM, check: bool = True):
+                   chunk: int = DEFAULT_CHUNK, item: int = DEFAULT_ITEM, check: bool = True,
+                   token_row: Optional[int] = None):
         """Index of a query-major table. ``check`` validates the table on the device first (row lengths
         within the width, the ids of every row's first row_len slots within [0, n_kv)) with one host
-        read; the edge builder's own tables skip it (valid by construction)."""
-        n_q_tab = table.shape[0] + (1 if global_token else 0)
+        read; the edge builder's own tables skip it (valid by construction).
+
+        ``token_row`` (with ``global_token``): the length of the Graphormer token's own row, attention
+        row 0 — by default the table's row count (the full query set); the node count N for a query
+        shard that starts at node 0; -1 for a shard without it, whose attention rows are its table rows."""
+        n_rows, width = table.shape
+        tr = _token_row(n_rows, global_token, token_row)
+        n_q_tab = n_rows + (1 if tr >= 0 else 0)
         n_kv = n_kv if n_kv is not None else n_q_tab
+        if global_token and tr > n_kv - 1:
+            raise ValueError(f"the token row lists kv 1..{tr}, beyond the {n_kv} kv rows")
         if check and table.numel():
             _require(table, "table", torch.int32)
             _require(row_len, "row_len", torch.int32, table.device)
-            width = table.shape[1]
             lens = row_len.to(torch.int64)
             used = torch.arange(width, device=table.device)[None, :] < lens[:, None]
             ids = torch.where(used, table, torch.zeros((), dtype=table.dtype, device=table.device))
@@ -769,23 +799,25 @@ class AttentionIndex:
             if stats[1] > 0 and (stats[2] < 0 or stats[3] + shift >= n_kv):
                 raise ValueError(f"table ids must lie in [0, {n_kv - shift}) (got [{stats[2]}, {stats[3]}])")
         # A table row holds at most `width` entries (+ key 0 with the token), so when that is within
-        # `chunk` only the token row (every key, n_rows entries) can be split: the query plan's counts
+        # `chunk` only the token row (every node, tr entries) can be split: the query plan's counts
         # follow from the sizes, with no read of the device.
-        n_rows, width = table.shape
         known = None
         if width + (1 if global_token else 0) <= chunk:
-            split = bool(global_token) and n_rows > chunk
-            known = (min(-(-n_rows // item), N.BF_MAX_ITEMS_PER_ROW) if split else 0, 1 if split else 0)
-        qptr = table_qptr(table, row_len, global_token)
-        # the token fill puts key 0 first in every row t >= 1 and shifts the table's own ids past it
+            split = tr > chunk
+            known = (split_row_items(tr, item) if split else 0, 1 if split else 0)
+        qptr = table_qptr(table, row_len, global_token, tr)
+        # the token fill puts key 0 first in every table row and shifts the table's own ids past it:
+        # key 0 is then attended by every query row from 1 on (with the token row) or from 0 on (without)
+        token_column = 0 if not global_token else (1 if tr >= 0 else 2)
         idx = cls(n_q=n_q_tab, n_kv=n_kv, qptr=qptr, kv=None, chunk=chunk, item=item,
-                  token_column=bool(global_token), _q_known=known)
+                  token_column=token_column, _q_known=known)
         if known is not None:
             # only the token row can be split: its plan is written in one pass, before the host waits
             # for nnz
-            bound = n_rows * width + (2 * n_rows if global_token else 0)
+            bound = n_rows * width + (n_rows if global_token else 0) + max(tr, 0)
             idx.qplan = split_plan_first_row(n_q_tab, known[0], bound, chunk, item, idx._plan_counts(0))
-        qptr, idx.kv, idx._rkeys = table_to_csr(table, row_len, global_token, with_keys=True, qptr=qptr)
+        qptr, idx.kv, idx._rkeys = table_to_csr(table, row_len, global_token, with_keys=True, qptr=qptr,
+                                                token_row=tr)
         return idx
 
     @classmethod
@@ -839,16 +871,29 @@ def attn_forward(idx: AttentionIndex, q, k, v, bias=None, factor=None):
     return out, Z
 
 
+def kv_pass_variant(n_q: int, n_kv: int, dtype: torch.dtype, heads: int, head_dim: int) -> dict:
+    """How the dk/dv pass runs for these sizes (bf_attn_bwd_kv_variant): rows per lane group, whether q
+    and dO are gathered non-temporally, whether a group's row slots are prefetched."""
+    s = N.AttnIndex()
+    s.n_q, s.n_kv = int(n_q), int(n_kv)
+    rpg, nt, pre = C.c_int32(), C.c_int32(), C.c_int32()
+    N.call("bf_attn_bwd_kv_variant", C.byref(s), _DT[dtype], int(heads), int(head_dim), C.byref(rpg), C.byref(nt),
+           C.byref(pre))
+    return {"rows_per_group": rpg.value, "stream_rows": bool(nt.value), "prefetch_slots": bool(pre.value)}
+
+
 def attn_backward(idx: AttentionIndex, q, k, v, out, Z, dout, bias=None, factor=None, need_dbias: bool = False):
-    """(dq, dk, dv, dbias-or-None) for attn_forward's outputs."""
+    """(dq, dk, dv, dbias-or-None) for attn_forward's outputs. ``out`` is accepted for the autograd
+    surface but not read: the backward sums Delta = dO . out from the entries in float32."""
     _check_qkv(q, k, v)
     H, hn = q.shape[1], q.shape[2]
-    _require(out, "out", q.dtype, q.device)
     _require(dout, "dout", q.dtype, q.device)
+    if tuple(dout.shape) != tuple(q.shape) or tuple(Z.shape) != (q.shape[0], H):
+        raise ValueError(f"dout {tuple(dout.shape)} / Z {tuple(Z.shape)} do not match q {tuple(q.shape)}")
     _require(Z, "Z", torch.float32, q.device)
     _check_edge_tensor(bias, "bias", idx, H, q.device)
     _check_edge_tensor(factor, "factor", idx, H, q.device)
-    st = idx.struct(backward=True, entries=bias is not None or factor is not None)
+    st = idx.struct(backward=True, entries=bias is not None or factor is not None or need_dbias)
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
@@ -856,6 +901,6 @@ def attn_backward(idx: AttentionIndex, q, k, v, out, Z, dout, bias=None, factor=
     rowstat = torch.empty(idx.n_q, H, 2, dtype=torch.float32, device=q.device)
     parts = torch.empty(max(int(N.load().bf_attn_partials_floats(C.byref(st), H, hn)), 1), dtype=torch.float32,
                         device=q.device)
-    N.call("bf_attn_bwd", C.byref(st), _DT[q.dtype], H, hn, _p(q), _p(k), _p(v), _p(bias), _p(factor), _p(out),
+    N.call("bf_attn_bwd", C.byref(st), _DT[q.dtype], H, hn, _p(q), _p(k), _p(v), _p(bias), _p(factor),
            _p(Z), _p(dout), _p(dq), _p(dk), _p(dv), _p(dbias), _p(rowstat), _p(parts), _stream(q.device))
     return dq, dk, dv, dbias

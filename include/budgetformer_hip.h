@@ -232,8 +232,15 @@ int bf_chung_lu(int64_t num_nodes, int64_t pairs, double exponent, double i0, do
 
 /* Query-major table -> attention CSR (qptr int64 [n_q+1], kv int32 [nnz]).
  * global_token != 0 applies the Graphormer virtual node (fix_edge_index,
- * gt_sp/utils.py:113-130): ids shift by one, query 0 attends to kv 1..n_rows,
- * every query t >= 1 also attends to kv 0; then n_q = n_rows + 1.
+ * gt_sp/utils.py:113-130): ids shift by one and every table row also attends
+ * to kv 0, first in its row. token_row says where the token's own row is:
+ *   token_row >= 0: attention row 0 is the token row, attending to kv
+ *     1..token_row (the graph's N nodes), and table row r is query r+1, so
+ *     n_q = n_rows + 1 (the full query set: token_row = n_rows; a query shard
+ *     that starts at node 0: token_row = N);
+ *   token_row < 0: no token row — a query shard [q_lo, q_lo + n_rows) with
+ *     q_lo > 0, whose table row r is attention row r; n_q = n_rows.
+ * With global_token == 0 token_row is ignored and n_q = n_rows.
  * bf_table_csr_ptr writes qptr (a prefix sum of the row lengths) and returns
  * nnz = qptr[n_q] on the host (it synchronises the stream, so the caller can
  * size kv; with nnz_host NULL it only enqueues the scan and the caller reads
@@ -244,10 +251,10 @@ int bf_chung_lu(int64_t num_nodes, int64_t pairs, double exponent, double i0, do
  * q_bits >= bits of n_q, slot_bits >= bits of width and q_bits + slot_bits
  * <= 33 (BF_ERR_INVALID otherwise). Workspace: bf_scan_workspace_size(n_q). */
 int bf_scan_workspace_size(int64_t n, size_t* bytes);
-int bf_table_csr_ptr(const int32_t* row_len, int64_t n_rows, int32_t global_token, int64_t* qptr,
-                     int64_t* nnz_host, void* workspace, size_t workspace_bytes, void* stream);
+int bf_table_csr_ptr(const int32_t* row_len, int64_t n_rows, int32_t global_token, int64_t token_row,
+                     int64_t* qptr, int64_t* nnz_host, void* workspace, size_t workspace_bytes, void* stream);
 int bf_table_to_csr(const int32_t* table, const int32_t* row_len, int64_t n_rows, int32_t width,
-                    int32_t global_token, const int64_t* qptr, int32_t* kv, uint64_t* rkey,
+                    int32_t global_token, int64_t token_row, const int64_t* qptr, int32_t* kv, uint64_t* rkey,
                     int32_t q_bits, int32_t slot_bits, void* stream);
 
 /* Reference COO edge_index [2, nnz] (row 0 = key/value node, row 1 = query
@@ -281,33 +288,39 @@ int bf_reverse_index(const int64_t* qptr, const int32_t* kv, int64_t n_q, int64_
  * 8-byte keys over their id bits only (stable, so each id's entries stay in
  * CSR order) into sorted uint64 [nnz], then one pass that writes kptr and
  * decodes kq. ke (may be NULL) is decoded in the same pass: qptr[query] +
- * slot, id - 1 for the token row when global_token; it is a random gather of
+ * slot, id - 1 for the token row when token_row != 0 (attention row 0 is the
+ * Graphormer token row, bf_table_to_csr with token_row >= 0); it is a random gather of
  * qptr, which the dk/dv pass needs only with a bias or factor, so a caller may
  * keep `sorted` and call bf_reverse_entries later instead. Same kptr / kq /
  * ke as bf_reverse_index. Workspace: bf_reverse_index_packed_workspace_size. */
 int bf_reverse_index_packed_workspace_size(int64_t nnz, size_t* bytes);
 int bf_reverse_index_packed(const uint64_t* rkey, const int64_t* qptr, int64_t nnz, int64_t n_q, int64_t n_kv,
-                            int32_t q_bits, int32_t slot_bits, int32_t global_token, uint64_t* sorted,
+                            int32_t q_bits, int32_t slot_bits, int32_t token_row, uint64_t* sorted,
                             int64_t* kptr, int32_t* kq, int32_t* ke, void* workspace, size_t workspace_bytes,
                             void* stream);
 /* ke [nnz] from bf_reverse_index_packed's sorted keys.                       */
 int bf_reverse_entries(const uint64_t* sorted, const int64_t* qptr, int64_t nnz, int64_t n_q, int32_t q_bits,
-                       int32_t slot_bits, int32_t global_token, int32_t* ke, void* stream);
+                       int32_t slot_bits, int32_t token_row, int32_t* ke, void* stream);
 
 /* Row id of every entry of a CSR (rows[i] = r for ptr[r] <= i < ptr[r+1]). */
 int bf_expand_rows(const int64_t* ptr, int64_t n_rows, int64_t nnz, int64_t* rows, void* stream);
 
 /* Split plan for rows longer than `threshold`: such a row is processed as
- * n = min(ceil(len/item_size), BF_MAX_ITEMS_PER_ROW) items of ceil(len/n)
- * entries (the last one shorter), one workgroup each, whose partial sums are
- * reduced in item order by one workgroup per split row, so results are
- * deterministic. The cap keeps the reduce of a very long row (the Graphormer
- * token row and column) short.
+ * n = bf_split_row_items(len, item_size) items of ceil(len/n) entries (the
+ * last one shorter), one workgroup each, whose partial sums are reduced in
+ * item order by one workgroup per split row, so results are deterministic.
+ * n = min(ceil(len/item_size), BF_MAX_ITEMS_PER_ROW): the cap keeps the reduce
+ * of a long row (the Graphormer token row and column) short; a row of more
+ * than BF_MAX_ITEMS_PER_ROW * BF_LONG_ROW_FACTOR * item_size entries (the
+ * token row of a 100M-node graph) takes ceil(len / (item_size *
+ * BF_LONG_ROW_FACTOR)) items instead, enough to spread it over the chip.
  *   nitems int32 [n_rows] (0 for short rows), item_off int32 [n_rows],
  *   item_row int32 [item_cap], heavy_rows int32 [heavy_cap] (the split rows,
  *   ascending), counts int32 [2] on the device = (#items, #split rows).
  *   Capacities: bf_split_item_capacity / bf_split_row_capacity.              */
 #define BF_MAX_ITEMS_PER_ROW 160
+#define BF_LONG_ROW_FACTOR 64
+int64_t bf_split_row_items(int64_t len, int32_t item_size);
 int64_t bf_split_item_capacity(int64_t nnz, int32_t threshold, int32_t item_size);
 int64_t bf_split_row_capacity(int64_t nnz, int32_t threshold);
 int bf_split_plan_workspace_size(int64_t n_rows, size_t* bytes);
@@ -320,7 +333,8 @@ int bf_split_plan(const int64_t* ptr, int64_t n_rows, int32_t threshold, int32_t
  * (the Graphormer token row of a table's CSR, every other row holding at most
  * the table width + 1 entries), cut into n_items items (0: no split row):
  * the same arrays and counts bf_split_plan writes, in one pass and without a
- * scan. The caller vouches for the premise; n_items <= BF_MAX_ITEMS_PER_ROW. */
+ * scan. The caller vouches for the premise; n_items = bf_split_row_items of
+ * row 0's length. */
 int bf_split_plan_first_row(int64_t n_rows, int32_t n_items, int32_t* nitems, int32_t* item_off,
                             int32_t* item_row, int64_t item_cap, int32_t* heavy_rows, int64_t heavy_cap,
                             int32_t* counts, void* stream);
@@ -384,8 +398,10 @@ typedef struct bf_attn_index {
   int32_t token_column;         /* 1: key 0 is the Graphormer token column — attended by
                                    queries 1..n_q-1 exactly once each, at the first
                                    position of their rows, and by no other entry
-                                   (bf_table_to_csr with global_token gives this);
-                                   the dq pass then also sums key 0's dK/dV terms,
+                                   (bf_table_to_csr with global_token and a token row
+                                   gives this); 2: the same for every query 0..n_q-1
+                                   (a query shard without the token row, token_row < 0).
+                                   The dq pass then also sums key 0's dK/dV terms,
                                    which the dk/dv pass would otherwise re-gather.
                                    0: no such promise. */
   const uint64_t* k_spans;      /* [n_kv] or NULL: bf_row_order's spans of k_order (needs
@@ -422,14 +438,29 @@ int bf_attn_fwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int3
 /* Backward of bf_attn_fwd (the autograd of the reference graph of ops,
  * models/graphormer_dist_node_level.py:231-263). Deterministic: dq by a
  * query-major pass, dk/dv by a key-major pass over the reverse index; no atomics.
- *   dbias: NULL or float32 [nnz, H]; rowstat: float32 [n_q, H, 2] scratch
- *   (per query and head {1/(Z+1e-6), Delta/(Z+1e-6)}, Delta = sum_j dO*out,
- *   written by the query-major pass and read by the key-major pass).        */
+ * Per query and head, Delta = sum_j dO*out is summed from the query's entries
+ * (sum_e p f (dO . v_s) / D', D' = Z + 1e-6) in float32, so the forward's
+ * output tensor is not read: a bfloat16 out would carry its rounding into the
+ * gradients (the reference, under autocast, keeps out in float32).
+ *   dbias: NULL or float32 [nnz, H] (per CSR position; needs idx->ke);
+ *   rowstat: float32 [n_q, H, 2] scratch (per query and head
+ *   {1/D', Delta/D'}, written by the query-major pass and read by the
+ *   key-major pass).                                                         */
 int bf_attn_bwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
                 const void* q, const void* k, const void* v, const float* bias, const float* factor,
-                const void* out, const float* Z, const void* dout,
-                void* dq, void* dk, void* dv, float* dbias, float* rowstat, float* partials,
-                void* stream);
+                const float* Z, const void* dout, void* dq, void* dk, void* dv, float* dbias, float* rowstat,
+                float* partials, void* stream);
+
+/* How bf_attn_bwd runs its key-major (dk/dv) pass on this index, for callers
+ * and tests that need to know which kernel instance a shape takes (host-only,
+ * launches nothing): rows_per_group = short kv rows per lane group (1, or 4
+ * past 16M kv rows in float32 / 1M in bfloat16); stream_rows = 1 when the q
+ * and dO tables exceed the 256 MB Infinity Cache and are gathered
+ * non-temporally; prefetch_slots = 1 when a group's row slots are loaded in
+ * one round before its loop (bfloat16 with several rows per group). No
+ * reference counterpart: the reference's scatter backward has no such choice. */
+int bf_attn_bwd_kv_variant(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
+                           int32_t* rows_per_group, int32_t* stream_rows, int32_t* prefetch_slots);
 
 #ifdef __cplusplus
 }

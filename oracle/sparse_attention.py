@@ -131,8 +131,9 @@ def attention_forward_stats(k, q, v, edge_index, bias_e=None, factor_e=None):
     p = torch.exp(a)
     dst = edge_index[1].to(torch.long)
     w = p if factor_e is None else p * factor_e
-    W = torch.zeros_like(v).index_add(0, dst, v[edge_index[0].to(torch.long)] * w.unsqueeze(-1))
-    Z = p.new_zeros(v.size(0), num_heads).index_add(0, dst, p)
+    # one output row per query row (the reference's zeros_like(v) has the same S rows as q)
+    W = v.new_zeros(q.size(0), num_heads, hn).index_add(0, dst, v[edge_index[0].to(torch.long)] * w.unsqueeze(-1))
+    Z = p.new_zeros(q.size(0), num_heads).index_add(0, dst, p)
     return W / (Z + EPS).unsqueeze(-1), Z
 
 

@@ -43,6 +43,40 @@ def test_argument_errors_surface_as_exceptions():
 def test_python_constants_match_the_header():
     text = open(N._HEADER).read()
     assert int(re.search(r"#define BF_MAX_ITEMS_PER_ROW (\d+)", text).group(1)) == N.BF_MAX_ITEMS_PER_ROW
+    assert int(re.search(r"#define BF_LONG_ROW_FACTOR (\d+)", text).group(1)) == N.BF_LONG_ROW_FACTOR
+
+
+def test_split_row_items_rule():
+    """ceil(len / item) up to the 160-item cap; past 160 * 64 items' worth, ceil(len / (64 * item)):
+    the rule is continuous at the boundary and never exceeds ceil(len / item) (the capacity bound)."""
+    lib = N.load()
+    cap, fac = N.BF_MAX_ITEMS_PER_ROW, N.BF_LONG_ROW_FACTOR
+    for item in (1, 2, 768):
+        for length in (1, item, item + 1, cap * item, cap * item + 1, cap * fac * item, cap * fac * item + 1,
+                       111_059_956, 27_800_000):
+            n = lib.bf_split_row_items(length, item)
+            plain = -(-length // item)
+            want = plain if plain <= cap else max(cap, -(-length // (fac * item)))
+            assert n == want, (length, item)
+            assert 1 <= n <= plain
+    assert lib.bf_split_row_items(111_059_956, 768) == 2260     # the c5 token row: 49,152 entries per item
+    assert lib.bf_split_row_items(0, 768) == 0
+
+
+def test_kv_pass_variant_thresholds():
+    """bf_attn_bwd_kv_variant reports the dk/dv pass instance a shape takes (host-only): four rows per
+    group past 1M kv rows in bf16 (16M in fp32), non-temporal gathers past 256 MB of q + dO, slot
+    prefetch for bf16 with several rows per group."""
+    import torch
+    from budgetformer_amd.hip_ops import kv_pass_variant
+    c3 = kv_pass_variant(2_449_030, 2_449_030, torch.bfloat16, 8, 16)
+    assert c3 == {"rows_per_group": 4, "stream_rows": True, "prefetch_slots": True}
+    c2 = kv_pass_variant(169_344, 169_344, torch.float32, 8, 16)
+    assert c2 == {"rows_per_group": 1, "stream_rows": False, "prefetch_slots": False}
+    assert kv_pass_variant(300_000, 17_000_000, torch.float32, 8, 16) == {
+        "rows_per_group": 4, "stream_rows": True, "prefetch_slots": False}
+    assert kv_pass_variant(600_000, 2_000_000, torch.bfloat16, 8, 16)["stream_rows"]      # 307 MB > 256 MB
+    assert not kv_pass_variant(500_000, 2_000_000, torch.bfloat16, 8, 16)["stream_rows"]  # 256 MB: not above
 
 
 def test_split_capacity_bound():

@@ -49,6 +49,16 @@ def test_philox_uniforms_and_walk_bit_exact(hip_device):
         assert np.array_equal(walks.cpu().numpy(), et.random_walk(rowptr, col, et.walk_starts(n, P), L, u_ref))
 
 
+def test_device_philox_known_answers(hip_device):
+    """The device Philox against the Random123 zero vector directly: walk 0, seed 0, offset 0,
+    steps 0..3 are the four published output words (0x6627E8D5, 0xE169C58D, 0xBC57AC4C,
+    0x9B00DBD8) mapped to (x >> 8) * 2^-24."""
+    from budgetformer_amd import hip_ops
+    u = hip_ops.walk_uniforms(0, 1, 1, 4, 0, 0, device=hip_device).cpu().numpy()[0]
+    words = (0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8)
+    assert [float(x) for x in u] == [float(np.float32((w >> 8) / 16777216.0)) for w in words]
+
+
 def test_philox_uniforms_are_uniform(hip_device):
     from budgetformer_amd import hip_ops
     u = hip_ops.walk_uniforms(0, 200_000, 2, 4, 1234, device=hip_device).cpu().numpy().ravel()

@@ -1,0 +1,143 @@
+"""Parity of the kernel instances and table shapes the large configurations run.
+
+c3 (2.45M nodes, bf16, B=16, P=4), c4 (2.92M nodes, bf16, B=32, L=8) and c5 (a 27.8M-query
+shard, bf16) take code paths the small parity graphs never reach:
+- the dk/dv pass with non-temporal q/dO gathers (q + dO above 256 MB), four kv rows per lane
+  group and prefetched row slots (past 1M kv rows in bf16) — and in fp32 past 16M kv rows;
+- edge tables of power-law graphs with ~17K-degree hubs at B=16 (8, 8) P=4 L=4 and
+  B=32 (16, 16) P=4 L=8, drawn from the production Philox stream.
+The attention problems keep a few thousand attended rows inside the large tables, so the
+float64 oracle runs on the compacted problem (the attended rows only) in seconds; every other
+row must come out zero.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import edge_table as et
+from oracle import philox
+from oracle import sparse_attention as sa
+from parity_helpers import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _compact_problem(dev, n_q, n_kv, active_q, touched_kv, E, hub_edges, dtype, seed, H=8, hn=16):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    qa = torch.randperm(n_q, generator=g, device=dev)[:active_q].sort().values
+    kt = torch.randperm(n_kv, generator=g, device=dev)[:touched_kv].sort().values
+    src_c = torch.randint(0, touched_kv, (E,), generator=g, device=dev)
+    src_c[:hub_edges] = 0                           # one hub key row: key-side split items
+    dst_c = torch.randint(0, active_q, (E,), generator=g, device=dev)
+    q = torch.empty(n_q, H, hn, device=dev, dtype=dtype).normal_(generator=g)
+    dout = torch.empty(n_q, H, hn, device=dev, dtype=dtype).normal_(generator=g)
+    k = torch.empty(n_kv, H, hn, device=dev, dtype=dtype).normal_(generator=g)
+    v = torch.empty(n_kv, H, hn, device=dev, dtype=dtype).normal_(generator=g)
+    return qa, kt, src_c, dst_c, q, dout, k, v
+
+
+def _check_compact(hip_device, n_q, n_kv, dtype, expect, tol):
+    from budgetformer_amd import hip_ops
+    from budgetformer_amd.hip_ops import AttentionIndex
+    H, hn = 8, 16
+    variant = hip_ops.kv_pass_variant(n_q, n_kv, dtype, H, hn)
+    assert variant == expect, variant
+    qa, kt, src_c, dst_c, q, dout, k, v = _compact_problem(hip_device, n_q, n_kv, 20_000, 6_000, 200_000, 3_000,
+                                                           dtype, seed=n_kv % 1000 + 11)
+    idx = AttentionIndex.from_coo(torch.stack([kt[src_c], qa[dst_c]]), n_q, n_kv)
+    out, Z = hip_ops.attn_forward(idx, q, k, v)
+    dq, dk, dv, _ = hip_ops.attn_backward(idx, q, k, v, out, Z, dout)
+    torch.cuda.synchronize()
+    idx.resolve()
+    assert idx.kplan.items > 0          # the hub key row ran as split items
+    ei = torch.stack([src_c, dst_c]).cpu()
+    qc, doc = q[qa].double().cpu(), dout[qa].double().cpu()
+    kc, vc = k[kt].double().cpu(), v[kt].double().cpu()
+    ro, rZ = sa.attention_forward_stats(kc, qc, vc, ei)
+    rdq, rdk, rdv, _ = sa.attention_backward_closed_form(kc, qc, vc, ei, ro, rZ, doc)
+    for name, got, ref in (("out", out[qa], ro), ("dq", dq[qa], rdq), ("dk", dk[kt], rdk), ("dv", dv[kt], rdv)):
+        assert_close(name, got, ref, tol)
+    for t, rows in ((out, qa), (dq, qa), (dk, kt), (dv, kt)):
+        t[rows] = 0
+        assert not t.any()
+
+
+def test_bf16_kv_pass_streaming_four_rows_prefetched_slots(hip_device):
+    """attn_bwd_kv_kernel<bf16, NT, PRE>, the dominant instance of c3-c5: 600K queries (q + dO = 307 MB)
+    and 2M kv rows, 20K attending queries, 6K attended kv rows (one a 3K-entry hub)."""
+    _check_compact(hip_device, 600_000, 2_000_000, torch.bfloat16,
+                   {"rows_per_group": 4, "stream_rows": True, "prefetch_slots": True}, 2e-2)
+
+
+def test_fp32_kv_pass_past_16m_rows_streaming(hip_device):
+    """fp32 with four kv rows per group (17M kv rows) and non-temporal gathers (300K queries)."""
+    _check_compact(hip_device, 300_000, 17_000_000, torch.float32,
+                   {"rows_per_group": 4, "stream_rows": True, "prefetch_slots": False}, 1e-5)
+
+
+@pytest.mark.parametrize("b_r,b_w,P,L", [(8, 8, 4, 4), (16, 16, 4, 8)])
+def test_power_law_tables_with_17k_hubs(hip_device, b_r, b_w, P, L):
+    """c3 (B=16 (8,8), P=4, L=4) and c4 (B=32 (16,16), P=4, L=8) table shapes on a device-generated
+    120K-node power-law graph (avg degree 50, hubs near 17K): bit-exact against the oracle with the
+    Philox uniforms the production walk draws; hub rows take the workgroup-per-query path."""
+    from budgetformer_amd import hip_ops
+    from budgetformer_amd.edges import build_attention_edges
+    from budgetformer_amd.graph import chung_lu_device
+    n = 120_000
+    g = chung_lu_device(n, 6_000_000, exponent=2.1, seed=5, max_degree=17_000, device=hip_device)
+    rowptr = g.rowptr.cpu().numpy()
+    col = g.col.cpu().numpy()
+    deg = np.diff(rowptr)
+    assert deg.max() > 10_000 and (deg > hip_ops.HUB_THRESHOLD).sum() > 10
+    tab = build_attention_edges(g, real_edges_per_query=b_r, rw_edges_per_query=b_w, walk_length=L,
+                                walks_per_node=P, edge_seed=42)
+    u = philox.walk_uniforms(0, n, P, L, 42)
+    ref_t, ref_len = et.build_edge_table(rowptr, col, n, b_r, b_w, L, P, 42, u)
+    got_len = tab.row_len.cpu().numpy()
+    assert np.array_equal(got_len, ref_len)
+    assert np.array_equal(tab.table.cpu().numpy(), ref_t)
+    assert (got_len == b_r + b_w).any() and (got_len < b_r + b_w).any()   # full and short rows both occur
+
+
+@pytest.mark.parametrize("module", ["gt", "gps"])
+def test_gt_and_gps_modules_bf16_forward_backward(hip_device, module):
+    """GTCoreAttention (models/gt_dist_node_level.py:179-262) and GPSCoreAttention._sparse
+    (models/graphgps_dist_node_level.py:151-177) in bf16 on an edge table, forward and backward,
+    against the float64 oracle forms (GPS: eval mode, then an injected keep mask)."""
+    from budgetformer_amd.attention import GPSCoreAttention, GTCoreAttention
+    from budgetformer_amd.edges import build_attention_edges
+    from budgetformer_amd.graph import CSRGraph, chung_lu_csr
+    n, H, hn = 3000, 8, 16
+    rowptr, col = chung_lu_csr(n, 30_000, seed=9)
+    g = CSRGraph.from_csr(rowptr, col, n, device=hip_device)
+    tab = build_attention_edges(g, real_edges_per_query=8, rw_edges_per_query=8, walk_length=4,
+                                walks_per_node=4, edge_seed=42)
+    idx = tab.attention_index()
+    ei = tab.to_edge_index().cpu()
+    gen = torch.Generator().manual_seed(21)
+    q, k, v, dout = (torch.randn(n, H, hn, generator=gen).to(torch.bfloat16) for _ in range(4))
+    masks = [None]
+    if module == "gps":
+        masks.append(torch.rand(idx.nnz, H, generator=gen) >= 0.5)
+    for mask in masks:
+        qd, kd, vd = (t[None].to(hip_device).requires_grad_(True) for t in (q, k, v))
+        if module == "gt":
+            mod = GTCoreAttention(H * hn, 0.0, H)
+            out = mod(qd, kd, vd, None, tab)
+        else:
+            mod = GPSCoreAttention(H * hn, 0.5, H).eval()
+            drop = None if mask is None else mask.to(hip_device)
+            out = mod._sparse(qd, kd, vd, tab, H, hn, drop_mask=drop)
+        assert out.dtype == torch.bfloat16 and out.shape == (1, n, H * hn)
+        out.backward(dout.reshape(1, n, H * hn).to(hip_device))
+        q64, k64, v64 = (t.double().requires_grad_(True) for t in (q, k, v))
+        if module == "gt":
+            ref = sa.gt_sparse_attention(q64, k64, v64, ei)
+        else:
+            # the mask is per CSR entry; the oracle's edge list is the index's CSR order
+            ei_o = torch.stack([idx.kv.cpu().long(), idx.entry_rows().cpu()])
+            ref = sa.gps_sparse_attention(q64, k64, v64, ei_o, mask, 2.0 if mask is not None else 1.0)
+        ref.backward(dout.double())
+        assert_close("out", out.view(n, H, hn), ref, 2e-2)
+        for name, got, r in (("dq", qd.grad[0], q64.grad), ("dk", kd.grad[0], k64.grad), ("dv", vd.grad[0], v64.grad)):
+            assert_close(name, got, r, 2e-2)

@@ -1,0 +1,88 @@
+"""Pins oracle/philox.py: the Philox4x32-10 block function against the known-answer
+vectors published with the Random123 library (Salmon et al., SC'11; file
+kat_vectors, rows "philox4x32 10"), and the walk-stream layout the walk kernels
+draw from (word l % 4 of counter (w_lo, w_hi, off_lo + l // 4, off_hi), key
+(seed_lo, seed_hi), mapped to (x >> 8) * 2^-24) by values worked from those
+vectors by hand.
+"""
+import numpy as np
+import pytest
+
+from oracle import philox
+
+# (counter words c0..c3, key words k0, k1) -> output words, as published.
+KAT = [
+    ((0x00000000, 0x00000000, 0x00000000, 0x00000000), (0x00000000, 0x00000000),
+     (0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8)),
+    ((0xFFFFFFFF, 0xFFFFFFFF, 0xFFFFFFFF, 0xFFFFFFFF), (0xFFFFFFFF, 0xFFFFFFFF),
+     (0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD)),
+    ((0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344), (0xA4093822, 0x299F31D0),
+     (0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1)),
+]
+
+
+@pytest.mark.parametrize("ctr,key,expect", KAT)
+def test_random123_known_answers(ctr, key, expect):
+    got = philox.philox4x32_10(np.array([ctr], dtype=np.uint32), key)[0]
+    assert [int(x) for x in got] == list(expect)
+
+
+def test_known_answers_batched_in_one_call():
+    """The vectorised form gives every row its own answer (no cross-row mixing)."""
+    ctrs = np.array([c for c, _, _ in KAT], dtype=np.uint32)
+    for i, (_, key, expect) in enumerate(KAT):
+        got = philox.philox4x32_10(ctrs, key)[i]
+        assert [int(x) for x in got] == list(expect)
+
+
+def _u24(word: int) -> np.float32:
+    return np.float32((word >> 8) / 16777216.0)
+
+
+def test_walk_stream_first_block_is_the_zero_vector():
+    """Walk 0, seed 0, offset 0: steps 0..3 are the four words of Philox(0; 0), step 4 opens block 1."""
+    u = philox.walk_uniforms(0, 1, 1, 5, seed=0, offset=0)
+    expect = [_u24(w) for w in KAT[0][2]]
+    assert u.shape == (1, 5)
+    assert list(u[0, :4]) == expect
+    # hand-worked: 0x6627E8D5 >> 8 = 0x6627E8 = 6694888 -> 6694888 / 2^24
+    assert u[0, 0] == np.float32(6694888 / 16777216.0)
+    # step 4 is word 0 of counter (0, 0, 1, 0): differs from step 0
+    assert u[0, 4] != u[0, 0]
+
+
+def test_walk_stream_layout_with_high_words():
+    """Walk id, offset and seed above 2^32: each lands in its counter / key word.
+
+    Query q_lo = 2^31 with P = 2 gives walk id 2^32 (w_lo = 0, w_hi = 1); offset
+    2^32 + 5 gives block words (5 + l // 4, 1); seed 2^32 * 7 + 3 gives key (3, 7).
+    Each uniform is checked against a direct block call on the counter built by hand.
+    """
+    q_lo, P, L = 1 << 31, 2, 6
+    seed = (7 << 32) | 3
+    off = (1 << 32) | 5
+    u = philox.walk_uniforms(q_lo, 1, P, L, seed=seed, offset=off)
+    for p in range(P):
+        w = q_lo * P + p
+        for l in range(L):
+            blk = off + l // 4
+            ctr = np.array([[w & 0xFFFFFFFF, w >> 32, blk & 0xFFFFFFFF, blk >> 32]], dtype=np.uint32)
+            word = int(philox.philox4x32_10(ctr, (seed & 0xFFFFFFFF, seed >> 32))[0, l % 4])
+            assert u[p, l] == _u24(word), (p, l)
+    assert q_lo * P == 1 << 32   # the walk id's high word is exercised
+
+
+def test_walk_stream_reaches_the_all_ones_vector():
+    """Counter and key all ones (the second vector) through the uniform mapping."""
+    ctr = np.array([[0xFFFFFFFF] * 4], dtype=np.uint32)
+    r = philox.philox4x32_10(ctr, (0xFFFFFFFF, 0xFFFFFFFF))[0]
+    assert [int(x) for x in r] == list(KAT[1][2])
+    # the same words through the uniform mapping: top 24 bits over 2^24
+    assert _u24(int(r[0])) == np.float32(0x408F27 / 16777216.0)
+
+
+def test_uniform_range_endpoints():
+    """(x >> 8) * 2^-24 spans [0, 1 - 2^-24]: exact in float32 at both ends."""
+    assert _u24(0) == np.float32(0.0)
+    assert _u24(0xFFFFFFFF) == np.float32(1.0 - 2.0 ** -24)
+    assert _u24(0xFFFFFFFF) < np.float32(1.0)
