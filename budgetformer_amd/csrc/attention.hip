@@ -24,6 +24,8 @@
 // not a dense contraction, and the kernels are bound by gather bandwidth.
 #include "bf_common.h"
 
+#include <mutex>
+
 namespace bf {
 namespace {
 
@@ -1281,4 +1283,66 @@ extern "C" int bf_attn_bwd(const bf_attn_index* idx, int32_t dtype, int32_t num_
                            as_stream(stream));
   return bwd_impl<uint16_t>(idx, sh, q, k, v, bias, factor, Z, dout, dq, dk, dv, dbias, rowstat, partials,
                             as_stream(stream));
+}
+
+// ------------------------------------------------------------------ allocation-free backward
+// bf_attn_bwd's scratch (the row stats and the split partials) for callers that
+// cannot allocate: one file-scope device array, BF_ATTN_NOALLOC_SCRATCH_BYTES
+// on every GPU the library runs on, held until the process ends. Its address on
+// a device is looked up once (hipGetSymbolAddress with that device current) and
+// kept; host code never passes the array's own name, which is a host-side
+// stand-in. Every call on a GPU shares that GPU's array and finds the previous
+// call's contents there; nothing in it needs to start at zero (each pass writes
+// every row stat and record before the next pass reads it). Calls that overlap
+// on one GPU, on any streams, race on it.
+static __device__ __align__(256) unsigned char scratch[BF_ATTN_NOALLOC_SCRATCH_BYTES];
+
+namespace bf {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];   // per device; a plain array: no destructor at exit
+
+int scratch_address(void** out) {
+  int dev = 0;
+  BF_CHECK_HIP(hipGetDevice(&dev));
+  BF_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "attn_bwd_noalloc: device %d beyond the %d the library tracks", dev,
+               kMaxDevices);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    BF_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    BF_CHECK_ARG(p != nullptr, "attn_bwd_noalloc: no device address for the scratch array");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return BF_OK;
+}
+
+}  // namespace
+}  // namespace bf
+
+extern "C" int bf_attn_bwd_noalloc(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
+                                   const void* q, const void* k, const void* v, const float* bias,
+                                   const float* factor, const float* Z, const void* dout, void* dq, void* dk,
+                                   void* dv, float* dbias, void* stream) {
+  Shape sh;
+  int rc = make_shape(dtype, num_heads, head_dim, sh);
+  if (rc) return rc;
+  if ((rc = check_index(idx, true))) return rc;
+  const size_t stat_bytes = (size_t(idx->n_q) * size_t(num_heads) * 2 * sizeof(float) + 255) & ~size_t(255);
+  const int64_t part_floats = bf_attn_partials_floats(idx, num_heads, head_dim);
+  const size_t need = stat_bytes + size_t(part_floats) * sizeof(float);
+  BF_CHECK_ARG(need <= size_t(BF_ATTN_NOALLOC_SCRATCH_BYTES),
+               "attn_bwd_noalloc: this index needs %zu bytes of scratch (row stats %zu + partials %zu); the static "
+               "array holds %zu (use bf_attn_bwd with caller-provided scratch)",
+               need, stat_bytes, size_t(part_floats) * sizeof(float), size_t(BF_ATTN_NOALLOC_SCRATCH_BYTES));
+  void* base = nullptr;
+  if ((rc = scratch_address(&base))) return rc;
+  float* rowstat = static_cast<float*>(base);
+  float* partials = reinterpret_cast<float*>(static_cast<unsigned char*>(base) + stat_bytes);
+  ProfPause no_timer;   // the timer would create events
+  return bf_attn_bwd(idx, dtype, num_heads, head_dim, q, k, v, bias, factor, Z, dout, dq, dk, dv, dbias, rowstat,
+                     partials, stream);
 }

@@ -38,6 +38,14 @@ bool prof_enabled();
 void prof_begin(const char* name, hipStream_t st, int* token);
 void prof_end(int token, hipStream_t st);
 
+// Keeps the timer off for the calling thread while in scope (the timer creates
+// events and grows host lists, which an allocation-free call must not do).
+struct ProfPause {
+  ProfPause();
+  ~ProfPause();
+  bool prev;
+};
+
 #define BF_LAUNCH(name, kern, grid, block, lds, st, ...)                 \
   do {                                                                  \
     int _bf_tok = -1;                                                   \

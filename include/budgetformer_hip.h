@@ -451,6 +451,23 @@ int bf_attn_bwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int3
                 const float* Z, const void* dout, void* dq, void* dk, void* dv, float* dbias, float* rowstat,
                 float* partials, void* stream);
 
+/* bf_attn_bwd for callers that cannot allocate (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference: its backward is autograd over torch_scatter. The caller passes
+ * the inputs and outputs; the row stats and split partials live in a
+ * file-scope device array of BF_ATTN_NOALLOC_SCRATCH_BYTES per GPU (held until
+ * the process ends), so the call allocates nothing: no hipMalloc, no library
+ * allocation, the per-kernel timer paused. An index whose scratch
+ * (n_q*H*8 bytes, 256-aligned, + 4 * bf_attn_partials_floats) exceeds the
+ * array is rejected with BF_ERR_INVALID before any launch. Every call on a GPU
+ * shares that GPU's array: calls that overlap on one GPU (any streams) race.
+ * Results equal bf_attn_bwd's bit for bit.                                   */
+#define BF_ATTN_NOALLOC_SCRATCH_BYTES (64u << 20)
+int bf_attn_bwd_noalloc(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
+                        const void* q, const void* k, const void* v, const float* bias, const float* factor,
+                        const float* Z, const void* dout, void* dq, void* dk, void* dv, float* dbias,
+                        void* stream);
+
 /* How bf_attn_bwd runs its key-major (dk/dv) pass on this index, for callers
  * and tests that need to know which kernel instance a shape takes (host-only,
  * launches nothing): rows_per_group = short kv rows per lane group (1, or 4
