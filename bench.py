@@ -1,19 +1,26 @@
 #!/usr/bin/env python
 """Benchmark of BudgetFormer's per-layer hot path on one MI355X.
 
-A step is one pass of the hot path over config c2 (the headline configuration):
+A step is one pass of the hot path over one configuration:
   1. budgeted edge construction (Philox walks, real/RW top-k, merge) into the
-     [N, 8] table, the Graphormer global-token CSR, the reverse index and the
-     split plans;
-  2. one sparse-attention layer forward + backward over those edges
-     (N+1 = 169,344 queries, 8 heads x 16, fp32).
+     [N, B] table, the attention CSR (with the Graphormer global token where the
+     model has it), the reverse index and the split plans;
+  2. one sparse-attention layer forward + backward over those edges.
 Inputs (graph, q/k/v, dO) are resident in HBM before the timed region.
 
-`value` is the attention layer's algorithmic HBM throughput (gather model:
-A_fwd + A_bwd bytes per layer / fwd+bwd time), which the north-star target
-(>= 50% of 8 TB/s) is quoted on; the edge builder's RW edges/s, table
-entries/s and the per-kernel HIP-event timings are reported beside it, with
-the CPU oracle timed on this host's cores as `cpu_baseline`.
+The default run measures c2 (the configuration the north-star target is quoted
+on) and, in the same JSON line, a c3 record whose working set exceeds the
+256 MB Infinity Cache (`extra_configs`), each with its own roofline.
+
+`value` is the attention layer's throughput under the gather model (SURVEY
+8(d) v1: every gathered K/V/q/dO row counted at full size per edge) =
+algorithmic bytes / fwd+bwd time. It is a work rate, not an HBM rate: at c2 the
+gathered rows are served from the Infinity Cache and it exceeds the 8 TB/s HBM
+peak. Beside it: the compulsory (unique-tensor) bytes and their rate, a lower
+bound of the HBM traffic; the dominant kernel's roofline (algorithmic bytes /
+its HIP-event time, and the HBM-side traffic from the committed rocprofv3
+counter summary); the edge builder's RW edges/s and table entries/s; and the
+CPU oracle timed on this host's cores as `cpu_baseline`.
 """
 from __future__ import annotations
 
@@ -46,17 +53,30 @@ CONFIGS = {
                n=2_923_922, e=13_975_788, kind="device", H=8, hn=16, L=8, P=4, b_r=16, b_w=16, dtype="bfloat16",
                token=False, cpu_sample=200_000),
     "c5": dict(name="c5: one GPU's 27.8M-query shard of a power-law graph N=111,059,956 E=1.6B (max deg 100K), "
-                    "Graphormer hidden 128, 8 heads, L=4 P=2 B=8 (4,4), bf16",
+                    "Graphormer hidden 128, 8 heads, L=4 P=2 B=8 (4,4), bf16, global token (the shard holds node 0)",
                n=111_059_956, e=1_600_000_000, kind="device", max_degree=100_000, H=8, hn=16, L=4, P=2, b_r=4,
-               b_w=4, dtype="bfloat16", token=False, n_q=27_800_000, cpu_sample=None),
+               b_w=4, dtype="bfloat16", token=True, n_q=27_800_000, cpu_sample=None),
 }
 
 
 def attention_bytes(s, D, H, n_q, n_kv, nnz):
-    """Gather-model algorithmic bytes (forward, backward) of one layer."""
+    """Gather-model algorithmic bytes (forward, backward) of one layer (as built: the
+    backward does not read the forward's output, so v1's O read is left out)."""
     a_fwd = s * D * (2 * n_q + 2 * nnz) + 4 * nnz + 4 * n_q * H
-    a_bwd = s * D * (4 * n_q + 2 * n_kv + 4 * nnz) + 8 * n_q * H + 8 * nnz * H + 12 * nnz
+    a_bwd = s * D * (3 * n_q + 2 * n_kv + 4 * nnz) + 8 * n_q * H + 8 * nnz * H + 12 * nnz
     return a_fwd, a_bwd
+
+
+def compulsory_bytes(s, D, H, n_q, n_kv, nnz, n_kv_touched):
+    """Unique-tensor bytes of one layer, each tensor read or written once: a lower bound of its HBM
+    traffic. Forward: q, the attended K and V rows, out, Z, the CSR (qptr, kv). Backward: q, dO, Z, the
+    attended K and V rows, dq, dK and dV of every kv row, the row stats (written, read), the CSR and the
+    reverse index (kptr, kq)."""
+    row = s * D
+    fwd = row * (2 * n_q + 2 * n_kv_touched) + 4 * H * n_q + 8 * n_q + 4 * nnz
+    bwd = (row * (3 * n_q + 2 * n_kv_touched + 2 * n_kv) + 4 * H * n_q + 16 * H * n_q + 8 * n_q + 4 * nnz
+           + 8 * n_kv + 4 * nnz)
+    return fwd + bwd
 
 
 def token_records(s, D, n_q, q_items):
@@ -85,8 +105,8 @@ def kernel_bytes(s, D, H, lens_q, lens_k, n_token_rec=0):
     return {
         # Q read, O write, K and V gathered per edge, kv ids, Z write, qptr
         "attn_fwd_kernel": row * (2 * n_q + 2 * nnz) + 4 * nnz + 4 * H * n_q + 8 * n_q,
-        # Q, dO, O read, dQ write, K and V per edge, kv ids, Z read + row stats write, qptr (+ token records)
-        "attn_bwd_q_kernel": row * (4 * n_q + 2 * nnz) + 4 * nnz + 12 * H * n_q + 8 * n_q + rec_bytes,
+        # Q, dO read, dQ write, K and V per edge, kv ids, Z read + row stats write, qptr (+ token records)
+        "attn_bwd_q_kernel": row * (3 * n_q + 2 * nnz) + 4 * nnz + 12 * H * n_q + 8 * n_q + rec_bytes,
         # dK, dV written for every row; K, V read for rows with entries; Q and dO per gathered entry,
         # the {1/D', Delta/D'} row stats per gathered entry, kq ids, kptr, row order (+ token records)
         "attn_bwd_kv_kernel": row * (2 * n_kv + 2 * nk_touched + 2 * gathered) + 8 * H * gathered
@@ -157,6 +177,58 @@ def pmc_summary(fetch_csv, write_csv, copy_fetch_csv, copy_write_csv, copy_bytes
     return "\n".join(lines), out
 
 
+def _counter_means_by_name(path: str) -> dict:
+    """{kernel: {counter: mean value per dispatch}} from a rocprofv3 counter_collection.csv holding several
+    counters (one row per dispatch and counter)."""
+    import collections
+    import csv
+    acc = collections.defaultdict(lambda: collections.defaultdict(list))
+    for r in csv.DictReader(open(path)):
+        acc[_short_kernel(r["Kernel_Name"])][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    return {k: {c: sum(v) / len(v) for c, v in d.items()} for k, d in acc.items()}
+
+
+def _req_bytes(rd: dict, wr: dict):
+    """(read bytes, write bytes) of one dispatch from the request-size counters: 32-, 64- and 128-byte reads
+    (TCC_EA0_RDREQ counts every read request once), 32- and 64-byte writes."""
+    n, n32, n128 = rd["TCC_EA0_RDREQ_sum"], rd["TCC_EA0_RDREQ_32B_sum"], rd["TCC_EA0_RDREQ_128B_sum"]
+    read = 32 * n32 + 128 * n128 + 64 * (n - n32 - n128)
+    w, w64 = wr["TCC_EA0_WRREQ_sum"], wr["TCC_EA0_WRREQ_64B_sum"]
+    write = 64 * w64 + 32 * (w - w64)
+    return read, write
+
+
+def request_summary(read_csv, write_csv, copy_read_csv, copy_write_csv, copy_bytes, kernels_of_interest):
+    """HBM-side (L2-to-fabric) bytes per dispatch summed by request size: reads = 32 x RDREQ_32B + 128 x
+    RDREQ_128B + 64 x the rest, writes = 64 x WRREQ_64B + 32 x the rest. A plain copy of ``copy_bytes``
+    (read and written) checks the sums; no scale factor is applied. Returns (markdown, dict)."""
+    rd, wr = _counter_means_by_name(read_csv), _counter_means_by_name(write_csv)
+    crd, cwr = _counter_means_by_name(copy_read_csv), _counter_means_by_name(copy_write_csv)
+    copy_name = max(crd, key=lambda k: crd[k].get("TCC_EA0_RDREQ_sum", 0))
+    c_read, c_write = _req_bytes(crd[copy_name], cwr[copy_name])
+    lines = [f"Check ({copy_name}, {copy_bytes / 2**30:.2f} GiB read + written): the request-size sums read "
+             f"{c_read / copy_bytes:.3f} x and write {c_write / copy_bytes:.3f} x the copied bytes.", "",
+             "| kernel | read requests (32 B / 64 B / 128 B) | write requests (32 B / 64 B) | read bytes | "
+             "write bytes | HBM-side bytes per dispatch |", "|---|---|---|---:|---:|---:|"]
+    out = {"method": "request-size sums (TCC_EA0_RDREQ, _32B, _128B; TCC_EA0_WRREQ, _64B)",
+           "copy_check": {"read": round(c_read / copy_bytes, 4), "write": round(c_write / copy_bytes, 4)},
+           "kernels": {}}
+    for k in kernels_of_interest:
+        if k not in rd or k not in wr:
+            continue
+        r, w = rd[k], wr[k]
+        rb, wb = _req_bytes(r, w)
+        n32, n128 = r["TCC_EA0_RDREQ_32B_sum"], r["TCC_EA0_RDREQ_128B_sum"]
+        n64 = r["TCC_EA0_RDREQ_sum"] - n32 - n128
+        w64 = w["TCC_EA0_WRREQ_64B_sum"]
+        out["kernels"][k] = {"read_bytes": int(rb), "write_bytes": int(wb), "traffic_bytes": int(rb + wb),
+                             "rdreq_32b": int(n32), "rdreq_64b": int(n64), "rdreq_128b": int(n128),
+                             "wrreq_32b": int(w["TCC_EA0_WRREQ_sum"] - w64), "wrreq_64b": int(w64)}
+        lines.append(f"| {k} | {n32:,.0f} / {n64:,.0f} / {n128:,.0f} | {w['TCC_EA0_WRREQ_sum'] - w64:,.0f} / "
+                     f"{w64:,.0f} | {rb:,.0f} | {wb:,.0f} | {rb + wb:,.0f} |")
+    return "\n".join(lines), out
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -174,6 +246,9 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--extra", default=None,
+                    help="comma-separated configs measured after the main one and reported in the same JSON line "
+                         "under extra_configs (default: c3 when --config is c2, else none; 'none' for none)")
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
     ap.add_argument("--chunk", type=int, default=None, help="split threshold (rows longer than this are split)")
     ap.add_argument("--item", type=int, default=None, help="entries per split item")
@@ -181,17 +256,23 @@ def main(argv=None):
                     help="print a markdown summary of a rocprofv3 kernel_stats.csv and exit")
     ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "COPY_FETCH_CSV", "COPY_WRITE_CSV"),
                     help="summarise FETCH_SIZE/WRITE_SIZE counter runs (calibrated by a copy kernel) and exit")
+    ap.add_argument("--req-summary", nargs=4, metavar=("READ_CSV", "WRITE_CSV", "COPY_READ_CSV", "COPY_WRITE_CSV"),
+                    help="summarise request-size counter runs (TCC_EA0_RDREQ/_32B/_128B and TCC_EA0_WRREQ/_64B) "
+                         "and exit")
     ap.add_argument("--copy-bytes", type=int, default=2 ** 30, help="bytes the calibration copy reads and writes")
-    ap.add_argument("--pmc-json", help="with --pmc-summary: also write the per-kernel traffic as JSON here")
+    ap.add_argument("--pmc-json", help="with --pmc-summary / --req-summary: also write the per-kernel traffic here")
     args = ap.parse_args(argv)
     if args.rocprof_summary:
         print(rocprof_summary(args.rocprof_summary))
         return 0
-    if args.pmc_summary:
-        names = ["attn_fwd_kernel", "attn_bwd_q_kernel", "attn_bwd_kv_kernel", "attn_fwd_reduce_kernel",
-                 "attn_bwd_kv_reduce_kernel", "rw_select_kernel", "real_select_fused_kernel",
-                 "table_fill_kernel", "unpack_rkey_kernel"]
-        md, data = pmc_summary(*args.pmc_summary, args.copy_bytes, names)
+    names = ["attn_fwd_kernel", "attn_bwd_q_kernel", "attn_bwd_kv_kernel", "attn_fwd_reduce_kernel",
+             "attn_bwd_q_reduce_kernel", "attn_bwd_kv_reduce_kernel", "rw_select_kernel", "real_select_fused_kernel",
+             "table_fill_kernel", "unpack_rkey_kernel"]
+    if args.pmc_summary or args.req_summary:
+        if args.pmc_summary:
+            md, data = pmc_summary(*args.pmc_summary, args.copy_bytes, names)
+        else:
+            md, data = request_summary(*args.req_summary, args.copy_bytes, names)
         print(md)
         if args.pmc_json:
             with open(args.pmc_json, "w") as fh:
@@ -203,6 +284,33 @@ def main(argv=None):
               file=sys.stderr)
         return 2
 
+    import torch
+
+    from budgetformer_amd import _native
+
+    _native.load()
+    chunk = args.chunk
+    item = args.item
+    result = run(args.config, args.steps, args.warmup, chunk, item, with_cpu=not args.no_cpu_baseline)
+    extra = args.extra if args.extra is not None else ("c3" if args.config == "c2" else "none")
+    extras = [c for c in extra.split(",") if c and c != "none"]
+    records = []
+    for name in extras:
+        if name not in CONFIGS:
+            raise SystemExit(f"bench.py: unknown config {name!r} in --extra")
+        torch.cuda.empty_cache()
+        rec = run(name, args.steps, args.warmup, chunk, item, with_cpu=False)
+        records.append({k: rec[k] for k in ("config", "dtype", "steps", "warmup", "ms_per_step", "value", "unit",
+                                            "value_basis", "attn_fwd_bwd_ms", "edge_build_ms", "attention",
+                                            "builder", "roofline", "kernels")})
+    if records:
+        result["extra_configs"] = records
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def run(config, steps, warmup, chunk=None, item=None, with_cpu=True):
+    """Measures one configuration; returns its result record."""
     import numpy as np
     import torch
 
@@ -210,12 +318,10 @@ def main(argv=None):
     from budgetformer_amd.edges import build_attention_edges
     from budgetformer_amd.graph import CSRGraph, chung_lu_csr, chung_lu_device, uniform_random_csr
 
-    cfg = CONFIGS[args.config]
+    cfg = CONFIGS[config]
     dev = torch.device("cuda:0")
-    _native.load()
     t_setup = time.time()
     n = cfg["n"]
-    rowptr = col = None
     if cfg["kind"] == "device":
         g = chung_lu_device(n, cfg["e"], exponent=2.1, seed=42, max_degree=cfg.get("max_degree"), device=dev)
     else:
@@ -228,8 +334,8 @@ def main(argv=None):
     D = H * hn
     dt = getattr(torch, cfg["dtype"])
     s_bytes = torch.finfo(dt).bits // 8
-    n_rows = cfg.get("n_q") or n                       # queries this GPU builds
-    S = n_rows + (1 if cfg["token"] else 0)            # attention query rows
+    n_rows = cfg.get("n_q") or n                       # queries this GPU builds (a shard from node 0 at c5)
+    S = n_rows + (1 if cfg["token"] else 0)            # attention query rows (+ the token row)
     S_kv = n + (1 if cfg["token"] else 0)              # key/value rows
     gq = torch.Generator(device=dev).manual_seed(43)
     q = torch.randn(S, H, hn, generator=gq, device=dev, dtype=torch.float32).to(dt)
@@ -239,8 +345,8 @@ def main(argv=None):
     torch.cuda.synchronize()
     print(f"[bench] {cfg['name']}: realized E={g.num_edges:,}; setup {time.time() - t_setup:.1f}s", flush=True)
 
-    chunk = args.chunk or hip_ops.DEFAULT_CHUNK
-    item = args.item or hip_ops.DEFAULT_ITEM
+    chunk = chunk or hip_ops.DEFAULT_CHUNK
+    item = item or hip_ops.DEFAULT_ITEM
 
     def build():
         tab = build_attention_edges(g, real_edges_per_query=cfg["b_r"], rw_edges_per_query=cfg["b_w"],
@@ -252,19 +358,19 @@ def main(argv=None):
 
     def layer(idx):
         out, Z = hip_ops.attn_forward(idx, q, k, v)
-        hip_ops.attn_backward(idx, q, k, v, out, Z, dout)
+        hip_ops.attn_backward(idx, q, k, v, None, Z, dout)
 
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         tab, idx = build()
         layer(idx)
     torch.cuda.synchronize()
-    print(f"[bench] warmup {args.warmup} steps done", flush=True)
+    print(f"[bench] {config}: warmup {warmup} steps done", flush=True)
 
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
-           torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+           torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(args.steps):
+    for i in range(steps):
         ev[i][0].record()
         tab, idx = build()
         ev[i][1].record()
@@ -275,25 +381,27 @@ def main(argv=None):
     # per-kernel durations from a separate pass of the same steps: the library's per-launch event
     # pairs cost host time, so they stay out of the timed loop above
     with _native.KernelTimer() as timer:
-        for i in range(args.steps):
+        for i in range(steps):
             tab, idx = build()
             layer(idx)
         torch.cuda.synchronize()
         kstats = timer.stats()
-    build_ms = sum(a.elapsed_time(b) for a, b, _ in ev) / args.steps
-    attn_ms = sum(b.elapsed_time(c) for _, b, c in ev) / args.steps
-    step_ms = wall * 1e3 / args.steps
-    print(f"[bench] timed {args.steps} steps: {step_ms:.3f} ms/step (build {build_ms:.3f}, attn fwd+bwd "
+    build_ms = sum(a.elapsed_time(b) for a, b, _ in ev) / steps
+    attn_ms = sum(b.elapsed_time(c) for _, b, c in ev) / steps
+    step_ms = wall * 1e3 / steps
+    print(f"[bench] {config}: timed {steps} steps: {step_ms:.3f} ms/step (build {build_ms:.3f}, attn fwd+bwd "
           f"{attn_ms:.3f})", flush=True)
 
     nnz = idx.nnz
     idx.resolve()                                      # plan counts for the report (after the timed loops)
-    a_fwd, a_bwd = attention_bytes(s_bytes, D, H, S, S_kv, nnz)
-    attn_gbs = (a_fwd + a_bwd) / (attn_ms * 1e-3) / 1e9
-
-    # per-kernel roofline of the three pass kernels
     lens_q = np.diff(idx.qptr.cpu().numpy())
     lens_k = np.diff(idx.kptr.cpu().numpy())
+    a_fwd, a_bwd = attention_bytes(s_bytes, D, H, S, S_kv, nnz)
+    attn_gbs = (a_fwd + a_bwd) / (attn_ms * 1e-3) / 1e9
+    comp = compulsory_bytes(s_bytes, D, H, S, S_kv, nnz, int((lens_k > 0).sum()))
+    comp_gbs = comp / (attn_ms * 1e-3) / 1e9
+
+    # per-kernel roofline of the three pass kernels
     n_rec = token_records(s_bytes, D, idx.n_q, idx.qplan.items) if idx.token_column else 0
     kb = kernel_bytes(s_bytes, D, H, lens_q, lens_k, n_rec)
     kernels = {}
@@ -306,15 +414,18 @@ def main(argv=None):
         kernels[name] = rec
     dominant = max((n_ for n_ in kernels if n_ in kb), key=lambda n_: kernels[n_]["avg_ms"])
     dom = kernels[dominant]
-    traffic = None
-    pmc_path = os.path.join(ROOT, "profiles", f"attention_{args.config}_{cfg['dtype']}_pmc.json")
+    traffic = traffic_src = None
+    pmc_path = os.path.join(ROOT, "profiles", f"attention_{config}_{cfg['dtype']}_pmc.json")
     if os.path.exists(pmc_path) and chunk == hip_ops.DEFAULT_CHUNK and item == hip_ops.DEFAULT_ITEM:
         with open(pmc_path) as fh:
             rec = json.load(fh).get("kernels", {}).get(dominant)
-        traffic = rec["traffic_bytes"] if rec else None
+        if rec:
+            traffic = rec["traffic_bytes"]
+            traffic_src = os.path.relpath(pmc_path, ROOT)
     roofline = {"kernel": dominant, "bound": "hbm", "achieved": dom["achieved_gbs"], "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(dom["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
-                "algorithmic_bytes": dom["algorithmic_bytes"]}
+                "algorithmic_bytes": dom["algorithmic_bytes"], "traffic_source": traffic_src,
+                "achieved_basis": "the kernel's algorithmic bytes (gather model) / its HIP-event average duration"}
 
     # edge-builder figures: RW pool edges = valid hop entries (d == 1, or the walk moved at step d)
     n_walks = n_rows * cfg["P"]
@@ -333,9 +444,13 @@ def main(argv=None):
         "metric": METRIC,
         "value": round(attn_gbs, 1),
         "unit": "GB/s",
+        "value_basis": "attention layer fwd+bwd under the gather model (SURVEY 8(d) v1: every gathered row counted "
+                       "at full size per edge) / its HIP-event time; a work rate, not HBM bandwidth (gathered rows "
+                       "served from the 256 MB Infinity Cache count in full); compulsory HBM bytes are under "
+                       "attention.compulsory_*",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": round(step_ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -350,28 +465,39 @@ def main(argv=None):
                    "split_plan": {"q_items": idx.qplan.items, "q_heavy": idx.qplan.heavy,
                                   "k_items": idx.kplan.items, "k_heavy": idx.kplan.heavy}},
         "attn_fwd_bwd_ms": round(attn_ms, 4),
-        "attn_algorithmic_bytes": a_fwd + a_bwd,
-        "attn_frac_of_hbm_peak": round(attn_gbs / HBM_PEAK_GBS, 4),
         "edge_build_ms": round(build_ms, 4),
-        "rw_pool_edges": pool_edges,
-        "rw_edges_per_s": round(pool_edges / (rw_ms * 1e-3), 1) if rw_ms else None,
-        "rw_walk_steps_per_s": round(n_walks * cfg["L"] / (rw_ms * 1e-3), 1) if rw_ms else None,
-        "rw_select_ms": rw_ms,
-        "real_select_merge_ms": merge_ms,
-        "table_entries_per_s": round(table_entries / (build_ms * 1e-3), 1),
+        "attention": {
+            "fwd_bwd_ms": round(attn_ms, 4),
+            "gather_model_bytes": a_fwd + a_bwd,
+            "gather_model_gbs": round(attn_gbs, 1),
+            "gather_model_frac_of_hbm_peak": round(attn_gbs / HBM_PEAK_GBS, 4),
+            "compulsory_bytes": comp,
+            "compulsory_gbs": round(comp_gbs, 1),
+            "compulsory_frac_of_hbm_peak": round(comp_gbs / HBM_PEAK_GBS, 4),
+        },
+        "builder": {
+            "edge_build_ms": round(build_ms, 4),
+            "rw_pool_edges": pool_edges,
+            "rw_edges_per_s": round(pool_edges / (rw_ms * 1e-3), 1) if rw_ms else None,
+            "rw_walk_steps_per_s": round(n_walks * cfg["L"] / (rw_ms * 1e-3), 1) if rw_ms else None,
+            "rw_select_ms": rw_ms,
+            "real_select_merge_ms": merge_ms,
+            "table_entries": table_entries,
+            "table_entries_per_s": round(table_entries / (build_ms * 1e-3), 1),
+        },
         "roofline": roofline,
         "kernels": kernels,
     }
 
-    if not args.no_cpu_baseline:
+    if with_cpu:
         if cfg.get("cpu_sample", 0) is None:
             result["cpu_baseline"] = {"value": None, "unit": "GB/s", "cores": os.cpu_count(), "kind": "port",
                                       "sample": "skipped: the CPU oracle would need the 111M-row K/V and 1.6B-edge "
                                                 "topology in host memory; see c3/c4 for sampled CPU timings"}
         else:
             result["cpu_baseline"] = cpu_baseline(cfg, g, tab, idx, q, k, v, dout, s_bytes, D, H)
-    print(json.dumps(result), flush=True)
-    return 0
+    del q, k, v, dout, tab, idx, g
+    return result
 
 
 def cpu_baseline(cfg, g, tab, idx, q, k, v, dout, s_bytes, D, H):
