@@ -49,9 +49,9 @@ CONFIGS = {
                n=2_449_029, e=61_859_140, kind="device", max_degree=17_000, H=8, hn=16, L=4, P=4, b_r=8, b_w=8,
                dtype="bfloat16", token=False, cpu_sample=200_000),
     "c4": dict(name="c4: power-law N=2,923,922 E=13,975,788, GraphGPS hidden 128, 8 heads, L=8 P=4 B=32 (16,16), "
-                    "bf16 (attention dropout off)",
+                    "bf16, attention dropout 0.5 (training; drawn in the kernels)",
                n=2_923_922, e=13_975_788, kind="device", H=8, hn=16, L=8, P=4, b_r=16, b_w=16, dtype="bfloat16",
-               token=False, cpu_sample=200_000),
+               token=False, dropout=0.5, cpu_sample=200_000),
     "c5": dict(name="c5: one GPU's 27.8M-query shard of a power-law graph N=111,059,956 E=1.6B (max deg 100K), "
                     "Graphormer hidden 128, 8 heads, L=4 P=2 B=8 (4,4), bf16, global token (the shard holds node 0)",
                n=111_059_956, e=1_600_000_000, kind="device", max_degree=100_000, H=8, hn=16, L=4, P=2, b_r=4,
@@ -88,11 +88,12 @@ def token_records(s, D, n_q, q_items):
     return q_items + -(-n_q // (256 // lpr))
 
 
-def kernel_bytes(s, D, H, lens_q, lens_k, n_token_rec=0):
+def kernel_bytes(s, D, H, lens_q, lens_k, n_token_rec=0, entry_ids=False):
     """Algorithmic bytes of the three pass kernels (each covers every entry: short rows and split items).
 
     With a token column (n_token_rec records) the dq pass also writes key 0's dK/dV terms, 2*D floats per
-    record, and the dk/dv pass reads those records instead of gathering key 0's entries and its K, V rows."""
+    record, and the dk/dv pass reads those records instead of gathering key 0's entries and its K, V rows.
+    entry_ids: the dk/dv pass also reads each gathered entry's CSR position (a dropout, bias or factor)."""
     n_q, nnz = lens_q.size, int(lens_q.sum())
     n_kv = lens_k.size
     nk_touched = int((lens_k > 0).sum())
@@ -110,7 +111,7 @@ def kernel_bytes(s, D, H, lens_q, lens_k, n_token_rec=0):
         # dK, dV written for every row; K, V read for rows with entries; Q and dO per gathered entry,
         # the {1/D', Delta/D'} row stats per gathered entry, kq ids, kptr, row order (+ token records)
         "attn_bwd_kv_kernel": row * (2 * n_kv + 2 * nk_touched + 2 * gathered) + 8 * H * gathered
-        + 4 * gathered + 12 * n_kv + rec_bytes,
+        + 4 * gathered + 12 * n_kv + rec_bytes + (4 * gathered if entry_ids else 0),
     }
 
 
@@ -347,6 +348,8 @@ def run(config, steps, warmup, chunk=None, item=None, with_cpu=True):
 
     chunk = chunk or hip_ops.DEFAULT_CHUNK
     item = item or hip_ops.DEFAULT_ITEM
+    rate = cfg.get("dropout", 0.0)
+    step_no = [0]
 
     def build():
         tab = build_attention_edges(g, real_edges_per_query=cfg["b_r"], rw_edges_per_query=cfg["b_w"],
@@ -354,11 +357,16 @@ def run(config, steps, warmup, chunk=None, item=None, with_cpu=True):
                                     global_token=cfg["token"])
         idx = tab.attention_index(chunk=chunk, item=item)
         idx.ensure_backward()
+        if rate:
+            idx.ensure_entries()    # the dropout's keep bits are keyed by CSR position
         return tab, idx
 
     def layer(idx):
-        out, Z = hip_ops.attn_forward(idx, q, k, v)
-        hip_ops.attn_backward(idx, q, k, v, None, Z, dout)
+        # training-mode GPS: a fresh Philox key per step, the same one for the forward and the backward
+        step_no[0] += 1
+        drop = hip_ops.Dropout(rate, seed=1000 + step_no[0]) if rate else None
+        out, Z = hip_ops.attn_forward(idx, q, k, v, dropout=drop)
+        hip_ops.attn_backward(idx, q, k, v, None, Z, dout, dropout=drop)
 
     for _ in range(warmup):
         tab, idx = build()
@@ -403,7 +411,7 @@ def run(config, steps, warmup, chunk=None, item=None, with_cpu=True):
 
     # per-kernel roofline of the three pass kernels
     n_rec = token_records(s_bytes, D, idx.n_q, idx.qplan.items) if idx.token_column else 0
-    kb = kernel_bytes(s_bytes, D, H, lens_q, lens_k, n_rec)
+    kb = kernel_bytes(s_bytes, D, H, lens_q, lens_k, n_rec, entry_ids=bool(rate))
     kernels = {}
     for name, (ms, launches) in sorted(kstats.items(), key=lambda x: -x[1][0]):
         avg = ms / max(launches, 1)
@@ -461,7 +469,8 @@ def run(config, steps, warmup, chunk=None, item=None, with_cpu=True):
                    "kv_rows": S_kv,
                    "table_entries": table_entries, "attention_edges": nnz, "heads": H, "head_dim": hn,
                    "walk_length": cfg["L"], "walks_per_node": cfg["P"], "budget": [cfg["b_r"], cfg["b_w"]],
-                   "global_token": cfg["token"], "split_chunk": chunk, "split_item": item,
+                   "global_token": cfg["token"], "attention_dropout": rate, "split_chunk": chunk,
+                   "split_item": item,
                    "split_plan": {"q_items": idx.qplan.items, "q_heavy": idx.qplan.heavy,
                                   "k_items": idx.kplan.items, "k_heavy": idx.kplan.heavy}},
         "attn_fwd_bwd_ms": round(attn_ms, 4),

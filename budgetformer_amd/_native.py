@@ -40,6 +40,11 @@ class AttnIndex(C.Structure):
     ]
 
 
+class AttnDropout(C.Structure):
+    """Mirror of ``struct bf_attn_dropout``."""
+    _fields_ = [("rate", C.c_float), ("seed", u64), ("offset", u64)]
+
+
 # name -> (restype, argtypes)
 _SIGS = {
     "bf_version": (C.c_int, []),
@@ -95,13 +100,14 @@ _SIGS = {
     "bf_row_order_and_plan": (C.c_int, [P_i64, i64, i32, i32, P_i32, vp, P_i32, P_i32, P_i32, i64, P_i32, i64,
                                         P_i32, vp, sz, vp]),
     "bf_attn_partials_floats": (i64, [C.POINTER(AttnIndex), i32, i32]),
-    "bf_attn_bwd_noalloc": (C.c_int, [C.POINTER(AttnIndex), i32, i32, i32, vp, vp, vp, P_f32, P_f32, P_f32, vp,
-                                      vp, vp, vp, P_f32, vp]),
+    "bf_attn_bwd_noalloc": (C.c_int, [C.POINTER(AttnIndex), i32, i32, i32, vp, vp, vp, P_f32, P_f32,
+                                      C.POINTER(AttnDropout), P_f32, vp, vp, vp, vp, P_f32, vp]),
     "bf_attn_bwd_kv_variant": (C.c_int, [C.POINTER(AttnIndex), i32, i32, i32, C.POINTER(i32), C.POINTER(i32),
                                          C.POINTER(i32)]),
-    "bf_attn_fwd": (C.c_int, [C.POINTER(AttnIndex), i32, i32, i32, vp, vp, vp, P_f32, P_f32, vp, P_f32, P_f32, vp]),
-    "bf_attn_bwd": (C.c_int, [C.POINTER(AttnIndex), i32, i32, i32, vp, vp, vp, P_f32, P_f32, P_f32, vp,
-                              vp, vp, vp, P_f32, P_f32, P_f32, vp]),
+    "bf_attn_fwd": (C.c_int, [C.POINTER(AttnIndex), i32, i32, i32, vp, vp, vp, P_f32, P_f32, C.POINTER(AttnDropout),
+                              vp, P_f32, P_f32, vp]),
+    "bf_attn_bwd": (C.c_int, [C.POINTER(AttnIndex), i32, i32, i32, vp, vp, vp, P_f32, P_f32, C.POINTER(AttnDropout),
+                              P_f32, vp, vp, vp, vp, P_f32, P_f32, P_f32, vp]),
 }
 
 _lib = None

@@ -34,11 +34,12 @@ class _SparseEdgeAttention(torch.autograd.Function):
     """out = sum_e exp(clamp(q.k/sqrt(hn)) + bias) * f * v / (Z + 1e-6), HIP fwd/bwd."""
 
     @staticmethod
-    def forward(ctx, q, k, v, bias_e, factor_e, index):
-        out, Z = hip_ops.attn_forward(index, q, k, v, bias_e, factor_e)
+    def forward(ctx, q, k, v, bias_e, factor_e, index, dropout):
+        out, Z = hip_ops.attn_forward(index, q, k, v, bias_e, factor_e, dropout)
         # the backward needs Z, not out (it sums Delta = dO . out from the entries in float32)
         ctx.save_for_backward(q, k, v, Z, bias_e, factor_e)
         ctx.index = index
+        ctx.dropout = dropout          # the same Philox key draws the same mask in the backward
         ctx.need_dbias = bias_e is not None and ctx.needs_input_grad[3]
         return out
 
@@ -46,20 +47,22 @@ class _SparseEdgeAttention(torch.autograd.Function):
     def backward(ctx, dout):
         q, k, v, Z, bias_e, factor_e = ctx.saved_tensors
         dq, dk, dv, dbias = hip_ops.attn_backward(ctx.index, q, k, v, None, Z, dout.contiguous(), bias_e, factor_e,
-                                                  need_dbias=ctx.need_dbias)
-        return dq, dk, dv, dbias, None, None
+                                                  need_dbias=ctx.need_dbias, dropout=ctx.dropout)
+        return dq, dk, dv, dbias, None, None, None
 
 
 def sparse_edge_attention(q, k, v, index: AttentionIndex, bias_e: Optional[torch.Tensor] = None,
-                          factor_e: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Functional form. q [n_q,H,hn], k/v [n_kv,H,hn]; bias_e/factor_e float32 [nnz,H]."""
+                          factor_e: Optional[torch.Tensor] = None,
+                          dropout: Optional[hip_ops.Dropout] = None) -> torch.Tensor:
+    """Functional form. q [n_q,H,hn], k/v [n_kv,H,hn]; bias_e/factor_e float32 [nnz,H]; dropout: the
+    in-kernel GraphGPS attention dropout (Philox keep mask per entry and head)."""
     dt = q.dtype
     q, k, v = q.contiguous(), k.to(dt).contiguous(), v.to(dt).contiguous()
     if bias_e is not None:
         bias_e = bias_e.float().contiguous()
     if factor_e is not None:
         factor_e = factor_e.float().contiguous()
-    return _SparseEdgeAttention.apply(q, k, v, bias_e, factor_e, index)
+    return _SparseEdgeAttention.apply(q, k, v, bias_e, factor_e, index, dropout)
 
 
 class _IndexCache:
@@ -195,9 +198,13 @@ class GTCoreAttention(nn.Module):
 class GPSCoreAttention(nn.Module):
     """GraphGPS core attention (models/graphgps_dist_node_level.py:135-209), sparse path on HIP.
 
-    Normalise per edge, then dropout, then aggregate (:166-176): the dropout
-    keep mask enters the kernels as a per-edge factor keep/(1-rate) on the V
-    message, which is the same arithmetic.
+    Normalise per edge, then dropout, then aggregate (:166-176). In training the
+    dropout is drawn inside the kernels (``hip_ops.Dropout``: a Philox keep bit
+    per CSR entry and head, the same bit in the forward and both backward
+    passes) and scales the kept V messages by 1/(1-rate), which is the
+    reference's arithmetic; no [nnz, H] mask is materialised. The Philox key is
+    drawn from torch's default generator, so ``torch.manual_seed`` fixes it. An
+    explicit ``drop_mask`` still enters as a per-edge factor.
     """
 
     def __init__(self, hidden_size, attention_dropout_rate, num_heads):
@@ -217,13 +224,13 @@ class GPSCoreAttention(nn.Module):
         vf = v.reshape(-1, num_heads, head_dim)
         idx = resolve_index(edge_index, qf.size(0), kf.size(0), q.device)
         rate = float(self.att_dropout.p)
-        factor = None
+        factor = dropout = None
         if drop_mask is not None:
             factor = drop_mask.float() / (1.0 - rate) if rate < 1.0 else torch.zeros_like(drop_mask, dtype=torch.float32)
         elif self.training and rate > 0.0:
-            keep = torch.rand(idx.nnz, num_heads, device=q.device) >= rate
-            factor = keep.float() / (1.0 - rate) if rate < 1.0 else torch.zeros(idx.nnz, num_heads, device=q.device)
-        out = sparse_edge_attention(qf, kf, vf, idx, None, factor)
+            seed = int(torch.randint(0, 2 ** 62, (1,), dtype=torch.int64).item())
+            dropout = hip_ops.Dropout(rate, seed)
+        out = sparse_edge_attention(qf, kf, vf, idx, None, factor, dropout)
         return out.view(batch_size, s_len, -1)
 
     def forward(self, q, k, v, attn_bias=None, edge_index=None, attn_type=None):

@@ -96,6 +96,102 @@ __device__ __forceinline__ typename Elem<T>::Raw load_row_raw_nt(const T* base, 
   return g.act ? Elem<T>::load_raw_nt(base + row * D + g.col0) : Elem<T>::zero_raw();
 }
 
+// ------------------------------------------------------------------ per-entry inputs
+// Beyond q, k and v an entry may carry an additive bias (after the clamp), a
+// factor on its V message (any caller factor), and the GraphGPS attention
+// dropout (models/graphgps_dist_node_level.py:166-176), drawn here rather than
+// read from a mask: entry e (its CSR position) and head h are kept iff
+// u < 1 - rate, u = word h % 4 of Philox4x32-10(counter (e_lo, e_hi,
+// offset + h / 4), key seed) mapped to (x >> 8) * 2^-24, and a kept entry's V
+// message is scaled by 1 / (1 - rate). The three passes evaluate the same bit.
+struct EdgeIn {
+  const float* bias;     // float32 [nnz, H] or NULL
+  const float* factor;   // float32 [nnz, H] or NULL
+  int drop;              // 1: the dropout factor applies
+  float keep;            // kept iff u < keep (= 1 - rate)
+  float scale;           // factor of a kept entry (1 / (1 - rate); 0 when rate = 1)
+  uint32_t seed_lo, seed_hi, off_lo, off_hi;
+};
+
+// Keep bits of entry e for heads 4*blk .. 4*blk + 3 (bit j: head 4*blk + j), one Philox call.
+__device__ __forceinline__ uint32_t keep_bits4(const EdgeIn& x, int64_t e, int blk) {
+  const uint64_t b = ((uint64_t(x.off_hi) << 32) | x.off_lo) + uint64_t(blk);
+  const U32x4 r = philox4x32_10(U32x4{uint32_t(e), uint32_t(uint64_t(e) >> 32), uint32_t(b), uint32_t(b >> 32)},
+                                x.seed_lo, x.seed_hi);
+  return (u24(r.x) < x.keep ? 1u : 0u) | (u24(r.y) < x.keep ? 2u : 0u) | (u24(r.z) < x.keep ? 4u : 0u) |
+         (u24(r.w) < x.keep ? 8u : 0u);
+}
+
+__device__ __forceinline__ float dropout_factor(const EdgeIn& x, int64_t e, int head) {
+  return ((keep_bits4(x, e, head >> 2) >> (head & 3)) & 1u) ? x.scale : 0.f;
+}
+
+// The keep bits of one iteration's kUnroll entries, drawn once per group: lane j < kUnroll * nb
+// (nb = ceil(H / 4) Philox blocks per entry) draws block j % nb of entry j / nb, and every lane then
+// takes its head's bit by a shuffle (iter_factor), instead of each lane drawing the block of its own
+// head for every entry. Groups narrower than kUnroll * nb lanes draw per lane (shared = false).
+template <int kUnroll>
+struct IterDrop {
+  bool shared;
+  uint32_t task;   // this lane's 4 keep bits
+};
+
+template <int kUnroll>
+__device__ __forceinline__ IterDrop<kUnroll> iter_drop(const EdgeIn& x, const int32_t (&epos)[kUnroll],
+                                                       const bool (&ok)[kUnroll], const Shape& sh,
+                                                       const GroupPos& g) {
+  IterDrop<kUnroll> it{false, 0u};
+  if (!x.drop) return it;
+  const int nb = (sh.H + 3) >> 2;
+  it.shared = kUnroll * nb <= (1 << sh.lpr_log2);
+  if (!it.shared) return it;
+  const int j = g.g_lane;
+  if (j < kUnroll * nb) {
+    const int u = j / nb, blk = j - u * nb;
+    int32_t e = 0;
+    bool live = false;
+#pragma unroll
+    for (int w = 0; w < kUnroll; ++w) {
+      if (w == u) {
+        e = epos[w];
+        live = ok[w];
+      }
+    }
+    if (live) it.task = keep_bits4(x, e, blk);
+  }
+  return it;
+}
+
+// V-message factor of entry u of the iteration (CSR position e) for this lane's head: the caller's
+// factor times the dropout factor. Every lane of the group calls it for the same u.
+template <int kUnroll, int EX>
+__device__ __forceinline__ float iter_factor(const EdgeIn& x, const IterDrop<kUnroll>& it, int u, int64_t e,
+                                             const Shape& sh, int head) {
+  float f = (EX == 2 && x.factor) ? x.factor[e * sh.H + head] : 1.f;
+  if (EX == 1 || x.drop) {
+    if (it.shared) {
+      const int nb = (sh.H + 3) >> 2;
+      const uint32_t bits = uint32_t(__shfl(int(it.task), u * nb + (head >> 2), 1 << sh.lpr_log2));
+      f *= ((bits >> (head & 3)) & 1u) ? x.scale : 0.f;
+    } else {
+      f *= dropout_factor(x, e, head);
+    }
+  }
+  return f;
+}
+
+// The V-message factor of a single entry e for this lane's head (1 without factor and dropout).
+template <int EX>
+__device__ __forceinline__ float edge_factor(const EdgeIn& x, int64_t e, const Shape& sh, int head) {
+  float f = (EX == 2 && x.factor) ? x.factor[e * sh.H + head] : 1.f;
+  if (EX == 1 || x.drop) f *= dropout_factor(x, e, head);
+  return f;
+}
+
+__device__ __forceinline__ float edge_bias(const EdgeIn& x, int64_t e, const Shape& sh, int head) {
+  return x.bias ? x.bias[e * sh.H + head] : 0.f;
+}
+
 // ------------------------------------------------------------------ forward
 // Entry ids of a row walked kUnroll at a time. bf16: a chunk of them comes in
 // one coalesced load, one id per lane of the group, and each iteration takes
@@ -132,11 +228,11 @@ struct ChunkIds {
   }
 };
 // Accumulates sum_e p*f*v (acc) and sum_e p (z) over entries [beg, end) of one row.
-template <typename T>
+// EX: the per-entry inputs compiled in (0 none, 1 dropout only, 2 bias, factor and dropout): each
+// instance carries only the code, and the registers, of what it uses.
+template <typename T, int EX>
 __device__ __forceinline__ void fwd_segment(const T* __restrict__ k, const T* __restrict__ v,
-                                            const int32_t* __restrict__ kv,
-                                            const float* __restrict__ bias,
-                                            const float* __restrict__ factor,
+                                            const int32_t* __restrict__ kv, const EdgeIn& ex,
                                             int64_t beg, int64_t end, const Shape& sh,
                                             const GroupPos& g, const typename Elem<T>::Raw& qr,
                                             float (&acc)[Elem<T>::kPerVec], float& z) {
@@ -171,14 +267,21 @@ __device__ __forceinline__ void fwd_segment(const T* __restrict__ k, const T* __
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) d[u] += __shfl_xor(d[u], o, 64);
     }
+    IterDrop<kUnroll> drop{false, 0u};
+    if (EX) {
+      int32_t epos[kUnroll];   // CSR positions (nnz < 2^31)
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) epos[u] = int32_t(e0 + u);
+      drop = iter_drop<kUnroll>(ex, epos, ok, sh, g);
+    }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       if (!ok[u]) continue;
       const int64_t e = e0 + u;
       float a = fminf(fmaxf(d[u] * sh.inv_scale, -kClamp), kClamp);
-      if (bias) a += bias[e * sh.H + g.head];
+      if (EX == 2) a += edge_bias(ex, e, sh, g.head);
       const float p = __expf(a);   // a is clamped to [-5, 5] (+ bias): exp2-based form is within 2 ulp
-      const float w = factor ? p * factor[e * sh.H + g.head] : p;
+      const float w = EX ? p * iter_factor<kUnroll, EX>(ex, drop, u, e, sh, g.head) : p;
       float vv[V];
       Elem<T>::unpack(vr[u], vv);
 #pragma unroll
@@ -360,11 +463,10 @@ __device__ __forceinline__ void store_out(T* __restrict__ out, float* __restrict
 }
 
 // Blocks [0, n_items) take the query-side items, the rest one short query row per group.
-template <typename T>
+template <typename T, int EX>
 __global__ __launch_bounds__(kBlock) void attn_fwd_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
-    const int64_t* __restrict__ qptr, const int32_t* __restrict__ kv,
-    const float* __restrict__ bias, const float* __restrict__ factor,
+    const int64_t* __restrict__ qptr, const int32_t* __restrict__ kv, EdgeIn ex,
     T* __restrict__ out, float* __restrict__ Z, Items it, int n_items_arg, int64_t n_q, Shape sh, int chunk,
     const int32_t* __restrict__ plan_counts) {
   constexpr int V = Elem<T>::kPerVec;
@@ -383,7 +485,7 @@ __global__ __launch_bounds__(kBlock) void attn_fwd_kernel(
 #pragma unroll
     for (int i = 0; i < V; ++i) unused[i] = 0.f;
     const typename Elem<T>::Raw qr = load_row_raw(q, r.row, sh.D, g);
-    fwd_segment<T>(k, v, kv, bias, factor, r.beg, r.end, sh, g, qr, acc, z);
+    fwd_segment<T, EX>(k, v, kv, ex, r.beg, r.end, sh, g, qr, acc, z);
     block_combine<V>(lds, it.stride, sh, g, acc, unused, false, z, true);
     if (r.single) {
       if ((threadIdx.x >> sh.lpr_log2) == 0) store_out(out, Z, r.row, sh, g, acc, z);
@@ -397,7 +499,7 @@ __global__ __launch_bounds__(kBlock) void attn_fwd_kernel(
   const int64_t beg = qptr[row], end = qptr[row + 1];
   if (end - beg > chunk) return;  // split row: its items and the reduce write it
   const typename Elem<T>::Raw qr = load_row_raw_nt(q, row, sh.D, g);
-  fwd_segment<T>(k, v, kv, bias, factor, beg, end, sh, g, qr, acc, z);
+  fwd_segment<T, EX>(k, v, kv, ex, beg, end, sh, g, qr, acc, z);
   store_out(out, Z, row, sh, g, acc, z);
 }
 
@@ -436,17 +538,16 @@ struct EntryTerms {
   float m;   // [inside the clamp] / sqrt(hn)
 };
 
-template <bool EXTRA>
-__device__ __forceinline__ EntryTerms entry_terms(float d, float wraw, float inv_dprime,
-                                                  const float* __restrict__ bias,
-                                                  const float* __restrict__ factor, int64_t e, const Shape& sh,
-                                                  const GroupPos& g) {
+// f: the entry's V-message factor (1 without a factor or dropout).
+template <int EX>
+__device__ __forceinline__ EntryTerms entry_terms(float d, float wraw, float inv_dprime, const EdgeIn& ex, int64_t e,
+                                                  float f, const Shape& sh, const GroupPos& g) {
   EntryTerms t;
   const float apre = d * sh.inv_scale;
   float a = fminf(fmaxf(apre, -kClamp), kClamp);
-  if (EXTRA && bias) a += bias[e * sh.H + g.head];
+  if (EX == 2) a += edge_bias(ex, e, sh, g.head);
   t.p = __expf(a);   // a is clamped to [-5, 5] (+ bias): exp2-based form is within 2 ulp
-  t.f = (EXTRA && factor) ? factor[e * sh.H + g.head] : 1.f;
+  t.f = EX ? f : 1.f;
   t.w = wraw * inv_dprime;
   t.m = (apre >= -kClamp && apre <= kClamp) ? sh.inv_scale : 0.f;
   return t;
@@ -465,13 +566,11 @@ __device__ __forceinline__ void add_entry(const EntryTerms& t, const float (&kk)
   c += fwp;
 }
 
-// A, B and c over entries [beg, end) of one query row. EXTRA: with a bias or
-// factor (compiled in only for the instance that uses them).
-template <typename T, bool EXTRA>
+// A, B and c over entries [beg, end) of one query row. EX: the per-entry
+// inputs compiled in (0 none, 1 dropout only, 2 bias, factor and dropout).
+template <typename T, int EX>
 __device__ __forceinline__ void dq_segment(const T* __restrict__ k, const T* __restrict__ v,
-                                           const int32_t* __restrict__ kv,
-                                           const float* __restrict__ bias,
-                                           const float* __restrict__ factor,
+                                           const int32_t* __restrict__ kv, const EdgeIn& ex,
                                            int64_t beg, int64_t end, const Shape& sh, const GroupPos& g,
                                            float inv_dprime, const typename Elem<T>::Raw& qr,
                                            const typename Elem<T>::Raw& gr,
@@ -513,10 +612,18 @@ __device__ __forceinline__ void dq_segment(const T* __restrict__ k, const T* __r
         w[u] += __shfl_xor(w[u], o, 64);
       }
     }
+    IterDrop<kUnroll> drop{false, 0u};
+    if (EX) {
+      int32_t epos[kUnroll];   // CSR positions (nnz < 2^31)
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) epos[u] = int32_t(e0 + u);
+      drop = iter_drop<kUnroll>(ex, epos, ok, sh, g);
+    }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       if (!ok[u]) continue;
-      const EntryTerms t = entry_terms<EXTRA>(d[u], w[u], inv_dprime, bias, factor, e0 + u, sh, g);
+      const float f = EX ? iter_factor<kUnroll, EX>(ex, drop, u, e0 + u, sh, g.head) : 1.f;
+      const EntryTerms t = entry_terms<EX>(d[u], w[u], inv_dprime, ex, e0 + u, f, sh, g);
       float kk[V];
       Elem<T>::unpack(kr[u], kk);
       add_entry<V>(t, kk, A, B, c);
@@ -537,9 +644,8 @@ struct TokenEntry {
   float m;     // [inside the clamp] / sqrt(hn)
 };
 
-template <typename T, bool EXTRA, bool ADD>
-__device__ __forceinline__ TokenEntry token_entry(const T* __restrict__ k, const T* __restrict__ v,
-                                                  const float* __restrict__ bias, const float* __restrict__ factor,
+template <typename T, int EX, bool ADD>
+__device__ __forceinline__ TokenEntry token_entry(const T* __restrict__ k, const T* __restrict__ v, const EdgeIn& ex,
                                                   int64_t e, const Shape& sh, const GroupPos& g, float inv_dprime,
                                                   const typename Elem<T>::Raw& qr, const typename Elem<T>::Raw& gr,
                                                   float (&A)[Elem<T>::kPerVec], float (&B)[Elem<T>::kPerVec],
@@ -551,7 +657,7 @@ __device__ __forceinline__ TokenEntry token_entry(const T* __restrict__ k, const
     d += __shfl_xor(d, o, 64);
     w += __shfl_xor(w, o, 64);
   }
-  const EntryTerms t = entry_terms<EXTRA>(d, w, inv_dprime, bias, factor, e, sh, g);
+  const EntryTerms t = entry_terms<EX>(d, w, inv_dprime, ex, e, EX ? edge_factor<EX>(ex, e, sh, g.head) : 1.f, sh, g);
   if (ADD) {
     float kk[V];
     Elem<T>::unpack(kr, kk);
@@ -563,14 +669,14 @@ __device__ __forceinline__ TokenEntry token_entry(const T* __restrict__ k, const
 // Key 0's terms from this row, dd = Delta / D': fk = g_b m q (its dK term),
 // fv = p f dO / D' (its dV term); and its dbias g_b at CSR position e. The
 // same expressions the key-major pass evaluates for an entry it gathers.
-template <typename T, bool EXTRA>
+template <typename T, int EX>
 __device__ __forceinline__ void finish_token(const TokenEntry& te, float inv_dprime, float dd,
                                              const typename Elem<T>::Raw& qr, const typename Elem<T>::Raw& gr,
                                              float* __restrict__ dbias, int64_t e, const Shape& sh, const GroupPos& g,
                                              float (&fk)[Elem<T>::kPerVec], float (&fv)[Elem<T>::kPerVec]) {
   constexpr int V = Elem<T>::kPerVec;
   const float gb = fmaf(te.fw, inv_dprime, -dd) * te.p;
-  if (EXTRA && dbias && g.lead) dbias[e * sh.H + g.head] = gb;
+  if (EX == 2 && dbias && g.lead) dbias[e * sh.H + g.head] = gb;
   const float gs = gb * te.m;
   const float pf = te.p * te.f * inv_dprime;
   float qq[V], gg[V];
@@ -641,11 +747,10 @@ __device__ __forceinline__ void sum_token_records(const float* __restrict__ rec0
 // With a token column (rows from tok_first on open with key 0) every workgroup also writes one
 // record of its rows' key-0 terms; a split row's key-0 terms are finished with the row: by its item
 // when the row has one, else by the dq reduce, which writes them into the row's first item's record.
-template <typename T, bool EXTRA>
+template <typename T, int EX>
 __global__ __launch_bounds__(kBlock) void attn_bwd_q_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
-    const int64_t* __restrict__ qptr, const int32_t* __restrict__ kv,
-    const float* __restrict__ bias, const float* __restrict__ factor,
+    const int64_t* __restrict__ qptr, const int32_t* __restrict__ kv, EdgeIn ex,
     const float* __restrict__ Z, const T* __restrict__ dout,
     T* __restrict__ dq, float* __restrict__ dbias, float2* __restrict__ rstat, Items it, int n_items_arg,
     int64_t n_q, Shape sh, int chunk, float* __restrict__ token_rec, int tok_first,
@@ -667,7 +772,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_q_kernel(
     const float inv_dprime = row_inv_dprime<T>(Z, r.row, sh, g);
     const int64_t e_tok = it.ptr[r.row];
     const bool tok_row = token_rec != nullptr && r.row >= tok_first && e_tok < it.ptr[r.row + 1];
-    dq_segment<T, EXTRA>(k, v, kv, bias, factor, r.beg, r.end, sh, g, inv_dprime, qr, gr, A, B, c);
+    dq_segment<T, EX>(k, v, kv, ex, r.beg, r.end, sh, g, inv_dprime, qr, gr, A, B, c);
     block_combine<V>(lds, it.stride, sh, g, A, B, true, c, true);
     float fk[V], fv[V];
 #pragma unroll
@@ -676,9 +781,9 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_q_kernel(
       if (grp == 0) {
         const float dd = c * inv_dprime;
         if (tok_row) {
-          const TokenEntry te = token_entry<T, EXTRA, false>(k, v, bias, factor, e_tok, sh, g, inv_dprime, qr, gr,
+          const TokenEntry te = token_entry<T, EX, false>(k, v, ex, e_tok, sh, g, inv_dprime, qr, gr,
                                                              A, B, c);
-          finish_token<T, EXTRA>(te, inv_dprime, dd, qr, gr, dbias, e_tok, sh, g, fk, fv);
+          finish_token<T, EX>(te, inv_dprime, dd, qr, gr, dbias, e_tok, sh, g, fk, fv);
         }
         store_dq<T, V>(dq, rstat, r.row, sh, g, A, B, inv_dprime, dd, false);
       }
@@ -708,12 +813,12 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_q_kernel(
   const int64_t e_tok = beg;
   TokenEntry te{};
   if (tok) {
-    te = token_entry<T, EXTRA, true>(k, v, bias, factor, e_tok, sh, g, inv_dprime, qr, gr, A, B, c);
+    te = token_entry<T, EX, true>(k, v, ex, e_tok, sh, g, inv_dprime, qr, gr, A, B, c);
     ++beg;
   }
   float dd = 0.f;
   if (live) {
-    dq_segment<T, EXTRA>(k, v, kv, bias, factor, beg, end, sh, g, inv_dprime, qr, gr, A, B, c);
+    dq_segment<T, EX>(k, v, kv, ex, beg, end, sh, g, inv_dprime, qr, gr, A, B, c);
     dd = c * inv_dprime;
     store_dq<T, V>(dq, rstat, row, sh, g, A, B, inv_dprime, dd, true);
   }
@@ -721,7 +826,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_q_kernel(
   float fk[V], fv[V];
 #pragma unroll
   for (int i = 0; i < V; ++i) fk[i] = fv[i] = 0.f;
-  if (tok) finish_token<T, EXTRA>(te, inv_dprime, dd, qr, gr, dbias, e_tok, sh, g, fk, fv);
+  if (tok) finish_token<T, EX>(te, inv_dprime, dd, qr, gr, dbias, e_tok, sh, g, fk, fv);
   // sum the wave's groups (a fixed butterfly), park the wave's sum in LDS, then the waves in order
   for (int o = 1 << sh.lpr_log2; o < 64; o <<= 1) {
 #pragma unroll
@@ -755,8 +860,8 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_q_kernel(
 // pass, which gathers the row stats.
 template <typename T>
 __global__ __launch_bounds__(kBlock) void attn_bwd_q_reduce_kernel(
-    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, const float* __restrict__ bias,
-    const float* __restrict__ factor, const float* __restrict__ Z, const T* __restrict__ dout, T* __restrict__ dq,
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, EdgeIn ex,
+    const float* __restrict__ Z, const T* __restrict__ dout, T* __restrict__ dq,
     float* __restrict__ dbias, float2* __restrict__ rstat, Items it, Shape sh, float* __restrict__ token_rec,
     int tok_first, const int32_t* __restrict__ plan_counts) {
   constexpr int V = Elem<T>::kPerVec;
@@ -777,8 +882,8 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_q_reduce_kernel(
   if (tok) {   // key 0 was summed by item 0; its scalars are recomputed here to finish its terms
     const typename Elem<T>::Raw qr = load_row_raw(q, row, sh.D, g);
     const typename Elem<T>::Raw gr = load_row_raw(dout, row, sh.D, g);
-    const TokenEntry te = token_entry<T, true, false>(k, v, bias, factor, e_tok, sh, g, inv_dprime, qr, gr, A, B, c);
-    finish_token<T, true>(te, inv_dprime, dd, qr, gr, dbias, e_tok, sh, g, fk, fv);
+    const TokenEntry te = token_entry<T, 2, false>(k, v, ex, e_tok, sh, g, inv_dprime, qr, gr, A, B, c);
+    finish_token<T, 2>(te, inv_dprime, dd, qr, gr, dbias, e_tok, sh, g, fk, fv);
     store_token_record<V>(token_rec + int64_t(it.item_off[row]) * (2 * sh.D), sh, g, fk, fv);
   }
 }
@@ -798,15 +903,13 @@ __device__ __forceinline__ typename Elem<T>::Raw gather_row(const T* base, int64
 
 // dK and dV of one kv row over its reverse entries [beg, end); with dbias, each
 // entry's g_b = (f w - Delta/D') p at its CSR position (the row stats carry the
-// exact Delta/D' the dq pass summed). EXTRA: the per-entry bias, factor and
-// dbias are compiled in only for the instance that uses them, so the plain
-// pass keeps its register count (fp32: 95 VGPRs, five waves per SIMD).
-template <typename T, bool NT, bool EXTRA>
+// exact Delta/D' the dq pass summed). EX: the per-entry inputs compiled in
+// (0 none, 1 dropout only, 2 bias, factor, dropout and dbias), so the plain
+// pass keeps its register count (fp32: 91 VGPRs, five waves per SIMD).
+template <typename T, bool NT, int EX>
 __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __restrict__ dout,
                                             const int32_t* __restrict__ kq,
-                                            const int32_t* __restrict__ ke,
-                                            const float* __restrict__ bias,
-                                            const float* __restrict__ factor,
+                                            const int32_t* __restrict__ ke, const EdgeIn& ex,
                                             float* __restrict__ dbias,
                                             const float2* __restrict__ rstat, int64_t beg,
                                             int64_t end, const Shape& sh, const GroupPos& g,
@@ -854,17 +957,24 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
         w[u] += __shfl_xor(w[u], o, 64);
       }
     }
+    int32_t epos[kUnroll];   // CSR positions of the entries (nnz < 2^31)
+    IterDrop<kUnroll> drop{false, 0u};
+    if (EX) {
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) epos[u] = ok[u] ? ke[i0 + u] : 0;
+      drop = iter_drop<kUnroll>(ex, epos, ok, sh, g);
+    }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       if (!ok[u]) continue;
-      const int64_t e = EXTRA ? int64_t(ke[i0 + u]) : 0;
+      const int64_t e = EX ? int64_t(epos[u]) : 0;
       const float apre = d[u] * sh.inv_scale;
       float a = fminf(fmaxf(apre, -kClamp), kClamp);
-      if (EXTRA && bias) a += bias[e * sh.H + g.head];
+      if (EX == 2) a += edge_bias(ex, e, sh, g.head);
       const float p = __expf(a);   // a is clamped to [-5, 5] (+ bias): exp2-based form is within 2 ulp
-      const float f = (EXTRA && factor) ? factor[e * sh.H + g.head] : 1.f;
+      const float f = EX ? iter_factor<kUnroll, EX>(ex, drop, u, e, sh, g.head) : 1.f;
       const float gb = fmaf(f * w[u], rs[u].x, -rs[u].y) * p;   // rs = {1/D', Delta/D'}
-      if (EXTRA && dbias && g.lead) dbias[e * sh.H + g.head] = gb;
+      if (EX == 2 && dbias && g.lead) dbias[e * sh.H + g.head] = gb;
       const float gs = (apre >= -kClamp && apre <= kClamp) ? gb * sh.inv_scale : 0.f;
       const float pf = p * f * rs[u].x;
       float qq[V], gg[V];
@@ -880,13 +990,13 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
 }
 
 // Blocks [0, k_items) take the key-side items, the rest one short key row per
-// group, longest rows first. EXTRA: with a bias, factor or dbias (needs ke).
-template <typename T, bool NT, bool PRE, bool EXTRA>
+// group, longest rows first. EX: 0 plain, 1 dropout only, 2 bias / factor / dropout / dbias
+// (EX > 0 needs ke).
+template <typename T, bool NT, bool PRE, int EX>
 __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const int64_t* __restrict__ kptr, const int32_t* __restrict__ kq,
-    const int32_t* __restrict__ ke, const float* __restrict__ bias,
-    const float* __restrict__ factor, float* __restrict__ dbias, const T* __restrict__ dout,
+    const int32_t* __restrict__ ke, EdgeIn ex, float* __restrict__ dbias, const T* __restrict__ dout,
     const float2* __restrict__ rstat, T* __restrict__ dk, T* __restrict__ dv, const int32_t* __restrict__ order,
     const uint64_t* __restrict__ spans, Items kit, int k_items_arg, int64_t n_kv, Shape sh, int chunk,
     int rows_per_group, const float* __restrict__ token_rec, int q_items_arg, int64_t q_row_blocks,
@@ -920,7 +1030,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
       sum_token_records<V>(token_rec, a0, a1, q_items, q_items_arg, sh, g, ak, av);
     } else {
       const typename Elem<T>::Raw kr = load_row_raw(k, r.row, sh.D, g), vr = load_row_raw(v, r.row, sh.D, g);
-      dkv_segment<T, NT, EXTRA>(q, dout, kq, ke, bias, factor, dbias, rstat, r.beg, r.end, sh, g, kr, vr, ak, av);
+      dkv_segment<T, NT, EX>(q, dout, kq, ke, ex, dbias, rstat, r.beg, r.end, sh, g, kr, vr, ak, av);
     }
     float z = 0.f;
     block_combine<V>(lds, kit.stride, sh, g, ak, av, true, z, false);
@@ -991,7 +1101,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
 #pragma unroll
     for (int i = 0; i < V; ++i) ak[i] = av[i] = 0.f;
     const typename Elem<T>::Raw kr = load_row_raw(k, row, sh.D, g), vr = load_row_raw(v, row, sh.D, g);
-    dkv_segment<T, NT, EXTRA>(q, dout, kq, ke, bias, factor, dbias, rstat, beg, end, sh, g, kr, vr, ak, av);
+    dkv_segment<T, NT, EX>(q, dout, kq, ke, ex, dbias, rstat, beg, end, sh, g, kr, vr, ak, av);
     if (g.act) {                  // written once, not read again in the pass: past the caches
       Elem<T>::store_nt(dk + row * sh.D + g.col0, ak);
       Elem<T>::store_nt(dv + row * sh.D + g.col0, av);
@@ -1100,9 +1210,36 @@ inline Items key_items(const bf_attn_index* idx, const Shape& sh, float* partial
                partials + int64_t(idx->q_items) * (2 * sh.D + sh.H), idx->item, 2 * sh.D + sh.H};
 }
 
+// The per-entry inputs of a call, with the dropout's Philox key and threshold.
+int make_edge_in(const float* bias, const float* factor, const bf_attn_dropout* dropout, EdgeIn& ex) {
+  ex = EdgeIn{bias, factor, 0, 1.f, 1.f, 0u, 0u, 0u, 0u};
+  if (dropout) {
+    BF_CHECK_ARG(dropout->rate >= 0.f && dropout->rate <= 1.f, "attention: dropout rate %g outside [0, 1]",
+                 double(dropout->rate));
+    if (dropout->rate > 0.f) {
+      ex.drop = 1;
+      ex.keep = 1.f - dropout->rate;
+      ex.scale = dropout->rate < 1.f ? 1.f / (1.f - dropout->rate) : 0.f;
+      ex.seed_lo = uint32_t(dropout->seed);
+      ex.seed_hi = uint32_t(dropout->seed >> 32);
+      ex.off_lo = uint32_t(dropout->offset);
+      ex.off_hi = uint32_t(dropout->offset >> 32);
+    }
+  }
+  return BF_OK;
+}
+
+inline bool has_extra(const EdgeIn& ex) { return ex.bias || ex.factor || ex.drop; }
+
+// The per-entry instance a call takes: 0 plain, 1 dropout only, 2 anything with a bias, factor or dbias.
+inline int edge_mode(const EdgeIn& ex, bool dbias) {
+  if (ex.bias || ex.factor || dbias) return 2;
+  return ex.drop ? 1 : 0;
+}
+
 template <typename T>
 int fwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const void* k, const void* v,
-             const float* bias, const float* factor, void* out, float* Z, float* partials, hipStream_t st) {
+             const EdgeIn& ex, void* out, float* Z, float* partials, hipStream_t st) {
   const T* Q = static_cast<const T*>(q);
   const T* K = static_cast<const T*>(k);
   const T* Vv = static_cast<const T*>(v);
@@ -1112,8 +1249,15 @@ int fwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
   const int64_t blocks = int64_t(n_items) + grid_for(idx->n_q, sh);
   if (blocks > 0) {
     const size_t lds = n_items > 0 ? combine_lds_bytes(sh) : 0;
-    BF_LAUNCH("attn_fwd_kernel", attn_fwd_kernel<T>, dim3(unsigned(blocks)), dim3(kBlock), lds, st, Q, K, Vv,
-              idx->qptr, idx->kv, bias, factor, O, Z, it, n_items, idx->n_q, sh, idx->chunk, idx->plan_counts);
+#define BF_LAUNCH_FWD(EX)                                                                                        \
+  BF_LAUNCH("attn_fwd_kernel", (attn_fwd_kernel<T, EX>), dim3(unsigned(blocks)), dim3(kBlock), lds, st, Q, K, Vv,  \
+            idx->qptr, idx->kv, ex, O, Z, it, n_items, idx->n_q, sh, idx->chunk, idx->plan_counts)
+    switch (edge_mode(ex, false)) {
+      case 2: BF_LAUNCH_FWD(2); break;
+      case 1: BF_LAUNCH_FWD(1); break;
+      default: BF_LAUNCH_FWD(0); break;
+    }
+#undef BF_LAUNCH_FWD
     BF_CHECK_LAUNCH();
   }
   if (idx->q_heavy > 0) {
@@ -1126,7 +1270,7 @@ int fwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
 
 template <typename T>
 int bwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const void* k, const void* v,
-             const float* bias, const float* factor, const float* Z, const void* dout, void* dq, void* dk, void* dv,
+             const EdgeIn& ex, const float* Z, const void* dout, void* dq, void* dk, void* dv,
              float* dbias, float* rstat_f, float* partials, hipStream_t st) {
   float2* rstat = reinterpret_cast<float2*>(rstat_f);
   const T* Q = static_cast<const T*>(q);
@@ -1145,19 +1289,20 @@ int bwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
     const size_t lds = (idx->q_items > 0 || token_rec) ? combine_lds_bytes(sh) : 0;
 #define BF_LAUNCH_Q(EX)                                                                                          \
   BF_LAUNCH("attn_bwd_q_kernel", (attn_bwd_q_kernel<T, EX>), dim3(unsigned(q_blocks)), dim3(kBlock), lds, st, Q, K, \
-            Vv, idx->qptr, idx->kv, bias, factor, Z, dO, static_cast<T*>(dq), dbias, rstat, qit, idx->q_items,      \
+            Vv, idx->qptr, idx->kv, ex, Z, dO, static_cast<T*>(dq), dbias, rstat, qit, idx->q_items,                \
             idx->n_q, sh, idx->chunk, token_rec, tok_first, idx->plan_counts)
-    if (bias || factor || dbias)
-      BF_LAUNCH_Q(true);
-    else
-      BF_LAUNCH_Q(false);
+    switch (edge_mode(ex, dbias != nullptr)) {
+      case 2: BF_LAUNCH_Q(2); break;
+      case 1: BF_LAUNCH_Q(1); break;
+      default: BF_LAUNCH_Q(0); break;
+    }
 #undef BF_LAUNCH_Q
     BF_CHECK_LAUNCH();
   }
   // the query-side split rows finish (dq, row stats) before the key-major pass gathers their stats
   if (idx->q_heavy > 0) {
     BF_LAUNCH("attn_bwd_q_reduce_kernel", attn_bwd_q_reduce_kernel<T>, dim3(unsigned(idx->q_heavy)), dim3(kBlock),
-              combine_lds_bytes(sh), st, Q, K, Vv, bias, factor, Z, dO, static_cast<T*>(dq), dbias, rstat, qit, sh,
+              combine_lds_bytes(sh), st, Q, K, Vv, ex, Z, dO, static_cast<T*>(dq), dbias, rstat, qit, sh,
               token_rec, tok_first, idx->plan_counts);
     BF_CHECK_LAUNCH();
   }
@@ -1166,18 +1311,20 @@ int bwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
   if (kv_blocks > 0) {
     const size_t lds = idx->k_items > 0 ? combine_lds_bytes(sh) : 0;
     const bool stream_rows = size_t(idx->n_q) * size_t(sh.D) * sizeof(T) * 2 > kStreamBytes;
-    const bool extra = bias != nullptr || factor != nullptr || dbias != nullptr;
+    const int mode = edge_mode(ex, dbias != nullptr);
 #define BF_LAUNCH_KV1(NT, PRE, EX)                                                                                 \
   BF_LAUNCH("attn_bwd_kv_kernel", (attn_bwd_kv_kernel<T, NT, PRE, EX>), dim3(unsigned(kv_blocks)), dim3(kBlock), lds, st, \
-            Q, K, Vv, idx->kptr, idx->kq, idx->ke, bias, factor, dbias, dO, rstat, static_cast<T*>(dk),              \
+            Q, K, Vv, idx->kptr, idx->kq, idx->ke, ex, dbias, dO, rstat, static_cast<T*>(dk),                        \
             static_cast<T*>(dv), idx->k_order, idx->k_spans, kit, idx->k_items, idx->n_kv, sh, idx->chunk,           \
             rows_per_group, token_rec, idx->q_items, int64_t(grid_for(idx->n_q, sh)), idx->plan_counts)
 #define BF_LAUNCH_KV(NT, PRE)           \
   do {                                  \
-    if (extra)                          \
-      BF_LAUNCH_KV1(NT, PRE, true);     \
+    if (mode == 2)                      \
+      BF_LAUNCH_KV1(NT, PRE, 2);        \
+    else if (mode == 1)                 \
+      BF_LAUNCH_KV1(NT, PRE, 1);        \
     else                                \
-      BF_LAUNCH_KV1(NT, PRE, false);    \
+      BF_LAUNCH_KV1(NT, PRE, 0);        \
   } while (0)
     if constexpr (sizeof(T) == 2) {
       // the group's slots prefetched (several rows per group)
@@ -1246,31 +1393,36 @@ extern "C" int bf_attn_bwd_kv_variant(const bf_attn_index* idx, int32_t dtype, i
 
 extern "C" int bf_attn_fwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
                            const void* q, const void* k, const void* v, const float* bias,
-                           const float* factor, void* out, float* Z, float* partials, void* stream) {
+                           const float* factor, const bf_attn_dropout* dropout, void* out, float* Z,
+                           float* partials, void* stream) {
   Shape sh;
   int rc = make_shape(dtype, num_heads, head_dim, sh);
   if (rc) return rc;
   if ((rc = check_index(idx, false))) return rc;
+  EdgeIn ex;
+  if ((rc = make_edge_in(bias, factor, dropout, ex))) return rc;
   BF_CHECK_ARG(q && k && v && out && Z, "attn_fwd: null tensor");
   BF_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out),
                "attn_fwd: q/k/v/out must be 16-byte aligned");
   BF_CHECK_ARG(idx->q_items == 0 || partials, "attn_fwd: partials buffer required for split rows");
   if (dtype == BF_DTYPE_F32)
-    return fwd_impl<float>(idx, sh, q, k, v, bias, factor, out, Z, partials, as_stream(stream));
-  return fwd_impl<uint16_t>(idx, sh, q, k, v, bias, factor, out, Z, partials, as_stream(stream));
+    return fwd_impl<float>(idx, sh, q, k, v, ex, out, Z, partials, as_stream(stream));
+  return fwd_impl<uint16_t>(idx, sh, q, k, v, ex, out, Z, partials, as_stream(stream));
 }
 
 extern "C" int bf_attn_bwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
                            const void* q, const void* k, const void* v, const float* bias,
-                           const float* factor, const float* Z, const void* dout,
+                           const float* factor, const bf_attn_dropout* dropout, const float* Z, const void* dout,
                            void* dq, void* dk, void* dv, float* dbias, float* rowstat, float* partials,
                            void* stream) {
   Shape sh;
   int rc = make_shape(dtype, num_heads, head_dim, sh);
   if (rc) return rc;
   if ((rc = check_index(idx, true))) return rc;
-  BF_CHECK_ARG(idx->ke || idx->nnz == 0 || (!bias && !factor && !dbias),
-               "attn_bwd: a bias, factor or dbias needs the reverse entries' CSR positions (ke)");
+  EdgeIn ex;
+  if ((rc = make_edge_in(bias, factor, dropout, ex))) return rc;
+  BF_CHECK_ARG(idx->ke || idx->nnz == 0 || (!has_extra(ex) && !dbias),
+               "attn_bwd: a bias, factor, dropout or dbias needs the reverse entries' CSR positions (ke)");
   BF_CHECK_ARG(q && k && v && Z && dout && dq && dk && dv && rowstat, "attn_bwd: null tensor");
   BF_CHECK_ARG((reinterpret_cast<uintptr_t>(rowstat) & 7u) == 0, "attn_bwd: rowstat must be 8-byte aligned");
   BF_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(dout) && aligned16(dq) && aligned16(dk) &&
@@ -1279,9 +1431,9 @@ extern "C" int bf_attn_bwd(const bf_attn_index* idx, int32_t dtype, int32_t num_
   BF_CHECK_ARG((idx->q_items == 0 && idx->k_items == 0 && !idx->token_column) || partials,
                "attn_bwd: partials buffer required for split rows and the token column");
   if (dtype == BF_DTYPE_F32)
-    return bwd_impl<float>(idx, sh, q, k, v, bias, factor, Z, dout, dq, dk, dv, dbias, rowstat, partials,
+    return bwd_impl<float>(idx, sh, q, k, v, ex, Z, dout, dq, dk, dv, dbias, rowstat, partials,
                            as_stream(stream));
-  return bwd_impl<uint16_t>(idx, sh, q, k, v, bias, factor, Z, dout, dq, dk, dv, dbias, rowstat, partials,
+  return bwd_impl<uint16_t>(idx, sh, q, k, v, ex, Z, dout, dq, dk, dv, dbias, rowstat, partials,
                             as_stream(stream));
 }
 
@@ -1325,8 +1477,8 @@ int scratch_address(void** out) {
 
 extern "C" int bf_attn_bwd_noalloc(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
                                    const void* q, const void* k, const void* v, const float* bias,
-                                   const float* factor, const float* Z, const void* dout, void* dq, void* dk,
-                                   void* dv, float* dbias, void* stream) {
+                                   const float* factor, const bf_attn_dropout* dropout, const float* Z,
+                                   const void* dout, void* dq, void* dk, void* dv, float* dbias, void* stream) {
   Shape sh;
   int rc = make_shape(dtype, num_heads, head_dim, sh);
   if (rc) return rc;
@@ -1343,6 +1495,7 @@ extern "C" int bf_attn_bwd_noalloc(const bf_attn_index* idx, int32_t dtype, int3
   float* rowstat = static_cast<float*>(base);
   float* partials = reinterpret_cast<float*>(static_cast<unsigned char*>(base) + stat_bytes);
   ProfPause no_timer;   // the timer would create events
-  return bf_attn_bwd(idx, dtype, num_heads, head_dim, q, k, v, bias, factor, Z, dout, dq, dk, dv, dbias, rowstat,
+  return bf_attn_bwd(idx, dtype, num_heads, head_dim, q, k, v, bias, factor, dropout, Z, dout, dq, dk, dv, dbias,
+                     rowstat,
                      partials, stream);
 }

@@ -896,7 +896,28 @@ def _check_edge_tensor(t, name, idx: AttentionIndex, heads: int, device):
         raise ValueError(f"{name} must be [{idx.nnz}, {heads}] (got {tuple(t.shape)})")
 
 
-def attn_forward(idx: AttentionIndex, q, k, v, bias=None, factor=None):
+@dataclass(frozen=True)
+class Dropout:
+    """The in-kernel GraphGPS attention dropout (bf_attn_dropout): entry e, head h kept iff Philox
+    word h % 4 of counter (e, offset + h // 4), key seed, maps below 1 - rate; kept V messages scaled
+    by 1 / (1 - rate)."""
+    rate: float
+    seed: int
+    offset: int = 0
+
+    def struct(self):
+        return N.AttnDropout(float(self.rate), int(self.seed) & (2 ** 64 - 1), int(self.offset) & (2 ** 64 - 1))
+
+
+def _dropout_arg(dropout: Optional[Dropout]):
+    if dropout is None or dropout.rate <= 0.0:
+        return None
+    if not 0.0 <= dropout.rate <= 1.0:
+        raise ValueError(f"dropout rate {dropout.rate} outside [0, 1]")
+    return C.byref(dropout.struct())
+
+
+def attn_forward(idx: AttentionIndex, q, k, v, bias=None, factor=None, dropout: Optional[Dropout] = None):
     """out [n_q,H,hn] (activation dtype), Z [n_q,H] float32."""
     _check_qkv(q, k, v)
     H, hn = q.shape[1], q.shape[2]
@@ -911,8 +932,8 @@ def attn_forward(idx: AttentionIndex, q, k, v, bias=None, factor=None):
     Z = torch.empty(idx.n_q, H, dtype=torch.float32, device=q.device)
     parts = torch.empty(max(int(N.load().bf_attn_partials_floats(C.byref(st), H, hn)), 1), dtype=torch.float32,
                         device=q.device)
-    N.call("bf_attn_fwd", C.byref(st), _DT[q.dtype], H, hn, _p(q), _p(k), _p(v), _p(bias), _p(factor), _p(out),
-           _p(Z), _p(parts), _stream(q.device))
+    N.call("bf_attn_fwd", C.byref(st), _DT[q.dtype], H, hn, _p(q), _p(k), _p(v), _p(bias), _p(factor),
+           _dropout_arg(dropout), _p(out), _p(Z), _p(parts), _stream(q.device))
     return out, Z
 
 
@@ -927,7 +948,8 @@ def kv_pass_variant(n_q: int, n_kv: int, dtype: torch.dtype, heads: int, head_di
     return {"rows_per_group": rpg.value, "stream_rows": bool(nt.value), "prefetch_slots": bool(pre.value)}
 
 
-def attn_backward(idx: AttentionIndex, q, k, v, out, Z, dout, bias=None, factor=None, need_dbias: bool = False):
+def attn_backward(idx: AttentionIndex, q, k, v, out, Z, dout, bias=None, factor=None, need_dbias: bool = False,
+                  dropout: Optional[Dropout] = None):
     """(dq, dk, dv, dbias-or-None) for attn_forward's outputs. ``out`` is accepted for the autograd
     surface but not read: the backward sums Delta = dO . out from the entries in float32."""
     _check_qkv(q, k, v)
@@ -938,7 +960,8 @@ def attn_backward(idx: AttentionIndex, q, k, v, out, Z, dout, bias=None, factor=
     _require(Z, "Z", torch.float32, q.device)
     _check_edge_tensor(bias, "bias", idx, H, q.device)
     _check_edge_tensor(factor, "factor", idx, H, q.device)
-    st = idx.struct(backward=True, entries=bias is not None or factor is not None or need_dbias)
+    drop = _dropout_arg(dropout)
+    st = idx.struct(backward=True, entries=bias is not None or factor is not None or need_dbias or drop is not None)
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
@@ -946,6 +969,6 @@ def attn_backward(idx: AttentionIndex, q, k, v, out, Z, dout, bias=None, factor=
     rowstat = torch.empty(idx.n_q, H, 2, dtype=torch.float32, device=q.device)
     parts = torch.empty(max(int(N.load().bf_attn_partials_floats(C.byref(st), H, hn)), 1), dtype=torch.float32,
                         device=q.device)
-    N.call("bf_attn_bwd", C.byref(st), _DT[q.dtype], H, hn, _p(q), _p(k), _p(v), _p(bias), _p(factor),
+    N.call("bf_attn_bwd", C.byref(st), _DT[q.dtype], H, hn, _p(q), _p(k), _p(v), _p(bias), _p(factor), drop,
            _p(Z), _p(dout), _p(dq), _p(dk), _p(dv), _p(dbias), _p(rowstat), _p(parts), _stream(q.device))
     return dq, dk, dv, dbias

@@ -417,6 +417,21 @@ typedef struct bf_attn_index {
                                    an index and running attention on it.            */
 } bf_attn_index;
 
+/* GraphGPS attention dropout drawn inside the kernels
+ * (models/graphgps_dist_node_level.py:166-176; rate = attention_dropout_rate,
+ * utils/parser_node_level.py:58). Entry e (its CSR position in the index) and
+ * head h are kept iff u < 1 - rate, where u = word h % 4 of Philox4x32-10 with
+ * counter (e_lo, e_hi, (offset + h/4)_lo, (offset + h/4)_hi) and key
+ * (seed_lo, seed_hi), mapped to (x >> 8) * 2^-24; a kept entry's V message
+ * (after the softmax normalisation) is scaled by 1/(1 - rate). Forward and
+ * backward given the same struct draw the same mask; no [nnz, H] mask exists.
+ * Pass NULL (or rate 0) for none.                                           */
+typedef struct bf_attn_dropout {
+  float rate;          /* drop probability in [0, 1] */
+  uint64_t seed;       /* Philox key */
+  uint64_t offset;     /* Philox counter offset */
+} bf_attn_dropout;
+
 /* float32 scratch the attention calls need for split rows (and, with
  * token_column, one record of 2*D floats per dq-pass workgroup). */
 int64_t bf_attn_partials_floats(const bf_attn_index* idx, int32_t num_heads, int32_t head_dim);
@@ -429,11 +444,12 @@ int64_t bf_attn_partials_floats(const bf_attn_index* idx, int32_t num_heads, int
  * with f = factor (GPS dropout keep*scale) or 1.
  *   q [n_q, H*hn], k, v [n_kv, H*hn] in `dtype`, rows 16-byte aligned;
  *   bias, factor: NULL or float32 [nnz, H] (per CSR position);
+ *   dropout: NULL or the in-kernel GraphGPS dropout (its factor multiplies f);
  *   out [n_q, H*hn] in `dtype`; Z float32 [n_q, H];
  *   partials: float32 [bf_attn_partials_floats].                           */
 int bf_attn_fwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
                 const void* q, const void* k, const void* v, const float* bias, const float* factor,
-                void* out, float* Z, float* partials, void* stream);
+                const bf_attn_dropout* dropout, void* out, float* Z, float* partials, void* stream);
 
 /* Backward of bf_attn_fwd (the autograd of the reference graph of ops,
  * models/graphormer_dist_node_level.py:231-263). Deterministic: dq by a
@@ -442,14 +458,16 @@ int bf_attn_fwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int3
  * (sum_e p f (dO . v_s) / D', D' = Z + 1e-6) in float32, so the forward's
  * output tensor is not read: a bfloat16 out would carry its rounding into the
  * gradients (the reference, under autocast, keeps out in float32).
- *   dbias: NULL or float32 [nnz, H] (per CSR position; needs idx->ke);
+ *   dbias: NULL or float32 [nnz, H] (per CSR position; needs idx->ke, as do
+ *   a bias, a factor and a dropout: the key-major pass finds each entry's CSR
+ *   position through it);
  *   rowstat: float32 [n_q, H, 2] scratch (per query and head
  *   {1/D', Delta/D'}, written by the query-major pass and read by the
  *   key-major pass).                                                         */
 int bf_attn_bwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
                 const void* q, const void* k, const void* v, const float* bias, const float* factor,
-                const float* Z, const void* dout, void* dq, void* dk, void* dv, float* dbias, float* rowstat,
-                float* partials, void* stream);
+                const bf_attn_dropout* dropout, const float* Z, const void* dout, void* dq, void* dk, void* dv,
+                float* dbias, float* rowstat, float* partials, void* stream);
 
 /* bf_attn_bwd for callers that cannot allocate (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
@@ -465,8 +483,8 @@ int bf_attn_bwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int3
 #define BF_ATTN_NOALLOC_SCRATCH_BYTES (64u << 20)
 int bf_attn_bwd_noalloc(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
                         const void* q, const void* k, const void* v, const float* bias, const float* factor,
-                        const float* Z, const void* dout, void* dq, void* dk, void* dv, float* dbias,
-                        void* stream);
+                        const bf_attn_dropout* dropout, const float* Z, const void* dout, void* dq, void* dk,
+                        void* dv, float* dbias, void* stream);
 
 /* How bf_attn_bwd runs its key-major (dk/dv) pass on this index, for callers
  * and tests that need to know which kernel instance a shape takes (host-only,

@@ -56,3 +56,25 @@ def walk_uniforms(q_lo: int, n_q: int, walks_per_node: int, walk_length: int, se
             if l < L:
                 out[:, l] = (r[:, j] >> np.uint32(8)).astype(np.float32) * np.float32(1.0 / 16777216.0)
     return out
+
+
+def dropout_keep(nnz: int, num_heads: int, rate: float, seed: int, offset: int = 0) -> np.ndarray:
+    """bool [nnz, H]: the GraphGPS attention-dropout keep mask the attention kernels draw. Entry e (its
+    CSR position), head h: word h % 4 of Philox(counter = (e_lo, e_hi, (offset + h // 4)_lo, _hi), key =
+    (seed_lo, seed_hi)) mapped to (x >> 8) * 2^-24; kept iff that is below 1 - rate (float32)."""
+    e = np.arange(nnz, dtype=np.uint64)
+    seed = int(seed) & 0xFFFFFFFFFFFFFFFF
+    key = (seed & 0xFFFFFFFF, seed >> 32)
+    keep_below = np.float32(1.0) - np.float32(rate)
+    out = np.zeros((nnz, num_heads), dtype=bool)
+    for blk in range((num_heads + 3) // 4):
+        b = (int(offset) + blk) & 0xFFFFFFFFFFFFFFFF
+        ctr = np.stack([e & MASK, e >> np.uint64(32), np.full_like(e, b & 0xFFFFFFFF), np.full_like(e, b >> 32)],
+                       axis=-1)
+        r = philox4x32_10(ctr, key)
+        for j in range(4):
+            h = blk * 4 + j
+            if h < num_heads:
+                u = (r[:, j] >> np.uint32(8)).astype(np.float32) * np.float32(1.0 / 16777216.0)
+                out[:, h] = u < keep_below
+    return out

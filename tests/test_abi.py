@@ -37,7 +37,15 @@ def test_argument_errors_surface_as_exceptions():
     idx = N.AttnIndex()
     with pytest.raises(NotImplementedError):     # head_dim 6 does not split into 16-byte lanes
         N.call("bf_attn_fwd", C.byref(idx), N.BF_DTYPE_F32, 2, 6, None, None, None, None, None, None, None, None,
-               None)
+               None, None)
+    # a dropout rate outside [0, 1] is rejected after the index checks and before any launch (the index
+    # here is an empty one: qptr is host memory the call never reads)
+    qptr = (C.c_int64 * 1)(0)
+    idx.chunk, idx.item, idx.qptr = 128, 768, C.cast(qptr, C.c_void_p)
+    drop = N.AttnDropout(1.5, 1, 0)
+    with pytest.raises(ValueError, match="dropout rate"):
+        N.call("bf_attn_fwd", C.byref(idx), N.BF_DTYPE_F32, 2, 8, None, None, None, None, None, C.byref(drop), None,
+               None, None, None)
 
 
 def test_python_constants_match_the_header():

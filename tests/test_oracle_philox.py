@@ -86,3 +86,32 @@ def test_uniform_range_endpoints():
     assert _u24(0) == np.float32(0.0)
     assert _u24(0xFFFFFFFF) == np.float32(1.0 - 2.0 ** -24)
     assert _u24(0xFFFFFFFF) < np.float32(1.0)
+
+
+def test_dropout_keep_layout_and_hand_values():
+    """The attention-dropout mask: entry e, head h is word h % 4 of Philox(counter (e, offset + h // 4)),
+    kept iff (x >> 8) * 2^-24 < 1 - rate. Entry 0 with seed 0, offset 0 draws the published zero vector
+    (heads 0..3): u = 0x6627E8, 0xE169C5, 0xBC57AC, 0x9B00DB over 2^24 = 0.3990, 0.8805, 0.7357, 0.6055."""
+    m = philox.dropout_keep(1, 4, 0.5, seed=0, offset=0)[0]
+    assert list(m) == [True, False, False, False]          # only 0.399 < 0.5
+    m = philox.dropout_keep(1, 4, 0.3, seed=0, offset=0)[0]
+    assert list(m) == [True, False, False, True]           # below 0.7: 0.399, 0.6055
+    # heads 4..7 take the next counter block; every element against a direct block call
+    seed, off, H = (5 << 32) | 9, 11, 8
+    m = philox.dropout_keep(40, H, 0.25, seed=seed, offset=off)
+    for e in (0, 1, 17, 39):
+        for h in range(H):
+            blk = off + h // 4
+            ctr = np.array([[e, 0, blk, 0]], dtype=np.uint32)
+            word = int(philox.philox4x32_10(ctr, (seed & 0xFFFFFFFF, seed >> 32))[0, h % 4])
+            assert m[e, h] == (np.float32((word >> 8) / 16777216.0) < np.float32(0.75)), (e, h)
+
+
+def test_dropout_keep_rate_limits_and_statistics():
+    assert philox.dropout_keep(1000, 8, 0.0, seed=3).all()
+    assert not philox.dropout_keep(1000, 8, 1.0, seed=3).any()
+    m = philox.dropout_keep(200_000, 8, 0.5, seed=12345)
+    frac = m.mean()
+    assert abs(frac - 0.5) < 0.003                         # 1.6M Bernoulli draws: sd 0.0004
+    # heads and entries are not correlated: the mask of head 0 agrees with head 1 about half the time
+    assert abs((m[:, 0] == m[:, 1]).mean() - 0.5) < 0.01
