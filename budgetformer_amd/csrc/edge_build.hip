@@ -13,13 +13,17 @@
 // MI355X design. Every RW pool entry of query q comes from q's own P walks, so
 // the pool is never materialised: one lane runs one walk (coalesced rowptr/col
 // gathers, Philox counter RNG or injected uniforms), the P lanes of a query
-// stage their P*L candidates in LDS and rank them there. The real-edge top-k
-// scans q's in-neighbour list with a 16-lane group (per-lane sorted register
-// lists, then k rounds of a group min), and the same group merges both parts
-// through LDS with a rank sort (dedup = first occurrence wins) into a
-// fixed-stride int32 table row. Keys are 31-bit, so (key << 32 | id) orders by
-// key and equal keys are the same pair: selection with multiplicity needs no
-// position tie-break.
+// stage their P*L candidates in LDS and sort them there with a bitonic
+// network. The real-edge top-k scans q's in-neighbour list with a 16-lane
+// group (per-lane sorted register lists, then rounds of a group min, in batches
+// of the list length), and the same group merges both parts through LDS with a
+// rank sort (dedup = first occurrence wins) into a fixed-stride int32 table
+// row. Keys are 31-bit: an RW candidate (key << 32 | id) orders by key, and
+// equal values are the same pair; a real candidate (key << 32 | position)
+// orders by (key, position), the reference's tie-break, and its source comes
+// back from the key (the key is a bijection of the source for a fixed query).
+// Budgets and walk shapes are bounded only by LDS: a merged row of up to 768
+// ids, up to 8191 walk candidates per query.
 #include "bf_common.h"
 
 namespace bf {
@@ -104,28 +108,34 @@ __device__ __forceinline__ bool sorted_contains(const int32_t* __restrict__ a, i
 }
 
 // One lane per walk; the P lanes of a query are adjacent. Candidates are staged
-// in LDS as (key << 32 | kv) (kNone = filtered step) and ranked by the P lanes.
-// With sub_ptr/sub_src (an in-neighbour CSR with ascending rows) a candidate kv
-// that is already a graph edge kv -> q is dropped: the probe pools' RW-minus-real
-// subtraction (utils/fullgraph_sp_support.py:1797-1812, 1536-1551).
+// in LDS as (key << 32 | kv) (kNone = filtered step), padded with kNone to M2 =
+// the power of two >= P*L, and the query's P lanes sort them ascending with a
+// bitonic network (log2(M2) (log2(M2) + 1) / 2 compare-exchange stages, one
+// barrier each): the first min(valid, K) slots are the selection, with
+// multiplicity (equal values are the same pair). The block holds qpb queries
+// (blockDim = qpb * P, sized so the staging fits LDS), so any P*L and K that
+// fit it are served. With sub_ptr/sub_src (an in-neighbour CSR with ascending
+// rows) a candidate kv that is already a graph edge kv -> q is dropped: the
+// probe pools' RW-minus-real subtraction (utils/fullgraph_sp_support.py:
+// 1797-1812, 1536-1551).
 __global__ __launch_bounds__(kThreads) void rw_select_kernel(
     const int64_t* __restrict__ rowptr, const int32_t* __restrict__ col, int64_t num_nodes, int64_t q_lo,
-    const int32_t* __restrict__ qids, int64_t n_q, int P, int L, int K, uint32_t kc, const float* __restrict__ u,
-    uint64_t seed, uint64_t offset, const int64_t* __restrict__ sub_ptr, const int32_t* __restrict__ sub_src,
-    int32_t* __restrict__ sel_kv, int32_t* __restrict__ sel_cnt) {
-  // [qpb][P*L + 1]: the odd row stride puts the rows the queries of a wave read
-  // at one time in different LDS banks (an unpadded stride of P*L*8 bytes maps
-  // them all to the same bank)
+    const int32_t* __restrict__ qids, int64_t n_q, int P, int L, int K, int M2, int qpb, uint32_t kc,
+    const float* __restrict__ u, uint64_t seed, uint64_t offset, const int64_t* __restrict__ sub_ptr,
+    const int32_t* __restrict__ sub_src, int32_t* __restrict__ sel_kv, int32_t* __restrict__ sel_cnt) {
+  // [qpb][M2 + 1]: the odd row stride puts the rows the queries of a wave read
+  // at one time in different LDS banks (a stride of M2 * 8 bytes maps them all
+  // to the same bank)
   extern __shared__ uint64_t cand[];
-  const int qpb = kThreads / P;
   const int tid = threadIdx.x;
   const int ql = tid / P;
   const int p = tid - ql * P;
   const int M = P * L;
-  uint64_t* const mine = cand + ql * (M + 1) + p * L;      // this walk's L candidates
+  uint64_t* const c = cand + ql * (M2 + 1);                // this query's slots
   const int64_t qi = int64_t(blockIdx.x) * qpb + ql;
   const bool active = ql < qpb && qi < n_q;
   if (active) {
+    uint64_t* const mine = c + p * L;                       // this walk's L candidates
     const int64_t q = row_query(qids, q_lo, qi, num_nodes);
     const int64_t w = q * P + p;
     const int64_t wl = qi * P + p;
@@ -143,32 +153,50 @@ __global__ __launch_bounds__(kThreads) void rw_select_kernel(
       mine[l] = keep ? (uint64_t(edge_key(uint32_t(nxt), uint32_t(q), kc)) << 32) | uint32_t(nxt) : kNone;
       cur = nxt;
     }
+    for (int i = M + p; i < M2; i += P) c[i] = kNone;       // the padding sorts last
   }
   __syncthreads();
-  if (!active) return;
-  const uint64_t* c = cand + ql * (M + 1);
-  for (int i = p; i < M; i += P) {
-    const uint64_t ci = c[i];
-    if (ci == kNone) continue;
-    int rank = 0;
-    for (int j = 0; j < M; ++j) {
-      const uint64_t cj = c[j];
-      rank += (cj < ci) || (cj == ci && j < i);
+  // bitonic sort of the M2 slots by the query's P lanes; every thread of the block takes part in the
+  // barriers (the stage count depends on M2 only)
+  for (int k = 2; k <= M2; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      if (active) {
+        for (int i = p; i < M2; i += P) {
+          const int l = i ^ j;
+          if (l > i) {
+            const uint64_t x = c[i], y = c[l];
+            if ((x > y) == ((i & k) == 0)) {
+              c[i] = y;
+              c[l] = x;
+            }
+          }
+        }
+      }
+      __syncthreads();
     }
-    if (rank < K) sel_kv[qi * K + rank] = int32_t(uint32_t(ci));
+  }
+  if (!active) return;
+  // the valid candidates are a prefix of the sorted slots
+  for (int r = p; r < K; r += P) {
+    const uint64_t v = r < M2 ? c[r] : kNone;
+    sel_kv[qi * K + r] = v != kNone ? int32_t(uint32_t(v)) : -1;
   }
   if (p == 0) {
-    int nv = 0;
-    for (int j = 0; j < M; ++j) nv += c[j] != kNone;
-    const int cnt = nv < K ? nv : K;
-    sel_cnt[qi] = cnt;
-    for (int r = cnt; r < K; ++r) sel_kv[qi * K + r] = -1;
+    int lo = 0, hi = K < M2 ? K : M2;       // count of valid slots in [0, min(K, M2)): binary search
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (c[mid] != kNone) lo = mid + 1; else hi = mid;
+    }
+    sel_cnt[qi] = lo;
   }
 }
 
 constexpr int kGroup = 16;                  // lanes per query in the real-edge pass
 constexpr int kQPB = kThreads / kGroup;     // queries per block
-constexpr int kMaxRow = 64;                 // k_real + k_rw
+// Merged rows are listed in LDS, kQPB rows of `cap` = k_real + k_rw ids per
+// block plus as many duplicate flags: up to 96 KB, i.e. budgets of up to 768.
+constexpr size_t kRowLdsBytes = size_t(96) << 10;
+constexpr int kMaxRowCap = int(kRowLdsBytes / (2 * sizeof(int32_t) * (kThreads / 16)));
 #ifndef BF_SCAN_UNROLL
 #define BF_SCAN_UNROLL 8
 #endif
@@ -178,20 +206,40 @@ constexpr int kScanUnroll = BF_SCAN_UNROLL;  // in-neighbour loads in flight per
 #endif
 constexpr int kScanX4Unroll = BF_SCAN_X4_UNROLL;  // 16-byte chunks in flight per thread (light rows)
 
+// ---- 32-bit key lists of the fused light/heavy kernel.
+// For a fixed query q, key(src) = (src*A + base_q) mod 2^31 with A odd is a
+// bijection of src < 2^31, so a row's candidates never tie and the KR smallest
+// keys alone name the winners: src = ((key - base_q) * A^-1) mod 2^31. A list
+// entry is then one 32-bit value, inserted without a branch.
+constexpr uint32_t kKeyMul = 1103515245u;
+constexpr uint32_t kKeyMulInv = 0xeeb9eb65u;   // kKeyMul * kKeyMulInv == 1 (mod 2^32)
+constexpr uint32_t kNoKey = 0xffffffffu;       // above every 31-bit key
+
+__device__ __forceinline__ uint32_t key_base(uint32_t q, uint32_t kc) { return q * 214013u + kc; }
+__device__ __forceinline__ uint32_t key_of(uint32_t src, uint32_t base) { return (src * kKeyMul + base) & 0x7fffffffu; }
+__device__ __forceinline__ int32_t src_of(uint32_t key, uint32_t base) {
+  return int32_t(((key - base) * kKeyMulInv) & 0x7fffffffu);
+}
+
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t x, int o) {
   const uint32_t lo = __shfl_xor(uint32_t(x), o, 64);
   const uint32_t hi = __shfl_xor(uint32_t(x >> 32), o, 64);
   return (uint64_t(hi) << 32) | lo;
 }
 
-// Folds candidates src[i], src[i+stride], ... (< end) of query q into the
-// sorted register list lk (the KMAX smallest (key << 32 | src) seen). U loads
-// are issued before any is used, so a lane keeps U gathers in flight instead
-// of one; the slots past end re-read src[end-1] (in bounds) and are skipped.
-// The list is the same whatever order the candidates arrive in.
+// Folds candidates src[i], src[i+stride], ... (< end) of query q, each as the
+// value (key << 32 | position in the row), into the sorted register list lk
+// (the KMAX smallest such values >= floor). The value orders by (key,
+// position) — the reference's tie-break — and is unique even where the row
+// repeats a source (a walk pool is a multiset); the source comes back from the
+// key (src_of). U loads are issued before any is used, so a lane keeps U
+// gathers in flight instead of one; the slots past end re-read src[end-1] (in
+// bounds) and are skipped. The list is the same whatever order the candidates
+// arrive in. A selection of more than KMAX winners runs in batches of KMAX,
+// each batch's floor one above the last value taken.
 template <int U, int KMAX>
-__device__ __forceinline__ void scan_topk(const int32_t* __restrict__ src, int64_t i, int64_t end, int stride,
-                                          uint32_t q, uint32_t kc, uint64_t (&lk)[KMAX]) {
+__device__ __forceinline__ void scan_topk(const int32_t* __restrict__ src, int64_t row_beg, int64_t i, int64_t end,
+                                          int stride, uint32_t q, uint32_t kc, uint64_t floor, uint64_t (&lk)[KMAX]) {
   for (; i < end; i += int64_t(stride) * U) {
     uint32_t s[U];
 #pragma unroll
@@ -201,8 +249,8 @@ __device__ __forceinline__ void scan_topk(const int32_t* __restrict__ src, int64
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const uint64_t c = (uint64_t(edge_key(s[u], q, kc)) << 32) | s[u];
-      if (i + int64_t(u) * stride < end && c < lk[KMAX - 1]) {
+      const uint64_t c = (uint64_t(edge_key(s[u], q, kc)) << 32) | uint32_t(i + int64_t(u) * stride - row_beg);
+      if (i + int64_t(u) * stride < end && c < lk[KMAX - 1] && c >= floor) {
 #pragma unroll
         for (int j = KMAX - 1; j > 0; --j) lk[j] = c < lk[j - 1] ? lk[j - 1] : (c < lk[j] ? c : lk[j]);
         lk[0] = c < lk[0] ? c : lk[0];
@@ -212,53 +260,63 @@ __device__ __forceinline__ void scan_topk(const int32_t* __restrict__ src, int64
 }
 
 // Top-k_real of one hub's in-neighbour list with a whole workgroup: every
-// thread keeps a sorted register list of its strided share, then k rounds of a
+// thread keeps a sorted register list of its strided share, then rounds of a
 // block-wide minimum (wave shuffles, then LDS across the 4 waves) pop the
-// winners in key order into out[0, cnt) (written by thread 0). Returns cnt,
-// the same in every thread. Every thread of the block must call it.
+// winners in key order into out[0, cnt) (written by thread 0), KMAX per batch
+// (a thread's list holds only its KMAX smallest, so after KMAX pops the block
+// rescans above the last winner). Returns cnt, the same in every thread. Every
+// thread of the block must call it.
 template <int KMAX>
 __device__ __forceinline__ int hub_topk(const int64_t* __restrict__ in_ptr, const int32_t* __restrict__ in_src,
                                         int64_t q, int k_real, uint32_t kc, uint64_t* wave_min, int* wave_win,
                                         int32_t* out) {
   uint64_t lk[KMAX];
-#pragma unroll
-  for (int j = 0; j < KMAX; ++j) lk[j] = kNone;
-  scan_topk<kScanUnroll>(in_src, in_ptr[q] + threadIdx.x, in_ptr[q + 1], kThreads, uint32_t(q), kc, lk);
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   int cnt = 0;
-  for (int r = 0; r < k_real; ++r) {
-    const uint64_t head = lk[0];
-    uint64_t m = head;
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint64_t y = shfl_xor_u64(m, o);
-      m = y < m ? y : m;
-    }
-    const uint64_t bal = __ballot(head == m);
-    if (lane == 0) {
-      wave_min[wave] = m;
-      wave_win[wave] = __ffsll((unsigned long long)bal) - 1;
-    }
-    __syncthreads();
-    uint64_t best = wave_min[0];
-    int best_wave = 0;
+  uint64_t floor = 0;
+  while (cnt < k_real) {
 #pragma unroll
-    for (int w = 1; w < kThreads / 64; ++w) {
-      if (wave_min[w] < best) {
-        best = wave_min[w];
-        best_wave = w;
+    for (int j = 0; j < KMAX; ++j) lk[j] = kNone;
+    scan_topk<kScanUnroll>(in_src, in_ptr[q], in_ptr[q] + threadIdx.x, in_ptr[q + 1], kThreads, uint32_t(q), kc,
+                           floor, lk);
+    int popped = 0;
+    uint64_t best = kNone;
+    while (popped < KMAX && cnt < k_real) {
+      const uint64_t head = lk[0];
+      uint64_t m = head;
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint64_t y = shfl_xor_u64(m, o);
+        m = y < m ? y : m;
       }
-    }
-    const int winner = best_wave * 64 + wave_win[best_wave];
-    __syncthreads();
-    if (best == kNone) break;   // the same value in every thread: uniform exit
-    if (int(threadIdx.x) == winner) {
+      const uint64_t bal = __ballot(head == m);
+      if (lane == 0) {
+        wave_min[wave] = m;
+        wave_win[wave] = __ffsll((unsigned long long)bal) - 1;
+      }
+      __syncthreads();
+      best = wave_min[0];
+      int best_wave = 0;
 #pragma unroll
-      for (int j = 0; j < KMAX - 1; ++j) lk[j] = lk[j + 1];
-      lk[KMAX - 1] = kNone;
+      for (int w = 1; w < kThreads / 64; ++w) {
+        if (wave_min[w] < best) {
+          best = wave_min[w];
+          best_wave = w;
+        }
+      }
+      const int winner = best_wave * 64 + wave_win[best_wave];
+      __syncthreads();
+      if (best == kNone) return cnt;   // the same value in every thread: uniform exit
+      if (int(threadIdx.x) == winner) {
+#pragma unroll
+        for (int j = 0; j < KMAX - 1; ++j) lk[j] = lk[j + 1];
+        lk[KMAX - 1] = kNone;
+      }
+      if (threadIdx.x == 0) out[cnt] = src_of(uint32_t(best >> 32), key_base(uint32_t(q), kc));
+      ++cnt;
+      ++popped;
     }
-    if (threadIdx.x == 0) out[r] = int32_t(uint32_t(best));
-    cnt = r + 1;
+    floor = best + 1;
   }
   return cnt;
 }
@@ -277,37 +335,45 @@ __global__ __launch_bounds__(kThreads) void real_select_hub_kernel(
 }
 
 // Top-k_real of query q's in-neighbour list by one 16-lane group: per-lane
-// sorted register lists of its strided share, then k rounds of a group
-// minimum; the winners land in row[0, n) in key order (lane 0 writes).
-// Returns n, the same in the group's lanes.
+// sorted register lists of its strided share, then rounds of a group minimum,
+// KMAX per batch (then a rescan above the last winner); the winners land in
+// row[0, n) in key order (lane 0 writes). Returns n, the same in the group's
+// lanes.
 template <int KMAX>
 __device__ __forceinline__ int group_topk(const int64_t* __restrict__ in_ptr, const int32_t* __restrict__ in_src,
                                           int64_t q, int k_real, uint32_t kc, int gl, int32_t* row) {
   uint64_t lk[KMAX];
-#pragma unroll
-  for (int j = 0; j < KMAX; ++j) lk[j] = kNone;
-  scan_topk<kScanUnroll>(in_src, in_ptr[q] + gl, in_ptr[q + 1], kGroup, uint32_t(q), kc, lk);
   const int lane = threadIdx.x & 63;
   const int gbase = lane & ~(kGroup - 1);
   int n = 0;
-  for (int r = 0; r < k_real; ++r) {
-    const uint64_t h = lk[0];
-    uint64_t m = h;
-    for (int o = 1; o < kGroup; o <<= 1) {
-      const uint64_t y = shfl_xor_u64(m, o);
-      m = y < m ? y : m;
-    }
-    if (m == kNone) break;      // uniform over the group
-    const uint64_t bal = __ballot(h == m);
-    const uint64_t mine = (bal >> gbase) & ((uint64_t(1) << kGroup) - 1);
-    const int winner = __ffsll((unsigned long long)mine) - 1;
-    if (gl == winner) {
+  uint64_t floor = 0;
+  while (n < k_real) {
 #pragma unroll
-      for (int j = 0; j < KMAX - 1; ++j) lk[j] = lk[j + 1];
-      lk[KMAX - 1] = kNone;
+    for (int j = 0; j < KMAX; ++j) lk[j] = kNone;
+    scan_topk<kScanUnroll>(in_src, in_ptr[q], in_ptr[q] + gl, in_ptr[q + 1], kGroup, uint32_t(q), kc, floor, lk);
+    int popped = 0;
+    uint64_t m = kNone;
+    while (popped < KMAX && n < k_real) {
+      const uint64_t h = lk[0];
+      m = h;
+      for (int o = 1; o < kGroup; o <<= 1) {
+        const uint64_t y = shfl_xor_u64(m, o);
+        m = y < m ? y : m;
+      }
+      if (m == kNone) return n;      // uniform over the group
+      const uint64_t bal = __ballot(h == m);
+      const uint64_t mine = (bal >> gbase) & ((uint64_t(1) << kGroup) - 1);
+      const int winner = __ffsll((unsigned long long)mine) - 1;
+      if (gl == winner) {
+#pragma unroll
+        for (int j = 0; j < KMAX - 1; ++j) lk[j] = lk[j + 1];
+        lk[KMAX - 1] = kNone;
+      }
+      if (gl == 0) row[n] = src_of(uint32_t(m >> 32), key_base(uint32_t(q), kc));
+      ++n;
+      ++popped;
     }
-    if (gl == 0) row[r] = int32_t(uint32_t(m));
-    n = r + 1;
+    floor = m + 1;
   }
   return n;
 }
@@ -316,32 +382,32 @@ __device__ __forceinline__ int group_topk(const int64_t* __restrict__ in_ptr, co
 // values ascending (first occurrence wins), without it the multiset ascending
 // (stable), or with key_order the list as it stands (the selection order, i.e.
 // ascending key). Every thread of the block calls it (it holds a barrier).
-__device__ __forceinline__ void write_row(int32_t (*lst)[kMaxRow], int32_t (*dupf)[kMaxRow], int gq, int gl,
-                                          bool active, int n_tot, int dedup, int key_order, int32_t* __restrict__ out,
-                                          int width, int32_t* __restrict__ len_out) {
+__device__ __forceinline__ void write_row(const int32_t* lst, int32_t* dupf, int gl, bool active, int n_tot, int dedup,
+                                          int key_order, int32_t* __restrict__ out, int width,
+                                          int32_t* __restrict__ len_out) {
   if (active && dedup) {
     for (int i = gl; i < n_tot; i += kGroup) {
-      const int32_t v = lst[gq][i];
+      const int32_t v = lst[i];
       int dup = 0;
-      for (int j = 0; j < i; ++j) dup |= lst[gq][j] == v;
-      dupf[gq][i] = dup;
+      for (int j = 0; j < i; ++j) dup |= lst[j] == v;
+      dupf[i] = dup;
     }
   }
   __syncthreads();
   if (!active) return;
   int len = 0;
-  for (int i = 0; i < n_tot; ++i) len += dedup ? !dupf[gq][i] : 1;
+  for (int i = 0; i < n_tot; ++i) len += dedup ? !dupf[i] : 1;
   for (int i = gl; i < n_tot; i += kGroup) {
-    const int32_t v = lst[gq][i];
+    const int32_t v = lst[i];
     int rank = 0;
     if (dedup) {
-      if (dupf[gq][i]) continue;
-      for (int j = 0; j < n_tot; ++j) rank += !dupf[gq][j] && lst[gq][j] < v;
+      if (dupf[i]) continue;
+      for (int j = 0; j < n_tot; ++j) rank += !dupf[j] && lst[j] < v;
     } else if (key_order) {
       rank = i;
     } else {
       for (int j = 0; j < n_tot; ++j) {
-        const int32_t w = lst[gq][j];
+        const int32_t w = lst[j];
         rank += (w < v) || (w == v && j < i);
       }
     }
@@ -360,10 +426,11 @@ __global__ __launch_bounds__(kThreads) void real_select_merge_kernel(
     const int32_t* __restrict__ rw_kv, const int32_t* __restrict__ rw_cnt, int k_rw, int dedup, int key_order,
     int32_t* __restrict__ table, int width, int32_t* __restrict__ row_len, const int32_t* __restrict__ hubs,
     const int32_t* __restrict__ hub_sel, const int32_t* __restrict__ hub_cnt, int64_t n_hubs,
-    int64_t hub_threshold) {
-  __shared__ int32_t lst[kQPB][kMaxRow];
-  __shared__ int32_t dupf[kQPB][kMaxRow];
+    int64_t hub_threshold, int cap) {
+  extern __shared__ int32_t row_lds[];         // [kQPB][cap] ids, then [kQPB][cap] duplicate flags
   const int gq = threadIdx.x / kGroup;
+  int32_t* const lst = row_lds + gq * cap;
+  int32_t* const dupf = row_lds + kQPB * cap + gq * cap;
   const int gl = threadIdx.x % kGroup;
   const int64_t li = int64_t(blockIdx.x) * kQPB + gq;
   const int64_t q = li < n_q ? row_query(qids, q_lo, li, num_nodes) : -1;
@@ -383,16 +450,16 @@ __global__ __launch_bounds__(kThreads) void real_select_merge_kernel(
   }
   if (hub >= 0) {
     n_r = hub_cnt[hub];
-    for (int i = gl; i < n_r; i += kGroup) lst[gq][i] = hub_sel[hub * k_real + i];
+    for (int i = gl; i < n_r; i += kGroup) lst[i] = hub_sel[hub * k_real + i];
   } else if (q >= 0 && k_real > 0) {
-    n_r = group_topk<KMAX>(in_ptr, in_src, q, k_real, kc, gl, lst[gq]);
+    n_r = group_topk<KMAX>(in_ptr, in_src, q, k_real, kc, gl, lst);
   }
   if (active && rw_kv != nullptr && k_rw > 0) {
     n_w = rw_cnt[qi];
-    for (int i = gl; i < n_w; i += kGroup) lst[gq][n_r + i] = rw_kv[qi * k_rw + i];
+    for (int i = gl; i < n_w; i += kGroup) lst[n_r + i] = rw_kv[qi * k_rw + i];
   }
   __syncthreads();
-  write_row(lst, dupf, gq, gl, active, n_r + n_w, dedup, key_order, table + (active ? qi : 0) * width, width,
+  write_row(lst, dupf, gl, active, n_r + n_w, dedup, key_order, table + (active ? qi : 0) * width, width,
             row_len + (active ? qi : 0));
 }
 
@@ -403,10 +470,11 @@ __global__ __launch_bounds__(kThreads) void real_select_merge_kernel(
 __global__ __launch_bounds__(kThreads) void assemble_rows_kernel(
     const int32_t* __restrict__ real_kv, const int32_t* __restrict__ real_cnt, int real_stride, int b_r,
     const int32_t* __restrict__ rw_kv, const int32_t* __restrict__ rw_cnt, int rw_stride, int b_w, int dedup,
-    int64_t n, int32_t* __restrict__ table, int width, int32_t* __restrict__ row_len) {
-  __shared__ int32_t lst[kQPB][kMaxRow];
-  __shared__ int32_t dupf[kQPB][kMaxRow];
+    int64_t n, int32_t* __restrict__ table, int width, int32_t* __restrict__ row_len, int cap) {
+  extern __shared__ int32_t row_lds[];         // [kQPB][cap] ids, then [kQPB][cap] duplicate flags
   const int gq = threadIdx.x / kGroup;
+  int32_t* const lst = row_lds + gq * cap;
+  int32_t* const dupf = row_lds + kQPB * cap + gq * cap;
   const int gl = threadIdx.x % kGroup;
   const int64_t qi = int64_t(blockIdx.x) * kQPB + gq;
   const bool active = qi < n;
@@ -414,27 +482,12 @@ __global__ __launch_bounds__(kThreads) void assemble_rows_kernel(
   if (active) {
     if (real_kv && b_r > 0) n_r = min(real_cnt[qi], b_r);
     if (rw_kv && b_w > 0) n_w = min(rw_cnt[qi], b_w);
-    for (int i = gl; i < n_r; i += kGroup) lst[gq][i] = real_kv[qi * real_stride + i];
-    for (int i = gl; i < n_w; i += kGroup) lst[gq][n_r + i] = rw_kv[qi * rw_stride + i];
+    for (int i = gl; i < n_r; i += kGroup) lst[i] = real_kv[qi * real_stride + i];
+    for (int i = gl; i < n_w; i += kGroup) lst[n_r + i] = rw_kv[qi * rw_stride + i];
   }
   __syncthreads();
-  write_row(lst, dupf, gq, gl, active, n_r + n_w, dedup, 0, table + (active ? qi : 0) * width, width,
+  write_row(lst, dupf, gl, active, n_r + n_w, dedup, 0, table + (active ? qi : 0) * width, width,
             row_len + (active ? qi : 0));
-}
-
-// ---- 32-bit key lists of the fused light/heavy kernel.
-// For a fixed query q, key(src) = (src*A + base_q) mod 2^31 with A odd is a
-// bijection of src < 2^31, so a row's candidates never tie and the KR smallest
-// keys alone name the winners: src = ((key - base_q) * A^-1) mod 2^31. A list
-// entry is then one 32-bit value, inserted without a branch.
-constexpr uint32_t kKeyMul = 1103515245u;
-constexpr uint32_t kKeyMulInv = 0xeeb9eb65u;   // kKeyMul * kKeyMulInv == 1 (mod 2^32)
-constexpr uint32_t kNoKey = 0xffffffffu;       // above every 31-bit key
-
-__device__ __forceinline__ uint32_t key_base(uint32_t q, uint32_t kc) { return q * 214013u + kc; }
-__device__ __forceinline__ uint32_t key_of(uint32_t src, uint32_t base) { return (src * kKeyMul + base) & 0x7fffffffu; }
-__device__ __forceinline__ int32_t src_of(uint32_t key, uint32_t base) {
-  return int32_t(((key - base) * kKeyMulInv) & 0x7fffffffu);
 }
 
 // Inserts c into the ascending list lk (the largest value drops out): a
@@ -672,15 +725,36 @@ int check_graph(const int64_t* ptr, const int32_t* idx, int64_t num_nodes, int64
   return BF_OK;
 }
 
+// LDS the RW staging may take per block: past 64 KB a block of few queries would lose more to
+// occupancy than it gains; 64 KB holds one query of P*L = 8191 candidates.
+constexpr size_t kRwLdsBytes = size_t(64) << 10;
+
+// The staging slots per query (a power of two >= P*L) and queries per block of a P, L shape; 0 when
+// one query's slots exceed the staging LDS.
+inline void rw_shape(int P, int L, int& M2, int& qpb) {
+  const int64_t M = int64_t(P) * L;
+  int64_t m2 = 1;
+  while (m2 < M) m2 <<= 1;
+  M2 = int(m2);
+  const int64_t by_lds = int64_t(kRwLdsBytes / ((m2 + 1) * sizeof(uint64_t)));
+  const int64_t by_threads = kThreads / P;
+  qpb = int(by_lds < by_threads ? by_lds : by_threads);
+}
+
 int launch_rw_select(const int64_t* rowptr, const int32_t* col, int64_t num_nodes, int64_t q_lo,
                      const int32_t* qids, int64_t n_q, int P, int L, int K, uint32_t kc, const float* u,
                      uint64_t seed, uint64_t offset, const int64_t* sub_ptr, const int32_t* sub_src,
                      int32_t* sel_kv, int32_t* sel_cnt, hipStream_t st) {
+  int M2 = 0, qpb = 0;
+  rw_shape(P, L, M2, qpb);
+  BF_CHECK_ARG(qpb >= 1, "rw_select: walks_per_node * walk_length = %lld candidates per query exceed the %zu-byte "
+               "LDS staging (at most %zu)", (long long)(int64_t(P) * L), kRwLdsBytes,
+               kRwLdsBytes / sizeof(uint64_t) - 1);
   if (n_q == 0) return BF_OK;
-  const int qpb = kThreads / P;
-  const size_t lds = size_t(qpb) * (size_t(P) * L + 1) * sizeof(uint64_t);
-  BF_LAUNCH("rw_select_kernel", rw_select_kernel, dim3(unsigned(ceil_div(n_q, qpb))), dim3(kThreads), lds, st, rowptr, col,
-            num_nodes, q_lo, qids, n_q, P, L, K, kc, u, seed, offset, sub_ptr, sub_src, sel_kv, sel_cnt);
+  const size_t lds = size_t(qpb) * (size_t(M2) + 1) * sizeof(uint64_t);
+  BF_LAUNCH("rw_select_kernel", rw_select_kernel, dim3(unsigned(ceil_div(n_q, qpb))), dim3(unsigned(qpb * P)), lds, st,
+            rowptr, col, num_nodes, q_lo, qids, n_q, P, L, K, M2, qpb, kc, u, seed, offset, sub_ptr, sub_src, sel_kv,
+            sel_cnt);
   BF_CHECK_LAUNCH();
   return BF_OK;
 }
@@ -699,6 +773,9 @@ int launch_real_merge(const int64_t* in_ptr, const int32_t* in_src, int64_t num_
                       const int32_t* rw_cnt, int k_rw, int dedup, int key_order, int32_t* table, int width,
                       int32_t* row_len, const int32_t* hubs, int64_t n_hubs, int64_t hub_threshold,
                       int32_t* hub_sel, int32_t* hub_cnt, hipStream_t st, LightSplit split = LightSplit()) {
+  BF_CHECK_ARG(k_real + (rw_kv ? k_rw : 0) <= kMaxRowCap,
+               "edge build: budget k_real + k_rw = %d exceeds the %d a merged row can hold in LDS",
+               k_real + (rw_kv ? k_rw : 0), kMaxRowCap);
   if (n_q == 0) return BF_OK;
   const bool light = split.light_max >= 0 && qids == nullptr && !key_order && k_real <= 16 &&
                      (rw_kv == nullptr || k_rw <= 16);
@@ -751,10 +828,12 @@ int launch_real_merge(const int64_t* in_ptr, const int32_t* in_src, int64_t num_
     BF_CHECK_LAUNCH();
   }
   const dim3 grid(unsigned(ceil_div(n_q, kQPB)));
+  const int cap = k_real + (rw_kv ? k_rw : 0) > 0 ? k_real + (rw_kv ? k_rw : 0) : 1;
+  const size_t row_lds = size_t(2) * kQPB * cap * sizeof(int32_t);
 #define BF_LAUNCH_MERGE(KM)                                                                                      \
-  BF_LAUNCH("real_select_merge_kernel", real_select_merge_kernel<KM>, grid, dim3(kThreads), 0, st, in_ptr, in_src, \
-            num_nodes, q_lo, qids, n_q, k_real, kc, rw_kv, rw_cnt, k_rw, dedup, key_order, table, width,          \
-            row_len, hubs, hub_sel, hub_cnt, n_hubs, hub_threshold)
+  BF_LAUNCH("real_select_merge_kernel", real_select_merge_kernel<KM>, grid, dim3(kThreads), row_lds, st, in_ptr,   \
+            in_src, num_nodes, q_lo, qids, n_q, k_real, kc, rw_kv, rw_cnt, k_rw, dedup, key_order, table, width,  \
+            row_len, hubs, hub_sel, hub_cnt, n_hubs, hub_threshold, cap)
   if (k_real <= 4)
     BF_LAUNCH_MERGE(4);
   else if (k_real <= 8)
@@ -829,9 +908,8 @@ extern "C" int bf_rw_select(const int64_t* rowptr, const int32_t* col, int64_t n
   if (rc) return rc;
   BF_CHECK_ARG(walks_per_node >= 1 && walks_per_node <= kThreads, "rw_select: walks_per_node %d outside [1,%d]",
                walks_per_node, kThreads);
-  BF_CHECK_ARG(walk_length >= 1 && walk_length <= 32, "rw_select: walk_length %d outside [1,32]", walk_length);
-  BF_CHECK_ARG(walks_per_node * walk_length <= 64, "rw_select: P*L=%d exceeds 64", walks_per_node * walk_length);
-  BF_CHECK_ARG(k_rw >= 1 && k_rw <= 32, "rw_select: k_rw %d outside [1,32]", k_rw);
+  BF_CHECK_ARG(walk_length >= 1, "rw_select: walk_length %d < 1", walk_length);
+  BF_CHECK_ARG(k_rw >= 1, "rw_select: k_rw %d < 1", k_rw);
   BF_CHECK_ARG((sel_kv && sel_cnt) || n_q == 0, "rw_select: null output");
   return launch_rw_select(rowptr, col, num_nodes, q_lo, nullptr, n_q, walks_per_node, walk_length, k_rw,
                           key_const(key_seed), u, philox_seed, philox_offset, nullptr, nullptr, sel_kv, sel_cnt,
@@ -848,9 +926,8 @@ extern "C" int bf_rw_select_rows(const int64_t* rowptr, const int32_t* col, int6
   BF_CHECK_ARG(n_q >= 0 && (qids || n_q == 0), "rw_select_rows: query id list is NULL");
   BF_CHECK_ARG(walks_per_node >= 1 && walks_per_node <= kThreads, "rw_select_rows: walks_per_node %d outside [1,%d]",
                walks_per_node, kThreads);
-  BF_CHECK_ARG(walk_length >= 1 && walk_length <= 32, "rw_select_rows: walk_length %d outside [1,32]", walk_length);
-  BF_CHECK_ARG(walks_per_node * walk_length <= 64, "rw_select_rows: P*L=%d exceeds 64", walks_per_node * walk_length);
-  BF_CHECK_ARG(k_rw >= 1 && k_rw <= 32, "rw_select_rows: k_rw %d outside [1,32]", k_rw);
+  BF_CHECK_ARG(walk_length >= 1, "rw_select_rows: walk_length %d < 1", walk_length);
+  BF_CHECK_ARG(k_rw >= 1, "rw_select_rows: k_rw %d < 1", k_rw);
   BF_CHECK_ARG((sub_ptr == nullptr) == (sub_src == nullptr), "rw_select_rows: sub_ptr and sub_src go together");
   BF_CHECK_ARG((sel_kv && sel_cnt) || n_q == 0, "rw_select_rows: null output");
   return launch_rw_select(rowptr, col, num_nodes, 0, qids, n_q, walks_per_node, walk_length, k_rw,
@@ -868,8 +945,7 @@ extern "C" int bf_real_select_merge(const int64_t* in_ptr, const int32_t* in_src
   if (rc) return rc;
   if (k_real < 0) k_real = 0;
   if (rw_kv == nullptr) k_rw = 0;
-  BF_CHECK_ARG(k_real <= 32 && k_rw >= 0 && k_rw <= 32, "real_select_merge: k_real=%d k_rw=%d must be <= 32",
-               k_real, k_rw);
+  BF_CHECK_ARG(k_rw >= 0, "real_select_merge: k_rw=%d < 0", k_rw);
   BF_CHECK_ARG(k_rw == 0 || rw_cnt != nullptr, "real_select_merge: rw_cnt is NULL");
   BF_CHECK_ARG(width >= k_real + k_rw && width >= 1, "real_select_merge: width %d < k_real + k_rw = %d", width,
                k_real + k_rw);
@@ -894,7 +970,7 @@ extern "C" int bf_real_select_rows(const int64_t* in_ptr, const int32_t* in_src,
   int rc = check_graph(in_ptr, in_src, num_nodes, 0, 0);
   if (rc) return rc;
   BF_CHECK_ARG(n_q >= 0 && (qids || n_q == 0), "real_select_rows: query id list is NULL");
-  BF_CHECK_ARG(k_real >= 1 && k_real <= 32, "real_select_rows: k_real %d outside [1,32]", k_real);
+  BF_CHECK_ARG(k_real >= 1, "real_select_rows: k_real %d < 1", k_real);
   BF_CHECK_ARG((sel_kv && sel_cnt) || n_q == 0, "real_select_rows: null output");
   BF_CHECK_ARG(n_hubs >= 0 && n_hubs < (int64_t(1) << 31), "real_select_rows: bad hub count");
   BF_CHECK_ARG(n_hubs == 0 || (hubs && hub_sel && hub_cnt && hub_threshold >= 0),
@@ -916,14 +992,17 @@ extern "C" int bf_assemble_rows(const int32_t* real_kv, const int32_t* real_cnt,
                b_real, real_stride);
   BF_CHECK_ARG(b_rw <= rw_stride || rw_kv == nullptr, "assemble_rows: b_rw %d exceeds the RW stride %d", b_rw,
                rw_stride);
-  BF_CHECK_ARG(b_real + b_rw <= kMaxRow, "assemble_rows: b_real + b_rw = %d exceeds %d", b_real + b_rw, kMaxRow);
+  BF_CHECK_ARG(b_real + b_rw <= kMaxRowCap, "assemble_rows: b_real + b_rw = %d exceeds the %d a row can hold in LDS",
+               b_real + b_rw, kMaxRowCap);
   BF_CHECK_ARG(width >= b_real + b_rw && width >= 1, "assemble_rows: width %d < %d", width, b_real + b_rw);
   BF_CHECK_ARG((b_real == 0 || real_cnt) && (b_rw == 0 || rw_cnt), "assemble_rows: counts missing");
   BF_CHECK_ARG((table && row_len) || n_rows == 0, "assemble_rows: null output");
   if (n_rows == 0) return BF_OK;
-  BF_LAUNCH("assemble_rows_kernel", assemble_rows_kernel, dim3(unsigned(ceil_div(n_rows, kQPB))), dim3(kThreads), 0,
-            as_stream(stream), b_real ? real_kv : nullptr, real_cnt, real_stride, b_real, b_rw ? rw_kv : nullptr,
-            rw_cnt, rw_stride, b_rw, dedup ? 1 : 0, n_rows, table, width, row_len);
+  const int cap = b_real + b_rw > 0 ? b_real + b_rw : 1;
+  BF_LAUNCH("assemble_rows_kernel", assemble_rows_kernel, dim3(unsigned(ceil_div(n_rows, kQPB))), dim3(kThreads),
+            size_t(2) * kQPB * cap * sizeof(int32_t), as_stream(stream), b_real ? real_kv : nullptr, real_cnt,
+            real_stride, b_real, b_rw ? rw_kv : nullptr, rw_cnt, rw_stride, b_rw, dedup ? 1 : 0, n_rows, table, width,
+            row_len, cap);
   BF_CHECK_LAUNCH();
   return BF_OK;
 }

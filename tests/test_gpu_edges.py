@@ -88,6 +88,28 @@ def test_edge_table_bit_exact(hip_device, b_r, b_w, P, L):
     assert np.array_equal(tab.table.cpu().numpy(), ref_t)
 
 
+@pytest.mark.parametrize("b_r,b_w,P,L", [(48, 48, 4, 20), (40, 0, 2, 4), (0, 40, 8, 10), (33, 64, 16, 6)])
+def test_edge_table_past_the_former_caps(hip_device, b_r, b_w, P, L):
+    """Budgets above 32 per part and walk shapes above 64 candidates per query (B = 96 with P*L = 80,
+    P*L = 96 with 16 walks): the real top-k in batches (including rows past the hub threshold), the RW
+    selection sorted in LDS, merged rows of up to 97 ids; bit-exact against the oracle."""
+    from budgetformer_amd import hip_ops
+    from budgetformer_amd.edges import build_attention_edges
+    n = 3000
+    rowptr, col = _graph(n, 240000, seed=b_r + b_w + P)
+    deg = np.diff(rowptr)
+    assert (deg > hip_ops.HUB_THRESHOLD).any() and (deg > 64).sum() > 20    # hub and batched rows occur
+    g = _dev_graph(rowptr, col, n, hip_device)
+    u = np.random.default_rng(P * L).random((n * P, L), dtype=np.float32)
+    tab = build_attention_edges(g, real_edges_per_query=b_r, rw_edges_per_query=b_w, walk_length=L,
+                                walks_per_node=P, edge_seed=42, u=torch.from_numpy(u).to(hip_device))
+    ref_t, ref_len = et.build_edge_table(rowptr, col, n, b_r, b_w, L, P, 42, u)
+    assert tab.width == b_r + b_w
+    assert np.array_equal(tab.row_len.cpu().numpy(), ref_len)
+    assert np.array_equal(tab.table.cpu().numpy(), ref_t)
+    assert ref_len.max() > 32
+
+
 def test_edge_table_shard_matches_full(hip_device):
     from budgetformer_amd.edges import build_attention_edges
     n, P, L = 3000, 2, 4

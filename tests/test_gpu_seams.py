@@ -54,6 +54,22 @@ def test_sample_edges_per_query_matches_oracle_multiset(hip_device):
         assert sorted(map(tuple, got.cpu().numpy().T.tolist())) == sorted(map(tuple, ref.T.tolist()))
 
 
+@pytest.mark.parametrize("k", [33, 40, 100])
+def test_sample_edges_per_query_beyond_one_batch_keeps_multiplicity(hip_device, k):
+    """K above the 32-entry register lists: the selection runs in batches, ordered by (key, position in the
+    row), so a pair repeated in the pool keeps its multiplicity across a batch boundary. A few queries
+    take 400-1600 candidates (a hub, several copies of the same pair each), the rest few."""
+    from budgetformer_amd.utils.fullgraph_sp_support import _sample_edges_per_query_random
+    rng = np.random.default_rng(k)
+    n = 600
+    base = np.stack([rng.integers(0, n, 20000), rng.integers(0, n, 20000)])
+    hub = np.stack([rng.integers(0, 30, 1600), np.full(1600, 7)])       # 1600 candidates over 30 sources
+    ei = np.concatenate([base, hub, hub[:, :400] * np.array([[1], [0]]) + np.array([[0], [9]])], axis=1)
+    got = _sample_edges_per_query_random(torch.from_numpy(ei).to(hip_device), k, 11)
+    ref = et.sample_edges_per_query_random(ei, k, 11)
+    assert sorted(map(tuple, got.cpu().numpy().T.tolist())) == sorted(map(tuple, ref.T.tolist()))
+
+
 def test_merge_edge_index_list_is_coalesce(hip_device):
     from budgetformer_amd.gt_sp.utils import _merge_edge_index_list
     rng = np.random.default_rng(4)
