@@ -344,6 +344,14 @@ def run(config, steps, warmup, chunk=None, item=None, with_cpu=True):
     dout = torch.randn(S, H, hn, generator=torch.Generator(device=dev).manual_seed(47), device=dev,
                        dtype=torch.float32).to(dt)
     torch.cuda.synchronize()
+    # the walk records are a layout of the CSR (16 B per edge), built once per graph and cached on it like
+    # the CSR itself: timed here, outside the per-step build
+    r0, r1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    r0.record()
+    walk_rec = g.walk_records() if cfg["b_w"] > 0 else None
+    r1.record()
+    torch.cuda.synchronize()
+    rec_ms = round(r0.elapsed_time(r1), 4) if walk_rec is not None else None
     print(f"[bench] {cfg['name']}: realized E={g.num_edges:,}; setup {time.time() - t_setup:.1f}s", flush=True)
 
     chunk = chunk or hip_ops.DEFAULT_CHUNK
@@ -486,6 +494,8 @@ def run(config, steps, warmup, chunk=None, item=None, with_cpu=True):
         },
         "builder": {
             "edge_build_ms": round(build_ms, 4),
+            "walk_records_once_ms": rec_ms,
+            "walk_records_bytes": int(walk_rec.numel() * 4) if walk_rec is not None else 0,
             "rw_pool_edges": pool_edges,
             "rw_edges_per_s": round(pool_edges / (rw_ms * 1e-3), 1) if rw_ms else None,
             "rw_walk_steps_per_s": round(n_walks * cfg["L"] / (rw_ms * 1e-3), 1) if rw_ms else None,

@@ -64,17 +64,19 @@ _SIGS = {
                               vp]),
     "bf_coalesce_workspace_size": (C.c_int, [i64, C.POINTER(sz)]),
     "bf_coalesce": (C.c_int, [P_i64, P_i64, i64, i64, P_i64, P_i64, C.POINTER(i64), vp, sz, vp]),
-    "bf_rw_select": (C.c_int, [P_i64, P_i32, i64, i64, i64, i32, i32, i32, i64, P_f32, u64, u64, P_i32, P_i32, vp]),
+    "bf_walk_records": (C.c_int, [P_i64, P_i32, i64, i64, vp, vp]),
+    "bf_rw_select": (C.c_int, [P_i64, P_i32, vp, i64, i64, i64, i32, i32, i32, i64, P_f32, u64, u64, P_i32, P_i32,
+                               vp]),
     "bf_real_select_merge": (C.c_int, [P_i64, P_i32, i64, i64, i64, i32, i64, P_i32, P_i32, i32, i32, P_i32, i32,
                                        P_i32, P_i32, i64, i64, P_i32, P_i32, P_i32, i64, i64, vp]),
-    "bf_rw_select_rows": (C.c_int, [P_i64, P_i32, i64, P_i32, i64, i32, i32, i32, i64, P_f32, u64, u64, P_i64, P_i32,
+    "bf_rw_select_rows": (C.c_int, [P_i64, P_i32, vp, i64, P_i32, i64, i32, i32, i32, i64, P_f32, u64, u64, P_i64, P_i32,
                                     P_i32, P_i32, vp]),
     "bf_real_select_rows": (C.c_int, [P_i64, P_i32, i64, P_i32, i64, i32, i64, P_i32, i64, i64, P_i32, P_i32, P_i32,
                                       P_i32, vp]),
     "bf_assemble_rows": (C.c_int, [P_i32, P_i32, i32, i32, P_i32, P_i32, i32, i32, i32, i64, P_i32, i32, P_i32, vp]),
     "bf_mark_in_neighbors": (C.c_int, [P_i64, P_i32, i64, vp, vp, vp]),
     "bf_build_edge_table_workspace_size": (C.c_int, [i64, i32, i64, i32, C.POINTER(sz)]),
-    "bf_build_edge_table": (C.c_int, [P_i64, P_i32, P_i64, P_i32, i64, i64, i64, i64, i32, i32, i32, i32, i64,
+    "bf_build_edge_table": (C.c_int, [P_i64, P_i32, vp, P_i64, P_i32, i64, i64, i64, i64, i32, i32, i32, i32, i64,
                                       P_f32, u64, u64, P_i32, i64, i64, P_i32, i64, i64, P_i32, P_i32, vp, sz, vp]),
     "bf_table_csr_ptr": (C.c_int, [P_i32, i64, i32, i64, P_i64, C.POINTER(i64), vp, sz, vp]),
     "bf_table_to_csr": (C.c_int, [P_i32, P_i32, i64, i32, i32, i64, P_i64, P_i32, vp, i32, i32, vp]),

@@ -42,6 +42,44 @@ __device__ __forceinline__ int64_t walk_step(const int64_t* __restrict__ rowptr,
   return col[beg + idx];
 }
 
+// Walk records (bf_walk_records): per CSR edge e, 16 bytes {target id, the
+// target's degree, the target's row start (low word, high word)}. A walk that
+// carries its node's (row start, degree) takes a step with one random 16-byte
+// read, the chosen edge's record, where walk_step makes two dependent ones
+// (the rowptr pair, then col). The step arithmetic is walk_step's.
+struct WalkCursor {
+  int64_t cur, beg, deg;
+};
+
+__device__ __forceinline__ WalkCursor walk_start(const int64_t* __restrict__ rowptr, int64_t q) {
+  const int64_t b = rowptr[q];
+  return WalkCursor{q, b, rowptr[q + 1] - b};
+}
+
+__device__ __forceinline__ void walk_step_rec(const int4* __restrict__ rec, WalkCursor& w, float u) {
+  if (w.deg <= 0) return;                         // dead end: stay
+  int64_t idx = int64_t(u * float(w.deg));        // as walk_step
+  if (idx > w.deg - 1) idx = w.deg - 1;
+  const int4 r = rec[w.beg + idx];
+  w.cur = r.x;
+  w.deg = r.y;
+  w.beg = int64_t((uint64_t(uint32_t(r.w)) << 32) | uint32_t(r.z));
+}
+
+__global__ __launch_bounds__(kThreads) void walk_records_kernel(const int64_t* __restrict__ rowptr,
+                                                                const int32_t* __restrict__ col, int64_t num_nodes,
+                                                                int64_t num_edges, int4* __restrict__ rec) {
+  const int64_t e = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (e >= num_edges) return;
+  const int32_t t = col[e];
+  int64_t b = 0, d = 0;                           // a target outside the graph reads as a dead end
+  if (t >= 0 && t < num_nodes) {
+    b = rowptr[t];
+    d = rowptr[t + 1] - b;
+  }
+  rec[e] = make_int4(t, int32_t(d), int32_t(uint32_t(uint64_t(b))), int32_t(uint32_t(uint64_t(b) >> 32)));
+}
+
 __global__ __launch_bounds__(kThreads) void random_walk_kernel(
     const int64_t* __restrict__ rowptr, const int32_t* __restrict__ col, int64_t q_lo, int64_t n_walks,
     int P, int L, const float* __restrict__ u, uint64_t seed, uint64_t offset, int64_t* __restrict__ walks) {
@@ -107,6 +145,137 @@ __device__ __forceinline__ bool sorted_contains(const int32_t* __restrict__ a, i
   return lo < end && a[lo] == x;
 }
 
+// The walk of lane p of query row qi (walk id q*P + p): step(l), called for
+// l = 0, 1, ... in turn, is candidate l, (key << 32 | kv) of the node reached
+// at step l, or kNone for a filtered step (a stay after step 0, a query
+// outside the graph, or with sub_ptr/sub_src a kv already joined to q by a
+// graph edge).
+struct RwWalk {
+  const int64_t* __restrict__ rowptr;
+  const int32_t* __restrict__ col;
+  const int4* __restrict__ rec;
+  const float* __restrict__ u;
+  const int64_t* __restrict__ sub_ptr;
+  const int32_t* __restrict__ sub_src;
+  int64_t q, cur, wl;
+  int L;
+  uint32_t kc;
+  WalkCursor wc;
+  WalkStream rng;
+
+  __device__ __forceinline__ RwWalk(const int64_t* rowptr_, const int32_t* col_, const int4* rec_,
+                                    int64_t num_nodes, int64_t q_lo, const int32_t* qids, int64_t qi, int P, int p,
+                                    int L_, uint32_t kc_, const float* u_, uint64_t seed, uint64_t offset,
+                                    const int64_t* sub_ptr_, const int32_t* sub_src_)
+      : rowptr(rowptr_), col(col_), rec(rec_), u(u_), sub_ptr(sub_ptr_), sub_src(sub_src_), L(L_), kc(kc_) {
+    q = row_query(qids, q_lo, qi, num_nodes);
+    cur = q;
+    wl = qi * P + p;
+    wc = WalkCursor{q, 0, 0};
+    if (rec && q >= 0) wc = walk_start(rowptr, q);
+    rng = WalkStream{seed, offset, uint64_t(q * P + p), {}};
+  }
+
+  __device__ __forceinline__ uint64_t step(int l) {
+    if (q < 0) return kNone;
+    const float uu = u ? u[wl * L + l] : rng.at(l);
+    int64_t nxt;
+    if (rec) {
+      walk_step_rec(rec, wc, uu);
+      nxt = wc.cur;
+    } else {
+      nxt = walk_step(rowptr, col, cur, uu);
+    }
+    bool keep = (l == 0) || (nxt != cur);
+    if (keep && sub_ptr) keep = !sorted_contains(sub_src, sub_ptr[q], sub_ptr[q + 1], int32_t(nxt));
+    cur = nxt;
+    return keep ? (uint64_t(edge_key(uint32_t(nxt), uint32_t(q), kc)) << 32) | uint32_t(nxt) : kNone;
+  }
+};
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t x, int o) {
+  const uint32_t lo = __shfl_xor(uint32_t(x), o, 64);
+  const uint32_t hi = __shfl_xor(uint32_t(x >> 32), o, 64);
+  return (uint64_t(hi) << 32) | lo;
+}
+
+// Orders a, b ascending (asc) or descending.
+__device__ __forceinline__ void cmp_swap(uint64_t& a, uint64_t& b, bool asc) {
+  const bool sw = (a > b) == asc;
+  const uint64_t x = sw ? b : a, y = sw ? a : b;
+  a = x;
+  b = y;
+}
+
+// rw_select for P a power of two <= 64 and L <= R (R a power of two <= 16):
+// lane p keeps its walk's candidates in registers x[0, R) (kNone past L), the
+// query's element i = p*R + r, and the query's P lanes sort the P*R elements
+// ascending with the bitonic network of the LDS kernel below: pairs closer
+// than R are compare-exchanged in a lane's registers, pairs R or more apart
+// across lanes (xor shuffles within the wave; a query's lanes are an aligned
+// group of P), with no LDS and no barrier. Blocks of 256 / P queries.
+template <int R>
+__global__ __launch_bounds__(kThreads) void rw_select_reg_kernel(
+    const int64_t* __restrict__ rowptr, const int32_t* __restrict__ col, const int4* __restrict__ rec,
+    int64_t num_nodes, int64_t q_lo, const int32_t* __restrict__ qids, int64_t n_q, int P, int L, int K,
+    uint32_t kc, const float* __restrict__ u, uint64_t seed, uint64_t offset, const int64_t* __restrict__ sub_ptr,
+    const int32_t* __restrict__ sub_src, int32_t* __restrict__ sel_kv, int32_t* __restrict__ sel_cnt) {
+  const int tid = threadIdx.x;
+  const int p = tid & (P - 1);
+  const int64_t qi = int64_t(blockIdx.x) * (kThreads / P) + tid / P;
+  if (qi >= n_q) return;                      // a query's P lanes leave together
+  uint64_t x[R];
+  {
+    RwWalk walk(rowptr, col, rec, num_nodes, q_lo, qids, qi, P, p, L, kc, u, seed, offset, sub_ptr, sub_src);
+#pragma unroll
+    for (int r = 0; r < R; ++r) x[r] = r < L ? walk.step(r) : kNone;
+  }
+  const int M2 = P * R;
+  // blocks of up to R elements: in registers
+#pragma unroll
+  for (int k = 2; k <= R; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if ((r ^ j) > r) cmp_swap(x[r], x[r ^ j], ((p * R + r) & k) == 0);
+      }
+    }
+  }
+  for (int k = 2 * R; k <= M2; k <<= 1) {
+    const bool asc = ((p * R) & k) == 0;      // the same for a lane's R elements (k > r)
+    for (int j = k >> 1; j >= R; j >>= 1) {
+      const int pm = j / R;                   // partner lane p ^ pm holds element i ^ j
+      const bool keep_min = ((p & pm) == 0) == asc;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const uint64_t y = shfl_xor_u64(x[r], pm);
+        x[r] = keep_min ? (y < x[r] ? y : x[r]) : (y > x[r] ? y : x[r]);
+      }
+    }
+#pragma unroll
+    for (int j = R >> 1; j > 0; j >>= 1) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if ((r ^ j) > r) cmp_swap(x[r], x[r ^ j], asc);
+      }
+    }
+  }
+  // the valid candidates are a prefix of the sorted elements
+  int cnt = 0;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = p * R + r;
+    if (i < K) {
+      sel_kv[qi * K + i] = x[r] != kNone ? int32_t(uint32_t(x[r])) : -1;
+      cnt += x[r] != kNone ? 1 : 0;
+    }
+  }
+  for (int i = M2 + p; i < K; i += P) sel_kv[qi * K + i] = -1;
+  for (int o = 1; o < P; o <<= 1) cnt += __shfl_xor(cnt, o, 64);
+  if (p == 0) sel_cnt[qi] = cnt;
+}
+
 // One lane per walk; the P lanes of a query are adjacent. Candidates are staged
 // in LDS as (key << 32 | kv) (kNone = filtered step), padded with kNone to M2 =
 // the power of two >= P*L, and the query's P lanes sort them ascending with a
@@ -119,7 +288,8 @@ __device__ __forceinline__ bool sorted_contains(const int32_t* __restrict__ a, i
 // probe pools' RW-minus-real subtraction (utils/fullgraph_sp_support.py:
 // 1797-1812, 1536-1551).
 __global__ __launch_bounds__(kThreads) void rw_select_kernel(
-    const int64_t* __restrict__ rowptr, const int32_t* __restrict__ col, int64_t num_nodes, int64_t q_lo,
+    const int64_t* __restrict__ rowptr, const int32_t* __restrict__ col, const int4* __restrict__ rec,
+    int64_t num_nodes, int64_t q_lo,
     const int32_t* __restrict__ qids, int64_t n_q, int P, int L, int K, int M2, int qpb, uint32_t kc,
     const float* __restrict__ u, uint64_t seed, uint64_t offset, const int64_t* __restrict__ sub_ptr,
     const int32_t* __restrict__ sub_src, int32_t* __restrict__ sel_kv, int32_t* __restrict__ sel_cnt) {
@@ -136,23 +306,8 @@ __global__ __launch_bounds__(kThreads) void rw_select_kernel(
   const bool active = ql < qpb && qi < n_q;
   if (active) {
     uint64_t* const mine = c + p * L;                       // this walk's L candidates
-    const int64_t q = row_query(qids, q_lo, qi, num_nodes);
-    const int64_t w = q * P + p;
-    const int64_t wl = qi * P + p;
-    int64_t cur = q;
-    WalkStream rng{seed, offset, uint64_t(w), {}};
-    for (int l = 0; l < L; ++l) {
-      if (q < 0) {
-        mine[l] = kNone;
-        continue;
-      }
-      const float uu = u ? u[wl * L + l] : rng.at(l);
-      const int64_t nxt = walk_step(rowptr, col, cur, uu);
-      bool keep = (l == 0) || (nxt != cur);
-      if (keep && sub_ptr) keep = !sorted_contains(sub_src, sub_ptr[q], sub_ptr[q + 1], int32_t(nxt));
-      mine[l] = keep ? (uint64_t(edge_key(uint32_t(nxt), uint32_t(q), kc)) << 32) | uint32_t(nxt) : kNone;
-      cur = nxt;
-    }
+    RwWalk walk(rowptr, col, rec, num_nodes, q_lo, qids, qi, P, p, L, kc, u, seed, offset, sub_ptr, sub_src);
+    for (int l = 0; l < L; ++l) mine[l] = walk.step(l);
     for (int i = M + p; i < M2; i += P) c[i] = kNone;       // the padding sorts last
   }
   __syncthreads();
@@ -219,12 +374,6 @@ __device__ __forceinline__ uint32_t key_base(uint32_t q, uint32_t kc) { return q
 __device__ __forceinline__ uint32_t key_of(uint32_t src, uint32_t base) { return (src * kKeyMul + base) & 0x7fffffffu; }
 __device__ __forceinline__ int32_t src_of(uint32_t key, uint32_t base) {
   return int32_t(((key - base) * kKeyMulInv) & 0x7fffffffu);
-}
-
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t x, int o) {
-  const uint32_t lo = __shfl_xor(uint32_t(x), o, 64);
-  const uint32_t hi = __shfl_xor(uint32_t(x >> 32), o, 64);
-  return (uint64_t(hi) << 32) | lo;
 }
 
 // Folds candidates src[i], src[i+stride], ... (< end) of query q, each as the
@@ -741,8 +890,8 @@ inline void rw_shape(int P, int L, int& M2, int& qpb) {
   qpb = int(by_lds < by_threads ? by_lds : by_threads);
 }
 
-int launch_rw_select(const int64_t* rowptr, const int32_t* col, int64_t num_nodes, int64_t q_lo,
-                     const int32_t* qids, int64_t n_q, int P, int L, int K, uint32_t kc, const float* u,
+int launch_rw_select(const int64_t* rowptr, const int32_t* col, const void* walk_rec, int64_t num_nodes,
+                     int64_t q_lo, const int32_t* qids, int64_t n_q, int P, int L, int K, uint32_t kc, const float* u,
                      uint64_t seed, uint64_t offset, const int64_t* sub_ptr, const int32_t* sub_src,
                      int32_t* sel_kv, int32_t* sel_cnt, hipStream_t st) {
   int M2 = 0, qpb = 0;
@@ -750,11 +899,33 @@ int launch_rw_select(const int64_t* rowptr, const int32_t* col, int64_t num_node
   BF_CHECK_ARG(qpb >= 1, "rw_select: walks_per_node * walk_length = %lld candidates per query exceed the %zu-byte "
                "LDS staging (at most %zu)", (long long)(int64_t(P) * L), kRwLdsBytes,
                kRwLdsBytes / sizeof(uint64_t) - 1);
+  BF_CHECK_ARG((reinterpret_cast<uintptr_t>(walk_rec) & 15) == 0, "rw_select: walk records must be 16-byte aligned");
   if (n_q == 0) return BF_OK;
+  const int4* rec = static_cast<const int4*>(walk_rec);
+  int R = 1;
+  while (R < L) R <<= 1;
+  if (P <= 64 && (P & (P - 1)) == 0 && R <= 16) {
+    // register sort: P lanes of R candidates each
+    const unsigned grid = unsigned(ceil_div(n_q, int64_t(kThreads / P)));
+#define BF_LAUNCH_RW_REG(RR)                                                                                          BF_LAUNCH("rw_select_kernel", rw_select_reg_kernel<RR>, dim3(grid), dim3(kThreads), 0, st, rowptr, col, rec,                 num_nodes, q_lo, qids, n_q, P, L, K, kc, u, seed, offset, sub_ptr, sub_src, sel_kv, sel_cnt)
+    if (R == 1)
+      BF_LAUNCH_RW_REG(1);
+    else if (R == 2)
+      BF_LAUNCH_RW_REG(2);
+    else if (R == 4)
+      BF_LAUNCH_RW_REG(4);
+    else if (R == 8)
+      BF_LAUNCH_RW_REG(8);
+    else
+      BF_LAUNCH_RW_REG(16);
+#undef BF_LAUNCH_RW_REG
+    BF_CHECK_LAUNCH();
+    return BF_OK;
+  }
   const size_t lds = size_t(qpb) * (size_t(M2) + 1) * sizeof(uint64_t);
   BF_LAUNCH("rw_select_kernel", rw_select_kernel, dim3(unsigned(ceil_div(n_q, qpb))), dim3(unsigned(qpb * P)), lds, st,
-            rowptr, col, num_nodes, q_lo, qids, n_q, P, L, K, M2, qpb, kc, u, seed, offset, sub_ptr, sub_src, sel_kv,
-            sel_cnt);
+            rowptr, col, rec, num_nodes, q_lo, qids, n_q, P, L, K, M2, qpb, kc, u, seed, offset, sub_ptr, sub_src,
+            sel_kv, sel_cnt);
   BF_CHECK_LAUNCH();
   return BF_OK;
 }
@@ -900,7 +1071,24 @@ extern "C" int bf_walk_uniforms(int64_t q_lo, int64_t n_q, int32_t walks_per_nod
   return BF_OK;
 }
 
-extern "C" int bf_rw_select(const int64_t* rowptr, const int32_t* col, int64_t num_nodes, int64_t q_lo,
+extern "C" int bf_walk_records(const int64_t* rowptr, const int32_t* col, int64_t num_nodes, int64_t num_edges,
+                               void* records, void* stream) {
+  int rc = check_graph(rowptr, col, num_nodes, 0, 0);
+  if (rc) return rc;
+  // a degree is at most num_edges: below 2^31 it fits the record's 32-bit field
+  BF_CHECK_ARG(num_edges >= 0 && num_edges < (int64_t(1) << 31), "walk_records: %lld edges (the records hold "
+               "32-bit degrees: at most 2^31 - 1 edges)", (long long)num_edges);
+  if (num_edges == 0) return BF_OK;
+  BF_CHECK_ARG(col && records, "walk_records: null tensor");
+  BF_CHECK_ARG((reinterpret_cast<uintptr_t>(records) & 15) == 0, "walk_records: records must be 16-byte aligned");
+  BF_LAUNCH("walk_records_kernel", walk_records_kernel, dim3(unsigned(ceil_div(num_edges, int64_t(kThreads)))),
+            dim3(kThreads), 0, as_stream(stream), rowptr, col, num_nodes, num_edges, static_cast<int4*>(records));
+  BF_CHECK_LAUNCH();
+  return BF_OK;
+}
+
+extern "C" int bf_rw_select(const int64_t* rowptr, const int32_t* col, const void* walk_rec, int64_t num_nodes,
+                            int64_t q_lo,
                             int64_t n_q, int32_t walks_per_node, int32_t walk_length, int32_t k_rw,
                             int64_t key_seed, const float* u, uint64_t philox_seed, uint64_t philox_offset,
                             int32_t* sel_kv, int32_t* sel_cnt, void* stream) {
@@ -911,12 +1099,13 @@ extern "C" int bf_rw_select(const int64_t* rowptr, const int32_t* col, int64_t n
   BF_CHECK_ARG(walk_length >= 1, "rw_select: walk_length %d < 1", walk_length);
   BF_CHECK_ARG(k_rw >= 1, "rw_select: k_rw %d < 1", k_rw);
   BF_CHECK_ARG((sel_kv && sel_cnt) || n_q == 0, "rw_select: null output");
-  return launch_rw_select(rowptr, col, num_nodes, q_lo, nullptr, n_q, walks_per_node, walk_length, k_rw,
+  return launch_rw_select(rowptr, col, walk_rec, num_nodes, q_lo, nullptr, n_q, walks_per_node, walk_length, k_rw,
                           key_const(key_seed), u, philox_seed, philox_offset, nullptr, nullptr, sel_kv, sel_cnt,
                           as_stream(stream));
 }
 
-extern "C" int bf_rw_select_rows(const int64_t* rowptr, const int32_t* col, int64_t num_nodes, const int32_t* qids,
+extern "C" int bf_rw_select_rows(const int64_t* rowptr, const int32_t* col, const void* walk_rec, int64_t num_nodes,
+                                 const int32_t* qids,
                                  int64_t n_q, int32_t walks_per_node, int32_t walk_length, int32_t k_rw,
                                  int64_t key_seed, const float* u, uint64_t philox_seed, uint64_t philox_offset,
                                  const int64_t* sub_ptr, const int32_t* sub_src, int32_t* sel_kv, int32_t* sel_cnt,
@@ -930,7 +1119,7 @@ extern "C" int bf_rw_select_rows(const int64_t* rowptr, const int32_t* col, int6
   BF_CHECK_ARG(k_rw >= 1, "rw_select_rows: k_rw %d < 1", k_rw);
   BF_CHECK_ARG((sub_ptr == nullptr) == (sub_src == nullptr), "rw_select_rows: sub_ptr and sub_src go together");
   BF_CHECK_ARG((sel_kv && sel_cnt) || n_q == 0, "rw_select_rows: null output");
-  return launch_rw_select(rowptr, col, num_nodes, 0, qids, n_q, walks_per_node, walk_length, k_rw,
+  return launch_rw_select(rowptr, col, walk_rec, num_nodes, 0, qids, n_q, walks_per_node, walk_length, k_rw,
                           key_const(key_seed), u, philox_seed, philox_offset, sub_ptr, sub_src, sel_kv, sel_cnt,
                           as_stream(stream));
 }
@@ -1016,8 +1205,8 @@ extern "C" int bf_build_edge_table_workspace_size(int64_t n_q, int32_t k_rw, int
   return BF_OK;
 }
 
-extern "C" int bf_build_edge_table(const int64_t* rowptr, const int32_t* col, const int64_t* in_ptr,
-                                   const int32_t* in_src, int64_t num_nodes, int64_t num_edges, int64_t q_lo,
+extern "C" int bf_build_edge_table(const int64_t* rowptr, const int32_t* col, const void* walk_rec,
+                                   const int64_t* in_ptr, const int32_t* in_src, int64_t num_nodes, int64_t num_edges, int64_t q_lo,
                                    int64_t n_q, int32_t walks_per_node, int32_t walk_length, int32_t k_real,
                                    int32_t k_rw, int64_t edge_seed, const float* u, uint64_t philox_seed,
                                    uint64_t philox_offset, const int32_t* hubs, int64_t n_hubs,
@@ -1044,7 +1233,7 @@ extern "C" int bf_build_edge_table(const int64_t* rowptr, const int32_t* col, co
   wp += align_up(size_t(n_hubs) * size_t(k_real > 0 ? k_real : 0) * 4);
   int32_t* hub_cnt = reinterpret_cast<int32_t*>(wp);
   if (use_rw) {
-    int rc = bf_rw_select(rowptr, col, num_nodes, q_lo, n_q, walks_per_node, walk_length, k_rw,
+    int rc = bf_rw_select(rowptr, col, walk_rec, num_nodes, q_lo, n_q, walks_per_node, walk_length, k_rw,
                           edge_seed + 37, u, philox_seed, philox_offset, sel_kv, sel_cnt, st);
     if (rc) return rc;
   }

@@ -135,6 +135,7 @@ def build_attention_edges(graph: CSRGraph, *, real_edges_per_query: int, rw_edge
     # queries above LIGHT_MAX in-neighbours take the group path; the rest one thread each (k <= 16)
     light = b_r > 0 and b_r <= 16 and b_w <= 16
     all_heavy = graph.heavy() if light else None
+    walk_rec = graph.walk_records() if b_w > 0 else None
 
     def in_range(lst, lo, cnt):
         if lst is None or lst.numel() == 0:
@@ -155,7 +156,8 @@ def build_attention_edges(graph: CSRGraph, *, real_edges_per_query: int, rw_edge
     if len(plan.shards) == 1:
         table, row_len = hip_ops.build_edge_table(
             graph.rowptr, graph.col, graph.in_ptr, graph.in_src, graph.num_edges, q_lo, n_q, P, walk_length,
-            b_r, b_w, int(edge_seed), u=u, philox_seed=seed, philox_offset=philox_offset, **split_args(q_lo, n_q))
+            b_r, b_w, int(edge_seed), u=u, philox_seed=seed, philox_offset=philox_offset, walk_rec=walk_rec,
+            **split_args(q_lo, n_q))
     else:
         table = torch.empty(n_q, b_r + b_w, dtype=torch.int32, device=graph.device)
         row_len = torch.empty(n_q, dtype=torch.int32, device=graph.device)
@@ -165,5 +167,5 @@ def build_attention_edges(graph: CSRGraph, *, real_edges_per_query: int, rw_edge
             hip_ops.build_edge_table(graph.rowptr, graph.col, graph.in_ptr, graph.in_src, graph.num_edges, lo, cnt,
                                      P, walk_length, b_r, b_w, int(edge_seed), u=u_s, philox_seed=seed,
                                      philox_offset=philox_offset, out=(table[a:a + cnt], row_len[a:a + cnt]),
-                                     **split_args(lo, cnt))
+                                     walk_rec=walk_rec, **split_args(lo, cnt))
     return EdgeTable(table, row_len, graph.num_nodes, q_lo=q_lo, global_token=global_token)

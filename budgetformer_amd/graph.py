@@ -52,6 +52,21 @@ class CSRGraph:
             cache[threshold] = plan.heavy_rows[: plan.heavy].clone()
         return cache[threshold]
 
+    def walk_records(self) -> Optional[torch.Tensor]:
+        """The walk records of (rowptr, col), int32 [E, 4] (16 bytes per edge), cached: a walk step
+        then reads one record instead of the rowptr pair and col. None when the graph has 2^31 edges or
+        more (the records hold 32-bit degrees), or when they would take more than a quarter of the
+        device's free memory; the walks then step through rowptr and col (the same walks)."""
+        if "_walk_rec" not in self.__dict__:
+            rec = None
+            e = self.num_edges
+            if 0 < e < 2 ** 31:
+                free = torch.cuda.mem_get_info(self.device)[0] if self.device.type == "cuda" else 0
+                if 16 * e <= free // 4:
+                    rec = hip_ops.walk_records(self.rowptr, self.col)
+            self.__dict__["_walk_rec"] = rec
+        return self.__dict__["_walk_rec"]
+
     @classmethod
     def from_csr(cls, rowptr, col, num_nodes: int, in_ptr=None, in_src=None, device="cuda"):
         rowptr = torch.as_tensor(rowptr, dtype=torch.int64).to(device).contiguous()

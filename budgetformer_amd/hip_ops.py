@@ -133,9 +133,31 @@ def walk_uniforms(q_lo: int, n_q: int, walks_per_node: int, walk_length: int, ph
     return u
 
 
+def walk_records(rowptr, col) -> torch.Tensor:
+    """Per-edge walk records (bf_walk_records): int32 [E, 4] = (target, target degree, target row start
+    low word, high word). With them a walk step reads one 16-byte record instead of the rowptr pair and
+    col; the walks are the same. Topology only: build once per graph."""
+    dev = rowptr.device
+    _require(rowptr, "rowptr", torch.int64)
+    _require(col, "col", torch.int32, dev)
+    rec = torch.empty(col.numel(), 4, dtype=torch.int32, device=dev)
+    N.call("bf_walk_records", _p(rowptr), _p(col), rowptr.numel() - 1, col.numel(), _p(rec), _stream(dev))
+    return rec
+
+
+def _walk_rec_arg(walk_rec, col, dev):
+    if walk_rec is None:
+        return None
+    _require(walk_rec, "walk_rec", torch.int32, dev)
+    if tuple(walk_rec.shape) != (col.numel(), 4):
+        raise ValueError(f"walk_rec must be [{col.numel()}, 4] (got {tuple(walk_rec.shape)})")
+    return _p(walk_rec)
+
+
 def rw_select(rowptr, col, q_lo: int, n_q: int, walks_per_node: int, walk_length: int, k_rw: int,
-              key_seed: int, u=None, philox_seed: int = 0, philox_offset: int = 0):
-    """Per-query top-k_rw of the query's own walk pool: (sel_kv [n_q,k_rw], sel_cnt [n_q])."""
+              key_seed: int, u=None, philox_seed: int = 0, philox_offset: int = 0, walk_rec=None):
+    """Per-query top-k_rw of the query's own walk pool: (sel_kv [n_q,k_rw], sel_cnt [n_q]).
+    ``walk_rec``: ``walk_records(rowptr, col)``, or None to step through rowptr and col."""
     dev = rowptr.device
     _require(rowptr, "rowptr", torch.int64)
     _require(col, "col", torch.int32, dev)
@@ -143,9 +165,9 @@ def rw_select(rowptr, col, q_lo: int, n_q: int, walks_per_node: int, walk_length
         _require(u, "u", torch.float32, dev)
     sel = torch.empty(n_q, k_rw, dtype=torch.int32, device=dev)
     cnt = torch.empty(n_q, dtype=torch.int32, device=dev)
-    N.call("bf_rw_select", _p(rowptr), _p(col), rowptr.numel() - 1, q_lo, n_q, walks_per_node, walk_length, k_rw,
-           key_seed, _p(u), philox_seed & (2 ** 64 - 1), philox_offset & (2 ** 64 - 1), _p(sel), _p(cnt),
-           _stream(dev))
+    N.call("bf_rw_select", _p(rowptr), _p(col), _walk_rec_arg(walk_rec, col, dev), rowptr.numel() - 1, q_lo, n_q,
+           walks_per_node, walk_length, k_rw, key_seed, _p(u), philox_seed & (2 ** 64 - 1),
+           philox_offset & (2 ** 64 - 1), _p(sel), _p(cnt), _stream(dev))
     return sel, cnt
 
 
@@ -189,7 +211,8 @@ def _check_qids(qids: torch.Tensor, num_nodes: int, dev) -> None:
 
 
 def rw_select_rows(rowptr, col, qids: torch.Tensor, walks_per_node: int, walk_length: int, k_rw: int,
-                   key_seed: int, u=None, philox_seed: int = 0, philox_offset: int = 0, subtract=None):
+                   key_seed: int, u=None, philox_seed: int = 0, philox_offset: int = 0, subtract=None,
+                   walk_rec=None):
     """bf_rw_select for an explicit query list; ``subtract=(in_ptr, in_src)`` drops candidates that are
     already graph edges into the query. Returns (sel_kv [n,k_rw] key order, sel_cnt [n])."""
     dev = rowptr.device
@@ -211,9 +234,9 @@ def rw_select_rows(rowptr, col, qids: torch.Tensor, walks_per_node: int, walk_le
             raise ValueError("subtract in_ptr must have num_nodes + 1 entries")
     sel = torch.empty(n, k_rw, dtype=torch.int32, device=dev)
     cnt = torch.empty(n, dtype=torch.int32, device=dev)
-    N.call("bf_rw_select_rows", _p(rowptr), _p(col), n_nodes, _p(qids), n, walks_per_node, walk_length, k_rw,
-           key_seed, _p(u), philox_seed & (2 ** 64 - 1), philox_offset & (2 ** 64 - 1), _p(sub_ptr), _p(sub_src),
-           _p(sel), _p(cnt), _stream(dev))
+    N.call("bf_rw_select_rows", _p(rowptr), _p(col), _walk_rec_arg(walk_rec, col, dev), n_nodes, _p(qids), n,
+           walks_per_node, walk_length, k_rw, key_seed, _p(u), philox_seed & (2 ** 64 - 1),
+           philox_offset & (2 ** 64 - 1), _p(sub_ptr), _p(sub_src), _p(sel), _p(cnt), _stream(dev))
     return sel, cnt
 
 
@@ -280,11 +303,11 @@ def build_edge_table(rowptr, col, in_ptr, in_src, num_edges: int, q_lo: int, n_q
                      walk_length: int, k_real: int, k_rw: int, edge_seed: int, u=None, philox_seed: int = 0,
                      philox_offset: int = 0, out=None, hubs: Optional[torch.Tensor] = None,
                      hub_threshold: int = HUB_THRESHOLD, heavy: Optional[torch.Tensor] = None,
-                     light_max: int = -1):
+                     light_max: int = -1, walk_rec=None):
     """Fused budgeted build (bf_build_edge_table): (table [n_q, k_real+k_rw], row_len [n_q]).
 
     ``out=(table, row_len)`` writes into caller-provided (contiguous) tensors.
-    ``heavy`` / ``light_max`` as in ``real_select_merge``.
+    ``heavy`` / ``light_max`` as in ``real_select_merge``; ``walk_rec`` as in ``rw_select``.
     """
     dev = rowptr.device
     _require(rowptr, "rowptr", torch.int64)
@@ -315,8 +338,8 @@ def build_edge_table(rowptr, col, in_ptr, in_src, num_edges: int, q_lo: int, n_q
         raise ValueError("light_max >= 0 needs the heavy-query list")
     ws_bytes = _size_query("bf_build_edge_table_workspace_size", n_q, max(k_rw, 0), n_hubs, max(k_real, 0))
     ws = _workspace(ws_bytes, dev)
-    N.call("bf_build_edge_table", _p(rowptr), _p(col), _p(in_ptr), _p(in_src), rowptr.numel() - 1, num_edges,
-           q_lo, n_q, walks_per_node, walk_length, k_real, k_rw, edge_seed, _p(u), philox_seed & (2 ** 64 - 1),
+    N.call("bf_build_edge_table", _p(rowptr), _p(col), _walk_rec_arg(walk_rec, col, dev), _p(in_ptr), _p(in_src),
+           rowptr.numel() - 1, num_edges, q_lo, n_q, walks_per_node, walk_length, k_real, k_rw, edge_seed, _p(u), philox_seed & (2 ** 64 - 1),
            philox_offset & (2 ** 64 - 1), _p(hubs) if n_hubs else None, n_hubs, hub_threshold,
            _p(heavy) if n_heavy else None, n_heavy, int(light_max), _p(table), _p(row_len), _p(ws), ws.numel(),
            _stream(dev))

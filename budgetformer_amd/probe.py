@@ -159,7 +159,8 @@ def build_probe(graph: CSRGraph, dst_filter: torch.Tensor, *, max_real: int, max
         subtract = (graph.in_ptr, graph.in_src) if real_nonempty else None
         k = max(int(max_rw), 1)
         sel, cnt = hip_ops.rw_select_rows(graph.rowptr, graph.col, qids, P, L, k, int(edge_seed) + RW_SEED_OFFSET,
-                                          u=u, philox_seed=seed, philox_offset=philox_offset, subtract=subtract)
+                                          u=u, philox_seed=seed, philox_offset=philox_offset, subtract=subtract,
+                                          walk_rec=graph.walk_records())
         rw_nonempty = bool((cnt > 0).any())
         if max_rw > 0:
             rw = (sel, cnt)

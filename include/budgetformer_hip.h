@@ -97,6 +97,15 @@ int bf_hop_pool(const int64_t* walks, int64_t n_walks, int32_t walk_length, int3
 int bf_walk_uniforms(int64_t q_lo, int64_t n_q, int32_t walks_per_node, int32_t walk_length,
                      uint64_t philox_seed, uint64_t philox_offset, float* u, void* stream);
 
+/* Walk records of a CSR (no reference counterpart: a layout of the CSR the
+ * reference caches, gt_sp/utils.py:29-33, 1387-1473): records int32
+ * [num_edges, 4], 16-byte aligned; record e = {col[e], deg(col[e]),
+ * rowptr[col[e]] low word, high word}. A walk holding its node's (row start,
+ * degree) reaches the next node's with one 16-byte read. Depends on the
+ * topology only: built once per graph. num_edges < 2^31.                    */
+int bf_walk_records(const int64_t* rowptr, const int32_t* col, int64_t num_nodes, int64_t num_edges,
+                    void* records, void* stream);
+
 /* Per-query top-k of the random-walk pool, fused with the walk.
  * Replaces build_head_hop_edges (gt_sp/utils.py:1251-1278) +
  * compute_hop_buckets_random_walk's hop loop (gt_sp/utils.py:1232-1248) +
@@ -105,8 +114,11 @@ int bf_walk_uniforms(int64_t q_lo, int64_t n_q, int32_t walks_per_node, int32_t 
  * holds (walks[w,d], q) for its own walks w, d=1..L, kept iff d==1 or the walk
  * moved at step d; the k_rw smallest keys key(kv, q, seed) are kept counting
  * multiplicity. Output sel_kv int32 [n_q, k_rw] (key order, -1 padded),
- * sel_cnt int32 [n_q]. Requires P*L <= 64.                                   */
-int bf_rw_select(const int64_t* rowptr, const int32_t* col, int64_t num_nodes,
+ * sel_cnt int32 [n_q]. A query's P*L candidates are ranked in LDS (at most
+ * 8191 per query). walk_rec: NULL, or bf_walk_records' records of this
+ * rowptr/col (16-byte aligned): each step then reads one record instead of
+ * the rowptr pair and col; the walks are the same.                           */
+int bf_rw_select(const int64_t* rowptr, const int32_t* col, const void* walk_rec, int64_t num_nodes,
                  int64_t q_lo, int64_t n_q, int32_t walks_per_node, int32_t walk_length,
                  int32_t k_rw, int64_t key_seed, const float* u, uint64_t philox_seed,
                  uint64_t philox_offset, int32_t* sel_kv, int32_t* sel_cnt, void* stream);
@@ -121,8 +133,8 @@ int bf_rw_select(const int64_t* rowptr, const int32_t* col, int64_t num_nodes,
  * (utils/fullgraph_sp_support.py:1743-1821: filter by dst :1520-1533,
  * _subtract_edge_index :1536-1551) followed by the RW sampling of
  * _assemble_edges_from_pools (:1824-1879, via :1262-1309). u, when given, is
- * float32 [n_q*P, L] in row order.                                          */
-int bf_rw_select_rows(const int64_t* rowptr, const int32_t* col, int64_t num_nodes,
+ * float32 [n_q*P, L] in row order. walk_rec as in bf_rw_select.            */
+int bf_rw_select_rows(const int64_t* rowptr, const int32_t* col, const void* walk_rec, int64_t num_nodes,
                       const int32_t* qids, int64_t n_q, int32_t walks_per_node,
                       int32_t walk_length, int32_t k_rw, int64_t key_seed, const float* u,
                       uint64_t philox_seed, uint64_t philox_offset, const int64_t* sub_ptr,
@@ -199,10 +211,11 @@ int bf_mark_in_neighbors(const int64_t* in_ptr, const int32_t* in_src, int64_t n
  * 2943-3026) without the Graphormer token. width = k_real + k_rw. hubs /
  * n_hubs / hub_threshold and heavy / n_heavy / light_max as in
  * bf_real_select_merge (n_hubs may be 0; light_max < 0 disables the split).
+ * walk_rec: NULL or bf_walk_records' records, as in bf_rw_select.
  * Workspace: bf_build_edge_table_workspace_size.                            */
 int bf_build_edge_table_workspace_size(int64_t n_q, int32_t k_rw, int64_t n_hubs, int32_t k_real,
                                        size_t* bytes);
-int bf_build_edge_table(const int64_t* rowptr, const int32_t* col,
+int bf_build_edge_table(const int64_t* rowptr, const int32_t* col, const void* walk_rec,
                         const int64_t* in_ptr, const int32_t* in_src, int64_t num_nodes,
                         int64_t num_edges, int64_t q_lo, int64_t n_q,
                         int32_t walks_per_node, int32_t walk_length,

@@ -33,7 +33,7 @@ def test_argument_errors_surface_as_exceptions():
     assert rc == N.BF_ERR_INVALID
     assert b"row pointer" in lib.bf_last_error()
     with pytest.raises(ValueError):
-        N.call("bf_rw_select", None, None, 10, 0, 5, 2, 4, 4, 0, None, 0, 0, None, None, None)
+        N.call("bf_rw_select", None, None, None, 10, 0, 5, 2, 4, 4, 0, None, 0, 0, None, None, None)
     idx = N.AttnIndex()
     with pytest.raises(NotImplementedError):     # head_dim 6 does not split into 16-byte lanes
         N.call("bf_attn_fwd", C.byref(idx), N.BF_DTYPE_F32, 2, 6, None, None, None, None, None, None, None, None,
@@ -46,6 +46,19 @@ def test_argument_errors_surface_as_exceptions():
     with pytest.raises(ValueError, match="dropout rate"):
         N.call("bf_attn_fwd", C.byref(idx), N.BF_DTYPE_F32, 2, 8, None, None, None, None, None, C.byref(drop), None,
                None, None, None)
+
+
+def test_walk_record_arguments_checked_on_the_host():
+    """bf_walk_records refuses 2^31 edges (32-bit degree field) and an unaligned record array, and the
+    walk entry points an unaligned record array, before any launch (host buffers, never read)."""
+    buf = (C.c_int64 * 4)(0, 1, 2, 3)
+    p = C.cast(buf, C.c_void_p)
+    with pytest.raises(ValueError, match="2\\^31"):
+        N.call("bf_walk_records", p, p, 2, 2 ** 31, p, None)
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        N.call("bf_walk_records", p, p, 2, 3, C.c_void_p(p.value + 4), None)
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        N.call("bf_rw_select", p, p, C.c_void_p(p.value + 8), 2, 0, 1, 2, 2, 2, 0, None, 0, 0, p, p, None)
 
 
 def test_python_constants_match_the_header():

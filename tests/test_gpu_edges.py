@@ -135,6 +135,54 @@ def test_philox_table_equals_injected_u_table(hip_device):
     assert np.array_equal(tab.table.cpu().numpy(), ref_t)
 
 
+def test_walk_records_layout(hip_device):
+    """Record e = (col[e], deg(col[e]), rowptr[col[e]] low word, high word), against numpy; a row
+    pointer shifted past 2^32 (read, never walked) checks the high word."""
+    from budgetformer_amd import hip_ops
+    n = 3000
+    rowptr, col = _graph(n, 25000, seed=21)
+    g = _dev_graph(rowptr, col, n, hip_device)
+    c = col.astype(np.int64)
+    for shift in (0, 5 << 32):
+        ptr = g.rowptr if shift == 0 else g.rowptr + shift
+        rec = hip_ops.walk_records(ptr, g.col).cpu().numpy().astype(np.int64)
+        beg = rowptr[c] + shift
+        assert np.array_equal(rec[:, 0], c)
+        assert np.array_equal(rec[:, 1], rowptr[c + 1] - rowptr[c])
+        assert np.array_equal((rec[:, 3] << 32) | (rec[:, 2] & 0xFFFFFFFF), beg)
+    assert hip_ops.walk_records(g.rowptr, g.col[:0]).shape == (0, 4)
+
+
+@pytest.mark.parametrize("P,L,k", [(2, 4, 4), (4, 8, 16), (16, 6, 40), (3, 5, 8), (2, 20, 24)])
+def test_walk_records_select_equals_plain_steps(hip_device, P, L, k):
+    """rw_select stepping through walk records equals stepping through rowptr and col (which the
+    oracle pins), on a directed graph where every 7th node has no out-edges (a walk there stays),
+    with Philox and injected uniforms, and for a query list with the probe's subtraction. P a power
+    of two with L <= 16 takes the register sort, (3, 5) and (2, 20) the LDS sort."""
+    from budgetformer_amd import hip_ops
+    from budgetformer_amd.graph import CSRGraph
+    n = 4000
+    rowptr, col = _graph(n, 40000, seed=P + L)
+    src = np.repeat(np.arange(n), np.diff(rowptr))
+    keep = src % 7 != 0
+    out_ptr = np.concatenate([[0], np.cumsum(np.bincount(src[keep], minlength=n))]).astype(np.int64)
+    g = CSRGraph.from_csr(out_ptr, col[keep], n, in_ptr=rowptr, in_src=col, device=hip_device)
+    rec = hip_ops.walk_records(g.rowptr, g.col)
+    gen = torch.Generator(device=hip_device).manual_seed(P * L)
+    u = torch.rand((n * P, L), generator=gen, device=hip_device)
+    for uu in (None, u):
+        a = hip_ops.rw_select(g.rowptr, g.col, 0, n, P, L, k, 79, u=uu, philox_seed=7, philox_offset=3)
+        b = hip_ops.rw_select(g.rowptr, g.col, 0, n, P, L, k, 79, u=uu, philox_seed=7, philox_offset=3,
+                              walk_rec=rec)
+        assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+        assert int(a[1].sum()) > 0
+    qids = torch.arange(1, n, 3, dtype=torch.int32, device=hip_device)
+    a = hip_ops.rw_select_rows(g.rowptr, g.col, qids, P, L, k, 79, philox_seed=9, subtract=(g.in_ptr, g.in_src))
+    b = hip_ops.rw_select_rows(g.rowptr, g.col, qids, P, L, k, 79, philox_seed=9, subtract=(g.in_ptr, g.in_src),
+                               walk_rec=rec)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
 def test_graphormer_coo_matches_reference_order(hip_device):
     """EdgeTable.to_edge_index reproduces _build_merged_edges + fix_edge_index exactly (order included)."""
     from budgetformer_amd.edges import build_attention_edges
