@@ -149,6 +149,30 @@ class HipError(RuntimeError):
     """A HIP runtime call or kernel launch inside the library failed."""
 
 
+_OPS_LIB = os.path.join(_PKG, "_lib", "libbf_torch_ops.so")
+_ops = None
+
+
+def ops_path() -> str:
+    return _OPS_LIB
+
+
+def load_ops():
+    """The TORCH_LIBRARY(bf, ...) operators (csrc/torch_ops.cpp), loaded once: returns torch.ops.bf.
+    Raises if the extension was not built (no CPU fallback exists)."""
+    global _ops
+    if _ops is not None:
+        return _ops
+    import torch
+    load()                      # the operators call into the HIP library: load it (and its checks) first
+    if not os.path.exists(_OPS_LIB):
+        raise RuntimeError(f"budgetformer_amd: torch operator library not found at {_OPS_LIB}; build it with "
+                           f"`python -m budgetformer_amd.build`")
+    torch.ops.load_library(_OPS_LIB)
+    _ops = torch.ops.bf
+    return _ops
+
+
 def check(rc: int, what: str) -> None:
     if rc == BF_OK:
         return

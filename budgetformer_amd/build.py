@@ -35,8 +35,15 @@ HIPCC_FLAGS = [
 HIPCC_FLAGS += os.environ.get("BF_HIPCC_EXTRA", "").split()
 
 
+OPS_NAME = "libbf_torch_ops.so"
+
+
 def lib_path() -> str:
     return os.path.join(OUT_DIR, LIB_NAME)
+
+
+def ops_path() -> str:
+    return os.path.join(OUT_DIR, OPS_NAME)
 
 
 def _hipcc() -> str:
@@ -78,7 +85,36 @@ def build(verbose: bool = True) -> str:
     os.replace(tmp, lib_path())
     if verbose:
         print(f"[budgetformer_amd] built {lib_path()}")
+    build_torch_ops(verbose)
     return lib_path()
+
+
+def build_torch_ops(verbose: bool = True) -> str:
+    """The TORCH_LIBRARY(bf, ...) operators (csrc/torch_ops.cpp): host C++ against PyTorch's headers,
+    linked to the HIP library beside it (rpath $ORIGIN); loaded with torch.ops.load_library."""
+    import torch
+    from torch.utils import cpp_extension
+
+    src = os.path.join(CSRC, "torch_ops.cpp")
+    abi = int(bool(torch._C._GLIBCXX_USE_CXX11_ABI))
+    incs = [f"-I{p}" for p in cpp_extension.include_paths()] + ["-I/opt/rocm/include", f"-I{os.path.join(ROOT, 'include')}"]
+    libdir = cpp_extension.library_paths()[0]
+    tmp = ops_path() + ".tmp"
+    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           # the platform macro HIP's runtime headers (included by PyTorch's c10/hip) require
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", *incs, src, "-o", tmp,
+           f"-L{libdir}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip",
+           f"-L{OUT_DIR}", "-lbudgetformer_hip", "-L/opt/rocm/lib", "-lamdhip64",
+           "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{libdir}"]
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"torch_ops build failed:\n{res.stdout}")
+    if res.stdout.strip():
+        print(res.stdout, file=sys.stderr)
+    os.replace(tmp, ops_path())
+    if verbose:
+        print(f"[budgetformer_amd] built {ops_path()}")
+    return ops_path()
 
 
 if __name__ == "__main__":

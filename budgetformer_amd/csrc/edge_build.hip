@@ -907,7 +907,9 @@ int launch_rw_select(const int64_t* rowptr, const int32_t* col, const void* walk
   if (P <= 64 && (P & (P - 1)) == 0 && R <= 16) {
     // register sort: P lanes of R candidates each
     const unsigned grid = unsigned(ceil_div(n_q, int64_t(kThreads / P)));
-#define BF_LAUNCH_RW_REG(RR)                                                                                          BF_LAUNCH("rw_select_kernel", rw_select_reg_kernel<RR>, dim3(grid), dim3(kThreads), 0, st, rowptr, col, rec,                 num_nodes, q_lo, qids, n_q, P, L, K, kc, u, seed, offset, sub_ptr, sub_src, sel_kv, sel_cnt)
+#define BF_LAUNCH_RW_REG(RR)                                                                                        \
+  BF_LAUNCH("rw_select_kernel", rw_select_reg_kernel<RR>, dim3(grid), dim3(kThreads), 0, st, rowptr, col, rec,     \
+            num_nodes, q_lo, qids, n_q, P, L, K, kc, u, seed, offset, sub_ptr, sub_src, sel_kv, sel_cnt)
     if (R == 1)
       BF_LAUNCH_RW_REG(1);
     else if (R == 2)

@@ -67,10 +67,8 @@ def random_walk(rowptr, col, q_lo: int, n_q: int, walks_per_node: int, walk_leng
         _require(u, "u", torch.float32, dev)
         if tuple(u.shape) != (n_q * walks_per_node, walk_length):
             raise ValueError(f"u must be [{n_q * walks_per_node}, {walk_length}], got {tuple(u.shape)}")
-    walks = torch.empty(n_q * walks_per_node, walk_length + 1, dtype=torch.int64, device=dev)
-    N.call("bf_random_walk", _p(rowptr), _p(col), rowptr.numel() - 1, q_lo, n_q, walks_per_node, walk_length,
-           _p(u), philox_seed & (2 ** 64 - 1), philox_offset & (2 ** 64 - 1), _p(walks), _stream(dev))
-    return walks
+    return N.load_ops().rw_walk(rowptr, col, q_lo, n_q, walks_per_node, walk_length, _i64(philox_seed),
+                                _i64(philox_offset), u)
 
 
 def random_walk_starts(rowptr, col, starts: torch.Tensor, walk_length: int, u: Optional[torch.Tensor] = None,
@@ -319,15 +317,6 @@ def build_edge_table(rowptr, col, in_ptr, in_src, num_edges: int, q_lo: int, n_q
         if tuple(u.shape) != (n_q * walks_per_node, walk_length):
             raise ValueError(f"u must be [{n_q * walks_per_node}, {walk_length}], got {tuple(u.shape)}")
     width = max(k_real, 0) + max(k_rw, 0)
-    if out is None:
-        table = torch.empty(n_q, width, dtype=torch.int32, device=dev)
-        row_len = torch.empty(n_q, dtype=torch.int32, device=dev)
-    else:
-        table, row_len = out
-        _require(table, "table", torch.int32, dev)
-        _require(row_len, "row_len", torch.int32, dev)
-        if tuple(table.shape) != (n_q, width) or tuple(row_len.shape) != (n_q,):
-            raise ValueError(f"out tensors must be [{n_q}, {width}] and [{n_q}]")
     n_hubs = 0 if hubs is None else hubs.numel()
     if n_hubs:
         _require(hubs, "hubs", torch.int32, dev)
@@ -336,11 +325,23 @@ def build_edge_table(rowptr, col, in_ptr, in_src, num_edges: int, q_lo: int, n_q
         _require(heavy, "heavy", torch.int32, dev)
     if light_max >= 0 and heavy is None:
         raise ValueError("light_max >= 0 needs the heavy-query list")
+    _walk_rec_arg(walk_rec, col, dev)
+    if out is None:
+        return N.load_ops().build_edge_table(
+            rowptr, col, walk_rec, in_ptr, in_src, q_lo, n_q, walks_per_node, walk_length, k_real, k_rw,
+            int(edge_seed), u, _i64(philox_seed), _i64(philox_offset), hubs if n_hubs else None, int(hub_threshold),
+            heavy, int(light_max))
+    # into caller-provided tensors (a shard of a larger table): the C ABI directly
+    table, row_len = out
+    _require(table, "table", torch.int32, dev)
+    _require(row_len, "row_len", torch.int32, dev)
+    if tuple(table.shape) != (n_q, width) or tuple(row_len.shape) != (n_q,):
+        raise ValueError(f"out tensors must be [{n_q}, {width}] and [{n_q}]")
     ws_bytes = _size_query("bf_build_edge_table_workspace_size", n_q, max(k_rw, 0), n_hubs, max(k_real, 0))
     ws = _workspace(ws_bytes, dev)
     N.call("bf_build_edge_table", _p(rowptr), _p(col), _walk_rec_arg(walk_rec, col, dev), _p(in_ptr), _p(in_src),
-           rowptr.numel() - 1, num_edges, q_lo, n_q, walks_per_node, walk_length, k_real, k_rw, edge_seed, _p(u), philox_seed & (2 ** 64 - 1),
-           philox_offset & (2 ** 64 - 1), _p(hubs) if n_hubs else None, n_hubs, hub_threshold,
+           rowptr.numel() - 1, num_edges, q_lo, n_q, walks_per_node, walk_length, k_real, k_rw, edge_seed, _p(u),
+           philox_seed & (2 ** 64 - 1), philox_offset & (2 ** 64 - 1), _p(hubs) if n_hubs else None, n_hubs, hub_threshold,
            _p(heavy) if n_heavy else None, n_heavy, int(light_max), _p(table), _p(row_len), _p(ws), ws.numel(),
            _stream(dev))
     return table, row_len
@@ -808,33 +809,63 @@ class AttentionIndex:
         self._structs[key] = s
         return s
 
-    def _make_struct(self, backward: bool) -> N.AttnIndex:
-        s = N.AttnIndex()
-        s.n_q, s.n_kv, s.nnz = self.n_q, self.n_kv, self.nnz
-        s.qptr, s.kv = self.qptr.data_ptr(), self.kv.data_ptr() if self.nnz else None
-        s.chunk, s.item = self.chunk, self.item
+    # bf_attn_index's pointer fields, in the order the torch operators take them (csrc/torch_ops.cpp)
+    _TENSOR_FIELDS = ("qptr", "kv", "kptr", "kq", "ke", "q_nitems", "q_item_off", "q_item_row", "q_heavy_rows",
+                      "k_nitems", "k_item_off", "k_item_row", "k_heavy_rows", "k_order", "k_spans", "plan_counts")
+    _INT_FIELDS = ("n_q", "n_kv", "nnz", "chunk", "item", "q_items", "q_heavy", "k_items", "k_heavy", "token_column")
+
+    def _fields(self, backward: bool):
+        """bf_attn_index's fields: ({pointer field: tensor or None}, {integer field: int})."""
+        t = dict.fromkeys(self._TENSOR_FIELDS)
+        n = dict.fromkeys(self._INT_FIELDS, 0)
+        n["n_q"], n["n_kv"], n["nnz"] = self.n_q, self.n_kv, self.nnz
+        t["qptr"], t["kv"] = self.qptr, self.kv if self.nnz else None
+        n["chunk"], n["item"] = self.chunk, self.item
         qp = self.qplan
         # plans with a pinned copy of their counts take them from it; the others stay pending, their
         # capacities size the grids and the kernels read the counts from the device
         resolve_plans(*[p for p in (qp, self.kplan if backward else None) if p is not None and p.ready is not None])
         # (a plan whose counts are known passes them: the device copy then holds the same values)
         on_device = qp.pending or (backward and self.kplan.pending)
-        s.q_items, s.q_heavy = (qp.item_cap, qp.heavy_cap) if qp.pending else (qp.items, qp.heavy)
-        s.plan_counts = self._counts.data_ptr() if on_device else None
-        s.q_nitems, s.q_item_off, s.q_item_row, s.q_heavy_rows = (
-            qp.nitems.data_ptr(), qp.item_off.data_ptr(), qp.item_row.data_ptr(), qp.heavy_rows.data_ptr())
+        n["q_items"], n["q_heavy"] = (qp.item_cap, qp.heavy_cap) if qp.pending else (qp.items, qp.heavy)
+        t["plan_counts"] = self._counts if on_device else None
+        t["q_nitems"], t["q_item_off"], t["q_item_row"], t["q_heavy_rows"] = (
+            qp.nitems, qp.item_off, qp.item_row, qp.heavy_rows)
         if backward:
             kp = self.kplan
-            s.kptr = self.kptr.data_ptr()
-            s.kq = self.kq.data_ptr() if self.nnz else None
-            s.ke = self.ke.data_ptr() if (self.nnz and self.ke is not None) else None
-            s.k_items, s.k_heavy = (kp.item_cap, kp.heavy_cap) if kp.pending else (kp.items, kp.heavy)
-            s.k_nitems, s.k_item_off, s.k_item_row, s.k_heavy_rows = (
-                kp.nitems.data_ptr(), kp.item_off.data_ptr(), kp.item_row.data_ptr(), kp.heavy_rows.data_ptr())
-            s.k_order = self.korder.data_ptr() if self.n_kv > 0 else None
-            s.k_spans = self.kspans.data_ptr() if (self.n_kv > 0 and self.kspans is not None) else None
-        s.token_column = int(self.token_column)
+            t["kptr"] = self.kptr
+            t["kq"] = self.kq if self.nnz else None
+            t["ke"] = self.ke if (self.nnz and self.ke is not None) else None
+            n["k_items"], n["k_heavy"] = (kp.item_cap, kp.heavy_cap) if kp.pending else (kp.items, kp.heavy)
+            t["k_nitems"], t["k_item_off"], t["k_item_row"], t["k_heavy_rows"] = (
+                kp.nitems, kp.item_off, kp.item_row, kp.heavy_rows)
+            t["k_order"] = self.korder if self.n_kv > 0 else None
+            t["k_spans"] = self.kspans if (self.n_kv > 0 and self.kspans is not None) else None
+        n["token_column"] = int(self.token_column)
+        return t, n
+
+    def _make_struct(self, backward: bool) -> N.AttnIndex:
+        t, n = self._fields(backward)
+        s = N.AttnIndex()
+        for name, tensor in t.items():
+            setattr(s, name, tensor.data_ptr() if tensor is not None else None)
+        for name, value in n.items():
+            setattr(s, name, value)
         return s
+
+    def op_args(self, backward: bool, entries: bool = False):
+        """The index as the torch operators take it: ([16 tensors or None], [10 ints]), in the order of
+        bf_attn_index's fields (``_TENSOR_FIELDS``, ``_INT_FIELDS``); cached like ``struct``."""
+        self.ensure_backward() if backward else self.ensure_forward()
+        if backward and entries:
+            self.ensure_entries()
+        key = ("op", backward, backward and self.ke is not None)
+        cached = self._structs.get(key)
+        if cached is None:
+            t, n = self._fields(backward)
+            cached = ([t[f] for f in self._TENSOR_FIELDS], [int(n[f]) for f in self._INT_FIELDS])
+            self._structs[key] = cached
+        return cached
 
     @classmethod
     def from_table(cls, table, row_len, global_token: bool = False, n_kv: Optional[int] = None,
@@ -900,25 +931,6 @@ class AttentionIndex:
 _DT = {torch.float32: N.BF_DTYPE_F32, torch.bfloat16: N.BF_DTYPE_BF16}
 
 
-def _check_qkv(q, k, v):
-    if q.dtype not in _DT:
-        raise TypeError(f"attention supports float32 and bfloat16 activations (got {q.dtype})")
-    for t, n in ((q, "q"), (k, "k"), (v, "v")):
-        _require(t, n, q.dtype, q.device)
-        if t.dim() != 3:
-            raise ValueError(f"{n} must be [rows, heads, head_dim] (got {tuple(t.shape)})")
-    if k.shape != v.shape or q.shape[1:] != k.shape[1:]:
-        raise ValueError(f"q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)} disagree")
-
-
-def _check_edge_tensor(t, name, idx: AttentionIndex, heads: int, device):
-    if t is None:
-        return
-    _require(t, name, torch.float32, device)
-    if tuple(t.shape) != (idx.nnz, heads):
-        raise ValueError(f"{name} must be [{idx.nnz}, {heads}] (got {tuple(t.shape)})")
-
-
 @dataclass(frozen=True)
 class Dropout:
     """The in-kernel GraphGPS attention dropout (bf_attn_dropout): entry e, head h kept iff Philox
@@ -940,24 +952,24 @@ def _dropout_arg(dropout: Optional[Dropout]):
     return C.byref(dropout.struct())
 
 
+def _i64(x: int) -> int:
+    """A 64-bit pattern as the signed value a torch operator's int argument carries."""
+    x = int(x) & (2 ** 64 - 1)
+    return x - 2 ** 64 if x >= 2 ** 63 else x
+
+
+def _dropout_op_args(dropout: Optional[Dropout]):
+    """(rate, seed, offset) for the torch operators; rate 0 is no dropout."""
+    if dropout is None or dropout.rate <= 0.0:
+        return 0.0, 0, 0
+    return float(dropout.rate), _i64(dropout.seed), _i64(dropout.offset)
+
+
 def attn_forward(idx: AttentionIndex, q, k, v, bias=None, factor=None, dropout: Optional[Dropout] = None):
-    """out [n_q,H,hn] (activation dtype), Z [n_q,H] float32."""
-    _check_qkv(q, k, v)
-    H, hn = q.shape[1], q.shape[2]
-    if q.shape[0] != idx.n_q or k.shape[0] != idx.n_kv:
-        raise ValueError(f"q rows {q.shape[0]} / kv rows {k.shape[0]} do not match index ({idx.n_q}, {idx.n_kv})")
-    if idx.device != q.device:
-        raise ValueError("index and activations are on different devices")
-    _check_edge_tensor(bias, "bias", idx, H, q.device)
-    _check_edge_tensor(factor, "factor", idx, H, q.device)
-    st = idx.struct(backward=False)
-    out = torch.empty_like(q)
-    Z = torch.empty(idx.n_q, H, dtype=torch.float32, device=q.device)
-    parts = torch.empty(max(int(N.load().bf_attn_partials_floats(C.byref(st), H, hn)), 1), dtype=torch.float32,
-                        device=q.device)
-    N.call("bf_attn_fwd", C.byref(st), _DT[q.dtype], H, hn, _p(q), _p(k), _p(v), _p(bias), _p(factor),
-           _dropout_arg(dropout), _p(out), _p(Z), _p(parts), _stream(q.device))
-    return out, Z
+    """out [n_q,H,hn] (activation dtype), Z [n_q,H] float32, through bf::sparse_attn_fwd (which checks
+    the shapes, dtypes and devices against the index)."""
+    t, n = idx.op_args(backward=False)
+    return N.load_ops().sparse_attn_fwd(q, k, v, t, n, bias, factor, *_dropout_op_args(dropout))
 
 
 def kv_pass_variant(n_q: int, n_kv: int, dtype: torch.dtype, heads: int, head_dim: int) -> dict:
@@ -974,24 +986,12 @@ def kv_pass_variant(n_q: int, n_kv: int, dtype: torch.dtype, heads: int, head_di
 def attn_backward(idx: AttentionIndex, q, k, v, out, Z, dout, bias=None, factor=None, need_dbias: bool = False,
                   dropout: Optional[Dropout] = None):
     """(dq, dk, dv, dbias-or-None) for attn_forward's outputs. ``out`` is accepted for the autograd
-    surface but not read: the backward sums Delta = dO . out from the entries in float32."""
-    _check_qkv(q, k, v)
-    H, hn = q.shape[1], q.shape[2]
-    _require(dout, "dout", q.dtype, q.device)
-    if tuple(dout.shape) != tuple(q.shape) or tuple(Z.shape) != (q.shape[0], H):
-        raise ValueError(f"dout {tuple(dout.shape)} / Z {tuple(Z.shape)} do not match q {tuple(q.shape)}")
-    _require(Z, "Z", torch.float32, q.device)
-    _check_edge_tensor(bias, "bias", idx, H, q.device)
-    _check_edge_tensor(factor, "factor", idx, H, q.device)
-    drop = _dropout_arg(dropout)
-    st = idx.struct(backward=True, entries=bias is not None or factor is not None or need_dbias or drop is not None)
-    dq = torch.empty_like(q)
-    dk = torch.empty_like(k)
-    dv = torch.empty_like(v)
-    dbias = torch.empty(idx.nnz, H, dtype=torch.float32, device=q.device) if need_dbias else None
-    rowstat = torch.empty(idx.n_q, H, 2, dtype=torch.float32, device=q.device)
-    parts = torch.empty(max(int(N.load().bf_attn_partials_floats(C.byref(st), H, hn)), 1), dtype=torch.float32,
-                        device=q.device)
-    N.call("bf_attn_bwd", C.byref(st), _DT[q.dtype], H, hn, _p(q), _p(k), _p(v), _p(bias), _p(factor), drop,
-           _p(Z), _p(dout), _p(dq), _p(dk), _p(dv), _p(dbias), _p(rowstat), _p(parts), _stream(q.device))
-    return dq, dk, dv, dbias
+    surface but not read: the backward sums Delta = dO . out from the entries in float32. Through
+    bf::sparse_attn_bwd, which checks the shapes, dtypes and devices."""
+    rate, seed, off = _dropout_op_args(dropout)
+    if not 0.0 <= rate <= 1.0:
+        raise ValueError(f"dropout rate {rate} outside [0, 1]")
+    t, n = idx.op_args(backward=True, entries=bias is not None or factor is not None or need_dbias or rate > 0.0)
+    dq, dk, dv, dbias = N.load_ops().sparse_attn_bwd(q, k, v, t, n, Z, dout, bias, factor, bool(need_dbias), rate,
+                                                     seed, off)
+    return dq, dk, dv, (dbias if need_dbias else None)

@@ -61,6 +61,21 @@ def test_walk_record_arguments_checked_on_the_host():
         N.call("bf_rw_select", p, p, C.c_void_p(p.value + 8), 2, 0, 1, 2, 2, 2, 0, None, 0, 0, p, p, None)
 
 
+def test_torch_operators_load_and_register():
+    """The TORCH_LIBRARY(bf, ...) extension loads beside the C library and registers the hot path's
+    operators; they have device kernels only, so CPU tensors find none (no CPU fallback)."""
+    import torch
+    ops = N.load_ops()
+    for name in ("sparse_attn_fwd", "sparse_attn_bwd", "rw_walk", "build_edge_table", "table_to_csr",
+                 "transpose_table"):
+        assert str(getattr(ops, name).default._schema).startswith(f"bf::{name}(")
+    z = torch.zeros(4, 2, 8)
+    with pytest.raises(NotImplementedError):
+        ops.sparse_attn_fwd(z, z, z, [None] * 16, [0] * 10)
+    with pytest.raises(NotImplementedError):
+        ops.rw_walk(torch.zeros(3, dtype=torch.int64), torch.zeros(2, dtype=torch.int32), 0, 2, 1, 2)
+
+
 def test_python_constants_match_the_header():
     text = open(N._HEADER).read()
     assert int(re.search(r"#define BF_MAX_ITEMS_PER_ROW (\d+)", text).group(1)) == N.BF_MAX_ITEMS_PER_ROW
