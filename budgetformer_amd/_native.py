@@ -79,6 +79,7 @@ _SIGS = {
     "bf_build_edge_table": (C.c_int, [P_i64, P_i32, vp, P_i64, P_i32, i64, i64, i64, i64, i32, i32, i32, i32, i64,
                                       P_f32, u64, u64, P_i32, i64, i64, P_i32, i64, i64, P_i32, P_i32, vp, sz, vp]),
     "bf_table_csr_ptr": (C.c_int, [P_i32, i64, i32, i64, P_i64, C.POINTER(i64), vp, sz, vp]),
+    "bf_check_table": (C.c_int, [P_i32, P_i32, i64, i32, i64, C.POINTER(i64), vp, sz, vp]),
     "bf_table_to_csr": (C.c_int, [P_i32, P_i32, i64, i32, i32, i64, P_i64, P_i32, vp, i32, i32, vp]),
     "bf_scan_workspace_size": (C.c_int, [i64, C.POINTER(sz)]),
     "bf_coo_to_csr_workspace_size": (C.c_int, [i64, i64, C.POINTER(sz)]),

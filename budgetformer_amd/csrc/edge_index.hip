@@ -44,6 +44,39 @@ __global__ void row_lengths_kernel(const int32_t* __restrict__ row_len, int64_t 
   lens[t] = (lead && t == 0) ? token_len : int64_t(row_len[t - lead]) + token;
 }
 
+// Validation of an externally supplied table (bf_check_table): bad[0] counts
+// rows whose length lies outside [0, width], bad[1] the ids of a row's first
+// min(row_len, width) slots outside [0, id_limit). One thread per table slot
+// (grid-stride), one pair of atomics per block.
+__global__ __launch_bounds__(kThreads) void check_table_kernel(const int32_t* __restrict__ table,
+                                                               const int32_t* __restrict__ row_len, int64_t n_rows,
+                                                               int width, int64_t id_limit,
+                                                               unsigned long long* __restrict__ bad) {
+  __shared__ unsigned long long blk[2];
+  if (threadIdx.x < 2) blk[threadIdx.x] = 0;
+  __syncthreads();
+  unsigned long long bad_len = 0, bad_id = 0;
+  const int64_t slots = n_rows * width;
+  const int64_t stride = int64_t(gridDim.x) * kThreads;
+  for (int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x; i < slots + n_rows; i += stride) {
+    if (i >= slots) {                           // one thread per row checks its length
+      const int32_t len = row_len[i - slots];
+      bad_len += (len < 0 || len > width) ? 1 : 0;
+      continue;
+    }
+    const int64_t r = i / width;
+    const int32_t len = row_len[r];
+    if (int64_t(i - r * width) < len) {
+      const int32_t id = table[i];
+      bad_id += (id < 0 || int64_t(id) >= id_limit) ? 1 : 0;
+    }
+  }
+  if (bad_len) atomicAdd(&blk[0], bad_len);
+  if (bad_id) atomicAdd(&blk[1], bad_id);
+  __syncthreads();
+  if (threadIdx.x < 2 && blk[threadIdx.x]) atomicAdd(&bad[threadIdx.x], blk[threadIdx.x]);
+}
+
 // Writes entry pos (slot `slot` of query row `row`): kv, and when rkey is
 // given the entry's reverse-index sort key (id << kshift | row << sbits | slot):
 // a stable radix sort over the id bits alone then leaves each kv's entries in
@@ -441,6 +474,36 @@ extern "C" int bf_table_csr_ptr(const int32_t* row_len, int64_t n_rows, int32_t 
   BF_CHECK_HIP(hipMemcpyAsync(&h, qptr + n_q, sizeof(h), hipMemcpyDeviceToHost, st));
   BF_CHECK_HIP(hipStreamSynchronize(st));
   *nnz_host = h;
+  return BF_OK;
+}
+
+extern "C" int bf_check_table(const int32_t* table, const int32_t* row_len, int64_t n_rows, int32_t width,
+                              int64_t id_limit, int64_t* bad_host, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  BF_CHECK_ARG(n_rows >= 0 && width >= 0 && id_limit >= 0, "check_table: bad sizes");
+  BF_CHECK_ARG(n_rows == 0 || (table && row_len), "check_table: null tensor");
+  BF_CHECK_ARG(workspace && workspace_bytes >= 2 * sizeof(int64_t), "check_table: workspace %zu < 16 bytes",
+               workspace_bytes);
+  hipStream_t st = as_stream(stream);
+  auto* bad = static_cast<unsigned long long*>(workspace);
+  BF_CHECK_HIP(hipMemsetAsync(bad, 0, 2 * sizeof(int64_t), st));
+  const int64_t work = n_rows * width + n_rows;
+  if (work > 0) {
+    const int64_t need = ceil_div(work, int64_t(kThreads));
+    const int64_t blocks = need < 4096 ? need : 4096;
+    BF_LAUNCH("check_table_kernel", check_table_kernel, dim3(unsigned(blocks)), dim3(kThreads), 0, st, table, row_len,
+              n_rows, width, id_limit, bad);
+    BF_CHECK_LAUNCH();
+  }
+  int64_t h[2] = {0, 0};
+  BF_CHECK_HIP(hipMemcpyAsync(h, bad, sizeof(h), hipMemcpyDeviceToHost, st));
+  BF_CHECK_HIP(hipStreamSynchronize(st));
+  if (bad_host) {
+    bad_host[0] = h[0];
+    bad_host[1] = h[1];
+  }
+  BF_CHECK_ARG(h[0] == 0, "check_table: %lld row lengths outside [0, %d]", (long long)h[0], width);
+  BF_CHECK_ARG(h[1] == 0, "check_table: %lld table ids outside [0, %lld)", (long long)h[1], (long long)id_limit);
   return BF_OK;
 }
 

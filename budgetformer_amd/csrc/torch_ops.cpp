@@ -248,9 +248,10 @@ std::tuple<at::Tensor, at::Tensor> build_edge_table(
 }
 
 // Query-major table -> attention CSR (bf_table_csr_ptr + bf_table_to_csr): (qptr int64 [n_q + 1], kv int32 [nnz]).
-// token_row as in the C ABI (< 0: no token row); reads nnz to the host once.
+// token_row as in the C ABI (< 0: no token row); reads nnz to the host once. With id_limit >= 0 the table is
+// validated on the device first (bf_check_table: row lengths in [0, width], ids in [0, id_limit)).
 std::tuple<at::Tensor, at::Tensor> table_to_csr(const at::Tensor& table, const at::Tensor& row_len, bool global_token,
-                                                int64_t token_row) {
+                                                int64_t token_row, int64_t id_limit) {
   const c10::DeviceGuard guard(table.device());
   const at::Device dev = table.device();
   require(table, "table", at::kInt, dev);
@@ -258,6 +259,12 @@ std::tuple<at::Tensor, at::Tensor> table_to_csr(const at::Tensor& table, const a
   TORCH_CHECK_VALUE(table.dim() == 2 && row_len.dim() == 1 && row_len.size(0) == table.size(0),
                     "table must be [n, width] and row_len [n]");
   const int64_t n_rows = table.size(0);
+  if (id_limit >= 0) {
+    at::Tensor bad = at::empty({2}, table.options().dtype(at::kLong));
+    check_rc(bf_check_table(table.data_ptr<int32_t>(), row_len.data_ptr<int32_t>(), n_rows, int32_t(table.size(1)),
+                            id_limit, nullptr, bad.data_ptr(), 16, stream_of(table)),
+             "bf::table_to_csr");
+  }
   const int64_t lead = (global_token && token_row >= 0) ? 1 : 0;
   const int64_t n_q = n_rows + lead;
   size_t ws_bytes = 0;
@@ -312,7 +319,8 @@ TORCH_LIBRARY(bf, m) {
         "int n_q, int walks_per_node, int walk_length, int k_real, int k_rw, int edge_seed, Tensor? u=None, "
         "int philox_seed=0, int philox_offset=0, Tensor? hubs=None, int hub_threshold=1024, Tensor? heavy=None, "
         "int light_max=-1) -> (Tensor, Tensor)");
-  m.def("table_to_csr(Tensor table, Tensor row_len, bool global_token=False, int token_row=-1) -> (Tensor, Tensor)");
+  m.def("table_to_csr(Tensor table, Tensor row_len, bool global_token=False, int token_row=-1, int id_limit=-1) "
+        "-> (Tensor, Tensor)");
   m.def("transpose_table(Tensor qptr, Tensor kv, int n_kv) -> (Tensor, Tensor, Tensor)");
 }
 

@@ -370,6 +370,20 @@ def _token_row(n_rows: int, global_token: bool, token_row: Optional[int]) -> int
     return n_rows if token_row is None else int(token_row)
 
 
+def check_table(table: torch.Tensor, row_len: torch.Tensor, id_limit: int) -> None:
+    """Device-side validation of an externally supplied table (bf_check_table): raises ValueError when a
+    row length lies outside [0, width] or an id of a row's first row_len slots outside [0, id_limit).
+    One kernel and one 16-byte read back."""
+    dev = table.device
+    _require(table, "table", torch.int32)
+    _require(row_len, "row_len", torch.int32, dev)
+    if table.dim() != 2 or row_len.shape != (table.shape[0],):
+        raise ValueError("table must be [n, width] and row_len [n]")
+    ws = torch.empty(2, dtype=torch.int64, device=dev)
+    N.call("bf_check_table", _p(table), _p(row_len), table.shape[0], table.shape[1], int(id_limit), None, _p(ws), 16,
+           _stream(dev))
+
+
 def table_qptr(table: torch.Tensor, row_len: torch.Tensor, global_token: bool = False,
                token_row: Optional[int] = None) -> torch.Tensor:
     """qptr [n_q+1] int64 of a query-major table (bf_table_csr_ptr without the host read of nnz).
@@ -885,18 +899,7 @@ class AttentionIndex:
         if global_token and tr > n_kv - 1:
             raise ValueError(f"the token row lists kv 1..{tr}, beyond the {n_kv} kv rows")
         if check and table.numel():
-            _require(table, "table", torch.int32)
-            _require(row_len, "row_len", torch.int32, table.device)
-            lens = row_len.to(torch.int64)
-            used = torch.arange(width, device=table.device)[None, :] < lens[:, None]
-            ids = torch.where(used, table, torch.zeros((), dtype=table.dtype, device=table.device))
-            lo = torch.where(used, table, torch.full((), 2**31 - 1, dtype=table.dtype, device=table.device))
-            stats = torch.stack([lens.min(), lens.max(), lo.min().to(torch.int64), ids.max().to(torch.int64)]).tolist()
-            shift = 1 if global_token else 0
-            if stats[0] < 0 or stats[1] > width:
-                raise ValueError(f"row_len must lie in [0, {width}] (got [{stats[0]}, {stats[1]}])")
-            if stats[1] > 0 and (stats[2] < 0 or stats[3] + shift >= n_kv):
-                raise ValueError(f"table ids must lie in [0, {n_kv - shift}) (got [{stats[2]}, {stats[3]}])")
+            check_table(table, row_len, n_kv - (1 if global_token else 0))
         # A table row holds at most `width` entries (+ key 0 with the token), so when that is within
         # `chunk` only the token row (every node, tr entries) can be split: the query plan's counts
         # follow from the sizes, with no read of the device.

@@ -264,6 +264,18 @@ int bf_chung_lu(int64_t num_nodes, int64_t pairs, double exponent, double i0, do
  * q_bits >= bits of n_q, slot_bits >= bits of width and q_bits + slot_bits
  * <= 33 (BF_ERR_INVALID otherwise). Workspace: bf_scan_workspace_size(n_q). */
 int bf_scan_workspace_size(int64_t n, size_t* bytes);
+
+/* Device-side validation of an externally supplied table before its index
+ * is built (the edge builder's own tables are valid by construction): counts
+ * the rows whose row_len lies outside [0, width] and the ids of each row's
+ * first row_len slots outside [0, id_limit) (id_limit = n_kv, or n_kv - 1
+ * with global_token, whose ids shift by one), writes the two counts to
+ * bad_host (may be NULL) and returns BF_ERR_INVALID when either is nonzero.
+ * Synchronises the stream. Workspace: 16 bytes of device memory. The
+ * reference builds its edge lists itself; the nearest check is
+ * fix_edge_index's id arithmetic (gt_sp/utils.py:113-130).                 */
+int bf_check_table(const int32_t* table, const int32_t* row_len, int64_t n_rows, int32_t width,
+                   int64_t id_limit, int64_t* bad_host, void* workspace, size_t workspace_bytes, void* stream);
 int bf_table_csr_ptr(const int32_t* row_len, int64_t n_rows, int32_t global_token, int64_t token_row,
                      int64_t* qptr, int64_t* nnz_host, void* workspace, size_t workspace_bytes, void* stream);
 int bf_table_to_csr(const int32_t* table, const int32_t* row_len, int64_t n_rows, int32_t width,

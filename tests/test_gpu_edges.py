@@ -315,7 +315,10 @@ def test_light_rows_with_unaligned_in_neighbour_array(hip_device):
 
 @pytest.mark.parametrize("token", [False, True])
 def test_from_table_rejects_invalid_tables(hip_device, token):
-    """An external table is validated on the host side before any index kernel reads it."""
+    """An external table is validated on the device (bf_check_table) before any index kernel reads it:
+    ids within [0, n_kv) (n_kv - 1 with the token's shift), row lengths within [0, width]; padding past
+    a row's length is not read. The same check behind the table_to_csr operator's id_limit."""
+    from budgetformer_amd import _native
     from budgetformer_amd.hip_ops import AttentionIndex
     n, width = 50, 4
     table = torch.full((n, width), -1, dtype=torch.int32, device=hip_device)
@@ -325,16 +328,23 @@ def test_from_table_rejects_invalid_tables(hip_device, token):
     AttentionIndex.from_table(table, row_len, token)                       # valid
     bad = table.clone()
     bad[7, 0] = n + 3                                                       # id beyond the kv rows
-    with pytest.raises(ValueError):
+    bad[8, 0] = n                                                           # the first id past the limit
+    with pytest.raises(ValueError, match="2 table ids outside"):
         AttentionIndex.from_table(bad, row_len, token)
     bad = table.clone()
     bad[9, 0] = -1                                                          # padding inside row_len
-    with pytest.raises(ValueError):
+    with pytest.raises(ValueError, match="1 table ids outside"):
         AttentionIndex.from_table(bad, row_len, token)
     long = row_len.clone()
     long[3] = width + 1
-    with pytest.raises(ValueError):
+    long[4] = -2
+    with pytest.raises(ValueError, match="2 row lengths outside"):
         AttentionIndex.from_table(table, long, token)
+    ops = _native.load_ops()
+    tr = n if token else -1
+    ops.table_to_csr(table, row_len, token, tr, n)      # n kv rows (n + 1 with the token, ids shifted by one)
+    with pytest.raises(ValueError, match="ids outside"):
+        ops.table_to_csr(bad, row_len, token, tr, n)
 
 
 @pytest.mark.parametrize("token", [False, True])
