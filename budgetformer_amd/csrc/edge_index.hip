@@ -3,11 +3,10 @@
 // used by the deterministic dK/dV pass and by the COO adaptor, and split plans
 // for rows longer than the attention chunk.
 //
-// Sorting and prefix sums use rocPRIM through hipCUB (LSD radix sort is stable,
+// Sorting and prefix sums use rocPRIM (bf_prim.h; its LSD radix sort is stable,
 // which makes the reverse index ordered by (kv, CSR position) = (src, dst)).
-#include <hipcub/hipcub.hpp>
-
 #include "bf_common.h"
+#include "bf_prim.h"
 
 namespace bf {
 namespace {
@@ -26,8 +25,8 @@ int bits_for(uint64_t maxval) {
 
 size_t scan_temp_bytes_i64(int64_t n) {
   size_t bytes = 0;
-  (void)hipcub::DeviceScan::InclusiveSum(nullptr, bytes, static_cast<const int64_t*>(nullptr),
-                                   static_cast<int64_t*>(nullptr), int(n > 0 ? n : 1));
+  (void)prim::inclusive_sum(nullptr, bytes, static_cast<const int64_t*>(nullptr), static_cast<int64_t*>(nullptr),
+                            n > 0 ? n : 1, hipStream_t(nullptr));
   return bytes;
 }
 
@@ -361,8 +360,8 @@ struct MaxOp {
 
 size_t row_ids_temp_bytes(int64_t nnz) {
   size_t bytes = 0;
-  (void)hipcub::DeviceScan::InclusiveScan(nullptr, bytes, static_cast<const int32_t*>(nullptr),
-                                          static_cast<int32_t*>(nullptr), MaxOp(), int(nnz > 0 ? nnz : 1));
+  (void)prim::inclusive_scan(nullptr, bytes, static_cast<const int32_t*>(nullptr), static_cast<int32_t*>(nullptr),
+                             MaxOp(), nnz > 0 ? nnz : 1, hipStream_t(nullptr));
   return bytes;
 }
 
@@ -372,7 +371,7 @@ int row_ids(const int64_t* ptr, int64_t n_rows, int64_t nnz, int32_t* marks, int
   BF_CHECK_HIP(hipMemsetAsync(marks, 0, size_t(nnz) * sizeof(int32_t), st));
   BF_LAUNCH("row_marks_kernel", row_marks_kernel, dim3(blocks_for(n_rows)), dim3(kThreads), 0, st, ptr, n_rows, marks);
   BF_CHECK_LAUNCH();
-  BF_CHECK_HIP(hipcub::DeviceScan::InclusiveScan(temp, temp_bytes, marks, rows, MaxOp(), int(nnz), st));
+  BF_CHECK_HIP(prim::inclusive_scan(temp, temp_bytes, static_cast<const int32_t*>(marks), rows, MaxOp(), nnz, st));
   return BF_OK;
 }
 
@@ -467,7 +466,7 @@ extern "C" int bf_table_csr_ptr(const int32_t* row_len, int64_t n_rows, int32_t 
     BF_LAUNCH("row_lengths_kernel", row_lengths_kernel, dim3(blocks_for(n_q)), dim3(kThreads), 0, st, row_len, n_rows,
               int(global_token != 0), lead, lead ? token_row : int64_t(0), lens, qptr);
     BF_CHECK_LAUNCH();
-    BF_CHECK_HIP(hipcub::DeviceScan::InclusiveSum(temp, temp_bytes, lens, qptr + 1, int(n_q), st));
+    BF_CHECK_HIP(prim::inclusive_sum(temp, temp_bytes, static_cast<const int64_t*>(lens), qptr + 1, n_q, st));
   }
   if (!nnz_host) return BF_OK;   // the caller reads qptr[n_q] itself, when it needs it
   int64_t h = 0;
@@ -539,8 +538,8 @@ extern "C" int bf_table_to_csr(const int32_t* table, const int32_t* row_len, int
 extern "C" int bf_coo_to_csr_workspace_size(int64_t nnz, int64_t n_q, size_t* bytes) {
   BF_CHECK_ARG(bytes && nnz >= 0 && n_q >= 0, "coo_to_csr_workspace_size: bad arguments");
   size_t sort_bytes = 0;
-  (void)hipcub::DeviceRadixSort::SortKeys(nullptr, sort_bytes, static_cast<const uint64_t*>(nullptr),
-                                    static_cast<uint64_t*>(nullptr), int(nnz > 0 ? nnz : 1));
+  (void)prim::sort_keys(nullptr, sort_bytes, static_cast<const uint64_t*>(nullptr), static_cast<uint64_t*>(nullptr),
+                        nnz > 0 ? nnz : 1, 0, 64, hipStream_t(nullptr));
   *bytes = 2 * align_up(size_t(nnz > 0 ? nnz : 1) * sizeof(uint64_t)) + align_up(sort_bytes) + 256;
   (void)n_q;
   return BF_OK;
@@ -562,12 +561,12 @@ extern "C" int bf_coo_to_csr(const int64_t* src, const int64_t* dst, int64_t nnz
   auto* keys_out = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + align_up(size_t(nnz) * 8));
   void* temp = static_cast<char*>(workspace) + 2 * align_up(size_t(nnz) * 8);
   size_t temp_bytes = 0;
-  (void)hipcub::DeviceRadixSort::SortKeys(nullptr, temp_bytes, keys_in, keys_out, int(nnz));
+  (void)prim::sort_keys(nullptr, temp_bytes, static_cast<const uint64_t*>(keys_in), keys_out, nnz, 0, 64, st);
   BF_LAUNCH("coo_keys_kernel", coo_keys_kernel, dim3(blocks_for(nnz)), dim3(kThreads), 0, st, src, dst, nnz,
                      uint64_t(n_kv), keys_in);
   BF_CHECK_LAUNCH();
   const int end_bit = bits_for(uint64_t(n_q) * uint64_t(n_kv));
-  BF_CHECK_HIP(hipcub::DeviceRadixSort::SortKeys(temp, temp_bytes, keys_in, keys_out, int(nnz), 0, end_bit, st));
+  BF_CHECK_HIP(prim::sort_keys(temp, temp_bytes, static_cast<const uint64_t*>(keys_in), keys_out, nnz, 0, end_bit, st));
   BF_LAUNCH("coo_kv_kernel", coo_kv_kernel, dim3(blocks_for(nnz)), dim3(kThreads), 0, st, keys_out, nnz,
                      uint64_t(n_kv), kv);
   BF_CHECK_LAUNCH();
@@ -580,10 +579,10 @@ extern "C" int bf_coo_to_csr(const int64_t* src, const int64_t* dst, int64_t nnz
 extern "C" int bf_reverse_index_workspace_size(int64_t nnz, int64_t n_kv, size_t* bytes) {
   BF_CHECK_ARG(bytes && nnz >= 0 && n_kv >= 0, "reverse_index_workspace_size: bad arguments");
   size_t sort_bytes = 0;
-  const int n = int(nnz > 0 ? nnz : 1);
-  (void)hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, static_cast<const uint32_t*>(nullptr),
-                                           static_cast<uint32_t*>(nullptr), static_cast<const uint64_t*>(nullptr),
-                                           static_cast<uint64_t*>(nullptr), n);
+  const int64_t n = nnz > 0 ? nnz : 1;
+  (void)prim::sort_pairs(nullptr, sort_bytes, static_cast<const uint32_t*>(nullptr), static_cast<uint32_t*>(nullptr),
+                         static_cast<const uint64_t*>(nullptr), static_cast<uint64_t*>(nullptr), n, 0, 32,
+                         hipStream_t(nullptr));
   const size_t scan_bytes = row_ids_temp_bytes(nnz);
   // keys_out (4) + marks (4) + rows (4) + packed values in/out (8 + 8) bytes per entry, then temp
   *bytes = 3 * align_up(size_t(n) * 4) + 2 * align_up(size_t(n) * 8) +
@@ -621,8 +620,8 @@ extern "C" int bf_reverse_index(const int64_t* qptr, const int32_t* kv, int64_t 
   BF_CHECK_LAUNCH();
   const int end_bit = bits_for(uint64_t(n_kv > 0 ? n_kv : 1));
   size_t tb = temp_bytes;
-  BF_CHECK_HIP(hipcub::DeviceRadixSort::SortPairs(temp, tb, reinterpret_cast<const uint32_t*>(kv), keys_out, vals_in,
-                                                  vals_out, int(nnz), 0, end_bit, st));
+  BF_CHECK_HIP(prim::sort_pairs(temp, tb, reinterpret_cast<const uint32_t*>(kv), keys_out,
+                                static_cast<const uint64_t*>(vals_in), vals_out, nnz, 0, end_bit, st));
   BF_LAUNCH("boundaries_kernel", boundaries_kernel<uint32_t>, dim3(blocks_for(nnz + 1)), dim3(kThreads), 0, st, keys_out,
             nnz, uint64_t(1), n_kv, kptr);
   BF_CHECK_LAUNCH();
@@ -635,8 +634,8 @@ extern "C" int bf_reverse_index(const int64_t* qptr, const int32_t* kv, int64_t 
 extern "C" int bf_reverse_index_packed_workspace_size(int64_t nnz, size_t* bytes) {
   BF_CHECK_ARG(bytes && nnz >= 0, "reverse_index_packed_workspace_size: bad arguments");
   size_t sort_bytes = 0;
-  (void)hipcub::DeviceRadixSort::SortKeys(nullptr, sort_bytes, static_cast<const uint64_t*>(nullptr),
-                                          static_cast<uint64_t*>(nullptr), int(nnz > 0 ? nnz : 1));
+  (void)prim::sort_keys(nullptr, sort_bytes, static_cast<const uint64_t*>(nullptr), static_cast<uint64_t*>(nullptr),
+                        nnz > 0 ? nnz : 1, 0, 64, hipStream_t(nullptr));
   *bytes = align_up(sort_bytes) + 256;
   return BF_OK;
 }
@@ -663,7 +662,7 @@ extern "C" int bf_reverse_index_packed(const uint64_t* rkey, const int64_t* qptr
   BF_CHECK_ARG(rkey && sorted && kq, "reverse_index_packed: null tensor");
   size_t tb = workspace_bytes;
   // only the id bits are sorted; the stable passes keep each id's entries in CSR order
-  BF_CHECK_HIP(hipcub::DeviceRadixSort::SortKeys(workspace, tb, rkey, sorted, int(nnz), kshift, kshift + id_bits, st));
+  BF_CHECK_HIP(prim::sort_keys(workspace, tb, rkey, sorted, nnz, kshift, kshift + id_bits, st));
   BF_LAUNCH("unpack_rkey_kernel", unpack_rkey_kernel,
             dim3(unsigned(ceil_div(nnz + 1, int64_t(kThreads) * kUnpackPerThread))), dim3(kThreads), 0, st, sorted, nnz,
             kshift, slot_bits, int(token_row != 0), qptr, n_kv, kptr, kq, ke);
@@ -714,8 +713,8 @@ extern "C" int64_t bf_split_row_capacity(int64_t nnz, int32_t threshold) {
 extern "C" int bf_split_plan_workspace_size(int64_t n_rows, size_t* bytes) {
   BF_CHECK_ARG(bytes && n_rows >= 0, "split_plan_workspace_size: bad arguments");
   size_t temp_bytes = 0;
-  (void)hipcub::DeviceScan::ExclusiveSum(nullptr, temp_bytes, static_cast<const uint64_t*>(nullptr),
-                                         static_cast<uint64_t*>(nullptr), int(n_rows > 0 ? n_rows : 1));
+  (void)prim::exclusive_sum(nullptr, temp_bytes, static_cast<const uint64_t*>(nullptr),
+                            static_cast<uint64_t*>(nullptr), n_rows > 0 ? n_rows : 1, hipStream_t(nullptr));
   *bytes = 2 * align_up(size_t(n_rows > 0 ? n_rows : 1) * 8) + align_up(temp_bytes) + 256;
   return BF_OK;
 }
@@ -743,11 +742,11 @@ extern "C" int bf_split_plan(const int64_t* ptr, int64_t n_rows, int32_t thresho
   auto* packed_off = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + slab);
   void* temp = static_cast<char*>(workspace) + 2 * slab;
   size_t temp_bytes = 0;
-  (void)hipcub::DeviceScan::ExclusiveSum(nullptr, temp_bytes, packed, packed_off, int(n_rows));
+  (void)prim::exclusive_sum(nullptr, temp_bytes, static_cast<const uint64_t*>(packed), packed_off, n_rows, st);
   BF_LAUNCH("split_count_kernel", split_count_kernel, dim3(blocks_for(n_rows)), dim3(kThreads), 0, st, ptr, n_rows,
             threshold, item_size, packed);
   BF_CHECK_LAUNCH();
-  BF_CHECK_HIP(hipcub::DeviceScan::ExclusiveSum(temp, temp_bytes, packed, packed_off, int(n_rows), st));
+  BF_CHECK_HIP(prim::exclusive_sum(temp, temp_bytes, static_cast<const uint64_t*>(packed), packed_off, n_rows, st));
   BF_LAUNCH("split_rows_kernel", split_rows_kernel, dim3(blocks_for(n_rows)), dim3(kThreads), 0, st, packed,
             packed_off, static_cast<const int32_t*>(nullptr), n_rows, item_cap, nitems, item_off, item_row,
             heavy_rows, heavy_cap, counts);
@@ -835,8 +834,8 @@ extern "C" int bf_hop_pool_workspace_size(int64_t n_walks, int32_t walk_length, 
   BF_CHECK_ARG(bytes && n_walks >= 0 && walk_length >= 1 && min_hop >= 1, "hop_pool_workspace_size: bad arguments");
   const int64_t m = n_walks * (min_hop <= walk_length ? walk_length - min_hop + 1 : 0);
   size_t scan_bytes = 0;
-  (void)hipcub::DeviceScan::ExclusiveSum(nullptr, scan_bytes, static_cast<const int64_t*>(nullptr),
-                                         static_cast<int64_t*>(nullptr), int(m > 0 ? m : 1));
+  (void)prim::exclusive_sum(nullptr, scan_bytes, static_cast<const int64_t*>(nullptr), static_cast<int64_t*>(nullptr),
+                            m > 0 ? m : 1, hipStream_t(nullptr));
   *bytes = align_up(size_t(m > 0 ? m : 1) * 4) + 2 * align_up(size_t(m > 0 ? m : 1) * 8) + align_up(scan_bytes) + 256;
   return BF_OK;
 }
@@ -859,13 +858,13 @@ extern "C" int bf_hop_pool(const int64_t* walks, int64_t n_walks, int32_t walk_l
   auto* pos = reinterpret_cast<int64_t*>(reinterpret_cast<char*>(flags64) + align_up(size_t(m) * 8));
   void* temp = reinterpret_cast<char*>(pos) + align_up(size_t(m) * 8);
   size_t temp_bytes = 0;
-  (void)hipcub::DeviceScan::ExclusiveSum(nullptr, temp_bytes, flags64, pos, int(m));
+  (void)prim::exclusive_sum(nullptr, temp_bytes, static_cast<const int64_t*>(flags64), pos, m, st);
   BF_LAUNCH("hop_flags_kernel", hop_flags_kernel, dim3(blocks_for(m)), dim3(kThreads), 0, st, walks, n_walks,
             walk_length, min_hop, flags);
   BF_CHECK_LAUNCH();
   BF_LAUNCH("i32_to_i64_kernel", i32_to_i64_kernel, dim3(blocks_for(m)), dim3(kThreads), 0, st, flags, m, flags64);
   BF_CHECK_LAUNCH();
-  BF_CHECK_HIP(hipcub::DeviceScan::ExclusiveSum(temp, temp_bytes, flags64, pos, int(m), st));
+  BF_CHECK_HIP(prim::exclusive_sum(temp, temp_bytes, static_cast<const int64_t*>(flags64), pos, m, st));
   BF_LAUNCH("hop_fill_kernel", hop_fill_kernel, dim3(blocks_for(m)), dim3(kThreads), 0, st, walks, n_walks,
             walk_length, min_hop, flags, pos, pool_kv, pool_q);
   BF_CHECK_LAUNCH();
@@ -880,12 +879,12 @@ extern "C" int bf_hop_pool(const int64_t* walks, int64_t n_walks, int32_t walk_l
 
 extern "C" int bf_coalesce_workspace_size(int64_t nnz, size_t* bytes) {
   BF_CHECK_ARG(bytes && nnz >= 0, "coalesce_workspace_size: bad arguments");
-  const int n = int(nnz > 0 ? nnz : 1);
+  const int64_t n = nnz > 0 ? nnz : 1;
   size_t sort_bytes = 0, scan_bytes = 0;
-  (void)hipcub::DeviceRadixSort::SortKeys(nullptr, sort_bytes, static_cast<const uint64_t*>(nullptr),
-                                          static_cast<uint64_t*>(nullptr), n);
-  (void)hipcub::DeviceScan::InclusiveSum(nullptr, scan_bytes, static_cast<const int64_t*>(nullptr),
-                                         static_cast<int64_t*>(nullptr), n);
+  (void)prim::sort_keys(nullptr, sort_bytes, static_cast<const uint64_t*>(nullptr), static_cast<uint64_t*>(nullptr),
+                        n, 0, 64, hipStream_t(nullptr));
+  (void)prim::inclusive_sum(nullptr, scan_bytes, static_cast<const int64_t*>(nullptr), static_cast<int64_t*>(nullptr),
+                            n, hipStream_t(nullptr));
   *bytes = 4 * align_up(size_t(n) * 8) + align_up(sort_bytes > scan_bytes ? sort_bytes : scan_bytes) + 256;
   return BF_OK;
 }
@@ -909,16 +908,16 @@ extern "C" int bf_coalesce(const int64_t* src, const int64_t* dst, int64_t nnz, 
   auto* incl = reinterpret_cast<int64_t*>(static_cast<char*>(workspace) + 3 * slab);
   void* temp = static_cast<char*>(workspace) + 4 * slab;
   size_t sort_bytes = 0, scan_bytes = 0;
-  (void)hipcub::DeviceRadixSort::SortKeys(nullptr, sort_bytes, keys_in, keys, int(nnz));
-  (void)hipcub::DeviceScan::InclusiveSum(nullptr, scan_bytes, flags, incl, int(nnz));
+  (void)prim::sort_keys(nullptr, sort_bytes, static_cast<const uint64_t*>(keys_in), keys, nnz, 0, 64, st);
+  (void)prim::inclusive_sum(nullptr, scan_bytes, static_cast<const int64_t*>(flags), incl, nnz, st);
   BF_LAUNCH("coalesce_keys_kernel", coalesce_keys_kernel, dim3(blocks_for(nnz)), dim3(kThreads), 0, st, src, dst, nnz,
             uint64_t(num_nodes), keys_in);
   BF_CHECK_LAUNCH();
   const int end_bit = bits_for(uint64_t(num_nodes) * uint64_t(num_nodes));
-  BF_CHECK_HIP(hipcub::DeviceRadixSort::SortKeys(temp, sort_bytes, keys_in, keys, int(nnz), 0, end_bit, st));
+  BF_CHECK_HIP(prim::sort_keys(temp, sort_bytes, static_cast<const uint64_t*>(keys_in), keys, nnz, 0, end_bit, st));
   BF_LAUNCH("unique_flags_kernel", unique_flags_kernel, dim3(blocks_for(nnz)), dim3(kThreads), 0, st, keys, nnz, flags);
   BF_CHECK_LAUNCH();
-  BF_CHECK_HIP(hipcub::DeviceScan::InclusiveSum(temp, scan_bytes, flags, incl, int(nnz), st));
+  BF_CHECK_HIP(prim::inclusive_sum(temp, scan_bytes, static_cast<const int64_t*>(flags), incl, nnz, st));
   BF_LAUNCH("unique_fill_kernel", unique_fill_kernel, dim3(blocks_for(nnz)), dim3(kThreads), 0, st, keys, incl, nnz,
             uint64_t(num_nodes), out_src, out_dst);
   BF_CHECK_LAUNCH();
@@ -934,8 +933,8 @@ constexpr size_t kOrderHistBytes = 2 * kBuckets * sizeof(uint32_t);
 
 size_t plan_slots_scan_bytes(int64_t n_slots) {
   size_t temp_bytes = 0;
-  (void)hipcub::DeviceScan::ExclusiveSum(nullptr, temp_bytes, static_cast<const uint64_t*>(nullptr),
-                                         static_cast<uint64_t*>(nullptr), int(n_slots > 0 ? n_slots : 1));
+  (void)prim::exclusive_sum(nullptr, temp_bytes, static_cast<const uint64_t*>(nullptr),
+                            static_cast<uint64_t*>(nullptr), n_slots > 0 ? n_slots : 1, hipStream_t(nullptr));
   return temp_bytes;
 }
 
@@ -1014,7 +1013,7 @@ extern "C" int bf_row_order_and_plan(const int64_t* ptr, int64_t n_rows, int32_t
   size_t temp_bytes = plan_slots_scan_bytes(n_slots);
   const int rc = launch_row_order(ptr, n_rows, order, spans, hist, threshold, item_size, n_slots, packed, st);
   if (rc) return rc;
-  BF_CHECK_HIP(hipcub::DeviceScan::ExclusiveSum(temp, temp_bytes, packed, packed_off, int(n_slots), st));
+  BF_CHECK_HIP(prim::exclusive_sum(temp, temp_bytes, static_cast<const uint64_t*>(packed), packed_off, n_slots, st));
   BF_LAUNCH("split_rows_kernel", split_rows_kernel, dim3(blocks_for(n_slots)), dim3(kThreads), 0, st, packed,
             packed_off, order, n_slots, item_cap, nitems, item_off, item_row, heavy_rows, heavy_cap, counts);
   BF_CHECK_LAUNCH();

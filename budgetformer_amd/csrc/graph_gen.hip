@@ -7,9 +7,8 @@
 // keyed by the seed, counter = draw index), self pairs dropped, unordered pairs
 // deduplicated by radix sort, trimmed to exactly `pairs` by a hash order, then
 // symmetrised into a coalesced CSR (int64 rowptr, int32 col).
-#include <hipcub/hipcub.hpp>
-
 #include "bf_common.h"
+#include "bf_prim.h"
 
 namespace bf {
 namespace {
@@ -120,18 +119,18 @@ extern "C" int bf_chung_lu_workspace_size(int64_t num_nodes, int64_t pairs, size
   const int64_t draws = pairs + pairs / 4 + 1024;
   const int64_t slab_n = 2 * pairs > draws ? 2 * pairs : draws;
   size_t sort_bytes = 0, sort2_bytes = 0, scan_bytes = 0, red_bytes = 0, sel_bytes = 0;
-  (void)hipcub::DeviceSelect::Flagged(nullptr, sel_bytes, static_cast<const uint64_t*>(nullptr),
-                                      static_cast<const int32_t*>(nullptr), static_cast<uint64_t*>(nullptr),
-                                      static_cast<int*>(nullptr), int(draws));
-  (void)hipcub::DeviceRadixSort::SortKeys(nullptr, sort_bytes, static_cast<const uint64_t*>(nullptr),
-                                          static_cast<uint64_t*>(nullptr), int(slab_n));
-  (void)hipcub::DeviceRadixSort::SortPairs(nullptr, sort2_bytes, static_cast<const uint64_t*>(nullptr),
-                                           static_cast<uint64_t*>(nullptr), static_cast<const uint64_t*>(nullptr),
-                                           static_cast<uint64_t*>(nullptr), int(draws));
-  (void)hipcub::DeviceScan::InclusiveSum(nullptr, scan_bytes, static_cast<const double*>(nullptr),
-                                         static_cast<double*>(nullptr), int(num_nodes));
-  (void)hipcub::DeviceReduce::Sum(nullptr, red_bytes, static_cast<const double*>(nullptr),
-                                  static_cast<double*>(nullptr), int(num_nodes));
+  const hipStream_t none = nullptr;
+  (void)prim::select_flagged(nullptr, sel_bytes, static_cast<const uint64_t*>(nullptr),
+                             static_cast<const int32_t*>(nullptr), static_cast<uint64_t*>(nullptr),
+                             static_cast<int*>(nullptr), draws, none);
+  (void)prim::sort_keys(nullptr, sort_bytes, static_cast<const uint64_t*>(nullptr), static_cast<uint64_t*>(nullptr),
+                        slab_n, 0, 64, none);
+  (void)prim::sort_pairs(nullptr, sort2_bytes, static_cast<const uint64_t*>(nullptr), static_cast<uint64_t*>(nullptr),
+                         static_cast<const uint64_t*>(nullptr), static_cast<uint64_t*>(nullptr), draws, 0, 64, none);
+  (void)prim::inclusive_sum(nullptr, scan_bytes, static_cast<const double*>(nullptr), static_cast<double*>(nullptr),
+                            num_nodes, none);
+  (void)prim::reduce_sum(nullptr, red_bytes, static_cast<const double*>(nullptr), static_cast<double*>(nullptr),
+                         num_nodes, none);
   size_t temp = sort_bytes;
   for (size_t t : {sort2_bytes, scan_bytes, red_bytes, sel_bytes}) temp = t > temp ? t : temp;
   *bytes = 4 * align_up(size_t(slab_n) * 8) + 2 * align_up(size_t(num_nodes) * 8) + align_up(size_t(draws) * 4) +
@@ -172,12 +171,12 @@ extern "C" int bf_chung_lu(int64_t num_nodes, int64_t pairs, double exponent, do
             exponent, dsum);
   BF_CHECK_LAUNCH();
   size_t tb = temp_bytes;
-  BF_CHECK_HIP(hipcub::DeviceReduce::Sum(temp, tb, dsum, cdf, int(num_nodes), st));
+  BF_CHECK_HIP(prim::reduce_sum(temp, tb, static_cast<const double*>(dsum), cdf, num_nodes, st));
   BF_LAUNCH("scale_cap_kernel", scale_cap_kernel, dim3(blocks_for(num_nodes)), dim3(kThreads), 0, st, num_nodes, cdf,
             double(2 * pairs), max_degree, dsum);
   BF_CHECK_LAUNCH();
   tb = temp_bytes;
-  BF_CHECK_HIP(hipcub::DeviceScan::InclusiveSum(temp, tb, dsum, cdf, int(num_nodes), st));
+  BF_CHECK_HIP(prim::inclusive_sum(temp, tb, static_cast<const double*>(dsum), cdf, num_nodes, st));
 
   // draw, sort, count unique; redraw into the tail until enough unique pairs exist
   int64_t have = 0;           // unique keys at the front of keys_a (sorted)
@@ -189,13 +188,14 @@ extern "C" int bf_chung_lu(int64_t num_nodes, int64_t pairs, double exponent, do
     BF_CHECK_LAUNCH();
     counter += uint64_t(fresh);
     tb = temp_bytes;
-    BF_CHECK_HIP(hipcub::DeviceRadixSort::SortKeys(temp, tb, keys_a, keys_b, int(draws), 0, 64, st));
+    BF_CHECK_HIP(prim::sort_keys(temp, tb, static_cast<const uint64_t*>(keys_a), keys_b, draws, 0, 64, st));
     BF_LAUNCH("unique_flag_kernel", unique_flag_kernel, dim3(blocks_for(draws)), dim3(kThreads), 0, st, keys_b, draws,
               flags);
     BF_CHECK_LAUNCH();
     int* d_count = reinterpret_cast<int*>(keys_d);
     tb = temp_bytes;
-    BF_CHECK_HIP(hipcub::DeviceSelect::Flagged(temp, tb, keys_b, flags, keys_a, d_count, int(draws), st));
+    BF_CHECK_HIP(prim::select_flagged(temp, tb, static_cast<const uint64_t*>(keys_b),
+                                      static_cast<const int32_t*>(flags), keys_a, d_count, draws, st));
     int h = 0;
     BF_CHECK_HIP(hipMemcpyAsync(&h, d_count, sizeof(int), hipMemcpyDeviceToHost, st));
     BF_CHECK_HIP(hipStreamSynchronize(st));
@@ -208,9 +208,10 @@ extern "C" int bf_chung_lu(int64_t num_nodes, int64_t pairs, double exponent, do
             keys_b);
   BF_CHECK_LAUNCH();
   tb = temp_bytes;
-  BF_CHECK_HIP(hipcub::DeviceRadixSort::SortPairs(temp, tb, keys_b, keys_c, keys_a, keys_d, int(have), 0, 64, st));
+  BF_CHECK_HIP(prim::sort_pairs(temp, tb, static_cast<const uint64_t*>(keys_b), keys_c,
+                                static_cast<const uint64_t*>(keys_a), keys_d, have, 0, 64, st));
   tb = temp_bytes;
-  BF_CHECK_HIP(hipcub::DeviceRadixSort::SortKeys(temp, tb, keys_d, keys_a, int(pairs), 0, pair_bits, st));
+  BF_CHECK_HIP(prim::sort_keys(temp, tb, static_cast<const uint64_t*>(keys_d), keys_a, pairs, 0, pair_bits, st));
 
   // symmetrise and sort (src, dst)
   BF_LAUNCH("symmetrize_kernel", symmetrize_kernel, dim3(blocks_for(pairs)), dim3(kThreads), 0, st, keys_a, pairs, n,
@@ -218,7 +219,7 @@ extern "C" int bf_chung_lu(int64_t num_nodes, int64_t pairs, double exponent, do
   BF_CHECK_LAUNCH();
   const int64_t m = 2 * pairs;
   tb = temp_bytes;
-  BF_CHECK_HIP(hipcub::DeviceRadixSort::SortKeys(temp, tb, keys_b, keys_c, int(m), 0, pair_bits, st));
+  BF_CHECK_HIP(prim::sort_keys(temp, tb, static_cast<const uint64_t*>(keys_b), keys_c, m, 0, pair_bits, st));
   BF_LAUNCH("csr_col_kernel", csr_col_kernel, dim3(blocks_for(m)), dim3(kThreads), 0, st, keys_c, m, n, col);
   BF_CHECK_LAUNCH();
   BF_LAUNCH("csr_rowptr_kernel", csr_rowptr_kernel, dim3(blocks_for(m + 1)), dim3(kThreads), 0, st, keys_c, m, n,
