@@ -267,8 +267,9 @@ def main(argv=None):
         print(rocprof_summary(args.rocprof_summary))
         return 0
     names = ["attn_fwd_kernel", "attn_bwd_q_kernel", "attn_bwd_kv_kernel", "attn_fwd_reduce_kernel",
-             "attn_bwd_q_reduce_kernel", "attn_bwd_kv_reduce_kernel", "rw_select_kernel", "real_select_fused_kernel",
-             "table_fill_kernel", "unpack_rkey_kernel"]
+             "attn_bwd_q_reduce_kernel", "attn_bwd_kv_reduce_kernel", "rw_select_reg_kernel", "rw_select_kernel",
+             "real_select_fused_kernel", "table_fill_kernel", "unpack_rkey_kernel", "reverse_entries_kernel",
+             "order_hist_kernel", "order_scatter_kernel", "rocprim"]
     if args.pmc_summary or args.req_summary:
         if args.pmc_summary:
             md, data = pmc_summary(*args.pmc_summary, args.copy_bytes, names)
