@@ -55,7 +55,7 @@ CONFIGS = {
     "c5": dict(name="c5: one GPU's 27.8M-query shard of a power-law graph N=111,059,956 E=1.6B (max deg 100K), "
                     "Graphormer hidden 128, 8 heads, L=4 P=2 B=8 (4,4), bf16, global token (the shard holds node 0)",
                n=111_059_956, e=1_600_000_000, kind="device", max_degree=100_000, H=8, hn=16, L=4, P=2, b_r=4,
-               b_w=4, dtype="bfloat16", token=True, n_q=27_800_000, cpu_sample=None),
+               b_w=4, dtype="bfloat16", token=True, n_q=27_800_000, cpu_sample=1_000_000),
 }
 
 
@@ -510,12 +510,7 @@ def run(config, steps, warmup, chunk=None, item=None, with_cpu=True):
     }
 
     if with_cpu:
-        if cfg.get("cpu_sample", 0) is None:
-            result["cpu_baseline"] = {"value": None, "unit": "GB/s", "cores": os.cpu_count(), "kind": "port",
-                                      "sample": "skipped: the CPU oracle would need the 111M-row K/V and 1.6B-edge "
-                                                "topology in host memory; see c3/c4 for sampled CPU timings"}
-        else:
-            result["cpu_baseline"] = cpu_baseline(cfg, g, tab, idx, q, k, v, dout, s_bytes, D, H)
+        result["cpu_baseline"] = cpu_baseline(cfg, g, tab, idx, q, k, v, dout, s_bytes, D, H)
     del q, k, v, dout, tab, idx, g
     return result
 
@@ -523,10 +518,17 @@ def run(config, steps, warmup, chunk=None, item=None, with_cpu=True):
 def cpu_baseline(cfg, g, tab, idx, q, k, v, dout, s_bytes, D, H):
     """The CPU oracle (the reference algorithm restated in torch/numpy) on this host's cores.
 
-    Small configs run the whole workload; large ones (``cpu_sample`` set) run
-    the first ``cpu_sample`` queries (their attention edges with the touched
-    K/V rows relabelled, and their edge-table rows) and scale the time linearly
-    to the full query count.
+    Small configs run the whole workload. Large ones (``cpu_sample`` set) run a
+    contiguous range of ``cpu_sample`` queries whose mean in-degree equals the
+    workload's (the power-law graphs put their hubs at the lowest ids, so a range
+    from node 0 would be mostly hubs):
+    - attention: the range's attention rows (their edges, the touched K/V rows
+      relabelled; never the Graphormer token's own row), time scaled by the
+      attention entries, all rows' over the sample's;
+    - edge build: the oracle build of the range, modelled as a fixed part (a
+      one-query build: the oracle's passes over the whole edge list) plus a
+      per-query part scaled linearly to the workload's queries.
+    GraphGPS configs with dropout time the GPS form with a drawn keep mask.
     """
     import numpy as np
     import torch
@@ -539,46 +541,85 @@ def cpu_baseline(cfg, g, tab, idx, q, k, v, dout, s_bytes, D, H):
     torch.set_num_threads(threads)
     n = cfg["n"]
     n_rows = cfg.get("n_q") or n
-    sample = cfg.get("cpu_sample") or n_rows
-    sample = min(sample, n_rows)
-    scale = n_rows / sample
-    # attention edges of the first `sample` query rows (+ the token row when present)
-    q_hi = sample + (1 if cfg["token"] else 0)
-    e_hi = int(idx.qptr[q_hi].item())
-    rows = idx.entry_rows()[:e_hi].cpu()
-    kv = idx.kv[:e_hi].cpu().long()
+    sample = min(cfg.get("cpu_sample") or n_rows, n_rows)
+    whole = sample == n_rows
+    tok = 1 if cfg["token"] else 0
+    q0 = 0
+    if not whole:
+        # the contiguous range of `sample` queries whose mean in-degree is closest to the workload's
+        deg = (g.in_ptr[1:n_rows + 1] - g.in_ptr[:n_rows]).double()
+        csum = torch.cat([torch.zeros(1, dtype=torch.float64, device=deg.device), deg.cumsum(0)])
+        target = float(csum[-1]) / n_rows
+        starts = torch.arange(0, n_rows - sample + 1, max(1, (n_rows - sample) // 512), device=deg.device)
+        means = (csum[starts + sample] - csum[starts]) / sample
+        q0 = int(starts[int(torch.argmin((means - target).abs()))])
+    # attention rows of those queries (query x is attention row x + tok); the whole workload adds the token row
+    r_lo = 0 if whole else q0 + tok
+    r_hi = n_rows + tok if whole else q0 + tok + sample
+    e_lo, e_hi = int(idx.qptr[r_lo].item()), int(idx.qptr[r_hi].item())
+    attn_scale = idx.nnz / max(e_hi - e_lo, 1)
+    print(f"[bench] cpu baseline: attention of rows {r_lo:,}..{r_hi - 1:,} ({e_hi - e_lo:,} entries) on "
+          f"{threads} threads", flush=True)
+    rows = idx.entry_rows()[e_lo:e_hi].cpu() - r_lo
+    kv = idx.kv[e_lo:e_hi].cpu().long()
     uniq, inv = torch.unique(kv, return_inverse=True)
     ei = torch.stack([inv, rows])
     # the oracle (like the reference) indexes queries and kv rows in one node space: pad both to M rows
-    M = max(q_hi, uniq.numel())
+    M = max(r_hi - r_lo, uniq.numel())
 
     def padded(t):
         out = torch.zeros(M, *t.shape[1:], dtype=torch.float32)
         out[: t.shape[0]] = t.float().cpu()
         return out
 
-    qc, dc = padded(q[:q_hi]), padded(dout[:q_hi])
+    qc, dc = padded(q[r_lo:r_hi]), padded(dout[r_lo:r_hi])
     kc, vc = padded(k[uniq.to(k.device)]), padded(v[uniq.to(v.device)])
+    rate = cfg.get("dropout", 0.0)
+    keep = torch.rand(ei.shape[1], H, generator=torch.Generator().manual_seed(5)) >= rate if rate else None
+
+    def attention_step():
+        if not rate:
+            sa.attention_fwd_bwd_autograd(kc, qc, vc, ei, dc)
+            return
+        kk, qq, vv = (t.detach().requires_grad_(True) for t in (kc, qc, vc))
+        sa.gps_sparse_attention(qq, kk, vv, ei, keep, 1.0 / (1.0 - rate)).backward(dc)
+
     times = []
     t_all = time.perf_counter()
     while True:
         t0 = time.perf_counter()
-        sa.attention_fwd_bwd_autograd(kc, qc, vc, ei, dc)
+        attention_step()
         times.append(time.perf_counter() - t0)
         if time.perf_counter() - t_all > 12.0 or len(times) >= 3:
             break
-    attn_s = min(times) * scale
+    attn_s = min(times) * attn_scale
     nnz = idx.nnz
     a_fwd, a_bwd = attention_bytes(s_bytes, D, H, idx.n_q, idx.n_kv, nnz)
     # edge build of the same queries
     rowptr = g.rowptr.cpu().numpy()
     col = g.col.cpu().numpy()
-    u = philox.walk_uniforms(0, sample, cfg["P"], cfg["L"], 42)
-    t0 = time.perf_counter()
-    et.build_edge_table(rowptr, col, n, cfg["b_r"], cfg["b_w"], cfg["L"], cfg["P"], 42, u, q_lo=0, n_q=sample)
-    build_s = (time.perf_counter() - t0) * scale
-    what = "the full workload" if sample == n_rows else \
-        f"first {sample:,} of {n_rows:,} queries, time scaled x{scale:.2f} to the workload"
+    P, L = cfg["P"], cfg["L"]
+
+    def build(lo, cnt):
+        u = philox.walk_uniforms(lo, cnt, P, L, 42)
+        t0 = time.perf_counter()
+        et.build_edge_table(rowptr, col, n, cfg["b_r"], cfg["b_w"], L, P, 42, u, q_lo=lo, n_q=cnt)
+        return time.perf_counter() - t0
+
+    print(f"[bench] cpu baseline: edge build of queries {q0:,}..{q0 + sample - 1:,}", flush=True)
+    t_s = build(q0, sample)
+    if whole:
+        build_s = t_s
+        what = "the full workload"
+    else:
+        print("[bench] cpu baseline: edge build of one query (the fixed part)", flush=True)
+        t_1 = build(q0, 1)
+        per_query = max(t_s - t_1, 0.0) / max(sample - 1, 1)
+        build_s = t_1 + per_query * (n_rows - 1)
+        what = (f"queries {q0:,}..{q0 + sample - 1:,} of {n_rows:,} (the range whose mean in-degree is the "
+                f"workload's): attention {e_hi - e_lo:,} of {nnz:,} entries, time scaled x{attn_scale:.2f} by "
+                f"entries; edge build {t_s:.2f} s for the range = a fixed {t_1:.2f} s (a one-query build) + "
+                f"{per_query * 1e6:.1f} us per query, scaled to {n_rows:,} queries")
     print(f"[bench] cpu baseline: attn fwd+bwd {attn_s * 1e3:.1f} ms, edge build {build_s * 1e3:.1f} ms "
           f"({threads} threads; {what})", flush=True)
     return {
@@ -587,7 +628,7 @@ def cpu_baseline(cfg, g, tab, idx, q, k, v, dout, s_bytes, D, H):
         "cores": torch.get_num_threads(),
         "kind": "port",
         "sample": f"{cfg['name'].split(':')[0]}, {what}: attention fwd+bwd (torch CPU autograd, fp32, best "
-                  f"of {len(times)}) and the numpy edge build of those queries",
+                  f"of {len(times)}{', GPS form with a keep mask' if rate else ''}) and the numpy edge build",
         "attn_fwd_bwd_ms": round(attn_s * 1e3, 2),
         "edge_build_ms": round(build_s * 1e3, 2),
         "cpu_model": cpu_model(),
