@@ -76,14 +76,17 @@ __global__ __launch_bounds__(kThreads) void check_table_kernel(const int32_t* __
   if (threadIdx.x < 2 && blk[threadIdx.x]) atomicAdd(&bad[threadIdx.x], blk[threadIdx.x]);
 }
 
-// Writes entry pos (slot `slot` of query row `row`): kv, and when rkey is
-// given the entry's reverse-index sort key (id << kshift | row << sbits | slot):
-// a stable radix sort over the id bits alone then leaves each kv's entries in
-// (row, slot) order, which is CSR order.
+// Writes table entry pos (slot `slot` of query row `row`): kv, and when rkey
+// is given the entry's reverse-index sort key (id << kshift | row << sbits |
+// slot) at kidx: a stable radix sort over the id bits alone then leaves each
+// kv's entries in (row, slot) order, which is CSR order. With the Graphormer
+// token only the table's own entries get keys (kidx counts them in CSR order):
+// the token's entries (kv 0 of every row, the token row) have a fixed place in
+// the reverse index, which token_reverse_kernel writes.
 __device__ __forceinline__ void put_entry(int32_t* __restrict__ kv, uint64_t* __restrict__ rkey, int64_t pos,
-                                          int64_t row, int slot, int32_t id, int kshift, int sbits) {
+                                          int64_t kidx, int64_t row, int slot, int32_t id, int kshift, int sbits) {
   kv[pos] = id;
-  if (rkey) rkey[pos] = (uint64_t(uint32_t(id)) << kshift) | (uint64_t(row) << sbits) | uint64_t(slot);
+  if (rkey) rkey[kidx] = (uint64_t(uint32_t(id)) << kshift) | (uint64_t(row) << sbits) | uint64_t(slot);
 }
 
 // One thread per table slot, then (with the Graphormer token) one thread per
@@ -129,18 +132,21 @@ __global__ __launch_bounds__(kThreads) void table_fill_kernel(
       if (i >= total) continue;
       const int64_t t = i - slots;
       // the token row's entry for kv t+1 sits at position t: its key carries slot 0
-      if (lead && t < token_len) put_entry(kv, rkey, t, 0, 0, int32_t(t + 1), kshift, sbits);
-      if (t < n_rows && row_len[t] == 0) put_entry(kv, rkey, qptr[t + lead], t + lead, 0, 0, kshift, sbits);
+      if (lead && t < token_len) kv[t] = int32_t(t + 1);
+      if (t < n_rows && row_len[t] == 0) kv[qptr[t + lead]] = 0;
       continue;
     }
     const int c = col[u];
     if (c >= len[u]) continue;
     const int64_t r = row[u] + lead;
     if (token) {
-      if (c == 0) put_entry(kv, rkey, start[u], r, 0, 0, kshift, sbits);
-      put_entry(kv, rkey, start[u] + 1 + c, r, c + 1, val[u] + 1, kshift, sbits);
+      if (c == 0) kv[start[u]] = 0;
+      // the table's own entries before this one: start - token_len (the token row) - r + lead (one kv 0
+      // per attention row from lead on)
+      const int64_t kidx = start[u] - lead * token_len - (r - lead) + c;
+      put_entry(kv, rkey, start[u] + 1 + c, kidx, r, c + 1, val[u] + 1, kshift, sbits);
     } else {
-      put_entry(kv, rkey, start[u] + c, r, c, val[u], kshift, sbits);
+      put_entry(kv, rkey, start[u] + c, start[u] + c, r, c, val[u], kshift, sbits);
     }
   }
 }
@@ -211,21 +217,40 @@ __global__ void unpack_row_entry_kernel(const uint64_t* __restrict__ vals, int64
   ke[i] = int32_t(uint32_t(x));
 }
 
-// Sorted reverse-index keys -> kptr (boundaries of the id field), kq, and ke
-// when asked for. ke of a token-row entry (query 0 with the Graphormer token)
-// is id - 1, the position table_fill gave it; every other entry sits at
-// qptr[query] + slot.
-__device__ __forceinline__ int32_t entry_of(uint64_t x, int kshift, int sbits, int token,
-                                            const int64_t* __restrict__ qptr) {
+// The Graphormer token's part of a table's reverse index (tok = 1): kv 0 is
+// attended by every attention row from `lead` on, first in the row (c0 = n_q -
+// lead entries), and with a token row (lead = 1) kv t+1 (t < token_len) by row
+// 0 at position t. Their reverse entries need no sort: kv 0's segment is those
+// rows in order, and a token-row entry opens its kv's segment (row 0 comes
+// first). The table's own entries, sorted, follow them: sorted key i with id k
+// lands at c0 + lead * min(k, token_len) + i, and kv r >= 1 starts at
+// c0 + lead * min(r - 1, token_len) + (keys with id < r).
+struct TokenLayout {
+  int tok;
+  int lead;
+  int64_t token_len;
+  int64_t c0;
+  __device__ __forceinline__ int64_t key_slot(int64_t i, int64_t k) const {
+    return tok ? c0 + (lead ? (k < token_len ? k : token_len) : 0) + i : i;
+  }
+  __device__ __forceinline__ int64_t row_base(int64_t r) const {
+    if (!tok || r == 0) return 0;
+    return c0 + (lead ? (r - 1 < token_len ? r - 1 : token_len) : 0);
+  }
+};
+
+// A table entry's CSR position from its key: qptr[query] + slot.
+__device__ __forceinline__ int32_t entry_of(uint64_t x, int kshift, int sbits, const int64_t* __restrict__ qptr) {
   const int64_t q = int64_t((x >> sbits) & ((uint64_t(1) << (kshift - sbits)) - 1));
   const int64_t slot = int64_t(x & ((uint64_t(1) << sbits) - 1));
-  return int32_t(token && q == 0 ? int64_t(x >> kshift) - 1 : qptr[q] + slot);
+  return int32_t(qptr[q] + slot);
 }
 
 constexpr int kUnpackPerThread = 4;  // sorted keys per thread (kThreads apart), loaded before any store
 
+// Sorted keys -> kptr (boundaries of the id field), kq, and ke when asked for.
 __global__ __launch_bounds__(kThreads) void unpack_rkey_kernel(
-    const uint64_t* __restrict__ keys, int64_t nnz, int kshift, int sbits, int token,
+    const uint64_t* __restrict__ keys, int64_t n_keys, int kshift, int sbits, TokenLayout tl,
     const int64_t* __restrict__ qptr, int64_t n_kv, int64_t* __restrict__ kptr, int32_t* __restrict__ kq,
     int32_t* __restrict__ ke) {
   const int64_t base = int64_t(blockIdx.x) * (kThreads * kUnpackPerThread) + threadIdx.x;
@@ -233,28 +258,73 @@ __global__ __launch_bounds__(kThreads) void unpack_rkey_kernel(
 #pragma unroll
   for (int u = 0; u < kUnpackPerThread; ++u) {
     const int64_t i = base + int64_t(u) * kThreads;
-    cur[u] = i < nnz ? keys[i] : 0;
-    prev[u] = (i > 0 && i <= nnz) ? keys[i - 1] : 0;
+    cur[u] = i < n_keys ? keys[i] : 0;
+    prev[u] = (i > 0 && i <= n_keys) ? keys[i - 1] : 0;
   }
 #pragma unroll
   for (int u = 0; u < kUnpackPerThread; ++u) {
     const int64_t i = base + int64_t(u) * kThreads;
-    if (i > nnz) break;
-    int64_t r_here = i < nnz ? int64_t(cur[u] >> kshift) : n_kv;
-    int64_t r_prev = i > 0 ? int64_t(prev[u] >> kshift) : -1;
+    if (i > n_keys) break;
+    int64_t r_here = i < n_keys ? int64_t(cur[u] >> kshift) : n_kv;
+    // with the token the keys' ids start at 1 and kptr[0] = 0 (kv 0's segment opens the index)
+    int64_t r_prev = i > 0 ? int64_t(prev[u] >> kshift) : (tl.tok ? 0 : -1);
     if (r_here > n_kv) r_here = n_kv;
     if (r_prev > n_kv) r_prev = n_kv;
-    for (int64_t r = r_prev + 1; r <= r_here; ++r) kptr[r] = i;
-    if (i == nnz) break;
-    kq[i] = int32_t((cur[u] >> sbits) & ((uint64_t(1) << (kshift - sbits)) - 1));
-    if (ke) ke[i] = entry_of(cur[u], kshift, sbits, token, qptr);
+    if (i == 0 && tl.tok) kptr[0] = 0;
+    for (int64_t r = r_prev + 1; r <= r_here; ++r) kptr[r] = tl.row_base(r) + i;
+    if (i == n_keys) break;
+    const int64_t o = tl.key_slot(i, int64_t(cur[u] >> kshift));
+    kq[o] = int32_t((cur[u] >> sbits) & ((uint64_t(1) << (kshift - sbits)) - 1));
+    if (ke) ke[o] = entry_of(cur[u], kshift, sbits, qptr);
   }
 }
 
-__global__ void reverse_entries_kernel(const uint64_t* __restrict__ keys, int64_t nnz, int kshift, int sbits,
-                                       int token, const int64_t* __restrict__ qptr, int32_t* __restrict__ ke) {
+__global__ void reverse_entries_kernel(const uint64_t* __restrict__ keys, int64_t n_keys, int kshift, int sbits,
+                                       TokenLayout tl, const int64_t* __restrict__ qptr, int32_t* __restrict__ ke) {
   const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
-  if (i < nnz) ke[i] = entry_of(keys[i], kshift, sbits, token, qptr);
+  if (i < n_keys) {
+    const uint64_t x = keys[i];
+    ke[tl.key_slot(i, int64_t(x >> kshift))] = entry_of(x, kshift, sbits, qptr);
+  }
+}
+
+// The token's reverse entries (kq and/or ke; after kptr is written): thread j < c0 writes kv 0's entry of
+// row lead + j (CSR position qptr[lead + j]); thread t < token_len (with a token row) the token row's entry
+// of kv t + 1, first in that kv's segment (position t).
+__global__ void token_reverse_kernel(TokenLayout tl, const int64_t* __restrict__ qptr,
+                                     const int64_t* __restrict__ kptr, int32_t* __restrict__ kq,
+                                     int32_t* __restrict__ ke) {
+  const int64_t j = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (j < tl.c0) {
+    if (kq) kq[j] = int32_t(tl.lead + j);
+    if (ke) ke[j] = int32_t(qptr[tl.lead + j]);
+  }
+  if (tl.lead && j < tl.token_len) {
+    const int64_t o = kptr[j + 1];
+    if (kq) kq[o] = 0;
+    if (ke) ke[o] = int32_t(j);
+  }
+}
+
+inline TokenLayout token_layout(int global_token, int64_t token_row, int64_t n_q) {
+  TokenLayout tl{0, 0, 0, 0};
+  if (!global_token) return tl;
+  tl.tok = 1;
+  tl.lead = token_row >= 0 ? 1 : 0;
+  tl.token_len = tl.lead ? token_row : 0;
+  tl.c0 = n_q - tl.lead;
+  return tl;
+}
+
+inline int launch_token_reverse(const TokenLayout& tl, const int64_t* qptr, const int64_t* kptr, int32_t* kq,
+                                int32_t* ke, hipStream_t st) {
+  if (!tl.tok) return BF_OK;
+  const int64_t n = tl.c0 > tl.token_len ? tl.c0 : tl.token_len;
+  if (n == 0) return BF_OK;
+  BF_LAUNCH("token_reverse_kernel", token_reverse_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, st, tl, qptr,
+            kptr, kq, ke);
+  BF_CHECK_LAUNCH();
+  return BF_OK;
 }
 
 // Row order, longest first: bucket 255 - min(len, 255), counted per block in
@@ -641,15 +711,22 @@ extern "C" int bf_reverse_index_packed_workspace_size(int64_t nnz, size_t* bytes
 }
 
 extern "C" int bf_reverse_index_packed(const uint64_t* rkey, const int64_t* qptr, int64_t nnz, int64_t n_q,
-                                       int64_t n_kv, int32_t q_bits, int32_t slot_bits, int32_t token_row,
-                                       uint64_t* sorted, int64_t* kptr, int32_t* kq, int32_t* ke, void* workspace,
-                                       size_t workspace_bytes, void* stream) {
+                                       int64_t n_kv, int32_t q_bits, int32_t slot_bits, int32_t global_token,
+                                       int64_t token_row, uint64_t* sorted, int64_t* kptr, int32_t* kq, int32_t* ke,
+                                       void* workspace, size_t workspace_bytes, void* stream) {
   BF_CHECK_ARG(kptr && qptr && n_q >= 0 && n_kv >= 0 && nnz >= 0, "reverse_index_packed: bad arguments");
   BF_CHECK_ARG(nnz < (int64_t(1) << 31), "reverse_index_packed: sizes must fit int32");
   const int kshift = q_bits + slot_bits;
   const int id_bits = bits_for(uint64_t(n_kv > 0 ? n_kv : 1));
   BF_CHECK_ARG(q_bits >= bits_for(uint64_t(n_q)) && slot_bits >= 1 && kshift + id_bits <= 64,
                "reverse_index_packed: key fields (%d + %d + %d bits) do not fit", q_bits, slot_bits, id_bits);
+  const TokenLayout tl = token_layout(global_token != 0, token_row, n_q);
+  BF_CHECK_ARG(!tl.tok || (tl.c0 >= 0 && tl.token_len < n_kv), "reverse_index_packed: token layout does not fit "
+               "(%lld queries, token row of %lld entries, %lld kv rows)", (long long)n_q, (long long)tl.token_len,
+               (long long)n_kv);
+  const int64_t n_keys = nnz - (tl.tok ? tl.c0 + tl.token_len : 0);
+  BF_CHECK_ARG(n_keys >= 0, "reverse_index_packed: %lld entries cannot hold the token's %lld", (long long)nnz,
+               (long long)(tl.c0 + tl.token_len));
   size_t need = 0;
   bf_reverse_index_packed_workspace_size(nnz, &need);
   BF_CHECK_ARG(workspace && workspace_bytes >= need, "reverse_index_packed: workspace %zu < %zu bytes",
@@ -659,29 +736,38 @@ extern "C" int bf_reverse_index_packed(const uint64_t* rkey, const int64_t* qptr
     BF_CHECK_HIP(hipMemsetAsync(kptr, 0, size_t(n_kv + 1) * sizeof(int64_t), st));
     return BF_OK;
   }
-  BF_CHECK_ARG(rkey && sorted && kq, "reverse_index_packed: null tensor");
-  size_t tb = workspace_bytes;
-  // only the id bits are sorted; the stable passes keep each id's entries in CSR order
-  BF_CHECK_HIP(prim::sort_keys(workspace, tb, rkey, sorted, nnz, kshift, kshift + id_bits, st));
+  BF_CHECK_ARG(kq && (n_keys == 0 || (rkey && sorted)), "reverse_index_packed: null tensor");
+  if (n_keys > 0) {
+    size_t tb = workspace_bytes;
+    // only the id bits are sorted; the stable passes keep each id's entries in CSR order
+    BF_CHECK_HIP(prim::sort_keys(workspace, tb, rkey, sorted, n_keys, kshift, kshift + id_bits, st));
+  }
   BF_LAUNCH("unpack_rkey_kernel", unpack_rkey_kernel,
-            dim3(unsigned(ceil_div(nnz + 1, int64_t(kThreads) * kUnpackPerThread))), dim3(kThreads), 0, st, sorted, nnz,
-            kshift, slot_bits, int(token_row != 0), qptr, n_kv, kptr, kq, ke);
+            dim3(unsigned(ceil_div(n_keys + 1, int64_t(kThreads) * kUnpackPerThread))), dim3(kThreads), 0, st, sorted,
+            n_keys, kshift, slot_bits, tl, qptr, n_kv, kptr, kq, ke);
   BF_CHECK_LAUNCH();
-  return BF_OK;
+  return launch_token_reverse(tl, qptr, kptr, kq, ke, st);
 }
 
-extern "C" int bf_reverse_entries(const uint64_t* sorted, const int64_t* qptr, int64_t nnz, int64_t n_q,
-                                  int32_t q_bits, int32_t slot_bits, int32_t token_row, int32_t* ke,
-                                  void* stream) {
-  BF_CHECK_ARG(qptr && nnz >= 0 && nnz < (int64_t(1) << 31) && n_q >= 0, "reverse_entries: bad arguments");
+extern "C" int bf_reverse_entries(const uint64_t* sorted, const int64_t* qptr, const int64_t* kptr, int64_t nnz,
+                                  int64_t n_q, int32_t q_bits, int32_t slot_bits, int32_t global_token,
+                                  int64_t token_row, int32_t* ke, void* stream) {
+  BF_CHECK_ARG(qptr && kptr && nnz >= 0 && nnz < (int64_t(1) << 31) && n_q >= 0, "reverse_entries: bad arguments");
   BF_CHECK_ARG(q_bits >= bits_for(uint64_t(n_q)) && slot_bits >= 1 && q_bits + slot_bits <= 33,
                "reverse_entries: bad key fields (%d + %d bits)", q_bits, slot_bits);
+  const TokenLayout tl = token_layout(global_token != 0, token_row, n_q);
+  const int64_t n_keys = nnz - (tl.tok ? tl.c0 + tl.token_len : 0);
+  BF_CHECK_ARG(n_keys >= 0, "reverse_entries: %lld entries cannot hold the token's %lld", (long long)nnz,
+               (long long)(tl.c0 + tl.token_len));
   if (nnz == 0) return BF_OK;
-  BF_CHECK_ARG(sorted && ke, "reverse_entries: null tensor");
-  BF_LAUNCH("reverse_entries_kernel", reverse_entries_kernel, dim3(blocks_for(nnz)), dim3(kThreads), 0,
-            as_stream(stream), sorted, nnz, q_bits + slot_bits, slot_bits, int(token_row != 0), qptr, ke);
-  BF_CHECK_LAUNCH();
-  return BF_OK;
+  BF_CHECK_ARG(ke && (n_keys == 0 || sorted), "reverse_entries: null tensor");
+  hipStream_t st = as_stream(stream);
+  if (n_keys > 0) {
+    BF_LAUNCH("reverse_entries_kernel", reverse_entries_kernel, dim3(blocks_for(n_keys)), dim3(kThreads), 0, st,
+              sorted, n_keys, q_bits + slot_bits, slot_bits, tl, qptr, ke);
+    BF_CHECK_LAUNCH();
+  }
+  return launch_token_reverse(tl, qptr, kptr, nullptr, ke, st);
 }
 
 extern "C" int bf_expand_rows(const int64_t* ptr, int64_t n_rows, int64_t nnz, int64_t* rows, void* stream) {

@@ -355,11 +355,13 @@ def _bits_for(maxval: int) -> int:
 
 @dataclass
 class ReverseKeys:
-    """table_to_csr's per-entry reverse-index sort keys: id << (q_bits + slot_bits) | query << slot_bits | slot."""
-    keys: torch.Tensor          # uint64 as int64 [nnz]
+    """table_to_csr's reverse-index sort keys, id << (q_bits + slot_bits) | query << slot_bits | slot, one per
+    table entry (with the Graphormer token its own entries get none: their reverse places are fixed)."""
+    keys: torch.Tensor          # uint64 as int64 [table entries]
     q_bits: int
     slot_bits: int
-    token_row: bool             # attention row 0 is the Graphormer token row
+    global_token: bool
+    token_row: int              # as in table_to_csr: the token row's length, or -1 for none
 
 
 def _token_row(n_rows: int, global_token: bool, token_row: Optional[int]) -> int:
@@ -421,8 +423,10 @@ def table_to_csr(table: torch.Tensor, row_len: torch.Tensor, global_token: bool 
     rk = None
     q_bits, slot_bits = _bits_for(n_q), _bits_for(width)
     if with_keys and q_bits + slot_bits <= 33:
-        rk = ReverseKeys(torch.empty(max(nnz, 1), dtype=torch.int64, device=dev)[:nnz], q_bits,
-                         slot_bits, tr >= 0)
+        # the token's entries (kv 0 of every table row, the token row) get no key
+        n_keys = nnz - ((n_rows + max(tr, 0)) if global_token else 0)
+        rk = ReverseKeys(torch.empty(max(n_keys, 1), dtype=torch.int64, device=dev)[:n_keys], q_bits,
+                         slot_bits, bool(global_token), tr)
     N.call("bf_table_to_csr", _p(table), _p(row_len), n_rows, width, int(global_token), tr, _p(qptr), _p(kv),
            _p(rk.keys) if rk is not None else None, q_bits, slot_bits, _stream(dev))
     return (qptr, kv, rk) if with_keys else (qptr, kv)
@@ -470,32 +474,35 @@ def reverse_index(qptr: torch.Tensor, kv: torch.Tensor, n_kv: int):
 def reverse_index_packed(rk: ReverseKeys, qptr: torch.Tensor, n_kv: int, entries: bool = True):
     """reverse_index from table_to_csr's sort keys (one sort of the id bits, no row recovery):
     (kptr, kq, ke, sorted). ``entries=False`` skips ke (a gather of qptr that only a bias or factor
-    needs; ``reverse_entries(sorted, qptr)`` gives it later) and returns ke = None."""
+    needs; ``reverse_entries(sorted, qptr, kptr)`` gives it later) and returns ke = None."""
     dev = qptr.device
     _require(qptr, "qptr", torch.int64)
     _require(rk.keys, "keys", torch.int64, dev)
-    nnz = rk.keys.numel()
+    n_keys = rk.keys.numel()
+    nnz = n_keys + ((qptr.numel() - 1 - (1 if rk.token_row >= 0 else 0)) + max(rk.token_row, 0)
+                    if rk.global_token else 0)
     ws = _workspace(_size_query("bf_reverse_index_packed_workspace_size", nnz), dev)
-    srt = ReverseKeys(torch.empty(max(nnz, 1), dtype=torch.int64, device=dev)[:nnz], rk.q_bits, rk.slot_bits,
-                      rk.token_row)
+    srt = ReverseKeys(torch.empty(max(n_keys, 1), dtype=torch.int64, device=dev)[:n_keys], rk.q_bits, rk.slot_bits,
+                      rk.global_token, rk.token_row)
     kptr = torch.empty(n_kv + 1, dtype=torch.int64, device=dev)
     kq = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)[:nnz]
     ke = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)[:nnz] if entries else None
     N.call("bf_reverse_index_packed", _p(rk.keys), _p(qptr), nnz, qptr.numel() - 1, n_kv, rk.q_bits, rk.slot_bits,
-           int(rk.token_row), _p(srt.keys), _p(kptr), _p(kq), _p(ke) if entries else None, _p(ws), ws.numel(),
-           _stream(dev))
+           int(rk.global_token), int(rk.token_row), _p(srt.keys), _p(kptr), _p(kq), _p(ke) if entries else None,
+           _p(ws), ws.numel(), _stream(dev))
     return kptr, kq, ke, srt
 
 
-def reverse_entries(srt: ReverseKeys, qptr: torch.Tensor) -> torch.Tensor:
-    """ke (CSR position per reverse entry, int32) from reverse_index_packed's sorted keys."""
+def reverse_entries(srt: ReverseKeys, qptr: torch.Tensor, kptr: torch.Tensor) -> torch.Tensor:
+    """ke (CSR position per reverse entry, int32) from reverse_index_packed's sorted keys and kptr."""
     dev = qptr.device
     _require(qptr, "qptr", torch.int64)
+    _require(kptr, "kptr", torch.int64, dev)
     _require(srt.keys, "keys", torch.int64, dev)
-    nnz = srt.keys.numel()
+    nnz = int(kptr[-1].item()) if kptr.numel() else 0
     ke = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)[:nnz]
-    N.call("bf_reverse_entries", _p(srt.keys), _p(qptr), nnz, qptr.numel() - 1, srt.q_bits, srt.slot_bits,
-           int(srt.token_row), _p(ke), _stream(dev))
+    N.call("bf_reverse_entries", _p(srt.keys), _p(qptr), _p(kptr), nnz, qptr.numel() - 1, srt.q_bits, srt.slot_bits,
+           int(srt.global_token), int(srt.token_row), _p(ke), _stream(dev))
     return ke
 
 
@@ -794,7 +801,7 @@ class AttentionIndex:
         """The CSR position of every reverse entry (ke), which the dk/dv pass reads only with a bias or factor."""
         self.ensure_backward()
         if self.ke is None and self.nnz:
-            self.ke = reverse_entries(self._sorted, self.qptr)
+            self.ke = reverse_entries(self._sorted, self.qptr, self.kptr)
             self._sorted = None
         return self
 

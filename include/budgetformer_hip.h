@@ -258,9 +258,11 @@ int bf_chung_lu(int64_t num_nodes, int64_t pairs, double exponent, double i0, do
  * nnz = qptr[n_q] on the host (it synchronises the stream, so the caller can
  * size kv; with nnz_host NULL it only enqueues the scan and the caller reads
  * qptr[n_q] when it needs it); bf_table_to_csr then fills kv, and, when rkey is not NULL,
- * rkey uint64 [nnz] = (id << (q_bits + slot_bits) | query << slot_bits | slot)
- * per entry, the sort keys bf_reverse_index_packed takes (slot = position in
- * the query's row; the token row's entries carry slot 0). Needs
+ * rkey uint64 = (id << (q_bits + slot_bits) | query << slot_bits | slot) for
+ * each of the table's own entries in CSR order (slot = position in the query's
+ * row), the sort keys bf_reverse_index_packed takes: [nnz] without the token,
+ * [sum of row_len] with it (the token's entries, kv 0 of every row and the
+ * token row, have a fixed place in the reverse index and get no key). Needs
  * q_bits >= bits of n_q, slot_bits >= bits of width and q_bits + slot_bits
  * <= 33 (BF_ERR_INVALID otherwise). Workspace: bf_scan_workspace_size(n_q). */
 int bf_scan_workspace_size(int64_t n, size_t* bytes);
@@ -311,21 +313,25 @@ int bf_reverse_index(const int64_t* qptr, const int32_t* kv, int64_t n_q, int64_
 
 /* bf_reverse_index from bf_table_to_csr's sort keys: one radix sort of the
  * 8-byte keys over their id bits only (stable, so each id's entries stay in
- * CSR order) into sorted uint64 [nnz], then one pass that writes kptr and
- * decodes kq. ke (may be NULL) is decoded in the same pass: qptr[query] +
- * slot, id - 1 for the token row when token_row != 0 (attention row 0 is the
- * Graphormer token row, bf_table_to_csr with token_row >= 0); it is a random gather of
- * qptr, which the dk/dv pass needs only with a bias or factor, so a caller may
- * keep `sorted` and call bf_reverse_entries later instead. Same kptr / kq /
- * ke as bf_reverse_index. Workspace: bf_reverse_index_packed_workspace_size. */
+ * CSR order) into sorted uint64 [keys], then one pass that writes kptr and
+ * decodes kq. (global_token, token_row) as given to bf_table_to_csr: the
+ * token's entries, which have no key, take their fixed places (kv 0's segment
+ * first, row by row; each token-row entry first in its kv's segment), the
+ * sorted keys the rest. nnz counts every entry. ke (may be NULL) is decoded in
+ * the same pass: qptr[query] + slot; it is a random gather of qptr, which the
+ * dk/dv pass needs only with a bias, factor or dropout, so a caller may keep
+ * `sorted` and call bf_reverse_entries (with the kptr written here) later
+ * instead. Same kptr / kq / ke as bf_reverse_index.
+ * Workspace: bf_reverse_index_packed_workspace_size(nnz).                   */
 int bf_reverse_index_packed_workspace_size(int64_t nnz, size_t* bytes);
 int bf_reverse_index_packed(const uint64_t* rkey, const int64_t* qptr, int64_t nnz, int64_t n_q, int64_t n_kv,
-                            int32_t q_bits, int32_t slot_bits, int32_t token_row, uint64_t* sorted,
-                            int64_t* kptr, int32_t* kq, int32_t* ke, void* workspace, size_t workspace_bytes,
-                            void* stream);
-/* ke [nnz] from bf_reverse_index_packed's sorted keys.                       */
-int bf_reverse_entries(const uint64_t* sorted, const int64_t* qptr, int64_t nnz, int64_t n_q, int32_t q_bits,
-                       int32_t slot_bits, int32_t token_row, int32_t* ke, void* stream);
+                            int32_t q_bits, int32_t slot_bits, int32_t global_token, int64_t token_row,
+                            uint64_t* sorted, int64_t* kptr, int32_t* kq, int32_t* ke, void* workspace,
+                            size_t workspace_bytes, void* stream);
+/* ke [nnz] from bf_reverse_index_packed's sorted keys and kptr.              */
+int bf_reverse_entries(const uint64_t* sorted, const int64_t* qptr, const int64_t* kptr, int64_t nnz, int64_t n_q,
+                       int32_t q_bits, int32_t slot_bits, int32_t global_token, int64_t token_row, int32_t* ke,
+                       void* stream);
 
 /* Row id of every entry of a CSR (rows[i] = r for ptr[r] <= i < ptr[r+1]). */
 int bf_expand_rows(const int64_t* ptr, int64_t n_rows, int64_t nnz, int64_t* rows, void* stream);

@@ -347,47 +347,53 @@ def test_from_table_rejects_invalid_tables(hip_device, token):
         ops.table_to_csr(bad, row_len, token, tr, n)
 
 
-@pytest.mark.parametrize("token", [False, True])
-def test_index_formats_against_numpy(hip_device, token):
-    """table -> CSR (with the fused token fill), both reverse-index routes, the split plan and the row order."""
+@pytest.mark.parametrize("token,token_row", [(False, None), (True, None), (True, -1), (True, 5400), (True, 3)])
+def test_index_formats_against_numpy(hip_device, token, token_row):
+    """table -> CSR (with the fused token fill), both reverse-index routes, the split plan and the row order.
+    With the token: the full query set (token row of n entries), a query shard without the token row (-1),
+    and token rows longer and shorter than the table (a shard starting at node 0 of a larger graph, and
+    one whose kv ids stop short of the table's)."""
     from budgetformer_amd import hip_ops
-    rng = np.random.default_rng(11 + token)
+    rng = np.random.default_rng(11 + token + (token_row or 0))
     n, width = 5000, 6
     row_len = rng.integers(0, width + 1, n).astype(np.int32)
     table = np.full((n, width), -1, dtype=np.int32)
     for r in range(n):
         table[r, :row_len[r]] = np.sort(rng.choice(n // 3 if r % 7 else 40, row_len[r], replace=False))
     t, rl = torch.from_numpy(table).to(hip_device), torch.from_numpy(row_len).to(hip_device)
-    qptr, kv, rk = hip_ops.table_to_csr(t, rl, token, with_keys=True)
+    qptr, kv, rk = hip_ops.table_to_csr(t, rl, token, with_keys=True, token_row=token_row)
+    tr = (n if token_row is None else token_row) if token else -1
     # numpy CSR of the same table
     rows, vals = [], []
-    if token:
-        rows += [0] * n
-        vals += list(range(1, n + 1))
+    if tr >= 0:
+        rows += [0] * tr
+        vals += list(range(1, tr + 1))
+    lead = 1 if tr >= 0 else 0
     for r in range(n):
-        q = r + 1 if token else r
         ids = ([0] if token else []) + [int(x) + (1 if token else 0) for x in table[r, :row_len[r]]]
-        rows += [q] * len(ids)
+        rows += [r + lead] * len(ids)
         vals += ids
-    n_q = n + (1 if token else 0)
+    n_q = n + lead
+    n_kv = max(n_q, tr + 1)
     assert np.array_equal(kv.cpu().numpy(), np.array(vals, dtype=np.int32))
     assert np.array_equal(np.diff(qptr.cpu().numpy()), np.bincount(np.array(rows), minlength=n_q))
     pos = np.arange(len(vals))
-    # sort keys: id << (q_bits + slot_bits) | query << slot_bits | slot (token-row entries: slot 0)
+    # sort keys: id << (q_bits + slot_bits) | query << slot_bits | slot, in CSR order, for the table's own
+    # entries only (with the token, kv 0 of every row and the token row have fixed reverse places)
     rows_a = np.array(rows, dtype=np.int64)
     slot = pos - qptr.cpu().numpy()[rows_a]
-    if token:
-        slot[rows_a == 0] = 0
     expect = (np.array(vals, dtype=np.int64) << (rk.q_bits + rk.slot_bits)) | (rows_a << rk.slot_bits) | slot
+    if token:
+        expect = expect[(rows_a >= lead) & (np.array(vals) != 0)]
     assert (rk.q_bits, rk.slot_bits) == (int(n_q).bit_length(), int(width).bit_length())
     assert np.array_equal(rk.keys.cpu().numpy(), expect)
-    a = hip_ops.reverse_index(qptr, kv, n_q)
-    b = hip_ops.reverse_index_packed(rk, qptr, n_q)
+    a = hip_ops.reverse_index(qptr, kv, n_kv)
+    b = hip_ops.reverse_index_packed(rk, qptr, n_kv)
     for x, y in zip(a, b[:3]):
         assert torch.equal(x, y)
-    lazy = hip_ops.reverse_index_packed(rk, qptr, n_q, entries=False)
+    lazy = hip_ops.reverse_index_packed(rk, qptr, n_kv, entries=False)
     assert lazy[2] is None and torch.equal(lazy[0], a[0]) and torch.equal(lazy[1], a[1])
-    assert torch.equal(hip_ops.reverse_entries(lazy[3], qptr), a[2])
+    assert torch.equal(hip_ops.reverse_entries(lazy[3], qptr, lazy[0]), a[2])
     order = np.lexsort((pos, np.array(vals)))                    # (kv, position) order
     assert np.array_equal(b[1].cpu().numpy(), np.array(rows)[order]) and np.array_equal(b[2].cpu().numpy(), order)
     # row order: a permutation, capped lengths non-increasing
@@ -395,7 +401,7 @@ def test_index_formats_against_numpy(hip_device, token):
     ro, sp = ro.cpu().numpy(), sp.cpu().numpy().astype(np.uint64)
     kp = b[0].cpu().numpy()
     lens = np.minimum(np.diff(kp), 255)
-    assert np.array_equal(np.sort(ro), np.arange(n_q)) and (np.diff(lens[ro]) <= 0).all()
+    assert np.array_equal(np.sort(ro), np.arange(n_kv)) and (np.diff(lens[ro]) <= 0).all()
     # spans: each slot's row as (begin << 32 | length)
     assert np.array_equal(sp >> np.uint64(32), kp[ro].astype(np.uint64))
     assert np.array_equal(sp & np.uint64(0xFFFFFFFF), (kp[ro + 1] - kp[ro]).astype(np.uint64))
@@ -405,9 +411,9 @@ def test_index_formats_against_numpy(hip_device, token):
     heavy = np.nonzero(L > 4)[0]
     assert plan.heavy == heavy.size and np.array_equal(plan.heavy_rows[:plan.heavy].cpu().numpy(), heavy)
     nit = np.where(L > 4, np.minimum(-(-L // 5), 160), 0)              # BF_MAX_ITEMS_PER_ROW = 160
-    assert plan.items == nit.sum() and np.array_equal(plan.nitems[:n_q].cpu().numpy(), nit)
-    assert np.array_equal(plan.item_off[:n_q].cpu().numpy(), np.concatenate([[0], np.cumsum(nit)[:-1]]))
-    assert np.array_equal(plan.item_row[:plan.items].cpu().numpy(), np.repeat(np.arange(n_q), nit))
+    assert plan.items == nit.sum() and np.array_equal(plan.nitems[:n_kv].cpu().numpy(), nit)
+    assert np.array_equal(plan.item_off[:n_kv].cpu().numpy(), np.concatenate([[0], np.cumsum(nit)[:-1]]))
+    assert np.array_equal(plan.item_row[:plan.items].cpu().numpy(), np.repeat(np.arange(n_kv), nit))
 
 
 @pytest.mark.parametrize("n_rows,chunk,item", [(3000, 128, 768), (1000, 16, 7), (50, 128, 768)])
@@ -459,10 +465,10 @@ def test_plan_from_the_row_order_equals_the_generic_plan(hip_device, chunk, item
     assert np.array_equal(plan.item_row[:plan.items].cpu().numpy(), np.repeat(heavy, nit[heavy]))
 
 
-@pytest.mark.parametrize("n,width,lo", [(120_000, 12, 8), (600_000, 4, 2)])
-def test_packed_reverse_index_past_1m_entries(hip_device, n, width, lo):
-    """Past 1M entries the sorts run as onesweep radix passes instead of a merge sort, the packed reverse
-    index over only its 17 or 20 kv-id bits. The result must equal the pair-sort route and numpy's stable
+@pytest.mark.parametrize("n,width,lo", [(120_000, 12, 8), (600_000, 4, 2), (40_000, 8, 2)])
+def test_packed_reverse_index_onesweep_sizes(hip_device, n, width, lo):
+    """Past 64K keys the sorts run as onesweep radix passes instead of a merge sort, the packed reverse
+    index over only its 16 to 20 kv-id bits. The result must equal the pair-sort route and numpy's stable
     order."""
     from budgetformer_amd import hip_ops
     rng = np.random.default_rng(n)
@@ -470,7 +476,7 @@ def test_packed_reverse_index_past_1m_entries(hip_device, n, width, lo):
     base = rng.integers(0, n, n)
     table = ((base[:, None] + np.arange(width)[None, :] * 104729) % n).astype(np.int32)   # distinct per row
     table[np.arange(width)[None, :] >= row_len[:, None]] = -1
-    assert row_len.sum() > 1_000_000
+    assert row_len.sum() > 65_536
     t, rl = torch.from_numpy(table).to(hip_device), torch.from_numpy(row_len).to(hip_device)
     qptr, kv, rk = hip_ops.table_to_csr(t, rl, False, with_keys=True)
     a = hip_ops.reverse_index(qptr, kv, n)
