@@ -89,7 +89,7 @@ _SIGS = {
     "bf_reverse_index_packed_workspace_size": (C.c_int, [i64, C.POINTER(sz)]),
     "bf_reverse_index_packed": (C.c_int, [vp, P_i64, i64, i64, i64, i32, i32, i32, i64, vp, P_i64, P_i32, P_i32,
                                           vp, sz, vp]),
-    "bf_reverse_entries": (C.c_int, [vp, P_i64, P_i64, i64, i64, i32, i32, i32, i64, P_i32, vp]),
+    "bf_reverse_entries": (C.c_int, [vp, P_i64, i64, i64, i32, i32, i32, i64, P_i32, vp]),
     "bf_expand_rows": (C.c_int, [P_i64, i64, i64, P_i64, vp]),
     "bf_split_item_capacity": (i64, [i64, i32, i32]),
     "bf_split_row_capacity": (i64, [i64, i32]),

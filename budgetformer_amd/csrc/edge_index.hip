@@ -224,7 +224,9 @@ __global__ void unpack_row_entry_kernel(const uint64_t* __restrict__ vals, int64
 // rows in order, and a token-row entry opens its kv's segment (row 0 comes
 // first). The table's own entries, sorted, follow them: sorted key i with id k
 // lands at c0 + lead * min(k, token_len) + i, and kv r >= 1 starts at
-// c0 + lead * min(r - 1, token_len) + (keys with id < r).
+// c0 + lead * min(r - 1, token_len) + (keys with id < r). The kernels that
+// write kv r's start (the sorted keys' boundaries) also write its token-row
+// entry there, beside the keys' own entries; kv 0's segment is written apart.
 struct TokenLayout {
   int tok;
   int lead;
@@ -237,6 +239,8 @@ struct TokenLayout {
     if (!tok || r == 0) return 0;
     return c0 + (lead ? (r - 1 < token_len ? r - 1 : token_len) : 0);
   }
+  // kv r opens with the token row's entry (CSR position r - 1)
+  __device__ __forceinline__ bool token_entry(int64_t r) const { return lead && r >= 1 && r - 1 < token_len; }
 };
 
 // A table entry's CSR position from its key: qptr[query] + slot.
@@ -271,7 +275,14 @@ __global__ __launch_bounds__(kThreads) void unpack_rkey_kernel(
     if (r_here > n_kv) r_here = n_kv;
     if (r_prev > n_kv) r_prev = n_kv;
     if (i == 0 && tl.tok) kptr[0] = 0;
-    for (int64_t r = r_prev + 1; r <= r_here; ++r) kptr[r] = tl.row_base(r) + i;
+    for (int64_t r = r_prev + 1; r <= r_here; ++r) {
+      const int64_t b = tl.row_base(r) + i;
+      kptr[r] = b;
+      if (r < n_kv && tl.token_entry(r)) {
+        kq[b] = 0;
+        if (ke) ke[b] = int32_t(r - 1);
+      }
+    }
     if (i == n_keys) break;
     const int64_t o = tl.key_slot(i, int64_t(cur[u] >> kshift));
     kq[o] = int32_t((cur[u] >> sbits) & ((uint64_t(1) << (kshift - sbits)) - 1));
@@ -279,30 +290,33 @@ __global__ __launch_bounds__(kThreads) void unpack_rkey_kernel(
   }
 }
 
+// ke from the sorted keys (one thread per key, plus one past the end): with
+// the token row, the thread that meets the first key with id >= r (or the
+// end) also writes kv r's token-row entry (r <= token_len), at kv r's start.
 __global__ void reverse_entries_kernel(const uint64_t* __restrict__ keys, int64_t n_keys, int kshift, int sbits,
                                        TokenLayout tl, const int64_t* __restrict__ qptr, int32_t* __restrict__ ke) {
   const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
-  if (i < n_keys) {
-    const uint64_t x = keys[i];
-    ke[tl.key_slot(i, int64_t(x >> kshift))] = entry_of(x, kshift, sbits, qptr);
+  if (i > n_keys) return;
+  const uint64_t x = i < n_keys ? keys[i] : 0;
+  if (tl.lead) {
+    const int64_t top = tl.token_len;    // the last kv row with a token-row entry
+    int64_t r_here = i < n_keys ? int64_t(x >> kshift) : top;
+    int64_t r_prev = i > 0 ? int64_t(keys[i - 1] >> kshift) : 0;
+    if (r_here > top) r_here = top;
+    if (r_prev > top) r_prev = top;
+    for (int64_t r = r_prev + 1; r <= r_here; ++r) ke[tl.row_base(r) + i] = int32_t(r - 1);
   }
+  if (i < n_keys) ke[tl.key_slot(i, int64_t(x >> kshift))] = entry_of(x, kshift, sbits, qptr);
 }
 
-// The token's reverse entries (kq and/or ke; after kptr is written): thread j < c0 writes kv 0's entry of
-// row lead + j (CSR position qptr[lead + j]); thread t < token_len (with a token row) the token row's entry
-// of kv t + 1, first in that kv's segment (position t).
-__global__ void token_reverse_kernel(TokenLayout tl, const int64_t* __restrict__ qptr,
-                                     const int64_t* __restrict__ kptr, int32_t* __restrict__ kq,
+// kv 0's reverse segment with the token (kq and/or ke): thread j < c0 writes the entry of attention row
+// lead + j, first in that row (CSR position qptr[lead + j]).
+__global__ void token_reverse_kernel(TokenLayout tl, const int64_t* __restrict__ qptr, int32_t* __restrict__ kq,
                                      int32_t* __restrict__ ke) {
   const int64_t j = int64_t(blockIdx.x) * kThreads + threadIdx.x;
   if (j < tl.c0) {
     if (kq) kq[j] = int32_t(tl.lead + j);
     if (ke) ke[j] = int32_t(qptr[tl.lead + j]);
-  }
-  if (tl.lead && j < tl.token_len) {
-    const int64_t o = kptr[j + 1];
-    if (kq) kq[o] = 0;
-    if (ke) ke[o] = int32_t(j);
   }
 }
 
@@ -316,13 +330,11 @@ inline TokenLayout token_layout(int global_token, int64_t token_row, int64_t n_q
   return tl;
 }
 
-inline int launch_token_reverse(const TokenLayout& tl, const int64_t* qptr, const int64_t* kptr, int32_t* kq,
-                                int32_t* ke, hipStream_t st) {
-  if (!tl.tok) return BF_OK;
-  const int64_t n = tl.c0 > tl.token_len ? tl.c0 : tl.token_len;
-  if (n == 0) return BF_OK;
-  BF_LAUNCH("token_reverse_kernel", token_reverse_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, st, tl, qptr,
-            kptr, kq, ke);
+inline int launch_token_reverse(const TokenLayout& tl, const int64_t* qptr, int32_t* kq, int32_t* ke,
+                                hipStream_t st) {
+  if (!tl.tok || tl.c0 == 0) return BF_OK;
+  BF_LAUNCH("token_reverse_kernel", token_reverse_kernel, dim3(blocks_for(tl.c0)), dim3(kThreads), 0, st, tl, qptr,
+            kq, ke);
   BF_CHECK_LAUNCH();
   return BF_OK;
 }
@@ -746,13 +758,13 @@ extern "C" int bf_reverse_index_packed(const uint64_t* rkey, const int64_t* qptr
             dim3(unsigned(ceil_div(n_keys + 1, int64_t(kThreads) * kUnpackPerThread))), dim3(kThreads), 0, st, sorted,
             n_keys, kshift, slot_bits, tl, qptr, n_kv, kptr, kq, ke);
   BF_CHECK_LAUNCH();
-  return launch_token_reverse(tl, qptr, kptr, kq, ke, st);
+  return launch_token_reverse(tl, qptr, kq, ke, st);
 }
 
-extern "C" int bf_reverse_entries(const uint64_t* sorted, const int64_t* qptr, const int64_t* kptr, int64_t nnz,
-                                  int64_t n_q, int32_t q_bits, int32_t slot_bits, int32_t global_token,
-                                  int64_t token_row, int32_t* ke, void* stream) {
-  BF_CHECK_ARG(qptr && kptr && nnz >= 0 && nnz < (int64_t(1) << 31) && n_q >= 0, "reverse_entries: bad arguments");
+extern "C" int bf_reverse_entries(const uint64_t* sorted, const int64_t* qptr, int64_t nnz, int64_t n_q,
+                                  int32_t q_bits, int32_t slot_bits, int32_t global_token, int64_t token_row,
+                                  int32_t* ke, void* stream) {
+  BF_CHECK_ARG(qptr && nnz >= 0 && nnz < (int64_t(1) << 31) && n_q >= 0, "reverse_entries: bad arguments");
   BF_CHECK_ARG(q_bits >= bits_for(uint64_t(n_q)) && slot_bits >= 1 && q_bits + slot_bits <= 33,
                "reverse_entries: bad key fields (%d + %d bits)", q_bits, slot_bits);
   const TokenLayout tl = token_layout(global_token != 0, token_row, n_q);
@@ -762,12 +774,12 @@ extern "C" int bf_reverse_entries(const uint64_t* sorted, const int64_t* qptr, c
   if (nnz == 0) return BF_OK;
   BF_CHECK_ARG(ke && (n_keys == 0 || sorted), "reverse_entries: null tensor");
   hipStream_t st = as_stream(stream);
-  if (n_keys > 0) {
-    BF_LAUNCH("reverse_entries_kernel", reverse_entries_kernel, dim3(blocks_for(n_keys)), dim3(kThreads), 0, st,
+  if (n_keys > 0 || tl.lead) {
+    BF_LAUNCH("reverse_entries_kernel", reverse_entries_kernel, dim3(blocks_for(n_keys + 1)), dim3(kThreads), 0, st,
               sorted, n_keys, q_bits + slot_bits, slot_bits, tl, qptr, ke);
     BF_CHECK_LAUNCH();
   }
-  return launch_token_reverse(tl, qptr, kptr, nullptr, ke, st);
+  return launch_token_reverse(tl, qptr, nullptr, ke, st);
 }
 
 extern "C" int bf_expand_rows(const int64_t* ptr, int64_t n_rows, int64_t nnz, int64_t* rows, void* stream) {

@@ -474,13 +474,12 @@ def reverse_index(qptr: torch.Tensor, kv: torch.Tensor, n_kv: int):
 def reverse_index_packed(rk: ReverseKeys, qptr: torch.Tensor, n_kv: int, entries: bool = True):
     """reverse_index from table_to_csr's sort keys (one sort of the id bits, no row recovery):
     (kptr, kq, ke, sorted). ``entries=False`` skips ke (a gather of qptr that only a bias or factor
-    needs; ``reverse_entries(sorted, qptr, kptr)`` gives it later) and returns ke = None."""
+    needs; ``reverse_entries(sorted, qptr)`` gives it later) and returns ke = None."""
     dev = qptr.device
     _require(qptr, "qptr", torch.int64)
     _require(rk.keys, "keys", torch.int64, dev)
     n_keys = rk.keys.numel()
-    nnz = n_keys + ((qptr.numel() - 1 - (1 if rk.token_row >= 0 else 0)) + max(rk.token_row, 0)
-                    if rk.global_token else 0)
+    nnz = _entries_of(rk, qptr)
     ws = _workspace(_size_query("bf_reverse_index_packed_workspace_size", nnz), dev)
     srt = ReverseKeys(torch.empty(max(n_keys, 1), dtype=torch.int64, device=dev)[:n_keys], rk.q_bits, rk.slot_bits,
                       rk.global_token, rk.token_row)
@@ -493,15 +492,21 @@ def reverse_index_packed(rk: ReverseKeys, qptr: torch.Tensor, n_kv: int, entries
     return kptr, kq, ke, srt
 
 
-def reverse_entries(srt: ReverseKeys, qptr: torch.Tensor, kptr: torch.Tensor) -> torch.Tensor:
-    """ke (CSR position per reverse entry, int32) from reverse_index_packed's sorted keys and kptr."""
+def _entries_of(rk: ReverseKeys, qptr: torch.Tensor) -> int:
+    """Entries of the index whose reverse-index keys are ``rk``: the keys plus the token's own entries."""
+    if not rk.global_token:
+        return rk.keys.numel()
+    return rk.keys.numel() + qptr.numel() - 1 - (1 if rk.token_row >= 0 else 0) + max(rk.token_row, 0)
+
+
+def reverse_entries(srt: ReverseKeys, qptr: torch.Tensor) -> torch.Tensor:
+    """ke (CSR position per reverse entry, int32) from reverse_index_packed's sorted keys."""
     dev = qptr.device
     _require(qptr, "qptr", torch.int64)
-    _require(kptr, "kptr", torch.int64, dev)
     _require(srt.keys, "keys", torch.int64, dev)
-    nnz = int(kptr[-1].item()) if kptr.numel() else 0
+    nnz = _entries_of(srt, qptr)
     ke = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)[:nnz]
-    N.call("bf_reverse_entries", _p(srt.keys), _p(qptr), _p(kptr), nnz, qptr.numel() - 1, srt.q_bits, srt.slot_bits,
+    N.call("bf_reverse_entries", _p(srt.keys), _p(qptr), nnz, qptr.numel() - 1, srt.q_bits, srt.slot_bits,
            int(srt.global_token), int(srt.token_row), _p(ke), _stream(dev))
     return ke
 
@@ -801,7 +806,7 @@ class AttentionIndex:
         """The CSR position of every reverse entry (ke), which the dk/dv pass reads only with a bias or factor."""
         self.ensure_backward()
         if self.ke is None and self.nnz:
-            self.ke = reverse_entries(self._sorted, self.qptr, self.kptr)
+            self.ke = reverse_entries(self._sorted, self.qptr)
             self._sorted = None
         return self
 

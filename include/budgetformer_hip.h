@@ -320,18 +320,17 @@ int bf_reverse_index(const int64_t* qptr, const int32_t* kv, int64_t n_q, int64_
  * sorted keys the rest. nnz counts every entry. ke (may be NULL) is decoded in
  * the same pass: qptr[query] + slot; it is a random gather of qptr, which the
  * dk/dv pass needs only with a bias, factor or dropout, so a caller may keep
- * `sorted` and call bf_reverse_entries (with the kptr written here) later
- * instead. Same kptr / kq / ke as bf_reverse_index.
+ * `sorted` and call bf_reverse_entries later instead. Same kptr / kq / ke as bf_reverse_index.
  * Workspace: bf_reverse_index_packed_workspace_size(nnz).                   */
 int bf_reverse_index_packed_workspace_size(int64_t nnz, size_t* bytes);
 int bf_reverse_index_packed(const uint64_t* rkey, const int64_t* qptr, int64_t nnz, int64_t n_q, int64_t n_kv,
                             int32_t q_bits, int32_t slot_bits, int32_t global_token, int64_t token_row,
                             uint64_t* sorted, int64_t* kptr, int32_t* kq, int32_t* ke, void* workspace,
                             size_t workspace_bytes, void* stream);
-/* ke [nnz] from bf_reverse_index_packed's sorted keys and kptr.              */
-int bf_reverse_entries(const uint64_t* sorted, const int64_t* qptr, const int64_t* kptr, int64_t nnz, int64_t n_q,
-                       int32_t q_bits, int32_t slot_bits, int32_t global_token, int64_t token_row, int32_t* ke,
-                       void* stream);
+/* ke [nnz] from bf_reverse_index_packed's sorted keys (the same nnz, n_q,
+ * key fields and token arguments).                                         */
+int bf_reverse_entries(const uint64_t* sorted, const int64_t* qptr, int64_t nnz, int64_t n_q, int32_t q_bits,
+                       int32_t slot_bits, int32_t global_token, int64_t token_row, int32_t* ke, void* stream);
 
 /* Row id of every entry of a CSR (rows[i] = r for ptr[r] <= i < ptr[r+1]). */
 int bf_expand_rows(const int64_t* ptr, int64_t n_rows, int64_t nnz, int64_t* rows, void* stream);

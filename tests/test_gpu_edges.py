@@ -393,7 +393,7 @@ def test_index_formats_against_numpy(hip_device, token, token_row):
         assert torch.equal(x, y)
     lazy = hip_ops.reverse_index_packed(rk, qptr, n_kv, entries=False)
     assert lazy[2] is None and torch.equal(lazy[0], a[0]) and torch.equal(lazy[1], a[1])
-    assert torch.equal(hip_ops.reverse_entries(lazy[3], qptr, lazy[0]), a[2])
+    assert torch.equal(hip_ops.reverse_entries(lazy[3], qptr), a[2])
     order = np.lexsort((pos, np.array(vals)))                    # (kv, position) order
     assert np.array_equal(b[1].cpu().numpy(), np.array(rows)[order]) and np.array_equal(b[2].cpu().numpy(), order)
     # row order: a permutation, capped lengths non-increasing
