@@ -19,7 +19,7 @@ BF_DTYPE_F32, BF_DTYPE_BF16 = 0, 1
 BF_MAX_ITEMS_PER_ROW = 160          # items a split row is cut into at most (the header's #define) ...
 BF_LONG_ROW_FACTOR = 64             # ... unless it is longer than 160 * 64 items' worth (the header's #define)
 
-i32, i64, u64, sz = C.c_int32, C.c_int64, C.c_uint64, C.c_size_t
+i32, i64, u64, sz, f32 = C.c_int32, C.c_int64, C.c_uint64, C.c_size_t, C.c_float
 vp = C.c_void_p
 P_i32 = vp  # device pointers are passed as plain addresses
 P_i64 = vp
@@ -103,14 +103,14 @@ _SIGS = {
     "bf_row_order_and_plan": (C.c_int, [P_i64, i64, i32, i32, P_i32, vp, P_i32, P_i32, P_i32, i64, P_i32, i64,
                                         P_i32, vp, sz, vp]),
     "bf_attn_partials_floats": (i64, [C.POINTER(AttnIndex), i32, i32]),
-    "bf_attn_bwd_noalloc": (C.c_int, [C.POINTER(AttnIndex), i32, i32, i32, vp, vp, vp, P_f32, P_f32,
+    "bf_attn_bwd_noalloc": (C.c_int, [C.POINTER(AttnIndex), i32, i32, i32, f32, vp, vp, vp, P_f32, P_f32,
                                       C.POINTER(AttnDropout), P_f32, vp, vp, vp, vp, P_f32, vp]),
     "bf_attn_bwd_kv_variant": (C.c_int, [C.POINTER(AttnIndex), i32, i32, i32, C.POINTER(i32), C.POINTER(i32),
                                          C.POINTER(i32)]),
-    "bf_attn_fwd": (C.c_int, [C.POINTER(AttnIndex), i32, i32, i32, vp, vp, vp, P_f32, P_f32, C.POINTER(AttnDropout),
-                              vp, P_f32, P_f32, vp]),
-    "bf_attn_bwd": (C.c_int, [C.POINTER(AttnIndex), i32, i32, i32, vp, vp, vp, P_f32, P_f32, C.POINTER(AttnDropout),
-                              P_f32, vp, vp, vp, vp, P_f32, P_f32, P_f32, vp]),
+    "bf_attn_fwd": (C.c_int, [C.POINTER(AttnIndex), i32, i32, i32, f32, vp, vp, vp, P_f32, P_f32,
+                              C.POINTER(AttnDropout), vp, P_f32, P_f32, vp]),
+    "bf_attn_bwd": (C.c_int, [C.POINTER(AttnIndex), i32, i32, i32, f32, vp, vp, vp, P_f32, P_f32,
+                              C.POINTER(AttnDropout), P_f32, vp, vp, vp, vp, P_f32, P_f32, P_f32, vp]),
 }
 
 _lib = None

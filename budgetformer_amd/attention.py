@@ -15,7 +15,11 @@ variants are not part of it and raise.
 type row, which the sparse path ignores, as the reference does), an
 ``AttentionIndex``, or an ``EdgeTable`` from the edge builder. COO inputs are
 converted once per distinct tensor and cached, since every layer of a step
-sees the same edge set (models/graphormer_dist_node_level.py:1374).
+sees the same edge set (models/graphormer_dist_node_level.py:1374). Graphormer
+and GT also take a list of such edge sets, one per head group
+(models/graphormer_dist_node_level.py:175-213) or per head
+(models/gt_dist_node_level.py:195-218): heads that share a set run as one
+call on their slice of q, k and v.
 """
 from __future__ import annotations
 
@@ -31,38 +35,45 @@ from .hip_ops import AttentionIndex
 
 
 class _SparseEdgeAttention(torch.autograd.Function):
-    """out = sum_e exp(clamp(q.k/sqrt(hn)) + bias) * f * v / (Z + 1e-6), HIP fwd/bwd."""
+    """out = sum_e exp(clamp(q.k/sqrt(hn)) + bias) * f * v / (Z + 1e-6), HIP fwd/bwd; also returns Z
+    (not differentiable)."""
 
     @staticmethod
-    def forward(ctx, q, k, v, bias_e, factor_e, index, dropout):
-        out, Z = hip_ops.attn_forward(index, q, k, v, bias_e, factor_e, dropout)
+    def forward(ctx, q, k, v, bias_e, factor_e, index, dropout, score_clamp):
+        out, Z = hip_ops.attn_forward(index, q, k, v, bias_e, factor_e, dropout, score_clamp)
         # the backward needs Z, not out (it sums Delta = dO . out from the entries in float32)
         ctx.save_for_backward(q, k, v, Z, bias_e, factor_e)
         ctx.index = index
         ctx.dropout = dropout          # the same Philox key draws the same mask in the backward
+        ctx.score_clamp = score_clamp
         ctx.need_dbias = bias_e is not None and ctx.needs_input_grad[3]
-        return out
+        ctx.mark_non_differentiable(Z)
+        return out, Z
 
     @staticmethod
-    def backward(ctx, dout):
+    def backward(ctx, dout, _dZ):
         q, k, v, Z, bias_e, factor_e = ctx.saved_tensors
         dq, dk, dv, dbias = hip_ops.attn_backward(ctx.index, q, k, v, None, Z, dout.contiguous(), bias_e, factor_e,
-                                                  need_dbias=ctx.need_dbias, dropout=ctx.dropout)
-        return dq, dk, dv, dbias, None, None, None
+                                                  need_dbias=ctx.need_dbias, dropout=ctx.dropout,
+                                                  score_clamp=ctx.score_clamp)
+        return dq, dk, dv, dbias, None, None, None, None
 
 
 def sparse_edge_attention(q, k, v, index: AttentionIndex, bias_e: Optional[torch.Tensor] = None,
-                          factor_e: Optional[torch.Tensor] = None,
-                          dropout: Optional[hip_ops.Dropout] = None) -> torch.Tensor:
+                          factor_e: Optional[torch.Tensor] = None, dropout: Optional[hip_ops.Dropout] = None,
+                          score_clamp: float = hip_ops.SCORE_CLAMP, with_z: bool = False):
     """Functional form. q [n_q,H,hn], k/v [n_kv,H,hn]; bias_e/factor_e float32 [nnz,H]; dropout: the
-    in-kernel GraphGPS attention dropout (Philox keep mask per entry and head)."""
+    in-kernel GraphGPS attention dropout (Philox keep mask per entry and head); score_clamp: the bound
+    of the clamp on q.k/sqrt(hn). Returns out, or (out, Z) with ``with_z`` (Z [n_q, H] float32, the
+    per-query sum of exp scores, not differentiable)."""
     dt = q.dtype
     q, k, v = q.contiguous(), k.to(dt).contiguous(), v.to(dt).contiguous()
     if bias_e is not None:
         bias_e = bias_e.float().contiguous()
     if factor_e is not None:
         factor_e = factor_e.float().contiguous()
-    return _SparseEdgeAttention.apply(q, k, v, bias_e, factor_e, index, dropout)
+    out, Z = _SparseEdgeAttention.apply(q, k, v, bias_e, factor_e, index, dropout, float(score_clamp))
+    return (out, Z) if with_z else out
 
 
 class _IndexCache:
@@ -102,7 +113,7 @@ def resolve_index(edge_index, n_q: int, n_kv: int, device, chunk: int = hip_ops.
             edge_index = edge_index.to(device)
         idx = _COO_CACHE.get(edge_index, n_q, n_kv, chunk)
     elif isinstance(edge_index, (list, tuple)):
-        raise NotImplementedError("per-head-group edge lists are not on the single-edge-set sparse path")
+        raise TypeError("a list of edge sets is taken by the modules' per-head paths, not as one edge set")
     else:
         raise TypeError(f"unsupported edge_index type {type(edge_index)}")
     if idx.n_q != n_q or idx.n_kv != n_kv:
@@ -110,11 +121,57 @@ def resolve_index(edge_index, n_q: int, n_kv: int, device, chunk: int = hip_ops.
     return idx
 
 
-def _dense_bias_to_edges(attn_bias: torch.Tensor, idx: AttentionIndex, S: int, H: int) -> torch.Tensor:
-    """bias_e[e, h] = attn_bias[src(e), dst(e), h] for a dense key-major [S, S, H] bias."""
-    b = attn_bias.reshape(S, S, H)
-    rows = idx.entry_rows()
-    return b[idx.kv.to(torch.int64), rows, :].float()
+def _dense_bias_to_edges(attn_bias: torch.Tensor, idx: AttentionIndex, batch: int, n: int, H: int) -> torch.Tensor:
+    """bias_e[e, h] for a dense key-major bias [batch, n, n, H] over the flattened batch*n rows, as
+    models/graphormer_dist_node_level.py:171-173 expands it (unsqueeze(2).repeat over the batch, then
+    view(b*n, b*n, H)): entry (src, dst) reads attn_bias[src // n, src % n, dst % n]. With batch 1
+    that is attn_bias[0, src, dst]."""
+    b = attn_bias.reshape(batch, n, n, H)
+    src = idx.kv.to(torch.int64)
+    dst = idx.entry_rows()
+    if batch == 1:
+        return b[0, src, dst, :].float()
+    return b[torch.div(src, n, rounding_mode="floor"), src % n, dst % n, :].float()
+
+
+def _head_runs(assign):
+    """Runs (h0, h1, edges) of consecutive heads assigned the same edge-set object (or None)."""
+    runs, h, H = [], 0, len(assign)
+    while h < H:
+        h1 = h + 1
+        while h1 < H and assign[h1] is assign[h]:
+            h1 += 1
+        runs.append((h, h1, assign[h]))
+        h = h1
+    return runs
+
+
+def _empty_edges(e) -> bool:
+    return e is None or (isinstance(e, torch.Tensor) and e.numel() == 0)
+
+
+def _per_head_attention(q, k, v, assign, score_clamp, bias_fn=None, stats=None):
+    """Attention with head h over edge set assign[h]: each run of heads sharing a set is one call on its
+    head slice; heads whose set is None or empty give zeros (wV = 0, Z = 0: 0 / 1e-6). bias_fn(idx, h0,
+    h1) gives a run's [nnz, h1-h0] bias; stats = (sum, count) accumulates each head's sum of exp scores
+    and edge count (float32 CPU tensors [H])."""
+    S, H, hn = q.shape
+    pieces = []
+    for h0, h1, e in _head_runs(assign):
+        if _empty_edges(e):
+            pieces.append(q.new_zeros(S, h1 - h0, hn))
+            continue
+        idx = resolve_index(e, S, k.size(0), q.device)
+        bias = bias_fn(idx, h0, h1) if bias_fn is not None else None
+        out, Z = sparse_edge_attention(q[:, h0:h1], k[:, h0:h1], v[:, h0:h1], idx, bias, score_clamp=score_clamp,
+                                       with_z=True)
+        if stats is not None:
+            mass = Z.sum(0).detach().cpu()
+            for h in range(h0, min(h1, stats[0].numel())):
+                stats[0][h] += float(mass[h - h0])
+                stats[1][h] += float(idx.nnz)
+        pieces.append(out)
+    return pieces[0] if len(pieces) == 1 else torch.cat(pieces, dim=1)
 
 
 class CoreAttention(nn.Module):
@@ -130,7 +187,9 @@ class CoreAttention(nn.Module):
         self.attention_dropout_rate = attention_dropout_rate
 
     def sparse_attention_bias(self, k, q, v, edge_index, attn_bias):
-        """Argument order (k, q, v, edge_index, attn_bias) as at :155; returns [b*S, H, hn]."""
+        """Argument order (k, q, v, edge_index, attn_bias) as at :155; returns [b*S, H, hn]. attn_bias
+        [b, S, S, H] is read as the reference expands it over the batch (:171-173). A list of G edge
+        sets serves head groups of ceil(H / G) heads (:175-213)."""
         batch_size, node_num = k.size(0), k.size(1)
         num_heads = q.size(2)
         hn = self.hidden_size_per_attention_head
@@ -138,12 +197,19 @@ class CoreAttention(nn.Module):
         k = k.reshape(-1, num_heads, hn)
         v = v.reshape(-1, num_heads, hn)
         S = q.size(0)
+        if isinstance(edge_index, (list, tuple)):
+            groups = max(1, len(edge_index))
+            per = (num_heads + groups - 1) // groups
+            assign = [edge_index[h // per] if h // per < len(edge_index) else None for h in range(num_heads)]
+            bias_fn = None
+            if attn_bias is not None:
+                def bias_fn(idx, h0, h1):
+                    return _dense_bias_to_edges(attn_bias, idx, batch_size, node_num, num_heads)[:, h0:h1]
+            return _per_head_attention(q, k, v, assign, hip_ops.SCORE_CLAMP, bias_fn)
         idx = resolve_index(edge_index, S, k.size(0), q.device)
         bias_e = None
         if attn_bias is not None:
-            if batch_size != 1:
-                raise NotImplementedError("dense attn_bias is supported for batch size 1 (the full-graph path)")
-            bias_e = _dense_bias_to_edges(attn_bias, idx, S, num_heads)
+            bias_e = _dense_bias_to_edges(attn_bias, idx, batch_size, node_num, num_heads)
         return sparse_edge_attention(q, k, v, idx, bias_e)
 
     def forward(self, q, k, v, attn_bias=None, edge_index=None, attn_type=None):
@@ -164,10 +230,27 @@ class GTCoreAttention(nn.Module):
         self.scale = math.sqrt(self.hidden_size_per_attention_head)
         self.num_heads = num_heads
         self.att_dropout = nn.Dropout(attention_dropout_rate)
+        self._head_mass_sum = None
+        self._head_mass_count = None
+
+    def reset_head_mass_stats(self):
+        """Start accumulating, per head, the sum of exp scores and the edge count of the per-head-list
+        path (models/gt_dist_node_level.py:75-84, 218-220)."""
+        self._head_mass_sum = torch.zeros(self.num_attention_heads_per_partition, dtype=torch.float32)
+        self._head_mass_count = torch.zeros(self.num_attention_heads_per_partition, dtype=torch.float32)
+
+    def get_head_mass_stats(self):
+        """Mean exp score per head since the reset, or None (models/gt_dist_node_level.py:86-90)."""
+        if self._head_mass_sum is None:
+            return None
+        return self._head_mass_sum / torch.clamp(self._head_mass_count, min=1.0)
 
     def sparse_attention_bias(self, q, k, v, edge_index, attn_bias):
-        """Argument order (q, k, v, ...) as at :179. attn_bias [b, np, s, s] is read key-major."""
-        batch_size = k.size(0)
+        """Argument order (q, k, v, ...) as at :179. attn_bias [b, np, s, s] is read key-major, expanded
+        over the batch as the Graphormer path does (the reference's own indexing of it at :236-242 fails
+        for any edge whose source is not row 0). A list holds one edge set per head, cycled to H
+        entries (:195-218): head h scores exp(clamp(q.k, -5, 5) / sqrt(hn)), without the bias."""
+        batch_size, node_num = k.size(0), k.size(1)
         num_heads = q.size(2)
         hn = self.hidden_size_per_attention_head
         if isinstance(edge_index, torch.Tensor) and edge_index.dim() == 2 and edge_index.size(0) == 3:
@@ -176,12 +259,17 @@ class GTCoreAttention(nn.Module):
         k = k.reshape(-1, num_heads, hn)
         v = v.reshape(-1, num_heads, hn)
         S = q.size(0)
+        if isinstance(edge_index, (list, tuple)):
+            if len(edge_index) == 0:
+                raise ValueError("an empty list of per-head edge sets")
+            assign = [edge_index[h % len(edge_index)] for h in range(num_heads)]
+            # clamp(q.k, -5, 5) / sqrt(hn) = clamp(q.k / sqrt(hn), -5 / sqrt(hn), 5 / sqrt(hn))
+            stats = (self._head_mass_sum, self._head_mass_count) if self._head_mass_sum is not None else None
+            return _per_head_attention(q, k, v, assign, hip_ops.SCORE_CLAMP / math.sqrt(hn), stats=stats)
         idx = resolve_index(edge_index, S, k.size(0), q.device)
         bias_e = None
         if attn_bias is not None:
-            if batch_size != 1:
-                raise NotImplementedError("dense attn_bias is supported for batch size 1 (the full-graph path)")
-            bias_e = _dense_bias_to_edges(attn_bias.permute(0, 2, 3, 1), idx, S, num_heads)
+            bias_e = _dense_bias_to_edges(attn_bias.permute(0, 2, 3, 1), idx, batch_size, node_num, num_heads)
         return sparse_edge_attention(q, k, v, idx, bias_e)
 
     def forward(self, q, k, v, attn_bias=None, edge_index=None, attn_type=None):

@@ -2,8 +2,12 @@
 //
 // Semantics: models/graphormer_dist_node_level.py:215-263 (GT :215-262, GraphGPS
 // models/graphgps_dist_node_level.py:151-177 through the per-edge factor):
-//   a = clamp(sum_j k[s,h,j] * q[t,h,j] / sqrt(hn), -5, 5) [+ bias[e,h]]
+//   a = clamp(sum_j k[s,h,j] * q[t,h,j] / sqrt(hn), -c, c) [+ bias[e,h]]
 //   p = exp(a)   (no max subtraction; the clamp bounds it when bias is absent)
+// with c = 5 on every path but GT's per-head edge lists
+// (models/gt_dist_node_level.py:195-218), which clamp the dot product to
+// [-5, 5] before the scaling: exp(clamp(x, -5, 5) / sqrt(hn)) is the same
+// expression with c = 5 / sqrt(hn).
 //   Z[t,h] = sum_e p,  out[t,h,:] = sum_e p * f[e,h] * v[s,h,:] / (Z[t,h] + 1e-6)
 //
 // Work mapping. A row of D = H*hn activations is split across a group of
@@ -52,7 +56,7 @@ template <> struct Unroll<uint16_t> {
   static constexpr int fwd = BF_UNROLL_FWD, q = BF_UNROLL_Q, kv = BF_UNROLL_KV_BF16;
 };
 constexpr float kEps = 1e-6f;
-constexpr float kClamp = 5.0f;
+constexpr float kClamp = 5.0f;   // the reference's clamp bound, the default
 
 struct Shape {
   int D;          // H * hn
@@ -61,6 +65,7 @@ struct Shape {
   int lph_log2;   // lanes per head (power of two)
   int act_lanes;  // D / EPL lanes carry data; the rest of the group idles
   float inv_scale;
+  float clamp;    // scores are clamped to [-clamp, clamp] after the 1/sqrt(hn) scaling
 };
 
 struct GroupPos {
@@ -278,7 +283,7 @@ __device__ __forceinline__ void fwd_segment(const T* __restrict__ k, const T* __
     for (int u = 0; u < kUnroll; ++u) {
       if (!ok[u]) continue;
       const int64_t e = e0 + u;
-      float a = fminf(fmaxf(d[u] * sh.inv_scale, -kClamp), kClamp);
+      float a = fminf(fmaxf(d[u] * sh.inv_scale, -sh.clamp), sh.clamp);
       if (EX == 2) a += edge_bias(ex, e, sh, g.head);
       const float p = __expf(a);   // a is clamped to [-5, 5] (+ bias): exp2-based form is within 2 ulp
       const float w = EX ? p * iter_factor<kUnroll, EX>(ex, drop, u, e, sh, g.head) : p;
@@ -544,12 +549,12 @@ __device__ __forceinline__ EntryTerms entry_terms(float d, float wraw, float inv
                                                   float f, const Shape& sh, const GroupPos& g) {
   EntryTerms t;
   const float apre = d * sh.inv_scale;
-  float a = fminf(fmaxf(apre, -kClamp), kClamp);
+  float a = fminf(fmaxf(apre, -sh.clamp), sh.clamp);
   if (EX == 2) a += edge_bias(ex, e, sh, g.head);
   t.p = __expf(a);   // a is clamped to [-5, 5] (+ bias): exp2-based form is within 2 ulp
   t.f = EX ? f : 1.f;
   t.w = wraw * inv_dprime;
-  t.m = (apre >= -kClamp && apre <= kClamp) ? sh.inv_scale : 0.f;
+  t.m = (apre >= -sh.clamp && apre <= sh.clamp) ? sh.inv_scale : 0.f;
   return t;
 }
 
@@ -969,13 +974,13 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
       if (!ok[u]) continue;
       const int64_t e = EX ? int64_t(epos[u]) : 0;
       const float apre = d[u] * sh.inv_scale;
-      float a = fminf(fmaxf(apre, -kClamp), kClamp);
+      float a = fminf(fmaxf(apre, -sh.clamp), sh.clamp);
       if (EX == 2) a += edge_bias(ex, e, sh, g.head);
       const float p = __expf(a);   // a is clamped to [-5, 5] (+ bias): exp2-based form is within 2 ulp
       const float f = EX ? iter_factor<kUnroll, EX>(ex, drop, u, e, sh, g.head) : 1.f;
       const float gb = fmaf(f * w[u], rs[u].x, -rs[u].y) * p;   // rs = {1/D', Delta/D'}
       if (EX == 2 && dbias && g.lead) dbias[e * sh.H + g.head] = gb;
-      const float gs = (apre >= -kClamp && apre <= kClamp) ? gb * sh.inv_scale : 0.f;
+      const float gs = (apre >= -sh.clamp && apre <= sh.clamp) ? gb * sh.inv_scale : 0.f;
       const float pf = p * f * rs[u].x;
       float qq[V], gg[V];
       Elem<T>::unpack(qr[u], qq);
@@ -1148,6 +1153,15 @@ int make_shape(int32_t dtype, int32_t H, int32_t hn, Shape& sh) {
   sh.lph_log2 = ilog2(hn / V);
   sh.act_lanes = lanes;
   sh.inv_scale = 1.0f / sqrtf(float(hn));
+  sh.clamp = kClamp;
+  return BF_OK;
+}
+
+// The score clamp a call asks for: in (0, 5] (the reference's 5, or GT's per-head-list 5 / sqrt(hn)).
+int set_clamp(float score_clamp, Shape& sh) {
+  BF_CHECK_ARG(score_clamp > 0.f && score_clamp <= kClamp, "attention: score_clamp %g outside (0, 5]",
+               double(score_clamp));
+  sh.clamp = score_clamp;
   return BF_OK;
 }
 
@@ -1392,12 +1406,12 @@ extern "C" int bf_attn_bwd_kv_variant(const bf_attn_index* idx, int32_t dtype, i
 }
 
 extern "C" int bf_attn_fwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
-                           const void* q, const void* k, const void* v, const float* bias,
+                           float score_clamp, const void* q, const void* k, const void* v, const float* bias,
                            const float* factor, const bf_attn_dropout* dropout, void* out, float* Z,
                            float* partials, void* stream) {
   Shape sh;
   int rc = make_shape(dtype, num_heads, head_dim, sh);
-  if (rc) return rc;
+  if (rc || (rc = set_clamp(score_clamp, sh))) return rc;
   if ((rc = check_index(idx, false))) return rc;
   EdgeIn ex;
   if ((rc = make_edge_in(bias, factor, dropout, ex))) return rc;
@@ -1411,13 +1425,13 @@ extern "C" int bf_attn_fwd(const bf_attn_index* idx, int32_t dtype, int32_t num_
 }
 
 extern "C" int bf_attn_bwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
-                           const void* q, const void* k, const void* v, const float* bias,
+                           float score_clamp, const void* q, const void* k, const void* v, const float* bias,
                            const float* factor, const bf_attn_dropout* dropout, const float* Z, const void* dout,
                            void* dq, void* dk, void* dv, float* dbias, float* rowstat, float* partials,
                            void* stream) {
   Shape sh;
   int rc = make_shape(dtype, num_heads, head_dim, sh);
-  if (rc) return rc;
+  if (rc || (rc = set_clamp(score_clamp, sh))) return rc;
   if ((rc = check_index(idx, true))) return rc;
   EdgeIn ex;
   if ((rc = make_edge_in(bias, factor, dropout, ex))) return rc;
@@ -1476,12 +1490,13 @@ int scratch_address(void** out) {
 }  // namespace bf
 
 extern "C" int bf_attn_bwd_noalloc(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
-                                   const void* q, const void* k, const void* v, const float* bias,
-                                   const float* factor, const bf_attn_dropout* dropout, const float* Z,
-                                   const void* dout, void* dq, void* dk, void* dv, float* dbias, void* stream) {
+                                   float score_clamp, const void* q, const void* k, const void* v,
+                                   const float* bias, const float* factor, const bf_attn_dropout* dropout,
+                                   const float* Z, const void* dout, void* dq, void* dk, void* dv, float* dbias,
+                                   void* stream) {
   Shape sh;
   int rc = make_shape(dtype, num_heads, head_dim, sh);
-  if (rc) return rc;
+  if (rc || (rc = set_clamp(score_clamp, sh))) return rc;
   if ((rc = check_index(idx, true))) return rc;
   const size_t stat_bytes = (size_t(idx->n_q) * size_t(num_heads) * 2 * sizeof(float) + 255) & ~size_t(255);
   const int64_t part_floats = bf_attn_partials_floats(idx, num_heads, head_dim);
@@ -1495,7 +1510,6 @@ extern "C" int bf_attn_bwd_noalloc(const bf_attn_index* idx, int32_t dtype, int3
   float* rowstat = static_cast<float*>(base);
   float* partials = reinterpret_cast<float*>(static_cast<unsigned char*>(base) + stat_bytes);
   ProfPause no_timer;   // the timer would create events
-  return bf_attn_bwd(idx, dtype, num_heads, head_dim, q, k, v, bias, factor, dropout, Z, dout, dq, dk, dv, dbias,
-                     rowstat,
-                     partials, stream);
+  return bf_attn_bwd(idx, dtype, num_heads, head_dim, score_clamp, q, k, v, bias, factor, dropout, Z, dout, dq, dk,
+                     dv, dbias, rowstat, partials, stream);
 }

@@ -132,7 +132,8 @@ std::tuple<at::Tensor, at::Tensor> sparse_attn_fwd(const at::Tensor& q, const at
                                                    const c10::List<std::optional<at::Tensor>>& index,
                                                    at::IntArrayRef sizes, const std::optional<at::Tensor>& bias,
                                                    const std::optional<at::Tensor>& factor, double dropout_rate,
-                                                   int64_t dropout_seed, int64_t dropout_offset) {
+                                                   int64_t dropout_seed, int64_t dropout_offset,
+                                                   double score_clamp) {
   TORCH_CHECK_VALUE(q.is_cuda(), "q must be a device tensor (got ", q.device(), ")");
   const c10::DeviceGuard guard(q.device());
   const at::Device dev = q.device();
@@ -146,7 +147,8 @@ std::tuple<at::Tensor, at::Tensor> sparse_attn_fwd(const at::Tensor& q, const at
   at::Tensor Z = at::empty({idx.n_q, H}, q.options().dtype(at::kFloat));
   const int64_t parts = bf_attn_partials_floats(&idx, int32_t(H), int32_t(hn));
   at::Tensor partials = at::empty({std::max<int64_t>(parts, 1)}, q.options().dtype(at::kFloat));
-  check_rc(bf_attn_fwd(&idx, dtype_code(q), int32_t(H), int32_t(hn), q.data_ptr(), k.data_ptr(), v.data_ptr(), b, f,
+  check_rc(bf_attn_fwd(&idx, dtype_code(q), int32_t(H), int32_t(hn), float(score_clamp), q.data_ptr(), k.data_ptr(),
+                       v.data_ptr(), b, f,
                        dropout_rate > 0.0 ? &drop : nullptr, out.data_ptr(), Z.data_ptr<float>(),
                        partials.data_ptr<float>(), stream_of(q)),
            "bf::sparse_attn_fwd");
@@ -158,7 +160,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> sparse_attn_bwd(
     const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, const c10::List<std::optional<at::Tensor>>& index,
     at::IntArrayRef sizes, const at::Tensor& Z, const at::Tensor& dout, const std::optional<at::Tensor>& bias,
     const std::optional<at::Tensor>& factor, bool need_dbias, double dropout_rate, int64_t dropout_seed,
-    int64_t dropout_offset) {
+    int64_t dropout_offset, double score_clamp) {
   TORCH_CHECK_VALUE(q.is_cuda(), "q must be a device tensor (got ", q.device(), ")");
   const c10::DeviceGuard guard(q.device());
   const at::Device dev = q.device();
@@ -178,7 +180,8 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> sparse_attn_bwd(
   at::Tensor rowstat = at::empty({idx.n_q, H, 2}, q.options().dtype(at::kFloat));
   const int64_t parts = bf_attn_partials_floats(&idx, int32_t(H), int32_t(hn));
   at::Tensor partials = at::empty({std::max<int64_t>(parts, 1)}, q.options().dtype(at::kFloat));
-  check_rc(bf_attn_bwd(&idx, dtype_code(q), int32_t(H), int32_t(hn), q.data_ptr(), k.data_ptr(), v.data_ptr(), b, f,
+  check_rc(bf_attn_bwd(&idx, dtype_code(q), int32_t(H), int32_t(hn), float(score_clamp), q.data_ptr(), k.data_ptr(),
+                       v.data_ptr(), b, f,
                        dropout_rate > 0.0 ? &drop : nullptr, Z.data_ptr<float>(), dout.data_ptr(), dq.data_ptr(),
                        dk.data_ptr(), dv.data_ptr(), need_dbias ? dbias.data_ptr<float>() : nullptr,
                        rowstat.data_ptr<float>(), partials.data_ptr<float>(), stream_of(q)),
@@ -309,10 +312,11 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> transpose_table(const at::Tensor&
 
 TORCH_LIBRARY(bf, m) {
   m.def("sparse_attn_fwd(Tensor q, Tensor k, Tensor v, Tensor?[] index, int[] sizes, Tensor? bias=None, "
-        "Tensor? factor=None, float dropout_rate=0.0, int dropout_seed=0, int dropout_offset=0) -> (Tensor, Tensor)");
+        "Tensor? factor=None, float dropout_rate=0.0, int dropout_seed=0, int dropout_offset=0, "
+        "float score_clamp=5.0) -> (Tensor, Tensor)");
   m.def("sparse_attn_bwd(Tensor q, Tensor k, Tensor v, Tensor?[] index, int[] sizes, Tensor Z, Tensor dout, "
         "Tensor? bias=None, Tensor? factor=None, bool need_dbias=False, float dropout_rate=0.0, int dropout_seed=0, "
-        "int dropout_offset=0) -> (Tensor, Tensor, Tensor, Tensor)");
+        "int dropout_offset=0, float score_clamp=5.0) -> (Tensor, Tensor, Tensor, Tensor)");
   m.def("rw_walk(Tensor rowptr, Tensor col, int q_lo, int n_q, int walks_per_node, int walk_length, "
         "int philox_seed=0, int philox_offset=0, Tensor? u=None) -> Tensor");
   m.def("build_edge_table(Tensor rowptr, Tensor col, Tensor? walk_rec, Tensor in_ptr, Tensor in_src, int q_lo, "

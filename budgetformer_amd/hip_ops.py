@@ -980,11 +980,16 @@ def _dropout_op_args(dropout: Optional[Dropout]):
     return float(dropout.rate), _i64(dropout.seed), _i64(dropout.offset)
 
 
-def attn_forward(idx: AttentionIndex, q, k, v, bias=None, factor=None, dropout: Optional[Dropout] = None):
+SCORE_CLAMP = 5.0   # the reference's clamp bound on q.k / sqrt(hn)
+
+
+def attn_forward(idx: AttentionIndex, q, k, v, bias=None, factor=None, dropout: Optional[Dropout] = None,
+                 score_clamp: float = SCORE_CLAMP):
     """out [n_q,H,hn] (activation dtype), Z [n_q,H] float32, through bf::sparse_attn_fwd (which checks
-    the shapes, dtypes and devices against the index)."""
+    the shapes, dtypes and devices against the index). ``score_clamp``: the bound of the clamp on
+    q.k / sqrt(hn), in (0, 5]."""
     t, n = idx.op_args(backward=False)
-    return N.load_ops().sparse_attn_fwd(q, k, v, t, n, bias, factor, *_dropout_op_args(dropout))
+    return N.load_ops().sparse_attn_fwd(q, k, v, t, n, bias, factor, *_dropout_op_args(dropout), float(score_clamp))
 
 
 def kv_pass_variant(n_q: int, n_kv: int, dtype: torch.dtype, heads: int, head_dim: int) -> dict:
@@ -999,7 +1004,7 @@ def kv_pass_variant(n_q: int, n_kv: int, dtype: torch.dtype, heads: int, head_di
 
 
 def attn_backward(idx: AttentionIndex, q, k, v, out, Z, dout, bias=None, factor=None, need_dbias: bool = False,
-                  dropout: Optional[Dropout] = None):
+                  dropout: Optional[Dropout] = None, score_clamp: float = SCORE_CLAMP):
     """(dq, dk, dv, dbias-or-None) for attn_forward's outputs. ``out`` is accepted for the autograd
     surface but not read: the backward sums Delta = dO . out from the entries in float32. Through
     bf::sparse_attn_bwd, which checks the shapes, dtypes and devices."""
@@ -1008,5 +1013,5 @@ def attn_backward(idx: AttentionIndex, q, k, v, out, Z, dout, bias=None, factor=
         raise ValueError(f"dropout rate {rate} outside [0, 1]")
     t, n = idx.op_args(backward=True, entries=bias is not None or factor is not None or need_dbias or rate > 0.0)
     dq, dk, dv, dbias = N.load_ops().sparse_attn_bwd(q, k, v, t, n, Z, dout, bias, factor, bool(need_dbias), rate,
-                                                     seed, off)
+                                                     seed, off, float(score_clamp))
     return dq, dk, dv, (dbias if need_dbias else None)

@@ -469,15 +469,18 @@ int64_t bf_attn_partials_floats(const bf_attn_index* idx, int32_t num_heads, int
 /* Forward. Replaces CoreAttention.sparse_attention_bias
  * (models/graphormer_dist_node_level.py:155-265; GT models/gt_dist_node_level.py:
  * 179-262; GraphGPS models/graphgps_dist_node_level.py:151-177) on one edge set:
- *   a = clamp(sum_j k[s,h,j]*q[t,h,j]/sqrt(hn), -5, 5) [+ bias[e,h]],
+ *   a = clamp(sum_j k[s,h,j]*q[t,h,j]/sqrt(hn), -c, c) [+ bias[e,h]],
  *   p = exp(a), Z[t,h] = sum_e p, out[t,h,:] = sum_e p*f[e,h]*v[s,h,:] / (Z+1e-6)
  * with f = factor (GPS dropout keep*scale) or 1.
+ *   score_clamp c in (0, 5]: 5 on the reference's tensor paths; GT's per-head
+ *   edge lists (models/gt_dist_node_level.py:195-218) take exp(clamp(q.k, -5,
+ *   5) / sqrt(hn)), which is c = 5 / sqrt(hn);
  *   q [n_q, H*hn], k, v [n_kv, H*hn] in `dtype`, rows 16-byte aligned;
  *   bias, factor: NULL or float32 [nnz, H] (per CSR position);
  *   dropout: NULL or the in-kernel GraphGPS dropout (its factor multiplies f);
  *   out [n_q, H*hn] in `dtype`; Z float32 [n_q, H];
  *   partials: float32 [bf_attn_partials_floats].                           */
-int bf_attn_fwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
+int bf_attn_fwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim, float score_clamp,
                 const void* q, const void* k, const void* v, const float* bias, const float* factor,
                 const bf_attn_dropout* dropout, void* out, float* Z, float* partials, void* stream);
 
@@ -494,7 +497,7 @@ int bf_attn_fwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int3
  *   rowstat: float32 [n_q, H, 2] scratch (per query and head
  *   {1/D', Delta/D'}, written by the query-major pass and read by the
  *   key-major pass).                                                         */
-int bf_attn_bwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
+int bf_attn_bwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim, float score_clamp,
                 const void* q, const void* k, const void* v, const float* bias, const float* factor,
                 const bf_attn_dropout* dropout, const float* Z, const void* dout, void* dq, void* dk, void* dv,
                 float* dbias, float* rowstat, float* partials, void* stream);
@@ -512,9 +515,9 @@ int bf_attn_bwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int3
  * Results equal bf_attn_bwd's bit for bit.                                   */
 #define BF_ATTN_NOALLOC_SCRATCH_BYTES (64u << 20)
 int bf_attn_bwd_noalloc(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
-                        const void* q, const void* k, const void* v, const float* bias, const float* factor,
-                        const bf_attn_dropout* dropout, const float* Z, const void* dout, void* dq, void* dk,
-                        void* dv, float* dbias, void* stream);
+                        float score_clamp, const void* q, const void* k, const void* v, const float* bias,
+                        const float* factor, const bf_attn_dropout* dropout, const float* Z, const void* dout,
+                        void* dq, void* dk, void* dv, float* dbias, void* stream);
 
 /* How bf_attn_bwd runs its key-major (dk/dv) pass on this index, for callers
  * and tests that need to know which kernel instance a shape takes (host-only,

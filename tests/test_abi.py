@@ -36,16 +36,21 @@ def test_argument_errors_surface_as_exceptions():
         N.call("bf_rw_select", None, None, None, 10, 0, 5, 2, 4, 4, 0, None, 0, 0, None, None, None)
     idx = N.AttnIndex()
     with pytest.raises(NotImplementedError):     # head_dim 6 does not split into 16-byte lanes
-        N.call("bf_attn_fwd", C.byref(idx), N.BF_DTYPE_F32, 2, 6, None, None, None, None, None, None, None, None,
-               None, None)
+        N.call("bf_attn_fwd", C.byref(idx), N.BF_DTYPE_F32, 2, 6, 5.0, None, None, None, None, None, None, None,
+               None, None, None)
     # a dropout rate outside [0, 1] is rejected after the index checks and before any launch (the index
     # here is an empty one: qptr is host memory the call never reads)
     qptr = (C.c_int64 * 1)(0)
     idx.chunk, idx.item, idx.qptr = 128, 768, C.cast(qptr, C.c_void_p)
     drop = N.AttnDropout(1.5, 1, 0)
     with pytest.raises(ValueError, match="dropout rate"):
-        N.call("bf_attn_fwd", C.byref(idx), N.BF_DTYPE_F32, 2, 8, None, None, None, None, None, C.byref(drop), None,
-               None, None, None)
+        N.call("bf_attn_fwd", C.byref(idx), N.BF_DTYPE_F32, 2, 8, 5.0, None, None, None, None, None, C.byref(drop),
+               None, None, None, None)
+    # the score clamp must lie in (0, 5] (checked before the index)
+    for bad in (0.0, -1.0, 5.5, float("nan")):
+        with pytest.raises(ValueError, match="score_clamp"):
+            N.call("bf_attn_fwd", C.byref(idx), N.BF_DTYPE_F32, 2, 8, bad, None, None, None, None, None, None,
+                   None, None, None, None)
 
 
 def test_walk_record_arguments_checked_on_the_host():

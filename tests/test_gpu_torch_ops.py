@@ -51,15 +51,15 @@ def _abi_fwd_bwd(idx, q, k, v, dout, bias, factor, drop):
     out = torch.empty_like(q)
     Z = torch.empty(q.shape[0], H, dtype=torch.float32, device=q.device)
     parts = torch.empty(max(int(N.load().bf_attn_partials_floats(C.byref(sf), H, hn)), 1), device=q.device)
-    N.call("bf_attn_fwd", C.byref(sf), dt, H, hn, p(q), p(k), p(v), p(bias), p(factor), d, p(out), p(Z), p(parts),
-           C.c_void_p(st))
+    N.call("bf_attn_fwd", C.byref(sf), dt, H, hn, 5.0, p(q), p(k), p(v), p(bias), p(factor), d, p(out), p(Z),
+           p(parts), C.c_void_p(st))
     sb = idx.struct(backward=True, entries=True)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     db = torch.empty(idx.nnz, H, dtype=torch.float32, device=q.device)
     rs = torch.empty(q.shape[0], H, 2, dtype=torch.float32, device=q.device)
     parts = torch.empty(max(int(N.load().bf_attn_partials_floats(C.byref(sb), H, hn)), 1), device=q.device)
-    N.call("bf_attn_bwd", C.byref(sb), dt, H, hn, p(q), p(k), p(v), p(bias), p(factor), d, p(Z), p(dout), p(dq),
-           p(dk), p(dv), p(db), p(rs), p(parts), C.c_void_p(st))
+    N.call("bf_attn_bwd", C.byref(sb), dt, H, hn, 5.0, p(q), p(k), p(v), p(bias), p(factor), d, p(Z), p(dout),
+           p(dq), p(dk), p(dv), p(db), p(rs), p(parts), C.c_void_p(st))
     return out, Z, dq, dk, dv, db
 
 

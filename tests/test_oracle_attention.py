@@ -134,3 +134,88 @@ def test_exphormer_oracle_reduces_to_plain_and_to_typed_keys():
     shifted = torch.stack([ei[0] + types * 30, ei[1]])
     got = sa.graphormer_sparse_attention(k2, q2, v2, shifted)[:30]
     torch.testing.assert_close(got, ref)
+
+
+def _edges(S, E, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.stack([torch.randint(0, S, (E,), generator=g), torch.randint(0, S, (E,), generator=g)])
+
+
+def test_head_group_lists_reduce_to_the_tensor_path():
+    S, H, hn = 40, 6, 4
+    q, k, v = _rand(S, H, hn, 21)
+    ei = _edges(S, 300, 22)
+    g = torch.Generator().manual_seed(23)
+    bias = torch.randn(S, S, H, generator=g, dtype=torch.float64)
+    full = sa.graphormer_sparse_attention(k, q, v, ei, bias)
+    # one group, and every group the same set (G = 2, 3, 4, 6, 7: the last has an empty head range)
+    for G in (1, 2, 3, 4, 6, 7):
+        torch.testing.assert_close(sa.graphormer_head_group_attention(k, q, v, [ei] * G, bias), full)
+    # G = H distinct sets: head h is the tensor path on head h alone
+    sets = [_edges(S, 50 + 30 * h, 30 + h) for h in range(H)]
+    out = sa.graphormer_head_group_attention(k, q, v, sets, bias)
+    for h in range(H):
+        one = sa.graphormer_sparse_attention(k[:, h:h + 1], q[:, h:h + 1], v[:, h:h + 1], sets[h],
+                                             bias[:, :, h:h + 1])
+        torch.testing.assert_close(out[:, h:h + 1], one)
+    # a None or empty set leaves its heads at zero (G = 3: heads 2, 3 belong to group 1)
+    out = sa.graphormer_head_group_attention(k, q, v, [ei, None, ei])
+    assert out[:, 2:4].abs().max() == 0 and out[:, :2].abs().max() > 0
+    out = sa.graphormer_head_group_attention(k, q, v, [ei, ei.new_zeros(2, 0), ei])
+    assert out[:, 2:4].abs().max() == 0
+
+
+def test_gt_head_list_clamps_before_scaling():
+    S, H, hn = 30, 4, 16
+    ei = _edges(S, 200, 41)
+    # small scores (|q.k| < 5): the clamp is inactive in both forms, so each head is the tensor path
+    q, k, v = _rand(S, H, hn, 42, mult=0.3)
+    assert (k[ei[0]] * q[ei[1]]).sum(-1).abs().max() < 5
+    torch.testing.assert_close(sa.gt_head_list_attention(q, k, v, [ei] * H), sa.gt_sparse_attention(q, k, v, ei))
+    # q.k in (5, 5 sqrt(hn)) for every edge: the tensor path does not clamp (q.k/4 < 5) but the list form
+    # saturates every score at exp(5/4), so each query's output is the plain mean of its sources' V rows
+    q = torch.ones(S, H, hn, dtype=torch.float64) * 0.4
+    k = torch.ones(S, H, hn, dtype=torch.float64) * (1.0 + torch.rand(S, 1, 1, dtype=torch.float64,
+                                                                      generator=torch.Generator().manual_seed(3)))
+    x = (k[ei[0]] * q[ei[1]]).sum(-1)
+    assert (x > 5).all() and (x / 4 < 5).all()
+    out = sa.gt_head_list_attention(q, k, v, [ei])          # a list of one set, cycled over the heads
+    p = math.exp(5 / 4)
+    cnt = torch.zeros(S, dtype=torch.float64).index_add(0, ei[1], torch.ones(ei.size(1), dtype=torch.float64))
+    mean = torch.zeros(S, H, hn, dtype=torch.float64).index_add(0, ei[1], v[ei[0]])
+    expect = mean * p / (cnt * p + 1e-6).view(S, 1, 1)
+    torch.testing.assert_close(out, expect)
+    assert not torch.allclose(out, sa.gt_sparse_attention(q, k, v, ei))
+    # and it is the stats form with the clamp bound 5 / sqrt(hn) after the scaling
+    q, k, v = _rand(S, H, hn, 43, mult=1.2)
+    got, _ = sa.attention_forward_stats(k, q, v, ei, clamp=5 / math.sqrt(hn))
+    torch.testing.assert_close(got, sa.gt_head_list_attention(q, k, v, [ei] * H))
+
+
+def test_batched_dense_bias_indexing():
+    b, n, H = 3, 5, 2
+    g = torch.Generator().manual_seed(9)
+    bias = torch.randn(b, n, n, H, generator=g, dtype=torch.float64)
+    full = sa.batched_dense_bias(bias, b, n)
+    assert full.shape == (b * n, b * n, H)
+    for i in range(b * n):
+        for j in range(b * n):
+            assert torch.equal(full[i, j], bias[i // n, i % n, j % n])
+    assert torch.equal(sa.batched_dense_bias(bias[:1], 1, n), bias[0])
+
+
+def test_closed_form_backward_with_a_clamp_bound_matches_autograd():
+    S, H, hn = 25, 2, 4
+    q, k, v = _rand(S, H, hn, 51, mult=1.5)
+    ei = _edges(S, 150, 52)
+    c = 5 / math.sqrt(hn)
+    q, k, v = (t.requires_grad_(True) for t in (q, k, v))
+    out, Z = sa.attention_forward_stats(k, q, v, ei, clamp=c)
+    dout = torch.randn(S, H, hn, dtype=torch.float64, generator=torch.Generator().manual_seed(53))
+    out.backward(dout)
+    a_pre = (k[ei[0]] * q[ei[1]] / math.sqrt(hn)).sum(-1)
+    assert (a_pre.abs() > c).any() and (a_pre.abs() < c).any()     # both sides of the bound occur
+    dq, dk, dv, _ = sa.attention_backward_closed_form(k.detach(), q.detach(), v.detach(), ei, out.detach(),
+                                                      Z.detach(), dout, clamp=c)
+    for got, ref in ((dq, q.grad), (dk, k.grad), (dv, v.grad)):
+        torch.testing.assert_close(got, ref)

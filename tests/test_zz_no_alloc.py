@@ -33,8 +33,8 @@ def _noalloc(idx, q, k, v, Z, dout, bias=None, need_dbias=False):
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     dbias = torch.empty(idx.nnz, H, dtype=torch.float32, device=q.device) if need_dbias else None
     p = hip_ops._p
-    N.call("bf_attn_bwd_noalloc", C.byref(st), hip_ops._DT[q.dtype], H, hn, p(q), p(k), p(v), p(bias), None, None,
-           p(Z), p(dout), p(dq), p(dk), p(dv), p(dbias), hip_ops._stream(q.device))
+    N.call("bf_attn_bwd_noalloc", C.byref(st), hip_ops._DT[q.dtype], H, hn, 5.0, p(q), p(k), p(v), p(bias), None,
+           None, p(Z), p(dout), p(dq), p(dk), p(dv), p(dbias), hip_ops._stream(q.device))
     return dq, dk, dv, dbias
 
 
