@@ -322,8 +322,9 @@ class GPSCoreAttention(nn.Module):
         return out.view(batch_size, s_len, -1)
 
     def forward(self, q, k, v, attn_bias=None, edge_index=None, attn_type=None):
+        """Every attn_type but "full" and "performer" takes the sparse path, as at :201-209."""
         attn_type = "sparse" if attn_type is None else str(attn_type).lower()
-        if attn_type != "sparse":
+        if attn_type in ("full", "performer"):
             raise NotImplementedError(f"attn_type={attn_type!r} is not on the sparse edge-attention path")
         return self._sparse(q, k, v, edge_index, q.size(2), self.hidden_size_per_attention_head)
 
