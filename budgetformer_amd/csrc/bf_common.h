@@ -203,6 +203,36 @@ __device__ __forceinline__ float group_sum(float x, int width) {
   return x;
 }
 
+// ---------------------------------------------------------------- row pointers from sorted keys
+// Kernels that turn sorted row ids into row pointers give each key's thread
+// the rows (lo, hi] that start at it: the rows between the previous key's id
+// and its own, which have no keys of their own. A gap of up to kGapInline rows
+// is written by its own lane; a longer one (a range of ids no entry reaches,
+// the tail past the largest id) by every active lane of the wave in turn, so
+// one lane never stores millions of pointers alone. write(r, val) stores row
+// r's pointer; val is the gap's value (its key's index). Call it from every
+// active lane of the wave (lanes without a gap pass hi <= lo).
+constexpr int64_t kGapInline = 32;
+
+template <typename F>
+__device__ __forceinline__ void fill_gap(int64_t lo, int64_t hi, int64_t val, F&& write) {
+  const bool wide = hi - lo > kGapInline;
+  if (!wide)
+    for (int64_t r = lo + 1; r <= hi; ++r) write(r, val);
+  uint64_t pending = __ballot(wide);
+  if (pending == 0) return;
+  const uint64_t active = __ballot(1);
+  const int lane = __lane_id();
+  const int64_t rank = __popcll(active & ((uint64_t(1) << lane) - 1));
+  const int64_t width = __popcll(active);
+  while (pending) {
+    const int src = __ffsll((unsigned long long)pending) - 1;
+    pending &= pending - 1;
+    const int64_t g_lo = __shfl(lo, src), g_hi = __shfl(hi, src), g_val = __shfl(val, src);
+    for (int64_t r = g_lo + 1 + rank; r <= g_hi; r += width) write(r, g_val);
+  }
+}
+
 // ---------------------------------------------------------------- keys
 // (src*1103515245 + dst*214013 + c) mod 2^31 with c = seed*2654435761 + 12345,
 // computed as the low 31 bits of the uint32-wrapped sum (utils/fullgraph_sp_support.py:984-989).

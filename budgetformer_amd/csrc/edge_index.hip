@@ -162,7 +162,7 @@ __global__ void boundaries_kernel(const K* __restrict__ keys, int64_t n, uint64_
   int64_t r_prev = i > 0 ? int64_t(uint64_t(keys[i - 1]) / divisor) : -1;
   if (r_here > n_rows) r_here = n_rows;
   if (r_prev > n_rows) r_prev = n_rows;
-  for (int64_t r = r_prev + 1; r <= r_here; ++r) ptr[r] = i;
+  fill_gap(r_prev, r_here, i, [&](int64_t r, int64_t v) { ptr[r] = v; });
 }
 
 __global__ void coo_keys_kernel(const int64_t* __restrict__ src, const int64_t* __restrict__ dst, int64_t nnz,
@@ -275,14 +275,14 @@ __global__ __launch_bounds__(kThreads) void unpack_rkey_kernel(
     if (r_here > n_kv) r_here = n_kv;
     if (r_prev > n_kv) r_prev = n_kv;
     if (i == 0 && tl.tok) kptr[0] = 0;
-    for (int64_t r = r_prev + 1; r <= r_here; ++r) {
-      const int64_t b = tl.row_base(r) + i;
+    fill_gap(r_prev, r_here, i, [&](int64_t r, int64_t v) {
+      const int64_t b = tl.row_base(r) + v;
       kptr[r] = b;
       if (r < n_kv && tl.token_entry(r)) {
         kq[b] = 0;
         if (ke) ke[b] = int32_t(r - 1);
       }
-    }
+    });
     if (i == n_keys) break;
     const int64_t o = tl.key_slot(i, int64_t(cur[u] >> kshift));
     kq[o] = int32_t((cur[u] >> sbits) & ((uint64_t(1) << (kshift - sbits)) - 1));
@@ -304,7 +304,7 @@ __global__ void reverse_entries_kernel(const uint64_t* __restrict__ keys, int64_
     int64_t r_prev = i > 0 ? int64_t(keys[i - 1] >> kshift) : 0;
     if (r_here > top) r_here = top;
     if (r_prev > top) r_prev = top;
-    for (int64_t r = r_prev + 1; r <= r_here; ++r) ke[tl.row_base(r) + i] = int32_t(r - 1);
+    fill_gap(r_prev, r_here, i, [&](int64_t r, int64_t v) { ke[tl.row_base(r) + v] = int32_t(r - 1); });
   }
   if (i < n_keys) ke[tl.key_slot(i, int64_t(x >> kshift))] = entry_of(x, kshift, sbits, qptr);
 }

@@ -105,7 +105,7 @@ __global__ void csr_rowptr_kernel(const uint64_t* __restrict__ keys, int64_t m, 
   if (i > m) return;
   const int64_t r_here = i < m ? int64_t(keys[i] / n) : int64_t(n);
   const int64_t r_prev = i > 0 ? int64_t(keys[i - 1] / n) : -1;
-  for (int64_t r = r_prev + 1; r <= r_here; ++r) rowptr[r] = i;
+  fill_gap(r_prev, r_here, i, [&](int64_t r, int64_t v) { rowptr[r] = v; });
 }
 
 }  // namespace

@@ -465,6 +465,40 @@ def test_plan_from_the_row_order_equals_the_generic_plan(hip_device, chunk, item
     assert np.array_equal(plan.item_row[:plan.items].cpu().numpy(), np.repeat(heavy, nit[heavy]))
 
 
+def test_row_pointers_across_long_runs_of_empty_rows(hip_device):
+    """Row pointers from sorted ids when long ranges of rows have no entries: COO queries and kv ids
+    clustered at both ends of 3M rows (gaps of ~1.5M rows inside and at the tail), and a table whose
+    ids stop far below the Graphormer token row's 2M kv rows. A wave writes each long gap together;
+    every pointer must equal numpy's counts."""
+    from budgetformer_amd import hip_ops
+    rng = np.random.default_rng(77)
+    n = 3_000_000
+    ids = np.concatenate([rng.integers(0, 50, 4000), rng.integers(1_500_000, 1_500_040, 3000),
+                          rng.integers(n - 30, n, 2000)])
+    src, dst = rng.permutation(ids), rng.permutation(ids)
+    ei = torch.from_numpy(np.stack([src, dst])).to(hip_device)
+    qptr, kv = hip_ops.coo_to_csr(ei, n + 5, n + 7)            # 5 and 7 empty rows past the last id
+    want_q = np.concatenate([[0], np.cumsum(np.bincount(dst, minlength=n + 5))])
+    assert np.array_equal(qptr.cpu().numpy(), want_q)
+    kptr, kq, ke = hip_ops.reverse_index(qptr, kv, n + 7)
+    want_k = np.concatenate([[0], np.cumsum(np.bincount(src, minlength=n + 7))])
+    assert np.array_equal(kptr.cpu().numpy(), want_k)
+    # a table of 3000 rows with ids below 3000 and a token row of 2M entries
+    m, width, tr = 3000, 4, 2_000_000
+    table = np.sort(rng.integers(0, m, (m, width)).astype(np.int32), axis=1)
+    row_len = np.full(m, width, dtype=np.int32)
+    t, rl = torch.from_numpy(table).to(hip_device), torch.from_numpy(row_len).to(hip_device)
+    qptr, kv, rk = hip_ops.table_to_csr(t, rl, True, with_keys=True, token_row=tr)
+    a = hip_ops.reverse_index(qptr, kv, tr + 1)
+    b = hip_ops.reverse_index_packed(rk, qptr, tr + 1)
+    for x, y in zip(a, b[:3]):
+        assert torch.equal(x, y)
+    lazy = hip_ops.reverse_index_packed(rk, qptr, tr + 1, entries=False)
+    assert torch.equal(hip_ops.reverse_entries(lazy[3], qptr), a[2])
+    kvn = kv.cpu().numpy()
+    assert np.array_equal(a[0].cpu().numpy(), np.concatenate([[0], np.cumsum(np.bincount(kvn, minlength=tr + 1))]))
+
+
 @pytest.mark.parametrize("n,width,lo", [(120_000, 12, 8), (600_000, 4, 2), (40_000, 8, 2)])
 def test_packed_reverse_index_onesweep_sizes(hip_device, n, width, lo):
     """Past 64K keys the sorts run as onesweep radix passes instead of a merge sort, the packed reverse
