@@ -183,7 +183,9 @@ def chung_lu_device(num_nodes: int, num_edges: int, exponent: float = 2.1, seed:
     """
     import ctypes as C
     from . import _native as N
+    from .hip_ops import _stream
     dev = torch.device(device)
+    stream = _stream(dev)          # refuses a host device before anything is allocated
     pairs = int(num_edges) // 2
     ws_bytes = C.c_size_t(0)
     N.call("bf_chung_lu_workspace_size", num_nodes, pairs, C.byref(ws_bytes))
@@ -193,7 +195,7 @@ def chung_lu_device(num_nodes: int, num_edges: int, exponent: float = 2.1, seed:
     m = C.c_int64(0)
     N.call("bf_chung_lu", num_nodes, pairs, float(exponent), float(i0), float(max_degree or 0.0), seed & (2 ** 64 - 1),
            C.c_void_p(rowptr.data_ptr()), C.c_void_p(col.data_ptr()), C.byref(m), C.c_void_p(ws.data_ptr()),
-           ws.numel(), C.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
+           ws.numel(), stream)
     del ws
     return CSRGraph(rowptr, col, rowptr, col, int(num_nodes))
 

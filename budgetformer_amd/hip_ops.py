@@ -28,7 +28,10 @@ def _p(t: Optional[torch.Tensor]):
 
 def _stream(device: torch.device):
     """The current HIP stream of ``device`` as a raw handle (what torch.cuda.current_stream(device).cuda_stream
-    gives, without building a Stream object on every call)."""
+    gives, without building a Stream object on every call). Every library call takes its stream from the
+    device of its tensors, so a host tensor is refused here, before any pointer reaches a kernel."""
+    if device.type != "cuda":
+        raise ValueError(f"the HIP path takes device tensors (got tensors on {device}); it has no CPU fallback")
     idx = device.index if device.index is not None else torch.cuda.current_device()
     return C.c_void_p(torch._C._cuda_getCurrentRawStream(idx))
 
