@@ -1,10 +1,13 @@
 """GPU parity of the HIP edge builder against the CPU oracle: bit-exact integer output."""
+import math
+
 import numpy as np
 import pytest
 import torch
 
 from oracle import edge_table as et
 from oracle import philox
+from oracle import sparse_attention as sa
 
 pytestmark = pytest.mark.gpu
 
@@ -463,6 +466,58 @@ def test_plan_from_the_row_order_equals_the_generic_plan(hip_device, chunk, item
     # items numbered in slot order, each row's items contiguous
     assert np.array_equal(off[heavy], np.concatenate([[0], np.cumsum(nit[heavy])[:-1]]))
     assert np.array_equal(plan.item_row[:plan.items].cpu().numpy(), np.repeat(heavy, nit[heavy]))
+
+
+@pytest.mark.parametrize("n,token_row", [(5000, None), (5000, -1), (5000, 7000), (0, None), (0, 3), (0, -1)])
+def test_token_index_of_tables_without_own_entries(hip_device, n, token_row):
+    """Tables whose rows are all empty (every key of the reverse-index sort is gone: only the token's
+    entries remain, placed without a sort) and tables with no rows at all: both reverse-index routes,
+    ke, and an attention layer over the index against the oracle."""
+    from budgetformer_amd import hip_ops
+    from budgetformer_amd.attention import sparse_edge_attention
+    from budgetformer_amd.hip_ops import AttentionIndex
+    width = 4
+    table = torch.full((n, width), -1, dtype=torch.int32, device=hip_device)
+    row_len = torch.zeros(n, dtype=torch.int32, device=hip_device)
+    tr = n if token_row is None else token_row
+    qptr, kv, rk = hip_ops.table_to_csr(table, row_len, True, with_keys=True, token_row=tr)
+    n_q = n + (1 if tr >= 0 else 0)
+    n_kv = max(n, tr) + 1
+    assert rk is not None and rk.keys.numel() == 0 and kv.numel() == n + max(tr, 0)
+    a = hip_ops.reverse_index(qptr, kv, n_kv)
+    b = hip_ops.reverse_index_packed(rk, qptr, n_kv)
+    for x, y in zip(a, b[:3]):
+        assert torch.equal(x, y)
+    lazy = hip_ops.reverse_index_packed(rk, qptr, n_kv, entries=False)
+    assert torch.equal(hip_ops.reverse_entries(lazy[3], qptr), a[2])
+    if n_q == 0 or kv.numel() == 0:
+        return
+    idx = AttentionIndex.from_table(table, row_len, True, n_kv=n_kv, token_row=tr)
+    H, hn = 2, 8
+    gen = torch.Generator().manual_seed(n + tr)
+    q = torch.randn(n_q, H, hn, generator=gen)
+    k, v = (torch.randn(n_kv, H, hn, generator=gen) for _ in range(2))
+    dout = torch.randn(n_q, H, hn, generator=gen)
+    qd, kd, vd = (t.to(hip_device).requires_grad_(True) for t in (q, k, v))
+    out = sparse_edge_attention(qd, kd, vd, idx)
+    out.backward(dout.to(hip_device))
+    ei = torch.stack([idx.kv.cpu().long(), idx.entry_rows().cpu()])
+    ro, rZ = sa.attention_forward_stats(k.double(), q.double(), v.double(), ei)
+    rdq, rdk, rdv, _ = sa.attention_backward_closed_form(k.double(), q.double(), v.double(), ei, ro, rZ,
+                                                         dout.double())
+    def rel(got, ref):
+        return ((got.detach().double().cpu() - ref).abs().max() / ref.abs().max().clamp_min(1e-30)).item()
+
+    assert rel(out, ro) < 1e-5 and rel(vd.grad, rdv) < 1e-5
+    # every table row attends kv 0 alone, so its dq and its term of kv 0's dK are softmax gradients over one
+    # key: differences of two equal terms, left over only through the 1e-6 in Z. kv 0's dK is held to an
+    # absolute bound of 1e-6 of those terms per entry (sqrt(n) for n independent roundings); the token row's
+    # kv rows 1.. keep the relative bar
+    dk = kd.grad.double().cpu()
+    if tr > 0:
+        assert rel(dk[1:], rdk[1:]) < 1e-5
+    terms = (dout.norm(dim=-1).max() * v.norm(dim=-1).max() * q.abs().max() / math.sqrt(hn)).item()
+    assert (dk[0] - rdk[0]).abs().max().item() < 1e-6 * terms * math.sqrt(max(n, 1))
 
 
 def test_row_pointers_across_long_runs_of_empty_rows(hip_device):
