@@ -81,8 +81,8 @@ __global__ __launch_bounds__(kThreads) void check_table_kernel(const int32_t* __
 // slot) at kidx: a stable radix sort over the id bits alone then leaves each
 // kv's entries in (row, slot) order, which is CSR order. With the Graphormer
 // token only the table's own entries get keys (kidx counts them in CSR order):
-// the token's entries (kv 0 of every row, the token row) have a fixed place in
-// the reverse index, which token_reverse_kernel writes.
+// the token's entries (kv 0 of every row, the token row) have fixed places in
+// the reverse index, written without a sort (TokenLayout below).
 __device__ __forceinline__ void put_entry(int32_t* __restrict__ kv, uint64_t* __restrict__ rkey, int64_t pos,
                                           int64_t kidx, int64_t row, int slot, int32_t id, int kshift, int sbits) {
   kv[pos] = id;
