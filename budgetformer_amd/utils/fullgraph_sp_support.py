@@ -17,7 +17,7 @@ from ..edges import build_attention_edges
 from ..graph import CSRGraph
 from ..gt_sp.utils import (_draw_walk_seed, _merge_edge_index_list, build_head_hop_edges,  # noqa: F401
                            fix_edge_index)
-from ..probe import build_probe, reception_cone
+from ..probe import reception_cone
 
 _GRAPHORMER_VIRTUAL_NODE_MODELS = frozenset({"graphormer"})   # utils/fullgraph_sp_support.py:60-63
 _EXPHORMER_MODELS = frozenset({"exphormer"})

@@ -13,7 +13,6 @@ The floor: bf16 results carry their own rounding (2^-9 of each value) and fp32 a
 fp32 rounding of those terms, ~1e-7 of the tensor's scale, so fp32 rows are floored at 0.1 —
 still ten times stricter than the per-tensor bar for every row below a tenth of the maximum.
 """
-import torch
 
 
 def rel_err(got, ref) -> float:

@@ -6,8 +6,6 @@ the larger of max|got - ref| / max|ref| per tensor and the same per row with eac
 scale floored at 0.1 x the tensor's (parity_helpers; the newer tests floor bf16 rows at
 1e-3).
 """
-import math
-
 import pytest
 import torch
 

@@ -1,6 +1,4 @@
 """Topology ingest: the safe edge_index.pt loader (CPU) and the device coalesce / bidirect / CSR build (GPU)."""
-import os
-
 import numpy as np
 import pytest
 import torch

@@ -1,5 +1,4 @@
 """Edge-build planning (a4): working-set estimates and the sharded on-GPU build."""
-import numpy as np
 import pytest
 import torch
 
