@@ -12,8 +12,8 @@ The default run measures c2 (the configuration the north-star target is quoted
 on) and, in the same JSON line, a c3 record whose working set exceeds the
 256 MB Infinity Cache (`extra_configs`), each with its own roofline.
 
-`value` is the attention layer's throughput under the gather model (SURVEY
-8(d) v1: every gathered K/V/q/dO row counted at full size per edge) =
+`value` is the attention layer's throughput under the gather model (every
+gathered K/V/q/dO row counted at full size per edge, the row streams once) =
 algorithmic bytes / fwd+bwd time. It is a work rate, not an HBM rate: at c2 the
 gathered rows are served from the Infinity Cache and it exceeds the 8 TB/s HBM
 peak. Beside it: the compulsory (unique-tensor) bytes and their rate, a lower
@@ -60,8 +60,10 @@ CONFIGS = {
 
 
 def attention_bytes(s, D, H, n_q, n_kv, nnz):
-    """Gather-model algorithmic bytes (forward, backward) of one layer (as built: the
-    backward does not read the forward's output, so v1's O read is left out)."""
+    """Gather-model algorithmic bytes (forward, backward) of one layer: every gathered row at full size per
+    edge, every streamed row once. Forward: Q read, O written, K and V per edge, kv ids, Z. Backward: dO and
+    Q read, dQ written, K and V per edge (dq pass), Q and dO per edge (dk/dv pass), dK and dV written, the
+    row statistics, kv ids, reverse ids and positions (the backward does not read the forward's output)."""
     a_fwd = s * D * (2 * n_q + 2 * nnz) + 4 * nnz + 4 * n_q * H
     a_bwd = s * D * (3 * n_q + 2 * n_kv + 4 * nnz) + 8 * n_q * H + 8 * nnz * H + 12 * nnz
     return a_fwd, a_bwd
@@ -461,8 +463,8 @@ def run(config, steps, warmup, chunk=None, item=None, with_cpu=True):
         "metric": METRIC,
         "value": round(attn_gbs, 1),
         "unit": "GB/s",
-        "value_basis": "attention layer fwd+bwd under the gather model (SURVEY 8(d) v1: every gathered row counted "
-                       "at full size per edge) / its HIP-event time; a work rate, not HBM bandwidth (gathered rows "
+        "value_basis": "attention layer fwd+bwd under the gather model (every gathered row counted at full size "
+                       "per edge) / its HIP-event time; a work rate, not HBM bandwidth (gathered rows "
                        "served from the 256 MB Infinity Cache count in full); compulsory HBM bytes are under "
                        "attention.compulsory_*",
         "n_gpus": 1,
