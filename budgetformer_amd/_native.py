@@ -59,6 +59,12 @@ _SIGS = {
     "bf_random_walk_starts": (C.c_int, [P_i64, P_i32, i64, P_i64, i64, i32, P_f32, u64, u64, u64, P_i64, vp]),
     "bf_hop_pool_workspace_size": (C.c_int, [i64, i32, i32, C.POINTER(sz)]),
     "bf_hop_pool": (C.c_int, [P_i64, i64, i32, i32, P_i64, P_i64, C.POINTER(i64), vp, sz, vp]),
+    "bf_fanout_sample": (C.c_int, [P_i64, P_i32, i64, i32, i32, u64, u64, P_i32, P_i32, vp]),
+    "bf_frontier_offsets_workspace_size": (C.c_int, [i64, C.POINTER(sz)]),
+    "bf_frontier_offsets": (C.c_int, [P_i32, i64, P_i64, P_i32, P_i64, vp, sz, vp]),
+    "bf_frontier_expand": (C.c_int, [P_i32, P_i32, i64, P_i64, P_i64, P_i32, i32, P_i32, P_i32, vp]),
+    "bf_frontier_emit_workspace_size": (C.c_int, [i64, C.POINTER(sz)]),
+    "bf_frontier_emit": (C.c_int, [P_i32, P_i32, i64, P_i64, P_i64, P_i64, vp, sz, vp]),
     "bf_chung_lu_workspace_size": (C.c_int, [i64, i64, C.POINTER(sz)]),
     "bf_chung_lu": (C.c_int, [i64, i64, C.c_double, C.c_double, C.c_double, u64, P_i64, P_i32, C.POINTER(i64), vp, sz,
                               vp]),

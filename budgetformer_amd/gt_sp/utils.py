@@ -291,6 +291,29 @@ def build_head_hop_edges(edge_index: torch.Tensor, num_nodes: int, num_heads: in
                                            u=u, seed=seed)[0]
 
 
+def compute_khop_pool_dgl_neighbor(edge_index: torch.Tensor, num_nodes: int, fanout: List[int], device="cpu",
+                                   min_hop: int = 1, seed: int = None) -> torch.Tensor:
+    """Fanout k-hop pool (gt_sp/utils.py:1281-1384) on the HIP device: hop d samples up to fanout[d-1]
+    out-neighbours of each frontier node (-1: all of them), one sample per node and hop shared by every
+    frontier entry at that node, and from ``min_hop`` on emits (neighbour -> origin query) pairs, self pairs
+    dropped. Returns [2, E] int64 on ``device`` (row 0 key/value node, row 1 query), hop-major.
+
+    Parallel edges stay separate edges, as in ``dgl.graph``. DGL's sampler RNG is not reproduced: Philox
+    keyed by ``seed`` (default: drawn from torch's generator, as the walk seed is) defines the samples."""
+    from .. import hip_ops
+    out_dev = torch.device(device)
+    k = len(fanout)
+    if edge_index.numel() == 0 or k == 0:
+        return torch.zeros((2, 0), dtype=torch.long, device=out_dev)
+    dev = out_dev if out_dev.type == "cuda" else torch.device("cuda", torch.cuda.current_device())
+    n = max(int(num_nodes), int(edge_index.max().item()) + 1)
+    ei = edge_index.to(dev)
+    rowptr, col = hip_ops.coo_to_csr(torch.stack([ei[1], ei[0]]), n, n)     # out-neighbour CSR
+    seed = _draw_walk_seed() if seed is None else int(seed)
+    return hip_ops.khop_fanout_pool(rowptr, col, [int(f) for f in fanout], seed=seed,
+                                    min_hop=int(min_hop)).to(out_dev)
+
+
 def _merge_edge_index_list(edge_list):
     """Merge edge lists (gt_sp/utils.py:877-887): >= 2 non-empty parts are concatenated and
     coalesced on the device; a single part passes through; none returns the first entry."""

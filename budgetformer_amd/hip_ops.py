@@ -26,6 +26,11 @@ def _p(t: Optional[torch.Tensor]):
     return None if t is None else C.c_void_p(t.data_ptr())
 
 
+def _u64(x: int) -> int:
+    """A seed or offset as the uint64 the library takes (two's complement for negatives)."""
+    return int(x) & (2 ** 64 - 1)
+
+
 def _stream(device: torch.device):
     """The current HIP stream of ``device`` as a raw handle (what torch.cuda.current_stream(device).cuda_stream
     gives, without building a Stream object on every call). Every library call takes its stream from the
@@ -109,6 +114,69 @@ def hop_pool(walks: torch.Tensor, min_hop: int = 1) -> torch.Tensor:
     N.call("bf_hop_pool", _p(walks), n, L, min_hop, C.c_void_p(out[0].data_ptr()), C.c_void_p(out[1].data_ptr()),
            C.byref(cnt), _p(ws), ws.numel(), _stream(dev))
     return out[:, : cnt.value]
+
+
+MAX_FANOUT = 64          # largest sampled fanout (BF_MAX_FANOUT); -1 takes every neighbour at any degree
+
+
+def fanout_sample(rowptr: torch.Tensor, col: torch.Tensor, fanout: int, hop: int, seed: int = 0, offset: int = 0):
+    """Every node's hop-``hop`` sample of at most ``fanout`` out-neighbours (bf_fanout_sample):
+    (cnt int32 [N], sel int32 [N, fanout])."""
+    dev = rowptr.device
+    _require(rowptr, "rowptr", torch.int64)
+    _require(col, "col", torch.int32, dev)
+    if not 1 <= int(fanout) <= MAX_FANOUT:
+        raise ValueError(f"fanout {fanout} outside [1, {MAX_FANOUT}] (-1 takes every neighbour without a sample)")
+    n = rowptr.numel() - 1
+    cnt = torch.empty(max(n, 1), dtype=torch.int32, device=dev)[:n]
+    sel = torch.empty(max(n * int(fanout), 1), dtype=torch.int32, device=dev)
+    N.call("bf_fanout_sample", _p(rowptr), _p(col), n, int(fanout), int(hop), _u64(seed), _u64(offset), _p(cnt),
+           _p(sel), _stream(dev))
+    return cnt, sel[: n * int(fanout)].view(n, int(fanout))
+
+
+def khop_fanout_pool(rowptr: torch.Tensor, col: torch.Tensor, fanout, seed: int = 0, offset: int = 0,
+                     min_hop: int = 1) -> torch.Tensor:
+    """Fanout k-hop pool [2, M] int64 (kv, query) over the out-CSR (rowptr, col): hop-major, then frontier
+    order (compute_khop_pool_dgl_neighbor, gt_sp/utils.py:1281-1384). ``fanout``: one entry per hop, -1 for
+    every neighbour; one host read per hop (the next frontier's size) and one per emitted hop."""
+    dev = rowptr.device
+    _require(rowptr, "rowptr", torch.int64)
+    _require(col, "col", torch.int32, dev)
+    n = rowptr.numel() - 1
+    origin = torch.arange(n, dtype=torch.int32, device=dev)
+    cur = origin.clone()
+    parts = []
+    for d, f in enumerate([int(x) for x in fanout], start=1):
+        m = cur.numel()
+        if m == 0 or f == 0:
+            break
+        if f < 0:
+            ptr, cnt, ids, stride = rowptr, None, col, 0
+        else:
+            cnt, sel = fanout_sample(rowptr, col, f, d, seed, offset)
+            ptr, ids, stride = None, sel.reshape(-1), f
+        offs = torch.empty(m + 1, dtype=torch.int64, device=dev)
+        ws = _workspace(_size_query("bf_frontier_offsets_workspace_size", m), dev)
+        N.call("bf_frontier_offsets", _p(cur), m, _p(ptr), _p(cnt), _p(offs), _p(ws), ws.numel(), _stream(dev))
+        total = int(offs[m].item())
+        if total == 0:             # no frontier node has a successor: later hops are empty too
+            break
+        new_origin = torch.empty(total, dtype=torch.int32, device=dev)
+        new_cur = torch.empty(total, dtype=torch.int32, device=dev)
+        N.call("bf_frontier_expand", _p(origin), _p(cur), m, _p(offs), _p(ptr), _p(ids), stride, _p(new_origin),
+               _p(new_cur), _stream(dev))
+        origin, cur = new_origin, new_cur
+        if d >= min_hop:
+            out = torch.empty(2, total, dtype=torch.int64, device=dev)
+            count = torch.zeros(1, dtype=torch.int64, device=dev)
+            ws = _workspace(_size_query("bf_frontier_emit_workspace_size", total), dev)
+            N.call("bf_frontier_emit", _p(origin), _p(cur), total, C.c_void_p(out[0].data_ptr()),
+                   C.c_void_p(out[1].data_ptr()), _p(count), _p(ws), ws.numel(), _stream(dev))
+            parts.append(out[:, : int(count.item())])
+    if not parts:
+        return torch.zeros((2, 0), dtype=torch.int64, device=dev)
+    return torch.cat(parts, dim=1)
 
 
 def coalesce(edge_index: torch.Tensor, num_nodes: int) -> torch.Tensor:

@@ -16,7 +16,7 @@ from .. import hip_ops
 from ..edges import build_attention_edges
 from ..graph import CSRGraph
 from ..gt_sp.utils import (_draw_walk_seed, _merge_edge_index_list, build_head_hop_edges,  # noqa: F401
-                           fix_edge_index)
+                           compute_khop_pool_dgl_neighbor, fix_edge_index)
 from ..probe import reception_cone
 
 _GRAPHORMER_VIRTUAL_NODE_MODELS = frozenset({"graphormer"})   # utils/fullgraph_sp_support.py:60-63
@@ -131,10 +131,8 @@ def _use_real_edges_for_state(args, edge_budget_state=None, adaptive_edge_budget
 
 
 def _use_rw_edges(args, edge_budget_state=None, adaptive_edge_budget_cfg=None) -> bool:
-    """utils/fullgraph_sp_support.py:905-916 (the DGL fanout mode is not on this path)."""
-    if _rw_edge_mode(args) != "random_walk":
-        raise NotImplementedError("rw_edge_mode 'dgl_neighbor' (DGL fanout sampling) is not on the HIP path")
-    if int(getattr(args, "walks_per_node", 0)) <= 0:
+    """utils/fullgraph_sp_support.py:905-916 (the fanout mode needs no walks_per_node)."""
+    if _rw_edge_mode(args) != "dgl_neighbor" and int(getattr(args, "walks_per_node", 0)) <= 0:
         return False
     if _fixed_edge_budget_enabled(args, adaptive_edge_budget_cfg) or \
             _random_block_sampling_enabled(args, adaptive_edge_budget_cfg):
@@ -143,7 +141,21 @@ def _use_rw_edges(args, edge_budget_state=None, adaptive_edge_budget_cfg=None) -
 
 
 def _rw_edge_mode(args) -> str:
-    return str(getattr(args, "rw_edge_mode", "random_walk"))
+    mode = str(getattr(args, "rw_edge_mode", "random_walk"))
+    if mode not in ("random_walk", "dgl_neighbor"):
+        raise ValueError(f"unknown rw_edge_mode {mode!r} (random_walk or dgl_neighbor)")
+    return mode
+
+
+def _parse_fanout(fanout) -> list:
+    """utils/fullgraph_sp_support.py:1642-1653: "10,5", [10, 5] or (10, 5) -> [10, 5]; -1 is every
+    neighbour at that hop; None or empty -> [10, 5]."""
+    if fanout is None:
+        return [10, 5]
+    items = list(fanout) if isinstance(fanout, (list, tuple)) else \
+        [p for p in str(fanout).replace(" ", "").split(",") if p != ""]
+    parsed = [int(x) for x in items]
+    return parsed if parsed else [10, 5]
 
 
 def _sample_edges_per_query_random(edge_index, max_edges_per_query: int, seed: int, *, dst_stats=None):
@@ -186,21 +198,26 @@ def _build_or_retrieve_full_rw_pool(args, edge_index_global, num_nodes, rw_devic
     node, kept in a single-slot cache on ``args`` keyed by everything that shapes it.
 
     The walk is the device kernel (Philox keyed by ``edge_seed`` and the global
-    walk id, so it draws what the fused builder draws); the pool lives on
-    ``rw_device`` (copied there when that is the host).
+    walk id, so it draws what the fused builder draws); rw_edge_mode
+    "dgl_neighbor" takes the fanout k-hop pool (``compute_khop_pool_dgl_neighbor``,
+    fanout from ``args.fanout``) instead. The pool lives on ``rw_device`` (copied
+    there when that is the host).
     """
     mode = _rw_edge_mode(args)
-    if mode != "random_walk":
-        raise NotImplementedError("rw_edge_mode 'dgl_neighbor' (DGL fanout sampling) is not on the HIP path")
+    fanout = _parse_fanout(getattr(args, "fanout", "10,5"))
     key = (id(edge_index_global), int(num_nodes), int(walk_length), int(walks_per_node), int(num_heads),
-           int(edge_seed) if edge_seed is not None else None, str(rw_device), mode)
+           int(edge_seed) if edge_seed is not None else None, str(rw_device), mode, tuple(fanout))
     cached = getattr(args, "_cached_full_rw_pool", None)
     if cached is not None and cached.get("key") == key:
         return cached["pool"]
     dev = _hip_device(rw_device)
     seed = _draw_walk_seed() if edge_seed is None else int(edge_seed)
-    pool = build_head_hop_edges(edge_index_global.to(dev), int(num_nodes), int(num_heads), 1, device=dev,
-                                walk_length=int(walk_length), walks_per_node=int(walks_per_node), seed=seed)
+    if mode == "dgl_neighbor":
+        pool = compute_khop_pool_dgl_neighbor(edge_index_global.to(dev), int(num_nodes), fanout, device=dev,
+                                              min_hop=1, seed=seed)
+    else:
+        pool = build_head_hop_edges(edge_index_global.to(dev), int(num_nodes), int(num_heads), 1, device=dev,
+                                    walk_length=int(walk_length), walks_per_node=int(walks_per_node), seed=seed)
     pool = pool.to(torch.device(rw_device))
     args._cached_full_rw_pool = {"key": key, "pool": pool}
     return pool
@@ -276,6 +293,21 @@ def _build_merged_edges(args, edge_index_global, num_nodes, final_device, rw_dev
         if use_rw:
             rw = _build_or_retrieve_full_rw_pool(args, edge_index_global, num_nodes, rw_device, L, P,
                                                  int(getattr(args, "num_heads", 1)), edge_seed).to(dev)
+        if exphormer_rw:
+            return _typed_edges(real, rw, dev).to(out_dev)
+        merged = _merge_edge_index_list([x for x in (real, rw) if x is not None])
+        if merged is None:
+            merged = torch.zeros((2, 0), dtype=torch.long, device=dev)
+        return (fix_edge_index(merged.to(torch.long), int(num_nodes)) if token else merged).to(out_dev)
+
+    if use_rw and _rw_edge_mode(args) == "dgl_neighbor":
+        # the fused builder walks; a fanout pool is ranked per query as the reference's pipeline does:
+        # real part and RW part each by the edge key, then merged (utils/fullgraph_sp_support.py:2943-3026)
+        real = _resolve_real_edges_for_state(args, edge_index_global, dev, edge_seed, edge_budget_state,
+                                             adaptive_edge_budget_cfg)
+        pool = _build_or_retrieve_full_rw_pool(args, edge_index_global, num_nodes, rw_device, L, P,
+                                               int(getattr(args, "num_heads", 1)), edge_seed)
+        rw = _resolve_rw_edges_for_state(args, pool.to(dev), edge_seed, edge_budget_state, adaptive_edge_budget_cfg)
         if exphormer_rw:
             return _typed_edges(real, rw, dev).to(out_dev)
         merged = _merge_edge_index_list([x for x in (real, rw) if x is not None])

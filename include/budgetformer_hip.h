@@ -92,6 +92,41 @@ int bf_hop_pool(const int64_t* walks, int64_t n_walks, int32_t walk_length, int3
                 int64_t* pool_kv, int64_t* pool_q, int64_t* count_host,
                 void* workspace, size_t workspace_bytes, void* stream);
 
+/* The fanout k-hop pool, the "dgl_neighbor" alternative to the walk pool
+ * (compute_khop_pool_dgl_neighbor, gt_sp/utils.py:1281-1384), run hop by hop by
+ * the host. The frontier starts as (origin u, node u) for every node; hop d
+ * replaces each entry (o, c) by (o, s) for each s in node c's hop-d sample and,
+ * from min_hop on, emits the pool pair (kv = s, q = o) when s != o.
+ *
+ * bf_fanout_sample: node u's hop sample of out-neighbours into sel[u*fanout ..]
+ * (count in cnt[u]): all of them, in CSR order, when out-degree <= fanout; else
+ * `fanout` distinct ones by Floyd's algorithm over Philox words (counter = (u,
+ * offset + hop * 2^32 + i / 4), key = seed, word i % 4, t = hi32(word * (j+1))
+ * for j = deg - fanout + i), in ascending index order. DGL's sampler RNG is not
+ * reproduced (sample_neighbors, gt_sp/utils.py:1330-1333); a fanout of -1 (all
+ * neighbours) needs no sample: pass the CSR to the frontier calls instead. */
+#define BF_MAX_FANOUT 64
+int bf_fanout_sample(const int64_t* rowptr, const int32_t* col, int64_t num_nodes, int32_t fanout, int32_t hop,
+                     uint64_t seed, uint64_t offset, int32_t* cnt, int32_t* sel, void* stream);
+/* offsets [n+1] int64 of the next frontier: the exclusive scan of each entry's
+ * sample size, from a sample's cnt (ptr NULL) or a CSR's ptr (cnt NULL); the
+ * next frontier's size is offsets[n]. Workspace: bf_frontier_offsets_workspace_size. */
+int bf_frontier_offsets_workspace_size(int64_t n, size_t* bytes);
+int bf_frontier_offsets(const int32_t* cur, int64_t n, const int64_t* ptr, const int32_t* cnt, int64_t* offsets,
+                        void* workspace, size_t workspace_bytes, void* stream);
+/* The next frontier: entry i writes (origin[i], s) at offsets[i] for each s of
+ * its node c's sample, read from ids[c*stride ..] (a sample table, stride =
+ * fanout) or ids[ptr[c] ..] (a CSR, stride 0). */
+int bf_frontier_expand(const int32_t* origin, const int32_t* cur, int64_t n, const int64_t* offsets,
+                       const int64_t* ptr, const int32_t* ids, int32_t stride, int32_t* new_origin, int32_t* new_cur,
+                       void* stream);
+/* The frontier's pool pairs in order: kv[k] = cur[i], q[k] = origin[i] for
+ * every i with cur[i] != origin[i] (capacity n each); count: device int64[1].
+ * Workspace: bf_frontier_emit_workspace_size. */
+int bf_frontier_emit_workspace_size(int64_t n, size_t* bytes);
+int bf_frontier_emit(const int32_t* origin, const int32_t* cur, int64_t n, int64_t* kv, int64_t* q, int64_t* count,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
 /* The Philox uniforms bf_random_walk draws when u == NULL, written as the
  * float32 [n_q*P, L] tensor that reproduces them through the u argument. */
 int bf_walk_uniforms(int64_t q_lo, int64_t n_q, int32_t walks_per_node, int32_t walk_length,

@@ -8,6 +8,8 @@ Reference call chain restated here (all paths relative to the reference root):
     _resolve_real_edges_for_state  utils/fullgraph_sp_support.py:1312-1491
     _build_or_retrieve_full_rw_pool utils/fullgraph_sp_support.py:1656-1740
       build_head_hop_edges           gt_sp/utils.py:1251-1278
+      compute_khop_pool_dgl_neighbor gt_sp/utils.py:1281-1384 (rw_edge_mode
+                                     "dgl_neighbor"; sampler RNG defined here)
       compute_hop_buckets_random_walk gt_sp/utils.py:1074-1248
       _get_random_walk_graph         gt_sp/utils.py:890-936
       _run_random_walk               gt_sp/utils.py:1387-1473 (torch_cluster 1.6.3 /
@@ -35,6 +37,10 @@ Pinning (tests/test_oracle_edges.py):
                     neighbour at u=0 / u=1-2^-24, an fp32-vs-fp64 rounding case
   hop_edges         hand-built walks with known pools (d=1 self-edge kept,
                     later stays dropped)
+  khop_fanout_pool  all-neighbour hops against path counts (powers of the
+                    adjacency matrix); samples shared per node and hop
+  fanout_sample     subsets of the right size of distinct out-neighbours,
+                    every neighbour equally likely (chi-square over seeds)
   sample_*          brute-force Python loops on small inputs; the sort branch
                     and the minhash branch agree as multisets
   merge/fix         Python set union; closed-form virtual edges
@@ -136,6 +142,88 @@ def hop_edges_from_walks(walks: np.ndarray, min_hop: int = 1) -> np.ndarray:
     if not parts:
         return np.zeros((2, 0), dtype=np.int64)
     return np.concatenate(parts, axis=1)
+
+
+def fanout_sample(rowptr, col, num_nodes: int, fanout: int, hop: int, seed: int, offset: int = 0):
+    """One hop's neighbour sample of every node (the sampler behind compute_khop_pool_dgl_neighbor,
+    gt_sp/utils.py:1330-1333, ``dgl.sampling.sample_neighbors(g, nodes, fanout, edge_dir="out")``), as a
+    CSR (ptr [N+1], ids). DGL's sampler RNG is not reproducible outside DGL (parity unpinned, as the walk's);
+    the build defines the sample: a node with deg <= fanout (or fanout -1) keeps all its out-neighbours in
+    CSR order; otherwise Floyd's algorithm draws `fanout` distinct indices of [0, deg): for i = 0..f-1 and
+    j = deg - f + i, t = hi32(r_i * (j + 1)) with r_i word i % 4 of Philox(counter = (u_lo, u_hi, b_lo,
+    b_hi), key = seed), b = offset + hop * 2^32 + i // 4; t joins the sample unless it is already in it,
+    then j does. The sample is kept in ascending index order."""
+    from .philox import philox4x32_10
+    rowptr = np.asarray(rowptr, dtype=np.int64)
+    col = np.asarray(col, dtype=np.int64)
+    deg = np.diff(rowptr)
+    f = int(fanout)
+    take = deg if f < 0 else np.minimum(deg, f)
+    ptr = np.concatenate([[0], np.cumsum(take)]).astype(np.int64)
+    ids = np.empty(int(ptr[-1]), dtype=np.int64)
+    big = np.nonzero(deg > f)[0] if f >= 0 else np.zeros(0, dtype=np.int64)
+    small = np.ones(num_nodes, dtype=bool)
+    small[big] = False
+    for u in np.nonzero(small)[0]:
+        ids[ptr[u]:ptr[u + 1]] = col[rowptr[u]:rowptr[u + 1]]
+    if big.size and f > 0:
+        seed = int(seed) & 0xFFFFFFFFFFFFFFFF
+        key = (seed & 0xFFFFFFFF, seed >> 32)
+        uu = big.astype(np.uint64)
+        words = np.empty((big.size, f), dtype=np.uint64)
+        for blk in range((f + 3) // 4):
+            b = (int(offset) + (int(hop) << 32) + blk) & 0xFFFFFFFFFFFFFFFF
+            ctr = np.stack([uu & np.uint64(0xFFFFFFFF), uu >> np.uint64(32), np.full_like(uu, b & 0xFFFFFFFF),
+                            np.full_like(uu, b >> 32)], axis=-1)
+            r = philox4x32_10(ctr, key).astype(np.uint64)
+            for w in range(4):
+                i = blk * 4 + w
+                if i < f:
+                    words[:, i] = r[:, w]
+        for row, u in enumerate(big):
+            d = int(deg[u])
+            chosen = []
+            for i in range(f):
+                j = d - f + i
+                t = int((int(words[row, i]) * (j + 1)) >> 32)
+                chosen.append(j if t in chosen else t)
+            chosen.sort()
+            ids[ptr[u]:ptr[u + 1]] = col[rowptr[u] + np.asarray(chosen, dtype=np.int64)]
+    return ptr, ids
+
+
+def khop_fanout_pool(rowptr, col, num_nodes: int, fanout, seed: int = 0, offset: int = 0, min_hop: int = 1,
+                     samples=None) -> np.ndarray:
+    """compute_khop_pool_dgl_neighbor (gt_sp/utils.py:1281-1384) -> pool [2, M] (row 0 kv, row 1 query).
+
+    The frontier starts as (origin u, node u) for every node. Hop d (1-based) replaces every entry
+    (o, c) by (o, s) for each s in c's hop-d sample, in order -- one sample per node and hop, shared by
+    every entry at that node (the reference samples the frontier's unique nodes once) -- and, from
+    min_hop on, emits (s -> o) for s != o; self pairs stay in the frontier. Hop-major, then frontier
+    order. ``samples`` (a list of per-hop (ptr, ids) CSRs) replaces the sampler, to test the expansion
+    on given samples."""
+    fanout = list(fanout)
+    rowptr = np.asarray(rowptr, dtype=np.int64)
+    origin = np.arange(num_nodes, dtype=np.int64)
+    cur = origin.copy()
+    parts = []
+    for d in range(1, len(fanout) + 1):
+        if cur.size == 0:
+            break
+        ptr, ids = samples[d - 1] if samples is not None else fanout_sample(rowptr, col, num_nodes, fanout[d - 1],
+                                                                              d, seed, offset)
+        cnt = ptr[cur + 1] - ptr[cur]
+        new_origin = np.repeat(origin, cnt)
+        first = np.repeat(ptr[cur], cnt)
+        within = np.arange(int(cnt.sum()), dtype=np.int64) - np.repeat(np.cumsum(cnt) - cnt, cnt)
+        new_cur = ids[first + within] if within.size else np.zeros(0, dtype=np.int64)
+        if d >= min_hop:
+            keep = new_cur != new_origin
+            parts.append(np.stack([new_cur[keep], new_origin[keep]]))
+        origin, cur = new_origin, new_cur
+    if not parts:
+        return np.zeros((2, 0), dtype=np.int64)
+    return np.concatenate(parts, axis=1).astype(np.int64)
 
 
 def walk_starts(num_nodes: int, walks_per_node: int, q_lo: int = 0, q_hi: int | None = None) -> np.ndarray:

@@ -244,3 +244,103 @@ def test_query_range_build_equals_rows_of_full_build():
         for lo, cnt in ((0, n), (100, 70), (350, 50)):
             t, l = et.build_edge_table(rowptr, col, n, b_r, b_w, 4, 2, 9, u[lo * 2:(lo + cnt) * 2], q_lo=lo, n_q=cnt)
             assert np.array_equal(t, full_t[lo:lo + cnt]) and np.array_equal(l, full_l[lo:lo + cnt])
+
+
+def _digraph(n, m, seed):
+    rng = np.random.default_rng(seed)
+    src, dst = rng.integers(0, n, m), rng.integers(0, n, m)
+    keep = src != dst
+    return et.csr_from_coo(np.stack([src[keep], dst[keep]]), n)
+
+
+def _hop_parts(rowptr, col, n, fanout, seed=0, samples=None):
+    """The pool of each hop separately (the pool of hops 1..d minus that of hops 1..d-1)."""
+    parts, prev = [], 0
+    for d in range(1, len(fanout) + 1):
+        pool = et.khop_fanout_pool(rowptr, col, n, fanout[:d], seed=seed,
+                                   samples=None if samples is None else samples[:d])
+        parts.append(pool[:, prev:])
+        prev = pool.shape[1]
+    return parts
+
+
+def _counts(pool, n):
+    c = np.zeros((n, n), dtype=np.int64)
+    np.add.at(c, (pool[1], pool[0]), 1)         # c[query, kv]
+    return c
+
+
+def test_khop_all_neighbours_equals_path_counts():
+    """fanout -1 at every hop: hop d emits, per origin u and node v != u, one pair per d-step out-path
+    u -> ... -> v, which is (A^d)[u, v]."""
+    n = 30
+    rowptr, col = _digraph(n, 120, 3)
+    A = np.zeros((n, n), dtype=np.int64)
+    A[np.repeat(np.arange(n), np.diff(rowptr)), col] = 1
+    Ad = np.eye(n, dtype=np.int64)
+    for d, part in enumerate(_hop_parts(rowptr, col, n, [-1, -1, -1]), start=1):
+        Ad = Ad @ A
+        want = Ad.copy()
+        np.fill_diagonal(want, 0)
+        assert np.array_equal(_counts(part, n), want), d
+
+
+def test_khop_expansion_follows_the_given_samples():
+    """With injected samples the hop-d counts are the products of the sampled adjacencies A_1 ... A_d
+    (one sample per node and hop, shared by every path through that node)."""
+    n = 25
+    rowptr, col = _digraph(n, 150, 8)
+    rng = np.random.default_rng(1)
+    samples, mats = [], []
+    for d in range(3):
+        ptr, ids = [0], []
+        M = np.zeros((n, n), dtype=np.int64)
+        for u in range(n):
+            nb = col[rowptr[u]:rowptr[u + 1]]
+            pick = sorted(rng.choice(nb, min(len(nb), 2), replace=False).tolist()) if len(nb) else []
+            ids += pick
+            ptr.append(len(ids))
+            M[u, pick] += 1
+        samples.append((np.array(ptr), np.array(ids, dtype=np.int64)))
+        mats.append(M)
+    P = np.eye(n, dtype=np.int64)
+    for d, part in enumerate(_hop_parts(rowptr, col, n, [2, 2, 2], samples=samples), start=1):
+        P = P @ mats[d - 1]
+        want = P.copy()
+        np.fill_diagonal(want, 0)
+        assert np.array_equal(_counts(part, n), want), d
+
+
+def test_fanout_sample_subsets_of_distinct_neighbours():
+    rowptr, col = _digraph(200, 3000, 4)
+    for f in (0, 1, 3, 8, 40):
+        ptr, ids = et.fanout_sample(rowptr, col, 200, f, hop=2, seed=11)
+        for u in range(200):
+            nb = col[rowptr[u]:rowptr[u + 1]]
+            got = ids[ptr[u]:ptr[u + 1]]
+            assert len(got) == min(len(nb), f)
+            assert len(set(got.tolist())) == len(got) and set(got.tolist()) <= set(nb.tolist())
+            assert np.all(np.diff(got) > 0)                   # ascending index order = ascending id here
+            if len(nb) <= f:
+                assert np.array_equal(got, nb)
+    ptr, ids = et.fanout_sample(rowptr, col, 200, -1, hop=1, seed=11)
+    assert np.array_equal(ptr, rowptr) and np.array_equal(ids, col)
+
+
+def test_fanout_sample_is_uniform_and_depends_on_seed_and_hop():
+    """A hub with 40 out-neighbours sampled 10 at a time: over 2000 seeds every neighbour is chosen
+    about 500 times (chi-square, 39 degrees of freedom); hop and seed change the draw."""
+    deg, f, trials = 40, 10, 2000
+    rowptr = np.array([0, deg] + [deg] * deg, dtype=np.int64)
+    col = np.arange(1, deg + 1, dtype=np.int64)
+    n = deg + 1
+    hits = np.zeros(n, dtype=np.int64)
+    for s in range(trials):
+        ptr, ids = et.fanout_sample(rowptr, col, n, f, hop=1, seed=s)
+        hits[ids[ptr[0]:ptr[1]]] += 1
+    expect = trials * f / deg
+    chi2 = (((hits[1:] - expect) ** 2) / expect).sum()
+    assert chi2 < 80.0                                  # P(chi2_39 > 80) < 1e-4
+    a = et.fanout_sample(rowptr, col, n, f, hop=1, seed=5)[1]
+    assert not np.array_equal(a, et.fanout_sample(rowptr, col, n, f, hop=2, seed=5)[1])
+    assert not np.array_equal(a, et.fanout_sample(rowptr, col, n, f, hop=1, seed=6)[1])
