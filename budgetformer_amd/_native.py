@@ -95,6 +95,8 @@ _SIGS = {
     "bf_reverse_index_packed_workspace_size": (C.c_int, [i64, C.POINTER(sz)]),
     "bf_reverse_index_packed": (C.c_int, [vp, P_i64, i64, i64, i64, i32, i32, i32, i64, vp, P_i64, P_i32, P_i32,
                                           vp, sz, vp]),
+    "bf_radix_sort_workspace_size": (C.c_int, [i64, i32, i32, C.POINTER(sz)]),
+    "bf_radix_sort_keys": (C.c_int, [vp, vp, i64, i32, i32, vp, sz, vp]),
     "bf_reverse_entries": (C.c_int, [vp, P_i64, i64, i64, i32, i32, i32, i64, P_i32, vp]),
     "bf_expand_rows": (C.c_int, [P_i64, i64, i64, P_i64, vp]),
     "bf_split_item_capacity": (i64, [i64, i32, i32]),

@@ -3,10 +3,13 @@
 // used by the deterministic dK/dV pass and by the COO adaptor, and split plans
 // for rows longer than the attention chunk.
 //
-// Sorting and prefix sums use rocPRIM (bf_prim.h; its LSD radix sort is stable,
-// which makes the reverse index ordered by (kv, CSR position) = (src, dst)).
+// The reverse index of a table is sorted by this build's own radix sort
+// (bf_sort.h); the other sorts and the prefix sums use rocPRIM (bf_prim.h).
+// Both sorts are stable LSD radix sorts, which makes the reverse index ordered
+// by (kv, CSR position) = (src, dst).
 #include "bf_common.h"
 #include "bf_prim.h"
+#include "bf_sort.h"
 
 namespace bf {
 namespace {
@@ -715,10 +718,7 @@ extern "C" int bf_reverse_index(const int64_t* qptr, const int32_t* kv, int64_t 
 
 extern "C" int bf_reverse_index_packed_workspace_size(int64_t nnz, size_t* bytes) {
   BF_CHECK_ARG(bytes && nnz >= 0, "reverse_index_packed_workspace_size: bad arguments");
-  size_t sort_bytes = 0;
-  (void)prim::sort_keys(nullptr, sort_bytes, static_cast<const uint64_t*>(nullptr), static_cast<uint64_t*>(nullptr),
-                        nnz > 0 ? nnz : 1, 0, 64, hipStream_t(nullptr));
-  *bytes = align_up(sort_bytes) + 256;
+  *bytes = sort::workspace_bytes_max(nnz) + 256;
   return BF_OK;
 }
 
@@ -750,15 +750,29 @@ extern "C" int bf_reverse_index_packed(const uint64_t* rkey, const int64_t* qptr
   }
   BF_CHECK_ARG(kq && (n_keys == 0 || (rkey && sorted)), "reverse_index_packed: null tensor");
   if (n_keys > 0) {
-    size_t tb = workspace_bytes;
     // only the id bits are sorted; the stable passes keep each id's entries in CSR order
-    BF_CHECK_HIP(prim::sort_keys(workspace, tb, rkey, sorted, n_keys, kshift, kshift + id_bits, st));
+    const int rc = sort::radix_sort_keys(rkey, sorted, n_keys, kshift, kshift + id_bits, workspace, workspace_bytes,
+                                         st);
+    if (rc) return rc;
   }
   BF_LAUNCH("unpack_rkey_kernel", unpack_rkey_kernel,
             dim3(unsigned(ceil_div(n_keys + 1, int64_t(kThreads) * kUnpackPerThread))), dim3(kThreads), 0, st, sorted,
             n_keys, kshift, slot_bits, tl, qptr, n_kv, kptr, kq, ke);
   BF_CHECK_LAUNCH();
   return launch_token_reverse(tl, qptr, kq, ke, st);
+}
+
+extern "C" int bf_radix_sort_workspace_size(int64_t n, int32_t begin_bit, int32_t end_bit, size_t* bytes) {
+  BF_CHECK_ARG(bytes && n >= 0 && begin_bit >= 0 && begin_bit <= end_bit && end_bit <= 64,
+               "radix_sort_workspace_size: bad arguments");
+  *bytes = sort::workspace_bytes(n, end_bit - begin_bit);
+  return BF_OK;
+}
+
+extern "C" int bf_radix_sort_keys(const uint64_t* in, uint64_t* out, int64_t n, int32_t begin_bit, int32_t end_bit,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  BF_CHECK_ARG(n == 0 || (in && out && in != out), "radix_sort_keys: bad buffers");
+  return sort::radix_sort_keys(in, out, n, begin_bit, end_bit, workspace, workspace_bytes, as_stream(stream));
 }
 
 extern "C" int bf_reverse_entries(const uint64_t* sorted, const int64_t* qptr, int64_t nnz, int64_t n_q,

@@ -582,6 +582,18 @@ def reverse_entries(srt: ReverseKeys, qptr: torch.Tensor) -> torch.Tensor:
     return ke
 
 
+def radix_sort_keys(keys: torch.Tensor, begin_bit: int, end_bit: int) -> torch.Tensor:
+    """``keys`` (int64 holding uint64 bit patterns) stably sorted by bits [begin_bit, end_bit), through the
+    reverse index's radix sort (bf_radix_sort_keys)."""
+    dev = keys.device
+    _require(keys, "keys", torch.int64)
+    n = keys.numel()
+    ws = _workspace(_size_query("bf_radix_sort_workspace_size", n, begin_bit, end_bit), dev)
+    out = torch.empty_like(keys)
+    N.call("bf_radix_sort_keys", _p(keys), _p(out), n, begin_bit, end_bit, _p(ws), ws.numel(), _stream(dev))
+    return out
+
+
 def expand_rows(ptr: torch.Tensor, nnz: int) -> torch.Tensor:
     """Row id (int64) of every CSR entry."""
     _require(ptr, "ptr", torch.int64)

@@ -362,6 +362,16 @@ int bf_reverse_index_packed(const uint64_t* rkey, const int64_t* qptr, int64_t n
                             int32_t q_bits, int32_t slot_bits, int32_t global_token, int64_t token_row,
                             uint64_t* sorted, int64_t* kptr, int32_t* kq, int32_t* ke, void* workspace,
                             size_t workspace_bytes, void* stream);
+/* The stable radix sort bf_reverse_index_packed uses, on its own: in[0, n)
+ * uint64 sorted by bits [begin_bit, end_bit) into out (n < 2^31; in and out
+ * must not overlap). 8- or 9-bit digits, whichever needs fewer passes; each
+ * pass counts digits per tile, scans the counts per digit and scatters. No
+ * counterpart in the reference (torch.sort / coalesce sort inside PyTorch).
+ * Workspace: bf_radix_sort_workspace_size(n, begin_bit, end_bit).          */
+int bf_radix_sort_workspace_size(int64_t n, int32_t begin_bit, int32_t end_bit, size_t* bytes);
+int bf_radix_sort_keys(const uint64_t* in, uint64_t* out, int64_t n, int32_t begin_bit, int32_t end_bit,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
 /* ke [nnz] from bf_reverse_index_packed's sorted keys (the same nnz, n_q,
  * key fields and token arguments).                                         */
 int bf_reverse_entries(const uint64_t* sorted, const int64_t* qptr, int64_t nnz, int64_t n_q, int32_t q_bits,
