@@ -50,6 +50,14 @@ inline Plan make_plan(int64_t n, int bits) {
 
 inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
+// The keys to sort: cap, or, with a device count, *n_dev - n_sub clamped to [0, cap] (the buffers and
+// the grids are sized for cap; the tiles past the count hold nothing).
+__device__ __forceinline__ int64_t live_count(int64_t cap, const int64_t* n_dev, int64_t n_sub) {
+  if (!n_dev) return cap;
+  const int64_t n = *n_dev - n_sub;
+  return n < 0 ? 0 : (n > cap ? cap : n);
+}
+
 // Workspace of make_plan(n, bits): the second key buffer, the per-tile counts and the digit totals.
 inline size_t workspace_bytes(int64_t n, int bits) {
   const Plan p = make_plan(n, bits);
@@ -92,11 +100,13 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* tmp, u
 }
 
 template <int R, int ITEMS>
-__global__ __launch_bounds__(kThreads) void radix_count_kernel(const uint64_t* __restrict__ in, int64_t n,
+__global__ __launch_bounds__(kThreads) void radix_count_kernel(const uint64_t* __restrict__ in, int64_t cap,
+                                                               const int64_t* __restrict__ n_dev, int64_t n_sub,
                                                                int shift, uint32_t mask, int64_t tiles,
                                                                uint32_t* __restrict__ counts) {
   constexpr int B = 1 << R;
   constexpr int64_t TILE = int64_t(kThreads) * ITEMS;
+  const int64_t n = live_count(cap, n_dev, n_sub);
   __shared__ uint32_t h[B];
   for (int i = threadIdx.x; i < B; i += kThreads) h[i] = 0;
   __syncthreads();
@@ -147,14 +157,17 @@ __global__ __launch_bounds__(kThreads) void radix_scan_kernel(uint32_t* __restri
 // and waves in order, follows the input order (the sort is stable).
 template <int R, int ITEMS>
 __global__ __launch_bounds__(kThreads) void radix_scatter_kernel(const uint64_t* __restrict__ in,
-                                                                 uint64_t* __restrict__ out, int64_t n, int shift,
-                                                                 uint32_t mask, int64_t tiles,
+                                                                 uint64_t* __restrict__ out, int64_t cap,
+                                                                 const int64_t* __restrict__ n_dev, int64_t n_sub,
+                                                                 int shift, uint32_t mask, int64_t tiles,
                                                                  const uint32_t* __restrict__ prefix,
                                                                  const uint32_t* __restrict__ totals) {
   constexpr int B = 1 << R;
   constexpr int DPT = B / kThreads;       // digits per thread
   constexpr int64_t TILE = int64_t(kThreads) * ITEMS;
   static_assert(B % kThreads == 0, "whole digits per thread");
+  const int64_t n = live_count(cap, n_dev, n_sub);
+  if (int64_t(blockIdx.x) * TILE >= n) return;   // a tile past the count (uniform over the block)
   __shared__ uint32_t wcnt[kWaves * B];   // per wave: running counts, then exclusive offsets over the waves
   __shared__ uint32_t s_scan[kWaves];
   __shared__ uint32_t dstart[B];          // the tile's first LDS slot of each digit
@@ -240,8 +253,8 @@ __global__ __launch_bounds__(kThreads) void radix_scatter_kernel(const uint64_t*
 }
 
 template <int R, int ITEMS>
-int run_passes(const Plan& p, const uint64_t* in, uint64_t* out, uint64_t* alt, int64_t n, int begin_bit,
-               int end_bit, uint32_t* counts, uint32_t* totals, hipStream_t st) {
+int run_passes(const Plan& p, const uint64_t* in, uint64_t* out, uint64_t* alt, int64_t n, const int64_t* n_dev,
+               int64_t n_sub, int begin_bit, int end_bit, uint32_t* counts, uint32_t* totals, hipStream_t st) {
   for (int pass = 0; pass < p.passes; ++pass) {
     // the last pass writes `out`: pass k writes out when passes - 1 - k is even, alt otherwise
     const uint64_t* src = pass == 0 ? in : ((p.passes - pass) % 2 == 0 ? out : alt);
@@ -250,12 +263,12 @@ int run_passes(const Plan& p, const uint64_t* in, uint64_t* out, uint64_t* alt, 
     const int bits = end_bit - shift < R ? end_bit - shift : R;
     const uint32_t mask = (1u << bits) - 1;
     BF_LAUNCH("radix_count_kernel", (radix_count_kernel<R, ITEMS>), dim3(unsigned(p.tiles)), dim3(kThreads), 0, st,
-              src, n, shift, mask, p.tiles, counts);
+              src, n, n_dev, n_sub, shift, mask, p.tiles, counts);
     BF_CHECK_LAUNCH();
     BF_LAUNCH("radix_scan_kernel", radix_scan_kernel, dim3(1u << R), dim3(kThreads), 0, st, counts, p.tiles, totals);
     BF_CHECK_LAUNCH();
     BF_LAUNCH("radix_scatter_kernel", (radix_scatter_kernel<R, ITEMS>), dim3(unsigned(p.tiles)), dim3(kThreads), 0,
-              st, src, dst, n, shift, mask, p.tiles, counts, totals);
+              st, src, dst, n, n_dev, n_sub, shift, mask, p.tiles, counts, totals);
     BF_CHECK_LAUNCH();
   }
   return BF_OK;
@@ -263,13 +276,17 @@ int run_passes(const Plan& p, const uint64_t* in, uint64_t* out, uint64_t* alt, 
 
 // Sorts in[0, n) by bits [begin_bit, end_bit) into out (stable). in and out
 // must not overlap; the workspace holds workspace_bytes(n, end_bit - begin_bit).
+// With n_dev the count is *n_dev - n_sub, read on the device (n is then a
+// capacity: it sizes the grids; out[count, n) is left as it was).
 inline int radix_sort_keys(const uint64_t* in, uint64_t* out, int64_t n, int begin_bit, int end_bit,
-                           void* workspace, size_t workspace_bytes_given, hipStream_t st) {
+                           void* workspace, size_t workspace_bytes_given, hipStream_t st,
+                           const int64_t* n_dev = nullptr, int64_t n_sub = 0) {
   BF_CHECK_ARG(n >= 0 && n < (int64_t(1) << 31), "radix_sort: %lld keys (at most 2^31 - 1)", (long long)n);
   BF_CHECK_ARG(begin_bit >= 0 && begin_bit <= end_bit && end_bit <= 64, "radix_sort: bits [%d, %d)", begin_bit,
                end_bit);
   if (n == 0) return BF_OK;
   const int bits = end_bit - begin_bit;
+  BF_CHECK_ARG(bits > 0 || !n_dev, "radix_sort: an empty bit range takes a host count");
   if (bits == 0) {
     BF_CHECK_HIP(hipMemcpyAsync(out, in, size_t(n) * 8, hipMemcpyDeviceToDevice, st));
     return BF_OK;
@@ -284,9 +301,10 @@ inline int radix_sort_keys(const uint64_t* in, uint64_t* out, int64_t n, int beg
   auto* totals = reinterpret_cast<uint32_t*>(ws + align256(size_t(n) * 8) +
                                              align256(size_t(p.tiles) * (size_t(1) << p.radix) * 4));
   if (p.radix == 9)
-    return p.items == 8 ? run_passes<9, 8>(p, in, out, alt, n, begin_bit, end_bit, counts, totals, st)
-                        : run_passes<9, 16>(p, in, out, alt, n, begin_bit, end_bit, counts, totals, st);
-  return run_passes<8, 16>(p, in, out, alt, n, begin_bit, end_bit, counts, totals, st);
+    return p.items == 8 ? run_passes<9, 8>(p, in, out, alt, n, n_dev, n_sub, begin_bit, end_bit, counts, totals, st)
+                        : run_passes<9, 16>(p, in, out, alt, n, n_dev, n_sub, begin_bit, end_bit, counts, totals,
+                                            st);
+  return run_passes<8, 16>(p, in, out, alt, n, n_dev, n_sub, begin_bit, end_bit, counts, totals, st);
 }
 
 }  // namespace sort

@@ -255,11 +255,20 @@ __device__ __forceinline__ int32_t entry_of(uint64_t x, int kshift, int sbits, c
 
 constexpr int kUnpackPerThread = 4;  // sorted keys per thread (kThreads apart), loaded before any store
 
+// The table entries that carry a sort key: the index's entries (qptr[n_q], read on the device) less the
+// token's own, clamped to the capacity the buffers and grids were sized for.
+__device__ __forceinline__ int64_t keyed_entries(const int64_t* __restrict__ nnz_dev, int64_t n_token,
+                                                 int64_t cap) {
+  const int64_t n = *nnz_dev - n_token;
+  return n < 0 ? 0 : (n > cap ? cap : n);
+}
+
 // Sorted keys -> kptr (boundaries of the id field), kq, and ke when asked for.
 __global__ __launch_bounds__(kThreads) void unpack_rkey_kernel(
-    const uint64_t* __restrict__ keys, int64_t n_keys, int kshift, int sbits, TokenLayout tl,
-    const int64_t* __restrict__ qptr, int64_t n_kv, int64_t* __restrict__ kptr, int32_t* __restrict__ kq,
-    int32_t* __restrict__ ke) {
+    const uint64_t* __restrict__ keys, const int64_t* __restrict__ nnz_dev, int64_t n_token, int64_t key_cap,
+    int kshift, int sbits, TokenLayout tl, const int64_t* __restrict__ qptr, int64_t n_kv,
+    int64_t* __restrict__ kptr, int32_t* __restrict__ kq, int32_t* __restrict__ ke) {
+  const int64_t n_keys = keyed_entries(nnz_dev, n_token, key_cap);
   const int64_t base = int64_t(blockIdx.x) * (kThreads * kUnpackPerThread) + threadIdx.x;
   uint64_t cur[kUnpackPerThread], prev[kUnpackPerThread];
 #pragma unroll
@@ -296,8 +305,10 @@ __global__ __launch_bounds__(kThreads) void unpack_rkey_kernel(
 // ke from the sorted keys (one thread per key, plus one past the end): with
 // the token row, the thread that meets the first key with id >= r (or the
 // end) also writes kv r's token-row entry (r <= token_len), at kv r's start.
-__global__ void reverse_entries_kernel(const uint64_t* __restrict__ keys, int64_t n_keys, int kshift, int sbits,
-                                       TokenLayout tl, const int64_t* __restrict__ qptr, int32_t* __restrict__ ke) {
+__global__ void reverse_entries_kernel(const uint64_t* __restrict__ keys, const int64_t* __restrict__ nnz_dev,
+                                       int64_t n_token, int64_t key_cap, int kshift, int sbits, TokenLayout tl,
+                                       const int64_t* __restrict__ qptr, int32_t* __restrict__ ke) {
+  const int64_t n_keys = keyed_entries(nnz_dev, n_token, key_cap);
   const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
   if (i > n_keys) return;
   const uint64_t x = i < n_keys ? keys[i] : 0;
@@ -736,7 +747,8 @@ extern "C" int bf_reverse_index_packed(const uint64_t* rkey, const int64_t* qptr
   BF_CHECK_ARG(!tl.tok || (tl.c0 >= 0 && tl.token_len < n_kv), "reverse_index_packed: token layout does not fit "
                "(%lld queries, token row of %lld entries, %lld kv rows)", (long long)n_q, (long long)tl.token_len,
                (long long)n_kv);
-  const int64_t n_keys = nnz - (tl.tok ? tl.c0 + tl.token_len : 0);
+  const int64_t n_token = tl.tok ? tl.c0 + tl.token_len : 0;
+  const int64_t n_keys = nnz - n_token;     // a capacity: the count itself is qptr[n_q] - n_token
   BF_CHECK_ARG(n_keys >= 0, "reverse_index_packed: %lld entries cannot hold the token's %lld", (long long)nnz,
                (long long)(tl.c0 + tl.token_len));
   size_t need = 0;
@@ -752,12 +764,12 @@ extern "C" int bf_reverse_index_packed(const uint64_t* rkey, const int64_t* qptr
   if (n_keys > 0) {
     // only the id bits are sorted; the stable passes keep each id's entries in CSR order
     const int rc = sort::radix_sort_keys(rkey, sorted, n_keys, kshift, kshift + id_bits, workspace, workspace_bytes,
-                                         st);
+                                         st, qptr + n_q, n_token);
     if (rc) return rc;
   }
   BF_LAUNCH("unpack_rkey_kernel", unpack_rkey_kernel,
             dim3(unsigned(ceil_div(n_keys + 1, int64_t(kThreads) * kUnpackPerThread))), dim3(kThreads), 0, st, sorted,
-            n_keys, kshift, slot_bits, tl, qptr, n_kv, kptr, kq, ke);
+            qptr + n_q, n_token, n_keys, kshift, slot_bits, tl, qptr, n_kv, kptr, kq, ke);
   BF_CHECK_LAUNCH();
   return launch_token_reverse(tl, qptr, kq, ke, st);
 }
@@ -782,7 +794,8 @@ extern "C" int bf_reverse_entries(const uint64_t* sorted, const int64_t* qptr, i
   BF_CHECK_ARG(q_bits >= bits_for(uint64_t(n_q)) && slot_bits >= 1 && q_bits + slot_bits <= 33,
                "reverse_entries: bad key fields (%d + %d bits)", q_bits, slot_bits);
   const TokenLayout tl = token_layout(global_token != 0, token_row, n_q);
-  const int64_t n_keys = nnz - (tl.tok ? tl.c0 + tl.token_len : 0);
+  const int64_t n_token = tl.tok ? tl.c0 + tl.token_len : 0;
+  const int64_t n_keys = nnz - n_token;     // a capacity, as in bf_reverse_index_packed
   BF_CHECK_ARG(n_keys >= 0, "reverse_entries: %lld entries cannot hold the token's %lld", (long long)nnz,
                (long long)(tl.c0 + tl.token_len));
   if (nnz == 0) return BF_OK;
@@ -790,7 +803,7 @@ extern "C" int bf_reverse_entries(const uint64_t* sorted, const int64_t* qptr, i
   hipStream_t st = as_stream(stream);
   if (n_keys > 0 || tl.lead) {
     BF_LAUNCH("reverse_entries_kernel", reverse_entries_kernel, dim3(blocks_for(n_keys + 1)), dim3(kThreads), 0, st,
-              sorted, n_keys, q_bits + slot_bits, slot_bits, tl, qptr, ke);
+              sorted, qptr + n_q, n_token, n_keys, q_bits + slot_bits, slot_bits, tl, qptr, ke);
     BF_CHECK_LAUNCH();
   }
   return launch_token_reverse(tl, qptr, nullptr, ke, st);

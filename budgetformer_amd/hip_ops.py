@@ -475,10 +475,12 @@ def table_qptr(table: torch.Tensor, row_len: torch.Tensor, global_token: bool = 
 
 
 def table_to_csr(table: torch.Tensor, row_len: torch.Tensor, global_token: bool = False, with_keys: bool = False,
-                 qptr: Optional[torch.Tensor] = None, token_row: Optional[int] = None):
+                 qptr: Optional[torch.Tensor] = None, token_row: Optional[int] = None, exact: bool = True):
     """Query-major table -> (qptr [n_q+1] int64, kv [nnz] int32), plus the reverse-index sort keys
     (``ReverseKeys``, or None when the query and slot fields need more than 33 bits) with ``with_keys``.
-    ``qptr`` from ``table_qptr`` saves the scan; nnz is read from it (one host read).
+    ``qptr`` from ``table_qptr`` saves the scan; nnz is read from it (one host read). Without ``exact``
+    nothing is read back: kv and the keys are sized for every row full (entries past qptr[n_q] hold
+    nothing), so the whole index can be built while the host runs ahead.
 
     With ``global_token`` every table row also attends to kv 0 and ids shift by one; ``token_row`` is the
     length of the token's own row, placed as attention row 0 (default n_rows: the full query set; N for
@@ -489,13 +491,14 @@ def table_to_csr(table: torch.Tensor, row_len: torch.Tensor, global_token: bool 
     if qptr is None:
         qptr = table_qptr(table, row_len, global_token, tr)
     n_q = n_rows + (1 if tr >= 0 else 0)
-    nnz = int(qptr[n_q].item())
+    n_token = (n_rows + max(tr, 0)) if global_token else 0    # kv 0 of every table row, the token row
+    nnz = int(qptr[n_q].item()) if exact else n_rows * width + n_token
     kv = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)[:nnz]
     rk = None
     q_bits, slot_bits = _bits_for(n_q), _bits_for(width)
     if with_keys and q_bits + slot_bits <= 33:
-        # the token's entries (kv 0 of every table row, the token row) get no key
-        n_keys = nnz - ((n_rows + max(tr, 0)) if global_token else 0)
+        # the token's entries get no key
+        n_keys = nnz - n_token
         rk = ReverseKeys(torch.empty(max(n_keys, 1), dtype=torch.int64, device=dev)[:n_keys], q_bits,
                          slot_bits, bool(global_token), tr)
     N.call("bf_table_to_csr", _p(table), _p(row_len), n_rows, width, int(global_token), tr, _p(qptr), _p(kv),
@@ -793,6 +796,15 @@ def split_plan(ptr: torch.Tensor, nnz: int, threshold: int = DEFAULT_CHUNK, item
 
 
 # ------------------------------------------------------------------ attention index
+def _to_cap(t: torch.Tensor, cap: int) -> torch.Tensor:
+    """An exact per-entry array in a buffer of the index's capacity (entries past its length hold nothing)."""
+    if t.numel() == cap:
+        return t
+    out = torch.empty(max(cap, 1), dtype=t.dtype, device=t.device)[:cap]
+    out[:t.numel()] = t
+    return out
+
+
 @dataclass
 class AttentionIndex:
     """One edge set in the layout the attention kernels walk.
@@ -800,17 +812,23 @@ class AttentionIndex:
     Query-major CSR (qptr, kv) for the forward and the dq pass; the key-major
     reverse index (kptr, kq, ke) for the dk/dv pass is built on first use and
     then reused by every layer and step that shares the edge set.
+
+    The per-entry arrays are held at a capacity (``kv_all``, ``kq_all``,
+    ``ke_all``; ``cap`` >= nnz): a table's index is sized for every row full,
+    so that building it reads nothing back to the host. The entry count is
+    qptr[n_q]; ``nnz`` and the exact views ``kv``, ``kq``, ``ke`` read it on
+    first use.
     """
     n_q: int
     n_kv: int
     qptr: torch.Tensor
-    kv: torch.Tensor
+    kv_all: Optional[torch.Tensor]
     chunk: int = DEFAULT_CHUNK
     item: int = DEFAULT_ITEM
     qplan: Optional[SplitPlan] = None
     kptr: Optional[torch.Tensor] = None
-    kq: Optional[torch.Tensor] = None
-    ke: Optional[torch.Tensor] = None
+    kq_all: Optional[torch.Tensor] = None
+    ke_all: Optional[torch.Tensor] = None
     kplan: Optional[SplitPlan] = None
     korder: Optional[torch.Tensor] = None
     kspans: Optional[torch.Tensor] = None      # per korder slot: (kptr[row] << 32 | row length)
@@ -830,10 +848,35 @@ class AttentionIndex:
     # (items, split rows) of the query-side plan when the row lengths fix them (from_table)
     _q_known: Optional[tuple] = field(default=None, repr=False)
     _structs: dict = field(default_factory=dict, repr=False)          # C view per (backward, with ke)
+    _nnz: Optional[int] = field(default=None, repr=False)             # qptr[n_q], once read
+
+    @property
+    def cap(self) -> int:
+        """The entries the per-entry arrays are sized for (>= nnz)."""
+        return self.kv_all.numel()
 
     @property
     def nnz(self) -> int:
-        return self.kv.numel()
+        """The entry count (qptr[n_q]; read from the device on first use unless the arrays are exact)."""
+        if self._nnz is None:
+            self._nnz = int(self.qptr[self.n_q].item()) if self.cap else 0
+        return self._nnz
+
+    @property
+    def nnz_known(self) -> bool:
+        return self._nnz is not None
+
+    @property
+    def kv(self) -> torch.Tensor:
+        return self.kv_all[:self.nnz]
+
+    @property
+    def kq(self) -> Optional[torch.Tensor]:
+        return None if self.kq_all is None else self.kq_all[:self.nnz]
+
+    @property
+    def ke(self) -> Optional[torch.Tensor]:
+        return None if self.ke_all is None else self.ke_all[:self.nnz]
 
     @property
     def device(self):
@@ -850,7 +893,7 @@ class AttentionIndex:
 
     def ensure_forward(self):
         if self.qplan is None:
-            self.qplan = split_plan(self.qptr, self.nnz, self.chunk, self.item, resolve=False,
+            self.qplan = split_plan(self.qptr, self.cap, self.chunk, self.item, resolve=False,
                                     counts=self._plan_counts(0), known=self._q_known,
                                     host_copy=self._host_copy())
         return self
@@ -863,23 +906,24 @@ class AttentionIndex:
 
     def ensure_backward(self):
         if self.qplan is None:
-            self.qplan = split_plan(self.qptr, self.nnz, self.chunk, self.item, resolve=False,
+            self.qplan = split_plan(self.qptr, self.cap, self.chunk, self.item, resolve=False,
                                     counts=self._plan_counts(0), known=self._q_known,
                                     host_copy=self._host_copy())
         if self.kptr is None:
             if self._rkeys is not None and self._rkeys.q_bits + self._rkeys.slot_bits + _bits_for(self.n_kv) <= 64:
-                self.kptr, self.kq, _, self._sorted = reverse_index_packed(self._rkeys, self.qptr, self.n_kv,
-                                                                           entries=False)
+                self.kptr, self.kq_all, _, self._sorted = reverse_index_packed(self._rkeys, self.qptr, self.n_kv,
+                                                                               entries=False)
                 self._rkeys = None
             else:
-                self.kptr, self.kq, self.ke = reverse_index(self.qptr, self.kv, self.n_kv)
+                self.kptr, kq, ke = reverse_index(self.qptr, self.kv, self.n_kv)
+                self.kq_all, self.ke_all = _to_cap(kq, self.cap), _to_cap(ke, self.cap)
         if self.kplan is None and self.korder is None and 1 <= self.chunk <= 254:
             # the rows to split are the longest-first order's first slots: one pass writes both
             self.korder, self.kspans, self.kplan = row_order_and_plan(
-                self.kptr, self.nnz, self.chunk, self.item, counts=self._plan_counts(1),
+                self.kptr, self.cap, self.chunk, self.item, counts=self._plan_counts(1),
                 host_copy=self._host_copy())
         if self.kplan is None:
-            self.kplan = split_plan(self.kptr, self.nnz, self.chunk, self.item, resolve=False,
+            self.kplan = split_plan(self.kptr, self.cap, self.chunk, self.item, resolve=False,
                                     counts=self._plan_counts(1), host_copy=self._host_copy())
         if self.korder is None:
             self.korder, self.kspans = row_order(self.kptr, spans=True)
@@ -888,8 +932,8 @@ class AttentionIndex:
     def ensure_entries(self):
         """The CSR position of every reverse entry (ke), which the dk/dv pass reads only with a bias or factor."""
         self.ensure_backward()
-        if self.ke is None and self.nnz:
-            self.ke = reverse_entries(self._sorted, self.qptr)
+        if self.ke_all is None and self.cap:
+            self.ke_all = reverse_entries(self._sorted, self.qptr)
             self._sorted = None
         return self
 
@@ -910,7 +954,7 @@ class AttentionIndex:
         if backward and entries:
             self.ensure_entries()
         # the index does not change once built: every layer and step reuses the same struct
-        key = (backward, backward and self.ke is not None)
+        key = (backward, backward and self.ke_all is not None, self.nnz_known)
         cached = self._structs.get(key)
         if cached is not None:
             return cached
@@ -927,8 +971,10 @@ class AttentionIndex:
         """bf_attn_index's fields: ({pointer field: tensor or None}, {integer field: int})."""
         t = dict.fromkeys(self._TENSOR_FIELDS)
         n = dict.fromkeys(self._INT_FIELDS, 0)
-        n["n_q"], n["n_kv"], n["nnz"] = self.n_q, self.n_kv, self.nnz
-        t["qptr"], t["kv"] = self.qptr, self.kv if self.nnz else None
+        # the kernels take the entries from the row pointers; nnz sizes only the per-edge tensors (bias,
+        # factor, dbias), whose calls read it first, and otherwise passes the capacity
+        n["n_q"], n["n_kv"], n["nnz"] = self.n_q, self.n_kv, self.nnz if self.nnz_known else self.cap
+        t["qptr"], t["kv"] = self.qptr, self.kv_all if self.cap else None
         n["chunk"], n["item"] = self.chunk, self.item
         qp = self.qplan
         # plans with a pinned copy of their counts take them from it; the others stay pending, their
@@ -943,8 +989,8 @@ class AttentionIndex:
         if backward:
             kp = self.kplan
             t["kptr"] = self.kptr
-            t["kq"] = self.kq if self.nnz else None
-            t["ke"] = self.ke if (self.nnz and self.ke is not None) else None
+            t["kq"] = self.kq_all if self.cap else None
+            t["ke"] = self.ke_all if (self.cap and self.ke_all is not None) else None
             n["k_items"], n["k_heavy"] = (kp.item_cap, kp.heavy_cap) if kp.pending else (kp.items, kp.heavy)
             t["k_nitems"], t["k_item_off"], t["k_item_row"], t["k_heavy_rows"] = (
                 kp.nitems, kp.item_off, kp.item_row, kp.heavy_rows)
@@ -968,7 +1014,7 @@ class AttentionIndex:
         self.ensure_backward() if backward else self.ensure_forward()
         if backward and entries:
             self.ensure_entries()
-        key = ("op", backward, backward and self.ke is not None)
+        key = ("op", backward, backward and self.ke_all is not None, self.nnz_known)
         cached = self._structs.get(key)
         if cached is None:
             t, n = self._fields(backward)
@@ -1006,15 +1052,15 @@ class AttentionIndex:
         # the token fill puts key 0 first in every table row and shifts the table's own ids past it:
         # key 0 is then attended by every query row from 1 on (with the token row) or from 0 on (without)
         token_column = 0 if not global_token else (1 if tr >= 0 else 2)
-        idx = cls(n_q=n_q_tab, n_kv=n_kv, qptr=qptr, kv=None, chunk=chunk, item=item,
+        idx = cls(n_q=n_q_tab, n_kv=n_kv, qptr=qptr, kv_all=None, chunk=chunk, item=item,
                   token_column=token_column, _q_known=known)
         if known is not None:
             # only the token row can be split: its plan is written in one pass, before the host waits
             # for nnz
             bound = n_rows * width + (n_rows if global_token else 0) + max(tr, 0)
             idx.qplan = split_plan_first_row(n_q_tab, known[0], bound, chunk, item, idx._plan_counts(0))
-        qptr, idx.kv, idx._rkeys = table_to_csr(table, row_len, global_token, with_keys=True, qptr=qptr,
-                                                token_row=tr)
+        qptr, idx.kv_all, idx._rkeys = table_to_csr(table, row_len, global_token, with_keys=True, qptr=qptr,
+                                                    token_row=tr, exact=False)
         return idx
 
     @classmethod
@@ -1022,7 +1068,7 @@ class AttentionIndex:
                  item: int = DEFAULT_ITEM):
         n_kv = n_q if n_kv is None else n_kv
         qptr, kv = coo_to_csr(edge_index, n_q, n_kv)
-        return cls(n_q=n_q, n_kv=n_kv, qptr=qptr, kv=kv, chunk=chunk, item=item)
+        return cls(n_q=n_q, n_kv=n_kv, qptr=qptr, kv_all=kv, chunk=chunk, item=item, _nnz=kv.numel())
 
 
 # ------------------------------------------------------------------ attention
@@ -1071,6 +1117,8 @@ def attn_forward(idx: AttentionIndex, q, k, v, bias=None, factor=None, dropout: 
     """out [n_q,H,hn] (activation dtype), Z [n_q,H] float32, through bf::sparse_attn_fwd (which checks
     the shapes, dtypes and devices against the index). ``score_clamp``: the bound of the clamp on
     q.k / sqrt(hn), in (0, 5]."""
+    if bias is not None or factor is not None:
+        idx.nnz      # per-edge tensors are [nnz, H]: the index passes the count itself
     t, n = idx.op_args(backward=False)
     return N.load_ops().sparse_attn_fwd(q, k, v, t, n, bias, factor, *_dropout_op_args(dropout), float(score_clamp))
 
@@ -1094,6 +1142,8 @@ def attn_backward(idx: AttentionIndex, q, k, v, out, Z, dout, bias=None, factor=
     rate, seed, off = _dropout_op_args(dropout)
     if not 0.0 <= rate <= 1.0:
         raise ValueError(f"dropout rate {rate} outside [0, 1]")
+    if bias is not None or factor is not None or need_dbias:
+        idx.nnz      # per-edge tensors are [nnz, H]: the index passes the count itself
     t, n = idx.op_args(backward=True, entries=bias is not None or factor is not None or need_dbias or rate > 0.0)
     dq, dk, dv, dbias = N.load_ops().sparse_attn_bwd(q, k, v, t, n, Z, dout, bias, factor, bool(need_dbias), rate,
                                                      seed, off, float(score_clamp))

@@ -397,6 +397,17 @@ def test_index_formats_against_numpy(hip_device, token, token_row):
     lazy = hip_ops.reverse_index_packed(rk, qptr, n_kv, entries=False)
     assert lazy[2] is None and torch.equal(lazy[0], a[0]) and torch.equal(lazy[1], a[1])
     assert torch.equal(hip_ops.reverse_entries(lazy[3], qptr), a[2])
+    # the same route with nothing read back: buffers sized for every row full, the kernels taking the
+    # entry count from qptr[n_q]; the first nnz entries equal the exact route's
+    nnz = kv.numel()
+    qc, kvc, rkc = hip_ops.table_to_csr(t, rl, token, with_keys=True, token_row=token_row, exact=False)
+    assert kvc.numel() == n * width + ((n + max(tr, 0)) if token else 0) > nnz
+    assert torch.equal(qc, qptr) and torch.equal(kvc[:nnz], kv)
+    assert torch.equal(rkc.keys[:rk.keys.numel()], rk.keys)
+    cap = hip_ops.reverse_index_packed(rkc, qc, n_kv)
+    assert torch.equal(cap[0], a[0]) and torch.equal(cap[1][:nnz], a[1]) and torch.equal(cap[2][:nnz], a[2])
+    lazy_c = hip_ops.reverse_index_packed(rkc, qc, n_kv, entries=False)
+    assert torch.equal(hip_ops.reverse_entries(lazy_c[3], qc)[:nnz], a[2])
     order = np.lexsort((pos, np.array(vals)))                    # (kv, position) order
     assert np.array_equal(b[1].cpu().numpy(), np.array(rows)[order]) and np.array_equal(b[2].cpu().numpy(), order)
     # row order: a permutation, capped lengths non-increasing
