@@ -33,6 +33,25 @@ size_t scan_temp_bytes_i64(int64_t n) {
   return bytes;
 }
 
+// block-wide exclusive scan of one 64-bit value per thread
+__device__ __forceinline__ uint64_t block_excl_scan_u64(uint64_t v, uint64_t* tmp /*[kThreads / 64]*/) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  uint64_t x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint64_t y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) tmp[w] = x;
+  __syncthreads();
+  uint64_t base = 0;
+#pragma unroll
+  for (int i = 0; i < kThreads / 64; ++i)
+    if (i < w) base += tmp[i];
+  __syncthreads();
+  return base + x - v;
+}
+
 // ---------------------------------------------------------------- table -> CSR
 // Row lengths of a table's attention CSR. With the Graphormer token (token):
 // every table row gains kv 0; with a token row (lead = 1) attention row 0 is
@@ -44,6 +63,75 @@ __global__ void row_lengths_kernel(const int32_t* __restrict__ row_len, int64_t 
   if (t == 0) qptr[0] = 0;     // the scan writes qptr[1..n_q]
   if (t >= n_q) return;
   lens[t] = (lead && t == 0) ? token_len : int64_t(row_len[t - lead]) + token;
+}
+
+// The same row pointers in two launches, for up to kPtrInBlockMax blocks of
+// kPtrRows rows: each block's sum of its rows' lengths, then each block adds
+// up the sums before it and scans its own rows (no scan state to clear).
+constexpr int kPtrRowsPerThread = 16;
+constexpr int64_t kPtrRows = int64_t(kThreads) * kPtrRowsPerThread;
+constexpr int64_t kPtrInBlockMax = 1024;
+
+__device__ __forceinline__ int64_t row_length(const int32_t* __restrict__ row_len, int64_t t, int token, int lead,
+                                              int64_t token_len) {
+  return (lead && t == 0) ? token_len : int64_t(row_len[t - lead]) + token;
+}
+
+__device__ __forceinline__ int64_t block_sum_i64(int64_t v, int64_t* tmp /*[kThreads / 64]*/) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  if ((threadIdx.x & 63) == 0) tmp[threadIdx.x >> 6] = v;
+  __syncthreads();
+  int64_t s = 0;
+#pragma unroll
+  for (int i = 0; i < kThreads / 64; ++i) s += tmp[i];
+  __syncthreads();
+  return s;
+}
+
+__global__ __launch_bounds__(kThreads) void row_block_sums_kernel(const int32_t* __restrict__ row_len,
+                                                                  int64_t n_rows, int token, int lead,
+                                                                  int64_t token_len, int64_t* __restrict__ bsum) {
+  __shared__ int64_t tmp[kThreads / 64];
+  const int64_t n_q = n_rows + lead;
+  const int64_t t0 = int64_t(blockIdx.x) * kPtrRows + threadIdx.x;
+  int64_t s = 0;
+#pragma unroll
+  for (int u = 0; u < kPtrRowsPerThread; ++u) {
+    const int64_t t = t0 + u * kThreads;
+    if (t < n_q) s += row_length(row_len, t, token, lead, token_len);
+  }
+  s = block_sum_i64(s, tmp);
+  if (threadIdx.x == 0) bsum[blockIdx.x] = s;
+}
+
+// Thread i of block b scans rows b * kPtrRows + i * kPtrRowsPerThread + [0, kPtrRowsPerThread).
+__global__ __launch_bounds__(kThreads) void row_ptr_kernel(const int32_t* __restrict__ row_len, int64_t n_rows,
+                                                           int token, int lead, int64_t token_len,
+                                                           const int64_t* __restrict__ bsum,
+                                                           int64_t* __restrict__ qptr) {
+  __shared__ int64_t tmp[kThreads / 64];
+  __shared__ uint64_t stmp[kThreads / 64];
+  const int64_t n_q = n_rows + lead;
+  int64_t before = 0;
+  for (int64_t k = threadIdx.x; k < int64_t(blockIdx.x); k += kThreads) before += bsum[k];
+  before = block_sum_i64(before, tmp);
+  const int64_t t0 = int64_t(blockIdx.x) * kPtrRows + int64_t(threadIdx.x) * kPtrRowsPerThread;
+  int64_t len[kPtrRowsPerThread], s = 0;
+#pragma unroll
+  for (int u = 0; u < kPtrRowsPerThread; ++u) {
+    const int64_t t = t0 + u;
+    len[u] = t < n_q ? row_length(row_len, t, token, lead, token_len) : 0;
+    s += len[u];
+  }
+  int64_t run = before + int64_t(block_excl_scan_u64(uint64_t(s), stmp));
+  if (blockIdx.x == 0 && threadIdx.x == 0) qptr[0] = 0;
+#pragma unroll
+  for (int u = 0; u < kPtrRowsPerThread; ++u) {
+    const int64_t t = t0 + u;
+    run += len[u];
+    if (t < n_q) qptr[t + 1] = run;
+  }
 }
 
 // Validation of an externally supplied table (bf_check_table): bad[0] counts
@@ -264,10 +352,20 @@ __device__ __forceinline__ int64_t keyed_entries(const int64_t* __restrict__ nnz
 }
 
 // Sorted keys -> kptr (boundaries of the id field), kq, and ke when asked for.
+// Blocks from key_blocks on write kv 0's segment with the token instead (what
+// token_reverse_kernel writes), saving its launch.
 __global__ __launch_bounds__(kThreads) void unpack_rkey_kernel(
     const uint64_t* __restrict__ keys, const int64_t* __restrict__ nnz_dev, int64_t n_token, int64_t key_cap,
     int kshift, int sbits, TokenLayout tl, const int64_t* __restrict__ qptr, int64_t n_kv,
-    int64_t* __restrict__ kptr, int32_t* __restrict__ kq, int32_t* __restrict__ ke) {
+    int64_t* __restrict__ kptr, int32_t* __restrict__ kq, int32_t* __restrict__ ke, int64_t key_blocks) {
+  if (int64_t(blockIdx.x) >= key_blocks) {
+    const int64_t j = (int64_t(blockIdx.x) - key_blocks) * kThreads + threadIdx.x;
+    if (j < tl.c0) {
+      kq[j] = int32_t(tl.lead + j);
+      if (ke) ke[j] = int32_t(qptr[tl.lead + j]);
+    }
+    return;
+  }
   const int64_t n_keys = keyed_entries(nnz_dev, n_token, key_cap);
   const int64_t base = int64_t(blockIdx.x) * (kThreads * kUnpackPerThread) + threadIdx.x;
   uint64_t cur[kUnpackPerThread], prev[kUnpackPerThread];
@@ -353,12 +451,17 @@ inline int launch_token_reverse(const TokenLayout& tl, const int64_t* qptr, int3
   return BF_OK;
 }
 
-// Row order, longest first: bucket 255 - min(len, 255), counted per block in
-// LDS and reserved per block with one global atomic per bucket. Rows of one
-// bucket come out in an arbitrary order: the order only decides which group
-// serves which row, never a row's arithmetic.
+// Row order, longest first: bucket 255 - min(len, 255). Three launches in
+// the radix sort's count / scan / place pattern over blocks of kOrderRows
+// rows: each block's bucket counts (bucket-major), an exclusive sum per bucket
+// over the blocks (sort::radix_scan_kernel), then each block places its rows
+// from its buckets' offsets. No global atomics and nothing to clear. Rows of
+// one bucket within a block come out in an arbitrary order: the order only
+// decides which group serves which row, never a row's arithmetic.
 constexpr int kBuckets = 256;
 static_assert(kBuckets == kThreads, "the order kernels keep one bucket per thread");
+constexpr int kOrderRowsPerThread = 8;
+constexpr int64_t kOrderRows = int64_t(kThreads) * kOrderRowsPerThread;
 
 // A row's split-plan entry: (items << 32) | (1 if it splits), items =
 // split_row_items(len) for rows longer than the threshold, else 0. The plan is
@@ -368,62 +471,51 @@ __device__ __forceinline__ uint64_t split_count(int64_t len, int threshold, int 
   return (uint64_t(split_row_items(len, item_size)) << 32) | 1u;
 }
 
-__device__ __forceinline__ int length_bucket(const int64_t* __restrict__ ptr, int64_t r) {
-  const int64_t len = ptr[r + 1] - ptr[r];
-  return 255 - int(len < 255 ? len : 255);
-}
+__device__ __forceinline__ int bucket_of(int64_t len) { return 255 - int(len < 255 ? len : 255); }
 
-__global__ __launch_bounds__(kThreads) void order_hist_kernel(const int64_t* __restrict__ ptr, int64_t n_rows,
-                                                              uint32_t* __restrict__ hist) {
+__global__ __launch_bounds__(kThreads) void order_count_kernel(const int64_t* __restrict__ ptr, int64_t n_rows,
+                                                               int64_t blocks, uint32_t* __restrict__ counts) {
   __shared__ uint32_t h[kBuckets];
   h[threadIdx.x] = 0;
   __syncthreads();
-  for (int64_t r = int64_t(blockIdx.x) * kThreads + threadIdx.x; r < n_rows; r += int64_t(gridDim.x) * kThreads)
-    atomicAdd(&h[length_bucket(ptr, r)], 1u);
+  const int64_t r0 = int64_t(blockIdx.x) * kOrderRows + threadIdx.x;
+#pragma unroll
+  for (int u = 0; u < kOrderRowsPerThread; ++u) {
+    const int64_t r = r0 + u * kThreads;
+    if (r < n_rows) atomicAdd(&h[bucket_of(ptr[r + 1] - ptr[r])], 1u);
+  }
   __syncthreads();
-  if (h[threadIdx.x]) atomicAdd(&hist[threadIdx.x], h[threadIdx.x]);
+  counts[int64_t(threadIdx.x) * blocks + blockIdx.x] = h[threadIdx.x];
 }
 
-// Each block orders `chunk` consecutive rows: it counts them per bucket in
-// LDS, reserves one range per bucket with a single global atomic (few blocks,
-// so the popular short-row buckets see little contention), then places them,
-// and with `spans` each slot's row as (begin << 32 | length), which the reader
-// then takes from the slot instead of a random read of the row pointers.
-// Smaller chunks were measured no faster on 169K rows and slower on 2.4M.
-constexpr int64_t kOrderChunk = 16 * kThreads;
-
-__global__ __launch_bounds__(kThreads) void order_scatter_kernel(const int64_t* __restrict__ ptr, int64_t n_rows,
-                                                                 int64_t chunk, const uint32_t* __restrict__ hist,
-                                                                 uint32_t* __restrict__ cursor,
-                                                                 int32_t* __restrict__ order,
-                                                                 uint64_t* __restrict__ spans, int threshold,
-                                                                 int item_size, int64_t n_slots,
-                                                                 uint64_t* __restrict__ packed) {
+// Places block b's rows: slot = (rows of longer buckets) + (rows of this
+// bucket in earlier blocks) + rank in the block; with `spans` each slot's row
+// as (begin << 32 | length), which the reader then takes from the slot instead
+// of a random read of the row pointers; with `packed` the split-plan entry of
+// each of the first n_slots slots.
+__global__ __launch_bounds__(kThreads) void order_place_kernel(const int64_t* __restrict__ ptr, int64_t n_rows,
+                                                               int64_t blocks, const uint32_t* __restrict__ prefix,
+                                                               const uint32_t* __restrict__ totals,
+                                                               int32_t* __restrict__ order,
+                                                               uint64_t* __restrict__ spans, int threshold,
+                                                               int item_size, int64_t n_slots,
+                                                               uint64_t* __restrict__ packed) {
   __shared__ uint32_t base[kBuckets];
   __shared__ uint32_t cnt[kBuckets];
+  __shared__ uint32_t tmp[kThreads / 64];
   const int tid = threadIdx.x;
-  base[tid] = hist[tid];
+  uint32_t all;
+  const uint32_t before = sort::block_excl_scan(totals[tid], tmp, &all);
+  base[tid] = before + prefix[int64_t(tid) * blocks + blockIdx.x];
   cnt[tid] = 0;
   __syncthreads();
-  for (int o = 1; o < kBuckets; o <<= 1) {      // inclusive scan of the bucket sizes
-    const uint32_t x = tid >= o ? base[tid - o] : 0u;
-    __syncthreads();
-    base[tid] += x;
-    __syncthreads();
-  }
-  const uint32_t start = tid ? base[tid - 1] : 0u;
-  __syncthreads();
-  base[tid] = start;
-  const int64_t r0 = int64_t(blockIdx.x) * chunk;
-  const int64_t r1 = r0 + chunk < n_rows ? r0 + chunk : n_rows;
-  for (int64_t r = r0 + tid; r < r1; r += kThreads) atomicAdd(&cnt[length_bucket(ptr, r)], 1u);
-  __syncthreads();
-  if (cnt[tid]) base[tid] += atomicAdd(&cursor[tid], cnt[tid]);
-  cnt[tid] = 0;
-  __syncthreads();
-  for (int64_t r = r0 + tid; r < r1; r += kThreads) {
+  const int64_t r0 = int64_t(blockIdx.x) * kOrderRows + tid;
+#pragma unroll
+  for (int u = 0; u < kOrderRowsPerThread; ++u) {
+    const int64_t r = r0 + u * kThreads;
+    if (r >= n_rows) break;
     const int64_t beg = ptr[r], len = ptr[r + 1] - beg;
-    const int b = 255 - int(len < 255 ? len : 255);
+    const int b = bucket_of(len);
     const uint32_t slot = base[b] + atomicAdd(&cnt[b], 1u);
     order[slot] = int32_t(r);
     if (spans) spans[slot] = (uint64_t(beg) << 32) | uint64_t(len);
@@ -486,7 +578,11 @@ __global__ void split_count_kernel(const int64_t* __restrict__ ptr, int64_t n_ro
 // entries are written. A row's thread writes the item_row of its first
 // kOwnItems items; rows with more (the Graphormer token row and column, hubs)
 // are queued in LDS and their remaining items written by the whole block.
+// packed_off NULL: the exclusive sums are formed here, each block adding up
+// the slots before it (plans of at most kPlanInBlockSlots slots).
 constexpr int kOwnItems = 32;
+constexpr int64_t kPlanInBlockSlots = 32768;
+
 __global__ __launch_bounds__(kThreads) void split_rows_kernel(
     const uint64_t* __restrict__ packed, const uint64_t* __restrict__ packed_off, const int32_t* __restrict__ order,
     int64_t n_slots, int64_t item_cap, int32_t* __restrict__ nitems, int32_t* __restrict__ item_off,
@@ -495,12 +591,24 @@ __global__ __launch_bounds__(kThreads) void split_rows_kernel(
   __shared__ int64_t long_first[kThreads];
   __shared__ int32_t long_n[kThreads], long_row[kThreads];
   __shared__ int n_long;
+  __shared__ uint64_t scan_tmp[kThreads / 64];
   if (threadIdx.x == 0) n_long = 0;
-  __syncthreads();
   const int64_t j = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  uint64_t in_block_off = 0;
+  if (!packed_off) {
+    uint64_t before = 0;
+    for (int64_t k = threadIdx.x; k < int64_t(blockIdx.x) * kThreads; k += kThreads) before += packed[k];
+    // the block's total of `before` is the sum over every earlier slot
+    const uint64_t lo = block_excl_scan_u64(before, scan_tmp);
+    __shared__ uint64_t s_before;
+    if (threadIdx.x == kThreads - 1) s_before = lo + before;
+    __syncthreads();
+    in_block_off = s_before + block_excl_scan_u64(j < n_slots ? packed[j] : 0, scan_tmp);
+  }
+  __syncthreads();
   if (j < n_slots) {
     const int n = int(packed[j] >> 32);
-    const uint64_t off = packed_off[j];
+    const uint64_t off = packed_off ? packed_off[j] : in_block_off;
     const int64_t first_item = int64_t(off >> 32);
     const int64_t slot = int64_t(uint32_t(off));
     if (!order || n > 0) {
@@ -555,7 +663,17 @@ extern "C" int bf_table_csr_ptr(const int32_t* row_len, int64_t n_rows, int32_t 
   BF_CHECK_ARG(workspace && workspace_bytes >= need, "table_csr_ptr: workspace %zu < %zu bytes", workspace_bytes, need);
   hipStream_t st = as_stream(stream);
   if (n_q == 0) BF_CHECK_HIP(hipMemsetAsync(qptr, 0, sizeof(int64_t), st));
-  if (n_q > 0) {
+  const int64_t ptr_blocks = ceil_div(n_q, kPtrRows);
+  if (n_q > 0 && ptr_blocks <= kPtrInBlockMax) {
+    auto* bsum = static_cast<int64_t*>(workspace);     // the first ptr_blocks of the n_q slots
+    const int64_t token_len = lead ? token_row : int64_t(0);
+    BF_LAUNCH("row_block_sums_kernel", row_block_sums_kernel, dim3(unsigned(ptr_blocks)), dim3(kThreads), 0, st,
+              row_len, n_rows, int(global_token != 0), lead, token_len, bsum);
+    BF_CHECK_LAUNCH();
+    BF_LAUNCH("row_ptr_kernel", row_ptr_kernel, dim3(unsigned(ptr_blocks)), dim3(kThreads), 0, st, row_len, n_rows,
+              int(global_token != 0), lead, token_len, static_cast<const int64_t*>(bsum), qptr);
+    BF_CHECK_LAUNCH();
+  } else if (n_q > 0) {
     auto* lens = static_cast<int64_t*>(workspace);
     void* temp = static_cast<char*>(workspace) + align_up(size_t(n_q) * sizeof(int64_t));
     size_t temp_bytes = scan_temp_bytes_i64(n_q);
@@ -767,11 +885,12 @@ extern "C" int bf_reverse_index_packed(const uint64_t* rkey, const int64_t* qptr
                                          st, qptr + n_q, n_token);
     if (rc) return rc;
   }
-  BF_LAUNCH("unpack_rkey_kernel", unpack_rkey_kernel,
-            dim3(unsigned(ceil_div(n_keys + 1, int64_t(kThreads) * kUnpackPerThread))), dim3(kThreads), 0, st, sorted,
-            qptr + n_q, n_token, n_keys, kshift, slot_bits, tl, qptr, n_kv, kptr, kq, ke);
+  const int64_t key_blocks = ceil_div(n_keys + 1, int64_t(kThreads) * kUnpackPerThread);
+  const int64_t tok_blocks = tl.tok ? ceil_div(tl.c0, int64_t(kThreads)) : 0;
+  BF_LAUNCH("unpack_rkey_kernel", unpack_rkey_kernel, dim3(unsigned(key_blocks + tok_blocks)), dim3(kThreads), 0, st,
+            sorted, qptr + n_q, n_token, n_keys, kshift, slot_bits, tl, qptr, n_kv, kptr, kq, ke, key_blocks);
   BF_CHECK_LAUNCH();
-  return launch_token_reverse(tl, qptr, kq, ke, st);
+  return BF_OK;
 }
 
 extern "C" int bf_radix_sort_workspace_size(int64_t n, int32_t begin_bit, int32_t end_bit, size_t* bytes) {
@@ -871,10 +990,13 @@ extern "C" int bf_split_plan(const int64_t* ptr, int64_t n_rows, int32_t thresho
   BF_LAUNCH("split_count_kernel", split_count_kernel, dim3(blocks_for(n_rows)), dim3(kThreads), 0, st, ptr, n_rows,
             threshold, item_size, packed);
   BF_CHECK_LAUNCH();
-  BF_CHECK_HIP(prim::exclusive_sum(temp, temp_bytes, static_cast<const uint64_t*>(packed), packed_off, n_rows, st));
+  const bool in_block = n_rows <= kPlanInBlockSlots;
+  if (!in_block)
+    BF_CHECK_HIP(prim::exclusive_sum(temp, temp_bytes, static_cast<const uint64_t*>(packed), packed_off, n_rows,
+                                     st));
   BF_LAUNCH("split_rows_kernel", split_rows_kernel, dim3(blocks_for(n_rows)), dim3(kThreads), 0, st, packed,
-            packed_off, static_cast<const int32_t*>(nullptr), n_rows, item_cap, nitems, item_off, item_row,
-            heavy_rows, heavy_cap, counts);
+            in_block ? nullptr : packed_off, static_cast<const int32_t*>(nullptr), n_rows, item_cap, nitems,
+            item_off, item_row, heavy_rows, heavy_cap, counts);
   BF_CHECK_LAUNCH();
   return BF_OK;
 }
@@ -1052,9 +1174,14 @@ extern "C" int bf_coalesce(const int64_t* src, const int64_t* dst, int64_t nnz, 
 }
 
 namespace {
-// hist / cursor of the order kernels, then (plans only) the slots' packed
-// counts, their exclusive sums and the scan's temporary storage.
-constexpr size_t kOrderHistBytes = 2 * kBuckets * sizeof(uint32_t);
+// The order kernels' per-block bucket counts and bucket totals, then (plans
+// only) the slots' packed counts, their exclusive sums and the scan's
+// temporary storage.
+int64_t order_blocks(int64_t n_rows) { return ceil_div(n_rows > 0 ? n_rows : 1, kOrderRows); }
+
+size_t order_counts_bytes(int64_t n_rows) {
+  return align_up(size_t(order_blocks(n_rows)) * kBuckets * sizeof(uint32_t)) + align_up(kBuckets * sizeof(uint32_t));
+}
 
 size_t plan_slots_scan_bytes(int64_t n_slots) {
   size_t temp_bytes = 0;
@@ -1063,17 +1190,20 @@ size_t plan_slots_scan_bytes(int64_t n_slots) {
   return temp_bytes;
 }
 
-int launch_row_order(const int64_t* ptr, int64_t n_rows, int32_t* order, uint64_t* spans, uint32_t* hist,
+int launch_row_order(const int64_t* ptr, int64_t n_rows, int32_t* order, uint64_t* spans, void* ws,
                      int threshold, int item_size, int64_t n_slots, uint64_t* packed, hipStream_t st) {
-  uint32_t* cursor = hist + kBuckets;
-  BF_CHECK_HIP(hipMemsetAsync(hist, 0, kOrderHistBytes, st));
-  const int64_t blocks = blocks_for(n_rows);
-  BF_LAUNCH("order_hist_kernel", order_hist_kernel, dim3(unsigned(blocks < 2048 ? blocks : 2048)), dim3(kThreads), 0,
-            st, ptr, n_rows, hist);
+  const int64_t blocks = order_blocks(n_rows);
+  auto* counts = static_cast<uint32_t*>(ws);
+  auto* totals = reinterpret_cast<uint32_t*>(static_cast<char*>(ws) +
+                                             align_up(size_t(blocks) * kBuckets * sizeof(uint32_t)));
+  BF_LAUNCH("order_count_kernel", order_count_kernel, dim3(unsigned(blocks)), dim3(kThreads), 0, st, ptr, n_rows,
+            blocks, counts);
   BF_CHECK_LAUNCH();
-  const int64_t chunk = kOrderChunk;
-  BF_LAUNCH("order_scatter_kernel", order_scatter_kernel, dim3(unsigned(ceil_div(n_rows, chunk))), dim3(kThreads), 0,
-            st, ptr, n_rows, chunk, hist, cursor, order, spans, threshold, item_size, n_slots, packed);
+  BF_LAUNCH("radix_scan_kernel", sort::radix_scan_kernel, dim3(kBuckets), dim3(kThreads), 0, st, counts, blocks,
+            totals);
+  BF_CHECK_LAUNCH();
+  BF_LAUNCH("order_place_kernel", order_place_kernel, dim3(unsigned(blocks)), dim3(kThreads), 0, st, ptr, n_rows,
+            blocks, counts, totals, order, spans, threshold, item_size, n_slots, packed);
   BF_CHECK_LAUNCH();
   return BF_OK;
 }
@@ -1081,7 +1211,7 @@ int launch_row_order(const int64_t* ptr, int64_t n_rows, int32_t* order, uint64_
 
 extern "C" int bf_row_order_workspace_size(int64_t n_rows, size_t* bytes) {
   BF_CHECK_ARG(bytes && n_rows >= 0, "row_order_workspace_size: bad arguments");
-  *bytes = kOrderHistBytes + 256;
+  *bytes = order_counts_bytes(n_rows) + 256;
   return BF_OK;
 }
 
@@ -1093,15 +1223,14 @@ extern "C" int bf_row_order(const int64_t* ptr, int64_t n_rows, int32_t* order, 
   size_t need = 0;
   bf_row_order_workspace_size(n_rows, &need);
   BF_CHECK_ARG(workspace && workspace_bytes >= need, "row_order: workspace %zu < %zu bytes", workspace_bytes, need);
-  return launch_row_order(ptr, n_rows, order, spans, static_cast<uint32_t*>(workspace), 0, 1, 0, nullptr,
-                          as_stream(stream));
+  return launch_row_order(ptr, n_rows, order, spans, workspace, 0, 1, 0, nullptr, as_stream(stream));
 }
 
 extern "C" int bf_row_order_and_plan_workspace_size(int64_t n_rows, int64_t heavy_cap, size_t* bytes) {
   BF_CHECK_ARG(bytes && n_rows >= 0 && heavy_cap >= 0, "row_order_and_plan_workspace_size: bad arguments");
   const int64_t n_slots = heavy_cap < n_rows ? heavy_cap : n_rows;
   const size_t slab = align_up(size_t(n_slots > 0 ? n_slots : 1) * 8);
-  *bytes = align_up(kOrderHistBytes) + 2 * slab + align_up(plan_slots_scan_bytes(n_slots)) + 256;
+  *bytes = order_counts_bytes(n_rows) + 2 * slab + align_up(plan_slots_scan_bytes(n_slots)) + 256;
   return BF_OK;
 }
 
@@ -1131,16 +1260,21 @@ extern "C" int bf_row_order_and_plan(const int64_t* ptr, int64_t n_rows, int32_t
   const int64_t n_slots = heavy_cap < n_rows ? heavy_cap : n_rows;
   const size_t slab = align_up(size_t(n_slots) * 8);
   char* ws = static_cast<char*>(workspace);
-  auto* hist = reinterpret_cast<uint32_t*>(ws);
-  auto* packed = reinterpret_cast<uint64_t*>(ws + align_up(kOrderHistBytes));
-  auto* packed_off = reinterpret_cast<uint64_t*>(ws + align_up(kOrderHistBytes) + slab);
-  void* temp = ws + align_up(kOrderHistBytes) + 2 * slab;
+  const size_t ob = order_counts_bytes(n_rows);
+  auto* packed = reinterpret_cast<uint64_t*>(ws + ob);
+  auto* packed_off = reinterpret_cast<uint64_t*>(ws + ob + slab);
+  void* temp = ws + ob + 2 * slab;
   size_t temp_bytes = plan_slots_scan_bytes(n_slots);
-  const int rc = launch_row_order(ptr, n_rows, order, spans, hist, threshold, item_size, n_slots, packed, st);
+  const int rc = launch_row_order(ptr, n_rows, order, spans, ws, threshold, item_size, n_slots, packed, st);
   if (rc) return rc;
-  BF_CHECK_HIP(prim::exclusive_sum(temp, temp_bytes, static_cast<const uint64_t*>(packed), packed_off, n_slots, st));
+  // few slots: split_rows_kernel sums the slots before its block itself, with no scan launch
+  const bool in_block = n_slots <= kPlanInBlockSlots;
+  if (!in_block)
+    BF_CHECK_HIP(prim::exclusive_sum(temp, temp_bytes, static_cast<const uint64_t*>(packed), packed_off, n_slots,
+                                     st));
   BF_LAUNCH("split_rows_kernel", split_rows_kernel, dim3(blocks_for(n_slots)), dim3(kThreads), 0, st, packed,
-            packed_off, order, n_slots, item_cap, nitems, item_off, item_row, heavy_rows, heavy_cap, counts);
+            in_block ? nullptr : packed_off, order, n_slots, item_cap, nitems, item_off, item_row, heavy_rows,
+            heavy_cap, counts);
   BF_CHECK_LAUNCH();
   return BF_OK;
 }

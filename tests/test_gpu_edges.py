@@ -456,19 +456,29 @@ def test_first_row_plan_equals_the_generic_plan(hip_device, n_rows, chunk, item)
     assert torch.equal(one.heavy_rows[:gen.heavy], gen.heavy_rows[:gen.heavy])
 
 
-@pytest.mark.parametrize("chunk,item", [(128, 768), (4, 5), (16, 3)])
-def test_plan_from_the_row_order_equals_the_generic_plan(hip_device, chunk, item):
+@pytest.mark.parametrize("chunk,item,n,e", [(128, 768, 3000, 30000), (4, 5, 3000, 30000), (16, 3, 3000, 30000),
+                                            (4, 5, 40000, 400000)])
+def test_plan_from_the_row_order_equals_the_generic_plan(hip_device, chunk, item, n, e):
     """The split rows are the longest-first order's first slots: the plan written from them holds the
-    same split rows, item counts and counts as the generic plan, only numbered in slot order."""
+    same split rows, item counts and counts as the generic plan, only numbered in slot order. Plans of at
+    most 32768 slots form their item offsets inside split_rows_kernel, larger ones through a device scan
+    (the 40000-row graph): the generic plan is also checked against numpy."""
     from budgetformer_amd import hip_ops
-    n, e = 3000, 30000
     rowptr, col = _graph(n, e, seed=chunk * 10 + item)
     ptr = torch.from_numpy(rowptr).to(hip_device)
     nnz = int(rowptr[-1])
     gen = hip_ops.split_plan(ptr, nnz, chunk, item)
+    L = np.diff(rowptr)
+    nit_ref = np.where(L > chunk, np.minimum(-(-L // item), 160), 0)
+    assert gen.items == nit_ref.sum() and gen.heavy == int((L > chunk).sum())
+    assert np.array_equal(gen.nitems[:n].cpu().numpy(), nit_ref)
+    assert np.array_equal(gen.item_off[:n].cpu().numpy(), np.concatenate([[0], np.cumsum(nit_ref)[:-1]]))
+    assert np.array_equal(gen.item_row[:gen.items].cpu().numpy(), np.repeat(np.arange(n), nit_ref))
     order, spans, plan = hip_ops.row_order_and_plan(ptr, nnz, chunk, item)
     hip_ops.resolve_plans(plan)
     assert (plan.items, plan.heavy) == (gen.items, gen.heavy) and gen.heavy > 0
+    ro = order.cpu().numpy()
+    assert np.array_equal(np.sort(ro), np.arange(n)) and (np.diff(np.minimum(L, 255)[ro]) <= 0).all()
     heavy = plan.heavy_rows[:plan.heavy].cpu().numpy()
     assert np.array_equal(np.sort(heavy), gen.heavy_rows[:gen.heavy].cpu().numpy())
     assert np.array_equal(heavy, order[:plan.heavy].cpu().numpy())           # slot order
@@ -565,11 +575,25 @@ def test_row_pointers_across_long_runs_of_empty_rows(hip_device):
     assert np.array_equal(a[0].cpu().numpy(), np.concatenate([[0], np.cumsum(np.bincount(kvn, minlength=tr + 1))]))
 
 
+@pytest.mark.parametrize("n_rows", [2_000_000, 4_300_000])
+def test_table_row_pointers_both_scan_routes(hip_device, n_rows):
+    """A table's row pointers (with the token row): up to 1024 blocks of 4096 rows in two launches that
+    sum the blocks before their own, past that through a device scan (4.3M rows). Both equal numpy's
+    running sum."""
+    from budgetformer_amd import hip_ops
+    rng = np.random.default_rng(n_rows)
+    row_len = rng.integers(0, 9, n_rows).astype(np.int32)
+    table = torch.zeros((n_rows, 8), dtype=torch.int32, device=hip_device)
+    qptr = hip_ops.table_qptr(table, torch.from_numpy(row_len).to(hip_device), global_token=True)
+    lens = np.concatenate([[n_rows], row_len.astype(np.int64) + 1])        # the token row, then kv 0 + row
+    assert np.array_equal(qptr.cpu().numpy(), np.concatenate([[0], np.cumsum(lens)]))
+
+
 @pytest.mark.parametrize("n,width,lo", [(120_000, 12, 8), (600_000, 4, 2), (40_000, 8, 2)])
 def test_packed_reverse_index_onesweep_sizes(hip_device, n, width, lo):
-    """Past 64K keys the sorts run as onesweep radix passes instead of a merge sort, the packed reverse
-    index over only its 16 to 20 kv-id bits. The result must equal the pair-sort route and numpy's stable
-    order."""
+    """Reverse indexes of 0.1M to 2M keys: the packed route sorts only the 16 to 20 kv-id bits with the
+    library's radix sort (two 9-bit passes for 18 bits, three 8-bit ones otherwise). The result must
+    equal the pair-sort route and numpy's stable order."""
     from budgetformer_amd import hip_ops
     rng = np.random.default_rng(n)
     row_len = rng.integers(lo, width + 1, n).astype(np.int32)
