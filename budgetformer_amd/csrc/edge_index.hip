@@ -105,32 +105,49 @@ __global__ __launch_bounds__(kThreads) void row_block_sums_kernel(const int32_t*
   if (threadIdx.x == 0) bsum[blockIdx.x] = s;
 }
 
-// Thread i of block b scans rows b * kPtrRows + i * kPtrRowsPerThread + [0, kPtrRowsPerThread).
+// Wave w of block b scans rows b * kPtrRows + w * (kPtrRows / 4) + [0, kPtrRows / 4) in rounds of 64
+// (coalesced loads and stores, shuffles only), then adds the earlier waves' and blocks' totals.
 __global__ __launch_bounds__(kThreads) void row_ptr_kernel(const int32_t* __restrict__ row_len, int64_t n_rows,
                                                            int token, int lead, int64_t token_len,
                                                            const int64_t* __restrict__ bsum,
                                                            int64_t* __restrict__ qptr) {
   __shared__ int64_t tmp[kThreads / 64];
-  __shared__ uint64_t stmp[kThreads / 64];
+  __shared__ int64_t wtot[kThreads / 64];
   const int64_t n_q = n_rows + lead;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   int64_t before = 0;
   for (int64_t k = threadIdx.x; k < int64_t(blockIdx.x); k += kThreads) before += bsum[k];
   before = block_sum_i64(before, tmp);
-  const int64_t t0 = int64_t(blockIdx.x) * kPtrRows + int64_t(threadIdx.x) * kPtrRowsPerThread;
-  int64_t len[kPtrRowsPerThread], s = 0;
+  const int64_t t0 = int64_t(blockIdx.x) * kPtrRows + int64_t(w) * (64 * kPtrRowsPerThread) + lane;
+  int64_t v[kPtrRowsPerThread];
 #pragma unroll
   for (int u = 0; u < kPtrRowsPerThread; ++u) {
-    const int64_t t = t0 + u;
-    len[u] = t < n_q ? row_length(row_len, t, token, lead, token_len) : 0;
-    s += len[u];
+    const int64_t t = t0 + u * 64;
+    v[u] = t < n_q ? row_length(row_len, t, token, lead, token_len) : 0;
   }
-  int64_t run = before + int64_t(block_excl_scan_u64(uint64_t(s), stmp));
+  int64_t run = 0;
+#pragma unroll
+  for (int u = 0; u < kPtrRowsPerThread; ++u) {
+    int64_t x = v[u];
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int64_t y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
+    }
+    v[u] = run + x;                                 // inclusive within the wave
+    run += __shfl(x, 63, 64);
+  }
+  if (lane == 0) wtot[w] = run;
+  __syncthreads();
+  int64_t base = before;
+#pragma unroll
+  for (int i = 0; i < kThreads / 64; ++i)
+    if (i < w) base += wtot[i];
   if (blockIdx.x == 0 && threadIdx.x == 0) qptr[0] = 0;
 #pragma unroll
   for (int u = 0; u < kPtrRowsPerThread; ++u) {
-    const int64_t t = t0 + u;
-    run += len[u];
-    if (t < n_q) qptr[t + 1] = run;
+    const int64_t t = t0 + u * 64;
+    if (t < n_q) qptr[t + 1] = base + v[u];
   }
 }
 
@@ -596,8 +613,17 @@ __global__ __launch_bounds__(kThreads) void split_rows_kernel(
   const int64_t j = int64_t(blockIdx.x) * kThreads + threadIdx.x;
   uint64_t in_block_off = 0;
   if (!packed_off) {
+    // With an order the split rows hold its first slots (longest first), so a slot's entry is zero only
+    // past the last split row: a thread stops at its first zero. Four loads in flight per step.
+    const int64_t lim = int64_t(blockIdx.x) * kThreads;
     uint64_t before = 0;
-    for (int64_t k = threadIdx.x; k < int64_t(blockIdx.x) * kThreads; k += kThreads) before += packed[k];
+    for (int64_t k = threadIdx.x; k < lim; k += 4 * kThreads) {
+      uint64_t x[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) x[u] = k + u * kThreads < lim ? packed[k + u * kThreads] : 0;
+      before += x[0] + x[1] + x[2] + x[3];
+      if (order && x[3] == 0) break;
+    }
     // the block's total of `before` is the sum over every earlier slot
     const uint64_t lo = block_excl_scan_u64(before, scan_tmp);
     __shared__ uint64_t s_before;
