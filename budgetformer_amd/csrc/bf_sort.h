@@ -15,7 +15,7 @@
 // rocPRIM's onesweep sort on the reverse-index keys of the benchmark builds
 // (gfx950): 0.82M keys, 18 bits: 39 us (2 passes of 9 bits) vs 76 us; 31M
 // keys, 22 bits: 584 us vs 614 us; 32M keys: 625 vs 639 us; 210M keys, 27
-// bits: 5.59 ms vs 5.15 ms (onesweep's single read per pass wins there).
+// bits: 5.28 ms vs 5.13 ms (onesweep's single read per pass wins there).
 #pragma once
 
 #include <cstdint>
@@ -29,7 +29,9 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 
 // The digit width and tile of a sort: 9-bit digits when they save a pass
-// (18 and 27 bits), else 8; 2048-key tiles up to 4M keys, else 4096.
+// (18 and 27 bits), else 8. 9-bit tiles grow with the key count (2048 keys up
+// to 4M keys, 4096 up to 32M, then 6144: fewer tiles, a smaller count array;
+// at 210M keys 5.28 ms against 5.61 with 4096); 8-bit tiles hold 4096.
 struct Plan {
   int radix;
   int items;
@@ -41,7 +43,7 @@ inline Plan make_plan(int64_t n, int bits) {
   Plan p{};
   const int p8 = (bits + 7) / 8, p9 = (bits + 8) / 9;
   p.radix = p9 < p8 ? 9 : 8;
-  p.items = (p.radix == 9 && n <= (int64_t(1) << 22)) ? 8 : 16;
+  p.items = p.radix == 8 ? 16 : n <= (int64_t(1) << 22) ? 8 : n <= (int64_t(1) << 25) ? 16 : 24;
   p.passes = bits > 0 ? (bits + p.radix - 1) / p.radix : 0;
   const int64_t tile = int64_t(kThreads) * p.items;
   p.tiles = (n + tile - 1) / tile;
@@ -301,9 +303,12 @@ inline int radix_sort_keys(const uint64_t* in, uint64_t* out, int64_t n, int beg
   auto* totals = reinterpret_cast<uint32_t*>(ws + align256(size_t(n) * 8) +
                                              align256(size_t(p.tiles) * (size_t(1) << p.radix) * 4));
   if (p.radix == 9)
-    return p.items == 8 ? run_passes<9, 8>(p, in, out, alt, n, n_dev, n_sub, begin_bit, end_bit, counts, totals, st)
-                        : run_passes<9, 16>(p, in, out, alt, n, n_dev, n_sub, begin_bit, end_bit, counts, totals,
-                                            st);
+    return p.items == 8    ? run_passes<9, 8>(p, in, out, alt, n, n_dev, n_sub, begin_bit, end_bit, counts, totals,
+                                              st)
+           : p.items == 16 ? run_passes<9, 16>(p, in, out, alt, n, n_dev, n_sub, begin_bit, end_bit, counts, totals,
+                                               st)
+                           : run_passes<9, 24>(p, in, out, alt, n, n_dev, n_sub, begin_bit, end_bit, counts, totals,
+                                               st);
   return run_passes<8, 16>(p, in, out, alt, n, n_dev, n_sub, begin_bit, end_bit, counts, totals, st);
 }
 

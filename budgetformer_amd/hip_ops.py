@@ -796,6 +796,9 @@ def split_plan(ptr: torch.Tensor, nnz: int, threshold: int = DEFAULT_CHUNK, item
 
 
 # ------------------------------------------------------------------ attention index
+NO_READBACK_MAX_ENTRIES = 1 << 23   # tables of up to this many entries (at capacity) build without a host read
+
+
 def _to_cap(t: torch.Tensor, cap: int) -> torch.Tensor:
     """An exact per-entry array in a buffer of the index's capacity (entries past its length hold nothing)."""
     if t.numel() == cap:
@@ -1054,13 +1057,17 @@ class AttentionIndex:
         token_column = 0 if not global_token else (1 if tr >= 0 else 2)
         idx = cls(n_q=n_q_tab, n_kv=n_kv, qptr=qptr, kv_all=None, chunk=chunk, item=item,
                   token_column=token_column, _q_known=known)
+        bound = n_rows * width + (n_rows if global_token else 0) + max(tr, 0)
         if known is not None:
-            # only the token row can be split: its plan is written in one pass, before the host waits
-            # for nnz
-            bound = n_rows * width + (n_rows if global_token else 0) + max(tr, 0)
+            # only the token row can be split: its plan is written in one pass, before any read of nnz
             idx.qplan = split_plan_first_row(n_q_tab, known[0], bound, chunk, item, idx._plan_counts(0))
+        # A small index is launch-bound: it is built at the capacity (every row full) with nothing read
+        # back, so the host runs ahead of the kernels. A large one reads nnz once and sizes its arrays and
+        # grids exactly (a B=32 table fills well under half of its capacity).
         qptr, idx.kv_all, idx._rkeys = table_to_csr(table, row_len, global_token, with_keys=True, qptr=qptr,
-                                                    token_row=tr, exact=False)
+                                                    token_row=tr, exact=bound > NO_READBACK_MAX_ENTRIES)
+        if bound > NO_READBACK_MAX_ENTRIES:
+            idx._nnz = idx.kv_all.numel()
         return idx
 
     @classmethod

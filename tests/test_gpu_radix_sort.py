@@ -1,5 +1,5 @@
 """The reverse index's radix sort (bf_radix_sort_keys) against numpy's stable argsort of the same bit
-field, for every digit plan it picks: 9-bit digits with 2048- and 4096-key tiles, 8-bit digits, one
+field, for every digit plan it picks: 9-bit digits with 2048-, 4096- and 6144-key tiles, 8-bit digits, one
 partial tile, a single-bit field, all 64 bits (sign bit included) and an empty bit range. Keys mix
 uniform 64-bit patterns with fields drawn from a steep power law (long runs of one digit, many equal
 fields), so stability is checked on ties. Integer work: bit-exact."""
@@ -40,6 +40,7 @@ def _expected(keys, b0, b1):
     (1000, 3, 21),             # 18 bits: two 9-bit passes, one partial tile
     (823_801, 22, 40),         # the c2 reverse-index shape
     (5_000_000, 10, 28),       # 18 bits past 4M keys: 4096-key tiles
+    (34_000_000, 5, 23),       # 18 bits past 32M keys: 6144-key tiles
     (3_000_000, 20, 42),       # 22 bits: three 8-bit passes
     (2_000_000, 0, 27),        # 27 bits: three 9-bit passes
     (300_000, 0, 64),          # every bit, the top one included: eight 8-bit passes
