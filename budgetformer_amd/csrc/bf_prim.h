@@ -28,7 +28,9 @@ namespace prim {
 // the shorter route: on gfx950 a 0.82M-key sort of 18 bits takes 86 us as
 // block sort + 10 merge passes and 63 us as onesweep (histogram + 3 digit
 // passes). Merge sort is kept for sizes where its few passes are cheaper than
-// onesweep's fixed launches.
+// onesweep's fixed launches. (The per-step reverse-index sort uses this
+// build's own radix sort, bf_sort.h; these wrappers serve the once-per-graph
+// COO -> CSR, coalesce and generator sorts.)
 constexpr size_t kMergeSortLimit = size_t(1) << 16;
 using radix_config = rocprim::radix_sort_config<rocprim::default_config, rocprim::default_config,
                                                 rocprim::default_config, kMergeSortLimit>;

@@ -292,7 +292,8 @@ int bf_chung_lu(int64_t num_nodes, int64_t pairs, double exponent, double i0, do
  * bf_table_csr_ptr writes qptr (a prefix sum of the row lengths) and returns
  * nnz = qptr[n_q] on the host (it synchronises the stream, so the caller can
  * size kv; with nnz_host NULL it only enqueues the scan and the caller reads
- * qptr[n_q] when it needs it); bf_table_to_csr then fills kv, and, when rkey is not NULL,
+ * qptr[n_q] when it needs it, or sizes kv and rkey for every row full, of
+ * which only the first nnz / key count are written); bf_table_to_csr then fills kv, and, when rkey is not NULL,
  * rkey uint64 = (id << (q_bits + slot_bits) | query << slot_bits | slot) for
  * each of the table's own entries in CSR order (slot = position in the query's
  * row), the sort keys bf_reverse_index_packed takes: [nnz] without the token,
@@ -352,7 +353,9 @@ int bf_reverse_index(const int64_t* qptr, const int32_t* kv, int64_t n_q, int64_
  * decodes kq. (global_token, token_row) as given to bf_table_to_csr: the
  * token's entries, which have no key, take their fixed places (kv 0's segment
  * first, row by row; each token-row entry first in its kv's segment), the
- * sorted keys the rest. nnz counts every entry. ke (may be NULL) is decoded in
+ * sorted keys the rest. nnz counts every entry, or is any capacity above that
+ * count (the keys, sorted, kq and ke then sized for it): the kernels take the
+ * count itself from qptr[n_q] on the device. ke (may be NULL) is decoded in
  * the same pass: qptr[query] + slot; it is a random gather of qptr, which the
  * dk/dv pass needs only with a bias, factor or dropout, so a caller may keep
  * `sorted` and call bf_reverse_entries later instead. Same kptr / kq / ke as bf_reverse_index.
