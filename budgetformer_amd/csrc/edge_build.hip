@@ -145,6 +145,21 @@ __device__ __forceinline__ bool sorted_contains(const int32_t* __restrict__ a, i
   return lo < end && a[lo] == x;
 }
 
+// ---- 32-bit keys (the RW register ranking and the fused light/heavy kernel).
+// For a fixed query q, key(src) = (src*A + base_q) mod 2^31 with A odd is a
+// bijection of src < 2^31, so a row's candidates never tie and the KR smallest
+// keys alone name the winners: src = ((key - base_q) * A^-1) mod 2^31. A list
+// entry is then one 32-bit value, inserted without a branch.
+constexpr uint32_t kKeyMul = 1103515245u;
+constexpr uint32_t kKeyMulInv = 0xeeb9eb65u;   // kKeyMul * kKeyMulInv == 1 (mod 2^32)
+constexpr uint32_t kNoKey = 0xffffffffu;       // above every 31-bit key
+
+__device__ __forceinline__ uint32_t key_base(uint32_t q, uint32_t kc) { return q * 214013u + kc; }
+__device__ __forceinline__ uint32_t key_of(uint32_t src, uint32_t base) { return (src * kKeyMul + base) & 0x7fffffffu; }
+__device__ __forceinline__ int32_t src_of(uint32_t key, uint32_t base) {
+  return int32_t(((key - base) * kKeyMulInv) & 0x7fffffffu);
+}
+
 // The walk of lane p of query row qi (walk id q*P + p): step(l), called for
 // l = 0, 1, ... in turn, is candidate l, (key << 32 | kv) of the node reached
 // at step l, or kNone for a filtered step (a stay after step 0, a query
@@ -191,6 +206,13 @@ struct RwWalk {
     cur = nxt;
     return keep ? (uint64_t(edge_key(uint32_t(nxt), uint32_t(q), kc)) << 32) | uint32_t(nxt) : kNone;
   }
+
+  // The same step as its key alone (kNoKey for a dropped step): for one query the key is a bijection of
+  // the source, so ordering keys orders the (key, kv) values above, and src_of recovers kv.
+  __device__ __forceinline__ uint32_t step_key(int l) {
+    const uint64_t v = step(l);
+    return v == kNone ? kNoKey : uint32_t(v >> 32);
+  }
 };
 
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t x, int o) {
@@ -200,12 +222,12 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t x, int o) {
 }
 
 // Orders a, b ascending (asc) or descending.
-__device__ __forceinline__ void cmp_swap(uint64_t& a, uint64_t& b, bool asc) {
-  const bool sw = (a > b) == asc;
-  const uint64_t x = sw ? b : a, y = sw ? a : b;
-  a = x;
-  b = y;
+__device__ __forceinline__ void cmp_swap32(uint32_t& a, uint32_t& b, bool asc) {
+  const uint32_t lo = min(a, b), hi = max(a, b);
+  a = asc ? lo : hi;
+  b = asc ? hi : lo;
 }
+
 
 // rw_select for P a power of two <= 64 and L <= R (R a power of two <= 16):
 // lane p keeps its walk's candidates in registers x[0, R) (kNone past L), the
@@ -224,11 +246,15 @@ __global__ __launch_bounds__(kThreads) void rw_select_reg_kernel(
   const int p = tid & (P - 1);
   const int64_t qi = int64_t(blockIdx.x) * (kThreads / P) + tid / P;
   if (qi >= n_q) return;                      // a query's P lanes leave together
-  uint64_t x[R];
+  // the candidates as 32-bit keys (src_of names their kv): min / max compare-exchanges and one shuffle
+  // per cross-lane step, where (key << 32 | kv) values took 64-bit compares, selects and two shuffles
+  uint32_t x[R];
+  uint32_t base;
   {
     RwWalk walk(rowptr, col, rec, num_nodes, q_lo, qids, qi, P, p, L, kc, u, seed, offset, sub_ptr, sub_src);
+    base = key_base(uint32_t(walk.q), kc);
 #pragma unroll
-    for (int r = 0; r < R; ++r) x[r] = r < L ? walk.step(r) : kNone;
+    for (int r = 0; r < R; ++r) x[r] = r < L ? walk.step_key(r) : kNoKey;
   }
   const int M2 = P * R;
   // blocks of up to R elements: in registers
@@ -238,7 +264,7 @@ __global__ __launch_bounds__(kThreads) void rw_select_reg_kernel(
     for (int j = k >> 1; j > 0; j >>= 1) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        if ((r ^ j) > r) cmp_swap(x[r], x[r ^ j], ((p * R + r) & k) == 0);
+        if ((r ^ j) > r) cmp_swap32(x[r], x[r ^ j], ((p * R + r) & k) == 0);
       }
     }
   }
@@ -249,15 +275,15 @@ __global__ __launch_bounds__(kThreads) void rw_select_reg_kernel(
       const bool keep_min = ((p & pm) == 0) == asc;
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const uint64_t y = shfl_xor_u64(x[r], pm);
-        x[r] = keep_min ? (y < x[r] ? y : x[r]) : (y > x[r] ? y : x[r]);
+        const uint32_t y = __shfl_xor(x[r], pm, 64);
+        x[r] = keep_min ? min(y, x[r]) : max(y, x[r]);
       }
     }
 #pragma unroll
     for (int j = R >> 1; j > 0; j >>= 1) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        if ((r ^ j) > r) cmp_swap(x[r], x[r ^ j], asc);
+        if ((r ^ j) > r) cmp_swap32(x[r], x[r ^ j], asc);
       }
     }
   }
@@ -267,8 +293,8 @@ __global__ __launch_bounds__(kThreads) void rw_select_reg_kernel(
   for (int r = 0; r < R; ++r) {
     const int i = p * R + r;
     if (i < K) {
-      sel_kv[qi * K + i] = x[r] != kNone ? int32_t(uint32_t(x[r])) : -1;
-      cnt += x[r] != kNone ? 1 : 0;
+      sel_kv[qi * K + i] = x[r] != kNoKey ? src_of(x[r], base) : -1;
+      cnt += x[r] != kNoKey ? 1 : 0;
     }
   }
   for (int i = M2 + p; i < K; i += P) sel_kv[qi * K + i] = -1;
@@ -361,20 +387,6 @@ constexpr int kScanUnroll = BF_SCAN_UNROLL;  // in-neighbour loads in flight per
 #endif
 constexpr int kScanX4Unroll = BF_SCAN_X4_UNROLL;  // 16-byte chunks in flight per thread (light rows)
 
-// ---- 32-bit key lists of the fused light/heavy kernel.
-// For a fixed query q, key(src) = (src*A + base_q) mod 2^31 with A odd is a
-// bijection of src < 2^31, so a row's candidates never tie and the KR smallest
-// keys alone name the winners: src = ((key - base_q) * A^-1) mod 2^31. A list
-// entry is then one 32-bit value, inserted without a branch.
-constexpr uint32_t kKeyMul = 1103515245u;
-constexpr uint32_t kKeyMulInv = 0xeeb9eb65u;   // kKeyMul * kKeyMulInv == 1 (mod 2^32)
-constexpr uint32_t kNoKey = 0xffffffffu;       // above every 31-bit key
-
-__device__ __forceinline__ uint32_t key_base(uint32_t q, uint32_t kc) { return q * 214013u + kc; }
-__device__ __forceinline__ uint32_t key_of(uint32_t src, uint32_t base) { return (src * kKeyMul + base) & 0x7fffffffu; }
-__device__ __forceinline__ int32_t src_of(uint32_t key, uint32_t base) {
-  return int32_t(((key - base) * kKeyMulInv) & 0x7fffffffu);
-}
 
 // Folds candidates src[i], src[i+stride], ... (< end) of query q, each as the
 // value (key << 32 | position in the row), into the sorted register list lk
