@@ -95,7 +95,8 @@ def kernel_bytes(s, D, H, lens_q, lens_k, n_token_rec=0, entry_ids=False):
 
     With a token column (n_token_rec records) the dq pass also writes key 0's dK/dV terms, 2*D floats per
     record, and the dk/dv pass reads those records instead of gathering key 0's entries and its K, V rows.
-    entry_ids: the dk/dv pass also reads each gathered entry's CSR position (a dropout, bias or factor)."""
+    entry_ids: the dk/dv pass also reads each gathered entry's slot and its query's row start (qptr), which
+    give its CSR position (a dropout, bias or factor)."""
     n_q, nnz = lens_q.size, int(lens_q.sum())
     n_kv = lens_k.size
     nk_touched = int((lens_k > 0).sum())
@@ -113,7 +114,7 @@ def kernel_bytes(s, D, H, lens_q, lens_k, n_token_rec=0, entry_ids=False):
         # dK, dV written for every row; K, V read for rows with entries; Q and dO per gathered entry,
         # the {1/D', Delta/D'} row stats per gathered entry, kq ids, kptr, row order (+ token records)
         "attn_bwd_kv_kernel": row * (2 * n_kv + 2 * nk_touched + 2 * gathered) + 8 * H * gathered
-        + 4 * gathered + 12 * n_kv + rec_bytes + (4 * gathered if entry_ids else 0),
+        + 4 * gathered + 12 * n_kv + rec_bytes + (12 * gathered if entry_ids else 0),
     }
 
 
@@ -272,7 +273,7 @@ def main(argv=None):
              "attn_bwd_q_reduce_kernel", "attn_bwd_kv_reduce_kernel", "rw_select_reg_kernel", "rw_select_kernel",
              "real_select_fused_kernel", "row_block_sums_kernel", "row_ptr_kernel", "table_fill_kernel",
              "radix_count_kernel", "radix_scan_kernel", "radix_scatter_kernel", "unpack_rkey_kernel",
-             "reverse_entries_kernel", "order_count_kernel", "order_place_kernel", "split_rows_kernel", "rocprim"]
+             "reverse_slots_kernel", "order_count_kernel", "order_place_kernel", "split_rows_kernel", "rocprim"]
     if args.pmc_summary or args.req_summary:
         if args.pmc_summary:
             md, data = pmc_summary(*args.pmc_summary, args.copy_bytes, names)

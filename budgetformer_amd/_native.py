@@ -30,7 +30,7 @@ class AttnIndex(C.Structure):
     """Mirror of ``struct bf_attn_index``."""
     _fields_ = [
         ("n_q", i64), ("n_kv", i64), ("nnz", i64),
-        ("qptr", vp), ("kv", vp), ("kptr", vp), ("kq", vp), ("ke", vp),
+        ("qptr", vp), ("kv", vp), ("kptr", vp), ("kq", vp), ("ks", vp),
         ("chunk", i32), ("item", i32),
         ("q_items", i32), ("q_heavy", i32),
         ("q_nitems", vp), ("q_item_off", vp), ("q_item_row", vp), ("q_heavy_rows", vp),
@@ -97,7 +97,7 @@ _SIGS = {
                                           vp, sz, vp]),
     "bf_radix_sort_workspace_size": (C.c_int, [i64, i32, i32, C.POINTER(sz)]),
     "bf_radix_sort_keys": (C.c_int, [vp, vp, i64, i32, i32, vp, sz, vp]),
-    "bf_reverse_entries": (C.c_int, [vp, P_i64, i64, i64, i32, i32, i32, i64, P_i32, vp]),
+    "bf_reverse_slots": (C.c_int, [vp, P_i64, i64, i64, i32, i32, i32, i64, P_i32, vp]),
     "bf_expand_rows": (C.c_int, [P_i64, i64, i64, P_i64, vp]),
     "bf_split_item_capacity": (i64, [i64, i32, i32]),
     "bf_split_row_capacity": (i64, [i64, i32]),

@@ -913,8 +913,8 @@ __device__ __forceinline__ typename Elem<T>::Raw gather_row(const T* base, int64
 // pass keeps its register count (fp32: 91 VGPRs, five waves per SIMD).
 template <typename T, bool NT, int EX>
 __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __restrict__ dout,
-                                            const int32_t* __restrict__ kq,
-                                            const int32_t* __restrict__ ke, const EdgeIn& ex,
+                                            const int32_t* __restrict__ kq, const int32_t* __restrict__ ks,
+                                            const int64_t* __restrict__ qptr, const EdgeIn& ex,
                                             float* __restrict__ dbias,
                                             const float2* __restrict__ rstat, int64_t beg,
                                             int64_t end, const Shape& sh, const GroupPos& g,
@@ -936,6 +936,13 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
       const int id = ids.get(kq, i0, u, ok[u]);
       t[u] = ok[u] ? id : 0;
     }
+    // each entry's CSR position: its query row's start plus its slot in that row; the row starts are
+    // gathered before the rows, so the keep bits below wait for them alone and overlap the row gathers
+    int32_t epos[kUnroll];   // nnz < 2^31
+    if (EX) {
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) epos[u] = ok[u] ? ks[i0 + u] + int32_t(qptr[t[u]]) : 0;
+    }
     typename Elem<T>::Raw qr[kUnroll], gr[kUnroll];
     float2 rs[kUnroll];
 #pragma unroll
@@ -949,6 +956,8 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
         rs[u] = make_float2(0.f, 0.f);
       }
     }
+    IterDrop<kUnroll> drop{false, 0u};
+    if (EX) drop = iter_drop<kUnroll>(ex, epos, ok, sh, g);
     float d[kUnroll], w[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
@@ -961,13 +970,6 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
         d[u] += __shfl_xor(d[u], o, 64);
         w[u] += __shfl_xor(w[u], o, 64);
       }
-    }
-    int32_t epos[kUnroll];   // CSR positions of the entries (nnz < 2^31)
-    IterDrop<kUnroll> drop{false, 0u};
-    if (EX) {
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) epos[u] = ok[u] ? ke[i0 + u] : 0;
-      drop = iter_drop<kUnroll>(ex, epos, ok, sh, g);
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
@@ -996,12 +998,13 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
 
 // Blocks [0, k_items) take the key-side items, the rest one short key row per
 // group, longest rows first. EX: 0 plain, 1 dropout only, 2 bias / factor / dropout / dbias
-// (EX > 0 needs ke).
+// (EX > 0 needs ks and qptr).
 template <typename T, bool NT, bool PRE, int EX>
 __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const int64_t* __restrict__ kptr, const int32_t* __restrict__ kq,
-    const int32_t* __restrict__ ke, EdgeIn ex, float* __restrict__ dbias, const T* __restrict__ dout,
+    const int32_t* __restrict__ ks, const int64_t* __restrict__ qptr, EdgeIn ex, float* __restrict__ dbias,
+    const T* __restrict__ dout,
     const float2* __restrict__ rstat, T* __restrict__ dk, T* __restrict__ dv, const int32_t* __restrict__ order,
     const uint64_t* __restrict__ spans, Items kit, int k_items_arg, int64_t n_kv, Shape sh, int chunk,
     int rows_per_group, const float* __restrict__ token_rec, int q_items_arg, int64_t q_row_blocks,
@@ -1035,7 +1038,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
       sum_token_records<V>(token_rec, a0, a1, q_items, q_items_arg, sh, g, ak, av);
     } else {
       const typename Elem<T>::Raw kr = load_row_raw(k, r.row, sh.D, g), vr = load_row_raw(v, r.row, sh.D, g);
-      dkv_segment<T, NT, EX>(q, dout, kq, ke, ex, dbias, rstat, r.beg, r.end, sh, g, kr, vr, ak, av);
+      dkv_segment<T, NT, EX>(q, dout, kq, ks, qptr, ex, dbias, rstat, r.beg, r.end, sh, g, kr, vr, ak, av);
     }
     float z = 0.f;
     block_combine<V>(lds, kit.stride, sh, g, ak, av, true, z, false);
@@ -1106,7 +1109,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
 #pragma unroll
     for (int i = 0; i < V; ++i) ak[i] = av[i] = 0.f;
     const typename Elem<T>::Raw kr = load_row_raw(k, row, sh.D, g), vr = load_row_raw(v, row, sh.D, g);
-    dkv_segment<T, NT, EX>(q, dout, kq, ke, ex, dbias, rstat, beg, end, sh, g, kr, vr, ak, av);
+    dkv_segment<T, NT, EX>(q, dout, kq, ks, qptr, ex, dbias, rstat, beg, end, sh, g, kr, vr, ak, av);
     if (g.act) {                  // written once, not read again in the pass: past the caches
       Elem<T>::store_nt(dk + row * sh.D + g.col0, ak);
       Elem<T>::store_nt(dv + row * sh.D + g.col0, av);
@@ -1328,7 +1331,7 @@ int bwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
     const int mode = edge_mode(ex, dbias != nullptr);
 #define BF_LAUNCH_KV1(NT, PRE, EX)                                                                                 \
   BF_LAUNCH("attn_bwd_kv_kernel", (attn_bwd_kv_kernel<T, NT, PRE, EX>), dim3(unsigned(kv_blocks)), dim3(kBlock), lds, st, \
-            Q, K, Vv, idx->kptr, idx->kq, idx->ke, ex, dbias, dO, rstat, static_cast<T*>(dk),                        \
+            Q, K, Vv, idx->kptr, idx->kq, idx->ks, idx->qptr, ex, dbias, dO, rstat, static_cast<T*>(dk),            \
             static_cast<T*>(dv), idx->k_order, idx->k_spans, kit, idx->k_items, idx->n_kv, sh, idx->chunk,           \
             rows_per_group, token_rec, idx->q_items, int64_t(grid_for(idx->n_q, sh)), idx->plan_counts)
 #define BF_LAUNCH_KV(NT, PRE)           \
@@ -1435,8 +1438,8 @@ extern "C" int bf_attn_bwd(const bf_attn_index* idx, int32_t dtype, int32_t num_
   if ((rc = check_index(idx, true))) return rc;
   EdgeIn ex;
   if ((rc = make_edge_in(bias, factor, dropout, ex))) return rc;
-  BF_CHECK_ARG(idx->ke || idx->nnz == 0 || (!has_extra(ex) && !dbias),
-               "attn_bwd: a bias, factor, dropout or dbias needs the reverse entries' CSR positions (ke)");
+  BF_CHECK_ARG(idx->ks || idx->nnz == 0 || (!has_extra(ex) && !dbias),
+               "attn_bwd: a bias, factor, dropout or dbias needs the reverse entries' slots (ks)");
   BF_CHECK_ARG(q && k && v && Z && dout && dq && dk && dv && rowstat, "attn_bwd: null tensor");
   BF_CHECK_ARG((reinterpret_cast<uintptr_t>(rowstat) & 7u) == 0, "attn_bwd: rowstat must be 8-byte aligned");
   BF_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(dout) && aligned16(dq) && aligned16(dk) &&

@@ -311,18 +311,22 @@ __global__ void row_marks_kernel(const int64_t* __restrict__ ptr, int64_t n_rows
   if (ptr[r + 1] > b) marks[b] = int32_t(r);
 }
 
-__global__ void pack_row_entry_kernel(const int32_t* __restrict__ rows, int64_t nnz, uint64_t* __restrict__ vals) {
+// Entry i of row r as (r << 32 | slot), slot = i - ptr[r]: the value the pair sort carries.
+__global__ void pack_row_entry_kernel(const int32_t* __restrict__ rows, const int64_t* __restrict__ ptr, int64_t nnz,
+                                      uint64_t* __restrict__ vals) {
   const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
-  if (i < nnz) vals[i] = (uint64_t(uint32_t(rows[i])) << 32) | uint32_t(i);
+  if (i >= nnz) return;
+  const int32_t r = rows[i];
+  vals[i] = (uint64_t(uint32_t(r)) << 32) | uint32_t(i - ptr[r]);
 }
 
 __global__ void unpack_row_entry_kernel(const uint64_t* __restrict__ vals, int64_t nnz, int32_t* __restrict__ kq,
-                                        int32_t* __restrict__ ke) {
+                                        int32_t* __restrict__ ks) {
   const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
   if (i >= nnz) return;
   const uint64_t x = vals[i];
   kq[i] = int32_t(x >> 32);
-  ke[i] = int32_t(uint32_t(x));
+  ks[i] = int32_t(uint32_t(x));
 }
 
 // The Graphormer token's part of a table's reverse index (tok = 1): kv 0 is
@@ -351,11 +355,9 @@ struct TokenLayout {
   __device__ __forceinline__ bool token_entry(int64_t r) const { return lead && r >= 1 && r - 1 < token_len; }
 };
 
-// A table entry's CSR position from its key: qptr[query] + slot.
-__device__ __forceinline__ int32_t entry_of(uint64_t x, int kshift, int sbits, const int64_t* __restrict__ qptr) {
-  const int64_t q = int64_t((x >> sbits) & ((uint64_t(1) << (kshift - sbits)) - 1));
-  const int64_t slot = int64_t(x & ((uint64_t(1) << sbits) - 1));
-  return int32_t(qptr[q] + slot);
+// A table entry's slot in its query's row, from its key (no read of qptr).
+__device__ __forceinline__ int32_t slot_of(uint64_t x, int sbits) {
+  return int32_t(x & ((uint64_t(1) << sbits) - 1));
 }
 
 constexpr int kUnpackPerThread = 4;  // sorted keys per thread (kThreads apart), loaded before any store
@@ -368,18 +370,18 @@ __device__ __forceinline__ int64_t keyed_entries(const int64_t* __restrict__ nnz
   return n < 0 ? 0 : (n > cap ? cap : n);
 }
 
-// Sorted keys -> kptr (boundaries of the id field), kq, and ke when asked for.
+// Sorted keys -> kptr (boundaries of the id field), kq, and ks when asked for.
 // Blocks from key_blocks on write kv 0's segment with the token instead (what
 // token_reverse_kernel writes), saving its launch.
 __global__ __launch_bounds__(kThreads) void unpack_rkey_kernel(
     const uint64_t* __restrict__ keys, const int64_t* __restrict__ nnz_dev, int64_t n_token, int64_t key_cap,
-    int kshift, int sbits, TokenLayout tl, const int64_t* __restrict__ qptr, int64_t n_kv,
-    int64_t* __restrict__ kptr, int32_t* __restrict__ kq, int32_t* __restrict__ ke, int64_t key_blocks) {
+    int kshift, int sbits, TokenLayout tl, int64_t n_kv, int64_t* __restrict__ kptr, int32_t* __restrict__ kq,
+    int32_t* __restrict__ ks, int64_t key_blocks) {
   if (int64_t(blockIdx.x) >= key_blocks) {
     const int64_t j = (int64_t(blockIdx.x) - key_blocks) * kThreads + threadIdx.x;
     if (j < tl.c0) {
       kq[j] = int32_t(tl.lead + j);
-      if (ke) ke[j] = int32_t(qptr[tl.lead + j]);
+      if (ks) ks[j] = 0;                 // kv 0 opens every row from `lead` on
     }
     return;
   }
@@ -407,22 +409,22 @@ __global__ __launch_bounds__(kThreads) void unpack_rkey_kernel(
       kptr[r] = b;
       if (r < n_kv && tl.token_entry(r)) {
         kq[b] = 0;
-        if (ke) ke[b] = int32_t(r - 1);
+        if (ks) ks[b] = int32_t(r - 1);  // the token row lists kv r at slot r - 1
       }
     });
     if (i == n_keys) break;
     const int64_t o = tl.key_slot(i, int64_t(cur[u] >> kshift));
     kq[o] = int32_t((cur[u] >> sbits) & ((uint64_t(1) << (kshift - sbits)) - 1));
-    if (ke) ke[o] = entry_of(cur[u], kshift, sbits, qptr);
+    if (ks) ks[o] = slot_of(cur[u], sbits);
   }
 }
 
-// ke from the sorted keys (one thread per key, plus one past the end): with
+// ks from the sorted keys (one thread per key, plus one past the end): with
 // the token row, the thread that meets the first key with id >= r (or the
 // end) also writes kv r's token-row entry (r <= token_len), at kv r's start.
-__global__ void reverse_entries_kernel(const uint64_t* __restrict__ keys, const int64_t* __restrict__ nnz_dev,
-                                       int64_t n_token, int64_t key_cap, int kshift, int sbits, TokenLayout tl,
-                                       const int64_t* __restrict__ qptr, int32_t* __restrict__ ke) {
+__global__ void reverse_slots_kernel(const uint64_t* __restrict__ keys, const int64_t* __restrict__ nnz_dev,
+                                     int64_t n_token, int64_t key_cap, int kshift, int sbits, TokenLayout tl,
+                                     int32_t* __restrict__ ks) {
   const int64_t n_keys = keyed_entries(nnz_dev, n_token, key_cap);
   const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
   if (i > n_keys) return;
@@ -433,19 +435,18 @@ __global__ void reverse_entries_kernel(const uint64_t* __restrict__ keys, const 
     int64_t r_prev = i > 0 ? int64_t(keys[i - 1] >> kshift) : 0;
     if (r_here > top) r_here = top;
     if (r_prev > top) r_prev = top;
-    fill_gap(r_prev, r_here, i, [&](int64_t r, int64_t v) { ke[tl.row_base(r) + v] = int32_t(r - 1); });
+    fill_gap(r_prev, r_here, i, [&](int64_t r, int64_t v) { ks[tl.row_base(r) + v] = int32_t(r - 1); });
   }
-  if (i < n_keys) ke[tl.key_slot(i, int64_t(x >> kshift))] = entry_of(x, kshift, sbits, qptr);
+  if (i < n_keys) ks[tl.key_slot(i, int64_t(x >> kshift))] = slot_of(x, sbits);
 }
 
-// kv 0's reverse segment with the token (kq and/or ke): thread j < c0 writes the entry of attention row
-// lead + j, first in that row (CSR position qptr[lead + j]).
-__global__ void token_reverse_kernel(TokenLayout tl, const int64_t* __restrict__ qptr, int32_t* __restrict__ kq,
-                                     int32_t* __restrict__ ke) {
+// kv 0's reverse segment with the token (kq and/or ks): thread j < c0 writes the entry of attention row
+// lead + j, first in that row (slot 0).
+__global__ void token_reverse_kernel(TokenLayout tl, int32_t* __restrict__ kq, int32_t* __restrict__ ks) {
   const int64_t j = int64_t(blockIdx.x) * kThreads + threadIdx.x;
   if (j < tl.c0) {
     if (kq) kq[j] = int32_t(tl.lead + j);
-    if (ke) ke[j] = int32_t(qptr[tl.lead + j]);
+    if (ks) ks[j] = 0;
   }
 }
 
@@ -459,11 +460,10 @@ inline TokenLayout token_layout(int global_token, int64_t token_row, int64_t n_q
   return tl;
 }
 
-inline int launch_token_reverse(const TokenLayout& tl, const int64_t* qptr, int32_t* kq, int32_t* ke,
-                                hipStream_t st) {
+inline int launch_token_reverse(const TokenLayout& tl, int32_t* kq, int32_t* ks, hipStream_t st) {
   if (!tl.tok || tl.c0 == 0) return BF_OK;
-  BF_LAUNCH("token_reverse_kernel", token_reverse_kernel, dim3(blocks_for(tl.c0)), dim3(kThreads), 0, st, tl, qptr,
-            kq, ke);
+  BF_LAUNCH("token_reverse_kernel", token_reverse_kernel, dim3(blocks_for(tl.c0)), dim3(kThreads), 0, st, tl, kq,
+            ks);
   BF_CHECK_LAUNCH();
   return BF_OK;
 }
@@ -831,7 +831,7 @@ extern "C" int bf_reverse_index_workspace_size(int64_t nnz, int64_t n_kv, size_t
 }
 
 extern "C" int bf_reverse_index(const int64_t* qptr, const int32_t* kv, int64_t n_q, int64_t n_kv, int64_t nnz,
-                                int64_t* kptr, int32_t* kq, int32_t* ke, void* workspace,
+                                int64_t* kptr, int32_t* kq, int32_t* ks, void* workspace,
                                 size_t workspace_bytes, void* stream) {
   BF_CHECK_ARG(qptr && kptr && n_q >= 0 && n_kv >= 0 && nnz >= 0, "reverse_index: bad arguments");
   BF_CHECK_ARG(nnz < (int64_t(1) << 31) && n_q < (int64_t(1) << 31), "reverse_index: sizes must fit int32");
@@ -843,7 +843,7 @@ extern "C" int bf_reverse_index(const int64_t* qptr, const int32_t* kv, int64_t 
     BF_CHECK_HIP(hipMemsetAsync(kptr, 0, size_t(n_kv + 1) * sizeof(int64_t), st));
     return BF_OK;
   }
-  BF_CHECK_ARG(kv && kq && ke, "reverse_index: null tensor");
+  BF_CHECK_ARG(kv && kq && ks, "reverse_index: null tensor");
   char* p = static_cast<char*>(workspace);
   auto take = [&](size_t b) { char* q = p; p += align_up(b); return q; };
   auto* keys_out = reinterpret_cast<uint32_t*>(take(size_t(nnz) * 4));
@@ -855,8 +855,8 @@ extern "C" int bf_reverse_index(const int64_t* qptr, const int32_t* kv, int64_t 
   const size_t temp_bytes = workspace_bytes - size_t(p - static_cast<char*>(workspace));
   int rc = row_ids(qptr, n_q, nnz, marks, rows, temp, temp_bytes, st);
   if (rc) return rc;
-  BF_LAUNCH("pack_row_entry_kernel", pack_row_entry_kernel, dim3(blocks_for(nnz)), dim3(kThreads), 0, st, rows, nnz,
-            vals_in);
+  BF_LAUNCH("pack_row_entry_kernel", pack_row_entry_kernel, dim3(blocks_for(nnz)), dim3(kThreads), 0, st, rows, qptr,
+            nnz, vals_in);
   BF_CHECK_LAUNCH();
   const int end_bit = bits_for(uint64_t(n_kv > 0 ? n_kv : 1));
   size_t tb = temp_bytes;
@@ -866,7 +866,7 @@ extern "C" int bf_reverse_index(const int64_t* qptr, const int32_t* kv, int64_t 
             nnz, uint64_t(1), n_kv, kptr);
   BF_CHECK_LAUNCH();
   BF_LAUNCH("unpack_row_entry_kernel", unpack_row_entry_kernel, dim3(blocks_for(nnz)), dim3(kThreads), 0, st, vals_out,
-            nnz, kq, ke);
+            nnz, kq, ks);
   BF_CHECK_LAUNCH();
   return BF_OK;
 }
@@ -879,7 +879,7 @@ extern "C" int bf_reverse_index_packed_workspace_size(int64_t nnz, size_t* bytes
 
 extern "C" int bf_reverse_index_packed(const uint64_t* rkey, const int64_t* qptr, int64_t nnz, int64_t n_q,
                                        int64_t n_kv, int32_t q_bits, int32_t slot_bits, int32_t global_token,
-                                       int64_t token_row, uint64_t* sorted, int64_t* kptr, int32_t* kq, int32_t* ke,
+                                       int64_t token_row, uint64_t* sorted, int64_t* kptr, int32_t* kq, int32_t* ks,
                                        void* workspace, size_t workspace_bytes, void* stream) {
   BF_CHECK_ARG(kptr && qptr && n_q >= 0 && n_kv >= 0 && nnz >= 0, "reverse_index_packed: bad arguments");
   BF_CHECK_ARG(nnz < (int64_t(1) << 31), "reverse_index_packed: sizes must fit int32");
@@ -914,7 +914,7 @@ extern "C" int bf_reverse_index_packed(const uint64_t* rkey, const int64_t* qptr
   const int64_t key_blocks = ceil_div(n_keys + 1, int64_t(kThreads) * kUnpackPerThread);
   const int64_t tok_blocks = tl.tok ? ceil_div(tl.c0, int64_t(kThreads)) : 0;
   BF_LAUNCH("unpack_rkey_kernel", unpack_rkey_kernel, dim3(unsigned(key_blocks + tok_blocks)), dim3(kThreads), 0, st,
-            sorted, qptr + n_q, n_token, n_keys, kshift, slot_bits, tl, qptr, n_kv, kptr, kq, ke, key_blocks);
+            sorted, qptr + n_q, n_token, n_keys, kshift, slot_bits, tl, n_kv, kptr, kq, ks, key_blocks);
   BF_CHECK_LAUNCH();
   return BF_OK;
 }
@@ -932,26 +932,26 @@ extern "C" int bf_radix_sort_keys(const uint64_t* in, uint64_t* out, int64_t n, 
   return sort::radix_sort_keys(in, out, n, begin_bit, end_bit, workspace, workspace_bytes, as_stream(stream));
 }
 
-extern "C" int bf_reverse_entries(const uint64_t* sorted, const int64_t* qptr, int64_t nnz, int64_t n_q,
-                                  int32_t q_bits, int32_t slot_bits, int32_t global_token, int64_t token_row,
-                                  int32_t* ke, void* stream) {
-  BF_CHECK_ARG(qptr && nnz >= 0 && nnz < (int64_t(1) << 31) && n_q >= 0, "reverse_entries: bad arguments");
+extern "C" int bf_reverse_slots(const uint64_t* sorted, const int64_t* qptr, int64_t nnz, int64_t n_q,
+                                int32_t q_bits, int32_t slot_bits, int32_t global_token, int64_t token_row, int32_t* ks,
+                                void* stream) {
+  BF_CHECK_ARG(qptr && nnz >= 0 && nnz < (int64_t(1) << 31) && n_q >= 0, "reverse_slots: bad arguments");
   BF_CHECK_ARG(q_bits >= bits_for(uint64_t(n_q)) && slot_bits >= 1 && q_bits + slot_bits <= 33,
-               "reverse_entries: bad key fields (%d + %d bits)", q_bits, slot_bits);
+               "reverse_slots: bad key fields (%d + %d bits)", q_bits, slot_bits);
   const TokenLayout tl = token_layout(global_token != 0, token_row, n_q);
   const int64_t n_token = tl.tok ? tl.c0 + tl.token_len : 0;
   const int64_t n_keys = nnz - n_token;     // a capacity, as in bf_reverse_index_packed
-  BF_CHECK_ARG(n_keys >= 0, "reverse_entries: %lld entries cannot hold the token's %lld", (long long)nnz,
+  BF_CHECK_ARG(n_keys >= 0, "reverse_slots: %lld entries cannot hold the token's %lld", (long long)nnz,
                (long long)(tl.c0 + tl.token_len));
   if (nnz == 0) return BF_OK;
-  BF_CHECK_ARG(ke && (n_keys == 0 || sorted), "reverse_entries: null tensor");
+  BF_CHECK_ARG(ks && (n_keys == 0 || sorted), "reverse_slots: null tensor");
   hipStream_t st = as_stream(stream);
   if (n_keys > 0 || tl.lead) {
-    BF_LAUNCH("reverse_entries_kernel", reverse_entries_kernel, dim3(blocks_for(n_keys + 1)), dim3(kThreads), 0, st,
-              sorted, qptr + n_q, n_token, n_keys, q_bits + slot_bits, slot_bits, tl, qptr, ke);
+    BF_LAUNCH("reverse_slots_kernel", reverse_slots_kernel, dim3(blocks_for(n_keys + 1)), dim3(kThreads), 0, st,
+              sorted, qptr + n_q, n_token, n_keys, q_bits + slot_bits, slot_bits, tl, ks);
     BF_CHECK_LAUNCH();
   }
-  return launch_token_reverse(tl, qptr, nullptr, ke, st);
+  return launch_token_reverse(tl, nullptr, ks, st);
 }
 
 extern "C" int bf_expand_rows(const int64_t* ptr, int64_t n_rows, int64_t nnz, int64_t* rows, void* stream) {

@@ -53,7 +53,7 @@ at::Tensor scratch_bytes(size_t bytes, const at::Device& dev) {
 
 // ---------------------------------------------------------------- attention index
 constexpr const char* kIndexTensors[16] = {"qptr",       "kv",         "kptr",         "kq",
-                                           "ke",         "q_nitems",   "q_item_off",   "q_item_row",
+                                           "ks",         "q_nitems",   "q_item_off",   "q_item_row",
                                            "q_heavy_rows", "k_nitems", "k_item_off",   "k_item_row",
                                            "k_heavy_rows", "k_order",  "k_spans",      "plan_counts"};
 // The 10 integers, in order: n_q, n_kv, nnz, chunk, item, q_items, q_heavy, k_items, k_heavy, token_column.
@@ -80,7 +80,7 @@ bf_attn_index make_index(const c10::List<std::optional<at::Tensor>>& t, at::IntA
   x.kv = static_cast<const int32_t*>(get(1, at::kInt));
   x.kptr = static_cast<const int64_t*>(get(2, at::kLong));
   x.kq = static_cast<const int32_t*>(get(3, at::kInt));
-  x.ke = static_cast<const int32_t*>(get(4, at::kInt));
+  x.ks = static_cast<const int32_t*>(get(4, at::kInt));
   x.q_nitems = static_cast<const int32_t*>(get(5, at::kInt));
   x.q_item_off = static_cast<const int32_t*>(get(6, at::kInt));
   x.q_item_row = static_cast<const int32_t*>(get(7, at::kInt));
@@ -287,8 +287,8 @@ std::tuple<at::Tensor, at::Tensor> table_to_csr(const at::Tensor& table, const a
   return {qptr, kv};
 }
 
-// Key-major view of an attention CSR (bf_reverse_index): (kptr int64 [n_kv + 1], kq int32 [nnz], ke int32 [nnz]),
-// entries of a key in CSR order.
+// Key-major view of an attention CSR (bf_reverse_index): (kptr int64 [n_kv + 1], kq int32 [nnz], ks int32 [nnz]:
+// each entry's query and its slot in the query's row), entries of a key in CSR order.
 std::tuple<at::Tensor, at::Tensor, at::Tensor> transpose_table(const at::Tensor& qptr, const at::Tensor& kv,
                                                                int64_t n_kv) {
   const c10::DeviceGuard guard(qptr.device());
@@ -300,12 +300,12 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> transpose_table(const at::Tensor&
   check_rc(bf_reverse_index_workspace_size(nnz, n_kv, &ws_bytes), "bf::transpose_table");
   at::Tensor ws = scratch_bytes(ws_bytes, dev);
   at::Tensor kptr = at::empty({n_kv + 1}, qptr.options());
-  at::Tensor kq = at::empty({nnz}, kv.options()), ke = at::empty({nnz}, kv.options());
+  at::Tensor kq = at::empty({nnz}, kv.options()), ks = at::empty({nnz}, kv.options());
   check_rc(bf_reverse_index(qptr.data_ptr<int64_t>(), kv.data_ptr<int32_t>(), qptr.numel() - 1, n_kv, nnz,
-                            kptr.data_ptr<int64_t>(), kq.data_ptr<int32_t>(), ke.data_ptr<int32_t>(), ws.data_ptr(),
+                            kptr.data_ptr<int64_t>(), kq.data_ptr<int32_t>(), ks.data_ptr<int32_t>(), ws.data_ptr(),
                             size_t(ws.numel()), stream_of(qptr)),
            "bf::transpose_table");
-  return {kptr, kq, ke};
+  return {kptr, kq, ks};
 }
 
 }  // namespace

@@ -531,7 +531,8 @@ def coo_to_csr(edge_index: torch.Tensor, n_q: int, n_kv: int):
 
 
 def reverse_index(qptr: torch.Tensor, kv: torch.Tensor, n_kv: int):
-    """Key-major view: (kptr [n_kv+1], kq [nnz], ke [nnz]) sorted by (kv, CSR position)."""
+    """Key-major view: (kptr [n_kv+1], kq [nnz], ks [nnz]) sorted by (kv, CSR position): each reverse
+    entry's query and its slot in the query's row."""
     dev = qptr.device
     _require(qptr, "qptr", torch.int64)
     _require(kv, "kv", torch.int32, dev)
@@ -539,16 +540,16 @@ def reverse_index(qptr: torch.Tensor, kv: torch.Tensor, n_kv: int):
     ws = _workspace(_size_query("bf_reverse_index_workspace_size", nnz, n_kv), dev)
     kptr = torch.empty(n_kv + 1, dtype=torch.int64, device=dev)
     kq = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)[:nnz]
-    ke = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)[:nnz]
-    N.call("bf_reverse_index", _p(qptr), _p(kv), qptr.numel() - 1, n_kv, nnz, _p(kptr), _p(kq), _p(ke), _p(ws),
+    ks = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)[:nnz]
+    N.call("bf_reverse_index", _p(qptr), _p(kv), qptr.numel() - 1, n_kv, nnz, _p(kptr), _p(kq), _p(ks), _p(ws),
            ws.numel(), _stream(dev))
-    return kptr, kq, ke
+    return kptr, kq, ks
 
 
 def reverse_index_packed(rk: ReverseKeys, qptr: torch.Tensor, n_kv: int, entries: bool = True):
     """reverse_index from table_to_csr's sort keys (one sort of the id bits, no row recovery):
-    (kptr, kq, ke, sorted). ``entries=False`` skips ke (a gather of qptr that only a bias or factor
-    needs; ``reverse_entries(sorted, qptr)`` gives it later) and returns ke = None."""
+    (kptr, kq, ks, sorted). ``entries=False`` skips ks (the slots, which only a bias, factor or dropout
+    needs; ``reverse_slots(sorted, qptr)`` gives them later) and returns ks = None."""
     dev = qptr.device
     _require(qptr, "qptr", torch.int64)
     _require(rk.keys, "keys", torch.int64, dev)
@@ -559,11 +560,11 @@ def reverse_index_packed(rk: ReverseKeys, qptr: torch.Tensor, n_kv: int, entries
                       rk.global_token, rk.token_row)
     kptr = torch.empty(n_kv + 1, dtype=torch.int64, device=dev)
     kq = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)[:nnz]
-    ke = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)[:nnz] if entries else None
+    ks = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)[:nnz] if entries else None
     N.call("bf_reverse_index_packed", _p(rk.keys), _p(qptr), nnz, qptr.numel() - 1, n_kv, rk.q_bits, rk.slot_bits,
-           int(rk.global_token), int(rk.token_row), _p(srt.keys), _p(kptr), _p(kq), _p(ke) if entries else None,
+           int(rk.global_token), int(rk.token_row), _p(srt.keys), _p(kptr), _p(kq), _p(ks) if entries else None,
            _p(ws), ws.numel(), _stream(dev))
-    return kptr, kq, ke, srt
+    return kptr, kq, ks, srt
 
 
 def _entries_of(rk: ReverseKeys, qptr: torch.Tensor) -> int:
@@ -573,16 +574,16 @@ def _entries_of(rk: ReverseKeys, qptr: torch.Tensor) -> int:
     return rk.keys.numel() + qptr.numel() - 1 - (1 if rk.token_row >= 0 else 0) + max(rk.token_row, 0)
 
 
-def reverse_entries(srt: ReverseKeys, qptr: torch.Tensor) -> torch.Tensor:
-    """ke (CSR position per reverse entry, int32) from reverse_index_packed's sorted keys."""
+def reverse_slots(srt: ReverseKeys, qptr: torch.Tensor) -> torch.Tensor:
+    """ks (each reverse entry's slot in its query's row, int32) from reverse_index_packed's sorted keys."""
     dev = qptr.device
     _require(qptr, "qptr", torch.int64)
     _require(srt.keys, "keys", torch.int64, dev)
     nnz = _entries_of(srt, qptr)
-    ke = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)[:nnz]
-    N.call("bf_reverse_entries", _p(srt.keys), _p(qptr), nnz, qptr.numel() - 1, srt.q_bits, srt.slot_bits,
-           int(srt.global_token), int(srt.token_row), _p(ke), _stream(dev))
-    return ke
+    ks = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)[:nnz]
+    N.call("bf_reverse_slots", _p(srt.keys), _p(qptr), nnz, qptr.numel() - 1, srt.q_bits, srt.slot_bits,
+           int(srt.global_token), int(srt.token_row), _p(ks), _stream(dev))
+    return ks
 
 
 def radix_sort_keys(keys: torch.Tensor, begin_bit: int, end_bit: int) -> torch.Tensor:
@@ -813,13 +814,13 @@ class AttentionIndex:
     """One edge set in the layout the attention kernels walk.
 
     Query-major CSR (qptr, kv) for the forward and the dq pass; the key-major
-    reverse index (kptr, kq, ke) for the dk/dv pass is built on first use and
+    reverse index (kptr, kq, ks) for the dk/dv pass is built on first use and
     then reused by every layer and step that shares the edge set.
 
     The per-entry arrays are held at a capacity (``kv_all``, ``kq_all``,
-    ``ke_all``; ``cap`` >= nnz): a table's index is sized for every row full,
+    ``ks_all``; ``cap`` >= nnz): a table's index is sized for every row full,
     so that building it reads nothing back to the host. The entry count is
-    qptr[n_q]; ``nnz`` and the exact views ``kv``, ``kq``, ``ke`` read it on
+    qptr[n_q]; ``nnz`` and the exact views ``kv``, ``kq``, ``ks`` read it on
     first use.
     """
     n_q: int
@@ -831,7 +832,7 @@ class AttentionIndex:
     qplan: Optional[SplitPlan] = None
     kptr: Optional[torch.Tensor] = None
     kq_all: Optional[torch.Tensor] = None
-    ke_all: Optional[torch.Tensor] = None
+    ks_all: Optional[torch.Tensor] = None    # each reverse entry's slot in its query's row
     kplan: Optional[SplitPlan] = None
     korder: Optional[torch.Tensor] = None
     kspans: Optional[torch.Tensor] = None      # per korder slot: (kptr[row] << 32 | row length)
@@ -841,7 +842,7 @@ class AttentionIndex:
     token_column: int = 0
     _rows: Optional[torch.Tensor] = field(default=None, repr=False)
     _rkeys: Optional[ReverseKeys] = field(default=None, repr=False)   # from_table: sort keys, until used
-    _sorted: Optional[ReverseKeys] = field(default=None, repr=False)  # sorted keys, until ke is needed
+    _sorted: Optional[ReverseKeys] = field(default=None, repr=False)  # sorted keys, until ks is needed
     _counts: Optional[torch.Tensor] = field(default=None, repr=False)  # both plans' device counts
     # True: the plans leave their counts on the device and the attention calls size their grids for the
     # capacities (no host read at all between building the index and using it, e.g. for a caller that
@@ -850,7 +851,7 @@ class AttentionIndex:
     device_counts: bool = False
     # (items, split rows) of the query-side plan when the row lengths fix them (from_table)
     _q_known: Optional[tuple] = field(default=None, repr=False)
-    _structs: dict = field(default_factory=dict, repr=False)          # C view per (backward, with ke)
+    _structs: dict = field(default_factory=dict, repr=False)          # C view per (backward, with ks)
     _nnz: Optional[int] = field(default=None, repr=False)             # qptr[n_q], once read
 
     @property
@@ -878,8 +879,8 @@ class AttentionIndex:
         return None if self.kq_all is None else self.kq_all[:self.nnz]
 
     @property
-    def ke(self) -> Optional[torch.Tensor]:
-        return None if self.ke_all is None else self.ke_all[:self.nnz]
+    def ks(self) -> Optional[torch.Tensor]:
+        return None if self.ks_all is None else self.ks_all[:self.nnz]
 
     @property
     def device(self):
@@ -918,8 +919,8 @@ class AttentionIndex:
                                                                                entries=False)
                 self._rkeys = None
             else:
-                self.kptr, kq, ke = reverse_index(self.qptr, self.kv, self.n_kv)
-                self.kq_all, self.ke_all = _to_cap(kq, self.cap), _to_cap(ke, self.cap)
+                self.kptr, kq, ks = reverse_index(self.qptr, self.kv, self.n_kv)
+                self.kq_all, self.ks_all = _to_cap(kq, self.cap), _to_cap(ks, self.cap)
         if self.kplan is None and self.korder is None and 1 <= self.chunk <= 254:
             # the rows to split are the longest-first order's first slots: one pass writes both
             self.korder, self.kspans, self.kplan = row_order_and_plan(
@@ -933,10 +934,11 @@ class AttentionIndex:
         return self
 
     def ensure_entries(self):
-        """The CSR position of every reverse entry (ke), which the dk/dv pass reads only with a bias or factor."""
+        """Each reverse entry's slot in its query's row (ks), which the dk/dv pass reads only with a bias,
+        factor or dropout (the dropout's entry id is (query, slot); the CSR position is qptr[kq] + ks)."""
         self.ensure_backward()
-        if self.ke_all is None and self.cap:
-            self.ke_all = reverse_entries(self._sorted, self.qptr)
+        if self.ks_all is None and self.cap:
+            self.ks_all = reverse_slots(self._sorted, self.qptr)
             self._sorted = None
         return self
 
@@ -957,7 +959,7 @@ class AttentionIndex:
         if backward and entries:
             self.ensure_entries()
         # the index does not change once built: every layer and step reuses the same struct
-        key = (backward, backward and self.ke_all is not None, self.nnz_known)
+        key = (backward, backward and self.ks_all is not None, self.nnz_known)
         cached = self._structs.get(key)
         if cached is not None:
             return cached
@@ -966,7 +968,7 @@ class AttentionIndex:
         return s
 
     # bf_attn_index's pointer fields, in the order the torch operators take them (csrc/torch_ops.cpp)
-    _TENSOR_FIELDS = ("qptr", "kv", "kptr", "kq", "ke", "q_nitems", "q_item_off", "q_item_row", "q_heavy_rows",
+    _TENSOR_FIELDS = ("qptr", "kv", "kptr", "kq", "ks", "q_nitems", "q_item_off", "q_item_row", "q_heavy_rows",
                       "k_nitems", "k_item_off", "k_item_row", "k_heavy_rows", "k_order", "k_spans", "plan_counts")
     _INT_FIELDS = ("n_q", "n_kv", "nnz", "chunk", "item", "q_items", "q_heavy", "k_items", "k_heavy", "token_column")
 
@@ -993,7 +995,7 @@ class AttentionIndex:
             kp = self.kplan
             t["kptr"] = self.kptr
             t["kq"] = self.kq_all if self.cap else None
-            t["ke"] = self.ke_all if (self.cap and self.ke_all is not None) else None
+            t["ks"] = self.ks_all if (self.cap and self.ks_all is not None) else None
             n["k_items"], n["k_heavy"] = (kp.item_cap, kp.heavy_cap) if kp.pending else (kp.items, kp.heavy)
             t["k_nitems"], t["k_item_off"], t["k_item_row"], t["k_heavy_rows"] = (
                 kp.nitems, kp.item_off, kp.item_row, kp.heavy_rows)
@@ -1017,7 +1019,7 @@ class AttentionIndex:
         self.ensure_backward() if backward else self.ensure_forward()
         if backward and entries:
             self.ensure_entries()
-        key = ("op", backward, backward and self.ke_all is not None, self.nnz_known)
+        key = ("op", backward, backward and self.ks_all is not None, self.nnz_known)
         cached = self._structs.get(key)
         if cached is None:
             t, n = self._fields(backward)

@@ -338,13 +338,14 @@ int bf_coalesce(const int64_t* src, const int64_t* dst, int64_t nnz, int64_t num
                 void* workspace, size_t workspace_bytes, void* stream);
 
 /* Reverse (key-major) index of an attention CSR: kptr int64 [n_kv+1], and for
- * each reverse entry its query kq int32 [nnz] and its CSR position ke int32
- * [nnz], sorted by (kv, position) — i.e. by (src, dst), the order PyG's
- * coalesce gives (gt_sp/utils.py:887). Drives the deterministic dK/dV pass and
- * the COO adaptor. Workspace: bf_reverse_index_workspace_size.              */
+ * each reverse entry its query kq int32 [nnz] and its slot ks int32 [nnz] (its
+ * position in the query's row: CSR position = qptr[kq] + ks), sorted by (kv,
+ * position) — i.e. by (src, dst), the order PyG's coalesce gives
+ * (gt_sp/utils.py:887). Drives the deterministic dK/dV pass and the COO
+ * adaptor. Workspace: bf_reverse_index_workspace_size.                      */
 int bf_reverse_index_workspace_size(int64_t nnz, int64_t n_kv, size_t* bytes);
 int bf_reverse_index(const int64_t* qptr, const int32_t* kv, int64_t n_q, int64_t n_kv, int64_t nnz,
-                     int64_t* kptr, int32_t* kq, int32_t* ke,
+                     int64_t* kptr, int32_t* kq, int32_t* ks,
                      void* workspace, size_t workspace_bytes, void* stream);
 
 /* bf_reverse_index from bf_table_to_csr's sort keys: one radix sort of the
@@ -354,16 +355,16 @@ int bf_reverse_index(const int64_t* qptr, const int32_t* kv, int64_t n_q, int64_
  * token's entries, which have no key, take their fixed places (kv 0's segment
  * first, row by row; each token-row entry first in its kv's segment), the
  * sorted keys the rest. nnz counts every entry, or is any capacity above that
- * count (the keys, sorted, kq and ke then sized for it): the kernels take the
- * count itself from qptr[n_q] on the device. ke (may be NULL) is decoded in
- * the same pass: qptr[query] + slot; it is a random gather of qptr, which the
- * dk/dv pass needs only with a bias, factor or dropout, so a caller may keep
- * `sorted` and call bf_reverse_entries later instead. Same kptr / kq / ke as bf_reverse_index.
+ * count (the keys, sorted, kq and ks then sized for it): the kernels take the
+ * count itself from qptr[n_q] on the device. ks (may be NULL) is decoded in
+ * the same pass, from the key's slot field; the dk/dv pass needs it only with
+ * a bias, factor or dropout, so a caller may also keep `sorted` and call
+ * bf_reverse_slots later. Same kptr / kq / ks as bf_reverse_index.
  * Workspace: bf_reverse_index_packed_workspace_size(nnz).                   */
 int bf_reverse_index_packed_workspace_size(int64_t nnz, size_t* bytes);
 int bf_reverse_index_packed(const uint64_t* rkey, const int64_t* qptr, int64_t nnz, int64_t n_q, int64_t n_kv,
                             int32_t q_bits, int32_t slot_bits, int32_t global_token, int64_t token_row,
-                            uint64_t* sorted, int64_t* kptr, int32_t* kq, int32_t* ke, void* workspace,
+                            uint64_t* sorted, int64_t* kptr, int32_t* kq, int32_t* ks, void* workspace,
                             size_t workspace_bytes, void* stream);
 /* The stable radix sort bf_reverse_index_packed uses, on its own: in[0, n)
  * uint64 sorted by bits [begin_bit, end_bit) into out (n < 2^31; in and out
@@ -375,10 +376,10 @@ int bf_radix_sort_workspace_size(int64_t n, int32_t begin_bit, int32_t end_bit, 
 int bf_radix_sort_keys(const uint64_t* in, uint64_t* out, int64_t n, int32_t begin_bit, int32_t end_bit,
                        void* workspace, size_t workspace_bytes, void* stream);
 
-/* ke [nnz] from bf_reverse_index_packed's sorted keys (the same nnz, n_q,
- * key fields and token arguments).                                         */
-int bf_reverse_entries(const uint64_t* sorted, const int64_t* qptr, int64_t nnz, int64_t n_q, int32_t q_bits,
-                       int32_t slot_bits, int32_t global_token, int64_t token_row, int32_t* ke, void* stream);
+/* ks [nnz] from bf_reverse_index_packed's sorted keys (the same nnz, n_q,
+ * key fields and token arguments): no counterpart in the reference.        */
+int bf_reverse_slots(const uint64_t* sorted, const int64_t* qptr, int64_t nnz, int64_t n_q, int32_t q_bits,
+                     int32_t slot_bits, int32_t global_token, int64_t token_row, int32_t* ks, void* stream);
 
 /* Row id of every entry of a CSR (rows[i] = r for ptr[r] <= i < ptr[r+1]). */
 int bf_expand_rows(const int64_t* ptr, int64_t n_rows, int64_t nnz, int64_t* rows, void* stream);
@@ -458,8 +459,9 @@ typedef struct bf_attn_index {
   const int32_t* kv;            /* [nnz]   kv id per edge, query-major              */
   const int64_t* kptr;          /* [n_kv+1] reverse offsets (backward only)         */
   const int32_t* kq;            /* [nnz]   query per reverse entry (backward only)  */
-  const int32_t* ke;            /* [nnz]   CSR position per reverse entry (backward
-                                   with a bias or factor only; else may be NULL)   */
+  const int32_t* ks;            /* [nnz]   slot of each reverse entry in its query's
+                                   row (backward with a bias, factor, dropout or
+                                   dbias only; else may be NULL)                   */
   int32_t chunk;                /* rows longer than this use the split plan         */
   int32_t item;                 /* entries per split item                           */
   int32_t q_items, q_heavy;     /* query-side plan (bf_split_plan on qptr): counts  */
@@ -539,9 +541,9 @@ int bf_attn_fwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int3
  * (sum_e p f (dO . v_s) / D', D' = Z + 1e-6) in float32, so the forward's
  * output tensor is not read: a bfloat16 out would carry its rounding into the
  * gradients (the reference, under autocast, keeps out in float32).
- *   dbias: NULL or float32 [nnz, H] (per CSR position; needs idx->ke, as do
- *   a bias, a factor and a dropout: the key-major pass finds each entry's CSR
- *   position through it);
+ *   dbias: NULL or float32 [nnz, H] (per CSR position; needs idx->ks, as do
+ *   a bias, a factor and a dropout: the key-major pass knows each entry by its
+ *   query and slot, and finds its CSR position as qptr[kq] + ks);
  *   rowstat: float32 [n_q, H, 2] scratch (per query and head
  *   {1/D', Delta/D'}, written by the query-major pass and read by the
  *   key-major pass).                                                         */

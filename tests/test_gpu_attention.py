@@ -145,7 +145,7 @@ def test_table_index_plain_then_bias_backward(hip_device, token):
     q, k, v, _, dout = _inputs(S, H, hn, 1, seed=31, mult=1.4)
     ei_o = _coo_order(idx)
     out, dq, dk, dv, _ = _run(hip_device, q, k, v, idx, dout)
-    assert idx.ke is None                       # not derived for a plain backward
+    assert idx.ks is None                       # not derived for a plain backward
     ro, rZ, rdq, rdk, rdv, _ = _oracle(q, k, v, ei_o, dout)
     for got, ref in ((out, ro), (dq, rdq), (dk, rdk), (dv, rdv)):
         assert _rel_err(got, ref) < 1e-5
@@ -153,7 +153,7 @@ def test_table_index_plain_then_bias_backward(hip_device, token):
     bias_e = torch.randn(idx.nnz, H, generator=g)
     factor = (torch.rand(idx.nnz, H, generator=g) >= 0.3).float() / 0.7
     out, dq, dk, dv, db = _run(hip_device, q, k, v, idx, dout, bias_e=bias_e, factor_e=factor)
-    assert idx.ke is not None
+    assert idx.ks is not None
     ro, rZ, rdq, rdk, rdv, rdb = _oracle(q, k, v, ei_o, dout, bias_e=bias_e, factor_e=factor)
     for got, ref in ((out, ro), (dq, rdq), (dk, rdk), (dv, rdv), (db, rdb)):
         assert _rel_err(got, ref) < 1e-5

@@ -396,7 +396,7 @@ def test_index_formats_against_numpy(hip_device, token, token_row):
         assert torch.equal(x, y)
     lazy = hip_ops.reverse_index_packed(rk, qptr, n_kv, entries=False)
     assert lazy[2] is None and torch.equal(lazy[0], a[0]) and torch.equal(lazy[1], a[1])
-    assert torch.equal(hip_ops.reverse_entries(lazy[3], qptr), a[2])
+    assert torch.equal(hip_ops.reverse_slots(lazy[3], qptr), a[2])
     # the same route with nothing read back: buffers sized for every row full, the kernels taking the
     # entry count from qptr[n_q]; the first nnz entries equal the exact route's
     nnz = kv.numel()
@@ -407,9 +407,10 @@ def test_index_formats_against_numpy(hip_device, token, token_row):
     cap = hip_ops.reverse_index_packed(rkc, qc, n_kv)
     assert torch.equal(cap[0], a[0]) and torch.equal(cap[1][:nnz], a[1]) and torch.equal(cap[2][:nnz], a[2])
     lazy_c = hip_ops.reverse_index_packed(rkc, qc, n_kv, entries=False)
-    assert torch.equal(hip_ops.reverse_entries(lazy_c[3], qc)[:nnz], a[2])
+    assert torch.equal(hip_ops.reverse_slots(lazy_c[3], qc)[:nnz], a[2])
     order = np.lexsort((pos, np.array(vals)))                    # (kv, position) order
-    assert np.array_equal(b[1].cpu().numpy(), np.array(rows)[order]) and np.array_equal(b[2].cpu().numpy(), order)
+    assert np.array_equal(b[1].cpu().numpy(), np.array(rows)[order])
+    assert np.array_equal(b[2].cpu().numpy(), slot[order])       # each entry's slot in its query's row
     # row order: a permutation, capped lengths non-increasing
     ro, sp = hip_ops.row_order(b[0], spans=True)
     ro, sp = ro.cpu().numpy(), sp.cpu().numpy().astype(np.uint64)
@@ -493,7 +494,7 @@ def test_plan_from_the_row_order_equals_the_generic_plan(hip_device, chunk, item
 def test_token_index_of_tables_without_own_entries(hip_device, n, token_row):
     """Tables whose rows are all empty (every key of the reverse-index sort is gone: only the token's
     entries remain, placed without a sort) and tables with no rows at all: both reverse-index routes,
-    ke, and an attention layer over the index against the oracle."""
+    the slots, and an attention layer over the index against the oracle."""
     from budgetformer_amd import hip_ops
     from budgetformer_amd.attention import sparse_edge_attention
     from budgetformer_amd.hip_ops import AttentionIndex
@@ -510,7 +511,7 @@ def test_token_index_of_tables_without_own_entries(hip_device, n, token_row):
     for x, y in zip(a, b[:3]):
         assert torch.equal(x, y)
     lazy = hip_ops.reverse_index_packed(rk, qptr, n_kv, entries=False)
-    assert torch.equal(hip_ops.reverse_entries(lazy[3], qptr), a[2])
+    assert torch.equal(hip_ops.reverse_slots(lazy[3], qptr), a[2])
     if n_q == 0 or kv.numel() == 0:
         return
     idx = AttentionIndex.from_table(table, row_len, True, n_kv=n_kv, token_row=tr)
@@ -556,7 +557,7 @@ def test_row_pointers_across_long_runs_of_empty_rows(hip_device):
     qptr, kv = hip_ops.coo_to_csr(ei, n + 5, n + 7)            # 5 and 7 empty rows past the last id
     want_q = np.concatenate([[0], np.cumsum(np.bincount(dst, minlength=n + 5))])
     assert np.array_equal(qptr.cpu().numpy(), want_q)
-    kptr, kq, ke = hip_ops.reverse_index(qptr, kv, n + 7)
+    kptr, kq, ks = hip_ops.reverse_index(qptr, kv, n + 7)
     want_k = np.concatenate([[0], np.cumsum(np.bincount(src, minlength=n + 7))])
     assert np.array_equal(kptr.cpu().numpy(), want_k)
     # a table of 3000 rows with ids below 3000 and a token row of 2M entries
@@ -570,7 +571,7 @@ def test_row_pointers_across_long_runs_of_empty_rows(hip_device):
     for x, y in zip(a, b[:3]):
         assert torch.equal(x, y)
     lazy = hip_ops.reverse_index_packed(rk, qptr, tr + 1, entries=False)
-    assert torch.equal(hip_ops.reverse_entries(lazy[3], qptr), a[2])
+    assert torch.equal(hip_ops.reverse_slots(lazy[3], qptr), a[2])
     kvn = kv.cpu().numpy()
     assert np.array_equal(a[0].cpu().numpy(), np.concatenate([[0], np.cumsum(np.bincount(kvn, minlength=tr + 1))]))
 
@@ -609,5 +610,8 @@ def test_packed_reverse_index_onesweep_sizes(hip_device, n, width, lo):
         assert torch.equal(x, y)
     vals = kv.cpu().numpy()
     order = np.argsort(vals, kind="stable")
-    assert np.array_equal(b[2].cpu().numpy(), order)
+    qp = qptr.cpu().numpy()
+    rows = np.repeat(np.arange(n), np.diff(qp))
+    assert np.array_equal(b[1].cpu().numpy(), rows[order])
+    assert np.array_equal(b[2].cpu().numpy(), (np.arange(vals.size) - qp[rows])[order])   # slots
     assert np.array_equal(np.diff(b[0].cpu().numpy()), np.bincount(vals, minlength=n))

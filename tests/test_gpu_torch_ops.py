@@ -150,9 +150,10 @@ def test_edge_ops_against_the_oracle(hip_device, records):
     assert np.array_equal(qptr.cpu().numpy(), np.concatenate([[0], np.cumsum(lens)]))
     flat = np.concatenate([ref_t[i, :lens[i]] for i in range(n)])
     assert np.array_equal(kv.cpu().numpy(), flat)
-    kptr, kq, ke = ops.transpose_table(qptr, kv, n)
+    kptr, kq, ks = ops.transpose_table(qptr, kv, n)
     order = np.argsort(flat, kind="stable")
     rows = np.repeat(np.arange(n), lens)
-    assert np.array_equal(ke.cpu().numpy(), order)
+    slots = np.arange(flat.size) - np.concatenate([[0], np.cumsum(lens)])[rows]
+    assert np.array_equal(ks.cpu().numpy(), slots[order])
     assert np.array_equal(kq.cpu().numpy(), rows[order])
     assert np.array_equal(kptr.cpu().numpy(), np.concatenate([[0], np.cumsum(np.bincount(flat, minlength=n))]))
