@@ -369,9 +369,8 @@ def run(config, steps, warmup, chunk=None, item=None, with_cpu=True):
                                     walk_length=cfg["L"], walks_per_node=cfg["P"], edge_seed=42, n_q=n_rows,
                                     global_token=cfg["token"])
         idx = tab.attention_index(chunk=chunk, item=item)
-        idx.ensure_backward()
-        if rate:
-            idx.ensure_entries()    # the dropout's keep bits are keyed by CSR position
+        # the dropout's keep bits are keyed by CSR position: the reverse index then carries each entry's slot
+        idx.ensure_backward(entries=bool(rate))
         return tab, idx
 
     def layer(idx):

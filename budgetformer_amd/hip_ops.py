@@ -908,15 +908,22 @@ class AttentionIndex:
             self._counts = torch.empty(4, dtype=torch.int32, device=self.device)
         return self._counts[2 * side:2 * side + 2]
 
-    def ensure_backward(self):
+    def ensure_backward(self, entries: bool = False):
+        """The backward's parts of the index: the query-side plan, the reverse index and the key-side
+        order and plan. ``entries``: also each reverse entry's slot (ks), decoded by the reverse index's
+        own unpack pass rather than by a later one (``ensure_entries``)."""
         if self.qplan is None:
             self.qplan = split_plan(self.qptr, self.cap, self.chunk, self.item, resolve=False,
                                     counts=self._plan_counts(0), known=self._q_known,
                                     host_copy=self._host_copy())
         if self.kptr is None:
             if self._rkeys is not None and self._rkeys.q_bits + self._rkeys.slot_bits + _bits_for(self.n_kv) <= 64:
-                self.kptr, self.kq_all, _, self._sorted = reverse_index_packed(self._rkeys, self.qptr, self.n_kv,
-                                                                               entries=False)
+                self.kptr, self.kq_all, ks, srt = reverse_index_packed(self._rkeys, self.qptr, self.n_kv,
+                                                                       entries=entries)
+                if entries:
+                    self.ks_all = ks
+                else:
+                    self._sorted = srt
                 self._rkeys = None
             else:
                 self.kptr, kq, ks = reverse_index(self.qptr, self.kv, self.n_kv)
@@ -935,7 +942,7 @@ class AttentionIndex:
 
     def ensure_entries(self):
         """Each reverse entry's slot in its query's row (ks), which the dk/dv pass reads only with a bias,
-        factor or dropout (the dropout's entry id is (query, slot); the CSR position is qptr[kq] + ks)."""
+        factor or dropout: the entry's CSR position is qptr[kq] + ks."""
         self.ensure_backward()
         if self.ks_all is None and self.cap:
             self.ks_all = reverse_slots(self._sorted, self.qptr)
@@ -955,7 +962,7 @@ class AttentionIndex:
         return torch.stack([src, self.kq.to(torch.int64)])
 
     def struct(self, backward: bool, entries: bool = False) -> N.AttnIndex:
-        self.ensure_backward() if backward else self.ensure_forward()
+        self.ensure_backward(entries) if backward else self.ensure_forward()
         if backward and entries:
             self.ensure_entries()
         # the index does not change once built: every layer and step reuses the same struct
@@ -1016,7 +1023,7 @@ class AttentionIndex:
     def op_args(self, backward: bool, entries: bool = False):
         """The index as the torch operators take it: ([16 tensors or None], [10 ints]), in the order of
         bf_attn_index's fields (``_TENSOR_FIELDS``, ``_INT_FIELDS``); cached like ``struct``."""
-        self.ensure_backward() if backward else self.ensure_forward()
+        self.ensure_backward(entries) if backward else self.ensure_forward()
         if backward and entries:
             self.ensure_entries()
         key = ("op", backward, backward and self.ks_all is not None, self.nnz_known)
