@@ -411,6 +411,14 @@ def test_index_formats_against_numpy(hip_device, token, token_row):
     order = np.lexsort((pos, np.array(vals)))                    # (kv, position) order
     assert np.array_equal(b[1].cpu().numpy(), np.array(rows)[order])
     assert np.array_equal(b[2].cpu().numpy(), slot[order])       # each entry's slot in its query's row
+    # the attention index's two routes to ks: the unpack pass, or later from the sorted keys it keeps
+    ia = hip_ops.AttentionIndex.from_table(t, rl, global_token=token, n_kv=n_kv, token_row=token_row, check=False)
+    ib = hip_ops.AttentionIndex.from_table(t, rl, global_token=token, n_kv=n_kv, token_row=token_row, check=False)
+    ia.ensure_backward(entries=True)
+    ib.ensure_backward()
+    assert ib.ks_all is None
+    ib.ensure_entries()
+    assert torch.equal(ia.ks, a[2]) and torch.equal(ib.ks, a[2]) and torch.equal(ia.kq, a[1])
     # row order: a permutation, capped lengths non-increasing
     ro, sp = hip_ops.row_order(b[0], spans=True)
     ro, sp = ro.cpu().numpy(), sp.cpu().numpy().astype(np.uint64)
