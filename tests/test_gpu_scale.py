@@ -69,6 +69,63 @@ def test_bf16_kv_pass_streaming_four_rows_prefetched_slots(hip_device):
                    {"rows_per_group": 4, "stream_rows": True, "prefetch_slots": True}, 2e-2)
 
 
+def _csr_edges_compacted(idx, qa, kt):
+    """The index's entries in CSR order as an oracle edge list [2, nnz] over the compacted rows (kv rows as
+    positions in kt, queries as positions in qa): entry e of the index is column e."""
+    kv = idx.kv.long()
+    rows = idx.entry_rows()
+    kv_c = torch.searchsorted(kt, kv)
+    q_c = torch.searchsorted(qa, rows)
+    assert torch.equal(kt[kv_c], kv) and torch.equal(qa[q_c], rows)
+    return torch.stack([kv_c, q_c]).cpu()
+
+
+@pytest.mark.parametrize("extras", ["dropout", "bias_dbias_dropout"])
+def test_bf16_kv_pass_c4_instance_with_dropout(hip_device, extras):
+    """The dk/dv instance c4 times: attn_bwd_kv_kernel<bf16, NT, PRE, EX=1> (dropout 0.5 drawn in the
+    kernels; q + dO above 256 MB, more than 1M kv rows: non-temporal gathers, four rows per lane group,
+    prefetched slots), and its general twin EX=2 (additive bias, dbias and dropout). Each entry's keep bits
+    come from its CSR position (qptr[kq] + ks in the key-major pass), so the float64 oracle takes the index's
+    own CSR order, remapped to the compacted rows, with the mask oracle.philox.dropout_keep draws."""
+    from budgetformer_amd import hip_ops
+    from budgetformer_amd.hip_ops import AttentionIndex, Dropout
+    H, hn, rate = 8, 16, 0.5
+    n_q, n_kv = 600_000, 2_000_000
+    variant = hip_ops.kv_pass_variant(n_q, n_kv, torch.bfloat16, H, hn)
+    assert variant == {"rows_per_group": 4, "stream_rows": True, "prefetch_slots": True}, variant
+    qa, kt, src_c, dst_c, q, dout, k, v = _compact_problem(hip_device, n_q, n_kv, 20_000, 6_000, 200_000, 3_000,
+                                                           torch.bfloat16, seed=404)
+    idx = AttentionIndex.from_coo(torch.stack([kt[src_c], qa[dst_c]]), n_q, n_kv)
+    nnz = idx.nnz
+    seed, offset = (3 << 33) | 77, 9
+    drop = Dropout(rate, seed, offset)
+    bias = None
+    if extras != "dropout":
+        bias = (torch.randn(nnz, H, generator=torch.Generator().manual_seed(8)) * 0.7).to(hip_device)
+    out, Z = hip_ops.attn_forward(idx, q, k, v, bias=bias, dropout=drop)
+    dq, dk, dv, dbias = hip_ops.attn_backward(idx, q, k, v, out, Z, dout, bias=bias, need_dbias=bias is not None,
+                                              dropout=drop)
+    torch.cuda.synchronize()
+    idx.resolve()
+    assert idx.kplan.items > 0          # the hub key row ran as split items
+    ei = _csr_edges_compacted(idx, qa, kt)
+    keep = torch.from_numpy(philox.dropout_keep(nnz, H, rate, seed, offset))
+    factor = keep.double() / (1.0 - rate)
+    qc, doc = q[qa].double().cpu(), dout[qa].double().cpu()
+    kc, vc = k[kt].double().cpu(), v[kt].double().cpu()
+    b64 = None if bias is None else bias.double().cpu()
+    ro, rZ = sa.attention_forward_stats(kc, qc, vc, ei, b64, factor)
+    rdq, rdk, rdv, rdb = sa.attention_backward_closed_form(kc, qc, vc, ei, ro, rZ, doc, b64, factor)
+    for name, got, ref in (("out", out[qa], ro), ("dq", dq[qa], rdq), ("dk", dk[kt], rdk), ("dv", dv[kt], rdv)):
+        assert_close(name, got, ref, 2e-2)
+    if bias is not None:
+        assert_close("dbias", dbias, rdb, 2e-2)
+    for t, rows in ((out, qa), (dq, qa), (dk, kt), (dv, kt)):
+        t[rows] = 0
+        assert not t.any()
+    assert abs(keep.float().mean().item() - (1 - rate)) < 0.01
+
+
 def test_fp32_kv_pass_past_16m_rows_streaming(hip_device):
     """fp32 with four kv rows per group (17M kv rows) and non-temporal gathers (300K queries)."""
     _check_compact(hip_device, 300_000, 17_000_000, torch.float32,
