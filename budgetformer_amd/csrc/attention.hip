@@ -215,23 +215,37 @@ struct ChunkIds {
       : lpr(1 << sh.lpr_log2),
         len((1 << sh.lpr_log2) >= kUnroll ? ((1 << sh.lpr_log2) / kUnroll) * kUnroll : 0),
         c0(beg - len) {}
-  // at the start of each chunk (uniform over the group): load its ids
-  __device__ __forceinline__ void next(const int32_t* __restrict__ idx, int64_t e0, int64_t end, const GroupPos& g) {
+  // The ids of entries e0 .. e0 + kUnroll - 1 (0 for those at or past `end`, with ok false), every
+  // lane of the group calling it with the same e0. All of an iteration's ids are in registers before
+  // any of its row gathers is issued, and the gathers are issued unconditionally (rows past the end
+  // read row 0): a gather issued under a branch, or an id load between two gathers, makes the compiler
+  // wait for the earlier gathers before the next one is issued, which leaves one row in flight.
+  __device__ __forceinline__ void fetch(const int32_t* __restrict__ idx, int64_t e0, int64_t end,
+                                        const GroupPos& g, int (&s)[kUnroll], bool (&ok)[kUnroll]) {
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) ok[u] = e0 + u < end;
     if constexpr (kChunk) {
-      if (len > 0 && e0 - c0 == len) {
-        c0 = e0;
-        ids = (g.g_lane < len && c0 + g.g_lane < end) ? idx[c0 + g.g_lane] : 0;
+      if (len > 0) {
+        if (e0 - c0 == len) {   // the start of a chunk (uniform over the group): load its ids
+          c0 = e0;
+          ids = (g.g_lane < len && c0 + g.g_lane < end) ? idx[c0 + g.g_lane] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) s[u] = __shfl(ids, int(e0 - c0) + u, lpr);
+        return;
       }
     }
-  }
-  // id of entry e0 + u (every lane of the group calls it)
-  __device__ __forceinline__ int get(const int32_t* __restrict__ idx, int64_t e0, int u, bool ok) const {
-    if constexpr (kChunk) {
-      if (len > 0) return __shfl(ids, int(e0 - c0) + u, lpr);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int id = idx[ok[u] ? e0 + u : end - 1];
+      s[u] = ok[u] ? id : 0;
     }
-    return ok ? idx[e0 + u] : 0;
   }
 };
+
+// Column of this lane's 16 bytes in a gathered row: idle lanes (past D) read the first 16 bytes, so
+// that every lane issues the same loads and none reads past the row; their values are never used.
+__device__ __forceinline__ int gather_col(const GroupPos& g) { return g.act ? g.col0 : 0; }
 // Accumulates sum_e p*f*v (acc) and sum_e p (z) over entries [beg, end) of one row.
 // EX: the per-entry inputs compiled in (0 none, 1 dropout only, 2 bias, factor and dropout): each
 // instance carries only the code, and the registers, of what it uses.
@@ -245,25 +259,16 @@ __device__ __forceinline__ void fwd_segment(const T* __restrict__ k, const T* __
   constexpr int kUnroll = Unroll<T>::fwd;
   const int lph = 1 << sh.lph_log2;
   ChunkIds<T, kUnroll> ids(sh, beg);
+  const int col = gather_col(g);
   for (int64_t e0 = beg; e0 < end; e0 += kUnroll) {
     int s[kUnroll];
     bool ok[kUnroll];
-    ids.next(kv, e0, end, g);
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      ok[u] = e0 + u < end;
-      const int id = ids.get(kv, e0, u, ok[u]);
-      s[u] = ok[u] ? id : 0;
-    }
+    ids.fetch(kv, e0, end, g, s, ok);
     typename Elem<T>::Raw kr[kUnroll], vr[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      if (ok[u] && g.act) {
-        kr[u] = Elem<T>::load_raw(k + int64_t(s[u]) * sh.D + g.col0);
-        vr[u] = Elem<T>::load_raw(v + int64_t(s[u]) * sh.D + g.col0);
-      } else {
-        kr[u] = vr[u] = Elem<T>::zero_raw();
-      }
+      kr[u] = Elem<T>::load_raw(k + int64_t(s[u]) * sh.D + col);
+      vr[u] = Elem<T>::load_raw(v + int64_t(s[u]) * sh.D + col);
     }
     float d[kUnroll];
 #pragma unroll
@@ -584,25 +589,16 @@ __device__ __forceinline__ void dq_segment(const T* __restrict__ k, const T* __r
   constexpr int kUnroll = Unroll<T>::q;
   const int lph = 1 << sh.lph_log2;
   ChunkIds<T, kUnroll> ids(sh, beg);
+  const int col = gather_col(g);
   for (int64_t e0 = beg; e0 < end; e0 += kUnroll) {
     int s[kUnroll];
     bool ok[kUnroll];
-    ids.next(kv, e0, end, g);
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      ok[u] = e0 + u < end;
-      const int id = ids.get(kv, e0, u, ok[u]);
-      s[u] = ok[u] ? id : 0;
-    }
+    ids.fetch(kv, e0, end, g, s, ok);
     typename Elem<T>::Raw kr[kUnroll], vr[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      if (ok[u] && g.act) {
-        kr[u] = Elem<T>::load_raw(k + int64_t(s[u]) * sh.D + g.col0);
-        vr[u] = Elem<T>::load_raw(v + int64_t(s[u]) * sh.D + g.col0);
-      } else {
-        kr[u] = vr[u] = Elem<T>::zero_raw();
-      }
+      kr[u] = Elem<T>::load_raw(k + int64_t(s[u]) * sh.D + col);
+      vr[u] = Elem<T>::load_raw(v + int64_t(s[u]) * sh.D + col);
     }
     float d[kUnroll], w[kUnroll];
 #pragma unroll
@@ -926,35 +922,25 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
   constexpr int kUnroll = Unroll<T>::kv;
   const int lph = 1 << sh.lph_log2;
   ChunkIds<T, kUnroll> ids(sh, beg);
+  const int col = gather_col(g);
   for (int64_t i0 = beg; i0 < end; i0 += kUnroll) {
     int t[kUnroll];
     bool ok[kUnroll];
-    ids.next(kq, i0, end, g);
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      ok[u] = i0 + u < end;
-      const int id = ids.get(kq, i0, u, ok[u]);
-      t[u] = ok[u] ? id : 0;
-    }
+    ids.fetch(kq, i0, end, g, t, ok);
     // each entry's CSR position: its query row's start plus its slot in that row; the row starts are
     // gathered before the rows, so the keep bits below wait for them alone and overlap the row gathers
     int32_t epos[kUnroll];   // nnz < 2^31
     if (EX) {
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) epos[u] = ok[u] ? ks[i0 + u] + int32_t(qptr[t[u]]) : 0;
+      for (int u = 0; u < kUnroll; ++u) epos[u] = ks[ok[u] ? i0 + u : end - 1] + int32_t(qptr[t[u]]);
     }
     typename Elem<T>::Raw qr[kUnroll], gr[kUnroll];
     float2 rs[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      if (ok[u] && g.act) {
-        qr[u] = gather_row<T, NT>(q, t[u], sh.D, g.col0);
-        gr[u] = gather_row<T, NT>(dout, t[u], sh.D, g.col0);
-        rs[u] = rstat[int64_t(t[u]) * sh.H + g.head];
-      } else {
-        qr[u] = gr[u] = Elem<T>::zero_raw();
-        rs[u] = make_float2(0.f, 0.f);
-      }
+      qr[u] = gather_row<T, NT>(q, t[u], sh.D, col);
+      gr[u] = gather_row<T, NT>(dout, t[u], sh.D, col);
+      rs[u] = rstat[int64_t(t[u]) * sh.H + g.head];
     }
     IterDrop<kUnroll> drop{false, 0u};
     if (EX) drop = iter_drop<kUnroll>(ex, epos, ok, sh, g);
