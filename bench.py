@@ -90,13 +90,14 @@ def token_records(s, D, n_q, q_items):
     return q_items + -(-n_q // (256 // lpr))
 
 
-def kernel_bytes(s, D, H, lens_q, lens_k, n_token_rec=0, entry_ids=False):
+def kernel_bytes(s, D, H, lens_q, lens_k, n_token_rec=0, entry_bytes=0):
     """Algorithmic bytes of the three pass kernels (each covers every entry: short rows and split items).
 
     With a token column (n_token_rec records) the dq pass also writes key 0's dK/dV terms, 2*D floats per
     record, and the dk/dv pass reads those records instead of gathering key 0's entries and its K, V rows.
-    entry_ids: the dk/dv pass also reads each gathered entry's slot and its query's row start (qptr), which
-    give its CSR position (a dropout, bias or factor)."""
+    entry_bytes: what the dk/dv pass reads per gathered entry beyond its query id: 4 for the entry's slot in
+    its query's row (with the query, the dropout's key), 12 with a bias or factor (the slot and the query's
+    row start, which give the CSR position they are indexed by)."""
     n_q, nnz = lens_q.size, int(lens_q.sum())
     n_kv = lens_k.size
     nk_touched = int((lens_k > 0).sum())
@@ -114,7 +115,7 @@ def kernel_bytes(s, D, H, lens_q, lens_k, n_token_rec=0, entry_ids=False):
         # dK, dV written for every row; K, V read for rows with entries; Q and dO per gathered entry,
         # the {1/D', Delta/D'} row stats per gathered entry, kq ids, kptr, row order (+ token records)
         "attn_bwd_kv_kernel": row * (2 * n_kv + 2 * nk_touched + 2 * gathered) + 8 * H * gathered
-        + 4 * gathered + 12 * n_kv + rec_bytes + (12 * gathered if entry_ids else 0),
+        + 4 * gathered + 12 * n_kv + rec_bytes + entry_bytes * gathered,
     }
 
 
@@ -369,7 +370,7 @@ def run(config, steps, warmup, chunk=None, item=None, with_cpu=True):
                                     walk_length=cfg["L"], walks_per_node=cfg["P"], edge_seed=42, n_q=n_rows,
                                     global_token=cfg["token"])
         idx = tab.attention_index(chunk=chunk, item=item)
-        # the dropout's keep bits are keyed by CSR position: the reverse index then carries each entry's slot
+        # the dropout's keep bits are keyed by (query, slot): the reverse index then carries each entry's slot
         idx.ensure_backward(entries=bool(rate))
         return tab, idx
 
@@ -423,7 +424,7 @@ def run(config, steps, warmup, chunk=None, item=None, with_cpu=True):
 
     # per-kernel roofline of the three pass kernels
     n_rec = token_records(s_bytes, D, idx.n_q, idx.qplan.items) if idx.token_column else 0
-    kb = kernel_bytes(s_bytes, D, H, lens_q, lens_k, n_rec, entry_ids=bool(rate))
+    kb = kernel_bytes(s_bytes, D, H, lens_q, lens_k, n_rec, entry_bytes=4 if rate else 0)
     kernels = {}
     for name, (ms, launches) in sorted(kstats.items(), key=lambda x: -x[1][0]):
         avg = ms / max(launches, 1)

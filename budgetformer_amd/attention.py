@@ -288,8 +288,8 @@ class GPSCoreAttention(nn.Module):
 
     Normalise per edge, then dropout, then aggregate (:166-176). In training the
     dropout is drawn inside the kernels (``hip_ops.Dropout``: a Philox keep bit
-    per CSR entry and head, the same bit in the forward and both backward
-    passes) and scales the kept V messages by 1/(1-rate), which is the
+    per entry, keyed by its query row and its slot in that row, and head, the
+    same bit in the forward and both backward passes) and scales the kept V messages by 1/(1-rate), which is the
     reference's arithmetic; no [nnz, H] mask is materialised. The Philox key is
     drawn from torch's default generator, so ``torch.manual_seed`` fixes it. An
     explicit ``drop_mask`` still enters as a per-edge factor.

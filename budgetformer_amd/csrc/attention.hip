@@ -105,10 +105,13 @@ __device__ __forceinline__ typename Elem<T>::Raw load_row_raw_nt(const T* base, 
 // Beyond q, k and v an entry may carry an additive bias (after the clamp), a
 // factor on its V message (any caller factor), and the GraphGPS attention
 // dropout (models/graphgps_dist_node_level.py:166-176), drawn here rather than
-// read from a mask: entry e (its CSR position) and head h are kept iff
-// u < 1 - rate, u = word h % 4 of Philox4x32-10(counter (e_lo, e_hi,
-// offset + h / 4), key seed) mapped to (x >> 8) * 2^-24, and a kept entry's V
-// message is scaled by 1 / (1 - rate). The three passes evaluate the same bit.
+// read from a mask: the entry at slot s of query row r (its place in the row's
+// ascending kv order) and head h are kept iff u < 1 - rate, u = word h % 4 of
+// Philox4x32-10(counter (s, r, offset + h / 4), key seed) mapped to
+// (x >> 8) * 2^-24, and a kept entry's V message is scaled by 1 / (1 - rate).
+// The three passes evaluate the same bit: the query-major passes know (r, s)
+// from the row they walk, the key-major pass from the reverse entry's query
+// and slot, so no pass needs an entry's CSR position for it.
 struct EdgeIn {
   const float* bias;     // float32 [nnz, H] or NULL
   const float* factor;   // float32 [nnz, H] or NULL
@@ -118,78 +121,90 @@ struct EdgeIn {
   uint32_t seed_lo, seed_hi, off_lo, off_hi;
 };
 
-// Keep bits of entry e for heads 4*blk .. 4*blk + 3 (bit j: head 4*blk + j), one Philox call.
-__device__ __forceinline__ uint32_t keep_bits4(const EdgeIn& x, int64_t e, int blk) {
+// Keep bits of the entry at slot s of query row r for heads 4*blk .. 4*blk + 3 (bit j: head 4*blk + j),
+// one Philox call.
+__device__ __forceinline__ uint32_t keep_bits4(const EdgeIn& x, int32_t r, int32_t s, int blk) {
   const uint64_t b = ((uint64_t(x.off_hi) << 32) | x.off_lo) + uint64_t(blk);
-  const U32x4 r = philox4x32_10(U32x4{uint32_t(e), uint32_t(uint64_t(e) >> 32), uint32_t(b), uint32_t(b >> 32)},
-                                x.seed_lo, x.seed_hi);
-  return (u24(r.x) < x.keep ? 1u : 0u) | (u24(r.y) < x.keep ? 2u : 0u) | (u24(r.z) < x.keep ? 4u : 0u) |
-         (u24(r.w) < x.keep ? 8u : 0u);
+  const U32x4 o = philox4x32_10(U32x4{uint32_t(s), uint32_t(r), uint32_t(b), uint32_t(b >> 32)}, x.seed_lo,
+                                x.seed_hi);
+  return (u24(o.x) < x.keep ? 1u : 0u) | (u24(o.y) < x.keep ? 2u : 0u) | (u24(o.z) < x.keep ? 4u : 0u) |
+         (u24(o.w) < x.keep ? 8u : 0u);
 }
 
-__device__ __forceinline__ float dropout_factor(const EdgeIn& x, int64_t e, int head) {
-  return ((keep_bits4(x, e, head >> 2) >> (head & 3)) & 1u) ? x.scale : 0.f;
+__device__ __forceinline__ float dropout_factor(const EdgeIn& x, int32_t r, int32_t s, int head) {
+  return ((keep_bits4(x, r, s, head >> 2) >> (head & 3)) & 1u) ? x.scale : 0.f;
 }
 
-// The keep bits of one iteration's kUnroll entries, drawn once per group: lane j < kUnroll * nb
-// (nb = ceil(H / 4) Philox blocks per entry) draws block j % nb of entry j / nb, and every lane then
-// takes its head's bit by a shuffle (iter_factor), instead of each lane drawing the block of its own
-// head for every entry. Groups narrower than kUnroll * nb lanes draw per lane (shared = false).
+// The keep bits of one iteration's kUnroll entries (query rows rows[u], slots slots[u]), drawn once per
+// group: lane j < kUnroll * nb (nb = ceil(H / 4) Philox blocks per entry) draws block j % nb of entry
+// j / nb, and every lane then takes its head's bit by a shuffle (iter_factor), instead of each lane
+// drawing the block of its own head for every entry (shared). Groups narrower than kUnroll * nb lanes
+// draw their own head's bit of every entry here (bit u of task), so the rows and slots are dead after.
 template <int kUnroll>
 struct IterDrop {
   bool shared;
-  uint32_t task;   // this lane's 4 keep bits
+  uint32_t task;   // shared: this lane's 4 keep bits of its (entry, block); else bit u: entry u, this lane's head
 };
 
 template <int kUnroll>
-__device__ __forceinline__ IterDrop<kUnroll> iter_drop(const EdgeIn& x, const int32_t (&epos)[kUnroll],
-                                                       const bool (&ok)[kUnroll], const Shape& sh,
-                                                       const GroupPos& g) {
+__device__ __forceinline__ IterDrop<kUnroll> iter_drop(const EdgeIn& x, const int32_t (&rows)[kUnroll],
+                                                       const int32_t (&slots)[kUnroll], const bool (&ok)[kUnroll],
+                                                       const Shape& sh, const GroupPos& g) {
   IterDrop<kUnroll> it{false, 0u};
   if (!x.drop) return it;
   const int nb = (sh.H + 3) >> 2;
   it.shared = kUnroll * nb <= (1 << sh.lpr_log2);
-  if (!it.shared) return it;
+  if (!it.shared) {
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+      if (ok[u]) it.task |= ((keep_bits4(x, rows[u], slots[u], g.head >> 2) >> (g.head & 3)) & 1u) << u;
+    return it;
+  }
   const int j = g.g_lane;
   if (j < kUnroll * nb) {
     const int u = j / nb, blk = j - u * nb;
-    int32_t e = 0;
+    int32_t r = 0, s = 0;
     bool live = false;
 #pragma unroll
     for (int w = 0; w < kUnroll; ++w) {
       if (w == u) {
-        e = epos[w];
+        r = rows[w];
+        s = slots[w];
         live = ok[w];
       }
     }
-    if (live) it.task = keep_bits4(x, e, blk);
+    if (live) it.task = keep_bits4(x, r, s, blk);
   }
   return it;
 }
 
-// V-message factor of entry u of the iteration (CSR position e) for this lane's head: the caller's
-// factor times the dropout factor. Every lane of the group calls it for the same u.
+// V-message factor of entry u of the iteration (CSR position e, which only a caller factor reads) for
+// this lane's head: the caller's factor times the dropout factor. Every lane of the group calls it for
+// the same u.
 template <int kUnroll, int EX>
 __device__ __forceinline__ float iter_factor(const EdgeIn& x, const IterDrop<kUnroll>& it, int u, int64_t e,
                                              const Shape& sh, int head) {
   float f = (EX == 2 && x.factor) ? x.factor[e * sh.H + head] : 1.f;
   if (EX == 1 || x.drop) {
+    uint32_t keep;
     if (it.shared) {
       const int nb = (sh.H + 3) >> 2;
-      const uint32_t bits = uint32_t(__shfl(int(it.task), u * nb + (head >> 2), 1 << sh.lpr_log2));
-      f *= ((bits >> (head & 3)) & 1u) ? x.scale : 0.f;
+      keep = (uint32_t(__shfl(int(it.task), u * nb + (head >> 2), 1 << sh.lpr_log2)) >> (head & 3)) & 1u;
     } else {
-      f *= dropout_factor(x, e, head);
+      keep = (it.task >> u) & 1u;
     }
+    f *= keep ? x.scale : 0.f;
   }
   return f;
 }
 
-// The V-message factor of a single entry e for this lane's head (1 without factor and dropout).
+// The V-message factor of a single entry (CSR position e, slot s of query row r) for this lane's head
+// (1 without factor and dropout).
 template <int EX>
-__device__ __forceinline__ float edge_factor(const EdgeIn& x, int64_t e, const Shape& sh, int head) {
+__device__ __forceinline__ float edge_factor(const EdgeIn& x, int64_t e, int32_t r, int32_t s, const Shape& sh,
+                                             int head) {
   float f = (EX == 2 && x.factor) ? x.factor[e * sh.H + head] : 1.f;
-  if (EX == 1 || x.drop) f *= dropout_factor(x, e, head);
+  if (EX == 1 || x.drop) f *= dropout_factor(x, r, s, head);
   return f;
 }
 
@@ -252,8 +267,9 @@ __device__ __forceinline__ int gather_col(const GroupPos& g) { return g.act ? g.
 template <typename T, int EX>
 __device__ __forceinline__ void fwd_segment(const T* __restrict__ k, const T* __restrict__ v,
                                             const int32_t* __restrict__ kv, const EdgeIn& ex,
-                                            int64_t beg, int64_t end, const Shape& sh,
-                                            const GroupPos& g, const typename Elem<T>::Raw& qr,
+                                            int64_t beg, int64_t end, int32_t row, int64_t row_beg,
+                                            const Shape& sh, const GroupPos& g,
+                                            const typename Elem<T>::Raw& qr,
                                             float (&acc)[Elem<T>::kPerVec], float& z) {
   constexpr int V = Elem<T>::kPerVec;
   constexpr int kUnroll = Unroll<T>::fwd;
@@ -279,10 +295,13 @@ __device__ __forceinline__ void fwd_segment(const T* __restrict__ k, const T* __
     }
     IterDrop<kUnroll> drop{false, 0u};
     if (EX) {
-      int32_t epos[kUnroll];   // CSR positions (nnz < 2^31)
+      int32_t rows[kUnroll], slots[kUnroll];   // the dropout's (query row, slot) of each entry
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) epos[u] = int32_t(e0 + u);
-      drop = iter_drop<kUnroll>(ex, epos, ok, sh, g);
+      for (int u = 0; u < kUnroll; ++u) {
+        rows[u] = row;
+        slots[u] = int32_t(e0 + u - row_beg);
+      }
+      drop = iter_drop<kUnroll>(ex, rows, slots, ok, sh, g);
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
@@ -495,7 +514,7 @@ __global__ __launch_bounds__(kBlock) void attn_fwd_kernel(
 #pragma unroll
     for (int i = 0; i < V; ++i) unused[i] = 0.f;
     const typename Elem<T>::Raw qr = load_row_raw(q, r.row, sh.D, g);
-    fwd_segment<T, EX>(k, v, kv, ex, r.beg, r.end, sh, g, qr, acc, z);
+    fwd_segment<T, EX>(k, v, kv, ex, r.beg, r.end, r.row, it.ptr[r.row], sh, g, qr, acc, z);
     block_combine<V>(lds, it.stride, sh, g, acc, unused, false, z, true);
     if (r.single) {
       if ((threadIdx.x >> sh.lpr_log2) == 0) store_out(out, Z, r.row, sh, g, acc, z);
@@ -509,7 +528,7 @@ __global__ __launch_bounds__(kBlock) void attn_fwd_kernel(
   const int64_t beg = qptr[row], end = qptr[row + 1];
   if (end - beg > chunk) return;  // split row: its items and the reduce write it
   const typename Elem<T>::Raw qr = load_row_raw_nt(q, row, sh.D, g);
-  fwd_segment<T, EX>(k, v, kv, ex, beg, end, sh, g, qr, acc, z);
+  fwd_segment<T, EX>(k, v, kv, ex, beg, end, int32_t(row), beg, sh, g, qr, acc, z);
   store_out(out, Z, row, sh, g, acc, z);
 }
 
@@ -581,8 +600,8 @@ __device__ __forceinline__ void add_entry(const EntryTerms& t, const float (&kk)
 template <typename T, int EX>
 __device__ __forceinline__ void dq_segment(const T* __restrict__ k, const T* __restrict__ v,
                                            const int32_t* __restrict__ kv, const EdgeIn& ex,
-                                           int64_t beg, int64_t end, const Shape& sh, const GroupPos& g,
-                                           float inv_dprime, const typename Elem<T>::Raw& qr,
+                                           int64_t beg, int64_t end, int32_t row, int64_t row_beg,
+                                           const Shape& sh, const GroupPos& g, float inv_dprime, const typename Elem<T>::Raw& qr,
                                            const typename Elem<T>::Raw& gr,
                                            float (&A)[Elem<T>::kPerVec], float (&B)[Elem<T>::kPerVec], float& c) {
   constexpr int V = Elem<T>::kPerVec;
@@ -615,10 +634,13 @@ __device__ __forceinline__ void dq_segment(const T* __restrict__ k, const T* __r
     }
     IterDrop<kUnroll> drop{false, 0u};
     if (EX) {
-      int32_t epos[kUnroll];   // CSR positions (nnz < 2^31)
+      int32_t rows[kUnroll], slots[kUnroll];   // the dropout's (query row, slot) of each entry
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) epos[u] = int32_t(e0 + u);
-      drop = iter_drop<kUnroll>(ex, epos, ok, sh, g);
+      for (int u = 0; u < kUnroll; ++u) {
+        rows[u] = row;
+        slots[u] = int32_t(e0 + u - row_beg);
+      }
+      drop = iter_drop<kUnroll>(ex, rows, slots, ok, sh, g);
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
@@ -647,7 +669,8 @@ struct TokenEntry {
 
 template <typename T, int EX, bool ADD>
 __device__ __forceinline__ TokenEntry token_entry(const T* __restrict__ k, const T* __restrict__ v, const EdgeIn& ex,
-                                                  int64_t e, const Shape& sh, const GroupPos& g, float inv_dprime,
+                                                  int64_t e, int32_t row, const Shape& sh, const GroupPos& g,
+                                                  float inv_dprime,
                                                   const typename Elem<T>::Raw& qr, const typename Elem<T>::Raw& gr,
                                                   float (&A)[Elem<T>::kPerVec], float (&B)[Elem<T>::kPerVec],
                                                   float& c) {
@@ -658,7 +681,9 @@ __device__ __forceinline__ TokenEntry token_entry(const T* __restrict__ k, const
     d += __shfl_xor(d, o, 64);
     w += __shfl_xor(w, o, 64);
   }
-  const EntryTerms t = entry_terms<EX>(d, w, inv_dprime, ex, e, EX ? edge_factor<EX>(ex, e, sh, g.head) : 1.f, sh, g);
+  // key 0 is the first entry of its row: slot 0
+  const EntryTerms t =
+      entry_terms<EX>(d, w, inv_dprime, ex, e, EX ? edge_factor<EX>(ex, e, row, 0, sh, g.head) : 1.f, sh, g);
   if (ADD) {
     float kk[V];
     Elem<T>::unpack(kr, kk);
@@ -773,7 +798,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_q_kernel(
     const float inv_dprime = row_inv_dprime<T>(Z, r.row, sh, g);
     const int64_t e_tok = it.ptr[r.row];
     const bool tok_row = token_rec != nullptr && r.row >= tok_first && e_tok < it.ptr[r.row + 1];
-    dq_segment<T, EX>(k, v, kv, ex, r.beg, r.end, sh, g, inv_dprime, qr, gr, A, B, c);
+    dq_segment<T, EX>(k, v, kv, ex, r.beg, r.end, r.row, e_tok, sh, g, inv_dprime, qr, gr, A, B, c);
     block_combine<V>(lds, it.stride, sh, g, A, B, true, c, true);
     float fk[V], fv[V];
 #pragma unroll
@@ -782,7 +807,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_q_kernel(
       if (grp == 0) {
         const float dd = c * inv_dprime;
         if (tok_row) {
-          const TokenEntry te = token_entry<T, EX, false>(k, v, ex, e_tok, sh, g, inv_dprime, qr, gr,
+          const TokenEntry te = token_entry<T, EX, false>(k, v, ex, e_tok, r.row, sh, g, inv_dprime, qr, gr,
                                                              A, B, c);
           finish_token<T, EX>(te, inv_dprime, dd, qr, gr, dbias, e_tok, sh, g, fk, fv);
         }
@@ -814,12 +839,12 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_q_kernel(
   const int64_t e_tok = beg;
   TokenEntry te{};
   if (tok) {
-    te = token_entry<T, EX, true>(k, v, ex, e_tok, sh, g, inv_dprime, qr, gr, A, B, c);
+    te = token_entry<T, EX, true>(k, v, ex, e_tok, int32_t(row), sh, g, inv_dprime, qr, gr, A, B, c);
     ++beg;
   }
   float dd = 0.f;
   if (live) {
-    dq_segment<T, EX>(k, v, kv, ex, beg, end, sh, g, inv_dprime, qr, gr, A, B, c);
+    dq_segment<T, EX>(k, v, kv, ex, beg, end, int32_t(row), e_tok, sh, g, inv_dprime, qr, gr, A, B, c);
     dd = c * inv_dprime;
     store_dq<T, V>(dq, rstat, row, sh, g, A, B, inv_dprime, dd, true);
   }
@@ -883,7 +908,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_q_reduce_kernel(
   if (tok) {   // key 0 was summed by item 0; its scalars are recomputed here to finish its terms
     const typename Elem<T>::Raw qr = load_row_raw(q, row, sh.D, g);
     const typename Elem<T>::Raw gr = load_row_raw(dout, row, sh.D, g);
-    const TokenEntry te = token_entry<T, 2, false>(k, v, ex, e_tok, sh, g, inv_dprime, qr, gr, A, B, c);
+    const TokenEntry te = token_entry<T, 2, false>(k, v, ex, e_tok, row, sh, g, inv_dprime, qr, gr, A, B, c);
     finish_token<T, 2>(te, inv_dprime, dd, qr, gr, dbias, e_tok, sh, g, fk, fv);
     store_token_record<V>(token_rec + int64_t(it.item_off[row]) * (2 * sh.D), sh, g, fk, fv);
   }
@@ -927,12 +952,17 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
     int t[kUnroll];
     bool ok[kUnroll];
     ids.fetch(kq, i0, end, g, t, ok);
-    // each entry's CSR position: its query row's start plus its slot in that row; the row starts are
-    // gathered before the rows, so the keep bits below wait for them alone and overlap the row gathers
-    int32_t epos[kUnroll];   // nnz < 2^31
+    // each entry's slot in its query's row: with the query, the dropout's key; with the row's start
+    // (gathered only by EX == 2, before the rows, so that it overlaps them), the CSR position that
+    // indexes the bias, factor and dbias
+    int32_t slot[kUnroll], epos[kUnroll];   // nnz < 2^31
     if (EX) {
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) epos[u] = ks[ok[u] ? i0 + u : end - 1] + int32_t(qptr[t[u]]);
+      for (int u = 0; u < kUnroll; ++u) slot[u] = ks[ok[u] ? i0 + u : end - 1];
+    }
+    if (EX == 2) {
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) epos[u] = slot[u] + int32_t(qptr[t[u]]);
     }
     typename Elem<T>::Raw qr[kUnroll], gr[kUnroll];
     float2 rs[kUnroll];
@@ -943,7 +973,7 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
       rs[u] = rstat[int64_t(t[u]) * sh.H + g.head];
     }
     IterDrop<kUnroll> drop{false, 0u};
-    if (EX) drop = iter_drop<kUnroll>(ex, epos, ok, sh, g);
+    if (EX) drop = iter_drop<kUnroll>(ex, t, slot, ok, sh, g);
     float d[kUnroll], w[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
@@ -960,7 +990,7 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       if (!ok[u]) continue;
-      const int64_t e = EX ? int64_t(epos[u]) : 0;
+      const int64_t e = EX == 2 ? int64_t(epos[u]) : 0;
       const float apre = d[u] * sh.inv_scale;
       float a = fminf(fmaxf(apre, -sh.clamp), sh.clamp);
       if (EX == 2) a += edge_bias(ex, e, sh, g.head);
@@ -984,7 +1014,7 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
 
 // Blocks [0, k_items) take the key-side items, the rest one short key row per
 // group, longest rows first. EX: 0 plain, 1 dropout only, 2 bias / factor / dropout / dbias
-// (EX > 0 needs ks and qptr).
+// (EX > 0 needs ks; EX == 2 also reads qptr).
 template <typename T, bool NT, bool PRE, int EX>
 __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,

@@ -942,7 +942,8 @@ class AttentionIndex:
 
     def ensure_entries(self):
         """Each reverse entry's slot in its query's row (ks), which the dk/dv pass reads only with a bias,
-        factor or dropout: the entry's CSR position is qptr[kq] + ks."""
+        factor or dropout: (kq, ks) keys the dropout, and qptr[kq] + ks is the CSR position a bias or
+        factor is indexed by."""
         self.ensure_backward()
         if self.ks_all is None and self.cap:
             self.ks_all = reverse_slots(self._sorted, self.qptr)
@@ -1093,9 +1094,9 @@ _DT = {torch.float32: N.BF_DTYPE_F32, torch.bfloat16: N.BF_DTYPE_BF16}
 
 @dataclass(frozen=True)
 class Dropout:
-    """The in-kernel GraphGPS attention dropout (bf_attn_dropout): entry e, head h kept iff Philox
-    word h % 4 of counter (e, offset + h // 4), key seed, maps below 1 - rate; kept V messages scaled
-    by 1 / (1 - rate)."""
+    """The in-kernel GraphGPS attention dropout (bf_attn_dropout): head h of the entry at slot s of query
+    row r is kept iff Philox word h % 4 of counter (s, r, offset + h // 4), key seed, maps below 1 - rate;
+    kept V messages scaled by 1 / (1 - rate)."""
     rate: float
     seed: int
     offset: int = 0

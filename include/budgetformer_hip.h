@@ -499,10 +499,12 @@ typedef struct bf_attn_index {
 
 /* GraphGPS attention dropout drawn inside the kernels
  * (models/graphgps_dist_node_level.py:166-176; rate = attention_dropout_rate,
- * utils/parser_node_level.py:58). Entry e (its CSR position in the index) and
- * head h are kept iff u < 1 - rate, where u = word h % 4 of Philox4x32-10 with
- * counter (e_lo, e_hi, (offset + h/4)_lo, (offset + h/4)_hi) and key
- * (seed_lo, seed_hi), mapped to (x >> 8) * 2^-24; a kept entry's V message
+ * utils/parser_node_level.py:58). The entry at slot s of query row r (its
+ * place in the row's ascending kv order) and head h are kept iff u < 1 - rate,
+ * where u = word h % 4 of Philox4x32-10 with counter (s, r, (offset + h/4)_lo,
+ * (offset + h/4)_hi) and key (seed_lo, seed_hi), mapped to (x >> 8) * 2^-24
+ * (the key-major pass knows an entry by its query kq and slot ks, so the mask
+ * needs no CSR position there); a kept entry's V message
  * (after the softmax normalisation) is scaled by 1/(1 - rate). Forward and
  * backward given the same struct draw the same mask; no [nnz, H] mask exists.
  * Pass NULL (or rate 0) for none.                                           */
@@ -543,7 +545,8 @@ int bf_attn_fwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int3
  * gradients (the reference, under autocast, keeps out in float32).
  *   dbias: NULL or float32 [nnz, H] (per CSR position; needs idx->ks, as do
  *   a bias, a factor and a dropout: the key-major pass knows each entry by its
- *   query and slot, and finds its CSR position as qptr[kq] + ks);
+ *   query and slot, which key the dropout, and finds the CSR position a bias,
+ *   factor or dbias is indexed by as qptr[kq] + ks);
  *   rowstat: float32 [n_q, H, 2] scratch (per query and head
  *   {1/D', Delta/D'}, written by the query-major pass and read by the
  *   key-major pass).                                                         */

@@ -10,6 +10,10 @@ with the Random123 library (tests/test_oracle_philox.py).
 The walk stream: uniform for global walk id w, step l is word (l % 4) of
 Philox(counter = (w_lo, w_hi, off_lo + l//4, off_hi), key = (seed_lo, seed_hi)),
 mapped to (x >> 8) * 2^-24.
+
+The attention-dropout stream: head h of the entry at slot s of query row r is
+word (h % 4) of Philox(counter = (s, r, off_lo + h//4, off_hi), key = (seed_lo,
+seed_hi)), mapped the same way and kept iff below 1 - rate.
 """
 from __future__ import annotations
 
@@ -58,23 +62,35 @@ def walk_uniforms(q_lo: int, n_q: int, walks_per_node: int, walk_length: int, se
     return out
 
 
-def dropout_keep(nnz: int, num_heads: int, rate: float, seed: int, offset: int = 0) -> np.ndarray:
-    """bool [nnz, H]: the GraphGPS attention-dropout keep mask the attention kernels draw. Entry e (its
-    CSR position), head h: word h % 4 of Philox(counter = (e_lo, e_hi, (offset + h // 4)_lo, _hi), key =
+def dropout_keep(rows, slots, num_heads: int, rate: float, seed: int, offset: int = 0) -> np.ndarray:
+    """bool [E, H]: the GraphGPS attention-dropout keep mask the attention kernels draw, for entries given by
+    their query row and their slot in that row (rows[i], slots[i], int arrays of length E). Head h of the
+    entry at slot s of row r: word h % 4 of Philox(counter = (s, r, (offset + h // 4)_lo, _hi), key =
     (seed_lo, seed_hi)) mapped to (x >> 8) * 2^-24; kept iff that is below 1 - rate (float32)."""
-    e = np.arange(nnz, dtype=np.uint64)
+    r = np.asarray(rows, dtype=np.uint64).reshape(-1)
+    s_ = np.asarray(slots, dtype=np.uint64).reshape(-1)
+    assert r.shape == s_.shape
     seed = int(seed) & 0xFFFFFFFFFFFFFFFF
     key = (seed & 0xFFFFFFFF, seed >> 32)
     keep_below = np.float32(1.0) - np.float32(rate)
-    out = np.zeros((nnz, num_heads), dtype=bool)
+    out = np.zeros((r.size, num_heads), dtype=bool)
     for blk in range((num_heads + 3) // 4):
         b = (int(offset) + blk) & 0xFFFFFFFFFFFFFFFF
-        ctr = np.stack([e & MASK, e >> np.uint64(32), np.full_like(e, b & 0xFFFFFFFF), np.full_like(e, b >> 32)],
-                       axis=-1)
-        r = philox4x32_10(ctr, key)
+        ctr = np.stack([s_ & MASK, r & MASK, np.full_like(r, b & 0xFFFFFFFF), np.full_like(r, b >> 32)], axis=-1)
+        x = philox4x32_10(ctr, key)
         for j in range(4):
             h = blk * 4 + j
             if h < num_heads:
-                u = (r[:, j] >> np.uint32(8)).astype(np.float32) * np.float32(1.0 / 16777216.0)
+                u = (x[:, j] >> np.uint32(8)).astype(np.float32) * np.float32(1.0 / 16777216.0)
                 out[:, h] = u < keep_below
     return out
+
+
+def dropout_keep_csr(qptr, num_heads: int, rate: float, seed: int, offset: int = 0) -> np.ndarray:
+    """dropout_keep for every entry of a query-major CSR (row pointers qptr [n_q + 1]), in CSR order: entry
+    e of row r sits at slot e - qptr[r]."""
+    qptr = np.asarray(qptr, dtype=np.int64)
+    lens = np.diff(qptr)
+    rows = np.repeat(np.arange(lens.size, dtype=np.int64), lens)
+    slots = np.arange(int(qptr[-1]) - int(qptr[0]), dtype=np.int64) - np.repeat(qptr[:-1] - qptr[0], lens)
+    return dropout_keep(rows, slots, num_heads, rate, seed, offset)

@@ -1,6 +1,7 @@
 """The GraphGPS attention dropout drawn inside the kernels (models/graphgps_dist_node_level.py:166-176)
 against the float64 oracle with the mask oracle.philox.dropout_keep draws: forward and both backward
-passes see the same keep bit per CSR entry and head, and kept V messages are scaled by 1/(1-rate)."""
+passes see the same keep bit per entry (its query row and its slot in the row) and head, and kept V
+messages are scaled by 1/(1-rate)."""
 import numpy as np
 import pytest
 import torch
@@ -23,7 +24,7 @@ def _run(dev, q, k, v, idx, dout, dropout):
 
 def _oracle(q, k, v, idx, dout, rate, seed, offset):
     H = q.shape[1]
-    keep = torch.from_numpy(philox.dropout_keep(idx.nnz, H, rate, seed, offset))
+    keep = torch.from_numpy(philox.dropout_keep_csr(idx.qptr.cpu().numpy(), H, rate, seed, offset))
     factor = keep.double() / (1.0 - rate)
     ei = torch.stack([idx.kv.cpu().long(), idx.entry_rows().cpu()])      # CSR order: entry e is column e
     q64, k64, v64, d64 = (t.double() for t in (q, k, v, dout))
@@ -53,7 +54,7 @@ def test_dropout_coo_index(hip_device, dtype, rate, chunk, item):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_dropout_table_index_with_token_column(hip_device, dtype):
     """A table index with the Graphormer token: key 0's entries are finished by the dq pass and summed
-    from its records; their keep bits must be the same ones the oracle draws at their CSR positions."""
+    from its records; their keep bits must be the same ones the oracle draws at their (row, slot 0)."""
     from budgetformer_amd.hip_ops import AttentionIndex, Dropout
     rng = np.random.default_rng(3)
     n, width, H, hn = 1200, 6, 8, 16
@@ -96,7 +97,7 @@ def test_gps_module_training_dropout_is_drawn_in_the_kernels(hip_device):
         assert torch.equal(a, b)
     torch.manual_seed(1234)
     seed = int(torch.randint(0, 2 ** 62, (1,), dtype=torch.int64).item())
-    keep = torch.from_numpy(philox.dropout_keep(idx.nnz, H, 0.5, seed, 0))
+    keep = torch.from_numpy(philox.dropout_keep_csr(idx.qptr.cpu().numpy(), H, 0.5, seed, 0))
     ei_o = torch.stack([idx.kv.cpu().long(), idx.entry_rows().cpu()])
     q64, k64, v64 = (t.double().requires_grad_(True) for t in (q, k, v))
     ref = sa.gps_sparse_attention(q64, k64, v64, ei_o, keep, 2.0)

@@ -85,8 +85,9 @@ def test_bf16_kv_pass_c4_instance_with_dropout(hip_device, extras):
     """The dk/dv instance c4 times: attn_bwd_kv_kernel<bf16, NT, PRE, EX=1> (dropout 0.5 drawn in the
     kernels; q + dO above 256 MB, more than 1M kv rows: non-temporal gathers, four rows per lane group,
     prefetched slots), and its general twin EX=2 (additive bias, dbias and dropout). Each entry's keep bits
-    come from its CSR position (qptr[kq] + ks in the key-major pass), so the float64 oracle takes the index's
-    own CSR order, remapped to the compacted rows, with the mask oracle.philox.dropout_keep draws."""
+    come from its query row and its slot in that row (kq and ks in the key-major pass), so the float64
+    oracle takes the index's own CSR order, remapped to the compacted rows, with the mask
+    oracle.philox.dropout_keep_csr draws over the index's row pointers."""
     from budgetformer_amd import hip_ops
     from budgetformer_amd.hip_ops import AttentionIndex, Dropout
     H, hn, rate = 8, 16, 0.5
@@ -109,7 +110,7 @@ def test_bf16_kv_pass_c4_instance_with_dropout(hip_device, extras):
     idx.resolve()
     assert idx.kplan.items > 0          # the hub key row ran as split items
     ei = _csr_edges_compacted(idx, qa, kt)
-    keep = torch.from_numpy(philox.dropout_keep(nnz, H, rate, seed, offset))
+    keep = torch.from_numpy(philox.dropout_keep_csr(idx.qptr.cpu().numpy(), H, rate, seed, offset))
     factor = keep.double() / (1.0 - rate)
     qc, doc = q[qa].double().cpu(), dout[qa].double().cpu()
     kc, vc = k[kt].double().cpu(), v[kt].double().cpu()

@@ -90,7 +90,7 @@ def test_attention_ops_equal_the_abi_and_the_oracle(hip_device, dtype, extras):
     ei = torch.stack([idx.kv.cpu().long(), idx.entry_rows().cpu()])
     f64 = None
     if extras:
-        keep = philox.dropout_keep(idx.nnz, H, drop[0], seed=drop[1], offset=drop[2])
+        keep = philox.dropout_keep_csr(idx.qptr.cpu().numpy(), H, drop[0], seed=drop[1], offset=drop[2])
         f64 = factor.cpu().double() * torch.from_numpy(keep).double() / (1.0 - drop[0])
     b64 = None if bias is None else bias.cpu().double()
     q64, k64, v64, d64 = (x.cpu().double() for x in (q, k, v, dout))

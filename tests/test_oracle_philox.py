@@ -89,29 +89,51 @@ def test_uniform_range_endpoints():
 
 
 def test_dropout_keep_layout_and_hand_values():
-    """The attention-dropout mask: entry e, head h is word h % 4 of Philox(counter (e, offset + h // 4)),
-    kept iff (x >> 8) * 2^-24 < 1 - rate. Entry 0 with seed 0, offset 0 draws the published zero vector
-    (heads 0..3): u = 0x6627E8, 0xE169C5, 0xBC57AC, 0x9B00DB over 2^24 = 0.3990, 0.8805, 0.7357, 0.6055."""
-    m = philox.dropout_keep(1, 4, 0.5, seed=0, offset=0)[0]
+    """The attention-dropout mask: head h of the entry at slot s of query row r is word h % 4 of
+    Philox(counter (s, r, offset + h // 4)), kept iff (x >> 8) * 2^-24 < 1 - rate. Slot 0 of row 0 with
+    seed 0, offset 0 draws the published zero vector (heads 0..3): u = 0x6627E8, 0xE169C5, 0xBC57AC, 0x9B00DB
+    over 2^24 = 0.3990, 0.8805, 0.7357, 0.6055."""
+    m = philox.dropout_keep([0], [0], 4, 0.5, seed=0, offset=0)[0]
     assert list(m) == [True, False, False, False]          # only 0.399 < 0.5
-    m = philox.dropout_keep(1, 4, 0.3, seed=0, offset=0)[0]
+    m = philox.dropout_keep([0], [0], 4, 0.3, seed=0, offset=0)[0]
     assert list(m) == [True, False, False, True]           # below 0.7: 0.399, 0.6055
-    # heads 4..7 take the next counter block; every element against a direct block call
+    # heads 4..7 take the next counter block; every element against a direct block call, with the slot in
+    # the counter's first word and the row in its second (a swap of the two fails here)
     seed, off, H = (5 << 32) | 9, 11, 8
-    m = philox.dropout_keep(40, H, 0.25, seed=seed, offset=off)
-    for e in (0, 1, 17, 39):
+    rows = np.array([0, 3, 3, 17, 2 ** 31 - 1])
+    slots = np.array([0, 1, 5, 3, 7])
+    m = philox.dropout_keep(rows, slots, H, 0.25, seed=seed, offset=off)
+    for i in range(rows.size):
         for h in range(H):
             blk = off + h // 4
-            ctr = np.array([[e, 0, blk, 0]], dtype=np.uint32)
+            ctr = np.array([[slots[i], rows[i], blk, 0]], dtype=np.uint32)
             word = int(philox.philox4x32_10(ctr, (seed & 0xFFFFFFFF, seed >> 32))[0, h % 4])
-            assert m[e, h] == (np.float32((word >> 8) / 16777216.0) < np.float32(0.75)), (e, h)
+            assert m[i, h] == (np.float32((word >> 8) / 16777216.0) < np.float32(0.75)), (i, h)
+    swapped = philox.dropout_keep(slots[1:4], rows[1:4], H, 0.25, seed=seed, offset=off)
+    assert not np.array_equal(swapped, m[1:4])
+
+
+def test_dropout_keep_csr_rows_and_slots():
+    """dropout_keep_csr takes each CSR entry's row and its slot e - qptr[row]: rows of lengths 2, 0, 3, 1
+    are the entries (row, slot) = (0,0) (0,1) (2,0) (2,1) (2,2) (3,0); a CSR whose row pointers start past 0
+    (a slice of a larger CSR) numbers its slots the same way."""
+    qptr = np.array([0, 2, 2, 5, 6])
+    want = philox.dropout_keep([0, 0, 2, 2, 2, 3], [0, 1, 0, 1, 2, 0], 8, 0.5, seed=77, offset=4)
+    assert np.array_equal(philox.dropout_keep_csr(qptr, 8, 0.5, seed=77, offset=4), want)
+    assert np.array_equal(philox.dropout_keep_csr(qptr + 10, 8, 0.5, seed=77, offset=4), want)
 
 
 def test_dropout_keep_rate_limits_and_statistics():
-    assert philox.dropout_keep(1000, 8, 0.0, seed=3).all()
-    assert not philox.dropout_keep(1000, 8, 1.0, seed=3).any()
-    m = philox.dropout_keep(200_000, 8, 0.5, seed=12345)
+    rows = np.repeat(np.arange(25_000), 8)
+    slots = np.tile(np.arange(8), 25_000)
+    assert philox.dropout_keep(rows[:1000], slots[:1000], 8, 0.0, seed=3).all()
+    assert not philox.dropout_keep(rows[:1000], slots[:1000], 8, 1.0, seed=3).any()
+    m = philox.dropout_keep(rows, slots, 8, 0.5, seed=12345)
     frac = m.mean()
     assert abs(frac - 0.5) < 0.003                         # 1.6M Bernoulli draws: sd 0.0004
-    # heads and entries are not correlated: the mask of head 0 agrees with head 1 about half the time
+    # heads, slots and rows are not correlated: head 0 agrees with head 1 about half the time, and so do
+    # neighbouring slots of a row and the same slot of neighbouring rows
     assert abs((m[:, 0] == m[:, 1]).mean() - 0.5) < 0.01
+    r = m.reshape(25_000, 8, 8)
+    assert abs((r[:, 0, :] == r[:, 1, :]).mean() - 0.5) < 0.01
+    assert abs((r[:-1, 0, :] == r[1:, 0, :]).mean() - 0.5) < 0.01
