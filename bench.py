@@ -9,18 +9,23 @@ A step is one pass of the hot path over one configuration:
 Inputs (graph, q/k/v, dO) are resident in HBM before the timed region.
 
 The default run measures c2 (the configuration the north-star target is quoted
-on) and, in the same JSON line, a c3 record whose working set exceeds the
-256 MB Infinity Cache (`extra_configs`), each with its own roofline.
+on) and, in the same JSON line under `extra_configs`, c3 (bf16, a working set
+above the 256 MB Infinity Cache), c4 (GraphGPS, B=32, in-kernel dropout 0.5)
+and c5 (a 27.8M-query shard of a 1.6B-edge graph with the Graphormer token),
+each with its own roofline and CPU baseline.
 
-`value` is the attention layer's throughput under the gather model (every
-gathered K/V/q/dO row counted at full size per edge, the row streams once) =
-algorithmic bytes / fwd+bwd time. It is a work rate, not an HBM rate: at c2 the
-gathered rows are served from the Infinity Cache and it exceeds the 8 TB/s HBM
-peak. Beside it: the compulsory (unique-tensor) bytes and their rate, a lower
-bound of the HBM traffic; the dominant kernel's roofline (algorithmic bytes /
-its HIP-event time, and the HBM-side traffic from the committed rocprofv3
-counter summary); the edge builder's RW edges/s and table entries/s; and the
-CPU oracle timed on this host's cores as `cpu_baseline`.
+`value` is the attention layer's memory traffic rate: the bytes its kernels
+move between L2 and the memory fabric per layer (request-size counter sums of
+the committed rocprofv3 profile, `profiles/attention_<config>_<dtype>_pmc.json`,
+per launch) over the layer's fwd+bwd HIP-event time. Requests the Infinity
+Cache serves count too, so it bounds the HBM rate from above, and it cannot
+exceed what the fabric moves. Beside it: the gather-model rate (every gathered
+K/V/q/dO row counted at full size per edge; a work rate that exceeds the HBM
+peak at c2, where the gathered rows are cache-resident) and the compulsory
+(unique-tensor) rate, a lower bound of the HBM traffic; the dominant kernel's
+roofline (algorithmic bytes / its HIP-event time, with its counter traffic and
+rate beside it); the edge builder's RW edges/s and table entries/s; and the CPU
+oracle timed on this host's cores as `cpu_baseline`.
 """
 from __future__ import annotations
 
@@ -47,15 +52,15 @@ CONFIGS = {
     "c3": dict(name="c3: Chung-Lu power-law N=2,449,029 E=61,859,140 (max deg 17K), GT hidden 128, 8 heads, L=4 P=4 "
                     "B=16 (8,8), bf16",
                n=2_449_029, e=61_859_140, kind="device", max_degree=17_000, H=8, hn=16, L=4, P=4, b_r=8, b_w=8,
-               dtype="bfloat16", token=False, cpu_sample=200_000),
+               dtype="bfloat16", token=False, cpu_sample=100_000),
     "c4": dict(name="c4: power-law N=2,923,922 E=13,975,788, GraphGPS hidden 128, 8 heads, L=8 P=4 B=32 (16,16), "
                     "bf16, attention dropout 0.5 (training; drawn in the kernels)",
                n=2_923_922, e=13_975_788, kind="device", H=8, hn=16, L=8, P=4, b_r=16, b_w=16, dtype="bfloat16",
-               token=False, dropout=0.5, cpu_sample=200_000),
+               token=False, dropout=0.5, cpu_sample=100_000),
     "c5": dict(name="c5: one GPU's 27.8M-query shard of a power-law graph N=111,059,956 E=1.6B (max deg 100K), "
                     "Graphormer hidden 128, 8 heads, L=4 P=2 B=8 (4,4), bf16, global token (the shard holds node 0)",
                n=111_059_956, e=1_600_000_000, kind="device", max_degree=100_000, H=8, hn=16, L=4, P=2, b_r=4,
-               b_w=4, dtype="bfloat16", token=True, n_q=27_800_000, cpu_sample=1_000_000),
+               b_w=4, dtype="bfloat16", token=True, n_q=27_800_000, cpu_sample=250_000),
 }
 
 
@@ -90,11 +95,14 @@ def token_records(s, D, n_q, q_items):
     return q_items + -(-n_q // (256 // lpr))
 
 
-def kernel_bytes(s, D, H, lens_q, lens_k, n_token_rec=0, entry_bytes=0):
+def kernel_bytes(s, D, H, lens_q, lens_k, n_token_rec=0, entry_bytes=0, token_row=0, chunk=128, kv_blocks=0):
     """Algorithmic bytes of the three pass kernels (each covers every entry: short rows and split items).
 
     With a token column (n_token_rec records) the dq pass also writes key 0's dK/dV terms, 2*D floats per
     record, and the dk/dv pass reads those records instead of gathering key 0's entries and its K, V rows.
+    With the token row (token_row = its length: query 0 attends kv 1..token_row) each of the dk/dv pass's
+    kv_blocks row workgroups reads query 0's q, dO and row stats once, and its short kv rows in 1..token_row
+    take their first entry (query 0's) from that copy instead of gathering it.
     entry_bytes: what the dk/dv pass reads per gathered entry beyond its query id: 4 for the entry's slot in
     its query's row (with the query, the dropout's key), 12 with a bias or factor (the slot and the query's
     row start, which give the CSR position they are indexed by)."""
@@ -107,6 +115,11 @@ def kernel_bytes(s, D, H, lens_q, lens_k, n_token_rec=0, entry_bytes=0):
         gathered -= int(lens_k[0])
         nk_touched -= int(lens_k[0] > 0)
     row = s * D
+    tok_bytes = 0
+    if token_row:
+        lk = lens_k[1:token_row + 1]
+        gathered -= int(((lk > 0) & (lk <= chunk)).sum())
+        tok_bytes = kv_blocks * (2 * row + 8 * H)
     return {
         # Q read, O write, K and V gathered per edge, kv ids, Z write, qptr
         "attn_fwd_kernel": row * (2 * n_q + 2 * nnz) + 4 * nnz + 4 * H * n_q + 8 * n_q,
@@ -115,7 +128,7 @@ def kernel_bytes(s, D, H, lens_q, lens_k, n_token_rec=0, entry_bytes=0):
         # dK, dV written for every row; K, V read for rows with entries; Q and dO per gathered entry,
         # the {1/D', Delta/D'} row stats per gathered entry, kq ids, kptr, row order (+ token records)
         "attn_bwd_kv_kernel": row * (2 * n_kv + 2 * nk_touched + 2 * gathered) + 8 * H * gathered
-        + 4 * gathered + 12 * n_kv + rec_bytes + entry_bytes * gathered,
+        + 4 * gathered + 12 * n_kv + rec_bytes + entry_bytes * gathered + tok_bytes,
     }
 
 
@@ -253,7 +266,7 @@ def main(argv=None):
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--extra", default=None,
                     help="comma-separated configs measured after the main one and reported in the same JSON line "
-                         "under extra_configs (default: c3 when --config is c2, else none; 'none' for none)")
+                         "under extra_configs (default: c3,c4,c5 when --config is c2, else none; 'none' for none)")
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
     ap.add_argument("--chunk", type=int, default=None, help="split threshold (rows longer than this are split)")
     ap.add_argument("--item", type=int, default=None, help="entries per split item")
@@ -299,17 +312,17 @@ def main(argv=None):
     chunk = args.chunk
     item = args.item
     result = run(args.config, args.steps, args.warmup, chunk, item, with_cpu=not args.no_cpu_baseline)
-    extra = args.extra if args.extra is not None else ("c3" if args.config == "c2" else "none")
+    extra = args.extra if args.extra is not None else ("c3,c4,c5" if args.config == "c2" else "none")
     extras = [c for c in extra.split(",") if c and c != "none"]
     records = []
     for name in extras:
         if name not in CONFIGS:
             raise SystemExit(f"bench.py: unknown config {name!r} in --extra")
         torch.cuda.empty_cache()
-        rec = run(name, args.steps, args.warmup, chunk, item, with_cpu=False)
+        rec = run(name, args.steps, args.warmup, chunk, item, with_cpu=not args.no_cpu_baseline)
         records.append({k: rec[k] for k in ("config", "dtype", "steps", "warmup", "ms_per_step", "value", "unit",
                                             "value_basis", "attn_fwd_bwd_ms", "edge_build_ms", "attention",
-                                            "builder", "roofline", "kernels")})
+                                            "builder", "roofline", "kernels", "cpu_baseline") if k in rec})
     if records:
         result["extra_configs"] = records
     print(json.dumps(result), flush=True)
@@ -424,7 +437,15 @@ def run(config, steps, warmup, chunk=None, item=None, with_cpu=True):
 
     # per-kernel roofline of the three pass kernels
     n_rec = token_records(s_bytes, D, idx.n_q, idx.qplan.items) if idx.token_column else 0
-    kb = kernel_bytes(s_bytes, D, H, lens_q, lens_k, n_rec, entry_bytes=4 if rate else 0)
+    kv_var = hip_ops.kv_pass_variant(idx.n_q, idx.n_kv, dt, H, hn)
+    # the dk/dv pass takes the token row's entries from a per-workgroup copy with several rows per group
+    tok_row = int(lens_q[0]) if idx.token_column == 1 and kv_var["rows_per_group"] > 1 else 0
+    lpr = 1
+    while lpr < D * s_bytes // 16:
+        lpr *= 2
+    kv_blocks = -(-(-(-idx.n_kv // kv_var["rows_per_group"])) // (256 // lpr))
+    kb = kernel_bytes(s_bytes, D, H, lens_q, lens_k, n_rec, entry_bytes=4 if rate else 0, token_row=tok_row,
+                      chunk=chunk, kv_blocks=kv_blocks)
     kernels = {}
     for name, (ms, launches) in sorted(kstats.items(), key=lambda x: -x[1][0]):
         avg = ms / max(launches, 1)
@@ -435,18 +456,31 @@ def run(config, steps, warmup, chunk=None, item=None, with_cpu=True):
         kernels[name] = rec
     dominant = max((n_ for n_ in kernels if n_ in kb), key=lambda n_: kernels[n_]["avg_ms"])
     dom = kernels[dominant]
-    traffic = traffic_src = None
+    # counter traffic per dispatch (request-size sums of the committed profile of this config and dtype)
+    prof, traffic_src = {}, None
     pmc_path = os.path.join(ROOT, "profiles", f"attention_{config}_{cfg['dtype']}_pmc.json")
     if os.path.exists(pmc_path) and chunk == hip_ops.DEFAULT_CHUNK and item == hip_ops.DEFAULT_ITEM:
         with open(pmc_path) as fh:
-            rec = json.load(fh).get("kernels", {}).get(dominant)
-        if rec:
-            traffic = rec["traffic_bytes"]
-            traffic_src = os.path.relpath(pmc_path, ROOT)
+            prof = json.load(fh).get("kernels", {})
+        traffic_src = os.path.relpath(pmc_path, ROOT)
+    for name_, rec_ in kernels.items():
+        if name_ in prof:
+            rec_["traffic_bytes"] = prof[name_]["traffic_bytes"]
+            rec_["traffic_gbs"] = round(prof[name_]["traffic_bytes"] / (rec_["avg_ms"] * 1e-3) / 1e9, 1)
+    traffic = prof.get(dominant, {}).get("traffic_bytes")
     roofline = {"kernel": dominant, "bound": "hbm", "achieved": dom["achieved_gbs"], "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(dom["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
                 "algorithmic_bytes": dom["algorithmic_bytes"], "traffic_source": traffic_src,
-                "achieved_basis": "the kernel's algorithmic bytes (gather model) / its HIP-event average duration"}
+                "achieved_basis": "the kernel's algorithmic bytes (gather model) / its HIP-event average duration",
+                "traffic_gbs": dom.get("traffic_gbs"),
+                "traffic_frac": round(dom["traffic_gbs"] / HBM_PEAK_GBS, 4) if "traffic_gbs" in dom else None,
+                "traffic_basis": "the kernel's L2-to-fabric bytes per dispatch (request-size counter sums) / its "
+                                 "HIP-event average duration"}
+    # the layer's traffic: every attention kernel's counter bytes per dispatch times its launches per layer
+    attn_kernels = [n_ for n_ in kernels if n_.startswith("attn_")]
+    layer_traffic = None
+    if attn_kernels and all(n_ in prof for n_ in attn_kernels):
+        layer_traffic = sum(prof[n_]["traffic_bytes"] * kernels[n_]["launches"] / steps for n_ in attn_kernels)
 
     # edge-builder figures: RW pool edges = valid hop entries (d == 1, or the walk moved at step d)
     n_walks = n_rows * cfg["P"]
@@ -461,14 +495,22 @@ def run(config, steps, warmup, chunk=None, item=None, with_cpu=True):
     merge_ms = sum(r["avg_ms"] for n_, r in kernels.items() if n_.startswith("real_select")) or None
     table_entries = int(tab.row_len.sum().item())
 
+    if layer_traffic is not None:
+        value = layer_traffic / (attn_ms * 1e-3) / 1e9
+        basis = (f"attention layer fwd+bwd: the L2-to-memory-fabric bytes of its kernels per layer "
+                 f"({layer_traffic / 1e9:.3f} GB: request-size counter sums per dispatch from {traffic_src}) / its "
+                 f"HIP-event time; requests the 256 MB Infinity Cache serves count too. The gather-model work rate "
+                 f"and the compulsory-byte rate are under attention.*")
+    else:
+        value = attn_gbs
+        basis = ("attention layer fwd+bwd under the gather model (every gathered row counted at full size per "
+                 "edge) / its HIP-event time: no counter profile of this configuration covers every attention "
+                 "kernel; a work rate, not HBM bandwidth")
     result = {
         "metric": METRIC,
-        "value": round(attn_gbs, 1),
+        "value": round(value, 1),
         "unit": "GB/s",
-        "value_basis": "attention layer fwd+bwd under the gather model (every gathered row counted at full size "
-                       "per edge) / its HIP-event time; a work rate, not HBM bandwidth (gathered rows "
-                       "served from the 256 MB Infinity Cache count in full); compulsory HBM bytes are under "
-                       "attention.compulsory_*",
+        "value_basis": basis,
         "n_gpus": 1,
         "steps": steps,
         "warmup": warmup,
@@ -490,6 +532,8 @@ def run(config, steps, warmup, chunk=None, item=None, with_cpu=True):
         "edge_build_ms": round(build_ms, 4),
         "attention": {
             "fwd_bwd_ms": round(attn_ms, 4),
+            "traffic_bytes": int(layer_traffic) if layer_traffic is not None else None,
+            "traffic_gbs": round(layer_traffic / (attn_ms * 1e-3) / 1e9, 1) if layer_traffic is not None else None,
             "gather_model_bytes": a_fwd + a_bwd,
             "gather_model_gbs": round(attn_gbs, 1),
             "gather_model_frac_of_hbm_peak": round(attn_gbs / HBM_PEAK_GBS, 4),

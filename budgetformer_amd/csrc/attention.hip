@@ -28,6 +28,7 @@
 // not a dense contraction, and the kernels are bound by gather bandwidth.
 #include "bf_common.h"
 
+#include <algorithm>
 #include <mutex>
 
 namespace bf {
@@ -927,6 +928,59 @@ __device__ __forceinline__ typename Elem<T>::Raw gather_row(const T* base, int64
   return NT ? Elem<T>::load_raw_nt(base + row * D + col0) : Elem<T>::load_raw(base + row * D + col0);
 }
 
+// One reverse entry's terms added to dK and dV of its kv row: d = q_t . k_s and w = dO_t . v_s (summed over
+// the head's lanes), rs = the query's {1/D', Delta/D'}, f its V-message factor, e its CSR position (read
+// only with EX == 2: bias and dbias).
+template <typename T, int EX>
+__device__ __forceinline__ void dkv_entry(float d, float w, float2 rs, const typename Elem<T>::Raw& qr,
+                                          const typename Elem<T>::Raw& gr, float f, int64_t e, const EdgeIn& ex,
+                                          float* __restrict__ dbias, const Shape& sh, const GroupPos& g,
+                                          float (&dk)[Elem<T>::kPerVec], float (&dv)[Elem<T>::kPerVec]) {
+  constexpr int V = Elem<T>::kPerVec;
+  const float apre = d * sh.inv_scale;
+  float a = fminf(fmaxf(apre, -sh.clamp), sh.clamp);
+  if (EX == 2) a += edge_bias(ex, e, sh, g.head);
+  const float p = __expf(a);   // a is clamped to [-5, 5] (+ bias): exp2-based form is within 2 ulp
+  const float gb = fmaf(f * w, rs.x, -rs.y) * p;   // rs = {1/D', Delta/D'}
+  if (EX == 2 && dbias && g.lead) dbias[e * sh.H + g.head] = gb;
+  const float gs = (apre >= -sh.clamp && apre <= sh.clamp) ? gb * sh.inv_scale : 0.f;
+  const float pf = p * f * rs.x;
+  float qq[V], gg[V];
+  Elem<T>::unpack(qr, qq);
+  Elem<T>::unpack(gr, gg);
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    dv[i] = fmaf(pf, gg[i], dv[i]);
+    dk[i] = fmaf(gs, qq[i], dk[i]);
+  }
+}
+
+// The Graphormer token row's entry of kv row s (1 <= s <= the token row's length): the first of s's
+// reverse entries, query 0 at slot s - 1 (CSR position s - 1, since the token row lists kv 1, 2, ...
+// in order from position 0). Its q and dO rows and row stats come from the workgroup's LDS copy (tok),
+// written once, instead of being gathered again for every kv row; the terms are the ones dkv_segment
+// adds for the same entry.
+template <typename T, int EX>
+__device__ __forceinline__ void dkv_token_entry(const unsigned char* tok, int64_t s, const EdgeIn& ex,
+                                                float* __restrict__ dbias, const Shape& sh, const GroupPos& g,
+                                                const typename Elem<T>::Raw& krow,
+                                                const typename Elem<T>::Raw& vrow,
+                                                float (&dk)[Elem<T>::kPerVec], float (&dv)[Elem<T>::kPerVec]) {
+  using Raw = typename Elem<T>::Raw;
+  const int col = gather_col(g);
+  const Raw qr = *reinterpret_cast<const Raw*>(tok + col * sizeof(T));
+  const Raw gr = *reinterpret_cast<const Raw*>(tok + (sh.D + col) * sizeof(T));
+  const float2 rs = reinterpret_cast<const float2*>(tok + 2 * sh.D * sizeof(T))[g.head];
+  float d = Elem<T>::dot(qr, krow, 0.f), w = Elem<T>::dot(gr, vrow, 0.f);
+  for (int o = 1; o < (1 << sh.lph_log2); o <<= 1) {
+    d += __shfl_xor(d, o, 64);
+    w += __shfl_xor(w, o, 64);
+  }
+  const int64_t e = s - 1;
+  const float f = EX ? edge_factor<EX>(ex, e, 0, int32_t(s - 1), sh, g.head) : 1.f;
+  dkv_entry<T, EX>(d, w, rs, qr, gr, f, e, ex, dbias, sh, g, dk, dv);
+}
+
 // dK and dV of one kv row over its reverse entries [beg, end); with dbias, each
 // entry's g_b = (f w - Delta/D') p at its CSR position (the row stats carry the
 // exact Delta/D' the dq pass summed). EX: the per-entry inputs compiled in
@@ -991,23 +1045,8 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
     for (int u = 0; u < kUnroll; ++u) {
       if (!ok[u]) continue;
       const int64_t e = EX == 2 ? int64_t(epos[u]) : 0;
-      const float apre = d[u] * sh.inv_scale;
-      float a = fminf(fmaxf(apre, -sh.clamp), sh.clamp);
-      if (EX == 2) a += edge_bias(ex, e, sh, g.head);
-      const float p = __expf(a);   // a is clamped to [-5, 5] (+ bias): exp2-based form is within 2 ulp
       const float f = EX ? iter_factor<kUnroll, EX>(ex, drop, u, e, sh, g.head) : 1.f;
-      const float gb = fmaf(f * w[u], rs[u].x, -rs[u].y) * p;   // rs = {1/D', Delta/D'}
-      if (EX == 2 && dbias && g.lead) dbias[e * sh.H + g.head] = gb;
-      const float gs = (apre >= -sh.clamp && apre <= sh.clamp) ? gb * sh.inv_scale : 0.f;
-      const float pf = p * f * rs[u].x;
-      float qq[V], gg[V];
-      Elem<T>::unpack(qr[u], qq);
-      Elem<T>::unpack(gr[u], gg);
-#pragma unroll
-      for (int i = 0; i < V; ++i) {
-        dv[i] = fmaf(pf, gg[i], dv[i]);
-        dk[i] = fmaf(gs, qq[i], dk[i]);
-      }
+      dkv_entry<T, EX>(d[u], w[u], rs[u], qr[u], gr[u], f, e, ex, dbias, sh, g, dk, dv);
     }
   }
 }
@@ -1024,7 +1063,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
     const float2* __restrict__ rstat, T* __restrict__ dk, T* __restrict__ dv, const int32_t* __restrict__ order,
     const uint64_t* __restrict__ spans, Items kit, int k_items_arg, int64_t n_kv, Shape sh, int chunk,
     int rows_per_group, const float* __restrict__ token_rec, int q_items_arg, int64_t q_row_blocks,
-    const int32_t* __restrict__ plan_counts) {
+    int tok_row, const int32_t* __restrict__ plan_counts) {
   constexpr int V = Elem<T>::kPerVec;
   extern __shared__ float lds[];
   const GroupPos g = group_pos<T>(sh);
@@ -1067,6 +1106,22 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
       store_record<V>(kit, item, sh, g, ak, av, true, z, false);
     }
     return;
+  }
+  // With the Graphormer token row (query 0 attends kv 1, 2, ..., tok_len in order) every kv row s in
+  // [1, tok_len] opens with query 0's entry: its q and dO rows and row stats are staged in LDS once per
+  // workgroup instead of being gathered again for each such row.
+  int64_t tok_len = 0;
+  const unsigned char* tok = nullptr;
+  if (tok_row) {                 // uniform over the launch
+    unsigned char* buf = reinterpret_cast<unsigned char*>(lds);
+    if (threadIdx.x < (1u << sh.lpr_log2) && g.act) {
+      *reinterpret_cast<typename Elem<T>::Raw*>(buf + g.col0 * sizeof(T)) = Elem<T>::load_raw(q + g.col0);
+      *reinterpret_cast<typename Elem<T>::Raw*>(buf + (sh.D + g.col0) * sizeof(T)) = Elem<T>::load_raw(dout + g.col0);
+      if (g.lead) reinterpret_cast<float2*>(buf + 2 * sh.D * sizeof(T))[g.head] = rstat[g.head];
+    }
+    tok_len = qptr[1] - qptr[0];
+    __syncthreads();
+    tok = buf;
   }
   // each group takes rows_per_group consecutive rows of the order (similar lengths)
   const int64_t first = row_slot(sh, unsigned(k_items_arg)) * rows_per_group;
@@ -1125,6 +1180,10 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_kernel(
 #pragma unroll
     for (int i = 0; i < V; ++i) ak[i] = av[i] = 0.f;
     const typename Elem<T>::Raw kr = load_row_raw(k, row, sh.D, g), vr = load_row_raw(v, row, sh.D, g);
+    if (tok && row >= 1 && row <= tok_len) {   // the token row's entry first, from LDS
+      dkv_token_entry<T, EX>(tok, row, ex, dbias, sh, g, kr, vr, ak, av);
+      ++beg;
+    }
     dkv_segment<T, NT, EX>(q, dout, kq, ks, qptr, ex, dbias, rstat, beg, end, sh, g, kr, vr, ak, av);
     if (g.act) {                  // written once, not read again in the pass: past the caches
       Elem<T>::store_nt(dk + row * sh.D + g.col0, ak);
@@ -1342,14 +1401,20 @@ int bwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
   const int rows_per_group = kv_rows_per_group(idx->n_kv, sizeof(T));
   const int64_t kv_blocks = int64_t(idx->k_items) + grid_for(ceil_div(idx->n_kv, rows_per_group), sh);
   if (kv_blocks > 0) {
-    const size_t lds = idx->k_items > 0 ? combine_lds_bytes(sh) : 0;
+    // the token row's entries of the short kv rows take query 0's rows and stats from LDS, where a
+    // workgroup's copy serves enough rows to pay for its wait (several rows per group: c5 dk/dv pass
+    // 45.6 -> 44.6 ms); with one row per group the copy costs more than the gathers it spares (the
+    // rows then gather query 0's entry like any other: c2 dk/dv pass 0.199 -> 0.205 ms with the copy)
+    const int tok_row = idx->token_column == 1 && idx->n_q > 0 && rows_per_group > 1 ? 1 : 0;
+    const size_t tok_lds = tok_row ? size_t(2 * sh.D) * sizeof(T) + size_t(sh.H) * sizeof(float2) : 0;
+    const size_t lds = std::max(idx->k_items > 0 ? combine_lds_bytes(sh) : size_t(0), tok_lds);
     const bool stream_rows = size_t(idx->n_q) * size_t(sh.D) * sizeof(T) * 2 > kStreamBytes;
     const int mode = edge_mode(ex, dbias != nullptr);
 #define BF_LAUNCH_KV1(NT, PRE, EX)                                                                                 \
   BF_LAUNCH("attn_bwd_kv_kernel", (attn_bwd_kv_kernel<T, NT, PRE, EX>), dim3(unsigned(kv_blocks)), dim3(kBlock), lds, st, \
             Q, K, Vv, idx->kptr, idx->kq, idx->ks, idx->qptr, ex, dbias, dO, rstat, static_cast<T*>(dk),            \
             static_cast<T*>(dv), idx->k_order, idx->k_spans, kit, idx->k_items, idx->n_kv, sh, idx->chunk,           \
-            rows_per_group, token_rec, idx->q_items, int64_t(grid_for(idx->n_q, sh)), idx->plan_counts)
+            rows_per_group, token_rec, idx->q_items, int64_t(grid_for(idx->n_q, sh)), tok_row, idx->plan_counts)
 #define BF_LAUNCH_KV(NT, PRE)           \
   do {                                  \
     if (mode == 2)                      \

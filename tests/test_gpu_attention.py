@@ -39,12 +39,12 @@ def _oracle(q, k, v, ei, dout, bias_e=None, factor_e=None):
     return out, Z, dq, dk, dv, db
 
 
-def _run(dev, q, k, v, idx, dout, bias_e=None, factor_e=None):
+def _run(dev, q, k, v, idx, dout, bias_e=None, factor_e=None, dropout=None):
     from budgetformer_amd.attention import sparse_edge_attention
     qd, kd, vd = (t.to(dev).requires_grad_(True) for t in (q, k, v))
     bd = None if bias_e is None else bias_e.to(dev).float().requires_grad_(True)
     fd = None if factor_e is None else factor_e.to(dev).float()
-    out = sparse_edge_attention(qd, kd, vd, idx, bd, fd)
+    out = sparse_edge_attention(qd, kd, vd, idx, bd, fd, dropout)
     out.backward(dout.to(dev))
     torch.cuda.synchronize()
     return out, qd.grad, kd.grad, vd.grad, (bd.grad if bd is not None else None)
@@ -159,18 +159,26 @@ def test_table_index_plain_then_bias_backward(hip_device, token):
         assert _rel_err(got, ref) < 1e-5
 
 
-@pytest.mark.parametrize("dtype,chunk,item,n", [(torch.float32, 128, 768, 3000), (torch.float32, 5, 7, 400),
-                                                 (torch.bfloat16, 16, 24, 1500), (torch.float32, 128, 768, 60)])
-def test_token_column_terms_summed_by_the_dq_pass(hip_device, dtype, chunk, item, n):
+@pytest.mark.parametrize("dtype,chunk,item,n,rate", [(torch.float32, 128, 768, 3000, 0.0),
+                                                      (torch.float32, 5, 7, 400, 0.0),
+                                                      (torch.bfloat16, 16, 24, 1500, 0.0),
+                                                      (torch.float32, 128, 768, 60, 0.0),
+                                                      (torch.bfloat16, 16, 24, 1500, 0.5),
+                                                      (torch.float32, 5, 7, 400, 0.3)])
+def test_token_column_terms_summed_by_the_dq_pass(hip_device, dtype, chunk, item, n, rate):
     """With a token column (key 0 first in every row t >= 1, as the table fill lays it out) the dq pass
     sums key 0's dK/dV terms per workgroup and the dk/dv pass reduces those records instead of gathering
-    each query's q, dO and row stats again. Against the gathering pass on the same index: out, dq, dbias
-    and every other key row equal bit for bit (the same arithmetic), key 0 within the parity bar
-    (another summation order); both against the oracle. (chunk, item) = (5, 7) also splits the query
-    rows, so key 0 opens item 0 of a split row; n = 60 leaves the token column shorter than `chunk`,
-    one group then sums every record. A third run leaves the split plans' counts on the device."""
+    each query's q, dO and row stats again; and the token row (query 0, attending kv 1..n in order) opens
+    every other key row's reverse entries, whose dk/dv terms then take query 0's q, dO and row stats from
+    the workgroup's LDS copy instead of gathering them per key row. Against the gathering pass on the
+    same index (no token promise): out, dq, dbias and every other key row equal bit for bit (the same
+    arithmetic), key 0 within the parity bar (another summation order); both against the oracle.
+    (chunk, item) = (5, 7) also splits the query rows, so key 0 opens item 0 of a split row; n = 60
+    leaves the token column shorter than `chunk`, one group then sums every record. A third run leaves
+    the split plans' counts on the device. rate > 0: the in-kernel dropout (keyed by query row and slot)."""
     import numpy as np
-    from budgetformer_amd.hip_ops import AttentionIndex
+    from budgetformer_amd.hip_ops import AttentionIndex, Dropout
+    from oracle import philox
     rng = np.random.default_rng(n + chunk)
     width, H, hn = 6, 8, 16
     row_len = rng.integers(0, width + 1, n).astype(np.int32)
@@ -188,7 +196,8 @@ def test_token_column_terms_summed_by_the_dq_pass(hip_device, dtype, chunk, item
         g = torch.Generator().manual_seed(9)
         bias_e = torch.randn(idx.nnz, H, generator=g) if dtype == torch.float32 else None
         factor = ((torch.rand(idx.nnz, H, generator=g) >= 0.25).float() / 0.75) if dtype == torch.float32 else None
-        runs.append(_run(hip_device, q, k, v, idx, dout, bias_e=bias_e, factor_e=factor))
+        drop = Dropout(rate, 4242, 3) if rate else None
+        runs.append(_run(hip_device, q, k, v, idx, dout, bias_e=bias_e, factor_e=factor, dropout=drop))
     (out_f, dq_f, dk_f, dv_f, db_f), (out_g, dq_g, dk_g, dv_g, db_g), on_dev = runs
     # the key plan's counts left on the device (the query plan's known from the sizes): the same result
     for a, b in zip(runs[0], on_dev):
@@ -202,7 +211,11 @@ def test_token_column_terms_summed_by_the_dq_pass(hip_device, dtype, chunk, item
     tol = 1e-5 if dtype == torch.float32 else 2e-2
     assert _rel_err(dk_f[0], dk_g[0]) < tol and _rel_err(dv_f[0], dv_g[0]) < tol
     ei_o = _coo_order(idx)
-    ro, rZ, rdq, rdk, rdv, rdb = _oracle(q, k, v, ei_o, dout, bias_e=bias_e, factor_e=factor)
+    f_all = factor
+    if rate:
+        keep = torch.from_numpy(philox.dropout_keep_csr(idx.qptr.cpu().numpy(), H, rate, 4242, 3)).float()
+        f_all = (keep if factor is None else factor * keep) / (1.0 - rate)
+    ro, rZ, rdq, rdk, rdv, rdb = _oracle(q, k, v, ei_o, dout, bias_e=bias_e, factor_e=f_all)
     for got, ref in ((out_f, ro), (dq_f, rdq), (dk_f, rdk), (dv_f, rdv)):
         assert _rel_err(got, ref) < tol
     if db_f is not None:

@@ -127,6 +127,54 @@ def test_bf16_kv_pass_c4_instance_with_dropout(hip_device, extras):
     assert abs(keep.float().mean().item() - (1 - rate)) < 0.01
 
 
+@pytest.mark.parametrize("extras", ["plain", "dropout", "bias_dbias_dropout"])
+def test_bf16_token_row_entries_from_lds_equal_the_gathering_form(hip_device, extras):
+    """With the Graphormer token row and four kv rows per lane group (c5's dk/dv instance: more than 1M kv
+    rows in bf16, q + dO above 256 MB) the dk/dv pass takes every short kv row's first entry, query 0's,
+    from a per-workgroup LDS copy of q[0], dO[0] and query 0's row stats. Against the same table's index
+    without the token promise (every entry gathered, key 0 too): out, dq and dbias equal bit for bit, and so
+    do dK and dV of every kv row but key 0 (whose terms the token form sums per dq-pass workgroup, in
+    another order: within the parity bar)."""
+    from budgetformer_amd import hip_ops
+    from budgetformer_amd.hip_ops import AttentionIndex, Dropout
+    n, width, H, hn = 1_200_000, 4, 8, 16
+    g = torch.Generator(device=hip_device).manual_seed(31)
+    row_len = torch.randint(0, width + 1, (n,), generator=g, device=hip_device, dtype=torch.int32)
+    ids = torch.randint(0, n, (n, width), generator=g, device=hip_device, dtype=torch.int32).sort(dim=1).values
+    table = torch.where(torch.arange(width, device=hip_device)[None, :] < row_len[:, None], ids,
+                        torch.full_like(ids, -1))
+    # a few hub kv rows longer than the split threshold (their first item keeps gathering query 0's entry)
+    table[:3000, 0] = 7
+    row_len[:3000] = torch.clamp(row_len[:3000], min=1)
+    S = n + 1
+    variant = hip_ops.kv_pass_variant(S, S, torch.bfloat16, H, hn)
+    assert variant == {"rows_per_group": 4, "stream_rows": True, "prefetch_slots": True}, variant
+    q, k, v, dout = (torch.empty(S, H, hn, device=hip_device, dtype=torch.bfloat16).normal_(generator=g)
+                     for _ in range(4))
+    runs = []
+    for token in (True, False):
+        idx = AttentionIndex.from_table(table, row_len, global_token=True)
+        assert idx.token_column == 1
+        idx.token_column = 1 if token else 0
+        bias = drop = None
+        if extras != "plain":
+            drop = Dropout(0.5, 1234, 2)
+        if extras == "bias_dbias_dropout":
+            bias = torch.empty(idx.nnz, H, device=hip_device).normal_(generator=torch.Generator(
+                device=hip_device).manual_seed(5))
+        out, Z = hip_ops.attn_forward(idx, q, k, v, bias=bias, dropout=drop)
+        dq, dk, dv, db = hip_ops.attn_backward(idx, q, k, v, out, Z, dout, bias=bias, need_dbias=bias is not None,
+                                               dropout=drop)
+        runs.append((out, dq, dk, dv, db))
+    torch.cuda.synchronize()
+    (out_t, dq_t, dk_t, dv_t, db_t), (out_g, dq_g, dk_g, dv_g, db_g) = runs
+    assert torch.equal(out_t, out_g) and torch.equal(dq_t, dq_g)
+    assert (db_t is None and db_g is None) or torch.equal(db_t, db_g)
+    assert torch.equal(dk_t[1:], dk_g[1:]) and torch.equal(dv_t[1:], dv_g[1:])
+    assert_close("dk[0]", dk_t[:1], dk_g[:1].float(), 2e-2)
+    assert_close("dv[0]", dv_t[:1], dv_g[:1].float(), 2e-2)
+
+
 def test_fp32_kv_pass_past_16m_rows_streaming(hip_device):
     """fp32 with four kv rows per group (17M kv rows) and non-temporal gathers (300K queries)."""
     _check_compact(hip_device, 300_000, 17_000_000, torch.float32,
