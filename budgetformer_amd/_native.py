@@ -15,7 +15,8 @@ _HEADER = os.path.join(_ROOT, "include", "budgetformer_hip.h")
 _LIB = os.path.join(_PKG, "_lib", "libbudgetformer_hip.so")
 
 BF_OK, BF_ERR_INVALID, BF_ERR_UNSUPPORTED, BF_ERR_HIP = 0, 1, 2, 3
-BF_DTYPE_F32, BF_DTYPE_BF16 = 0, 1
+BF_DTYPE_F32, BF_DTYPE_BF16, BF_DTYPE_F16 = 0, 1, 2
+ABI_VERSION = 300                   # the header's BF_ABI_VERSION this binding is written against
 BF_MAX_ITEMS_PER_ROW = 160          # items a split row is cut into at most (the header's #define) ...
 BF_LONG_ROW_FACTOR = 64             # ... unless it is longer than 160 * 64 items' worth (the header's #define)
 
@@ -150,6 +151,9 @@ def load():
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
+    if lib.bf_version() != ABI_VERSION:
+        raise RuntimeError(f"budgetformer_amd: {path} implements ABI {lib.bf_version()}, this binding expects "
+                           f"{ABI_VERSION}; rebuild it with `python -m budgetformer_amd.build`")
     _lib = lib
     return lib
 

@@ -56,6 +56,9 @@ template <> struct Unroll<float> {
 template <> struct Unroll<uint16_t> {
   static constexpr int fwd = BF_UNROLL_FWD, q = BF_UNROLL_Q, kv = BF_UNROLL_KV_BF16;
 };
+template <> struct Unroll<_Float16> {   // the same row bytes and lane mapping as bf16
+  static constexpr int fwd = BF_UNROLL_FWD, q = BF_UNROLL_Q, kv = BF_UNROLL_KV_BF16;
+};
 constexpr float kEps = 1e-6f;
 constexpr float kClamp = 5.0f;   // the reference's clamp bound, the default
 
@@ -1209,12 +1212,13 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_reduce_kernel(T* __restric
 
 // ------------------------------------------------------------------ host side
 int make_shape(int32_t dtype, int32_t H, int32_t hn, Shape& sh) {
-  BF_CHECK_ARG(dtype == BF_DTYPE_F32 || dtype == BF_DTYPE_BF16, "attention: unknown dtype %d", dtype);
+  BF_CHECK_ARG(dtype == BF_DTYPE_F32 || dtype == BF_DTYPE_BF16 || dtype == BF_DTYPE_F16,
+               "attention: unknown dtype %d", dtype);
   BF_CHECK_ARG(H > 0 && hn > 0, "attention: num_heads=%d head_dim=%d must be positive", H, hn);
   const int V = dtype == BF_DTYPE_F32 ? Elem<float>::kPerVec : Elem<uint16_t>::kPerVec;
   if (hn % V != 0 || !is_pow2(hn / V)) {
     set_error("attention: head_dim %d unsupported for %s (needs head_dim/%d a power of two)", hn,
-              dtype == BF_DTYPE_F32 ? "float32" : "bfloat16", V);
+              dtype == BF_DTYPE_F32 ? "float32" : dtype == BF_DTYPE_BF16 ? "bfloat16" : "float16", V);
     return BF_ERR_UNSUPPORTED;
   }
   const int D = H * hn;
@@ -1481,7 +1485,7 @@ extern "C" int bf_attn_bwd_kv_variant(const bf_attn_index* idx, int32_t dtype, i
   if (rc) return rc;
   BF_CHECK_ARG(idx && idx->n_q >= 0 && idx->n_kv >= 0, "attn_bwd_kv_variant: bad index");
   BF_CHECK_ARG(rows_per_group && stream_rows && prefetch_slots, "attn_bwd_kv_variant: null output");
-  const size_t s = dtype == BF_DTYPE_F32 ? sizeof(float) : sizeof(uint16_t);
+  const size_t s = dtype == BF_DTYPE_F32 ? sizeof(float) : sizeof(uint16_t);   // bf16 and fp16: 2 bytes
   const int rpg = kv_rows_per_group(idx->n_kv, s);
   *rows_per_group = rpg;
   *stream_rows = size_t(idx->n_q) * size_t(sh.D) * s * 2 > kStreamBytes ? 1 : 0;
@@ -1505,6 +1509,8 @@ extern "C" int bf_attn_fwd(const bf_attn_index* idx, int32_t dtype, int32_t num_
   BF_CHECK_ARG(idx->q_items == 0 || partials, "attn_fwd: partials buffer required for split rows");
   if (dtype == BF_DTYPE_F32)
     return fwd_impl<float>(idx, sh, q, k, v, ex, out, Z, partials, as_stream(stream));
+  if (dtype == BF_DTYPE_F16)
+    return fwd_impl<_Float16>(idx, sh, q, k, v, ex, out, Z, partials, as_stream(stream));
   return fwd_impl<uint16_t>(idx, sh, q, k, v, ex, out, Z, partials, as_stream(stream));
 }
 
@@ -1531,6 +1537,9 @@ extern "C" int bf_attn_bwd(const bf_attn_index* idx, int32_t dtype, int32_t num_
   if (dtype == BF_DTYPE_F32)
     return bwd_impl<float>(idx, sh, q, k, v, ex, Z, dout, dq, dk, dv, dbias, rowstat, partials,
                            as_stream(stream));
+  if (dtype == BF_DTYPE_F16)
+    return bwd_impl<_Float16>(idx, sh, q, k, v, ex, Z, dout, dq, dk, dv, dbias, rowstat, partials,
+                              as_stream(stream));
   return bwd_impl<uint16_t>(idx, sh, q, k, v, ex, Z, dout, dq, dk, dv, dbias, rowstat, partials,
                             as_stream(stream));
 }

@@ -189,6 +189,55 @@ template <> struct Elem<uint16_t> {
   }
 };
 
+// IEEE fp16 activations (the reference's fp16 autocast: utils/parser_node_level.py:266-272). Products of
+// two fp16 values are exact in fp32, so v_dot2_f32_f16 with an fp32 accumulator forms the same sums the
+// fp32 path forms; results are rounded to fp16 (round to nearest even) only when stored.
+template <> struct Elem<_Float16> {
+  static constexpr int kPerVec = 8;
+  using Raw = uint4;
+  typedef _Float16 Pair __attribute__((ext_vector_type(2)));
+  __device__ __forceinline__ static Pair as_pair(uint32_t w) { return __builtin_bit_cast(Pair, w); }
+  __device__ __forceinline__ static uint32_t pack(float a, float b) {
+    const Pair p = {_Float16(a), _Float16(b)};
+    return __builtin_bit_cast(uint32_t, p);
+  }
+  __device__ __forceinline__ static Raw load_raw(const _Float16* p) { return *reinterpret_cast<const uint4*>(p); }
+  __device__ __forceinline__ static Raw load_raw_nt(const _Float16* p) {
+    typedef unsigned V4 __attribute__((ext_vector_type(4)));
+    const V4 v = __builtin_nontemporal_load(reinterpret_cast<const V4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+  }
+  __device__ __forceinline__ static Raw zero_raw() { return make_uint4(0u, 0u, 0u, 0u); }
+  __device__ __forceinline__ static float dot(const Raw& a, const Raw& b, float acc) {
+    acc = __builtin_amdgcn_fdot2(as_pair(a.x), as_pair(b.x), acc, false);
+    acc = __builtin_amdgcn_fdot2(as_pair(a.y), as_pair(b.y), acc, false);
+    acc = __builtin_amdgcn_fdot2(as_pair(a.z), as_pair(b.z), acc, false);
+    return __builtin_amdgcn_fdot2(as_pair(a.w), as_pair(b.w), acc, false);
+  }
+  __device__ __forceinline__ static void unpack(const Raw& v, float (&o)[8]) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const Pair p = as_pair(w[i]);
+      o[2 * i] = float(p.x);
+      o[2 * i + 1] = float(p.y);
+    }
+  }
+  __device__ __forceinline__ static void load(const _Float16* p, float (&o)[8]) { unpack(load_raw(p), o); }
+  __device__ __forceinline__ static void store(_Float16* p, const float (&o)[8]) {
+    *reinterpret_cast<uint4*>(p) = make_uint4(pack(o[0], o[1]), pack(o[2], o[3]), pack(o[4], o[5]), pack(o[6], o[7]));
+  }
+  __device__ __forceinline__ static void store_nt(_Float16* p, const float (&o)[8]) {
+    typedef unsigned V4 __attribute__((ext_vector_type(4)));
+    V4 w;
+    w.x = pack(o[0], o[1]);
+    w.y = pack(o[2], o[3]);
+    w.z = pack(o[4], o[5]);
+    w.w = pack(o[6], o[7]);
+    __builtin_nontemporal_store(w, reinterpret_cast<V4*>(p));
+  }
+};
+
 // 16 zero bytes at p (16-byte aligned) by a non-temporal vector store: rows
 // written once and not read again in the pass do not displace cached data.
 __device__ __forceinline__ void store_zero16_nt(void* p) {

@@ -92,7 +92,7 @@ void prof_end(int token, hipStream_t st) {
 
 using namespace bf;
 
-extern "C" int bf_version(void) { return 100; }
+extern "C" int bf_version(void) { return BF_ABI_VERSION; }
 
 extern "C" const char* bf_last_error(void) { return bf::g_error; }
 

@@ -97,8 +97,9 @@ bf_attn_index make_index(const c10::List<std::optional<at::Tensor>>& t, at::IntA
 
 int32_t dtype_code(const at::Tensor& q) {
   if (q.scalar_type() == at::kFloat) return BF_DTYPE_F32;
-  TORCH_CHECK_VALUE(q.scalar_type() == at::kBFloat16, "attention supports float32 and bfloat16 activations (got ",
-                    q.scalar_type(), ")");
+  if (q.scalar_type() == at::kHalf) return BF_DTYPE_F16;
+  TORCH_CHECK_VALUE(q.scalar_type() == at::kBFloat16,
+                    "attention supports float32, bfloat16 and float16 activations (got ", q.scalar_type(), ")");
   return BF_DTYPE_BF16;
 }
 

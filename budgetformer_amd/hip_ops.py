@@ -1089,7 +1089,7 @@ class AttentionIndex:
 
 
 # ------------------------------------------------------------------ attention
-_DT = {torch.float32: N.BF_DTYPE_F32, torch.bfloat16: N.BF_DTYPE_BF16}
+_DT = {torch.float32: N.BF_DTYPE_F32, torch.bfloat16: N.BF_DTYPE_BF16, torch.float16: N.BF_DTYPE_F16}
 
 
 @dataclass(frozen=True)

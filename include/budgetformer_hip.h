@@ -33,9 +33,25 @@ enum {
   BF_ERR_HIP = 3           /* a HIP runtime call or kernel launch failed   */
 };
 
-enum { BF_DTYPE_F32 = 0, BF_DTYPE_BF16 = 1 };
+/* Activation dtypes of the attention entry points: float32, bfloat16 and IEEE
+ * float16 (the reference's bf16 / fp16 autocast, utils/parser_node_level.py:
+ * 266-272; utils/fullgraph_sp_support.py:350-360, 440). Every dtype
+ * accumulates in float32.                                                    */
+enum { BF_DTYPE_F32 = 0, BF_DTYPE_BF16 = 1, BF_DTYPE_F16 = 2 };
 
-/* Library version (major*10000 + minor*100 + patch). */
+/* ABI version (major*10000 + minor*100 + patch), returned by bf_version(). A
+ * binding checks it for equality: any change to an entry point's arguments,
+ * to a struct's fields or to their meaning bumps it. History (each version's
+ * changes are listed in INTEGRATION.md):
+ *   100  first ABI;
+ *   200  bf_attn_fwd / bf_attn_bwd take score_clamp and a dropout; bf_attn_bwd
+ *        no longer takes `out`; bf_reverse_slots replaces bf_reverse_entries;
+ *        bf_attn_index's fifth pointer (ks) holds each reverse entry's slot in
+ *        its query's row instead of its CSR position;
+ *   300  BF_DTYPE_F16 (float16 activations); the in-kernel dropout is keyed by
+ *        (query row, slot) instead of the CSR position (a new mask for the same
+ *        seed and offset).                                                   */
+#define BF_ABI_VERSION 300
 int bf_version(void);
 /* Message of the last failed call on this thread ("" if none). */
 const char* bf_last_error(void);

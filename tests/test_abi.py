@@ -15,7 +15,11 @@ def test_library_loads_and_exports_every_header_symbol():
     for name in names:
         assert hasattr(lib, name), name
         assert name in N._SIGS, f"{name} has no ctypes signature"
-    assert lib.bf_version() >= 100
+    # the exact ABI version the header declares: a binding written against another one must not load
+    import re
+    declared = int(re.search(r"#define BF_ABI_VERSION (\d+)", open(N._HEADER).read()).group(1))
+    assert declared == 300 == N.ABI_VERSION
+    assert lib.bf_version() == declared
 
 
 def test_every_entry_point_cites_the_reference():
