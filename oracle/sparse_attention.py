@@ -139,7 +139,12 @@ def graphormer_head_group_attention(k, q, v, edge_list, attn_bias=None):
     """models/graphormer_dist_node_level.py:175-213: a list of G edge sets, group g serving heads
     [g*ceil(H/G), min((g+1)*ceil(H/G), H)); a None or empty set leaves its heads zero, and so does a
     group whose head range is empty. Each group's heads follow the single-set arithmetic
-    (clamp of q.k/sqrt(hn), bias of those heads after the clamp). attn_bias: dense [S, S, H] or None."""
+    (clamp of q.k/sqrt(hn), bias of those heads after the clamp). attn_bias: dense [S, S, H] or None.
+
+    Deliberate divergence with a bias: the reference adds attn_bias[src, dst, h0:h1], shape [E, h], to a
+    score of shape [E, h, 1] (:200-205), which broadcasts to [E, E, h] or raises; this restatement adds
+    each entry's bias to its own heads (the `.unsqueeze(-1)` below), the evident intent. Tests of the
+    list form with a bias pin that intent, not the reference's result."""
     num_heads, hn = q.size(1), q.size(2)
     scale = math.sqrt(hn)
     groups = max(1, len(edge_list))
