@@ -367,7 +367,9 @@ def run(config, steps, warmup, chunk=None, item=None, with_cpu=True):
     # the CSR itself: timed here, outside the per-step build
     r0, r1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     r0.record()
-    walk_rec = g.walk_records() if cfg["b_w"] > 0 else None
+    from budgetformer_amd.gt_sp.utils import estimate_hot_path_bytes
+    reserve = estimate_hot_path_bytes(n, g.num_edges, n_rows, cfg["b_r"], cfg["b_w"], global_token=cfg["token"])
+    walk_rec = g.walk_records(reserve_bytes=reserve["peak"]) if cfg["b_w"] > 0 else None
     r1.record()
     torch.cuda.synchronize()
     rec_ms = round(r0.elapsed_time(r1), 4) if walk_rec is not None else None

@@ -7,6 +7,11 @@
 // keyed by the seed, counter = draw index), self pairs dropped, unordered pairs
 // deduplicated by radix sort, trimmed to exactly `pairs` by a hash order, then
 // symmetrised into a coalesced CSR (int64 rowptr, int32 col).
+//
+// The weights' sum and prefix sums are taken in 64-bit fixed point: integer
+// sums do not depend on the order a parallel scan adds them in (a
+// floating-point look-back scan rounds differently from run to run), so a
+// seed always gives the same graph.
 #include "bf_common.h"
 #include "bf_prim.h"
 
@@ -25,21 +30,27 @@ int bits_for(uint64_t maxval) {
   return b;
 }
 
-__global__ void weights_kernel(int64_t n, double i0, double expo, double* __restrict__ w) {
+// Fixed-point scales: raw weights (each at most i0^(-1/(exponent-1)) <= 1) in units of 2^-36, so that the
+// sum of up to 2^31 of them stays below 2^63; scaled weights (expected degrees, summing to 2*pairs < 2^31)
+// in units of 2^-24.
+constexpr double kRawScale = 68719476736.0;     // 2^36
+constexpr double kCdfScale = 16777216.0;        // 2^24
+
+__global__ void weights_kernel(int64_t n, double i0, double expo, uint64_t* __restrict__ w) {
   const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
-  if (i < n) w[i] = pow(double(i) + i0, -1.0 / (expo - 1.0));
+  if (i < n) w[i] = uint64_t(llrint(pow(double(i) + i0, -1.0 / (expo - 1.0)) * kRawScale));
 }
 
-__global__ void scale_cap_kernel(int64_t n, const double* __restrict__ raw_sum, double target, double cap,
-                                 double* __restrict__ w) {
+__global__ void scale_cap_kernel(int64_t n, const uint64_t* __restrict__ raw_sum, double target, double cap,
+                                 uint64_t* __restrict__ w) {
   const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
   if (i >= n) return;
-  double x = w[i] * (target / *raw_sum);
+  double x = double(w[i]) * (target / double(*raw_sum));
   if (cap > 0.0 && x > cap) x = cap;
-  w[i] = x;
+  w[i] = uint64_t(llrint(x * kCdfScale));
 }
 
-__device__ __forceinline__ int64_t inverse_cdf(const double* __restrict__ cdf, int64_t n, double x) {
+__device__ __forceinline__ int64_t inverse_cdf(const uint64_t* __restrict__ cdf, int64_t n, uint64_t x) {
   int64_t lo = 0, hi = n - 1;  // first i with cdf[i] > x
   while (lo < hi) {
     const int64_t mid = (lo + hi) >> 1;
@@ -52,16 +63,17 @@ __device__ __forceinline__ double u53(uint32_t a, uint32_t b) {
   return (double(a >> 5) * 67108864.0 + double(b >> 6)) * (1.0 / 9007199254740992.0);
 }
 
-__global__ void draw_pairs_kernel(const double* __restrict__ cdf, int64_t n, int64_t draws, uint64_t seed,
+__global__ void draw_pairs_kernel(const uint64_t* __restrict__ cdf, int64_t n, int64_t draws, uint64_t seed,
                                   uint64_t counter_base, uint64_t* __restrict__ keys) {
   const int64_t j = int64_t(blockIdx.x) * kThreads + threadIdx.x;
   if (j >= draws) return;
   const uint64_t c = counter_base + uint64_t(j);
   const U32x4 r = philox4x32_10(U32x4{uint32_t(c), uint32_t(c >> 32), 0x5eed5eedu, 0u}, uint32_t(seed),
                                 uint32_t(seed >> 32));
-  const double total = cdf[n - 1];
-  const int64_t a = inverse_cdf(cdf, n, u53(r.x, r.y) * total);
-  const int64_t b = inverse_cdf(cdf, n, u53(r.z, r.w) * total);
+  const double total = double(cdf[n - 1]);
+  // u in [0, 1): the point lies below the total (u * total rounds to at most total - 1 below 2^53)
+  const int64_t a = inverse_cdf(cdf, n, uint64_t(u53(r.x, r.y) * total));
+  const int64_t b = inverse_cdf(cdf, n, uint64_t(u53(r.z, r.w) * total));
   if (a == b) {
     keys[j] = kNone;
     return;
@@ -127,9 +139,9 @@ extern "C" int bf_chung_lu_workspace_size(int64_t num_nodes, int64_t pairs, size
                         slab_n, 0, 64, none);
   (void)prim::sort_pairs(nullptr, sort2_bytes, static_cast<const uint64_t*>(nullptr), static_cast<uint64_t*>(nullptr),
                          static_cast<const uint64_t*>(nullptr), static_cast<uint64_t*>(nullptr), draws, 0, 64, none);
-  (void)prim::inclusive_sum(nullptr, scan_bytes, static_cast<const double*>(nullptr), static_cast<double*>(nullptr),
-                            num_nodes, none);
-  (void)prim::reduce_sum(nullptr, red_bytes, static_cast<const double*>(nullptr), static_cast<double*>(nullptr),
+  (void)prim::inclusive_sum(nullptr, scan_bytes, static_cast<const uint64_t*>(nullptr),
+                            static_cast<uint64_t*>(nullptr), num_nodes, none);
+  (void)prim::reduce_sum(nullptr, red_bytes, static_cast<const uint64_t*>(nullptr), static_cast<uint64_t*>(nullptr),
                          num_nodes, none);
   size_t temp = sort_bytes;
   for (size_t t : {sort2_bytes, scan_bytes, red_bytes, sel_bytes}) temp = t > temp ? t : temp;
@@ -146,6 +158,9 @@ extern "C" int bf_chung_lu(int64_t num_nodes, int64_t pairs, double exponent, do
   BF_CHECK_ARG(rowptr && col && num_edges_host, "chung_lu: null output");
   BF_CHECK_ARG(2 * pairs < (int64_t(1) << 31), "chung_lu: 2*pairs must fit int32 item counts");
   BF_CHECK_ARG(uint64_t(pairs) <= uint64_t(num_nodes) * uint64_t(num_nodes - 1) / 2, "chung_lu: too many pairs");
+  // the raw weights' fixed-point sum (2^-36 units) stays below 2^63: num_nodes times node 0's weight < 2^27
+  BF_CHECK_ARG(double(num_nodes) * pow(i0, -1.0 / (exponent - 1.0)) < 134217728.0,
+               "chung_lu: weights too large for the fixed-point sum (raise i0 or the exponent)");
   size_t need = 0;
   bf_chung_lu_workspace_size(num_nodes, pairs, &need);
   BF_CHECK_ARG(workspace && workspace_bytes >= need, "chung_lu: workspace %zu < %zu bytes", workspace_bytes, need);
@@ -158,8 +173,8 @@ extern "C" int bf_chung_lu(int64_t num_nodes, int64_t pairs, double exponent, do
   auto* keys_b = reinterpret_cast<uint64_t*>(take(size_t(slab_n) * 8));
   auto* keys_c = reinterpret_cast<uint64_t*>(take(size_t(slab_n) * 8));
   auto* keys_d = reinterpret_cast<uint64_t*>(take(size_t(slab_n) * 8));
-  auto* cdf = reinterpret_cast<double*>(take(size_t(num_nodes) * 8));
-  auto* dsum = reinterpret_cast<double*>(take(size_t(num_nodes) * 8));
+  auto* cdf = reinterpret_cast<uint64_t*>(take(size_t(num_nodes) * 8));
+  auto* dsum = reinterpret_cast<uint64_t*>(take(size_t(num_nodes) * 8));
   auto* flags = reinterpret_cast<int32_t*>(take(size_t(draws) * 4));
   void* temp = p;
   size_t temp_bytes = workspace_bytes - size_t(p - static_cast<char*>(workspace));
@@ -171,12 +186,12 @@ extern "C" int bf_chung_lu(int64_t num_nodes, int64_t pairs, double exponent, do
             exponent, dsum);
   BF_CHECK_LAUNCH();
   size_t tb = temp_bytes;
-  BF_CHECK_HIP(prim::reduce_sum(temp, tb, static_cast<const double*>(dsum), cdf, num_nodes, st));
+  BF_CHECK_HIP(prim::reduce_sum(temp, tb, static_cast<const uint64_t*>(dsum), cdf, num_nodes, st));
   BF_LAUNCH("scale_cap_kernel", scale_cap_kernel, dim3(blocks_for(num_nodes)), dim3(kThreads), 0, st, num_nodes, cdf,
             double(2 * pairs), max_degree, dsum);
   BF_CHECK_LAUNCH();
   tb = temp_bytes;
-  BF_CHECK_HIP(prim::inclusive_sum(temp, tb, static_cast<const double*>(dsum), cdf, num_nodes, st));
+  BF_CHECK_HIP(prim::inclusive_sum(temp, tb, static_cast<const uint64_t*>(dsum), cdf, num_nodes, st));
 
   // draw, sort, count unique; redraw into the tail until enough unique pairs exist
   int64_t have = 0;           // unique keys at the front of keys_a (sorted)

@@ -23,7 +23,7 @@ import torch
 
 from . import hip_ops
 from .graph import CSRGraph
-from .gt_sp.utils import plan_edge_build
+from .gt_sp.utils import estimate_edge_build_bytes, estimate_hot_path_bytes, plan_edge_build
 from .hip_ops import AttentionIndex
 
 REAL_SEED_OFFSET = 17   # utils/fullgraph_sp_support.py:1413
@@ -130,12 +130,18 @@ def build_attention_edges(graph: CSRGraph, *, real_edges_per_query: int, rw_edge
     walk_length = max(1, int(walk_length))
     P = max(int(walks_per_node), 1)
     seed = int(edge_seed if philox_seed is None else philox_seed)
-    plan = plan_edge_build(graph.device, n_q, b_r, b_w, q_lo=q_lo, usable_bytes=usable_bytes)
     all_hubs = graph.hubs() if b_r > 0 else None
     # queries above LIGHT_MAX in-neighbours take the group path; the rest one thread each (k <= 16)
     light = b_r > 0 and b_r <= 16 and b_w <= 16
     all_heavy = graph.heavy() if light else None
-    walk_rec = graph.walk_records() if b_w > 0 else None
+    # the table's attention index follows the build: its bytes beyond the table are reserved while
+    # planning the build, and the graph's walk records are kept only where both still fit beside them
+    est = estimate_hot_path_bytes(graph.num_nodes, graph.num_edges, n_q, b_r, b_w, global_token=global_token,
+                                  holds_token_row=q_lo == 0, n_hubs=0 if all_hubs is None else all_hubs.numel())
+    table_bytes = estimate_edge_build_bytes(n_q, b_r, b_w)["output"]
+    walk_rec = graph.walk_records(reserve_bytes=est["peak"]) if b_w > 0 else None
+    plan = plan_edge_build(graph.device, n_q, b_r, b_w, q_lo=q_lo, usable_bytes=usable_bytes,
+                           reserve_bytes=est["peak"] - table_bytes)
 
     def in_range(lst, lo, cnt):
         if lst is None or lst.numel() == 0:

@@ -52,17 +52,22 @@ class CSRGraph:
             cache[threshold] = plan.heavy_rows[: plan.heavy].clone()
         return cache[threshold]
 
-    def walk_records(self) -> Optional[torch.Tensor]:
+    def walk_records(self, reserve_bytes: Optional[int] = None) -> Optional[torch.Tensor]:
         """The walk records of (rowptr, col), int32 [E, 4] (16 bytes per edge), cached: a walk step
         then reads one record instead of the rowptr pair and col. None when the graph has 2^31 edges or
-        more (the records hold 32-bit degrees), or when they would take more than a quarter of the
-        device's free memory; the walks then step through rowptr and col (the same walks)."""
+        more (the records hold 32-bit degrees), or when the records and ``reserve_bytes`` (what the
+        caller's build and index need next; by default an all-node build at B = 32 with its index,
+        ``estimate_hot_path_bytes``) do not both fit the usable HBM; the walks then step through rowptr
+        and col (the same walks). Decided once per graph."""
         if "_walk_rec" not in self.__dict__:
+            from .gt_sp.utils import _rw_gpu_usable_bytes, estimate_hot_path_bytes
             rec = None
             e = self.num_edges
-            if 0 < e < 2 ** 31:
-                free = torch.cuda.mem_get_info(self.device)[0] if self.device.type == "cuda" else 0
-                if 16 * e <= free // 4:
+            if 0 < e < 2 ** 31 and self.device.type == "cuda":
+                if reserve_bytes is None:
+                    reserve_bytes = estimate_hot_path_bytes(self.num_nodes, e, self.num_nodes, 16, 16)["peak"]
+                usable = _rw_gpu_usable_bytes(self.device)
+                if usable < 0 or 16 * e + int(reserve_bytes) <= usable:
                     rec = hip_ops.walk_records(self.rowptr, self.col)
             self.__dict__["_walk_rec"] = rec
         return self.__dict__["_walk_rec"]

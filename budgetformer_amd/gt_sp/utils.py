@@ -17,6 +17,7 @@ global walk id), so the table is bit-identical. There is no CPU path.
 """
 from __future__ import annotations
 
+import functools
 import math
 import os
 from dataclasses import dataclass
@@ -66,28 +67,135 @@ def estimate_edge_build_bytes(n_queries: int, real_edges_per_query: int, rw_edge
     return {"transient": int(transient), "output": int(output), "per_query_transient": 4 * (b_w + 1)}
 
 
-def estimate_attention_index_bytes(n_q: int, n_kv: int, nnz: int, chunk: int = 64, item: int = 512) -> int:
-    """Device bytes of an attention index: CSR, reverse index and both split plans
-    (plus the reverse-index sort workspace, the largest transient)."""
-    csr = 8 * (n_q + 1) + 4 * nnz
-    reverse = 8 * (n_kv + 1) + 8 * nnz
-    sort_ws = 3 * _align(4 * nnz) + 2 * 4 * nnz + _WS_ALIGN     # keys/values/rows slabs + radix temp
-    plans = 4 * 2 * (n_q + n_kv) + 4 * 2 * (nnz // item + nnz // chunk + 1)
-    return int(csr + reverse + sort_ws + plans)
+_ALLOC_ROUND = 512     # the caching allocator rounds every block up to a multiple of 512 bytes
+
+
+def _block(nbytes: int) -> int:
+    """Bytes the caching allocator books for a tensor of ``nbytes`` (torch.empty(max(n, 1)) included)."""
+    return max(1, -(-max(int(nbytes), 1) // _ALLOC_ROUND)) * _ALLOC_ROUND
+
+
+def _ws_size(fn_name: str, *args) -> int:
+    import ctypes as C
+    from .. import _native as N
+    out = C.c_size_t(0)
+    N.call(fn_name, *args, C.byref(out))
+    return int(out.value)
+
+
+class _LiveSet:
+    """Replays a sequence of device allocations and frees; ``peak`` is the largest live total."""
+
+    def __init__(self):
+        self.live, self.total, self.peak = {}, 0, 0
+
+    def alloc(self, name: str, nbytes: int) -> None:
+        b = _block(nbytes)
+        self.live[name] = b
+        self.total += b
+        self.peak = max(self.peak, self.total)
+
+    def free(self, *names: str) -> None:
+        for n in names:
+            self.total -= self.live.pop(n)
+
+
+@functools.lru_cache(maxsize=64)
+def estimate_hot_path_bytes(num_nodes: int, num_edges: int, n_q: int, real_edges_per_query: int,
+                            rw_edges_per_query: int, *, global_token: bool = False, holds_token_row: bool = True,
+                            nnz: int = None, entries: bool = False, n_hubs: int = 0, walk_records: bool = True,
+                            chunk: int = 128, item: int = 768) -> dict:
+    """Device bytes of one budgeted edge build and its attention index, by replaying the allocations
+    ``build_attention_edges`` and ``EdgeTable.attention_index().ensure_backward(entries)`` make, with each
+    workspace taken from the library's own size query (gt_sp/utils.py:160-236 and :1121-1165 estimate the
+    reference's walk pipeline the same way: every transient it allocates).
+
+    - ``walk_records``: the graph's walk records (16 bytes per edge), built once per graph and kept with
+      it (``CSRGraph.walk_records``); reported apart, since a graph holds them across builds;
+    - the build: the table [n_q, b_r + b_w] and row lengths, plus its workspace (the RW selection);
+    - the index: row pointers, kv ids, the reverse-index sort keys (8 bytes per table entry) and their
+      sorted copy, the sort's workspace, kptr / kq (/ ks with ``entries``), the query and key split plans,
+      the key rows' order and spans. ``nnz``: the index's entry count when known (a table's index of more
+      than 8M entries at capacity is sized exactly); None sizes it for every table row full, an upper
+      bound.
+
+    Returns the phases' peaks and ``peak`` (the largest live total over the build and the index, on top
+    of what is resident before: graph, activations) and ``resident`` (what stays allocated after:
+    table, row lengths and the index). Cached per argument set (a build asks once per call); the
+    returned dict is shared, not to be modified."""
+    from .. import _native as N
+    from ..hip_ops import NO_READBACK_MAX_ENTRIES
+    lib = N.load()
+    n_q, N_ = int(n_q), int(num_nodes)
+    b_r, b_w = max(0, int(real_edges_per_query)), max(0, int(rw_edges_per_query))
+    width = max(1, b_r + b_w)
+    tr = (N_ if holds_token_row else -1) if global_token else -1
+    n_q_tab = n_q + (1 if tr >= 0 else 0)
+    n_kv = N_ + (1 if global_token else 0)
+    n_token = (n_q + max(tr, 0)) if global_token else 0
+    bound = n_q * width + n_token
+    exact = bound > NO_READBACK_MAX_ENTRIES
+    entries_n = bound if (nnz is None or not exact) else int(nnz)
+    n_keys = max(entries_n - n_token, 0)
+    L = _LiveSet()
+    # the build (one shard)
+    L.alloc("table", 4 * n_q * width)
+    L.alloc("row_len", 4 * n_q)
+    L.alloc("build_ws", _ws_size("bf_build_edge_table_workspace_size", n_q, b_w, int(n_hubs), b_r))
+    build_peak = L.peak
+    L.free("build_ws")
+    # AttentionIndex.from_table: row pointers (scan workspace), the query plan when the sizes fix it, kv, keys
+    L.alloc("scan_ws", _ws_size("bf_scan_workspace_size", n_q_tab))
+    L.alloc("qptr", 8 * (n_q_tab + 1))
+    L.free("scan_ws")
+    L.alloc("plan_counts", 16)
+    known = width + (1 if global_token else 0) <= chunk
+    q_item_cap = int(lib.bf_split_item_capacity(bound, chunk, item))
+    q_heavy_cap = int(lib.bf_split_row_capacity(bound, chunk))
+    q_plan = 4 * (2 * max(n_q_tab, 1) + max(q_item_cap, 1) + max(q_heavy_cap, 1))
+    if known:
+        L.alloc("q_plan", q_plan)
+    L.alloc("kv", 4 * entries_n)
+    L.alloc("keys", 8 * n_keys)
+    if not known:                                  # split_plan over the capacity, with its workspace
+        L.alloc("q_plan", q_plan)
+        L.alloc("q_plan_ws", _ws_size("bf_split_plan_workspace_size", n_q_tab))
+        L.free("q_plan_ws")
+    # ensure_backward: the reverse index from the keys (one sort), then the key rows' order and plan
+    L.alloc("rev_ws", _ws_size("bf_reverse_index_packed_workspace_size", entries_n))
+    L.alloc("sorted_keys", 8 * n_keys)
+    L.alloc("kptr", 8 * (n_kv + 1))
+    L.alloc("kq", 4 * entries_n)
+    if entries:
+        L.alloc("ks", 4 * entries_n)
+    L.free("rev_ws", "keys")
+    k_item_cap = int(lib.bf_split_item_capacity(entries_n, chunk, item))
+    k_heavy_cap = int(lib.bf_split_row_capacity(entries_n, chunk))
+    L.alloc("k_order", 4 * max(n_kv, 1))
+    L.alloc("k_spans", 8 * max(n_kv, 1))
+    L.alloc("k_plan", 4 * (2 * max(n_kv, 1) + max(k_item_cap, 1) + max(k_heavy_cap, 1)))
+    L.alloc("k_plan_ws", _ws_size("bf_row_order_and_plan_workspace_size", n_kv, k_heavy_cap))
+    L.free("k_plan_ws")
+    if entries:
+        L.free("sorted_keys")     # the slots came with the unpack: the sorted keys go with the call
+    return {"walk_records": 16 * int(num_edges) if walk_records else 0,
+            "build_peak": build_peak, "peak": L.peak, "resident": L.total,
+            "entries": entries_n, "exact": exact, "live_after": dict(L.live)}
 
 
 def _estimate_rw_working_set_bytes(num_nodes: int, num_edges: int, walks_per_node: int, walk_length: int,
-                                   num_heads: int = 1) -> int:
-    """Transient bytes of an all-node fused build (gt_sp/utils.py:160-236 counterpart).
-
-    The RW budget is at most the pool size per query (P·L, the cap used by
-    _resolve_adaptive_edge_budget_config, utils/fullgraph_sp_support.py:949-952),
-    so this bounds any budget state. ``num_edges`` and ``num_heads`` do not enter:
-    the topology is read in place and heads share one edge set.
-    """
-    _ = (num_edges, num_heads)
-    b_w_max = max(1, int(walks_per_node)) * max(1, int(walk_length))
-    return estimate_edge_build_bytes(max(1, int(num_nodes)), 0, b_w_max)["transient"]
+                                   num_heads: int = 1, real_edges_per_query: int = None,
+                                   global_token: bool = False, walk_records_built: bool = False) -> int:
+    """Working set of an all-node build and its attention index (gt_sp/utils.py:160-236 counterpart): the
+    walk records when the graph has none yet, plus the peak of ``estimate_hot_path_bytes`` with every
+    table row full. The RW budget is at most the pool size per query (P·L, the cap
+    _resolve_adaptive_edge_budget_config uses, utils/fullgraph_sp_support.py:949-952), and so is the real
+    budget unless given, which bounds any budget state. Heads share one edge set."""
+    _ = num_heads
+    b_w = max(1, int(walks_per_node)) * max(1, int(walk_length))
+    b_r = b_w if real_edges_per_query is None else int(real_edges_per_query)
+    est = estimate_hot_path_bytes(num_nodes, num_edges, num_nodes, b_r, b_w, global_token=global_token)
+    return int(est["peak"] + (0 if walk_records_built else est["walk_records"]))
 
 
 def _gpu_concurrent_overhead_bytes(device) -> int:
@@ -157,28 +265,31 @@ _SMALL_BUILD_BYTES = 64 * 1024 * 1024
 
 
 def plan_edge_build(device, n_queries: int, real_edges_per_query: int, rw_edges_per_query: int, q_lo: int = 0,
-                    usable_bytes: int = None) -> EdgeBuildPlan:
-    """Shard the query range so each shard's transient fits next to the output table.
+                    usable_bytes: int = None, reserve_bytes: int = 0) -> EdgeBuildPlan:
+    """Shard the query range so each shard's transient fits next to the output table and ``reserve_bytes``
+    (what the table's attention index will need beyond the table: ``estimate_hot_path_bytes``' peak less
+    the table).
 
-    Raises torch.cuda.OutOfMemoryError when not even the output table plus a
-    one-query shard fits: there is no CPU build to fall back to.
+    Raises torch.cuda.OutOfMemoryError when not even the output table, the reserve and a one-query shard
+    fit: there is no CPU build to fall back to.
     """
     dev = torch.device(device)
     full = estimate_edge_build_bytes(n_queries, real_edges_per_query, rw_edges_per_query)
+    reserve = max(0, int(reserve_bytes))
     if usable_bytes is None and _GPU_PROCESS_MEMORY_CAP_BYTES <= 0 and \
-            full["transient"] + full["output"] <= _SMALL_BUILD_BYTES:
+            full["transient"] + full["output"] + reserve <= _SMALL_BUILD_BYTES:
         # too small to be worth sharding: one build, without querying the driver's free memory
         # (a shortfall this small surfaces as the allocator's own OutOfMemoryError)
         return EdgeBuildPlan(dev, [(q_lo, n_queries)], full["transient"], full["output"], -1)
     usable = _rw_gpu_usable_bytes(dev) if usable_bytes is None else int(usable_bytes)
-    if usable < 0 or _FORCE_RW_ON_GPU or full["transient"] + full["output"] <= usable:
+    if usable < 0 or _FORCE_RW_ON_GPU or full["transient"] + full["output"] + reserve <= usable:
         return EdgeBuildPlan(dev, [(q_lo, n_queries)], full["transient"], full["output"], usable)
-    room = usable - full["output"] - 2 * _WS_ALIGN
+    room = usable - full["output"] - reserve - 2 * _WS_ALIGN
     per_q = full["per_query_transient"]
     if room < per_q:
         raise torch.cuda.OutOfMemoryError(
-            f"edge build: the output table needs {full['output'] / 2**20:.0f} MiB and the usable HBM is "
-            f"{usable / 2**20:.0f} MiB; no query shard fits")
+            f"edge build: the output table needs {full['output'] / 2**20:.0f} MiB and its attention index "
+            f"{reserve / 2**20:.0f} MiB more, the usable HBM is {usable / 2**20:.0f} MiB; no query shard fits")
     shard = max(1, room // per_q)
     n_shards = math.ceil(n_queries / shard)
     shard = math.ceil(n_queries / n_shards)

@@ -251,6 +251,21 @@ def test_device_chung_lu_graph_properties(hip_device):
     assert torch.equal(g2.col, g.col)                                # deterministic
 
 
+def test_device_chung_lu_is_deterministic_at_scale(hip_device):
+    """A seed gives the same graph every time at the benchmark scales too: the weights' sum and prefix sums
+    are integer (fixed point), which no parallel summation order can change (a floating-point look-back
+    scan rounded differently from run to run, and 1.6B-edge graphs then differed by a few edges)."""
+    from budgetformer_amd.graph import chung_lu_device
+    n, e = 30_000_000, 200_000_000
+    g1 = chung_lu_device(n, e, exponent=2.1, seed=42, max_degree=20_000, device=hip_device)
+    c1 = g1.col.clone()
+    r1 = g1.rowptr.clone()
+    del g1
+    g2 = chung_lu_device(n, e, exponent=2.1, seed=42, max_degree=20_000, device=hip_device)
+    assert int(r1[-1].item()) == e
+    assert torch.equal(r1, g2.rowptr) and torch.equal(c1, g2.col)
+
+
 @pytest.mark.parametrize("b_r,b_w,thr", [(4, 4, 16), (8, 8, 64), (3, 0, 8), (16, 16, 32)])
 def test_hub_path_bit_exact(hip_device, b_r, b_w, thr):
     """Rows above the hub threshold take the workgroup top-k; the table must not change."""
