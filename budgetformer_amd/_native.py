@@ -120,6 +120,10 @@ _SIGS = {
                               C.POINTER(AttnDropout), vp, P_f32, P_f32, vp]),
     "bf_attn_bwd": (C.c_int, [C.POINTER(AttnIndex), i32, i32, i32, f32, vp, vp, vp, P_f32, P_f32,
                               C.POINTER(AttnDropout), P_f32, vp, vp, vp, vp, P_f32, P_f32, P_f32, vp]),
+    "bf_attn_typed_partials_floats": (i64, [C.POINTER(AttnIndex), i32, i32, i32]),
+    "bf_attn_fwd_typed": (C.c_int, [C.POINTER(AttnIndex), i32, i32, i32, vp, vp, vp, P_f32, vp, P_f32, vp]),
+    "bf_attn_bwd_typed": (C.c_int, [C.POINTER(AttnIndex), i32, i32, i32, vp, vp, vp, P_f32, P_f32, vp, vp, vp, vp,
+                                    P_f32, P_f32, P_f32, vp]),
 }
 
 _lib = None

@@ -76,6 +76,33 @@ def sparse_edge_attention(q, k, v, index: AttentionIndex, bias_e: Optional[torch
     return (out, Z) if with_z else out
 
 
+class _TypedEdgeAttention(torch.autograd.Function):
+    """Exphormer's typed-edge attention on a typed index: score = clamp(sum_j k q E[type] / sqrt(hn)),
+    HIP fwd/bwd (bf::sparse_attn_fwd_typed / _bwd_typed); returns out and takes the gradient of E too."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, type_mod, index):
+        out, Z = hip_ops.attn_forward_typed(index, q, k, v, type_mod)
+        ctx.save_for_backward(q, k, v, type_mod, Z)
+        ctx.index = index
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, type_mod, Z = ctx.saved_tensors
+        dq, dk, dv, dmod = hip_ops.attn_backward_typed(ctx.index, q, k, v, type_mod, Z, dout.contiguous())
+        return dq, dk, dv, dmod, None
+
+
+def typed_edge_attention(q, k, v, type_mod, index: AttentionIndex):
+    """Functional form of the typed path: q [n_q,H,hn], k/v [n_kv,H,hn] (one dtype), type_mod = E
+    [2, H, hn] (any float dtype: the kernels take it in float32, and its gradient flows back through the
+    cast), index from ``AttentionIndex.from_typed_coo``."""
+    dt = q.dtype
+    q, k, v = q.contiguous(), k.to(dt).contiguous(), v.to(dt).contiguous()
+    return _TypedEdgeAttention.apply(q, k, v, type_mod.float().contiguous(), index)
+
+
 class _IndexCache:
     """Small LRU of COO -> AttentionIndex conversions keyed by tensor identity."""
 
@@ -333,11 +360,9 @@ class ExphormerCoreAttention(nn.Module):
     """Exphormer core attention (models/exphormer_dist_node_level.py:45-121) on the HIP kernels.
 
     score = sum_j (k_j * q_j / sqrt(d)) * E[type]_j with E = edge_proj(edge_type_emb(type)).
-    Since E depends only on the edge type (2 types), edge e of type t is routed
-    to key/value row ``src + t * N_kv`` of the stacked keys ``cat(k*E_0, k*E_1)``
-    and values ``cat(v, v)``: the HIP kernels compute exactly the reference
-    score, and autograd of the two elementwise products returns dk, dv and the
-    gradients of the edge encoder.
+    A [3, E] edge set becomes a typed index (each entry's type in bit 31 of its ids) and the typed
+    kernels apply E[type] inside the three passes: no typed copy of K or V is made. Their backward
+    returns dq, dk, dv and dE, through which autograd reaches the edge encoder.
     """
 
     N_EDGE_TYPES = 2
@@ -371,15 +396,9 @@ class ExphormerCoreAttention(nn.Module):
             # the key holds the edge tensor itself, so a match is that tensor, not a reused address
             key = (edge_index, edge_index._version, str(q.device), qf.size(0), n_kv)
             if self._typed_key is None or self._typed_key[0] is not edge_index or self._typed_key[1:] != key[1:]:
-                ei = edge_index.to(q.device)
-                shifted = torch.stack([ei[0].long() + ei[2].long() * n_kv, ei[1].long()])
-                self._typed_idx = AttentionIndex.from_coo(shifted, qf.size(0), self.N_EDGE_TYPES * n_kv)
+                self._typed_idx = AttentionIndex.from_typed_coo(edge_index.to(q.device), qf.size(0), n_kv)
                 self._typed_key = key
-            idx = self._typed_idx
-            E = self.edge_modulation(q.device).to(kf.dtype)
-            k_typed = torch.cat([kf * E[t] for t in range(self.N_EDGE_TYPES)], dim=0)
-            v_typed = torch.cat([vf] * self.N_EDGE_TYPES, dim=0)
-            out = sparse_edge_attention(qf, k_typed, v_typed, idx)
+            out = typed_edge_attention(qf, kf, vf, self.edge_modulation(q.device), self._typed_idx)
         else:
             idx = resolve_index(edge_index, qf.size(0), n_kv, q.device)
             out = sparse_edge_attention(qf, kf, vf, idx)

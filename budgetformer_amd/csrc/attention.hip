@@ -119,6 +119,7 @@ __device__ __forceinline__ typename Elem<T>::Raw load_row_raw_nt(const T* base, 
 struct EdgeIn {
   const float* bias;     // float32 [nnz, H] or NULL
   const float* factor;   // float32 [nnz, H] or NULL
+  const float* mod;      // typed edges (EX = 3 only): E, float32 [2, H * hn]
   int drop;              // 1: the dropout factor applies
   float keep;            // kept iff u < keep (= 1 - rate)
   float scale;           // factor of a kept entry (1 / (1 - rate); 0 when rate = 1)
@@ -984,42 +985,73 @@ __device__ __forceinline__ void dkv_token_entry(const unsigned char* tok, int64_
   dkv_entry<T, EX>(d, w, rs, qr, gr, f, e, ex, dbias, sh, g, dk, dv);
 }
 
-// dK and dV of one kv row over its reverse entries [beg, end); with dbias, each
-// entry's g_b = (f w - Delta/D') p at its CSR position (the row stats carry the
-// exact Delta/D' the dq pass summed). EX: the per-entry inputs compiled in
-// (0 none, 1 dropout only, 2 bias, factor, dropout and dbias), so the plain
-// pass keeps its register count (fp32: 91 VGPRs, five waves per SIMD).
-template <typename T, bool NT, int EX>
-__device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __restrict__ dout,
-                                            const int32_t* __restrict__ kq, const int32_t* __restrict__ ks,
-                                            const int64_t* __restrict__ qptr, const EdgeIn& ex,
-                                            float* __restrict__ dbias,
-                                            const float2* __restrict__ rstat, int64_t beg,
-                                            int64_t end, const Shape& sh, const GroupPos& g,
-                                            const typename Elem<T>::Raw& krow,
-                                            const typename Elem<T>::Raw& vrow,
-                                            float (&dk)[Elem<T>::kPerVec],
-                                            float (&dv)[Elem<T>::kPerVec]) {
+// ------------------------------------------------------------------ typed edges (Exphormer)
+// models/exphormer_dist_node_level.py:92-117: an edge of type t in {0, 1} scores
+//   a = clamp(sum_j k[s,h,j] * q[t,h,j] * E[t,h,j] / sqrt(hn), -5, 5),  E = edge_proj(edge_type_emb(t)),
+// with no bias, factor or dropout. The type travels in bit 31 of the entry's id (kv in the query-major
+// CSR, kq in the reverse index; ids are below 2^31), so the passes read no per-entry type array and no
+// typed copy of K or V exists. dq and dK follow from the same scores with the modulation on the other
+// operand, and the gradient of E,
+//   dE[t,h,j] = sum over type-t entries of g_a * k[s,h,j] * q[t,h,j] / sqrt(hn),
+// is formed by the dq pass per query row (q times its type-t part of dq before the modulation), summed
+// per workgroup into one record of 2*D floats and over the records by a reduce in a fixed order.
+__device__ __forceinline__ int typed_id(int enc) { return enc & 0x7fffffff; }
+__device__ __forceinline__ bool typed_one(int enc) { return enc < 0; }
+
+// This lane's V values of E[t] (float32 [2, D]).
+template <int V>
+__device__ __forceinline__ void load_mod(const float* __restrict__ mod, int t, const Shape& sh, int col,
+                                         float (&e)[V]) {
+  const float* p = mod + int64_t(t) * sh.D + col;
+#pragma unroll
+  for (int i = 0; i < V; ++i) e[i] = p[i];
+}
+
+// sum_i a[i] * (one ? b1[i] : b0[i]) in element order (the modulated dot product of one entry).
+template <int V>
+__device__ __forceinline__ float typed_dot(const float (&a)[V], const float (&b0)[V], const float (&b1)[V], bool one) {
+  float d = 0.f;
+#pragma unroll
+  for (int i = 0; i < V; ++i) d = fmaf(a[i], one ? b1[i] : b0[i], d);
+  return d;
+}
+
+// dkv_segment for typed entries: dK accumulates q_t * g_a per type and takes E[0] * dK0 + E[1] * dK1 at
+// the end (the modulation is linear, so a split row's items may each apply it to their part).
+template <typename T, bool NT>
+__device__ __forceinline__ void dkv_segment_typed(const T* __restrict__ q, const T* __restrict__ dout,
+                                                  const int32_t* __restrict__ kq, const EdgeIn& ex,
+                                                  const float2* __restrict__ rstat, int64_t beg, int64_t end,
+                                                  const Shape& sh, const GroupPos& g,
+                                                  const typename Elem<T>::Raw& krow,
+                                                  const typename Elem<T>::Raw& vrow,
+                                                  float (&dk)[Elem<T>::kPerVec], float (&dv)[Elem<T>::kPerVec]) {
   constexpr int V = Elem<T>::kPerVec;
   constexpr int kUnroll = Unroll<T>::kv;
   const int lph = 1 << sh.lph_log2;
-  ChunkIds<T, kUnroll> ids(sh, beg);
   const int col = gather_col(g);
+  float ke0[V], ke1[V], dk0[V], dk1[V];
+  {
+    float kk[V], e[V];
+    Elem<T>::unpack(krow, kk);
+    load_mod<V>(ex.mod, 0, sh, col, e);
+#pragma unroll
+    for (int i = 0; i < V; ++i) ke0[i] = kk[i] * e[i];
+    load_mod<V>(ex.mod, 1, sh, col, e);
+#pragma unroll
+    for (int i = 0; i < V; ++i) ke1[i] = kk[i] * e[i];
+  }
+#pragma unroll
+  for (int i = 0; i < V; ++i) dk0[i] = dk1[i] = 0.f;
+  ChunkIds<T, kUnroll> ids(sh, beg);
   for (int64_t i0 = beg; i0 < end; i0 += kUnroll) {
     int t[kUnroll];
-    bool ok[kUnroll];
+    bool ok[kUnroll], one[kUnroll];
     ids.fetch(kq, i0, end, g, t, ok);
-    // each entry's slot in its query's row: with the query, the dropout's key; with the row's start
-    // (gathered only by EX == 2, before the rows, so that it overlaps them), the CSR position that
-    // indexes the bias, factor and dbias
-    int32_t slot[kUnroll], epos[kUnroll];   // nnz < 2^31
-    if (EX) {
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) slot[u] = ks[ok[u] ? i0 + u : end - 1];
-    }
-    if (EX == 2) {
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) epos[u] = slot[u] + int32_t(qptr[t[u]]);
+    for (int u = 0; u < kUnroll; ++u) {
+      one[u] = typed_one(t[u]);
+      t[u] = typed_id(t[u]);
     }
     typename Elem<T>::Raw qr[kUnroll], gr[kUnroll];
     float2 rs[kUnroll];
@@ -1029,12 +1061,12 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
       gr[u] = gather_row<T, NT>(dout, t[u], sh.D, col);
       rs[u] = rstat[int64_t(t[u]) * sh.H + g.head];
     }
-    IterDrop<kUnroll> drop{false, 0u};
-    if (EX) drop = iter_drop<kUnroll>(ex, t, slot, ok, sh, g);
     float d[kUnroll], w[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      d[u] = Elem<T>::dot(qr[u], krow, 0.f);
+      float qq[V];
+      Elem<T>::unpack(qr[u], qq);
+      d[u] = typed_dot<V>(qq, ke0, ke1, one[u]);
       w[u] = Elem<T>::dot(gr[u], vrow, 0.f);
     }
     for (int o = 1; o < lph; o <<= 1) {
@@ -1047,9 +1079,100 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       if (!ok[u]) continue;
-      const int64_t e = EX == 2 ? int64_t(epos[u]) : 0;
-      const float f = EX ? iter_factor<kUnroll, EX>(ex, drop, u, e, sh, g.head) : 1.f;
-      dkv_entry<T, EX>(d[u], w[u], rs[u], qr[u], gr[u], f, e, ex, dbias, sh, g, dk, dv);
+      const float apre = d[u] * sh.inv_scale;
+      const float a = fminf(fmaxf(apre, -sh.clamp), sh.clamp);
+      const float p = __expf(a);   // a is clamped to [-5, 5]: exp2-based form is within 2 ulp
+      const float gb = fmaf(w[u], rs[u].x, -rs[u].y) * p;   // rs = {1/D', Delta/D'}
+      const float gs = (apre >= -sh.clamp && apre <= sh.clamp) ? gb * sh.inv_scale : 0.f;
+      const float gs1 = one[u] ? gs : 0.f, gs0 = gs - gs1;
+      const float pf = p * rs[u].x;
+      float qq[V], gg[V];
+      Elem<T>::unpack(qr[u], qq);
+      Elem<T>::unpack(gr[u], gg);
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        dv[i] = fmaf(pf, gg[i], dv[i]);
+        dk0[i] = fmaf(gs0, qq[i], dk0[i]);
+        dk1[i] = fmaf(gs1, qq[i], dk1[i]);
+      }
+    }
+  }
+  float e0[V], e1[V];
+  load_mod<V>(ex.mod, 0, sh, col, e0);
+  load_mod<V>(ex.mod, 1, sh, col, e1);
+#pragma unroll
+  for (int i = 0; i < V; ++i) dk[i] = fmaf(e0[i], dk0[i], fmaf(e1[i], dk1[i], dk[i]));
+}
+
+// dK and dV of one kv row over its reverse entries [beg, end); with dbias, each
+// entry's g_b = (f w - Delta/D') p at its CSR position (the row stats carry the
+// exact Delta/D' the dq pass summed). EX: the per-entry inputs compiled in
+// (0 none, 1 dropout only, 2 bias, factor, dropout and dbias, 3 typed edges),
+// so the plain pass keeps its register count (fp32: 96 VGPRs, five waves per SIMD).
+template <typename T, bool NT, int EX>
+__device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __restrict__ dout,
+                                            const int32_t* __restrict__ kq, const int32_t* __restrict__ ks,
+                                            const int64_t* __restrict__ qptr, const EdgeIn& ex,
+                                            float* __restrict__ dbias,
+                                            const float2* __restrict__ rstat, int64_t beg,
+                                            int64_t end, const Shape& sh, const GroupPos& g,
+                                            const typename Elem<T>::Raw& krow,
+                                            const typename Elem<T>::Raw& vrow,
+                                            float (&dk)[Elem<T>::kPerVec],
+                                            float (&dv)[Elem<T>::kPerVec]) {
+  if constexpr (EX == 3) {
+    dkv_segment_typed<T, NT>(q, dout, kq, ex, rstat, beg, end, sh, g, krow, vrow, dk, dv);
+  } else {
+    constexpr int kUnroll = Unroll<T>::kv;
+    const int lph = 1 << sh.lph_log2;
+    ChunkIds<T, kUnroll> ids(sh, beg);
+    const int col = gather_col(g);
+    for (int64_t i0 = beg; i0 < end; i0 += kUnroll) {
+      int t[kUnroll];
+      bool ok[kUnroll];
+      ids.fetch(kq, i0, end, g, t, ok);
+      // each entry's slot in its query's row: with the query, the dropout's key; with the row's start
+      // (gathered only by EX == 2, before the rows, so that it overlaps them), the CSR position that
+      // indexes the bias, factor and dbias
+      int32_t slot[kUnroll], epos[kUnroll];   // nnz < 2^31
+      if (EX) {
+  #pragma unroll
+        for (int u = 0; u < kUnroll; ++u) slot[u] = ks[ok[u] ? i0 + u : end - 1];
+      }
+      if (EX == 2) {
+  #pragma unroll
+        for (int u = 0; u < kUnroll; ++u) epos[u] = slot[u] + int32_t(qptr[t[u]]);
+      }
+      typename Elem<T>::Raw qr[kUnroll], gr[kUnroll];
+      float2 rs[kUnroll];
+  #pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        qr[u] = gather_row<T, NT>(q, t[u], sh.D, col);
+        gr[u] = gather_row<T, NT>(dout, t[u], sh.D, col);
+        rs[u] = rstat[int64_t(t[u]) * sh.H + g.head];
+      }
+      IterDrop<kUnroll> drop{false, 0u};
+      if (EX) drop = iter_drop<kUnroll>(ex, t, slot, ok, sh, g);
+      float d[kUnroll], w[kUnroll];
+  #pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        d[u] = Elem<T>::dot(qr[u], krow, 0.f);
+        w[u] = Elem<T>::dot(gr[u], vrow, 0.f);
+      }
+      for (int o = 1; o < lph; o <<= 1) {
+  #pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+          d[u] += __shfl_xor(d[u], o, 64);
+          w[u] += __shfl_xor(w[u], o, 64);
+        }
+      }
+  #pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        if (!ok[u]) continue;
+        const int64_t e = EX == 2 ? int64_t(epos[u]) : 0;
+        const float f = EX ? iter_factor<kUnroll, EX>(ex, drop, u, e, sh, g.head) : 1.f;
+        dkv_entry<T, EX>(d[u], w[u], rs[u], qr[u], gr[u], f, e, ex, dbias, sh, g, dk, dv);
+      }
     }
   }
 }
@@ -1210,6 +1333,218 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kv_reduce_kernel(T* __restric
   Elem<T>::store(dv + int64_t(row) * sh.D + g.col0, av);
 }
 
+// ------------------------------------------------------------------ typed-edge query passes
+// One query row per lane group, every row on the row path (a typed index splits no query row: its rows
+// are a query's budget plus its expander edges). The forward keeps q * E[0] and q * E[1] for the row.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void attn_fwd_typed_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, const int64_t* __restrict__ qptr,
+    const int32_t* __restrict__ kv, const float* __restrict__ mod, T* __restrict__ out, float* __restrict__ Z,
+    int64_t n_q, Shape sh) {
+  constexpr int V = Elem<T>::kPerVec;
+  constexpr int kUnroll = Unroll<T>::fwd;
+  const GroupPos g = group_pos<T>(sh);
+  const int64_t row = row_slot(sh, 0);
+  if (row >= n_q) return;
+  const int64_t beg = qptr[row], end = qptr[row + 1];
+  const int col = gather_col(g);
+  const int lph = 1 << sh.lph_log2;
+  float qe0[V], qe1[V];
+  {
+    float qq[V], e[V];
+    Elem<T>::unpack(load_row_raw_nt(q, row, sh.D, g), qq);
+    load_mod<V>(mod, 0, sh, col, e);
+#pragma unroll
+    for (int i = 0; i < V; ++i) qe0[i] = qq[i] * e[i];
+    load_mod<V>(mod, 1, sh, col, e);
+#pragma unroll
+    for (int i = 0; i < V; ++i) qe1[i] = qq[i] * e[i];
+  }
+  float acc[V], z = 0.f;
+#pragma unroll
+  for (int i = 0; i < V; ++i) acc[i] = 0.f;
+  ChunkIds<T, kUnroll> ids(sh, beg);
+  for (int64_t e0 = beg; e0 < end; e0 += kUnroll) {
+    int s[kUnroll];
+    bool ok[kUnroll], one[kUnroll];
+    ids.fetch(kv, e0, end, g, s, ok);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      one[u] = typed_one(s[u]);
+      s[u] = typed_id(s[u]);
+    }
+    typename Elem<T>::Raw kr[kUnroll], vr[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      kr[u] = Elem<T>::load_raw(k + int64_t(s[u]) * sh.D + col);
+      vr[u] = Elem<T>::load_raw(v + int64_t(s[u]) * sh.D + col);
+    }
+    float d[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      float kk[V];
+      Elem<T>::unpack(kr[u], kk);
+      d[u] = typed_dot<V>(kk, qe0, qe1, one[u]);
+    }
+    for (int o = 1; o < lph; o <<= 1) {
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) d[u] += __shfl_xor(d[u], o, 64);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      if (!ok[u]) continue;
+      const float a = fminf(fmaxf(d[u] * sh.inv_scale, -sh.clamp), sh.clamp);
+      const float p = __expf(a);
+      float vv[V];
+      Elem<T>::unpack(vr[u], vv);
+#pragma unroll
+      for (int i = 0; i < V; ++i) acc[i] = fmaf(p, vv[i], acc[i]);
+      z += p;
+    }
+  }
+  store_out(out, Z, row, sh, g, acc, z);
+}
+
+// dq of typed rows: per row and type, A_t = sum f w p m k_s and B_t = sum p m k_s over the row's type-t
+// entries; S_t = A_t - (Delta / D') B_t is dq's type-t part before the modulation, dq = E[0] S_0 + E[1] S_1,
+// and q * S_t is the row's share of dE[t]. Each lane group takes rows_per_group consecutive rows, and
+// each workgroup writes one record {dE[0], dE[1]} (2 * D floats) of its rows' shares.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void attn_bwd_q_typed_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, const int64_t* __restrict__ qptr,
+    const int32_t* __restrict__ kv, const float* __restrict__ mod, const float* __restrict__ Z,
+    const T* __restrict__ dout, T* __restrict__ dq, float2* __restrict__ rstat, float* __restrict__ mod_rec,
+    int64_t n_q, int rows_per_group, Shape sh) {
+  constexpr int V = Elem<T>::kPerVec;
+  constexpr int kUnroll = Unroll<T>::q;
+  extern __shared__ float lds[];
+  const GroupPos g = group_pos<T>(sh);
+  const int col = gather_col(g);
+  const int lph = 1 << sh.lph_log2;
+  const EdgeIn none{nullptr, nullptr, nullptr, 0, 1.f, 1.f, 0u, 0u, 0u, 0u};
+  float e0[V], e1[V], r0[V], r1[V];
+  load_mod<V>(mod, 0, sh, col, e0);
+  load_mod<V>(mod, 1, sh, col, e1);
+#pragma unroll
+  for (int i = 0; i < V; ++i) r0[i] = r1[i] = 0.f;
+  const int64_t first = row_slot(sh, 0) * rows_per_group;
+  const int64_t last = first + rows_per_group < n_q ? first + rows_per_group : n_q;
+  for (int64_t row = first; row < last; ++row) {
+    const int64_t beg = qptr[row], end = qptr[row + 1];
+    const typename Elem<T>::Raw qr = load_row_raw_nt(q, row, sh.D, g);
+    const typename Elem<T>::Raw gr = load_row_raw_nt(dout, row, sh.D, g);
+    const float inv_dprime = row_inv_dprime<T>(Z, row, sh, g);
+    float qq[V], qe0[V], qe1[V], A0[V], B0[V], A1[V], B1[V], c = 0.f;
+    Elem<T>::unpack(qr, qq);
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      qe0[i] = qq[i] * e0[i];
+      qe1[i] = qq[i] * e1[i];
+      A0[i] = B0[i] = A1[i] = B1[i] = 0.f;
+    }
+    ChunkIds<T, kUnroll> ids(sh, beg);
+    for (int64_t x0 = beg; x0 < end; x0 += kUnroll) {
+      int s[kUnroll];
+      bool ok[kUnroll], one[kUnroll];
+      ids.fetch(kv, x0, end, g, s, ok);
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        one[u] = typed_one(s[u]);
+        s[u] = typed_id(s[u]);
+      }
+      typename Elem<T>::Raw kr[kUnroll], vr[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        kr[u] = Elem<T>::load_raw(k + int64_t(s[u]) * sh.D + col);
+        vr[u] = Elem<T>::load_raw(v + int64_t(s[u]) * sh.D + col);
+      }
+      float d[kUnroll], w[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        float kk[V];
+        Elem<T>::unpack(kr[u], kk);
+        d[u] = typed_dot<V>(kk, qe0, qe1, one[u]);
+        w[u] = Elem<T>::dot(vr[u], gr, 0.f);
+      }
+      for (int o = 1; o < lph; o <<= 1) {
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+          d[u] += __shfl_xor(d[u], o, 64);
+          w[u] += __shfl_xor(w[u], o, 64);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        if (!ok[u]) continue;
+        const EntryTerms t = entry_terms<0>(d[u], w[u], inv_dprime, none, 0, 1.f, sh, g);
+        const float fwp = t.w * t.p;
+        const float ca = fwp * t.m, cb = t.p * t.m;
+        const float ca1 = one[u] ? ca : 0.f, cb1 = one[u] ? cb : 0.f, ca0 = ca - ca1, cb0 = cb - cb1;
+        float kk[V];
+        Elem<T>::unpack(kr[u], kk);
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+          A0[i] = fmaf(ca0, kk[i], A0[i]);
+          B0[i] = fmaf(cb0, kk[i], B0[i]);
+          A1[i] = fmaf(ca1, kk[i], A1[i]);
+          B1[i] = fmaf(cb1, kk[i], B1[i]);
+        }
+        c += fwp;
+      }
+    }
+    const float dd = c * inv_dprime;
+    float o[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float s0 = fmaf(-dd, B0[i], A0[i]), s1 = fmaf(-dd, B1[i], A1[i]);
+      o[i] = fmaf(e0[i], s0, e1[i] * s1);
+      r0[i] = fmaf(qq[i], s0, r0[i]);
+      r1[i] = fmaf(qq[i], s1, r1[i]);
+    }
+    if (g.act) {
+      Elem<T>::store_nt(dq + row * sh.D + g.col0, o);
+      if (g.lead) rstat[row * sh.H + g.head] = make_float2(inv_dprime, dd);
+    }
+  }
+  // the workgroup's record: the wave's groups by a fixed butterfly, then its waves in order through LDS
+  for (int o = 1 << sh.lpr_log2; o < 64; o <<= 1) {
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      r0[i] += __shfl_xor(r0[i], o, 64);
+      r1[i] += __shfl_xor(r1[i], o, 64);
+    }
+  }
+  if ((threadIdx.x & 63) < (1u << sh.lpr_log2)) store_token_record<V>(lds + (threadIdx.x >> 6) * (2 * sh.D), sh, g, r0, r1);
+  __syncthreads();
+  if (threadIdx.x < (1u << sh.lpr_log2) && g.act) {
+    float s0[V], s1[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) s0[i] = s1[i] = 0.f;
+    for (int w = 0; w < kBlock / 64; ++w) {
+      const float* slot = lds + w * (2 * sh.D);
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        s0[i] += slot[g.col0 + i];
+        s1[i] += slot[sh.D + g.col0 + i];
+      }
+    }
+    store_token_record<V>(mod_rec + int64_t(blockIdx.x) * (2 * sh.D), sh, g, s0, s1);
+  }
+}
+
+// out[b][c] = sum of rec[r][c] over records r in [b * per_block, (b + 1) * per_block), in record order
+// (cols floats per record): one pass of the fixed-order reduction of the dE records.
+__global__ __launch_bounds__(kBlock) void mod_rec_reduce_kernel(const float* __restrict__ rec, int64_t n_rec, int cols,
+                                                                int64_t per_block, float* __restrict__ out) {
+  const int64_t r0 = int64_t(blockIdx.x) * per_block;
+  const int64_t r1 = r0 + per_block < n_rec ? r0 + per_block : n_rec;
+  for (int c = threadIdx.x; c < cols; c += kBlock) {
+    float s = 0.f;
+    for (int64_t r = r0; r < r1; ++r) s += rec[r * cols + c];
+    out[int64_t(blockIdx.x) * cols + c] = s;
+  }
+}
+
 // ------------------------------------------------------------------ host side
 int make_shape(int32_t dtype, int32_t H, int32_t hn, Shape& sh) {
   BF_CHECK_ARG(dtype == BF_DTYPE_F32 || dtype == BF_DTYPE_BF16 || dtype == BF_DTYPE_F16,
@@ -1308,7 +1643,7 @@ inline Items key_items(const bf_attn_index* idx, const Shape& sh, float* partial
 
 // The per-entry inputs of a call, with the dropout's Philox key and threshold.
 int make_edge_in(const float* bias, const float* factor, const bf_attn_dropout* dropout, EdgeIn& ex) {
-  ex = EdgeIn{bias, factor, 0, 1.f, 1.f, 0u, 0u, 0u, 0u};
+  ex = EdgeIn{bias, factor, nullptr, 0, 1.f, 1.f, 0u, 0u, 0u, 0u};
   if (dropout) {
     BF_CHECK_ARG(dropout->rate >= 0.f && dropout->rate <= 1.f, "attention: dropout rate %g outside [0, 1]",
                  double(dropout->rate));
@@ -1364,6 +1699,69 @@ int fwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
   return BF_OK;
 }
 
+// The key-major pass and its reduce: the instance for the sizes (rows per group, non-temporal gathers,
+// prefetched slots) and the per-entry mode (EX: 0 plain, 1 dropout, 2 bias / factor / dropout / dbias,
+// 3 typed edges).
+template <typename T>
+int kv_pass_impl(const bf_attn_index* idx, const Shape& sh, const T* Q, const T* K, const T* Vv, const EdgeIn& ex,
+                 int mode, float* dbias, const T* dO, const float2* rstat, void* dk, void* dv, const Items& kit,
+                 const float* token_rec, hipStream_t st) {
+  const int rows_per_group = kv_rows_per_group(idx->n_kv, sizeof(T));
+  const int64_t kv_blocks = int64_t(idx->k_items) + grid_for(ceil_div(idx->n_kv, rows_per_group), sh);
+  if (kv_blocks > 0) {
+    // the token row's entries of the short kv rows take query 0's rows and stats from LDS, where a
+    // workgroup's copy serves enough rows to pay for its wait (several rows per group: c5 dk/dv pass
+    // 45.6 -> 44.6 ms); with one row per group the copy costs more than the gathers it spares (the
+    // rows then gather query 0's entry like any other: c2 dk/dv pass 0.199 -> 0.205 ms with the copy)
+    const int tok_row = idx->token_column == 1 && idx->n_q > 0 && rows_per_group > 1 ? 1 : 0;
+    const size_t tok_lds = tok_row ? size_t(2 * sh.D) * sizeof(T) + size_t(sh.H) * sizeof(float2) : 0;
+    const size_t lds = std::max(idx->k_items > 0 ? combine_lds_bytes(sh) : size_t(0), tok_lds);
+    const bool stream_rows = size_t(idx->n_q) * size_t(sh.D) * sizeof(T) * 2 > kStreamBytes;
+#define BF_LAUNCH_KV1(NT, PRE, EX)                                                                                 \
+  BF_LAUNCH("attn_bwd_kv_kernel", (attn_bwd_kv_kernel<T, NT, PRE, EX>), dim3(unsigned(kv_blocks)), dim3(kBlock), lds, st, \
+            Q, K, Vv, idx->kptr, idx->kq, idx->ks, idx->qptr, ex, dbias, dO, rstat, static_cast<T*>(dk),            \
+            static_cast<T*>(dv), idx->k_order, idx->k_spans, kit, idx->k_items, idx->n_kv, sh, idx->chunk,           \
+            rows_per_group, token_rec, idx->q_items, int64_t(grid_for(idx->n_q, sh)), tok_row, idx->plan_counts)
+#define BF_LAUNCH_KV(NT, PRE)           \
+  do {                                  \
+    if (mode == 3)                      \
+      BF_LAUNCH_KV1(NT, PRE, 3);        \
+    else if (mode == 2)                 \
+      BF_LAUNCH_KV1(NT, PRE, 2);        \
+    else if (mode == 1)                 \
+      BF_LAUNCH_KV1(NT, PRE, 1);        \
+    else                                \
+      BF_LAUNCH_KV1(NT, PRE, 0);        \
+  } while (0)
+    if constexpr (sizeof(T) == 2) {
+      // the group's slots prefetched (several rows per group)
+      const bool pre = rows_per_group > 1 && rows_per_group <= (1 << sh.lpr_log2);
+      if (pre && stream_rows)
+        BF_LAUNCH_KV(true, true);
+      else if (pre)
+        BF_LAUNCH_KV(false, true);
+      else if (stream_rows)
+        BF_LAUNCH_KV(true, false);
+      else
+        BF_LAUNCH_KV(false, false);
+    } else {
+      if (stream_rows)
+        BF_LAUNCH_KV(true, false);
+      else
+        BF_LAUNCH_KV(false, false);
+    }
+#undef BF_LAUNCH_KV
+#undef BF_LAUNCH_KV1
+    BF_CHECK_LAUNCH();
+  }
+  if (idx->k_heavy > 0) {
+    BF_LAUNCH("attn_bwd_kv_reduce_kernel", attn_bwd_kv_reduce_kernel<T>, dim3(unsigned(idx->k_heavy)), dim3(kBlock),
+              combine_lds_bytes(sh), st, static_cast<T*>(dk), static_cast<T*>(dv), kit, sh, idx->plan_counts);
+    BF_CHECK_LAUNCH();
+  }
+  return BF_OK;
+}
+
 template <typename T>
 int bwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const void* k, const void* v,
              const EdgeIn& ex, const float* Z, const void* dout, void* dq, void* dk, void* dv,
@@ -1402,58 +1800,80 @@ int bwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
               token_rec, tok_first, idx->plan_counts);
     BF_CHECK_LAUNCH();
   }
-  const int rows_per_group = kv_rows_per_group(idx->n_kv, sizeof(T));
-  const int64_t kv_blocks = int64_t(idx->k_items) + grid_for(ceil_div(idx->n_kv, rows_per_group), sh);
-  if (kv_blocks > 0) {
-    // the token row's entries of the short kv rows take query 0's rows and stats from LDS, where a
-    // workgroup's copy serves enough rows to pay for its wait (several rows per group: c5 dk/dv pass
-    // 45.6 -> 44.6 ms); with one row per group the copy costs more than the gathers it spares (the
-    // rows then gather query 0's entry like any other: c2 dk/dv pass 0.199 -> 0.205 ms with the copy)
-    const int tok_row = idx->token_column == 1 && idx->n_q > 0 && rows_per_group > 1 ? 1 : 0;
-    const size_t tok_lds = tok_row ? size_t(2 * sh.D) * sizeof(T) + size_t(sh.H) * sizeof(float2) : 0;
-    const size_t lds = std::max(idx->k_items > 0 ? combine_lds_bytes(sh) : size_t(0), tok_lds);
-    const bool stream_rows = size_t(idx->n_q) * size_t(sh.D) * sizeof(T) * 2 > kStreamBytes;
-    const int mode = edge_mode(ex, dbias != nullptr);
-#define BF_LAUNCH_KV1(NT, PRE, EX)                                                                                 \
-  BF_LAUNCH("attn_bwd_kv_kernel", (attn_bwd_kv_kernel<T, NT, PRE, EX>), dim3(unsigned(kv_blocks)), dim3(kBlock), lds, st, \
-            Q, K, Vv, idx->kptr, idx->kq, idx->ks, idx->qptr, ex, dbias, dO, rstat, static_cast<T*>(dk),            \
-            static_cast<T*>(dv), idx->k_order, idx->k_spans, kit, idx->k_items, idx->n_kv, sh, idx->chunk,           \
-            rows_per_group, token_rec, idx->q_items, int64_t(grid_for(idx->n_q, sh)), tok_row, idx->plan_counts)
-#define BF_LAUNCH_KV(NT, PRE)           \
-  do {                                  \
-    if (mode == 2)                      \
-      BF_LAUNCH_KV1(NT, PRE, 2);        \
-    else if (mode == 1)                 \
-      BF_LAUNCH_KV1(NT, PRE, 1);        \
-    else                                \
-      BF_LAUNCH_KV1(NT, PRE, 0);        \
-  } while (0)
-    if constexpr (sizeof(T) == 2) {
-      // the group's slots prefetched (several rows per group)
-      const bool pre = rows_per_group > 1 && rows_per_group <= (1 << sh.lpr_log2);
-      if (pre && stream_rows)
-        BF_LAUNCH_KV(true, true);
-      else if (pre)
-        BF_LAUNCH_KV(false, true);
-      else if (stream_rows)
-        BF_LAUNCH_KV(true, false);
-      else
-        BF_LAUNCH_KV(false, false);
-    } else {
-      if (stream_rows)
-        BF_LAUNCH_KV(true, false);
-      else
-        BF_LAUNCH_KV(false, false);
-    }
-#undef BF_LAUNCH_KV
-#undef BF_LAUNCH_KV1
+  BF_CHECK_OK(kv_pass_impl<T>(idx, sh, Q, K, Vv, ex, edge_mode(ex, dbias != nullptr), dbias, dO, rstat, dk, dv,
+                               kit, token_rec, st));
+  return BF_OK;
+}
+
+// ------------------------------------------------------------------ typed edges: host side
+// Rows per lane group of the typed dq pass: about 2048 workgroups for large query sets (each writes one
+// dE record), at most 16 rows per group.
+inline int typed_rows_per_group(int64_t n_q, const Shape& sh) {
+  const int64_t gpb = kBlock >> sh.lpr_log2;
+  const int64_t r = n_q / (gpb * 2048);
+  return int(r < 1 ? 1 : (r > 16 ? 16 : r));
+}
+
+inline int64_t typed_q_blocks(int64_t n_q, const Shape& sh) {
+  return int64_t(grid_for(ceil_div(n_q, typed_rows_per_group(n_q, sh)), sh));
+}
+
+constexpr int64_t kModRecPerBlock = 256;   // dE records summed per workgroup in the first reduce pass
+
+int check_typed(const bf_attn_index* idx, const float* mod) {
+  BF_CHECK_ARG(mod != nullptr, "attn typed: type_mod is NULL");
+  BF_CHECK_ARG(idx->token_column == 0, "attn typed: a typed index has no token column");
+  BF_CHECK_ARG(idx->q_items == 0, "attn typed: a typed index splits no query row (q_items = %d)", idx->q_items);
+  return BF_OK;
+}
+
+template <typename T>
+int fwd_typed_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const void* k, const void* v,
+                   const float* mod, void* out, float* Z, hipStream_t st) {
+  const unsigned blocks = grid_for(idx->n_q, sh);
+  if (blocks == 0) return BF_OK;
+  BF_LAUNCH("attn_fwd_typed_kernel", attn_fwd_typed_kernel<T>, dim3(blocks), dim3(kBlock), 0, st,
+            static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), idx->qptr, idx->kv, mod,
+            static_cast<T*>(out), Z, idx->n_q, sh);
+  BF_CHECK_LAUNCH();
+  return BF_OK;
+}
+
+template <typename T>
+int bwd_typed_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const void* k, const void* v,
+                   const float* mod, const float* Z, const void* dout, void* dq, void* dk, void* dv, float* dmod,
+                   float* rstat_f, float* partials, hipStream_t st) {
+  float2* rstat = reinterpret_cast<float2*>(rstat_f);
+  const T* Q = static_cast<const T*>(q);
+  const T* K = static_cast<const T*>(k);
+  const T* Vv = static_cast<const T*>(v);
+  const T* dO = static_cast<const T*>(dout);
+  const Items kit = key_items(idx, sh, partials);     // the key-side records first (q_items is 0)
+  const int64_t n_rec = typed_q_blocks(idx->n_q, sh);
+  float* mod_rec = partials + int64_t(idx->k_items) * (2 * sh.D + sh.H);
+  float* mod_part = mod_rec + n_rec * (2 * sh.D);
+  if (n_rec > 0) {
+    BF_LAUNCH("attn_bwd_q_typed_kernel", attn_bwd_q_typed_kernel<T>, dim3(unsigned(n_rec)), dim3(kBlock),
+              size_t(kBlock / 64) * size_t(2 * sh.D) * sizeof(float), st, Q, K, Vv, idx->qptr, idx->kv, mod, Z, dO,
+              static_cast<T*>(dq), rstat, mod_rec, idx->n_q, typed_rows_per_group(idx->n_q, sh), sh);
     BF_CHECK_LAUNCH();
   }
-  if (idx->k_heavy > 0) {
-    BF_LAUNCH("attn_bwd_kv_reduce_kernel", attn_bwd_kv_reduce_kernel<T>, dim3(unsigned(idx->k_heavy)), dim3(kBlock),
-              combine_lds_bytes(sh), st, static_cast<T*>(dk), static_cast<T*>(dv), kit, sh, idx->plan_counts);
+  EdgeIn ex{nullptr, nullptr, mod, 0, 1.f, 1.f, 0u, 0u, 0u, 0u};
+  BF_CHECK_OK(kv_pass_impl<T>(idx, sh, Q, K, Vv, ex, 3, nullptr, dO, rstat, dk, dv, kit, nullptr, st));
+  // dE: the records summed in a fixed order, in two passes (an empty query set writes zeros)
+  const int cols = 2 * sh.D;
+  const int64_t n_part = n_rec > 0 ? ceil_div(n_rec, kModRecPerBlock) : 0;
+  if (n_part > 1) {
+    BF_LAUNCH("mod_rec_reduce_kernel", mod_rec_reduce_kernel, dim3(unsigned(n_part)), dim3(kBlock), 0, st, mod_rec,
+              n_rec, cols, kModRecPerBlock, mod_part);
     BF_CHECK_LAUNCH();
+    BF_LAUNCH("mod_rec_reduce_kernel", mod_rec_reduce_kernel, dim3(1), dim3(kBlock), 0, st, mod_part, n_part, cols,
+              n_part, dmod);
+  } else {
+    BF_LAUNCH("mod_rec_reduce_kernel", mod_rec_reduce_kernel, dim3(1), dim3(kBlock), 0, st, mod_rec, n_rec, cols,
+              n_rec, dmod);
   }
+  BF_CHECK_LAUNCH();
   return BF_OK;
 }
 
@@ -1542,6 +1962,52 @@ extern "C" int bf_attn_bwd(const bf_attn_index* idx, int32_t dtype, int32_t num_
                               as_stream(stream));
   return bwd_impl<uint16_t>(idx, sh, q, k, v, ex, Z, dout, dq, dk, dv, dbias, rowstat, partials,
                             as_stream(stream));
+}
+
+// ------------------------------------------------------------------ typed edges (Exphormer)
+extern "C" int64_t bf_attn_typed_partials_floats(const bf_attn_index* idx, int32_t dtype, int32_t num_heads,
+                                                 int32_t head_dim) {
+  Shape sh;
+  if (!idx || make_shape(dtype, num_heads, head_dim, sh) != BF_OK) return 0;
+  const int64_t n_rec = typed_q_blocks(idx->n_q, sh);
+  const int64_t n_part = n_rec > 0 ? ceil_div(n_rec, kModRecPerBlock) : 0;
+  return int64_t(idx->k_items) * (2 * sh.D + sh.H) + (n_rec + n_part) * (2 * sh.D);
+}
+
+extern "C" int bf_attn_fwd_typed(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
+                                 const void* q, const void* k, const void* v, const float* type_mod, void* out,
+                                 float* Z, void* stream) {
+  Shape sh;
+  int rc = make_shape(dtype, num_heads, head_dim, sh);
+  if (rc || (rc = check_index(idx, false)) || (rc = check_typed(idx, type_mod))) return rc;
+  BF_CHECK_ARG(q && k && v && out && Z, "attn_fwd_typed: null tensor");
+  BF_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out) && aligned16(type_mod),
+               "attn_fwd_typed: q/k/v/out/type_mod must be 16-byte aligned");
+  if (dtype == BF_DTYPE_F32) return fwd_typed_impl<float>(idx, sh, q, k, v, type_mod, out, Z, as_stream(stream));
+  if (dtype == BF_DTYPE_F16) return fwd_typed_impl<_Float16>(idx, sh, q, k, v, type_mod, out, Z, as_stream(stream));
+  return fwd_typed_impl<uint16_t>(idx, sh, q, k, v, type_mod, out, Z, as_stream(stream));
+}
+
+extern "C" int bf_attn_bwd_typed(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
+                                 const void* q, const void* k, const void* v, const float* type_mod, const float* Z,
+                                 const void* dout, void* dq, void* dk, void* dv, float* dtype_mod, float* rowstat,
+                                 float* partials, void* stream) {
+  Shape sh;
+  int rc = make_shape(dtype, num_heads, head_dim, sh);
+  if (rc || (rc = check_index(idx, true)) || (rc = check_typed(idx, type_mod))) return rc;
+  BF_CHECK_ARG(q && k && v && Z && dout && dq && dk && dv && dtype_mod && rowstat && partials,
+               "attn_bwd_typed: null tensor");
+  BF_CHECK_ARG((reinterpret_cast<uintptr_t>(rowstat) & 7u) == 0, "attn_bwd_typed: rowstat must be 8-byte aligned");
+  BF_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(dout) && aligned16(dq) && aligned16(dk) &&
+                   aligned16(dv) && aligned16(type_mod),
+               "attn_bwd_typed: tensors must be 16-byte aligned");
+  hipStream_t st = as_stream(stream);
+  if (dtype == BF_DTYPE_F32)
+    return bwd_typed_impl<float>(idx, sh, q, k, v, type_mod, Z, dout, dq, dk, dv, dtype_mod, rowstat, partials, st);
+  if (dtype == BF_DTYPE_F16)
+    return bwd_typed_impl<_Float16>(idx, sh, q, k, v, type_mod, Z, dout, dq, dk, dv, dtype_mod, rowstat, partials,
+                                    st);
+  return bwd_typed_impl<uint16_t>(idx, sh, q, k, v, type_mod, Z, dout, dq, dk, dv, dtype_mod, rowstat, partials, st);
 }
 
 // ------------------------------------------------------------------ allocation-free backward

@@ -33,6 +33,13 @@ void set_error(const char* fmt, ...);
 
 #define BF_CHECK_LAUNCH() BF_CHECK_HIP(hipGetLastError())
 
+// Returns the code of a failing library call (its message is already set).
+#define BF_CHECK_OK(expr)       \
+  do {                          \
+    const int _rc = (expr);     \
+    if (_rc != BF_OK) return _rc; \
+  } while (0)
+
 // Optional per-kernel timing (bf_prof_enable): an event pair around each launch.
 bool prof_enabled();
 void prof_begin(const char* name, hipStream_t st, int* token);

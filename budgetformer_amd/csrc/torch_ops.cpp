@@ -190,6 +190,62 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> sparse_attn_bwd(
   return {dq, dk, dv, dbias};
 }
 
+// Typed-edge (Exphormer) attention: type_mod = E, float32 [2, H, hn]; the index's ids carry the types.
+const float* type_mod_ptr(const at::Tensor& mod, int64_t H, int64_t hn, const at::Device& dev) {
+  require(mod, "type_mod", at::kFloat, dev);
+  TORCH_CHECK_VALUE(mod.numel() == 2 * H * hn && mod.size(0) == 2, "type_mod must be [2, ", H, ", ", hn, "] (got ",
+                    mod.sizes(), ")");
+  return mod.data_ptr<float>();
+}
+
+// Forward (bf_attn_fwd_typed): (out [n_q, H, hn] in q's dtype, Z [n_q, H] float32).
+std::tuple<at::Tensor, at::Tensor> sparse_attn_fwd_typed(const at::Tensor& q, const at::Tensor& k,
+                                                         const at::Tensor& v,
+                                                         const c10::List<std::optional<at::Tensor>>& index,
+                                                         at::IntArrayRef sizes, const at::Tensor& type_mod) {
+  TORCH_CHECK_VALUE(q.is_cuda(), "q must be a device tensor (got ", q.device(), ")");
+  const c10::DeviceGuard guard(q.device());
+  const at::Device dev = q.device();
+  const bf_attn_index idx = make_index(index, sizes, dev);
+  check_qkv(q, k, v, idx);
+  const int64_t H = q.size(1), hn = q.size(2);
+  const float* mod = type_mod_ptr(type_mod, H, hn, dev);
+  at::Tensor out = at::empty_like(q);
+  at::Tensor Z = at::empty({idx.n_q, H}, q.options().dtype(at::kFloat));
+  check_rc(bf_attn_fwd_typed(&idx, dtype_code(q), int32_t(H), int32_t(hn), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                             mod, out.data_ptr(), Z.data_ptr<float>(), stream_of(q)),
+           "bf::sparse_attn_fwd_typed");
+  return {out, Z};
+}
+
+// Backward (bf_attn_bwd_typed): (dq, dk, dv, dtype_mod [2, H, hn] float32).
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> sparse_attn_bwd_typed(
+    const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, const c10::List<std::optional<at::Tensor>>& index,
+    at::IntArrayRef sizes, const at::Tensor& type_mod, const at::Tensor& Z, const at::Tensor& dout) {
+  TORCH_CHECK_VALUE(q.is_cuda(), "q must be a device tensor (got ", q.device(), ")");
+  const c10::DeviceGuard guard(q.device());
+  const at::Device dev = q.device();
+  const bf_attn_index idx = make_index(index, sizes, dev);
+  check_qkv(q, k, v, idx);
+  const int64_t H = q.size(1), hn = q.size(2);
+  const float* mod = type_mod_ptr(type_mod, H, hn, dev);
+  require(dout, "dout", q.scalar_type(), dev);
+  require(Z, "Z", at::kFloat, dev);
+  TORCH_CHECK_VALUE(dout.sizes() == q.sizes() && Z.dim() == 2 && Z.size(0) == q.size(0) && Z.size(1) == H, "dout ",
+                    dout.sizes(), " / Z ", Z.sizes(), " do not match q ", q.sizes());
+  at::Tensor dq = at::empty_like(q), dk = at::empty_like(k), dv = at::empty_like(v);
+  at::Tensor dmod = at::empty({2, H, hn}, q.options().dtype(at::kFloat));
+  at::Tensor rowstat = at::empty({idx.n_q, H, 2}, q.options().dtype(at::kFloat));
+  const int64_t parts = bf_attn_typed_partials_floats(&idx, dtype_code(q), int32_t(H), int32_t(hn));
+  at::Tensor partials = at::empty({std::max<int64_t>(parts, 1)}, q.options().dtype(at::kFloat));
+  check_rc(bf_attn_bwd_typed(&idx, dtype_code(q), int32_t(H), int32_t(hn), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                             mod, Z.data_ptr<float>(), dout.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                             dmod.data_ptr<float>(), rowstat.data_ptr<float>(), partials.data_ptr<float>(),
+                             stream_of(q)),
+           "bf::sparse_attn_bwd_typed");
+  return {dq, dk, dv, dmod};
+}
+
 // ---------------------------------------------------------------- edge construction
 // Walks (bf_random_walk): int64 [n_q * P, L + 1], walk q*P + p starting at query q_lo + q.
 at::Tensor rw_walk(const at::Tensor& rowptr, const at::Tensor& col, int64_t q_lo, int64_t n_q, int64_t walks_per_node,
@@ -318,6 +374,10 @@ TORCH_LIBRARY(bf, m) {
   m.def("sparse_attn_bwd(Tensor q, Tensor k, Tensor v, Tensor?[] index, int[] sizes, Tensor Z, Tensor dout, "
         "Tensor? bias=None, Tensor? factor=None, bool need_dbias=False, float dropout_rate=0.0, int dropout_seed=0, "
         "int dropout_offset=0, float score_clamp=5.0) -> (Tensor, Tensor, Tensor, Tensor)");
+  m.def("sparse_attn_fwd_typed(Tensor q, Tensor k, Tensor v, Tensor?[] index, int[] sizes, Tensor type_mod) "
+        "-> (Tensor, Tensor)");
+  m.def("sparse_attn_bwd_typed(Tensor q, Tensor k, Tensor v, Tensor?[] index, int[] sizes, Tensor type_mod, "
+        "Tensor Z, Tensor dout) -> (Tensor, Tensor, Tensor, Tensor)");
   m.def("rw_walk(Tensor rowptr, Tensor col, int q_lo, int n_q, int walks_per_node, int walk_length, "
         "int philox_seed=0, int philox_offset=0, Tensor? u=None) -> Tensor");
   m.def("build_edge_table(Tensor rowptr, Tensor col, Tensor? walk_rec, Tensor in_ptr, Tensor in_src, int q_lo, "
@@ -332,6 +392,8 @@ TORCH_LIBRARY(bf, m) {
 TORCH_LIBRARY_IMPL(bf, CUDA, m) {
   m.impl("sparse_attn_fwd", &sparse_attn_fwd);
   m.impl("sparse_attn_bwd", &sparse_attn_bwd);
+  m.impl("sparse_attn_fwd_typed", &sparse_attn_fwd_typed);
+  m.impl("sparse_attn_bwd_typed", &sparse_attn_bwd_typed);
   m.impl("rw_walk", &rw_walk);
   m.impl("build_edge_table", &build_edge_table);
   m.impl("table_to_csr", &table_to_csr);

@@ -849,6 +849,8 @@ class AttentionIndex:
     # cannot synchronise). False: a plan copies its counts to pinned host memory behind its kernels and
     # a call reads them when it is launched, by which time the copy has landed
     device_counts: bool = False
+    # typed edges (Exphormer): bit 31 of each kv id and kq id is the entry's type; no query row is split
+    typed: bool = False
     # (items, split rows) of the query-side plan when the row lengths fix them (from_table)
     _q_known: Optional[tuple] = field(default=None, repr=False)
     _structs: dict = field(default_factory=dict, repr=False)          # C view per (backward, with ks)
@@ -1081,6 +1083,40 @@ class AttentionIndex:
         return idx
 
     @classmethod
+    def from_typed_coo(cls, edge_index, n_q: int, n_kv: Optional[int] = None, chunk: int = DEFAULT_CHUNK,
+                       item: int = DEFAULT_ITEM):
+        """Typed index of the reference's Exphormer edge set [3, E] (row 0 key/value node, row 1 query, row 2
+        the edge type, 0 or 1; models/exphormer_dist_node_level.py:77-121): bit 31 of every kv id (CSR,
+        rows ordered by (type, kv)) and kq id (reverse index, by (kv, CSR position)) is the entry's type,
+        so the typed kernels need no type array and no typed copy of K or V. No query row is split (a
+        query's row is its budget and expander edges); key rows are, as for any index."""
+        n_kv = n_q if n_kv is None else n_kv
+        if edge_index.dim() != 2 or edge_index.size(0) != 3:
+            raise ValueError(f"a typed edge set is [3, E] (got {tuple(edge_index.shape)})")
+        if 2 * n_kv >= 2 ** 31 or n_q >= 2 ** 31:
+            raise ValueError("typed indexes need n_q and 2 * n_kv below 2^31")
+        types = edge_index[2].to(torch.int64)
+        if types.numel() and (types.min().item() < 0 or types.max().item() > 1):
+            raise ValueError("edge types must be 0 or 1")
+        src = edge_index[0].to(torch.int64)
+        # rows ordered by (type, kv): the CSR of the type-shifted ids, then the type moved to bit 31
+        qptr, kvp = coo_to_csr(torch.stack([src + types * n_kv, edge_index[1].to(torch.int64)]), n_q, 2 * n_kv)
+        nnz = kvp.numel()
+        kvp = kvp.to(torch.int64)
+        one = kvp >= n_kv
+        kv_enc = torch.where(one, kvp - n_kv - 2 ** 31, kvp).to(torch.int32)
+        kptr, kq, ks = reverse_index(qptr, torch.where(one, kvp - n_kv, kvp).to(torch.int32), n_kv)
+        pos = qptr[kq.to(torch.int64)] + ks.to(torch.int64)
+        kq_enc = torch.where(kv_enc[pos] < 0, kq.to(torch.int64) - 2 ** 31, kq.to(torch.int64)).to(torch.int32)
+        idx = cls(n_q=n_q, n_kv=n_kv, qptr=qptr, kv_all=kv_enc, chunk=chunk, item=item, _nnz=nnz, typed=True)
+        # no split query rows: the query plan's threshold is above every row's length
+        idx.qplan = split_plan(qptr, nnz, min(nnz + 1, 2 ** 31 - 1), item, resolve=False,
+                               counts=idx._plan_counts(0), known=(0, 0), host_copy=False)
+        idx.kptr, idx.kq_all, idx.ks_all = kptr, kq_enc, ks
+        idx.ensure_backward()
+        return idx
+
+    @classmethod
     def from_coo(cls, edge_index, n_q: int, n_kv: Optional[int] = None, chunk: int = DEFAULT_CHUNK,
                  item: int = DEFAULT_ITEM):
         n_kv = n_q if n_kv is None else n_kv
@@ -1138,6 +1174,23 @@ def attn_forward(idx: AttentionIndex, q, k, v, bias=None, factor=None, dropout: 
         idx.nnz      # per-edge tensors are [nnz, H]: the index passes the count itself
     t, n = idx.op_args(backward=False)
     return N.load_ops().sparse_attn_fwd(q, k, v, t, n, bias, factor, *_dropout_op_args(dropout), float(score_clamp))
+
+
+def attn_forward_typed(idx: AttentionIndex, q, k, v, type_mod):
+    """Typed-edge (Exphormer) forward on a typed index (``AttentionIndex.from_typed_coo``): out [n_q,H,hn],
+    Z [n_q,H] float32; type_mod = E, float32 [2, H, hn] (bf::sparse_attn_fwd_typed)."""
+    if not idx.typed:
+        raise ValueError("attn_forward_typed needs a typed index (AttentionIndex.from_typed_coo)")
+    t, n = idx.op_args(backward=False)
+    return N.load_ops().sparse_attn_fwd_typed(q, k, v, t, n, type_mod)
+
+
+def attn_backward_typed(idx: AttentionIndex, q, k, v, type_mod, Z, dout):
+    """(dq, dk, dv, dE) of attn_forward_typed; dE float32 [2, H, hn] (bf::sparse_attn_bwd_typed)."""
+    if not idx.typed:
+        raise ValueError("attn_backward_typed needs a typed index (AttentionIndex.from_typed_coo)")
+    t, n = idx.op_args(backward=True)
+    return N.load_ops().sparse_attn_bwd_typed(q, k, v, t, n, type_mod, Z, dout)
 
 
 def kv_pass_variant(n_q: int, n_kv: int, dtype: torch.dtype, heads: int, head_dim: int) -> dict:

@@ -50,7 +50,8 @@ enum { BF_DTYPE_F32 = 0, BF_DTYPE_BF16 = 1, BF_DTYPE_F16 = 2 };
  *        its query's row instead of its CSR position;
  *   300  BF_DTYPE_F16 (float16 activations); the in-kernel dropout is keyed by
  *        (query row, slot) instead of the CSR position (a new mask for the same
- *        seed and offset).                                                   */
+ *        seed and offset); typed-edge attention (bf_attn_fwd_typed,
+ *        bf_attn_bwd_typed, bf_attn_typed_partials_floats).                  */
 #define BF_ABI_VERSION 300
 int bf_version(void);
 /* Message of the last failed call on this thread ("" if none). */
@@ -570,6 +571,25 @@ int bf_attn_bwd(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int3
                 const void* q, const void* k, const void* v, const float* bias, const float* factor,
                 const bf_attn_dropout* dropout, const float* Z, const void* dout, void* dq, void* dk, void* dv,
                 float* dbias, float* rowstat, float* partials, void* stream);
+
+/* Typed edges (Exphormer). Replace ExphormerCoreAttention.forward's typed
+ * path (models/exphormer_dist_node_level.py:77-121: an edge_index with a type
+ * row, score = clamp(sum_j k*q*E[type] / sqrt(hn), -5, 5), E =
+ * edge_proj(edge_type_emb(type)), no bias, factor or dropout) and its autograd.
+ * The index is typed: bit 31 of each kv id (query-major CSR) and of each kq id
+ * (reverse index) is the entry's type (0 or 1), the other bits the id (ids and
+ * sizes below 2^31); it has no token column and splits no query row
+ * (q_items = 0; key rows may be split). type_mod: E, float32 [2, H * hn].
+ * Forward: out [n_q, H * hn] in `dtype`, Z float32 [n_q, H].
+ * Backward: dq, dk, dv, and dtype_mod = dE, float32 [2, H * hn] (summed over
+ * the entries of each type in a fixed order); rowstat float32 [n_q, H, 2];
+ * partials float32 [bf_attn_typed_partials_floats].                        */
+int64_t bf_attn_typed_partials_floats(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim);
+int bf_attn_fwd_typed(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim, const void* q,
+                      const void* k, const void* v, const float* type_mod, void* out, float* Z, void* stream);
+int bf_attn_bwd_typed(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim, const void* q,
+                      const void* k, const void* v, const float* type_mod, const float* Z, const void* dout, void* dq,
+                      void* dk, void* dv, float* dtype_mod, float* rowstat, float* partials, void* stream);
 
 /* bf_attn_bwd for callers that cannot allocate (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
