@@ -22,8 +22,10 @@
 // equal values are the same pair; a real candidate (key << 32 | position)
 // orders by (key, position), the reference's tie-break, and its source comes
 // back from the key (the key is a bijection of the source for a fixed query).
-// Budgets and walk shapes are bounded only by LDS: a merged row of up to 768
-// ids, up to 8191 walk candidates per query.
+// Budgets and walk shapes are unbounded: a merged row of up to 768 ids is
+// ranked in LDS, a wider one by a workgroup in its own table slots; up to 8191
+// walk candidates per query are sorted in LDS, more are selected by a
+// streaming top-k that re-runs the walks (no staging memory either way).
 #include "bf_common.h"
 
 namespace bf {
@@ -375,7 +377,8 @@ __global__ __launch_bounds__(kThreads) void rw_select_kernel(
 constexpr int kGroup = 16;                  // lanes per query in the real-edge pass
 constexpr int kQPB = kThreads / kGroup;     // queries per block
 // Merged rows are listed in LDS, kQPB rows of `cap` = k_real + k_rw ids per
-// block plus as many duplicate flags: up to 96 KB, i.e. budgets of up to 768.
+// block plus as many duplicate flags: up to 96 KB, i.e. budgets of up to 768;
+// wider rows go to merge_rows_wide_kernel / assemble_rows_wide_kernel.
 constexpr size_t kRowLdsBytes = size_t(96) << 10;
 constexpr int kMaxRowCap = int(kRowLdsBytes / (2 * sizeof(int32_t) * (kThreads / 16)));
 #ifndef BF_SCAN_UNROLL
@@ -420,20 +423,58 @@ __device__ __forceinline__ void scan_topk(const int32_t* __restrict__ src, int64
   }
 }
 
-// Top-k_real of one hub's in-neighbour list with a whole workgroup: every
-// thread keeps a sorted register list of its strided share, then rounds of a
-// block-wide minimum (wave shuffles, then LDS across the 4 waves) pop the
-// winners in key order into out[0, cnt) (written by thread 0), KMAX per batch
-// (a thread's list holds only its KMAX smallest, so after KMAX pops the block
-// rescans above the last winner). Returns cnt, the same in every thread. Every
-// thread of the block must call it.
+// One round of a block-wide minimum over the heads lk[0] of every thread's
+// ascending register list (wave shuffles, then LDS across the 4 waves):
+// returns the smallest head, the same in every thread, and shifts it out of
+// its holder's list (the lowest thread on a tie; nothing moves when it is
+// kNone). Every thread of the block calls it.
+template <int KMAX>
+__device__ __forceinline__ uint64_t block_pop_min(uint64_t (&lk)[KMAX], uint64_t* wave_min, int* wave_win) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const uint64_t head = lk[0];
+  uint64_t m = head;
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint64_t y = shfl_xor_u64(m, o);
+    m = y < m ? y : m;
+  }
+  const uint64_t bal = __ballot(head == m);
+  if (lane == 0) {
+    wave_min[wave] = m;
+    wave_win[wave] = __ffsll((unsigned long long)bal) - 1;
+  }
+  __syncthreads();
+  uint64_t best = wave_min[0];
+  int best_wave = 0;
+#pragma unroll
+  for (int w = 1; w < kThreads / 64; ++w) {
+    if (wave_min[w] < best) {
+      best = wave_min[w];
+      best_wave = w;
+    }
+  }
+  const int winner = best_wave * 64 + wave_win[best_wave];
+  __syncthreads();
+  if (best != kNone && int(threadIdx.x) == winner) {
+#pragma unroll
+    for (int j = 0; j < KMAX - 1; ++j) lk[j] = lk[j + 1];
+    lk[KMAX - 1] = kNone;
+  }
+  return best;
+}
+
+// Top-k_real of one in-neighbour list with a whole workgroup (hubs, and every
+// row of a merged row too wide for LDS): every thread keeps a sorted register
+// list of its strided share, then rounds of block_pop_min pop the winners in
+// key order into out[0, cnt) (written by thread 0), KMAX per batch (a thread's
+// list holds only its KMAX smallest, so after KMAX pops the block rescans
+// above the last winner). Returns cnt, the same in every thread. Every thread
+// of the block must call it.
 template <int KMAX>
 __device__ __forceinline__ int hub_topk(const int64_t* __restrict__ in_ptr, const int32_t* __restrict__ in_src,
                                         int64_t q, int k_real, uint32_t kc, uint64_t* wave_min, int* wave_win,
                                         int32_t* out) {
   uint64_t lk[KMAX];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
   int cnt = 0;
   uint64_t floor = 0;
   while (cnt < k_real) {
@@ -444,35 +485,8 @@ __device__ __forceinline__ int hub_topk(const int64_t* __restrict__ in_ptr, cons
     int popped = 0;
     uint64_t best = kNone;
     while (popped < KMAX && cnt < k_real) {
-      const uint64_t head = lk[0];
-      uint64_t m = head;
-      for (int o = 1; o < 64; o <<= 1) {
-        const uint64_t y = shfl_xor_u64(m, o);
-        m = y < m ? y : m;
-      }
-      const uint64_t bal = __ballot(head == m);
-      if (lane == 0) {
-        wave_min[wave] = m;
-        wave_win[wave] = __ffsll((unsigned long long)bal) - 1;
-      }
-      __syncthreads();
-      best = wave_min[0];
-      int best_wave = 0;
-#pragma unroll
-      for (int w = 1; w < kThreads / 64; ++w) {
-        if (wave_min[w] < best) {
-          best = wave_min[w];
-          best_wave = w;
-        }
-      }
-      const int winner = best_wave * 64 + wave_win[best_wave];
-      __syncthreads();
+      best = block_pop_min<KMAX>(lk, wave_min, wave_win);
       if (best == kNone) return cnt;   // the same value in every thread: uniform exit
-      if (int(threadIdx.x) == winner) {
-#pragma unroll
-        for (int j = 0; j < KMAX - 1; ++j) lk[j] = lk[j + 1];
-        lk[KMAX - 1] = kNone;
-      }
       if (threadIdx.x == 0) out[cnt] = src_of(uint32_t(best >> 32), key_base(uint32_t(q), kc));
       ++cnt;
       ++popped;
@@ -649,6 +663,186 @@ __global__ __launch_bounds__(kThreads) void assemble_rows_kernel(
   __syncthreads();
   write_row(lst, dupf, gl, active, n_r + n_w, dedup, 0, table + (active ? qi : 0) * width, width,
             row_len + (active ? qi : 0));
+}
+
+// ---- Past the LDS staging: one row per workgroup, nothing staged.
+
+// Finishes a merged row that sits in its table slots out[0, n): with dedup
+// the set of values ascending, without it the multiset ascending, with
+// key_order the list as it stands; slots [len, width) get -1. Returns len, the
+// same in every thread. The sort is the all-ascending bitonic network over n
+// rounded up to a power of two (each compare-exchange puts the smaller value
+// at the lower index; the first step of a merge over blocks of k pairs slot i
+// with its mirror k-1-i in the block): the virtual slots past n hold +inf and
+// never move, so a comparator reaching past n is skipped and no slot past n is
+// read or written. The dedup compaction keeps a value that differs from its
+// left neighbour; a round reads its 256 slots before it writes, and a kept
+// value lands at or left of where it was read, so no round overwrites a slot
+// a later round reads with another value. Every thread of the block calls it,
+// with out[0, n) written and visible to the block.
+__device__ int wide_row_finish(int32_t* out, int n, int dedup, int key_order, int width, int* wave_cnt) {
+  if (!key_order && n > 1) {
+    int m2 = 1;
+    while (m2 < n) m2 <<= 1;
+    for (int k = 2; k <= m2; k <<= 1) {
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        for (int t = threadIdx.x; t < (m2 >> 1); t += kThreads) {
+          const int blk = t / j;
+          const int off = t - blk * j;
+          const int i = blk * 2 * j + off;
+          const int l = j == (k >> 1) ? blk * 2 * j + k - 1 - off : i + j;
+          if (l < n) {
+            const int32_t a = out[i], b = out[l];
+            if (b < a) {
+              out[i] = b;
+              out[l] = a;
+            }
+          }
+        }
+        __syncthreads();
+      }
+    }
+  }
+  int len = n;
+  if (dedup && n > 1) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    int base = 0;
+    for (int r0 = 0; r0 < n; r0 += kThreads) {
+      const int i = r0 + threadIdx.x;
+      int32_t v = 0;
+      bool keep = false;
+      if (i < n) {
+        v = out[i];
+        keep = i == 0 || out[i - 1] != v;
+      }
+      const uint64_t bal = __ballot(keep);
+      if (lane == 0) wave_cnt[wave] = __popcll(bal);
+      __syncthreads();
+      int at = base + __popcll(bal & ((uint64_t(1) << lane) - 1));
+      int total = 0;
+#pragma unroll
+      for (int w = 0; w < kThreads / 64; ++w) {
+        const int c = wave_cnt[w];
+        at += w < wave ? c : 0;
+        total += c;
+      }
+      if (keep) out[at] = v;
+      base += total;
+      __syncthreads();
+    }
+    len = base;
+  }
+  for (int c = len + threadIdx.x; c < width; c += kThreads) out[c] = -1;
+  return len;
+}
+
+// real_select_merge for budgets whose merged row does not fit the LDS
+// staging: a workgroup per row (grid-stride), the real top-k by the whole
+// block (hub_topk, for every row: a block per row already), the RW part
+// appended, then the row finished in place in its table slots.
+template <int KMAX>
+__global__ __launch_bounds__(kThreads) void merge_rows_wide_kernel(
+    const int64_t* __restrict__ in_ptr, const int32_t* __restrict__ in_src, int64_t num_nodes, int64_t q_lo,
+    const int32_t* __restrict__ qids, int64_t n_q, int k_real, uint32_t kc, const int32_t* __restrict__ rw_kv,
+    const int32_t* __restrict__ rw_cnt, int k_rw, int dedup, int key_order, int32_t* table, int width,
+    int32_t* __restrict__ row_len) {
+  __shared__ uint64_t wave_min[kThreads / 64];
+  __shared__ int wave_win[kThreads / 64];
+  __shared__ int wave_cnt[kThreads / 64];
+  for (int64_t li = blockIdx.x; li < n_q; li += gridDim.x) {
+    const int64_t q = row_query(qids, q_lo, li, num_nodes);
+    int32_t* const out = table + li * width;
+    const int n_r = (q >= 0 && k_real > 0) ? hub_topk<KMAX>(in_ptr, in_src, q, k_real, kc, wave_min, wave_win, out)
+                                           : 0;
+    const int n_w = (rw_kv != nullptr && k_rw > 0) ? min(rw_cnt[li], k_rw) : 0;
+    for (int i = threadIdx.x; i < n_w; i += kThreads) out[n_r + i] = rw_kv[li * k_rw + i];
+    __syncthreads();
+    const int len = wide_row_finish(out, n_r + n_w, dedup, key_order, width, wave_cnt);
+    if (threadIdx.x == 0) row_len[li] = len;
+  }
+}
+
+// assemble_rows for candidates too wide for the LDS staging: a workgroup per
+// row (grid-stride) copies the two prefixes into the row's table slots and
+// finishes the row there.
+__global__ __launch_bounds__(kThreads) void assemble_rows_wide_kernel(
+    const int32_t* __restrict__ real_kv, const int32_t* __restrict__ real_cnt, int real_stride, int b_r,
+    const int32_t* __restrict__ rw_kv, const int32_t* __restrict__ rw_cnt, int rw_stride, int b_w, int dedup,
+    int64_t n, int32_t* table, int width, int32_t* __restrict__ row_len) {
+  __shared__ int wave_cnt[kThreads / 64];
+  for (int64_t li = blockIdx.x; li < n; li += gridDim.x) {
+    int32_t* const out = table + li * width;
+    const int n_r = (real_kv && b_r > 0) ? min(real_cnt[li], b_r) : 0;
+    const int n_w = (rw_kv && b_w > 0) ? min(rw_cnt[li], b_w) : 0;
+    for (int i = threadIdx.x; i < n_r; i += kThreads) out[i] = real_kv[li * real_stride + i];
+    for (int i = threadIdx.x; i < n_w; i += kThreads) out[n_r + i] = rw_kv[li * rw_stride + i];
+    __syncthreads();
+    const int len = wide_row_finish(out, n_r + n_w, dedup, 0, width, wave_cnt);
+    if (threadIdx.x == 0) row_len[li] = len;
+  }
+}
+
+// rw_select for walk shapes whose P*L candidates do not fit one query's LDS
+// staging: a workgroup per query (grid-stride), lane p < P runs walk p, and the
+// selection streams instead of staging. Each round re-runs the P walks from
+// their start (a walk is a pure function of its Philox counters or injected
+// uniforms, and of the graph) and every lane keeps the KMAX smallest of its
+// candidates at or above `floor` as (key << 32 | p*L + l): values that are
+// unique, and that order as the staged (key << 32 | kv) do, since for one
+// query the key names the kv. Rounds of block_pop_min then pop up to KMAX
+// winners in order (after KMAX pops a lane's list may be spent, so the next
+// round rescans above the last winner). A pair drawn by several steps is
+// popped once per step: the selection keeps the multiplicity, as the sorting
+// kernels do. P*L < 2^32 (checked on the host).
+template <int KMAX>
+__global__ __launch_bounds__(kThreads) void rw_select_stream_kernel(
+    const int64_t* __restrict__ rowptr, const int32_t* __restrict__ col, const int4* __restrict__ rec,
+    int64_t num_nodes, int64_t q_lo, const int32_t* __restrict__ qids, int64_t n_q, int P, int L, int K,
+    uint32_t kc, const float* __restrict__ u, uint64_t seed, uint64_t offset, const int64_t* __restrict__ sub_ptr,
+    const int32_t* __restrict__ sub_src, int32_t* __restrict__ sel_kv, int32_t* __restrict__ sel_cnt) {
+  __shared__ uint64_t wave_min[kThreads / 64];
+  __shared__ int wave_win[kThreads / 64];
+  const int p = threadIdx.x;
+  for (int64_t qi = blockIdx.x; qi < n_q; qi += gridDim.x) {
+    const int64_t q = row_query(qids, q_lo, qi, num_nodes);
+    const uint32_t base = key_base(uint32_t(q), kc);
+    int32_t* const out = sel_kv + qi * K;
+    int cnt = 0;
+    uint64_t floor = 0;
+    bool more = q >= 0;                                   // the same in every thread
+    while (more && cnt < K) {
+      uint64_t lk[KMAX];
+#pragma unroll
+      for (int j = 0; j < KMAX; ++j) lk[j] = kNone;
+      if (p < P) {
+        RwWalk walk(rowptr, col, rec, num_nodes, q_lo, qids, qi, P, p, L, kc, u, seed, offset, sub_ptr, sub_src);
+        const uint32_t id0 = uint32_t(p) * uint32_t(L);
+        for (int l = 0; l < L; ++l) {
+          const uint32_t key = walk.step_key(l);
+          const uint64_t c = (uint64_t(key) << 32) | (id0 + uint32_t(l));
+          if (key != kNoKey && c >= floor && c < lk[KMAX - 1]) {
+#pragma unroll
+            for (int j = KMAX - 1; j > 0; --j) lk[j] = c < lk[j - 1] ? lk[j - 1] : (c < lk[j] ? c : lk[j]);
+            lk[0] = c < lk[0] ? c : lk[0];
+          }
+        }
+      }
+      int popped = 0;
+      uint64_t best = kNone;
+      while (popped < KMAX && cnt < K) {
+        best = block_pop_min<KMAX>(lk, wave_min, wave_win);
+        if (best == kNone) break;
+        if (threadIdx.x == 0) out[cnt] = src_of(uint32_t(best >> 32), base);
+        ++cnt;
+        ++popped;
+      }
+      more = best != kNone;
+      floor = best + 1;
+    }
+    for (int i = cnt + threadIdx.x; i < K; i += kThreads) out[i] = -1;
+    if (threadIdx.x == 0) sel_cnt[qi] = cnt;
+  }
 }
 
 // Inserts c into the ascending list lk (the largest value drops out): a
@@ -887,19 +1081,23 @@ int check_graph(const int64_t* ptr, const int32_t* idx, int64_t num_nodes, int64
 }
 
 // LDS the RW staging may take per block: past 64 KB a block of few queries would lose more to
-// occupancy than it gains; 64 KB holds one query of P*L = 8191 candidates.
+// occupancy than it gains; 64 KB holds one query of P*L = 8191 candidates. Larger shapes stream
+// (rw_select_stream_kernel).
 constexpr size_t kRwLdsBytes = size_t(64) << 10;
 
-// The staging slots per query (a power of two >= P*L) and queries per block of a P, L shape; 0 when
-// one query's slots exceed the staging LDS.
+// Blocks of the one-row-per-workgroup kernels (grid-stride past it): enough to fill the 256 CUs.
+constexpr int64_t kWideGrid = 65536;
+
+// The staging slots per query (a power of two >= P*L) and queries per block of a P, L shape; qpb = 0
+// (and M2 = 0) when one query's slots exceed the staging LDS.
 inline void rw_shape(int P, int L, int& M2, int& qpb) {
   const int64_t M = int64_t(P) * L;
   int64_t m2 = 1;
   while (m2 < M) m2 <<= 1;
-  M2 = int(m2);
   const int64_t by_lds = int64_t(kRwLdsBytes / ((m2 + 1) * sizeof(uint64_t)));
   const int64_t by_threads = kThreads / P;
   qpb = int(by_lds < by_threads ? by_lds : by_threads);
+  M2 = qpb >= 1 ? int(m2) : 0;
 }
 
 int launch_rw_select(const int64_t* rowptr, const int32_t* col, const void* walk_rec, int64_t num_nodes,
@@ -908,12 +1106,25 @@ int launch_rw_select(const int64_t* rowptr, const int32_t* col, const void* walk
                      int32_t* sel_kv, int32_t* sel_cnt, hipStream_t st) {
   int M2 = 0, qpb = 0;
   rw_shape(P, L, M2, qpb);
-  BF_CHECK_ARG(qpb >= 1, "rw_select: walks_per_node * walk_length = %lld candidates per query exceed the %zu-byte "
-               "LDS staging (at most %zu)", (long long)(int64_t(P) * L), kRwLdsBytes,
-               kRwLdsBytes / sizeof(uint64_t) - 1);
+  BF_CHECK_ARG(int64_t(P) * L < (int64_t(1) << 32), "rw_select: walks_per_node * walk_length = %lld candidates per "
+               "query (at most 2^32 - 1)", (long long)(int64_t(P) * L));
   BF_CHECK_ARG((reinterpret_cast<uintptr_t>(walk_rec) & 15) == 0, "rw_select: walk records must be 16-byte aligned");
   if (n_q == 0) return BF_OK;
   const int4* rec = static_cast<const int4*>(walk_rec);
+  if (qpb < 1) {
+    // past the LDS staging: stream the selection, a workgroup per query
+    const dim3 grid(unsigned(n_q < kWideGrid ? n_q : kWideGrid));
+#define BF_LAUNCH_RW_STREAM(KM)                                                                                   \
+  BF_LAUNCH("rw_select_stream_kernel", rw_select_stream_kernel<KM>, grid, dim3(kThreads), 0, st, rowptr, col, rec,  \
+            num_nodes, q_lo, qids, n_q, P, L, K, kc, u, seed, offset, sub_ptr, sub_src, sel_kv, sel_cnt)
+    if (K <= 8)
+      BF_LAUNCH_RW_STREAM(8);
+    else
+      BF_LAUNCH_RW_STREAM(32);
+#undef BF_LAUNCH_RW_STREAM
+    BF_CHECK_LAUNCH();
+    return BF_OK;
+  }
   int R = 1;
   while (R < L) R <<= 1;
   if (P <= 64 && (P & (P - 1)) == 0 && R <= 16) {
@@ -958,9 +1169,9 @@ int launch_real_merge(const int64_t* in_ptr, const int32_t* in_src, int64_t num_
                       const int32_t* rw_cnt, int k_rw, int dedup, int key_order, int32_t* table, int width,
                       int32_t* row_len, const int32_t* hubs, int64_t n_hubs, int64_t hub_threshold,
                       int32_t* hub_sel, int32_t* hub_cnt, hipStream_t st, LightSplit split = LightSplit()) {
-  BF_CHECK_ARG(k_real + (rw_kv ? k_rw : 0) <= kMaxRowCap,
-               "edge build: budget k_real + k_rw = %d exceeds the %d a merged row can hold in LDS",
-               k_real + (rw_kv ? k_rw : 0), kMaxRowCap);
+  const int64_t row_ids = int64_t(k_real) + (rw_kv ? k_rw : 0);
+  BF_CHECK_ARG(row_ids < (int64_t(1) << 30), "edge build: budget k_real + k_rw = %lld too large",
+               (long long)row_ids);
   if (n_q == 0) return BF_OK;
   const bool light = split.light_max >= 0 && qids == nullptr && !key_order && k_real <= 16 &&
                      (rw_kv == nullptr || k_rw <= 16);
@@ -994,6 +1205,14 @@ int launch_real_merge(const int64_t* in_ptr, const int32_t* in_src, int64_t num_
     else
       BF_LAUNCH_FUSED(8, 16);
 #undef BF_LAUNCH_FUSED
+    BF_CHECK_LAUNCH();
+    return BF_OK;
+  }
+  if (row_ids > kMaxRowCap) {
+    // a merged row wider than the LDS staging: a workgroup per row, finished in its table slots
+    BF_LAUNCH("merge_rows_wide_kernel", merge_rows_wide_kernel<32>, dim3(unsigned(n_q < kWideGrid ? n_q : kWideGrid)),
+              dim3(kThreads), 0, st, in_ptr, in_src, num_nodes, q_lo, qids, n_q, k_real, kc, rw_kv, rw_cnt, k_rw,
+              dedup, key_order, table, width, row_len);
     BF_CHECK_LAUNCH();
     return BF_OK;
   }
@@ -1195,12 +1414,20 @@ extern "C" int bf_assemble_rows(const int32_t* real_kv, const int32_t* real_cnt,
                b_real, real_stride);
   BF_CHECK_ARG(b_rw <= rw_stride || rw_kv == nullptr, "assemble_rows: b_rw %d exceeds the RW stride %d", b_rw,
                rw_stride);
-  BF_CHECK_ARG(b_real + b_rw <= kMaxRowCap, "assemble_rows: b_real + b_rw = %d exceeds the %d a row can hold in LDS",
-               b_real + b_rw, kMaxRowCap);
+  BF_CHECK_ARG(int64_t(b_real) + b_rw < (int64_t(1) << 30), "assemble_rows: b_real + b_rw too large");
   BF_CHECK_ARG(width >= b_real + b_rw && width >= 1, "assemble_rows: width %d < %d", width, b_real + b_rw);
   BF_CHECK_ARG((b_real == 0 || real_cnt) && (b_rw == 0 || rw_cnt), "assemble_rows: counts missing");
   BF_CHECK_ARG((table && row_len) || n_rows == 0, "assemble_rows: null output");
   if (n_rows == 0) return BF_OK;
+  if (b_real + b_rw > kMaxRowCap) {
+    // a row wider than the LDS staging: a workgroup per row, finished in its table slots
+    BF_LAUNCH("assemble_rows_wide_kernel", assemble_rows_wide_kernel,
+              dim3(unsigned(n_rows < kWideGrid ? n_rows : kWideGrid)), dim3(kThreads), 0, as_stream(stream),
+              b_real ? real_kv : nullptr, real_cnt, real_stride, b_real, b_rw ? rw_kv : nullptr, rw_cnt, rw_stride,
+              b_rw, dedup ? 1 : 0, n_rows, table, width, row_len);
+    BF_CHECK_LAUNCH();
+    return BF_OK;
+  }
   const int cap = b_real + b_rw > 0 ? b_real + b_rw : 1;
   BF_LAUNCH("assemble_rows_kernel", assemble_rows_kernel, dim3(unsigned(ceil_div(n_rows, kQPB))), dim3(kThreads),
             size_t(2) * kQPB * cap * sizeof(int32_t), as_stream(stream), b_real ? real_kv : nullptr, real_cnt,

@@ -113,6 +113,50 @@ def test_edge_table_past_the_former_caps(hip_device, b_r, b_w, P, L):
     assert ref_len.max() > 32
 
 
+@pytest.mark.parametrize("b_r,b_w,P,L", [(512, 512, 8, 100), (8, 64, 10, 1000), (0, 600, 100, 100),
+                                         (512, 512, 100, 100)])
+def test_edge_table_wide_rows_and_long_walks(hip_device, b_r, b_w, P, L):
+    """Past the LDS staging. B = 1024 as (512, 512): every merged row is ranked by a workgroup in its own
+    table slots (17 rows of (512, 512, 8, 100) hold more than 768 ids). P*L = 10,000 walk candidates per
+    query: the streaming top-k re-runs the walks per batch of winners. (8, 64, 10, 1000) draws each pair
+    about six times, so the multiset selection (64) and the merge's set union (12 to 24) both count
+    repeats. Walk records, injected uniforms; bit-exact against the oracle."""
+    from budgetformer_amd.edges import build_attention_edges
+    n = 1500
+    rowptr, col = _graph(n, 300_000, seed=b_r + b_w + P)
+    g = _dev_graph(rowptr, col, n, hip_device)
+    u = np.random.default_rng(P * L + b_w).random((n * P, L), dtype=np.float32)
+    tab = build_attention_edges(g, real_edges_per_query=b_r, rw_edges_per_query=b_w, walk_length=L,
+                                walks_per_node=P, edge_seed=42, u=torch.from_numpy(u).to(hip_device))
+    ref_t, ref_len = et.build_edge_table(rowptr, col, n, b_r, b_w, L, P, 42, u)
+    assert tab.width == b_r + b_w
+    assert np.array_equal(tab.row_len.cpu().numpy(), ref_len)
+    assert np.array_equal(tab.table.cpu().numpy(), ref_t)
+    if (b_r, P) == (512, 8):
+        assert (ref_len > 768).sum() > 10
+
+
+def test_streamed_walk_selection_under_philox(hip_device):
+    """The streaming RW selection (P*L = 10,000) with the in-kernel Philox uniforms, over the walk
+    records and over rowptr/col, for the full range and a shard: equal to the oracle's table on the
+    same counter stream."""
+    from budgetformer_amd import hip_ops
+    from budgetformer_amd.edges import build_attention_edges
+    n, P, L, b_r, b_w, seed = 1000, 50, 200, 4, 40, 43
+    rowptr, col = _graph(n, 60_000, seed=17)
+    g = _dev_graph(rowptr, col, n, hip_device)
+    tab = build_attention_edges(g, real_edges_per_query=b_r, rw_edges_per_query=b_w, walk_length=L,
+                                walks_per_node=P, edge_seed=seed)
+    u = philox.walk_uniforms(0, n, P, L, seed)
+    ref_t, ref_len = et.build_edge_table(rowptr, col, n, b_r, b_w, L, P, seed, u)
+    assert np.array_equal(tab.row_len.cpu().numpy(), ref_len)
+    assert np.array_equal(tab.table.cpu().numpy(), ref_t)
+    a = hip_ops.rw_select(g.rowptr, g.col, 200, 500, P, L, b_w, 79, philox_seed=seed)
+    b = hip_ops.rw_select(g.rowptr, g.col, 200, 500, P, L, b_w, 79, philox_seed=seed,
+                          walk_rec=hip_ops.walk_records(g.rowptr, g.col))
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1]) and int(a[1].min()) == b_w
+
+
 def test_edge_table_shard_matches_full(hip_device):
     from budgetformer_amd.edges import build_attention_edges
     n, P, L = 3000, 2, 4

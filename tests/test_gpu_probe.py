@@ -93,3 +93,28 @@ def test_probe_rows_equal_training_rows_under_philox(hip_device):
     pb2 = build_probe(g, F, max_real=0, max_rw=5, walk_length=L, walks_per_node=P, edge_seed=seed, use_real=False,
                       u=torch.from_numpy(u_F).to(hip_device))
     assert torch.equal(pb2.table(0, 5).table, tab.table)
+
+
+def test_probe_wide_budgets_and_long_walks(hip_device):
+    """The probe past the LDS staging: the real ranking at max_real = 800 (a workgroup per row, key
+    order kept in the row's own slots), the RW ranking of P*L = 10,000 candidates with the real pool
+    subtracted (streaming top-k), and candidates of up to 1,000 ids assembled in their table slots;
+    bit-exact against the oracle's pools."""
+    from budgetformer_amd.probe import build_probe
+    n, P, L, seed = 1500, 100, 100, 11
+    g, ei = _setup(n, 300_000, 29, hip_device)
+    rng = np.random.default_rng(4)
+    u_full = rng.random((n * P, L), dtype=np.float32)
+    Fn = np.sort(rng.choice(n, 200, replace=False))
+    u_F = torch.from_numpy(u_full.reshape(n, P, L)[Fn].reshape(-1, L)).to(hip_device)
+    pb = build_probe(g, torch.from_numpy(Fn).to(hip_device), max_real=800, max_rw=500, walk_length=L,
+                     walks_per_node=P, edge_seed=seed, u=u_F)
+    pools = et.probe_edge_pools(ei, n, Fn, L, P, u_full)
+    assert int(pb.real[1].max()) > 768
+    for b_r, b_w in [(800, 200), (500, 500), (300, 300), (800, 0), (0, 500)]:
+        got = pb.table(b_r, b_w).to_edge_index().cpu().numpy()
+        ref = et.assemble_edges_from_pools(pools, n, b_r, b_w, seed)
+        if b_r > 0 and b_w > 0:
+            assert np.array_equal(got, ref)
+        else:
+            assert _pairs(got) == _pairs(ref)
