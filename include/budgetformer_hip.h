@@ -166,8 +166,10 @@ int bf_walk_records(const int64_t* rowptr, const int32_t* col, int64_t num_nodes
  * holds (walks[w,d], q) for its own walks w, d=1..L, kept iff d==1 or the walk
  * moved at step d; the k_rw smallest keys key(kv, q, seed) are kept counting
  * multiplicity. Output sel_kv int32 [n_q, k_rw] (key order, -1 padded),
- * sel_cnt int32 [n_q]. A query's P*L candidates are ranked in LDS (at most
- * 8191 per query). walk_rec: NULL, or bf_walk_records' records of this
+ * sel_cnt int32 [n_q]. Any P*L below 2^32: up to 8191 candidates per query
+ * are sorted in LDS, more are selected by a streaming top-k (a workgroup per
+ * query re-runs its walks per batch of winners; nothing is staged), with the
+ * same result. walk_rec: NULL, or bf_walk_records' records of this
  * rowptr/col (16-byte aligned): each step then reads one record instead of
  * the rowptr pair and col; the walks are the same.                           */
 int bf_rw_select(const int64_t* rowptr, const int32_t* col, const void* walk_rec, int64_t num_nodes,
@@ -212,7 +214,9 @@ int bf_rw_select_rows(const int64_t* rowptr, const int32_t* col, const void* wal
  *     ascending (hubs included), and those take the 16-lane group path.
  *     light_max < 0: no split (heavy ignored). The table is the same either way.
  *   table int32 [n_q, width] rows ascending, -1 padded; row_len int32 [n_q].
- *   Requires k_real <= 32, k_rw <= 32, width >= k_real + k_rw.               */
+ *   Any budgets, width >= k_real + k_rw: a merged row of up to 768 ids is
+ *   ranked in LDS, a wider one by a workgroup in its own table slots (the
+ *   hub arrays are then not used).                                          */
 int bf_real_select_merge(const int64_t* in_ptr, const int32_t* in_src, int64_t num_nodes,
                          int64_t q_lo, int64_t n_q, int32_t k_real, int64_t key_seed,
                          const int32_t* rw_kv, const int32_t* rw_cnt, int32_t k_rw,
@@ -241,8 +245,10 @@ int bf_real_select_rows(const int64_t* in_ptr, const int32_t* in_src, int64_t nu
  * _assemble_edges_from_pools merges them (utils/fullgraph_sp_support.py:
  * 1824-1879 -> gt_sp/utils.py:877-887): dedup != 0 gives the set union
  * ascending (both parts globally non-empty), else the multiset ascending.
- * NULL real_kv / rw_kv (or a zero budget) drops that part. b_real + b_rw <= 64.
- *   table int32 [n_rows, width] (-1 padded), row_len int32 [n_rows].        */
+ * NULL real_kv / rw_kv (or a zero budget) drops that part. Any budgets; a
+ * row of more than 768 ids is finished by a workgroup in its table slots.
+ *   table int32 [n_rows, width] (-1 padded), row_len int32 [n_rows], not
+ *   overlapping the selections.                                            */
 int bf_assemble_rows(const int32_t* real_kv, const int32_t* real_cnt, int32_t real_stride,
                      int32_t b_real, const int32_t* rw_kv, const int32_t* rw_cnt,
                      int32_t rw_stride, int32_t b_rw, int32_t dedup, int64_t n_rows,
