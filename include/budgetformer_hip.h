@@ -208,7 +208,7 @@ int bf_rw_select_rows(const int64_t* rowptr, const int32_t* col, const void* wal
  *     hub_threshold, or n_hubs = 0): their top-k is computed by one workgroup
  *     each into hub_sel int32 [n_hubs, k_real] / hub_cnt int32 [n_hubs]
  *     (caller-provided scratch) instead of by a 16-lane group.
- *   light_max >= 0 (with k_real <= 8, k_rw <= 8) splits the work: queries of
+ *   light_max >= 0 (with k_real <= 16, k_rw <= 16) splits the work: queries of
  *     in-degree <= light_max are served one per thread; heavy int32 [n_heavy]
  *     must list every query of [q_lo, q_lo+n_q) with in-degree > light_max,
  *     ascending (hubs included), and those take the 16-lane group path.
@@ -617,10 +617,10 @@ int bf_attn_bwd_noalloc(const bf_attn_index* idx, int32_t dtype, int32_t num_hea
 /* How bf_attn_bwd runs its key-major (dk/dv) pass on this index, for callers
  * and tests that need to know which kernel instance a shape takes (host-only,
  * launches nothing): rows_per_group = short kv rows per lane group (1, or 4
- * past 16M kv rows in float32 / 1M in bfloat16); stream_rows = 1 when the q
- * and dO tables exceed the 256 MB Infinity Cache and are gathered
+ * past 16M kv rows in float32 / 1M in the 2-byte dtypes); stream_rows = 1 when
+ * the q and dO tables exceed the 256 MB Infinity Cache and are gathered
  * non-temporally; prefetch_slots = 1 when a group's row slots are loaded in
- * one round before its loop (bfloat16 with several rows per group). No
+ * one round before its loop (a 2-byte dtype with several rows per group). No
  * reference counterpart: the reference's scatter backward has no such choice. */
 int bf_attn_bwd_kv_variant(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
                            int32_t* rows_per_group, int32_t* stream_rows, int32_t* prefetch_slots);
