@@ -322,7 +322,8 @@ def main(argv=None):
         rec = run(name, args.steps, args.warmup, chunk, item, with_cpu=not args.no_cpu_baseline)
         records.append({k: rec[k] for k in ("config", "dtype", "steps", "warmup", "ms_per_step", "value", "unit",
                                             "value_basis", "attn_fwd_bwd_ms", "edge_build_ms", "attention",
-                                            "builder", "roofline", "kernels", "cpu_baseline") if k in rec})
+                                            "builder", "roofline", "gather_floor", "kernels", "cpu_baseline")
+                        if k in rec})
     if records:
         result["extra_configs"] = records
     print(json.dumps(result), flush=True)
@@ -478,6 +479,11 @@ def run(config, steps, warmup, chunk=None, item=None, with_cpu=True):
                 "traffic_frac": round(dom["traffic_gbs"] / HBM_PEAK_GBS, 4) if "traffic_gbs" in dom else None,
                 "traffic_basis": "the kernel's L2-to-fabric bytes per dispatch (request-size counter sums) / its "
                                  "HIP-event average duration"}
+    floor = gather_floor(idx, q, k, v, dout, H, s_bytes, D, kv_var, tok_row, chunk, kernels,
+                         reps=max(3, min(steps, 10)))
+    if dominant == "attn_bwd_kv_kernel":
+        roofline["gather_floor_ms"] = floor["kv_pass"]["ms"]
+        roofline["frac_of_gather_floor"] = round(floor["kv_pass"]["ms"] / dom["avg_ms"], 4)
     # the layer's traffic: every attention kernel's counter bytes per dispatch times its launches per layer
     attn_kernels = [n_ for n_ in kernels if n_.startswith("attn_")]
     layer_traffic = None
@@ -556,6 +562,7 @@ def run(config, steps, warmup, chunk=None, item=None, with_cpu=True):
             "table_entries_per_s": round(table_entries / (build_ms * 1e-3), 1),
         },
         "roofline": roofline,
+        "gather_floor": floor,
         "kernels": kernels,
     }
 
@@ -563,6 +570,68 @@ def run(config, steps, warmup, chunk=None, item=None, with_cpu=True):
         result["cpu_baseline"] = cpu_baseline(cfg, g, tab, idx, q, k, v, dout, s_bytes, D, H)
     del q, k, v, dout, tab, idx, g
     return result
+
+
+def gather_floor(idx, q, k, v, dout, H, s_bytes, D, kv_var, tok_row, chunk, kernels, reps):
+    """The gathers of each attention pass alone, timed with bf_gather_probe on the pass's own ids and tables
+    (HIP events on the library's stream, the mean over ``reps`` launches after one untimed launch):
+
+    - key-major (dk/dv) pass: per reverse entry the q and dO rows of its query and the query's row-stats
+      record ({1/D', Delta/D'} per head, 8·H bytes), non-temporal where the pass streams them; kv 0's
+      segment is left out when the dq pass sums the token column, and query 0's entries of the unsplit kv
+      rows when the pass takes the token row from its per-workgroup copy;
+    - query-major (forward, dq) passes: per entry the k and v rows of its kv id.
+
+    The passes also read and write their rows sequentially and do the arithmetic, so a pass's time over its
+    floor is at least 1; near 1, the pass is as fast as its gathers can be served."""
+    import torch
+
+    from budgetformer_amd import _native as N
+    from budgetformer_amd import hip_ops
+
+    dev = q.device
+    row = D * s_bytes
+    stat = torch.zeros(idx.n_q, H, 2, dtype=torch.float32, device=dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    kq = idx.kq
+    if idx.token_column:
+        kq = kq[int(idx.kptr[1].item()):]
+    if tok_row:
+        rows = hip_ops.expand_rows(idx.kptr, idx.nnz)
+        if idx.token_column:
+            rows = rows[int(idx.kptr[1].item()):]
+        lens = idx.kptr[rows + 1] - idx.kptr[rows]
+        kq = kq[(kq != 0) | (lens > chunk)]
+        del rows, lens
+    kq = kq.contiguous()
+    kv = idx.kv.contiguous()
+    st = hip_ops._stream(dev)
+
+    def timed(t0, b0, t1, b1, t2, b2, ids, nt):
+        def launch():
+            N.call("bf_gather_probe", hip_ops._p(t0), b0, hip_ops._p(t1), b1, hip_ops._p(t2), b2, hip_ops._p(ids),
+                   ids.numel(), 0x7FFFFFFF, int(nt), hip_ops._p(sink), st)
+        launch()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            launch()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    kv_ms = timed(q, row, dout, row, stat, 8 * H, kq, kv_var["stream_rows"])
+    qp_ms = timed(k, row, v, row, None, 0, kv, False)
+    out = {"basis": gather_floor.__doc__.split("\n\n")[0].replace("\n", " ").replace("    ", " ")}
+    for key, ms, ids, per, names in (("kv_pass", kv_ms, kq, 2 * row + 8 * H, ("attn_bwd_kv_kernel",)),
+                                     ("q_passes", qp_ms, kv, 2 * row, ("attn_fwd_kernel", "attn_bwd_q_kernel"))):
+        rec = {"ids": int(ids.numel()), "bytes_per_id": per, "ms": round(ms, 5),
+               "record_gbs": round(ids.numel() * per / (ms * 1e-3) / 1e9, 1)}
+        for name in names:
+            if name in kernels:
+                rec[f"{name}_over_floor"] = round(kernels[name]["avg_ms"] / ms, 3)
+        out[key] = rec
+    return out
 
 
 def cpu_baseline(cfg, g, tab, idx, q, k, v, dout, s_bytes, D, H):

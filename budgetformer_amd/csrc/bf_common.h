@@ -53,12 +53,19 @@ struct ProfPause {
   bool prev;
 };
 
-#define BF_LAUNCH(name, kern, grid, block, lds, st, ...)                 \
-  do {                                                                  \
-    int _bf_tok = -1;                                                   \
-    if (::bf::prof_enabled()) ::bf::prof_begin(name, st, &_bf_tok);     \
-    hipLaunchKernelGGL(kern, grid, block, lds, st, __VA_ARGS__);        \
-    if (_bf_tok >= 0) ::bf::prof_end(_bf_tok, st);                      \
+// Launches a kernel (in a function returning an error code). A dispatch counts
+// its work-items per dimension in 32 bits, so a grid of 2^32 or more would be
+// cut short without an error: such a launch is refused instead.
+#define BF_LAUNCH(name, kern, grid, block, lds, st, ...)                                        \
+  do {                                                                                         \
+    const dim3 _bf_g = (grid), _bf_b = (block);                                                \
+    BF_CHECK_ARG(uint64_t(_bf_g.x) * _bf_b.x <= 0xffffffffull,                                  \
+                 "%s: a grid of %llu work-items (a dispatch takes at most 2^32 - 1)", name,     \
+                 (unsigned long long)(uint64_t(_bf_g.x) * _bf_b.x));                            \
+    int _bf_tok = -1;                                                                          \
+    if (::bf::prof_enabled()) ::bf::prof_begin(name, st, &_bf_tok);                            \
+    hipLaunchKernelGGL(kern, _bf_g, _bf_b, lds, st, __VA_ARGS__);                              \
+    if (_bf_tok >= 0) ::bf::prof_end(_bf_tok, st);                                             \
   } while (0)
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }

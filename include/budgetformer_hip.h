@@ -51,8 +51,12 @@ enum { BF_DTYPE_F32 = 0, BF_DTYPE_BF16 = 1, BF_DTYPE_F16 = 2 };
  *   300  BF_DTYPE_F16 (float16 activations); the in-kernel dropout is keyed by
  *        (query row, slot) instead of the CSR position (a new mask for the same
  *        seed and offset); typed-edge attention (bf_attn_fwd_typed,
- *        bf_attn_bwd_typed, bf_attn_typed_partials_floats).                  */
-#define BF_ABI_VERSION 300
+ *        bf_attn_bwd_typed, bf_attn_typed_partials_floats);
+ *   301  bf_gather_probe (calibration); bf_rw_select, bf_rw_select_rows,
+ *        bf_real_select_merge, bf_real_select_rows and bf_assemble_rows take
+ *        any budget and walk shape (they used to reject rows above 768 ids
+ *        and more than 8191 walk candidates per query).                      */
+#define BF_ABI_VERSION 301
 int bf_version(void);
 /* Message of the last failed call on this thread ("" if none). */
 const char* bf_last_error(void);
@@ -624,6 +628,24 @@ int bf_attn_bwd_noalloc(const bf_attn_index* idx, int32_t dtype, int32_t num_hea
  * reference counterpart: the reference's scatter backward has no such choice. */
 int bf_attn_bwd_kv_variant(const bf_attn_index* idx, int32_t dtype, int32_t num_heads, int32_t head_dim,
                            int32_t* rows_per_group, int32_t* stream_rows, int32_t* prefetch_slots);
+
+/* ======================================================================
+ * Measurement
+ * ====================================================================== */
+
+/* Gather-rate calibration (no reference counterpart: it serves the benchmark,
+ * as a plain copy kernel serves a bandwidth figure). For e in [0, n_ids) reads
+ * row ids[e] & id_mask of each non-NULL table t0..t2 (row_bytes of 16 to 512,
+ * a multiple of 16; rows at a stride of their size; 16-byte aligned) with
+ * 16-byte loads, non-temporal when `nontemporal` != 0, and writes nothing
+ * (sink, a device uint32, is written only in the practically impossible case
+ * that the folded words equal a fixed constant). The ids must lie in the
+ * tables. Timing it on an attention pass's own ids and tables (the key-major
+ * pass: kq over q, dO and the row stats; the query-major passes: kv over k
+ * and v) gives the time those gathers alone take.                          */
+int bf_gather_probe(const void* t0, int32_t row_bytes0, const void* t1, int32_t row_bytes1, const void* t2,
+                    int32_t row_bytes2, const int32_t* ids, int64_t n_ids, uint32_t id_mask,
+                    int32_t nontemporal, uint32_t* sink, void* stream);
 
 #ifdef __cplusplus
 }

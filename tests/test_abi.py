@@ -18,7 +18,7 @@ def test_library_loads_and_exports_every_header_symbol():
     # the exact ABI version the header declares: a binding written against another one must not load
     import re
     declared = int(re.search(r"#define BF_ABI_VERSION (\d+)", open(N._HEADER).read()).group(1))
-    assert declared == 300 == N.ABI_VERSION
+    assert declared == 301 == N.ABI_VERSION
     assert lib.bf_version() == declared
 
 
@@ -55,6 +55,24 @@ def test_argument_errors_surface_as_exceptions():
         with pytest.raises(ValueError, match="score_clamp"):
             N.call("bf_attn_fwd", C.byref(idx), N.BF_DTYPE_F32, 2, 8, bad, None, None, None, None, None, None,
                    None, None, None, None)
+
+
+def test_gather_probe_arguments_checked_on_the_host():
+    """bf_gather_probe refuses rows that are not 16..512 bytes in 16-byte steps, an unaligned table, a call
+    with no table and ids missing for a non-empty list, before any launch; an empty id list launches
+    nothing (host buffers, never read)."""
+    buf = (C.c_int64 * 8)()
+    p = C.cast(buf, C.c_void_p)
+    for rb in (8, 20, 528):
+        with pytest.raises(ValueError, match="row of"):
+            N.call("bf_gather_probe", p, rb, None, 0, None, 0, p, 4, 0x7FFFFFFF, 0, p, None)
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        N.call("bf_gather_probe", C.c_void_p(p.value + 4), 64, None, 0, None, 0, p, 4, 0x7FFFFFFF, 0, p, None)
+    with pytest.raises(ValueError, match="no table"):
+        N.call("bf_gather_probe", None, 0, None, 0, None, 0, p, 4, 0x7FFFFFFF, 0, p, None)
+    with pytest.raises(ValueError, match="bad ids"):
+        N.call("bf_gather_probe", p, 64, None, 0, None, 0, None, 4, 0x7FFFFFFF, 0, p, None)
+    N.call("bf_gather_probe", p, 64, p, 256, p, 512, p, 0, 0x7FFFFFFF, 1, p, None)
 
 
 def test_walk_record_arguments_checked_on_the_host():
