@@ -70,6 +70,19 @@ struct ProfPause {
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// The chip's 8 XCDs each have their own L2, and workgroup i of a launch runs on
+// XCD i % 8. xcd_slot maps workgroup i of n to a slot such that each XCD takes
+// one contiguous run of slots (XCD x: slots [x*q + min(x, r), ...) with n =
+// 8q + r, q + 1 of them for x < r, else q), in its own dispatch order; a
+// bijection of [0, n). Neighbouring slots then share their L2 lines in one
+// L2 instead of eight.
+constexpr int kXcds = 8;
+__device__ __forceinline__ int64_t xcd_slot(int64_t i, int64_t n) {
+  const int64_t q = n / kXcds, r = n % kXcds;
+  const int64_t x = i % kXcds, local = i / kXcds;
+  return x * q + (x < r ? x : r) + local;
+}
+
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 inline bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }

@@ -15,7 +15,7 @@
 // rocPRIM's onesweep sort on the reverse-index keys of the benchmark builds
 // (gfx950): 0.82M keys, 18 bits: 39 us (2 passes of 9 bits) vs 76 us; 31M
 // keys, 22 bits: 584 us vs 614 us; 32M keys: 625 vs 639 us; 210M keys, 27
-// bits: 5.28 ms vs 5.13 ms (onesweep's single read per pass wins there).
+// bits: 4.57 ms vs 5.13 ms.
 #pragma once
 
 #include <cstdint>
@@ -30,8 +30,13 @@ constexpr int kWaves = kThreads / 64;
 
 // The digit width and tile of a sort: 9-bit digits when they save a pass
 // (18 and 27 bits), else 8. 9-bit tiles grow with the key count (2048 keys up
-// to 4M keys, 4096 up to 32M, then 6144: fewer tiles, a smaller count array;
-// at 210M keys 5.28 ms against 5.61 with 4096); 8-bit tiles hold 4096.
+// to 4M keys, 4096 up to 32M, then 8192: fewer tiles, a smaller count array,
+// longer digit runs per tile to write; at 210M keys the scatter pass takes
+// 0.99 ms with 8192-key tiles, 1.03 with 6144 and 1.81 with 12288, whose 256
+// VGPRs and 110 KB of LDS leave one wave per SIMD); 8-bit tiles hold 4096.
+// Both passes map workgroups to tiles XCD by XCD (xcd_slot), so the tiles
+// that share a line of the digit-major count array meet in one L2: the
+// scatter pass at 210M keys went from 1.18 to 1.03 ms with it.
 struct Plan {
   int radix;
   int items;
@@ -39,11 +44,14 @@ struct Plan {
   int64_t tiles;
 };
 
+#ifndef BF_SORT_ITEMS_LARGE
+#define BF_SORT_ITEMS_LARGE 32
+#endif
 inline Plan make_plan(int64_t n, int bits) {
   Plan p{};
   const int p8 = (bits + 7) / 8, p9 = (bits + 8) / 9;
   p.radix = p9 < p8 ? 9 : 8;
-  p.items = p.radix == 8 ? 16 : n <= (int64_t(1) << 22) ? 8 : n <= (int64_t(1) << 25) ? 16 : 24;
+  p.items = p.radix == 8 ? 16 : n <= (int64_t(1) << 22) ? 8 : n <= (int64_t(1) << 25) ? 16 : BF_SORT_ITEMS_LARGE;
   p.passes = bits > 0 ? (bits + p.radix - 1) / p.radix : 0;
   const int64_t tile = int64_t(kThreads) * p.items;
   p.tiles = (n + tile - 1) / tile;
@@ -112,7 +120,8 @@ __global__ __launch_bounds__(kThreads) void radix_count_kernel(const uint64_t* _
   __shared__ uint32_t h[B];
   for (int i = threadIdx.x; i < B; i += kThreads) h[i] = 0;
   __syncthreads();
-  const int64_t t0 = int64_t(blockIdx.x) * TILE;
+  const int64_t tile = xcd_slot(blockIdx.x, gridDim.x);   // the tiles sharing a counts line on one XCD
+  const int64_t t0 = tile * TILE;
   uint64_t key[ITEMS];
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
@@ -125,7 +134,7 @@ __global__ __launch_bounds__(kThreads) void radix_count_kernel(const uint64_t* _
     if (pos < n) atomicAdd(&h[uint32_t(key[i] >> shift) & mask], 1u);
   }
   __syncthreads();
-  for (int d = threadIdx.x; d < B; d += kThreads) counts[int64_t(d) * tiles + blockIdx.x] = h[d];
+  for (int d = threadIdx.x; d < B; d += kThreads) counts[int64_t(d) * tiles + tile] = h[d];
 }
 
 __global__ __launch_bounds__(kThreads) void radix_scan_kernel(uint32_t* __restrict__ counts, int64_t tiles,
@@ -169,7 +178,8 @@ __global__ __launch_bounds__(kThreads) void radix_scatter_kernel(const uint64_t*
   constexpr int64_t TILE = int64_t(kThreads) * ITEMS;
   static_assert(B % kThreads == 0, "whole digits per thread");
   const int64_t n = live_count(cap, n_dev, n_sub);
-  if (int64_t(blockIdx.x) * TILE >= n) return;   // a tile past the count (uniform over the block)
+  const int64_t tile = xcd_slot(blockIdx.x, gridDim.x);   // as in radix_count_kernel
+  if (tile * TILE >= n) return;   // a tile past the count (uniform over the block)
   __shared__ uint32_t wcnt[kWaves * B];   // per wave: running counts, then exclusive offsets over the waves
   __shared__ uint32_t s_scan[kWaves];
   __shared__ uint32_t dstart[B];          // the tile's first LDS slot of each digit
@@ -182,11 +192,11 @@ __global__ __launch_bounds__(kThreads) void radix_scatter_kernel(const uint64_t*
   for (int j = 0; j < DPT; ++j) {
     const int d = tid * DPT + j;
     tv[j] = totals[d];
-    pv[j] = prefix[int64_t(d) * tiles + blockIdx.x];
+    pv[j] = prefix[int64_t(d) * tiles + tile];
     tsum += tv[j];
   }
   __syncthreads();
-  const int64_t t0 = int64_t(blockIdx.x) * TILE + int64_t(w) * (64 * ITEMS) + lane;
+  const int64_t t0 = tile * TILE + int64_t(w) * (64 * ITEMS) + lane;
   uint64_t key[ITEMS];
   uint32_t dig[ITEMS], rank[ITEMS];
 #pragma unroll
@@ -307,7 +317,9 @@ inline int radix_sort_keys(const uint64_t* in, uint64_t* out, int64_t n, int beg
                                               st)
            : p.items == 16 ? run_passes<9, 16>(p, in, out, alt, n, n_dev, n_sub, begin_bit, end_bit, counts, totals,
                                                st)
-                           : run_passes<9, 24>(p, in, out, alt, n, n_dev, n_sub, begin_bit, end_bit, counts, totals,
+           : p.items == 24 ? run_passes<9, 24>(p, in, out, alt, n, n_dev, n_sub, begin_bit, end_bit, counts, totals,
+                                               st)
+                           : run_passes<9, 32>(p, in, out, alt, n, n_dev, n_sub, begin_bit, end_bit, counts, totals,
                                                st);
   return run_passes<8, 16>(p, in, out, alt, n, n_dev, n_sub, begin_bit, end_bit, counts, totals, st);
 }
