@@ -75,6 +75,16 @@ def test_gather_probe_arguments_checked_on_the_host():
     N.call("bf_gather_probe", p, 64, p, 256, p, 512, p, 0, 0x7FFFFFFF, 1, p, None)
 
 
+def test_launches_past_32_bit_work_item_counts_are_refused():
+    """A dispatch counts its work-items in 32 bits; a grid of 2^32 or more would be cut short without an
+    error, so every launch refuses one before reaching HIP (here bf_expand_rows with 2^32 entries, one
+    thread each: host buffers, never read)."""
+    buf = (C.c_int64 * 4)(0, 1, 2, 3)
+    p = C.cast(buf, C.c_void_p)
+    with pytest.raises(ValueError, match="work-items"):
+        N.call("bf_expand_rows", p, 1, 2 ** 32, p, None)
+
+
 def test_walk_record_arguments_checked_on_the_host():
     """bf_walk_records refuses 2^31 edges (32-bit degree field) and an unaligned record array, and the
     walk entry points an unaligned record array, before any launch (host buffers, never read)."""
