@@ -171,3 +171,31 @@ def test_core_attention_under_fp16_autocast(hip_device):
     ref = _oracle(q.detach()[0].cpu(), k.detach()[0].cpu(), v.detach()[0].cpu(), ei, dout.view(S, H, hn).cpu())
     _check((out.detach().view(S, H, hn), q.grad[0], k.grad[0], v.grad[0]), ref)
     assert idx.nnz == 8000
+
+
+@pytest.mark.parametrize("chunk,item", [(128, 768), (6, 10)])
+def test_fp16_bias_factor_and_dbias(hip_device, chunk, item):
+    """The EX = 2 instances in fp16: a float32 bias per entry (its gradient, dbias, in float32) and a V
+    factor per entry, with and without split rows; out, dq, dk, dv and dbias against the float64 oracle on
+    the same fp16 inputs."""
+    from budgetformer_amd.attention import sparse_edge_attention
+    from budgetformer_amd.hip_ops import AttentionIndex
+    S, H, hn = 900, 8, 16
+    q, k, v, ei, dout = _inputs(S, H, hn, 9000, seed=81 + chunk)
+    idx = AttentionIndex.from_coo(ei.to(hip_device), S, chunk=chunk, item=item)
+    g = torch.Generator().manual_seed(5 + chunk)
+    bias = torch.randn(idx.nnz, H, generator=g)
+    factor = (torch.rand(idx.nnz, H, generator=g) >= 0.3).float() / 0.7
+    qd, kd, vd = (t.to(hip_device).requires_grad_(True) for t in (q, k, v))
+    bd = bias.to(hip_device).requires_grad_(True)
+    out = sparse_edge_attention(qd, kd, vd, idx, bd, factor.to(hip_device), None)
+    out.backward(dout.to(hip_device))
+    torch.cuda.synchronize()
+    assert out.dtype == F16 and bd.grad.dtype == torch.float32
+    q64, k64, v64, d64 = (t.double() for t in (q, k, v, dout))
+    ei_o = _coo_order(idx)
+    r_out, r_Z = sa.attention_forward_stats(k64, q64, v64, ei_o, bias.double(), factor.double())
+    r_dq, r_dk, r_dv, r_db = sa.attention_backward_closed_form(k64, q64, v64, ei_o, r_out, r_Z, d64,
+                                                              bias.double(), factor.double())
+    _check((out.detach(), qd.grad, kd.grad, vd.grad), (r_out, r_dq, r_dk, r_dv))
+    assert_close("dbias", bd.grad, r_db, FP16_TOL)

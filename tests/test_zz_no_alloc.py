@@ -38,7 +38,7 @@ def _noalloc(idx, q, k, v, Z, dout, bias=None, need_dbias=False):
     return dq, dk, dv, dbias
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_noalloc_equals_bf_attn_bwd_on_two_calls_the_second_smaller(hip_device, dtype):
     from budgetformer_amd import hip_ops
     H, hn = 8, 16
