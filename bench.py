@@ -287,7 +287,8 @@ def main(argv=None):
              "attn_bwd_q_reduce_kernel", "attn_bwd_kv_reduce_kernel", "rw_select_reg_kernel", "rw_select_kernel",
              "real_select_fused_kernel", "row_block_sums_kernel", "row_ptr_kernel", "table_fill_kernel",
              "radix_count_kernel", "radix_scan_kernel", "radix_scatter_kernel", "unpack_rkey_kernel",
-             "reverse_slots_kernel", "order_count_kernel", "order_place_kernel", "split_rows_kernel", "rocprim"]
+             "reverse_slots_kernel", "order_count_kernel", "order_place_kernel", "split_rows_kernel", "gather_probe_kernel",
+             "rocprim"]
     if args.pmc_summary or args.req_summary:
         if args.pmc_summary:
             md, data = pmc_summary(*args.pmc_summary, args.copy_bytes, names)
