@@ -41,8 +41,7 @@ enum { BF_DTYPE_F32 = 0, BF_DTYPE_BF16 = 1, BF_DTYPE_F16 = 2 };
 
 /* ABI version (major*10000 + minor*100 + patch), returned by bf_version(). A
  * binding checks it for equality: any change to an entry point's arguments,
- * to a struct's fields or to their meaning bumps it. History (each version's
- * changes are listed in INTEGRATION.md):
+ * to a struct's fields or to their meaning bumps it. History:
  *   100  first ABI;
  *   200  bf_attn_fwd / bf_attn_bwd take score_clamp and a dropout; bf_attn_bwd
  *        no longer takes `out`; bf_reverse_slots replaces bf_reverse_entries;
