@@ -136,6 +136,37 @@ def test_edge_table_wide_rows_and_long_walks(hip_device, b_r, b_w, P, L):
         assert (ref_len > 768).sum() > 10
 
 
+@pytest.mark.parametrize("b_r,b_w,P,L", [(700, 300, 3, 3000), (0, 900, 4, 2500), (800, 0, 2, 4), (5, 40, 100, 90)])
+def test_wide_and_streamed_paths_on_isolated_and_dense_nodes(hip_device, b_r, b_w, P, L):
+    """Edge cases of the paths past LDS on a 60-node graph: ten isolated nodes (no real part; their walks
+    stay, so each walk offers only its step-1 self pair, kept with multiplicity), a dense core whose rows
+    fill neither budget, a chain; merged rows wider than 768 (a workgroup per row) with dedup, an RW-only
+    and a real-only table (no dedup), and walk shapes of 9,000 and 10,000 candidates (streaming top-k).
+    Bit-exact against the oracle."""
+    from budgetformer_amd.edges import build_attention_edges
+    n = 60
+    rng = np.random.default_rng(b_r + b_w + P)
+    pairs = {(int(a), int(b)) for a, b in rng.integers(20, n, (600, 2)) if a != b}
+    pairs |= {(i, i + 1) for i in range(10, 19)}                     # a chain 10 - 19
+    und = {(min(a, b), max(a, b)) for a, b in pairs}
+    src = np.array([a for a, b in und] + [b for a, b in und])
+    dst = np.array([b for a, b in und] + [a for a, b in und])
+    order = np.lexsort((dst, src))
+    src, dst = src[order], dst[order]
+    rowptr = np.concatenate([[0], np.cumsum(np.bincount(src, minlength=n))]).astype(np.int64)
+    col = dst.astype(np.int32)
+    assert (np.diff(rowptr)[:10] == 0).all()
+    g = _dev_graph(rowptr, col, n, hip_device)
+    u = rng.random((n * P, L), dtype=np.float32)
+    tab = build_attention_edges(g, real_edges_per_query=b_r, rw_edges_per_query=b_w, walk_length=L,
+                                walks_per_node=P, edge_seed=42, u=torch.from_numpy(u).to(hip_device))
+    ref_t, ref_len = et.build_edge_table(rowptr, col, n, b_r, b_w, L, P, 42, u)
+    assert np.array_equal(tab.row_len.cpu().numpy(), ref_len)
+    assert np.array_equal(tab.table.cpu().numpy(), ref_t)
+    if b_w and not b_r:
+        assert (ref_len[:10] == P).all()                             # the isolated nodes' self pairs
+
+
 def test_streamed_walk_selection_under_philox(hip_device):
     """The streaming RW selection (P*L = 10,000) with the in-kernel Philox uniforms, over the walk
     records and over rowptr/col, for the full range and a shard: equal to the oracle's table on the
