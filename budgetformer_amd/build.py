@@ -31,7 +31,7 @@ HIPCC_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{os.path.join(ROOT, 'include')}",
 ]
-# Extra compile definitions for tuning sweeps (e.g. "-DBF_UNROLL_FWD=2"); empty by default.
+# Extra compile definitions for tuning sweeps (e.g. "-DBF_UNROLL_FWD_F32=2"); empty by default.
 HIPCC_FLAGS += os.environ.get("BF_HIPCC_EXTRA", "").split()
 
 

@@ -37,11 +37,22 @@ namespace {
 constexpr int kBlock = 256;
 // Edges whose gathers are in flight together per group, per pass and element
 // type (measured on MI355X: more edges per group cost registers, hence waves).
-#ifndef BF_UNROLL_FWD
-#define BF_UNROLL_FWD 3
+// Four where they fit the same waves or win anyway: the bf16 dq pass (94
+// VGPRs, five waves as with three: c4's dq 2.72 -> 2.61 ms) and the fp32
+// forward (66 VGPRs, seven waves instead of eight: c2 131 -> 130 us); three
+// elsewhere (the fp32 dq pass at four loses two waves and 7%, the bf16 kv
+// pass a wave).
+#ifndef BF_UNROLL_FWD_F32
+#define BF_UNROLL_FWD_F32 4
 #endif
-#ifndef BF_UNROLL_Q
-#define BF_UNROLL_Q 3
+#ifndef BF_UNROLL_FWD_BF16
+#define BF_UNROLL_FWD_BF16 3
+#endif
+#ifndef BF_UNROLL_Q_F32
+#define BF_UNROLL_Q_F32 3
+#endif
+#ifndef BF_UNROLL_Q_BF16
+#define BF_UNROLL_Q_BF16 4
 #endif
 #ifndef BF_UNROLL_KV_F32
 #define BF_UNROLL_KV_F32 3
@@ -51,13 +62,13 @@ constexpr int kBlock = 256;
 #endif
 template <typename T> struct Unroll;
 template <> struct Unroll<float> {
-  static constexpr int fwd = BF_UNROLL_FWD, q = BF_UNROLL_Q, kv = BF_UNROLL_KV_F32;
+  static constexpr int fwd = BF_UNROLL_FWD_F32, q = BF_UNROLL_Q_F32, kv = BF_UNROLL_KV_F32;
 };
 template <> struct Unroll<uint16_t> {
-  static constexpr int fwd = BF_UNROLL_FWD, q = BF_UNROLL_Q, kv = BF_UNROLL_KV_BF16;
+  static constexpr int fwd = BF_UNROLL_FWD_BF16, q = BF_UNROLL_Q_BF16, kv = BF_UNROLL_KV_BF16;
 };
 template <> struct Unroll<_Float16> {   // the same row bytes and lane mapping as bf16
-  static constexpr int fwd = BF_UNROLL_FWD, q = BF_UNROLL_Q, kv = BF_UNROLL_KV_BF16;
+  static constexpr int fwd = BF_UNROLL_FWD_BF16, q = BF_UNROLL_Q_BF16, kv = BF_UNROLL_KV_BF16;
 };
 constexpr float kEps = 1e-6f;
 constexpr float kClamp = 5.0f;   // the reference's clamp bound, the default
