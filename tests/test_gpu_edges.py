@@ -167,6 +167,44 @@ def test_wide_and_streamed_paths_on_isolated_and_dense_nodes(hip_device, b_r, b_
         assert (ref_len[:10] == P).all()                             # the isolated nodes' self pairs
 
 
+def _random_symmetric_csr(rng, n, m):
+    src, dst = rng.integers(0, n, m), rng.integers(0, n, m)
+    und = {(min(a, b), max(a, b)) for a, b in zip(src.tolist(), dst.tolist()) if a != b}
+    s = np.array([a for a, b in und] + [b for a, b in und], dtype=np.int64)
+    d = np.array([b for a, b in und] + [a for a, b in und], dtype=np.int64)
+    order = np.lexsort((d, s))
+    s, d = s[order], d[order]
+    rowptr = np.concatenate([[0], np.cumsum(np.bincount(s, minlength=n))]).astype(np.int64)
+    return rowptr, d.astype(np.int32)
+
+
+def test_edge_table_randomized_small_cases(hip_device):
+    """60 random small configurations (1 to 200 nodes, 0 to 4 edges per node, budgets 0 to 40 per part,
+    1 to 8 walks of 1 to 12 steps, random seeds, injected or Philox uniforms) plus the degenerate ones (a
+    single node, graphs without edges, one edge): bit-exact against the oracle, case by case."""
+    from budgetformer_amd.edges import build_attention_edges
+    rng = np.random.default_rng(2024)
+    cases = [(1, 0, 2, 2, 2, 4), (5, 0, 3, 0, 2, 3), (5, 0, 0, 3, 2, 3), (2, 1, 1, 1, 1, 1), (2, 1, 0, 4, 3, 5)]
+    for _ in range(60):
+        b_r, b_w = int(rng.integers(0, 41)), int(rng.integers(0, 41))
+        n = int(rng.integers(1, 201))
+        cases.append((n, int(rng.integers(0, 4 * n + 1)), b_r, b_w if b_r + b_w else 1, int(rng.integers(1, 9)),
+                      int(rng.integers(1, 13))))
+    for i, (n, m, b_r, b_w, P, L) in enumerate(cases):
+        rowptr, col = _random_symmetric_csr(rng, n, m)
+        seed = int(rng.integers(0, 10_000))
+        g = _dev_graph(rowptr, col, n, hip_device)
+        philox_u = i % 3 == 2
+        u = philox.walk_uniforms(0, n, P, L, seed) if philox_u else rng.random((n * P, L), dtype=np.float32)
+        tab = build_attention_edges(g, real_edges_per_query=b_r, rw_edges_per_query=b_w, walk_length=L,
+                                    walks_per_node=P, edge_seed=seed,
+                                    u=None if philox_u else torch.from_numpy(u).to(hip_device))
+        ref_t, ref_len = et.build_edge_table(rowptr, col, n, b_r, b_w, L, P, seed, u)
+        case = f"case {i}: n={n} E={col.size} b=({b_r},{b_w}) P={P} L={L} seed={seed} philox={philox_u}"
+        assert np.array_equal(tab.row_len.cpu().numpy(), ref_len), case
+        assert np.array_equal(tab.table.cpu().numpy(), ref_t), case
+
+
 def test_streamed_walk_selection_under_philox(hip_device):
     """The streaming RW selection (P*L = 10,000) with the in-kernel Philox uniforms, over the walk
     records and over rowptr/col, for the full range and a shard: equal to the oracle's table on the
