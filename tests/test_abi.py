@@ -1,6 +1,7 @@
 """CPU checks of the C ABI: the library loads, exports every declared symbol,
 and its host-side argument checks reject bad calls without touching a GPU."""
 import ctypes as C
+import os
 import re
 
 import pytest
@@ -197,3 +198,26 @@ def test_key_inverse_constant_recovers_sources():
         base = et.edge_key(np.zeros_like(q), q, seed).astype(np.int64)
         back = (((key - base) % 2**32) * inv) % 2**32 & 0x7FFFFFFF
         assert np.array_equal(back, s)
+
+
+@pytest.mark.parametrize("struct,mirror", [("bf_attn_index", "AttnIndex"), ("bf_attn_dropout", "AttnDropout")])
+def test_struct_mirrors_match_the_header(tmp_path, struct, mirror):
+    """The ctypes mirrors have the header's size and field offsets: a C program built against the header
+    prints them (a field added to one side only, or reordered, fails here instead of shifting pointers)."""
+    import shutil
+    import subprocess
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    cls = getattr(N, mirror)
+    names = [f[0] for f in cls._fields_]
+    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "budgetformer_hip.h"', "int main(void) {",
+             f'  printf("%zu\\n", sizeof({struct}));']
+    lines += [f'  printf("%zu\\n", offsetof({struct}, {f}));' for f in names]
+    lines += ["  return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run([cc, "-I", os.path.dirname(N._HEADER), str(src), "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()]
+    assert got == [C.sizeof(cls)] + [getattr(cls, f).offset for f in names]
