@@ -296,6 +296,46 @@ def test_narrow_rows(hip_device, dtype, H, hn, chunk, item):
         assert_close(name, got, ref, tol)
 
 
+@pytest.mark.parametrize("dtype,H,hn", [(torch.float32, 8, 32), (torch.float32, 2, 128), (torch.float32, 16, 16),
+                                        (torch.bfloat16, 8, 64), (torch.bfloat16, 4, 128), (torch.bfloat16, 32, 16),
+                                        (torch.float16, 8, 64)])
+@pytest.mark.parametrize("extra", ["plain", "token", "dropout"])
+def test_widest_rows(hip_device, dtype, H, hn, extra):
+    """Rows of 256 (float32) or 512 (bfloat16, float16) elements, the widest the kernels take: a lane
+    group is a whole wavefront (64 lanes of 16 bytes), one group per wave, four per workgroup, and a
+    head spans 4 to 32 lanes. Forward and both backward passes against the oracle, with split query and
+    key rows (chunk 6, item 10). "token": the Graphormer token row and column (query 0 attends every key,
+    every query attends key 0; the dq pass's key-0 records), with a bias and its gradient in float32.
+    "dropout": the in-kernel dropout at rate 0.3 against the oracle's mask."""
+    from budgetformer_amd.hip_ops import AttentionIndex, Dropout
+    from oracle import philox
+    from parity_helpers import assert_close
+    S = 600
+    q, k, v, ei, dout = _inputs(S, H, hn, 5000, seed=H * 1000 + hn, dtype=dtype, mult=1.1)
+    if extra == "token":
+        ei = ei[:, (ei[0] > 0) & (ei[1] > 0)]
+        ar = torch.arange(1, S)
+        ei = torch.cat([ei, torch.stack([ar, torch.zeros_like(ar)]), torch.stack([torch.zeros_like(ar), ar])], 1)
+    idx = AttentionIndex.from_coo(ei.to(hip_device), S, chunk=6, item=10)
+    idx.token_column = extra == "token"
+    g = torch.Generator().manual_seed(5)
+    bias_e = torch.randn(idx.nnz, H, generator=g) if (extra == "token" and dtype == torch.float32) else None
+    rate, seed, off = 0.3, 91, 4
+    drop = Dropout(rate, seed, off) if extra == "dropout" else None
+    out, dq, dk, dv, db = _run(hip_device, q, k, v, idx, dout, bias_e=bias_e, dropout=drop)
+    factor = None
+    if drop is not None:
+        factor = torch.from_numpy(philox.dropout_keep_csr(idx.qptr.cpu().numpy(), H, rate, seed, off)).float()
+        factor = factor / (1.0 - rate)
+    ro, rZ, rdq, rdk, rdv, rdb = _oracle(q, k, v, _coo_order(idx), dout, bias_e=bias_e, factor_e=factor)
+    tol = 1e-5 if dtype == torch.float32 else (2e-2 if dtype == torch.bfloat16 else 5e-3)
+    for name, got, ref in (("out", out, ro), ("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv)):
+        assert_close(name, got, ref, tol)
+    if bias_e is not None:
+        assert_close("dbias", db, rdb, tol)
+    assert idx.qplan.items > 0 and idx.kplan.items > 0
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_row_past_the_long_row_threshold(hip_device, dtype):
     """A token row and column longer than BF_MAX_ITEMS_PER_ROW * BF_LONG_ROW_FACTOR items' worth of
