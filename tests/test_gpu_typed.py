@@ -76,6 +76,20 @@ def test_typed_attention_against_the_oracle(hip_device, dtype, chunk, item):
     _check(_run(hip_device, q, k, v, dout, idx, mod), _oracle(q, k, v, dout, ei, mod), TOL[dtype])
 
 
+@pytest.mark.parametrize("dtype,H,hn", [(torch.float32, 8, 32), (torch.float32, 2, 128), (torch.bfloat16, 8, 64),
+                                        (torch.bfloat16, 4, 128), (torch.float16, 8, 64)])
+def test_typed_attention_at_the_widest_rows(hip_device, dtype, H, hn):
+    """Typed edges with rows of 256 (float32) or 512 (bfloat16, float16) elements, one lane group per
+    wavefront, key rows split into items: out, dq, dk, dv and dE against the oracle."""
+    from budgetformer_amd.hip_ops import AttentionIndex
+    S, n_kv = 500, 450
+    q, k, v, dout, ei, mod = _problem(S, n_kv, H, hn, 6000, seed=H + hn, dtype=dtype, mult=1.2)
+    idx = AttentionIndex.from_typed_coo(ei.to(hip_device), S, n_kv, chunk=6, item=10)
+    idx.resolve()
+    assert idx.typed and idx.kplan.items > 0
+    _check(_run(hip_device, q, k, v, dout, idx, mod), _oracle(q, k, v, dout, ei, mod), TOL[dtype])
+
+
 def test_typed_long_query_rows_and_hub_keys(hip_device):
     """Query rows of up to 600 entries (no query row is split: they run whole on the row path) and a
     2,000-entry hub key row (split into items on the key side)."""
