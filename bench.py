@@ -499,6 +499,10 @@ def run(config, steps, warmup, chunk=None, item=None, with_cpu=True):
     if dominant == "attn_bwd_kv_kernel":
         roofline["gather_floor_ms"] = floor["kv_pass"]["ms"]
         roofline["frac_of_gather_floor"] = round(floor["kv_pass"]["ms"] / dom["avg_ms"], 4)
+        roofline["floor_ms"] = floor["kv_pass"]["attn_bwd_kv_kernel_floor_ms"]
+        roofline["frac_of_floor"] = round(roofline["floor_ms"] / dom["avg_ms"], 4)
+        roofline["floor_basis"] = "the pass's gathers alone plus its kv rows alone (k, v read, dK, dV written, " \
+                                  "in its row order), each timed with a probe that only moves those bytes"
     # the layer's traffic: every attention kernel's counter bytes per dispatch times its launches per layer
     attn_kernels = [n_ for n_ in kernels if n_.startswith("attn_")]
     layer_traffic = None
@@ -589,17 +593,21 @@ def run(config, steps, warmup, chunk=None, item=None, with_cpu=True):
 
 
 def gather_floor(idx, q, k, v, dout, H, s_bytes, D, kv_var, tok_row, chunk, kernels, reps):
-    """The gathers of each attention pass alone, timed with bf_gather_probe on the pass's own ids and tables
-    (HIP events on the library's stream, the mean over ``reps`` launches after one untimed launch):
+    """Each attention pass's memory floor: its gathers alone (bf_gather_probe) plus its own rows alone
+    (bf_row_stream_probe), both timed on the pass's own ids, tables and order (HIP events on the library's
+    stream, the mean over ``reps`` launches after one untimed launch):
 
-    - key-major (dk/dv) pass: per reverse entry the q and dO rows of its query and the query's row-stats
-      record ({1/D', Delta/D'} per head, 8·H bytes), non-temporal where the pass streams them; kv 0's
-      segment is left out when the dq pass sums the token column, and query 0's entries of the unsplit kv
-      rows when the pass takes the token row from its per-workgroup copy;
-    - query-major (forward, dq) passes: per entry the k and v rows of its kv id.
+    - key-major (dk/dv) pass: gathers, per reverse entry, of the q and dO rows of its query and the query's
+      row-stats record ({1/D', Delta/D'} per head, 8·H bytes), non-temporal where the pass streams them
+      (kv 0's segment left out when the dq pass sums the token column, and query 0's entries of the
+      unsplit kv rows when the pass takes the token row from its per-workgroup copy); rows: every kv row
+      in the pass's order (k_order), k and v read, dK and dV written;
+    - query-major passes: gathers, per entry, of the k and v rows of its kv id; rows: the forward reads q
+      and writes out, the dq pass reads q and dO and writes dq, in row order.
 
-    The passes also read and write their rows sequentially and do the arithmetic, so a pass's time over its
-    floor is at least 1; near 1, the pass is as fast as its gathers can be served."""
+    The two parts are timed apart and added: each alone keeps HBM busy, so together they take about their
+    sum. A pass also does its arithmetic and its small per-row records, so its time over its floor is at
+    least about 1; near 1, the pass is as fast as its memory traffic can be served."""
     import torch
 
     from budgetformer_amd import _native as N
@@ -623,10 +631,7 @@ def gather_floor(idx, q, k, v, dout, H, s_bytes, D, kv_var, tok_row, chunk, kern
     kv = idx.kv.contiguous()
     st = hip_ops._stream(dev)
 
-    def timed(t0, b0, t1, b1, t2, b2, ids, nt):
-        def launch():
-            N.call("bf_gather_probe", hip_ops._p(t0), b0, hip_ops._p(t1), b1, hip_ops._p(t2), b2, hip_ops._p(ids),
-                   ids.numel(), 0x7FFFFFFF, int(nt), hip_ops._p(sink), st)
+    def timed(launch):
         launch()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
@@ -636,16 +641,43 @@ def gather_floor(idx, q, k, v, dout, H, s_bytes, D, kv_var, tok_row, chunk, kern
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / reps
 
-    kv_ms = timed(q, row, dout, row, stat, 8 * H, kq, kv_var["stream_rows"])
-    qp_ms = timed(k, row, v, row, None, 0, kv, False)
+    def gathers(t0, b0, t1, b1, t2, b2, ids, nt):
+        return timed(lambda: N.call("bf_gather_probe", hip_ops._p(t0), b0, hip_ops._p(t1), b1, hip_ops._p(t2), b2,
+                                    hip_ops._p(ids), ids.numel(), 0x7FFFFFFF, int(nt), hip_ops._p(sink), st))
+
+    def streams(r0, r1, w0, w1, ids, n_rows, nt):
+        return timed(lambda: N.call("bf_row_stream_probe", hip_ops._p(r0), hip_ops._p(r1), hip_ops._p(w0),
+                                    hip_ops._p(w1), row, hip_ops._p(ids) if ids is not None else None, n_rows,
+                                    int(nt), hip_ops._p(sink), st))
+
+    kv_ms = gathers(q, row, dout, row, stat, 8 * H, kq, kv_var["stream_rows"])
+    qp_ms = gathers(k, row, v, row, None, 0, kv, False)
+    del stat
+    # the rows each pass reads and writes once (outputs into scratch of the outputs' shapes)
+    out_q = torch.empty_like(q)
+    fwd_rows_ms = streams(q, None, out_q, None, None, idx.n_q, True)
+    dq_rows_ms = streams(q, dout, out_q, None, None, idx.n_q, True)
+    del out_q
+    kv_order = idx.korder.contiguous()
+    w_k, w_v = torch.empty_like(k), torch.empty_like(v)
+    kv_rows_ms = streams(k, v, w_k, w_v, kv_order, idx.n_kv, False)
+    del w_k, w_v
     out = {"basis": gather_floor.__doc__.split("\n\n")[0].replace("\n", " ").replace("    ", " ")}
-    for key, ms, ids, per, names in (("kv_pass", kv_ms, kq, 2 * row + 8 * H, ("attn_bwd_kv_kernel",)),
-                                     ("q_passes", qp_ms, kv, 2 * row, ("attn_fwd_kernel", "attn_bwd_q_kernel"))):
+    for key, ms, ids, per, rows_part in (
+            ("kv_pass", kv_ms, kq, 2 * row + 8 * H,
+             {"attn_bwd_kv_kernel": (kv_rows_ms, idx.n_kv, 4 * row)}),
+            ("q_passes", qp_ms, kv, 2 * row,
+             {"attn_fwd_kernel": (fwd_rows_ms, idx.n_q, 2 * row), "attn_bwd_q_kernel": (dq_rows_ms, idx.n_q, 3 * row)})):
         rec = {"ids": int(ids.numel()), "bytes_per_id": per, "ms": round(ms, 5),
                "record_gbs": round(ids.numel() * per / (ms * 1e-3) / 1e9, 1)}
-        for name in names:
+        for name, (rows_ms, n_rows, row_bytes) in rows_part.items():
+            floor_ms = ms + rows_ms
+            rec[f"{name}_rows"] = {"rows": int(n_rows), "bytes_per_row": row_bytes, "ms": round(rows_ms, 5),
+                                   "gbs": round(n_rows * row_bytes / (rows_ms * 1e-3) / 1e9, 1)}
+            rec[f"{name}_floor_ms"] = round(floor_ms, 5)
             if name in kernels:
-                rec[f"{name}_over_floor"] = round(kernels[name]["avg_ms"] / ms, 3)
+                rec[f"{name}_over_gathers"] = round(kernels[name]["avg_ms"] / ms, 3)
+                rec[f"{name}_over_floor"] = round(kernels[name]["avg_ms"] / floor_ms, 3)
         out[key] = rec
     return out
 

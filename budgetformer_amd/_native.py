@@ -16,7 +16,7 @@ _LIB = os.path.join(_PKG, "_lib", "libbudgetformer_hip.so")
 
 BF_OK, BF_ERR_INVALID, BF_ERR_UNSUPPORTED, BF_ERR_HIP = 0, 1, 2, 3
 BF_DTYPE_F32, BF_DTYPE_BF16, BF_DTYPE_F16 = 0, 1, 2
-ABI_VERSION = 301                   # the header's BF_ABI_VERSION this binding is written against
+ABI_VERSION = 302                   # the header's BF_ABI_VERSION this binding is written against
 BF_MAX_ITEMS_PER_ROW = 160          # items a split row is cut into at most (the header's #define) ...
 BF_LONG_ROW_FACTOR = 64             # ... unless it is longer than 160 * 64 items' worth (the header's #define)
 
@@ -122,6 +122,7 @@ _SIGS = {
                               C.POINTER(AttnDropout), P_f32, vp, vp, vp, vp, P_f32, P_f32, P_f32, vp]),
     "bf_attn_typed_partials_floats": (i64, [C.POINTER(AttnIndex), i32, i32, i32]),
     "bf_gather_probe": (C.c_int, [vp, i32, vp, i32, vp, i32, P_i32, i64, C.c_uint32, i32, vp, vp]),
+    "bf_row_stream_probe": (C.c_int, [vp, vp, vp, vp, i32, P_i32, i64, i32, vp, vp]),
     "bf_attn_fwd_typed": (C.c_int, [C.POINTER(AttnIndex), i32, i32, i32, vp, vp, vp, P_f32, vp, P_f32, vp]),
     "bf_attn_bwd_typed": (C.c_int, [C.POINTER(AttnIndex), i32, i32, i32, vp, vp, vp, P_f32, P_f32, vp, vp, vp, vp,
                                     P_f32, P_f32, P_f32, vp]),

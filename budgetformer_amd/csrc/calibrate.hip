@@ -67,6 +67,59 @@ __global__ __launch_bounds__(kThreads) void gather_probe_kernel(const V4u* __res
   if (acc == kSinkMatch) atomicXor(sink, acc);
 }
 
+// Row streams: id e (row ids[e], or row e when ids is NULL) reads that row of
+// r0 and r1 and writes zeros over it in w0 and w1 (non-temporal stores, as the
+// passes write their outputs), G lanes of 16 bytes per row: the rows a pass
+// reads and writes once each, in its own order, without its gathers or its
+// arithmetic. Same grid-stride and sink as the gather probe.
+template <int G, bool NT>
+__global__ __launch_bounds__(kThreads) void row_stream_probe_kernel(const V4u* __restrict__ r0,
+                                                                    const V4u* __restrict__ r1, V4u* __restrict__ w0,
+                                                                    V4u* __restrict__ w1, int chunks,
+                                                                    const int32_t* __restrict__ ids, int64_t n,
+                                                                    uint32_t* __restrict__ sink) {
+  const int j = int(threadIdx.x % G);
+  const int64_t stride = int64_t(gridDim.x) * (kThreads / G);
+  const V4u zero = {0u, 0u, 0u, 0u};
+  uint32_t acc = 0;
+  for (int64_t e = (int64_t(blockIdx.x) * kThreads + threadIdx.x) / G; e < n; e += kUnroll * stride) {
+    int64_t row[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t eu = e + u * stride;
+      row[u] = eu < n ? (ids ? int64_t(ids[eu]) : eu) : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      if (row[u] < 0) continue;
+      if (r0) acc ^= fold_row<NT>(r0, row[u], chunks, j, G);
+      if (r1) acc ^= fold_row<NT>(r1, row[u], chunks, j, G);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      if (row[u] < 0) continue;
+      for (int k = j; k < chunks; k += G) {
+        if (w0) __builtin_nontemporal_store(zero, w0 + row[u] * chunks + k);
+        if (w1) __builtin_nontemporal_store(zero, w1 + row[u] * chunks + k);
+      }
+    }
+  }
+  if (acc == kSinkMatch) atomicXor(sink, acc);
+}
+
+template <int G>
+int launch_stream(bool nt, dim3 grid, hipStream_t st, const V4u* r0, const V4u* r1, V4u* w0, V4u* w1, int chunks,
+                  const int32_t* ids, int64_t n, uint32_t* sink) {
+  if (nt)
+    BF_LAUNCH("row_stream_probe_kernel", (row_stream_probe_kernel<G, true>), grid, dim3(kThreads), 0, st, r0, r1, w0,
+              w1, chunks, ids, n, sink);
+  else
+    BF_LAUNCH("row_stream_probe_kernel", (row_stream_probe_kernel<G, false>), grid, dim3(kThreads), 0, st, r0, r1,
+              w0, w1, chunks, ids, n, sink);
+  BF_CHECK_LAUNCH();
+  return BF_OK;
+}
+
 template <int G>
 int launch_probe(bool nt, dim3 grid, hipStream_t st, const V4u* t0, const V4u* t1, const V4u* t2, int c0, int c1,
                  int c2, const int32_t* ids, int64_t n, uint32_t id_mask, uint32_t* sink) {
@@ -118,5 +171,43 @@ extern "C" int bf_gather_probe(const void* t0, int32_t row_bytes0, const void* t
     case 8: return launch_probe<8>(nt, grid, st, p0, p1, p2, c0, c1, c2, ids, n_ids, id_mask, sink);
     case 16: return launch_probe<16>(nt, grid, st, p0, p1, p2, c0, c1, c2, ids, n_ids, id_mask, sink);
     default: return launch_probe<32>(nt, grid, st, p0, p1, p2, c0, c1, c2, ids, n_ids, id_mask, sink);
+  }
+}
+
+extern "C" int bf_row_stream_probe(const void* r0, const void* r1, void* w0, void* w1, int32_t row_bytes,
+                                   const int32_t* ids, int64_t n_rows, int32_t nontemporal, uint32_t* sink,
+                                   void* stream) {
+  const void* tabs[4] = {r0, r1, w0, w1};
+  bool any = false;
+  for (int i = 0; i < 4; ++i) {
+    if (!tabs[i]) continue;
+    any = true;
+    BF_CHECK_ARG((reinterpret_cast<uintptr_t>(tabs[i]) & 15) == 0, "row_stream_probe: table %d is not 16-byte "
+                 "aligned", i);
+  }
+  BF_CHECK_ARG(any, "row_stream_probe: no table");
+  BF_CHECK_ARG(row_bytes >= 16 && row_bytes <= 1024 && row_bytes % 16 == 0, "row_stream_probe: row of %d bytes "
+               "(16..1024, a multiple of 16)", row_bytes);
+  BF_CHECK_ARG(n_rows >= 0 && sink, "row_stream_probe: bad row count or sink");
+  if (n_rows == 0) return BF_OK;
+  const int chunks = row_bytes / 16;
+  int g = 1;
+  while (g < chunks) g <<= 1;
+  const int64_t need = ceil_div(n_rows * g, int64_t(kThreads));
+  const dim3 grid{unsigned(need < kMaxBlocks ? need : kMaxBlocks)};
+  const V4u* p0 = static_cast<const V4u*>(r0);
+  const V4u* p1 = static_cast<const V4u*>(r1);
+  V4u* q0 = static_cast<V4u*>(w0);
+  V4u* q1 = static_cast<V4u*>(w1);
+  hipStream_t st = as_stream(stream);
+  const bool nt = nontemporal != 0;
+  switch (g) {
+    case 1: return launch_stream<1>(nt, grid, st, p0, p1, q0, q1, chunks, ids, n_rows, sink);
+    case 2: return launch_stream<2>(nt, grid, st, p0, p1, q0, q1, chunks, ids, n_rows, sink);
+    case 4: return launch_stream<4>(nt, grid, st, p0, p1, q0, q1, chunks, ids, n_rows, sink);
+    case 8: return launch_stream<8>(nt, grid, st, p0, p1, q0, q1, chunks, ids, n_rows, sink);
+    case 16: return launch_stream<16>(nt, grid, st, p0, p1, q0, q1, chunks, ids, n_rows, sink);
+    case 32: return launch_stream<32>(nt, grid, st, p0, p1, q0, q1, chunks, ids, n_rows, sink);
+    default: return launch_stream<64>(nt, grid, st, p0, p1, q0, q1, chunks, ids, n_rows, sink);
   }
 }

@@ -54,8 +54,9 @@ enum { BF_DTYPE_F32 = 0, BF_DTYPE_BF16 = 1, BF_DTYPE_F16 = 2 };
  *   301  bf_gather_probe (calibration); bf_rw_select, bf_rw_select_rows,
  *        bf_real_select_merge, bf_real_select_rows and bf_assemble_rows take
  *        any budget and walk shape (they used to reject rows above 768 ids
- *        and more than 8191 walk candidates per query).                      */
-#define BF_ABI_VERSION 301
+ *        and more than 8191 walk candidates per query);
+ *   302  bf_row_stream_probe (calibration).                                  */
+#define BF_ABI_VERSION 302
 int bf_version(void);
 /* Message of the last failed call on this thread ("" if none). */
 const char* bf_last_error(void);
@@ -645,6 +646,21 @@ int bf_attn_bwd_kv_variant(const bf_attn_index* idx, int32_t dtype, int32_t num_
 int bf_gather_probe(const void* t0, int32_t row_bytes0, const void* t1, int32_t row_bytes1, const void* t2,
                     int32_t row_bytes2, const int32_t* ids, int64_t n_ids, uint32_t id_mask,
                     int32_t nontemporal, uint32_t* sink, void* stream);
+
+/* Row-stream calibration, the other half of a pass's memory floor (no
+ * reference counterpart). For e in [0, n_rows), row ids[e] (row e when ids is
+ * NULL) is read from each non-NULL r0, r1 (non-temporal loads when
+ * `nontemporal` != 0) and overwritten with zeros in each non-NULL w0, w1
+ * (non-temporal stores), row_bytes (16 to 1024, a multiple of 16) per row,
+ * tables 16-byte aligned at a stride of their row size; sink as for
+ * bf_gather_probe. The ids must lie in the tables (negative ids are skipped).
+ * On a pass's own rows in its own order (the key-major pass: its kv rows in
+ * k_order, k and v read, dK and dV written; the forward: q read, out written;
+ * the dq pass: q and dO read, dq written) it gives the time those rows alone
+ * take; with the gathers' time it bounds the pass from below.               */
+int bf_row_stream_probe(const void* r0, const void* r1, void* w0, void* w1, int32_t row_bytes,
+                        const int32_t* ids, int64_t n_rows, int32_t nontemporal, uint32_t* sink,
+                        void* stream);
 
 #ifdef __cplusplus
 }

@@ -19,7 +19,7 @@ def test_library_loads_and_exports_every_header_symbol():
     # the exact ABI version the header declares: a binding written against another one must not load
     import re
     declared = int(re.search(r"#define BF_ABI_VERSION (\d+)", open(N._HEADER).read()).group(1))
-    assert declared == 301 == N.ABI_VERSION
+    assert declared == 302 == N.ABI_VERSION
     assert lib.bf_version() == declared
 
 
@@ -74,6 +74,26 @@ def test_gather_probe_arguments_checked_on_the_host():
     with pytest.raises(ValueError, match="bad ids"):
         N.call("bf_gather_probe", p, 64, None, 0, None, 0, None, 4, 0x7FFFFFFF, 0, p, None)
     N.call("bf_gather_probe", p, 64, p, 256, p, 512, p, 0, 0x7FFFFFFF, 1, p, None)
+
+
+def test_row_stream_probe_arguments_checked_on_the_host():
+    """bf_row_stream_probe refuses rows that are not 16..1024 bytes in 16-byte steps, an unaligned table, a
+    call with no table, a negative row count and a missing sink, before any launch; zero rows launch
+    nothing (host buffers, never touched)."""
+    buf = (C.c_int64 * 8)()
+    p = C.cast(buf, C.c_void_p)
+    for rb in (8, 20, 1040):
+        with pytest.raises(ValueError, match="row of"):
+            N.call("bf_row_stream_probe", p, None, None, None, rb, None, 4, 0, p, None)
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        N.call("bf_row_stream_probe", None, None, C.c_void_p(p.value + 4), None, 64, None, 4, 0, p, None)
+    with pytest.raises(ValueError, match="no table"):
+        N.call("bf_row_stream_probe", None, None, None, None, 64, None, 4, 0, p, None)
+    with pytest.raises(ValueError, match="bad row count or sink"):
+        N.call("bf_row_stream_probe", p, None, None, None, 64, None, -1, 0, p, None)
+    with pytest.raises(ValueError, match="bad row count or sink"):
+        N.call("bf_row_stream_probe", p, None, None, None, 64, None, 4, 0, None, None)
+    N.call("bf_row_stream_probe", p, p, p, p, 1024, p, 0, 1, p, None)
 
 
 def test_launches_past_32_bit_work_item_counts_are_refused():
