@@ -98,7 +98,8 @@ def token_records(s, D, n_q, q_items):
     return q_items + -(-n_q // (256 // lpr))
 
 
-def kernel_bytes(s, D, H, lens_q, lens_k, n_token_rec=0, entry_bytes=0, token_row=0, chunk=128, kv_blocks=0):
+def kernel_bytes(s, D, H, lens_q, lens_k, n_token_rec=0, entry_bytes=0, token_row=0, chunk=128, kv_blocks=0,
+                 keep_mask=False):
     """Algorithmic bytes of the three pass kernels (each covers every entry: short rows and split items).
 
     With a token column (n_token_rec records) the dq pass also writes key 0's dK/dV terms, 2*D floats per
@@ -108,7 +109,9 @@ def kernel_bytes(s, D, H, lens_q, lens_k, n_token_rec=0, entry_bytes=0, token_ro
     take their first entry (query 0's) from that copy instead of gathering it.
     entry_bytes: what the dk/dv pass reads per gathered entry beyond its query id: 4 for the entry's slot in
     its query's row (with the query, the dropout's key), 12 with a bias or factor (the slot and the query's
-    row start, which give the CSR position they are indexed by)."""
+    row start, which give the CSR position they are indexed by).
+    keep_mask: a dropout's keep mask, one byte per entry and 8 heads, written by the forward and read by the
+    dq pass."""
     n_q, nnz = lens_q.size, int(lens_q.sum())
     n_kv = lens_k.size
     nk_touched = int((lens_k > 0).sum())
@@ -123,11 +126,13 @@ def kernel_bytes(s, D, H, lens_q, lens_k, n_token_rec=0, entry_bytes=0, token_ro
         lk = lens_k[1:token_row + 1]
         gathered -= int(((lk > 0) & (lk <= chunk)).sum())
         tok_bytes = kv_blocks * (2 * row + 8 * H)
+    mask = (H + 7) // 8 * nnz if keep_mask else 0
     return {
-        # Q read, O write, K and V gathered per edge, kv ids, Z write, qptr
-        "attn_fwd_kernel": row * (2 * n_q + 2 * nnz) + 4 * nnz + 4 * H * n_q + 8 * n_q,
-        # Q, dO read, dQ write, K and V per edge, kv ids, Z read + row stats write, qptr (+ token records)
-        "attn_bwd_q_kernel": row * (3 * n_q + 2 * nnz) + 4 * nnz + 12 * H * n_q + 8 * n_q + rec_bytes,
+        # Q read, O write, K and V gathered per edge, kv ids, Z write, qptr (+ the keep mask written)
+        "attn_fwd_kernel": row * (2 * n_q + 2 * nnz) + 4 * nnz + 4 * H * n_q + 8 * n_q + mask,
+        # Q, dO read, dQ write, K and V per edge, kv ids, Z read + row stats write, qptr (+ token records,
+        # + the keep mask read)
+        "attn_bwd_q_kernel": row * (3 * n_q + 2 * nnz) + 4 * nnz + 12 * H * n_q + 8 * n_q + rec_bytes + mask,
         # dK, dV written for every row; K, V read for rows with entries; Q and dO per gathered entry,
         # the {1/D', Delta/D'} row stats per gathered entry, kq ids, kptr, row order (+ token records)
         "attn_bwd_kv_kernel": row * (2 * n_kv + 2 * nk_touched + 2 * gathered) + 8 * H * gathered
@@ -399,8 +404,9 @@ def run(config, steps, warmup, chunk=None, item=None, with_cpu=True):
         # training-mode GPS: a fresh Philox key per step, the same one for the forward and the backward
         step_no[0] += 1
         drop = hip_ops.Dropout(rate, seed=1000 + step_no[0]) if rate else None
-        out, Z = hip_ops.attn_forward(idx, q, k, v, dropout=drop)
-        hip_ops.attn_backward(idx, q, k, v, None, Z, dout, dropout=drop)
+        # as the attention modules do: the forward keeps the keep bits it draws and the dq pass reads them
+        out, Z, keep = hip_ops.attn_forward(idx, q, k, v, dropout=drop, keep_mask=True)
+        hip_ops.attn_backward(idx, q, k, v, None, Z, dout, dropout=drop, keep=keep)
 
     # W warmup steps, then more (at most 5) while the last one still grew the caching allocator: a step
     # that maps fresh device memory pays for its first touch (c5, whose steps hold about 184 GB, has taken
@@ -463,7 +469,7 @@ def run(config, steps, warmup, chunk=None, item=None, with_cpu=True):
         lpr *= 2
     kv_blocks = -(-(-(-idx.n_kv // kv_var["rows_per_group"])) // (256 // lpr))
     kb = kernel_bytes(s_bytes, D, H, lens_q, lens_k, n_rec, entry_bytes=4 if rate else 0, token_row=tok_row,
-                      chunk=chunk, kv_blocks=kv_blocks)
+                      chunk=chunk, kv_blocks=kv_blocks, keep_mask=bool(rate))
     kernels = {}
     for name, (ms, launches) in sorted(kstats.items(), key=lambda x: -x[1][0]):
         avg = ms / max(launches, 1)

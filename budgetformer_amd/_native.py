@@ -16,7 +16,7 @@ _LIB = os.path.join(_PKG, "_lib", "libbudgetformer_hip.so")
 
 BF_OK, BF_ERR_INVALID, BF_ERR_UNSUPPORTED, BF_ERR_HIP = 0, 1, 2, 3
 BF_DTYPE_F32, BF_DTYPE_BF16, BF_DTYPE_F16 = 0, 1, 2
-ABI_VERSION = 302                   # the header's BF_ABI_VERSION this binding is written against
+ABI_VERSION = 303                   # the header's BF_ABI_VERSION this binding is written against
 BF_MAX_ITEMS_PER_ROW = 160          # items a split row is cut into at most (the header's #define) ...
 BF_LONG_ROW_FACTOR = 64             # ... unless it is longer than 160 * 64 items' worth (the header's #define)
 
@@ -43,7 +43,7 @@ class AttnIndex(C.Structure):
 
 class AttnDropout(C.Structure):
     """Mirror of ``struct bf_attn_dropout``."""
-    _fields_ = [("rate", C.c_float), ("seed", u64), ("offset", u64)]
+    _fields_ = [("rate", C.c_float), ("seed", u64), ("offset", u64), ("keep", vp)]
 
 
 # name -> (restype, argtypes)

@@ -40,7 +40,12 @@ class _SparseEdgeAttention(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, bias_e, factor_e, index, dropout, score_clamp):
-        out, Z = hip_ops.attn_forward(index, q, k, v, bias_e, factor_e, dropout, score_clamp)
+        # a dropout without bias or factor keeps the forward's keep bits for the dq pass, which then reads
+        # them instead of drawing them (with a bias or factor every pass draws: the same bits either way)
+        keep_mask = dropout is not None and dropout.rate > 0.0 and bias_e is None and factor_e is None
+        res = hip_ops.attn_forward(index, q, k, v, bias_e, factor_e, dropout, score_clamp, keep_mask=keep_mask)
+        out, Z = res[0], res[1]
+        ctx.keep = res[2] if keep_mask else None
         # the backward needs Z, not out (it sums Delta = dO . out from the entries in float32)
         ctx.save_for_backward(q, k, v, Z, bias_e, factor_e)
         ctx.index = index
@@ -55,7 +60,8 @@ class _SparseEdgeAttention(torch.autograd.Function):
         q, k, v, Z, bias_e, factor_e = ctx.saved_tensors
         dq, dk, dv, dbias = hip_ops.attn_backward(ctx.index, q, k, v, None, Z, dout.contiguous(), bias_e, factor_e,
                                                   need_dbias=ctx.need_dbias, dropout=ctx.dropout,
-                                                  score_clamp=ctx.score_clamp)
+                                                  score_clamp=ctx.score_clamp, keep=ctx.keep)
+        ctx.keep = None
         return dq, dk, dv, dbias, None, None, None, None
 
 

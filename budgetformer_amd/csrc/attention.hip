@@ -127,6 +127,11 @@ __device__ __forceinline__ typename Elem<T>::Raw load_row_raw_nt(const T* base, 
 // The three passes evaluate the same bit: the query-major passes know (r, s)
 // from the row they walk, the key-major pass from the reverse entry's query
 // and slot, so no pass needs an entry's CSR position for it.
+// With a keep mask (keepm: byte b of entry e at e * kbytes + b holds heads
+// 8b .. 8b + 7, bit h % 8) the forward also stores the bits it draws, and the
+// dq pass reads them back instead of drawing them again (EX = 4): the Philox
+// rounds cost that pass a wave per SIMD while its rows are in flight. The
+// key-major pass, which meets the entries in reverse-index order, keeps drawing.
 struct EdgeIn {
   const float* bias;     // float32 [nnz, H] or NULL
   const float* factor;   // float32 [nnz, H] or NULL
@@ -135,6 +140,8 @@ struct EdgeIn {
   float keep;            // kept iff u < keep (= 1 - rate)
   float scale;           // factor of a kept entry (1 / (1 - rate); 0 when rate = 1)
   uint32_t seed_lo, seed_hi, off_lo, off_hi;
+  uint8_t* keepm;        // NULL, or the keep mask, uint8 [nnz, kbytes] in CSR order
+  int kbytes;            // ceil(H / 8)
 };
 
 // Keep bits of the entry at slot s of query row r for heads 4*blk .. 4*blk + 3 (bit j: head 4*blk + j),
@@ -214,14 +221,118 @@ __device__ __forceinline__ float iter_factor(const EdgeIn& x, const IterDrop<kUn
   return f;
 }
 
+// The dropout factor of head `head` from an entry's keep-mask byte (the byte that holds the head).
+__device__ __forceinline__ float mask_factor(const EdgeIn& x, uint32_t byte, int head) {
+  return ((byte >> (head & 7)) & 1u) ? x.scale : 0.f;
+}
+
 // The V-message factor of a single entry (CSR position e, slot s of query row r) for this lane's head
-// (1 without factor and dropout).
+// (1 without factor and dropout). EX == 4 reads the keep mask the forward wrote.
 template <int EX>
 __device__ __forceinline__ float edge_factor(const EdgeIn& x, int64_t e, int32_t r, int32_t s, const Shape& sh,
                                              int head) {
   float f = (EX == 2 && x.factor) ? x.factor[e * sh.H + head] : 1.f;
-  if (EX == 1 || x.drop) f *= dropout_factor(x, r, s, head);
+  if (EX == 4)   // one byte per entry (H <= 8)
+    f *= mask_factor(x, x.keepm[e], head);
+  else if (EX == 1 || x.drop)
+    f *= dropout_factor(x, r, s, head);
   return f;
+}
+
+// Stores the keep bits of one iteration's entries (CSR positions e0 + u, those below `end`) into the keep
+// mask: byte b of an entry holds heads 8b .. 8b + 7, i.e. Philox blocks 2b (low nibble) and 2b + 1 (high).
+// With shared draws lane u * nb + blk holds the bits of (entry u, block blk); lane u * kbytes + b fetches
+// the two nibbles of its byte by shuffles and stores it (with one byte per entry, lane u stores entry u's).
+// Otherwise every lane holds its own head's bit of each entry (bit u), and the writer of each byte collects
+// bit u from the first lane of each of its heads. Every lane of the group takes part in the shuffles;
+// nothing is drawn again.
+// The general instance's form (any head count and group width); the dropout-only instance stores its
+// mask a window at a time (keep_window_add).
+template <int kUnroll>
+__device__ __forceinline__ void store_keep(const EdgeIn& x, const IterDrop<kUnroll>& it, int64_t e0, int64_t end,
+                                           const Shape& sh, const GroupPos& g) {
+  const int nb = (sh.H + 3) >> 2;
+  if (it.shared) {
+    const int j = g.g_lane;
+    const int u = x.kbytes == 1 ? j : j / x.kbytes, b = j - u * x.kbytes;
+    const int src = u * nb + 2 * b;                 // past the group for idle lanes: wraps, unused
+    const uint32_t lo = uint32_t(__shfl(int(it.task), src, 1 << sh.lpr_log2));
+    const uint32_t hi = uint32_t(__shfl(int(it.task), src + 1, 1 << sh.lpr_log2));
+    if (u < kUnroll && e0 + u < end)
+      x.keepm[(e0 + u) * x.kbytes + b] = uint8_t((lo & 15u) | (2 * b + 1 < nb ? (hi & 15u) << 4 : 0u));
+  } else {
+    // narrow groups (fewer lanes than the iteration has bytes, possibly): in rounds of the group's width,
+    // lane w = round * lpr + j (w = u * kbytes + b) collects bit u of each head of its byte from the
+    // head's first lane; every lane takes part in every round's shuffles
+    const int lpr = 1 << sh.lpr_log2;
+    const int n = kUnroll * x.kbytes;
+    for (int w0 = 0; w0 < n; w0 += lpr) {
+      const int w = w0 + g.g_lane;
+      const int u = x.kbytes == 1 ? w : w / x.kbytes, b = w - u * x.kbytes;
+      uint32_t byte = 0;
+#pragma unroll
+      for (int h = 0; h < 8; ++h) {
+        const int hh = 8 * b + h;
+        const uint32_t t = uint32_t(__shfl(int(it.task), hh << sh.lph_log2, lpr));
+        if (hh < sh.H) byte |= ((t >> (u & 31)) & 1u) << h;
+      }
+      if (u < kUnroll && e0 + u < end) x.keepm[(e0 + u) * x.kbytes + b] = uint8_t(byte);
+    }
+  }
+}
+
+// The keep mask of the dropout-only forward (one byte per entry, groups that share an iteration's draws),
+// stored a window at a time: lane j of the group owns entry w0 + j of a window of `len` entries (the group's
+// width rounded down to whole iterations, so no iteration straddles two windows: for the 2-byte types the
+// id chunk of ChunkIds), takes its byte's two nibbles straight from the lanes that drew them (lane
+// u * nb + blk holds block blk of entry u), and the window goes out as one store of len consecutive bytes
+// once its last iteration is done (or the segment ends). Byte stores per iteration instead left each row's
+// bytes to be written a few at a time, the lines partly written and evicted between writes (c4 forward
+// 2.13 -> 2.37 ms, windows 2.29 ms). Storing each segment's last window after the walk, so that the groups
+// of a wave store together, cost the instance its sixth wave and was slower (2.40 ms). Returns whether the
+// window was stored (the caller's window then starts at w0 + len).
+// buf: this lane's byte; for the 2-byte types the lane's id register of the chunk, dead once the
+// iteration that takes the lane's entry has shuffled it out (the lane's byte arrives in that iteration, and
+// the window is stored before the next chunk's ids are loaded), which spares the instance a register.
+template <int kUnroll>
+__device__ __forceinline__ bool keep_window_add(const EdgeIn& x, const IterDrop<kUnroll>& it, int& buf,
+                                                int64_t w0, int len, int64_t e0, int64_t end, const Shape& sh,
+                                                const GroupPos& g) {
+  const int nb = (sh.H + 3) >> 2;
+  const int lpr = 1 << sh.lpr_log2;
+  const int u = g.g_lane - int(e0 - w0);          // this lane's entry of the iteration, if 0 <= u < kUnroll
+  const int src = (u >= 0 && u < kUnroll ? u : 0) * nb;
+  const uint32_t lo = uint32_t(__shfl(int(it.task), src, lpr));
+  const uint32_t hi = uint32_t(__shfl(int(it.task), src + 1, lpr));
+  if (u >= 0 && u < kUnroll) buf = int((lo & 15u) | (nb > 1 ? (hi & 15u) << 4 : 0u));
+  if (e0 + kUnroll >= w0 + len || e0 + kUnroll >= end) {   // the window's last iteration (uniform)
+    if (g.g_lane < len && w0 + g.g_lane < end) x.keepm[w0 + g.g_lane] = uint8_t(buf);
+    return true;
+  }
+  return false;
+}
+
+// The keep-mask bytes of entries e0 .. e0 + 3 (one byte per entry: H <= 8) of a row ending at `end`, as
+// the two aligned dwords that hold them: w0 at e0 & ~3 and, only when the row has entries past it, w1 (no
+// load reaches past the row's last byte, so none past the mask). Byte of entry e0 + u: keep_byte(w, o, u).
+struct KeepWords {
+  uint32_t w0, w1;
+  int o;   // e0 & 3
+};
+
+__device__ __forceinline__ KeepWords load_keep_words(const uint8_t* __restrict__ keepm, int64_t e0, int64_t end) {
+  const int64_t a = e0 >> 2;
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(keepm);
+  KeepWords k;
+  k.o = int(e0 & 3);
+  k.w0 = w[a];                                    // bytes 4a .. 4a + 3: e0 is one of them
+  k.w1 = 4 * a + 4 < end ? w[a + 1] : 0u;
+  return k;
+}
+
+__device__ __forceinline__ uint32_t keep_byte(const KeepWords& k, int u) {
+  const int sh = 8 * (k.o + u);                   // 0 .. 48
+  return (sh < 32 ? (k.w0 >> sh) : (k.w1 >> (sh - 32))) & 0xffu;
 }
 
 __device__ __forceinline__ float edge_bias(const EdgeIn& x, int64_t e, const Shape& sh, int head) {
@@ -291,6 +402,8 @@ __device__ __forceinline__ void fwd_segment(const T* __restrict__ k, const T* __
   constexpr int kUnroll = Unroll<T>::fwd;
   const int lph = 1 << sh.lph_log2;
   ChunkIds<T, kUnroll> ids(sh, beg);
+  int kbuf = 0;                                   // EX == 4, float32: this lane's byte of the keep window
+  int64_t kw0 = beg;                              // and the window's start (2-byte types: ids.ids, ids.c0)
   const int col = gather_col(g);
   for (int64_t e0 = beg; e0 < end; e0 += kUnroll) {
     int s[kUnroll];
@@ -333,6 +446,16 @@ __device__ __forceinline__ void fwd_segment(const T* __restrict__ k, const T* __
       for (int i = 0; i < V; ++i) acc[i] = fmaf(w, vv[i], acc[i]);
       z += p;
     }
+    // the keep mask, once the iteration's rows are spent (stored earlier, its temporaries would sit beside
+    // the V rows still in flight)
+    if constexpr (EX == 4) {
+      const int klen = ((1 << sh.lpr_log2) / kUnroll) * kUnroll;   // = ids.len for the 2-byte types
+      constexpr bool kChunk = ChunkIds<T, kUnroll>::kChunk;
+      if (keep_window_add<kUnroll>(ex, drop, kChunk ? ids.ids : kbuf, kChunk ? ids.c0 : kw0, klen, e0, end, sh,
+                                   g))
+        kw0 += klen;
+    }
+    if (EX == 2 && ex.drop && ex.keepm) store_keep<kUnroll>(ex, drop, e0, end, sh, g);
   }
 }
 
@@ -635,11 +758,18 @@ __device__ __forceinline__ void dq_segment(const T* __restrict__ k, const T* __r
       kr[u] = Elem<T>::load_raw(k + int64_t(s[u]) * sh.D + col);
       vr[u] = Elem<T>::load_raw(v + int64_t(s[u]) * sh.D + col);
     }
-    // the keep bits depend on the entries' places only: drawn while the rows are in flight (c4's dq
-    // pass 2.90 -> 2.72 ms; the forward, one wave per SIMD short of this pass's pressure, keeps its
+    // with a keep mask (EX == 4: one byte per entry) the iteration's bytes in two aligned dwords, loaded
+    // after the rows (loads return in order, and the bits are used after the dots)
+    KeepWords kw{0u, 0u, 0};
+    if constexpr (EX == 4) {
+      static_assert(kUnroll <= 4, "an iteration's keep bytes span at most two dwords");
+      kw = load_keep_words(ex.keepm, e0, end);
+    }
+    // otherwise the keep bits depend on the entries' places only: drawn while the rows are in flight (c4's
+    // dq pass 2.90 -> 2.72 ms; the forward, one wave per SIMD short of this pass's pressure, keeps its
     // draw after the dots: there the same move costs it its sixth wave and 1%)
     IterDrop<kUnroll> drop{false, 0u};
-    if (EX) {
+    if (EX && EX != 4) {
       int32_t rows[kUnroll], slots[kUnroll];   // the dropout's (query row, slot) of each entry
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
@@ -664,7 +794,8 @@ __device__ __forceinline__ void dq_segment(const T* __restrict__ k, const T* __r
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       if (!ok[u]) continue;
-      const float f = EX ? iter_factor<kUnroll, EX>(ex, drop, u, e0 + u, sh, g.head) : 1.f;
+      const float f = EX == 4 ? mask_factor(ex, keep_byte(kw, u), g.head)
+                              : (EX ? iter_factor<kUnroll, EX>(ex, drop, u, e0 + u, sh, g.head) : 1.f);
       const EntryTerms t = entry_terms<EX>(d[u], w[u], inv_dprime, ex, e0 + u, f, sh, g);
       float kk[V];
       Elem<T>::unpack(kr[u], kk);
@@ -1656,8 +1787,8 @@ inline Items key_items(const bf_attn_index* idx, const Shape& sh, float* partial
 }
 
 // The per-entry inputs of a call, with the dropout's Philox key and threshold.
-int make_edge_in(const float* bias, const float* factor, const bf_attn_dropout* dropout, EdgeIn& ex) {
-  ex = EdgeIn{bias, factor, nullptr, 0, 1.f, 1.f, 0u, 0u, 0u, 0u};
+int make_edge_in(const float* bias, const float* factor, const bf_attn_dropout* dropout, int H, EdgeIn& ex) {
+  ex = EdgeIn{bias, factor, nullptr, 0, 1.f, 1.f, 0u, 0u, 0u, 0u, nullptr, (H + 7) / 8};
   if (dropout) {
     BF_CHECK_ARG(dropout->rate >= 0.f && dropout->rate <= 1.f, "attention: dropout rate %g outside [0, 1]",
                  double(dropout->rate));
@@ -1669,6 +1800,8 @@ int make_edge_in(const float* bias, const float* factor, const bf_attn_dropout* 
       ex.seed_hi = uint32_t(dropout->seed >> 32);
       ex.off_lo = uint32_t(dropout->offset);
       ex.off_hi = uint32_t(dropout->offset >> 32);
+      ex.keepm = dropout->keep;
+      BF_CHECK_ARG((reinterpret_cast<uintptr_t>(ex.keepm) & 3u) == 0, "attention: the keep mask must be 4-byte aligned");
     }
   }
   return BF_OK;
@@ -1676,10 +1809,12 @@ int make_edge_in(const float* bias, const float* factor, const bf_attn_dropout* 
 
 inline bool has_extra(const EdgeIn& ex) { return ex.bias || ex.factor || ex.drop; }
 
-// The per-entry instance a call takes: 0 plain, 1 dropout only, 2 anything with a bias, factor or dbias.
+// The per-entry instance a call takes: 0 plain, 1 dropout only, 2 anything with a bias, factor or dbias,
+// 4 dropout only with a keep mask (the forward stores the bits it draws, the dq pass reads them; the
+// key-major pass takes instance 1 and draws).
 inline int edge_mode(const EdgeIn& ex, bool dbias) {
   if (ex.bias || ex.factor || dbias) return 2;
-  return ex.drop ? 1 : 0;
+  return ex.drop ? (ex.keepm ? 4 : 1) : 0;
 }
 
 template <typename T>
@@ -1697,7 +1832,18 @@ int fwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
 #define BF_LAUNCH_FWD(EX)                                                                                        \
   BF_LAUNCH("attn_fwd_kernel", (attn_fwd_kernel<T, EX>), dim3(unsigned(blocks)), dim3(kBlock), lds, st, Q, K, Vv,  \
             idx->qptr, idx->kv, ex, O, Z, it, n_items, idx->n_q, sh, idx->chunk, idx->plan_counts)
+    // the dropout-only instance stores the keep mask a window at a time, for one byte per entry (H <= 8)
+    // and groups wide enough to share an iteration's draws; other shapes (more heads; H <= 3 with one lane
+    // per head) take the general instance, which stores it too
+    const bool shared_draws = Unroll<T>::fwd * ((sh.H + 3) >> 2) <= (1 << sh.lpr_log2);
     switch (edge_mode(ex, false)) {
+      case 4:
+        if (shared_draws && ex.kbytes == 1) {
+          BF_LAUNCH_FWD(4);
+        } else {
+          BF_LAUNCH_FWD(2);
+        }
+        break;
       case 2: BF_LAUNCH_FWD(2); break;
       case 1: BF_LAUNCH_FWD(1); break;
       default: BF_LAUNCH_FWD(0); break;
@@ -1799,7 +1945,15 @@ int bwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
   BF_LAUNCH("attn_bwd_q_kernel", (attn_bwd_q_kernel<T, EX>), dim3(unsigned(q_blocks)), dim3(kBlock), lds, st, Q, K, \
             Vv, idx->qptr, idx->kv, ex, Z, dO, static_cast<T*>(dq), dbias, rstat, qit, idx->q_items,                \
             idx->n_q, sh, idx->chunk, token_rec, tok_first, idx->plan_counts)
+    // the mask is read back where an entry's bits fill one byte (H <= 8); wider rows of heads draw
     switch (edge_mode(ex, dbias != nullptr)) {
+      case 4:
+        if (ex.kbytes == 1) {
+          BF_LAUNCH_Q(4);
+        } else {
+          BF_LAUNCH_Q(1);
+        }
+        break;
       case 2: BF_LAUNCH_Q(2); break;
       case 1: BF_LAUNCH_Q(1); break;
       default: BF_LAUNCH_Q(0); break;
@@ -1814,8 +1968,9 @@ int bwd_impl(const bf_attn_index* idx, const Shape& sh, const void* q, const voi
               token_rec, tok_first, idx->plan_counts);
     BF_CHECK_LAUNCH();
   }
-  BF_CHECK_OK(kv_pass_impl<T>(idx, sh, Q, K, Vv, ex, edge_mode(ex, dbias != nullptr), dbias, dO, rstat, dk, dv,
-                               kit, token_rec, st));
+  const int kv_mode = edge_mode(ex, dbias != nullptr);
+  BF_CHECK_OK(kv_pass_impl<T>(idx, sh, Q, K, Vv, ex, kv_mode == 4 ? 1 : kv_mode, dbias, dO, rstat, dk, dv, kit,
+                               token_rec, st));
   return BF_OK;
 }
 
@@ -1936,7 +2091,7 @@ extern "C" int bf_attn_fwd(const bf_attn_index* idx, int32_t dtype, int32_t num_
   if (rc || (rc = set_clamp(score_clamp, sh))) return rc;
   if ((rc = check_index(idx, false))) return rc;
   EdgeIn ex;
-  if ((rc = make_edge_in(bias, factor, dropout, ex))) return rc;
+  if ((rc = make_edge_in(bias, factor, dropout, num_heads, ex))) return rc;
   BF_CHECK_ARG(q && k && v && out && Z, "attn_fwd: null tensor");
   BF_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out),
                "attn_fwd: q/k/v/out must be 16-byte aligned");
@@ -1958,7 +2113,7 @@ extern "C" int bf_attn_bwd(const bf_attn_index* idx, int32_t dtype, int32_t num_
   if (rc || (rc = set_clamp(score_clamp, sh))) return rc;
   if ((rc = check_index(idx, true))) return rc;
   EdgeIn ex;
-  if ((rc = make_edge_in(bias, factor, dropout, ex))) return rc;
+  if ((rc = make_edge_in(bias, factor, dropout, num_heads, ex))) return rc;
   BF_CHECK_ARG(idx->ks || idx->nnz == 0 || (!has_extra(ex) && !dbias),
                "attn_bwd: a bias, factor, dropout or dbias needs the reverse entries' slots (ks)");
   BF_CHECK_ARG(q && k && v && Z && dout && dq && dk && dv && rowstat, "attn_bwd: null tensor");

@@ -125,16 +125,23 @@ const float* edge_tensor(const std::optional<at::Tensor>& t, const char* name, c
 
 bf_attn_dropout make_dropout(double rate, int64_t seed, int64_t offset) {
   TORCH_CHECK_VALUE(rate >= 0.0 && rate <= 1.0, "dropout rate ", rate, " outside [0, 1]");
-  return bf_attn_dropout{float(rate), uint64_t(seed), uint64_t(offset)};
+  return bf_attn_dropout{float(rate), uint64_t(seed), uint64_t(offset), nullptr};
 }
 
-// Forward (bf_attn_fwd): (out [n_q, H, hn] in q's dtype, Z [n_q, H] float32).
-std::tuple<at::Tensor, at::Tensor> sparse_attn_fwd(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
-                                                   const c10::List<std::optional<at::Tensor>>& index,
-                                                   at::IntArrayRef sizes, const std::optional<at::Tensor>& bias,
-                                                   const std::optional<at::Tensor>& factor, double dropout_rate,
-                                                   int64_t dropout_seed, int64_t dropout_offset,
-                                                   double score_clamp) {
+// Entries the index's kv array holds room for (its capacity; nnz when sized exactly): the keep mask's
+// rows, known without reading the entry count back.
+int64_t kv_capacity(const c10::List<std::optional<at::Tensor>>& index) {
+  const std::optional<at::Tensor> kv = index.get(1);
+  return kv.has_value() ? kv->numel() : 0;
+}
+
+// Forward (bf_attn_fwd): (out [n_q, H, hn] in q's dtype, Z [n_q, H] float32, keep). With keep_mask and a
+// dropout, keep is the mask of the bits drawn, uint8 [kv capacity, ceil(H / 8)], for the backward; else
+// empty.
+std::tuple<at::Tensor, at::Tensor, at::Tensor> sparse_attn_fwd(
+    const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, const c10::List<std::optional<at::Tensor>>& index,
+    at::IntArrayRef sizes, const std::optional<at::Tensor>& bias, const std::optional<at::Tensor>& factor,
+    double dropout_rate, int64_t dropout_seed, int64_t dropout_offset, double score_clamp, bool keep_mask) {
   TORCH_CHECK_VALUE(q.is_cuda(), "q must be a device tensor (got ", q.device(), ")");
   const c10::DeviceGuard guard(q.device());
   const at::Device dev = q.device();
@@ -143,7 +150,12 @@ std::tuple<at::Tensor, at::Tensor> sparse_attn_fwd(const at::Tensor& q, const at
   const int64_t H = q.size(1), hn = q.size(2);
   const float* b = edge_tensor(bias, "bias", idx, H, dev);
   const float* f = edge_tensor(factor, "factor", idx, H, dev);
-  const bf_attn_dropout drop = make_dropout(dropout_rate, dropout_seed, dropout_offset);
+  bf_attn_dropout drop = make_dropout(dropout_rate, dropout_seed, dropout_offset);
+  // the kernels read the mask by aligned dwords: its storage is rounded up to a multiple of 4 bytes
+  const int64_t kb = (H + 7) / 8, rows = keep_mask && dropout_rate > 0.0 ? kv_capacity(index) : 0;
+  at::Tensor keep =
+      at::empty({(rows * kb + 3) / 4 * 4}, q.options().dtype(at::kByte)).narrow(0, 0, rows * kb).view({rows, kb});
+  if (keep.numel()) drop.keep = keep.data_ptr<uint8_t>();
   at::Tensor out = at::empty_like(q);
   at::Tensor Z = at::empty({idx.n_q, H}, q.options().dtype(at::kFloat));
   const int64_t parts = bf_attn_partials_floats(&idx, int32_t(H), int32_t(hn));
@@ -153,7 +165,7 @@ std::tuple<at::Tensor, at::Tensor> sparse_attn_fwd(const at::Tensor& q, const at
                        dropout_rate > 0.0 ? &drop : nullptr, out.data_ptr(), Z.data_ptr<float>(),
                        partials.data_ptr<float>(), stream_of(q)),
            "bf::sparse_attn_fwd");
-  return {out, Z};
+  return {out, Z, keep};
 }
 
 // Backward (bf_attn_bwd): (dq, dk, dv, dbias); dbias is [nnz, H] float32 with need_dbias, else empty.
@@ -161,7 +173,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> sparse_attn_bwd(
     const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, const c10::List<std::optional<at::Tensor>>& index,
     at::IntArrayRef sizes, const at::Tensor& Z, const at::Tensor& dout, const std::optional<at::Tensor>& bias,
     const std::optional<at::Tensor>& factor, bool need_dbias, double dropout_rate, int64_t dropout_seed,
-    int64_t dropout_offset, double score_clamp) {
+    int64_t dropout_offset, double score_clamp, const std::optional<at::Tensor>& keep) {
   TORCH_CHECK_VALUE(q.is_cuda(), "q must be a device tensor (got ", q.device(), ")");
   const c10::DeviceGuard guard(q.device());
   const at::Device dev = q.device();
@@ -174,7 +186,16 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> sparse_attn_bwd(
                     dout.sizes(), " / Z ", Z.sizes(), " do not match q ", q.sizes());
   const float* b = edge_tensor(bias, "bias", idx, H, dev);
   const float* f = edge_tensor(factor, "factor", idx, H, dev);
-  const bf_attn_dropout drop = make_dropout(dropout_rate, dropout_seed, dropout_offset);
+  bf_attn_dropout drop = make_dropout(dropout_rate, dropout_seed, dropout_offset);
+  if (keep.has_value() && keep->numel() && dropout_rate > 0.0) {
+    // the forward's mask of this index, dropout and head count (a [kv capacity, ceil(H / 8)] byte tensor)
+    drop.keep = opt_ptr<uint8_t>(keep, "keep", at::kByte, dev);
+    TORCH_CHECK_VALUE(keep->dim() == 2 && keep->size(0) >= kv_capacity(index) && keep->size(1) == (H + 7) / 8 &&
+                          keep->storage_offset() % 4 == 0 &&
+                          int64_t(keep->storage().nbytes()) >= keep->storage_offset() + (keep->numel() + 3) / 4 * 4,
+                      "keep must be the forward's [", kv_capacity(index), ", ", (H + 7) / 8, "] mask (got ",
+                      keep->sizes(), ")");
+  }
   at::Tensor dq = at::empty_like(q), dk = at::empty_like(k), dv = at::empty_like(v);
   at::Tensor dbias = need_dbias ? at::empty({idx.nnz, H}, q.options().dtype(at::kFloat))
                                 : at::empty({0}, q.options().dtype(at::kFloat));
@@ -370,10 +391,10 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> transpose_table(const at::Tensor&
 TORCH_LIBRARY(bf, m) {
   m.def("sparse_attn_fwd(Tensor q, Tensor k, Tensor v, Tensor?[] index, int[] sizes, Tensor? bias=None, "
         "Tensor? factor=None, float dropout_rate=0.0, int dropout_seed=0, int dropout_offset=0, "
-        "float score_clamp=5.0) -> (Tensor, Tensor)");
+        "float score_clamp=5.0, bool keep_mask=False) -> (Tensor, Tensor, Tensor)");
   m.def("sparse_attn_bwd(Tensor q, Tensor k, Tensor v, Tensor?[] index, int[] sizes, Tensor Z, Tensor dout, "
         "Tensor? bias=None, Tensor? factor=None, bool need_dbias=False, float dropout_rate=0.0, int dropout_seed=0, "
-        "int dropout_offset=0, float score_clamp=5.0) -> (Tensor, Tensor, Tensor, Tensor)");
+        "int dropout_offset=0, float score_clamp=5.0, Tensor? keep=None) -> (Tensor, Tensor, Tensor, Tensor)");
   m.def("sparse_attn_fwd_typed(Tensor q, Tensor k, Tensor v, Tensor?[] index, int[] sizes, Tensor type_mod) "
         "-> (Tensor, Tensor)");
   m.def("sparse_attn_bwd_typed(Tensor q, Tensor k, Tensor v, Tensor?[] index, int[] sizes, Tensor type_mod, "

@@ -1137,8 +1137,10 @@ class Dropout:
     seed: int
     offset: int = 0
 
-    def struct(self):
-        return N.AttnDropout(float(self.rate), int(self.seed) & (2 ** 64 - 1), int(self.offset) & (2 ** 64 - 1))
+    def struct(self, keep=None):
+        """The C struct; ``keep``: the forward's keep mask (a uint8 device tensor, bf_attn_dropout.keep)."""
+        return N.AttnDropout(float(self.rate), int(self.seed) & (2 ** 64 - 1), int(self.offset) & (2 ** 64 - 1),
+                             None if keep is None else keep.data_ptr())
 
 
 def _dropout_arg(dropout: Optional[Dropout]):
@@ -1166,14 +1168,18 @@ SCORE_CLAMP = 5.0   # the reference's clamp bound on q.k / sqrt(hn)
 
 
 def attn_forward(idx: AttentionIndex, q, k, v, bias=None, factor=None, dropout: Optional[Dropout] = None,
-                 score_clamp: float = SCORE_CLAMP):
+                 score_clamp: float = SCORE_CLAMP, keep_mask: bool = False):
     """out [n_q,H,hn] (activation dtype), Z [n_q,H] float32, through bf::sparse_attn_fwd (which checks
     the shapes, dtypes and devices against the index). ``score_clamp``: the bound of the clamp on
-    q.k / sqrt(hn), in (0, 5]."""
+    q.k / sqrt(hn), in (0, 5]. With ``keep_mask`` also returns the dropout's keep mask (uint8
+    [kv capacity, ceil(H/8)], empty without a dropout) for ``attn_backward(keep=...)``, whose dq pass then
+    reads the bits instead of drawing them again (the same bits: results equal bit for bit)."""
     if bias is not None or factor is not None:
         idx.nnz      # per-edge tensors are [nnz, H]: the index passes the count itself
     t, n = idx.op_args(backward=False)
-    return N.load_ops().sparse_attn_fwd(q, k, v, t, n, bias, factor, *_dropout_op_args(dropout), float(score_clamp))
+    out, Z, keep = N.load_ops().sparse_attn_fwd(q, k, v, t, n, bias, factor, *_dropout_op_args(dropout),
+                                                float(score_clamp), bool(keep_mask))
+    return (out, Z, keep) if keep_mask else (out, Z)
 
 
 def attn_forward_typed(idx: AttentionIndex, q, k, v, type_mod):
@@ -1205,10 +1211,11 @@ def kv_pass_variant(n_q: int, n_kv: int, dtype: torch.dtype, heads: int, head_di
 
 
 def attn_backward(idx: AttentionIndex, q, k, v, out, Z, dout, bias=None, factor=None, need_dbias: bool = False,
-                  dropout: Optional[Dropout] = None, score_clamp: float = SCORE_CLAMP):
+                  dropout: Optional[Dropout] = None, score_clamp: float = SCORE_CLAMP, keep=None):
     """(dq, dk, dv, dbias-or-None) for attn_forward's outputs. ``out`` is accepted for the autograd
     surface but not read: the backward sums Delta = dO . out from the entries in float32. Through
-    bf::sparse_attn_bwd, which checks the shapes, dtypes and devices."""
+    bf::sparse_attn_bwd, which checks the shapes, dtypes and devices. ``keep``: the keep mask
+    ``attn_forward(keep_mask=True)`` returned for the same index and dropout, or None."""
     rate, seed, off = _dropout_op_args(dropout)
     if not 0.0 <= rate <= 1.0:
         raise ValueError(f"dropout rate {rate} outside [0, 1]")
@@ -1216,5 +1223,5 @@ def attn_backward(idx: AttentionIndex, q, k, v, out, Z, dout, bias=None, factor=
         idx.nnz      # per-edge tensors are [nnz, H]: the index passes the count itself
     t, n = idx.op_args(backward=True, entries=bias is not None or factor is not None or need_dbias or rate > 0.0)
     dq, dk, dv, dbias = N.load_ops().sparse_attn_bwd(q, k, v, t, n, Z, dout, bias, factor, bool(need_dbias), rate,
-                                                     seed, off, float(score_clamp))
+                                                     seed, off, float(score_clamp), keep)
     return dq, dk, dv, (dbias if need_dbias else None)

@@ -55,8 +55,10 @@ enum { BF_DTYPE_F32 = 0, BF_DTYPE_BF16 = 1, BF_DTYPE_F16 = 2 };
  *        bf_real_select_merge, bf_real_select_rows and bf_assemble_rows take
  *        any budget and walk shape (they used to reject rows above 768 ids
  *        and more than 8191 walk candidates per query);
- *   302  bf_row_stream_probe (calibration).                                  */
-#define BF_ABI_VERSION 302
+ *   302  bf_row_stream_probe (calibration);
+ *   303  bf_attn_dropout gains `keep` (the forward stores its keep bits, the
+ *        backward's query-major pass reads them back).                      */
+#define BF_ABI_VERSION 303
 int bf_version(void);
 /* Message of the last failed call on this thread ("" if none). */
 const char* bf_last_error(void);
@@ -533,12 +535,22 @@ typedef struct bf_attn_index {
  * (the key-major pass knows an entry by its query kq and slot ks, so the mask
  * needs no CSR position there); a kept entry's V message
  * (after the softmax normalisation) is scaled by 1/(1 - rate). Forward and
- * backward given the same struct draw the same mask; no [nnz, H] mask exists.
- * Pass NULL (or rate 0) for none.                                           */
+ * backward given the same struct draw the same mask. Pass NULL (or rate 0)
+ * for none.
+ *   keep: NULL, or a byte mask of ceil(H/8) bytes per CSR position (byte b of
+ *   entry e, at e * ceil(H/8) + b, holds heads 8b .. 8b + 7, bit h % 8 set
+ *   when head h is kept), 4-byte aligned, of at least nnz * ceil(H/8) bytes
+ *   rounded up to a multiple of 4 (the kernels read it by aligned dwords).
+ *   bf_attn_fwd stores every entry's bits there; bf_attn_bwd, given the same
+ *   struct after that forward, reads them back in its query-major pass when
+ *   the call has no bias, factor or dbias and H <= 8 (the pass then skips the
+ *   Philox rounds) and draws them elsewhere: the same bits either way, so the
+ *   results are the same bit for bit with or without it.                    */
 typedef struct bf_attn_dropout {
   float rate;          /* drop probability in [0, 1] */
   uint64_t seed;       /* Philox key */
   uint64_t offset;     /* Philox counter offset */
+  uint8_t* keep;       /* NULL or the keep mask (above) */
 } bf_attn_dropout;
 
 /* float32 scratch the attention calls need for split rows (and, with

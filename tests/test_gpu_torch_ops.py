@@ -79,7 +79,7 @@ def test_attention_ops_equal_the_abi_and_the_oracle(hip_device, dtype, extras):
     ops = _ops()
     t, n = idx.op_args(backward=False)
     seed = drop[1] - 2 ** 64 if drop[1] >= 2 ** 63 else drop[1]
-    out, Z = ops.sparse_attn_fwd(q, k, v, t, n, bias, factor, drop[0], seed, drop[2])
+    out, Z, _ = ops.sparse_attn_fwd(q, k, v, t, n, bias, factor, drop[0], seed, drop[2])
     t, n = idx.op_args(backward=True, entries=True)
     dq, dk, dv, db = ops.sparse_attn_bwd(q, k, v, t, n, Z, dout, bias, factor, True, drop[0], seed, drop[2])
     torch.cuda.synchronize()
