@@ -937,33 +937,15 @@ __device__ __forceinline__ void group_merge_keys(uint32_t (&lk)[K]) {
 
 constexpr int pow2_at_least(int x) { return x <= 1 ? 1 : 2 * pow2_at_least((x + 1) / 2); }
 
-// Writes table row qi from the real winners lk[0, k_real) (kNoKey = none) and
-// the RW selection rw_kv[qi, 0 .. rw_cnt[qi]): the KR + KW ids, padded to a
-// power of two, are sorted by a bitonic network in registers and stored
-// ascending (unique values when dedup), padded with -1 to width.
-template <int KR, int KW>
-__device__ __forceinline__ void emit_row(const uint32_t (&lk)[KR], uint32_t base, int k_real,
-                                         const int32_t* __restrict__ rw_kv, const int32_t* __restrict__ rw_cnt,
-                                         int k_rw, int64_t qi, int dedup, int32_t* __restrict__ table, int width,
-                                         int32_t* __restrict__ row_len) {
-  constexpr int NV = pow2_at_least(KR + KW);
-  constexpr int32_t kPad = 0x7fffffff;          // sorts after every node id (ids < 2^31 - 1)
-  int32_t v[NV];
+// Ascending bitonic sort of N (a power of two) values in registers.
+template <int N>
+__device__ __forceinline__ void sort_regs(int32_t (&v)[N]) {
 #pragma unroll
-  for (int j = 0; j < KR; ++j) v[j] = (j < k_real && lk[j] != kNoKey) ? src_of(lk[j], base) : kPad;
-#pragma unroll
-  for (int j = KR; j < NV; ++j) v[j] = kPad;
-  if (rw_kv != nullptr && KW > 0) {
-    const int n_w = rw_cnt[qi];
-#pragma unroll
-    for (int j = 0; j < KW; ++j) v[KR + j] = (j < n_w && j < k_rw) ? rw_kv[qi * k_rw + j] : kPad;
-  }
-#pragma unroll
-  for (int k = 2; k <= NV; k <<= 1) {
+  for (int k = 2; k <= N; k <<= 1) {
 #pragma unroll
     for (int j = k >> 1; j > 0; j >>= 1) {
 #pragma unroll
-      for (int i = 0; i < NV; ++i) {
+      for (int i = 0; i < N; ++i) {
         const int l = i ^ j;
         if (l > i) {
           const int32_t x = v[i], y = v[l];
@@ -974,14 +956,80 @@ __device__ __forceinline__ void emit_row(const uint32_t (&lk)[KR], uint32_t base
       }
     }
   }
-  int32_t* out = table + qi * width;
+}
+
+// Row-access flags of emit_row (bits of `vec`): the RW selection's rows and the table's rows are
+// 16-byte aligned (k_rw and width multiples of 4 on aligned bases), so they move as 16-byte loads and stores.
+constexpr int kVecRw = 4, kVecTable = 2;
+
+// Writes table row qi from the real winners lk[0, k_real) (kNoKey = none) and
+// the RW selection rw_kv[qi, 0 .. rw_cnt[qi]): the KR + KW ids, padded to a
+// power of two, are sorted by a bitonic network in registers, duplicates
+// (with dedup) turned into padding and sorted behind the ids, so that the row
+// is the register prefix: stored whole, ascending, -1 past its length. Every
+// register index is static, so the row goes out as 16-byte stores (and the
+// selection comes in as 16-byte loads) where aligned. Writing the kept ids one
+// dword at a time at a running index (each store instruction touching a line
+// per lane) left the c4 build's fused kernel far below its memory rate.
+template <int KR, int KW>
+__device__ __forceinline__ void emit_row(const uint32_t (&lk)[KR], uint32_t base, int k_real,
+                                         const int32_t* __restrict__ rw_kv, const int32_t* __restrict__ rw_cnt,
+                                         int k_rw, int64_t qi, int dedup, int32_t* __restrict__ table, int width,
+                                         int32_t* __restrict__ row_len, int vec) {
+  constexpr int NV = pow2_at_least(KR + KW);
+  constexpr int32_t kPad = 0x7fffffff;          // sorts after every node id (ids < 2^31 - 1)
+  int32_t v[NV];
+#pragma unroll
+  for (int j = 0; j < KR; ++j) v[j] = (j < k_real && lk[j] != kNoKey) ? src_of(lk[j], base) : kPad;
+#pragma unroll
+  for (int j = KR; j < NV; ++j) v[j] = kPad;
+  if (rw_kv != nullptr && KW > 0) {
+    const int n_w = rw_cnt[qi];
+    const int32_t* r = rw_kv + qi * k_rw;
+    if ((vec & kVecRw) && KW % 4 == 0) {
+#pragma unroll
+      for (int j = 0; j < KW; j += 4) {
+        if (j < k_rw && j < n_w) {              // k_rw is a multiple of 4: the 4 ids are in the row
+          const int4 x = *reinterpret_cast<const int4*>(r + j);
+          v[KR + j] = x.x;
+          v[KR + j + 1] = j + 1 < n_w ? x.y : kPad;
+          v[KR + j + 2] = j + 2 < n_w ? x.z : kPad;
+          v[KR + j + 3] = j + 3 < n_w ? x.w : kPad;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < KW; ++j) v[KR + j] = (j < n_w && j < k_rw) ? r[j] : kPad;
+    }
+  }
+  sort_regs<NV>(v);
+  if (dedup) {
+    bool dup[NV];
+    dup[0] = false;
+#pragma unroll
+    for (int j = 1; j < NV; ++j) dup[j] = v[j] != kPad && v[j] == v[j - 1];
+#pragma unroll
+    for (int j = 1; j < NV; ++j)
+      if (dup[j]) v[j] = kPad;
+    sort_regs<NV>(v);
+  }
   int len = 0;
 #pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const bool keep = v[j] != kPad && !(dedup && j > 0 && v[j] == v[j - 1]);
-    if (keep) out[len++] = v[j];
+  for (int j = 0; j < NV; ++j) len += v[j] != kPad ? 1 : 0;
+  int32_t* out = table + qi * width;              // the row is v[0, min(width, NV)), then -1
+  if (vec & kVecTable) {
+#pragma unroll
+    for (int j = 0; j < NV; j += 4)
+      if (j < width)
+        *reinterpret_cast<int4*>(out + j) = make_int4(v[j] == kPad ? -1 : v[j], v[j + 1] == kPad ? -1 : v[j + 1],
+                                                      v[j + 2] == kPad ? -1 : v[j + 2],
+                                                      v[j + 3] == kPad ? -1 : v[j + 3]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+      if (j < width) out[j] = v[j] == kPad ? -1 : v[j];
   }
-  for (int c = len; c < width; ++c) out[c] = -1;
+  for (int c = NV; c < width; ++c) out[c] = -1;   // a table wider than the row's parts (no RW selection)
   row_len[qi] = len;
 }
 
@@ -1020,7 +1068,7 @@ __global__ __launch_bounds__(kThreads) void real_select_fused_kernel(
       scan_keys<kScanUnroll>(in_src + beg, int32_t(in_ptr[q + 1] - beg), lane, 64, base, lk);
       group_merge_keys<64, KR>(lk);
     }
-    if (lane == 0) emit_row<KR, KW>(lk, base, k_real, rw_kv, rw_cnt, k_rw, q - q_lo, dedup, table, width, row_len);
+    if (lane == 0) emit_row<KR, KW>(lk, base, k_real, rw_kv, rw_cnt, k_rw, q - q_lo, dedup, table, width, row_len, vec4);
     return;
   }
   if (b < hub_blocks + heavy_blocks) {
@@ -1035,7 +1083,7 @@ __global__ __launch_bounds__(kThreads) void real_select_fused_kernel(
       scan_keys<kScanUnroll>(in_src + beg, int32_t(deg), gl, kGroup, base, lk);
       group_merge_keys<kGroup, KR>(lk);
     }
-    if (gl == 0) emit_row<KR, KW>(lk, base, k_real, rw_kv, rw_cnt, k_rw, q - q_lo, dedup, table, width, row_len);
+    if (gl == 0) emit_row<KR, KW>(lk, base, k_real, rw_kv, rw_cnt, k_rw, q - q_lo, dedup, table, width, row_len, vec4);
     return;
   }
   const int64_t qi = (b - hub_blocks - heavy_blocks) * kThreads + threadIdx.x;
@@ -1046,12 +1094,12 @@ __global__ __launch_bounds__(kThreads) void real_select_fused_kernel(
     const int64_t beg = in_ptr[q], end = in_ptr[q + 1];
     if (end - beg > light_max) return;          // a heavy query: a group writes its row
     // 16-byte chunks read up to 3 entries past `end`: only where they stay inside the array
-    if (vec4 && ((end - 1) | 3) < in_ptr[num_nodes])
+    if ((vec4 & 1) && ((end - 1) | 3) < in_ptr[num_nodes])
       scan_keys_x4<kScanX4Unroll>(in_src, beg, end, base, lk);
     else
       scan_keys<kScanUnroll>(in_src + beg, int32_t(end - beg), 0, 1, base, lk);
   }
-  emit_row<KR, KW>(lk, base, k_real, rw_kv, rw_cnt, k_rw, qi, dedup, table, width, row_len);
+  emit_row<KR, KW>(lk, base, k_real, rw_kv, rw_cnt, k_rw, qi, dedup, table, width, row_len, vec4);
 }
 
 // One BFS layer of the probe's reception cone (utils/fullgraph_sp_support.py:
@@ -1180,7 +1228,10 @@ int launch_real_merge(const int64_t* in_ptr, const int32_t* in_src, int64_t num_
     const int64_t heavy = k_real > 0 ? split.n_heavy : 0;
     const int64_t blocks = ceil_div(n_hubs, int64_t(kHubsPerBlock)) + ceil_div(heavy, int64_t(kQPB)) +
                            ceil_div(n_q, int64_t(kThreads));
-    const int vec4 = (reinterpret_cast<uintptr_t>(in_src) & 15) == 0;
+    // bit 0: in_src 16-byte aligned (the light rows' 16-byte chunks); kVecTable, kVecRw: emit_row's rows
+    const int vec4 = ((reinterpret_cast<uintptr_t>(in_src) & 15) == 0 ? 1 : 0) |
+                     ((reinterpret_cast<uintptr_t>(table) & 15) == 0 && width % 4 == 0 ? kVecTable : 0) |
+                     (rw_kv && (reinterpret_cast<uintptr_t>(rw_kv) & 15) == 0 && k_rw % 4 == 0 ? kVecRw : 0);
     const int64_t hub_thr = n_hubs > 0 ? hub_threshold : (int64_t(1) << 62);
     const int64_t light_max = k_real > 0 ? split.light_max : (int64_t(1) << 62);
 #define BF_LAUNCH_FUSED(KR, KW)                                                                                     \
