@@ -66,6 +66,12 @@ constexpr int kBlock = 256;
 #ifndef BF_UNROLL_KV_CACHED_F32
 #define BF_UNROLL_KV_CACHED_F32 2
 #endif
+// The dk/dv pass with the in-kernel dropout (EX = 1): two entries in flight, whose registers leave room
+// for the Philox draw at four waves per SIMD (bf16 four-row instance 121 VGPRs, against 135 and three
+// waves with three entries: c4 3.97 -> 3.86 ms).
+#ifndef BF_UNROLL_KV_DROPOUT
+#define BF_UNROLL_KV_DROPOUT 2
+#endif
 template <typename T> struct Unroll;
 template <> struct Unroll<float> {
   static constexpr int fwd = BF_UNROLL_FWD_F32, q = BF_UNROLL_Q_F32, kv = BF_UNROLL_KV_F32,
@@ -1277,7 +1283,7 @@ __device__ __forceinline__ void dkv_segment(const T* __restrict__ q, const T* __
   if constexpr (EX == 3) {
     dkv_segment_typed<T, NT>(q, dout, kq, ex, rstat, beg, end, sh, g, krow, vrow, dk, dv);
   } else {
-    constexpr int kUnroll = NT ? Unroll<T>::kv : Unroll<T>::kv_cached;
+    constexpr int kUnroll = EX == 1 ? BF_UNROLL_KV_DROPOUT : (NT ? Unroll<T>::kv : Unroll<T>::kv_cached);
     const int lph = 1 << sh.lph_log2;
     ChunkIds<T, kUnroll> ids(sh, beg);
     const int col = gather_col(g);
