@@ -121,6 +121,20 @@ def test_bf16_kv_pass_c4_instance_with_dropout(hip_device, extras):
         assert_close(name, got, ref, 2e-2)
     if bias is not None:
         assert_close("dbias", dbias, rdb, 2e-2)
+    # c4's timed step as the modules run it: the forward stores its keep bits and the dq pass reads them
+    # (the dropout-only instances) — every output equal to the drawing form's bit for bit, the mask equal
+    # to the oracle's bits
+    out1, Z1, kmask = hip_ops.attn_forward(idx, q, k, v, bias=bias, dropout=drop, keep_mask=True)
+    r1 = hip_ops.attn_backward(idx, q, k, v, out1, Z1, dout, bias=bias, need_dbias=bias is not None,
+                               dropout=drop, keep=kmask)
+    torch.cuda.synchronize()
+    for name, a, b in (("out", out1, out), ("Z", Z1, Z), ("dq", r1[0], dq), ("dk", r1[1], dk), ("dv", r1[2], dv)):
+        assert torch.equal(a, b), name
+    if bias is not None:
+        assert torch.equal(r1[3], dbias)
+    bits = keep.numpy().astype(np.uint8) << np.arange(H, dtype=np.uint8)[None, :]
+    assert np.array_equal(kmask[:nnz, 0].cpu().numpy(), np.bitwise_or.reduce(bits, axis=1))
+    del out1, Z1, r1, kmask
     for t, rows in ((out, qa), (dq, qa), (dk, kt), (dv, kt)):
         t[rows] = 0
         assert not t.any()
