@@ -72,6 +72,16 @@ constexpr int kBlock = 256;
 #ifndef BF_UNROLL_KV_DROPOUT
 #define BF_UNROLL_KV_DROPOUT 2
 #endif
+// The typed-edge (Exphormer) passes: entries in flight of the dk/dv segment and the dq pass (0: the
+// untyped pass's setting). Two in the dk/dv segment (bf16 instances 157-171 VGPRs, three waves for most,
+// against 181-194 and two): a typed backward over 2.45M queries of 12 entries, 6.90 -> 6.75 ms; the dq
+// pass at three or two entries was slower (7.00, 6.92 ms).
+#ifndef BF_UNROLL_KV_TYPED
+#define BF_UNROLL_KV_TYPED 2
+#endif
+#ifndef BF_UNROLL_Q_TYPED
+#define BF_UNROLL_Q_TYPED 0
+#endif
 template <typename T> struct Unroll;
 template <> struct Unroll<float> {
   static constexpr int fwd = BF_UNROLL_FWD_F32, q = BF_UNROLL_Q_F32, kv = BF_UNROLL_KV_F32,
@@ -1187,7 +1197,7 @@ __device__ __forceinline__ void dkv_segment_typed(const T* __restrict__ q, const
                                                   const typename Elem<T>::Raw& vrow,
                                                   float (&dk)[Elem<T>::kPerVec], float (&dv)[Elem<T>::kPerVec]) {
   constexpr int V = Elem<T>::kPerVec;
-  constexpr int kUnroll = Unroll<T>::kv;
+  constexpr int kUnroll = BF_UNROLL_KV_TYPED ? BF_UNROLL_KV_TYPED : Unroll<T>::kv;
   const int lph = 1 << sh.lph_log2;
   const int col = gather_col(g);
   float ke0[V], ke1[V], dk0[V], dk1[V];
@@ -1576,7 +1586,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_q_typed_kernel(
     const T* __restrict__ dout, T* __restrict__ dq, float2* __restrict__ rstat, float* __restrict__ mod_rec,
     int64_t n_q, int rows_per_group, Shape sh) {
   constexpr int V = Elem<T>::kPerVec;
-  constexpr int kUnroll = Unroll<T>::q;
+  constexpr int kUnroll = BF_UNROLL_Q_TYPED ? BF_UNROLL_Q_TYPED : Unroll<T>::q;
   extern __shared__ float lds[];
   const GroupPos g = group_pos<T>(sh);
   const int col = gather_col(g);
