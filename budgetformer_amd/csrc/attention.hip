@@ -61,8 +61,8 @@ constexpr int kBlock = 256;
 #define BF_UNROLL_KV_BF16 3
 #endif
 // The dk/dv pass over cache-resident q and dO tables (the instance that gathers them with normal loads):
-// two entries in flight in float32 (c2: 0.196 -> 0.192 ms against three; four 0.202 ms); the streaming
-// instance keeps `kv`.
+// two entries in flight in float32 (c2: 0.196 -> 0.192 ms against three; four 0.202 ms; one, at seven
+// waves in 66 VGPRs, 0.196 against 0.189 for two at six); the streaming instance keeps `kv`.
 #ifndef BF_UNROLL_KV_CACHED_F32
 #define BF_UNROLL_KV_CACHED_F32 2
 #endif
